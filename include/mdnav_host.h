@@ -1,0 +1,168 @@
+/*
+ * mdnav_host.h — host-side definitions that both the HIP library and the CPU
+ * oracle must agree on bit for bit: default plant parameters, the policy
+ * initialisation stream, and the minibatch order of a PPO update.
+ * Header-only C++17; no GPU code.
+ */
+#ifndef MDNAV_HOST_H
+#define MDNAV_HOST_H
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include "mdnav_math.h"
+#include "mdnav_types.h"
+
+namespace mdn {
+
+// Layout of the flat actor/critic parameter vectors (ppo.hpp:35-45): actor
+// W1[hidden][obs] @0, b1, W2[4][hidden], b2, log_std[4]; critic W1[hidden][32],
+// b1, w2[hidden], b2.
+struct PolicyShape {
+    uint32_t obs = MDN_ACTOR_OBS_POOLED;
+    uint32_t hidden = MDN_HIDDEN;
+    uint32_t critic_obs = MDN_CRITIC_OBS;
+    uint32_t critic_hidden = MDN_HIDDEN;
+    uint32_t actor_b1() const { return hidden * obs; }
+    uint32_t actor_w2() const { return actor_b1() + hidden; }
+    uint32_t actor_b2() const { return actor_w2() + MDN_ACTIONS * hidden; }
+    uint32_t actor_log_std() const { return actor_b2() + MDN_ACTIONS; }
+    uint32_t actor_count() const { return actor_log_std() + MDN_ACTIONS; }
+    uint32_t critic_b1() const { return critic_hidden * critic_obs; }
+    uint32_t critic_w2() const { return critic_b1() + critic_hidden; }
+    uint32_t critic_b2() const { return critic_w2() + critic_hidden; }
+    uint32_t critic_count() const { return critic_b2() + 1; }
+};
+
+// xorshift32 (13,17,5) and its 24-bit uniform (world.hpp:30-31).
+MDN_HD uint32_t xorshift(uint32_t& s) { s ^= s << 13; s ^= s >> 17; s ^= s << 5; return s; }
+MDN_HD float urand(uint32_t& s) { return float(xorshift(s) >> 8) * (1.0f / 16777216.0f); }
+
+// L2F Crazyflie profile (physics.hpp:184-219).
+inline MdnPhysicsParams crazyflie_params() {
+    MdnPhysicsParams p;
+    std::memset(&p, 0, sizeof(p));
+    const float positions[12] = {.028f, -.028f, 0, -.028f, -.028f, 0, -.028f, .028f, 0, .028f, .028f, 0};
+    const float torque_z[4] = {-1, 1, -1, 1};
+    const float inertia_diag[3] = {9.416556729130406e-6f, 9.644051701582312e-6f, 1.745951732253285e-5f};
+    const float inertia_inv_diag[3] = {106195.93007988465f, 103690.85846314249f, 57275.35197719487f};
+    for (int r = 0; r < 4; ++r) {
+        const int i = 3 * r;
+        p.rotor_positions[i] = positions[i];
+        p.rotor_positions[i + 1] = positions[i + 1];
+        p.rotor_thrust_directions[i + 2] = 1.0f;
+        p.rotor_torque_directions[i + 2] = torque_z[r];
+        p.rotor_thrust_coefficients[i] = 0.00352526f;
+        p.rotor_thrust_coefficients[i + 1] = 0.01437313f;
+        p.rotor_thrust_coefficients[i + 2] = 0.09223048f;
+        p.rotor_torque_constants[r] = 4.665e-3f;
+        p.rotor_time_constants_rising[r] = 0.05545454545454546f;
+        p.rotor_time_constants_falling[r] = 0.24939393939393945f;
+    }
+    for (int i = 0; i < 3; ++i) {
+        p.inertia[4 * i] = inertia_diag[i];
+        p.inertia_inverse[4 * i] = inertia_inv_diag[i];
+    }
+    p.gravity_world[2] = -9.81f;
+    p.mass = 0.027f + 0.0017f + 0.0003f + 0.0016f;
+    p.action_min = 0.0f;
+    p.action_max = 1.0f;
+    p.dt = 0.01f;
+    p.position_limit = 100000.0f;
+    p.velocity_limit = 100000.0f;
+    p.angular_velocity_limit = 100000.0f;
+    return p;
+}
+
+// Default run configuration of main.mm:461-464.
+inline MdnSimConfig default_config() {
+    MdnSimConfig c;
+    std::memset(&c, 0, sizeof(c));
+    c.n = 128; c.tick = 0; c.mode = 0; c.family = 0; c.substeps = 5; c.sensor_period = 1;
+    c.sensor_delay = 0; c.command_delay = 0; c.max_steps = 200; c.seed = 42; c.eval = 0;
+    c.speed = 2; c.distance = 4; c.wind = 0; c.depth_noise = 0; c.dropout = 0; c.risk_coef = 0;
+    c.entropy_coef = .005f; c.learning_rate = .0003f; c.velocity_contract = 1; c.geometry_memory = 0;
+    return c;
+}
+
+// Policy initialisation (cpu_reference.hpp:89-103 == main.mm:548-554): seed
+// 1789 xorshift Box–Muller; actor W1*0.04, W2*0.01, log_std=-1; critic
+// W1*0.15, w2*0.1; biases zero.
+inline void init_policy(const PolicyShape& s, float* actor, float* critic) {
+    std::fill(actor, actor + s.actor_count(), 0.0f);
+    std::fill(critic, critic + s.critic_count(), 0.0f);
+    uint32_t seed = 1789;
+    auto normal = [&]() {
+        const float u = max_f(urand(seed), 1.0e-7f);
+        const float lu = log_f(u);
+        const float v = urand(seed);
+        return sqrt_f(-2.0f * lu) * cos_f(6.2831853f * v);
+    };
+    for (uint32_t i = 0; i < s.actor_b1(); i++) actor[i] = normal() * 0.04f;
+    for (uint32_t i = s.actor_w2(); i < s.actor_b2(); i++) actor[i] = normal() * 0.01f;
+    for (uint32_t i = 0; i < MDN_ACTIONS; i++) actor[s.actor_log_std() + i] = -1.0f;
+    for (uint32_t i = 0; i < s.critic_b1(); i++) critic[i] = normal() * 0.15f;
+    for (uint32_t i = s.critic_w2(); i < s.critic_b2(); i++) critic[i] = normal() * 0.1f;
+}
+
+// Minibatch order of one rollout update (cpu_reference.hpp:569-579 ==
+// main.mm:1331-1338): contiguous row blocks, shuffled with
+// mt19937(0x9e3779b9 + rollout*0x85ebca6b), reshuffled only before epoch 1.
+// std::shuffle is implementation-defined, so the permutation is a
+// Fisher–Yates over the mt19937 stream (whose output the C++ standard fixes):
+// for i = n-1 .. 1, j = (u32 * (i+1)) >> 32.  Returns the start row of every
+// update in execution order.
+inline void fisher_yates(std::vector<uint32_t>& v, std::mt19937& rng) {
+    for (size_t i = v.size(); i > 1; --i) {
+        const uint64_t j = (uint64_t(rng()) * uint64_t(i)) >> 32;
+        std::swap(v[i - 1], v[size_t(j)]);
+    }
+}
+
+inline std::vector<uint32_t> minibatch_schedule(uint32_t rows, uint32_t minibatch, uint32_t epochs,
+                                                uint32_t rollout_index) {
+    std::vector<uint32_t> starts;
+    for (uint32_t s = 0; s < rows; s += minibatch) starts.push_back(s);
+    std::mt19937 rng(0x9e3779b9u + rollout_index * 0x85ebca6bu);
+    fisher_yates(starts, rng);
+    std::vector<uint32_t> order;
+    order.reserve(size_t(starts.size()) * epochs);
+    for (uint32_t e = 0; e < epochs; ++e) {
+        if (e == 1) fisher_yates(starts, rng);
+        order.insert(order.end(), starts.begin(), starts.end());
+    }
+    return order;
+}
+
+// Adam bias corrections 1 - beta^step, evaluated on the host in float with the
+// platform pow exactly as cpu_reference.hpp:558-559 does.
+inline void adam_corrections(uint64_t step, float beta1, float beta2, float* c1, float* c2) {
+    *c1 = 1.0f - std::pow(beta1, float(step));
+    *c2 = 1.0f - std::pow(beta2, float(step));
+}
+
+// RAPTOR1 loader (raptor.hpp:25-40).
+inline bool load_raptor_file(const char* path, MdnRaptorWeights* w) {
+    if (!path || !w) return false;
+    FILE* f = std::fopen(path, "rb");
+    if (!f) return false;
+    unsigned char header[16];
+    bool ok = std::fread(header, 1, 16, f) == 16;
+    static const unsigned char magic[8] = {'R', 'A', 'P', 'T', 'O', 'R', '1', 0};
+    ok = ok && std::memcmp(header, magic, 8) == 0;
+    uint32_t version = 0, count = 0;
+    std::memcpy(&version, header + 8, 4);
+    std::memcpy(&count, header + 12, 4);
+    ok = ok && version == 1 && count == 2084;
+    ok = ok && std::fread(w, 1, sizeof(*w), f) == sizeof(*w);
+    std::fclose(f);
+    return ok;
+}
+
+} // namespace mdn
+
+#endif /* MDNAV_HOST_H */

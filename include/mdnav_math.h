@@ -1,0 +1,213 @@
+/*
+ * mdnav_math.h — elementary functions with one definition for CPU and GPU.
+ *
+ * The reference evaluates exp/log/sin/cos/tanh with the platform libm (Apple
+ * libm on the CPU path, Metal "precise" on the GPU path), so its two paths
+ * already differ in the last bits.  Here both paths compile the functions
+ * below, built only from IEEE operations that are correctly rounded on x86-64
+ * SSE and on gfx950 (+, -, *, /, sqrt, floor, ldexp) with contraction off.
+ * The same input therefore gives the same bits on the host and the device,
+ * which is what lets integer outcomes (contact/done flags, reset decisions,
+ * RNG streams) agree exactly between the HIP path and the CPU oracle.
+ *
+ * Methods (published, restated from the mathematics):
+ *   exp, expm1  Cody–Waite reduction x = k ln2 + r, |r| <= ln2/2 (ln2 split in
+ *               a 16-bit head and a tail), Taylor polynomial of degree 7/8 in r
+ *               (truncation < 1e-8 relative), scaling by 2^k with ldexp.
+ *   log         x = 2^e m, m in [sqrt(1/2), sqrt(2)), log m = 2 atanh(s),
+ *               s = (m-1)/(m+1), odd series to s^11 (|s| <= 0.1716).
+ *   sin, cos    Cody–Waite reduction by pi/2 with the three-part split of
+ *               Cephes (Moshier), Taylor polynomials on [-pi/4, pi/4].
+ *   tanh        t = expm1(2|x|), tanh = sign(x) t / (t + 2).
+ * Accuracy is a few ulp against glibc (checked in tests/test_oracle_math.py);
+ * the reference's own CPU/GPU tolerance is 2e-5 absolute.
+ *
+ * Build rule: every translation unit that includes this header must be
+ * compiled with -ffp-contract=off and without fast-math.
+ */
+#ifndef MDNAV_MATH_H
+#define MDNAV_MATH_H
+
+#include <stdint.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#include <hip/hip_runtime.h>
+#define MDN_HD __host__ __device__ __forceinline__
+#else
+#include <cmath>
+#include <cstring>
+#define MDN_HD inline
+#endif
+
+#ifdef __clang__
+#pragma clang fp contract(off)
+#endif
+
+namespace mdn {
+
+MDN_HD float floor_f(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return floorf(x);
+#else
+    return std::floor(x);
+#endif
+}
+
+MDN_HD float ldexp_f(float x, int k) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return ldexpf(x, k);
+#else
+    return std::ldexp(x, k);
+#endif
+}
+
+MDN_HD float sqrt_f(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_sqrtf(x);
+#else
+    return std::sqrt(x);
+#endif
+}
+
+MDN_HD float fabs_f(float x) { return x < 0.0f ? -x : (x == 0.0f ? 0.0f : x); }
+
+MDN_HD uint32_t float_bits(float x) {
+    uint32_t u;
+#if defined(__HIP_DEVICE_COMPILE__)
+    u = __float_as_uint(x);
+#else
+    std::memcpy(&u, &x, 4);
+#endif
+    return u;
+}
+
+MDN_HD float bits_float(uint32_t u) {
+    float x;
+#if defined(__HIP_DEVICE_COMPILE__)
+    x = __uint_as_float(u);
+#else
+    std::memcpy(&x, &u, 4);
+#endif
+    return x;
+}
+
+MDN_HD float inf_f() { return bits_float(0x7f800000u); }
+MDN_HD float nan_f() { return bits_float(0x7fc00000u); }
+MDN_HD bool isfinite_f(float x) { return (float_bits(x) & 0x7f800000u) != 0x7f800000u; }
+
+// ln2 = LN2_HI + LN2_LO; LN2_HI has 16 significant bits so k*LN2_HI is exact.
+constexpr float LN2_HI = 0.693145751953125f;
+constexpr float LN2_LO = 1.42860677e-06f;
+constexpr float LOG2E = 1.44269502f;
+
+MDN_HD float exp_f(float x) {
+    if (!(x == x)) return x;
+    if (x > 88.8f) return inf_f();
+    if (x < -104.0f) return 0.0f;
+    const float k = floor_f(x * LOG2E + 0.5f);
+    const float r = (x - k * LN2_HI) - k * LN2_LO;
+    float p = 1.98412698e-04f;      // 1/7!
+    p = p * r + 1.38888889e-03f;    // 1/6!
+    p = p * r + 8.33333333e-03f;    // 1/5!
+    p = p * r + 4.16666667e-02f;    // 1/4!
+    p = p * r + 1.66666667e-01f;    // 1/3!
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return ldexp_f(p, (int)k);
+}
+
+MDN_HD float expm1_f(float x) {
+    if (!(x == x)) return x;
+    if (x > 88.0f) return inf_f();
+    if (x < -18.0f) return -1.0f;
+    const float k = floor_f(x * LOG2E + 0.5f);
+    const float r = (x - k * LN2_HI) - k * LN2_LO;
+    float p = 2.48015873e-05f;      // 1/8!
+    p = p * r + 1.98412698e-04f;    // 1/7!
+    p = p * r + 1.38888889e-03f;    // 1/6!
+    p = p * r + 8.33333333e-03f;    // 1/5!
+    p = p * r + 4.16666667e-02f;    // 1/4!
+    p = p * r + 1.66666667e-01f;    // 1/3!
+    p = p * r + 0.5f;               // 1/2!
+    const float em1 = r + (r * r) * p;
+    if (k == 0.0f) return em1;
+    const float scale = ldexp_f(1.0f, (int)k);
+    return scale * em1 + (scale - 1.0f);
+}
+
+MDN_HD float log_f(float x) {
+    if (!(x > 0.0f)) return x == 0.0f ? -inf_f() : nan_f();
+    if (!isfinite_f(x)) return x;
+    int e = 0;
+    if (x < 1.17549435e-38f) { x = x * 8388608.0f; e = -23; }
+    const uint32_t bits = float_bits(x);
+    e += (int)((bits >> 23) & 0xffu) - 127;
+    float m = bits_float((bits & 0x007fffffu) | 0x3f800000u);
+    if (m > 1.41421356f) { m = m * 0.5f; e += 1; }
+    const float s = (m - 1.0f) / (m + 1.0f);
+    const float z = s * s;
+    float p = 9.09090909e-02f;      // 1/11
+    p = p * z + 1.11111111e-01f;    // 1/9
+    p = p * z + 1.42857143e-01f;    // 1/7
+    p = p * z + 2.0e-01f;           // 1/5
+    p = p * z + 3.33333333e-01f;    // 1/3
+    p = p * z + 1.0f;
+    const float lm = (2.0f * s) * p;
+    const float ef = (float)e;
+    return ef * LN2_HI + (ef * LN2_LO + lm);
+}
+
+// Cephes pi/2 split: PIO2_1 + PIO2_2 + PIO2_3 = pi/2; k*PIO2_1 is exact.
+MDN_HD void sincos_f(float x, float* s_out, float* c_out) {
+    const float k = floor_f(x * 0.636619772f + 0.5f);
+    const float r = ((x - k * 1.5703125f) - k * 4.83751297e-04f) - k * 7.54978995e-08f;
+    const float z = r * r;
+    float sp = 2.75573192e-06f;     // 1/9!
+    sp = sp * z - 1.98412698e-04f;  // 1/7!
+    sp = sp * z + 8.33333333e-03f;  // 1/5!
+    sp = sp * z - 1.66666667e-01f;  // 1/3!
+    const float sr = r + (r * z) * sp;
+    float cp = -2.75573192e-07f;    // 1/10!
+    cp = cp * z + 2.48015873e-05f;  // 1/8!
+    cp = cp * z - 1.38888889e-03f;  // 1/6!
+    cp = cp * z + 4.16666667e-02f;  // 1/4!
+    cp = cp * z - 0.5f;
+    const float cr = 1.0f + z * cp;
+    const int q = ((int)k) & 3;
+    float s, c;
+    if (q == 0) { s = sr; c = cr; }
+    else if (q == 1) { s = cr; c = -sr; }
+    else if (q == 2) { s = -sr; c = -cr; }
+    else { s = -cr; c = sr; }
+    *s_out = s;
+    *c_out = c;
+}
+
+MDN_HD float sin_f(float x) { float s, c; sincos_f(x, &s, &c); return s; }
+MDN_HD float cos_f(float x) { float s, c; sincos_f(x, &s, &c); return c; }
+
+MDN_HD float tanh_f(float x) {
+    const float a = fabs_f(x);
+    if (!(a == a)) return x;
+    float t;
+    if (a > 10.0f) t = 1.0f;
+    else {
+        const float e = expm1_f(2.0f * a);
+        t = e / (e + 2.0f);
+    }
+    return x < 0.0f ? -t : t;
+}
+
+MDN_HD float sigmoid_f(float x) { return 1.0f / (1.0f + exp_f(-x)); }
+
+MDN_HD float min_f(float a, float b) { return b < a ? b : a; }
+MDN_HD float max_f(float a, float b) { return a < b ? b : a; }
+MDN_HD float clamp_f(float x, float lo, float hi) { return max_f(lo, min_f(hi, x)); }
+// C fmin/fmax semantics (a NaN operand yields the other operand).
+MDN_HD float fmin_f(float a, float b) { return (b < a || !(a == a)) ? b : a; }
+MDN_HD float fmax_f(float a, float b) { return (a < b || !(a == a)) ? b : a; }
+
+} // namespace mdn
+
+#endif /* MDNAV_MATH_H */

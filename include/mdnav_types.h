@@ -1,0 +1,125 @@
+/*
+ * mdnav_types.h — byte layouts shared by the C ABI, the HIP kernels and the
+ * CPU oracle.  Every struct reproduces the host layout of the reference so a
+ * caller can hand over buffers it already holds:
+ *
+ *   MdnPhysicsState  == RLPhysicsState   physics.hpp:12-18   (68 B)
+ *   MdnPhysicsParams == RLPhysicsParams  physics.hpp:20-38   (352 B)
+ *   MdnRaptorWeights == RaptorWeights    raptor.hpp:11-21    (8336 B)
+ *   MdnObstacle/World== WObstacle/WWorld world.hpp:28-29     (40 B / 676 B)
+ *   MdnSimRun        == SimRun           main.mm:454-460     (184 B)
+ *   MdnSimConfig     == SimConfig        main.mm:461-464     (84 B)
+ *
+ * Plain C so that cgo/ctypes/JNI style bindings can include it directly.
+ */
+#ifndef MDNAV_TYPES_H
+#define MDNAV_TYPES_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Sensor contract of the legacy camera (sensor_profile.hpp:39-50). */
+#define MDN_SENSOR_WIDTH 20u
+#define MDN_SENSOR_HEIGHT 16u
+#define MDN_SENSOR_PIXELS 320u
+#define MDN_SENSOR_FRAMES 8u
+#define MDN_POOLED_FEATURES 80u
+#define MDN_SENSOR_TAN_H 1.0f
+#define MDN_SENSOR_TAN_V 0.75f
+#define MDN_SENSOR_MAX_RANGE 12.0f
+#define MDN_MAX_OBSTACLES 16u
+
+/* Policy shapes (ppo.hpp:26-45 with FIXED_PPO_ACTOR_OBS_DIM=181). */
+#define MDN_CONTEXT_DIM 21u
+#define MDN_ACTOR_OBS_POOLED 181u
+#define MDN_CRITIC_OBS 32u
+#define MDN_HIDDEN 64u
+#define MDN_ACTIONS 4u
+
+typedef struct MdnPhysicsState {
+    float position[3];
+    float orientation_wxyz[4];
+    float linear_velocity[3];
+    float angular_velocity_body[3];
+    float rpm[4];
+} MdnPhysicsState;
+
+typedef struct MdnPhysicsParams {
+    float rotor_positions[12];
+    float rotor_thrust_directions[12];
+    float rotor_torque_directions[12];
+    float rotor_thrust_coefficients[12];
+    float rotor_torque_constants[4];
+    float rotor_time_constants_rising[4];
+    float rotor_time_constants_falling[4];
+    float inertia[9];
+    float inertia_inverse[9];
+    float gravity_world[3];
+    float mass;
+    float action_min;
+    float action_max;
+    float dt;
+    float position_limit;
+    float velocity_limit;
+    float angular_velocity_limit;
+} MdnPhysicsParams;
+
+typedef struct MdnRaptorWeights {
+    float input_weights[16 * 22];
+    float input_bias[16];
+    float gru_input_weights[48 * 16];
+    float gru_hidden_weights[48 * 16];
+    float gru_input_bias[48];
+    float gru_hidden_bias[48];
+    float initial_hidden_state[16];
+    float output_weights[4 * 16];
+    float output_bias[4];
+} MdnRaptorWeights;
+
+typedef struct MdnObstacle {
+    uint32_t kind; /* 0 box, 1 sphere, 2 cylinder, 3 bounded mover */
+    float center[3], size[3], velocity[3];
+} MdnObstacle;
+
+typedef struct MdnWorld {
+    MdnObstacle obstacles[16];
+    uint32_t count, seed, family;
+    float goal[3], wind[3];
+} MdnWorld;
+
+typedef struct MdnSimRun {
+    float hidden[16], motors[4], previous_nav[4], desired_velocity[3], yaw;
+    uint32_t rng, steps;
+    float path, elapsed, peak_speed, min_clearance, initial_distance;
+    uint32_t successes, collisions, timeouts, episodes;
+    float success_time, total_path, total_elapsed, final_progress, reference_position[3];
+} MdnSimRun;
+
+typedef struct MdnSimConfig {
+    uint32_t n, tick, mode, family, substeps, sensor_period, sensor_delay, command_delay, max_steps, seed, eval;
+    float speed, distance, wind, depth_noise, dropout, risk_coef, entropy_coef, learning_rate;
+    uint32_t velocity_contract, geometry_memory;
+} MdnSimConfig;
+
+/* Rollout metrics of cpu_reference.hpp:55-70. */
+typedef struct MdnMetrics {
+    double wall_seconds;
+    uint64_t updates, episodes, successes, collisions, timeouts;
+    double final_progress, total_path, total_elapsed, success_time;
+    float policy_loss, value_loss, entropy_loss, ratio;
+} MdnMetrics;
+
+#ifdef __cplusplus
+}
+static_assert(sizeof(MdnPhysicsState) == 68, "RLPhysicsState layout");
+static_assert(sizeof(MdnPhysicsParams) == 352, "RLPhysicsParams layout");
+static_assert(sizeof(MdnRaptorWeights) == 2084 * 4, "RaptorWeights layout");
+static_assert(sizeof(MdnWorld) == 676, "WWorld layout");
+static_assert(sizeof(MdnSimRun) == 184, "SimRun layout");
+static_assert(sizeof(MdnSimConfig) == 84, "SimConfig layout");
+#endif
+
+#endif /* MDNAV_TYPES_H */

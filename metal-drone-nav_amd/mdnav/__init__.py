@@ -1,0 +1,11 @@
+"""mdnav — MI355X-native drop-in for the metal-drone-nav RL hot path.
+
+Host-side Python face of the C ABI in include/mdnav.h: ``Sim`` and
+``PPOTrainer`` mirror the reference's host classes (main.mm:516-603,
+1110-1474) and ``Trainer`` mirrors cpu_reference::Trainer
+(cpu_reference.hpp:112-615), all running on the HIP library
+``lib/libmdnav.so``.  ``abi`` holds the struct layouts.
+"""
+from . import abi  # noqa: F401
+
+__all__ = ["abi"]

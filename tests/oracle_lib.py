@@ -1,0 +1,230 @@
+"""ctypes bindings of the CPU oracle (oracle/_build/liboracle.so) and of the
+reference's own header code compiled into oracle/_ref/libmdnref.so.
+
+Test infrastructure: only tests, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg load these libraries, and only as the checker.
+"""
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(ROOT, "metal-drone-nav_amd"))
+from mdnav import abi  # noqa: E402
+
+ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libmdnref.so")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+P = ctypes.c_void_p
+U32, U64, F32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
+
+
+def ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _sig(lib, name, res, *args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+    return f
+
+
+_oracle = None
+_ref = None
+
+
+def oracle():
+    global _oracle
+    if _oracle is None:
+        lib = ctypes.CDLL(ORACLE_SO)
+        _sig(lib, "orc_trainer_create", P, P, U32, P, P, U32, U32)
+        _sig(lib, "orc_trainer_destroy", None, P)
+        _sig(lib, "orc_trainer_collect", None, P, U32)
+        _sig(lib, "orc_trainer_gae", None, P)
+        _sig(lib, "orc_trainer_normalize", None, P)
+        _sig(lib, "orc_trainer_update", None, P, U32)
+        _sig(lib, "orc_trainer_iteration", None, P, U32)
+        _sig(lib, "orc_trainer_set_config", None, P, P)
+        _sig(lib, "orc_trainer_minibatch_grads", None, P, U32, U32, P, P, P, P, P, P)
+        _sig(lib, "orc_trainer_optimizer_step", U64, P)
+        _sig(lib, "orc_trainer_metric_mean", None, P, P)
+        _sig(lib, "orc_trainer_buffer", P, P, U32, ctypes.POINTER(U64))
+        _sig(lib, "orc_physics_step_batch", None, P, P, P, P, P, U64)
+        _sig(lib, "orc_raptor_sequence", None, P, P, U32, P, P)
+        _sig(lib, "orc_generate_world", None, P, U32, U32, F32)
+        _sig(lib, "orc_ray_world_batch", None, P, P, P, U32, P, U64)
+        _sig(lib, "orc_clearance_batch", None, P, P, P, P, U64)
+        _sig(lib, "orc_ray_box", F32, P, P, P, P)
+        _sig(lib, "orc_ray_sphere", F32, P, P, P, F32)
+        _sig(lib, "orc_ray_cylinder", F32, P, P, P, F32, F32)
+        _sig(lib, "orc_camera_rays", None, P)
+        _sig(lib, "orc_math_batch", None, U32, P, P, U64)
+        _sig(lib, "orc_compute_gae", None, U32, U32, P, P, P, P, P, F32, F32, P, P)
+        _sig(lib, "orc_normalize_advantages", None, P, U64, F32)
+        _sig(lib, "orc_squared_norm", F32, P, U64)
+        _sig(lib, "orc_sample_loss_and_grad", None, P, P, P, F32, F32, F32, F32, F32, F32, F32, F32,
+             P, P, P, P)
+        _sig(lib, "orc_actor_forward_batch", None, P, P, U32, U32, U64, P, P)
+        _sig(lib, "orc_critic_forward_batch", None, P, P, U64, P, P)
+        _sig(lib, "orc_init_policy", None, P, P)
+        _sig(lib, "orc_minibatch_schedule", None, U32, U32, U32, U32, P)
+        _sig(lib, "orc_crazyflie_params", None, P)
+        _sig(lib, "orc_default_config", None, P)
+        _sig(lib, "orc_num_threads", ctypes.c_int)
+        _oracle = lib
+    return _oracle
+
+
+def ref_available():
+    return os.path.exists(REF_SO)
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        lib = ctypes.CDLL(REF_SO)
+        _sig(lib, "ref_generate_world", None, P, U32, U32, F32)
+        _sig(lib, "ref_ray_world_batch", None, P, P, P, U32, P, U64)
+        _sig(lib, "ref_clearance_batch", None, P, P, P, P, U64)
+        _sig(lib, "ref_camera_rays", None, P)
+        _sig(lib, "ref_physics_step_batch", None, P, P, P, P, P, U64)
+        _sig(lib, "ref_crazyflie_params", None, P)
+        _sig(lib, "ref_raptor_sequence", None, P, P, U32, P, P)
+        _sig(lib, "ref_raptor_forward", None, P, P, P, P)
+        _sig(lib, "ref_raptor_pack_observation", None, P, P, P, P, P, P, P, P, P)
+        _sig(lib, "ref_quaternion_matrix", None, P, P)
+        _sig(lib, "ref_ppo_self_tests", ctypes.c_int, F32)
+        _sig(lib, "ref_actor_param_count", U32)
+        _sig(lib, "ref_critic_param_count", U32)
+        _sig(lib, "ref_actor_forward", None, P, P, P, P)
+        _sig(lib, "ref_critic_forward", F32, P, P, P)
+        _sig(lib, "ref_gaussian_log_prob", F32, P, P, P)
+        _sig(lib, "ref_compute_gae", None, U32, U32, P, P, P, P, P, F32, F32, P, P)
+        _sig(lib, "ref_normalize_advantages", None, P, U64, F32)
+        _sig(lib, "ref_sample_loss_and_grad", None, P, P, P, F32, F32, F32, F32, F32, F32, F32, F32, F32,
+             P, P, P, P)
+        _sig(lib, "ref_actor_critic_grads", None, P, P, P, P, P, P, P, U32, P, P)
+        _sig(lib, "ref_adam_update", None, P, P, P, P, U64, U64, F32, F32, F32, F32, F32)
+        _sig(lib, "ref_urand", F32, ctypes.POINTER(U32))
+        _ref = lib
+    return _ref
+
+
+# ---------------------------------------------------------------- fixtures
+def physics_fixture():
+    """assets/physics.bin (reference.cpp:83-155): params + 512 transitions."""
+    data = open(os.path.join(GOLDEN, "physics.bin"), "rb").read()
+    assert data[:8] == b"RLPHYS1\x00"
+    version, cases, horizon = np.frombuffer(data[8:20], np.uint32)
+    assert version == 1
+    params = np.frombuffer(data[20:372], abi.PHYSICS_PARAMS)[0].copy()
+    rec = np.dtype([("state", abi.PHYSICS_STATE), ("action", np.float32, 4),
+                    ("wind", np.float32, 3), ("next", abi.PHYSICS_STATE)])
+    n = int(cases) * int(horizon)
+    recs = np.frombuffer(data[372:372 + n * rec.itemsize], rec).copy()
+    assert 372 + n * rec.itemsize == len(data)
+    return params, recs, int(cases), int(horizon)
+
+
+def raptor_fixture():
+    """assets/raptor.bin (export_raptor.py:86-105): weights + official sequence."""
+    path = os.path.join(GOLDEN, "raptor.bin")
+    weights = abi.load_raptor(path)
+    data = open(path, "rb").read()
+    off = 16 + 8336
+    assert data[off:off + 8] == b"RPFIX1\x00\x00"
+    steps, obs_dim, act_dim = np.frombuffer(data[off + 8:off + 20], np.uint32)
+    off += 20
+    obs = np.frombuffer(data[off:off + 4 * steps * obs_dim], np.float32).reshape(steps, obs_dim).copy()
+    off += 4 * steps * obs_dim
+    actions = np.frombuffer(data[off:off + 4 * steps * act_dim], np.float32).reshape(steps, act_dim).copy()
+    return weights, obs, actions
+
+
+def crazyflie():
+    p = np.zeros((), abi.PHYSICS_PARAMS)
+    oracle().orc_crazyflie_params(ptr(p))
+    return p
+
+
+class OracleTrainer:
+    """Python face of the oracle's Trainer (cpu_reference::Trainer shape)."""
+
+    def __init__(self, cfg, horizon, raptor, physics=None, epochs=2, minibatch=256):
+        self.lib = oracle()
+        self.cfg = np.array(cfg, abi.SIM_CONFIG)
+        self.raptor = np.array(raptor, abi.RAPTOR_WEIGHTS)
+        self.physics = np.array(crazyflie() if physics is None else physics, abi.PHYSICS_PARAMS)
+        self.h = self.lib.orc_trainer_create(ptr(self.cfg), horizon, ptr(self.raptor), ptr(self.physics),
+                                             epochs, minibatch)
+        self.horizon = horizon
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.lib.orc_trainer_destroy(self.h)
+            self.h = None
+
+    def buffer(self, name):
+        bid, dtype = abi.BUFFERS[name]
+        nbytes = U64(0)
+        p = self.lib.orc_trainer_buffer(self.h, bid, ctypes.byref(nbytes))
+        count = nbytes.value // np.dtype(dtype).itemsize
+        if count == 0:
+            return np.zeros(0, dtype)
+        arr = np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint8)), (nbytes.value,))
+        return arr.view(dtype)
+
+    def get(self, name):
+        return self.buffer(name).copy()
+
+    def set(self, name, values):
+        b = self.buffer(name)
+        b[...] = np.asarray(values, b.dtype).reshape(b.shape)
+
+    def collect(self, count=0):
+        self.lib.orc_trainer_collect(self.h, count)
+
+    def gae(self):
+        self.lib.orc_trainer_gae(self.h)
+
+    def normalize(self):
+        self.lib.orc_trainer_normalize(self.h)
+
+    def update(self, rollout_index):
+        self.lib.orc_trainer_update(self.h, rollout_index)
+
+    def iteration(self, rollout_index):
+        self.lib.orc_trainer_iteration(self.h, rollout_index)
+
+    def minibatch_grads(self, begin, b):
+        sh = abi.policy_shape()
+        ag = np.zeros(sh["actor_count"], np.float32)
+        cg = np.zeros(sh["critic_count"], np.float32)
+        row = np.zeros(4, np.float32)
+        dm = np.zeros((b, 4), np.float32)
+        dls = np.zeros((b, 4), np.float32)
+        dv = np.zeros(b, np.float32)
+        self.lib.orc_trainer_minibatch_grads(self.h, begin, b, ptr(ag), ptr(cg), ptr(row), ptr(dm), ptr(dls),
+                                             ptr(dv))
+        return ag, cg, row, dm, dls, dv
+
+    def metric_mean(self):
+        out = np.zeros(4, np.float32)
+        self.lib.orc_trainer_metric_mean(self.h, ptr(out))
+        return out
+
+    @property
+    def optimizer_step(self):
+        return int(self.lib.orc_trainer_optimizer_step(self.h))
+
+
+def math_batch(fn, x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros_like(x)
+    oracle().orc_math_batch({"exp": 0, "log": 1, "sin": 2, "cos": 3, "tanh": 4, "expm1": 5,
+                             "sigmoid": 6}[fn], ptr(x), ptr(y), x.size)
+    return y

@@ -1,0 +1,64 @@
+"""The shared elementary functions (include/mdnav_math.h) against float64
+numpy: these pin the numerics that both the oracle and the HIP path compile."""
+import numpy as np
+import pytest
+
+from oracle_lib import math_batch
+
+
+def ulps(got, want64):
+    want = want64.astype(np.float32)
+    spacing = np.spacing(np.abs(want).astype(np.float32))
+    spacing = np.where(spacing == 0, np.float32(1e-45), spacing)
+    return np.abs(got.astype(np.float64) - want64) / spacing.astype(np.float64)
+
+
+def test_exp_expm1_accuracy():
+    x = np.linspace(-30, 30, 200001, dtype=np.float32)
+    assert ulps(math_batch("exp", x), np.exp(x.astype(np.float64))).max() <= 2.0
+    x = np.linspace(-10, 20, 200001, dtype=np.float32)
+    assert ulps(math_batch("expm1", x), np.expm1(x.astype(np.float64))).max() <= 3.0
+    assert math_batch("exp", np.array([0.0], np.float32))[0] == 1.0
+    assert math_batch("exp", np.array([100.0], np.float32))[0] == np.inf
+    assert math_batch("exp", np.array([-200.0], np.float32))[0] == 0.0
+
+
+def test_log_accuracy():
+    x = np.concatenate([np.geomspace(1e-7, 1e4, 200001), np.linspace(0.5, 2.0, 10001)]).astype(np.float32)
+    y = math_batch("log", x)
+    ref = np.log(x.astype(np.float64))
+    err = np.abs(y - ref)
+    # relative-to-ulp away from log(1)=0, absolute near it
+    assert (np.minimum(ulps(y, ref), err / 1.2e-7)).max() <= 3.0
+    assert math_batch("log", np.array([1.0], np.float32))[0] == 0.0
+    assert math_batch("log", np.array([0.0], np.float32))[0] == -np.inf
+
+
+def test_sin_cos_accuracy():
+    x = np.linspace(-12, 12, 400001, dtype=np.float32)
+    for fn, ref in (("sin", np.sin), ("cos", np.cos)):
+        y = math_batch(fn, x)
+        assert np.abs(y - ref(x.astype(np.float64))).max() < 2.5e-7, fn
+    assert math_batch("sin", np.array([0.0], np.float32))[0] == 0.0
+    assert math_batch("cos", np.array([0.0], np.float32))[0] == 1.0
+    # the Box-Muller argument range [0, 2pi) stays within a couple of ulp
+    x = np.linspace(0, 6.2831853, 100001, dtype=np.float32)
+    assert np.abs(math_batch("cos", x) - np.cos(x.astype(np.float64))).max() < 1.8e-7
+
+
+def test_tanh_sigmoid_accuracy():
+    x = np.linspace(-15, 15, 300001, dtype=np.float32)
+    y = math_batch("tanh", x)
+    ref = np.tanh(x.astype(np.float64))
+    assert (np.minimum(ulps(y, ref), np.abs(y - ref) / 6e-8)).max() <= 4.0
+    assert np.all(np.abs(y) <= 1.0)
+    assert np.array_equal(y[::-1], -y)  # odd symmetry holds exactly
+    s = math_batch("sigmoid", x)
+    assert np.abs(s - 1 / (1 + np.exp(-x.astype(np.float64)))).max() < 2e-7
+
+
+@pytest.mark.parametrize("fn", ["exp", "log", "tanh"])
+def test_monotone(fn):
+    x = np.linspace(0.01 if fn == "log" else -8, 8, 100001, dtype=np.float32)
+    y = math_batch(fn, x)
+    assert np.all(np.diff(y) >= 0)

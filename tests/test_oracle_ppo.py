@@ -1,0 +1,338 @@
+"""PPO operators of the oracle: closed forms, finite differences, and the
+reference's own operators from ppo.hpp compiled into oracle/_ref."""
+import numpy as np
+import pytest
+
+from oracle_lib import OracleTrainer, oracle, ptr, raptor_fixture, ref, ref_available
+from mdnav import abi
+
+needs_ref = pytest.mark.skipif(not ref_available(), reason="oracle/_ref not built")
+F = np.float32
+LOG2PI = 1.8378770664093453
+
+
+def loss_and_grad(action, mean, log_std, old_logp, value, adv, target, batch=1.0, clip=0.2, vc=0.7, ec=0.03):
+    dm = np.zeros(4, F)
+    dls = np.zeros(4, F)
+    dv = np.zeros(1, F)
+    losses = np.zeros(4, F)
+    oracle().orc_sample_loss_and_grad(ptr(np.asarray(action, F)), ptr(np.asarray(mean, F)),
+                                      ptr(np.asarray(log_std, F)), F(old_logp), F(value), F(adv), F(target),
+                                      F(batch), F(clip), F(vc), F(ec), ptr(dm), ptr(dls), ptr(dv), ptr(losses))
+    return losses, dm, dls, float(dv[0])
+
+
+def objective(*args, **kw):
+    losses = loss_and_grad(*args, **kw)[0]
+    return float(losses[0]) + float(losses[1]) + float(losses[2])
+
+
+@needs_ref
+def test_reference_self_tests_pass():
+    assert ref().ref_ppo_self_tests(F(2e-3)) == 1
+
+
+def test_loss_grad_finite_differences_all_branches():
+    """run_cpu_self_tests (ppo.hpp:204-267) restated on the oracle's own loss
+    outputs: all four clip branches, mean and log-std derivatives, value."""
+    action = np.array([0.4, 0, 0, 0], F)
+    mean = np.array([0.1, 0, 0, 0], F)
+    log_std = np.zeros(4, F)
+    base = -0.5 * (0.3 ** 2 + LOG2PI) - 3 * 0.5 * LOG2PI
+    h = 1e-3
+    for old, adv in [(base - np.log(1.1), 1.0), (base - np.log(0.9), -1.0), (base - np.log(1.3), 1.0),
+                     (base - np.log(0.7), -1.0)]:
+        _, dm, dls, _ = loss_and_grad(action, mean, log_std, old, 0.25, adv, -0.3)
+        for k in (0, 2):
+            mp, mm = mean.copy(), mean.copy()
+            mp[k] += h
+            mm[k] -= h
+            num = (objective(action, mp, log_std, old, 0.25, adv, -0.3)
+                   - objective(action, mm, log_std, old, 0.25, adv, -0.3)) / (2 * h)
+            assert abs(num - dm[k]) < 2e-3, (adv, k, num, dm[k])
+            lp, lm = log_std.copy(), log_std.copy()
+            lp[k] += h
+            lm[k] -= h
+            num = (objective(action, mean, lp, old, 0.25, adv, -0.3)
+                   - objective(action, mean, lm, old, 0.25, adv, -0.3)) / (2 * h)
+            assert abs(num - dls[k]) < 2e-3, (adv, k, num, dls[k])
+    _, _, _, dv = loss_and_grad(action, mean, log_std, base, 0.25, 0.0, -0.3)
+    assert abs(dv - 0.7 * (0.25 + 0.3)) < 1e-6
+    # a clipped sample carries no policy gradient, only the entropy term
+    _, dm, dls, _ = loss_and_grad(action, mean, log_std, base - np.log(1.3), 0.25, 1.0, -0.3)
+    assert np.all(dm == 0) and np.allclose(dls, -0.03)
+
+
+@needs_ref
+def test_loss_grad_against_reference():
+    rng = np.random.default_rng(1)
+    lib = ref()
+    for _ in range(200):
+        a, m = rng.normal(0, 0.5, 4).astype(F), rng.normal(0, 0.5, 4).astype(F)
+        ls = rng.uniform(-2, 0.5, 4).astype(F)
+        old, v, adv, tgt = (F(x) for x in rng.normal(0, 1, 4))
+        ours = loss_and_grad(a, m, ls, old, v, adv, tgt, 256.0, 0.2, 0.5, 0.005)
+        dm, dls, dv, losses = np.zeros(4, F), np.zeros(4, F), np.zeros(1, F), np.zeros(4, F)
+        lib.ref_sample_loss_and_grad(ptr(a), ptr(m), ptr(ls), old, v, v, adv, tgt, F(256), F(0.2), F(0.5),
+                                     F(0.005), ptr(dm), ptr(dls), ptr(dv), ptr(losses))
+        assert np.allclose(ours[0], losses, rtol=1e-5, atol=1e-7)
+        assert np.allclose(ours[1], dm, rtol=1e-5, atol=1e-8)
+        assert np.allclose(ours[2], dls, rtol=1e-5, atol=1e-8)
+        assert abs(ours[3] - dv[0]) < 1e-7
+
+
+def gae(fn, T, N, r, v, nv, te, tr):
+    adv = np.zeros(T * N, F)
+    ret = np.zeros(T * N, F)
+    args = [np.ascontiguousarray(x, F) for x in (r, v, nv)] + [np.ascontiguousarray(x, np.uint8) for x in (te, tr)]
+    fn(T, N, *[ptr(x) for x in args], F(0.99), F(0.95), ptr(adv), ptr(ret))
+    return adv, ret
+
+
+def test_gae_hand_case():
+    """main.mm:286-297: T=3, N=2 with a terminal (t=1, env 0) and a
+    truncation (t=1, env 1), solved on paper."""
+    adv, ret = gae(oracle().orc_compute_gae, 3, 2, [1, 2, 3, 4, 5, 6], [.1, .2, .3, .4, .5, .6],
+                   [.2, .3, .4, .5, .6, .7], [0, 0, 1, 0, 0, 0], [0, 0, 0, 1, 0, 0])
+    gl = 0.99 * 0.95
+    e0 = [1 + .99 * .2 - .1 + gl * 2.7, None, 3 - .3, None, 5 + .99 * .6 - .5, None]
+    e1 = [None, 2 + .99 * .3 - .2 + gl * (4 + .99 * .5 - .4), None, 4 + .99 * .5 - .4, None, 6 + .99 * .7 - .6]
+    want = np.array([x if x is not None else y for x, y in zip(e0, e1)])
+    assert np.abs(adv - want).max() < 2e-5
+    assert np.abs(ret - (want + np.array([.1, .2, .3, .4, .5, .6]))).max() < 2e-5
+    if ref_available():
+        radv, rret = gae(ref().ref_compute_gae, 3, 2, [1, 2, 3, 4, 5, 6], [.1, .2, .3, .4, .5, .6],
+                         [.2, .3, .4, .5, .6, .7], [0, 0, 1, 0, 0, 0], [0, 0, 0, 1, 0, 0])
+        assert adv.tobytes() == radv.tobytes() and ret.tobytes() == rret.tobytes()
+
+
+def test_gae_constant_reward_closed_form():
+    T, N = 64, 3
+    adv, _ = gae(oracle().orc_compute_gae, T, N, np.ones(T * N), np.zeros(T * N), np.zeros(T * N),
+                 np.zeros(T * N), np.zeros(T * N))
+    gl = 0.99 * 0.95
+    want = np.repeat([(1 - gl ** (T - t)) / (1 - gl) for t in range(T)], N)
+    assert np.abs(adv - want).max() < 1e-4
+
+
+def test_normalize_closed_form():
+    x = np.array([-40, -2, -1, 0, 1, 2, 10, 40], F)
+    y = x.copy()
+    oracle().orc_normalize_advantages(ptr(y), len(y), F(1e-8))
+    x64 = x.astype(np.float64)
+    want = (x64 - x64.mean()) / np.sqrt(x64.var() + 1e-8)
+    assert np.abs(y - want).max() < 2e-6
+    big = np.random.default_rng(3).normal(3, 7, 100_003).astype(F)
+    y = big.copy()
+    oracle().orc_normalize_advantages(ptr(y), len(y), F(1e-8))
+    assert abs(y.astype(np.float64).mean()) < 1e-6 and abs(y.astype(np.float64).std() - 1) < 1e-5
+    if ref_available():
+        z = big.copy()
+        ref().ref_normalize_advantages(ptr(z), len(z), F(1e-8))
+        assert np.abs(y - z).max() < 1e-6
+
+
+def test_squared_norm_order_and_value():
+    g = np.random.default_rng(4).normal(0, 1e-2, 12_105).astype(F)
+    got = oracle().orc_squared_norm(ptr(g), len(g))
+    assert abs(got - float(np.sum(g.astype(np.float64) ** 2))) / got < 1e-6
+
+
+@needs_ref
+def test_forward_against_reference():
+    rng = np.random.default_rng(7)
+    actor = np.zeros(12_104 + 0, F)
+    critic = np.zeros(2177, F)
+    oracle().orc_init_policy(ptr(actor), ptr(critic))
+    actor[:] += rng.normal(0, 0.02, actor.size).astype(F)
+    critic[:] += rng.normal(0, 0.05, critic.size).astype(F)
+    assert ref().ref_actor_param_count() == 181 * 64 + 64 + 256 + 4 + 4
+    actor = actor[:ref().ref_actor_param_count()].copy()
+    obs = rng.uniform(-1, 1, (8, 181)).astype(F)
+    cobs = rng.uniform(-1, 1, (8, 32)).astype(F)
+    h = np.zeros((8, 64), F)
+    m = np.zeros((8, 4), F)
+    oracle().orc_actor_forward_batch(ptr(actor), ptr(obs), 181, 64, 8, ptr(h), ptr(m))
+    ch = np.zeros((8, 64), F)
+    cv = np.zeros(8, F)
+    oracle().orc_critic_forward_batch(ptr(critic), ptr(cobs), 8, ptr(ch), ptr(cv))
+    for n in range(8):
+        rh, rm = np.zeros(64, F), np.zeros(4, F)
+        ref().ref_actor_forward(ptr(actor), ptr(obs[n]), ptr(rh), ptr(rm))
+        assert np.abs(rh - h[n]).max() < 2e-6 and np.abs(rm - m[n]).max() < 2e-6
+        v = ref().ref_critic_forward(ptr(critic), ptr(cobs[n]), ptr(rh))
+        assert abs(v - cv[n]) < 2e-6
+
+
+@pytest.fixture(scope="module")
+def filled_trainer():
+    weights = raptor_fixture()[0]
+    cfg = abi.default_config(n=16, family=1, speed=1.0, distance=3.0)
+    t = OracleTrainer(cfg, 16, weights, epochs=2, minibatch=256)
+    t.collect()
+    t.gae()
+    t.normalize()
+    return t
+
+
+@needs_ref
+def test_minibatch_grads_against_reference_backprop(filled_trainer):
+    """The oracle's batched gradients against the reference's per-sample
+    backprop + reduction (ppo.hpp:269-308), fed the same row derivatives."""
+    t = filled_trainer
+    ag, cg, row, dm, dls, dv = t.minibatch_grads(0, 256)
+    ra = np.zeros_like(ag)
+    rc = np.zeros_like(cg)
+    actor, critic = t.get("actor"), t.get("critic")
+    obs = t.get("obs")[:256 * 181].copy()
+    co = t.get("critic_obs")[:256 * 32].copy()
+    ref().ref_actor_critic_grads(ptr(actor), ptr(critic), ptr(obs), ptr(co), ptr(dm), ptr(dls), ptr(dv), 256,
+                                 ptr(ra), ptr(rc))
+    scale = max(np.abs(ra).max(), 1e-6)
+    assert np.abs(ag - ra).max() < 3e-5 * max(1.0, scale), np.abs(ag - ra).max()
+    assert np.abs(cg - rc).max() < 3e-5 * max(1.0, np.abs(rc).max())
+    assert np.abs(ag).max() > 0 and np.abs(cg).max() > 0
+
+
+def test_minibatch_grads_finite_differences(filled_trainer):
+    """Gradient of the minibatch objective sum(policy+value+entropy) through
+    the whole actor and critic MLPs, by central differences on the oracle's
+    own loss (old log-probs, advantages and returns held fixed)."""
+    t = filled_trainer
+    sh = abi.policy_shape()
+    actor0, critic0 = t.get("actor"), t.get("critic")
+    ag, cg, row0 = t.minibatch_grads(0, 256)[:3]
+    rng = np.random.default_rng(11)
+
+    def J():
+        r = t.minibatch_grads(0, 256)[2]
+        return float(r[0]) + float(r[1]) + float(r[2])
+
+    picks = [("actor", i) for i in rng.integers(0, sh["actor_b1"], 6)]
+    picks += [("actor", sh["actor_b1"] + 3), ("actor", sh["actor_w2"] + 70), ("actor", sh["actor_b2"] + 1),
+              ("actor", sh["actor_log_std"] + 2)]
+    picks += [("critic", i) for i in rng.integers(0, sh["critic_b1"], 4)]
+    picks += [("critic", sh["critic_b1"] + 5), ("critic", sh["critic_w2"] + 9), ("critic", sh["critic_b2"])]
+    for net, i in picks:
+        base = (actor0 if net == "actor" else critic0).copy()
+        grad = (ag if net == "actor" else cg)[i]
+        h = 2e-3
+        base[i] += h
+        t.set(net, base)
+        jp = J()
+        base[i] -= 2 * h
+        t.set(net, base)
+        jm = J()
+        base[i] += h
+        t.set(net, base)
+        num = (jp - jm) / (2 * h)
+        assert abs(num - grad) <= 2e-2 * abs(grad) + 2e-4, (net, i, num, grad)
+    t.set("actor", actor0)
+    t.set("critic", critic0)
+
+
+@needs_ref
+def test_adam_step_against_reference():
+    """One rollout update of a single minibatch equals norm-clip then the
+    reference's adam_update (ppo.hpp:310-324) on the clipped gradient."""
+    weights = raptor_fixture()[0]
+    cfg = abi.default_config(n=16, family=1, speed=1.0, distance=3.0)
+    t = OracleTrainer(cfg, 16, weights, epochs=1, minibatch=256)
+    t.collect()
+    t.gae()
+    t.normalize()
+    ag, cg = t.minibatch_grads(0, 256)[:2]
+    a0, c0 = t.get("actor"), t.get("critic")
+    t.update(0)
+    assert t.optimizer_step == 1
+    for g, p0, name in [(ag, a0, "actor"), (cg, c0, "critic")]:
+        norm = np.sqrt(np.float32(oracle().orc_squared_norm(ptr(g), len(g))) + F(1e-20))
+        scale = min(F(1), F(0.5) / F(norm))
+        gs = (g * F(scale)).astype(F)
+        p = p0.copy()
+        m = np.zeros_like(p)
+        v = np.zeros_like(p)
+        ref().ref_adam_update(ptr(p), ptr(gs), ptr(m), ptr(v), len(p), 1, F(3e-4), F(.9), F(.999), F(1e-8), F(0))
+        if name == "actor":
+            ls = slice(abi.policy_shape()["actor_log_std"], None)
+            p[ls] = np.clip(p[ls], -2, 0.5)
+        got = t.get(name)
+        assert np.abs(got - p).max() < 1e-7, name
+        assert np.abs(t.get(name + "_m") - m).max() < 1e-9
+
+
+def mt19937(seed):
+    """std::mt19937 (the standard fixes its output sequence)."""
+    mt = [0] * 624
+    mt[0] = seed & 0xffffffff
+    for i in range(1, 624):
+        mt[i] = (1812433253 * (mt[i - 1] ^ (mt[i - 1] >> 30)) + i) & 0xffffffff
+    idx = 624
+    while True:
+        if idx >= 624:
+            for i in range(624):
+                y = (mt[i] & 0x80000000) | (mt[(i + 1) % 624] & 0x7fffffff)
+                mt[i] = mt[(i + 397) % 624] ^ (y >> 1) ^ (0x9908b0df if y & 1 else 0)
+            idx = 0
+        y = mt[idx]
+        idx += 1
+        y ^= y >> 11
+        y ^= (y << 7) & 0x9d2c5680
+        y ^= (y << 15) & 0xefc60000
+        y ^= y >> 18
+        yield y
+
+
+def test_minibatch_schedule():
+    g = mt19937(5489)
+    for _ in range(9999):
+        next(g)
+    assert next(g) == 4123659995  # C++ standard [rand.predef]
+    rows, mb, epochs, rollout = 4096, 256, 3, 5
+    got = np.zeros(16 * epochs, np.uint32)
+    oracle().orc_minibatch_schedule(rows, mb, epochs, rollout, ptr(got))
+    starts = list(range(0, rows, mb))
+    gen = mt19937((0x9e3779b9 + rollout * 0x85ebca6b) & 0xffffffff)
+
+    def fy(v):
+        for i in range(len(v), 1, -1):
+            j = (next(gen) * i) >> 32
+            v[i - 1], v[j] = v[j], v[i - 1]
+    fy(starts)
+    e0 = list(starts)
+    fy(starts)
+    want = e0 + starts + starts  # reshuffled only before epoch 1
+    assert got.tolist() == want
+    for e in range(epochs):
+        assert sorted(got[16 * e:16 * (e + 1)].tolist()) == list(range(0, rows, mb))
+
+
+@needs_ref
+def test_policy_initialisation_stream():
+    """initialize_policy (cpu_reference.hpp:89-103): seed-1789 stream drawn
+    with the reference's own wurand, transformed with float64 libm."""
+    import ctypes
+    actor = np.zeros(abi.policy_shape()["actor_count"], F)
+    critic = np.zeros(abi.policy_shape()["critic_count"], F)
+    oracle().orc_init_policy(ptr(actor), ptr(critic))
+    seed = ctypes.c_uint32(1789)
+    lib = ref()
+
+    def normal():
+        u = max(lib.ref_urand(ctypes.byref(seed)), 1e-7)
+        v = lib.ref_urand(ctypes.byref(seed))
+        return np.sqrt(-2 * np.log(np.float64(F(u)))) * np.cos(np.float64(F(6.2831853)) * np.float64(F(v)))
+    sh = abi.policy_shape()
+    want_a = np.zeros_like(actor, np.float64)
+    for i in range(sh["actor_b1"]):
+        want_a[i] = normal() * 0.04
+    for i in range(sh["actor_w2"], sh["actor_b2"]):
+        want_a[i] = normal() * 0.01
+    want_a[sh["actor_log_std"]:] = -1
+    want_c = np.zeros_like(critic, np.float64)
+    for i in range(sh["critic_b1"]):
+        want_c[i] = normal() * 0.15
+    for i in range(sh["critic_w2"], sh["critic_b2"]):
+        want_c[i] = normal() * 0.1
+    assert np.abs(actor - want_a).max() < 1e-6
+    assert np.abs(critic - want_c).max() < 2e-6
