@@ -1,0 +1,147 @@
+/*
+ * mdnav.h — C ABI of the MI355X hot path (libmdnav.so).
+ *
+ * Drop-in for the reference's GPU host classes: the Sim and PPOTrainer of
+ * main.mm (Metal) and, through include/mdnav.hpp, the Trainer interface of
+ * cpu_reference.hpp.  Plain pointers and sizes only; every function returns
+ * 0 on success and a negative MDN_E_* code otherwise, with the message in
+ * mdn_last_error() (the reference throws std::runtime_error through
+ * require(), main.mm:27; mdnav.hpp turns codes back into exceptions).
+ * Handles own their device memory; host arrays are caller-owned copies in the
+ * reference's host layouts (AoS structs, time-major [T][N] rollout rows).
+ * One host thread per handle; all work is ordered on the handle's stream.
+ */
+#ifndef MDNAV_H
+#define MDNAV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mdnav_types.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MDN_OK 0
+#define MDN_E_ARG -1     /* invalid argument or size */
+#define MDN_E_HIP -2     /* HIP runtime error (message names the call) */
+#define MDN_E_STATE -3   /* call not valid in the handle's state */
+
+typedef struct MdnSim MdnSim;
+typedef struct MdnPPO MdnPPO;
+
+/* Buffer ids for mdn_sim_download / mdn_sim_upload.  Sizes follow the
+ * reference's shared buffers of Sim (main.mm:519, 540-555). */
+enum MdnBuffer {
+    MDN_BUF_STATES = 0,      /* MdnPhysicsState[N]            states       */
+    MDN_BUF_RUNS = 1,        /* MdnSimRun[N]                  runs         */
+    MDN_BUF_WORLDS = 2,      /* MdnWorld[N]                   worlds       */
+    MDN_BUF_SENSORS = 3,     /* float[N][8][320]              sensors      */
+    MDN_BUF_POSES = 4,       /* float[N][8][12]               poses        */
+    MDN_BUF_COMMANDS = 5,    /* float[N][8][4]                commands     */
+    MDN_BUF_ACTOR = 6,       /* float[actor_param_count]      actor        */
+    MDN_BUF_CRITIC = 7,      /* float[critic_param_count]     critic       */
+    MDN_BUF_OBS = 8,         /* float[T][N][181]              obs          */
+    MDN_BUF_CRITIC_OBS = 9,  /* float[T][N][32]               co           */
+    MDN_BUF_ACTIONS = 10,    /* float[T][N][4]                actions      */
+    MDN_BUF_LOGP = 11,       /* float[T][N]                   logp         */
+    MDN_BUF_VALUES = 12,
+    MDN_BUF_REWARDS = 13,
+    MDN_BUF_NEXT_VALUES = 14,
+    MDN_BUF_TERMINATED = 15, /* uint8[T][N] */
+    MDN_BUF_TRUNCATED = 16,  /* uint8[T][N] */
+    MDN_BUF_ADVANTAGES = 17,
+    MDN_BUF_RETURNS = 18,
+    MDN_BUF_ACTOR_M = 19,    /* PPO Adam moments (needs a PPO handle) */
+    MDN_BUF_ACTOR_V = 20,
+    MDN_BUF_CRITIC_M = 21,
+    MDN_BUF_CRITIC_V = 22,
+    MDN_BUF_METRIC_ROWS = 23 /* float[updates][4] of the last rollout_update */
+};
+
+/* Kernel ids for mdn_sim_kernel_time. */
+enum MdnKernel {
+    MDN_K_ROLLOUT = 0,   /* fused env step + rollout forward, all ticks of one collect */
+    MDN_K_GAE = 1,       /* ppo_gae */
+    MDN_K_NORMALIZE = 2, /* ppo_normalize_advantages (all passes) */
+    MDN_K_ROWS = 3,      /* minibatch forward + loss/grad + hidden deltas */
+    MDN_K_GRADS = 4,     /* gradient chunk partials + reduction */
+    MDN_K_ADAM = 5,      /* norm clip + Adam + log-std clamp */
+    MDN_K_COUNT = 6
+};
+
+const char* mdn_last_error(void);
+const char* mdn_version(void);
+
+/* Sim(Metal&, SimConfig, horizon) — main.mm:530-563: allocates the env,
+ * rollout and policy buffers, initialises the policy (seed 1789,
+ * main.mm:548-554) and runs the first reset (sim_reset, main.mm:565). */
+int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWeights* raptor,
+                   const MdnPhysicsParams* physics, MdnSim** out);
+void mdn_sim_destroy(MdnSim* sim);
+/* Sim::set_config (main.mm:564); n cannot change. */
+int mdn_sim_set_config(MdnSim* sim, const MdnSimConfig* cfg);
+int mdn_sim_get_config(const MdnSim* sim, MdnSimConfig* cfg, uint32_t* horizon);
+/* Sim::reset (main.mm:565): first reset of every env. */
+int mdn_sim_reset(MdnSim* sim);
+/* Sim::collect(cmdbuf, count) (main.mm:573-598): `count` ticks (0 = horizon),
+ * tick t writes row block t % horizon.  Asynchronous on the sim's stream. */
+int mdn_sim_collect(MdnSim* sim, uint32_t count);
+/* Metal::finish (main.mm:71): waits for the stream, reports GPU seconds of
+ * the work since the previous sync (may be NULL). */
+int mdn_sim_sync(MdnSim* sim, double* gpu_seconds);
+/* Shared-buffer access (the reference reads buffer.contents, e.g.
+ * navigation_training.hpp:28-29): blocking copies in host layout. */
+int mdn_sim_buffer_bytes(const MdnSim* sim, uint32_t buffer, uint64_t* bytes);
+int mdn_sim_download(MdnSim* sim, uint32_t buffer, void* host, uint64_t bytes);
+int mdn_sim_upload(MdnSim* sim, uint32_t buffer, const void* host, uint64_t bytes);
+/* Per-kernel timing with HIP events on the sim's stream. */
+int mdn_sim_set_timing(MdnSim* sim, int enabled);
+int mdn_sim_kernel_time(MdnSim* sim, uint32_t kernel, double* total_ms, uint64_t* launches);
+int mdn_sim_reset_timing(MdnSim* sim);
+/* Lanes per environment in the rollout kernel (4, 8 or 16; default 8). */
+int mdn_sim_set_lanes(MdnSim* sim, uint32_t lanes);
+
+/* PPOTrainer(Sim&, epochs) — main.mm:1166-1217, with the minibatch size
+ * (PPOTrainer::minibatch, main.mm:1113) as an argument. */
+int mdn_ppo_create(MdnSim* sim, uint32_t epochs, uint32_t minibatch, MdnPPO** out);
+void mdn_ppo_destroy(MdnPPO* ppo);
+/* PPOTrainer::rollout_update (main.mm:1321-1384): GAE, advantage
+ * normalisation, epochs x minibatches of loss/grad, norm clip, Adam,
+ * log-std clamp, metric mean.  Asynchronous on the sim's stream. */
+int mdn_ppo_rollout_update(MdnPPO* ppo, uint32_t rollout_index);
+/* Pieces of rollout_update, for callers that validate between them
+ * (navigation_training.hpp:149-152). */
+int mdn_ppo_gae(MdnPPO* ppo);
+int mdn_ppo_normalize(MdnPPO* ppo);
+int mdn_ppo_update(MdnPPO* ppo, uint32_t rollout_index);
+/* PPOTrainer::metric_mean (main.mm:1383): [policy, value, entropy, ratio]. */
+int mdn_ppo_metric_mean(MdnPPO* ppo, float out[4]);
+int mdn_ppo_optimizer_step(const MdnPPO* ppo, uint64_t* step);
+int mdn_ppo_updates_per_rollout(const MdnPPO* ppo, uint32_t* updates);
+
+/* Stateless operators over host arrays (the reference's fixture kernels
+ * physics_fixture / raptor_fixture / world_depth / world_clearance,
+ * main.mm:29-43, 74-81, and ppo_gae / ppo_normalize_advantages). */
+int mdn_op_physics_step(const MdnPhysicsState* states, const float* actions, const float* winds,
+                        const MdnPhysicsParams* params, MdnPhysicsState* out, uint64_t n);
+/* RAPTOR over `steps` observations (obs[steps][22]) from the initial hidden
+ * state, evaluated by `copies` independent lane groups: actions[copies][steps][4],
+ * hidden[copies][16]. */
+int mdn_op_raptor_sequence(const MdnRaptorWeights* weights, const float* obs, uint32_t steps, uint32_t copies,
+                           float* actions, float* hidden);
+/* rays[n][6] = origin, unit direction; world of ray i = worlds[i / rays_per_world]. */
+int mdn_op_ray_world(const MdnWorld* worlds, const float* rays, const float* times, uint32_t rays_per_world,
+                     float* out, uint64_t n);
+int mdn_op_clearance(const MdnWorld* worlds, const float* points, const float* times, float* out, uint64_t n);
+int mdn_op_gae(uint32_t horizon, uint32_t n, const float* rewards, const float* values, const float* next_values,
+               const uint8_t* terminated, const uint8_t* truncated, float gamma, float lambda, float* advantages,
+               float* returns);
+int mdn_op_normalize(float* advantages, uint64_t count, float epsilon);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MDNAV_H */

@@ -1,0 +1,144 @@
+/*
+ * mdnav.hpp — header-only C++ façade over the C ABI (mdnav.h) that restores
+ * the reference's host interfaces:
+ *   mdnav::Sim         ~ Sim (main.mm:516-603)
+ *   mdnav::PPOTrainer  ~ PPOTrainer (main.mm:1110-1474)
+ *   mdnav::Trainer     ~ cpu_reference::Trainer (cpu_reference.hpp:112-615),
+ *                        same constructor and run() -> Metrics, on the GPU.
+ * Non-zero status codes become std::runtime_error, the reference's require()
+ * convention (main.mm:27).  The reference exposes shared buffers as public
+ * members; here they are methods returning host copies (sim.states() for
+ * sim.states.contents).
+ */
+#ifndef MDNAV_HPP
+#define MDNAV_HPP
+
+#include <array>
+#include <chrono>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "mdnav.h"
+
+namespace mdnav {
+
+inline void require(int rc) {
+    if (rc != MDN_OK) throw std::runtime_error(std::string("mdnav: ") + mdn_last_error());
+}
+
+class Sim {
+public:
+    Sim(const MdnSimConfig& config, uint32_t horizon, const MdnRaptorWeights& raptor,
+        const MdnPhysicsParams& physics)
+        : cfg(config), horizon(horizon) {
+        require(mdn_sim_create(&config, horizon, &raptor, &physics, &handle_));
+    }
+    ~Sim() { mdn_sim_destroy(handle_); }
+    Sim(const Sim&) = delete;
+    Sim& operator=(const Sim&) = delete;
+
+    void set_config(const MdnSimConfig& config) {
+        require(mdn_sim_set_config(handle_, &config));
+        cfg = config;
+    }
+    void reset() { require(mdn_sim_reset(handle_)); }
+    // Sim::collect(cmdbuf, count): enqueue; finish() waits like Metal::finish.
+    void collect(uint32_t count = 0) { require(mdn_sim_collect(handle_, count)); }
+    double finish() {
+        double s = 0;
+        require(mdn_sim_sync(handle_, &s));
+        return s;
+    }
+
+    template <class T>
+    std::vector<T> download(MdnBuffer id) {
+        uint64_t bytes = 0;
+        require(mdn_sim_buffer_bytes(handle_, id, &bytes));
+        std::vector<T> out(bytes / sizeof(T));
+        require(mdn_sim_download(handle_, id, out.data(), bytes));
+        return out;
+    }
+    template <class T>
+    void upload(MdnBuffer id, const std::vector<T>& v) {
+        require(mdn_sim_upload(handle_, id, v.data(), uint64_t(v.size()) * sizeof(T)));
+    }
+    std::vector<MdnPhysicsState> states() { return download<MdnPhysicsState>(MDN_BUF_STATES); }
+    std::vector<MdnSimRun> runs() { return download<MdnSimRun>(MDN_BUF_RUNS); }
+    std::vector<MdnWorld> worlds() { return download<MdnWorld>(MDN_BUF_WORLDS); }
+    std::vector<float> actor() { return download<float>(MDN_BUF_ACTOR); }
+    std::vector<float> critic() { return download<float>(MDN_BUF_CRITIC); }
+    std::vector<float> rewards() { return download<float>(MDN_BUF_REWARDS); }
+
+    MdnSim* handle() const { return handle_; }
+    MdnSimConfig cfg;
+    uint32_t horizon;
+
+private:
+    MdnSim* handle_ = nullptr;
+};
+
+class PPOTrainer {
+public:
+    explicit PPOTrainer(Sim& sim, uint32_t epochs = 2, uint32_t minibatch = 256) : sim_(sim) {
+        require(mdn_ppo_create(sim.handle(), epochs, minibatch, &handle_));
+    }
+    ~PPOTrainer() { mdn_ppo_destroy(handle_); }
+    PPOTrainer(const PPOTrainer&) = delete;
+    PPOTrainer& operator=(const PPOTrainer&) = delete;
+
+    void rollout_update(uint32_t rollout_index) { require(mdn_ppo_rollout_update(handle_, rollout_index)); }
+    std::array<float, 4> metric_mean() {
+        std::array<float, 4> m{};
+        require(mdn_ppo_metric_mean(handle_, m.data()));
+        return m;
+    }
+    uint64_t optimizer_step() const {
+        uint64_t s = 0;
+        require(mdn_ppo_optimizer_step(handle_, &s));
+        return s;
+    }
+
+private:
+    Sim& sim_;
+    MdnPPO* handle_ = nullptr;
+};
+
+// cpu_reference::Trainer on the GPU: Trainer(cfg, horizon, raptor, physics),
+// run(rollouts) -> Metrics (cpu_reference.hpp:132-185).
+class Trainer {
+public:
+    Trainer(const MdnSimConfig& config, uint32_t rollout_horizon, const MdnRaptorWeights& motor_policy,
+            const MdnPhysicsParams& dynamics, uint32_t epochs = 2, uint32_t minibatch = 256)
+        : sim(config, rollout_horizon, motor_policy, dynamics), ppo(sim, epochs, minibatch) {}
+
+    MdnMetrics run(uint32_t rollouts) {
+        MdnMetrics m{};
+        const auto start = std::chrono::steady_clock::now();
+        for (uint32_t r = 0; r < rollouts; r++) {
+            sim.collect();
+            ppo.rollout_update(r);
+        }
+        sim.finish();
+        m.wall_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count();
+        m.updates = ppo.optimizer_step();
+        for (const MdnSimRun& run : sim.runs()) {
+            m.episodes += run.episodes; m.successes += run.successes;
+            m.collisions += run.collisions; m.timeouts += run.timeouts;
+            m.final_progress += run.final_progress; m.total_path += run.total_path;
+            m.total_elapsed += run.total_elapsed; m.success_time += run.success_time;
+        }
+        const auto mean = ppo.metric_mean();
+        m.policy_loss = mean[0]; m.value_loss = mean[1]; m.entropy_loss = mean[2]; m.ratio = mean[3];
+        return m;
+    }
+    void reset_all() { sim.reset(); }
+
+    Sim sim;
+    PPOTrainer ppo;
+};
+
+}  // namespace mdnav
+
+#endif /* MDNAV_HPP */

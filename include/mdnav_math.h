@@ -30,12 +30,12 @@
 
 #include <stdint.h>
 
+#include <cmath>
+#include <cstring>
 #if defined(__HIPCC__) || defined(__HIP__)
 #include <hip/hip_runtime.h>
 #define MDN_HD __host__ __device__ __forceinline__
 #else
-#include <cmath>
-#include <cstring>
 #define MDN_HD inline
 #endif
 

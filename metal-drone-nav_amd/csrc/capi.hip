@@ -1,0 +1,736 @@
+// capi.hip — host side of the C ABI (include/mdnav.h).
+//
+// MdnSim owns the environment, rollout and policy buffers of one simulator on
+// one HIP stream (the reference's Sim, main.mm:516-603); MdnPPO owns the
+// optimiser state and minibatch workspaces (PPOTrainer, main.mm:1110-1474).
+// Device layouts: physics state and SimRun as struct-of-arrays [word][env];
+// worlds, rings and rollout rows in the reference's host layouts.  Downloads
+// and uploads transpose to and from the reference's AoS structs.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernel_args.h"
+#include "mdnav.h"
+#include "mdnav_host.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+    g_error = msg;
+    return code;
+}
+
+#define HIP_TRY(call)                                                                    \
+    do {                                                                                 \
+        hipError_t e_ = (call);                                                          \
+        if (e_ != hipSuccess) return fail(MDN_E_HIP, std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+constexpr uint32_t OBS = MDN_ACTOR_OBS_POOLED;
+constexpr uint32_t COBS = MDN_CRITIC_OBS;
+constexpr uint32_t HID = MDN_HIDDEN;
+constexpr uint32_t STATE_WORDS = 17, RUN_WORDS = 46, WORLD_WORDS = 169;
+
+template <class T>
+int dev_alloc(T** p, size_t count) {
+    *p = nullptr;
+    if (count == 0) count = 1;
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(p), count * sizeof(T)));
+    HIP_TRY(hipMemset(*p, 0, count * sizeof(T)));
+    return MDN_OK;
+}
+
+struct Timing {
+    bool enabled = false;
+    struct Pending { uint32_t id; hipEvent_t a, b; };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> spare;
+    double total_ms[MDN_K_COUNT] = {0};
+    uint64_t launches[MDN_K_COUNT] = {0};
+    hipEvent_t get() {
+        if (!spare.empty()) {
+            hipEvent_t e = spare.back();
+            spare.pop_back();
+            return e;
+        }
+        hipEvent_t e;
+        hipEventCreate(&e);
+        return e;
+    }
+};
+
+}  // namespace
+
+struct MdnSim {
+    MdnSimConfig cfg;
+    uint32_t horizon = 0;
+    uint32_t lanes = 8;
+    MdnPhysicsParams phys;
+    mdn::PolicyShape shape;
+    hipStream_t stream = nullptr;
+    hipEvent_t sync_start = nullptr, sync_stop = nullptr;
+    bool sync_open = false;
+    Timing timing;
+    // environment
+    float* state = nullptr;
+    uint32_t* run = nullptr;
+    float* world = nullptr;
+    float* sensors = nullptr;
+    float* poses = nullptr;
+    float* commands = nullptr;
+    float* raptor = nullptr;
+    float* camera = nullptr;
+    // policy
+    float* actor = nullptr;
+    float* critic = nullptr;
+    float* actor_w1t = nullptr;
+    float* critic_w1t = nullptr;
+    // rollout rows
+    float *obs = nullptr, *co = nullptr, *actions = nullptr, *logp = nullptr, *values = nullptr;
+    float *rewards = nullptr, *next_values = nullptr, *advantages = nullptr, *returns = nullptr;
+    uint8_t *terminated = nullptr, *truncated = nullptr;
+    MdnPPO* ppo = nullptr;
+
+    size_t rows() const { return size_t(cfg.n) * horizon; }
+    nav::RolloutArgs args(uint32_t count) const {
+        nav::RolloutArgs a;
+        a.state = state; a.run = run; a.world = world; a.sensors = sensors; a.poses = poses; a.commands = commands;
+        a.raptor = raptor; a.actor = actor; a.actor_w1t = actor_w1t; a.critic = critic; a.critic_w1t = critic_w1t;
+        a.camera = camera; a.obs = obs; a.co = co; a.actions = actions; a.logp = logp; a.values = values;
+        a.rewards = rewards; a.next_values = next_values; a.terminated = terminated; a.truncated = truncated;
+        a.cfg = cfg; a.phys = phys; a.count = count; a.horizon = horizon;
+        return a;
+    }
+};
+
+struct MdnPPO {
+    MdnSim* sim = nullptr;
+    uint32_t epochs = 2, minibatch = 256;
+    uint64_t optimizer_step = 0;
+    uint32_t updates = 0;
+    float *am = nullptr, *av = nullptr, *cm = nullptr, *cv = nullptr;
+    // minibatch workspaces
+    float *ah = nullptr, *adelta = nullptr, *ch = nullptr, *cdelta = nullptr;
+    float *dm = nullptr, *dls = nullptr, *dv = nullptr, *loss = nullptr;
+    float *part = nullptr, *grad = nullptr;
+    double* norm_part = nullptr;
+    float* norm_stats = nullptr;
+    float *metric_rows = nullptr, *metric_mean = nullptr;
+};
+
+namespace {
+
+// Record a timed launch on the sim's stream.
+template <class F>
+int timed(MdnSim* s, uint32_t id, F launch) {
+    hipEvent_t a = nullptr, b = nullptr;
+    if (s->timing.enabled) {
+        a = s->timing.get();
+        b = s->timing.get();
+        HIP_TRY(hipEventRecord(a, s->stream));
+    }
+    const hipError_t e = launch();
+    if (e != hipSuccess) return fail(MDN_E_HIP, std::string("kernel launch: ") + hipGetErrorString(e));
+    if (s->timing.enabled) {
+        HIP_TRY(hipEventRecord(b, s->stream));
+        s->timing.pending.push_back({id, a, b});
+    }
+    return MDN_OK;
+}
+
+int open_sync_window(MdnSim* s) {
+    if (!s->sync_open) {
+        HIP_TRY(hipEventRecord(s->sync_start, s->stream));
+        s->sync_open = true;
+    }
+    return MDN_OK;
+}
+
+int refresh_transposes(MdnSim* s) {
+    HIP_TRY(ppo_launch_transpose(s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->stream));
+    return MDN_OK;
+}
+
+int ring_slots(const MdnSimConfig& c) {
+    const uint32_t need = c.sensor_delay + 2;
+    return need <= 2 ? 2 : (need <= 4 ? 4 : 8);
+}
+
+struct BufInfo { void* dev; size_t bytes; };
+
+BufInfo row_buffer(MdnSim* s, uint32_t id) {
+    const size_t R = s->rows();
+    switch (id) {
+        case MDN_BUF_OBS: return {s->obs, R * OBS * 4};
+        case MDN_BUF_CRITIC_OBS: return {s->co, R * COBS * 4};
+        case MDN_BUF_ACTIONS: return {s->actions, R * 4 * 4};
+        case MDN_BUF_LOGP: return {s->logp, R * 4};
+        case MDN_BUF_VALUES: return {s->values, R * 4};
+        case MDN_BUF_REWARDS: return {s->rewards, R * 4};
+        case MDN_BUF_NEXT_VALUES: return {s->next_values, R * 4};
+        case MDN_BUF_TERMINATED: return {s->terminated, R};
+        case MDN_BUF_TRUNCATED: return {s->truncated, R};
+        case MDN_BUF_ADVANTAGES: return {s->advantages, R * 4};
+        case MDN_BUF_RETURNS: return {s->returns, R * 4};
+        case MDN_BUF_SENSORS: return {s->sensors, size_t(s->cfg.n) * 8 * 320 * 4};
+        case MDN_BUF_POSES: return {s->poses, size_t(s->cfg.n) * 96 * 4};
+        case MDN_BUF_COMMANDS: return {s->commands, size_t(s->cfg.n) * 32 * 4};
+        case MDN_BUF_WORLDS: return {s->world, size_t(s->cfg.n) * WORLD_WORDS * 4};
+        case MDN_BUF_ACTOR: return {s->actor, size_t(s->shape.actor_count()) * 4};
+        case MDN_BUF_CRITIC: return {s->critic, size_t(s->shape.critic_count()) * 4};
+        default: break;
+    }
+    if (s->ppo) {
+        MdnPPO* p = s->ppo;
+        switch (id) {
+            case MDN_BUF_ACTOR_M: return {p->am, size_t(s->shape.actor_count()) * 4};
+            case MDN_BUF_ACTOR_V: return {p->av, size_t(s->shape.actor_count()) * 4};
+            case MDN_BUF_CRITIC_M: return {p->cm, size_t(s->shape.critic_count()) * 4};
+            case MDN_BUF_CRITIC_V: return {p->cv, size_t(s->shape.critic_count()) * 4};
+            case MDN_BUF_METRIC_ROWS: return {p->metric_rows, size_t(p->updates) * 16};
+            default: break;
+        }
+    }
+    return {nullptr, 0};
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mdn_last_error(void) { return g_error.c_str(); }
+const char* mdn_version(void) { return "mdnav 0.1 gfx950"; }
+
+int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWeights* raptor,
+                   const MdnPhysicsParams* physics, MdnSim** out) {
+    if (!cfg || !raptor || !physics || !out) return fail(MDN_E_ARG, "mdn_sim_create: null argument");
+    *out = nullptr;
+    if (cfg->n == 0 || horizon == 0) return fail(MDN_E_ARG, "mdn_sim_create: n and horizon must be positive");
+    if (cfg->sensor_period == 0) return fail(MDN_E_ARG, "mdn_sim_create: sensor_period must be positive");
+    if (cfg->sensor_delay > 6 || cfg->command_delay > 7)
+        return fail(MDN_E_ARG, "delay rings support <=6 sensor frames and <=7 command steps");
+    MdnSim* s = new MdnSim();
+    s->cfg = *cfg;
+    s->horizon = horizon;
+    s->phys = *physics;
+    const uint32_t N = cfg->n;
+    const size_t R = size_t(N) * horizon;
+    int rc = MDN_OK;
+    auto guard = [&](int r) { if (r != MDN_OK && rc == MDN_OK) rc = r; };
+    guard(hipStreamCreate(&s->stream) == hipSuccess ? MDN_OK : fail(MDN_E_HIP, "hipStreamCreate failed"));
+    guard(hipEventCreate(&s->sync_start) == hipSuccess ? MDN_OK : fail(MDN_E_HIP, "hipEventCreate"));
+    guard(hipEventCreate(&s->sync_stop) == hipSuccess ? MDN_OK : fail(MDN_E_HIP, "hipEventCreate"));
+    guard(dev_alloc(&s->state, size_t(STATE_WORDS) * N));
+    guard(dev_alloc(&s->run, size_t(RUN_WORDS) * N));
+    guard(dev_alloc(&s->world, size_t(WORLD_WORDS) * N));
+    guard(dev_alloc(&s->sensors, size_t(N) * 8 * 320));
+    guard(dev_alloc(&s->poses, size_t(N) * 96));
+    guard(dev_alloc(&s->commands, size_t(N) * 32));
+    guard(dev_alloc(&s->raptor, 2084));
+    guard(dev_alloc(&s->camera, 960));
+    guard(dev_alloc(&s->actor, s->shape.actor_count()));
+    guard(dev_alloc(&s->critic, s->shape.critic_count()));
+    guard(dev_alloc(&s->actor_w1t, size_t(OBS) * HID));
+    guard(dev_alloc(&s->critic_w1t, size_t(COBS) * HID));
+    guard(dev_alloc(&s->obs, R * OBS));
+    guard(dev_alloc(&s->co, R * COBS));
+    guard(dev_alloc(&s->actions, R * 4));
+    guard(dev_alloc(&s->logp, R));
+    guard(dev_alloc(&s->values, R));
+    guard(dev_alloc(&s->rewards, R));
+    guard(dev_alloc(&s->next_values, R));
+    guard(dev_alloc(&s->advantages, R));
+    guard(dev_alloc(&s->returns, R));
+    guard(dev_alloc(&s->terminated, R));
+    guard(dev_alloc(&s->truncated, R));
+    if (rc == MDN_OK && hipDeviceSynchronize() != hipSuccess) rc = fail(MDN_E_HIP, "mdn_sim_create: allocation sync");
+    if (rc != MDN_OK) {
+        mdn_sim_destroy(s);
+        return rc;
+    }
+    // camera rays and policy initialisation are host computations shared with
+    // the oracle (mdnav_host.h); copies are synchronous.
+    std::vector<float> cam(960);
+    for (uint32_t k = 0; k < 320; k++) {
+        const uint32_t row = k / 20, col = k % 20;
+        const float y = ((float(col) + 0.5f) / 20.0f * 2.0f - 1.0f) * MDN_SENSOR_TAN_H;
+        const float z = ((float(row) + 0.5f) / 16.0f * 2.0f - 1.0f) * MDN_SENSOR_TAN_V;
+        const float dx = 1.0f, dy = -y, dz = -z;
+        const float len = mdn::sqrt_f(dx * dx + dy * dy + dz * dz);
+        const float inv = 1.0f / mdn::fmax_f(len, 1e-8f);
+        cam[3 * k] = dx * inv; cam[3 * k + 1] = dy * inv; cam[3 * k + 2] = dz * inv;
+    }
+    std::vector<float> actor(s->shape.actor_count()), critic(s->shape.critic_count());
+    mdn::init_policy(s->shape, actor.data(), critic.data());
+    if (hipMemcpy(s->camera, cam.data(), cam.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(s->raptor, raptor, sizeof(MdnRaptorWeights), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(s->actor, actor.data(), actor.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(s->critic, critic.data(), critic.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        mdn_sim_destroy(s);
+        return fail(MDN_E_HIP, "mdn_sim_create: upload failed");
+    }
+    rc = refresh_transposes(s);
+    if (rc == MDN_OK) rc = mdn_sim_reset(s);
+    if (rc == MDN_OK && hipStreamSynchronize(s->stream) != hipSuccess) rc = fail(MDN_E_HIP, "mdn_sim_create: sync");
+    if (rc != MDN_OK) {
+        mdn_sim_destroy(s);
+        return rc;
+    }
+    *out = s;
+    return MDN_OK;
+}
+
+void mdn_sim_destroy(MdnSim* s) {
+    if (!s) return;
+    if (s->stream) hipStreamSynchronize(s->stream);
+    if (s->ppo) mdn_ppo_destroy(s->ppo);
+    void* bufs[] = {s->state, s->run, s->world, s->sensors, s->poses, s->commands, s->raptor, s->camera,
+                    s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->obs, s->co, s->actions, s->logp,
+                    s->values, s->rewards, s->next_values, s->advantages, s->returns, s->terminated, s->truncated};
+    for (void* b : bufs)
+        if (b) hipFree(b);
+    for (auto& p : s->timing.pending) { hipEventDestroy(p.a); hipEventDestroy(p.b); }
+    for (auto e : s->timing.spare) hipEventDestroy(e);
+    if (s->sync_start) hipEventDestroy(s->sync_start);
+    if (s->sync_stop) hipEventDestroy(s->sync_stop);
+    if (s->stream) hipStreamDestroy(s->stream);
+    delete s;
+}
+
+int mdn_sim_set_config(MdnSim* s, const MdnSimConfig* cfg) {
+    if (!s || !cfg) return fail(MDN_E_ARG, "mdn_sim_set_config: null argument");
+    if (cfg->n != s->cfg.n) return fail(MDN_E_ARG, "cannot resize simulator");
+    if (cfg->sensor_period == 0) return fail(MDN_E_ARG, "sensor_period must be positive");
+    if (cfg->sensor_delay > 6 || cfg->command_delay > 7)
+        return fail(MDN_E_ARG, "delay rings support <=6 sensor frames and <=7 command steps");
+    s->cfg = *cfg;
+    return MDN_OK;
+}
+
+int mdn_sim_get_config(const MdnSim* s, MdnSimConfig* cfg, uint32_t* horizon) {
+    if (!s) return fail(MDN_E_ARG, "mdn_sim_get_config: null sim");
+    if (cfg) *cfg = s->cfg;
+    if (horizon) *horizon = s->horizon;
+    return MDN_OK;
+}
+
+int mdn_sim_set_lanes(MdnSim* s, uint32_t lanes) {
+    if (!s || (lanes != 4 && lanes != 8 && lanes != 16)) return fail(MDN_E_ARG, "lanes per env must be 4, 8 or 16");
+    s->lanes = lanes;
+    return MDN_OK;
+}
+
+int mdn_sim_reset(MdnSim* s) {
+    if (!s) return fail(MDN_E_ARG, "mdn_sim_reset: null sim");
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    const nav::RolloutArgs a = s->args(0);
+    HIP_TRY(nav_launch_reset(&a, s->stream));
+    return MDN_OK;
+}
+
+int mdn_sim_collect(MdnSim* s, uint32_t count) {
+    if (!s) return fail(MDN_E_ARG, "mdn_sim_collect: null sim");
+    if (count == 0) count = s->horizon;
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    const nav::RolloutArgs a = s->args(count);
+    const int lanes = int(s->lanes), slots = ring_slots(s->cfg);
+    return timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, lanes, slots, s->stream); });
+}
+
+int mdn_sim_sync(MdnSim* s, double* gpu_seconds) {
+    if (!s) return fail(MDN_E_ARG, "mdn_sim_sync: null sim");
+    double seconds = 0.0;
+    if (s->sync_open) {
+        HIP_TRY(hipEventRecord(s->sync_stop, s->stream));
+        HIP_TRY(hipEventSynchronize(s->sync_stop));
+        float ms = 0;
+        HIP_TRY(hipEventElapsedTime(&ms, s->sync_start, s->sync_stop));
+        seconds = ms * 1e-3;
+        s->sync_open = false;
+    } else {
+        HIP_TRY(hipStreamSynchronize(s->stream));
+    }
+    for (auto& p : s->timing.pending) {
+        float ms = 0;
+        HIP_TRY(hipEventElapsedTime(&ms, p.a, p.b));
+        s->timing.total_ms[p.id] += ms;
+        s->timing.launches[p.id] += 1;
+        s->timing.spare.push_back(p.a);
+        s->timing.spare.push_back(p.b);
+    }
+    s->timing.pending.clear();
+    if (gpu_seconds) *gpu_seconds = seconds;
+    return MDN_OK;
+}
+
+int mdn_sim_set_timing(MdnSim* s, int enabled) {
+    if (!s) return fail(MDN_E_ARG, "mdn_sim_set_timing: null sim");
+    s->timing.enabled = enabled != 0;
+    return MDN_OK;
+}
+
+int mdn_sim_kernel_time(MdnSim* s, uint32_t kernel, double* total_ms, uint64_t* launches) {
+    if (!s || kernel >= MDN_K_COUNT) return fail(MDN_E_ARG, "mdn_sim_kernel_time: bad kernel id");
+    if (total_ms) *total_ms = s->timing.total_ms[kernel];
+    if (launches) *launches = s->timing.launches[kernel];
+    return MDN_OK;
+}
+
+int mdn_sim_reset_timing(MdnSim* s) {
+    if (!s) return fail(MDN_E_ARG, "mdn_sim_reset_timing: null sim");
+    for (int i = 0; i < MDN_K_COUNT; i++) { s->timing.total_ms[i] = 0; s->timing.launches[i] = 0; }
+    return MDN_OK;
+}
+
+int mdn_sim_buffer_bytes(const MdnSim* s, uint32_t buffer, uint64_t* bytes) {
+    if (!s || !bytes) return fail(MDN_E_ARG, "mdn_sim_buffer_bytes: null argument");
+    const uint32_t N = s->cfg.n;
+    if (buffer == MDN_BUF_STATES) { *bytes = uint64_t(N) * sizeof(MdnPhysicsState); return MDN_OK; }
+    if (buffer == MDN_BUF_RUNS) { *bytes = uint64_t(N) * sizeof(MdnSimRun); return MDN_OK; }
+    const BufInfo b = row_buffer(const_cast<MdnSim*>(s), buffer);
+    if (!b.dev) return fail(MDN_E_ARG, "unknown buffer id " + std::to_string(buffer) + " (Adam buffers need a PPO handle)");
+    *bytes = b.bytes;
+    return MDN_OK;
+}
+
+int mdn_sim_download(MdnSim* s, uint32_t buffer, void* host, uint64_t bytes) {
+    uint64_t need = 0;
+    int rc = mdn_sim_buffer_bytes(s, buffer, &need);
+    if (rc) return rc;
+    if (!host || bytes != need) return fail(MDN_E_ARG, "download size mismatch: need " + std::to_string(need));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    const uint32_t N = s->cfg.n;
+    if (buffer == MDN_BUF_STATES || buffer == MDN_BUF_RUNS) {
+        const uint32_t W = buffer == MDN_BUF_STATES ? STATE_WORDS : RUN_WORDS;
+        std::vector<uint32_t> soa(size_t(W) * N);
+        HIP_TRY(hipMemcpy(soa.data(), buffer == MDN_BUF_STATES ? static_cast<void*>(s->state) : static_cast<void*>(s->run),
+                          soa.size() * 4, hipMemcpyDeviceToHost));
+        uint32_t* aos = static_cast<uint32_t*>(host);
+        for (uint32_t n = 0; n < N; n++)
+            for (uint32_t w = 0; w < W; w++) aos[size_t(n) * W + w] = soa[size_t(w) * N + n];
+        return MDN_OK;
+    }
+    const BufInfo b = row_buffer(s, buffer);
+    HIP_TRY(hipMemcpy(host, b.dev, b.bytes, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_sim_upload(MdnSim* s, uint32_t buffer, const void* host, uint64_t bytes) {
+    uint64_t need = 0;
+    int rc = mdn_sim_buffer_bytes(s, buffer, &need);
+    if (rc) return rc;
+    if (!host || bytes != need) return fail(MDN_E_ARG, "upload size mismatch: need " + std::to_string(need));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    const uint32_t N = s->cfg.n;
+    if (buffer == MDN_BUF_STATES || buffer == MDN_BUF_RUNS) {
+        const uint32_t W = buffer == MDN_BUF_STATES ? STATE_WORDS : RUN_WORDS;
+        std::vector<uint32_t> soa(size_t(W) * N);
+        const uint32_t* aos = static_cast<const uint32_t*>(host);
+        for (uint32_t n = 0; n < N; n++)
+            for (uint32_t w = 0; w < W; w++) soa[size_t(w) * N + n] = aos[size_t(n) * W + w];
+        HIP_TRY(hipMemcpy(buffer == MDN_BUF_STATES ? static_cast<void*>(s->state) : static_cast<void*>(s->run), soa.data(),
+                          soa.size() * 4, hipMemcpyHostToDevice));
+        return MDN_OK;
+    }
+    const BufInfo b = row_buffer(s, buffer);
+    HIP_TRY(hipMemcpy(b.dev, host, b.bytes, hipMemcpyHostToDevice));
+    if (buffer == MDN_BUF_ACTOR || buffer == MDN_BUF_CRITIC) {
+        rc = refresh_transposes(s);
+        if (rc) return rc;
+        HIP_TRY(hipStreamSynchronize(s->stream));
+    }
+    return MDN_OK;
+}
+
+// ---------------------------------------------------------------- PPO
+int mdn_ppo_create(MdnSim* s, uint32_t epochs, uint32_t minibatch, MdnPPO** out) {
+    if (!s || !out) return fail(MDN_E_ARG, "mdn_ppo_create: null argument");
+    *out = nullptr;
+    if (epochs < 1 || epochs > 4) return fail(MDN_E_ARG, "PPO epochs must be1..4");
+    if (minibatch == 0) return fail(MDN_E_ARG, "minibatch must be positive");
+    if (s->ppo) return fail(MDN_E_STATE, "simulator already has a PPO trainer");
+    MdnPPO* p = new MdnPPO();
+    p->sim = s;
+    p->epochs = epochs;
+    p->minibatch = uint32_t(std::min<size_t>(minibatch, s->rows()));
+    const size_t M = p->minibatch;
+    const uint32_t minibatches = uint32_t((s->rows() + p->minibatch - 1) / p->minibatch);
+    p->updates = minibatches * epochs;
+    const uint32_t chunks = uint32_t((M + 255) / 256);
+    int rc = MDN_OK;
+    auto guard = [&](int r) { if (r != MDN_OK && rc == MDN_OK) rc = r; };
+    guard(dev_alloc(&p->am, s->shape.actor_count()));
+    guard(dev_alloc(&p->av, s->shape.actor_count()));
+    guard(dev_alloc(&p->cm, s->shape.critic_count()));
+    guard(dev_alloc(&p->cv, s->shape.critic_count()));
+    guard(dev_alloc(&p->ah, M * HID));
+    guard(dev_alloc(&p->adelta, M * HID));
+    guard(dev_alloc(&p->ch, M * HID));
+    guard(dev_alloc(&p->cdelta, M * HID));
+    guard(dev_alloc(&p->dm, M * 4));
+    guard(dev_alloc(&p->dls, M * 4));
+    guard(dev_alloc(&p->dv, M));
+    guard(dev_alloc(&p->loss, M * 4));
+    guard(dev_alloc(&p->part, size_t(chunks) * ppo_partial_stride()));
+    guard(dev_alloc(&p->grad, ppo_partial_stride()));
+    guard(dev_alloc(&p->norm_part, (s->rows() + 255) / 256));
+    guard(dev_alloc(&p->norm_stats, 2));
+    guard(dev_alloc(&p->metric_rows, size_t(p->updates) * 4));
+    guard(dev_alloc(&p->metric_mean, 4));
+    s->ppo = p;
+    if (rc == MDN_OK && hipDeviceSynchronize() != hipSuccess) rc = fail(MDN_E_HIP, "mdn_ppo_create: allocation sync");
+    if (rc != MDN_OK) {
+        mdn_ppo_destroy(p);
+        return rc;
+    }
+    *out = p;
+    return MDN_OK;
+}
+
+void mdn_ppo_destroy(MdnPPO* p) {
+    if (!p) return;
+    if (p->sim) {
+        hipStreamSynchronize(p->sim->stream);
+        if (p->sim->ppo == p) p->sim->ppo = nullptr;
+    }
+    void* bufs[] = {p->am, p->av, p->cm, p->cv, p->ah, p->adelta, p->ch, p->cdelta, p->dm, p->dls, p->dv,
+                    p->loss, p->part, p->grad, p->norm_part, p->norm_stats, p->metric_rows, p->metric_mean};
+    for (void* b : bufs)
+        if (b) hipFree(b);
+    delete p;
+}
+
+int mdn_ppo_gae(MdnPPO* p) {
+    if (!p) return fail(MDN_E_ARG, "mdn_ppo_gae: null");
+    MdnSim* s = p->sim;
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    return timed(s, MDN_K_GAE, [&] {
+        return ppo_launch_gae(s->rewards, s->values, s->next_values, s->terminated, s->truncated, s->advantages,
+                              s->returns, s->horizon, s->cfg.n, 0.99f, 0.95f, s->stream);
+    });
+}
+
+int mdn_ppo_normalize(MdnPPO* p) {
+    if (!p) return fail(MDN_E_ARG, "mdn_ppo_normalize: null");
+    MdnSim* s = p->sim;
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    return timed(s, MDN_K_NORMALIZE, [&] {
+        return ppo_launch_normalize(s->advantages, s->rows(), p->norm_part, p->norm_stats, 1.0e-8f, s->stream);
+    });
+}
+
+int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
+    if (!p) return fail(MDN_E_ARG, "mdn_ppo_update: null");
+    MdnSim* s = p->sim;
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    const uint32_t rows = uint32_t(s->rows());
+    const std::vector<uint32_t> order = mdn::minibatch_schedule(rows, p->minibatch, p->epochs, rollout_index);
+    if (order.size() != p->updates) return fail(MDN_E_STATE, "PPO update count mismatch");
+    for (size_t u = 0; u < order.size(); u++) {
+        const uint32_t begin = order[u];
+        const uint32_t b = std::min(p->minibatch, rows - begin);
+        ppo::RowArgs ra;
+        ra.obs = s->obs + size_t(begin) * OBS;
+        ra.co = s->co + size_t(begin) * COBS;
+        ra.actions = s->actions + size_t(begin) * 4;
+        ra.old_logp = s->logp + begin;
+        ra.adv = s->advantages + begin;
+        ra.ret = s->returns + begin;
+        ra.actor = s->actor; ra.actor_w1t = s->actor_w1t; ra.critic = s->critic; ra.critic_w1t = s->critic_w1t;
+        ra.ah = p->ah; ra.adelta = p->adelta; ra.ch = p->ch; ra.cdelta = p->cdelta;
+        ra.dm = p->dm; ra.dls = p->dls; ra.dv = p->dv; ra.loss = p->loss;
+        ra.b = b; ra.clip = 0.2f; ra.vcoef = 0.5f; ra.ecoef = s->cfg.entropy_coef;
+        rc = timed(s, MDN_K_ROWS, [&] { return ppo_launch_rows(&ra, s->stream); });
+        if (rc) return rc;
+        rc = timed(s, MDN_K_GRADS, [&] {
+            return ppo_launch_grads(ra.obs, ra.co, p->ah, p->adelta, p->ch, p->cdelta, p->dm, p->dls, p->dv, p->loss,
+                                    p->part, p->grad, b, s->stream);
+        });
+        if (rc) return rc;
+        ++p->optimizer_step;
+        ppo::AdamArgs aa;
+        aa.actor = s->actor; aa.critic = s->critic; aa.actor_w1t = s->actor_w1t; aa.critic_w1t = s->critic_w1t;
+        aa.am = p->am; aa.av = p->av; aa.cm = p->cm; aa.cv = p->cv;
+        aa.grad = p->grad; aa.metric_row = p->metric_rows + u * 4;
+        aa.lr = s->cfg.learning_rate;
+        mdn::adam_corrections(p->optimizer_step, 0.9f, 0.999f, &aa.c1, &aa.c2);
+        aa.b = b;
+        rc = timed(s, MDN_K_ADAM, [&] { return ppo_launch_adam(&aa, s->stream); });
+        if (rc) return rc;
+    }
+    HIP_TRY(ppo_launch_metric_mean(p->metric_rows, p->metric_mean, p->updates, s->stream));
+    return MDN_OK;
+}
+
+int mdn_ppo_rollout_update(MdnPPO* p, uint32_t rollout_index) {
+    int rc = mdn_ppo_gae(p);
+    if (!rc) rc = mdn_ppo_normalize(p);
+    if (!rc) rc = mdn_ppo_update(p, rollout_index);
+    return rc;
+}
+
+int mdn_ppo_metric_mean(MdnPPO* p, float out[4]) {
+    if (!p || !out) return fail(MDN_E_ARG, "mdn_ppo_metric_mean: null");
+    HIP_TRY(hipStreamSynchronize(p->sim->stream));
+    HIP_TRY(hipMemcpy(out, p->metric_mean, 16, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_ppo_optimizer_step(const MdnPPO* p, uint64_t* step) {
+    if (!p || !step) return fail(MDN_E_ARG, "mdn_ppo_optimizer_step: null");
+    *step = p->optimizer_step;
+    return MDN_OK;
+}
+
+int mdn_ppo_updates_per_rollout(const MdnPPO* p, uint32_t* updates) {
+    if (!p || !updates) return fail(MDN_E_ARG, "mdn_ppo_updates_per_rollout: null");
+    *updates = p->updates;
+    return MDN_OK;
+}
+
+// ---------------------------------------------------------------- operators
+namespace {
+struct DevBuf {
+    void* p = nullptr;
+    ~DevBuf() { if (p) hipFree(p); }
+};
+int upload_tmp(DevBuf& d, const void* host, size_t bytes) {
+    HIP_TRY(hipMalloc(&d.p, bytes ? bytes : 4));
+    if (host && bytes) HIP_TRY(hipMemcpy(d.p, host, bytes, hipMemcpyHostToDevice));
+    return MDN_OK;
+}
+}  // namespace
+
+int mdn_op_physics_step(const MdnPhysicsState* states, const float* actions, const float* winds,
+                        const MdnPhysicsParams* params, MdnPhysicsState* out, uint64_t n) {
+    if (!states || !actions || !winds || !params || !out) return fail(MDN_E_ARG, "mdn_op_physics_step: null");
+    if (n == 0) return MDN_OK;
+    DevBuf ds, da, dw, dout;
+    int rc = upload_tmp(ds, states, n * sizeof(MdnPhysicsState));
+    if (!rc) rc = upload_tmp(da, actions, n * 16);
+    if (!rc) rc = upload_tmp(dw, winds, n * 12);
+    if (!rc) rc = upload_tmp(dout, nullptr, n * sizeof(MdnPhysicsState));
+    if (rc) return rc;
+    HIP_TRY(nav_launch_physics_fixture(static_cast<const MdnPhysicsState*>(ds.p), static_cast<const float*>(da.p),
+                                       static_cast<const float*>(dw.p), params, static_cast<MdnPhysicsState*>(dout.p), n,
+                                       nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(out, dout.p, n * sizeof(MdnPhysicsState), hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_op_raptor_sequence(const MdnRaptorWeights* weights, const float* obs, uint32_t steps, uint32_t copies,
+                           float* actions, float* hidden) {
+    if (!weights || !obs || !actions || !hidden) return fail(MDN_E_ARG, "mdn_op_raptor_sequence: null");
+    if (steps == 0 || copies == 0) return MDN_OK;
+    DevBuf dw, dobs, dact, dh;
+    int rc = upload_tmp(dw, weights, sizeof(MdnRaptorWeights));
+    if (!rc) rc = upload_tmp(dobs, obs, size_t(steps) * 22 * 4);
+    if (!rc) rc = upload_tmp(dact, nullptr, size_t(copies) * steps * 16);
+    if (!rc) rc = upload_tmp(dh, nullptr, size_t(copies) * 64);
+    if (rc) return rc;
+    // copies are spread over the three lane-group widths the rollout uses
+    const uint32_t third = (copies + 2) / 3;
+    const int widths[3] = {4, 8, 16};
+    for (int k = 0; k < 3; k++) {
+        const uint32_t first = third * uint32_t(k);
+        if (first >= copies) break;
+        const uint32_t cnt = std::min(third, copies - first);
+        HIP_TRY(nav_launch_raptor_fixture(static_cast<const float*>(dw.p), static_cast<const float*>(dobs.p), steps, cnt,
+                                          static_cast<float*>(dact.p) + size_t(first) * steps * 4,
+                                          static_cast<float*>(dh.p) + size_t(first) * 16, widths[k], nullptr));
+    }
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(actions, dact.p, size_t(copies) * steps * 16, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(hidden, dh.p, size_t(copies) * 64, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_op_ray_world(const MdnWorld* worlds, const float* rays, const float* times, uint32_t rays_per_world,
+                     float* out, uint64_t n) {
+    if (!worlds || !rays || !times || !out || rays_per_world == 0) return fail(MDN_E_ARG, "mdn_op_ray_world: bad argument");
+    if (n == 0) return MDN_OK;
+    const uint64_t nw = (n + rays_per_world - 1) / rays_per_world;
+    DevBuf dw, dr, dt, dout;
+    int rc = upload_tmp(dw, worlds, nw * sizeof(MdnWorld));
+    if (!rc) rc = upload_tmp(dr, rays, n * 24);
+    if (!rc) rc = upload_tmp(dt, times, nw * 4);
+    if (!rc) rc = upload_tmp(dout, nullptr, n * 4);
+    if (rc) return rc;
+    HIP_TRY(nav_launch_ray_fixture(static_cast<const float*>(dw.p), static_cast<const float*>(dr.p),
+                                   static_cast<const float*>(dt.p), rays_per_world, static_cast<float*>(dout.p), n,
+                                   nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(out, dout.p, n * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_op_clearance(const MdnWorld* worlds, const float* points, const float* times, float* out, uint64_t n) {
+    if (!worlds || !points || !times || !out) return fail(MDN_E_ARG, "mdn_op_clearance: null");
+    if (n == 0) return MDN_OK;
+    DevBuf dw, dp, dt, dout;
+    int rc = upload_tmp(dw, worlds, n * sizeof(MdnWorld));
+    if (!rc) rc = upload_tmp(dp, points, n * 12);
+    if (!rc) rc = upload_tmp(dt, times, n * 4);
+    if (!rc) rc = upload_tmp(dout, nullptr, n * 4);
+    if (rc) return rc;
+    HIP_TRY(nav_launch_clearance_fixture(static_cast<const float*>(dw.p), static_cast<const float*>(dp.p),
+                                         static_cast<const float*>(dt.p), static_cast<float*>(dout.p), n, nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(out, dout.p, n * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_op_gae(uint32_t horizon, uint32_t n, const float* rewards, const float* values, const float* next_values,
+               const uint8_t* terminated, const uint8_t* truncated, float gamma, float lambda, float* advantages,
+               float* returns) {
+    if (!rewards || !values || !next_values || !terminated || !truncated || !advantages || !returns)
+        return fail(MDN_E_ARG, "mdn_op_gae: null");
+    const size_t R = size_t(horizon) * n;
+    if (R == 0) return MDN_OK;
+    DevBuf r, v, nv, te, tr, adv, ret;
+    int rc = upload_tmp(r, rewards, R * 4);
+    if (!rc) rc = upload_tmp(v, values, R * 4);
+    if (!rc) rc = upload_tmp(nv, next_values, R * 4);
+    if (!rc) rc = upload_tmp(te, terminated, R);
+    if (!rc) rc = upload_tmp(tr, truncated, R);
+    if (!rc) rc = upload_tmp(adv, nullptr, R * 4);
+    if (!rc) rc = upload_tmp(ret, nullptr, R * 4);
+    if (rc) return rc;
+    HIP_TRY(ppo_launch_gae(static_cast<float*>(r.p), static_cast<float*>(v.p), static_cast<float*>(nv.p),
+                           static_cast<uint8_t*>(te.p), static_cast<uint8_t*>(tr.p), static_cast<float*>(adv.p),
+                           static_cast<float*>(ret.p), horizon, n, gamma, lambda, nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(advantages, adv.p, R * 4, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(returns, ret.p, R * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_op_normalize(float* advantages, uint64_t count, float epsilon) {
+    if (!advantages) return fail(MDN_E_ARG, "mdn_op_normalize: null");
+    if (count == 0) return MDN_OK;
+    DevBuf a, part, stats;
+    int rc = upload_tmp(a, advantages, count * 4);
+    if (!rc) rc = upload_tmp(part, nullptr, ((count + 255) / 256) * 8);
+    if (!rc) rc = upload_tmp(stats, nullptr, 8);
+    if (rc) return rc;
+    HIP_TRY(ppo_launch_normalize(static_cast<float*>(a.p), count, static_cast<double*>(part.p),
+                                 static_cast<float*>(stats.p), epsilon, nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(advantages, a.p, count * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+}  // extern "C"

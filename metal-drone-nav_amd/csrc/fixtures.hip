@@ -1,0 +1,98 @@
+// fixtures.hip — stateless operators over caller arrays, built from the same
+// device functions as the rollout kernel.  They play the role of the
+// reference's fixture kernels (physics_fixture, raptor_fixture, world_depth,
+// world_clearance; main.mm:29-43, 74-81) for golden-vector tests.
+#include "nav_device.h"
+
+namespace nav {
+
+__device__ __forceinline__ void fx_sync() { __syncthreads(); }
+
+// One thread per sample: physics_step on AoS states (physics.hpp:149-179).
+__global__ __launch_bounds__(256) void physics_fixture_kernel(const MdnPhysicsState* __restrict__ in,
+                                                              const float* __restrict__ actions,
+                                                              const float* __restrict__ winds, MdnPhysicsParams P,
+                                                              MdnPhysicsState* __restrict__ out, uint64_t n) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    State s, nx;
+    const float* src = &in[i].position[0];
+    float* d = &s.p[0];
+#pragma unroll
+    for (int j = 0; j < 17; j++) d[j] = src[j];
+    float act[4], wind[3];
+#pragma unroll
+    for (int j = 0; j < 4; j++) act[j] = actions[4 * i + j];
+#pragma unroll
+    for (int j = 0; j < 3; j++) wind[j] = winds[3 * i + j];
+    physics_step(P, s, act, wind, nx);
+    float* dst = &out[i].position[0];
+    const float* o = &nx.p[0];
+#pragma unroll
+    for (int j = 0; j < 17; j++) dst[j] = o[j];
+}
+
+// One workgroup per world: obstacles and their centres in LDS exactly as the
+// rollout kernel holds them; threads stride over the world's rays.
+__global__ __launch_bounds__(256) void ray_fixture_kernel(const float* __restrict__ worlds,
+                                                          const float* __restrict__ rays,
+                                                          const float* __restrict__ times, uint32_t rays_per_world,
+                                                          float* __restrict__ out, uint64_t n) {
+    __shared__ float w[WORLD_WORDS + 3];
+    __shared__ float cent[48];
+    const uint64_t wi = blockIdx.x;
+    for (uint32_t i = threadIdx.x; i < WORLD_WORDS; i += 256) w[i] = worlds[wi * WORLD_WORDS + i];
+    fx_sync();
+    const uint32_t count = min(float_bits(w[160]), 16u);
+    if (threadIdx.x < count) {
+        const V c = obstacle_center(w + 10 * threadIdx.x, times[wi]);
+        cent[3 * threadIdx.x] = c.x; cent[3 * threadIdx.x + 1] = c.y; cent[3 * threadIdx.x + 2] = c.z;
+    }
+    fx_sync();
+    for (uint32_t k = threadIdx.x; k < rays_per_world; k += 256) {
+        const uint64_t i = wi * rays_per_world + k;
+        if (i >= n) break;
+        const float* r = rays + 6 * i;
+        out[i] = cast_ray(w, cent, count, mk(r[0], r[1], r[2]), mk(r[3], r[4], r[5]));
+    }
+}
+
+__global__ __launch_bounds__(256) void clearance_fixture_kernel(const float* __restrict__ worlds,
+                                                                const float* __restrict__ points,
+                                                                const float* __restrict__ times,
+                                                                float* __restrict__ out, uint64_t n) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float* w = worlds + i * WORLD_WORDS;
+    out[i] = clearance_at(w, min(float_bits(w[160]), 16u), mk(points[3 * i], points[3 * i + 1], points[3 * i + 2]), times[i]);
+}
+
+}  // namespace nav
+
+// The RAPTOR fixture needs the lane-group step of the rollout kernel, which
+// lives in rollout.hip; it is launched from there (nav_launch_raptor_fixture).
+extern "C" {
+
+hipError_t nav_launch_physics_fixture(const MdnPhysicsState* in, const float* actions, const float* winds,
+                                      const MdnPhysicsParams* P, MdnPhysicsState* out, uint64_t n, hipStream_t st) {
+    hipLaunchKernelGGL(nav::physics_fixture_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, in, actions, winds,
+                       *P, out, n);
+    return hipGetLastError();
+}
+
+hipError_t nav_launch_ray_fixture(const float* worlds, const float* rays, const float* times, uint32_t rays_per_world,
+                                  float* out, uint64_t n, hipStream_t st) {
+    const uint64_t nw = (n + rays_per_world - 1) / rays_per_world;
+    hipLaunchKernelGGL(nav::ray_fixture_kernel, dim3(uint32_t(nw)), dim3(256), 0, st, worlds, rays, times, rays_per_world,
+                       out, n);
+    return hipGetLastError();
+}
+
+hipError_t nav_launch_clearance_fixture(const float* worlds, const float* points, const float* times, float* out,
+                                        uint64_t n, hipStream_t st) {
+    hipLaunchKernelGGL(nav::clearance_fixture_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, worlds, points,
+                       times, out, n);
+    return hipGetLastError();
+}
+
+}  // extern "C"

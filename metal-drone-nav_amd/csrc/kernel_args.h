@@ -1,0 +1,98 @@
+// kernel_args.h — argument blocks and launchers shared by the kernels and
+// the host side of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mdnav_types.h"
+
+namespace nav {
+struct RolloutArgs {
+    float* state;          // [17][N]
+    uint32_t* run;         // [46][N]
+    float* world;          // [N][169]
+    float* sensors;        // [N][8][320]
+    float* poses;          // [N][8][12]
+    float* commands;       // [N][8][4]
+    const float* raptor;   // RaptorWeights, 2084 floats
+    const float* actor;    // flat actor vector (ppo.hpp:35-40)
+    const float* actor_w1t;   // W1 transposed [OBS][64]
+    const float* critic;      // flat critic vector (ppo.hpp:41-45)
+    const float* critic_w1t;  // [32][64]
+    const float* camera;      // unit pixel rays [320][3]
+    float* obs;            // [T][N][181]
+    float* co;             // [T][N][32]
+    float* actions;        // [T][N][4]
+    float* logp;           // [T][N]
+    float* values;
+    float* rewards;
+    float* next_values;
+    uint8_t* terminated;
+    uint8_t* truncated;
+    MdnSimConfig cfg;
+    MdnPhysicsParams phys;
+    uint32_t count;        // ticks in this launch
+    uint32_t horizon;      // row blocks of the rollout buffers
+};
+}  // namespace nav
+
+namespace ppo {
+struct RowArgs {
+    const float* obs;       // minibatch rows [b][OBS]
+    const float* co;        // [b][COBS]
+    const float* actions;   // [b][4]
+    const float* old_logp;  // [b]
+    const float* adv;       // [b]
+    const float* ret;       // [b]
+    const float* actor;     // flat params
+    const float* actor_w1t; // [OBS][HID]
+    const float* critic;
+    const float* critic_w1t; // [COBS][HID]
+    float* ah;      // [b][HID] actor hidden
+    float* adelta;  // [b][HID]
+    float* ch;      // [b][HID] critic hidden
+    float* cdelta;  // [b][HID]
+    float* dm;      // [b][4]
+    float* dls;     // [b][4]
+    float* dv;      // [b]
+    float* loss;    // [b][4]
+    uint32_t b;
+    float clip, vcoef, ecoef;
+};
+
+// cpu_reference.hpp:553-567 inputs for one update of both networks.
+struct AdamArgs {
+    float* actor; float* critic; float* actor_w1t; float* critic_w1t;
+    float* am; float* av; float* cm; float* cv;
+    const float* grad;   // P_TOTAL: actor, critic, metric sums
+    float* metric_row;   // [4]
+    float lr, c1, c2;    // host bias corrections 1-beta^step
+    uint32_t b;
+};
+}  // namespace ppo
+
+extern "C" {
+hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream);
+hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, hipStream_t stream);
+hipError_t nav_launch_raptor_fixture(const float* RW, const float* obs, uint32_t steps, uint32_t copies,
+                                     float* actions, float* hidden, int lanes_per_env, hipStream_t st);
+hipError_t nav_launch_physics_fixture(const MdnPhysicsState* in, const float* actions, const float* winds,
+                                      const MdnPhysicsParams* P, MdnPhysicsState* out, uint64_t n, hipStream_t st);
+hipError_t nav_launch_ray_fixture(const float* worlds, const float* rays, const float* times, uint32_t rays_per_world,
+                                  float* out, uint64_t n, hipStream_t st);
+hipError_t nav_launch_clearance_fixture(const float* worlds, const float* points, const float* times, float* out,
+                                        uint64_t n, hipStream_t st);
+hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const uint8_t* te, const uint8_t* tr,
+                          float* adv, float* ret, uint32_t horizon, uint32_t n, float gamma, float lambda,
+                          hipStream_t st);
+hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st);
+hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st);
+hipError_t ppo_launch_grads(const float* obs, const float* co, const float* ah, const float* adelta, const float* ch,
+                            const float* cdelta, const float* dm, const float* dls, const float* dv, const float* loss,
+                            float* part, float* grad, uint32_t b, hipStream_t st);
+hipError_t ppo_launch_adam(const ppo::AdamArgs* a, hipStream_t st);
+hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* aw, float* cw, hipStream_t st);
+hipError_t ppo_launch_metric_mean(const float* rows, float* mean, uint32_t updates, hipStream_t st);
+uint32_t ppo_partial_stride();
+}

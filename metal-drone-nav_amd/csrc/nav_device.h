@@ -1,0 +1,540 @@
+// nav_device.h — device functions of the environment step for gfx950.
+//
+// Register-resident state, one env per lane group.  Arithmetic follows the
+// reference expressions term by term (no re-association, contraction off) so
+// the device and the CPU oracle round identically; file:line cites the
+// reference function each block follows.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "mdnav_math.h"
+#include "mdnav_types.h"
+
+namespace nav {
+using namespace mdn;
+
+constexpr uint32_t PIX = MDN_SENSOR_PIXELS;
+constexpr uint32_t POOL = MDN_POOLED_FEATURES;
+constexpr uint32_t OBS = MDN_ACTOR_OBS_POOLED;
+constexpr uint32_t COBS = MDN_CRITIC_OBS;
+constexpr uint32_t HID = MDN_HIDDEN;
+constexpr float LOG_TWO_PI = 1.8378770664093453f;
+
+// Word offsets of SimRun (main.mm:454-460); the run block is stored as
+// struct-of-arrays run[word][env].
+enum RunWord : uint32_t {
+    RW_HIDDEN = 0, RW_MOTORS = 16, RW_PREV_NAV = 20, RW_DESIRED_VEL = 24, RW_YAW = 27, RW_RNG = 28,
+    RW_STEPS = 29, RW_PATH = 30, RW_ELAPSED = 31, RW_PEAK_SPEED = 32, RW_MIN_CLEARANCE = 33,
+    RW_INITIAL_DISTANCE = 34, RW_SUCCESSES = 35, RW_COLLISIONS = 36, RW_TIMEOUTS = 37, RW_EPISODES = 38,
+    RW_SUCCESS_TIME = 39, RW_TOTAL_PATH = 40, RW_TOTAL_ELAPSED = 41, RW_FINAL_PROGRESS = 42, RW_REF_POS = 43,
+    RW_COUNT = 46
+};
+constexpr uint32_t STATE_WORDS = 17;
+constexpr uint32_t WORLD_WORDS = 169;
+
+struct State { float p[3], q[4], v[3], w[3], rpm[4]; };
+
+struct Run {
+    float hidden[16], motors[4], prev_nav[4], desired_vel[3], yaw;
+    uint32_t rng, steps;
+    float path, elapsed, peak_speed, min_clearance, initial_distance;
+    uint32_t successes, collisions, timeouts, episodes;
+    float success_time, total_path, total_elapsed, final_progress, ref_pos[3];
+};
+static_assert(sizeof(Run) == RW_COUNT * 4, "Run block");
+static_assert(sizeof(State) == STATE_WORDS * 4, "State block");
+
+// ---------------------------------------------------------------- RNG
+// world.hpp:30-31
+__device__ __forceinline__ uint32_t xs(uint32_t& s) { s ^= s << 13; s ^= s >> 17; s ^= s << 5; return s; }
+__device__ __forceinline__ float ur(uint32_t& s) { return float(xs(s) >> 8) * (1.0f / 16777216.0f); }
+// sim.metal:49
+__device__ __forceinline__ float normal_draw(uint32_t& rng) {
+    const float u = max_f(ur(rng), 1e-7f);
+    const float v = ur(rng);
+    return sqrt_f(-2.0f * log_f(u)) * cos_f(6.28318530718f * v);
+}
+
+// ---------------------------------------------------------------- geometry
+struct V { float x, y, z; };
+__device__ __forceinline__ V mk(float x, float y, float z) { V r; r.x = x; r.y = y; r.z = z; return r; }
+__device__ __forceinline__ float dot3(V a, V b) { return a.x * b.x + a.y * b.y + a.z * b.z; }
+__device__ __forceinline__ float len3(V a) { return sqrt_f(dot3(a, a)); }
+__device__ __forceinline__ V sub3(V a, V b) { return mk(a.x - b.x, a.y - b.y, a.z - b.z); }
+
+// Obstacle record as laid out in WWorld (world.hpp:28): kind, centre, size, velocity.
+__device__ __forceinline__ V obstacle_center(const float* o, float t) {
+    const uint32_t kind = float_bits(o[0]);
+    if (kind == 3u) {  // world.hpp:33-38
+        const V vel = mk(o[7], o[8], o[9]);
+        const float speed = len3(vel), amplitude = o[5];
+        if (speed <= 1e-8f || amplitude <= 1e-8f) return mk(o[1], o[2], o[3]);
+        const float offset = amplitude * sin_f(t * speed / amplitude + o[6]) / speed;
+        return mk(o[1] + vel.x * offset, o[2] + vel.y * offset, o[3] + vel.z * offset);
+    }
+    return mk(o[1] + t * o[7], o[2] + t * o[8], o[3] + t * o[9]);  // world.hpp:40
+}
+
+// world.hpp:42-47
+__device__ __forceinline__ float hit_sphere(V p, V d, V c, float r) {
+    const V q = sub3(p, c);
+    const float b = dot3(q, d), k = dot3(q, q) - r * r, disc = b * b - k;
+    if (disc < 0) return 1000;
+    const float lo = -b - sqrt_f(disc), hi = -b + sqrt_f(disc);
+    return lo >= 0 ? lo : (hi >= 0 ? hi : 1000);
+}
+
+// Slab test of world.hpp:48-57 with the per-ray reciprocal (1/d computed
+// once per ray; the reference divides per box).
+struct Slab { float inv[3]; bool par[3]; };
+__device__ __forceinline__ Slab make_slab(V d) {
+    Slab s;
+    const float dd[3] = {d.x, d.y, d.z};
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        s.par[j] = fabs_f(dd[j]) < 1e-8f;
+        s.inv[j] = s.par[j] ? 0.0f : 1.0f / dd[j];
+    }
+    return s;
+}
+__device__ __forceinline__ float hit_box(V p, const Slab& sl, V c, V e) {
+    float lo = -1e20f, hi = 1e20f;
+    const float pp[3] = {p.x - c.x, p.y - c.y, p.z - c.z}, ee[3] = {e.x, e.y, e.z};
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        if (sl.par[j]) {
+            if (fabs_f(pp[j]) > ee[j]) return 1000;
+        } else {
+            const float a = (-ee[j] - pp[j]) * sl.inv[j], b = (ee[j] - pp[j]) * sl.inv[j];
+            lo = fmax_f(lo, fmin_f(a, b));
+            hi = fmin_f(hi, fmax_f(a, b));
+        }
+    }
+    if (hi < fmax_f(lo, 0.0f)) return 1000;
+    return lo >= 0 ? lo : hi;
+}
+// world.hpp:58-70
+__device__ __noinline__ float hit_cylinder(V p, V d, V c, float r, float h) {
+    const V q = sub3(p, c);
+    const float a = d.x * d.x + d.y * d.y, b = q.x * d.x + q.y * d.y, k = q.x * q.x + q.y * q.y - r * r;
+    float best = 1000;
+    const float disc = b * b - a * k;
+    if (a > 1e-10f && disc >= 0) {
+        const float r0 = (-b - sqrt_f(disc)) / a, r1 = (-b + sqrt_f(disc)) / a;
+        if (r0 >= 0 && fabs_f(q.z + r0 * d.z) <= h) best = fmin_f(best, r0);
+        if (r1 >= 0 && fabs_f(q.z + r1 * d.z) <= h) best = fmin_f(best, r1);
+    }
+    if (fabs_f(d.z) > 1e-8f)
+        for (int sign = -1; sign <= 1; sign += 2) {
+            const float t = (float(sign) * h - q.z) / d.z;
+            const float x = q.x + t * d.x, y = q.y + t * d.y;
+            if (t >= 0 && x * x + y * y <= r * r) best = fmin_f(best, t);
+        }
+    return best;
+}
+
+// world.hpp:71-83 — obstacles in LDS (`world` = WWorld words), centres for
+// the current time precomputed in `centers`.
+__device__ __forceinline__ float cast_ray(const float* world, const float* centers, uint32_t count, V p, V d) {
+    const Slab sl = make_slab(d);
+    float best = 12;
+    best = fmin_f(best, hit_box(p, sl, mk(6, 0, 2.5f), mk(8, 5, 2.5f)));
+    for (uint32_t i = 0; i < count; i++) {
+        const float* o = world + 10 * i;
+        const uint32_t kind = float_bits(o[0]);
+        const V c = mk(centers[3 * i], centers[3 * i + 1], centers[3 * i + 2]);
+        float t = 1000;
+        if (kind == 0u) t = hit_box(p, sl, c, mk(o[4], o[5], o[6]));
+        else if (kind == 1u || kind == 3u) t = hit_sphere(p, d, c, o[4]);
+        else if (kind == 2u) t = hit_cylinder(p, d, c, o[4], o[6]);
+        best = fmin_f(best, t);
+    }
+    return fmax_f(0.0f, best);
+}
+
+// world.hpp:84-99
+__device__ __forceinline__ float clearance_at(const float* world, uint32_t count, V p, float time) {
+    float best = fmin_f(fmin_f(p.x + 2, 14 - p.x), fmin_f(fmin_f(p.y + 5, 5 - p.y), fmin_f(p.z, 5 - p.z))) - 0.18f;
+    for (uint32_t i = 0; i < count; i++) {
+        const float* o = world + 10 * i;
+        const uint32_t kind = float_bits(o[0]);
+        const V q = sub3(p, obstacle_center(o, time));
+        float distance;
+        if (kind == 1u || kind == 3u) distance = len3(q) - o[4];
+        else if (kind == 2u) {
+            const float a = sqrt_f(q.x * q.x + q.y * q.y) - o[4], b = fabs_f(q.z) - o[6];
+            distance = sqrt_f(fmax_f(a, 0.0f) * fmax_f(a, 0.0f) + fmax_f(b, 0.0f) * fmax_f(b, 0.0f)) + fmin_f(fmax_f(a, b), 0.0f);
+        } else {
+            const V k = mk(fabs_f(q.x) - o[4], fabs_f(q.y) - o[5], fabs_f(q.z) - o[6]);
+            distance = len3(mk(fmax_f(k.x, 0.0f), fmax_f(k.y, 0.0f), fmax_f(k.z, 0.0f))) + fmin_f(fmax_f(k.x, fmax_f(k.y, k.z)), 0.0f);
+        }
+        best = fmin_f(best, distance - 0.18f);
+    }
+    return best;
+}
+
+// sim.metal:43-48
+__device__ __forceinline__ void rotation(const float q[4], float r[9]) {
+    const float w = q[0], x = q[1], y = q[2], z = q[3];
+    r[0] = 1 - 2 * (y * y + z * z); r[1] = 2 * (x * y - w * z); r[2] = 2 * (x * z + w * y);
+    r[3] = 2 * (x * y + w * z); r[4] = 1 - 2 * (x * x + z * z); r[5] = 2 * (y * z - w * x);
+    r[6] = 2 * (x * z - w * y); r[7] = 2 * (y * z + w * x); r[8] = 1 - 2 * (x * x + y * y);
+}
+
+// ---------------------------------------------------------------- plant
+// physics.hpp:60-112
+__device__ __forceinline__ void derivative(const MdnPhysicsParams& P, const State& s, const float sp[4],
+                                           const float wind[3], State& d) {
+    float thrust[3] = {0, 0, 0}, torque[3] = {0, 0, 0};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float speed = s.rpm[r];
+        const float* c = &P.rotor_thrust_coefficients[3 * r];
+        const float magnitude = c[0] + c[1] * speed + c[2] * speed * speed;
+        float rt[3];
+        const float* dir = &P.rotor_thrust_directions[3 * r];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            rt[i] = dir[i] * magnitude;
+            thrust[i] += rt[i];
+            torque[i] += P.rotor_torque_directions[3 * r + i] * magnitude * P.rotor_torque_constants[r];
+        }
+        const float* a = &P.rotor_positions[3 * r];
+        const float arm0 = a[1] * rt[2] - a[2] * rt[1];
+        const float arm1 = a[2] * rt[0] - a[0] * rt[2];
+        const float arm2 = a[0] * rt[1] - a[1] * rt[0];
+        torque[0] += arm0; torque[1] += arm1; torque[2] += arm2;
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) d.p[i] = s.v[i];
+    const float* q = s.q;
+    const float* w = s.w;
+    d.q[0] = -q[1] * w[0] - q[2] * w[1] - q[3] * w[2];
+    d.q[1] = q[0] * w[0] + q[2] * w[2] - q[3] * w[1];
+    d.q[2] = q[0] * w[1] + q[3] * w[0] - q[1] * w[2];
+    d.q[3] = q[0] * w[2] + q[1] * w[1] - q[2] * w[0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d.q[i] *= 0.5f;
+    // rotate_body_to_world (physics.hpp:51-58)
+    const float tx = 2.0f * (q[2] * thrust[2] - q[3] * thrust[1]);
+    const float ty = 2.0f * (q[3] * thrust[0] - q[1] * thrust[2]);
+    const float tz = 2.0f * (q[1] * thrust[1] - q[2] * thrust[0]);
+    d.v[0] = thrust[0] + q[0] * tx + q[2] * tz - q[3] * ty;
+    d.v[1] = thrust[1] + q[0] * ty + q[3] * tx - q[1] * tz;
+    d.v[2] = thrust[2] + q[0] * tz + q[1] * ty - q[2] * tx;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) d.v[i] = d.v[i] / P.mass + P.gravity_world[i] + wind[i] / P.mass;
+    float am[3] = {0, 0, 0};
+#pragma unroll
+    for (int row = 0; row < 3; ++row)
+#pragma unroll
+        for (int col = 0; col < 3; ++col) am[row] += P.inertia[3 * row + col] * w[col];
+    const float g0 = w[1] * am[2] - w[2] * am[1];
+    const float g1 = w[2] * am[0] - w[0] * am[2];
+    const float g2 = w[0] * am[1] - w[1] * am[0];
+    am[0] = torque[0] - g0; am[1] = torque[1] - g1; am[2] = torque[2] - g2;
+#pragma unroll
+    for (int row = 0; row < 3; ++row) {
+        d.w[row] = 0.0f;
+#pragma unroll
+        for (int col = 0; col < 3; ++col) d.w[row] += P.inertia_inverse[3 * row + col] * am[col];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float tau = sp[r] >= s.rpm[r] ? P.rotor_time_constants_rising[r] : P.rotor_time_constants_falling[r];
+        d.rpm[r] = (sp[r] - s.rpm[r]) / tau;
+    }
+}
+
+__device__ __forceinline__ void axpy_state(const State& s, const State& d, float scale, State& out) {
+    const float* a = &s.p[0];
+    const float* b = &d.p[0];
+    float* o = &out.p[0];
+#pragma unroll
+    for (int i = 0; i < 17; ++i) o[i] = a[i] + scale * b[i];
+}
+
+// physics.hpp:122-179
+__device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const State& s, const float action[4],
+                                             const float wind[3], State& next) {
+    float sp[4];
+    const float half = (P.action_max - P.action_min) * 0.5f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float a = action[i];
+        if (a < -1.0f) a = -1.0f;
+        if (a > 1.0f) a = 1.0f;
+        sp[i] = a * half + P.action_min + half;
+    }
+    State k1, k2, k3, k4, tmp;
+    derivative(P, s, sp, wind, k1);
+    axpy_state(s, k1, 0.5f * P.dt, tmp);
+    derivative(P, tmp, sp, wind, k2);
+    axpy_state(s, k2, 0.5f * P.dt, tmp);
+    derivative(P, tmp, sp, wind, k3);
+    axpy_state(s, k3, P.dt, tmp);
+    derivative(P, tmp, sp, wind, k4);
+    const float* a0 = &s.p[0];
+    const float* a1 = &k1.p[0];
+    const float* a2 = &k2.p[0];
+    const float* a3 = &k3.p[0];
+    const float* a4 = &k4.p[0];
+    float* o = &next.p[0];
+#pragma unroll
+    for (int i = 0; i < 17; ++i) o[i] = a0[i] + P.dt * (a1[i] + 2.0f * a2[i] + 2.0f * a3[i] + a4[i]) / 6.0f;
+    const float norm = sqrt_f(next.q[0] * next.q[0] + next.q[1] * next.q[1] + next.q[2] * next.q[2] + next.q[3] * next.q[3]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) next.q[i] /= norm;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (next.p[i] < -P.position_limit) next.p[i] = -P.position_limit;
+        if (next.p[i] > P.position_limit) next.p[i] = P.position_limit;
+        if (next.v[i] < -P.velocity_limit) next.v[i] = -P.velocity_limit;
+        if (next.v[i] > P.velocity_limit) next.v[i] = P.velocity_limit;
+        if (next.w[i] < -P.angular_velocity_limit) next.w[i] = -P.angular_velocity_limit;
+        if (next.w[i] > P.angular_velocity_limit) next.w[i] = P.angular_velocity_limit;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (next.rpm[i] < P.action_min) next.rpm[i] = P.action_min;
+        if (next.rpm[i] > P.action_max) next.rpm[i] = P.action_max;
+    }
+}
+
+// ---------------------------------------------------------------- world generation
+// world.hpp:104-318, written over a WWorld word array; multi-draw argument
+// lists are sequenced left to right.
+struct WorldGen {
+    float* w;  // WORLD_WORDS words
+    __device__ uint32_t count() const { return float_bits(w[160]); }
+    __device__ void set_count(uint32_t c) { w[160] = bits_float(c); }
+    __device__ float goal(int j) const { return w[163 + j]; }
+    __device__ void add(uint32_t kind, V c, V e, V v) {
+        const uint32_t n = count();
+        if (n >= 16) return;
+        float* o = w + 10 * n;
+        o[0] = bits_float(kind);
+        o[1] = c.x; o[2] = c.y; o[3] = c.z;
+        o[4] = e.x; o[5] = e.y; o[6] = e.z;
+        o[7] = v.x; o[8] = v.y; o[9] = v.z;
+        set_count(n + 1);
+    }
+    __device__ void box(V c, V e) { add(0, c, e, mk(0, 0, 0)); }
+    __device__ void table(float x, float y, float hx, float hy, float top) {
+        const float slab = 0.08f, underside = top - slab;
+        box(mk(x, y, top), mk(hx, hy, slab));
+        const float lx = hx - 0.12f, ly = hy - 0.12f, leg = 0.08f;
+        const float lcz = underside * 0.5f, lhz = underside * 0.5f;
+        box(mk(x - lx, y - ly, lcz), mk(leg, leg, lhz));
+        box(mk(x - lx, y + ly, lcz), mk(leg, leg, lhz));
+        box(mk(x + lx, y - ly, lcz), mk(leg, leg, lhz));
+        box(mk(x + lx, y + ly, lcz), mk(leg, leg, lhz));
+    }
+    __device__ float route_y(float x, float distance) const { return goal(1) * (x / distance); }
+    __device__ void doorway(float wall_x, float gy, float gz, float hg, float hgz) {
+        const float low_y = gy - hg, high_y = gy + hg, low_z = gz - hgz, high_z = gz + hgz, whx = 0.12f;
+        box(mk(wall_x, (-5.0f + low_y) * 0.5f, 2.5f), mk(whx, (low_y + 5.0f) * 0.5f, 2.5f));
+        box(mk(wall_x, (high_y + 5.0f) * 0.5f, 2.5f), mk(whx, (5.0f - high_y) * 0.5f, 2.5f));
+        box(mk(wall_x, 0, low_z * 0.5f), mk(whx, 5.0f, low_z * 0.5f));
+        box(mk(wall_x, 0, (high_z + 5.0f) * 0.5f), mk(whx, 5.0f, (5.0f - high_z) * 0.5f));
+    }
+    __device__ void goal_span(uint32_t& rng, float distance) {
+        const float span = fmin_f(fmax_f(distance, 3.0f), 10.0f);
+        w[163] = span * (0.90f + 0.10f * ur(rng));
+        w[164] = (ur(rng) - 0.5f) * 1.20f;
+        w[165] = 1.10f + 0.80f * ur(rng);
+    }
+    // Like wgenerate, slots beyond the new count keep their previous contents.
+    __device__ void generate(uint32_t seed, uint32_t family, float distance) {
+        uint32_t rng = seed ? seed : 1;
+        w[161] = bits_float(seed);
+        w[162] = bits_float(family);
+        set_count(family == 0 ? 0 : 8);
+        w[163] = distance;
+        w[164] = (ur(rng) - 0.5f) * 2;
+        w[165] = 1.5f + (ur(rng) - 0.5f) * 0.8f;
+        if (family == 4) {  // world.hpp:138-147
+            set_count(0);
+            const float wall_x = distance * (0.42f + 0.16f * ur(rng));
+            const float rf = wall_x / distance;
+            const float gy = goal(1) * rf + (ur(rng) - 0.5f) * 1.20f;
+            const float hg = 0.40f + 0.30f * ur(rng);
+            const float rz = 1.5f + (goal(2) - 1.5f) * rf;
+            const float gz = rz + (ur(rng) - 0.5f) * 0.20f;
+            const float hgz = 0.65f + 0.25f * ur(rng);
+            doorway(wall_x, gy, gz, hg, hgz);
+            return;
+        }
+        if (family == 5) {  // world.hpp:161-176
+            set_count(0);
+            const float x = distance * (0.45f + 0.10f * ur(rng));
+            const float y = route_y(x, distance) + (ur(rng) - 0.5f) * 0.20f;
+            if (ur(rng) < 0.5f) {
+                const float hx = 0.55f + 0.20f * ur(rng);
+                const float hy = 0.75f + 0.20f * ur(rng);
+                const float top = 1.55f + 0.50f * ur(rng);
+                table(x, y, hx, hy, top);
+            } else {
+                const float hx = 0.60f + 0.20f * ur(rng);
+                const float hy = 0.80f + 0.20f * ur(rng);
+                const float height = 1.35f + 0.80f * ur(rng);
+                box(mk(x, y, height * 0.5f), mk(hx, hy, height * 0.5f));
+            }
+            return;
+        }
+        if (family == 6) {  // world.hpp:177-201
+            set_count(0);
+            const float table_x = distance * (0.46f + 0.08f * ur(rng));
+            const float table_y = route_y(table_x, distance) + (ur(rng) - 0.5f) * 0.16f;
+            const float thx = 0.58f + 0.10f * ur(rng);
+            const float thy = 0.76f + 0.10f * ur(rng);
+            const float ttop = 1.62f + 0.42f * ur(rng);
+            table(table_x, table_y, thx, thy, ttop);
+            const float counter_x = distance * 0.22f;
+            const float counter_y = route_y(counter_x, distance) - 1.30f;
+            const float counter_h = 1.55f + 0.45f * ur(rng);
+            box(mk(counter_x, counter_y, counter_h * 0.5f), mk(0.30f, 0.50f, counter_h * 0.5f));
+            const float sphere_x = distance * 0.72f;
+            const float sphere_y = route_y(sphere_x, distance) + 1.35f;
+            const float sphere_r = 0.34f + 0.10f * ur(rng);
+            const float sphere_z = 1.05f + 1.10f * ur(rng);
+            const float sign = ur(rng) < 0.5f ? -1.0f : 1.0f;
+            const float sphere_vy = sign * (0.18f + 0.16f * ur(rng));
+            add(1, mk(sphere_x, sphere_y, sphere_z), mk(sphere_r, sphere_r, sphere_r), mk(0, sphere_vy, 0));
+            const float pole_r0 = 0.20f + 0.08f * ur(rng);
+            const float pole_r1 = 0.20f + 0.08f * ur(rng);
+            add(2, mk(distance * 0.34f, route_y(distance * 0.34f, distance) + 2.05f, 2.5f), mk(pole_r0, pole_r0, 2.5f), mk(0, 0, 0));
+            add(2, mk(distance * 0.82f, route_y(distance * 0.82f, distance) - 2.05f, 2.5f), mk(pole_r1, pole_r1, 2.5f), mk(0, 0, 0));
+            const float low_box_x = distance * 0.74f;
+            const float low_box_y = route_y(low_box_x, distance) - 0.88f;
+            box(mk(low_box_x, low_box_y, 0.48f), mk(0.34f, 0.30f, 0.48f));
+            return;
+        }
+        if (family == 8) {  // world.hpp:148-160
+            set_count(0);
+            for (uint32_t door = 0; door < 2; door++) {
+                const float u0 = ur(rng);
+                const float fraction = door == 0 ? 0.33f + 0.02f * (u0 - 0.5f) : 0.67f + 0.02f * (u0 - 0.5f);
+                const float wall_x = distance * fraction;
+                const float rf = wall_x / distance;
+                const float gy = route_y(wall_x, distance) + (ur(rng) - 0.5f) * 1.00f;
+                const float rz = 1.5f + (goal(2) - 1.5f) * rf;
+                const float gz = rz + (ur(rng) - 0.5f) * 0.24f;
+                const float hg = 0.40f + 0.30f * ur(rng);
+                const float hgz = 0.65f + 0.25f * ur(rng);
+                doorway(wall_x, gy, gz, hg, hgz);
+            }
+            return;
+        }
+        if (family == 10 || family == 11) {  // world.hpp:202-222
+            set_count(0);
+            const float drone_speed = 1.5f;
+            uint32_t tr = seed ^ 0x9e3779b9u;
+            if (tr == 0) tr = 1;
+            const float lateral = (ur(tr) - 0.5f) * 0.20f;
+            const float vertical = (ur(tr) - 0.5f) * 0.16f;
+            const uint32_t speed_choice = xs(tr) % 3;
+            const float threat_speed = speed_choice == 0 ? 0.5f : (speed_choice == 1 ? 1.0f : 2.0f);
+            const float nominal_ttc = 0.7f + 0.8f * ur(tr);
+            const float combined_radius = 0.18f + 0.35f;
+            V center, velocity = mk(0, 0, 0);
+            if (family == 10) {
+                center = mk((drone_speed + threat_speed) * nominal_ttc + combined_radius, lateral, 1.5f + vertical);
+                velocity.x = -threat_speed;
+            } else {
+                center = mk(drone_speed * nominal_ttc, -threat_speed * nominal_ttc + lateral, 1.5f + vertical);
+                velocity.y = threat_speed;
+            }
+            w[163] = 4.0f; w[164] = 0.0f; w[165] = 1.5f;
+            add(1, center, mk(0.35f, 0.35f, 0.35f), velocity);
+            return;
+        }
+        if (family == 14) {  // world.hpp:226-241
+            set_count(0);
+            const float difficulty = ur(rng);
+            goal_span(rng, distance);
+            const float wall_x = goal(0) * (0.24f + 0.04f * ur(rng));
+            const float gap_x = goal(0) * (0.70f + 0.08f * difficulty);
+            const float lane_width = 1.80f - 0.80f * difficulty;
+            const float lane_edge = 5.0f - lane_width;
+            const float wall_y = (-5.0f + lane_edge) * 0.5f;
+            const float wall_half_y = (lane_edge + 5.0f) * 0.5f;
+            box(mk(wall_x, wall_y, 2.5f), mk(0.15f, wall_half_y, 2.5f));
+            box(mk((wall_x + gap_x) * 0.5f, lane_edge + 0.03f, 2.5f), mk((gap_x - wall_x) * 0.5f + 0.15f, 0.15f, 2.5f));
+            return;
+        }
+        if (family == 15) {  // world.hpp:242-269
+            set_count(0);
+            const float difficulty = ur(rng);
+            goal_span(rng, distance);
+            const float wall_1 = goal(0) * (0.16f + 0.02f * ur(rng));
+            const float wall_2 = goal(0) * 0.85f;
+            const float gap_1 = -(0.60f + 0.80f * difficulty);
+            const float gap_2 = +(0.60f + 0.80f * difficulty);
+            const float gap_half = 0.85f - 0.30f * difficulty;
+            const float gap_half_z = 0.85f - 0.10f * difficulty;
+            doorway(wall_1, gap_1, 1.50f, gap_half, gap_half_z);
+            doorway(wall_2, gap_2, 1.50f, gap_half, gap_half_z);
+            const float table_x = goal(0) * 0.50f;
+            const float table_y = (ur(rng) - 0.5f) * 0.20f;
+            const float table_half_x = fmin_f(0.45f, goal(0) * 0.06f);
+            const float table_half_y = 0.60f + 0.20f * difficulty;
+            const float table_top = 1.45f + 0.25f * difficulty;
+            table(table_x, table_y, table_half_x, table_half_y, table_top);
+            box(mk(goal(0) * 0.38f, 3.75f, 0.55f), mk(0.22f, 0.35f, 0.55f));
+            box(mk(goal(0) * 0.50f, -3.80f, 0.80f), mk(0.25f, 0.35f, 0.80f));
+            box(mk(goal(0) * 0.62f, 3.70f, 0.50f), mk(0.22f, 0.40f, 0.50f));
+            return;
+        }
+        if (family == 16) {  // world.hpp:270-291
+            set_count(0);
+            const float difficulty = ur(rng);
+            goal_span(rng, distance);
+            const float low_x = goal(0) * (0.14f + 0.02f * (1.0f - difficulty));
+            const float overhead_x = goal(0) * (0.46f + 0.02f * difficulty);
+            const float choice_x = goal(0) * (0.76f + 0.02f * difficulty);
+            const float low_top = 1.50f + 0.25f * difficulty;
+            const float overhead_bottom = 2.80f - 0.20f * difficulty;
+            const float choice_half_z = 0.10f + 0.05f * difficulty;
+            box(mk(low_x, 0, low_top * 0.5f), mk(0.12f, 5.0f, low_top * 0.5f));
+            const float overhead_half_z = (5.0f - overhead_bottom) * 0.5f;
+            box(mk(overhead_x, 0, overhead_bottom + overhead_half_z), mk(0.12f, 5.0f, overhead_half_z));
+            box(mk(choice_x, 0, 2.0f + choice_half_z), mk(0.10f, 5.0f, choice_half_z));
+            return;
+        }
+        // world.hpp:311-317: sixteen random slots, the first eight live
+        for (uint32_t i = 0; i < 16; i++) {
+            float* o = w + 10 * i;
+            o[0] = bits_float(family == 2 ? 2u : (family == 3 ? 1u : 0u));
+            o[1] = 1.2f + ur(rng) * fmax_f(0.1f, distance - 2.2f);
+            o[2] = (ur(rng) - 0.5f) * 7;
+            o[3] = family == 2 ? 2.5f : 0.6f + ur(rng) * 3;
+            o[4] = 0.2f + ur(rng) * 0.35f;
+            o[5] = 0.3f + ur(rng) * 0.55f;
+            o[6] = family == 2 ? 2.5f : 0.2f + ur(rng) * 0.75f;
+            o[7] = 0;
+            o[8] = family == 3 ? (ur(rng) - 0.5f) * 0.8f : 0;
+            o[9] = 0;
+        }
+    }
+};
+
+// world.hpp:293-298
+__device__ __forceinline__ uint32_t training_family(uint32_t family, uint32_t& rng) {
+    if (family == 7) return xs(rng) % 7;
+    if (family == 9 || family == 12) {
+        const uint32_t choice = xs(rng) % 4;
+        return choice < 2 ? 4 : (choice == 2 ? 5 : xs(rng) % 7);
+    }
+    if (family == 13) {
+        const uint32_t choice = xs(rng) % 6;
+        if (choice < 2) return 4;
+        if (choice == 2) return 5;
+        if (choice == 3) return xs(rng) % 7;
+        return choice == 4 ? 10 : 11;
+    }
+    return family;
+}
+
+}  // namespace nav

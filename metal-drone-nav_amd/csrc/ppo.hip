@@ -1,0 +1,424 @@
+// ppo.hip — GAE, advantage normalisation and the PPO minibatch update for gfx950.
+//
+// Reductions follow one canonical order shared with the CPU oracle so both
+// round identically:
+//   * dot products accumulate from the bias, inputs ascending (ppo.hpp:65-93);
+//   * sums over minibatch rows: sequential within 256-row chunks, then
+//     sequential over chunks (a single chunk at the reference's 256-row
+//     minibatch, i.e. ppo_actor_grad_direct's order, ppo.metal:497-519);
+//   * squared gradient norm: 256 strided partials then a pairwise tree;
+//   * advantage statistics in double: chunks of 256, then over chunks.
+// The 64-wide hidden layers are evaluated on the VALU with weights as
+// wave-uniform scalar loads: one lane owns one row (forward) or one input
+// feature (weight gradient), so every accumulation is a private serial chain.
+#include <hip/hip_runtime.h>
+
+#include "mdnav_math.h"
+#include "mdnav_types.h"
+#include "kernel_args.h"
+
+namespace ppo {
+using namespace mdn;
+
+constexpr uint32_t OBS = MDN_ACTOR_OBS_POOLED;
+constexpr uint32_t COBS = MDN_CRITIC_OBS;
+constexpr uint32_t HID = MDN_HIDDEN;
+constexpr uint32_t CHUNK = 256;
+constexpr float LOG_TWO_PI = 1.8378770664093453f;
+
+constexpr uint32_t A_B1 = HID * OBS, A_W2 = A_B1 + HID, A_B2 = A_W2 + 4 * HID, A_LS = A_B2 + 4, A_COUNT = A_LS + 4;
+constexpr uint32_t C_B1 = HID * COBS, C_W2 = C_B1 + HID, C_B2 = C_W2 + HID, C_COUNT = C_B2 + 1;
+// Per-chunk partial layout: actor params, critic params, 4 metric sums.
+constexpr uint32_t P_TOTAL = A_COUNT + C_COUNT + 4;
+
+// ---------------------------------------------------------------- GAE
+// ppo.hpp:108-126 == ppo.metal:279-304: one thread per env, reverse scan.
+__global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, const float* __restrict__ v,
+                                                  const float* __restrict__ nv, const uint8_t* __restrict__ te,
+                                                  const uint8_t* __restrict__ tr, float* __restrict__ adv,
+                                                  float* __restrict__ ret, uint32_t horizon, uint32_t n,
+                                                  float gamma, float lambda) {
+    const uint32_t env = blockIdx.x * 256 + threadIdx.x;
+    if (env >= n) return;
+    float carry = 0.0f;
+    for (uint32_t rev = 0; rev < horizon; ++rev) {
+        const uint32_t t = horizon - 1 - rev;
+        const size_t k = size_t(t) * n + env;
+        const bool term = te[k] != 0;
+        const bool boundary = term || tr[k] != 0;
+        const float bootstrap = term ? 0.0f : nv[k];
+        const float delta = r[k] + gamma * bootstrap - v[k];
+        carry = delta + (boundary ? 0.0f : gamma * lambda * carry);
+        adv[k] = carry;
+        ret[k] = carry + v[k];
+    }
+}
+
+// ---------------------------------------------------------------- normalisation
+// ppo.hpp:128-140: chunk sums in double (pass 0: sum a; pass 1: sum (a-mean)^2).
+__global__ __launch_bounds__(256) void norm_chunks_kernel(const float* __restrict__ a, uint64_t count,
+                                                          double* __restrict__ part, const float* __restrict__ stats,
+                                                          int pass) {
+    const uint64_t c = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
+    if (c >= chunks) return;
+    const uint64_t end = (c + 1) * CHUNK < count ? (c + 1) * CHUNK : count;
+    double s = 0.0;
+    if (pass == 0) {
+        for (uint64_t i = c * CHUNK; i < end; ++i) s += double(a[i]);
+    } else {
+        const float mean = stats[0];
+        for (uint64_t i = c * CHUNK; i < end; ++i) {
+            const double d = double(a[i] - mean);
+            s += d * d;
+        }
+    }
+    part[c] = s;
+}
+// Sequential sum over chunks; pass 0 writes the float mean, pass 1 the
+// inverse standard deviation 1/sqrt(var + eps).
+__global__ void norm_finish_kernel(const double* __restrict__ part, uint64_t count, float* __restrict__ stats,
+                                   float eps, int pass) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
+    double s = 0.0;
+    for (uint64_t c = 0; c < chunks; ++c) s += part[c];
+    if (pass == 0) stats[0] = float(s / double(count));
+    else stats[1] = 1.0f / sqrt_f(float(s / double(count)) + eps);
+}
+__global__ __launch_bounds__(256) void norm_apply_kernel(float* __restrict__ a, uint64_t count,
+                                                         const float* __restrict__ stats) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= count) return;
+    a[i] = (a[i] - stats[0]) * stats[1];
+}
+
+// ---------------------------------------------------------------- minibatch rows
+
+
+// Forward, per-row loss/derivatives (ppo.hpp:144-181) and hidden deltas
+// (ppo.metal:470-485, 618-631); one lane per row.
+__global__ __launch_bounds__(256) void rows_kernel(RowArgs a) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= a.b) return;
+    const float* x = a.obs + size_t(n) * OBS;
+    float h[HID];
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) h[k] = a.actor[A_B1 + k];
+    for (uint32_t i = 0; i < OBS; i++) {
+        const float xi = x[i];
+        const float* w = a.actor_w1t + size_t(i) * HID;
+#pragma unroll
+        for (uint32_t k = 0; k < HID; k++) h[k] += w[k] * xi;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) h[k] = tanh_f(h[k]);
+    float mean[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        float z = a.actor[A_B2 + q];
+#pragma unroll
+        for (uint32_t k = 0; k < HID; k++) z += a.actor[A_W2 + q * HID + k] * h[k];
+        mean[q] = z;
+    }
+    const float* cx = a.co + size_t(n) * COBS;
+    float g[HID];
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) g[k] = a.critic[C_B1 + k];
+    for (uint32_t i = 0; i < COBS; i++) {
+        const float xi = cx[i];
+        const float* w = a.critic_w1t + size_t(i) * HID;
+#pragma unroll
+        for (uint32_t k = 0; k < HID; k++) g[k] += w[k] * xi;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) g[k] = tanh_f(g[k]);
+    float value = a.critic[C_B2];
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) value += a.critic[C_W2 + k] * g[k];
+
+    // sample_loss_and_grad
+    const float* act = a.actions + size_t(n) * 4;
+    const float* ls = a.actor + A_LS;
+    float logp = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        const float inv_std = exp_f(-ls[q]);
+        const float d = (act[q] - mean[q]) * inv_std;
+        logp += -0.5f * (d * d + 2.0f * ls[q] + LOG_TWO_PI);
+    }
+    const float raw = logp - a.old_logp[n];
+    const float lr = clamp_f(raw, -20.0f, 20.0f);
+    const float ratio = exp_f(lr);
+    const float adv = a.adv[n], target = a.ret[n];
+    const float clipped = clamp_f(ratio, 1.0f - a.clip, 1.0f + a.clip);
+    const float chosen = min_f(ratio * adv, clipped * adv);
+    const bool in_range = raw >= -20.0f && raw <= 20.0f;
+    const bool active = in_range && (adv >= 0.0f ? ratio <= 1.0f + a.clip : ratio >= 1.0f - a.clip);
+    const float scale = 1.0f / max_f(float(a.b), 1.0f);
+    float dmean[4], dlog[4], entropy = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        const float inv_var = exp_f(-2.0f * ls[q]);
+        const float diff = act[q] - mean[q];
+        if (active) {
+            const float dlogp = -ratio * adv * scale;
+            dmean[q] = dlogp * diff * inv_var;
+            dlog[q] = dlogp * (diff * diff * inv_var - 1.0f);
+        } else {
+            dmean[q] = 0.0f;
+            dlog[q] = 0.0f;
+        }
+        dlog[q] -= a.ecoef * scale;
+        entropy += -a.ecoef * (ls[q] + 0.5f * (1.0f + LOG_TWO_PI)) * scale;
+    }
+    const float dvalue = a.vcoef * (value - target) * scale;
+    float* lo = a.loss + size_t(n) * 4;
+    lo[0] = -chosen * scale;
+    lo[1] = 0.5f * a.vcoef * (value - target) * (value - target) * scale;
+    lo[2] = entropy;
+    lo[3] = ratio;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        a.dm[size_t(n) * 4 + q] = dmean[q];
+        a.dls[size_t(n) * 4 + q] = dlog[q];
+    }
+    a.dv[n] = dvalue;
+    float* ah = a.ah + size_t(n) * HID;
+    float* ad = a.adelta + size_t(n) * HID;
+    float* ch = a.ch + size_t(n) * HID;
+    float* cd = a.cdelta + size_t(n) * HID;
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) {
+        float d = 0.0f;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; q++) d += dmean[q] * a.actor[A_W2 + q * HID + k];
+        ah[k] = h[k];
+        ad[k] = d * (1.0f - h[k] * h[k]);
+        ch[k] = g[k];
+        cd[k] = dvalue * a.critic[C_W2 + k] * (1.0f - g[k] * g[k]);
+    }
+}
+
+// ---------------------------------------------------------------- gradient partials
+// First-layer weight gradients of one 256-row chunk: lane = input feature,
+// 64 accumulators (one per hidden unit), rows ascending; deltas are
+// wave-uniform scalar loads.  grid.x = chunk, grid.y = 0 actor / 1 critic.
+__global__ __launch_bounds__(192) void w1_grad_kernel(const float* __restrict__ obs, const float* __restrict__ co,
+                                                      const float* __restrict__ adelta,
+                                                      const float* __restrict__ cdelta, float* __restrict__ part,
+                                                      uint32_t b) {
+    const uint32_t c = blockIdx.x;
+    const bool critic = blockIdx.y == 1;
+    const uint32_t D = critic ? COBS : OBS;
+    const uint32_t i = threadIdx.x;
+    if (i >= D) return;
+    const float* X = critic ? co : obs;
+    const float* delta = critic ? cdelta : adelta;
+    float acc[HID];
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) acc[k] = 0.0f;
+    const uint32_t end = (c + 1) * CHUNK < b ? (c + 1) * CHUNK : b;
+    for (uint32_t n = c * CHUNK; n < end; n++) {
+        const float x = X[size_t(n) * D + i];
+        const float* d = delta + size_t(n) * HID;
+#pragma unroll
+        for (uint32_t k = 0; k < HID; k++) acc[k] += d[k] * x;
+    }
+    float* out = part + size_t(c) * P_TOTAL + (critic ? A_COUNT : 0);
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) out[size_t(k) * D + i] = acc[k];
+}
+
+// The remaining sums of one chunk: actor b1, W2, b2, log_std; critic b1, w2,
+// b2; the four metric sums.  One thread per output slot.
+constexpr uint32_t SMALL_SLOTS = HID + 4 * HID + 4 + 4 + HID + HID + 1 + 4;  // 461
+__global__ __launch_bounds__(512) void small_grad_kernel(const float* __restrict__ ah, const float* __restrict__ adelta,
+                                                         const float* __restrict__ ch, const float* __restrict__ cdelta,
+                                                         const float* __restrict__ dm, const float* __restrict__ dls,
+                                                         const float* __restrict__ dv, const float* __restrict__ loss,
+                                                         float* __restrict__ part, uint32_t b) {
+    const uint32_t c = blockIdx.x;
+    uint32_t s = threadIdx.x;
+    if (s >= SMALL_SLOTS) return;
+    const uint32_t begin = c * CHUNK, end = (c + 1) * CHUNK < b ? (c + 1) * CHUNK : b;
+    float acc = 0.0f;
+    size_t out;
+    float* P = part + size_t(c) * P_TOTAL;
+    if (s < HID) {  // actor b1
+        for (uint32_t n = begin; n < end; n++) acc += adelta[size_t(n) * HID + s];
+        out = A_B1 + s;
+    } else if ((s -= HID) < 4 * HID) {  // actor W2[a][h]
+        const uint32_t q = s / HID, h = s % HID;
+        for (uint32_t n = begin; n < end; n++) acc += dm[size_t(n) * 4 + q] * ah[size_t(n) * HID + h];
+        out = A_W2 + s;
+    } else if ((s -= 4 * HID) < 4) {  // actor b2
+        for (uint32_t n = begin; n < end; n++) acc += dm[size_t(n) * 4 + s];
+        out = A_B2 + s;
+    } else if ((s -= 4) < 4) {  // actor log_std
+        for (uint32_t n = begin; n < end; n++) acc += dls[size_t(n) * 4 + s];
+        out = A_LS + s;
+    } else if ((s -= 4) < HID) {  // critic b1
+        for (uint32_t n = begin; n < end; n++) acc += cdelta[size_t(n) * HID + s];
+        out = A_COUNT + C_B1 + s;
+    } else if ((s -= HID) < HID) {  // critic w2
+        for (uint32_t n = begin; n < end; n++) acc += dv[n] * ch[size_t(n) * HID + s];
+        out = A_COUNT + C_W2 + s;
+    } else if ((s -= HID) < 1) {  // critic b2
+        for (uint32_t n = begin; n < end; n++) acc += dv[n];
+        out = A_COUNT + C_B2;
+    } else {  // metric sums (main.mm:941-951)
+        s -= 1;
+        for (uint32_t n = begin; n < end; n++) acc += loss[size_t(n) * 4 + s];
+        out = A_COUNT + C_COUNT + s;
+    }
+    P[out] = acc;
+}
+
+// Sequential sum over chunks: grad[p] = 0 + part[0][p] + part[1][p] + ...
+__global__ __launch_bounds__(256) void chunk_reduce_kernel(const float* __restrict__ part, float* __restrict__ grad,
+                                                           uint32_t chunks) {
+    const uint32_t p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= P_TOTAL) return;
+    float total = 0.0f;
+    for (uint32_t c = 0; c < chunks; c++) total += part[size_t(c) * P_TOTAL + p];
+    grad[p] = total;
+}
+
+// ---------------------------------------------------------------- clip + Adam
+// cpu_reference.hpp:553-567 + log-std clamp (603); block 0 = actor, 1 = critic.
+// Also refreshes the transposed first-layer copy and the metric row.
+
+__global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
+    const bool critic = blockIdx.x == 1;
+    const uint32_t P = critic ? C_COUNT : A_COUNT;
+    float* params = critic ? a.critic : a.actor;
+    float* m = critic ? a.cm : a.am;
+    float* v = critic ? a.cv : a.av;
+    const float* g = a.grad + (critic ? A_COUNT : 0);
+    __shared__ float part[256];
+    const uint32_t t = threadIdx.x;
+    float s = 0.0f;
+    for (uint32_t i = t; i < P; i += 256) s += g[i] * g[i];
+    part[t] = s;
+    __syncthreads();
+    for (uint32_t stride = 128; stride > 0; stride >>= 1) {
+        if (t < stride) part[t] = part[t] + part[t + stride];
+        __syncthreads();
+    }
+    const float norm = sqrt_f(part[0] + 1.0e-20f);
+    const float scale = min_f(1.0f, 0.5f / norm);
+    const float b1 = 0.9f, b2 = 0.999f;
+    for (uint32_t i = t; i < P; i += 256) {
+        const float gi = g[i] * scale;
+        m[i] = b1 * m[i] + (1.0f - b1) * gi;
+        v[i] = b2 * v[i] + (1.0f - b2) * gi * gi;
+        const float mh = m[i] / a.c1, vh = v[i] / a.c2;
+        params[i] -= a.lr * mh / (sqrt_f(vh) + 1.0e-8f);
+    }
+    __syncthreads();
+    if (!critic) {
+        if (t < 4) params[A_LS + t] = clamp_f(params[A_LS + t], -2.0f, .5f);
+        for (uint32_t e = t; e < HID * OBS; e += 256) {
+            const uint32_t h = e / OBS, i = e % OBS;
+            a.actor_w1t[size_t(i) * HID + h] = params[e];
+        }
+        if (t == 0) {
+            const float* ms = a.grad + A_COUNT + C_COUNT;
+            a.metric_row[0] = ms[0];
+            a.metric_row[1] = ms[1];
+            a.metric_row[2] = ms[2];
+            a.metric_row[3] = ms[3] / float(a.b);
+        }
+    } else {
+        for (uint32_t e = t; e < HID * COBS; e += 256) {
+            const uint32_t h = e / COBS, i = e % COBS;
+            a.critic_w1t[size_t(i) * HID + h] = params[e];
+        }
+    }
+}
+
+// Transposed first-layer copies from the flat vectors (after uploads/init).
+__global__ __launch_bounds__(256) void transpose_w1_kernel(const float* __restrict__ actor,
+                                                           const float* __restrict__ critic, float* __restrict__ aw,
+                                                           float* __restrict__ cw) {
+    const uint32_t e = blockIdx.x * 256 + threadIdx.x;
+    if (e < HID * OBS) {
+        const uint32_t h = e / OBS, i = e % OBS;
+        aw[size_t(i) * HID + h] = actor[e];
+    }
+    if (e < HID * COBS) {
+        const uint32_t h = e / COBS, i = e % COBS;
+        cw[size_t(i) * HID + h] = critic[e];
+    }
+}
+
+// metric_mean (main.mm:952-962): sequential over updates.
+__global__ void metric_mean_kernel(const float* __restrict__ rows, float* __restrict__ mean, uint32_t updates) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    float s[4] = {0, 0, 0, 0};
+    for (uint32_t u = 0; u < updates; u++)
+        for (int k = 0; k < 4; k++) s[k] += rows[size_t(u) * 4 + k];
+    for (int k = 0; k < 4; k++) mean[k] = updates ? s[k] / float(updates) : 0.0f;
+}
+
+}  // namespace ppo
+
+// ---------------------------------------------------------------- launchers
+extern "C" {
+
+hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const uint8_t* te, const uint8_t* tr,
+                          float* adv, float* ret, uint32_t horizon, uint32_t n, float gamma, float lambda,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(ppo::gae_kernel, dim3((n + 255) / 256), dim3(256), 0, st, r, v, nv, te, tr, adv, ret, horizon, n,
+                       gamma, lambda);
+    return hipGetLastError();
+}
+
+// stats: device float[2] (mean, inv_std); part: device double[ceil(count/256)]
+hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st) {
+    const uint64_t chunks = (count + ppo::CHUNK - 1) / ppo::CHUNK;
+    const uint32_t cb = uint32_t((chunks + 255) / 256);
+    for (int pass = 0; pass < 2; pass++) {
+        hipLaunchKernelGGL(ppo::norm_chunks_kernel, dim3(cb), dim3(256), 0, st, a, count, part, stats, pass);
+        hipLaunchKernelGGL(ppo::norm_finish_kernel, dim3(1), dim3(64), 0, st, part, count, stats, eps, pass);
+    }
+    hipLaunchKernelGGL(ppo::norm_apply_kernel, dim3(uint32_t((count + 255) / 256)), dim3(256), 0, st, a, count, stats);
+    return hipGetLastError();
+}
+
+hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st) {
+    hipLaunchKernelGGL(ppo::rows_kernel, dim3((a->b + 255) / 256), dim3(256), 0, st, *a);
+    return hipGetLastError();
+}
+
+hipError_t ppo_launch_grads(const float* obs, const float* co, const float* ah, const float* adelta, const float* ch,
+                            const float* cdelta, const float* dm, const float* dls, const float* dv, const float* loss,
+                            float* part, float* grad, uint32_t b, hipStream_t st) {
+    const uint32_t chunks = (b + ppo::CHUNK - 1) / ppo::CHUNK;
+    hipLaunchKernelGGL(ppo::w1_grad_kernel, dim3(chunks, 2), dim3(192), 0, st, obs, co, adelta, cdelta, part, b);
+    hipLaunchKernelGGL(ppo::small_grad_kernel, dim3(chunks), dim3(512), 0, st, ah, adelta, ch, cdelta, dm, dls, dv, loss,
+                       part, b);
+    hipLaunchKernelGGL(ppo::chunk_reduce_kernel, dim3((ppo::P_TOTAL + 255) / 256), dim3(256), 0, st, part, grad, chunks);
+    return hipGetLastError();
+}
+
+hipError_t ppo_launch_adam(const ppo::AdamArgs* a, hipStream_t st) {
+    hipLaunchKernelGGL(ppo::adam_kernel, dim3(2), dim3(256), 0, st, *a);
+    return hipGetLastError();
+}
+
+hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* aw, float* cw, hipStream_t st) {
+    hipLaunchKernelGGL(ppo::transpose_w1_kernel, dim3((ppo::HID * ppo::OBS + 255) / 256), dim3(256), 0, st, actor, critic,
+                       aw, cw);
+    return hipGetLastError();
+}
+
+hipError_t ppo_launch_metric_mean(const float* rows, float* mean, uint32_t updates, hipStream_t st) {
+    hipLaunchKernelGGL(ppo::metric_mean_kernel, dim3(1), dim3(64), 0, st, rows, mean, updates);
+    return hipGetLastError();
+}
+
+uint32_t ppo_partial_stride() { return ppo::P_TOTAL; }
+
+}  // extern "C"

@@ -1,0 +1,728 @@
+// rollout.hip — batched environment step + rollout actor/critic for gfx950.
+//
+// One persistent launch runs `count` ticks of Sim::collect (main.mm:573-598):
+// per tick sim_depth, sim_observe, the actor forward, sim_act and
+// sim_advance (sim.metal:145-332) of the reference, fused.  Environments are
+// independent, so a workgroup never waits on another: each env is owned by a
+// group of G lanes of one wave for the whole launch, its state and controller
+// memory stay in registers, and its obstacles, pooled depth ring, observation
+// row and hidden activations live in LDS.  The G lanes split the data-parallel
+// parts (pooled ray blocks, hidden units, RAPTOR rows) and compute the serial
+// RK4 chain redundantly.  Every dot product keeps the reference's sequential
+// order, so results round exactly like the CPU oracle.
+#include "nav_device.h"
+#include "kernel_args.h"
+
+namespace nav {
+
+
+
+// ---------------------------------------------------------------- group helpers
+__device__ __forceinline__ void group_sync() { __syncthreads(); }
+
+__device__ __forceinline__ float fbits(uint32_t u) { return bits_float(u); }
+__device__ __forceinline__ uint32_t ubits(float f) { return float_bits(f); }
+
+// RAPTOR step over a group of G lanes (raptor.hpp:52-97): lane `lane` owns
+// input rows and GRU units lane + G*j; the dense output and the clip are
+// evaluated by every lane.  `hidden` is the full recurrent state (identical in
+// all lanes), `hu` this lane's own units.  Two group barriers; call from
+// uniform control flow with `on` masking inactive groups.
+template <int G>
+__device__ __forceinline__ void raptor_group(const float* RW, const float (&mo)[22], float (&hidden)[16],
+                                             float (&hu)[16 / G], float* sx, float* sh, uint32_t lane, bool on,
+                                             float (&act)[4]) {
+    constexpr int U = 16 / G;
+    if (on) {
+#pragma unroll
+        for (int j = 0; j < U; j++) {  // Dense 22->16 + ReLU (raptor.hpp:54-60)
+            const uint32_t row16 = lane + G * j;
+            float val = RW[352 + row16];
+#pragma unroll
+            for (int col = 0; col < 22; col++) val += RW[row16 * 22 + col] * mo[col];
+            sx[row16] = max_f(val, 0.0f);
+        }
+    }
+    group_sync();
+    float nh[U];
+    if (on) {
+        float x[16];
+#pragma unroll
+        for (int col = 0; col < 16; col++) x[col] = sx[col];
+#pragma unroll
+        for (int j = 0; j < U; j++) {  // GRU (raptor.hpp:62-84): unit u uses rows u, 16+u, 32+u
+            const uint32_t u = lane + G * j;
+            float iv[3], hv[3];
+#pragma unroll
+            for (int g3 = 0; g3 < 3; g3++) {
+                const uint32_t rowg = u + 16 * g3;
+                float ivv = RW[1904 + rowg], hvv = RW[1952 + rowg];
+#pragma unroll
+                for (int col = 0; col < 16; col++) {
+                    ivv += RW[368 + rowg * 16 + col] * x[col];
+                    hvv += RW[1136 + rowg * 16 + col] * hidden[col];
+                }
+                iv[g3] = ivv;
+                hv[g3] = hvv;
+            }
+            const float reset = sigmoid_f(iv[0] + hv[0]);
+            const float update = sigmoid_f(iv[1] + hv[1]);
+            const float cand = tanh_f(iv[2] + reset * hv[2]);
+            nh[j] = (1.0f - update) * cand + update * hu[j];
+            sh[u] = nh[j];
+        }
+    }
+    group_sync();
+    if (on) {
+#pragma unroll
+        for (int j = 0; j < U; j++) hu[j] = nh[j];
+#pragma unroll
+        for (int col = 0; col < 16; col++) hidden[col] = sh[col];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {  // output dense + clip (raptor.hpp:86-97)
+            float val = RW[2080 + q];
+#pragma unroll
+            for (int col = 0; col < 16; col++) val += RW[2016 + q * 16 + col] * hidden[col];
+            act[q] = max_f(-1.0f, min_f(1.0f, val));
+        }
+    }
+}
+
+__device__ __forceinline__ bool clean_env(const MdnSimConfig& c, uint32_t n) {
+    return c.eval == 0 && ((c.family == 12 || c.family == 13) && n % 2 == 0);  // sim.metal:17-21
+}
+
+__device__ __forceinline__ void load_state(const float* g, uint32_t N, uint32_t n, State& s) {
+    float* d = &s.p[0];
+#pragma unroll
+    for (uint32_t i = 0; i < STATE_WORDS; i++) d[i] = g[size_t(i) * N + n];
+}
+__device__ __forceinline__ void store_state(float* g, uint32_t N, uint32_t n, const State& s, uint32_t lane, uint32_t G) {
+    const float* d = &s.p[0];
+#pragma unroll
+    for (uint32_t i = 0; i < STATE_WORDS; i++)
+        if (i % G == lane) g[size_t(i) * N + n] = d[i];
+}
+__device__ __forceinline__ void load_run(const uint32_t* g, uint32_t N, uint32_t n, Run& r) {
+    uint32_t* d = reinterpret_cast<uint32_t*>(&r);
+#pragma unroll
+    for (uint32_t i = 0; i < RW_COUNT; i++) d[i] = g[size_t(i) * N + n];
+}
+__device__ __forceinline__ void store_run(uint32_t* g, uint32_t N, uint32_t n, const Run& r, uint32_t lane, uint32_t G) {
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(&r);
+#pragma unroll
+    for (uint32_t i = 0; i < RW_COUNT; i++)
+        if (i % G == lane) g[size_t(i) * N + n] = d[i];
+}
+
+// Reset bookkeeping shared by the first reset and the auto-reset
+// (sim.metal:55-94 == cpu_reference.hpp:240-273): returns the episode
+// family and world seed drawn from the env's RNG.
+__device__ __forceinline__ void reset_draw(const MdnSimConfig& c, uint32_t n, bool first, uint32_t& rng,
+                                           uint32_t& family, uint32_t& world_seed) {
+    rng = first ? c.seed + n * 747796405u + 2891336453u : rng;
+    family = training_family(c.family, rng);
+    world_seed = xs(rng);
+}
+
+// After the world is generated: wind, start pose, hover rpm, controller
+// memory, episode counters.
+__device__ __forceinline__ void reset_apply(const MdnSimConfig& c, const MdnPhysicsParams& P, const float* raptor,
+                                            uint32_t n, bool first, uint32_t rng, float* world, State& s, Run& r) {
+    world[166] = clean_env(c, n) ? 0.0f : c.wind;
+    world[167] = 0;
+    world[168] = 0;
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        s.p[j] = j == 2 ? 1.5f : 0;
+        s.v[j] = 0;
+        s.w[j] = 0;
+        r.desired_vel[j] = 0;
+        r.ref_pos[j] = s.p[j];
+    }
+    s.q[0] = 1; s.q[1] = 0; s.q[2] = 0; s.q[3] = 0;
+    const float target = P.mass * 9.81f / 4;
+    const float c0 = P.rotor_thrust_coefficients[0], c1 = P.rotor_thrust_coefficients[1], c2 = P.rotor_thrust_coefficients[2];
+    const float hover = clamp_f((-c1 + sqrt_f(c1 * c1 - 4 * c2 * (c0 - target))) / (2 * c2), P.action_min, P.action_max);
+#pragma unroll
+    for (int j = 0; j < 16; j++) r.hidden[j] = raptor[2000 + j];
+#pragma unroll
+    for (int j = 0; j < 4; j++) { s.rpm[j] = hover; r.motors[j] = 0; r.prev_nav[j] = 0; }
+    const uint32_t wfam = float_bits(world[162]);
+    if (wfam == 10 || wfam == 11) {
+        s.v[0] = c.speed;
+        r.desired_vel[0] = c.speed;
+        r.prev_nav[0] = 1.0f;
+    }
+    r.yaw = 0; r.rng = rng; r.steps = 0; r.path = 0; r.elapsed = 0; r.peak_speed = 0;
+    r.min_clearance = 12;
+    const float gx = world[163], gy = world[164], gz = world[165] - 1.5f;
+    r.initial_distance = sqrt_f(gx * gx + gy * gy + gz * gz);
+    if (first) {
+        r.successes = r.collisions = r.timeouts = r.episodes = 0;
+        r.success_time = r.total_path = r.total_elapsed = r.final_progress = 0;
+    }
+}
+
+// First reset of every env (sim_reset kernel, sim.metal:142-144): one
+// thread per env, writes straight to the global buffers.
+__global__ __launch_bounds__(64) void reset_kernel(RolloutArgs a) {
+    const uint32_t n = blockIdx.x * 64 + threadIdx.x;
+    const uint32_t N = a.cfg.n;
+    if (n >= N) return;
+    State s;
+    Run r;
+    load_run(a.run, N, n, r);
+    uint32_t rng = 0, family = 0, seed = 0;
+    reset_draw(a.cfg, n, true, rng, family, seed);
+    float* world = a.world + size_t(n) * WORLD_WORDS;
+    WorldGen wg{world};
+    wg.generate(seed, family, a.cfg.distance);
+    reset_apply(a.cfg, a.phys, a.raptor, n, true, rng, world, s, r);
+    store_state(a.state, N, n, s, 0, 1);
+    store_run(a.run, N, n, r, 0, 1);
+    for (uint32_t j = 0; j < 8 * PIX; j++) a.sensors[size_t(n) * 8 * PIX + j] = 12.0f;
+    for (uint32_t j = 0; j < 32; j++) a.commands[size_t(n) * 32 + j] = 0.0f;
+    for (uint32_t j = 0; j < 96; j++) a.poses[size_t(n) * 96 + j] = 0.0f;
+}
+
+// ---------------------------------------------------------------- rollout
+template <int G, int K>
+__global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
+    constexpr int E = 64 / G;        // envs per workgroup (one wave)
+    constexpr int U = 16 / G;        // RAPTOR units per lane
+    constexpr int HU = 64 / G;       // actor/critic hidden units per lane
+    const MdnSimConfig& C = a.cfg;
+    const MdnPhysicsParams& P = a.phys;
+    const uint32_t N = C.n;
+    const uint32_t lane = threadIdx.x % G, grp = threadIdx.x / G;
+    const uint32_t n = blockIdx.x * E + grp;
+    const bool live = n < N;
+    const uint32_t nn = live ? n : 0;
+
+    __shared__ float s_world[E][WORLD_WORDS + 3];
+    __shared__ float s_cent[E][48];
+    __shared__ float s_ring[E][K][POOL];
+    __shared__ float s_obs[E][OBS + 3];
+    __shared__ float s_co[E][COBS];
+    __shared__ float s_ah[E][HID];
+    __shared__ float s_ch[E][HID];
+    __shared__ float s_cmd[E][32];
+    __shared__ float s_x[E][16];
+    __shared__ float s_h[E][16];
+
+    float* world = s_world[grp];
+    State s;
+    Run r;
+    load_state(a.state, N, nn, s);
+    load_run(a.run, N, nn, r);
+    for (uint32_t i = lane; i < WORLD_WORDS; i += G) world[i] = a.world[size_t(nn) * WORLD_WORDS + i];
+    for (uint32_t i = lane; i < 32; i += G) s_cmd[grp][i] = a.commands[size_t(nn) * 32 + i];
+    {   // pooled ring cache: LDS slot f%K holds frame f for the last K frames
+        const int last = r.steps == 0 ? -1 : int((r.steps - 1) / C.sensor_period);
+        for (uint32_t e = lane; e < uint32_t(K) * POOL; e += G) {
+            const int j = int(e / POOL), b = int(e % POOL);
+            const int f = last - j;
+            const uint32_t slot8 = uint32_t(((f % 8) + 8) % 8), slotk = uint32_t(((f % K) + K) % K);
+            const float* src = a.sensors + (size_t(nn) * 8 + slot8) * PIX;
+            const uint32_t y = (b / 10) * 2, x = (b % 10) * 2;
+            float m = 12.0f;
+            for (uint32_t dy = 0; dy < 2; dy++)
+                for (uint32_t dx = 0; dx < 2; dx++) m = min_f(m, src[(y + dy) * 20 + x + dx]);
+            s_ring[grp][slotk][b] = m;
+        }
+    }
+    // this lane's RAPTOR units (hidden values it owns)
+    float hu[U];
+#pragma unroll
+    for (int j = 0; j < U; j++) hu[j] = bits_float(a.run[size_t(RW_HIDDEN + lane + G * j) * N + nn]);
+    const float* RW = a.raptor;
+    const float* A = a.actor;
+    const float* CR = a.critic;
+    const uint32_t a_b1 = HID * OBS, a_w2 = a_b1 + HID, a_b2 = a_w2 + 4 * HID, a_ls = a_b2 + 4;
+    const uint32_t c_b1 = HID * COBS, c_w2 = c_b1 + HID, c_b2 = c_w2 + HID;
+    const uint32_t sdelay = clean_env(C, nn) ? 0 : C.sensor_delay;
+    const uint32_t cdelay = clean_env(C, nn) ? 0 : C.command_delay;
+    group_sync();
+
+    for (uint32_t t = 0; t < a.count; t++) {
+        const uint32_t tick = t % a.horizon;
+        const size_t row = size_t(tick) * N + nn;
+        const bool active = live && !(C.eval && r.episodes);
+        const uint32_t count = min(float_bits(world[160]), 16u);  // slots of WWorld
+
+        // ---- obstacle centres at the current time (world.hpp:32-41)
+        if (active)
+            for (uint32_t i = lane; i < count; i += G) {
+                const V c = obstacle_center(world + 10 * i, r.elapsed);
+                s_cent[grp][3 * i] = c.x; s_cent[grp][3 * i + 1] = c.y; s_cent[grp][3 * i + 2] = c.z;
+            }
+        group_sync();
+
+        // ---- depth (sim.metal:145-158): each lane casts the four rays of
+        // its pooled 2x2 blocks and keeps their minimum
+        float R[9];
+        rotation(s.q, R);
+        if (active && r.steps % C.sensor_period == 0) {
+            const uint32_t fidx = r.steps / C.sensor_period;
+            const uint32_t slot8 = fidx % 8, slotk = fidx % K;
+            const float mx = 0.0f;
+            const V origin = mk(s.p[0] + mx * R[0], s.p[1] + mx * R[3], s.p[2] + mx * R[6]);
+            if (lane == 0) {
+                float* pose = a.poses + (size_t(nn) * 8 + slot8) * 12;
+                pose[0] = origin.x; pose[1] = origin.y; pose[2] = origin.z;
+#pragma unroll
+                for (int j = 0; j < 9; j++) pose[3 + j] = R[j];
+            }
+            const float noise = clean_env(C, nn) ? 0.0f : C.depth_noise;
+            const float drop = clean_env(C, nn) ? 0.0f : C.dropout;
+            float* ring = a.sensors + (size_t(nn) * 8 + slot8) * PIX;
+            for (uint32_t b = lane; b < POOL; b += G) {
+                const uint32_t y = (b / 10) * 2, x = (b % 10) * 2;
+                float pooled = 12.0f;
+#pragma unroll
+                for (uint32_t dy = 0; dy < 2; dy++)
+#pragma unroll
+                    for (uint32_t dx = 0; dx < 2; dx++) {
+                        const uint32_t k = (y + dy) * 20 + x + dx;
+                        const float rx = a.camera[3 * k], ry = a.camera[3 * k + 1], rz = a.camera[3 * k + 2];
+                        const V d = mk(R[0] * rx + R[1] * ry + R[2] * rz, R[3] * rx + R[4] * ry + R[5] * rz,
+                                       R[6] * rx + R[7] * ry + R[8] * rz);
+                        float depth = cast_ray(world, s_cent[grp], count, origin, d);
+                        if (noise != 0 || drop != 0) {
+                            uint32_t nr = r.rng + k * 1664525u + r.steps * 1013904223u;
+                            depth = clamp_f(depth + noise * normal_draw(nr), 0.0f, 12.0f);
+                            if (ur(nr) < drop) depth = 12.0f;
+                        }
+                        ring[k] = depth;
+                        pooled = min_f(pooled, depth);
+                    }
+                s_ring[grp][slotk][b] = pooled;
+            }
+        }
+        group_sync();
+
+        // ---- observe (sim.metal:182-228, pooled 181-input actor)
+        const uint32_t available = r.steps / C.sensor_period;
+        const uint32_t frame = available > sdelay ? available - sdelay : 0;
+        const uint32_t prev = frame > 0 ? frame - 1 : 0;
+        const bool have = available >= sdelay;
+        float* og = a.obs + row * OBS;
+        if (active) {
+            for (uint32_t b = lane; b < POOL; b += G) {
+                const float cur = have ? s_ring[grp][frame % K][b] / 12.0f : 1.0f;
+                const float pre = have ? s_ring[grp][prev % K][b] / 12.0f : 1.0f;
+                s_obs[grp][b] = cur;
+                s_obs[grp][POOL + b] = pre;
+                og[b] = cur;
+                og[POOL + b] = pre;
+            }
+            const float* gw = world + 163;
+            const float dx = gw[0] - s.p[0], dy = gw[1] - s.p[1], dz = gw[2] - s.p[2];
+            const float distance = max_f(sqrt_f(dx * dx + dy * dy + dz * dz), 1.0e-6f);
+            float ctx[21];
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                ctx[j] = (R[j] * dx + R[3 + j] * dy + R[6 + j] * dz) / distance;
+                ctx[4 + j] = (R[j] * s.v[0] + R[3 + j] * s.v[1] + R[6 + j] * s.v[2]) / 4.0f;
+                ctx[7 + j] = s.w[j] / 4.0f;
+                ctx[10 + j] = R[6 + j];
+            }
+            ctx[3] = min_f(distance / 10.0f, 1.5f);
+#pragma unroll
+            for (int j = 0; j < 4; j++) ctx[13 + j] = r.prev_nav[j];
+            ctx[17] = float(r.steps - frame * C.sensor_period) * P.dt * float(C.substeps);
+            const float ref0 = r.ref_pos[0] - s.p[0], ref1 = r.ref_pos[1] - s.p[1], ref2 = r.ref_pos[2] - s.p[2];
+#pragma unroll
+            for (int j = 0; j < 3; j++) ctx[18 + j] = clamp_f((R[j] * ref0 + R[3 + j] * ref1 + R[6 + j] * ref2) * 2.0f, -1.0f, 1.0f);
+#pragma unroll
+            for (int j = 0; j < 21; j++)
+                if (j % G == int(lane)) { s_obs[grp][2 * POOL + j] = ctx[j]; og[2 * POOL + j] = ctx[j]; }
+            // critic observation (sim.metal:159-181)
+            float cob[COBS];
+#pragma unroll
+            for (int j = 0; j < 32; j++) cob[j] = 0;
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                cob[j] = (gw[j] - s.p[j]) / 10.0f;
+                cob[j + 3] = s.v[j] / 4.0f;
+                cob[j + 6] = s.w[j] / 4.0f;
+                cob[j + 13] = s.p[j] / 10.0f;
+                cob[j + 16] = (r.ref_pos[j] - s.p[j]) * 2.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
+            cob[30] = world[166];
+            cob[31] = world[167];
+            cob[19] = clearance_at(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed) / 5.0f;
+            cob[20] = float(r.steps) / 200.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < 3; j++)
+                if (j < count) {
+                    cob[21 + j * 3] = (s_cent[grp][3 * j] - s.p[0]) / 10.0f;
+                    cob[22 + j * 3] = (s_cent[grp][3 * j + 1] - s.p[1]) / 10.0f;
+                    cob[23 + j * 3] = (s_cent[grp][3 * j + 2] - s.p[2]) / 10.0f;
+                }
+            float* cg = a.co + row * COBS;
+#pragma unroll
+            for (int j = 0; j < 32; j++)
+                if (j % G == int(lane)) { s_co[grp][j] = cob[j]; cg[j] = cob[j]; }
+        }
+        group_sync();
+
+        // ---- actor and critic hidden layers (ppo.hpp:65-72, 82-89)
+        if (active) {
+            float acc[HU];
+#pragma unroll
+            for (int k = 0; k < HU; k++) acc[k] = A[a_b1 + lane * HU + k];
+            for (uint32_t i = 0; i < OBS; i++) {
+                const float x = s_obs[grp][i];
+                const float* w = a.actor_w1t + size_t(i) * HID + lane * HU;
+#pragma unroll
+                for (int k = 0; k < HU; k++) acc[k] += w[k] * x;
+            }
+#pragma unroll
+            for (int k = 0; k < HU; k++) s_ah[grp][lane * HU + k] = tanh_f(acc[k]);
+#pragma unroll
+            for (int k = 0; k < HU; k++) acc[k] = CR[c_b1 + lane * HU + k];
+            for (uint32_t i = 0; i < COBS; i++) {
+                const float x = s_co[grp][i];
+                const float* w = a.critic_w1t + size_t(i) * HID + lane * HU;
+#pragma unroll
+                for (int k = 0; k < HU; k++) acc[k] += w[k] * x;
+            }
+#pragma unroll
+            for (int k = 0; k < HU; k++) s_ch[grp][lane * HU + k] = tanh_f(acc[k]);
+        }
+        group_sync();
+
+        // ---- act (sim.metal:229-256): means, value, sample, log-prob, command
+        float a_cmd[4] = {0, 0, 0, 0};
+        if (active) {
+            float mean[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float z = A[a_b2 + q];
+                for (uint32_t h = 0; h < HID; h++) z += A[a_w2 + q * HID + h] * s_ah[grp][h];
+                mean[q] = z;
+            }
+            float value = CR[c_b2];
+            for (uint32_t h = 0; h < HID; h++) value += CR[c_w2 + h] * s_ch[grp][h];
+            uint32_t rng = r.rng;
+            float lp = 0, act[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float ls = A[a_ls + j];
+                act[j] = mean[j] + ((C.mode == 0 || C.mode == 22) ? exp_f(ls) * normal_draw(rng) : 0.0f);
+                if (C.mode == 1) act[j] = normal_draw(rng);
+                const float diff = (act[j] - mean[j]) * exp_f(-ls);
+                lp += -0.5f * (diff * diff + 2 * ls + LOG_TWO_PI);
+                a_cmd[j] = tanh_f(act[j]);
+            }
+            r.rng = rng;
+            if (C.mode == 2 || C.mode == 3 || C.mode == 20) {  // sim.metal:257-262
+                float dd[3] = {world[163] - s.p[0], world[164] - s.p[1], world[165] - s.p[2]};
+                const float ln = sqrt_f(dd[0] * dd[0] + dd[1] * dd[1] + dd[2] * dd[2]);
+                const float inv = 1.0f / ln, lim = min_f(ln, C.speed);
+#pragma unroll
+                for (int j = 0; j < 3; j++) dd[j] = (dd[j] * inv) * lim;
+                a_cmd[0] = (R[0] * dd[0] + R[3] * dd[1] + R[6] * dd[2]) / C.speed;
+                a_cmd[1] = (R[1] * dd[0] + R[4] * dd[1] + R[7] * dd[2]) / C.speed;
+                a_cmd[2] = (R[2] * dd[0] + R[5] * dd[1] + R[8] * dd[2]) / C.speed;
+                a_cmd[3] = 0;
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) a.actions[row * 4 + j] = act[j];
+                a.logp[row] = lp;
+                a.values[row] = value;
+                const uint32_t slot = r.steps % 8;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    s_cmd[grp][slot * 4 + j] = a_cmd[j];
+                    a.commands[size_t(nn) * 32 + slot * 4 + j] = a_cmd[j];
+                }
+            }
+        }
+        group_sync();
+        if (active) {  // sim.metal:263-270
+            const uint32_t applied = r.steps > cdelay ? r.steps - cdelay : 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) r.prev_nav[j] = r.steps < cdelay ? 0.0f : s_cmd[grp][(applied % 8) * 4 + j];
+            float v[3] = {r.prev_nav[0] * C.speed, r.prev_nav[1] * C.speed,
+                          r.prev_nav[2] * C.speed * (C.velocity_contract == 0 ? 0.5f : 1.0f)};
+            if (C.velocity_contract == 1) {
+                const float m = sqrt_f(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+                const float scale = min_f(1.0f, C.speed / max_f(m, 1e-8f));
+#pragma unroll
+                for (int j = 0; j < 3; j++) v[j] *= scale;
+            }
+            if (C.mode == 19) {
+                const float m = sqrt_f(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+                if (m > 1e-8f) {
+                    const float scale = C.speed / m;
+#pragma unroll
+                    for (int j = 0; j < 3; j++) v[j] *= scale;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 3; j++) r.desired_vel[j] = R[j * 3] * v[0] + R[j * 3 + 1] * v[1] + R[j * 3 + 2] * v[2];
+            r.yaw += r.prev_nav[3] * P.dt * float(C.substeps) * 0.5f;
+        }
+
+        // ---- advance (sim.metal:272-304): substeps of RAPTOR + RK4
+        const float gx = world[163], gy = world[164], gz = world[165];
+        float before = 0;
+        {
+            const float dx = gx - s.p[0], dy = gy - s.p[1], dz = gz - s.p[2];
+            before = sqrt_f(dx * dx + dy * dy + dz * dz);
+        }
+        float si, c, sh, ch;
+        sincos_f(r.yaw, &si, &c);
+        sincos_f(r.yaw * 0.5f, &sh, &ch);
+        bool collision = false, done = !active;
+        float step_clearance = 12.0f;
+        const float wind[3] = {world[166] * P.mass, world[167] * P.mass, world[168] * P.mass};
+        for (uint32_t step = 0; step < C.substeps; step++) {
+            float mo[22] = {0};
+            if (!done) {
+                const float v0 = r.desired_vel[0], v1 = r.desired_vel[1], v2 = r.desired_vel[2];
+                r.ref_pos[0] += v0 * P.dt; r.ref_pos[1] += v1 * P.dt; r.ref_pos[2] += v2 * P.dt;
+                const float dp0 = s.p[0] - r.ref_pos[0], dp1 = s.p[1] - r.ref_pos[1], dp2 = s.p[2] - r.ref_pos[2];
+                const float dv0 = s.v[0] - v0, dv1 = s.v[1] - v1, dv2 = s.v[2] - v2;
+                mo[0] = clamp_f(c * dp0 + si * dp1, -.5f, .5f);
+                mo[1] = clamp_f(-si * dp0 + c * dp1, -.5f, .5f);
+                mo[2] = clamp_f(dp2, -.5f, .5f);
+                const float q[4] = {ch * s.q[0] + sh * s.q[3], ch * s.q[1] + sh * s.q[2], ch * s.q[2] - sh * s.q[1],
+                                    ch * s.q[3] - sh * s.q[0]};
+                rotation(q, mo + 3);
+                mo[12] = clamp_f(c * dv0 + si * dv1, -1.0f, 1.0f);
+                mo[13] = clamp_f(-si * dv0 + c * dv1, -1.0f, 1.0f);
+                mo[14] = clamp_f(dv2, -1.0f, 1.0f);
+                mo[15] = s.w[0]; mo[16] = s.w[1]; mo[17] = s.w[2];
+#pragma unroll
+                for (int j = 0; j < 4; j++) mo[18 + j] = r.motors[j];
+            }
+            float act[4];
+            raptor_group<G>(RW, mo, r.hidden, hu, s_x[grp], s_h[grp], lane, !done, act);
+            if (!done) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) r.motors[q] = act[q];
+                State nx;
+                physics_step(P, s, act, wind, nx);
+                bool valid = true;
+                const float* nf = &nx.p[0];
+#pragma unroll
+                for (int j = 0; j < 17; j++) valid = valid && isfinite_f(nf[j]);
+                if (!valid) {
+                    collision = true;
+                    done = true;
+                } else {
+                    const float ex = s.p[0] - nx.p[0], ey = s.p[1] - nx.p[1], ez = s.p[2] - nx.p[2];
+                    r.path += sqrt_f(ex * ex + ey * ey + ez * ez);
+                    s = nx;
+                    r.elapsed += P.dt;
+                    const float cl = clearance_at(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed);
+                    step_clearance = min_f(step_clearance, cl);
+                    r.min_clearance = min_f(r.min_clearance, cl);
+                    r.peak_speed = max_f(r.peak_speed, sqrt_f(s.v[0] * s.v[0] + s.v[1] * s.v[1] + s.v[2] * s.v[2]));
+                    if (cl <= 0) {
+                        collision = true;
+                        done = true;
+                    }
+                }
+            }
+        }
+
+        // ---- outcome (sim.metal:304-306), next value, episode end
+        bool ended = false;
+        if (active) {
+            r.steps++;
+            const float dx = gx - s.p[0], dy = gy - s.p[1], dz = gz - s.p[2];
+            const float after = sqrt_f(dx * dx + dy * dy + dz * dz);
+            const bool success = after < (C.mode == 20 ? .10f : .35f) && !collision;
+            const bool timeout = r.steps >= C.max_steps;
+            const bool term = collision || success;
+            const bool trunc = timeout && !term;
+            if (lane == 0) {
+                a.rewards[row] = (before - after) * 2.0f - .01f -
+                                 C.risk_coef * clamp_f((0.6f - step_clearance) / 0.6f, 0.0f, 1.0f) +
+                                 (success ? 10.0f : 0.0f) - (collision ? 10.0f : 0.0f);
+                a.terminated[row] = term ? 1 : 0;
+                a.truncated[row] = trunc ? 1 : 0;
+            }
+            // critic observation of the next state (time elapsed after the substeps)
+            float cob[COBS];
+#pragma unroll
+            for (int j = 0; j < 32; j++) cob[j] = 0;
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                cob[j] = (world[163 + j] - s.p[j]) / 10.0f;
+                cob[j + 3] = s.v[j] / 4.0f;
+                cob[j + 6] = s.w[j] / 4.0f;
+                cob[j + 13] = s.p[j] / 10.0f;
+                cob[j + 16] = (r.ref_pos[j] - s.p[j]) * 2.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
+            cob[30] = world[166];
+            cob[31] = world[167];
+            cob[19] = clearance_at(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed) / 5.0f;
+            cob[20] = float(r.steps) / 200.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < 3; j++)
+                if (j < count) {
+                    const V cc = obstacle_center(world + 10 * j, r.elapsed);
+                    cob[21 + j * 3] = (cc.x - s.p[0]) / 10.0f;
+                    cob[22 + j * 3] = (cc.y - s.p[1]) / 10.0f;
+                    cob[23 + j * 3] = (cc.z - s.p[2]) / 10.0f;
+                }
+#pragma unroll
+            for (int j = 0; j < 32; j++)
+                if (j % G == int(lane)) s_co[grp][j] = cob[j];
+            if (success || collision || timeout) {  // sim.metal:328-331
+                r.successes += success;
+                r.collisions += collision;
+                r.timeouts += trunc;
+                r.episodes++;
+                r.success_time += success ? r.elapsed : 0;
+                r.total_path += r.path;
+                r.total_elapsed += r.elapsed;
+                r.final_progress += 1.0f - after / max_f(r.initial_distance, 1.0e-4f);
+                ended = !C.eval;
+            }
+        }
+        group_sync();
+        if (active) {  // next value: critic hidden split over the group
+            float acc[HU];
+#pragma unroll
+            for (int k = 0; k < HU; k++) acc[k] = CR[c_b1 + lane * HU + k];
+            for (uint32_t i = 0; i < COBS; i++) {
+                const float x = s_co[grp][i];
+                const float* w = a.critic_w1t + size_t(i) * HID + lane * HU;
+#pragma unroll
+                for (int k = 0; k < HU; k++) acc[k] += w[k] * x;
+            }
+#pragma unroll
+            for (int k = 0; k < HU; k++) s_ch[grp][lane * HU + k] = tanh_f(acc[k]);
+        }
+        group_sync();
+        uint32_t reset_rng = 0, reset_family = 0, reset_seed = 0;
+        if (active) {
+            float value = CR[c_b2];
+            for (uint32_t h = 0; h < HID; h++) value += CR[c_w2 + h] * s_ch[grp][h];
+            if (lane == 0) a.next_values[row] = value;
+            if (ended) {
+                reset_rng = r.rng;
+                reset_draw(C, nn, false, reset_rng, reset_family, reset_seed);
+                if (lane == 0) {
+                    WorldGen wg{world};
+                    wg.generate(reset_seed, reset_family, C.distance);
+                }
+            }
+        }
+        group_sync();
+        if (ended) {  // sim_reset_one, not first
+            reset_apply(C, P, RW, nn, false, reset_rng, world, s, r);
+#pragma unroll
+            for (int j = 0; j < U; j++) hu[j] = RW[2000 + lane + G * j];
+            for (uint32_t i = lane; i < uint32_t(K) * POOL; i += G) (&s_ring[grp][0][0])[i] = 12.0f;
+            for (uint32_t i = lane; i < 32; i += G) {
+                s_cmd[grp][i] = 0.0f;
+                a.commands[size_t(nn) * 32 + i] = 0.0f;
+            }
+            float* ring = a.sensors + size_t(nn) * 8 * PIX;
+            for (uint32_t i = lane; i < 8 * PIX; i += G) ring[i] = 12.0f;
+        }
+        group_sync();
+        if (ended)
+            for (uint32_t i = lane; i < WORLD_WORDS; i += G) a.world[size_t(nn) * WORLD_WORDS + i] = world[i];
+    }
+    if (live) {
+        store_state(a.state, N, n, s, lane, G);
+        store_run(a.run, N, n, r, lane, G);
+    }
+}
+
+}  // namespace nav
+
+// ---------------------------------------------------------------- launchers
+extern "C" {
+
+hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream) {
+    const uint32_t blocks = (a->cfg.n + 63) / 64;
+    hipLaunchKernelGGL(nav::reset_kernel, dim3(blocks), dim3(64), 0, stream, *a);
+    return hipGetLastError();
+}
+
+// Lanes per env G and LDS ring slots K are compile-time; K = sensor_delay+2
+// rounded up to 2, 4 or 8.
+hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, hipStream_t stream) {
+    const uint32_t envs_per_block = 64 / lanes_per_env;
+    const uint32_t blocks = (a->cfg.n + envs_per_block - 1) / envs_per_block;
+#define NAV_ROLLOUT_CASE(G, K)                                                                       \
+    if (lanes_per_env == G && ring_slots == K) {                                                     \
+        hipLaunchKernelGGL((nav::rollout_kernel<G, K>), dim3(blocks), dim3(64), 0, stream, *a);      \
+        return hipGetLastError();                                                                    \
+    }
+    NAV_ROLLOUT_CASE(8, 2) NAV_ROLLOUT_CASE(8, 4) NAV_ROLLOUT_CASE(8, 8)
+    NAV_ROLLOUT_CASE(16, 2) NAV_ROLLOUT_CASE(16, 4) NAV_ROLLOUT_CASE(16, 8)
+    NAV_ROLLOUT_CASE(4, 2) NAV_ROLLOUT_CASE(4, 4) NAV_ROLLOUT_CASE(4, 8)
+#undef NAV_ROLLOUT_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- RAPTOR fixture
+namespace nav {
+// Each lane group runs RAPTOR from the initial hidden state over obs[steps][22]
+// with the production group step (raptor_fixture, main.mm:74-77).
+template <int G>
+__global__ __launch_bounds__(64) void raptor_fixture_kernel(const float* __restrict__ RW, const float* __restrict__ obs,
+                                                            uint32_t steps, uint32_t copies, float* __restrict__ actions,
+                                                            float* __restrict__ hidden_out) {
+    constexpr int E = 64 / G, U = 16 / G;
+    __shared__ float s_x[E][16];
+    __shared__ float s_h[E][16];
+    const uint32_t lane = threadIdx.x % G, grp = threadIdx.x / G;
+    const uint32_t copy = blockIdx.x * E + grp;
+    const bool live = copy < copies;
+    float hidden[16], hu[U];
+#pragma unroll
+    for (int j = 0; j < 16; j++) hidden[j] = RW[2000 + j];
+#pragma unroll
+    for (int j = 0; j < U; j++) hu[j] = RW[2000 + lane + G * j];
+    for (uint32_t t = 0; t < steps; t++) {
+        float mo[22];
+#pragma unroll
+        for (int j = 0; j < 22; j++) mo[j] = obs[t * 22 + j];
+        float act[4];
+        raptor_group<G>(RW, mo, hidden, hu, s_x[grp], s_h[grp], lane, live, act);
+        if (live && lane == 0) {
+            // the fixture reports the raw network output (raptor.hpp:51),
+            // recomputed here without the clip
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float val = RW[2080 + q];
+#pragma unroll
+                for (int col = 0; col < 16; col++) val += RW[2016 + q * 16 + col] * hidden[col];
+                actions[(size_t(copy) * steps + t) * 4 + q] = val;
+            }
+        }
+    }
+    if (live && lane == 0)
+        for (int j = 0; j < 16; j++) hidden_out[size_t(copy) * 16 + j] = hidden[j];
+}
+}  // namespace nav
+
+extern "C" hipError_t nav_launch_raptor_fixture(const float* RW, const float* obs, uint32_t steps, uint32_t copies,
+                                                float* actions, float* hidden, int lanes_per_env, hipStream_t st) {
+    const uint32_t per = 64 / lanes_per_env;
+    const dim3 grid((copies + per - 1) / per);
+    if (lanes_per_env == 4) hipLaunchKernelGGL(nav::raptor_fixture_kernel<4>, grid, dim3(64), 0, st, RW, obs, steps, copies, actions, hidden);
+    else if (lanes_per_env == 8) hipLaunchKernelGGL(nav::raptor_fixture_kernel<8>, grid, dim3(64), 0, st, RW, obs, steps, copies, actions, hidden);
+    else if (lanes_per_env == 16) hipLaunchKernelGGL(nav::raptor_fixture_kernel<16>, grid, dim3(64), 0, st, RW, obs, steps, copies, actions, hidden);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}

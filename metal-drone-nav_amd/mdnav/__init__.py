@@ -4,8 +4,12 @@ Host-side Python face of the C ABI in include/mdnav.h: ``Sim`` and
 ``PPOTrainer`` mirror the reference's host classes (main.mm:516-603,
 1110-1474) and ``Trainer`` mirrors cpu_reference::Trainer
 (cpu_reference.hpp:112-615), all running on the HIP library
-``lib/libmdnav.so``.  ``abi`` holds the struct layouts.
+``lib/libmdnav.so``.  ``abi`` holds the struct layouts, ``ops`` the stateless
+operators.  Importing is cheap; the library loads on first use and raises if
+it is missing.
 """
 from . import abi  # noqa: F401
+from .native import MdnError  # noqa: F401
+from .sim import PPOTrainer, Sim, Trainer, crazyflie_params, load_raptor  # noqa: F401
 
-__all__ = ["abi"]
+__all__ = ["abi", "MdnError", "Sim", "PPOTrainer", "Trainer", "crazyflie_params", "load_raptor"]

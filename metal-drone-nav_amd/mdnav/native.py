@@ -1,0 +1,93 @@
+"""ctypes binding of lib/libmdnav.so (include/mdnav.h).
+
+Loading fails loudly: there is no CPU fallback behind this module.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from . import abi
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG, "lib", "libmdnav.so")
+EXPORTS = [
+    "mdn_last_error", "mdn_version", "mdn_sim_create", "mdn_sim_destroy", "mdn_sim_set_config",
+    "mdn_sim_get_config", "mdn_sim_reset", "mdn_sim_collect", "mdn_sim_sync", "mdn_sim_buffer_bytes",
+    "mdn_sim_download", "mdn_sim_upload", "mdn_sim_set_timing", "mdn_sim_kernel_time",
+    "mdn_sim_reset_timing", "mdn_sim_set_lanes", "mdn_ppo_create", "mdn_ppo_destroy",
+    "mdn_ppo_rollout_update", "mdn_ppo_gae", "mdn_ppo_normalize", "mdn_ppo_update",
+    "mdn_ppo_metric_mean", "mdn_ppo_optimizer_step", "mdn_ppo_updates_per_rollout",
+    "mdn_op_physics_step", "mdn_op_raptor_sequence", "mdn_op_ray_world", "mdn_op_clearance",
+    "mdn_op_gae", "mdn_op_normalize",
+]
+
+P = ctypes.c_void_p
+U32, U64, F32, I32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_int
+KERNELS = {"rollout": 0, "gae": 1, "normalize": 2, "rows": 3, "grads": 4, "adam": 5}
+
+_lib = None
+
+
+class MdnError(RuntimeError):
+    """A non-zero status of the C ABI (the reference's require() failures)."""
+
+
+def _sig(lib, name, res, *args):
+    f = getattr(lib, name)
+    f.restype = res
+    f.argtypes = list(args)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError("libmdnav.so is not built (%s); run __graft_entry__.build()" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        _sig(L, "mdn_last_error", ctypes.c_char_p)
+        _sig(L, "mdn_version", ctypes.c_char_p)
+        _sig(L, "mdn_sim_create", I32, P, U32, P, P, ctypes.POINTER(P))
+        _sig(L, "mdn_sim_destroy", None, P)
+        _sig(L, "mdn_sim_set_config", I32, P, P)
+        _sig(L, "mdn_sim_get_config", I32, P, P, ctypes.POINTER(U32))
+        _sig(L, "mdn_sim_reset", I32, P)
+        _sig(L, "mdn_sim_collect", I32, P, U32)
+        _sig(L, "mdn_sim_sync", I32, P, ctypes.POINTER(ctypes.c_double))
+        _sig(L, "mdn_sim_buffer_bytes", I32, P, U32, ctypes.POINTER(U64))
+        _sig(L, "mdn_sim_download", I32, P, U32, P, U64)
+        _sig(L, "mdn_sim_upload", I32, P, U32, P, U64)
+        _sig(L, "mdn_sim_set_timing", I32, P, I32)
+        _sig(L, "mdn_sim_kernel_time", I32, P, U32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(U64))
+        _sig(L, "mdn_sim_reset_timing", I32, P)
+        _sig(L, "mdn_sim_set_lanes", I32, P, U32)
+        _sig(L, "mdn_ppo_create", I32, P, U32, U32, ctypes.POINTER(P))
+        _sig(L, "mdn_ppo_destroy", None, P)
+        _sig(L, "mdn_ppo_rollout_update", I32, P, U32)
+        _sig(L, "mdn_ppo_gae", I32, P)
+        _sig(L, "mdn_ppo_normalize", I32, P)
+        _sig(L, "mdn_ppo_update", I32, P, U32)
+        _sig(L, "mdn_ppo_metric_mean", I32, P, P)
+        _sig(L, "mdn_ppo_optimizer_step", I32, P, ctypes.POINTER(U64))
+        _sig(L, "mdn_ppo_updates_per_rollout", I32, P, ctypes.POINTER(U32))
+        _sig(L, "mdn_op_physics_step", I32, P, P, P, P, P, U64)
+        _sig(L, "mdn_op_raptor_sequence", I32, P, P, U32, U32, P, P)
+        _sig(L, "mdn_op_ray_world", I32, P, P, P, U32, P, U64)
+        _sig(L, "mdn_op_clearance", I32, P, P, P, P, U64)
+        _sig(L, "mdn_op_gae", I32, U32, U32, P, P, P, P, P, F32, F32, P, P)
+        _sig(L, "mdn_op_normalize", I32, P, U64, F32)
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        raise MdnError(lib().mdn_last_error().decode() or ("status %d" % rc))
+
+
+def ptr(a):
+    return a.ctypes.data_as(P)
+
+
+def contiguous(a, dtype):
+    return np.ascontiguousarray(np.asarray(a, dtype))

@@ -1,0 +1,242 @@
+"""Host classes mirroring the reference's API over the HIP library.
+
+* ``Sim``        — main.mm:516-603 (``Sim(Metal&, SimConfig, horizon)``,
+  ``set_config``, ``reset``, ``collect``, ``report`` and the shared buffers).
+* ``PPOTrainer`` — main.mm:1110-1474 (``PPOTrainer(Sim&, epochs)``,
+  ``rollout_update``, ``metric_mean``, ``optimizer_step``).
+* ``Trainer``    — cpu_reference.hpp:112-615 (``Trainer(cfg, horizon, raptor,
+  physics)``, ``run(rollouts) -> Metrics``, public buffers), here running on
+  the GPU: a drop-in for callers of the CPU trainer's interface.
+
+The reference reads buffers through ``MTLBuffer.contents``; here ``get``/``set``
+copy them in the reference's host layouts.  Errors raise ``MdnError`` where
+the reference's ``require`` throws ``std::runtime_error``.
+"""
+import ctypes
+import os
+import time
+
+import numpy as np
+
+from . import abi
+from .native import KERNELS, MdnError, check, contiguous, lib, ptr
+
+ASSETS = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "assets")
+
+
+def load_raptor(path=None):
+    """The frozen RAPTOR controller (raptor.hpp:25-40; main.mm:126)."""
+    return abi.load_raptor(path or os.path.join(ASSETS, "raptor.bin"))
+
+
+def crazyflie_params():
+    """rl_physics_crazyflie_default (physics.hpp:184-219)."""
+    p = np.zeros((), abi.PHYSICS_PARAMS)
+    pos = [.028, -.028, 0, -.028, -.028, 0, -.028, .028, 0, .028, .028, 0]
+    tz = [-1, 1, -1, 1]
+    for r in range(4):
+        i = 3 * r
+        p["rotor_positions"][i:i + 2] = pos[i:i + 2]
+        p["rotor_thrust_directions"][i + 2] = 1.0
+        p["rotor_torque_directions"][i + 2] = tz[r]
+        p["rotor_thrust_coefficients"][i:i + 3] = [0.00352526, 0.01437313, 0.09223048]
+        p["rotor_torque_constants"][r] = 4.665e-3
+        p["rotor_time_constants_rising"][r] = 0.05545454545454546
+        p["rotor_time_constants_falling"][r] = 0.24939393939393945
+    diag = [9.416556729130406e-6, 9.644051701582312e-6, 1.745951732253285e-5]
+    inv = [106195.93007988465, 103690.85846314249, 57275.35197719487]
+    for i in range(3):
+        p["inertia"][4 * i] = diag[i]
+        p["inertia_inverse"][4 * i] = inv[i]
+    p["gravity_world"][2] = -9.81
+    p["mass"] = np.float32(np.float32(np.float32(np.float32(0.027) + np.float32(0.0017)) + np.float32(0.0003))
+                           + np.float32(0.0016))
+    p["action_min"], p["action_max"], p["dt"] = 0.0, 1.0, 0.01
+    p["position_limit"] = p["velocity_limit"] = p["angular_velocity_limit"] = 100000.0
+    return p
+
+
+class Sim:
+    """Batched simulator handle (Sim, main.mm:516-603)."""
+
+    def __init__(self, cfg, horizon, raptor=None, physics=None, lanes=8):
+        L = lib()
+        self.cfg = np.array(cfg, abi.SIM_CONFIG)
+        self.horizon = int(horizon)
+        self._raptor = np.array(load_raptor() if raptor is None else raptor, abi.RAPTOR_WEIGHTS)
+        self._physics = np.array(crazyflie_params() if physics is None else physics, abi.PHYSICS_PARAMS)
+        h = ctypes.c_void_p()
+        check(L.mdn_sim_create(ptr(self.cfg), self.horizon, ptr(self._raptor), ptr(self._physics),
+                               ctypes.byref(h)))
+        self.h = h
+        self.ppo = None
+        if lanes != 8:
+            check(L.mdn_sim_set_lanes(self.h, lanes))
+
+    @property
+    def n(self):
+        return int(self.cfg["n"])
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().mdn_sim_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def set_config(self, cfg):
+        c = np.array(cfg, abi.SIM_CONFIG)
+        check(lib().mdn_sim_set_config(self.h, ptr(c)))
+        self.cfg = c
+
+    def set_lanes(self, lanes):
+        check(lib().mdn_sim_set_lanes(self.h, lanes))
+
+    def reset(self):
+        check(lib().mdn_sim_reset(self.h))
+        return self.sync()
+
+    def collect(self, count=0):
+        """Enqueue ``count`` ticks (0 = horizon); returns immediately."""
+        check(lib().mdn_sim_collect(self.h, count))
+
+    def sync(self):
+        """Metal::finish: wait, return GPU seconds since the previous sync."""
+        s = ctypes.c_double()
+        check(lib().mdn_sim_sync(self.h, ctypes.byref(s)))
+        return s.value
+
+    def _bytes(self, bid):
+        b = ctypes.c_uint64()
+        check(lib().mdn_sim_buffer_bytes(self.h, bid, ctypes.byref(b)))
+        return b.value
+
+    def get(self, name):
+        bid, dtype = abi.BUFFERS[name]
+        nbytes = self._bytes(bid)
+        out = np.zeros(nbytes // np.dtype(dtype).itemsize, dtype)
+        check(lib().mdn_sim_download(self.h, bid, ptr(out), nbytes))
+        return out
+
+    def set(self, name, values):
+        bid, dtype = abi.BUFFERS[name]
+        nbytes = self._bytes(bid)
+        arr = contiguous(values, dtype).reshape(-1)
+        if arr.nbytes != nbytes:
+            raise MdnError("upload of %s needs %d bytes, got %d" % (name, nbytes, arr.nbytes))
+        check(lib().mdn_sim_upload(self.h, bid, ptr(arr), nbytes))
+
+    # timing of individual kernels (HIP events on the sim's stream)
+    def set_timing(self, on=True):
+        check(lib().mdn_sim_set_timing(self.h, 1 if on else 0))
+
+    def reset_timing(self):
+        check(lib().mdn_sim_reset_timing(self.h))
+
+    def kernel_time(self, name):
+        ms, n = ctypes.c_double(), ctypes.c_uint64()
+        check(lib().mdn_sim_kernel_time(self.h, KERNELS[name], ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
+    def report(self, label="", wall=0.0):
+        """Sim::report (main.mm:599-602) as a dict of episode statistics."""
+        r = self.get("runs")
+        ep = int(r["episodes"].sum())
+        succ = int(r["successes"].sum())
+        tot = float(r["total_elapsed"].astype(np.float64).sum())
+        return dict(label=label, episodes=ep, success=succ / ep if ep else 0.0,
+                    collision=int(r["collisions"].sum()) / ep if ep else 0.0,
+                    timeout=int(r["timeouts"].sum()) / ep if ep else 0.0,
+                    progress=float(r["final_progress"].astype(np.float64).sum()) / ep if ep else 0.0,
+                    mean_goal_time=float(r["success_time"].astype(np.float64).sum()) / succ if succ else 0.0,
+                    mean_speed=float(r["total_path"].astype(np.float64).sum()) / tot if tot else 0.0,
+                    peak_speed=float(r["peak_speed"].max()), min_clearance=float(r["min_clearance"].min()),
+                    wall_s=wall)
+
+
+class PPOTrainer:
+    """Optimiser over a Sim's rollout (PPOTrainer, main.mm:1110-1474)."""
+
+    def __init__(self, sim, epochs=2, minibatch=256):
+        h = ctypes.c_void_p()
+        check(lib().mdn_ppo_create(sim.h, epochs, minibatch, ctypes.byref(h)))
+        self.h = h
+        self.sim = sim
+        sim.ppo = self
+        self.epochs = epochs
+        self.minibatch = minibatch
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().mdn_ppo_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        # the Sim destroys its trainer with itself; only free if still attached
+        if getattr(self, "h", None) and getattr(self.sim, "h", None):
+            self.close()
+
+    def rollout_update(self, rollout_index):
+        check(lib().mdn_ppo_rollout_update(self.h, rollout_index))
+
+    def gae(self):
+        check(lib().mdn_ppo_gae(self.h))
+
+    def normalize(self):
+        check(lib().mdn_ppo_normalize(self.h))
+
+    def update(self, rollout_index):
+        check(lib().mdn_ppo_update(self.h, rollout_index))
+
+    def metric_mean(self):
+        out = np.zeros(4, np.float32)
+        check(lib().mdn_ppo_metric_mean(self.h, ptr(out)))
+        return out
+
+    @property
+    def optimizer_step(self):
+        s = ctypes.c_uint64()
+        check(lib().mdn_ppo_optimizer_step(self.h, ctypes.byref(s)))
+        return s.value
+
+    @property
+    def updates_per_rollout(self):
+        u = ctypes.c_uint32()
+        check(lib().mdn_ppo_updates_per_rollout(self.h, ctypes.byref(u)))
+        return u.value
+
+
+class Trainer:
+    """cpu_reference::Trainer interface (cpu_reference.hpp:112-615) on the GPU."""
+
+    def __init__(self, cfg, horizon, raptor=None, physics=None, epochs=2, minibatch=256, lanes=8):
+        self.sim = Sim(cfg, horizon, raptor, physics, lanes=lanes)
+        self.ppo = PPOTrainer(self.sim, epochs, minibatch)
+        self.horizon = horizon
+
+    def run(self, rollouts):
+        """Trainer::run (cpu_reference.hpp:163-185): rollout + GAE + update."""
+        start = time.perf_counter()
+        for r in range(rollouts):
+            self.sim.collect()
+            self.ppo.rollout_update(r)
+        self.sim.sync()
+        wall = time.perf_counter() - start
+        runs = self.sim.get("runs")
+        m = self.ppo.metric_mean()
+        metrics = abi.Metrics()
+        metrics.wall_seconds = wall
+        metrics.updates = self.ppo.optimizer_step
+        for f in ("episodes", "successes", "collisions", "timeouts"):
+            setattr(metrics, f, int(runs[f].sum()))
+        for f in ("final_progress", "total_path", "total_elapsed", "success_time"):
+            setattr(metrics, f, float(runs[f].astype(np.float64).sum()))
+        metrics.policy_loss, metrics.value_loss, metrics.entropy_loss, metrics.ratio = (float(x) for x in m)
+        return metrics
+
+    def get(self, name):
+        return self.sim.get(name)
+
+    def set(self, name, values):
+        self.sim.set(name, values)

@@ -1,0 +1,30 @@
+// Caller-side use of the C++ façade, written the way main.mm's cpu-bench
+// and gpu-bench drive the reference (main.mm:478-509, 2704-2709).
+#include <cstdio>
+#include <cstring>
+
+#include "mdnav.hpp"
+#include "mdnav_host.h"
+
+int main(int argc, char** argv) {
+    if (argc < 2) {
+        std::fprintf(stderr, "usage: facade_example RAPTOR_BIN [envs] [rollouts]\n");
+        return 2;
+    }
+    MdnRaptorWeights raptor;
+    if (!mdn::load_raptor_file(argv[1], &raptor)) { std::fprintf(stderr, "RAPTOR load failed\n"); return 2; }
+    MdnSimConfig cfg = mdn::default_config();
+    cfg.n = argc > 2 ? uint32_t(std::atoi(argv[2])) : 128;
+    cfg.family = 1; cfg.speed = 1; cfg.distance = 3;
+    const uint32_t rollouts = argc > 3 ? uint32_t(std::atoi(argv[3])) : 2;
+    try {
+        mdnav::Trainer trainer(cfg, 32, raptor, mdn::crazyflie_params());
+        const MdnMetrics m = trainer.run(rollouts);
+        std::printf("envs=%u rollouts=%u wall_s=%.4f updates=%llu episodes=%llu ratio=%.4f\n", cfg.n, rollouts,
+                    m.wall_seconds, (unsigned long long)m.updates, (unsigned long long)m.episodes, m.ratio);
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ERROR: %s\n", e.what());
+        return 1;
+    }
+    return 0;
+}

@@ -1,0 +1,51 @@
+"""The C-ABI library loads on a machine without a GPU and exports every
+entry point include/mdnav.h declares (no compute calls here)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+
+from mdnav import abi, native
+from oracle_lib import crazyflie, oracle, ptr
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    text = open(os.path.join(ROOT, "include", "mdnav.h")).read()
+    return sorted(set(re.findall(r"\b(mdn_[a-z_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared()
+    assert len(names) >= 30
+    lib = ctypes.CDLL(native.LIB_PATH)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(native.EXPORTS)
+    assert native.lib().mdn_version().decode().startswith("mdnav")
+
+
+def test_struct_sizes_match_reference_layouts():
+    for dt, size in [(abi.PHYSICS_STATE, 68), (abi.PHYSICS_PARAMS, 352), (abi.RAPTOR_WEIGHTS, 8336),
+                     (abi.WORLD, 676), (abi.SIM_RUN, 184), (abi.SIM_CONFIG, 84)]:
+        assert dt.itemsize == size
+
+
+def test_python_host_constants_match_oracle():
+    from mdnav.sim import crazyflie_params
+    assert crazyflie_params().tobytes() == crazyflie().tobytes()
+    c = np.zeros((), abi.SIM_CONFIG)
+    oracle().orc_default_config(ptr(c))
+    assert c.tobytes() == abi.default_config().tobytes()
+
+
+def test_error_path_without_gpu_call():
+    """Argument validation fails before any device work and reports text."""
+    lib = native.lib()
+    out = ctypes.c_void_p()
+    rc = lib.mdn_sim_create(None, 4, None, None, ctypes.byref(out))
+    assert rc == -1 and b"null" in lib.mdn_last_error()
+    rc = lib.mdn_ppo_create(None, 2, 256, ctypes.byref(out))
+    assert rc == -1

@@ -1,0 +1,177 @@
+"""HIP path against the CPU oracle and the reference's golden vectors.
+
+Integer outcomes (flags, counters, RNG states, world seeds/families) must
+match exactly.  Floating-point fields carry the stated tolerances; the
+arithmetic is designed to round identically on both sides, and the observed
+error is reported in each assertion message.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from gpu_compare import ENV_BUFFERS, ROW_BUFFERS, compare, config, make_pair
+from mdnav import Sim, abi, ops
+from oracle_lib import oracle, physics_fixture, ptr, raptor_fixture
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5  # absolute, fp32 fields (reference gates: 2e-5 physics/RAPTOR, 3e-5 depth)
+
+
+def say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+def flat_state(s):
+    return np.ascontiguousarray(s).view(np.float32).reshape(len(s), 17)
+
+
+def test_physics_golden():
+    say("case: physics golden 64x8")
+    params, recs, _, _ = physics_fixture()
+    out = ops.physics_step(recs["state"], recs["action"], recs["wind"], params)
+    err = np.abs(flat_state(out) - flat_state(recs["next"])).max()
+    assert err < 2e-5, err
+    ora = np.zeros(len(recs), abi.PHYSICS_STATE)
+    p = np.array(params, abi.PHYSICS_PARAMS)
+    s, a, w = (np.ascontiguousarray(recs[k]) for k in ("state", "action", "wind"))
+    oracle().orc_physics_step_batch(ptr(s), ptr(a), ptr(w), ptr(p), ptr(ora), len(recs))
+    assert out.tobytes() == ora.tobytes(), np.abs(flat_state(out) - flat_state(ora)).max()
+
+
+def test_raptor_golden_all_lane_widths():
+    say("case: RAPTOR official sequence, 48 copies over lane widths 4/8/16")
+    weights, obs, expected = raptor_fixture()
+    actions, hidden = ops.raptor_sequence(weights, obs, copies=48)
+    err = np.abs(actions - expected[None]).max()
+    assert err < 2e-5, err
+    ref_a = np.zeros((16, 4), np.float32)
+    ref_h = np.zeros(16, np.float32)
+    w = np.array(weights, abi.RAPTOR_WEIGHTS)
+    oracle().orc_raptor_sequence(ptr(w), ptr(obs), 16, ptr(ref_a), ptr(ref_h))
+    assert np.array_equal(actions, np.broadcast_to(ref_a, actions.shape)), np.abs(actions - ref_a).max()
+    assert np.array_equal(hidden, np.broadcast_to(ref_h, hidden.shape))
+
+
+def test_ray_cast_and_clearance():
+    say("case: world_tests setup, 128 worlds x 320 rays")
+    n = 128
+    worlds = np.zeros(n, abi.WORLD)
+    for i in range(n):
+        oracle().orc_generate_world(ptr(worlds[i:i + 1]), i + 197, i % 4, np.float32(8.0))
+    times = np.array([(i % 7) * 0.1 for i in range(n)], np.float32)
+    cam = np.zeros((320, 3), np.float32)
+    oracle().orc_camera_rays(ptr(cam))
+    rays = np.zeros((n, 320, 6), np.float32)
+    for i in range(n):
+        rays[i, :, 0:3] = [0, (i % 5 - 2) * 0.3, 1.5]
+        rays[i, :, 3:6] = cam
+    got = ops.ray_world(worlds, rays, times, 320)
+    want = np.zeros(n * 320, np.float32)
+    oracle().orc_ray_world_batch(ptr(worlds), ptr(rays), ptr(times), 320, ptr(want), n * 320)
+    assert np.array_equal(got, want), np.abs(got - want).max()
+    pts = np.ascontiguousarray(rays[:, 0, 0:3])
+    c = ops.clearance(worlds, pts, times)
+    cw = np.zeros(n, np.float32)
+    oracle().orc_clearance_batch(ptr(worlds), ptr(pts), ptr(times), ptr(cw), n)
+    assert np.array_equal(c, cw), np.abs(c - cw).max()
+
+
+def test_gae_and_normalize_operators():
+    say("case: GAE hand case + random, normalisation")
+    adv, ret = ops.gae(3, 2, [1, 2, 3, 4, 5, 6], [.1, .2, .3, .4, .5, .6], [.2, .3, .4, .5, .6, .7],
+                       [0, 0, 1, 0, 0, 0], [0, 0, 0, 1, 0, 0])
+    gl = 0.99 * 0.95
+    want = np.array([1 + .99 * .2 - .1 + gl * 2.7, 2 + .99 * .3 - .2 + gl * (4 + .99 * .5 - .4), 3 - .3,
+                     4 + .99 * .5 - .4, 5 + .99 * .6 - .5, 6 + .99 * .7 - .6])
+    assert np.abs(adv - want).max() < 2e-5
+    rng = np.random.default_rng(0)
+    T, N = 37, 101
+    r, v, nv = (rng.normal(0, 1, T * N).astype(np.float32) for _ in range(3))
+    te = (rng.random(T * N) < 0.05).astype(np.uint8)
+    tr = ((rng.random(T * N) < 0.03) & (te == 0)).astype(np.uint8)
+    a_g, r_g = ops.gae(T, N, r, v, nv, te, tr)
+    a_o, r_o = np.zeros(T * N, np.float32), np.zeros(T * N, np.float32)
+    oracle().orc_compute_gae(T, N, ptr(r), ptr(v), ptr(nv), ptr(te), ptr(tr), np.float32(.99), np.float32(.95),
+                             ptr(a_o), ptr(r_o))
+    assert np.array_equal(a_g, a_o) and np.array_equal(r_g, r_o)
+    x = rng.normal(3, 5, 300_001).astype(np.float32)
+    y = ops.normalize(x)
+    z = x.copy()
+    oracle().orc_normalize_advantages(ptr(z), len(z), np.float32(1e-8))
+    assert np.abs(y - z).max() <= 1e-6, np.abs(y - z).max()
+
+
+@pytest.mark.parametrize("lanes", [8, 16, 4])
+def test_rollout_parity(lanes):
+    say("case: rollout N=64 T=40 family=1 lanes=%d" % lanes)
+    cfg = config(n=64, family=1, speed=1.0, distance=3.0, max_steps=25)
+    sim, _, ora = make_pair(cfg, 40, lanes=lanes)
+    bad = compare(sim, ora, ENV_BUFFERS)
+    assert not bad, ("after reset", bad)
+    sim.collect()
+    sim.sync()
+    ora.collect()
+    bad = compare(sim, ora, ENV_BUFFERS + ROW_BUFFERS, tol=TOL)
+    assert not bad, bad
+    assert ora.get("runs")["episodes"].sum() > 0
+
+
+@pytest.mark.parametrize("variant", ["delays_wind_noise", "eval", "movers3", "mixed6", "rehearsal13",
+                                     "goal_script"])
+def test_rollout_parity_variants(variant):
+    kw = dict(n=48, family=1, speed=1.0, distance=3.0, max_steps=30)
+    if variant == "delays_wind_noise":
+        kw.update(sensor_delay=2, command_delay=1, wind=0.5, depth_noise=0.05, dropout=0.1)
+    elif variant == "eval":
+        kw.update(eval=1, max_steps=14)
+    elif variant == "movers3":
+        kw.update(family=3)
+    elif variant == "mixed6":
+        kw.update(family=6, distance=4.0)
+    elif variant == "rehearsal13":
+        kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=1, wind=0.5)
+    elif variant == "goal_script":
+        kw.update(mode=2, family=0, eval=1, speed=0.5, distance=4.0, max_steps=200)
+    say("case: rollout variant %s" % variant)
+    cfg = config(**kw)
+    sim, _, ora = make_pair(cfg, 36)
+    sim.collect()
+    sim.sync()
+    ora.collect()
+    bad = compare(sim, ora, ENV_BUFFERS + ROW_BUFFERS, tol=TOL)
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("epochs,minibatch", [(2, 256), (1, 512)])
+def test_iteration_parity(epochs, minibatch):
+    say("case: iteration N=32 T=64 epochs=%d minibatch=%d" % (epochs, minibatch))
+    cfg = config(n=32, family=1, speed=1.0, distance=3.0, max_steps=40)
+    sim, ppo, ora = make_pair(cfg, 64, epochs=epochs, minibatch=minibatch)
+    for it in range(2):
+        sim.collect()
+        ppo.rollout_update(it)
+        sim.sync()
+        ora.iteration(it)
+        bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "actor_v", "critic_m",
+                                 "critic_v", "metric_rows"] + ENV_BUFFERS + ROW_BUFFERS, tol=TOL)
+        assert not bad, (it, bad)
+        assert ppo.optimizer_step == ora.optimizer_step
+        assert np.abs(ppo.metric_mean() - ora.metric_mean()).max() <= TOL
+
+
+def test_baseline_schedule_parity_large_minibatch():
+    """One epoch of four minibatches (the benchmark schedule) at N=256, T=64:
+    minibatches of 4096 rows exercise the multi-chunk gradient reduction."""
+    say("case: iteration N=256 T=64 epochs=1 minibatch=4096")
+    cfg = config(n=256, family=1, speed=1.0, distance=3.0)
+    sim, ppo, ora = make_pair(cfg, 64, epochs=1, minibatch=4096)
+    sim.collect()
+    ppo.rollout_update(0)
+    sim.sync()
+    ora.iteration(0)
+    bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "critic_v", "metric_rows"]
+                  + ROW_BUFFERS + ENV_BUFFERS, tol=TOL)
+    assert not bad, bad
