@@ -1,0 +1,163 @@
+"""Benchmark: env-steps/sec of the full rollout + PPO update on one MI355X.
+
+Workload (default): 8,192 environments x 128 ticks per iteration, the static
+box world of the reference (family 1: 8 boxes per env), its 20x16 depth
+camera (12 m range, 2x2-pooled 181-input actor 181->64->4 with 4 log-stds,
+32->64->1 critic), RAPTOR + L2F RK4 at 100 Hz with 5 substeps per 20 Hz
+action, GAE(0.99, 0.95), then one PPO epoch of 4 minibatches (262,144 rows
+each), clip 0.2, Adam 3e-4.  fp32 throughout.  A step is one iteration:
+collect all ticks, GAE, normalisation, every minibatch update.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Prints one JSON line.  ``value`` is env-steps/s with every buffer resident in
+HBM.  ``roofline`` is for the dominant kernel (the fused rollout kernel),
+from HIP-event timing on its own stream; ``cpu_baseline`` times the CPU oracle
+(a port of the reference's CPU trainer) on this host on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "metal-drone-nav_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+# Algorithmic work per env-step (the per-unit figures of the measurement
+# plan): env step (5 substeps of RAPTOR + RK4 + clearance, one 320-ray depth
+# frame over 8 boxes + room, observation) 117 kFLOP; rollout actor forward
+# 24.2 kFLOP; critic at s and s' 8.7 kFLOP.  Bytes: SoA state/run read+write,
+# world, one depth frame written, observation rows written: 4.34 KB.
+FLOP_ENV_STEP = 117e3 + 24.2e3 + 8.7e3
+BYTES_ENV_STEP = 4.34e3
+# GAE + normalisation: 14 B in + 8 B out (GAE) + 3 passes over advantages.
+BYTES_GAE = 22.0
+BYTES_NORM = 16.0
+PEAK_FP32 = 157.3e12
+PEAK_HBM = 8.0e12
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(envs, target_s=12.0):
+    """Bounded sample of the CPU oracle on this host: same world, policy and
+    PPO schedule shape (1 epoch x 4 minibatches) at 16 ticks per iteration."""
+    import numpy as np
+    from oracle_lib import OracleTrainer, oracle, raptor_fixture
+    from mdnav import abi
+    horizon = 16
+    cfg = abi.default_config(n=envs, family=1, speed=1.0, distance=3.0)
+    t = OracleTrainer(cfg, horizon, raptor_fixture()[0], epochs=1, minibatch=envs * horizon // 4)
+    done, start = 0, time.perf_counter()
+    while True:
+        t.iteration(done)
+        done += 1
+        el = time.perf_counter() - start
+        if el >= target_s or done >= 4:
+            break
+    threads = int(oracle().orc_num_threads())
+    return {"value": envs * horizon * done / el, "unit": "env-steps/s", "cores": threads, "kind": "port",
+            "sample": "%d envs x %d ticks x %d iterations (rollout + GAE + 1 epoch x 4 minibatches), %.1f s, "
+                      "%d OpenMP threads on %d host CPUs" % (envs, horizon, done, el, threads, os.cpu_count())}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--envs", type=int, default=8192)
+    ap.add_argument("--horizon", type=int, default=128)
+    ap.add_argument("--schedule", choices=["baseline", "reference"], default="baseline",
+                    help="baseline: 1 epoch x 4 minibatches; reference: 2 epochs x 256-row minibatches")
+    ap.add_argument("--lanes", type=int, default=8)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box holds one MI355X); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from mdnav import PPOTrainer, Sim, abi
+    N, T = args.envs, args.horizon
+    epochs, minibatch = (1, N * T // 4) if args.schedule == "baseline" else (2, 256)
+    cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0)
+    log("bench: creating sim N=%d T=%d schedule=%s" % (N, T, args.schedule))
+    sim = Sim(cfg, T, lanes=args.lanes)
+    ppo = PPOTrainer(sim, epochs, minibatch)
+    it = 0
+    for _ in range(args.warmup):
+        sim.collect()
+        ppo.rollout_update(it)
+        it += 1
+    sim.sync()
+    log("bench: warmup done (%d iterations)" % args.warmup)
+    sim.set_timing(True)
+    sim.reset_timing()
+    sim.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        sim.collect()
+        ppo.rollout_update(it)
+        it += 1
+    gpu_s = sim.sync()
+    t1 = time.perf_counter()
+    wall = t1 - t0
+    log("bench: timed %d iterations in %.3f s (GPU %.3f s)" % (args.steps, wall, gpu_s))
+
+    kernels = {}
+    for name in ("rollout", "gae", "normalize", "rows", "grads", "adam"):
+        ms, n = sim.kernel_time(name)
+        kernels[name] = {"total_ms": round(ms, 4), "launches": n, "avg_ms": round(ms / n, 5) if n else None}
+    roll = kernels["rollout"]
+    env_steps_launch = N * T
+    avg_s = roll["avg_ms"] * 1e-3
+    achieved = FLOP_ENV_STEP * env_steps_launch / avg_s
+    roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP32, 4), "traffic": None,
+                "kernel": "rollout_kernel (fused env step + rollout actor/critic, %d ticks per launch)" % T,
+                "roof_note": "fp32 compute roof (VALU work, no MFMA); algorithmic %.1f kFLOP and %.2f KB per "
+                             "env-step x %d env-steps per launch" % (FLOP_ENV_STEP / 1e3, BYTES_ENV_STEP / 1e3,
+                                                                     env_steps_launch),
+                "hbm_frac_algorithmic": round(BYTES_ENV_STEP * env_steps_launch / avg_s / PEAK_HBM, 5)}
+    secondary = {}
+    if kernels["gae"]["launches"]:
+        gae_s = kernels["gae"]["avg_ms"] * 1e-3
+        secondary["gae"] = {"bound": "hbm", "achieved_GBps": round(BYTES_GAE * N * T / gae_s / 1e9, 1),
+                            "frac": round(BYTES_GAE * N * T / gae_s / PEAK_HBM, 4)}
+    if kernels["normalize"]["launches"]:
+        ns = kernels["normalize"]["avg_ms"] * 1e-3
+        secondary["normalize"] = {"bound": "hbm", "achieved_GBps": round(BYTES_NORM * N * T / ns / 1e9, 1),
+                                  "frac": round(BYTES_NORM * N * T / ns / PEAK_HBM, 4)}
+
+    value = N * T * args.steps / wall
+    out = {
+        "metric": "env-steps/sec (rollout+PPO update) at 8,192 envs; HBM GB/s and MFMA util %",
+        "value": round(value, 1), "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic: seeded procedural worlds (reference family 1), random-init policy (seed 1789)",
+        "config": {"workload": "static-box world, %d envs x %d ticks, small actor 181-64-4, %s PPO schedule"
+                               % (N, T, args.schedule),
+                   "envs": N, "horizon": T, "family": 1, "rays": 320, "actor": "181-64-4", "critic": "32-64-1",
+                   "epochs": epochs, "minibatch": minibatch, "lanes_per_env": args.lanes,
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "kernels": kernels,
+        "secondary_roofline": secondary,
+        "gpu_seconds": round(gpu_s, 4),
+    }
+    if not args.no_cpu_baseline:
+        log("bench: cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(N)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -96,3 +96,38 @@ hipError_t nav_launch_clearance_fixture(const float* worlds, const float* points
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- calibration copy
+namespace nav {
+__global__ __launch_bounds__(256) void calib_copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                         uint64_t n) {
+    for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256)
+        dst[i] = src[i];
+}
+}  // namespace nav
+
+extern "C" int mdn_calib_copy(uint64_t bytes, uint32_t repeats, double* ms) {
+    if (bytes == 0 || bytes % 16 || repeats == 0 || !ms) return -1;
+    void *a = nullptr, *b = nullptr;
+    if (hipMalloc(&a, bytes) != hipSuccess) return -2;
+    if (hipMalloc(&b, bytes) != hipSuccess) { hipFree(a); return -2; }
+    hipMemset(a, 1, bytes);
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0);
+    hipEventCreate(&e1);
+    const uint64_t n = bytes / 16;
+    hipLaunchKernelGGL(nav::calib_copy_kernel, dim3(2048), dim3(256), 0, nullptr, (const uint4*)a, (uint4*)b, n);
+    hipEventRecord(e0, nullptr);
+    for (uint32_t r = 0; r < repeats; r++)
+        hipLaunchKernelGGL(nav::calib_copy_kernel, dim3(2048), dim3(256), 0, nullptr, (const uint4*)a, (uint4*)b, n);
+    hipEventRecord(e1, nullptr);
+    hipEventSynchronize(e1);
+    float t = 0;
+    hipEventElapsedTime(&t, e0, e1);
+    *ms = double(t) / repeats;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipFree(a);
+    hipFree(b);
+    return 0;
+}

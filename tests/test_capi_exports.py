@@ -12,8 +12,8 @@ from oracle_lib import crazyflie, oracle, ptr
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared():
-    text = open(os.path.join(ROOT, "include", "mdnav.h")).read()
+def declared(header="mdnav.h"):
+    text = open(os.path.join(ROOT, "include", header)).read()
     return sorted(set(re.findall(r"\b(mdn_[a-z_]+)\s*\(", text)))
 
 
@@ -24,6 +24,8 @@ def test_every_declared_symbol_is_exported():
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     assert set(names) == set(native.EXPORTS)
+    for n in declared("mdnav_calib.h"):
+        assert hasattr(lib, n), n
     assert native.lib().mdn_version().decode().startswith("mdnav")
 
 
