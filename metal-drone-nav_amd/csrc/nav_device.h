@@ -153,6 +153,63 @@ __device__ __forceinline__ float cast_ray(const float* world, const float* cente
     return fmax_f(0.0f, best);
 }
 
+// Fast path of cast_ray for a world of up to 8 axis-aligned boxes when no
+// ray direction component is below the slab epsilon.  Per env and tick the
+// constants (-e - pp) and (e - pp) of world.hpp:53 are formed once (same
+// operations, hoisted out of the ray loop); per ray only the products with
+// 1/d and the interval updates remain.  Inside the slab the hardware
+// min/max may differ from the select form only in the sign of a zero, which
+// the final fmax(0, best) of world.hpp:82 maps to +0, so depths are
+// bit-identical to cast_ray.
+struct BoxSlabs {
+    float A[9][3], B[9][3];  // slot 0: room, 1..8: boxes
+    uint32_t n;              // live boxes
+};
+__device__ __forceinline__ void make_box_slabs(const float* world, const float* centers, uint32_t count, V p,
+                                               BoxSlabs& bs) {
+    const float pr[3] = {p.x - 6.0f, p.y - 0.0f, p.z - 2.5f}, er[3] = {8.0f, 5.0f, 2.5f};
+#pragma unroll
+    for (int j = 0; j < 3; j++) { bs.A[0][j] = -er[j] - pr[j]; bs.B[0][j] = er[j] - pr[j]; }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float* o = world + 10 * i;
+        const float cc[3] = {centers[3 * i], centers[3 * i + 1], centers[3 * i + 2]};
+        const float pp[3] = {p.x - cc[0], p.y - cc[1], p.z - cc[2]};
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            bs.A[i + 1][j] = -o[4 + j] - pp[j];
+            bs.B[i + 1][j] = o[4 + j] - pp[j];
+        }
+    }
+    bs.n = count;
+}
+__device__ __forceinline__ bool boxes_only(const float* world, uint32_t count) {
+    if (count > 8) return false;
+    bool ok = true;
+    for (uint32_t i = 0; i < count; i++) ok = ok && float_bits(world[10 * i]) == 0u;
+    return ok;
+}
+__device__ __forceinline__ float slab_fast(const float (&A)[3], const float (&B)[3], const float (&inv)[3]) {
+    float a = A[0] * inv[0], b = B[0] * inv[0];
+    float lo = __builtin_fminf(a, b), hi = __builtin_fmaxf(a, b);
+#pragma unroll
+    for (int j = 1; j < 3; j++) {
+        a = A[j] * inv[j];
+        b = B[j] * inv[j];
+        lo = __builtin_fmaxf(lo, __builtin_fminf(a, b));
+        hi = __builtin_fminf(hi, __builtin_fmaxf(a, b));
+    }
+    return hi < __builtin_fmaxf(lo, 0.0f) ? 1000.0f : (lo >= 0 ? lo : hi);
+}
+__device__ __forceinline__ float cast_ray_boxes(const BoxSlabs& bs, V d) {
+    const float inv[3] = {1.0f / d.x, 1.0f / d.y, 1.0f / d.z};
+    float best = __builtin_fminf(12.0f, slab_fast(bs.A[0], bs.B[0], inv));
+#pragma unroll
+    for (int i = 1; i < 9; i++)
+        if (uint32_t(i) <= bs.n) best = __builtin_fminf(best, slab_fast(bs.A[i], bs.B[i], inv));
+    return fmax_f(0.0f, best);
+}
+
 // world.hpp:84-99
 __device__ __forceinline__ float clearance_at(const float* world, uint32_t count, V p, float time) {
     float best = fmin_f(fmin_f(p.x + 2, 14 - p.x), fmin_f(fmin_f(p.y + 5, 5 - p.y), fmin_f(p.z, 5 - p.z))) - 0.18f;
@@ -267,22 +324,35 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const St
         if (a > 1.0f) a = 1.0f;
         sp[i] = a * half + P.action_min + half;
     }
-    State k1, k2, k3, k4, tmp;
-    derivative(P, s, sp, wind, k1);
-    axpy_state(s, k1, 0.5f * P.dt, tmp);
-    derivative(P, tmp, sp, wind, k2);
-    axpy_state(s, k2, 0.5f * P.dt, tmp);
-    derivative(P, tmp, sp, wind, k3);
-    axpy_state(s, k3, P.dt, tmp);
-    derivative(P, tmp, sp, wind, k4);
+    // k1 + 2 k2 + 2 k3 + k4 accumulated left to right as it is written in
+    // physics.hpp:133-142, so only one stage derivative is live at a time.
+    State k, acc, tmp;
+    derivative(P, s, sp, wind, k);
+    axpy_state(s, k, 0.5f * P.dt, tmp);
+    acc = k;
+    derivative(P, tmp, sp, wind, k);
+    axpy_state(s, k, 0.5f * P.dt, tmp);
+    {
+        float* a = &acc.p[0];
+        const float* b = &k.p[0];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) a[i] = a[i] + 2.0f * b[i];
+    }
+    derivative(P, tmp, sp, wind, k);
+    axpy_state(s, k, P.dt, tmp);
+    {
+        float* a = &acc.p[0];
+        const float* b = &k.p[0];
+#pragma unroll
+        for (int i = 0; i < 17; ++i) a[i] = a[i] + 2.0f * b[i];
+    }
+    derivative(P, tmp, sp, wind, k);
     const float* a0 = &s.p[0];
-    const float* a1 = &k1.p[0];
-    const float* a2 = &k2.p[0];
-    const float* a3 = &k3.p[0];
-    const float* a4 = &k4.p[0];
+    const float* ak = &k.p[0];
+    float* ac = &acc.p[0];
     float* o = &next.p[0];
 #pragma unroll
-    for (int i = 0; i < 17; ++i) o[i] = a0[i] + P.dt * (a1[i] + 2.0f * a2[i] + 2.0f * a3[i] + a4[i]) / 6.0f;
+    for (int i = 0; i < 17; ++i) o[i] = a0[i] + P.dt * (ac[i] + ak[i]) / 6.0f;
     const float norm = sqrt_f(next.q[0] * next.q[0] + next.q[1] * next.q[1] + next.q[2] * next.q[2] + next.q[3] * next.q[3]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) next.q[i] /= norm;

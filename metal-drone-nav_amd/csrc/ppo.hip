@@ -3,11 +3,13 @@
 // Reductions follow one canonical order shared with the CPU oracle so both
 // round identically:
 //   * dot products accumulate from the bias, inputs ascending (ppo.hpp:65-93);
-//   * sums over minibatch rows: sequential within 256-row chunks, then
-//     sequential over chunks (a single chunk at the reference's 256-row
-//     minibatch, i.e. ppo_actor_grad_direct's order, ppo.metal:497-519);
+//   * sums over minibatch rows: sequential within 256-row chunks, chunk
+//     partials sequential within groups of 32 chunks, then over the groups
+//     (a single chunk at the reference's 256-row minibatch, i.e.
+//     ppo_actor_grad_direct's order, ppo.metal:497-519);
 //   * squared gradient norm: 256 strided partials then a pairwise tree;
-//   * advantage statistics in double: chunks of 256, then over chunks.
+//   * advantage statistics in double: chunks of 256, groups of 64 chunks,
+//     then over groups.
 // The 64-wide hidden layers are evaluated on the VALU with weights as
 // wave-uniform scalar loads: one lane owns one row (forward) or one input
 // feature (weight gradient), so every accumulation is a private serial chain.
@@ -24,6 +26,8 @@ constexpr uint32_t OBS = MDN_ACTOR_OBS_POOLED;
 constexpr uint32_t COBS = MDN_CRITIC_OBS;
 constexpr uint32_t HID = MDN_HIDDEN;
 constexpr uint32_t CHUNK = 256;
+constexpr uint32_t GRAD_GROUP = 32;   // chunk partials per group (gradient sums)
+constexpr uint32_t NORM_GROUP = 64;   // chunk partials per group (advantage statistics)
 constexpr float LOG_TWO_PI = 1.8378770664093453f;
 
 constexpr uint32_t A_B1 = HID * OBS, A_W2 = A_B1 + HID, A_B2 = A_W2 + 4 * HID, A_LS = A_B2 + 4, A_COUNT = A_LS + 4;
@@ -75,14 +79,26 @@ __global__ __launch_bounds__(256) void norm_chunks_kernel(const float* __restric
     }
     part[c] = s;
 }
-// Sequential sum over chunks; pass 0 writes the float mean, pass 1 the
-// inverse standard deviation 1/sqrt(var + eps).
+// Chunk partials summed within groups of NORM_GROUP (one thread per group),
+// in place into part[group * NORM_GROUP].
+__global__ __launch_bounds__(256) void norm_groups_kernel(double* __restrict__ part, uint64_t count) {
+    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
+    const uint64_t g = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    const uint64_t c0 = g * NORM_GROUP;
+    if (c0 >= chunks) return;
+    const uint64_t end = c0 + NORM_GROUP < chunks ? c0 + NORM_GROUP : chunks;
+    double s = 0.0;
+    for (uint64_t c = c0; c < end; ++c) s += part[c];
+    part[c0] = s;
+}
+// Sequential sum over the group sums; pass 0 writes the float mean, pass 1
+// the inverse standard deviation 1/sqrt(var + eps).
 __global__ void norm_finish_kernel(const double* __restrict__ part, uint64_t count, float* __restrict__ stats,
                                    float eps, int pass) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
     double s = 0.0;
-    for (uint64_t c = 0; c < chunks; ++c) s += part[c];
+    for (uint64_t c = 0; c < chunks; c += NORM_GROUP) s += part[c];
     if (pass == 0) stats[0] = float(s / double(count));
     else stats[1] = 1.0f / sqrt_f(float(s / double(count)) + eps);
 }
@@ -99,17 +115,34 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(float* __restrict__ a, 
 // Forward, per-row loss/derivatives (ppo.hpp:144-181) and hidden deltas
 // (ppo.metal:470-485, 618-631); one lane per row.
 __global__ __launch_bounds__(256) void rows_kernel(RowArgs a) {
-    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
-    if (n >= a.b) return;
-    const float* x = a.obs + size_t(n) * OBS;
+    // Row tiles are staged through LDS 16 features at a time with coalesced
+    // loads; each lane then walks its own row (padding 17 avoids bank
+    // conflicts) while the weights arrive as wave-uniform scalar loads.
+    __shared__ float tile[256][17];
+    const uint32_t t = threadIdx.x, n0 = blockIdx.x * 256;
+    const uint32_t n = n0 + t;
+    const bool live = n < a.b;
     float h[HID];
 #pragma unroll
     for (uint32_t k = 0; k < HID; k++) h[k] = a.actor[A_B1 + k];
-    for (uint32_t i = 0; i < OBS; i++) {
-        const float xi = x[i];
-        const float* w = a.actor_w1t + size_t(i) * HID;
+    for (uint32_t i0 = 0; i0 < OBS; i0 += 16) {
+        for (uint32_t e = t; e < 256 * 16; e += 256) {
+            const uint32_t rr = e / 16, cc = e % 16;
+            const uint32_t row = n0 + rr, col = i0 + cc;
+            tile[rr][cc] = (row < a.b && col < OBS) ? a.obs[size_t(row) * OBS + col] : 0.0f;
+        }
+        __syncthreads();
+        const uint32_t cnt = OBS - i0 < 16 ? OBS - i0 : 16;
 #pragma unroll
-        for (uint32_t k = 0; k < HID; k++) h[k] += w[k] * xi;
+        for (uint32_t c = 0; c < 16; c++) {
+            if (c < cnt) {
+                const float xi = tile[t][c];
+                const float* w = a.actor_w1t + size_t(i0 + c) * HID;
+#pragma unroll
+                for (uint32_t k = 0; k < HID; k++) h[k] += w[k] * xi;
+            }
+        }
+        __syncthreads();
     }
 #pragma unroll
     for (uint32_t k = 0; k < HID; k++) h[k] = tanh_f(h[k]);
@@ -121,16 +154,26 @@ __global__ __launch_bounds__(256) void rows_kernel(RowArgs a) {
         for (uint32_t k = 0; k < HID; k++) z += a.actor[A_W2 + q * HID + k] * h[k];
         mean[q] = z;
     }
-    const float* cx = a.co + size_t(n) * COBS;
     float g[HID];
 #pragma unroll
     for (uint32_t k = 0; k < HID; k++) g[k] = a.critic[C_B1 + k];
-    for (uint32_t i = 0; i < COBS; i++) {
-        const float xi = cx[i];
-        const float* w = a.critic_w1t + size_t(i) * HID;
+    for (uint32_t i0 = 0; i0 < COBS; i0 += 16) {
+        for (uint32_t e = t; e < 256 * 16; e += 256) {
+            const uint32_t rr = e / 16, cc = e % 16;
+            const uint32_t row = n0 + rr;
+            tile[rr][cc] = row < a.b ? a.co[size_t(row) * COBS + i0 + cc] : 0.0f;
+        }
+        __syncthreads();
 #pragma unroll
-        for (uint32_t k = 0; k < HID; k++) g[k] += w[k] * xi;
+        for (uint32_t c = 0; c < 16; c++) {
+            const float xi = tile[t][c];
+            const float* w = a.critic_w1t + size_t(i0 + c) * HID;
+#pragma unroll
+            for (uint32_t k = 0; k < HID; k++) g[k] += w[k] * xi;
+        }
+        __syncthreads();
     }
+    if (!live) return;
 #pragma unroll
     for (uint32_t k = 0; k < HID; k++) g[k] = tanh_f(g[k]);
     float value = a.critic[C_B2];
@@ -275,13 +318,24 @@ __global__ __launch_bounds__(512) void small_grad_kernel(const float* __restrict
     P[out] = acc;
 }
 
-// Sequential sum over chunks: grad[p] = 0 + part[0][p] + part[1][p] + ...
+// Chunk partials summed within groups of GRAD_GROUP chunks, in place into
+// the group's first chunk row; grid (param blocks, groups).
+__global__ __launch_bounds__(256) void group_reduce_kernel(float* __restrict__ part, uint32_t chunks) {
+    const uint32_t p = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t c0 = blockIdx.y * GRAD_GROUP;
+    if (p >= P_TOTAL || c0 >= chunks) return;
+    const uint32_t end = c0 + GRAD_GROUP < chunks ? c0 + GRAD_GROUP : chunks;
+    float s = 0.0f;
+    for (uint32_t c = c0; c < end; c++) s += part[size_t(c) * P_TOTAL + p];
+    part[size_t(c0) * P_TOTAL + p] = s;
+}
+// Sequential sum over the group sums: grad[p] = 0 + g0[p] + g1[p] + ...
 __global__ __launch_bounds__(256) void chunk_reduce_kernel(const float* __restrict__ part, float* __restrict__ grad,
                                                            uint32_t chunks) {
     const uint32_t p = blockIdx.x * 256 + threadIdx.x;
     if (p >= P_TOTAL) return;
     float total = 0.0f;
-    for (uint32_t c = 0; c < chunks; c++) total += part[size_t(c) * P_TOTAL + p];
+    for (uint32_t c = 0; c < chunks; c += GRAD_GROUP) total += part[size_t(c) * P_TOTAL + p];
     grad[p] = total;
 }
 
@@ -381,6 +435,8 @@ hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* s
     const uint32_t cb = uint32_t((chunks + 255) / 256);
     for (int pass = 0; pass < 2; pass++) {
         hipLaunchKernelGGL(ppo::norm_chunks_kernel, dim3(cb), dim3(256), 0, st, a, count, part, stats, pass);
+        const uint64_t groups = (chunks + ppo::NORM_GROUP - 1) / ppo::NORM_GROUP;
+        hipLaunchKernelGGL(ppo::norm_groups_kernel, dim3(uint32_t((groups + 255) / 256)), dim3(256), 0, st, part, count);
         hipLaunchKernelGGL(ppo::norm_finish_kernel, dim3(1), dim3(64), 0, st, part, count, stats, eps, pass);
     }
     hipLaunchKernelGGL(ppo::norm_apply_kernel, dim3(uint32_t((count + 255) / 256)), dim3(256), 0, st, a, count, stats);
@@ -399,6 +455,8 @@ hipError_t ppo_launch_grads(const float* obs, const float* co, const float* ah, 
     hipLaunchKernelGGL(ppo::w1_grad_kernel, dim3(chunks, 2), dim3(192), 0, st, obs, co, adelta, cdelta, part, b);
     hipLaunchKernelGGL(ppo::small_grad_kernel, dim3(chunks), dim3(512), 0, st, ah, adelta, ch, cdelta, dm, dls, dv, loss,
                        part, b);
+    const uint32_t groups = (chunks + ppo::GRAD_GROUP - 1) / ppo::GRAD_GROUP;
+    hipLaunchKernelGGL(ppo::group_reduce_kernel, dim3((ppo::P_TOTAL + 255) / 256, groups), dim3(256), 0, st, part, chunks);
     hipLaunchKernelGGL(ppo::chunk_reduce_kernel, dim3((ppo::P_TOTAL + 255) / 256), dim3(256), 0, st, part, grad, chunks);
     return hipGetLastError();
 }

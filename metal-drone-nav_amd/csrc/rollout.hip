@@ -277,6 +277,9 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
             const float noise = clean_env(C, nn) ? 0.0f : C.depth_noise;
             const float drop = clean_env(C, nn) ? 0.0f : C.dropout;
             float* ring = a.sensors + (size_t(nn) * 8 + slot8) * PIX;
+            const bool fast = boxes_only(world, count);
+            BoxSlabs bs;
+            if (fast) make_box_slabs(world, s_cent[grp], count, origin, bs);
             for (uint32_t b = lane; b < POOL; b += G) {
                 const uint32_t y = (b / 10) * 2, x = (b % 10) * 2;
                 float pooled = 12.0f;
@@ -288,7 +291,11 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
                         const float rx = a.camera[3 * k], ry = a.camera[3 * k + 1], rz = a.camera[3 * k + 2];
                         const V d = mk(R[0] * rx + R[1] * ry + R[2] * rz, R[3] * rx + R[4] * ry + R[5] * rz,
                                        R[6] * rx + R[7] * ry + R[8] * rz);
-                        float depth = cast_ray(world, s_cent[grp], count, origin, d);
+                        float depth;
+                        if (fast && fabs_f(d.x) >= 1e-8f && fabs_f(d.y) >= 1e-8f && fabs_f(d.z) >= 1e-8f)
+                            depth = cast_ray_boxes(bs, d);
+                        else
+                            depth = cast_ray(world, s_cent[grp], count, origin, d);
                         if (noise != 0 || drop != 0) {
                             uint32_t nr = r.rng + k * 1664525u + r.steps * 1013904223u;
                             depth = clamp_f(depth + noise * normal_draw(nr), 0.0f, 12.0f);
@@ -375,6 +382,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
             float acc[HU];
 #pragma unroll
             for (int k = 0; k < HU; k++) acc[k] = A[a_b1 + lane * HU + k];
+#pragma unroll 4
             for (uint32_t i = 0; i < OBS; i++) {
                 const float x = s_obs[grp][i];
                 const float* w = a.actor_w1t + size_t(i) * HID + lane * HU;
@@ -385,6 +393,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
             for (int k = 0; k < HU; k++) s_ah[grp][lane * HU + k] = tanh_f(acc[k]);
 #pragma unroll
             for (int k = 0; k < HU; k++) acc[k] = CR[c_b1 + lane * HU + k];
+#pragma unroll 4
             for (uint32_t i = 0; i < COBS; i++) {
                 const float x = s_co[grp][i];
                 const float* w = a.critic_w1t + size_t(i) * HID + lane * HU;
@@ -403,10 +412,12 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 float z = A[a_b2 + q];
+#pragma unroll 8
                 for (uint32_t h = 0; h < HID; h++) z += A[a_w2 + q * HID + h] * s_ah[grp][h];
                 mean[q] = z;
             }
             float value = CR[c_b2];
+#pragma unroll 8
             for (uint32_t h = 0; h < HID; h++) value += CR[c_w2 + h] * s_ch[grp][h];
             uint32_t rng = r.rng;
             float lp = 0, act[4];
@@ -597,6 +608,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
             float acc[HU];
 #pragma unroll
             for (int k = 0; k < HU; k++) acc[k] = CR[c_b1 + lane * HU + k];
+#pragma unroll 4
             for (uint32_t i = 0; i < COBS; i++) {
                 const float x = s_co[grp][i];
                 const float* w = a.critic_w1t + size_t(i) * HID + lane * HU;
@@ -610,6 +622,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
         uint32_t reset_rng = 0, reset_family = 0, reset_seed = 0;
         if (active) {
             float value = CR[c_b2];
+#pragma unroll 8
             for (uint32_t h = 0; h < HID; h++) value += CR[c_w2 + h] * s_ch[grp][h];
             if (lane == 0) a.next_values[row] = value;
             if (ended) {

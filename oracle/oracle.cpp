@@ -9,11 +9,13 @@
  * also uses (one definition, so both produce the same bits):
  *   - dot products:   z = b; z += w[i]*x[i] for i ascending (ppo.hpp:65-93);
  *   - sums over the rows of a minibatch: sequential within 256-row chunks,
- *     then sequentially over chunks (a single chunk at the reference's
- *     256-row minibatch, i.e. the order of ppo_actor_grad_direct,
+ *     chunk partials summed sequentially within groups of 32 chunks, group
+ *     sums sequentially (a single chunk at the reference's 256-row
+ *     minibatch, i.e. the order of ppo_actor_grad_direct,
  *     ppo.metal:497-519);
  *   - squared gradient norm: 256 strided partial sums, then a pairwise tree;
- *   - advantage mean/variance: double, chunks of 256 rows then over chunks.
+ *   - advantage mean/variance: double, chunks of 256 rows, groups of 64
+ *     chunks, then over groups.
  * Build: g++ -O2 -fopenmp -ffp-contract=off (see oracle/Makefile).
  */
 #include <omp.h>
@@ -29,6 +31,8 @@
 namespace orc {
 
 constexpr uint32_t kChunk = 256;
+constexpr uint32_t kGradGroup = 32;   // chunk partials per group (gradient sums)
+constexpr uint32_t kNormGroup = 64;   // chunk partials per group (advantage statistics)
 constexpr float kGamma = 0.99f, kLambda = 0.95f, kClip = 0.2f, kValueCoef = 0.5f, kGradClip = 0.5f;
 constexpr float kBeta1 = 0.9f, kBeta2 = 0.999f, kAdamEps = 1.0e-8f;
 constexpr float kLogTwoPi = 1.8378770664093453f;
@@ -123,6 +127,17 @@ inline void compute_gae(uint32_t horizon, uint32_t n, const float* r, const floa
         }
     }
 }
+// Sequential within groups of `group` partials, then over the group sums.
+template <class T>
+inline T grouped_sum(const std::vector<T>& part, size_t group) {
+    T total = T(0);
+    for (size_t g0 = 0; g0 < part.size(); g0 += group) {
+        T s = T(0);
+        for (size_t c = g0; c < std::min(part.size(), g0 + group); ++c) s += part[c];
+        total += s;
+    }
+    return total;
+}
 // ppo.hpp:128-140 with the canonical chunked double sums.
 inline void normalize_advantages(float* a, size_t count, float eps) {
     if (count == 0) return;
@@ -134,8 +149,7 @@ inline void normalize_advantages(float* a, size_t count, float eps) {
         for (size_t i = size_t(c) * kChunk; i < std::min(count, size_t(c + 1) * kChunk); ++i) s += double(a[i]);
         part[c] = s;
     }
-    double sum = 0.0;
-    for (size_t c = 0; c < chunks; ++c) sum += part[c];
+    const double sum = grouped_sum(part, kNormGroup);
     const float mean = float(sum / double(count));
 #pragma omp parallel for schedule(static)
     for (int64_t c = 0; c < int64_t(chunks); ++c) {
@@ -146,8 +160,7 @@ inline void normalize_advantages(float* a, size_t count, float eps) {
         }
         part[c] = s;
     }
-    double sq = 0.0;
-    for (size_t c = 0; c < chunks; ++c) sq += part[c];
+    const double sq = grouped_sum(part, kNormGroup);
     const float inv = 1.0f / sqrt_f(float(sq / double(count)) + eps);
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < int64_t(count); ++i) a[i] = (a[i] - mean) * inv;
@@ -571,11 +584,11 @@ struct Trainer {
         // metrics row (main.mm:941-951) with chunked sums
         const uint32_t chunks = (b + kChunk - 1) / kChunk;
         float msum[4] = {0, 0, 0, 0};
-        for (uint32_t c = 0; c < chunks; c++) {
-            float part[4] = {0, 0, 0, 0};
-            for (uint32_t n = c * kChunk; n < std::min(b, (c + 1) * kChunk); n++)
-                for (int k = 0; k < 4; k++) part[k] += losses[size_t(n) * 4 + k];
-            for (int k = 0; k < 4; k++) msum[k] += part[k];
+        for (int k = 0; k < 4; k++) {
+            std::vector<float> part(chunks, 0.0f);
+            for (uint32_t c = 0; c < chunks; c++)
+                for (uint32_t n = c * kChunk; n < std::min(b, (c + 1) * kChunk); n++) part[c] += losses[size_t(n) * 4 + k];
+            msum[k] = grouped_sum(part, kGradGroup);
         }
         msum[3] /= float(b);
         for (int k = 0; k < 4; k++) metric_row[k] = msum[k];
@@ -619,12 +632,20 @@ struct Trainer {
 #pragma omp parallel for schedule(static)
         for (int64_t p = 0; p < int64_t(AP); p++) {
             float total = 0.0f;
-            for (uint32_t c = 0; c < chunks; c++) total += apart[size_t(c) * AP + size_t(p)];
+            for (uint32_t g0 = 0; g0 < chunks; g0 += kGradGroup) {
+                float s = 0.0f;
+                for (uint32_t c = g0; c < std::min(chunks, g0 + kGradGroup); c++) s += apart[size_t(c) * AP + size_t(p)];
+                total += s;
+            }
             ag[p] = total;
         }
         for (uint32_t p = 0; p < CP; p++) {
             float total = 0.0f;
-            for (uint32_t c = 0; c < chunks; c++) total += cpart[size_t(c) * CP + p];
+            for (uint32_t g0 = 0; g0 < chunks; g0 += kGradGroup) {
+                float s = 0.0f;
+                for (uint32_t c = g0; c < std::min(chunks, g0 + kGradGroup); c++) s += cpart[size_t(c) * CP + p];
+                total += s;
+            }
             cg[p] = total;
         }
         if (dm_out) std::copy(dm.begin(), dm.end(), dm_out);

@@ -162,12 +162,15 @@ def test_iteration_parity(epochs, minibatch):
         assert np.abs(ppo.metric_mean() - ora.metric_mean()).max() <= TOL
 
 
-def test_baseline_schedule_parity_large_minibatch():
-    """One epoch of four minibatches (the benchmark schedule) at N=256, T=64:
-    minibatches of 4096 rows exercise the multi-chunk gradient reduction."""
-    say("case: iteration N=256 T=64 epochs=1 minibatch=4096")
-    cfg = config(n=256, family=1, speed=1.0, distance=3.0)
-    sim, ppo, ora = make_pair(cfg, 64, epochs=1, minibatch=4096)
+@pytest.mark.parametrize("n,minibatch", [(256, 4096), (512, 16384)])
+def test_baseline_schedule_parity_large_minibatch(n, minibatch):
+    """One epoch of four minibatches (the benchmark schedule) at T=64:
+    minibatches of 4096 rows exercise the multi-chunk gradient reduction,
+    16384 rows (64 chunks) its two-level grouping, and 32768 rows (128
+    chunks) the grouped advantage statistics."""
+    say("case: iteration N=%d T=64 epochs=1 minibatch=%d" % (n, minibatch))
+    cfg = config(n=n, family=1, speed=1.0, distance=3.0)
+    sim, ppo, ora = make_pair(cfg, 64, epochs=1, minibatch=minibatch)
     sim.collect()
     ppo.rollout_update(0)
     sim.sync()
