@@ -65,6 +65,34 @@ def cpu_baseline(envs, target_s=12.0):
                       "%d OpenMP threads on %d host CPUs" % (envs, horizon, done, el, threads, os.cpu_count())}
 
 
+def calib_copy(nbytes, repeats=3):
+    import ctypes
+    from mdnav import native
+    lib = native.lib()
+    lib.mdn_calib_copy.restype = ctypes.c_int
+    lib.mdn_calib_copy.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double)]
+    ms = ctypes.c_double()
+    rc = lib.mdn_calib_copy(nbytes, repeats, ctypes.byref(ms))
+    if rc:
+        raise SystemExit("mdn_calib_copy failed: %d" % rc)
+    print(json.dumps({"calib_copy_bytes": nbytes, "launches": repeats + 1, "avg_ms": ms.value,
+                      "GBps": 2 * nbytes / (ms.value * 1e-3) / 1e9}), flush=True)
+
+
+def traffic_from_profile():
+    """HBM bytes per rollout launch from the committed PMC summary (the line
+    'traffic_bytes_per_launch: N'), or None when it is absent."""
+    path = os.path.join(ROOT, "profiles", "rollout_kernel_pmc_8192x128.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -76,11 +104,18 @@ def main():
                     help="baseline: 1 epoch x 4 minibatches; reference: 2 epochs x 256-row minibatches")
     ap.add_argument("--lanes", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="BYTES",
+                    help="run only the plain copy kernel over BYTES (reads BYTES, writes BYTES per launch); "
+                         "its FETCH_SIZE/WRITE_SIZE readings scale the rollout kernel's counters to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box holds one MI355X); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.calib_copy:
+        calib_copy(args.calib_copy)
+        return
 
     from mdnav import PPOTrainer, Sim, abi
     N, T = args.envs, args.horizon
@@ -118,7 +153,8 @@ def main():
     avg_s = roll["avg_ms"] * 1e-3
     achieved = FLOP_ENV_STEP * env_steps_launch / avg_s
     roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP32, 4), "traffic": None,
+                "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic_from_profile(),
+                "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)",
                 "kernel": "rollout_kernel (fused env step + rollout actor/critic, %d ticks per launch)" % T,
                 "roof_note": "fp32 compute roof (VALU work, no MFMA); algorithmic %.1f kFLOP and %.2f KB per "
                              "env-step x %d env-steps per launch" % (FLOP_ENV_STEP / 1e3, BYTES_ENV_STEP / 1e3,

@@ -32,6 +32,7 @@ enum RunWord : uint32_t {
 };
 constexpr uint32_t STATE_WORDS = 17;
 constexpr uint32_t WORLD_WORDS = 169;
+constexpr uint32_t RAPTOR_WORDS = sizeof(MdnRaptorWeights) / sizeof(float);
 
 struct State { float p[3], q[4], v[3], w[3], rpm[4]; };
 

@@ -114,14 +114,31 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(float* __restrict__ a, 
 
 // Forward, per-row loss/derivatives (ppo.hpp:144-181) and hidden deltas
 // (ppo.metal:470-485, 618-631); one lane per row.
+// Writes one 64-float value per row of the block's 256-row tile, transposed
+// through LDS so that global stores are contiguous across lanes (the row-major
+// [row][64] layout the gradient kernels read).
+__device__ __forceinline__ void store_rows64(float* lds, const float (&v)[HID], float* __restrict__ dst, uint32_t n0,
+                                             uint32_t rows) {
+    const uint32_t t = threadIdx.x;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) lds[t * (HID + 1) + k] = v[k];
+    __syncthreads();
+    float* out = dst + size_t(n0) * HID;
+    for (uint32_t e = t; e < rows * HID; e += 256) out[e] = lds[(e / HID) * (HID + 1) + e % HID];
+}
+
 __global__ __launch_bounds__(256) void rows_kernel(RowArgs a) {
     // Row tiles are staged through LDS 16 features at a time with coalesced
     // loads; each lane then walks its own row (padding 17 avoids bank
-    // conflicts) while the weights arrive as wave-uniform scalar loads.
-    __shared__ float tile[256][17];
+    // conflicts) while the weights arrive as wave-uniform scalar loads.  The
+    // same LDS then stages the per-row outputs.
+    __shared__ float lds[256 * (HID + 1)];
+    float(*tile)[17] = reinterpret_cast<float(*)[17]>(lds);
     const uint32_t t = threadIdx.x, n0 = blockIdx.x * 256;
     const uint32_t n = n0 + t;
     const bool live = n < a.b;
+    const uint32_t rows = a.b - n0 < 256 ? a.b - n0 : 256;
     float h[HID];
 #pragma unroll
     for (uint32_t k = 0; k < HID; k++) h[k] = a.actor[A_B1 + k];
@@ -173,15 +190,16 @@ __global__ __launch_bounds__(256) void rows_kernel(RowArgs a) {
         }
         __syncthreads();
     }
-    if (!live) return;
 #pragma unroll
     for (uint32_t k = 0; k < HID; k++) g[k] = tanh_f(g[k]);
     float value = a.critic[C_B2];
 #pragma unroll
     for (uint32_t k = 0; k < HID; k++) value += a.critic[C_W2 + k] * g[k];
 
-    // sample_loss_and_grad
-    const float* act = a.actions + size_t(n) * 4;
+    // sample_loss_and_grad (rows past the minibatch compute on index 0 and
+    // store nothing)
+    const uint32_t m = live ? n : 0;
+    const float* act = a.actions + size_t(m) * 4;
     const float* ls = a.actor + A_LS;
     float logp = 0.0f;
 #pragma unroll
@@ -190,10 +208,10 @@ __global__ __launch_bounds__(256) void rows_kernel(RowArgs a) {
         const float d = (act[q] - mean[q]) * inv_std;
         logp += -0.5f * (d * d + 2.0f * ls[q] + LOG_TWO_PI);
     }
-    const float raw = logp - a.old_logp[n];
+    const float raw = logp - a.old_logp[m];
     const float lr = clamp_f(raw, -20.0f, 20.0f);
     const float ratio = exp_f(lr);
-    const float adv = a.adv[n], target = a.ret[n];
+    const float adv = a.adv[m], target = a.ret[m];
     const float clipped = clamp_f(ratio, 1.0f - a.clip, 1.0f + a.clip);
     const float chosen = min_f(ratio * adv, clipped * adv);
     const bool in_range = raw >= -20.0f && raw <= 20.0f;
@@ -216,31 +234,32 @@ __global__ __launch_bounds__(256) void rows_kernel(RowArgs a) {
         entropy += -a.ecoef * (ls[q] + 0.5f * (1.0f + LOG_TWO_PI)) * scale;
     }
     const float dvalue = a.vcoef * (value - target) * scale;
-    float* lo = a.loss + size_t(n) * 4;
-    lo[0] = -chosen * scale;
-    lo[1] = 0.5f * a.vcoef * (value - target) * (value - target) * scale;
-    lo[2] = entropy;
-    lo[3] = ratio;
+    if (live) {
+        float* lo = a.loss + size_t(n) * 4;
+        lo[0] = -chosen * scale;
+        lo[1] = 0.5f * a.vcoef * (value - target) * (value - target) * scale;
+        lo[2] = entropy;
+        lo[3] = ratio;
 #pragma unroll
-    for (uint32_t q = 0; q < 4; q++) {
-        a.dm[size_t(n) * 4 + q] = dmean[q];
-        a.dls[size_t(n) * 4 + q] = dlog[q];
+        for (uint32_t q = 0; q < 4; q++) {
+            a.dm[size_t(n) * 4 + q] = dmean[q];
+            a.dls[size_t(n) * 4 + q] = dlog[q];
+        }
+        a.dv[n] = dvalue;
     }
-    a.dv[n] = dvalue;
-    float* ah = a.ah + size_t(n) * HID;
-    float* ad = a.adelta + size_t(n) * HID;
-    float* ch = a.ch + size_t(n) * HID;
-    float* cd = a.cdelta + size_t(n) * HID;
+    store_rows64(lds, h, a.ah, n0, rows);
 #pragma unroll
     for (uint32_t k = 0; k < HID; k++) {
         float d = 0.0f;
 #pragma unroll
         for (uint32_t q = 0; q < 4; q++) d += dmean[q] * a.actor[A_W2 + q * HID + k];
-        ah[k] = h[k];
-        ad[k] = d * (1.0f - h[k] * h[k]);
-        ch[k] = g[k];
-        cd[k] = dvalue * a.critic[C_W2 + k] * (1.0f - g[k] * g[k]);
+        h[k] = d * (1.0f - h[k] * h[k]);
     }
+    store_rows64(lds, h, a.adelta, n0, rows);
+    store_rows64(lds, g, a.ch, n0, rows);
+#pragma unroll
+    for (uint32_t k = 0; k < HID; k++) g[k] = dvalue * a.critic[C_W2 + k] * (1.0f - g[k] * g[k]);
+    store_rows64(lds, g, a.cdelta, n0, rows);
 }
 
 // ---------------------------------------------------------------- gradient partials

@@ -18,7 +18,15 @@ namespace nav {
 
 
 // ---------------------------------------------------------------- group helpers
-__device__ __forceinline__ void group_sync() { __syncthreads(); }
+// A lane group never straddles a wavefront (64 % G == 0), and LDS accesses of
+// one wavefront are performed in program order, so ordering the group's LDS
+// traffic only needs a wavefront-scope fence that the compiler cannot move
+// accesses across.
+__device__ __forceinline__ void group_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 __device__ __forceinline__ float fbits(uint32_t u) { return bits_float(u); }
 __device__ __forceinline__ uint32_t ubits(float f) { return float_bits(f); }
@@ -187,9 +195,22 @@ __global__ __launch_bounds__(64) void reset_kernel(RolloutArgs a) {
 }
 
 // ---------------------------------------------------------------- rollout
-template <int G, int K>
-__global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
-    constexpr int E = 64 / G;        // envs per workgroup (one wave)
+// W = wavefronts per workgroup.  W == 1: weights and camera rays are read from
+// global memory (L1/L2 resident).  W > 1: the workgroup stages one copy of the
+// actor first layer, the RAPTOR weights and the camera rays in LDS, shared by
+// its 64*W/G envs.
+template <int W>
+struct WeightLds {
+    float aw[OBS * HID];
+    float rw[RAPTOR_WORDS];
+    float cam[3 * PIX];
+};
+template <>
+struct WeightLds<1> {};
+
+template <int G, int K, int W>
+__global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
+    constexpr int E = 64 * W / G;    // envs per workgroup
     constexpr int U = 16 / G;        // RAPTOR units per lane
     constexpr int HU = 64 / G;       // actor/critic hidden units per lane
     const MdnSimConfig& C = a.cfg;
@@ -200,16 +221,36 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
     const bool live = n < N;
     const uint32_t nn = live ? n : 0;
 
+    __shared__ WeightLds<W> s_wt;
+    const float* AW1;   // actor W1 transposed [input][hidden]
+    const float* RW;    // RAPTOR weights (RaptorWeights layout)
+    const float* CAM;   // camera rays [pixel][3]
+    if constexpr (W > 1) {
+        for (uint32_t i = threadIdx.x; i < OBS * HID; i += 64 * W) s_wt.aw[i] = a.actor_w1t[i];
+        for (uint32_t i = threadIdx.x; i < RAPTOR_WORDS; i += 64 * W) s_wt.rw[i] = a.raptor[i];
+        for (uint32_t i = threadIdx.x; i < 3 * PIX; i += 64 * W) s_wt.cam[i] = a.camera[i];
+        __syncthreads();
+        AW1 = s_wt.aw;
+        RW = s_wt.rw;
+        CAM = s_wt.cam;
+    } else {
+        AW1 = a.actor_w1t;
+        RW = a.raptor;
+        CAM = a.camera;
+    }
+
     __shared__ float s_world[E][WORLD_WORDS + 3];
-    __shared__ float s_cent[E][48];
-    __shared__ float s_ring[E][K][POOL];
-    __shared__ float s_obs[E][OBS + 3];
-    __shared__ float s_co[E][COBS];
-    __shared__ float s_ah[E][HID];
-    __shared__ float s_ch[E][HID];
-    __shared__ float s_cmd[E][32];
-    __shared__ float s_x[E][16];
-    __shared__ float s_h[E][16];
+    // Per-env rows have odd word strides so that the E groups of a wavefront,
+    // reading the same offset of their own rows, fall in distinct banks.
+    __shared__ float s_cent[E][49];
+    __shared__ float s_ring[E][K * POOL + 1];   // slot j at [j * POOL]
+    __shared__ float s_obs[E][OBS + 4];
+    __shared__ float s_co[E][COBS + 1];
+    __shared__ float s_ah[E][HID + 1];
+    __shared__ float s_ch[E][HID + 1];
+    __shared__ float s_cmd[E][33];
+    __shared__ float s_x[E][17];
+    __shared__ float s_h[E][17];
 
     float* world = s_world[grp];
     State s;
@@ -229,14 +270,13 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
             float m = 12.0f;
             for (uint32_t dy = 0; dy < 2; dy++)
                 for (uint32_t dx = 0; dx < 2; dx++) m = min_f(m, src[(y + dy) * 20 + x + dx]);
-            s_ring[grp][slotk][b] = m;
+            s_ring[grp][slotk * POOL + b] = m;
         }
     }
     // this lane's RAPTOR units (hidden values it owns)
     float hu[U];
 #pragma unroll
     for (int j = 0; j < U; j++) hu[j] = bits_float(a.run[size_t(RW_HIDDEN + lane + G * j) * N + nn]);
-    const float* RW = a.raptor;
     const float* A = a.actor;
     const float* CR = a.critic;
     const uint32_t a_b1 = HID * OBS, a_w2 = a_b1 + HID, a_b2 = a_w2 + 4 * HID, a_ls = a_b2 + 4;
@@ -288,7 +328,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
                     for (uint32_t dx = 0; dx < 2; dx++) {
                         const uint32_t k = (y + dy) * 20 + x + dx;
-                        const float rx = a.camera[3 * k], ry = a.camera[3 * k + 1], rz = a.camera[3 * k + 2];
+                        const float rx = CAM[3 * k], ry = CAM[3 * k + 1], rz = CAM[3 * k + 2];
                         const V d = mk(R[0] * rx + R[1] * ry + R[2] * rz, R[3] * rx + R[4] * ry + R[5] * rz,
                                        R[6] * rx + R[7] * ry + R[8] * rz);
                         float depth;
@@ -304,7 +344,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
                         ring[k] = depth;
                         pooled = min_f(pooled, depth);
                     }
-                s_ring[grp][slotk][b] = pooled;
+                s_ring[grp][slotk * POOL + b] = pooled;
             }
         }
         group_sync();
@@ -317,8 +357,8 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
         float* og = a.obs + row * OBS;
         if (active) {
             for (uint32_t b = lane; b < POOL; b += G) {
-                const float cur = have ? s_ring[grp][frame % K][b] / 12.0f : 1.0f;
-                const float pre = have ? s_ring[grp][prev % K][b] / 12.0f : 1.0f;
+                const float cur = have ? s_ring[grp][(frame % K) * POOL + b] / 12.0f : 1.0f;
+                const float pre = have ? s_ring[grp][(prev % K) * POOL + b] / 12.0f : 1.0f;
                 s_obs[grp][b] = cur;
                 s_obs[grp][POOL + b] = pre;
                 og[b] = cur;
@@ -385,7 +425,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
 #pragma unroll 4
             for (uint32_t i = 0; i < OBS; i++) {
                 const float x = s_obs[grp][i];
-                const float* w = a.actor_w1t + size_t(i) * HID + lane * HU;
+                const float* w = AW1 + i * HID + lane * HU;
 #pragma unroll
                 for (int k = 0; k < HU; k++) acc[k] += w[k] * x;
             }
@@ -639,7 +679,7 @@ __global__ __launch_bounds__(64) void rollout_kernel(RolloutArgs a) {
             reset_apply(C, P, RW, nn, false, reset_rng, world, s, r);
 #pragma unroll
             for (int j = 0; j < U; j++) hu[j] = RW[2000 + lane + G * j];
-            for (uint32_t i = lane; i < uint32_t(K) * POOL; i += G) (&s_ring[grp][0][0])[i] = 12.0f;
+            for (uint32_t i = lane; i < uint32_t(K) * POOL; i += G) s_ring[grp][i] = 12.0f;
             for (uint32_t i = lane; i < 32; i += G) {
                 s_cmd[grp][i] = 0.0f;
                 a.commands[size_t(nn) * 32 + i] = 0.0f;
@@ -670,17 +710,21 @@ hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream) {
 
 // Lanes per env G and LDS ring slots K are compile-time; K = sensor_delay+2
 // rounded up to 2, 4 or 8.
+// The (8 lanes, 2 slots) case runs four wavefronts per workgroup with the
+// weights in LDS (32 envs, 159 KB of LDS, one workgroup per CU); the ring of
+// the other slot counts leaves no room for that, so they run one wavefront per
+// workgroup with the weights in L1/L2.
 hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, hipStream_t stream) {
-    const uint32_t envs_per_block = 64 / lanes_per_env;
-    const uint32_t blocks = (a->cfg.n + envs_per_block - 1) / envs_per_block;
-#define NAV_ROLLOUT_CASE(G, K)                                                                       \
-    if (lanes_per_env == G && ring_slots == K) {                                                     \
-        hipLaunchKernelGGL((nav::rollout_kernel<G, K>), dim3(blocks), dim3(64), 0, stream, *a);      \
-        return hipGetLastError();                                                                    \
+#define NAV_ROLLOUT_CASE(G, K, W)                                                                         \
+    if (lanes_per_env == G && ring_slots == K) {                                                          \
+        const uint32_t envs_per_block = 64 * W / G;                                                       \
+        const uint32_t blocks = (a->cfg.n + envs_per_block - 1) / envs_per_block;                         \
+        hipLaunchKernelGGL((nav::rollout_kernel<G, K, W>), dim3(blocks), dim3(64 * W), 0, stream, *a);    \
+        return hipGetLastError();                                                                         \
     }
-    NAV_ROLLOUT_CASE(8, 2) NAV_ROLLOUT_CASE(8, 4) NAV_ROLLOUT_CASE(8, 8)
-    NAV_ROLLOUT_CASE(16, 2) NAV_ROLLOUT_CASE(16, 4) NAV_ROLLOUT_CASE(16, 8)
-    NAV_ROLLOUT_CASE(4, 2) NAV_ROLLOUT_CASE(4, 4) NAV_ROLLOUT_CASE(4, 8)
+    NAV_ROLLOUT_CASE(8, 2, 4) NAV_ROLLOUT_CASE(8, 4, 1) NAV_ROLLOUT_CASE(8, 8, 1)
+    NAV_ROLLOUT_CASE(16, 2, 1) NAV_ROLLOUT_CASE(16, 4, 1) NAV_ROLLOUT_CASE(16, 8, 1)
+    NAV_ROLLOUT_CASE(4, 2, 1) NAV_ROLLOUT_CASE(4, 4, 1) NAV_ROLLOUT_CASE(4, 8, 1)
 #undef NAV_ROLLOUT_CASE
     return hipErrorInvalidValue;
 }
@@ -696,8 +740,8 @@ __global__ __launch_bounds__(64) void raptor_fixture_kernel(const float* __restr
                                                             uint32_t steps, uint32_t copies, float* __restrict__ actions,
                                                             float* __restrict__ hidden_out) {
     constexpr int E = 64 / G, U = 16 / G;
-    __shared__ float s_x[E][16];
-    __shared__ float s_h[E][16];
+    __shared__ float s_x[E][17];
+    __shared__ float s_h[E][17];
     const uint32_t lane = threadIdx.x % G, grp = threadIdx.x / G;
     const uint32_t copy = blockIdx.x * E + grp;
     const bool live = copy < copies;
