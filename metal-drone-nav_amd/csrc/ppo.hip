@@ -8,8 +8,9 @@
 //     (a single chunk at the reference's 256-row minibatch, i.e.
 //     ppo_actor_grad_direct's order, ppo.metal:497-519);
 //   * squared gradient norm: 256 strided partials then a pairwise tree;
-//   * advantage statistics in double: chunks of 256, groups of 64 chunks,
-//     then over groups.
+//   * advantage statistics in double: within each 256-element chunk, lane
+//     sums of 4 elements combined by a wavefront xor butterfly; chunk
+//     partials sequential within groups of 64, then over the groups.
 // The 64-wide hidden layers are evaluated on the VALU with weights as
 // wave-uniform scalar loads: one lane owns one row (forward) or one input
 // feature (weight gradient), so every accumulation is a private serial chain.
@@ -36,71 +37,146 @@ constexpr uint32_t C_B1 = HID * COBS, C_W2 = C_B1 + HID, C_B2 = C_W2 + HID, C_CO
 constexpr uint32_t P_TOTAL = A_COUNT + C_COUNT + 4;
 
 // ---------------------------------------------------------------- GAE
-// ppo.hpp:108-126 == ppo.metal:279-304: one thread per env, reverse scan.
+// ppo.hpp:108-126 == ppo.metal:279-304, reverse scan per env.  A workgroup
+// owns 32 envs and walks the horizon backwards in tiles of 32 ticks: all 256
+// threads load the tile coalesced and form delta = r + gamma*V'(s') - V(s)
+// in LDS, one lane per env then runs the carry recurrence over the tile (the
+// only serial part), and the tile of advantages/returns is stored coalesced.
+constexpr uint32_t GAE_ENVS = 32, GAE_TICKS = 32, GAE_PER = GAE_ENVS * GAE_TICKS / 256;
+struct GaeTile {
+    float delta[GAE_PER], value[GAE_PER];
+    uint32_t boundary[GAE_PER];
+};
+// Loads the tile [t0, t1) x [e0, e0+32) into registers (4 elements per
+// thread) and forms the deltas.
+__device__ __forceinline__ void gae_load(GaeTile& g, const float* __restrict__ r, const float* __restrict__ v,
+                                         const float* __restrict__ nv, const uint8_t* __restrict__ te,
+                                         const uint8_t* __restrict__ tr, uint32_t t0, uint32_t t1, uint32_t e0,
+                                         uint32_t n, float gamma) {
+#pragma unroll
+    for (uint32_t j = 0; j < GAE_PER; j++) {
+        const uint32_t i = threadIdx.x + 256 * j;
+        const uint32_t t = t0 + i / GAE_ENVS, env = e0 + i % GAE_ENVS;
+        g.delta[j] = 0.0f; g.value[j] = 0.0f; g.boundary[j] = 0;
+        if (t < t1 && env < n) {
+            const size_t k = size_t(t) * n + env;
+            const bool term = te[k] != 0;
+            const bool boundary = term || tr[k] != 0;
+            const float bootstrap = term ? 0.0f : nv[k];
+            const float value = v[k];
+            g.delta[j] = r[k] + gamma * bootstrap - value;
+            g.value[j] = value;
+            g.boundary[j] = boundary;
+        }
+    }
+}
 __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, const float* __restrict__ v,
                                                   const float* __restrict__ nv, const uint8_t* __restrict__ te,
                                                   const uint8_t* __restrict__ tr, float* __restrict__ adv,
                                                   float* __restrict__ ret, uint32_t horizon, uint32_t n,
                                                   float gamma, float lambda) {
-    const uint32_t env = blockIdx.x * 256 + threadIdx.x;
-    if (env >= n) return;
+    __shared__ float s_delta[GAE_TICKS][GAE_ENVS + 1];
+    __shared__ float s_val[GAE_TICKS][GAE_ENVS + 1];
+    __shared__ float s_adv[GAE_TICKS][GAE_ENVS + 1];
+    __shared__ uint32_t s_bnd[GAE_TICKS][GAE_ENVS + 1];
+    const uint32_t e0 = blockIdx.x * GAE_ENVS, tid = threadIdx.x;
     float carry = 0.0f;
-    for (uint32_t rev = 0; rev < horizon; ++rev) {
-        const uint32_t t = horizon - 1 - rev;
-        const size_t k = size_t(t) * n + env;
-        const bool term = te[k] != 0;
-        const bool boundary = term || tr[k] != 0;
-        const float bootstrap = term ? 0.0f : nv[k];
-        const float delta = r[k] + gamma * bootstrap - v[k];
-        carry = delta + (boundary ? 0.0f : gamma * lambda * carry);
-        adv[k] = carry;
-        ret[k] = carry + v[k];
+    GaeTile cur;
+    uint32_t t1 = horizon, t0 = t1 > GAE_TICKS ? t1 - GAE_TICKS : 0;
+    gae_load(cur, r, v, nv, te, tr, t0, t1, e0, n, gamma);
+    while (t1 > 0) {
+#pragma unroll
+        for (uint32_t j = 0; j < GAE_PER; j++) {
+            const uint32_t i = tid + 256 * j, tt = i / GAE_ENVS, e = i % GAE_ENVS;
+            s_delta[tt][e] = cur.delta[j];
+            s_val[tt][e] = cur.value[j];
+            s_bnd[tt][e] = cur.boundary[j];
+        }
+        __syncthreads();
+        // the next (earlier) tile's loads are in flight during the scan
+        const uint32_t n1 = t0, n0 = n1 > GAE_TICKS ? n1 - GAE_TICKS : 0;
+        if (n1 > 0) gae_load(cur, r, v, nv, te, tr, n0, n1, e0, n, gamma);
+        if (tid < GAE_ENVS && e0 + tid < n) {
+            for (uint32_t tt = t1 - t0; tt-- > 0;) {
+                carry = s_delta[tt][tid] + (s_bnd[tt][tid] ? 0.0f : gamma * lambda * carry);
+                s_adv[tt][tid] = carry;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t j = 0; j < GAE_PER; j++) {
+            const uint32_t i = tid + 256 * j, tt = i / GAE_ENVS, e = i % GAE_ENVS;
+            const uint32_t t = t0 + tt, env = e0 + e;
+            if (t < t1 && env < n) {
+                const size_t k = size_t(t) * n + env;
+                const float a = s_adv[tt][e];
+                adv[k] = a;
+                ret[k] = a + s_val[tt][e];
+            }
+        }
+        __syncthreads();
+        t1 = n1;
+        t0 = n0;
     }
 }
 
 // ---------------------------------------------------------------- normalisation
-// ppo.hpp:128-140: chunk sums in double (pass 0: sum a; pass 1: sum (a-mean)^2).
+// ppo.hpp:128-140 with double statistics.  One wavefront per 256-element
+// chunk: lane l adds elements 4l..4l+3 in order, then an xor butterfly over
+// the 64 lanes (pass 0: sum a; pass 1: sum (a-mean)^2).
 __global__ __launch_bounds__(256) void norm_chunks_kernel(const float* __restrict__ a, uint64_t count,
                                                           double* __restrict__ part, const float* __restrict__ stats,
                                                           int pass) {
-    const uint64_t c = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    const uint64_t c = uint64_t(blockIdx.x) * 4 + threadIdx.x / 64;
+    const uint32_t l = threadIdx.x % 64;
     const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
-    if (c >= chunks) return;
-    const uint64_t end = (c + 1) * CHUNK < count ? (c + 1) * CHUNK : count;
+    if (c >= chunks) return;  // whole wavefronts leave together
+    const uint64_t begin = c * CHUNK + 4 * l;
+    const float mean = pass == 0 ? 0.0f : stats[0];
     double s = 0.0;
-    if (pass == 0) {
-        for (uint64_t i = c * CHUNK; i < end; ++i) s += double(a[i]);
-    } else {
-        const float mean = stats[0];
-        for (uint64_t i = c * CHUNK; i < end; ++i) {
-            const double d = double(a[i] - mean);
-            s += d * d;
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const uint64_t i = begin + j;
+        if (i < count) {
+            if (pass == 0) {
+                s += double(a[i]);
+            } else {
+                const double d = double(a[i] - mean);
+                s += d * d;
+            }
         }
     }
-    part[c] = s;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s = s + __shfl_xor(s, off, 64);
+    if (l == 0) part[c] = s;
 }
-// Chunk partials summed within groups of NORM_GROUP (one thread per group),
-// in place into part[group * NORM_GROUP].
-__global__ __launch_bounds__(256) void norm_groups_kernel(double* __restrict__ part, uint64_t count) {
+// Chunk partials summed sequentially within groups of NORM_GROUP, then the
+// group sums sequentially; pass 0 writes the float mean, pass 1 the inverse
+// standard deviation 1/sqrt(var + eps).
+__global__ __launch_bounds__(256) void norm_finish_kernel(const double* __restrict__ part, uint64_t count,
+                                                          float* __restrict__ stats, float eps, int pass) {
+    __shared__ double gs[256];
     const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
-    const uint64_t g = uint64_t(blockIdx.x) * 256 + threadIdx.x;
-    const uint64_t c0 = g * NORM_GROUP;
-    if (c0 >= chunks) return;
-    const uint64_t end = c0 + NORM_GROUP < chunks ? c0 + NORM_GROUP : chunks;
-    double s = 0.0;
-    for (uint64_t c = c0; c < end; ++c) s += part[c];
-    part[c0] = s;
-}
-// Sequential sum over the group sums; pass 0 writes the float mean, pass 1
-// the inverse standard deviation 1/sqrt(var + eps).
-__global__ void norm_finish_kernel(const double* __restrict__ part, uint64_t count, float* __restrict__ stats,
-                                   float eps, int pass) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
-    double s = 0.0;
-    for (uint64_t c = 0; c < chunks; c += NORM_GROUP) s += part[c];
-    if (pass == 0) stats[0] = float(s / double(count));
-    else stats[1] = 1.0f / sqrt_f(float(s / double(count)) + eps);
+    const uint64_t groups = (chunks + NORM_GROUP - 1) / NORM_GROUP;
+    double total = 0.0;
+    for (uint64_t g0 = 0; g0 < groups; g0 += 256) {
+        const uint64_t g = g0 + threadIdx.x;
+        if (g < groups) {
+            const uint64_t c0 = g * NORM_GROUP, end = c0 + NORM_GROUP < chunks ? c0 + NORM_GROUP : chunks;
+            double s = 0.0;
+            for (uint64_t c = c0; c < end; ++c) s += part[c];
+            gs[threadIdx.x] = s;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const uint64_t m = groups - g0 < 256 ? groups - g0 : 256;
+            for (uint64_t j = 0; j < m; ++j) total += gs[j];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x != 0) return;
+    if (pass == 0) stats[0] = float(total / double(count));
+    else stats[1] = 1.0f / sqrt_f(float(total / double(count)) + eps);
 }
 __global__ __launch_bounds__(256) void norm_apply_kernel(float* __restrict__ a, uint64_t count,
                                                          const float* __restrict__ stats) {
@@ -443,20 +519,20 @@ extern "C" {
 hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const uint8_t* te, const uint8_t* tr,
                           float* adv, float* ret, uint32_t horizon, uint32_t n, float gamma, float lambda,
                           hipStream_t st) {
-    hipLaunchKernelGGL(ppo::gae_kernel, dim3((n + 255) / 256), dim3(256), 0, st, r, v, nv, te, tr, adv, ret, horizon, n,
-                       gamma, lambda);
+    if (n == 0 || horizon == 0) return hipSuccess;
+    hipLaunchKernelGGL(ppo::gae_kernel, dim3((n + ppo::GAE_ENVS - 1) / ppo::GAE_ENVS), dim3(256), 0, st, r, v, nv, te, tr,
+                       adv, ret, horizon, n, gamma, lambda);
     return hipGetLastError();
 }
 
 // stats: device float[2] (mean, inv_std); part: device double[ceil(count/256)]
 hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st) {
+    if (count == 0) return hipSuccess;
     const uint64_t chunks = (count + ppo::CHUNK - 1) / ppo::CHUNK;
-    const uint32_t cb = uint32_t((chunks + 255) / 256);
+    const uint32_t cb = uint32_t((chunks + 3) / 4);  // one wavefront per chunk
     for (int pass = 0; pass < 2; pass++) {
         hipLaunchKernelGGL(ppo::norm_chunks_kernel, dim3(cb), dim3(256), 0, st, a, count, part, stats, pass);
-        const uint64_t groups = (chunks + ppo::NORM_GROUP - 1) / ppo::NORM_GROUP;
-        hipLaunchKernelGGL(ppo::norm_groups_kernel, dim3(uint32_t((groups + 255) / 256)), dim3(256), 0, st, part, count);
-        hipLaunchKernelGGL(ppo::norm_finish_kernel, dim3(1), dim3(64), 0, st, part, count, stats, eps, pass);
+        hipLaunchKernelGGL(ppo::norm_finish_kernel, dim3(1), dim3(256), 0, st, part, count, stats, eps, pass);
     }
     hipLaunchKernelGGL(ppo::norm_apply_kernel, dim3(uint32_t((count + 255) / 256)), dim3(256), 0, st, a, count, stats);
     return hipGetLastError();

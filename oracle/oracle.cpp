@@ -14,8 +14,9 @@
  *     minibatch, i.e. the order of ppo_actor_grad_direct,
  *     ppo.metal:497-519);
  *   - squared gradient norm: 256 strided partial sums, then a pairwise tree;
- *   - advantage mean/variance: double, chunks of 256 rows, groups of 64
- *     chunks, then over groups.
+ *   - advantage mean/variance: double; within each 256-row chunk 64 slots
+ *     of 4 sequential rows combined by an xor butterfly, chunk partials
+ *     sequential within groups of 64 chunks, then over the groups.
  * Build: g++ -O2 -fopenmp -ffp-contract=off (see oracle/Makefile).
  */
 #include <omp.h>
@@ -138,28 +139,45 @@ inline T grouped_sum(const std::vector<T>& part, size_t group) {
     }
     return total;
 }
-// ppo.hpp:128-140 with the canonical chunked double sums.
+// Sum of f(a[i]) over one 256-element chunk in the canonical order: slot l
+// (0..63) adds elements 4l..4l+3 sequentially from 0.0, then six butterfly
+// levels s[l] = s[l] + s[l ^ off] for off = 32, 16, ..., 1 (a wavefront xor
+// reduction; every slot ends with the same value since + is commutative).
+template <class F>
+inline double chunk_tree_sum(const float* a, size_t begin, size_t end, F f) {
+    double s[64];
+    for (size_t l = 0; l < 64; ++l) {
+        s[l] = 0.0;
+        for (size_t j = 0; j < 4; ++j) {
+            const size_t i = begin + 4 * l + j;
+            if (i < end) s[l] += f(a[i]);
+        }
+    }
+    for (size_t off = 32; off > 0; off >>= 1) {
+        double t[64];
+        for (size_t l = 0; l < 64; ++l) t[l] = s[l] + s[l ^ off];
+        for (size_t l = 0; l < 64; ++l) s[l] = t[l];
+    }
+    return s[0];
+}
+// ppo.hpp:128-140 with the canonical double sums: chunk tree sums, chunk
+// partials sequential within groups of 64, then over the groups.
 inline void normalize_advantages(float* a, size_t count, float eps) {
     if (count == 0) return;
     const size_t chunks = (count + kChunk - 1) / kChunk;
     std::vector<double> part(chunks);
 #pragma omp parallel for schedule(static)
-    for (int64_t c = 0; c < int64_t(chunks); ++c) {
-        double s = 0.0;
-        for (size_t i = size_t(c) * kChunk; i < std::min(count, size_t(c + 1) * kChunk); ++i) s += double(a[i]);
-        part[c] = s;
-    }
+    for (int64_t c = 0; c < int64_t(chunks); ++c)
+        part[c] = chunk_tree_sum(a, size_t(c) * kChunk, std::min(count, size_t(c + 1) * kChunk),
+                                 [](float x) { return double(x); });
     const double sum = grouped_sum(part, kNormGroup);
     const float mean = float(sum / double(count));
 #pragma omp parallel for schedule(static)
-    for (int64_t c = 0; c < int64_t(chunks); ++c) {
-        double s = 0.0;
-        for (size_t i = size_t(c) * kChunk; i < std::min(count, size_t(c + 1) * kChunk); ++i) {
-            const double d = double(a[i] - mean);
-            s += d * d;
-        }
-        part[c] = s;
-    }
+    for (int64_t c = 0; c < int64_t(chunks); ++c)
+        part[c] = chunk_tree_sum(a, size_t(c) * kChunk, std::min(count, size_t(c + 1) * kChunk), [mean](float x) {
+            const double d = double(x - mean);
+            return d * d;
+        });
     const double sq = grouped_sum(part, kNormGroup);
     const float inv = 1.0f / sqrt_f(float(sq / double(count)) + eps);
 #pragma omp parallel for schedule(static)
