@@ -116,9 +116,7 @@ struct MdnPPO {
     uint64_t optimizer_step = 0;
     uint32_t updates = 0;
     float *am = nullptr, *av = nullptr, *cm = nullptr, *cv = nullptr;
-    // minibatch workspaces
-    float *ah = nullptr, *adelta = nullptr, *ch = nullptr, *cdelta = nullptr;
-    float *dm = nullptr, *dls = nullptr, *dv = nullptr, *loss = nullptr;
+    // minibatch workspaces: per-chunk partials and the reduced gradient
     float *part = nullptr, *grad = nullptr;
     double* norm_part = nullptr;
     float* norm_stats = nullptr;
@@ -472,14 +470,6 @@ int mdn_ppo_create(MdnSim* s, uint32_t epochs, uint32_t minibatch, MdnPPO** out)
     guard(dev_alloc(&p->av, s->shape.actor_count()));
     guard(dev_alloc(&p->cm, s->shape.critic_count()));
     guard(dev_alloc(&p->cv, s->shape.critic_count()));
-    guard(dev_alloc(&p->ah, M * HID));
-    guard(dev_alloc(&p->adelta, M * HID));
-    guard(dev_alloc(&p->ch, M * HID));
-    guard(dev_alloc(&p->cdelta, M * HID));
-    guard(dev_alloc(&p->dm, M * 4));
-    guard(dev_alloc(&p->dls, M * 4));
-    guard(dev_alloc(&p->dv, M));
-    guard(dev_alloc(&p->loss, M * 4));
     guard(dev_alloc(&p->part, size_t(chunks) * ppo_partial_stride()));
     guard(dev_alloc(&p->grad, ppo_partial_stride()));
     guard(dev_alloc(&p->norm_part, (s->rows() + 255) / 256));
@@ -502,8 +492,8 @@ void mdn_ppo_destroy(MdnPPO* p) {
         hipStreamSynchronize(p->sim->stream);
         if (p->sim->ppo == p) p->sim->ppo = nullptr;
     }
-    void* bufs[] = {p->am, p->av, p->cm, p->cv, p->ah, p->adelta, p->ch, p->cdelta, p->dm, p->dls, p->dv,
-                    p->loss, p->part, p->grad, p->norm_part, p->norm_stats, p->metric_rows, p->metric_mean};
+    void* bufs[] = {p->am, p->av, p->cm, p->cv, p->part, p->grad, p->norm_part, p->norm_stats, p->metric_rows,
+                    p->metric_mean};
     for (void* b : bufs)
         if (b) hipFree(b);
     delete p;
@@ -549,14 +539,12 @@ int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
         ra.adv = s->advantages + begin;
         ra.ret = s->returns + begin;
         ra.actor = s->actor; ra.actor_w1t = s->actor_w1t; ra.critic = s->critic; ra.critic_w1t = s->critic_w1t;
-        ra.ah = p->ah; ra.adelta = p->adelta; ra.ch = p->ch; ra.cdelta = p->cdelta;
-        ra.dm = p->dm; ra.dls = p->dls; ra.dv = p->dv; ra.loss = p->loss;
+        ra.part = p->part;
         ra.b = b; ra.clip = 0.2f; ra.vcoef = 0.5f; ra.ecoef = s->cfg.entropy_coef;
         rc = timed(s, MDN_K_ROWS, [&] { return ppo_launch_rows(&ra, s->stream); });
         if (rc) return rc;
         rc = timed(s, MDN_K_GRADS, [&] {
-            return ppo_launch_grads(ra.obs, ra.co, p->ah, p->adelta, p->ch, p->cdelta, p->dm, p->dls, p->dv, p->loss,
-                                    p->part, p->grad, b, s->stream);
+            return ppo_launch_grads(p->part, p->grad, b, s->stream);
         });
         if (rc) return rc;
         ++p->optimizer_step;

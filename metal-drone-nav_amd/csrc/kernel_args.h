@@ -49,14 +49,7 @@ struct RowArgs {
     const float* actor_w1t; // [OBS][HID]
     const float* critic;
     const float* critic_w1t; // [COBS][HID]
-    float* ah;      // [b][HID] actor hidden
-    float* adelta;  // [b][HID]
-    float* ch;      // [b][HID] critic hidden
-    float* cdelta;  // [b][HID]
-    float* dm;      // [b][4]
-    float* dls;     // [b][4]
-    float* dv;      // [b]
-    float* loss;    // [b][4]
+    float* part;            // [ceil(b/256)][P_TOTAL] per-chunk gradient and metric partials
     uint32_t b;
     float clip, vcoef, ecoef;
 };
@@ -88,9 +81,7 @@ hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const
                           hipStream_t st);
 hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st);
 hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st);
-hipError_t ppo_launch_grads(const float* obs, const float* co, const float* ah, const float* adelta, const float* ch,
-                            const float* cdelta, const float* dm, const float* dls, const float* dv, const float* loss,
-                            float* part, float* grad, uint32_t b, hipStream_t st);
+hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, hipStream_t st);
 hipError_t ppo_launch_adam(const ppo::AdamArgs* a, hipStream_t st);
 hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* aw, float* cw, hipStream_t st);
 hipError_t ppo_launch_metric_mean(const float* rows, float* mean, uint32_t updates, hipStream_t st);

@@ -2,7 +2,8 @@
 //
 // Reductions follow one canonical order shared with the CPU oracle so both
 // round identically:
-//   * dot products accumulate from the bias, inputs ascending (ppo.hpp:65-93);
+//   * dot products: fma chain from the bias, inputs ascending (ppo.hpp:65-93);
+//   * weight gradients: fma chain over rows in the row order below;
 //   * sums over minibatch rows: sequential within 256-row chunks, chunk
 //     partials sequential within groups of 32 chunks, then over the groups
 //     (a single chunk at the reference's 256-row minibatch, i.e.
@@ -11,9 +12,8 @@
 //   * advantage statistics in double: within each 256-element chunk, lane
 //     sums of 4 elements combined by a wavefront xor butterfly; chunk
 //     partials sequential within groups of 64, then over the groups.
-// The 64-wide hidden layers are evaluated on the VALU with weights as
-// wave-uniform scalar loads: one lane owns one row (forward) or one input
-// feature (weight gradient), so every accumulation is a private serial chain.
+// Dot products and weight-gradient sums are fma chains (one rounding per
+// step), which the fp32 matrix-core GEMMs below reproduce exactly.
 #include <hip/hip_runtime.h>
 
 #include "mdnav_math.h"
@@ -185,96 +185,231 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(float* __restrict__ a, 
     a[i] = (a[i] - stats[0]) * stats[1];
 }
 
-// ---------------------------------------------------------------- minibatch rows
+// ---------------------------------------------------------------- minibatch chunk
+// One workgroup per 256-row chunk of a minibatch: critic and actor forward,
+// per-row loss and derivatives (ppo.hpp:144-181), hidden deltas
+// (ppo.metal:470-485, 618-631) and every parameter's partial sum over the
+// chunk's rows (cpu_reference.hpp:515-551), written to the chunk's partial
+// vector.  Activations and deltas stay in LDS.
+//
+// The GEMMs run on the fp32 matrix cores.  v_mfma_f32_32x32x2_f32 applies
+// acc = fma(a[k], b[k], acc) for k = 0 then 1 with one rounding per step, so
+// a chain of them over k ascending is exactly the canonical fma chain:
+//   forward:  h[row][j] = fma over inputs i ascending, from b1[j];
+//   backward: dW1[j][i] = fma over the chunk's rows ascending, from 0.
+// Operand layout (per wavefront, one 32x32 tile): A lane a holds A[a%32][k0 +
+// a/32], B lane a holds B[k0 + a/32][a%32]; accumulator register r of lane l
+// holds D[8(r/4) + 4(l/32) + r%4][l%32].  Padding steps multiply by -0.0,
+// which leaves every accumulator (including -0.0) unchanged.
+typedef float v16f __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ v16f mfma32(float a, float b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ uint32_t acc_row(uint32_t l, uint32_t r) { return 8 * (r / 4) + 4 * (l / 32) + (r % 4); }
 
+constexpr uint32_t HS = HID + 1;       // row stride of the [256][64] activation buffer
+constexpr uint32_t XK = 16;            // forward: inputs per k-slab
+constexpr uint32_t XKS = XK + 1;       // stride of the forward row tile [256][16]
+constexpr uint32_t WKS = HID + 32;     // stride of the forward weight slab [16][64]
+constexpr uint32_t BR = 32;            // backward: rows per row-slab
+constexpr uint32_t OBS_PAD = 192;      // inputs rounded up to whole 32-wide tiles
+constexpr uint32_t XRS = OBS_PAD + 32; // stride of the backward row slab [32][192]
+constexpr uint32_t RS = 13;            // per-row scalars: dm[4], dls[4], loss[4]
+constexpr uint32_t U_WORDS = BR * XRS > 256 * XKS + XK * WKS ? BR * XRS : 256 * XKS + XK * WKS;
+static_assert(256 % XK == 0 && (256 / XK) * XK == 256 && 16 * XK == 256, "forward slab mapping");
+static_assert(256 * RS <= U_WORDS, "per-row scalars fit the shared scratch");
 
-// Forward, per-row loss/derivatives (ppo.hpp:144-181) and hidden deltas
-// (ppo.metal:470-485, 618-631); one lane per row.
-// Writes one 64-float value per row of the block's 256-row tile, transposed
-// through LDS so that global stores are contiguous across lanes (the row-major
-// [row][64] layout the gradient kernels read).
-__device__ __forceinline__ void store_rows64(float* lds, const float (&v)[HID], float* __restrict__ dst, uint32_t n0,
-                                             uint32_t rows) {
-    const uint32_t t = threadIdx.x;
-    __syncthreads();
+// Forward slab in registers: thread t holds column t % XK of rows t/XK + 16j
+// (j < XK) and weights [t/64 + 4j][t % 64] (j < 4).
+struct FwdSlab {
+    float x[XK];
+    float w[XK * HID / 256];
+};
+template <uint32_t D>
+__device__ __forceinline__ void fwd_load(FwdSlab& f, const float* __restrict__ X, const float* __restrict__ W1T,
+                                         uint32_t n0, uint32_t b, uint32_t k0) {
+    const uint32_t t = threadIdx.x, cc = t % XK, col = k0 + cc;
 #pragma unroll
-    for (uint32_t k = 0; k < HID; k++) lds[t * (HID + 1) + k] = v[k];
-    __syncthreads();
-    float* out = dst + size_t(n0) * HID;
-    for (uint32_t e = t; e < rows * HID; e += 256) out[e] = lds[(e / HID) * (HID + 1) + e % HID];
+    for (uint32_t j = 0; j < XK; j++) {
+        const uint32_t row = n0 + t / XK + 16 * j;
+        f.x[j] = (row < b && col < D) ? X[size_t(row) * D + col] : 0.0f;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < XK * HID / 256; j++) {
+        const uint32_t kc = k0 + t / HID + 4 * j;
+        f.w[j] = kc < D ? W1T[kc * HID + t % HID] : -0.0f;
+    }
 }
 
-__global__ __launch_bounds__(256) void rows_kernel(RowArgs a) {
-    // Row tiles are staged through LDS 16 features at a time with coalesced
-    // loads; each lane then walks its own row (padding 17 avoids bank
-    // conflicts) while the weights arrive as wave-uniform scalar loads.  The
-    // same LDS then stages the per-row outputs.
-    __shared__ float lds[256 * (HID + 1)];
-    float(*tile)[17] = reinterpret_cast<float(*)[17]>(lds);
-    const uint32_t t = threadIdx.x, n0 = blockIdx.x * 256;
-    const uint32_t n = n0 + t;
-    const bool live = n < a.b;
-    const uint32_t rows = a.b - n0 < 256 ? a.b - n0 : 256;
-    float h[HID];
+// h[256][64] = tanh(X W1^T + b1) for the chunk's rows (rows past b read as 0).
+// Wavefront w owns rows 64w..64w+63 as 2x2 tiles of 32x32.  The next slab's
+// global loads are in flight while the current slab's MFMAs run.
+template <uint32_t D>
+__device__ __forceinline__ void chunk_forward(const float* __restrict__ X, const float* __restrict__ W1T,
+                                              const float* __restrict__ b1, uint32_t n0, uint32_t b, float* s_u,
+                                              float* s_h) {
+    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
+    float* sx = s_u;                 // [256][XKS]
+    float* sw = s_u + 256 * XKS;     // [XK][WKS]
+    v16f acc[2][2];
 #pragma unroll
-    for (uint32_t k = 0; k < HID; k++) h[k] = a.actor[A_B1 + k];
-    for (uint32_t i0 = 0; i0 < OBS; i0 += 16) {
-        for (uint32_t e = t; e < 256 * 16; e += 256) {
-            const uint32_t rr = e / 16, cc = e % 16;
-            const uint32_t row = n0 + rr, col = i0 + cc;
-            tile[rr][cc] = (row < a.b && col < OBS) ? a.obs[size_t(row) * OBS + col] : 0.0f;
+    for (uint32_t ct = 0; ct < 2; ct++) {
+        const float bias = b1[32 * ct + l % 32];
+#pragma unroll
+        for (uint32_t r = 0; r < 16; r++) { acc[0][ct][r] = bias; acc[1][ct][r] = bias; }
+    }
+    FwdSlab f;
+    fwd_load<D>(f, X, W1T, n0, b, 0);
+    for (uint32_t k0 = 0; k0 < D; k0 += XK) {
+#pragma unroll
+        for (uint32_t j = 0; j < XK; j++) sx[(t / XK + 16 * j) * XKS + t % XK] = f.x[j];
+#pragma unroll
+        for (uint32_t j = 0; j < XK * HID / 256; j++) sw[(t / HID + 4 * j) * WKS + t % HID] = f.w[j];
+        __syncthreads();
+        if (k0 + XK < D) fwd_load<D>(f, X, W1T, n0, b, k0 + XK);
+        const uint32_t cnt = D - k0 < XK ? D - k0 : XK;
+        for (uint32_t kk = 0; kk < cnt; kk += 2) {
+            const uint32_t kr = kk + l / 32;
+            float av[2], bv[2];
+#pragma unroll
+            for (uint32_t rt = 0; rt < 2; rt++) av[rt] = sx[(64 * wv + 32 * rt + l % 32) * XKS + kr];
+#pragma unroll
+            for (uint32_t ct = 0; ct < 2; ct++) bv[ct] = sw[kr * WKS + 32 * ct + l % 32];
+#pragma unroll
+            for (uint32_t rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (uint32_t ct = 0; ct < 2; ct++) acc[rt][ct] = mfma32(av[rt], bv[ct], acc[rt][ct]);
         }
         __syncthreads();
-        const uint32_t cnt = OBS - i0 < 16 ? OBS - i0 : 16;
+    }
 #pragma unroll
-        for (uint32_t c = 0; c < 16; c++) {
-            if (c < cnt) {
-                const float xi = tile[t][c];
-                const float* w = a.actor_w1t + size_t(i0 + c) * HID;
+    for (uint32_t rt = 0; rt < 2; rt++)
 #pragma unroll
-                for (uint32_t k = 0; k < HID; k++) h[k] += w[k] * xi;
+        for (uint32_t ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (uint32_t r = 0; r < 16; r++)
+                s_h[(64 * wv + 32 * rt + acc_row(l, r)) * HS + 32 * ct + l % 32] = tanh_f(acc[rt][ct][r]);
+    __syncthreads();
+}
+
+// Backward row slab in registers: BR rows x W columns, element e = t + 256 j.
+template <uint32_t W>
+struct RowSlab {
+    float x[BR * W / 256];
+};
+template <uint32_t D, uint32_t W>
+__device__ __forceinline__ void row_load(RowSlab<W>& f, const float* __restrict__ X, uint32_t n0, uint32_t rows,
+                                         uint32_t r0) {
+#pragma unroll
+    for (uint32_t j = 0; j < BR * W / 256; j++) {
+        const uint32_t e = threadIdx.x + 256 * j, rr = e / W, cc = e % W;
+        f.x[j] = (r0 + rr < rows && cc < D) ? X[size_t(n0 + r0 + rr) * D + cc] : -0.0f;
+    }
+}
+
+// dW1[j][i] partial over the chunk's rows: A = delta^T (s_h, [row][64]),
+// B = the input rows streamed from global in slabs of 32 rows (W columns, a
+// multiple of 32 covering D).  Wavefront tiles are the (jt[q], it[q]) pairs.
+template <uint32_t D, uint32_t W, uint32_t T>
+__device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, uint32_t n0, uint32_t rows,
+                                                  const uint32_t (&jt)[T], const uint32_t (&it)[T], bool owner,
+                                                  float* s_u, const float* s_h, float* __restrict__ out) {
+    constexpr uint32_t WS = W + 32;  // slab row stride: the two k halves fall in different banks
+    const uint32_t t = threadIdx.x, l = t % 64;
+    float* sx = s_u;  // [BR][WS]
+    v16f acc[T];
+#pragma unroll
+    for (uint32_t q = 0; q < T; q++)
+#pragma unroll
+        for (uint32_t r = 0; r < 16; r++) acc[q][r] = 0.0f;
+    RowSlab<W> f;
+    row_load<D, W>(f, X, n0, rows, 0);
+    for (uint32_t r0 = 0; r0 < rows; r0 += BR) {
+#pragma unroll
+        for (uint32_t j = 0; j < BR * W / 256; j++) {
+            const uint32_t e = t + 256 * j;
+            sx[(e / W) * WS + e % W] = f.x[j];
+        }
+        __syncthreads();
+        if (r0 + BR < rows) row_load<D, W>(f, X, n0, rows, r0 + BR);
+        if (owner) {
+            const uint32_t steps = rows - r0 < BR ? rows - r0 : BR;
+            for (uint32_t k = 0; k < steps; k += 2) {
+                const uint32_t rr = k + l / 32;
+#pragma unroll
+                for (uint32_t q = 0; q < T; q++) {
+                    const float av = s_h[(r0 + rr) * HS + 32 * jt[q] + l % 32];
+                    const float bv = sx[rr * WS + 32 * it[q] + l % 32];
+                    acc[q] = mfma32(av, bv, acc[q]);
+                }
             }
         }
         __syncthreads();
     }
+    if (!owner) return;
 #pragma unroll
-    for (uint32_t k = 0; k < HID; k++) h[k] = tanh_f(h[k]);
+    for (uint32_t q = 0; q < T; q++) {
+        const uint32_t i = 32 * it[q] + l % 32;
+        if (i < D)
+#pragma unroll
+            for (uint32_t r = 0; r < 16; r++) out[(32 * jt[q] + acc_row(l, r)) * D + i] = acc[q][r];
+    }
+}
+
+__global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
+    __shared__ float s_h[256 * HS];
+    __shared__ float s_u[U_WORDS];
+    __shared__ float s_dv[256];
+    const uint32_t t = threadIdx.x, wv = t / 64;
+    const uint32_t n0 = blockIdx.x * 256;
+    const uint32_t rows = a.b - n0 < 256 ? a.b - n0 : 256;
+    const bool live = t < rows;
+    const uint32_t n = n0 + t, m = live ? n : n0;
+    float* P = a.part + size_t(blockIdx.x) * P_TOTAL;
+    const float scale = 1.0f / max_f(float(a.b), 1.0f);
+
+    // ---- critic: forward, value, dV (ppo.hpp:82-93, 176-180)
+    chunk_forward<COBS>(a.co, a.critic_w1t, a.critic + C_B1, n0, a.b, s_u, s_h);
+    float value = a.critic[C_B2];
+    for (uint32_t k = 0; k < HID; k++) value = fma_f(a.critic[C_W2 + k], s_h[t * HS + k], value);
+    const float target = a.ret[m];
+    const float dvalue = a.vcoef * (value - target) * scale;
+    s_dv[t] = live ? dvalue : 0.0f;
+    __syncthreads();
+    if (t < HID) {  // critic w2: fma over rows
+        float g = 0.0f;
+        for (uint32_t r = 0; r < rows; r++) g = fma_f(s_dv[r], s_h[r * HS + t], g);
+        P[A_COUNT + C_W2 + t] = g;
+    } else if (t == HID) {  // critic b2
+        float g = 0.0f;
+        for (uint32_t r = 0; r < rows; r++) g += s_dv[r];
+        P[A_COUNT + C_B2] = g;
+    }
+    __syncthreads();
+    for (uint32_t k = 0; k < HID; k++) {  // critic hidden delta, in place
+        const float g = s_h[t * HS + k];
+        s_h[t * HS + k] = live ? dvalue * a.critic[C_W2 + k] * (1.0f - g * g) : 0.0f;
+    }
+    __syncthreads();
+    if (t < HID) {  // critic b1
+        float g = 0.0f;
+        for (uint32_t r = 0; r < rows; r++) g += s_h[r * HS + t];
+        P[A_COUNT + C_B1 + t] = g;
+    }
+    {   // critic W1 [64][32]: wavefronts 0 and 1 own one 32x32 tile each
+        const uint32_t jt[1] = {wv & 1}, it[1] = {0};
+        chunk_weight_grad<COBS, 32, 1>(a.co, n0, rows, jt, it, wv < 2, s_u, s_h, P + A_COUNT);
+    }
+
+    // ---- actor: forward, means, loss and derivatives
+    chunk_forward<OBS>(a.obs, a.actor_w1t, a.actor + A_B1, n0, a.b, s_u, s_h);
     float mean[4];
 #pragma unroll
     for (uint32_t q = 0; q < 4; q++) {
         float z = a.actor[A_B2 + q];
-#pragma unroll
-        for (uint32_t k = 0; k < HID; k++) z += a.actor[A_W2 + q * HID + k] * h[k];
+        for (uint32_t k = 0; k < HID; k++) z = fma_f(a.actor[A_W2 + q * HID + k], s_h[t * HS + k], z);
         mean[q] = z;
     }
-    float g[HID];
-#pragma unroll
-    for (uint32_t k = 0; k < HID; k++) g[k] = a.critic[C_B1 + k];
-    for (uint32_t i0 = 0; i0 < COBS; i0 += 16) {
-        for (uint32_t e = t; e < 256 * 16; e += 256) {
-            const uint32_t rr = e / 16, cc = e % 16;
-            const uint32_t row = n0 + rr;
-            tile[rr][cc] = row < a.b ? a.co[size_t(row) * COBS + i0 + cc] : 0.0f;
-        }
-        __syncthreads();
-#pragma unroll
-        for (uint32_t c = 0; c < 16; c++) {
-            const float xi = tile[t][c];
-            const float* w = a.critic_w1t + size_t(i0 + c) * HID;
-#pragma unroll
-            for (uint32_t k = 0; k < HID; k++) g[k] += w[k] * xi;
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (uint32_t k = 0; k < HID; k++) g[k] = tanh_f(g[k]);
-    float value = a.critic[C_B2];
-#pragma unroll
-    for (uint32_t k = 0; k < HID; k++) value += a.critic[C_W2 + k] * g[k];
-
-    // sample_loss_and_grad (rows past the minibatch compute on index 0 and
-    // store nothing)
-    const uint32_t m = live ? n : 0;
     const float* act = a.actions + size_t(m) * 4;
     const float* ls = a.actor + A_LS;
     float logp = 0.0f;
@@ -287,130 +422,67 @@ __global__ __launch_bounds__(256) void rows_kernel(RowArgs a) {
     const float raw = logp - a.old_logp[m];
     const float lr = clamp_f(raw, -20.0f, 20.0f);
     const float ratio = exp_f(lr);
-    const float adv = a.adv[m], target = a.ret[m];
+    const float adv = a.adv[m];
     const float clipped = clamp_f(ratio, 1.0f - a.clip, 1.0f + a.clip);
     const float chosen = min_f(ratio * adv, clipped * adv);
     const bool in_range = raw >= -20.0f && raw <= 20.0f;
     const bool active = in_range && (adv >= 0.0f ? ratio <= 1.0f + a.clip : ratio >= 1.0f - a.clip);
-    const float scale = 1.0f / max_f(float(a.b), 1.0f);
-    float dmean[4], dlog[4], entropy = 0.0f;
+    float dmean[4], entropy = 0.0f;
+    float* rs = s_u + t * RS;  // the forward's scratch is free now
 #pragma unroll
     for (uint32_t q = 0; q < 4; q++) {
         const float inv_var = exp_f(-2.0f * ls[q]);
         const float diff = act[q] - mean[q];
+        float dl;
         if (active) {
             const float dlogp = -ratio * adv * scale;
             dmean[q] = dlogp * diff * inv_var;
-            dlog[q] = dlogp * (diff * diff * inv_var - 1.0f);
+            dl = dlogp * (diff * diff * inv_var - 1.0f);
         } else {
             dmean[q] = 0.0f;
-            dlog[q] = 0.0f;
+            dl = 0.0f;
         }
-        dlog[q] -= a.ecoef * scale;
+        dl -= a.ecoef * scale;
         entropy += -a.ecoef * (ls[q] + 0.5f * (1.0f + LOG_TWO_PI)) * scale;
+        rs[q] = dmean[q];
+        rs[4 + q] = dl;
     }
-    const float dvalue = a.vcoef * (value - target) * scale;
-    if (live) {
-        float* lo = a.loss + size_t(n) * 4;
-        lo[0] = -chosen * scale;
-        lo[1] = 0.5f * a.vcoef * (value - target) * (value - target) * scale;
-        lo[2] = entropy;
-        lo[3] = ratio;
-#pragma unroll
-        for (uint32_t q = 0; q < 4; q++) {
-            a.dm[size_t(n) * 4 + q] = dmean[q];
-            a.dls[size_t(n) * 4 + q] = dlog[q];
+    rs[8] = -chosen * scale;
+    rs[9] = 0.5f * a.vcoef * (value - target) * (value - target) * scale;
+    rs[10] = entropy;
+    rs[11] = ratio;
+    __syncthreads();
+    {   // actor W2[q][k]: fma over rows; then b2, log_std and the metric sums
+        const uint32_t q = t / HID, k = t % HID;
+        float g = 0.0f;
+        for (uint32_t r = 0; r < rows; r++) g = fma_f(s_u[r * RS + q], s_h[r * HS + k], g);
+        P[A_W2 + q * HID + k] = g;
+        if (t < 12) {
+            const uint32_t col = t < 4 ? t : t < 8 ? 4 + (t - 4) : 8 + (t - 8);
+            float g2 = 0.0f;
+            for (uint32_t r = 0; r < rows; r++) g2 += s_u[r * RS + col];
+            P[t < 4 ? A_B2 + t : t < 8 ? A_LS + (t - 4) : A_COUNT + C_COUNT + (t - 8)] = g2;
         }
-        a.dv[n] = dvalue;
     }
-    store_rows64(lds, h, a.ah, n0, rows);
-#pragma unroll
-    for (uint32_t k = 0; k < HID; k++) {
+    __syncthreads();
+    for (uint32_t k = 0; k < HID; k++) {  // actor hidden delta, in place
         float d = 0.0f;
 #pragma unroll
-        for (uint32_t q = 0; q < 4; q++) d += dmean[q] * a.actor[A_W2 + q * HID + k];
-        h[k] = d * (1.0f - h[k] * h[k]);
+        for (uint32_t q = 0; q < 4; q++) d = fma_f(dmean[q], a.actor[A_W2 + q * HID + k], d);
+        const float h = s_h[t * HS + k];
+        s_h[t * HS + k] = live ? d * (1.0f - h * h) : 0.0f;
     }
-    store_rows64(lds, h, a.adelta, n0, rows);
-    store_rows64(lds, g, a.ch, n0, rows);
-#pragma unroll
-    for (uint32_t k = 0; k < HID; k++) g[k] = dvalue * a.critic[C_W2 + k] * (1.0f - g[k] * g[k]);
-    store_rows64(lds, g, a.cdelta, n0, rows);
-}
-
-// ---------------------------------------------------------------- gradient partials
-// First-layer weight gradients of one 256-row chunk: lane = input feature,
-// 64 accumulators (one per hidden unit), rows ascending; deltas are
-// wave-uniform scalar loads.  grid.x = chunk, grid.y = 0 actor / 1 critic.
-__global__ __launch_bounds__(192) void w1_grad_kernel(const float* __restrict__ obs, const float* __restrict__ co,
-                                                      const float* __restrict__ adelta,
-                                                      const float* __restrict__ cdelta, float* __restrict__ part,
-                                                      uint32_t b) {
-    const uint32_t c = blockIdx.x;
-    const bool critic = blockIdx.y == 1;
-    const uint32_t D = critic ? COBS : OBS;
-    const uint32_t i = threadIdx.x;
-    if (i >= D) return;
-    const float* X = critic ? co : obs;
-    const float* delta = critic ? cdelta : adelta;
-    float acc[HID];
-#pragma unroll
-    for (uint32_t k = 0; k < HID; k++) acc[k] = 0.0f;
-    const uint32_t end = (c + 1) * CHUNK < b ? (c + 1) * CHUNK : b;
-    for (uint32_t n = c * CHUNK; n < end; n++) {
-        const float x = X[size_t(n) * D + i];
-        const float* d = delta + size_t(n) * HID;
-#pragma unroll
-        for (uint32_t k = 0; k < HID; k++) acc[k] += d[k] * x;
+    __syncthreads();
+    if (t < HID) {  // actor b1
+        float g = 0.0f;
+        for (uint32_t r = 0; r < rows; r++) g += s_h[r * HS + t];
+        P[A_B1 + t] = g;
     }
-    float* out = part + size_t(c) * P_TOTAL + (critic ? A_COUNT : 0);
-#pragma unroll
-    for (uint32_t k = 0; k < HID; k++) out[size_t(k) * D + i] = acc[k];
-}
-
-// The remaining sums of one chunk: actor b1, W2, b2, log_std; critic b1, w2,
-// b2; the four metric sums.  One thread per output slot.
-constexpr uint32_t SMALL_SLOTS = HID + 4 * HID + 4 + 4 + HID + HID + 1 + 4;  // 461
-__global__ __launch_bounds__(512) void small_grad_kernel(const float* __restrict__ ah, const float* __restrict__ adelta,
-                                                         const float* __restrict__ ch, const float* __restrict__ cdelta,
-                                                         const float* __restrict__ dm, const float* __restrict__ dls,
-                                                         const float* __restrict__ dv, const float* __restrict__ loss,
-                                                         float* __restrict__ part, uint32_t b) {
-    const uint32_t c = blockIdx.x;
-    uint32_t s = threadIdx.x;
-    if (s >= SMALL_SLOTS) return;
-    const uint32_t begin = c * CHUNK, end = (c + 1) * CHUNK < b ? (c + 1) * CHUNK : b;
-    float acc = 0.0f;
-    size_t out;
-    float* P = part + size_t(c) * P_TOTAL;
-    if (s < HID) {  // actor b1
-        for (uint32_t n = begin; n < end; n++) acc += adelta[size_t(n) * HID + s];
-        out = A_B1 + s;
-    } else if ((s -= HID) < 4 * HID) {  // actor W2[a][h]
-        const uint32_t q = s / HID, h = s % HID;
-        for (uint32_t n = begin; n < end; n++) acc += dm[size_t(n) * 4 + q] * ah[size_t(n) * HID + h];
-        out = A_W2 + s;
-    } else if ((s -= 4 * HID) < 4) {  // actor b2
-        for (uint32_t n = begin; n < end; n++) acc += dm[size_t(n) * 4 + s];
-        out = A_B2 + s;
-    } else if ((s -= 4) < 4) {  // actor log_std
-        for (uint32_t n = begin; n < end; n++) acc += dls[size_t(n) * 4 + s];
-        out = A_LS + s;
-    } else if ((s -= 4) < HID) {  // critic b1
-        for (uint32_t n = begin; n < end; n++) acc += cdelta[size_t(n) * HID + s];
-        out = A_COUNT + C_B1 + s;
-    } else if ((s -= HID) < HID) {  // critic w2
-        for (uint32_t n = begin; n < end; n++) acc += dv[n] * ch[size_t(n) * HID + s];
-        out = A_COUNT + C_W2 + s;
-    } else if ((s -= HID) < 1) {  // critic b2
-        for (uint32_t n = begin; n < end; n++) acc += dv[n];
-        out = A_COUNT + C_B2;
-    } else {  // metric sums (main.mm:941-951)
-        s -= 1;
-        for (uint32_t n = begin; n < end; n++) acc += loss[size_t(n) * 4 + s];
-        out = A_COUNT + C_COUNT + s;
+    {   // actor W1 [64][181]: 2 x 6 tiles, three per wavefront
+        const uint32_t jt[3] = {(3 * wv) / 6, (3 * wv + 1) / 6, (3 * wv + 2) / 6};
+        const uint32_t it[3] = {(3 * wv) % 6, (3 * wv + 1) % 6, (3 * wv + 2) % 6};
+        chunk_weight_grad<OBS, OBS_PAD, 3>(a.obs, n0, rows, jt, it, true, s_u, s_h, P);
     }
-    P[out] = acc;
 }
 
 // Chunk partials summed within groups of GRAD_GROUP chunks, in place into
@@ -539,17 +611,13 @@ hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* s
 }
 
 hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st) {
-    hipLaunchKernelGGL(ppo::rows_kernel, dim3((a->b + 255) / 256), dim3(256), 0, st, *a);
+    if (a->b == 0) return hipSuccess;
+    hipLaunchKernelGGL(ppo::chunk_kernel, dim3((a->b + 255) / 256), dim3(256), 0, st, *a);
     return hipGetLastError();
 }
 
-hipError_t ppo_launch_grads(const float* obs, const float* co, const float* ah, const float* adelta, const float* ch,
-                            const float* cdelta, const float* dm, const float* dls, const float* dv, const float* loss,
-                            float* part, float* grad, uint32_t b, hipStream_t st) {
+hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, hipStream_t st) {
     const uint32_t chunks = (b + ppo::CHUNK - 1) / ppo::CHUNK;
-    hipLaunchKernelGGL(ppo::w1_grad_kernel, dim3(chunks, 2), dim3(192), 0, st, obs, co, adelta, cdelta, part, b);
-    hipLaunchKernelGGL(ppo::small_grad_kernel, dim3(chunks), dim3(512), 0, st, ah, adelta, ch, cdelta, dm, dls, dv, loss,
-                       part, b);
     const uint32_t groups = (chunks + ppo::GRAD_GROUP - 1) / ppo::GRAD_GROUP;
     hipLaunchKernelGGL(ppo::group_reduce_kernel, dim3((ppo::P_TOTAL + 255) / 256, groups), dim3(256), 0, st, part, chunks);
     hipLaunchKernelGGL(ppo::chunk_reduce_kernel, dim3((ppo::P_TOTAL + 255) / 256), dim3(256), 0, st, part, grad, chunks);

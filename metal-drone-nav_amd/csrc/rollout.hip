@@ -427,7 +427,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 const float x = s_obs[grp][i];
                 const float* w = AW1 + i * HID + lane * HU;
 #pragma unroll
-                for (int k = 0; k < HU; k++) acc[k] += w[k] * x;
+                for (int k = 0; k < HU; k++) acc[k] = fma_f(w[k], x, acc[k]);
             }
 #pragma unroll
             for (int k = 0; k < HU; k++) s_ah[grp][lane * HU + k] = tanh_f(acc[k]);
@@ -438,7 +438,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 const float x = s_co[grp][i];
                 const float* w = a.critic_w1t + size_t(i) * HID + lane * HU;
 #pragma unroll
-                for (int k = 0; k < HU; k++) acc[k] += w[k] * x;
+                for (int k = 0; k < HU; k++) acc[k] = fma_f(w[k], x, acc[k]);
             }
 #pragma unroll
             for (int k = 0; k < HU; k++) s_ch[grp][lane * HU + k] = tanh_f(acc[k]);
@@ -453,12 +453,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             for (int q = 0; q < 4; q++) {
                 float z = A[a_b2 + q];
 #pragma unroll 8
-                for (uint32_t h = 0; h < HID; h++) z += A[a_w2 + q * HID + h] * s_ah[grp][h];
+                for (uint32_t h = 0; h < HID; h++) z = fma_f(A[a_w2 + q * HID + h], s_ah[grp][h], z);
                 mean[q] = z;
             }
             float value = CR[c_b2];
 #pragma unroll 8
-            for (uint32_t h = 0; h < HID; h++) value += CR[c_w2 + h] * s_ch[grp][h];
+            for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
             uint32_t rng = r.rng;
             float lp = 0, act[4];
 #pragma unroll
@@ -653,7 +653,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 const float x = s_co[grp][i];
                 const float* w = a.critic_w1t + size_t(i) * HID + lane * HU;
 #pragma unroll
-                for (int k = 0; k < HU; k++) acc[k] += w[k] * x;
+                for (int k = 0; k < HU; k++) acc[k] = fma_f(w[k], x, acc[k]);
             }
 #pragma unroll
             for (int k = 0; k < HU; k++) s_ch[grp][lane * HU + k] = tanh_f(acc[k]);
@@ -663,7 +663,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         if (active) {
             float value = CR[c_b2];
 #pragma unroll 8
-            for (uint32_t h = 0; h < HID; h++) value += CR[c_w2 + h] * s_ch[grp][h];
+            for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
             if (lane == 0) a.next_values[row] = value;
             if (ended) {
                 reset_rng = r.rng;

@@ -7,7 +7,10 @@
  * Accelerate SGEMM) and, where the GPU path of the reference differs, the
  * kernels of sim.metal.  Reductions follow the canonical orders the HIP path
  * also uses (one definition, so both produce the same bits):
- *   - dot products:   z = b; z += w[i]*x[i] for i ascending (ppo.hpp:65-93);
+ *   - dot products:   z = b; z = fma(w[i], x[i], z) for i ascending
+ *     (ppo.hpp:65-93, one rounding per step);
+ *   - weight-gradient sums: g = fma(delta, x, g) over rows, same row order
+ *     as the sums below;
  *   - sums over the rows of a minibatch: sequential within 256-row chunks,
  *     chunk partials summed sequentially within groups of 32 chunks, group
  *     sums sequentially (a single chunk at the reference's 256-row
@@ -43,13 +46,13 @@ inline void actor_forward(const PolicyShape& s, const float* w, const float* obs
     for (uint32_t h = 0; h < s.hidden; ++h) {
         float z = w[s.actor_b1() + h];
         const float* row = w + size_t(h) * s.obs;
-        for (uint32_t i = 0; i < s.obs; ++i) z += row[i] * obs[i];
+        for (uint32_t i = 0; i < s.obs; ++i) z = fma_f(row[i], obs[i], z);
         hidden[h] = tanh_f(z);
     }
     for (uint32_t a = 0; a < MDN_ACTIONS; ++a) {
         float z = w[s.actor_b2() + a];
         const float* row = w + s.actor_w2() + size_t(a) * s.hidden;
-        for (uint32_t h = 0; h < s.hidden; ++h) z += row[h] * hidden[h];
+        for (uint32_t h = 0; h < s.hidden; ++h) z = fma_f(row[h], hidden[h], z);
         mean[a] = z;
     }
 }
@@ -57,11 +60,11 @@ inline float critic_forward(const PolicyShape& s, const float* w, const float* o
     for (uint32_t h = 0; h < s.critic_hidden; ++h) {
         float z = w[s.critic_b1() + h];
         const float* row = w + size_t(h) * s.critic_obs;
-        for (uint32_t i = 0; i < s.critic_obs; ++i) z += row[i] * obs[i];
+        for (uint32_t i = 0; i < s.critic_obs; ++i) z = fma_f(row[i], obs[i], z);
         hidden[h] = tanh_f(z);
     }
     float value = w[s.critic_b2()];
-    for (uint32_t h = 0; h < s.critic_hidden; ++h) value += w[s.critic_w2() + h] * hidden[h];
+    for (uint32_t h = 0; h < s.critic_hidden; ++h) value = fma_f(w[s.critic_w2() + h], hidden[h], value);
     return value;
 }
 inline float gaussian_log_prob(const float* action, const float* mean, const float* log_std) {
@@ -590,7 +593,7 @@ struct Trainer {
             // ppo.metal:470-485 and 618-631
             for (uint32_t h = 0; h < H; h++) {
                 float d = 0.0f;
-                for (uint32_t a = 0; a < 4; a++) d += dm[size_t(n) * 4 + a] * actor[S.actor_w2() + a * H + h];
+                for (uint32_t a = 0; a < 4; a++) d = fma_f(dm[size_t(n) * 4 + a], actor[S.actor_w2() + a * H + h], d);
                 const float act = ah[size_t(n) * H + h];
                 adelta[size_t(n) * H + h] = d * (1.0f - act * act);
             }
@@ -626,21 +629,22 @@ struct Trainer {
                 for (uint32_t h = 0; h < H; h++) {
                     const float d = adelta[size_t(n) * H + h];
                     float* row = ga + size_t(h) * D;
-                    for (uint32_t i = 0; i < D; i++) row[i] += d * x[i];
+                    for (uint32_t i = 0; i < D; i++) row[i] = fma_f(d, x[i], row[i]);
                     ga[S.actor_b1() + h] += d;
                 }
                 for (uint32_t a = 0; a < 4; a++) {
                     const float g = dm[size_t(n) * 4 + a];
-                    for (uint32_t h = 0; h < H; h++) ga[S.actor_w2() + a * H + h] += g * ah[size_t(n) * H + h];
+                    for (uint32_t h = 0; h < H; h++)
+                        ga[S.actor_w2() + a * H + h] = fma_f(g, ah[size_t(n) * H + h], ga[S.actor_w2() + a * H + h]);
                     ga[S.actor_b2() + a] += g;
                     ga[S.actor_log_std() + a] += dls[size_t(n) * 4 + a];
                 }
                 for (uint32_t h = 0; h < CH; h++) {
                     const float d = cdelta[size_t(n) * CH + h];
                     float* row = gc + size_t(h) * CD;
-                    for (uint32_t i = 0; i < CD; i++) row[i] += d * cx[i];
+                    for (uint32_t i = 0; i < CD; i++) row[i] = fma_f(d, cx[i], row[i]);
                     gc[S.critic_b1() + h] += d;
-                    gc[S.critic_w2() + h] += dv[n] * ch[size_t(n) * CH + h];
+                    gc[S.critic_w2() + h] = fma_f(dv[n], ch[size_t(n) * CH + h], gc[S.critic_w2() + h]);
                 }
                 gc[S.critic_b2()] += dv[n];
             }
