@@ -47,7 +47,7 @@ __device__ __forceinline__ void raptor_group(const float* RW, const float (&mo)[
             const uint32_t row16 = lane + G * j;
             float val = RW[352 + row16];
 #pragma unroll
-            for (int col = 0; col < 22; col++) val += RW[row16 * 22 + col] * mo[col];
+            for (int col = 0; col < 22; col++) val = fma_f(RW[row16 * 22 + col], mo[col], val);
             sx[row16] = max_f(val, 0.0f);
         }
     }
@@ -67,8 +67,8 @@ __device__ __forceinline__ void raptor_group(const float* RW, const float (&mo)[
                 float ivv = RW[1904 + rowg], hvv = RW[1952 + rowg];
 #pragma unroll
                 for (int col = 0; col < 16; col++) {
-                    ivv += RW[368 + rowg * 16 + col] * x[col];
-                    hvv += RW[1136 + rowg * 16 + col] * hidden[col];
+                    ivv = fma_f(RW[368 + rowg * 16 + col], x[col], ivv);
+                    hvv = fma_f(RW[1136 + rowg * 16 + col], hidden[col], hvv);
                 }
                 iv[g3] = ivv;
                 hv[g3] = hvv;
@@ -90,7 +90,7 @@ __device__ __forceinline__ void raptor_group(const float* RW, const float (&mo)[
         for (int q = 0; q < 4; q++) {  // output dense + clip (raptor.hpp:86-97)
             float val = RW[2080 + q];
 #pragma unroll
-            for (int col = 0; col < 16; col++) val += RW[2016 + q * 16 + col] * hidden[col];
+            for (int col = 0; col < 16; col++) val = fma_f(RW[2016 + q * 16 + col], hidden[col], val);
             act[q] = max_f(-1.0f, min_f(1.0f, val));
         }
     }
@@ -194,6 +194,124 @@ __global__ __launch_bounds__(64) void reset_kernel(RolloutArgs a) {
     for (uint32_t j = 0; j < 96; j++) a.poses[size_t(n) * 96 + j] = 0.0f;
 }
 
+// ---------------------------------------------------------------- matrix-core layer
+// One hidden layer for 32 envs on the fp32 matrix cores: out[env][unit] =
+// tanh(b1[unit] + sum_k x[env][k] * w1t[k][unit]).  v_mfma_f32_16x16x4_f32
+// applies acc = fma(a[k], b[k], acc) for its four k in ascending order with
+// one rounding each, so the chain over k0 = 0, 4, 8, ... is exactly the
+// canonical fma chain from the bias.  A lane a holds A[a%16][k0 + a/16], B
+// lane a holds B[k0 + a/16][a%16], accumulator r of lane l is
+// D[4(l/16) + r][l%16].  Wavefront w computes tiles 2w and 2w+1 of the 2 x 4
+// grid of 16x16 tiles (env block = tile / 4, unit block = tile % 4).
+typedef float v4f __attribute__((ext_vector_type(4)));
+template <uint32_t D, uint32_t XS, uint32_t OS>
+__device__ __forceinline__ void wg_layer(const float* x, const float* w1t, const float* b1, float* out) {
+    const uint32_t wv = threadIdx.x / 64, l = threadIdx.x % 64;
+    uint32_t env[2], unit[2];
+    v4f acc[2];
+#pragma unroll
+    for (uint32_t q = 0; q < 2; q++) {
+        const uint32_t tile = 2 * wv + q;
+        env[q] = 16 * (tile / 4) + l % 16;
+        unit[q] = 16 * (tile % 4) + l % 16;
+        const float bias = b1[unit[q]];
+        acc[q][0] = bias; acc[q][1] = bias; acc[q][2] = bias; acc[q][3] = bias;
+    }
+#pragma unroll 8
+    for (uint32_t k0 = 0; k0 < D; k0 += 4) {
+        const uint32_t k = k0 + l / 16;
+#pragma unroll
+        for (uint32_t q = 0; q < 2; q++) {
+            const float av = k < D ? x[env[q] * XS + k] : 0.0f;
+            const float bv = k < D ? w1t[k * HID + unit[q]] : -0.0f;
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[q], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < 2; q++) {
+        const uint32_t e0 = env[q] - l % 16 + 4 * (l / 16);
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) out[(e0 + r) * OS + unit[q]] = tanh_f(acc[q][r]);
+    }
+}
+
+// RAPTOR step (raptor.hpp:52-97) for the 32 envs of a workgroup with the
+// dense and GRU layers on the matrix cores (16x16x4 tiles, fma chains from the
+// biases as in the group step).  Every env's group writes its observation row
+// mo[22] to `smo` (stride MS); wavefronts 0 and 1 evaluate env blocks 0 and 1;
+// the new hidden state lands in `snh`, the old one is read from `srh`.  Three
+// workgroup barriers; call from uniform control flow.  `on` masks envs whose
+// step is skipped (their rows are computed and ignored).
+template <int G, uint32_t MS>
+__device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22], float* smo, float* sx, float* srh,
+                                          float* snh, uint32_t grp, uint32_t lane, bool on, float (&act)[4]) {
+    const uint32_t wv = threadIdx.x / 64, l = threadIdx.x % 64, j = l % 16;
+#pragma unroll
+    for (int c = 0; c < 22; c++)
+        if (c % G == int(lane)) smo[grp * MS + c] = mo[c];
+    __syncthreads();
+    if (wv < 2) {  // Dense 22->16 + ReLU (raptor.hpp:54-60)
+        const uint32_t env = 16 * wv + j;
+        v4f acc;
+        const float bias = RW[352 + j];
+        acc[0] = bias; acc[1] = bias; acc[2] = bias; acc[3] = bias;
+#pragma unroll
+        for (uint32_t k0 = 0; k0 < 22; k0 += 4) {
+            const uint32_t k = k0 + l / 16;
+            const float av = k < 22 ? smo[env * MS + k] : 0.0f;
+            const float bv = k < 22 ? RW[j * 22 + k] : -0.0f;
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) sx[(16 * wv + 4 * (l / 16) + r) * 17 + j] = max_f(acc[r], 0.0f);
+    }
+    __syncthreads();
+    if (wv < 2) {  // GRU (raptor.hpp:62-84): gate g of unit u is row 16g + u
+        const uint32_t env = 16 * wv + j;
+        v4f iv[3], hv[3];
+#pragma unroll
+        for (uint32_t g = 0; g < 3; g++) {
+            const float bi = RW[1904 + 16 * g + j], bh = RW[1952 + 16 * g + j];
+            iv[g][0] = bi; iv[g][1] = bi; iv[g][2] = bi; iv[g][3] = bi;
+            hv[g][0] = bh; hv[g][1] = bh; hv[g][2] = bh; hv[g][3] = bh;
+        }
+#pragma unroll
+        for (uint32_t k0 = 0; k0 < 16; k0 += 4) {
+            const uint32_t k = k0 + l / 16;
+            const float ax = sx[env * 17 + k], ah = srh[env * 17 + k];
+#pragma unroll
+            for (uint32_t g = 0; g < 3; g++) {
+                iv[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(ax, RW[368 + (16 * g + j) * 16 + k], iv[g], 0, 0, 0);
+                hv[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(ah, RW[1136 + (16 * g + j) * 16 + k], hv[g], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) {
+            const uint32_t e = 16 * wv + 4 * (l / 16) + r;
+            const float reset = sigmoid_f(iv[0][r] + hv[0][r]);
+            const float update = sigmoid_f(iv[1][r] + hv[1][r]);
+            const float cand = tanh_f(iv[2][r] + reset * hv[2][r]);
+            snh[e * 17 + j] = (1.0f - update) * cand + update * srh[e * 17 + j];
+        }
+    }
+    __syncthreads();
+    if (on) {  // output dense + clip (raptor.hpp:86-97), commit the hidden state
+        float hidden[16];
+#pragma unroll
+        for (int c = 0; c < 16; c++) hidden[c] = snh[grp * 17 + c];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float val = RW[2080 + q];
+#pragma unroll
+            for (int c = 0; c < 16; c++) val = fma_f(RW[2016 + q * 16 + c], hidden[c], val);
+            act[q] = max_f(-1.0f, min_f(1.0f, val));
+        }
+#pragma unroll
+        for (int c = 0; c < 16; c++)
+            if (c % G == int(lane)) srh[grp * 17 + c] = hidden[c];
+    }
+}
+
 // ---------------------------------------------------------------- rollout
 // W = wavefronts per workgroup.  W == 1: weights and camera rays are read from
 // global memory (L1/L2 resident).  W > 1: the workgroup stages one copy of the
@@ -251,6 +369,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     __shared__ float s_cmd[E][33];
     __shared__ float s_x[E][17];
     __shared__ float s_h[E][17];
+    // W > 1: RAPTOR hidden state of each env, resident in LDS for the launch
+    __shared__ float s_rh[W > 1 ? E : 1][17];
 
     float* world = s_world[grp];
     State s;
@@ -277,6 +397,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     float hu[U];
 #pragma unroll
     for (int j = 0; j < U; j++) hu[j] = bits_float(a.run[size_t(RW_HIDDEN + lane + G * j) * N + nn]);
+    if constexpr (W > 1)
+        for (uint32_t c = lane; c < 16; c += G) s_rh[grp][c] = bits_float(a.run[size_t(RW_HIDDEN + c) * N + nn]);
     const float* A = a.actor;
     const float* CR = a.critic;
     const uint32_t a_b1 = HID * OBS, a_w2 = a_b1 + HID, a_b2 = a_w2 + 4 * HID, a_ls = a_b2 + 4;
@@ -418,7 +540,13 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         group_sync();
 
         // ---- actor and critic hidden layers (ppo.hpp:65-72, 82-89)
-        if (active) {
+        if constexpr (W > 1) {  // all 32 envs of the workgroup on the matrix cores
+            static_assert(E == 32, "matrix-core layers assume 32 envs per workgroup");
+            __syncthreads();
+            wg_layer<OBS, OBS + 4, HID + 1>(&s_obs[0][0], AW1, A + a_b1, &s_ah[0][0]);
+            wg_layer<COBS, COBS + 1, HID + 1>(&s_co[0][0], a.critic_w1t, CR + c_b1, &s_ch[0][0]);
+            __syncthreads();
+        } else if (active) {
             float acc[HU];
 #pragma unroll
             for (int k = 0; k < HU; k++) acc[k] = A[a_b1 + lane * HU + k];
@@ -555,7 +683,10 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 for (int j = 0; j < 4; j++) mo[18 + j] = r.motors[j];
             }
             float act[4];
-            raptor_group<G>(RW, mo, r.hidden, hu, s_x[grp], s_h[grp], lane, !done, act);
+            if constexpr (W > 1)
+                raptor_wg<G, OBS + 4>(RW, mo, &s_obs[0][0], &s_x[0][0], &s_rh[0][0], &s_h[0][0], grp, lane, !done, act);
+            else
+                raptor_group<G>(RW, mo, r.hidden, hu, s_x[grp], s_h[grp], lane, !done, act);
             if (!done) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) r.motors[q] = act[q];
@@ -643,22 +774,28 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 ended = !C.eval;
             }
         }
-        group_sync();
-        if (active) {  // next value: critic hidden split over the group
-            float acc[HU];
+        if constexpr (W > 1) {  // next value: critic hidden of s' for all 32 envs
+            __syncthreads();
+            wg_layer<COBS, COBS + 1, HID + 1>(&s_co[0][0], a.critic_w1t, CR + c_b1, &s_ch[0][0]);
+            __syncthreads();
+        } else {  // next value: critic hidden split over the group
+            group_sync();
+            if (active) {
+                float acc[HU];
 #pragma unroll
-            for (int k = 0; k < HU; k++) acc[k] = CR[c_b1 + lane * HU + k];
+                for (int k = 0; k < HU; k++) acc[k] = CR[c_b1 + lane * HU + k];
 #pragma unroll 4
-            for (uint32_t i = 0; i < COBS; i++) {
-                const float x = s_co[grp][i];
-                const float* w = a.critic_w1t + size_t(i) * HID + lane * HU;
+                for (uint32_t i = 0; i < COBS; i++) {
+                    const float x = s_co[grp][i];
+                    const float* w = a.critic_w1t + size_t(i) * HID + lane * HU;
 #pragma unroll
-                for (int k = 0; k < HU; k++) acc[k] = fma_f(w[k], x, acc[k]);
+                    for (int k = 0; k < HU; k++) acc[k] = fma_f(w[k], x, acc[k]);
+                }
+#pragma unroll
+                for (int k = 0; k < HU; k++) s_ch[grp][lane * HU + k] = tanh_f(acc[k]);
             }
-#pragma unroll
-            for (int k = 0; k < HU; k++) s_ch[grp][lane * HU + k] = tanh_f(acc[k]);
+            group_sync();
         }
-        group_sync();
         uint32_t reset_rng = 0, reset_family = 0, reset_seed = 0;
         if (active) {
             float value = CR[c_b2];
@@ -679,6 +816,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             reset_apply(C, P, RW, nn, false, reset_rng, world, s, r);
 #pragma unroll
             for (int j = 0; j < U; j++) hu[j] = RW[2000 + lane + G * j];
+            if constexpr (W > 1)
+                for (uint32_t c = lane; c < 16; c += G) s_rh[grp][c] = RW[2000 + c];
             for (uint32_t i = lane; i < uint32_t(K) * POOL; i += G) s_ring[grp][i] = 12.0f;
             for (uint32_t i = lane; i < 32; i += G) {
                 s_cmd[grp][i] = 0.0f;
@@ -690,6 +829,11 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         group_sync();
         if (ended)
             for (uint32_t i = lane; i < WORLD_WORDS; i += G) a.world[size_t(nn) * WORLD_WORDS + i] = world[i];
+    }
+    if constexpr (W > 1) {
+        group_sync();
+#pragma unroll
+        for (int c = 0; c < 16; c++) r.hidden[c] = s_rh[grp][c];
     }
     if (live) {
         store_state(a.state, N, n, s, lane, G);
@@ -763,7 +907,7 @@ __global__ __launch_bounds__(64) void raptor_fixture_kernel(const float* __restr
             for (int q = 0; q < 4; q++) {
                 float val = RW[2080 + q];
 #pragma unroll
-                for (int col = 0; col < 16; col++) val += RW[2016 + q * 16 + col] * hidden[col];
+                for (int col = 0; col < 16; col++) val = fma_f(RW[2016 + q * 16 + col], hidden[col], val);
                 actions[(size_t(copy) * steps + t) * 4 + q] = val;
             }
         }

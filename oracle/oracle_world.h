@@ -480,6 +480,8 @@ inline void physics_step(const MdnPhysicsState& state, const float action[4], co
 }
 
 // ---- RAPTOR inner loop: raptor.hpp:42-97 --------------------------------
+// Dense and GRU dot products are fma chains from the bias, inputs ascending
+// (the same canonical form as the policy networks).
 inline void raptor_reset(const MdnRaptorWeights& w, float hidden[16]) {
     for (int i = 0; i < 16; i++) hidden[i] = w.initial_hidden_state[i];
 }
@@ -487,15 +489,15 @@ inline void raptor_forward(const MdnRaptorWeights& w, const float obs[22], float
     float x[16];
     for (int row = 0; row < 16; ++row) {
         float value = w.input_bias[row];
-        for (int col = 0; col < 22; ++col) value += w.input_weights[row * 22 + col] * obs[col];
+        for (int col = 0; col < 22; ++col) value = fma_f(w.input_weights[row * 22 + col], obs[col], value);
         x[row] = max_f(value, 0.0f);
     }
     float ig[48], hg[48];
     for (int row = 0; row < 48; ++row) {
         float iv = w.gru_input_bias[row], hv = w.gru_hidden_bias[row];
         for (int col = 0; col < 16; ++col) {
-            iv += w.gru_input_weights[row * 16 + col] * x[col];
-            hv += w.gru_hidden_weights[row * 16 + col] * hidden[col];
+            iv = fma_f(w.gru_input_weights[row * 16 + col], x[col], iv);
+            hv = fma_f(w.gru_hidden_weights[row * 16 + col], hidden[col], hv);
         }
         ig[row] = iv;
         hg[row] = hv;
@@ -510,7 +512,7 @@ inline void raptor_forward(const MdnRaptorWeights& w, const float obs[22], float
     for (int i = 0; i < 16; ++i) hidden[i] = nh[i];
     for (int row = 0; row < 4; ++row) {
         float value = w.output_bias[row];
-        for (int col = 0; col < 16; ++col) value += w.output_weights[row * 16 + col] * hidden[col];
+        for (int col = 0; col < 16; ++col) value = fma_f(w.output_weights[row * 16 + col], hidden[col], value);
         action[row] = value;
     }
 }
