@@ -212,23 +212,39 @@ __device__ __forceinline__ float cast_ray_boxes(const BoxSlabs& bs, V d) {
 }
 
 // world.hpp:84-99
-__device__ __forceinline__ float clearance_at(const float* world, uint32_t count, V p, float time) {
-    float best = fmin_f(fmin_f(p.x + 2, 14 - p.x), fmin_f(fmin_f(p.y + 5, 5 - p.y), fmin_f(p.z, 5 - p.z))) - 0.18f;
-    for (uint32_t i = 0; i < count; i++) {
-        const float* o = world + 10 * i;
-        const uint32_t kind = float_bits(o[0]);
-        const V q = sub3(p, obstacle_center(o, time));
-        float distance;
-        if (kind == 1u || kind == 3u) distance = len3(q) - o[4];
-        else if (kind == 2u) {
-            const float a = sqrt_f(q.x * q.x + q.y * q.y) - o[4], b = fabs_f(q.z) - o[6];
-            distance = sqrt_f(fmax_f(a, 0.0f) * fmax_f(a, 0.0f) + fmax_f(b, 0.0f) * fmax_f(b, 0.0f)) + fmin_f(fmax_f(a, b), 0.0f);
-        } else {
-            const V k = mk(fabs_f(q.x) - o[4], fabs_f(q.y) - o[5], fabs_f(q.z) - o[6]);
-            distance = len3(mk(fmax_f(k.x, 0.0f), fmax_f(k.y, 0.0f), fmax_f(k.z, 0.0f))) + fmin_f(fmax_f(k.x, fmax_f(k.y, k.z)), 0.0f);
-        }
-        best = fmin_f(best, distance - 0.18f);
+__device__ __forceinline__ float room_clearance(V p) {
+    return fmin_f(fmin_f(p.x + 2, 14 - p.x), fmin_f(fmin_f(p.y + 5, 5 - p.y), fmin_f(p.z, 5 - p.z))) - 0.18f;
+}
+__device__ __forceinline__ float obstacle_clearance(const float* o, V p, float time) {
+    const uint32_t kind = float_bits(o[0]);
+    const V q = sub3(p, obstacle_center(o, time));
+    float distance;
+    if (kind == 1u || kind == 3u) distance = len3(q) - o[4];
+    else if (kind == 2u) {
+        const float a = sqrt_f(q.x * q.x + q.y * q.y) - o[4], b = fabs_f(q.z) - o[6];
+        distance = sqrt_f(fmax_f(a, 0.0f) * fmax_f(a, 0.0f) + fmax_f(b, 0.0f) * fmax_f(b, 0.0f)) + fmin_f(fmax_f(a, b), 0.0f);
+    } else {
+        const V k = mk(fabs_f(q.x) - o[4], fabs_f(q.y) - o[5], fabs_f(q.z) - o[6]);
+        distance = len3(mk(fmax_f(k.x, 0.0f), fmax_f(k.y, 0.0f), fmax_f(k.z, 0.0f))) + fmin_f(fmax_f(k.x, fmax_f(k.y, k.z)), 0.0f);
     }
+    return distance - 0.18f;
+}
+__device__ __forceinline__ float clearance_at(const float* world, uint32_t count, V p, float time) {
+    float best = room_clearance(p);
+    for (uint32_t i = 0; i < count; i++) best = fmin_f(best, obstacle_clearance(world + 10 * i, p, time));
+    return best;
+}
+// The same clearance evaluated by a lane group: lane l takes obstacles l,
+// l+G, ... and the group combines by xor shuffles.  For a finite point every
+// term is finite and none is -0 (x - 0.18f rounds an exact cancellation to
+// +0), so the minimum does not depend on the order and equals clearance_at.
+// Call with the whole group active.
+template <int G>
+__device__ __forceinline__ float clearance_group(const float* world, uint32_t count, V p, float time, uint32_t lane) {
+    float best = room_clearance(p);
+    for (uint32_t i = lane; i < count; i += G) best = fmin_f(best, obstacle_clearance(world + 10 * i, p, time));
+#pragma unroll
+    for (int off = 1; off < G; off <<= 1) best = fmin_f(best, __shfl_xor(best, off, G));
     return best;
 }
 

@@ -523,7 +523,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
             cob[30] = world[166];
             cob[31] = world[167];
-            cob[19] = clearance_at(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed) / 5.0f;
+            cob[19] = clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane) / 5.0f;
             cob[20] = float(r.steps) / 200.0f;
 #pragma unroll
             for (uint32_t j = 0; j < 3; j++)
@@ -704,7 +704,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                     r.path += sqrt_f(ex * ex + ey * ey + ez * ez);
                     s = nx;
                     r.elapsed += P.dt;
-                    const float cl = clearance_at(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed);
+                    const float cl = clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane);
                     step_clearance = min_f(step_clearance, cl);
                     r.min_clearance = min_f(r.min_clearance, cl);
                     r.peak_speed = max_f(r.peak_speed, sqrt_f(s.v[0] * s.v[0] + s.v[1] * s.v[1] + s.v[2] * s.v[2]));
@@ -749,7 +749,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
             cob[30] = world[166];
             cob[31] = world[167];
-            cob[19] = clearance_at(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed) / 5.0f;
+            cob[19] = clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane) / 5.0f;
             cob[20] = float(r.steps) / 200.0f;
 #pragma unroll
             for (uint32_t j = 0; j < 3; j++)
