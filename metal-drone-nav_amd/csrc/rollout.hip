@@ -235,6 +235,31 @@ __device__ __forceinline__ void wg_layer(const float* x, const float* w1t, const
     }
 }
 
+// Output heads for the 32 envs of a workgroup on the matrix cores:
+// out[env * 17 + c] = b[c] + sum_h w[c][h] * x[env][h] (c < NC), the fma chain
+// over the 64 hidden units ascending from the bias, as a 16x16x4 tile per
+// env block (columns c >= NC multiply by -0.0 and are not stored).  Wavefronts
+// w0 and w0+1 compute env blocks 0 and 1; `wstride` is the row stride of w.
+template <uint32_t NC, uint32_t XS>
+__device__ __forceinline__ void wg_head(const float* x, const float* w, uint32_t wstride, const float* b, uint32_t w0,
+                                        float* out, uint32_t col0) {
+    const uint32_t wv = threadIdx.x / 64, l = threadIdx.x % 64, c = l % 16;
+    if (wv < w0 || wv >= w0 + 2) return;
+    const uint32_t eb = wv - w0, env = 16 * eb + c;
+    v4f acc;
+    const float bias = c < NC ? b[c] : 0.0f;
+    acc[0] = bias; acc[1] = bias; acc[2] = bias; acc[3] = bias;
+#pragma unroll
+    for (uint32_t k0 = 0; k0 < HID; k0 += 4) {
+        const uint32_t k = k0 + l / 16;
+        const float bv = c < NC ? w[c * wstride + k] : -0.0f;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[env * XS + k], bv, acc, 0, 0, 0);
+    }
+    if (c < NC)
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) out[(16 * eb + 4 * (l / 16) + r) * 17 + col0 + c] = acc[r];
+}
+
 // RAPTOR step (raptor.hpp:52-97) for the 32 envs of a workgroup with the
 // dense and GRU layers on the matrix cores (16x16x4 tiles, fma chains from the
 // biases as in the group step).  Every env's group writes its observation row
@@ -546,6 +571,10 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             wg_layer<OBS, OBS + 4, HID + 1>(&s_obs[0][0], AW1, A + a_b1, &s_ah[0][0]);
             wg_layer<COBS, COBS + 1, HID + 1>(&s_co[0][0], a.critic_w1t, CR + c_b1, &s_ch[0][0]);
             __syncthreads();
+            // heads: means (waves 0-1) and value (waves 2-3) into s_x[env][0..4]
+            wg_head<4, HID + 1>(&s_ah[0][0], A + a_w2, HID, A + a_b2, 0, &s_x[0][0], 0);
+            wg_head<1, HID + 1>(&s_ch[0][0], CR + c_w2, 0, CR + c_b2, 2, &s_x[0][0], 4);
+            __syncthreads();
         } else if (active) {
             float acc[HU];
 #pragma unroll
@@ -576,17 +605,23 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         // ---- act (sim.metal:229-256): means, value, sample, log-prob, command
         float a_cmd[4] = {0, 0, 0, 0};
         if (active) {
-            float mean[4];
+            float mean[4], value;
+            if constexpr (W > 1) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float z = A[a_b2 + q];
+                for (int q = 0; q < 4; q++) mean[q] = s_x[grp][q];
+                value = s_x[grp][4];
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float z = A[a_b2 + q];
 #pragma unroll 8
-                for (uint32_t h = 0; h < HID; h++) z = fma_f(A[a_w2 + q * HID + h], s_ah[grp][h], z);
-                mean[q] = z;
+                    for (uint32_t h = 0; h < HID; h++) z = fma_f(A[a_w2 + q * HID + h], s_ah[grp][h], z);
+                    mean[q] = z;
+                }
+                value = CR[c_b2];
+#pragma unroll 8
+                for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
             }
-            float value = CR[c_b2];
-#pragma unroll 8
-            for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
             uint32_t rng = r.rng;
             float lp = 0, act[4];
 #pragma unroll
@@ -778,6 +813,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             __syncthreads();
             wg_layer<COBS, COBS + 1, HID + 1>(&s_co[0][0], a.critic_w1t, CR + c_b1, &s_ch[0][0]);
             __syncthreads();
+            wg_head<1, HID + 1>(&s_ch[0][0], CR + c_w2, 0, CR + c_b2, 0, &s_x[0][0], 4);
+            __syncthreads();
         } else {  // next value: critic hidden split over the group
             group_sync();
             if (active) {
@@ -798,9 +835,14 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         }
         uint32_t reset_rng = 0, reset_family = 0, reset_seed = 0;
         if (active) {
-            float value = CR[c_b2];
+            float value;
+            if constexpr (W > 1) {
+                value = s_x[grp][4];
+            } else {
+                value = CR[c_b2];
 #pragma unroll 8
-            for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
+                for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
+            }
             if (lane == 0) a.next_values[row] = value;
             if (ended) {
                 reset_rng = r.rng;
