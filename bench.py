@@ -57,7 +57,7 @@ def cpu_baseline(envs, target_s=12.0):
         t.iteration(done)
         done += 1
         el = time.perf_counter() - start
-        if el >= target_s or done >= 4:
+        if el >= target_s or done >= 64:
             break
     threads = int(oracle().orc_num_threads())
     return {"value": envs * horizon * done / el, "unit": "env-steps/s", "cores": threads, "kind": "port",
@@ -156,9 +156,9 @@ def main():
                 "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic_from_profile(),
                 "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)",
                 "kernel": "rollout_kernel (fused env step + rollout actor/critic, %d ticks per launch)" % T,
-                "roof_note": "fp32 compute roof (VALU work, no MFMA); algorithmic %.1f kFLOP and %.2f KB per "
-                             "env-step x %d env-steps per launch" % (FLOP_ENV_STEP / 1e3, BYTES_ENV_STEP / 1e3,
-                                                                     env_steps_launch),
+                "roof_note": "fp32 compute roof: env step on the VALU, policy/critic layers and RAPTOR dense/GRU "
+                             "on fp32 MFMA; algorithmic %.1f kFLOP and %.2f KB per env-step x %d env-steps per "
+                             "launch" % (FLOP_ENV_STEP / 1e3, BYTES_ENV_STEP / 1e3, env_steps_launch),
                 "hbm_frac_algorithmic": round(BYTES_ENV_STEP * env_steps_launch / avg_s / PEAK_HBM, 5)}
     secondary = {}
     if kernels["gae"]["launches"]:
