@@ -30,6 +30,7 @@ extern "C" {
 
 typedef struct MdnSim MdnSim;
 typedef struct MdnPPO MdnPPO;
+typedef struct MdnLargePPO MdnLargePPO;
 
 /* Buffer ids for mdn_sim_download / mdn_sim_upload.  Sizes follow the
  * reference's shared buffers of Sim (main.mm:519, 540-555). */
@@ -57,7 +58,8 @@ enum MdnBuffer {
     MDN_BUF_ACTOR_V = 20,
     MDN_BUF_CRITIC_M = 21,
     MDN_BUF_CRITIC_V = 22,
-    MDN_BUF_METRIC_ROWS = 23 /* float[updates][4] of the last rollout_update */
+    MDN_BUF_METRIC_ROWS = 23, /* float[updates][4] of the last rollout_update */
+    MDN_BUF_NEXT_CRITIC_OBS = 24 /* float[T][N][32] critic observation of s' (the next_values input) */
 };
 
 /* Kernel ids for mdn_sim_kernel_time. */
@@ -68,7 +70,10 @@ enum MdnKernel {
     MDN_K_ROWS = 3,      /* minibatch forward + loss/grad + hidden deltas */
     MDN_K_GRADS = 4,     /* gradient chunk partials + reduction */
     MDN_K_ADAM = 5,      /* norm clip + Adam + log-std clamp */
-    MDN_K_COUNT = 6
+    MDN_K_LP_FORWARD = 6,  /* wide-policy forward (evaluation and minibatch) + loss terms */
+    MDN_K_LP_BACKWARD = 7, /* wide-policy backward partials and their sums */
+    MDN_K_LP_ADAM = 8,     /* wide-policy clip + Adam + bf16 refresh */
+    MDN_K_COUNT = 9
 };
 
 const char* mdn_last_error(void);
@@ -120,6 +125,30 @@ int mdn_ppo_update(MdnPPO* ppo, uint32_t rollout_index);
 int mdn_ppo_metric_mean(MdnPPO* ppo, float out[4]);
 int mdn_ppo_optimizer_step(const MdnPPO* ppo, uint64_t* step);
 int mdn_ppo_updates_per_rollout(const MdnPPO* ppo, uint32_t* updates);
+
+/* PPOTrainer with the reference's FIXED_PPO_HIDDEN_DIM raised to `hidden`
+ * (ppo.hpp:17-45; the capacity actors of ACTOR_CAPACITY_RESULTS, width 5120
+ * for the 967,688-parameter actor at 184 inputs): actor 181 -> hidden -> 4,
+ * critic 32 -> hidden -> 1, fp32 parameters and Adam, first-layer GEMMs on
+ * bf16 matrix cores (results within bf16 tolerance of fp32).  `hidden` must
+ * be a positive multiple of 128.  Parameters start from the reference's
+ * initialisation stream (seed 1789, cpu_reference.hpp:89-103).  Works on the
+ * rollout buffers of `sim`. */
+int mdn_lppo_create(MdnSim* sim, uint32_t hidden, uint32_t epochs, uint32_t minibatch, MdnLargePPO** out);
+void mdn_lppo_destroy(MdnLargePPO* lp);
+/* Log-probabilities of the stored actions and values at s and s' under the
+ * wide policy, written into the sim's logp, values and next_values rows
+ * (the rollout's sim_act / next-value outputs for this policy). */
+int mdn_lppo_evaluate(MdnLargePPO* lp);
+/* PPOTrainer::rollout_update for the wide policy: GAE, normalisation,
+ * epochs x minibatches of forward, loss, backward, clip and Adam. */
+int mdn_lppo_rollout_update(MdnLargePPO* lp, uint32_t rollout_index);
+/* which: 0 actor, 1 critic, 2 actor Adam m, 3 actor v, 4 critic m, 5 critic v. */
+int mdn_lppo_param_count(const MdnLargePPO* lp, uint32_t which, uint64_t* count);
+int mdn_lppo_get_params(MdnLargePPO* lp, uint32_t which, float* host, uint64_t count);
+int mdn_lppo_set_params(MdnLargePPO* lp, uint32_t which, const float* host, uint64_t count);
+int mdn_lppo_metric_mean(MdnLargePPO* lp, float out[4]);
+int mdn_lppo_optimizer_step(const MdnLargePPO* lp, uint64_t* step);
 
 /* Stateless operators over host arrays (the reference's fixture kernels
  * physics_fixture / raptor_fixture / world_depth / world_clearance,

@@ -93,7 +93,7 @@ struct MdnSim {
     float* actor_w1t = nullptr;
     float* critic_w1t = nullptr;
     // rollout rows
-    float *obs = nullptr, *co = nullptr, *actions = nullptr, *logp = nullptr, *values = nullptr;
+    float *obs = nullptr, *co = nullptr, *nco = nullptr, *actions = nullptr, *logp = nullptr, *values = nullptr;
     float *rewards = nullptr, *next_values = nullptr, *advantages = nullptr, *returns = nullptr;
     uint8_t *terminated = nullptr, *truncated = nullptr;
     MdnPPO* ppo = nullptr;
@@ -103,7 +103,7 @@ struct MdnSim {
         nav::RolloutArgs a;
         a.state = state; a.run = run; a.world = world; a.sensors = sensors; a.poses = poses; a.commands = commands;
         a.raptor = raptor; a.actor = actor; a.actor_w1t = actor_w1t; a.critic = critic; a.critic_w1t = critic_w1t;
-        a.camera = camera; a.obs = obs; a.co = co; a.actions = actions; a.logp = logp; a.values = values;
+        a.camera = camera; a.obs = obs; a.co = co; a.nco = nco; a.actions = actions; a.logp = logp; a.values = values;
         a.rewards = rewards; a.next_values = next_values; a.terminated = terminated; a.truncated = truncated;
         a.cfg = cfg; a.phys = phys; a.count = count; a.horizon = horizon;
         return a;
@@ -168,6 +168,7 @@ BufInfo row_buffer(MdnSim* s, uint32_t id) {
     switch (id) {
         case MDN_BUF_OBS: return {s->obs, R * OBS * 4};
         case MDN_BUF_CRITIC_OBS: return {s->co, R * COBS * 4};
+        case MDN_BUF_NEXT_CRITIC_OBS: return {s->nco, R * COBS * 4};
         case MDN_BUF_ACTIONS: return {s->actions, R * 4 * 4};
         case MDN_BUF_LOGP: return {s->logp, R * 4};
         case MDN_BUF_VALUES: return {s->values, R * 4};
@@ -239,6 +240,7 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
     guard(dev_alloc(&s->critic_w1t, size_t(COBS) * HID));
     guard(dev_alloc(&s->obs, R * OBS));
     guard(dev_alloc(&s->co, R * COBS));
+    guard(dev_alloc(&s->nco, R * COBS));
     guard(dev_alloc(&s->actions, R * 4));
     guard(dev_alloc(&s->logp, R));
     guard(dev_alloc(&s->values, R));
@@ -290,7 +292,7 @@ void mdn_sim_destroy(MdnSim* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->ppo) mdn_ppo_destroy(s->ppo);
     void* bufs[] = {s->state, s->run, s->world, s->sensors, s->poses, s->commands, s->raptor, s->camera,
-                    s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->obs, s->co, s->actions, s->logp,
+                    s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->obs, s->co, s->nco, s->actions, s->logp,
                     s->values, s->rewards, s->next_values, s->advantages, s->returns, s->terminated, s->truncated};
     for (void* b : bufs)
         if (b) hipFree(b);
@@ -718,6 +720,236 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon) {
                                  static_cast<float*>(stats.p), epsilon, nullptr));
     HIP_TRY(hipDeviceSynchronize());
     HIP_TRY(hipMemcpy(advantages, a.p, count * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+
+// ---------------------------------------------------------------- wide policy
+}  // extern "C"
+
+struct MdnLargePPO {
+    MdnSim* sim = nullptr;
+    uint32_t hidden = 0, epochs = 1, minibatch = 0, updates = 0, chunks = 1;
+    uint64_t optimizer_step = 0;
+    mdn::PolicyShape shape;
+    float *actor = nullptr, *critic = nullptr, *am = nullptr, *av = nullptr, *cm = nullptr, *cv = nullptr;
+    __bf16 *awb = nullptr, *cwb = nullptr;
+    float* eval_means = nullptr;                         // [rows][4]
+    float *means = nullptr, *values = nullptr, *dm = nullptr, *dls = nullptr, *dv = nullptr, *loss = nullptr;
+    float *part = nullptr, *ga = nullptr, *gc = nullptr, *col_part = nullptr, *scratch = nullptr;
+    double* norm_part = nullptr;
+    float* norm_stats = nullptr;
+    float *metric_rows = nullptr, *metric_mean = nullptr;
+};
+
+namespace {
+int lp_pack(MdnLargePPO* p) {
+    MdnSim* s = p->sim;
+    HIP_TRY(lp_launch_pack(p->actor, p->hidden, OBS, 192, p->awb, s->stream));
+    HIP_TRY(lp_launch_pack(p->critic, p->hidden, COBS, 32, p->cwb, s->stream));
+    return MDN_OK;
+}
+float* lp_param(MdnLargePPO* p, uint32_t which, uint64_t* count) {
+    const uint64_t A = p->shape.actor_count(), C = p->shape.critic_count();
+    switch (which) {
+        case 0: *count = A; return p->actor;
+        case 1: *count = C; return p->critic;
+        case 2: *count = A; return p->am;
+        case 3: *count = A; return p->av;
+        case 4: *count = C; return p->cm;
+        case 5: *count = C; return p->cv;
+        default: *count = 0; return nullptr;
+    }
+}
+}  // namespace
+
+extern "C" {
+
+void mdn_lppo_destroy(MdnLargePPO* p) {
+    if (!p) return;
+    if (p->sim) hipStreamSynchronize(p->sim->stream);
+    void* bufs[] = {p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->eval_means, p->means,
+                    p->values, p->dm, p->dls, p->dv, p->loss, p->part, p->ga, p->gc, p->col_part, p->scratch,
+                    p->norm_part, p->norm_stats, p->metric_rows, p->metric_mean};
+    for (void* b : bufs)
+        if (b) hipFree(b);
+    delete p;
+}
+
+int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t minibatch, MdnLargePPO** out) {
+    if (!s || !out) return fail(MDN_E_ARG, "mdn_lppo_create: null argument");
+    *out = nullptr;
+    if (hidden == 0 || hidden % 128) return fail(MDN_E_ARG, "mdn_lppo_create: hidden must be a positive multiple of 128");
+    if (hidden > 8192) return fail(MDN_E_ARG, "mdn_lppo_create: hidden above 8192");
+    if (epochs < 1 || epochs > 8) return fail(MDN_E_ARG, "mdn_lppo_create: epochs must be 1..8");
+    if (minibatch == 0) return fail(MDN_E_ARG, "mdn_lppo_create: minibatch must be positive");
+    MdnLargePPO* p = new MdnLargePPO();
+    p->sim = s;
+    p->hidden = hidden;
+    p->epochs = epochs;
+    p->minibatch = uint32_t(std::min<size_t>(minibatch, s->rows()));
+    p->shape.hidden = p->shape.critic_hidden = hidden;
+    p->updates = uint32_t((s->rows() + p->minibatch - 1) / p->minibatch) * epochs;
+    // row chunks of the backward: enough (hidden tile, chunk) workgroups for every CU
+    const uint32_t tiles = hidden / 128, mb_blocks = (p->minibatch + 127) / 128;
+    p->chunks = std::max(1u, std::min(mb_blocks, (256 + tiles - 1) / tiles));
+    const size_t A = p->shape.actor_count(), C = p->shape.critic_count(), M = p->minibatch, R = s->rows();
+    int rc = MDN_OK;
+    auto guard = [&](int r) { if (r != MDN_OK && rc == MDN_OK) rc = r; };
+    guard(dev_alloc(&p->actor, A));
+    guard(dev_alloc(&p->critic, C));
+    guard(dev_alloc(&p->am, A));
+    guard(dev_alloc(&p->av, A));
+    guard(dev_alloc(&p->cm, C));
+    guard(dev_alloc(&p->cv, C));
+    guard(dev_alloc(&p->awb, size_t(hidden) * 192));
+    guard(dev_alloc(&p->cwb, size_t(hidden) * 32));
+    guard(dev_alloc(&p->eval_means, R * 4));
+    guard(dev_alloc(&p->means, M * 4));
+    guard(dev_alloc(&p->values, M));
+    guard(dev_alloc(&p->dm, M * 4));
+    guard(dev_alloc(&p->dls, M * 4));
+    guard(dev_alloc(&p->dv, M));
+    guard(dev_alloc(&p->loss, M * 4));
+    guard(dev_alloc(&p->part, size_t(p->chunks) * hidden * (OBS + 1 + 4 + COBS + 1 + 1)));
+    guard(dev_alloc(&p->ga, A));
+    guard(dev_alloc(&p->gc, C));
+    guard(dev_alloc(&p->col_part, ((M + 127) / 128) * 13));
+    guard(dev_alloc(&p->scratch, 2 * 512 + 2 + 4));
+    guard(dev_alloc(&p->norm_part, (R + 255) / 256));
+    guard(dev_alloc(&p->norm_stats, 2));
+    guard(dev_alloc(&p->metric_rows, size_t(p->updates) * 4));
+    guard(dev_alloc(&p->metric_mean, 4));
+    if (rc == MDN_OK) {
+        std::vector<float> a(A), c(C);
+        mdn::init_policy(p->shape, a.data(), c.data());
+        if (hipMemcpy(p->actor, a.data(), A * 4, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(p->critic, c.data(), C * 4, hipMemcpyHostToDevice) != hipSuccess)
+            rc = fail(MDN_E_HIP, "mdn_lppo_create: policy upload");
+    }
+    if (rc == MDN_OK) rc = lp_pack(p);
+    if (rc == MDN_OK && hipStreamSynchronize(s->stream) != hipSuccess) rc = fail(MDN_E_HIP, "mdn_lppo_create: sync");
+    if (rc != MDN_OK) {
+        mdn_lppo_destroy(p);
+        return rc;
+    }
+    *out = p;
+    return MDN_OK;
+}
+
+int mdn_lppo_evaluate(MdnLargePPO* p) {
+    if (!p) return fail(MDN_E_ARG, "mdn_lppo_evaluate: null");
+    MdnSim* s = p->sim;
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    const uint32_t R = uint32_t(s->rows());
+    return timed(s, MDN_K_LP_FORWARD, [&] {
+        hipError_t e = lp_launch_forward(s->obs, s->co, p->awb, p->cwb, p->actor, p->critic, p->hidden, R,
+                                         p->eval_means, s->values, s->stream);
+        if (e == hipSuccess)
+            e = lp_launch_forward(nullptr, s->nco, p->awb, p->cwb, p->actor, p->critic, p->hidden, R, nullptr,
+                                  s->next_values, s->stream);
+        if (e == hipSuccess)
+            e = lp_launch_logp(p->eval_means, s->actions, p->actor + p->shape.actor_log_std(), R, s->logp, s->stream);
+        return e;
+    });
+}
+
+int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
+    if (!p) return fail(MDN_E_ARG, "mdn_lppo_rollout_update: null");
+    MdnSim* s = p->sim;
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    const uint32_t rows = uint32_t(s->rows());
+    rc = timed(s, MDN_K_GAE, [&] {
+        return ppo_launch_gae(s->rewards, s->values, s->next_values, s->terminated, s->truncated, s->advantages,
+                              s->returns, s->horizon, s->cfg.n, 0.99f, 0.95f, s->stream);
+    });
+    if (rc) return rc;
+    rc = timed(s, MDN_K_NORMALIZE, [&] {
+        return ppo_launch_normalize(s->advantages, rows, p->norm_part, p->norm_stats, 1.0e-8f, s->stream);
+    });
+    if (rc) return rc;
+    const std::vector<uint32_t> order = mdn::minibatch_schedule(rows, p->minibatch, p->epochs, rollout_index);
+    if (order.size() != p->updates) return fail(MDN_E_STATE, "wide PPO update count mismatch");
+    const uint32_t H = p->hidden;
+    for (size_t u = 0; u < order.size(); u++) {
+        const uint32_t begin = order[u];
+        const uint32_t b = std::min(p->minibatch, rows - begin);
+        const float* obs = s->obs + size_t(begin) * OBS;
+        const float* co = s->co + size_t(begin) * COBS;
+        rc = timed(s, MDN_K_LP_FORWARD, [&] {
+            hipError_t e = lp_launch_forward(obs, co, p->awb, p->cwb, p->actor, p->critic, H, b, p->means, p->values,
+                                             s->stream);
+            if (e == hipSuccess)
+                e = lp_launch_loss(p->means, p->values, s->actions + size_t(begin) * 4, s->logp + begin,
+                                   s->advantages + begin, s->returns + begin, p->actor + p->shape.actor_log_std(), b,
+                                   0.2f, 0.5f, s->cfg.entropy_coef, p->dm, p->dls, p->dv, p->loss, s->stream);
+            return e;
+        });
+        if (rc) return rc;
+        rc = timed(s, MDN_K_LP_BACKWARD, [&] {
+            return lp_launch_backward(obs, co, p->awb, p->cwb, p->actor, p->critic, p->dm, p->dls, p->dv, p->loss, H, b,
+                                      p->chunks, p->part, p->ga, p->gc, p->col_part, s->stream);
+        });
+        if (rc) return rc;
+        ++p->optimizer_step;
+        float c1 = 1.0f, c2 = 1.0f;
+        mdn::adam_corrections(p->optimizer_step, 0.9f, 0.999f, &c1, &c2);
+        rc = timed(s, MDN_K_LP_ADAM, [&] {
+            return lp_launch_adam(p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->ga, p->gc,
+                                  p->scratch, p->col_part, b, H, s->cfg.learning_rate, c1, c2, p->metric_rows + u * 4,
+                                  s->stream);
+        });
+        if (rc) return rc;
+    }
+    HIP_TRY(ppo_launch_metric_mean(p->metric_rows, p->metric_mean, p->updates, s->stream));
+    return MDN_OK;
+}
+
+int mdn_lppo_param_count(const MdnLargePPO* p, uint32_t which, uint64_t* count) {
+    if (!p || !count) return fail(MDN_E_ARG, "mdn_lppo_param_count: null");
+    if (!lp_param(const_cast<MdnLargePPO*>(p), which, count)) return fail(MDN_E_ARG, "mdn_lppo_param_count: bad id");
+    return MDN_OK;
+}
+
+int mdn_lppo_get_params(MdnLargePPO* p, uint32_t which, float* host, uint64_t count) {
+    if (!p || !host) return fail(MDN_E_ARG, "mdn_lppo_get_params: null");
+    uint64_t n = 0;
+    float* d = lp_param(p, which, &n);
+    if (!d) return fail(MDN_E_ARG, "mdn_lppo_get_params: bad id");
+    if (count != n) return fail(MDN_E_ARG, "mdn_lppo_get_params: count mismatch");
+    HIP_TRY(hipStreamSynchronize(p->sim->stream));
+    HIP_TRY(hipMemcpy(host, d, n * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_lppo_set_params(MdnLargePPO* p, uint32_t which, const float* host, uint64_t count) {
+    if (!p || !host) return fail(MDN_E_ARG, "mdn_lppo_set_params: null");
+    uint64_t n = 0;
+    float* d = lp_param(p, which, &n);
+    if (!d) return fail(MDN_E_ARG, "mdn_lppo_set_params: bad id");
+    if (count != n) return fail(MDN_E_ARG, "mdn_lppo_set_params: count mismatch");
+    HIP_TRY(hipStreamSynchronize(p->sim->stream));
+    HIP_TRY(hipMemcpy(d, host, n * 4, hipMemcpyHostToDevice));
+    if (which <= 1) {
+        const int rc = lp_pack(p);
+        if (rc) return rc;
+        HIP_TRY(hipStreamSynchronize(p->sim->stream));
+    }
+    return MDN_OK;
+}
+
+int mdn_lppo_metric_mean(MdnLargePPO* p, float out[4]) {
+    if (!p || !out) return fail(MDN_E_ARG, "mdn_lppo_metric_mean: null");
+    HIP_TRY(hipStreamSynchronize(p->sim->stream));
+    HIP_TRY(hipMemcpy(out, p->metric_mean, 16, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_lppo_optimizer_step(const MdnLargePPO* p, uint64_t* step) {
+    if (!p || !step) return fail(MDN_E_ARG, "mdn_lppo_optimizer_step: null");
+    *step = p->optimizer_step;
     return MDN_OK;
 }
 

@@ -23,6 +23,7 @@ struct RolloutArgs {
     const float* camera;      // unit pixel rays [320][3]
     float* obs;            // [T][N][181]
     float* co;             // [T][N][32]
+    float* nco;            // [T][N][32] critic observation of s'
     float* actions;        // [T][N][4]
     float* logp;           // [T][N]
     float* values;
@@ -85,5 +86,22 @@ hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, hipStream_t st
 hipError_t ppo_launch_adam(const ppo::AdamArgs* a, hipStream_t st);
 hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* aw, float* cw, hipStream_t st);
 hipError_t ppo_launch_metric_mean(const float* rows, float* mean, uint32_t updates, hipStream_t st);
+// wide-policy kernels (large.hip)
+hipError_t lp_launch_pack(const float* W, uint32_t H, uint32_t D, uint32_t K, __bf16* out, hipStream_t st);
+hipError_t lp_launch_forward(const float* obs, const float* co, const __bf16* awb, const __bf16* cwb,
+                             const float* actor, const float* critic, uint32_t H, uint32_t B, float* means,
+                             float* values, hipStream_t st);
+hipError_t lp_launch_logp(const float* means, const float* actions, const float* log_std, uint32_t B, float* logp,
+                          hipStream_t st);
+hipError_t lp_launch_loss(const float* means, const float* values, const float* actions, const float* old_logp,
+                          const float* adv, const float* ret, const float* log_std, uint32_t B, float clip,
+                          float vcoef, float ecoef, float* dm, float* dls, float* dv, float* loss, hipStream_t st);
+hipError_t lp_launch_backward(const float* obs, const float* co, const __bf16* awb, const __bf16* cwb,
+                              const float* actor, const float* critic, const float* dm, const float* dls,
+                              const float* dv, const float* loss, uint32_t H, uint32_t B, uint32_t chunks,
+                              float* part, float* ga, float* gc, float* col_part, hipStream_t st);
+hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
+                          __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
+                          uint32_t H, float lr, float c1, float c2, float* metric_row, hipStream_t st);
 uint32_t ppo_partial_stride();
 }

@@ -1,0 +1,522 @@
+// large.hip — PPO with a wide single hidden layer (the reference's
+// FIXED_PPO_HIDDEN_DIM, ppo.hpp:17-45, e.g. 5120 for the 967,688-parameter
+// capacity actor) on gfx950 bf16 matrix cores.
+//
+// Parameters stay fp32 in the reference's flat layout (actor: W1 [H][181],
+// b1 [H], W2 [4][H], b2 [4], log_std [4]; critic: W1 [H][32], b1 [H],
+// w2 [H], b2) with fp32 Adam moments.  The first-layer matrices are also
+// kept as bf16 copies [H][K] (inputs zero-padded to K = 192 / 32) for the
+// GEMMs, refreshed by every Adam step.  GEMMs accumulate in fp32
+// (v_mfma_f32_32x32x16_bf16); activations use a fast exp-based tanh; the
+// hidden activations are never written to HBM: the backward pass recomputes
+// each tile.  Results match the fp32 CPU oracle within bf16 tolerance, not
+// bit for bit.
+//
+// MFMA operand layout (32x32x16): A lane a holds A[a%32][8(a/32) .. +7],
+// B lane b holds B[8(b/32) .. +7][b%32], accumulator r of lane l holds
+// D[8(r/4) + 4(l/32) + r%4][l%32].
+#include <hip/hip_runtime.h>
+
+#include "mdnav_math.h"
+#include "mdnav_types.h"
+#include "kernel_args.h"
+
+namespace lp {
+using namespace mdn;
+
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t OBS = MDN_ACTOR_OBS_POOLED;
+constexpr uint32_t COBS = MDN_CRITIC_OBS;
+constexpr uint32_t KA = 192, KC = 32;  // first-layer inputs padded to whole 32-wide tiles
+constexpr uint32_t RB = 128;           // rows per block
+constexpr uint32_t UT = 128;           // hidden units per tile: four wavefronts x 32
+constexpr float LOG_TWO_PI = 1.8378770664093453f;
+
+__device__ __forceinline__ v16f mfma(bf8 a, bf8 b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ uint32_t acc_row(uint32_t l, uint32_t r) { return 8 * (r / 4) + 4 * (l / 32) + (r % 4); }
+// tanh(x) = 1 - 2 / (e^{2x} + 1) with the hardware exponential and reciprocal.
+__device__ __forceinline__ float tanh_fast(float x) { return 1.0f - __fdividef(2.0f, __expf(2.0f * x) + 1.0f); }
+
+// Rows r0 .. r0+RB of X[B][D] as bf16 [RB][XS] (row-major, K inputs, zero
+// padding) and, when `xt` is given, transposed [K][TS].  Loads are clamped
+// to valid addresses and then masked, so they issue back to back.
+template <uint32_t D, uint32_t K, uint32_t XS, uint32_t TS>
+__device__ __forceinline__ void stage_rows(const float* __restrict__ X, uint32_t r0, uint32_t rend, __bf16* xs,
+                                           __bf16* xt) {
+#pragma unroll 8
+    for (uint32_t e = threadIdx.x; e < RB * K; e += 256) {
+        const uint32_t rr = e / K, k = e % K, row = r0 + rr;
+        const bool ok = row < rend && k < D;
+        const float v = X[size_t(ok ? row : 0) * D + (k < D ? k : 0)];
+        const __bf16 b = (__bf16)(ok ? v : 0.0f);
+        xs[rr * XS + k] = b;
+        if (xt) xt[k * TS + rr] = b;
+    }
+}
+
+// ---------------------------------------------------------------- weights
+// bf16 copy [H][K] of a first-layer matrix W [H][D].
+__global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ W, uint32_t H, uint32_t D, uint32_t K,
+                                                   __bf16* __restrict__ out) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= uint64_t(H) * K) return;
+    const uint32_t u = uint32_t(i / K), k = uint32_t(i % K);
+    out[i] = (__bf16)(k < D ? W[uint64_t(u) * D + k] : 0.0f);
+}
+
+// ---------------------------------------------------------------- forward
+// out[row][q] = b2[q] + sum_u W2[q][u] tanh(b1[u] + sum_k W1[u][k] X[row][k])
+// for q < NQ (actor means: NQ = 4 over W2 [4][H]; critic value: NQ = 1).
+// A workgroup owns RB rows and walks the hidden units in tiles of UT.
+template <uint32_t D, uint32_t K, uint32_t NQ>
+__global__ __launch_bounds__(256) void forward_kernel(const float* __restrict__ X, const __bf16* __restrict__ Wb,
+                                                      const float* __restrict__ b1, const float* __restrict__ W2,
+                                                      const float* __restrict__ b2, uint32_t H, uint32_t B,
+                                                      float* __restrict__ out) {
+    constexpr uint32_t XS = K + 8, HS = UT + 1;
+    __shared__ __bf16 xs[RB * XS];
+    __shared__ float hs[RB * HS];
+    __shared__ float w2s[NQ * UT];
+    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
+    const uint32_t r0 = blockIdx.x * RB;
+    stage_rows<D, K, XS, 1>(X, r0, B, xs, nullptr);
+    // second layer: NQ = 4: thread t -> row t/2, outputs 2(t%2), 2(t%2)+1; NQ = 1: thread t < RB -> row t
+    const uint32_t srow = NQ == 4 ? t / 2 : t, q0 = NQ == 4 ? 2 * (t % 2) : 0;
+    float z0 = 0.0f, z1 = 0.0f;
+    for (uint32_t u0 = 0; u0 < H; u0 += UT) {
+        const uint32_t unit = u0 + 32 * wv + l % 32;
+        const float bias = b1[unit];
+        v16f acc[4];
+#pragma unroll
+        for (uint32_t rt = 0; rt < 4; rt++)
+#pragma unroll
+            for (uint32_t r = 0; r < 16; r++) acc[rt][r] = bias;
+        __syncthreads();  // rows staged; the previous tile's hs/w2s consumed
+#pragma unroll
+        for (uint32_t ks = 0; ks < K / 16; ks++) {
+            const uint32_t kb = 16 * ks + 8 * (l / 32);
+            const bf8 bv = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + kb);
+#pragma unroll
+            for (uint32_t rt = 0; rt < 4; rt++) {
+                const bf8 av = *reinterpret_cast<const bf8*>(xs + (32 * rt + l % 32) * XS + kb);
+                acc[rt] = mfma(av, bv, acc[rt]);
+            }
+        }
+#pragma unroll
+        for (uint32_t rt = 0; rt < 4; rt++)
+#pragma unroll
+            for (uint32_t r = 0; r < 16; r++)
+                hs[(32 * rt + acc_row(l, r)) * HS + 32 * wv + l % 32] = tanh_fast(acc[rt][r]);
+        for (uint32_t i = t; i < NQ * UT; i += 256) w2s[i] = W2[size_t(i / UT) * H + u0 + i % UT];
+        __syncthreads();
+        if (NQ == 4 || t < RB) {
+            const float* hr = hs + srow * HS;
+#pragma unroll 8
+            for (uint32_t c = 0; c < UT; c++) {
+                const float h = hr[c];
+                z0 = fma_f(w2s[q0 * UT + c], h, z0);
+                if (NQ == 4) z1 = fma_f(w2s[(q0 + 1) * UT + c], h, z1);
+            }
+        }
+    }
+    const uint32_t row = r0 + srow;
+    if ((NQ == 4 || t < RB) && row < B) {
+        out[size_t(row) * NQ + q0] = b2[q0] + z0;
+        if (NQ == 4) out[size_t(row) * NQ + q0 + 1] = b2[q0 + 1] + z1;
+    }
+}
+
+// ---------------------------------------------------------------- loss
+// sample_loss_and_grad (ppo.hpp:144-181) per minibatch row from the means and
+// values of the forward kernels.  Writes dmean[4], dlog_std[4], dvalue and the
+// four loss terms.
+__global__ __launch_bounds__(256) void loss_kernel(const float* __restrict__ mean, const float* __restrict__ value,
+                                                   const float* __restrict__ actions, const float* __restrict__ old_logp,
+                                                   const float* __restrict__ adv, const float* __restrict__ ret,
+                                                   const float* __restrict__ log_std, uint32_t B, float clip,
+                                                   float vcoef, float ecoef, float* __restrict__ dm,
+                                                   float* __restrict__ dls, float* __restrict__ dv,
+                                                   float* __restrict__ loss) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= B) return;
+    const float* act = actions + size_t(n) * 4;
+    const float* mu = mean + size_t(n) * 4;
+    const float scale = 1.0f / max_f(float(B), 1.0f);
+    float logp = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        const float d = (act[q] - mu[q]) * exp_f(-log_std[q]);
+        logp += -0.5f * (d * d + 2.0f * log_std[q] + LOG_TWO_PI);
+    }
+    const float raw = logp - old_logp[n];
+    const float ratio = exp_f(clamp_f(raw, -20.0f, 20.0f));
+    const float a = adv[n], target = ret[n], v = value[n];
+    const float clipped = clamp_f(ratio, 1.0f - clip, 1.0f + clip);
+    const float chosen = min_f(ratio * a, clipped * a);
+    const bool in_range = raw >= -20.0f && raw <= 20.0f;
+    const bool active = in_range && (a >= 0.0f ? ratio <= 1.0f + clip : ratio >= 1.0f - clip);
+    float entropy = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        const float inv_var = exp_f(-2.0f * log_std[q]);
+        const float diff = act[q] - mu[q];
+        float g = 0.0f, gl = 0.0f;
+        if (active) {
+            const float dlogp = -ratio * a * scale;
+            g = dlogp * diff * inv_var;
+            gl = dlogp * (diff * diff * inv_var - 1.0f);
+        }
+        gl -= ecoef * scale;
+        entropy += -ecoef * (log_std[q] + 0.5f * (1.0f + LOG_TWO_PI)) * scale;
+        dm[size_t(n) * 4 + q] = g;
+        dls[size_t(n) * 4 + q] = gl;
+    }
+    dv[n] = vcoef * (v - target) * scale;
+    float* lo = loss + size_t(n) * 4;
+    lo[0] = -chosen * scale;
+    lo[1] = 0.5f * vcoef * (v - target) * (v - target) * scale;
+    lo[2] = entropy;
+    lo[3] = ratio;
+}
+
+// gaussian_log_prob (ppo.hpp:95-103) of the stored actions under the means.
+__global__ __launch_bounds__(256) void logp_kernel(const float* __restrict__ mean, const float* __restrict__ actions,
+                                                   const float* __restrict__ log_std, uint32_t B,
+                                                   float* __restrict__ logp) {
+    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= B) return;
+    float lp = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        const float d = (actions[size_t(n) * 4 + q] - mean[size_t(n) * 4 + q]) * exp_f(-log_std[q]);
+        lp += -0.5f * (d * d + 2.0f * log_std[q] + LOG_TWO_PI);
+    }
+    logp[n] = lp;
+}
+
+// ---------------------------------------------------------------- backward
+// Partial gradients of one (hidden tile, row chunk): the tile's hidden values
+// are recomputed from the rows, delta = (sum_q dm[row][q] W2[q][u]) (1 - h^2),
+// then dW1[u][k] += sum_rows delta[row][u] X[row][k] on the matrix cores (the
+// rows are the reduction dimension), db1[u] += sum delta, dW2[q][u] +=
+// sum dm[row][q] h[row][u].  Output: partial slot `c = blockIdx.y` of
+// dW1p [c][H][D], db1p [c][H], dW2p [c][NQ][H].
+template <uint32_t D, uint32_t K, uint32_t NQ>
+__global__ __launch_bounds__(256) void backward_kernel(const float* __restrict__ X, const __bf16* __restrict__ Wb,
+                                                       const float* __restrict__ b1, const float* __restrict__ W2,
+                                                       const float* __restrict__ dm, uint32_t H, uint32_t B,
+                                                       uint32_t RC, float* __restrict__ dW1p,
+                                                       float* __restrict__ db1p, float* __restrict__ dW2p) {
+    constexpr uint32_t XS = K + 8, TS = RB + 8;
+    __shared__ __bf16 xs[RB * XS];   // [row][k]
+    __shared__ __bf16 xt[K * TS];    // [k][row]
+    __shared__ __bf16 dt[UT * TS];   // delta^T [unit][row]
+    __shared__ float dms[RB * NQ];
+    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
+    const uint32_t u0 = blockIdx.x * UT, c = blockIdx.y;
+    const uint32_t unit = u0 + 32 * wv + l % 32;
+    const uint32_t rbeg = c * RC, rend = min(B, rbeg + RC);
+    float w2r[NQ];
+#pragma unroll
+    for (uint32_t q = 0; q < NQ; q++) w2r[q] = W2[size_t(q) * H + unit];
+    const float bias = b1[unit];
+    v16f gacc[K / 32];
+#pragma unroll
+    for (uint32_t jt = 0; jt < K / 32; jt++)
+#pragma unroll
+        for (uint32_t r = 0; r < 16; r++) gacc[jt][r] = 0.0f;
+    float db1a = 0.0f, dw2a[NQ];
+#pragma unroll
+    for (uint32_t q = 0; q < NQ; q++) dw2a[q] = 0.0f;
+    for (uint32_t r0 = rbeg; r0 < rend; r0 += RB) {
+        __syncthreads();  // the previous block's LDS reads are done
+        stage_rows<D, K, XS, TS>(X, r0, rend, xs, xt);
+        for (uint32_t e = t; e < RB * NQ; e += 256) {
+            const uint32_t row = r0 + e / NQ;
+            dms[e] = row < rend ? dm[size_t(row) * NQ + e % NQ] : 0.0f;
+        }
+        __syncthreads();
+        v16f acc[4];
+#pragma unroll
+        for (uint32_t rt = 0; rt < 4; rt++)
+#pragma unroll
+            for (uint32_t r = 0; r < 16; r++) acc[rt][r] = bias;
+#pragma unroll
+        for (uint32_t ks = 0; ks < K / 16; ks++) {
+            const uint32_t kb = 16 * ks + 8 * (l / 32);
+            const bf8 bv = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + kb);
+#pragma unroll
+            for (uint32_t rt = 0; rt < 4; rt++) {
+                const bf8 av = *reinterpret_cast<const bf8*>(xs + (32 * rt + l % 32) * XS + kb);
+                acc[rt] = mfma(av, bv, acc[rt]);
+            }
+        }
+#pragma unroll
+        for (uint32_t rt = 0; rt < 4; rt++)
+#pragma unroll
+            for (uint32_t r = 0; r < 16; r++) {
+                const uint32_t rr = 32 * rt + acc_row(l, r);
+                const float h = tanh_fast(acc[rt][r]);
+                float g = 0.0f;
+#pragma unroll
+                for (uint32_t q = 0; q < NQ; q++) {
+                    const float d = dms[rr * NQ + q];
+                    g = fma_f(d, w2r[q], g);
+                    dw2a[q] = fma_f(d, h, dw2a[q]);
+                }
+                const float delta = g * (1.0f - h * h);
+                db1a += delta;
+                dt[(32 * wv + l % 32) * TS + rr] = (__bf16)delta;
+            }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t ks = 0; ks < RB / 16; ks++) {
+            const uint32_t kb = 16 * ks + 8 * (l / 32);
+            const bf8 av = *reinterpret_cast<const bf8*>(dt + (32 * wv + l % 32) * TS + kb);
+#pragma unroll
+            for (uint32_t jt = 0; jt < K / 32; jt++) {
+                const bf8 bv = *reinterpret_cast<const bf8*>(xt + (32 * jt + l % 32) * TS + kb);
+                gacc[jt] = mfma(av, bv, gacc[jt]);
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t jt = 0; jt < K / 32; jt++) {
+        const uint32_t j = 32 * jt + l % 32;
+        if (j < D)
+#pragma unroll
+            for (uint32_t r = 0; r < 16; r++)
+                dW1p[(size_t(c) * H + u0 + 32 * wv + acc_row(l, r)) * D + j] = gacc[jt][r];
+    }
+    // lanes l and l + 32 hold the same unit
+    db1a += __shfl_xor(db1a, 32, 64);
+#pragma unroll
+    for (uint32_t q = 0; q < NQ; q++) dw2a[q] += __shfl_xor(dw2a[q], 32, 64);
+    if (l < 32) {
+        db1p[size_t(c) * H + unit] = db1a;
+#pragma unroll
+        for (uint32_t q = 0; q < NQ; q++) dW2p[(size_t(c) * NQ + q) * H + unit] = dw2a[q];
+    }
+}
+
+// ---------------------------------------------------------------- reductions
+// grad[i] = sum over the `chunks` partial slots (slot-major, stride n).
+__global__ __launch_bounds__(256) void sum_slots_kernel(const float* __restrict__ part, uint64_t n, uint32_t chunks,
+                                                        float* __restrict__ grad) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    float s = 0.0f;
+    for (uint32_t c = 0; c < chunks; c++) s += part[uint64_t(c) * n + i];
+    grad[i] = s;
+}
+// Column sums over the minibatch rows of the 13 per-row terms (dm[4] -> b2,
+// dls[4] -> log_std, dv -> critic b2, loss[4] -> metrics): block b sums rows
+// b*RB .. into part[b][13]; column_finish_kernel adds the blocks in order.
+__global__ __launch_bounds__(256) void column_part_kernel(const float* __restrict__ dm, const float* __restrict__ dls,
+                                                          const float* __restrict__ dv, const float* __restrict__ loss,
+                                                          uint32_t B, float* __restrict__ part) {
+    __shared__ float s[13][RB + 1];
+    const uint32_t t = threadIdx.x, r0 = blockIdx.x * RB;
+    for (uint32_t e = t; e < 13 * RB; e += 256) {
+        const uint32_t col = e / RB, rr = e % RB, row = r0 + rr;
+        float v = 0.0f;
+        if (row < B) v = col < 4 ? dm[size_t(row) * 4 + col] : col < 8 ? dls[size_t(row) * 4 + col - 4]
+                         : col == 8 ? dv[row] : loss[size_t(row) * 4 + col - 9];
+        s[col][rr] = v;
+    }
+    __syncthreads();
+    if (t < 13) {
+        float a = 0.0f;
+        for (uint32_t rr = 0; rr < RB; rr++) a += s[t][rr];
+        part[size_t(blockIdx.x) * 13 + t] = a;
+    }
+}
+
+// Adds the column partials in block order and writes the per-row-column
+// gradients into the flat vectors (actor b2, log_std; critic b2) and the four
+// metric sums into metric_sums.
+__global__ void column_finish_kernel(const float* __restrict__ col_part, uint32_t blocks, uint32_t H,
+                                     float* __restrict__ ga, float* __restrict__ gc, float* __restrict__ metric_sums) {
+    const uint32_t t = threadIdx.x;
+    if (t >= 13) return;
+    float s = 0.0f;
+    for (uint32_t b = 0; b < blocks; b++) s += col_part[size_t(b) * 13 + t];
+    const uint32_t A_B2 = H * OBS + H + 4 * H, A_LS = A_B2 + 4, C_B2 = H * COBS + 2 * H;
+    if (t < 4) ga[A_B2 + t] = s;
+    else if (t < 8) ga[A_LS + t - 4] = s;
+    else if (t == 8) gc[C_B2] = s;
+    else metric_sums[t - 9] = s;
+}
+
+constexpr uint32_t NP = 512;  // squared-norm partial slots per network
+
+// Per-network squared-norm partials: slot s of net k sums g[i]^2 for i = s,
+// s + NP, ... (both networks in one grid: blockIdx.y = net).
+__global__ __launch_bounds__(256) void sqnorm_kernel(const float* __restrict__ ga, const float* __restrict__ gc,
+                                                     uint32_t PA, uint32_t PC, float* __restrict__ part) {
+    const uint32_t s = blockIdx.x * 256 + threadIdx.x;
+    if (s >= NP) return;
+    const bool critic = blockIdx.y == 1;
+    const float* g = critic ? gc : ga;
+    const uint32_t P = critic ? PC : PA;
+    float a = 0.0f;
+    for (uint32_t i = s; i < P; i += NP) a += g[i] * g[i];
+    part[blockIdx.y * NP + s] = a;
+}
+// Clip scales min(1, 0.5 / ||g||) of both networks (partials added in slot
+// order) and the update's metric row.
+__global__ void norm_finish_kernel(const float* __restrict__ part, const float* __restrict__ metric_sums, uint32_t b,
+                                   float* __restrict__ scale, float* __restrict__ metric_row) {
+    const uint32_t t = threadIdx.x;
+    if (t < 2) {
+        float s = 0.0f;
+        for (uint32_t i = 0; i < NP; i++) s += part[t * NP + i];
+        scale[t] = min_f(1.0f, 0.5f / sqrt_f(s + 1.0e-20f));
+    } else if (t < 6) {
+        metric_row[t - 2] = t == 5 ? metric_sums[3] / float(b) : metric_sums[t - 2];
+    }
+}
+
+struct LargeAdamArgs {
+    float* actor; float* critic;
+    float* am; float* av; float* cm; float* cv;
+    __bf16* actor_wb; __bf16* critic_wb;
+    const float* ga; const float* gc;   // gradients in the flat layouts
+    const float* scale;                 // [2] clip scales
+    uint32_t H, PA, PC;
+    float lr, c1, c2;
+};
+
+// cpu_reference.hpp:553-567 per element: clipped gradient, Adam (0.9, 0.999,
+// 1e-8) with host bias corrections, log-std clamp (603), bf16 refresh of the
+// first-layer copies.
+__global__ __launch_bounds__(256) void adam_kernel(LargeAdamArgs a) {
+    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= uint64_t(a.PA) + a.PC) return;
+    const bool critic = i >= a.PA;
+    const uint32_t p = uint32_t(critic ? i - a.PA : i);
+    const uint32_t A_B1 = a.H * OBS, A_LS = A_B1 + a.H + 4 * a.H + 4, C_B1 = a.H * COBS;
+    const float gi = (critic ? a.gc[p] : a.ga[p]) * a.scale[critic ? 1 : 0];
+    float* params = critic ? a.critic : a.actor;
+    float* m = critic ? a.cm : a.am;
+    float* v = critic ? a.cv : a.av;
+    const float mi = 0.9f * m[p] + (1.0f - 0.9f) * gi;
+    const float vi = 0.999f * v[p] + (1.0f - 0.999f) * gi * gi;
+    m[p] = mi;
+    v[p] = vi;
+    float w = params[p] - a.lr * (mi / a.c1) / (sqrt_f(vi / a.c2) + 1.0e-8f);
+    if (!critic && p >= A_LS) w = clamp_f(w, -2.0f, 0.5f);
+    params[p] = w;
+    if (!critic && p < A_B1) a.actor_wb[size_t(p / OBS) * KA + p % OBS] = (__bf16)w;
+    if (critic && p < C_B1) a.critic_wb[size_t(p / COBS) * KC + p % COBS] = (__bf16)w;
+}
+
+}  // namespace lp
+
+// ---------------------------------------------------------------- launchers
+extern "C" {
+
+hipError_t lp_launch_pack(const float* W, uint32_t H, uint32_t D, uint32_t K, __bf16* out, hipStream_t st) {
+    const uint64_t n = uint64_t(H) * K;
+    hipLaunchKernelGGL(lp::pack_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, W, H, D, K, out);
+    return hipGetLastError();
+}
+
+// Actor means [B][4] and critic values [B] of B rows.
+hipError_t lp_launch_forward(const float* obs, const float* co, const __bf16* awb, const __bf16* cwb,
+                             const float* actor, const float* critic, uint32_t H, uint32_t B, float* means,
+                             float* values, hipStream_t st) {
+    if (B == 0) return hipSuccess;
+    const dim3 grid((B + lp::RB - 1) / lp::RB);
+    const uint32_t A_B1 = H * lp::OBS, A_W2 = A_B1 + H, A_B2 = A_W2 + 4 * H;
+    const uint32_t C_B1 = H * lp::COBS, C_W2 = C_B1 + H, C_B2 = C_W2 + H;
+    if (means)
+        hipLaunchKernelGGL((lp::forward_kernel<lp::OBS, lp::KA, 4>), grid, dim3(256), 0, st, obs, awb, actor + A_B1,
+                           actor + A_W2, actor + A_B2, H, B, means);
+    if (values)
+        hipLaunchKernelGGL((lp::forward_kernel<lp::COBS, lp::KC, 1>), grid, dim3(256), 0, st, co, cwb, critic + C_B1,
+                           critic + C_W2, critic + C_B2, H, B, values);
+    return hipGetLastError();
+}
+
+hipError_t lp_launch_logp(const float* means, const float* actions, const float* log_std, uint32_t B, float* logp,
+                          hipStream_t st) {
+    if (B == 0) return hipSuccess;
+    hipLaunchKernelGGL(lp::logp_kernel, dim3((B + 255) / 256), dim3(256), 0, st, means, actions, log_std, B, logp);
+    return hipGetLastError();
+}
+
+hipError_t lp_launch_loss(const float* means, const float* values, const float* actions, const float* old_logp,
+                          const float* adv, const float* ret, const float* log_std, uint32_t B, float clip,
+                          float vcoef, float ecoef, float* dm, float* dls, float* dv, float* loss, hipStream_t st) {
+    if (B == 0) return hipSuccess;
+    hipLaunchKernelGGL(lp::loss_kernel, dim3((B + 255) / 256), dim3(256), 0, st, means, values, actions, old_logp, adv,
+                       ret, log_std, B, clip, vcoef, ecoef, dm, dls, dv, loss);
+    return hipGetLastError();
+}
+
+// Backward of both networks into the partial slots, then the slot sums into
+// the flat gradients ga (actor layout) and gc (critic layout) and the
+// per-row column partials.  Scratch: part >= chunks * (H*(181+1+4) +
+// H*(32+1+1)) floats, col_part >= ceil(B/128) * 13.
+hipError_t lp_launch_backward(const float* obs, const float* co, const __bf16* awb, const __bf16* cwb,
+                              const float* actor, const float* critic, const float* dm, const float* dls,
+                              const float* dv, const float* loss, uint32_t H, uint32_t B, uint32_t chunks,
+                              float* part, float* ga, float* gc, float* col_part, hipStream_t st) {
+    if (B == 0) return hipSuccess;
+    const uint32_t RC = ((B + chunks - 1) / chunks + lp::RB - 1) / lp::RB * lp::RB;
+    const uint32_t nc = (B + RC - 1) / RC;
+    const uint32_t A_B1 = H * lp::OBS, A_W2 = A_B1 + H;
+    const uint32_t C_B1 = H * lp::COBS, C_W2 = C_B1 + H;
+    // partial slot layout: actor [nc][H*181], [nc][H], [nc][4][H]; critic [nc][H*32], [nc][H], [nc][1][H]
+    float* aW1 = part;
+    float* ab1 = aW1 + size_t(nc) * H * lp::OBS;
+    float* aW2 = ab1 + size_t(nc) * H;
+    float* cW1 = aW2 + size_t(nc) * 4 * H;
+    float* cb1 = cW1 + size_t(nc) * H * lp::COBS;
+    float* cw2 = cb1 + size_t(nc) * H;
+    const dim3 grid(H / lp::UT, nc);
+    hipLaunchKernelGGL((lp::backward_kernel<lp::OBS, lp::KA, 4>), grid, dim3(256), 0, st, obs, awb, actor + A_B1,
+                       actor + A_W2, dm, H, B, RC, aW1, ab1, aW2);
+    hipLaunchKernelGGL((lp::backward_kernel<lp::COBS, lp::KC, 1>), grid, dim3(256), 0, st, co, cwb, critic + C_B1,
+                       critic + C_W2, dv, H, B, RC, cW1, cb1, cw2);
+    auto sum = [&](const float* p, uint64_t n, float* out) {
+        hipLaunchKernelGGL(lp::sum_slots_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, p, n, nc, out);
+    };
+    sum(aW1, uint64_t(H) * lp::OBS, ga);
+    sum(ab1, H, ga + A_B1);
+    sum(aW2, 4ull * H, ga + A_W2);
+    sum(cW1, uint64_t(H) * lp::COBS, gc);
+    sum(cb1, H, gc + C_B1);
+    sum(cw2, H, gc + C_W2);
+    hipLaunchKernelGGL(lp::column_part_kernel, dim3((B + lp::RB - 1) / lp::RB), dim3(256), 0, st, dm, dls, dv, loss, B,
+                       col_part);
+    return hipGetLastError();
+}
+
+// Clip + Adam of both networks.  scratch >= 2 * 512 + 2 + 4 floats;
+// col_part as written by lp_launch_backward.
+hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
+                          __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
+                          uint32_t H, float lr, float c1, float c2, float* metric_row, hipStream_t st) {
+    const uint32_t PA = H * lp::OBS + H + 4 * H + 8, PC = H * lp::COBS + 2 * H + 1;
+    float* norm_part = scratch;
+    float* scale = scratch + 2 * lp::NP;
+    float* metric_sums = scale + 2;
+    hipLaunchKernelGGL(lp::column_finish_kernel, dim3(1), dim3(64), 0, st, col_part, (B + lp::RB - 1) / lp::RB, H, ga,
+                       gc, metric_sums);
+    hipLaunchKernelGGL(lp::sqnorm_kernel, dim3((lp::NP + 255) / 256, 2), dim3(256), 0, st, ga, gc, PA, PC, norm_part);
+    hipLaunchKernelGGL(lp::norm_finish_kernel, dim3(1), dim3(64), 0, st, norm_part, metric_sums, B, scale, metric_row);
+    lp::LargeAdamArgs a;
+    a.actor = actor; a.critic = critic; a.am = am; a.av = av; a.cm = cm; a.cv = cv;
+    a.actor_wb = awb; a.critic_wb = cwb; a.ga = ga; a.gc = gc; a.scale = scale;
+    a.H = H; a.PA = PA; a.PC = PC; a.lr = lr; a.c1 = c1; a.c2 = c2;
+    hipLaunchKernelGGL(lp::adam_kernel, dim3((PA + PC + 255) / 256), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // extern "C"

@@ -794,9 +794,10 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                     cob[22 + j * 3] = (cc.y - s.p[1]) / 10.0f;
                     cob[23 + j * 3] = (cc.z - s.p[2]) / 10.0f;
                 }
+            float* ncg = a.nco + row * COBS;
 #pragma unroll
             for (int j = 0; j < 32; j++)
-                if (j % G == int(lane)) s_co[grp][j] = cob[j];
+                if (j % G == int(lane)) { s_co[grp][j] = cob[j]; ncg[j] = cob[j]; }
             if (success || collision || timeout) {  // sim.metal:328-331
                 r.successes += success;
                 r.collisions += collision;

@@ -10,6 +10,6 @@ it is missing.
 """
 from . import abi  # noqa: F401
 from .native import MdnError  # noqa: F401
-from .sim import PPOTrainer, Sim, Trainer, crazyflie_params, load_raptor  # noqa: F401
+from .sim import LargePPOTrainer, PPOTrainer, Sim, Trainer, crazyflie_params, load_raptor  # noqa: F401
 
 __all__ = ["abi", "MdnError", "Sim", "PPOTrainer", "Trainer", "crazyflie_params", "load_raptor"]

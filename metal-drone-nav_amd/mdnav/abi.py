@@ -116,4 +116,5 @@ BUFFERS = {
     "terminated": (15, np.uint8), "truncated": (16, np.uint8), "advantages": (17, np.float32),
     "returns": (18, np.float32), "actor_m": (19, np.float32), "actor_v": (20, np.float32),
     "critic_m": (21, np.float32), "critic_v": (22, np.float32), "metric_rows": (23, np.float32),
+    "next_critic_obs": (24, np.float32),
 }

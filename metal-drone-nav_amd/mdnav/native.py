@@ -19,12 +19,15 @@ EXPORTS = [
     "mdn_ppo_rollout_update", "mdn_ppo_gae", "mdn_ppo_normalize", "mdn_ppo_update",
     "mdn_ppo_metric_mean", "mdn_ppo_optimizer_step", "mdn_ppo_updates_per_rollout",
     "mdn_op_physics_step", "mdn_op_raptor_sequence", "mdn_op_ray_world", "mdn_op_clearance",
-    "mdn_op_gae", "mdn_op_normalize",
+    "mdn_op_gae", "mdn_op_normalize", "mdn_lppo_create", "mdn_lppo_destroy", "mdn_lppo_evaluate",
+    "mdn_lppo_rollout_update", "mdn_lppo_param_count", "mdn_lppo_get_params", "mdn_lppo_set_params",
+    "mdn_lppo_metric_mean", "mdn_lppo_optimizer_step",
 ]
 
 P = ctypes.c_void_p
 U32, U64, F32, I32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_int
-KERNELS = {"rollout": 0, "gae": 1, "normalize": 2, "rows": 3, "grads": 4, "adam": 5}
+KERNELS = {"rollout": 0, "gae": 1, "normalize": 2, "rows": 3, "grads": 4, "adam": 5, "lp_forward": 6,
+           "lp_backward": 7, "lp_adam": 8}
 
 _lib = None
 
@@ -70,6 +73,15 @@ def lib():
         _sig(L, "mdn_ppo_metric_mean", I32, P, P)
         _sig(L, "mdn_ppo_optimizer_step", I32, P, ctypes.POINTER(U64))
         _sig(L, "mdn_ppo_updates_per_rollout", I32, P, ctypes.POINTER(U32))
+        _sig(L, "mdn_lppo_create", I32, P, U32, U32, U32, ctypes.POINTER(P))
+        _sig(L, "mdn_lppo_destroy", None, P)
+        _sig(L, "mdn_lppo_evaluate", I32, P)
+        _sig(L, "mdn_lppo_rollout_update", I32, P, U32)
+        _sig(L, "mdn_lppo_param_count", I32, P, U32, ctypes.POINTER(U64))
+        _sig(L, "mdn_lppo_get_params", I32, P, U32, P, U64)
+        _sig(L, "mdn_lppo_set_params", I32, P, U32, P, U64)
+        _sig(L, "mdn_lppo_metric_mean", I32, P, P)
+        _sig(L, "mdn_lppo_optimizer_step", I32, P, ctypes.POINTER(U64))
         _sig(L, "mdn_op_physics_step", I32, P, P, P, P, P, U64)
         _sig(L, "mdn_op_raptor_sequence", I32, P, P, U32, U32, P, P)
         _sig(L, "mdn_op_ray_world", I32, P, P, P, U32, P, U64)

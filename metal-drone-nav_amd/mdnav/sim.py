@@ -19,7 +19,7 @@ import time
 import numpy as np
 
 from . import abi
-from .native import KERNELS, MdnError, check, contiguous, lib, ptr
+from .native import KERNELS, MdnError, P, check, contiguous, lib, ptr
 
 ASSETS = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "assets")
 
@@ -205,6 +205,60 @@ class PPOTrainer:
         u = ctypes.c_uint32()
         check(lib().mdn_ppo_updates_per_rollout(self.h, ctypes.byref(u)))
         return u.value
+
+
+class LargePPOTrainer:
+    """PPO with the hidden width raised to `hidden` (ppo.hpp FIXED_PPO_HIDDEN_DIM;
+    5120 gives the reference's capacity actor): bf16 matrix-core GEMMs with
+    fp32 master weights and Adam, on the rollout buffers of `sim`."""
+
+    PARAMS = {"actor": 0, "critic": 1, "actor_m": 2, "actor_v": 3, "critic_m": 4, "critic_v": 5}
+
+    def __init__(self, sim, hidden=5120, epochs=4, minibatch=32768):
+        self.sim = sim
+        self.hidden = hidden
+        h = P()
+        check(lib().mdn_lppo_create(sim.h, hidden, epochs, minibatch, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().mdn_lppo_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def evaluate(self):
+        """logp of the stored actions and values at s and s' under this policy."""
+        check(lib().mdn_lppo_evaluate(self.h))
+
+    def rollout_update(self, rollout_index):
+        check(lib().mdn_lppo_rollout_update(self.h, rollout_index))
+
+    def get(self, name):
+        which = self.PARAMS[name]
+        n = ctypes.c_uint64()
+        check(lib().mdn_lppo_param_count(self.h, which, ctypes.byref(n)))
+        out = np.zeros(n.value, np.float32)
+        check(lib().mdn_lppo_get_params(self.h, which, ptr(out), n.value))
+        return out
+
+    def set(self, name, values):
+        which = self.PARAMS[name]
+        v = contiguous(values, np.float32)
+        check(lib().mdn_lppo_set_params(self.h, which, ptr(v), v.size))
+
+    def metric_mean(self):
+        out = np.zeros(4, np.float32)
+        check(lib().mdn_lppo_metric_mean(self.h, ptr(out)))
+        return out
+
+    @property
+    def optimizer_step(self):
+        s = ctypes.c_uint64()
+        check(lib().mdn_lppo_optimizer_step(self.h, ctypes.byref(s)))
+        return s.value
 
 
 class Trainer:

@@ -227,7 +227,7 @@ struct Trainer {
     std::vector<MdnSimRun> runs;
     std::vector<MdnWorld> worlds;
     std::vector<float> sensors, poses, commands;
-    std::vector<float> obs, co, actions, logp, values, rewards, next_values, advantages, returns;
+    std::vector<float> obs, co, nco, actions, logp, values, rewards, next_values, advantages, returns;
     std::vector<uint8_t> terminated, truncated;
     std::vector<float> metric_rows;
     float metric_mean[4] = {0, 0, 0, 0};
@@ -250,6 +250,7 @@ struct Trainer {
         poses.assign(n * MDN_SENSOR_FRAMES * 12, 0.0f);
         commands.assign(n * MDN_SENSOR_FRAMES * MDN_ACTIONS, 0.0f);
         obs.assign(rows * shape.obs, 0.0f); co.assign(rows * shape.critic_obs, 0.0f);
+        nco.assign(rows * shape.critic_obs, 0.0f);
         actions.assign(rows * MDN_ACTIONS, 0.0f); logp.assign(rows, 0.0f); values.assign(rows, 0.0f);
         rewards.assign(rows, 0.0f); next_values.assign(rows, 0.0f); advantages.assign(rows, 0.0f);
         returns.assign(rows, 0.0f); terminated.assign(rows, 0); truncated.assign(rows, 0);
@@ -529,7 +530,8 @@ struct Trainer {
                        (success ? 10.0f : 0.0f) - (collision ? 10.0f : 0.0f);
         terminated[row] = uint8_t(collision || success);
         truncated[row] = uint8_t(timeout && !terminated[row]);
-        float cobs[MDN_CRITIC_OBS], hidden[8192];
+        float hidden[8192];
+        float* cobs = &nco[row * shape.critic_obs];
         critic_observation(s, world, run, cobs);
         next_values[row] = critic_forward(shape, critic.data(), cobs, hidden);
         if (success || collision || timeout) {
@@ -708,6 +710,33 @@ struct Trainer {
             for (int k = 0; k < 4; k++) metric_mean[k] /= float(order.size());
     }
 
+    // A policy of hidden width h (ppo.hpp:17-45 FIXED_PPO_HIDDEN_DIM) in
+    // place of the current one: fresh initialisation, zero Adam moments.
+    void set_hidden(uint32_t h) {
+        shape.hidden = shape.critic_hidden = h;
+        actor.assign(shape.actor_count(), 0.0f);
+        critic.assign(shape.critic_count(), 0.0f);
+        init_policy(shape, actor.data(), critic.data());
+        actor_m.assign(actor.size(), 0.0f); actor_v.assign(actor.size(), 0.0f);
+        critic_m.assign(critic.size(), 0.0f); critic_v.assign(critic.size(), 0.0f);
+        optimizer_step = 0;
+    }
+    // Log-probabilities of the stored actions and values at s and s' under the
+    // current policy for every rollout row (the rollout's act and next-value
+    // outputs re-evaluated with this policy).
+    void evaluate() {
+        const int64_t rows = int64_t(cfg.n) * horizon;
+        const float* log_std = &actor[shape.actor_log_std()];
+#pragma omp parallel for schedule(static)
+        for (int64_t row = 0; row < rows; row++) {
+            float hidden[8192], mean[4];
+            actor_forward(shape, actor.data(), &obs[size_t(row) * shape.obs], hidden, mean);
+            logp[row] = gaussian_log_prob(&actions[size_t(row) * 4], mean, log_std);
+            values[row] = critic_forward(shape, critic.data(), &co[size_t(row) * shape.critic_obs], hidden);
+            next_values[row] = critic_forward(shape, critic.data(), &nco[size_t(row) * shape.critic_obs], hidden);
+        }
+    }
+
     void iteration(uint32_t rollout_index) {
         collect(horizon);
         gae();
@@ -742,6 +771,8 @@ void orc_trainer_minibatch_grads(void* h, uint32_t begin, uint32_t b, float* act
     std::copy(cg.begin(), cg.end(), critic_grad);
 }
 void orc_trainer_set_config(void* h, const MdnSimConfig* cfg) { static_cast<Trainer*>(h)->cfg = *cfg; }
+void orc_trainer_set_hidden(void* h, uint32_t hidden) { static_cast<Trainer*>(h)->set_hidden(hidden); }
+void orc_trainer_evaluate(void* h) { static_cast<Trainer*>(h)->evaluate(); }
 uint64_t orc_trainer_optimizer_step(void* h) { return static_cast<Trainer*>(h)->optimizer_step; }
 void orc_trainer_metric_mean(void* h, float* out) {
     for (int k = 0; k < 4; k++) out[k] = static_cast<Trainer*>(h)->metric_mean[k];
@@ -779,6 +810,7 @@ void* orc_trainer_buffer(void* hp, uint32_t id, uint64_t* bytes) {
         case 21: return ret(t->critic_m);
         case 22: return ret(t->critic_v);
         case 23: return ret(t->metric_rows);
+        case 24: return ret(t->nco);
         default: *bytes = 0; return nullptr;
     }
 }

@@ -5,7 +5,7 @@ from mdnav import Sim, PPOTrainer, abi
 from oracle_lib import OracleTrainer, raptor_fixture
 
 ENV_BUFFERS = ["states", "runs", "worlds", "sensors", "poses", "commands"]
-ROW_BUFFERS = ["obs", "critic_obs", "actions", "logp", "values", "rewards", "next_values", "terminated",
+ROW_BUFFERS = ["obs", "critic_obs", "next_critic_obs", "actions", "logp", "values", "rewards", "next_values", "terminated",
                "truncated"]
 INT_FIELDS = {"rng", "steps", "successes", "collisions", "timeouts", "episodes", "count", "seed", "family"}
 

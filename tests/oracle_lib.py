@@ -49,6 +49,8 @@ def oracle():
         _sig(lib, "orc_trainer_update", None, P, U32)
         _sig(lib, "orc_trainer_iteration", None, P, U32)
         _sig(lib, "orc_trainer_set_config", None, P, P)
+        _sig(lib, "orc_trainer_set_hidden", None, P, U32)
+        _sig(lib, "orc_trainer_evaluate", None, P)
         _sig(lib, "orc_trainer_minibatch_grads", None, P, U32, U32, P, P, P, P, P, P)
         _sig(lib, "orc_trainer_optimizer_step", U64, P)
         _sig(lib, "orc_trainer_metric_mean", None, P, P)
@@ -196,6 +198,14 @@ class OracleTrainer:
 
     def update(self, rollout_index):
         self.lib.orc_trainer_update(self.h, rollout_index)
+
+    def set_hidden(self, hidden):
+        """Replace the policy by one of hidden width `hidden` (fresh init)."""
+        self.lib.orc_trainer_set_hidden(self.h, hidden)
+
+    def evaluate(self):
+        """logp / values / next_values of the stored rollout under the policy."""
+        self.lib.orc_trainer_evaluate(self.h)
 
     def iteration(self, rollout_index):
         self.lib.orc_trainer_iteration(self.h, rollout_index)
