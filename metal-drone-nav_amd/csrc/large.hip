@@ -38,8 +38,12 @@ __device__ __forceinline__ v16f mfma(bf8 a, bf8 b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ uint32_t acc_row(uint32_t l, uint32_t r) { return 8 * (r / 4) + 4 * (l / 32) + (r % 4); }
-// tanh(x) = 1 - 2 / (e^{2x} + 1) with the hardware exponential and reciprocal.
-__device__ __forceinline__ float tanh_fast(float x) { return 1.0f - __fdividef(2.0f, __expf(2.0f * x) + 1.0f); }
+// tanh(x) = 1 - 2 / (e^{2x} + 1) with the hardware base-2 exponential and
+// reciprocal (v_exp_f32, v_rcp_f32; about 1 ulp each).
+__device__ __forceinline__ float tanh_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(x * 2.8853900817779268f);  // 2 log2(e) x
+    return fma_f(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+}
 
 // Rows r0 .. r0+RB of X[B][D] as bf16 [RB][XS] (row-major, K inputs, zero
 // padding) and, when `xt` is given, transposed [K][TS].  Loads are clamped
@@ -47,14 +51,23 @@ __device__ __forceinline__ float tanh_fast(float x) { return 1.0f - __fdividef(2
 template <uint32_t D, uint32_t K, uint32_t XS, uint32_t TS>
 __device__ __forceinline__ void stage_rows(const float* __restrict__ X, uint32_t r0, uint32_t rend, __bf16* xs,
                                            __bf16* xt) {
-#pragma unroll 8
-    for (uint32_t e = threadIdx.x; e < RB * K; e += 256) {
-        const uint32_t rr = e / K, k = e % K, row = r0 + rr;
-        const bool ok = row < rend && k < D;
-        const float v = X[size_t(ok ? row : 0) * D + (k < D ? k : 0)];
-        const __bf16 b = (__bf16)(ok ? v : 0.0f);
-        xs[rr * XS + k] = b;
-        if (xt) xt[k * TS + rr] = b;
+    constexpr uint32_t CH = K / 8;  // 8-input chunks per row
+#pragma unroll 4
+    for (uint32_t e = threadIdx.x; e < RB * CH; e += 256) {
+        const uint32_t rr = e / CH, k0 = 8 * (e % CH), row = r0 + rr;
+        const bool rok = row < rend;
+        const float* src = X + size_t(rok ? row : 0) * D;
+        bf8 v;
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) {
+            const uint32_t k = k0 + j;
+            const float x = src[k < D ? k : 0];
+            v[j] = (__bf16)((rok && k < D) ? x : 0.0f);
+        }
+        *reinterpret_cast<bf8*>(xs + rr * XS + k0) = v;
+        if (xt)
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++) xt[(k0 + j) * TS + rr] = v[j];
     }
 }
 
@@ -87,9 +100,21 @@ __global__ __launch_bounds__(256) void forward_kernel(const float* __restrict__ 
     // second layer: NQ = 4: thread t -> row t/2, outputs 2(t%2), 2(t%2)+1; NQ = 1: thread t < RB -> row t
     const uint32_t srow = NQ == 4 ? t / 2 : t, q0 = NQ == 4 ? 2 * (t % 2) : 0;
     float z0 = 0.0f, z1 = 0.0f;
+    // this lane's B fragments (weights of one unit, 8 inputs per k step), one tile ahead
+    bf8 bnext[K / 16];
+#pragma unroll
+    for (uint32_t ks = 0; ks < K / 16; ks++)
+        bnext[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(32 * wv + l % 32) * K + 16 * ks + 8 * (l / 32));
     for (uint32_t u0 = 0; u0 < H; u0 += UT) {
         const uint32_t unit = u0 + 32 * wv + l % 32;
         const float bias = b1[unit];
+        bf8 bcur[K / 16];
+#pragma unroll
+        for (uint32_t ks = 0; ks < K / 16; ks++) bcur[ks] = bnext[ks];
+        if (u0 + UT < H)
+#pragma unroll
+            for (uint32_t ks = 0; ks < K / 16; ks++)
+                bnext[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(unit + UT) * K + 16 * ks + 8 * (l / 32));
         v16f acc[4];
 #pragma unroll
         for (uint32_t rt = 0; rt < 4; rt++)
@@ -99,11 +124,10 @@ __global__ __launch_bounds__(256) void forward_kernel(const float* __restrict__ 
 #pragma unroll
         for (uint32_t ks = 0; ks < K / 16; ks++) {
             const uint32_t kb = 16 * ks + 8 * (l / 32);
-            const bf8 bv = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + kb);
 #pragma unroll
             for (uint32_t rt = 0; rt < 4; rt++) {
                 const bf8 av = *reinterpret_cast<const bf8*>(xs + (32 * rt + l % 32) * XS + kb);
-                acc[rt] = mfma(av, bv, acc[rt]);
+                acc[rt] = mfma(av, bcur[ks], acc[rt]);
             }
         }
 #pragma unroll
@@ -215,7 +239,7 @@ __global__ __launch_bounds__(256) void backward_kernel(const float* __restrict__
     __shared__ __bf16 xs[RB * XS];   // [row][k]
     __shared__ __bf16 xt[K * TS];    // [k][row]
     __shared__ __bf16 dt[UT * TS];   // delta^T [unit][row]
-    __shared__ float dms[RB * NQ];
+    __shared__ __attribute__((aligned(16))) float dms[RB * NQ];
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
     const uint32_t u0 = blockIdx.x * UT, c = blockIdx.y;
     const uint32_t unit = u0 + 32 * wv + l % 32;
@@ -224,6 +248,10 @@ __global__ __launch_bounds__(256) void backward_kernel(const float* __restrict__
 #pragma unroll
     for (uint32_t q = 0; q < NQ; q++) w2r[q] = W2[size_t(q) * H + unit];
     const float bias = b1[unit];
+    bf8 bw[K / 16];  // this lane's weight fragments of the workgroup's hidden tile
+#pragma unroll
+    for (uint32_t ks = 0; ks < K / 16; ks++)
+        bw[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + 16 * ks + 8 * (l / 32));
     v16f gacc[K / 32];
 #pragma unroll
     for (uint32_t jt = 0; jt < K / 32; jt++)
@@ -248,11 +276,10 @@ __global__ __launch_bounds__(256) void backward_kernel(const float* __restrict__
 #pragma unroll
         for (uint32_t ks = 0; ks < K / 16; ks++) {
             const uint32_t kb = 16 * ks + 8 * (l / 32);
-            const bf8 bv = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + kb);
 #pragma unroll
             for (uint32_t rt = 0; rt < 4; rt++) {
                 const bf8 av = *reinterpret_cast<const bf8*>(xs + (32 * rt + l % 32) * XS + kb);
-                acc[rt] = mfma(av, bv, acc[rt]);
+                acc[rt] = mfma(av, bw[ks], acc[rt]);
             }
         }
 #pragma unroll
@@ -261,12 +288,18 @@ __global__ __launch_bounds__(256) void backward_kernel(const float* __restrict__
             for (uint32_t r = 0; r < 16; r++) {
                 const uint32_t rr = 32 * rt + acc_row(l, r);
                 const float h = tanh_fast(acc[rt][r]);
+                float dq[NQ];
+                if constexpr (NQ == 4) {
+                    const float4 d4 = *reinterpret_cast<const float4*>(dms + rr * 4);
+                    dq[0] = d4.x; dq[1] = d4.y; dq[2] = d4.z; dq[3] = d4.w;
+                } else {
+                    dq[0] = dms[rr];
+                }
                 float g = 0.0f;
 #pragma unroll
                 for (uint32_t q = 0; q < NQ; q++) {
-                    const float d = dms[rr * NQ + q];
-                    g = fma_f(d, w2r[q], g);
-                    dw2a[q] = fma_f(d, h, dw2a[q]);
+                    g = fma_f(dq[q], w2r[q], g);
+                    dw2a[q] = fma_f(dq[q], h, dw2a[q]);
                 }
                 const float delta = g * (1.0f - h * h);
                 db1a += delta;
@@ -339,12 +372,15 @@ __global__ __launch_bounds__(256) void column_part_kernel(const float* __restric
 // Adds the column partials in block order and writes the per-row-column
 // gradients into the flat vectors (actor b2, log_std; critic b2) and the four
 // metric sums into metric_sums.
-__global__ void column_finish_kernel(const float* __restrict__ col_part, uint32_t blocks, uint32_t H,
-                                     float* __restrict__ ga, float* __restrict__ gc, float* __restrict__ metric_sums) {
-    const uint32_t t = threadIdx.x;
-    if (t >= 13) return;
+__global__ __launch_bounds__(64) void column_finish_kernel(const float* __restrict__ col_part, uint32_t blocks,
+                                                           uint32_t H, float* __restrict__ ga, float* __restrict__ gc,
+                                                           float* __restrict__ metric_sums) {
+    const uint32_t t = blockIdx.x, l = threadIdx.x;  // column t, lane l adds blocks l, l + 64, ...
     float s = 0.0f;
-    for (uint32_t b = 0; b < blocks; b++) s += col_part[size_t(b) * 13 + t];
+    for (uint32_t b = l; b < blocks; b += 64) s += col_part[size_t(b) * 13 + t];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (l != 0) return;
     const uint32_t A_B2 = H * OBS + H + 4 * H, A_LS = A_B2 + 4, C_B2 = H * COBS + 2 * H;
     if (t < 4) ga[A_B2 + t] = s;
     else if (t < 8) ga[A_LS + t - 4] = s;
@@ -352,20 +388,27 @@ __global__ void column_finish_kernel(const float* __restrict__ col_part, uint32_
     else metric_sums[t - 9] = s;
 }
 
-constexpr uint32_t NP = 512;  // squared-norm partial slots per network
+constexpr uint32_t NP = 512;  // squared-norm partial slots (workgroups) per network
 
-// Per-network squared-norm partials: slot s of net k sums g[i]^2 for i = s,
-// s + NP, ... (both networks in one grid: blockIdx.y = net).
+// Per-network squared-norm partials: workgroup s of net k sums g[i]^2 over
+// i = 256 s + t, + 256 NP, ... and reduces its 256 lanes by a tree
+// (both networks in one grid: blockIdx.y = net).
 __global__ __launch_bounds__(256) void sqnorm_kernel(const float* __restrict__ ga, const float* __restrict__ gc,
                                                      uint32_t PA, uint32_t PC, float* __restrict__ part) {
-    const uint32_t s = blockIdx.x * 256 + threadIdx.x;
-    if (s >= NP) return;
+    __shared__ float red[256];
+    const uint32_t t = threadIdx.x, s = blockIdx.x;
     const bool critic = blockIdx.y == 1;
     const float* g = critic ? gc : ga;
     const uint32_t P = critic ? PC : PA;
     float a = 0.0f;
-    for (uint32_t i = s; i < P; i += NP) a += g[i] * g[i];
-    part[blockIdx.y * NP + s] = a;
+    for (uint32_t i = 256 * s + t; i < P; i += 256 * NP) a += g[i] * g[i];
+    red[t] = a;
+    __syncthreads();
+    for (uint32_t w = 128; w > 0; w >>= 1) {
+        if (t < w) red[t] += red[t + w];
+        __syncthreads();
+    }
+    if (t == 0) part[blockIdx.y * NP + s] = red[0];
 }
 // Clip scales min(1, 0.5 / ||g||) of both networks (partials added in slot
 // order) and the update's metric row.
@@ -507,9 +550,9 @@ hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, flo
     float* norm_part = scratch;
     float* scale = scratch + 2 * lp::NP;
     float* metric_sums = scale + 2;
-    hipLaunchKernelGGL(lp::column_finish_kernel, dim3(1), dim3(64), 0, st, col_part, (B + lp::RB - 1) / lp::RB, H, ga,
+    hipLaunchKernelGGL(lp::column_finish_kernel, dim3(13), dim3(64), 0, st, col_part, (B + lp::RB - 1) / lp::RB, H, ga,
                        gc, metric_sums);
-    hipLaunchKernelGGL(lp::sqnorm_kernel, dim3((lp::NP + 255) / 256, 2), dim3(256), 0, st, ga, gc, PA, PC, norm_part);
+    hipLaunchKernelGGL(lp::sqnorm_kernel, dim3(lp::NP, 2), dim3(256), 0, st, ga, gc, PA, PC, norm_part);
     hipLaunchKernelGGL(lp::norm_finish_kernel, dim3(1), dim3(64), 0, st, norm_part, metric_sums, B, scale, metric_row);
     lp::LargeAdamArgs a;
     a.actor = actor; a.critic = critic; a.am = am; a.av = av; a.cm = cm; a.cv = cv;
