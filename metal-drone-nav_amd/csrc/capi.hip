@@ -734,6 +734,7 @@ struct MdnLargePPO {
     mdn::PolicyShape shape;
     float *actor = nullptr, *critic = nullptr, *am = nullptr, *av = nullptr, *cm = nullptr, *cv = nullptr;
     __bf16 *awb = nullptr, *cwb = nullptr;
+    __bf16 *xa = nullptr, *xaT = nullptr, *xc = nullptr, *xcT = nullptr;  // bf16 rows of one minibatch
     float* eval_means = nullptr;                         // [rows][4]
     float *means = nullptr, *values = nullptr, *dm = nullptr, *dls = nullptr, *dv = nullptr, *loss = nullptr;
     float *part = nullptr, *ga = nullptr, *gc = nullptr, *col_part = nullptr, *scratch = nullptr;
@@ -768,7 +769,8 @@ extern "C" {
 void mdn_lppo_destroy(MdnLargePPO* p) {
     if (!p) return;
     if (p->sim) hipStreamSynchronize(p->sim->stream);
-    void* bufs[] = {p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->eval_means, p->means,
+    void* bufs[] = {p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->xa, p->xaT, p->xc, p->xcT,
+                    p->eval_means, p->means,
                     p->values, p->dm, p->dls, p->dv, p->loss, p->part, p->ga, p->gc, p->col_part, p->scratch,
                     p->norm_part, p->norm_stats, p->metric_rows, p->metric_mean};
     for (void* b : bufs)
@@ -790,9 +792,9 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     p->minibatch = uint32_t(std::min<size_t>(minibatch, s->rows()));
     p->shape.hidden = p->shape.critic_hidden = hidden;
     p->updates = uint32_t((s->rows() + p->minibatch - 1) / p->minibatch) * epochs;
-    // row chunks of the backward: enough (hidden tile, chunk) workgroups for every CU
-    const uint32_t tiles = hidden / 128, mb_blocks = (p->minibatch + 127) / 128;
-    p->chunks = std::max(1u, std::min(mb_blocks, (256 + tiles - 1) / tiles));
+    // row chunks of the backward: enough (hidden tile, chunk) workgroups for two per CU
+    const uint32_t tiles = hidden / 128, mb_blocks = (p->minibatch + 63) / 64;
+    p->chunks = std::max(1u, std::min(mb_blocks, (512 + tiles - 1) / tiles));
     const size_t A = p->shape.actor_count(), C = p->shape.critic_count(), M = p->minibatch, R = s->rows();
     int rc = MDN_OK;
     auto guard = [&](int r) { if (r != MDN_OK && rc == MDN_OK) rc = r; };
@@ -804,6 +806,11 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     guard(dev_alloc(&p->cv, C));
     guard(dev_alloc(&p->awb, size_t(hidden) * 192));
     guard(dev_alloc(&p->cwb, size_t(hidden) * 32));
+    const size_t MP = (M + 127) / 128 * 128;
+    guard(dev_alloc(&p->xa, MP * 192));
+    guard(dev_alloc(&p->xaT, MP * 192));
+    guard(dev_alloc(&p->xc, MP * 32));
+    guard(dev_alloc(&p->xcT, MP * 32));
     guard(dev_alloc(&p->eval_means, R * 4));
     guard(dev_alloc(&p->means, M * 4));
     guard(dev_alloc(&p->values, M));
@@ -814,7 +821,7 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     guard(dev_alloc(&p->part, size_t(p->chunks) * hidden * (OBS + 1 + 4 + COBS + 1 + 1)));
     guard(dev_alloc(&p->ga, A));
     guard(dev_alloc(&p->gc, C));
-    guard(dev_alloc(&p->col_part, ((M + 127) / 128) * 13));
+    guard(dev_alloc(&p->col_part, ((M + 63) / 64) * 13));
     guard(dev_alloc(&p->scratch, 2 * 512 + 2 + 4));
     guard(dev_alloc(&p->norm_part, (R + 255) / 256));
     guard(dev_alloc(&p->norm_stats, 2));
@@ -843,12 +850,23 @@ int mdn_lppo_evaluate(MdnLargePPO* p) {
     int rc = open_sync_window(s);
     if (rc) return rc;
     const uint32_t R = uint32_t(s->rows());
+    // slices of one minibatch of rows through the prepared-copy buffers
     return timed(s, MDN_K_LP_FORWARD, [&] {
-        hipError_t e = lp_launch_forward(s->obs, s->co, p->awb, p->cwb, p->actor, p->critic, p->hidden, R,
-                                         p->eval_means, s->values, s->stream);
-        if (e == hipSuccess)
-            e = lp_launch_forward(nullptr, s->nco, p->awb, p->cwb, p->actor, p->critic, p->hidden, R, nullptr,
-                                  s->next_values, s->stream);
+        hipError_t e = hipSuccess;
+        for (uint32_t r0 = 0; r0 < R && e == hipSuccess; r0 += p->minibatch) {
+            const uint32_t b = std::min(p->minibatch, R - r0);
+            e = lp_launch_prep(s->obs + size_t(r0) * OBS, s->co + size_t(r0) * COBS, b, p->xa, p->xaT, p->xc, p->xcT,
+                               false, s->stream);
+            if (e == hipSuccess)
+                e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, p->hidden, b,
+                                      p->eval_means + size_t(r0) * 4, s->values + r0, s->stream);
+            if (e == hipSuccess)
+                e = lp_launch_prep(nullptr, s->nco + size_t(r0) * COBS, b, p->xa, p->xaT, p->xc, p->xcT, false,
+                                   s->stream);
+            if (e == hipSuccess)
+                e = lp_launch_forward(nullptr, p->xc, p->awb, p->cwb, p->actor, p->critic, p->hidden, b, nullptr,
+                                      s->next_values + r0, s->stream);
+        }
         if (e == hipSuccess)
             e = lp_launch_logp(p->eval_means, s->actions, p->actor + p->shape.actor_log_std(), R, s->logp, s->stream);
         return e;
@@ -879,8 +897,10 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
         const float* obs = s->obs + size_t(begin) * OBS;
         const float* co = s->co + size_t(begin) * COBS;
         rc = timed(s, MDN_K_LP_FORWARD, [&] {
-            hipError_t e = lp_launch_forward(obs, co, p->awb, p->cwb, p->actor, p->critic, H, b, p->means, p->values,
-                                             s->stream);
+            hipError_t e = lp_launch_prep(obs, co, b, p->xa, p->xaT, p->xc, p->xcT, true, s->stream);
+            if (e == hipSuccess)
+                e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, H, b, p->means, p->values,
+                                      s->stream);
             if (e == hipSuccess)
                 e = lp_launch_loss(p->means, p->values, s->actions + size_t(begin) * 4, s->logp + begin,
                                    s->advantages + begin, s->returns + begin, p->actor + p->shape.actor_log_std(), b,
@@ -889,8 +909,8 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
         });
         if (rc) return rc;
         rc = timed(s, MDN_K_LP_BACKWARD, [&] {
-            return lp_launch_backward(obs, co, p->awb, p->cwb, p->actor, p->critic, p->dm, p->dls, p->dv, p->loss, H, b,
-                                      p->chunks, p->part, p->ga, p->gc, p->col_part, s->stream);
+            return lp_launch_backward(p->xa, p->xaT, p->xc, p->xcT, p->awb, p->cwb, p->actor, p->critic, p->dm, p->dls,
+                                      p->dv, p->loss, H, b, p->chunks, p->part, p->ga, p->gc, p->col_part, s->stream);
         });
         if (rc) return rc;
         ++p->optimizer_step;

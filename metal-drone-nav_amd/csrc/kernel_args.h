@@ -88,7 +88,9 @@ hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* 
 hipError_t ppo_launch_metric_mean(const float* rows, float* mean, uint32_t updates, hipStream_t st);
 // wide-policy kernels (large.hip)
 hipError_t lp_launch_pack(const float* W, uint32_t H, uint32_t D, uint32_t K, __bf16* out, hipStream_t st);
-hipError_t lp_launch_forward(const float* obs, const float* co, const __bf16* awb, const __bf16* cwb,
+hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, __bf16* xa, __bf16* xaT, __bf16* xc,
+                          __bf16* xcT, bool transposed, hipStream_t st);
+hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* awb, const __bf16* cwb,
                              const float* actor, const float* critic, uint32_t H, uint32_t B, float* means,
                              float* values, hipStream_t st);
 hipError_t lp_launch_logp(const float* means, const float* actions, const float* log_std, uint32_t B, float* logp,
@@ -96,7 +98,8 @@ hipError_t lp_launch_logp(const float* means, const float* actions, const float*
 hipError_t lp_launch_loss(const float* means, const float* values, const float* actions, const float* old_logp,
                           const float* adv, const float* ret, const float* log_std, uint32_t B, float clip,
                           float vcoef, float ecoef, float* dm, float* dls, float* dv, float* loss, hipStream_t st);
-hipError_t lp_launch_backward(const float* obs, const float* co, const __bf16* awb, const __bf16* cwb,
+hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16* xc, const __bf16* xcT,
+                              const __bf16* awb, const __bf16* cwb,
                               const float* actor, const float* critic, const float* dm, const float* dls,
                               const float* dv, const float* loss, uint32_t H, uint32_t B, uint32_t chunks,
                               float* part, float* ga, float* gc, float* col_part, hipStream_t st);

@@ -30,7 +30,8 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr uint32_t OBS = MDN_ACTOR_OBS_POOLED;
 constexpr uint32_t COBS = MDN_CRITIC_OBS;
 constexpr uint32_t KA = 192, KC = 32;  // first-layer inputs padded to whole 32-wide tiles
-constexpr uint32_t RB = 128;           // rows per block
+constexpr uint32_t RB = 64;            // rows per block (two 32-row tiles); 2 workgroups fit a CU
+constexpr uint32_t RT = RB / 32;       // 32-row tiles per block
 constexpr uint32_t UT = 128;           // hidden units per tile: four wavefronts x 32
 constexpr float LOG_TWO_PI = 1.8378770664093453f;
 
@@ -45,30 +46,44 @@ __device__ __forceinline__ float tanh_fast(float x) {
     return fma_f(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
 }
 
-// Rows r0 .. r0+RB of X[B][D] as bf16 [RB][XS] (row-major, K inputs, zero
-// padding) and, when `xt` is given, transposed [K][TS].  Loads are clamped
-// to valid addresses and then masked, so they issue back to back.
-template <uint32_t D, uint32_t K, uint32_t XS, uint32_t TS>
-__device__ __forceinline__ void stage_rows(const float* __restrict__ X, uint32_t r0, uint32_t rend, __bf16* xs,
-                                           __bf16* xt) {
-    constexpr uint32_t CH = K / 8;  // 8-input chunks per row
+// bf16 copies of the B rows of X[B][D] prepared once per minibatch: Xb
+// [BP][K] row-major and XbT [K][BP] transposed (BP = B rounded up to RB; inputs
+// past D and rows past B are zero).  Every hidden tile reads these instead of
+// converting the rows itself.
+template <uint32_t D, uint32_t K>
+__global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ X, uint32_t B, uint32_t BP,
+                                                   __bf16* __restrict__ Xb, __bf16* __restrict__ XbT) {
+    const uint32_t row = blockIdx.x * 256 + threadIdx.x, k0 = 8 * blockIdx.y;
+    if (row >= BP) return;
+    bf8 v;
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) {
+        const uint32_t k = k0 + j;
+        v[j] = (__bf16)((row < B && k < D) ? X[size_t(row) * D + k] : 0.0f);
+    }
+    *reinterpret_cast<bf8*>(Xb + size_t(row) * K + k0) = v;
+    if (XbT)
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j++) XbT[size_t(k0 + j) * BP + row] = v[j];
+}
+
+// Rows r0 .. r0+RB of the prepared copies into LDS: xs [RB][XS] from Xb and,
+// when xt is given, xt [K][TS] from XbT (16-byte copies).
+template <uint32_t K, uint32_t XS, uint32_t TS>
+__device__ __forceinline__ void stage_rows(const __bf16* __restrict__ Xb, const __bf16* __restrict__ XbT, uint32_t BP,
+                                           uint32_t r0, __bf16* xs, __bf16* xt) {
+    constexpr uint32_t CH = K / 8;
 #pragma unroll 4
     for (uint32_t e = threadIdx.x; e < RB * CH; e += 256) {
-        const uint32_t rr = e / CH, k0 = 8 * (e % CH), row = r0 + rr;
-        const bool rok = row < rend;
-        const float* src = X + size_t(rok ? row : 0) * D;
-        bf8 v;
-#pragma unroll
-        for (uint32_t j = 0; j < 8; j++) {
-            const uint32_t k = k0 + j;
-            const float x = src[k < D ? k : 0];
-            v[j] = (__bf16)((rok && k < D) ? x : 0.0f);
-        }
-        *reinterpret_cast<bf8*>(xs + rr * XS + k0) = v;
-        if (xt)
-#pragma unroll
-            for (uint32_t j = 0; j < 8; j++) xt[(k0 + j) * TS + rr] = v[j];
+        const uint32_t rr = e / CH, k0 = 8 * (e % CH);
+        *reinterpret_cast<bf8*>(xs + rr * XS + k0) = *reinterpret_cast<const bf8*>(Xb + size_t(r0 + rr) * K + k0);
     }
+    if (xt)
+#pragma unroll 4
+        for (uint32_t e = threadIdx.x; e < K * (RB / 8); e += 256) {
+            const uint32_t k = e / (RB / 8), c = 8 * (e % (RB / 8));
+            *reinterpret_cast<bf8*>(xt + k * TS + c) = *reinterpret_cast<const bf8*>(XbT + size_t(k) * BP + r0 + c);
+        }
 }
 
 // ---------------------------------------------------------------- weights
@@ -84,9 +99,11 @@ __global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ W, 
 // ---------------------------------------------------------------- forward
 // out[row][q] = b2[q] + sum_u W2[q][u] tanh(b1[u] + sum_k W1[u][k] X[row][k])
 // for q < NQ (actor means: NQ = 4 over W2 [4][H]; critic value: NQ = 1).
-// A workgroup owns RB rows and walks the hidden units in tiles of UT.
+// A workgroup owns RB rows and walks the hidden units in tiles of UT; the
+// second layer runs from LDS with one (row, output) per thread.
 template <uint32_t D, uint32_t K, uint32_t NQ>
-__global__ __launch_bounds__(256) void forward_kernel(const float* __restrict__ X, const __bf16* __restrict__ Wb,
+__global__ __launch_bounds__(256, 2) void forward_kernel(const __bf16* __restrict__ Xb, uint32_t BP,
+                                                      const __bf16* __restrict__ Wb,
                                                       const float* __restrict__ b1, const float* __restrict__ W2,
                                                       const float* __restrict__ b2, uint32_t H, uint32_t B,
                                                       float* __restrict__ out) {
@@ -96,28 +113,20 @@ __global__ __launch_bounds__(256) void forward_kernel(const float* __restrict__ 
     __shared__ float w2s[NQ * UT];
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
     const uint32_t r0 = blockIdx.x * RB;
-    stage_rows<D, K, XS, 1>(X, r0, B, xs, nullptr);
-    // second layer: NQ = 4: thread t -> row t/2, outputs 2(t%2), 2(t%2)+1; NQ = 1: thread t < RB -> row t
-    const uint32_t srow = NQ == 4 ? t / 2 : t, q0 = NQ == 4 ? 2 * (t % 2) : 0;
-    float z0 = 0.0f, z1 = 0.0f;
-    // this lane's B fragments (weights of one unit, 8 inputs per k step), one tile ahead
-    bf8 bnext[K / 16];
-#pragma unroll
-    for (uint32_t ks = 0; ks < K / 16; ks++)
-        bnext[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(32 * wv + l % 32) * K + 16 * ks + 8 * (l / 32));
+    stage_rows<K, XS, 1>(Xb, nullptr, BP, r0, xs, nullptr);
+    const uint32_t srow = t / NQ, q = t % NQ;  // second layer: thread -> (row, output), rows < RB
+    const bool second = srow < RB;
+    float z = 0.0f;
     for (uint32_t u0 = 0; u0 < H; u0 += UT) {
         const uint32_t unit = u0 + 32 * wv + l % 32;
         const float bias = b1[unit];
-        bf8 bcur[K / 16];
+        bf8 bw[K / 16];
 #pragma unroll
-        for (uint32_t ks = 0; ks < K / 16; ks++) bcur[ks] = bnext[ks];
-        if (u0 + UT < H)
+        for (uint32_t ks = 0; ks < K / 16; ks++)
+            bw[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + 16 * ks + 8 * (l / 32));
+        v16f acc[RT];
 #pragma unroll
-            for (uint32_t ks = 0; ks < K / 16; ks++)
-                bnext[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(unit + UT) * K + 16 * ks + 8 * (l / 32));
-        v16f acc[4];
-#pragma unroll
-        for (uint32_t rt = 0; rt < 4; rt++)
+        for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++) acc[rt][r] = bias;
         __syncthreads();  // rows staged; the previous tile's hs/w2s consumed
@@ -125,33 +134,27 @@ __global__ __launch_bounds__(256) void forward_kernel(const float* __restrict__ 
         for (uint32_t ks = 0; ks < K / 16; ks++) {
             const uint32_t kb = 16 * ks + 8 * (l / 32);
 #pragma unroll
-            for (uint32_t rt = 0; rt < 4; rt++) {
+            for (uint32_t rt = 0; rt < RT; rt++) {
                 const bf8 av = *reinterpret_cast<const bf8*>(xs + (32 * rt + l % 32) * XS + kb);
-                acc[rt] = mfma(av, bcur[ks], acc[rt]);
+                acc[rt] = mfma(av, bw[ks], acc[rt]);
             }
         }
 #pragma unroll
-        for (uint32_t rt = 0; rt < 4; rt++)
+        for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++)
                 hs[(32 * rt + acc_row(l, r)) * HS + 32 * wv + l % 32] = tanh_fast(acc[rt][r]);
         for (uint32_t i = t; i < NQ * UT; i += 256) w2s[i] = W2[size_t(i / UT) * H + u0 + i % UT];
         __syncthreads();
-        if (NQ == 4 || t < RB) {
+        if (second) {
             const float* hr = hs + srow * HS;
-#pragma unroll 8
-            for (uint32_t c = 0; c < UT; c++) {
-                const float h = hr[c];
-                z0 = fma_f(w2s[q0 * UT + c], h, z0);
-                if (NQ == 4) z1 = fma_f(w2s[(q0 + 1) * UT + c], h, z1);
-            }
+            const float* wr = w2s + q * UT;
+#pragma unroll 16
+            for (uint32_t c = 0; c < UT; c++) z = fma_f(wr[c], hr[c], z);
         }
     }
     const uint32_t row = r0 + srow;
-    if ((NQ == 4 || t < RB) && row < B) {
-        out[size_t(row) * NQ + q0] = b2[q0] + z0;
-        if (NQ == 4) out[size_t(row) * NQ + q0 + 1] = b2[q0 + 1] + z1;
-    }
+    if (second && row < B) out[size_t(row) * NQ + q] = b2[q] + z;
 }
 
 // ---------------------------------------------------------------- loss
@@ -228,9 +231,11 @@ __global__ __launch_bounds__(256) void logp_kernel(const float* __restrict__ mea
 // then dW1[u][k] += sum_rows delta[row][u] X[row][k] on the matrix cores (the
 // rows are the reduction dimension), db1[u] += sum delta, dW2[q][u] +=
 // sum dm[row][q] h[row][u].  Output: partial slot `c = blockIdx.y` of
-// dW1p [c][H][D], db1p [c][H], dW2p [c][NQ][H].
+// dW1p [c][H][D], db1p [c][H], dW2p [c][NQ][H].  About 73 KB of LDS, so two
+// workgroups share a CU and one's matrix work overlaps the other's VALU work.
 template <uint32_t D, uint32_t K, uint32_t NQ>
-__global__ __launch_bounds__(256) void backward_kernel(const float* __restrict__ X, const __bf16* __restrict__ Wb,
+__global__ __launch_bounds__(256, 2) void backward_kernel(const __bf16* __restrict__ Xb, const __bf16* __restrict__ XbT,
+                                                       uint32_t BP, const __bf16* __restrict__ Wb,
                                                        const float* __restrict__ b1, const float* __restrict__ W2,
                                                        const float* __restrict__ dm, uint32_t H, uint32_t B,
                                                        uint32_t RC, float* __restrict__ dW1p,
@@ -262,48 +267,56 @@ __global__ __launch_bounds__(256) void backward_kernel(const float* __restrict__
     for (uint32_t q = 0; q < NQ; q++) dw2a[q] = 0.0f;
     for (uint32_t r0 = rbeg; r0 < rend; r0 += RB) {
         __syncthreads();  // the previous block's LDS reads are done
-        stage_rows<D, K, XS, TS>(X, r0, rend, xs, xt);
+        stage_rows<K, XS, TS>(Xb, XbT, BP, r0, xs, xt);
         for (uint32_t e = t; e < RB * NQ; e += 256) {
             const uint32_t row = r0 + e / NQ;
             dms[e] = row < rend ? dm[size_t(row) * NQ + e % NQ] : 0.0f;
         }
         __syncthreads();
-        v16f acc[4];
+        v16f acc[RT];
 #pragma unroll
-        for (uint32_t rt = 0; rt < 4; rt++)
+        for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++) acc[rt][r] = bias;
 #pragma unroll
         for (uint32_t ks = 0; ks < K / 16; ks++) {
             const uint32_t kb = 16 * ks + 8 * (l / 32);
 #pragma unroll
-            for (uint32_t rt = 0; rt < 4; rt++) {
+            for (uint32_t rt = 0; rt < RT; rt++) {
                 const bf8 av = *reinterpret_cast<const bf8*>(xs + (32 * rt + l % 32) * XS + kb);
                 acc[rt] = mfma(av, bw[ks], acc[rt]);
             }
         }
+        // lane l holds rows 8g + 4(l/32) + 0..3 (g = r/4) of unit l%32: four
+        // consecutive rows per group, stored to delta^T as one 8-byte write
 #pragma unroll
-        for (uint32_t rt = 0; rt < 4; rt++)
+        for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (uint32_t r = 0; r < 16; r++) {
-                const uint32_t rr = 32 * rt + acc_row(l, r);
-                const float h = tanh_fast(acc[rt][r]);
-                float dq[NQ];
-                if constexpr (NQ == 4) {
-                    const float4 d4 = *reinterpret_cast<const float4*>(dms + rr * 4);
-                    dq[0] = d4.x; dq[1] = d4.y; dq[2] = d4.z; dq[3] = d4.w;
-                } else {
-                    dq[0] = dms[rr];
+            for (uint32_t g4 = 0; g4 < 4; g4++) {
+                __attribute__((ext_vector_type(4))) __bf16 d4;
+#pragma unroll
+                for (uint32_t i = 0; i < 4; i++) {
+                    const uint32_t r = 4 * g4 + i, rr = 32 * rt + acc_row(l, r);
+                    const float h = tanh_fast(acc[rt][r]);
+                    float dq[NQ];
+                    if constexpr (NQ == 4) {
+                        const float4 v4 = *reinterpret_cast<const float4*>(dms + rr * 4);
+                        dq[0] = v4.x; dq[1] = v4.y; dq[2] = v4.z; dq[3] = v4.w;
+                    } else {
+                        dq[0] = dms[rr];
+                    }
+                    float gsum = 0.0f;
+#pragma unroll
+                    for (uint32_t q = 0; q < NQ; q++) {
+                        gsum = fma_f(dq[q], w2r[q], gsum);
+                        dw2a[q] = fma_f(dq[q], h, dw2a[q]);
+                    }
+                    const float delta = gsum * (1.0f - h * h);
+                    db1a += delta;
+                    d4[i] = (__bf16)delta;
                 }
-                float g = 0.0f;
-#pragma unroll
-                for (uint32_t q = 0; q < NQ; q++) {
-                    g = fma_f(dq[q], w2r[q], g);
-                    dw2a[q] = fma_f(dq[q], h, dw2a[q]);
-                }
-                const float delta = g * (1.0f - h * h);
-                db1a += delta;
-                dt[(32 * wv + l % 32) * TS + rr] = (__bf16)delta;
+                const uint32_t rr0 = 32 * rt + acc_row(l, 4 * g4);
+                *reinterpret_cast<__attribute__((ext_vector_type(4))) __bf16*>(dt + (32 * wv + l % 32) * TS + rr0) = d4;
             }
         __syncthreads();
 #pragma unroll
@@ -469,20 +482,38 @@ hipError_t lp_launch_pack(const float* W, uint32_t H, uint32_t D, uint32_t K, __
     return hipGetLastError();
 }
 
-// Actor means [B][4] and critic values [B] of B rows.
-hipError_t lp_launch_forward(const float* obs, const float* co, const __bf16* awb, const __bf16* cwb,
+// bf16 copies of the B rows (actor inputs and critic inputs): xa [BP][192],
+// xaT [192][BP], xc [BP][32], xcT [32][BP] with BP = B rounded up to 128.
+// `transposed` = false skips the transposed copies (forward-only use).
+hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, __bf16* xa, __bf16* xaT, __bf16* xc,
+                          __bf16* xcT, bool transposed, hipStream_t st) {
+    if (B == 0) return hipSuccess;
+    const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
+    const uint32_t gx = (BP + 255) / 256;
+    if (obs)
+        hipLaunchKernelGGL((lp::prep_kernel<lp::OBS, lp::KA>), dim3(gx, lp::KA / 8), dim3(256), 0, st, obs, B, BP, xa,
+                           transposed ? xaT : nullptr);
+    if (co)
+        hipLaunchKernelGGL((lp::prep_kernel<lp::COBS, lp::KC>), dim3(gx, lp::KC / 8), dim3(256), 0, st, co, B, BP, xc,
+                           transposed ? xcT : nullptr);
+    return hipGetLastError();
+}
+
+// Actor means [B][4] and critic values [B] of B prepared rows.
+hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* awb, const __bf16* cwb,
                              const float* actor, const float* critic, uint32_t H, uint32_t B, float* means,
                              float* values, hipStream_t st) {
     if (B == 0) return hipSuccess;
-    const dim3 grid((B + lp::RB - 1) / lp::RB);
+    const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
+    const dim3 grid(BP / lp::RB);
     const uint32_t A_B1 = H * lp::OBS, A_W2 = A_B1 + H, A_B2 = A_W2 + 4 * H;
     const uint32_t C_B1 = H * lp::COBS, C_W2 = C_B1 + H, C_B2 = C_W2 + H;
     if (means)
-        hipLaunchKernelGGL((lp::forward_kernel<lp::OBS, lp::KA, 4>), grid, dim3(256), 0, st, obs, awb, actor + A_B1,
+        hipLaunchKernelGGL((lp::forward_kernel<lp::OBS, lp::KA, 4>), grid, dim3(256), 0, st, xa, BP, awb, actor + A_B1,
                            actor + A_W2, actor + A_B2, H, B, means);
     if (values)
-        hipLaunchKernelGGL((lp::forward_kernel<lp::COBS, lp::KC, 1>), grid, dim3(256), 0, st, co, cwb, critic + C_B1,
-                           critic + C_W2, critic + C_B2, H, B, values);
+        hipLaunchKernelGGL((lp::forward_kernel<lp::COBS, lp::KC, 1>), grid, dim3(256), 0, st, xc, BP, cwb,
+                           critic + C_B1, critic + C_W2, critic + C_B2, H, B, values);
     return hipGetLastError();
 }
 
@@ -506,11 +537,13 @@ hipError_t lp_launch_loss(const float* means, const float* values, const float* 
 // the flat gradients ga (actor layout) and gc (critic layout) and the
 // per-row column partials.  Scratch: part >= chunks * (H*(181+1+4) +
 // H*(32+1+1)) floats, col_part >= ceil(B/128) * 13.
-hipError_t lp_launch_backward(const float* obs, const float* co, const __bf16* awb, const __bf16* cwb,
+hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16* xc, const __bf16* xcT,
+                              const __bf16* awb, const __bf16* cwb,
                               const float* actor, const float* critic, const float* dm, const float* dls,
                               const float* dv, const float* loss, uint32_t H, uint32_t B, uint32_t chunks,
                               float* part, float* ga, float* gc, float* col_part, hipStream_t st) {
     if (B == 0) return hipSuccess;
+    const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
     const uint32_t RC = ((B + chunks - 1) / chunks + lp::RB - 1) / lp::RB * lp::RB;
     const uint32_t nc = (B + RC - 1) / RC;
     const uint32_t A_B1 = H * lp::OBS, A_W2 = A_B1 + H;
@@ -523,10 +556,10 @@ hipError_t lp_launch_backward(const float* obs, const float* co, const __bf16* a
     float* cb1 = cW1 + size_t(nc) * H * lp::COBS;
     float* cw2 = cb1 + size_t(nc) * H;
     const dim3 grid(H / lp::UT, nc);
-    hipLaunchKernelGGL((lp::backward_kernel<lp::OBS, lp::KA, 4>), grid, dim3(256), 0, st, obs, awb, actor + A_B1,
-                       actor + A_W2, dm, H, B, RC, aW1, ab1, aW2);
-    hipLaunchKernelGGL((lp::backward_kernel<lp::COBS, lp::KC, 1>), grid, dim3(256), 0, st, co, cwb, critic + C_B1,
-                       critic + C_W2, dv, H, B, RC, cW1, cb1, cw2);
+    hipLaunchKernelGGL((lp::backward_kernel<lp::OBS, lp::KA, 4>), grid, dim3(256), 0, st, xa, xaT, BP, awb,
+                       actor + A_B1, actor + A_W2, dm, H, B, RC, aW1, ab1, aW2);
+    hipLaunchKernelGGL((lp::backward_kernel<lp::COBS, lp::KC, 1>), grid, dim3(256), 0, st, xc, xcT, BP, cwb,
+                       critic + C_B1, critic + C_W2, dv, H, B, RC, cW1, cb1, cw2);
     auto sum = [&](const float* p, uint64_t n, float* out) {
         hipLaunchKernelGGL(lp::sum_slots_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, p, n, nc, out);
     };
