@@ -120,7 +120,7 @@ def test_rollout_parity(lanes):
 
 
 @pytest.mark.parametrize("variant", ["delays_wind_noise", "eval", "movers3", "mixed6", "rehearsal13",
-                                     "goal_script"])
+                                     "goal_script", "threat_mix_delays"])
 def test_rollout_parity_variants(variant):
     kw = dict(n=48, family=1, speed=1.0, distance=3.0, max_steps=30)
     if variant == "delays_wind_noise":
@@ -133,6 +133,8 @@ def test_rollout_parity_variants(variant):
         kw.update(family=6, distance=4.0)
     elif variant == "rehearsal13":
         kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=1, wind=0.5)
+    elif variant == "threat_mix_delays":  # moving-threat mix with 100 ms sensor and command delays
+        kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=2, max_steps=60)
     elif variant == "goal_script":
         kw.update(mode=2, family=0, eval=1, speed=0.5, distance=4.0, max_steps=200)
     say("case: rollout variant %s" % variant)
@@ -177,4 +179,21 @@ def test_baseline_schedule_parity_large_minibatch(n, minibatch):
     ora.iteration(0)
     bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "critic_v", "metric_rows"]
                   + ROW_BUFFERS + ENV_BUFFERS, tol=TOL)
+    assert not bad, bad
+
+
+def test_production_path_bit_exact():
+    """The benchmark's code path (8 lanes per env, 2 ring slots: the 4-wavefront
+    workgroup with matrix-core layers) and one PPO iteration of 4096-row
+    minibatches reproduce the oracle bit for bit: every buffer, float fields
+    included, compared at tolerance 0."""
+    say("case: bit-exact iteration N=128 T=64 epochs=1 minibatch=4096")
+    cfg = config(n=128, family=1, speed=1.0, distance=3.0, max_steps=40)
+    sim, ppo, ora = make_pair(cfg, 64, epochs=1, minibatch=4096)
+    sim.collect()
+    ppo.rollout_update(0)
+    sim.sync()
+    ora.iteration(0)
+    bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v",
+                             "metric_rows"] + ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
     assert not bad, bad
