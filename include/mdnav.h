@@ -140,6 +140,15 @@ void mdn_lppo_destroy(MdnLargePPO* lp);
  * wide policy, written into the sim's logp, values and next_values rows
  * (the rollout's sim_act / next-value outputs for this policy). */
 int mdn_lppo_evaluate(MdnLargePPO* lp);
+/* Sim::collect (main.mm:573-598) of a build whose actor is the wide policy:
+ * every tick the wide actor's means drive sim_act (sim.metal:229-256); the
+ * wide critic gives values at s and s' (sim.metal:254, 322).  `count` ticks,
+ * 0 = horizon.  Needs 8 lanes per env. */
+int mdn_lppo_collect(MdnLargePPO* lp, uint32_t count);
+/* Means [rows][4] of the last mdn_lppo_collect or mdn_lppo_evaluate (the
+ * actor output each row's action was sampled around / re-evaluated at);
+ * count = horizon * n * 4. */
+int mdn_lppo_means(MdnLargePPO* lp, float* host, uint64_t count);
 /* PPOTrainer::rollout_update for the wide policy: GAE, normalisation,
  * epochs x minibatches of forward, loss, backward, clip and Adam. */
 int mdn_lppo_rollout_update(MdnLargePPO* lp, uint32_t rollout_index);

@@ -106,6 +106,7 @@ struct MdnSim {
         a.camera = camera; a.obs = obs; a.co = co; a.nco = nco; a.actions = actions; a.logp = logp; a.values = values;
         a.rewards = rewards; a.next_values = next_values; a.terminated = terminated; a.truncated = truncated;
         a.cfg = cfg; a.phys = phys; a.count = count; a.horizon = horizon;
+        a.ext_means = nullptr; a.ext_log_std = nullptr; a.tick0 = 0; a.split = 0;
         return a;
     }
 };
@@ -750,6 +751,25 @@ int lp_pack(MdnLargePPO* p) {
     HIP_TRY(lp_launch_pack(p->critic, p->hidden, COBS, 32, p->cwb, s->stream));
     return MDN_OK;
 }
+// Wide forward over `rows` stored rows in slices of one minibatch (the size of
+// the prepared-copy buffers): actor means from obs rows and/or critic values
+// from critic-observation rows.
+hipError_t lp_forward_rows(MdnLargePPO* p, const float* obs, const float* co, uint32_t rows, float* means,
+                           float* values) {
+    MdnSim* s = p->sim;
+    hipError_t e = hipSuccess;
+    for (uint32_t r0 = 0; r0 < rows && e == hipSuccess; r0 += p->minibatch) {
+        const uint32_t b = std::min(p->minibatch, rows - r0);
+        e = lp_launch_prep(obs ? obs + size_t(r0) * OBS : nullptr, co ? co + size_t(r0) * COBS : nullptr, b, p->xa,
+                           p->xaT, p->xc, p->xcT, false, s->stream);
+        if (e == hipSuccess)
+            e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, p->hidden, b,
+                                  means ? means + size_t(r0) * 4 : nullptr, values ? values + r0 : nullptr,
+                                  s->stream);
+    }
+    return e;
+}
+
 float* lp_param(MdnLargePPO* p, uint32_t which, uint64_t* count) {
     const uint64_t A = p->shape.actor_count(), C = p->shape.critic_count();
     switch (which) {
@@ -850,27 +870,61 @@ int mdn_lppo_evaluate(MdnLargePPO* p) {
     int rc = open_sync_window(s);
     if (rc) return rc;
     const uint32_t R = uint32_t(s->rows());
-    // slices of one minibatch of rows through the prepared-copy buffers
     return timed(s, MDN_K_LP_FORWARD, [&] {
-        hipError_t e = hipSuccess;
-        for (uint32_t r0 = 0; r0 < R && e == hipSuccess; r0 += p->minibatch) {
-            const uint32_t b = std::min(p->minibatch, R - r0);
-            e = lp_launch_prep(s->obs + size_t(r0) * OBS, s->co + size_t(r0) * COBS, b, p->xa, p->xaT, p->xc, p->xcT,
-                               false, s->stream);
-            if (e == hipSuccess)
-                e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, p->hidden, b,
-                                      p->eval_means + size_t(r0) * 4, s->values + r0, s->stream);
-            if (e == hipSuccess)
-                e = lp_launch_prep(nullptr, s->nco + size_t(r0) * COBS, b, p->xa, p->xaT, p->xc, p->xcT, false,
-                                   s->stream);
-            if (e == hipSuccess)
-                e = lp_launch_forward(nullptr, p->xc, p->awb, p->cwb, p->actor, p->critic, p->hidden, b, nullptr,
-                                      s->next_values + r0, s->stream);
-        }
+        hipError_t e = lp_forward_rows(p, s->obs, s->co, R, p->eval_means, s->values);
+        if (e == hipSuccess) e = lp_forward_rows(p, nullptr, s->nco, R, nullptr, s->next_values);
         if (e == hipSuccess)
             e = lp_launch_logp(p->eval_means, s->actions, p->actor + p->shape.actor_log_std(), R, s->logp, s->stream);
         return e;
     });
+}
+
+int mdn_lppo_collect(MdnLargePPO* p, uint32_t count) {
+    if (!p) return fail(MDN_E_ARG, "mdn_lppo_collect: null");
+    MdnSim* s = p->sim;
+    if (s->lanes != 8) return fail(MDN_E_ARG, "mdn_lppo_collect: the split-tick env step runs 8 lanes per env");
+    if (count == 0) count = s->horizon;
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    const uint32_t N = s->cfg.n;
+    const int slots = ring_slots(s->cfg);
+    nav::RolloutArgs a = s->args(1);
+    a.ext_means = p->eval_means;
+    a.ext_log_std = p->actor + p->shape.actor_log_std();
+    // tick 0 up to its observation; then per tick: wide actor means of the
+    // tick's rows, and one launch that acts, advances, resets and observes the
+    // next tick
+    a.split = nav::SPLIT_END_AFTER_OBSERVE;
+    rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, 8, slots, s->stream); });
+    for (uint32_t t = 0; t < count && rc == MDN_OK; t++) {
+        const size_t row0 = size_t(t % s->horizon) * N;
+        rc = timed(s, MDN_K_LP_FORWARD, [&] {
+            return lp_forward_rows(p, s->obs + row0 * OBS, nullptr, N, p->eval_means + row0 * 4, nullptr);
+        });
+        if (rc) break;
+        const bool more = t + 1 < count;
+        a.count = more ? 2 : 1;
+        a.tick0 = t;
+        a.split = nav::SPLIT_BEGIN_AT_ACT | (more ? nav::SPLIT_END_AFTER_OBSERVE : 0u);
+        rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, 8, slots, s->stream); });
+    }
+    if (rc) return rc;
+    // values at s and s' (sim.metal:254, 322) under the wide critic
+    const uint32_t rows = uint32_t(size_t(std::min(count, s->horizon)) * N);
+    return timed(s, MDN_K_LP_FORWARD, [&] {
+        hipError_t e = lp_forward_rows(p, nullptr, s->co, rows, nullptr, s->values);
+        if (e == hipSuccess) e = lp_forward_rows(p, nullptr, s->nco, rows, nullptr, s->next_values);
+        return e;
+    });
+}
+
+int mdn_lppo_means(MdnLargePPO* p, float* host, uint64_t count) {
+    if (!p || !host) return fail(MDN_E_ARG, "mdn_lppo_means: null");
+    const uint64_t n = uint64_t(p->sim->rows()) * 4;
+    if (count != n) return fail(MDN_E_ARG, "mdn_lppo_means: count must be rows * 4");
+    HIP_TRY(hipStreamSynchronize(p->sim->stream));
+    HIP_TRY(hipMemcpy(host, p->eval_means, n * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
 }
 
 int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {

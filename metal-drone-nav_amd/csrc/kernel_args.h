@@ -35,7 +35,19 @@ struct RolloutArgs {
     MdnPhysicsParams phys;
     uint32_t count;        // ticks in this launch
     uint32_t horizon;      // row blocks of the rollout buffers
+    // Split ticks (policy evaluated outside the kernel, e.g. a wide actor):
+    // tick t of this launch writes row block (tick0 + t) % horizon; means come
+    // from ext_means [T][N][4] and log_std from ext_log_std; values and next
+    // values are left to the caller.
+    const float* ext_means;
+    const float* ext_log_std;
+    uint32_t tick0;
+    uint32_t split;        // SPLIT_* flags
 };
+// The first tick's depth and observation were produced by the previous launch.
+constexpr uint32_t SPLIT_BEGIN_AT_ACT = 1;
+// The last tick stops after its observation (its means are not known yet).
+constexpr uint32_t SPLIT_END_AFTER_OBSERVE = 2;
 }  // namespace nav
 
 namespace ppo {

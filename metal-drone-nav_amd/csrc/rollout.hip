@@ -351,7 +351,10 @@ struct WeightLds {
 template <>
 struct WeightLds<1> {};
 
-template <int G, int K, int W>
+// X: split ticks. The kernel stops at the policy call and takes the means
+// from a.ext_means (a policy evaluated by other kernels between launches);
+// values and next values are the caller's.
+template <int G, int K, int W, bool X>
 __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     constexpr int E = 64 * W / G;    // envs per workgroup
     constexpr int U = 16 / G;        // RAPTOR units per lane
@@ -369,7 +372,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     const float* RW;    // RAPTOR weights (RaptorWeights layout)
     const float* CAM;   // camera rays [pixel][3]
     if constexpr (W > 1) {
-        for (uint32_t i = threadIdx.x; i < OBS * HID; i += 64 * W) s_wt.aw[i] = a.actor_w1t[i];
+        if constexpr (!X)
+            for (uint32_t i = threadIdx.x; i < OBS * HID; i += 64 * W) s_wt.aw[i] = a.actor_w1t[i];
         for (uint32_t i = threadIdx.x; i < RAPTOR_WORDS; i += 64 * W) s_wt.rw[i] = a.raptor[i];
         for (uint32_t i = threadIdx.x; i < 3 * PIX; i += 64 * W) s_wt.cam[i] = a.camera[i];
         __syncthreads();
@@ -405,7 +409,11 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     for (uint32_t i = lane; i < WORLD_WORDS; i += G) world[i] = a.world[size_t(nn) * WORLD_WORDS + i];
     for (uint32_t i = lane; i < 32; i += G) s_cmd[grp][i] = a.commands[size_t(nn) * 32 + i];
     {   // pooled ring cache: LDS slot f%K holds frame f for the last K frames
-        const int last = r.steps == 0 ? -1 : int((r.steps - 1) / C.sensor_period);
+        // (a launch that begins at act already holds the frame cast for the
+        // current step, if one was due)
+        const int last = (X && (a.split & SPLIT_BEGIN_AT_ACT)) ? int(r.steps / C.sensor_period)
+                         : r.steps == 0                         ? -1
+                                                                : int((r.steps - 1) / C.sensor_period);
         for (uint32_t e = lane; e < uint32_t(K) * POOL; e += G) {
             const int j = int(e / POOL), b = int(e % POOL);
             const int f = last - j;
@@ -433,13 +441,15 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     group_sync();
 
     for (uint32_t t = 0; t < a.count; t++) {
-        const uint32_t tick = t % a.horizon;
+        const uint32_t tick = X ? (a.tick0 + t) % a.horizon : t % a.horizon;
         const size_t row = size_t(tick) * N + nn;
         const bool active = live && !(C.eval && r.episodes);
+        // depth and observation of this tick still to do
+        const bool observe = !X || t != 0 || !(a.split & SPLIT_BEGIN_AT_ACT);
         const uint32_t count = min(float_bits(world[160]), 16u);  // slots of WWorld
 
         // ---- obstacle centres at the current time (world.hpp:32-41)
-        if (active)
+        if (active && observe)
             for (uint32_t i = lane; i < count; i += G) {
                 const V c = obstacle_center(world + 10 * i, r.elapsed);
                 s_cent[grp][3 * i] = c.x; s_cent[grp][3 * i + 1] = c.y; s_cent[grp][3 * i + 2] = c.z;
@@ -450,7 +460,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         // its pooled 2x2 blocks and keeps their minimum
         float R[9];
         rotation(s.q, R);
-        if (active && r.steps % C.sensor_period == 0) {
+        if (active && observe && r.steps % C.sensor_period == 0) {
             const uint32_t fidx = r.steps / C.sensor_period;
             const uint32_t slot8 = fidx % 8, slotk = fidx % K;
             const float mx = 0.0f;
@@ -502,7 +512,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         const uint32_t prev = frame > 0 ? frame - 1 : 0;
         const bool have = available >= sdelay;
         float* og = a.obs + row * OBS;
-        if (active) {
+        if (active && observe) {
             for (uint32_t b = lane; b < POOL; b += G) {
                 const float cur = have ? s_ring[grp][(frame % K) * POOL + b] / 12.0f : 1.0f;
                 const float pre = have ? s_ring[grp][(prev % K) * POOL + b] / 12.0f : 1.0f;
@@ -563,9 +573,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 if (j % G == int(lane)) { s_co[grp][j] = cob[j]; cg[j] = cob[j]; }
         }
         group_sync();
+        if (X && t + 1 == a.count && (a.split & SPLIT_END_AFTER_OBSERVE)) break;
 
         // ---- actor and critic hidden layers (ppo.hpp:65-72, 82-89)
-        if constexpr (W > 1) {  // all 32 envs of the workgroup on the matrix cores
+        if constexpr (X) {
+            // means come from the caller's policy
+        } else if constexpr (W > 1) {  // all 32 envs of the workgroup on the matrix cores
             static_assert(E == 32, "matrix-core layers assume 32 envs per workgroup");
             __syncthreads();
             wg_layer<OBS, OBS + 4, HID + 1>(&s_obs[0][0], AW1, A + a_b1, &s_ah[0][0]);
@@ -605,8 +618,11 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         // ---- act (sim.metal:229-256): means, value, sample, log-prob, command
         float a_cmd[4] = {0, 0, 0, 0};
         if (active) {
-            float mean[4], value;
-            if constexpr (W > 1) {
+            float mean[4], value = 0.0f;
+            if constexpr (X) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) mean[q] = a.ext_means[row * 4 + q];
+            } else if constexpr (W > 1) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) mean[q] = s_x[grp][q];
                 value = s_x[grp][4];
@@ -626,7 +642,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             float lp = 0, act[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float ls = A[a_ls + j];
+                const float ls = X ? a.ext_log_std[j] : A[a_ls + j];
                 act[j] = mean[j] + ((C.mode == 0 || C.mode == 22) ? exp_f(ls) * normal_draw(rng) : 0.0f);
                 if (C.mode == 1) act[j] = normal_draw(rng);
                 const float diff = (act[j] - mean[j]) * exp_f(-ls);
@@ -649,7 +665,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
                 for (int j = 0; j < 4; j++) a.actions[row * 4 + j] = act[j];
                 a.logp[row] = lp;
-                a.values[row] = value;
+                if constexpr (!X) a.values[row] = value;
                 const uint32_t slot = r.steps % 8;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
@@ -810,7 +826,9 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 ended = !C.eval;
             }
         }
-        if constexpr (W > 1) {  // next value: critic hidden of s' for all 32 envs
+        if constexpr (X) {
+            // next values are the caller's (from the stored next critic observations)
+        } else if constexpr (W > 1) {  // next value: critic hidden of s' for all 32 envs
             __syncthreads();
             wg_layer<COBS, COBS + 1, HID + 1>(&s_co[0][0], a.critic_w1t, CR + c_b1, &s_ch[0][0]);
             __syncthreads();
@@ -836,15 +854,17 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         }
         uint32_t reset_rng = 0, reset_family = 0, reset_seed = 0;
         if (active) {
-            float value;
-            if constexpr (W > 1) {
-                value = s_x[grp][4];
-            } else {
-                value = CR[c_b2];
+            if constexpr (!X) {
+                float value;
+                if constexpr (W > 1) {
+                    value = s_x[grp][4];
+                } else {
+                    value = CR[c_b2];
 #pragma unroll 8
-                for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
+                    for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
+                }
+                if (lane == 0) a.next_values[row] = value;
             }
-            if (lane == 0) a.next_values[row] = value;
             if (ended) {
                 reset_rng = r.rng;
                 reset_draw(C, nn, false, reset_rng, reset_family, reset_seed);
@@ -901,17 +921,19 @@ hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream) {
 // weights in LDS (32 envs, 159 KB of LDS, one workgroup per CU); the ring of
 // the other slot counts leaves no room for that, so they run one wavefront per
 // workgroup with the weights in L1/L2.
+// Split ticks (a->ext_means set) are built for 8 lanes per env only.
 hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, hipStream_t stream) {
-#define NAV_ROLLOUT_CASE(G, K, W)                                                                         \
-    if (lanes_per_env == G && ring_slots == K) {                                                          \
+#define NAV_ROLLOUT_CASE(G, K, W, X)                                                                      \
+    if (lanes_per_env == G && ring_slots == K && (a->ext_means != nullptr) == X) {                        \
         const uint32_t envs_per_block = 64 * W / G;                                                       \
         const uint32_t blocks = (a->cfg.n + envs_per_block - 1) / envs_per_block;                         \
-        hipLaunchKernelGGL((nav::rollout_kernel<G, K, W>), dim3(blocks), dim3(64 * W), 0, stream, *a);    \
+        hipLaunchKernelGGL((nav::rollout_kernel<G, K, W, X>), dim3(blocks), dim3(64 * W), 0, stream, *a); \
         return hipGetLastError();                                                                         \
     }
-    NAV_ROLLOUT_CASE(8, 2, 4) NAV_ROLLOUT_CASE(8, 4, 1) NAV_ROLLOUT_CASE(8, 8, 1)
-    NAV_ROLLOUT_CASE(16, 2, 1) NAV_ROLLOUT_CASE(16, 4, 1) NAV_ROLLOUT_CASE(16, 8, 1)
-    NAV_ROLLOUT_CASE(4, 2, 1) NAV_ROLLOUT_CASE(4, 4, 1) NAV_ROLLOUT_CASE(4, 8, 1)
+    NAV_ROLLOUT_CASE(8, 2, 4, false) NAV_ROLLOUT_CASE(8, 4, 1, false) NAV_ROLLOUT_CASE(8, 8, 1, false)
+    NAV_ROLLOUT_CASE(16, 2, 1, false) NAV_ROLLOUT_CASE(16, 4, 1, false) NAV_ROLLOUT_CASE(16, 8, 1, false)
+    NAV_ROLLOUT_CASE(4, 2, 1, false) NAV_ROLLOUT_CASE(4, 4, 1, false) NAV_ROLLOUT_CASE(4, 8, 1, false)
+    NAV_ROLLOUT_CASE(8, 2, 4, true) NAV_ROLLOUT_CASE(8, 4, 1, true) NAV_ROLLOUT_CASE(8, 8, 1, true)
 #undef NAV_ROLLOUT_CASE
     return hipErrorInvalidValue;
 }

@@ -233,6 +233,17 @@ class LargePPOTrainer:
         """logp of the stored actions and values at s and s' under this policy."""
         check(lib().mdn_lppo_evaluate(self.h))
 
+    def collect(self, count=0):
+        """Sim::collect with this policy acting every tick (0 = horizon ticks);
+        values at s and s' from this critic."""
+        check(lib().mdn_lppo_collect(self.h, count))
+
+    def means(self):
+        """Actor means [rows][4] of the last collect or evaluate."""
+        out = np.zeros(self.sim.horizon * self.sim.n * 4, np.float32)
+        check(lib().mdn_lppo_means(self.h, ptr(out), out.size))
+        return out
+
     def rollout_update(self, rollout_index):
         check(lib().mdn_lppo_rollout_update(self.h, rollout_index))
 

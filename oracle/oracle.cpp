@@ -411,7 +411,10 @@ struct Trainer {
         const size_t row = size_t(tick) * cfg.n + n;
         float hidden[8192];
         float mean[4];
-        actor_forward(shape, actor.data(), &obs[row * shape.obs], hidden, mean);
+        if (ext_means)  // means supplied from outside (a policy evaluated elsewhere)
+            for (int j = 0; j < 4; j++) mean[j] = ext_means[row * 4 + j];
+        else
+            actor_forward(shape, actor.data(), &obs[row * shape.obs], hidden, mean);
         values[row] = critic_forward(shape, critic.data(), &co[row * shape.critic_obs], hidden);
         const float* log_std = &actor[shape.actor_log_std()];
         uint32_t rng = run.rng;
@@ -710,6 +713,11 @@ struct Trainer {
             for (int k = 0; k < 4; k++) metric_mean[k] /= float(order.size());
     }
 
+    // Means [T][N][4] that act() uses in place of the actor's forward pass
+    // (nullptr: the actor).  The sampling, log-probability and everything
+    // downstream are unchanged (sim.metal:229-256 with mean given).
+    const float* ext_means = nullptr;
+
     // A policy of hidden width h (ppo.hpp:17-45 FIXED_PPO_HIDDEN_DIM) in
     // place of the current one: fresh initialisation, zero Adam moments.
     void set_hidden(uint32_t h) {
@@ -773,6 +781,7 @@ void orc_trainer_minibatch_grads(void* h, uint32_t begin, uint32_t b, float* act
 void orc_trainer_set_config(void* h, const MdnSimConfig* cfg) { static_cast<Trainer*>(h)->cfg = *cfg; }
 void orc_trainer_set_hidden(void* h, uint32_t hidden) { static_cast<Trainer*>(h)->set_hidden(hidden); }
 void orc_trainer_evaluate(void* h) { static_cast<Trainer*>(h)->evaluate(); }
+void orc_trainer_set_ext_means(void* h, const float* means) { static_cast<Trainer*>(h)->ext_means = means; }
 uint64_t orc_trainer_optimizer_step(void* h) { return static_cast<Trainer*>(h)->optimizer_step; }
 void orc_trainer_metric_mean(void* h, float* out) {
     for (int k = 0; k < 4; k++) out[k] = static_cast<Trainer*>(h)->metric_mean[k];

@@ -51,6 +51,7 @@ def oracle():
         _sig(lib, "orc_trainer_set_config", None, P, P)
         _sig(lib, "orc_trainer_set_hidden", None, P, U32)
         _sig(lib, "orc_trainer_evaluate", None, P)
+        _sig(lib, "orc_trainer_set_ext_means", None, P, P)
         _sig(lib, "orc_trainer_minibatch_grads", None, P, U32, U32, P, P, P, P, P, P)
         _sig(lib, "orc_trainer_optimizer_step", U64, P)
         _sig(lib, "orc_trainer_metric_mean", None, P, P)
@@ -206,6 +207,11 @@ class OracleTrainer:
     def evaluate(self):
         """logp / values / next_values of the stored rollout under the policy."""
         self.lib.orc_trainer_evaluate(self.h)
+
+    def set_ext_means(self, means):
+        """Means [T*N*4] used by act() in place of the actor (None: the actor)."""
+        self._ext_means = None if means is None else np.ascontiguousarray(means, np.float32)
+        self.lib.orc_trainer_set_ext_means(self.h, None if means is None else ptr(self._ext_means))
 
     def iteration(self, rollout_index):
         self.lib.orc_trainer_iteration(self.h, rollout_index)

@@ -24,6 +24,7 @@ pytestmark = pytest.mark.gpu
 
 LOGP_TOL = 5e-2    # abs, sum over 4 action dims of (a - mu)^2 / sigma^2 terms; sigma = e^-1
 VALUE_TOL = 2e-2   # abs
+MEAN_TOL = 1e-2    # abs, actor means (bf16 inputs and first-layer weights, fp32 accumulation)
 
 
 def say(*args):
@@ -76,3 +77,55 @@ def test_wide_policy_against_oracle(hidden):
     say("  metric means gpu", m_gpu, "oracle", m_ora)
     assert np.all(np.isfinite(m_gpu))
     assert np.abs(m_gpu - m_ora).max() <= 1e-2 + 1e-2 * np.abs(m_ora).max()
+
+
+@pytest.mark.parametrize("variant", ["static", "threat_mix_delays", "sensor_period2"])
+def test_wide_policy_closed_loop(variant):
+    """Sim::collect with the wide actor choosing every action (split ticks:
+    env kernel up to the observation, wide forward, env kernel from act).
+
+    The env step is checked bit for bit against the oracle driven by the same
+    means (the oracle's act() takes them in place of its own forward pass);
+    the means themselves against the oracle's fp32 forward of the same
+    observation rows at bf16 tolerance, and the values at s and s' likewise.
+    Two collects in a row cover the hand-over at a collect boundary; resets
+    happen inside the split launches (max_steps below the ticks run)."""
+    from gpu_compare import ENV_BUFFERS, compare
+    from oracle_lib import oracle, ptr
+
+    hidden, T = 256, 24
+    kw = dict(n=64, family=1, speed=1.0, distance=3.0, max_steps=25)
+    if variant == "threat_mix_delays":  # 4 ring slots: the one-wavefront kernel
+        kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=2, max_steps=30)
+    elif variant == "sensor_period2":   # a frame every other tick, one frame of delay
+        kw.update(sensor_period=2, sensor_delay=1, command_delay=1)
+    say("case: wide closed loop %s hidden=%d N=64 T=%d, two collects" % (variant, hidden, T))
+    cfg = config(**kw)
+    sim, _, ora = make_pair(cfg, T, epochs=1, minibatch=1024)
+    lp = LargePPOTrainer(sim, hidden, epochs=1, minibatch=1024)
+    ora.set_hidden(hidden)
+    actor = lp.get("actor")
+    assert np.array_equal(actor, ora.get("actor"))
+    exact = ["obs", "critic_obs", "next_critic_obs", "actions", "logp", "rewards", "terminated", "truncated"]
+    for rollout in range(2):
+        lp.collect()
+        sim.sync()
+        means = lp.means()
+        obs = np.ascontiguousarray(sim.get("obs"), np.float32)
+        rows = obs.size // 181
+        want = np.zeros(rows * 4, np.float32)
+        scratch = np.zeros(rows * hidden, np.float32)
+        oracle().orc_actor_forward_batch(ptr(actor), ptr(obs), 181, hidden, rows, ptr(scratch), ptr(want))
+        merr = float(np.abs(means.astype(np.float64) - want).max())
+        ora.set_ext_means(means)
+        ora.collect()
+        ora.set_ext_means(None)
+        bad = compare(sim, ora, ENV_BUFFERS + exact, tol=0.0)
+        verr = {name: float(np.abs(sim.get(name).astype(np.float64) - ora.get(name)).max())
+                for name in ("values", "next_values")}
+        say("  collect %d: means max |gpu - fp32| %.3g, values %s, episodes %d" %
+            (rollout, merr, verr, int(ora.get("runs")["episodes"].sum())))
+        assert not bad, (rollout, bad)
+        assert merr <= MEAN_TOL, merr
+        assert verr["values"] <= VALUE_TOL and verr["next_values"] <= VALUE_TOL, verr
+    assert ora.get("runs")["episodes"].sum() > 0

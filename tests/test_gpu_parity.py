@@ -120,7 +120,7 @@ def test_rollout_parity(lanes):
 
 
 @pytest.mark.parametrize("variant", ["delays_wind_noise", "eval", "movers3", "mixed6", "rehearsal13",
-                                     "goal_script", "threat_mix_delays"])
+                                     "goal_script", "threat_mix_delays", "sensor_period2"])
 def test_rollout_parity_variants(variant):
     kw = dict(n=48, family=1, speed=1.0, distance=3.0, max_steps=30)
     if variant == "delays_wind_noise":
@@ -135,6 +135,8 @@ def test_rollout_parity_variants(variant):
         kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=1, wind=0.5)
     elif variant == "threat_mix_delays":  # moving-threat mix with 100 ms sensor and command delays
         kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=2, max_steps=60)
+    elif variant == "sensor_period2":  # a depth frame every other tick, one frame of sensor delay
+        kw.update(sensor_period=2, sensor_delay=1, command_delay=1)
     elif variant == "goal_script":
         kw.update(mode=2, family=0, eval=1, speed=0.5, distance=4.0, max_steps=200)
     say("case: rollout variant %s" % variant)
