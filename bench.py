@@ -94,9 +94,10 @@ def traffic_from_profile():
 
 
 def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatch=32768):
-    """Rollout (small-policy behaviour actions) + wide-policy evaluation of the
-    rollout + wide-policy PPO update; roofline of the wide-policy GEMMs against
-    the dense bf16 matrix-core peak."""
+    """Closed-loop rollout with the wide actor choosing every action (split
+    ticks: env kernel, wide forward of the tick's rows, env kernel) and wide
+    critic values, then the wide-policy PPO update; roofline of the
+    wide-policy GEMMs against the dense bf16 matrix-core peak."""
     from mdnav import LargePPOTrainer, Sim, abi
     N, T = envs, horizon
     cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0)
@@ -105,8 +106,7 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
     lp = LargePPOTrainer(sim, hidden, epochs, minibatch)
     it = 0
     for _ in range(args.warmup):
-        sim.collect()
-        lp.evaluate()
+        lp.collect()
         lp.rollout_update(it)
         it += 1
     sim.sync()
@@ -116,8 +116,7 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
     steps = max(1, min(args.steps, 3))
     t0 = time.perf_counter()
     for _ in range(steps):
-        sim.collect()
-        lp.evaluate()
+        lp.collect()
         lp.rollout_update(it)
         it += 1
     gpu_s = sim.sync()
@@ -128,7 +127,7 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
         kernels[name] = {"total_ms": round(ms, 3), "launches": n}
     rows = N * T
     P = (181 * hidden + hidden + 4 * hidden + 8) + (32 * hidden + 2 * hidden + 1)
-    # algorithmic FLOP: evaluation 2P per row (actor at s, critic at s and s'); update per row per epoch:
+    # algorithmic FLOP: rollout 2P per row (actor at s, critic at s and s'); update per row per epoch:
     # forward 2P, first/second-layer weight gradients 2P (the backward's recomputed forward is not counted)
     flop_eval = 2.0 * rows * (P + (32 * hidden + 2 * hidden + 1))
     flop_fwd = 2.0 * rows * epochs * P
@@ -145,7 +144,7 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
         "config": {"workload": "large actor: %d envs x %d ticks, actor 181-%d-4 and critic 32-%d-1, "
                                "%d epochs x %d minibatches of %d" % (N, T, hidden, hidden, epochs, rows // minibatch,
                                                                      minibatch),
-                   "behaviour_actions": "small-policy rollout kernel; the wide policy re-evaluates logp and values"},
+                   "behaviour_actions": "wide actor in the loop every tick; wide critic values at s and s'"},
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(achieved / 2.5e15, 4), "traffic": None,
                      "kernel": "wide-policy forward + backward GEMM kernels (bf16 dense peak 2.5 PFLOP/s)",
@@ -166,10 +165,10 @@ def main():
                     help="baseline: 1 epoch x 4 minibatches; reference: 2 epochs x 256-row minibatches")
     ap.add_argument("--lanes", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["small", "large"], default="small",
+    ap.add_argument("--workload", choices=["small", "large", "stress"], default="small",
                     help="small: 8,192 envs x 128 ticks, 181-64-4 actor (the headline metric); large: 8,192 envs x "
                          "256 ticks, 181-5120-4 actor and 32-5120-1 critic on bf16 matrix cores, 4 epochs x 64 "
-                         "minibatches of 32,768")
+                         "minibatches of 32,768; stress: 65,536 envs x 128 ticks, small actor")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="BYTES",
                     help="run only the plain copy kernel over BYTES (reads BYTES, writes BYTES per launch); "
                          "its FETCH_SIZE/WRITE_SIZE readings scale the rollout kernel's counters to bytes")
@@ -187,7 +186,10 @@ def main():
         return
 
     from mdnav import PPOTrainer, Sim, abi
+    if args.workload == "stress":
+        args.envs, args.horizon, args.no_cpu_baseline = 65536, 128, True
     N, T = args.envs, args.horizon
+    headline = (N, T) == (8192, 128)
     epochs, minibatch = (1, N * T // 4) if args.schedule == "baseline" else (2, 256)
     cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0)
     log("bench: creating sim N=%d T=%d schedule=%s" % (N, T, args.schedule))
@@ -222,7 +224,7 @@ def main():
     avg_s = roll["avg_ms"] * 1e-3
     achieved = FLOP_ENV_STEP * env_steps_launch / avg_s
     roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic_from_profile(),
+                "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic_from_profile() if headline else None,
                 "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)",
                 "kernel": "rollout_kernel (fused env step + rollout actor/critic, %d ticks per launch)" % T,
                 "roof_note": "fp32 compute roof: env step on the VALU, policy/critic layers and RAPTOR dense/GRU "
@@ -241,7 +243,8 @@ def main():
 
     value = N * T * args.steps / wall
     out = {
-        "metric": "env-steps/sec (rollout+PPO update) at 8,192 envs; HBM GB/s and MFMA util %",
+        "metric": ("env-steps/sec (rollout+PPO update) at 8,192 envs; HBM GB/s and MFMA util %" if headline else
+                   "env-steps/sec (rollout+PPO update) at %d envs x %d ticks" % (N, T)),
         "value": round(value, 1), "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32",

@@ -737,6 +737,7 @@ struct MdnLargePPO {
     __bf16 *awb = nullptr, *cwb = nullptr;
     __bf16 *xa = nullptr, *xaT = nullptr, *xc = nullptr, *xcT = nullptr;  // bf16 rows of one minibatch
     float* eval_means = nullptr;                         // [rows][4]
+    float* fwd_part = nullptr;                           // forward partial sums over hidden slices
     float *means = nullptr, *values = nullptr, *dm = nullptr, *dls = nullptr, *dv = nullptr, *loss = nullptr;
     float *part = nullptr, *ga = nullptr, *gc = nullptr, *col_part = nullptr, *scratch = nullptr;
     double* norm_part = nullptr;
@@ -765,7 +766,7 @@ hipError_t lp_forward_rows(MdnLargePPO* p, const float* obs, const float* co, ui
         if (e == hipSuccess)
             e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, p->hidden, b,
                                   means ? means + size_t(r0) * 4 : nullptr, values ? values + r0 : nullptr,
-                                  s->stream);
+                                  p->fwd_part, s->stream);
     }
     return e;
 }
@@ -790,7 +791,7 @@ void mdn_lppo_destroy(MdnLargePPO* p) {
     if (!p) return;
     if (p->sim) hipStreamSynchronize(p->sim->stream);
     void* bufs[] = {p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->xa, p->xaT, p->xc, p->xcT,
-                    p->eval_means, p->means,
+                    p->eval_means, p->fwd_part, p->means,
                     p->values, p->dm, p->dls, p->dv, p->loss, p->part, p->ga, p->gc, p->col_part, p->scratch,
                     p->norm_part, p->norm_stats, p->metric_rows, p->metric_mean};
     for (void* b : bufs)
@@ -832,6 +833,7 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     guard(dev_alloc(&p->xc, MP * 32));
     guard(dev_alloc(&p->xcT, MP * 32));
     guard(dev_alloc(&p->eval_means, R * 4));
+    guard(dev_alloc(&p->fwd_part, size_t(lp_forward_part_floats(p->minibatch))));
     guard(dev_alloc(&p->means, M * 4));
     guard(dev_alloc(&p->values, M));
     guard(dev_alloc(&p->dm, M * 4));
@@ -954,7 +956,7 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
             hipError_t e = lp_launch_prep(obs, co, b, p->xa, p->xaT, p->xc, p->xcT, true, s->stream);
             if (e == hipSuccess)
                 e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, H, b, p->means, p->values,
-                                      s->stream);
+                                      p->fwd_part, s->stream);
             if (e == hipSuccess)
                 e = lp_launch_loss(p->means, p->values, s->actions + size_t(begin) * 4, s->logp + begin,
                                    s->advantages + begin, s->returns + begin, p->actor + p->shape.actor_log_std(), b,

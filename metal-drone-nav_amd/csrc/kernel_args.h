@@ -104,7 +104,8 @@ hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, __bf16*
                           __bf16* xcT, bool transposed, hipStream_t st);
 hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* awb, const __bf16* cwb,
                              const float* actor, const float* critic, uint32_t H, uint32_t B, float* means,
-                             float* values, hipStream_t st);
+                             float* values, float* part, hipStream_t st);
+uint64_t lp_forward_part_floats(uint32_t B);
 hipError_t lp_launch_logp(const float* means, const float* actions, const float* log_std, uint32_t B, float* logp,
                           hipStream_t st);
 hipError_t lp_launch_loss(const float* means, const float* values, const float* actions, const float* old_logp,

@@ -99,62 +99,128 @@ __global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ W, 
 // ---------------------------------------------------------------- forward
 // out[row][q] = b2[q] + sum_u W2[q][u] tanh(b1[u] + sum_k W1[u][k] X[row][k])
 // for q < NQ (actor means: NQ = 4 over W2 [4][H]; critic value: NQ = 1).
-// A workgroup owns RB rows and walks the hidden units in tiles of UT; the
-// second layer runs from LDS with one (row, output) per thread.
-template <uint32_t D, uint32_t K, uint32_t NQ>
-__global__ __launch_bounds__(256, 2) void forward_kernel(const __bf16* __restrict__ Xb, uint32_t BP,
+//
+// Both layers run on the matrix cores.  The first is computed transposed,
+// hT[unit][row] = W1 X^T (weights as the A operand, rows as B), so that a
+// wavefront's accumulator (lane -> row l%32, register r -> unit
+// 8(r/4) + 4(l/32) + r%4) is, rounded to bf16, already the B operand of the
+// second product zT[q][row] += W2[q][units] hT[units][row]: k slot
+// 8(l/32) + e of product m is register 8m + e, and the A operand holds W2
+// columns in that same unit order (rows q >= NQ zero).  A workgroup owns RB
+// rows; each wavefront takes 32 units of every 128-unit tile, keeps its rows'
+// fragments in registers, prefetches the next tile's weights and runs the
+// tile loop without barriers; the four wavefronts' partial sums meet once
+// in LDS.  blockIdx.y splits the hidden units into gridDim.y slices when
+// there are too few rows to fill the GPU: each slice writes part [S][BP][NQ]
+// and part_sum_kernel adds them in slice order.
+template <uint32_t K, uint32_t NQ>
+struct FwdTile {
+    bf8 w[K / 16];  // W1 rows of the wavefront's 32 units (A operand)
+    float4 bias[4]; // b1 of accumulator registers 4g .. 4g+3
+    float4 w2[4];   // W2[q = l%32][the same units] (zero for q >= NQ)
+};
+
+template <uint32_t K, uint32_t NQ>
+__device__ __forceinline__ void fwd_load(FwdTile<K, NQ>& f, const __bf16* __restrict__ Wb, const float* __restrict__ b1,
+                                         const float* __restrict__ W2, uint32_t H, uint32_t ub, uint32_t l) {
+    const uint32_t half = l / 32, lr = l % 32;
+#pragma unroll
+    for (uint32_t ks = 0; ks < K / 16; ks++)
+        f.w[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(ub + lr) * K + 16 * ks + 8 * half);
+    const float* w2row = W2 + size_t(min(lr, NQ - 1)) * H;
+#pragma unroll
+    for (uint32_t g = 0; g < 4; g++) {
+        const uint32_t u = ub + 8 * g + 4 * half;
+        f.bias[g] = *reinterpret_cast<const float4*>(b1 + u);
+        const float4 v = *reinterpret_cast<const float4*>(w2row + u);
+        f.w2[g] = lr < NQ ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+}
+
+template <uint32_t K, uint32_t NQ>
+__global__ __launch_bounds__(256, 1) void forward_kernel(const __bf16* __restrict__ Xb, uint32_t BP,
                                                       const __bf16* __restrict__ Wb,
                                                       const float* __restrict__ b1, const float* __restrict__ W2,
                                                       const float* __restrict__ b2, uint32_t H, uint32_t B,
-                                                      float* __restrict__ out) {
-    constexpr uint32_t XS = K + 8, HS = UT + 1;
-    __shared__ __bf16 xs[RB * XS];
-    __shared__ float hs[RB * HS];
-    __shared__ float w2s[NQ * UT];
-    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
+                                                      float* __restrict__ out, float* __restrict__ part) {
+    constexpr uint32_t KS = K / 16;
+    __shared__ float zs[4][RB * NQ];
+    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64, half = l / 32, lr = l % 32;
     const uint32_t r0 = blockIdx.x * RB;
-    stage_rows<K, XS, 1>(Xb, nullptr, BP, r0, xs, nullptr);
-    const uint32_t srow = t / NQ, q = t % NQ;  // second layer: thread -> (row, output), rows < RB
-    const bool second = srow < RB;
-    float z = 0.0f;
-    for (uint32_t u0 = 0; u0 < H; u0 += UT) {
-        const uint32_t unit = u0 + 32 * wv + l % 32;
-        const float bias = b1[unit];
-        bf8 bw[K / 16];
+    const uint32_t span = H / gridDim.y, h0 = blockIdx.y * span, h1 = h0 + span;
+    bf8 xf[RT][KS];  // B operand: X[row r0 + 32 rt + l%32][16 ks + 8(l/32) ..]
 #pragma unroll
-        for (uint32_t ks = 0; ks < K / 16; ks++)
-            bw[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + 16 * ks + 8 * (l / 32));
+    for (uint32_t rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (uint32_t ks = 0; ks < KS; ks++)
+            xf[rt][ks] = *reinterpret_cast<const bf8*>(Xb + size_t(r0 + 32 * rt + lr) * K + 16 * ks + 8 * half);
+    v16f z[RT];
+#pragma unroll
+    for (uint32_t rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (uint32_t r = 0; r < 16; r++) z[rt][r] = 0.0f;
+    FwdTile<K, NQ> cur;
+    fwd_load(cur, Wb, b1, W2, H, h0 + 32 * wv, l);
+    for (uint32_t u0 = h0; u0 < h1; u0 += UT) {
+        FwdTile<K, NQ> nxt;  // the last tile reloads itself (no conditional loads)
+        fwd_load(nxt, Wb, b1, W2, H, min(u0 + UT, h1 - UT) + 32 * wv, l);
         v16f acc[RT];
 #pragma unroll
         for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (uint32_t r = 0; r < 16; r++) acc[rt][r] = bias;
-        __syncthreads();  // rows staged; the previous tile's hs/w2s consumed
-#pragma unroll
-        for (uint32_t ks = 0; ks < K / 16; ks++) {
-            const uint32_t kb = 16 * ks + 8 * (l / 32);
-#pragma unroll
-            for (uint32_t rt = 0; rt < RT; rt++) {
-                const bf8 av = *reinterpret_cast<const bf8*>(xs + (32 * rt + l % 32) * XS + kb);
-                acc[rt] = mfma(av, bw[ks], acc[rt]);
+            for (uint32_t g = 0; g < 4; g++) {
+                acc[rt][4 * g] = cur.bias[g].x; acc[rt][4 * g + 1] = cur.bias[g].y;
+                acc[rt][4 * g + 2] = cur.bias[g].z; acc[rt][4 * g + 3] = cur.bias[g].w;
             }
+#pragma unroll
+        for (uint32_t ks = 0; ks < KS; ks++)
+#pragma unroll
+            for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = mfma(cur.w[ks], xf[rt][ks], acc[rt]);
+        bf8 wa[2];
+#pragma unroll
+        for (uint32_t m = 0; m < 2; m++) {
+            const float4 p = cur.w2[2 * m], q = cur.w2[2 * m + 1];
+            wa[m][0] = (__bf16)p.x; wa[m][1] = (__bf16)p.y; wa[m][2] = (__bf16)p.z; wa[m][3] = (__bf16)p.w;
+            wa[m][4] = (__bf16)q.x; wa[m][5] = (__bf16)q.y; wa[m][6] = (__bf16)q.z; wa[m][7] = (__bf16)q.w;
         }
 #pragma unroll
         for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (uint32_t r = 0; r < 16; r++)
-                hs[(32 * rt + acc_row(l, r)) * HS + 32 * wv + l % 32] = tanh_fast(acc[rt][r]);
-        for (uint32_t i = t; i < NQ * UT; i += 256) w2s[i] = W2[size_t(i / UT) * H + u0 + i % UT];
-        __syncthreads();
-        if (second) {
-            const float* hr = hs + srow * HS;
-            const float* wr = w2s + q * UT;
-#pragma unroll 16
-            for (uint32_t c = 0; c < UT; c++) z = fma_f(wr[c], hr[c], z);
-        }
+            for (uint32_t m = 0; m < 2; m++) {
+                bf8 hb;
+#pragma unroll
+                for (uint32_t e = 0; e < 8; e++) hb[e] = (__bf16)tanh_fast(acc[rt][8 * m + e]);
+                z[rt] = mfma(wa[m], hb, z[rt]);
+            }
+        cur = nxt;
     }
-    const uint32_t row = r0 + srow;
-    if (second && row < B) out[size_t(row) * NQ + q] = b2[q] + z;
+    // zT[q][row]: lanes 0-31, registers q < NQ
+    if (half == 0)
+#pragma unroll
+        for (uint32_t rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (uint32_t q = 0; q < NQ; q++) zs[wv][(32 * rt + lr) * NQ + q] = z[rt][q];
+    __syncthreads();
+    for (uint32_t i = t; i < RB * NQ; i += 256) {
+        const uint32_t row = r0 + i / NQ, q = i % NQ;
+        const float v = ((zs[0][i] + zs[1][i]) + zs[2][i]) + zs[3][i];
+        if (row >= B) continue;
+        if (gridDim.y == 1)
+            out[size_t(row) * NQ + q] = b2[q] + v;
+        else
+            part[(size_t(blockIdx.y) * BP + row) * NQ + q] = v;
+    }
+}
+
+// out[row][q] = b2[q] + the hidden slices' partial sums, in slice order.
+__global__ __launch_bounds__(256) void part_sum_kernel(const float* __restrict__ part, uint32_t S, uint32_t BP,
+                                                       uint32_t B, uint32_t NQ, const float* __restrict__ b2,
+                                                       float* __restrict__ out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= B * NQ) return;
+    float v = part[i];
+    for (uint32_t s = 1; s < S; s++) v += part[size_t(s) * BP * NQ + i];
+    out[i] = b2[i % NQ] + v;
 }
 
 // ---------------------------------------------------------------- loss
@@ -499,21 +565,45 @@ hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, __bf16*
     return hipGetLastError();
 }
 
-// Actor means [B][4] and critic values [B] of B prepared rows.
+// Actor means [B][4] and critic values [B] of B prepared rows.  When the
+// row blocks alone would leave CUs idle the hidden units are split in up to 8
+// slices; `part` then holds the slices' partial sums (capacity
+// lp_forward_part_floats(B)).
+static uint32_t forward_slices(uint32_t B, uint32_t H) {
+    const uint32_t blocks = (B + lp::RB - 1) / lp::RB, tiles = H / lp::UT;
+    uint32_t S = 1;
+    while (blocks * S < 256 && S < 8 && tiles % (2 * S) == 0) S *= 2;
+    return S;
+}
+
+uint64_t lp_forward_part_floats(uint32_t B) {
+    const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
+    return uint64_t(8) * BP * 4;
+}
+
 hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* awb, const __bf16* cwb,
                              const float* actor, const float* critic, uint32_t H, uint32_t B, float* means,
-                             float* values, hipStream_t st) {
+                             float* values, float* part, hipStream_t st) {
     if (B == 0) return hipSuccess;
     const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
-    const dim3 grid(BP / lp::RB);
+    const uint32_t S = forward_slices(B, H);
+    const dim3 grid(BP / lp::RB, S);
     const uint32_t A_B1 = H * lp::OBS, A_W2 = A_B1 + H, A_B2 = A_W2 + 4 * H;
     const uint32_t C_B1 = H * lp::COBS, C_W2 = C_B1 + H, C_B2 = C_W2 + H;
-    if (means)
-        hipLaunchKernelGGL((lp::forward_kernel<lp::OBS, lp::KA, 4>), grid, dim3(256), 0, st, xa, BP, awb, actor + A_B1,
-                           actor + A_W2, actor + A_B2, H, B, means);
-    if (values)
-        hipLaunchKernelGGL((lp::forward_kernel<lp::COBS, lp::KC, 1>), grid, dim3(256), 0, st, xc, BP, cwb,
-                           critic + C_B1, critic + C_W2, critic + C_B2, H, B, values);
+    if (means) {
+        hipLaunchKernelGGL((lp::forward_kernel<lp::KA, 4>), grid, dim3(256), 0, st, xa, BP, awb, actor + A_B1,
+                           actor + A_W2, actor + A_B2, H, B, means, part);
+        if (S > 1)
+            hipLaunchKernelGGL(lp::part_sum_kernel, dim3((B * 4 + 255) / 256), dim3(256), 0, st, part, S, BP, B, 4u,
+                               actor + A_B2, means);
+    }
+    if (values) {
+        hipLaunchKernelGGL((lp::forward_kernel<lp::KC, 1>), grid, dim3(256), 0, st, xc, BP, cwb, critic + C_B1,
+                           critic + C_W2, critic + C_B2, H, B, values, part);
+        if (S > 1)
+            hipLaunchKernelGGL(lp::part_sum_kernel, dim3((B + 255) / 256), dim3(256), 0, st, part, S, BP, B, 1u,
+                               critic + C_B2, values);
+    }
     return hipGetLastError();
 }
 

@@ -199,3 +199,22 @@ def test_production_path_bit_exact():
     bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v",
                              "metric_rows"] + ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
     assert not bad, bad
+
+
+def test_stress_scale_bit_exact():
+    """65,536 envs (the scale-stress env count: 2,048 workgroups of the
+    benchmark kernel), 4 ticks with episodes ending after 3 steps (resets at
+    scale) and one PPO iteration of four 65,536-row minibatches (256 chunks
+    each, the two-level gradient grouping): every buffer bit-identical to the
+    oracle."""
+    say("case: bit-exact N=65536 T=4 max_steps=3, 1 epoch x 4 minibatches of 65536")
+    cfg = config(n=65536, family=1, speed=1.0, distance=3.0, max_steps=3)
+    sim, ppo, ora = make_pair(cfg, 4, epochs=1, minibatch=65536)
+    sim.collect()
+    ppo.rollout_update(0)
+    sim.sync()
+    ora.iteration(0)
+    bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v",
+                             "metric_rows"] + ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
+    assert not bad, bad
+    assert ora.get("runs")["episodes"].sum() >= 65536
