@@ -730,7 +730,7 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon) {
 
 struct MdnLargePPO {
     MdnSim* sim = nullptr;
-    uint32_t hidden = 0, epochs = 1, minibatch = 0, updates = 0, chunks = 1;
+    uint32_t hidden = 0, epochs = 1, minibatch = 0, updates = 0;
     uint64_t optimizer_step = 0;
     mdn::PolicyShape shape;
     float *actor = nullptr, *critic = nullptr, *am = nullptr, *av = nullptr, *cm = nullptr, *cv = nullptr;
@@ -813,9 +813,6 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     p->minibatch = uint32_t(std::min<size_t>(minibatch, s->rows()));
     p->shape.hidden = p->shape.critic_hidden = hidden;
     p->updates = uint32_t((s->rows() + p->minibatch - 1) / p->minibatch) * epochs;
-    // row chunks of the backward: enough (hidden tile, chunk) workgroups for two per CU
-    const uint32_t tiles = hidden / 128, mb_blocks = (p->minibatch + 63) / 64;
-    p->chunks = std::max(1u, std::min(mb_blocks, (512 + tiles - 1) / tiles));
     const size_t A = p->shape.actor_count(), C = p->shape.critic_count(), M = p->minibatch, R = s->rows();
     int rc = MDN_OK;
     auto guard = [&](int r) { if (r != MDN_OK && rc == MDN_OK) rc = r; };
@@ -840,7 +837,7 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     guard(dev_alloc(&p->dls, M * 4));
     guard(dev_alloc(&p->dv, M));
     guard(dev_alloc(&p->loss, M * 4));
-    guard(dev_alloc(&p->part, size_t(p->chunks) * hidden * (OBS + 1 + 4 + COBS + 1 + 1)));
+    guard(dev_alloc(&p->part, size_t(lp_backward_part_floats(p->minibatch, hidden))));
     guard(dev_alloc(&p->ga, A));
     guard(dev_alloc(&p->gc, C));
     guard(dev_alloc(&p->col_part, ((M + 63) / 64) * 13));
@@ -966,7 +963,7 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
         if (rc) return rc;
         rc = timed(s, MDN_K_LP_BACKWARD, [&] {
             return lp_launch_backward(p->xa, p->xaT, p->xc, p->xcT, p->awb, p->cwb, p->actor, p->critic, p->dm, p->dls,
-                                      p->dv, p->loss, H, b, p->chunks, p->part, p->ga, p->gc, p->col_part, s->stream);
+                                      p->dv, p->loss, H, b, p->part, p->ga, p->gc, p->col_part, s->stream);
         });
         if (rc) return rc;
         ++p->optimizer_step;

@@ -17,6 +17,8 @@
 // D[8(r/4) + 4(l/32) + r%4][l%32].
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "mdnav_math.h"
 #include "mdnav_types.h"
 #include "kernel_args.h"
@@ -113,28 +115,54 @@ __global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ W, 
 // in LDS.  blockIdx.y splits the hidden units into gridDim.y slices when
 // there are too few rows to fill the GPU: each slice writes part [S][BP][NQ]
 // and part_sum_kernel adds them in slice order.
-template <uint32_t K, uint32_t NQ>
-struct FwdTile {
+template <uint32_t K>
+struct FwdW1 {
     bf8 w[K / 16];  // W1 rows of the wavefront's 32 units (A operand)
     float4 bias[4]; // b1 of accumulator registers 4g .. 4g+3
-    float4 w2[4];   // W2[q = l%32][the same units] (zero for q >= NQ)
 };
 
-template <uint32_t K, uint32_t NQ>
-__device__ __forceinline__ void fwd_load(FwdTile<K, NQ>& f, const __bf16* __restrict__ Wb, const float* __restrict__ b1,
-                                         const float* __restrict__ W2, uint32_t H, uint32_t ub, uint32_t l) {
+template <uint32_t K>
+__device__ __forceinline__ void fwd_load_w1(FwdW1<K>& f, const __bf16* __restrict__ Wb, const float* __restrict__ b1,
+                                            uint32_t ub, uint32_t l) {
     const uint32_t half = l / 32, lr = l % 32;
 #pragma unroll
     for (uint32_t ks = 0; ks < K / 16; ks++)
         f.w[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(ub + lr) * K + 16 * ks + 8 * half);
+#pragma unroll
+    for (uint32_t g = 0; g < 4; g++) f.bias[g] = *reinterpret_cast<const float4*>(b1 + ub + 8 * g + 4 * half);
+}
+
+// second-layer A operands of 32 units: W2[q = l%32][unit of k slot 8(l/32) + e] (zero for q >= NQ)
+template <uint32_t NQ>
+__device__ __forceinline__ void fwd_load_w2(bf8 (&wa)[2], const float* __restrict__ W2, uint32_t H, uint32_t ub,
+                                            uint32_t l) {
+    const uint32_t half = l / 32, lr = l % 32;
     const float* w2row = W2 + size_t(min(lr, NQ - 1)) * H;
 #pragma unroll
-    for (uint32_t g = 0; g < 4; g++) {
-        const uint32_t u = ub + 8 * g + 4 * half;
-        f.bias[g] = *reinterpret_cast<const float4*>(b1 + u);
-        const float4 v = *reinterpret_cast<const float4*>(w2row + u);
-        f.w2[g] = lr < NQ ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t m = 0; m < 2; m++) {
+        const float4 p = *reinterpret_cast<const float4*>(w2row + ub + 16 * m + 4 * half);
+        const float4 q = *reinterpret_cast<const float4*>(w2row + ub + 16 * m + 8 + 4 * half);
+        const bool on = lr < NQ;
+        wa[m][0] = (__bf16)(on ? p.x : 0.0f); wa[m][1] = (__bf16)(on ? p.y : 0.0f);
+        wa[m][2] = (__bf16)(on ? p.z : 0.0f); wa[m][3] = (__bf16)(on ? p.w : 0.0f);
+        wa[m][4] = (__bf16)(on ? q.x : 0.0f); wa[m][5] = (__bf16)(on ? q.y : 0.0f);
+        wa[m][6] = (__bf16)(on ? q.z : 0.0f); wa[m][7] = (__bf16)(on ? q.w : 0.0f);
     }
+}
+
+template <uint32_t K>
+__device__ __forceinline__ void fwd_first(v16f (&acc)[RT], const FwdW1<K>& f, const bf8 (&xf)[RT][K / 16]) {
+#pragma unroll
+    for (uint32_t rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (uint32_t g = 0; g < 4; g++) {
+            acc[rt][4 * g] = f.bias[g].x; acc[rt][4 * g + 1] = f.bias[g].y;
+            acc[rt][4 * g + 2] = f.bias[g].z; acc[rt][4 * g + 3] = f.bias[g].w;
+        }
+#pragma unroll
+    for (uint32_t ks = 0; ks < K / 16; ks++)
+#pragma unroll
+        for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = mfma(f.w[ks], xf[rt][ks], acc[rt]);
 }
 
 template <uint32_t K, uint32_t NQ>
@@ -159,30 +187,25 @@ __global__ __launch_bounds__(256, 1) void forward_kernel(const __bf16* __restric
     for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
         for (uint32_t r = 0; r < 16; r++) z[rt][r] = 0.0f;
-    FwdTile<K, NQ> cur;
-    fwd_load(cur, Wb, b1, W2, H, h0 + 32 * wv, l);
-    for (uint32_t u0 = h0; u0 < h1; u0 += UT) {
-        FwdTile<K, NQ> nxt;  // the last tile reloads itself (no conditional loads)
-        fwd_load(nxt, Wb, b1, W2, H, min(u0 + UT, h1 - UT) + 32 * wv, l);
-        v16f acc[RT];
-#pragma unroll
-        for (uint32_t rt = 0; rt < RT; rt++)
-#pragma unroll
-            for (uint32_t g = 0; g < 4; g++) {
-                acc[rt][4 * g] = cur.bias[g].x; acc[rt][4 * g + 1] = cur.bias[g].y;
-                acc[rt][4 * g + 2] = cur.bias[g].z; acc[rt][4 * g + 3] = cur.bias[g].w;
-            }
-#pragma unroll
-        for (uint32_t ks = 0; ks < KS; ks++)
-#pragma unroll
-            for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = mfma(cur.w[ks], xf[rt][ks], acc[rt]);
-        bf8 wa[2];
-#pragma unroll
-        for (uint32_t m = 0; m < 2; m++) {
-            const float4 p = cur.w2[2 * m], q = cur.w2[2 * m + 1];
-            wa[m][0] = (__bf16)p.x; wa[m][1] = (__bf16)p.y; wa[m][2] = (__bf16)p.z; wa[m][3] = (__bf16)p.w;
-            wa[m][4] = (__bf16)q.x; wa[m][5] = (__bf16)q.y; wa[m][6] = (__bf16)q.z; wa[m][7] = (__bf16)q.w;
-        }
+    // Software pipeline: the first layer of tile i+1 is issued before the
+    // activation and second layer of tile i, so the matrix cores work while
+    // the VALU evaluates tanh; weights are fetched two tiles ahead.  Tile
+    // indices past the slice are clamped (the extra work is discarded).
+    auto tile_unit = [&](uint32_t i) { return min(h0 + UT * i, h1 - UT) + 32 * wv; };
+    const uint32_t ntile = span / UT;
+    FwdW1<K> w1;
+    fwd_load_w1(w1, Wb, b1, tile_unit(0), l);
+    bf8 wa[2];
+    fwd_load_w2<NQ>(wa, W2, H, tile_unit(0), l);
+    v16f acc[RT];
+    fwd_first(acc, w1, xf);
+    fwd_load_w1(w1, Wb, b1, tile_unit(1), l);
+    for (uint32_t i = 0; i < ntile; i++) {
+        bf8 wn[2];
+        fwd_load_w2<NQ>(wn, W2, H, tile_unit(i + 1), l);
+        v16f nx[RT];
+        fwd_first(nx, w1, xf);
+        fwd_load_w1(w1, Wb, b1, tile_unit(i + 2), l);
 #pragma unroll
         for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
@@ -192,7 +215,10 @@ __global__ __launch_bounds__(256, 1) void forward_kernel(const __bf16* __restric
                 for (uint32_t e = 0; e < 8; e++) hb[e] = (__bf16)tanh_fast(acc[rt][8 * m + e]);
                 z[rt] = mfma(wa[m], hb, z[rt]);
             }
-        cur = nxt;
+#pragma unroll
+        for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = nx[rt];
+        wa[0] = wn[0];
+        wa[1] = wn[1];
     }
     // zT[q][row]: lanes 0-31, registers q < NQ
     if (half == 0)
@@ -292,126 +318,198 @@ __global__ __launch_bounds__(256) void logp_kernel(const float* __restrict__ mea
 }
 
 // ---------------------------------------------------------------- backward
-// Partial gradients of one (hidden tile, row chunk): the tile's hidden values
-// are recomputed from the rows, delta = (sum_q dm[row][q] W2[q][u]) (1 - h^2),
-// then dW1[u][k] += sum_rows delta[row][u] X[row][k] on the matrix cores (the
-// rows are the reduction dimension), db1[u] += sum delta, dW2[q][u] +=
-// sum dm[row][q] h[row][u].  Output: partial slot `c = blockIdx.y` of
-// dW1p [c][H][D], db1p [c][H], dW2p [c][NQ][H].  About 73 KB of LDS, so two
-// workgroups share a CU and one's matrix work overlaps the other's VALU work.
+// Partial gradients of one (hidden tile, row chunk).  Each wavefront owns 32
+// units of the workgroup's 128-unit tile (W1 rows resident in registers) and
+// walks the chunk's rows in blocks of RB, everything in one accumulator
+// layout (lane -> unit l%32, register r -> row 32 rt + 8(r/4) + 4(l/32) + r%4):
+//   h      = tanh(X W1^T + b1)            bf16 MFMA, rows as A (from LDS)
+//   g      = dm W2^T                      fp32 MFMA 32x32x2 (the fma chain over q)
+//   delta  = g (1 - h^2);  db1 += delta   VALU, per lane
+//   dW2^T += dm^T h                       bf16 MFMA, h from registers as B
+//   dW1   += delta^T X                    bf16 MFMA, delta from registers as A,
+//                                         X^T rows from LDS as B
+// The rows are the reduction dimension of the last two products; their k
+// slots follow the accumulator's row order (slot 8(l/32) + e of product m is
+// register 8m + e), and the LDS operands are read in that order.  Rows of the
+// next block are fetched into registers during the current block (two LDS
+// buffers, one barrier per block).  Rows past the chunk carry dm = 0 and
+// contribute nothing.  Output: partial slot c = blockIdx.y of dW1p [c][H][D],
+// db1p [c][H], dW2p [c][NQ][H].
+template <uint32_t K, uint32_t NQ>
+struct BwdStage {
+    static constexpr uint32_t XS = K + 8, TS = RB + 4;   // row strides (bf16) of xs and xt
+    static constexpr uint32_t XCH = RB * K / 8;          // 16-byte chunks of a block's rows
+    static constexpr uint32_t TCH = K * RB / 8;
+    static constexpr uint32_t NX = (XCH + 255) / 256, NT = (TCH + 255) / 256;
+    bf8 x[NX], xt[NT];
+    float d;
+};
+
+template <uint32_t K, uint32_t NQ>
+__device__ __forceinline__ void bwd_fetch(BwdStage<K, NQ>& f, const __bf16* __restrict__ Xb,
+                                          const __bf16* __restrict__ XbT, uint32_t BP, uint32_t r0, uint32_t rend,
+                                          const float* __restrict__ dm, uint32_t t) {
+    using S = BwdStage<K, NQ>;
+    constexpr uint32_t CH = K / 8;
+#pragma unroll
+    for (uint32_t i = 0; i < S::NX; i++) {
+        const uint32_t e = min(t + 256 * i, S::XCH - 1);
+        f.x[i] = *reinterpret_cast<const bf8*>(Xb + size_t(r0 + e / CH) * K + 8 * (e % CH));
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < S::NT; i++) {
+        const uint32_t e = min(t + 256 * i, S::TCH - 1);
+        f.xt[i] = *reinterpret_cast<const bf8*>(XbT + size_t(e / (RB / 8)) * BP + r0 + 8 * (e % (RB / 8)));
+    }
+    const uint32_t row = r0 + t / NQ;  // t < RB * NQ (256 threads cover RB * 4)
+    f.d = (t < RB * NQ && row < rend) ? dm[size_t(min(row, rend - 1)) * NQ + t % NQ] : 0.0f;
+}
+
+template <uint32_t K, uint32_t NQ>
+__device__ __forceinline__ void bwd_store(const BwdStage<K, NQ>& f, __bf16* xs, __bf16* xt, float* dmt, uint32_t t) {
+    using S = BwdStage<K, NQ>;
+    constexpr uint32_t CH = K / 8;
+    typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (uint32_t i = 0; i < S::NX; i++) {
+        const uint32_t e = t + 256 * i;
+        if (e < S::XCH) *reinterpret_cast<bf8*>(xs + (e / CH) * S::XS + 8 * (e % CH)) = f.x[i];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < S::NT; i++) {
+        const uint32_t e = t + 256 * i;
+        if (e < S::TCH) {
+            __bf16* dst = xt + (e / (RB / 8)) * S::TS + 8 * (e % (RB / 8));  // 8-byte aligned rows
+            const bf8 v = f.xt[i];
+            *reinterpret_cast<bf4*>(dst) = bf4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<bf4*>(dst + 4) = bf4{v[4], v[5], v[6], v[7]};
+        }
+    }
+    if (t < RB * NQ) dmt[(t % NQ) * RB + t / NQ] = f.d;  // transposed: dmt [q][row]
+}
+
 template <uint32_t D, uint32_t K, uint32_t NQ>
-__global__ __launch_bounds__(256, 2) void backward_kernel(const __bf16* __restrict__ Xb, const __bf16* __restrict__ XbT,
+__global__ __launch_bounds__(256, NQ == 1 ? 2 : 1) void backward_kernel(const __bf16* __restrict__ Xb, const __bf16* __restrict__ XbT,
                                                        uint32_t BP, const __bf16* __restrict__ Wb,
                                                        const float* __restrict__ b1, const float* __restrict__ W2,
                                                        const float* __restrict__ dm, uint32_t H, uint32_t B,
                                                        uint32_t RC, float* __restrict__ dW1p,
                                                        float* __restrict__ db1p, float* __restrict__ dW2p) {
-    constexpr uint32_t XS = K + 8, TS = RB + 8;
-    __shared__ __bf16 xs[RB * XS];   // [row][k]
-    __shared__ __bf16 xt[K * TS];    // [k][row]
-    __shared__ __bf16 dt[UT * TS];   // delta^T [unit][row]
-    __shared__ __attribute__((aligned(16))) float dms[RB * NQ];
-    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
+    using S = BwdStage<K, NQ>;
+    constexpr uint32_t XS = S::XS, TS = S::TS, JT = K / 32;
+    typedef float v2f __attribute__((ext_vector_type(2)));
+    __shared__ __bf16 xs[2][RB * XS];   // [row][k]
+    __shared__ __bf16 xt[2][K * TS];    // [k][row]
+    __shared__ __attribute__((aligned(16))) float dmt[2][NQ * RB];  // [q][row]
+    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64, half = l / 32, lr = l % 32;
     const uint32_t u0 = blockIdx.x * UT, c = blockIdx.y;
-    const uint32_t unit = u0 + 32 * wv + l % 32;
+    const uint32_t unit = u0 + 32 * wv + lr;
     const uint32_t rbeg = c * RC, rend = min(B, rbeg + RC);
-    float w2r[NQ];
-#pragma unroll
-    for (uint32_t q = 0; q < NQ; q++) w2r[q] = W2[size_t(q) * H + unit];
     const float bias = b1[unit];
-    bf8 bw[K / 16];  // this lane's weight fragments of the workgroup's hidden tile
+    bf8 bw[K / 16];  // B operand of h: W1[unit][16 ks + 8(l/32) ..]
 #pragma unroll
     for (uint32_t ks = 0; ks < K / 16; ks++)
-        bw[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + 16 * ks + 8 * (l / 32));
-    v16f gacc[K / 32];
+        bw[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + 16 * ks + 8 * half);
+    // B operand of g: W2[q = 2 p + l/32][unit] (zero for q >= NQ)
+    constexpr uint32_t NP = (NQ + 1) / 2;
+    float w2f[NP];
 #pragma unroll
-    for (uint32_t jt = 0; jt < K / 32; jt++)
+    for (uint32_t p = 0; p < NP; p++) {
+        const uint32_t q = 2 * p + half;
+        w2f[p] = q < NQ ? W2[size_t(min(q, NQ - 1)) * H + unit] : 0.0f;
+    }
+    v16f gacc[JT], w2acc;
+#pragma unroll
+    for (uint32_t jt = 0; jt < JT; jt++)
 #pragma unroll
         for (uint32_t r = 0; r < 16; r++) gacc[jt][r] = 0.0f;
-    float db1a = 0.0f, dw2a[NQ];
 #pragma unroll
-    for (uint32_t q = 0; q < NQ; q++) dw2a[q] = 0.0f;
-    for (uint32_t r0 = rbeg; r0 < rend; r0 += RB) {
-        __syncthreads();  // the previous block's LDS reads are done
-        stage_rows<K, XS, TS>(Xb, XbT, BP, r0, xs, xt);
-        for (uint32_t e = t; e < RB * NQ; e += 256) {
-            const uint32_t row = r0 + e / NQ;
-            dms[e] = row < rend ? dm[size_t(row) * NQ + e % NQ] : 0.0f;
-        }
-        __syncthreads();
-        v16f acc[RT];
+    for (uint32_t r = 0; r < 16; r++) w2acc[r] = 0.0f;
+    float db1a = 0.0f;
+
+    BwdStage<K, NQ> st;
+    if (rbeg < rend) {
+        bwd_fetch(st, Xb, XbT, BP, rbeg, rend, dm, t);
+        bwd_store(st, xs[0], xt[0], dmt[0], t);
+    }
+    uint32_t buf = 0;
+    for (uint32_t r0 = rbeg; r0 < rend; r0 += RB, buf ^= 1) {
+        __syncthreads();  // block r0 staged in buf; buf ^ 1 no longer read
+        const bool more = r0 + RB < rend;
+        if (more) bwd_fetch(st, Xb, XbT, BP, r0 + RB, rend, dm, t);
+        const __bf16* X = xs[buf];
+        const __bf16* XT = xt[buf];
+        const float* DM = dmt[buf];
 #pragma unroll
-        for (uint32_t rt = 0; rt < RT; rt++)
+        for (uint32_t rt = 0; rt < RT; rt++) {
+            v16f h;
 #pragma unroll
-            for (uint32_t r = 0; r < 16; r++) acc[rt][r] = bias;
+            for (uint32_t r = 0; r < 16; r++) h[r] = bias;
 #pragma unroll
-        for (uint32_t ks = 0; ks < K / 16; ks++) {
-            const uint32_t kb = 16 * ks + 8 * (l / 32);
-#pragma unroll
-            for (uint32_t rt = 0; rt < RT; rt++) {
-                const bf8 av = *reinterpret_cast<const bf8*>(xs + (32 * rt + l % 32) * XS + kb);
-                acc[rt] = mfma(av, bw[ks], acc[rt]);
+            for (uint32_t ks = 0; ks < K / 16; ks++) {
+                const bf8 av = *reinterpret_cast<const bf8*>(X + (32 * rt + lr) * XS + 16 * ks + 8 * half);
+                h = mfma(av, bw[ks], h);
             }
-        }
-        // lane l holds rows 8g + 4(l/32) + 0..3 (g = r/4) of unit l%32: four
-        // consecutive rows per group, stored to delta^T as one 8-byte write
+            v16f g;
 #pragma unroll
-        for (uint32_t rt = 0; rt < RT; rt++)
+            for (uint32_t r = 0; r < 16; r++) g[r] = 0.0f;
 #pragma unroll
-            for (uint32_t g4 = 0; g4 < 4; g4++) {
-                __attribute__((ext_vector_type(4))) __bf16 d4;
+            for (uint32_t p = 0; p < NP; p++) {
+                const uint32_t q = 2 * p + half;
+                const float a = q < NQ ? DM[min(q, NQ - 1) * RB + 32 * rt + lr] : 0.0f;
+                g = __builtin_amdgcn_mfma_f32_32x32x2f32(a, w2f[p], g, 0, 0, 0);
+            }
 #pragma unroll
-                for (uint32_t i = 0; i < 4; i++) {
-                    const uint32_t r = 4 * g4 + i, rr = 32 * rt + acc_row(l, r);
-                    const float h = tanh_fast(acc[rt][r]);
-                    float dq[NQ];
-                    if constexpr (NQ == 4) {
-                        const float4 v4 = *reinterpret_cast<const float4*>(dms + rr * 4);
-                        dq[0] = v4.x; dq[1] = v4.y; dq[2] = v4.z; dq[3] = v4.w;
-                    } else {
-                        dq[0] = dms[rr];
-                    }
-                    float gsum = 0.0f;
+            for (uint32_t m = 0; m < 2; m++) {
+                bf8 hb, db;
 #pragma unroll
-                    for (uint32_t q = 0; q < NQ; q++) {
-                        gsum = fma_f(dq[q], w2r[q], gsum);
-                        dw2a[q] = fma_f(dq[q], h, dw2a[q]);
-                    }
-                    const float delta = gsum * (1.0f - h * h);
-                    db1a += delta;
-                    d4[i] = (__bf16)delta;
+                for (uint32_t e = 0; e < 8; e++) {
+                    const float hv = tanh_fast(h[8 * m + e]);
+                    const float d = g[8 * m + e] * (1.0f - hv * hv);
+                    db1a += d;
+                    hb[e] = (__bf16)hv;
+                    db[e] = (__bf16)d;
                 }
-                const uint32_t rr0 = 32 * rt + acc_row(l, 4 * g4);
-                *reinterpret_cast<__attribute__((ext_vector_type(4))) __bf16*>(dt + (32 * wv + l % 32) * TS + rr0) = d4;
-            }
-        __syncthreads();
+                // rows of this product's k slots: 32 rt + 16 m + 4(l/32) + {0..3, 8..11}
+                const uint32_t rr = 32 * rt + 16 * m + 4 * half;
+                {   // dW2^T: A = dm^T [q][rows] (q = l%32, zero past NQ)
+                    const float* dq = DM + min(lr, NQ - 1) * RB + rr;
+                    const float4 v0 = *reinterpret_cast<const float4*>(dq);
+                    const float4 v1 = *reinterpret_cast<const float4*>(dq + 8);
+                    const bool on = lr < NQ;
+                    bf8 am;
+                    am[0] = (__bf16)(on ? v0.x : 0.0f); am[1] = (__bf16)(on ? v0.y : 0.0f);
+                    am[2] = (__bf16)(on ? v0.z : 0.0f); am[3] = (__bf16)(on ? v0.w : 0.0f);
+                    am[4] = (__bf16)(on ? v1.x : 0.0f); am[5] = (__bf16)(on ? v1.y : 0.0f);
+                    am[6] = (__bf16)(on ? v1.z : 0.0f); am[7] = (__bf16)(on ? v1.w : 0.0f);
+                    w2acc = mfma(am, hb, w2acc);
+                }
 #pragma unroll
-        for (uint32_t ks = 0; ks < RB / 16; ks++) {
-            const uint32_t kb = 16 * ks + 8 * (l / 32);
-            const bf8 av = *reinterpret_cast<const bf8*>(dt + (32 * wv + l % 32) * TS + kb);
-#pragma unroll
-            for (uint32_t jt = 0; jt < K / 32; jt++) {
-                const bf8 bv = *reinterpret_cast<const bf8*>(xt + (32 * jt + l % 32) * TS + kb);
-                gacc[jt] = mfma(av, bv, gacc[jt]);
+                for (uint32_t jt = 0; jt < JT; jt++) {  // dW1: B = X [rows][k = 32 jt + l%32]
+                    typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+                    const __bf16* src = XT + (32 * jt + lr) * TS + rr;
+                    const bf4 lo = *reinterpret_cast<const bf4*>(src), hi = *reinterpret_cast<const bf4*>(src + 8);
+                    const bf8 xb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    gacc[jt] = mfma(db, xb, gacc[jt]);
+                }
             }
         }
+        if (more) bwd_store(st, xs[buf ^ 1], xt[buf ^ 1], dmt[buf ^ 1], t);
     }
 #pragma unroll
-    for (uint32_t jt = 0; jt < K / 32; jt++) {
-        const uint32_t j = 32 * jt + l % 32;
+    for (uint32_t jt = 0; jt < JT; jt++) {
+        const uint32_t j = 32 * jt + lr;
         if (j < D)
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++)
                 dW1p[(size_t(c) * H + u0 + 32 * wv + acc_row(l, r)) * D + j] = gacc[jt][r];
     }
-    // lanes l and l + 32 hold the same unit
+    // lanes l and l + 32 hold the same unit; dW2^T[q][unit] sits in lanes 0-31, registers q
     db1a += __shfl_xor(db1a, 32, 64);
-#pragma unroll
-    for (uint32_t q = 0; q < NQ; q++) dw2a[q] += __shfl_xor(dw2a[q], 32, 64);
-    if (l < 32) {
+    if (half == 0) {
         db1p[size_t(c) * H + unit] = db1a;
 #pragma unroll
-        for (uint32_t q = 0; q < NQ; q++) dW2p[(size_t(c) * NQ + q) * H + unit] = dw2a[q];
+        for (uint32_t q = 0; q < NQ; q++) dW2p[(size_t(c) * NQ + q) * H + unit] = w2acc[q];
     }
 }
 
@@ -566,13 +664,14 @@ hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, __bf16*
 }
 
 // Actor means [B][4] and critic values [B] of B prepared rows.  When the
-// row blocks alone would leave CUs idle the hidden units are split in up to 8
+// row blocks alone would leave CUs short of two workgroups each, the hidden
+// units are split in up to 8
 // slices; `part` then holds the slices' partial sums (capacity
 // lp_forward_part_floats(B)).
 static uint32_t forward_slices(uint32_t B, uint32_t H) {
     const uint32_t blocks = (B + lp::RB - 1) / lp::RB, tiles = H / lp::UT;
     uint32_t S = 1;
-    while (blocks * S < 256 && S < 8 && tiles % (2 * S) == 0) S *= 2;
+    while (blocks * S < 512 && S < 8 && tiles % (2 * S) == 0) S *= 2;  // two workgroups per CU
     return S;
 }
 
@@ -627,38 +726,55 @@ hipError_t lp_launch_loss(const float* means, const float* values, const float* 
 // the flat gradients ga (actor layout) and gc (critic layout) and the
 // per-row column partials.  Scratch: part >= chunks * (H*(181+1+4) +
 // H*(32+1+1)) floats, col_part >= ceil(B/128) * 13.
+// Row chunks of the backward for B rows: the actor's (hidden tile, chunk)
+// workgroups fill one round at one per CU; the critic, whose blocks are light,
+// takes four times as many chunks and runs two workgroups per CU.
+void lp_backward_chunks(uint32_t B, uint32_t H, uint32_t* actor_chunks, uint32_t* critic_chunks) {
+    const uint32_t tiles = H / lp::UT, blocks = (B + lp::RB - 1) / lp::RB;
+    *actor_chunks = std::max(1u, std::min(blocks, 256 / tiles));
+    *critic_chunks = std::max(1u, std::min(blocks, 4 * (256 / tiles)));
+}
+
+uint64_t lp_backward_part_floats(uint32_t B, uint32_t H) {
+    uint32_t na, nc;
+    lp_backward_chunks(B, H, &na, &nc);
+    return uint64_t(na) * H * (lp::OBS + 1 + 4) + uint64_t(nc) * H * (lp::COBS + 1 + 1);
+}
+
 hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16* xc, const __bf16* xcT,
                               const __bf16* awb, const __bf16* cwb,
                               const float* actor, const float* critic, const float* dm, const float* dls,
-                              const float* dv, const float* loss, uint32_t H, uint32_t B, uint32_t chunks,
+                              const float* dv, const float* loss, uint32_t H, uint32_t B,
                               float* part, float* ga, float* gc, float* col_part, hipStream_t st) {
     if (B == 0) return hipSuccess;
     const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
-    const uint32_t RC = ((B + chunks - 1) / chunks + lp::RB - 1) / lp::RB * lp::RB;
-    const uint32_t nc = (B + RC - 1) / RC;
+    uint32_t ca, cc;
+    lp_backward_chunks(B, H, &ca, &cc);
+    auto rows_per = [&](uint32_t chunks) { return ((B + chunks - 1) / chunks + lp::RB - 1) / lp::RB * lp::RB; };
+    const uint32_t RA = rows_per(ca), RCc = rows_per(cc);
+    const uint32_t na = (B + RA - 1) / RA, nc = (B + RCc - 1) / RCc;
     const uint32_t A_B1 = H * lp::OBS, A_W2 = A_B1 + H;
     const uint32_t C_B1 = H * lp::COBS, C_W2 = C_B1 + H;
-    // partial slot layout: actor [nc][H*181], [nc][H], [nc][4][H]; critic [nc][H*32], [nc][H], [nc][1][H]
+    // partial slot layout: actor [na][H*181], [na][H], [na][4][H]; critic [nc][H*32], [nc][H], [nc][1][H]
     float* aW1 = part;
-    float* ab1 = aW1 + size_t(nc) * H * lp::OBS;
-    float* aW2 = ab1 + size_t(nc) * H;
-    float* cW1 = aW2 + size_t(nc) * 4 * H;
+    float* ab1 = aW1 + size_t(na) * H * lp::OBS;
+    float* aW2 = ab1 + size_t(na) * H;
+    float* cW1 = aW2 + size_t(na) * 4 * H;
     float* cb1 = cW1 + size_t(nc) * H * lp::COBS;
     float* cw2 = cb1 + size_t(nc) * H;
-    const dim3 grid(H / lp::UT, nc);
-    hipLaunchKernelGGL((lp::backward_kernel<lp::OBS, lp::KA, 4>), grid, dim3(256), 0, st, xa, xaT, BP, awb,
-                       actor + A_B1, actor + A_W2, dm, H, B, RC, aW1, ab1, aW2);
-    hipLaunchKernelGGL((lp::backward_kernel<lp::COBS, lp::KC, 1>), grid, dim3(256), 0, st, xc, xcT, BP, cwb,
-                       critic + C_B1, critic + C_W2, dv, H, B, RC, cW1, cb1, cw2);
-    auto sum = [&](const float* p, uint64_t n, float* out) {
-        hipLaunchKernelGGL(lp::sum_slots_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, p, n, nc, out);
+    hipLaunchKernelGGL((lp::backward_kernel<lp::OBS, lp::KA, 4>), dim3(H / lp::UT, na), dim3(256), 0, st, xa, xaT,
+                       BP, awb, actor + A_B1, actor + A_W2, dm, H, B, RA, aW1, ab1, aW2);
+    hipLaunchKernelGGL((lp::backward_kernel<lp::COBS, lp::KC, 1>), dim3(H / lp::UT, nc), dim3(256), 0, st, xc, xcT,
+                       BP, cwb, critic + C_B1, critic + C_W2, dv, H, B, RCc, cW1, cb1, cw2);
+    auto sum = [&](const float* p, uint64_t n, uint32_t slots, float* out) {
+        hipLaunchKernelGGL(lp::sum_slots_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, p, n, slots, out);
     };
-    sum(aW1, uint64_t(H) * lp::OBS, ga);
-    sum(ab1, H, ga + A_B1);
-    sum(aW2, 4ull * H, ga + A_W2);
-    sum(cW1, uint64_t(H) * lp::COBS, gc);
-    sum(cb1, H, gc + C_B1);
-    sum(cw2, H, gc + C_W2);
+    sum(aW1, uint64_t(H) * lp::OBS, na, ga);
+    sum(ab1, H, na, ga + A_B1);
+    sum(aW2, 4ull * H, na, ga + A_W2);
+    sum(cW1, uint64_t(H) * lp::COBS, nc, gc);
+    sum(cb1, H, nc, gc + C_B1);
+    sum(cw2, H, nc, gc + C_W2);
     hipLaunchKernelGGL(lp::column_part_kernel, dim3((B + lp::RB - 1) / lp::RB), dim3(256), 0, st, dm, dls, dv, loss, B,
                        col_part);
     return hipGetLastError();
