@@ -162,9 +162,12 @@ __device__ __forceinline__ float cast_ray(const float* world, const float* cente
 // min/max may differ from the select form only in the sign of a zero, which
 // the final fmax(0, best) of world.hpp:82 maps to +0, so depths are
 // bit-identical to cast_ray.
+// Slot 0: room; slots 1..8: boxes.  Slots past the world's count hold a
+// zero-size box at (1e30, 1e30, 1e30): a ray either misses it (1000) or hits
+// it beyond 1e22, so it never lowers a depth capped at 12 and the slab loop
+// needs no per-box test.
 struct BoxSlabs {
-    float A[9][3], B[9][3];  // slot 0: room, 1..8: boxes
-    uint32_t n;              // live boxes
+    float A[9][3], B[9][3];
 };
 __device__ __forceinline__ void make_box_slabs(const float* world, const float* centers, uint32_t count, V p,
                                                BoxSlabs& bs) {
@@ -174,15 +177,15 @@ __device__ __forceinline__ void make_box_slabs(const float* world, const float* 
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const float* o = world + 10 * i;
+        const bool live = uint32_t(i) < count;
         const float cc[3] = {centers[3 * i], centers[3 * i + 1], centers[3 * i + 2]};
         const float pp[3] = {p.x - cc[0], p.y - cc[1], p.z - cc[2]};
 #pragma unroll
         for (int j = 0; j < 3; j++) {
-            bs.A[i + 1][j] = -o[4 + j] - pp[j];
-            bs.B[i + 1][j] = o[4 + j] - pp[j];
+            bs.A[i + 1][j] = live ? -o[4 + j] - pp[j] : 1e30f;
+            bs.B[i + 1][j] = live ? o[4 + j] - pp[j] : 1e30f;
         }
     }
-    bs.n = count;
 }
 __device__ __forceinline__ bool boxes_only(const float* world, uint32_t count) {
     if (count > 8) return false;
@@ -202,12 +205,19 @@ __device__ __forceinline__ float slab_fast(const float (&A)[3], const float (&B)
     }
     return hi < __builtin_fmaxf(lo, 0.0f) ? 1000.0f : (lo >= 0 ? lo : hi);
 }
+// 1/d by the hardware reciprocal (v_rcp_f32) and one Newton step.  Over all
+// 2^32 floats this equals the correctly rounded 1.0f / d for every finite d
+// whose reciprocal is a normal number (|d| <= 2^126); the ray components here
+// satisfy 1e-8 <= |d| <= 1.
+__device__ __forceinline__ float recip_rn(float d) {
+    const float y = __builtin_amdgcn_rcpf(d);
+    return __builtin_fmaf(__builtin_fmaf(-d, y, 1.0f), y, y);
+}
 __device__ __forceinline__ float cast_ray_boxes(const BoxSlabs& bs, V d) {
-    const float inv[3] = {1.0f / d.x, 1.0f / d.y, 1.0f / d.z};
+    const float inv[3] = {recip_rn(d.x), recip_rn(d.y), recip_rn(d.z)};
     float best = __builtin_fminf(12.0f, slab_fast(bs.A[0], bs.B[0], inv));
 #pragma unroll
-    for (int i = 1; i < 9; i++)
-        if (uint32_t(i) <= bs.n) best = __builtin_fminf(best, slab_fast(bs.A[i], bs.B[i], inv));
+    for (int i = 1; i < 9; i++) best = __builtin_fminf(best, slab_fast(bs.A[i], bs.B[i], inv));
     return fmax_f(0.0f, best);
 }
 

@@ -489,7 +489,9 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                         const V d = mk(R[0] * rx + R[1] * ry + R[2] * rz, R[3] * rx + R[4] * ry + R[5] * rz,
                                        R[6] * rx + R[7] * ry + R[8] * rz);
                         float depth;
-                        if (fast && fabs_f(d.x) >= 1e-8f && fabs_f(d.y) >= 1e-8f && fabs_f(d.z) >= 1e-8f)
+                        const bool axes = (__builtin_fabsf(d.x) >= 1e-8f) & (__builtin_fabsf(d.y) >= 1e-8f) &
+                                          (__builtin_fabsf(d.z) >= 1e-8f);
+                        if (fast && axes)
                             depth = cast_ray_boxes(bs, d);
                         else
                             depth = cast_ray(world, s_cent[grp], count, origin, d);
