@@ -273,7 +273,7 @@ __device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22]
     const uint32_t wv = threadIdx.x / 64, l = threadIdx.x % 64, j = l % 16;
 #pragma unroll
     for (int c = 0; c < 22; c++)
-        if (c % G == int(lane)) smo[grp * MS + c] = mo[c];
+        smo[grp * MS + c] = mo[c];  // the group's lanes hold equal values: no owner test
     __syncthreads();
     if (wv < 2) {  // Dense 22->16 + ReLU (raptor.hpp:54-60)
         const uint32_t env = 16 * wv + j;
@@ -333,7 +333,7 @@ __device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22]
         }
 #pragma unroll
         for (int c = 0; c < 16; c++)
-            if (c % G == int(lane)) srh[grp * 17 + c] = hidden[c];
+            srh[grp * 17 + c] = hidden[c];
     }
 }
 
@@ -360,7 +360,11 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     constexpr int U = 16 / G;        // RAPTOR units per lane
     constexpr int HU = 64 / G;       // actor/critic hidden units per lane
     const MdnSimConfig& C = a.cfg;
-    const MdnPhysicsParams& P = a.phys;
+    __shared__ MdnPhysicsParams s_phys;
+    for (uint32_t i = threadIdx.x; i < sizeof(MdnPhysicsParams) / 4; i += 64 * W)
+        reinterpret_cast<float*>(&s_phys)[i] = reinterpret_cast<const float*>(&a.phys)[i];
+    __syncthreads();
+    const MdnPhysicsParams& P = s_phys;
     const uint32_t N = C.n;
     const uint32_t lane = threadIdx.x % G, grp = threadIdx.x / G;
     const uint32_t n = blockIdx.x * E + grp;
@@ -542,8 +546,9 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
             for (int j = 0; j < 3; j++) ctx[18 + j] = clamp_f((R[j] * ref0 + R[3 + j] * ref1 + R[6 + j] * ref2) * 2.0f, -1.0f, 1.0f);
 #pragma unroll
-            for (int j = 0; j < 21; j++)
-                if (j % G == int(lane)) { s_obs[grp][2 * POOL + j] = ctx[j]; og[2 * POOL + j] = ctx[j]; }
+            // every lane of the group holds the same values and writes them
+            // (equal stores to one address; cheaper than per-value owner branches)
+            for (int j = 0; j < 21; j++) { s_obs[grp][2 * POOL + j] = ctx[j]; og[2 * POOL + j] = ctx[j]; }
             // critic observation (sim.metal:159-181)
             float cob[COBS];
 #pragma unroll
@@ -571,8 +576,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 }
             float* cg = a.co + row * COBS;
 #pragma unroll
-            for (int j = 0; j < 32; j++)
-                if (j % G == int(lane)) { s_co[grp][j] = cob[j]; cg[j] = cob[j]; }
+            for (int j = 0; j < 32; j++) { s_co[grp][j] = cob[j]; cg[j] = cob[j]; }
         }
         group_sync();
         if (X && t + 1 == a.count && (a.split & SPLIT_END_AFTER_OBSERVE)) break;
@@ -814,8 +818,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 }
             float* ncg = a.nco + row * COBS;
 #pragma unroll
-            for (int j = 0; j < 32; j++)
-                if (j % G == int(lane)) { s_co[grp][j] = cob[j]; ncg[j] = cob[j]; }
+            for (int j = 0; j < 32; j++) { s_co[grp][j] = cob[j]; ncg[j] = cob[j]; }
             if (success || collision || timeout) {  // sim.metal:328-331
                 r.successes += success;
                 r.collisions += collision;
