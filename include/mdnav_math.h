@@ -106,11 +106,10 @@ constexpr float LN2_LO = 1.42860677e-06f;
 constexpr float LOG2E = 1.44269502f;
 
 MDN_HD float exp_f(float x) {
-    if (!(x == x)) return x;
-    if (x > 88.8f) return inf_f();
-    if (x < -104.0f) return 0.0f;
-    const float k = floor_f(x * LOG2E + 0.5f);
-    const float r = (x - k * LN2_HI) - k * LN2_LO;
+    // straight-line: the special cases are selected at the end (no branches)
+    const float xc = (x == x) ? (x > 88.8f ? 88.8f : (x < -104.0f ? -104.0f : x)) : 0.0f;
+    const float k = floor_f(xc * LOG2E + 0.5f);
+    const float r = (xc - k * LN2_HI) - k * LN2_LO;
     float p = 1.98412698e-04f;      // 1/7!
     p = p * r + 1.38888889e-03f;    // 1/6!
     p = p * r + 8.33333333e-03f;    // 1/5!
@@ -119,15 +118,14 @@ MDN_HD float exp_f(float x) {
     p = p * r + 0.5f;
     p = p * r + 1.0f;
     p = p * r + 1.0f;
-    return ldexp_f(p, (int)k);
+    const float v = ldexp_f(p, (int)k);
+    return !(x == x) ? x : (x > 88.8f ? inf_f() : (x < -104.0f ? 0.0f : v));
 }
 
 MDN_HD float expm1_f(float x) {
-    if (!(x == x)) return x;
-    if (x > 88.0f) return inf_f();
-    if (x < -18.0f) return -1.0f;
-    const float k = floor_f(x * LOG2E + 0.5f);
-    const float r = (x - k * LN2_HI) - k * LN2_LO;
+    const float xc = (x == x) ? (x > 88.0f ? 88.0f : (x < -18.0f ? -18.0f : x)) : 0.0f;
+    const float k = floor_f(xc * LOG2E + 0.5f);
+    const float r = (xc - k * LN2_HI) - k * LN2_LO;
     float p = 2.48015873e-05f;      // 1/8!
     p = p * r + 1.98412698e-04f;    // 1/7!
     p = p * r + 1.38888889e-03f;    // 1/6!
@@ -136,20 +134,20 @@ MDN_HD float expm1_f(float x) {
     p = p * r + 1.66666667e-01f;    // 1/3!
     p = p * r + 0.5f;               // 1/2!
     const float em1 = r + (r * r) * p;
-    if (k == 0.0f) return em1;
     const float scale = ldexp_f(1.0f, (int)k);
-    return scale * em1 + (scale - 1.0f);
+    const float v = k == 0.0f ? em1 : scale * em1 + (scale - 1.0f);
+    return !(x == x) ? x : (x > 88.0f ? inf_f() : (x < -18.0f ? -1.0f : v));
 }
 
 MDN_HD float log_f(float x) {
-    if (!(x > 0.0f)) return x == 0.0f ? -inf_f() : nan_f();
-    if (!isfinite_f(x)) return x;
-    int e = 0;
-    if (x < 1.17549435e-38f) { x = x * 8388608.0f; e = -23; }
-    const uint32_t bits = float_bits(x);
-    e += (int)((bits >> 23) & 0xffu) - 127;
+    const bool sub = x < 1.17549435e-38f;
+    const float xs = sub ? x * 8388608.0f : x;
+    const uint32_t bits = float_bits(xs);
+    int e = (sub ? -23 : 0) + (int)((bits >> 23) & 0xffu) - 127;
     float m = bits_float((bits & 0x007fffffu) | 0x3f800000u);
-    if (m > 1.41421356f) { m = m * 0.5f; e += 1; }
+    const bool high = m > 1.41421356f;
+    m = high ? m * 0.5f : m;
+    e += high ? 1 : 0;
     const float s = (m - 1.0f) / (m + 1.0f);
     const float z = s * s;
     float p = 9.09090909e-02f;      // 1/11
@@ -160,7 +158,8 @@ MDN_HD float log_f(float x) {
     p = p * z + 1.0f;
     const float lm = (2.0f * s) * p;
     const float ef = (float)e;
-    return ef * LN2_HI + (ef * LN2_LO + lm);
+    const float v = ef * LN2_HI + (ef * LN2_LO + lm);
+    return !(x > 0.0f) ? (x == 0.0f ? -inf_f() : nan_f()) : (!isfinite_f(x) ? x : v);
 }
 
 // Cephes pi/2 split: PIO2_1 + PIO2_2 + PIO2_3 = pi/2; k*PIO2_1 is exact.
@@ -179,14 +178,11 @@ MDN_HD void sincos_f(float x, float* s_out, float* c_out) {
     cp = cp * z + 4.16666667e-02f;  // 1/4!
     cp = cp * z - 0.5f;
     const float cr = 1.0f + z * cp;
-    const int q = ((int)k) & 3;
-    float s, c;
-    if (q == 0) { s = sr; c = cr; }
-    else if (q == 1) { s = cr; c = -sr; }
-    else if (q == 2) { s = -sr; c = -cr; }
-    else { s = -cr; c = sr; }
-    *s_out = s;
-    *c_out = c;
+    const int q = (k == k && k > -2147483648.0f && k < 2147483648.0f) ? (((int)k) & 3) : 0;
+    const bool odd = (q & 1) != 0, neg_s = q >= 2, neg_c = q == 1 || q == 2;
+    const float s = odd ? cr : sr, c = odd ? sr : cr;
+    *s_out = neg_s ? -s : s;
+    *c_out = neg_c ? -c : c;
 }
 
 MDN_HD float sin_f(float x) { float s, c; sincos_f(x, &s, &c); return s; }
@@ -194,14 +190,10 @@ MDN_HD float cos_f(float x) { float s, c; sincos_f(x, &s, &c); return c; }
 
 MDN_HD float tanh_f(float x) {
     const float a = fabs_f(x);
-    if (!(a == a)) return x;
-    float t;
-    if (a > 10.0f) t = 1.0f;
-    else {
-        const float e = expm1_f(2.0f * a);
-        t = e / (e + 2.0f);
-    }
-    return x < 0.0f ? -t : t;
+    const float e = expm1_f(2.0f * (a > 10.0f ? 10.0f : a));
+    const float t = a > 10.0f ? 1.0f : e / (e + 2.0f);
+    const float v = x < 0.0f ? -t : t;
+    return !(a == a) ? x : v;
 }
 
 MDN_HD float sigmoid_f(float x) { return 1.0f / (1.0f + exp_f(-x)); }

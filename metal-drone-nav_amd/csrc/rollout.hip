@@ -263,10 +263,12 @@ __device__ __forceinline__ void wg_head(const float* x, const float* w, uint32_t
 // RAPTOR step (raptor.hpp:52-97) for the 32 envs of a workgroup with the
 // dense and GRU layers on the matrix cores (16x16x4 tiles, fma chains from the
 // biases as in the group step).  Every env's group writes its observation row
-// mo[22] to `smo` (stride MS); wavefronts 0 and 1 evaluate env blocks 0 and 1;
-// the new hidden state lands in `snh`, the old one is read from `srh`.  Three
-// workgroup barriers; call from uniform control flow.  `on` masks envs whose
-// step is skipped (their rows are computed and ignored).
+// mo[22] to `smo` (stride MS, at least 120 words per env row: the gate
+// pre-activations are staged there too); wavefronts 0 and 1 evaluate the
+// dense layer of env blocks 0 and 1, all four the GRU products; each env's
+// group evaluates its own gates.  The new hidden state lands in `snh`, the old
+// one is read from `srh`.  Three workgroup barriers; call from uniform control
+// flow.  `on` masks envs whose step is skipped.
 template <int G, uint32_t MS>
 __device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22], float* smo, float* sx, float* srh,
                                           float* snh, uint32_t grp, uint32_t lane, bool on, float (&act)[4]) {
@@ -291,35 +293,49 @@ __device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22]
         for (uint32_t r = 0; r < 4; r++) sx[(16 * wv + 4 * (l / 16) + r) * 17 + j] = max_f(acc[r], 0.0f);
     }
     __syncthreads();
-    if (wv < 2) {  // GRU (raptor.hpp:62-84): gate g of unit u is row 16g + u
-        const uint32_t env = 16 * wv + j;
-        v4f iv[3], hv[3];
+    {   // GRU gate products (raptor.hpp:62-84): wavefront w takes env block w%2,
+        // input side (x, w < 2) or hidden side (h, w >= 2); gate g of unit u is
+        // row 16g + u.  Pre-activations go to the env rows of smo at 24 + 16g
+        // (input side) and 72 + 16g (hidden side).
+        const uint32_t eb = wv % 2, env = 16 * eb + j;
+        const bool hid = wv >= 2;
+        const float* src = hid ? srh : sx;
+        const uint32_t wofs = hid ? 1136u : 368u, bofs = hid ? 1952u : 1904u, gofs = hid ? 72u : 24u;
+        v4f acc[3];
 #pragma unroll
         for (uint32_t g = 0; g < 3; g++) {
-            const float bi = RW[1904 + 16 * g + j], bh = RW[1952 + 16 * g + j];
-            iv[g][0] = bi; iv[g][1] = bi; iv[g][2] = bi; iv[g][3] = bi;
-            hv[g][0] = bh; hv[g][1] = bh; hv[g][2] = bh; hv[g][3] = bh;
+            const float bias = RW[bofs + 16 * g + j];
+            acc[g][0] = bias; acc[g][1] = bias; acc[g][2] = bias; acc[g][3] = bias;
         }
 #pragma unroll
         for (uint32_t k0 = 0; k0 < 16; k0 += 4) {
             const uint32_t k = k0 + l / 16;
-            const float ax = sx[env * 17 + k], ah = srh[env * 17 + k];
+            const float av = src[env * 17 + k];
 #pragma unroll
-            for (uint32_t g = 0; g < 3; g++) {
-                iv[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(ax, RW[368 + (16 * g + j) * 16 + k], iv[g], 0, 0, 0);
-                hv[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(ah, RW[1136 + (16 * g + j) * 16 + k], hv[g], 0, 0, 0);
-            }
+            for (uint32_t g = 0; g < 3; g++)
+                acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, RW[wofs + (16 * g + j) * 16 + k], acc[g], 0, 0, 0);
         }
 #pragma unroll
         for (uint32_t r = 0; r < 4; r++) {
-            const uint32_t e = 16 * wv + 4 * (l / 16) + r;
-            const float reset = sigmoid_f(iv[0][r] + hv[0][r]);
-            const float update = sigmoid_f(iv[1][r] + hv[1][r]);
-            const float cand = tanh_f(iv[2][r] + reset * hv[2][r]);
-            snh[e * 17 + j] = (1.0f - update) * cand + update * srh[e * 17 + j];
+            const uint32_t e = 16 * eb + 4 * (l / 16) + r;
+#pragma unroll
+            for (uint32_t g = 0; g < 3; g++) smo[e * MS + gofs + 16 * g + j] = acc[g][r];
         }
     }
     __syncthreads();
+    if (on) {  // gates of this lane's units, new hidden state
+        const float* gi = smo + grp * MS + 24;
+        const float* gh = gi + 48;
+#pragma unroll
+        for (int i = 0; i < 16 / G; i++) {
+            const uint32_t u = lane + G * i;
+            const float reset = sigmoid_f(gi[u] + gh[u]);
+            const float update = sigmoid_f(gi[16 + u] + gh[16 + u]);
+            const float cand = tanh_f(gi[32 + u] + reset * gh[32 + u]);
+            snh[grp * 17 + u] = (1.0f - update) * cand + update * srh[grp * 17 + u];
+        }
+    }
+    group_sync();
     if (on) {  // output dense + clip (raptor.hpp:86-97), commit the hidden state
         float hidden[16];
 #pragma unroll
@@ -332,8 +348,7 @@ __device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22]
             act[q] = max_f(-1.0f, min_f(1.0f, val));
         }
 #pragma unroll
-        for (int c = 0; c < 16; c++)
-            srh[grp * 17 + c] = hidden[c];
+        for (int c = 0; c < 16; c++) srh[grp * 17 + c] = hidden[c];
     }
 }
 
