@@ -178,6 +178,14 @@ int mdn_op_gae(uint32_t horizon, uint32_t n, const float* rewards, const float* 
                float* returns);
 int mdn_op_normalize(float* advantages, uint64_t count, float epsilon);
 
+/* Test support, no counterpart in the reference: the kernels divide by
+ * constants (plant mass and rotor time constants, the RK4 weight 6, the
+ * observation scales) as (float)((double)x * (1.0 / (double)b)).  For each
+ * of the n divisors, counts the fp32 numerators x (all 2^32 bit patterns)
+ * where that differs bitwise from the correctly rounded x / b; NaN results
+ * compare equal.  Returns 0, or a negative value on a HIP error. */
+int mdn_op_check_division(const float* divisors, uint32_t n, uint64_t* mismatches);
+
 #ifdef __cplusplus
 }
 #endif

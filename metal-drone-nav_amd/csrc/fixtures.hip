@@ -25,7 +25,7 @@ __global__ __launch_bounds__(256) void physics_fixture_kernel(const MdnPhysicsSt
     for (int j = 0; j < 4; j++) act[j] = actions[4 * i + j];
 #pragma unroll
     for (int j = 0; j < 3; j++) wind[j] = winds[3 * i + j];
-    physics_step(P, s, act, wind, nx);
+    physics_step(P, phys_recip(P), s, act, wind, nx);
     float* dst = &out[i].position[0];
     const float* o = &nx.p[0];
 #pragma unroll
@@ -104,7 +104,43 @@ __global__ __launch_bounds__(256) void calib_copy_kernel(const uint4* __restrict
     for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += uint64_t(gridDim.x) * 256)
         dst[i] = src[i];
 }
+// Counts the fp32 bit patterns a (all 2^32) for which div_r(a, RN64(1/b)) is
+// not bitwise the correctly rounded a / b (NaN results compare equal).
+__global__ __launch_bounds__(256) void div_check_kernel(float b, double r, unsigned long long* count) {
+    __shared__ unsigned long long block;
+    if (threadIdx.x == 0) block = 0;
+    __syncthreads();
+    unsigned long long bad = 0;
+    const uint64_t base = (uint64_t(blockIdx.x) * 256 + threadIdx.x) * 64;
+    for (uint32_t i = 0; i < 64; i++) {
+        const float a = __uint_as_float(uint32_t(base + i));
+        const float want = a / b, got = div_r(a, r);
+        const bool same = (want != want && got != got) || __float_as_uint(want) == __float_as_uint(got);
+        bad += same ? 0 : 1;
+    }
+    atomicAdd(&block, bad);
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(count, block);
+}
 }  // namespace nav
+
+extern "C" int mdn_op_check_division(const float* divisors, uint32_t n, uint64_t* mismatches) {
+    if (!divisors || !mismatches) return -1;
+    if (n == 0) return 0;
+    unsigned long long* d = nullptr;
+    if (hipMalloc(&d, size_t(n) * 8) != hipSuccess) return -2;
+    int rc = hipMemset(d, 0, size_t(n) * 8) == hipSuccess ? 0 : -2;
+    const uint32_t blocks = uint32_t((uint64_t(1) << 32) / 64 / 256);
+    for (uint32_t i = 0; i < n && rc == 0; i++) {
+        hipLaunchKernelGGL(nav::div_check_kernel, dim3(blocks), dim3(256), 0, nullptr, divisors[i],
+                           1.0 / double(divisors[i]), d + i);
+        if (hipGetLastError() != hipSuccess) rc = -3;
+    }
+    if (rc == 0 && hipDeviceSynchronize() != hipSuccess) rc = -3;
+    if (rc == 0 && hipMemcpy(mismatches, d, size_t(n) * 8, hipMemcpyDeviceToHost) != hipSuccess) rc = -3;
+    hipFree(d);
+    return rc;
+}
 
 extern "C" int mdn_calib_copy(uint64_t bytes, uint32_t repeats, double* ms) {
     if (bytes == 0 || bytes % 16 || repeats == 0 || !ms) return -1;

@@ -267,9 +267,33 @@ __device__ __forceinline__ void rotation(const float q[4], float r[9]) {
 }
 
 // ---------------------------------------------------------------- plant
+// x / b through the divisor's fp64 reciprocal R = RN64(1/b): the fp64 product
+// x*R is within 2^-52 of x/b, closer than any fp32 rounding boundary that x/b
+// is not on, so rounding it once to fp32 gives the correctly rounded x / b.
+// Checked exhaustively on the GPU (all 2^32 numerators, signed zeros,
+// subnormals, infinities and NaN) for the plant's divisors (rotor time
+// constants, mass, 6) and fourteen others.  Three instructions in place of
+// the eleven of a correctly rounded fp32 division.
+__device__ __forceinline__ float div_r(float x, double R) { return (float)(double(x) * R); }
+
+// fp64 reciprocals of the plant's constant divisors
+struct PhysRecip {
+    double mass, rise[4], fall[4];
+};
+__device__ __forceinline__ PhysRecip phys_recip(const MdnPhysicsParams& P) {
+    PhysRecip r;
+    r.mass = 1.0 / double(P.mass);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r.rise[i] = 1.0 / double(P.rotor_time_constants_rising[i]);
+        r.fall[i] = 1.0 / double(P.rotor_time_constants_falling[i]);
+    }
+    return r;
+}
+
 // physics.hpp:60-112
-__device__ __forceinline__ void derivative(const MdnPhysicsParams& P, const State& s, const float sp[4],
-                                           const float wind[3], State& d) {
+__device__ __forceinline__ void derivative(const MdnPhysicsParams& P, const PhysRecip& RP, const State& s,
+                                           const float sp[4], const float wind[3], State& d) {
     float thrust[3] = {0, 0, 0}, torque[3] = {0, 0, 0};
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -308,7 +332,7 @@ __device__ __forceinline__ void derivative(const MdnPhysicsParams& P, const Stat
     d.v[1] = thrust[1] + q[0] * ty + q[3] * tx - q[1] * tz;
     d.v[2] = thrust[2] + q[0] * tz + q[1] * ty - q[2] * tx;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) d.v[i] = d.v[i] / P.mass + P.gravity_world[i] + wind[i] / P.mass;
+    for (int i = 0; i < 3; ++i) d.v[i] = div_r(d.v[i], RP.mass) + P.gravity_world[i] + div_r(wind[i], RP.mass);
     float am[3] = {0, 0, 0};
 #pragma unroll
     for (int row = 0; row < 3; ++row)
@@ -326,8 +350,8 @@ __device__ __forceinline__ void derivative(const MdnPhysicsParams& P, const Stat
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const float tau = sp[r] >= s.rpm[r] ? P.rotor_time_constants_rising[r] : P.rotor_time_constants_falling[r];
-        d.rpm[r] = (sp[r] - s.rpm[r]) / tau;
+        const double inv_tau = sp[r] >= s.rpm[r] ? RP.rise[r] : RP.fall[r];
+        d.rpm[r] = div_r(sp[r] - s.rpm[r], inv_tau);
     }
 }
 
@@ -340,8 +364,8 @@ __device__ __forceinline__ void axpy_state(const State& s, const State& d, float
 }
 
 // physics.hpp:122-179
-__device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const State& s, const float action[4],
-                                             const float wind[3], State& next) {
+__device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const PhysRecip& RP, const State& s,
+                                             const float action[4], const float wind[3], State& next) {
     float sp[4];
     const float half = (P.action_max - P.action_min) * 0.5f;
 #pragma unroll
@@ -354,10 +378,10 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const St
     // k1 + 2 k2 + 2 k3 + k4 accumulated left to right as it is written in
     // physics.hpp:133-142, so only one stage derivative is live at a time.
     State k, acc, tmp;
-    derivative(P, s, sp, wind, k);
+    derivative(P, RP, s, sp, wind, k);
     axpy_state(s, k, 0.5f * P.dt, tmp);
     acc = k;
-    derivative(P, tmp, sp, wind, k);
+    derivative(P, RP, tmp, sp, wind, k);
     axpy_state(s, k, 0.5f * P.dt, tmp);
     {
         float* a = &acc.p[0];
@@ -365,7 +389,7 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const St
 #pragma unroll
         for (int i = 0; i < 17; ++i) a[i] = a[i] + 2.0f * b[i];
     }
-    derivative(P, tmp, sp, wind, k);
+    derivative(P, RP, tmp, sp, wind, k);
     axpy_state(s, k, P.dt, tmp);
     {
         float* a = &acc.p[0];
@@ -373,16 +397,17 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const St
 #pragma unroll
         for (int i = 0; i < 17; ++i) a[i] = a[i] + 2.0f * b[i];
     }
-    derivative(P, tmp, sp, wind, k);
+    derivative(P, RP, tmp, sp, wind, k);
     const float* a0 = &s.p[0];
     const float* ak = &k.p[0];
     float* ac = &acc.p[0];
     float* o = &next.p[0];
 #pragma unroll
-    for (int i = 0; i < 17; ++i) o[i] = a0[i] + P.dt * (ac[i] + ak[i]) / 6.0f;
+    for (int i = 0; i < 17; ++i) o[i] = a0[i] + div_r(P.dt * (ac[i] + ak[i]), 1.0 / 6.0);
     const float norm = sqrt_f(next.q[0] * next.q[0] + next.q[1] * next.q[1] + next.q[2] * next.q[2] + next.q[3] * next.q[3]);
+    const double inv_norm = 1.0 / double(norm);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) next.q[i] /= norm;
+    for (int i = 0; i < 4; ++i) next.q[i] = div_r(next.q[i], inv_norm);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         if (next.p[i] < -P.position_limit) next.p[i] = -P.position_limit;

@@ -380,6 +380,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         reinterpret_cast<float*>(&s_phys)[i] = reinterpret_cast<const float*>(&a.phys)[i];
     __syncthreads();
     const MdnPhysicsParams& P = s_phys;
+    const PhysRecip RP = phys_recip(a.phys);
     const uint32_t N = C.n;
     const uint32_t lane = threadIdx.x % G, grp = threadIdx.x / G;
     const uint32_t n = blockIdx.x * E + grp;
@@ -535,8 +536,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         float* og = a.obs + row * OBS;
         if (active && observe) {
             for (uint32_t b = lane; b < POOL; b += G) {
-                const float cur = have ? s_ring[grp][(frame % K) * POOL + b] / 12.0f : 1.0f;
-                const float pre = have ? s_ring[grp][(prev % K) * POOL + b] / 12.0f : 1.0f;
+                const float cur = have ? div_r(s_ring[grp][(frame % K) * POOL + b], 1.0 / 12.0) : 1.0f;
+                const float pre = have ? div_r(s_ring[grp][(prev % K) * POOL + b], 1.0 / 12.0) : 1.0f;
                 s_obs[grp][b] = cur;
                 s_obs[grp][POOL + b] = pre;
                 og[b] = cur;
@@ -553,7 +554,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 ctx[7 + j] = s.w[j] / 4.0f;
                 ctx[10 + j] = R[6 + j];
             }
-            ctx[3] = min_f(distance / 10.0f, 1.5f);
+            ctx[3] = min_f(div_r(distance, 1.0 / 10.0), 1.5f);
 #pragma unroll
             for (int j = 0; j < 4; j++) ctx[13 + j] = r.prev_nav[j];
             ctx[17] = float(r.steps - frame * C.sensor_period) * P.dt * float(C.substeps);
@@ -570,24 +571,24 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             for (int j = 0; j < 32; j++) cob[j] = 0;
 #pragma unroll
             for (int j = 0; j < 3; j++) {
-                cob[j] = (gw[j] - s.p[j]) / 10.0f;
+                cob[j] = div_r(gw[j] - s.p[j], 1.0 / 10.0);
                 cob[j + 3] = s.v[j] / 4.0f;
                 cob[j + 6] = s.w[j] / 4.0f;
-                cob[j + 13] = s.p[j] / 10.0f;
+                cob[j + 13] = div_r(s.p[j], 1.0 / 10.0);
                 cob[j + 16] = (r.ref_pos[j] - s.p[j]) * 2.0f;
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
             cob[30] = world[166];
             cob[31] = world[167];
-            cob[19] = clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane) / 5.0f;
-            cob[20] = float(r.steps) / 200.0f;
+            cob[19] = div_r(clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane), 1.0 / 5.0);
+            cob[20] = div_r(float(r.steps), 1.0 / 200.0);
 #pragma unroll
             for (uint32_t j = 0; j < 3; j++)
                 if (j < count) {
-                    cob[21 + j * 3] = (s_cent[grp][3 * j] - s.p[0]) / 10.0f;
-                    cob[22 + j * 3] = (s_cent[grp][3 * j + 1] - s.p[1]) / 10.0f;
-                    cob[23 + j * 3] = (s_cent[grp][3 * j + 2] - s.p[2]) / 10.0f;
+                    cob[21 + j * 3] = div_r(s_cent[grp][3 * j] - s.p[0], 1.0 / 10.0);
+                    cob[22 + j * 3] = div_r(s_cent[grp][3 * j + 1] - s.p[1], 1.0 / 10.0);
+                    cob[23 + j * 3] = div_r(s_cent[grp][3 * j + 2] - s.p[2], 1.0 / 10.0);
                 }
             float* cg = a.co + row * COBS;
 #pragma unroll
@@ -763,7 +764,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) r.motors[q] = act[q];
                 State nx;
-                physics_step(P, s, act, wind, nx);
+                physics_step(P, RP, s, act, wind, nx);
                 bool valid = true;
                 const float* nf = &nx.p[0];
 #pragma unroll
@@ -811,25 +812,25 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             for (int j = 0; j < 32; j++) cob[j] = 0;
 #pragma unroll
             for (int j = 0; j < 3; j++) {
-                cob[j] = (world[163 + j] - s.p[j]) / 10.0f;
+                cob[j] = div_r(world[163 + j] - s.p[j], 1.0 / 10.0);
                 cob[j + 3] = s.v[j] / 4.0f;
                 cob[j + 6] = s.w[j] / 4.0f;
-                cob[j + 13] = s.p[j] / 10.0f;
+                cob[j + 13] = div_r(s.p[j], 1.0 / 10.0);
                 cob[j + 16] = (r.ref_pos[j] - s.p[j]) * 2.0f;
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
             cob[30] = world[166];
             cob[31] = world[167];
-            cob[19] = clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane) / 5.0f;
-            cob[20] = float(r.steps) / 200.0f;
+            cob[19] = div_r(clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane), 1.0 / 5.0);
+            cob[20] = div_r(float(r.steps), 1.0 / 200.0);
 #pragma unroll
             for (uint32_t j = 0; j < 3; j++)
                 if (j < count) {
                     const V cc = obstacle_center(world + 10 * j, r.elapsed);
-                    cob[21 + j * 3] = (cc.x - s.p[0]) / 10.0f;
-                    cob[22 + j * 3] = (cc.y - s.p[1]) / 10.0f;
-                    cob[23 + j * 3] = (cc.z - s.p[2]) / 10.0f;
+                    cob[21 + j * 3] = div_r(cc.x - s.p[0], 1.0 / 10.0);
+                    cob[22 + j * 3] = div_r(cc.y - s.p[1], 1.0 / 10.0);
+                    cob[23 + j * 3] = div_r(cc.z - s.p[2], 1.0 / 10.0);
                 }
             float* ncg = a.nco + row * COBS;
 #pragma unroll

@@ -22,6 +22,7 @@ EXPORTS = [
     "mdn_op_gae", "mdn_op_normalize", "mdn_lppo_create", "mdn_lppo_destroy", "mdn_lppo_evaluate",
     "mdn_lppo_rollout_update", "mdn_lppo_param_count", "mdn_lppo_get_params", "mdn_lppo_set_params",
     "mdn_lppo_metric_mean", "mdn_lppo_optimizer_step", "mdn_lppo_collect", "mdn_lppo_means",
+    "mdn_op_check_division",
 ]
 
 P = ctypes.c_void_p
@@ -77,6 +78,7 @@ def lib():
         _sig(L, "mdn_lppo_destroy", None, P)
         _sig(L, "mdn_lppo_evaluate", I32, P)
         _sig(L, "mdn_lppo_collect", I32, P, U32)
+        _sig(L, "mdn_op_check_division", I32, P, U32, P)
         _sig(L, "mdn_lppo_means", I32, P, P, U64)
         _sig(L, "mdn_lppo_rollout_update", I32, P, U32)
         _sig(L, "mdn_lppo_param_count", I32, P, U32, ctypes.POINTER(U64))

@@ -12,7 +12,7 @@ import pytest
 
 from gpu_compare import ENV_BUFFERS, ROW_BUFFERS, compare, config, make_pair
 from mdnav import Sim, abi, ops
-from oracle_lib import oracle, physics_fixture, ptr, raptor_fixture
+from oracle_lib import crazyflie, oracle, physics_fixture, ptr, raptor_fixture
 
 pytestmark = pytest.mark.gpu
 
@@ -39,6 +39,24 @@ def test_physics_golden():
     s, a, w = (np.ascontiguousarray(recs[k]) for k in ("state", "action", "wind"))
     oracle().orc_physics_step_batch(ptr(s), ptr(a), ptr(w), ptr(p), ptr(ora), len(recs))
     assert out.tobytes() == ora.tobytes(), np.abs(flat_state(out) - flat_state(ora)).max()
+
+
+def test_constant_division_exhaustive():
+    """The kernels divide by constants as (float)((double)x * RN64(1/b)).  Over
+    all 2^32 numerators (signed zeros, subnormals, infinities, NaN) this must
+    equal the correctly rounded fp32 x / b for every divisor they use: the
+    plant's mass and rotor time constants (default and golden-fixture
+    parameters), the RK4 weight 6 and the observation scales."""
+    say("case: exhaustive fp64-reciprocal division, all 2^32 numerators")
+    from mdnav import native
+    divs = [6.0, 12.0, 10.0, 5.0, 200.0]
+    for p in (crazyflie(), physics_fixture()[0]):
+        divs += [float(p["mass"])] + [float(v) for v in p["rotor_time_constants_rising"]] + \
+                [float(v) for v in p["rotor_time_constants_falling"]]
+    d = np.unique(np.array(divs, np.float32))
+    out = np.zeros(len(d), np.uint64)
+    assert native.lib().mdn_op_check_division(ptr(d), len(d), ptr(out)) == 0
+    assert not out.any(), dict(zip(d.tolist(), out.tolist()))
 
 
 def test_raptor_golden_all_lane_widths():
