@@ -89,13 +89,24 @@ __device__ __forceinline__ void stage_rows(const __bf16* __restrict__ Xb, const 
 }
 
 // ---------------------------------------------------------------- weights
-// bf16 copy [H][K] of a first-layer matrix W [H][D].
+// The bf16 copy of a first-layer matrix W [H][D] (inputs zero-padded to K) is
+// stored in fragment order: for each group of 32 units and each 16-wide k
+// step, the 64 lanes' 8-element matrix-core fragments (lane l: unit l % 32,
+// inputs 8(l / 32) ..) lie contiguously, so a wavefront's fragment load reads
+// 1 KB in one piece.  wsw(u, k) is the position of W[u][k]; frag(ub, ks, l)
+// the first element of lane l's fragment for units ub .. ub+31 (ub % 32 == 0).
+__device__ __forceinline__ size_t frag(uint32_t ub, uint32_t ks, uint32_t l, uint32_t K) {
+    return ((size_t(ub / 32) * (K / 16) + ks) * 64 + l) * 8;
+}
+__device__ __forceinline__ size_t wsw(uint32_t u, uint32_t k, uint32_t K) {
+    return frag(u - u % 32, k / 16, u % 32 + 32 * ((k % 16) / 8), K) + k % 8;
+}
 __global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ W, uint32_t H, uint32_t D, uint32_t K,
                                                    __bf16* __restrict__ out) {
     const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= uint64_t(H) * K) return;
     const uint32_t u = uint32_t(i / K), k = uint32_t(i % K);
-    out[i] = (__bf16)(k < D ? W[uint64_t(u) * D + k] : 0.0f);
+    out[wsw(u, k, K)] = (__bf16)(k < D ? W[uint64_t(u) * D + k] : 0.0f);
 }
 
 // ---------------------------------------------------------------- forward
@@ -124,10 +135,10 @@ struct FwdW1 {
 template <uint32_t K>
 __device__ __forceinline__ void fwd_load_w1(FwdW1<K>& f, const __bf16* __restrict__ Wb, const float* __restrict__ b1,
                                             uint32_t ub, uint32_t l) {
-    const uint32_t half = l / 32, lr = l % 32;
+    const uint32_t half = l / 32;
 #pragma unroll
     for (uint32_t ks = 0; ks < K / 16; ks++)
-        f.w[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(ub + lr) * K + 16 * ks + 8 * half);
+        f.w[ks] = *reinterpret_cast<const bf8*>(Wb + frag(ub, ks, l, K));
 #pragma unroll
     for (uint32_t g = 0; g < 4; g++) f.bias[g] = *reinterpret_cast<const float4*>(b1 + ub + 8 * g + 4 * half);
 }
@@ -409,7 +420,7 @@ __global__ __launch_bounds__(256, NQ == 1 ? 2 : 1) void backward_kernel(const __
     bf8 bw[K / 16];  // B operand of h: W1[unit][16 ks + 8(l/32) ..]
 #pragma unroll
     for (uint32_t ks = 0; ks < K / 16; ks++)
-        bw[ks] = *reinterpret_cast<const bf8*>(Wb + size_t(unit) * K + 16 * ks + 8 * half);
+        bw[ks] = *reinterpret_cast<const bf8*>(Wb + frag(u0 + 32 * wv, ks, l, K));
     // B operand of g: W2[q = 2 p + l/32][unit] (zero for q >= NQ)
     constexpr uint32_t NP = (NQ + 1) / 2;
     float w2f[NP];
@@ -631,8 +642,8 @@ __global__ __launch_bounds__(256) void adam_kernel(LargeAdamArgs a) {
     float w = params[p] - a.lr * (mi / a.c1) / (sqrt_f(vi / a.c2) + 1.0e-8f);
     if (!critic && p >= A_LS) w = clamp_f(w, -2.0f, 0.5f);
     params[p] = w;
-    if (!critic && p < A_B1) a.actor_wb[size_t(p / OBS) * KA + p % OBS] = (__bf16)w;
-    if (critic && p < C_B1) a.critic_wb[size_t(p / COBS) * KC + p % COBS] = (__bf16)w;
+    if (!critic && p < A_B1) a.actor_wb[wsw(p / OBS, p % OBS, KA)] = (__bf16)w;
+    if (critic && p < C_B1) a.critic_wb[wsw(p / COBS, p % COBS, KC)] = (__bf16)w;
 }
 
 }  // namespace lp
