@@ -107,6 +107,17 @@ int mdn_sim_kernel_time(MdnSim* sim, uint32_t kernel, double* total_ms, uint64_t
 int mdn_sim_reset_timing(MdnSim* sim);
 /* Lanes per environment in the rollout kernel (4, 8 or 16; default 8). */
 int mdn_sim_set_lanes(MdnSim* sim, uint32_t lanes);
+/* Actor input width, the reference's build-time FIXED_PPO_ACTOR_OBS_DIM
+ * (ppo.hpp:11-13, 30-34): 181 (pooled depth + context, the default) or 184,
+ * which appends the geometry-prior hint (sim.metal:226, guidance.hpp:38-96)
+ * and adds it to the first three action means (ppo.hpp:77,
+ * cpu_reference.hpp:446).  Replaces the policy by a fresh initialisation of
+ * the new shape (actor and critic, one seed stream) and resizes the
+ * observation rows.  Call before mdn_ppo_create / mdn_lppo_create.  The
+ * 184-input rollout runs 8 lanes per env; the geometry-memory variant of the
+ * hint (cfg.geometry_memory = 1) returns MDN_E_ARG. */
+int mdn_sim_set_actor_obs(MdnSim* sim, uint32_t actor_obs);
+int mdn_sim_get_actor_obs(const MdnSim* sim, uint32_t* actor_obs);
 
 /* PPOTrainer(Sim&, epochs) — main.mm:1166-1217, with the minibatch size
  * (PPOTrainer::minibatch, main.mm:1113) as an argument. */

@@ -35,6 +35,8 @@ extern "C" {
 /* Policy shapes (ppo.hpp:26-45 with FIXED_PPO_ACTOR_OBS_DIM=181). */
 #define MDN_CONTEXT_DIM 21u
 #define MDN_ACTOR_OBS_POOLED 181u
+/* pooled observation + the 3-value geometry-prior hint (ppo.hpp:30, 77) */
+#define MDN_ACTOR_OBS_PRIOR 184u
 #define MDN_CRITIC_OBS 32u
 #define MDN_HIDDEN 64u
 #define MDN_ACTIONS 4u

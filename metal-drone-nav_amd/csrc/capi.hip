@@ -87,6 +87,7 @@ struct MdnSim {
     float* commands = nullptr;
     float* raptor = nullptr;
     float* camera = nullptr;
+    float* cells = nullptr;  // pooled-cell directions of the guidance hint [80][3]
     // policy
     float* actor = nullptr;
     float* critic = nullptr;
@@ -103,7 +104,7 @@ struct MdnSim {
         nav::RolloutArgs a;
         a.state = state; a.run = run; a.world = world; a.sensors = sensors; a.poses = poses; a.commands = commands;
         a.raptor = raptor; a.actor = actor; a.actor_w1t = actor_w1t; a.critic = critic; a.critic_w1t = critic_w1t;
-        a.camera = camera; a.obs = obs; a.co = co; a.nco = nco; a.actions = actions; a.logp = logp; a.values = values;
+        a.camera = camera; a.cells = cells; a.obs = obs; a.co = co; a.nco = nco; a.actions = actions; a.logp = logp; a.values = values;
         a.rewards = rewards; a.next_values = next_values; a.terminated = terminated; a.truncated = truncated;
         a.cfg = cfg; a.phys = phys; a.count = count; a.horizon = horizon;
         a.ext_means = nullptr; a.ext_log_std = nullptr; a.tick0 = 0; a.split = 0;
@@ -153,7 +154,7 @@ int open_sync_window(MdnSim* s) {
 }
 
 int refresh_transposes(MdnSim* s) {
-    HIP_TRY(ppo_launch_transpose(s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->stream));
+    HIP_TRY(ppo_launch_transpose(s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->shape.obs, s->stream));
     return MDN_OK;
 }
 
@@ -167,7 +168,7 @@ struct BufInfo { void* dev; size_t bytes; };
 BufInfo row_buffer(MdnSim* s, uint32_t id) {
     const size_t R = s->rows();
     switch (id) {
-        case MDN_BUF_OBS: return {s->obs, R * OBS * 4};
+        case MDN_BUF_OBS: return {s->obs, R * s->shape.obs * 4};
         case MDN_BUF_CRITIC_OBS: return {s->co, R * COBS * 4};
         case MDN_BUF_NEXT_CRITIC_OBS: return {s->nco, R * COBS * 4};
         case MDN_BUF_ACTIONS: return {s->actions, R * 4 * 4};
@@ -235,6 +236,7 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
     guard(dev_alloc(&s->commands, size_t(N) * 32));
     guard(dev_alloc(&s->raptor, 2084));
     guard(dev_alloc(&s->camera, 960));
+    guard(dev_alloc(&s->cells, 240));
     guard(dev_alloc(&s->actor, s->shape.actor_count()));
     guard(dev_alloc(&s->critic, s->shape.critic_count()));
     guard(dev_alloc(&s->actor_w1t, size_t(OBS) * HID));
@@ -268,9 +270,19 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
         const float inv = 1.0f / mdn::fmax_f(len, 1e-8f);
         cam[3 * k] = dx * inv; cam[3 * k + 1] = dy * inv; cam[3 * k + 2] = dz * inv;
     }
+    // guidance.hpp:21-26: unit direction through the centre of pooled cell
+    // (row, col) of the 8x10 grid
+    std::vector<float> cells(240);
+    for (uint32_t k = 0; k < 80; k++) {
+        const uint32_t row = k / 10, col = k % 10;
+        const float y = 0.9f - 0.2f * float(col), z = (0.875f - 0.25f * float(row)) * MDN_SENSOR_TAN_V;
+        const float inv = 1.0f / mdn::sqrt_f(1.0f + y * y + z * z);
+        cells[3 * k] = inv; cells[3 * k + 1] = y * inv; cells[3 * k + 2] = z * inv;
+    }
     std::vector<float> actor(s->shape.actor_count()), critic(s->shape.critic_count());
     mdn::init_policy(s->shape, actor.data(), critic.data());
     if (hipMemcpy(s->camera, cam.data(), cam.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(s->cells, cells.data(), cells.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(s->raptor, raptor, sizeof(MdnRaptorWeights), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(s->actor, actor.data(), actor.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(s->critic, critic.data(), critic.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
@@ -292,7 +304,7 @@ void mdn_sim_destroy(MdnSim* s) {
     if (!s) return;
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->ppo) mdn_ppo_destroy(s->ppo);
-    void* bufs[] = {s->state, s->run, s->world, s->sensors, s->poses, s->commands, s->raptor, s->camera,
+    void* bufs[] = {s->state, s->run, s->world, s->sensors, s->poses, s->commands, s->raptor, s->camera, s->cells,
                     s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->obs, s->co, s->nco, s->actions, s->logp,
                     s->values, s->rewards, s->next_values, s->advantages, s->returns, s->terminated, s->truncated};
     for (void* b : bufs)
@@ -311,6 +323,8 @@ int mdn_sim_set_config(MdnSim* s, const MdnSimConfig* cfg) {
     if (cfg->sensor_period == 0) return fail(MDN_E_ARG, "sensor_period must be positive");
     if (cfg->sensor_delay > 6 || cfg->command_delay > 7)
         return fail(MDN_E_ARG, "delay rings support <=6 sensor frames and <=7 command steps");
+    if (cfg->geometry_memory && s->shape.obs == MDN_ACTOR_OBS_PRIOR)
+        return fail(MDN_E_ARG, "the geometry-memory hint is not built; set geometry_memory = 0");
     s->cfg = *cfg;
     return MDN_OK;
 }
@@ -319,6 +333,43 @@ int mdn_sim_get_config(const MdnSim* s, MdnSimConfig* cfg, uint32_t* horizon) {
     if (!s) return fail(MDN_E_ARG, "mdn_sim_get_config: null sim");
     if (cfg) *cfg = s->cfg;
     if (horizon) *horizon = s->horizon;
+    return MDN_OK;
+}
+
+int mdn_sim_set_actor_obs(MdnSim* s, uint32_t actor_obs) {
+    if (!s) return fail(MDN_E_ARG, "mdn_sim_set_actor_obs: null sim");
+    if (actor_obs != MDN_ACTOR_OBS_POOLED && actor_obs != MDN_ACTOR_OBS_PRIOR)
+        return fail(MDN_E_ARG, "actor inputs must be 181 (pooled) or 184 (with the geometry-prior hint)");
+    if (s->ppo) return fail(MDN_E_STATE, "set the actor's inputs before creating the PPO trainer");
+    if (s->cfg.geometry_memory && actor_obs == MDN_ACTOR_OBS_PRIOR)
+        return fail(MDN_E_ARG, "the geometry-memory hint is not built; set geometry_memory = 0");
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    mdn::PolicyShape shape = s->shape;
+    shape.obs = actor_obs;
+    float *obs = nullptr, *actor = nullptr, *w1t = nullptr;
+    int rc = dev_alloc(&obs, s->rows() * actor_obs);
+    if (!rc) rc = dev_alloc(&actor, shape.actor_count());
+    if (!rc) rc = dev_alloc(&w1t, size_t(actor_obs) * HID);
+    std::vector<float> a(shape.actor_count()), c(shape.critic_count());
+    mdn::init_policy(shape, a.data(), c.data());
+    if (!rc && (hipMemcpy(actor, a.data(), a.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(s->critic, c.data(), c.size() * 4, hipMemcpyHostToDevice) != hipSuccess))
+        rc = fail(MDN_E_HIP, "mdn_sim_set_actor_obs: policy upload");
+    if (rc) {
+        hipFree(obs); hipFree(actor); hipFree(w1t);
+        return rc;
+    }
+    hipFree(s->obs); hipFree(s->actor); hipFree(s->actor_w1t);
+    s->obs = obs; s->actor = actor; s->actor_w1t = w1t;
+    s->shape = shape;
+    rc = refresh_transposes(s);
+    if (!rc) HIP_TRY(hipStreamSynchronize(s->stream));
+    return rc;
+}
+
+int mdn_sim_get_actor_obs(const MdnSim* s, uint32_t* actor_obs) {
+    if (!s || !actor_obs) return fail(MDN_E_ARG, "mdn_sim_get_actor_obs: null argument");
+    *actor_obs = s->shape.obs;
     return MDN_OK;
 }
 
@@ -344,7 +395,9 @@ int mdn_sim_collect(MdnSim* s, uint32_t count) {
     if (rc) return rc;
     const nav::RolloutArgs a = s->args(count);
     const int lanes = int(s->lanes), slots = ring_slots(s->cfg);
-    return timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, lanes, slots, s->stream); });
+    if (s->shape.obs == MDN_ACTOR_OBS_PRIOR && lanes != 8)
+        return fail(MDN_E_ARG, "the 184-input actor's rollout runs 8 lanes per env");
+    return timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, lanes, slots, s->shape.obs, s->stream); });
 }
 
 int mdn_sim_sync(MdnSim* s, double* gpu_seconds) {
@@ -473,8 +526,8 @@ int mdn_ppo_create(MdnSim* s, uint32_t epochs, uint32_t minibatch, MdnPPO** out)
     guard(dev_alloc(&p->av, s->shape.actor_count()));
     guard(dev_alloc(&p->cm, s->shape.critic_count()));
     guard(dev_alloc(&p->cv, s->shape.critic_count()));
-    guard(dev_alloc(&p->part, size_t(chunks) * ppo_partial_stride()));
-    guard(dev_alloc(&p->grad, ppo_partial_stride()));
+    guard(dev_alloc(&p->part, size_t(chunks) * ppo_partial_stride(s->shape.obs)));
+    guard(dev_alloc(&p->grad, ppo_partial_stride(s->shape.obs)));
     guard(dev_alloc(&p->norm_part, (s->rows() + 255) / 256));
     guard(dev_alloc(&p->norm_stats, 2));
     guard(dev_alloc(&p->metric_rows, size_t(p->updates) * 4));
@@ -535,7 +588,7 @@ int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
         const uint32_t begin = order[u];
         const uint32_t b = std::min(p->minibatch, rows - begin);
         ppo::RowArgs ra;
-        ra.obs = s->obs + size_t(begin) * OBS;
+        ra.obs = s->obs + size_t(begin) * s->shape.obs;
         ra.co = s->co + size_t(begin) * COBS;
         ra.actions = s->actions + size_t(begin) * 4;
         ra.old_logp = s->logp + begin;
@@ -543,11 +596,11 @@ int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
         ra.ret = s->returns + begin;
         ra.actor = s->actor; ra.actor_w1t = s->actor_w1t; ra.critic = s->critic; ra.critic_w1t = s->critic_w1t;
         ra.part = p->part;
-        ra.b = b; ra.clip = 0.2f; ra.vcoef = 0.5f; ra.ecoef = s->cfg.entropy_coef;
+        ra.b = b; ra.d = s->shape.obs; ra.clip = 0.2f; ra.vcoef = 0.5f; ra.ecoef = s->cfg.entropy_coef;
         rc = timed(s, MDN_K_ROWS, [&] { return ppo_launch_rows(&ra, s->stream); });
         if (rc) return rc;
         rc = timed(s, MDN_K_GRADS, [&] {
-            return ppo_launch_grads(p->part, p->grad, b, s->stream);
+            return ppo_launch_grads(p->part, p->grad, b, s->shape.obs, s->stream);
         });
         if (rc) return rc;
         ++p->optimizer_step;
@@ -558,6 +611,7 @@ int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
         aa.lr = s->cfg.learning_rate;
         mdn::adam_corrections(p->optimizer_step, 0.9f, 0.999f, &aa.c1, &aa.c2);
         aa.b = b;
+        aa.d = s->shape.obs;
         rc = timed(s, MDN_K_ADAM, [&] { return ppo_launch_adam(&aa, s->stream); });
         if (rc) return rc;
     }
@@ -806,6 +860,7 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     if (hidden > 8192) return fail(MDN_E_ARG, "mdn_lppo_create: hidden above 8192");
     if (epochs < 1 || epochs > 8) return fail(MDN_E_ARG, "mdn_lppo_create: epochs must be 1..8");
     if (minibatch == 0) return fail(MDN_E_ARG, "mdn_lppo_create: minibatch must be positive");
+    if (s->shape.obs != OBS) return fail(MDN_E_ARG, "mdn_lppo_create: the wide policy takes the 181-input actor");
     MdnLargePPO* p = new MdnLargePPO();
     p->sim = s;
     p->hidden = hidden;
@@ -894,7 +949,7 @@ int mdn_lppo_collect(MdnLargePPO* p, uint32_t count) {
     // tick's rows, and one launch that acts, advances, resets and observes the
     // next tick
     a.split = nav::SPLIT_END_AFTER_OBSERVE;
-    rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, 8, slots, s->stream); });
+    rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, 8, slots, s->shape.obs, s->stream); });
     for (uint32_t t = 0; t < count && rc == MDN_OK; t++) {
         const size_t row0 = size_t(t % s->horizon) * N;
         rc = timed(s, MDN_K_LP_FORWARD, [&] {
@@ -905,7 +960,7 @@ int mdn_lppo_collect(MdnLargePPO* p, uint32_t count) {
         a.count = more ? 2 : 1;
         a.tick0 = t;
         a.split = nav::SPLIT_BEGIN_AT_ACT | (more ? nav::SPLIT_END_AFTER_OBSERVE : 0u);
-        rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, 8, slots, s->stream); });
+        rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, 8, slots, s->shape.obs, s->stream); });
     }
     if (rc) return rc;
     // values at s and s' (sim.metal:254, 322) under the wide critic

@@ -21,6 +21,7 @@ struct RolloutArgs {
     const float* critic;      // flat critic vector (ppo.hpp:41-45)
     const float* critic_w1t;  // [32][64]
     const float* camera;      // unit pixel rays [320][3]
+    const float* cells;       // pooled-cell directions [80][3] (guidance.hpp:21-26 nav_ray)
     float* obs;            // [T][N][181]
     float* co;             // [T][N][32]
     float* nco;            // [T][N][32] critic observation of s'
@@ -65,6 +66,7 @@ struct RowArgs {
     float* part;            // [ceil(b/256)][P_TOTAL] per-chunk gradient and metric partials
     uint32_t b;
     float clip, vcoef, ecoef;
+    uint32_t d;             // actor inputs: 181, or 184 with the geometry-prior hint
 };
 
 // cpu_reference.hpp:553-567 inputs for one update of both networks.
@@ -75,12 +77,14 @@ struct AdamArgs {
     float* metric_row;   // [4]
     float lr, c1, c2;    // host bias corrections 1-beta^step
     uint32_t b;
+    uint32_t d;          // actor inputs
 };
 }  // namespace ppo
 
 extern "C" {
 hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream);
-hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, hipStream_t stream);
+hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, uint32_t actor_obs,
+                              hipStream_t stream);
 hipError_t nav_launch_raptor_fixture(const float* RW, const float* obs, uint32_t steps, uint32_t copies,
                                      float* actions, float* hidden, int lanes_per_env, hipStream_t st);
 hipError_t nav_launch_physics_fixture(const MdnPhysicsState* in, const float* actions, const float* winds,
@@ -94,9 +98,10 @@ hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const
                           hipStream_t st);
 hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st);
 hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st);
-hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, hipStream_t st);
+hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, uint32_t d, hipStream_t st);
 hipError_t ppo_launch_adam(const ppo::AdamArgs* a, hipStream_t st);
-hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* aw, float* cw, hipStream_t st);
+hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* aw, float* cw, uint32_t d,
+                                hipStream_t st);
 hipError_t ppo_launch_metric_mean(const float* rows, float* mean, uint32_t updates, hipStream_t st);
 // wide-policy kernels (large.hip)
 hipError_t lp_launch_pack(const float* W, uint32_t H, uint32_t D, uint32_t K, __bf16* out, hipStream_t st);
@@ -120,5 +125,5 @@ uint64_t lp_backward_part_floats(uint32_t B, uint32_t H);
 hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
                           __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
                           uint32_t H, float lr, float c1, float c2, float* metric_row, hipStream_t st);
-uint32_t ppo_partial_stride();
+uint32_t ppo_partial_stride(uint32_t d);
 }

@@ -276,6 +276,105 @@ __device__ __forceinline__ void rotation(const float q[4], float r[9]) {
 // the eleven of a correctly rounded fp32 division.
 __device__ __forceinline__ float div_r(float x, double R) { return (float)(double(x) * R); }
 
+// ---------------------------------------------------------------- guidance
+// Geometry-prior hint of a 184-input actor (guidance.hpp:38-98,
+// nav_guidance): one env's lane group scores the 80 pooled cells (cell
+// c = lane + G i), reduces the best cell and the goal cell over the group with
+// the sequential scan's rule (the maximum; on equal values the first cell in
+// row-major order), and finishes replicated in every lane.  `orow` is the
+// env's observation row (pooled ranges / 12, current then previous), `cells`
+// the 80 cell directions nav_ray(row, col) (computed on the host with the same
+// fp32 operations), `inv_dt` = RN64(1 / max(sensor_dt, 1e-3)).
+__device__ __forceinline__ float guid_min3x3(const float* orow, int row, int col) {
+    float nearest = 12.0f;
+#pragma unroll
+    for (int dr = -1; dr <= 1; dr++)
+#pragma unroll
+        for (int dc = -1; dc <= 1; dc++) {
+            const int r = row + dr, c = col + dc;
+            if (r >= 0 && r < 8 && c >= 0 && c < 10) nearest = fmin_f(nearest, orow[r * 10 + c] * 12.0f);
+        }
+    return nearest;
+}
+__device__ __forceinline__ float guid_atanh(float x) { return 0.5f * log_f((1.0f + x) / (1.0f - x)); }
+
+template <int G>
+__device__ __forceinline__ void guidance_group(const float* orow, const float* __restrict__ cells, const float* goal_in,
+                                               float goal_distance, const float* vel, float sensor_dt, double inv_dt,
+                                               uint32_t lane, float (&hint)[3]) {
+    const float gnorm = sqrt_f(goal_in[0] * goal_in[0] + goal_in[1] * goal_in[1] + goal_in[2] * goal_in[2]);
+    if (gnorm < 1e-6f || goal_distance < 0.05f) {
+        hint[0] = hint[1] = hint[2] = 0.0f;
+        return;
+    }
+    const float goal[3] = {goal_in[0] / gnorm, goal_in[1] / gnorm, goal_in[2] / gnorm};
+    const float speed = sqrt_f(vel[0] * vel[0] + vel[1] * vel[1] + vel[2] * vel[2]);
+    const float stop_margin = 0.28f + speed * fmax_f(sensor_dt, 0.0f) + 0.25f * speed * speed;
+    const bool temporal = sensor_dt > 1e-4f;
+    float bscore = -1e20f, brange = 0.0f, galign = -1e20f;
+    uint32_t bcell = 80, gcell = 80;  // 80: none (the scan's initial state)
+    for (uint32_t c = lane; c < 80; c += G) {
+        const int row = int(c / 10), col = int(c % 10);
+        const float* d = cells + 3 * c;
+        const float alignment = d[0] * goal[0] + d[1] * goal[1] + d[2] * goal[2];
+        const float nearby = guid_min3x3(orow, row, col);
+        float risk = 0.0f;
+        if (temporal)
+#pragma unroll
+            for (int dr = -1; dr <= 1; dr++)
+#pragma unroll
+                for (int dc = -1; dc <= 1; dc++) {
+                    const int r = row + dr, cc = col + dc;
+                    if (r < 0 || r >= 8 || cc < 0 || cc >= 10) continue;
+                    const uint32_t k = uint32_t(r * 10 + cc);
+                    const float old = orow[80 + k] * 12.0f, now = orow[k] * 12.0f;
+                    if (old < 11.9f && now < 11.9f) {
+                        const float* ray = cells + 3 * k;
+                        const float unexpected = div_r(old - now, inv_dt) -
+                                                 (vel[0] * ray[0] + vel[1] * ray[1] + vel[2] * ray[2]);
+                        if (unexpected > 0.5f) risk = fmax_f(risk, fmin_f(0.20f * unexpected, 1.0f));
+                    }
+                }
+        const float safe_range = fmax_f(nearby - risk, 0.0f);
+        const float score = 1.4f * alignment + 0.12f * fmin_f(safe_range, 6.0f);
+        if (score > bscore) { bscore = score; bcell = c; brange = safe_range; }
+        if (alignment > galign) { galign = alignment; gcell = c; }
+    }
+#pragma unroll
+    for (int off = 1; off < G; off <<= 1) {
+        const float os = __shfl_xor(bscore, off, G), orr = __shfl_xor(brange, off, G);
+        const uint32_t oc = __shfl_xor(bcell, off, G);
+        if (os > bscore || (os == bscore && oc < bcell)) { bscore = os; bcell = oc; brange = orr; }
+        const float oa = __shfl_xor(galign, off, G);
+        const uint32_t og = __shfl_xor(gcell, off, G);
+        if (oa > galign || (oa == galign && og < gcell)) { galign = oa; gcell = og; }
+    }
+    float best_dir[3] = {1.0f, 0.0f, 0.0f};
+    if (bcell < 80) { best_dir[0] = cells[3 * bcell]; best_dir[1] = cells[3 * bcell + 1]; best_dir[2] = cells[3 * bcell + 2]; }
+    const int goal_row = gcell < 80 ? int(gcell / 10) : 0, goal_col = gcell < 80 ? int(gcell % 10) : 0;
+    const float max_speed = 1.6f;
+    const float desired_speed = fmin_f(max_speed, sqrt_f(4.0f * fmax_f(goal_distance - 0.28f, 0.0f)));
+    const float direct_range = fmax_f(guid_min3x3(orow, goal_row, goal_col), 0.0f);
+    float direction[3] = {best_dir[0], best_dir[1], best_dir[2]}, available = brange;
+    if (goal[0] > 0.0f && direct_range > stop_margin + 0.25f * desired_speed * desired_speed) {
+        direction[0] = goal[0]; direction[1] = goal[1]; direction[2] = goal[2];
+        available = direct_range;
+    }
+    const float after_stop = fmax_f(available - stop_margin - 0.15f, 0.0f);
+    const float command_speed = fmin_f(desired_speed, sqrt_f(4.0f * after_stop));
+    const float fraction = fmin_f(0.8f, command_speed * 0.5f);
+    if (direct_range < 1.2f && available > direct_range + 0.25f) {
+        const float advance = fmax_f(0.05f, fmin_f(1.0f, (direct_range - 0.25f) / 0.95f));
+        direction[0] *= advance;
+        const float norm = sqrt_f(direction[0] * direction[0] + direction[1] * direction[1] + direction[2] * direction[2]);
+#pragma unroll
+        for (int i = 0; i < 3; i++) direction[i] /= fmax_f(norm, 1e-6f);
+    }
+#pragma unroll
+    for (int i = 0; i < 3; i++) hint[i] = guid_atanh(fraction * direction[i]);
+}
+
+
 // fp64 reciprocals of the plant's constant divisors
 struct PhysRecip {
     double mass, rise[4], fall[4];

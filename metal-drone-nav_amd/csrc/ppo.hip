@@ -23,7 +23,6 @@
 namespace ppo {
 using namespace mdn;
 
-constexpr uint32_t OBS = MDN_ACTOR_OBS_POOLED;
 constexpr uint32_t COBS = MDN_CRITIC_OBS;
 constexpr uint32_t HID = MDN_HIDDEN;
 constexpr uint32_t CHUNK = 256;
@@ -31,10 +30,15 @@ constexpr uint32_t GRAD_GROUP = 32;   // chunk partials per group (gradient sums
 constexpr uint32_t NORM_GROUP = 64;   // chunk partials per group (advantage statistics)
 constexpr float LOG_TWO_PI = 1.8378770664093453f;
 
-constexpr uint32_t A_B1 = HID * OBS, A_W2 = A_B1 + HID, A_B2 = A_W2 + 4 * HID, A_LS = A_B2 + 4, A_COUNT = A_LS + 4;
 constexpr uint32_t C_B1 = HID * COBS, C_W2 = C_B1 + HID, C_B2 = C_W2 + HID, C_COUNT = C_B2 + 1;
-// Per-chunk partial layout: actor params, critic params, 4 metric sums.
-constexpr uint32_t P_TOTAL = A_COUNT + C_COUNT + 4;
+// Flat actor layout (ppo.hpp:35-40) for D inputs: 181 (pooled observation) or
+// 184 (with the geometry-prior hint).  Per-chunk partial layout: actor
+// params, critic params, 4 metric sums.
+template <uint32_t D>
+struct AL {
+    static constexpr uint32_t B1 = HID * D, W2 = B1 + HID, B2 = W2 + 4 * HID, LS = B2 + 4, COUNT = LS + 4;
+    static constexpr uint32_t P_TOTAL = COUNT + C_COUNT + 4;
+};
 
 // ---------------------------------------------------------------- GAE
 // ppo.hpp:108-126 == ppo.metal:279-304, reverse scan per env.  A workgroup
@@ -356,7 +360,9 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
     }
 }
 
+template <uint32_t D>
 __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
+    using L = AL<D>;
     __shared__ float s_h[256 * HS];
     __shared__ float s_u[U_WORDS];
     __shared__ float s_dv[256];
@@ -365,7 +371,7 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
     const uint32_t rows = a.b - n0 < 256 ? a.b - n0 : 256;
     const bool live = t < rows;
     const uint32_t n = n0 + t, m = live ? n : n0;
-    float* P = a.part + size_t(blockIdx.x) * P_TOTAL;
+    float* P = a.part + size_t(blockIdx.x) * L::P_TOTAL;
     const float scale = 1.0f / max_f(float(a.b), 1.0f);
 
     // ---- critic: forward, value, dV (ppo.hpp:82-93, 176-180)
@@ -379,11 +385,11 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
     if (t < HID) {  // critic w2: fma over rows
         float g = 0.0f;
         for (uint32_t r = 0; r < rows; r++) g = fma_f(s_dv[r], s_h[r * HS + t], g);
-        P[A_COUNT + C_W2 + t] = g;
+        P[L::COUNT + C_W2 + t] = g;
     } else if (t == HID) {  // critic b2
         float g = 0.0f;
         for (uint32_t r = 0; r < rows; r++) g += s_dv[r];
-        P[A_COUNT + C_B2] = g;
+        P[L::COUNT + C_B2] = g;
     }
     __syncthreads();
     for (uint32_t k = 0; k < HID; k++) {  // critic hidden delta, in place
@@ -394,24 +400,26 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
     if (t < HID) {  // critic b1
         float g = 0.0f;
         for (uint32_t r = 0; r < rows; r++) g += s_h[r * HS + t];
-        P[A_COUNT + C_B1 + t] = g;
+        P[L::COUNT + C_B1 + t] = g;
     }
     {   // critic W1 [64][32]: wavefronts 0 and 1 own one 32x32 tile each
         const uint32_t jt[1] = {wv & 1}, it[1] = {0};
-        chunk_weight_grad<COBS, 32, 1>(a.co, n0, rows, jt, it, wv < 2, s_u, s_h, P + A_COUNT);
+        chunk_weight_grad<COBS, 32, 1>(a.co, n0, rows, jt, it, wv < 2, s_u, s_h, P + L::COUNT);
     }
 
     // ---- actor: forward, means, loss and derivatives
-    chunk_forward<OBS>(a.obs, a.actor_w1t, a.actor + A_B1, n0, a.b, s_u, s_h);
+    chunk_forward<D>(a.obs, a.actor_w1t, a.actor + L::B1, n0, a.b, s_u, s_h);
     float mean[4];
 #pragma unroll
     for (uint32_t q = 0; q < 4; q++) {
-        float z = a.actor[A_B2 + q];
-        for (uint32_t k = 0; k < HID; k++) z = fma_f(a.actor[A_W2 + q * HID + k], s_h[t * HS + k], z);
+        float z = a.actor[L::B2 + q];
+        for (uint32_t k = 0; k < HID; k++) z = fma_f(a.actor[L::W2 + q * HID + k], s_h[t * HS + k], z);
+        // geometry prior (ppo.hpp:77): the hint inputs add to the first three means
+        if (D == MDN_ACTOR_OBS_PRIOR && q < 3) z += a.obs[size_t(m) * D + D - 3 + q];
         mean[q] = z;
     }
     const float* act = a.actions + size_t(m) * 4;
-    const float* ls = a.actor + A_LS;
+    const float* ls = a.actor + L::LS;
     float logp = 0.0f;
 #pragma unroll
     for (uint32_t q = 0; q < 4; q++) {
@@ -456,19 +464,19 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
         const uint32_t q = t / HID, k = t % HID;
         float g = 0.0f;
         for (uint32_t r = 0; r < rows; r++) g = fma_f(s_u[r * RS + q], s_h[r * HS + k], g);
-        P[A_W2 + q * HID + k] = g;
+        P[L::W2 + q * HID + k] = g;
         if (t < 12) {
             const uint32_t col = t < 4 ? t : t < 8 ? 4 + (t - 4) : 8 + (t - 8);
             float g2 = 0.0f;
             for (uint32_t r = 0; r < rows; r++) g2 += s_u[r * RS + col];
-            P[t < 4 ? A_B2 + t : t < 8 ? A_LS + (t - 4) : A_COUNT + C_COUNT + (t - 8)] = g2;
+            P[t < 4 ? L::B2 + t : t < 8 ? L::LS + (t - 4) : L::COUNT + C_COUNT + (t - 8)] = g2;
         }
     }
     __syncthreads();
     for (uint32_t k = 0; k < HID; k++) {  // actor hidden delta, in place
         float d = 0.0f;
 #pragma unroll
-        for (uint32_t q = 0; q < 4; q++) d = fma_f(dmean[q], a.actor[A_W2 + q * HID + k], d);
+        for (uint32_t q = 0; q < 4; q++) d = fma_f(dmean[q], a.actor[L::W2 + q * HID + k], d);
         const float h = s_h[t * HS + k];
         s_h[t * HS + k] = live ? d * (1.0f - h * h) : 0.0f;
     }
@@ -476,33 +484,33 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
     if (t < HID) {  // actor b1
         float g = 0.0f;
         for (uint32_t r = 0; r < rows; r++) g += s_h[r * HS + t];
-        P[A_B1 + t] = g;
+        P[L::B1 + t] = g;
     }
-    {   // actor W1 [64][181]: 2 x 6 tiles, three per wavefront
+    {   // actor W1 [64][D]: 2 x 6 tiles, three per wavefront
         const uint32_t jt[3] = {(3 * wv) / 6, (3 * wv + 1) / 6, (3 * wv + 2) / 6};
         const uint32_t it[3] = {(3 * wv) % 6, (3 * wv + 1) % 6, (3 * wv + 2) % 6};
-        chunk_weight_grad<OBS, OBS_PAD, 3>(a.obs, n0, rows, jt, it, true, s_u, s_h, P);
+        chunk_weight_grad<D, OBS_PAD, 3>(a.obs, n0, rows, jt, it, true, s_u, s_h, P);
     }
 }
 
 // Chunk partials summed within groups of GRAD_GROUP chunks, in place into
 // the group's first chunk row; grid (param blocks, groups).
-__global__ __launch_bounds__(256) void group_reduce_kernel(float* __restrict__ part, uint32_t chunks) {
+__global__ __launch_bounds__(256) void group_reduce_kernel(float* __restrict__ part, uint32_t chunks, uint32_t ptot) {
     const uint32_t p = blockIdx.x * 256 + threadIdx.x;
     const uint32_t c0 = blockIdx.y * GRAD_GROUP;
-    if (p >= P_TOTAL || c0 >= chunks) return;
+    if (p >= ptot || c0 >= chunks) return;
     const uint32_t end = c0 + GRAD_GROUP < chunks ? c0 + GRAD_GROUP : chunks;
     float s = 0.0f;
-    for (uint32_t c = c0; c < end; c++) s += part[size_t(c) * P_TOTAL + p];
-    part[size_t(c0) * P_TOTAL + p] = s;
+    for (uint32_t c = c0; c < end; c++) s += part[size_t(c) * ptot + p];
+    part[size_t(c0) * ptot + p] = s;
 }
 // Sequential sum over the group sums: grad[p] = 0 + g0[p] + g1[p] + ...
 __global__ __launch_bounds__(256) void chunk_reduce_kernel(const float* __restrict__ part, float* __restrict__ grad,
-                                                           uint32_t chunks) {
+                                                           uint32_t chunks, uint32_t ptot) {
     const uint32_t p = blockIdx.x * 256 + threadIdx.x;
-    if (p >= P_TOTAL) return;
+    if (p >= ptot) return;
     float total = 0.0f;
-    for (uint32_t c = 0; c < chunks; c += GRAD_GROUP) total += part[size_t(c) * P_TOTAL + p];
+    for (uint32_t c = 0; c < chunks; c += GRAD_GROUP) total += part[size_t(c) * ptot + p];
     grad[p] = total;
 }
 
@@ -510,13 +518,15 @@ __global__ __launch_bounds__(256) void chunk_reduce_kernel(const float* __restri
 // cpu_reference.hpp:553-567 + log-std clamp (603); block 0 = actor, 1 = critic.
 // Also refreshes the transposed first-layer copy and the metric row.
 
+template <uint32_t D>
 __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
+    using L = AL<D>;
     const bool critic = blockIdx.x == 1;
-    const uint32_t P = critic ? C_COUNT : A_COUNT;
+    const uint32_t P = critic ? C_COUNT : L::COUNT;
     float* params = critic ? a.critic : a.actor;
     float* m = critic ? a.cm : a.am;
     float* v = critic ? a.cv : a.av;
-    const float* g = a.grad + (critic ? A_COUNT : 0);
+    const float* g = a.grad + (critic ? L::COUNT : 0);
     __shared__ float part[256];
     const uint32_t t = threadIdx.x;
     float s = 0.0f;
@@ -539,13 +549,13 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
     }
     __syncthreads();
     if (!critic) {
-        if (t < 4) params[A_LS + t] = clamp_f(params[A_LS + t], -2.0f, .5f);
-        for (uint32_t e = t; e < HID * OBS; e += 256) {
-            const uint32_t h = e / OBS, i = e % OBS;
+        if (t < 4) params[L::LS + t] = clamp_f(params[L::LS + t], -2.0f, .5f);
+        for (uint32_t e = t; e < HID * D; e += 256) {
+            const uint32_t h = e / D, i = e % D;
             a.actor_w1t[size_t(i) * HID + h] = params[e];
         }
         if (t == 0) {
-            const float* ms = a.grad + A_COUNT + C_COUNT;
+            const float* ms = a.grad + L::COUNT + C_COUNT;
             a.metric_row[0] = ms[0];
             a.metric_row[1] = ms[1];
             a.metric_row[2] = ms[2];
@@ -560,12 +570,13 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
 }
 
 // Transposed first-layer copies from the flat vectors (after uploads/init).
+template <uint32_t D>
 __global__ __launch_bounds__(256) void transpose_w1_kernel(const float* __restrict__ actor,
                                                            const float* __restrict__ critic, float* __restrict__ aw,
                                                            float* __restrict__ cw) {
     const uint32_t e = blockIdx.x * 256 + threadIdx.x;
-    if (e < HID * OBS) {
-        const uint32_t h = e / OBS, i = e % OBS;
+    if (e < HID * D) {
+        const uint32_t h = e / D, i = e % D;
         aw[size_t(i) * HID + h] = actor[e];
     }
     if (e < HID * COBS) {
@@ -610,28 +621,48 @@ hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* s
     return hipGetLastError();
 }
 
+// Actor input widths built: 181 (pooled observation) and 184 (with the
+// geometry-prior hint).
 hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st) {
     if (a->b == 0) return hipSuccess;
-    hipLaunchKernelGGL(ppo::chunk_kernel, dim3((a->b + 255) / 256), dim3(256), 0, st, *a);
+    if (a->d == MDN_ACTOR_OBS_POOLED)
+        hipLaunchKernelGGL(ppo::chunk_kernel<MDN_ACTOR_OBS_POOLED>, dim3((a->b + 255) / 256), dim3(256), 0, st, *a);
+    else if (a->d == MDN_ACTOR_OBS_PRIOR)
+        hipLaunchKernelGGL(ppo::chunk_kernel<MDN_ACTOR_OBS_PRIOR>, dim3((a->b + 255) / 256), dim3(256), 0, st, *a);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, hipStream_t st) {
+hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, uint32_t d, hipStream_t st) {
     const uint32_t chunks = (b + ppo::CHUNK - 1) / ppo::CHUNK;
     const uint32_t groups = (chunks + ppo::GRAD_GROUP - 1) / ppo::GRAD_GROUP;
-    hipLaunchKernelGGL(ppo::group_reduce_kernel, dim3((ppo::P_TOTAL + 255) / 256, groups), dim3(256), 0, st, part, chunks);
-    hipLaunchKernelGGL(ppo::chunk_reduce_kernel, dim3((ppo::P_TOTAL + 255) / 256), dim3(256), 0, st, part, grad, chunks);
+    const uint32_t ptot = ppo_partial_stride(d);
+    hipLaunchKernelGGL(ppo::group_reduce_kernel, dim3((ptot + 255) / 256, groups), dim3(256), 0, st, part, chunks, ptot);
+    hipLaunchKernelGGL(ppo::chunk_reduce_kernel, dim3((ptot + 255) / 256), dim3(256), 0, st, part, grad, chunks, ptot);
     return hipGetLastError();
 }
 
 hipError_t ppo_launch_adam(const ppo::AdamArgs* a, hipStream_t st) {
-    hipLaunchKernelGGL(ppo::adam_kernel, dim3(2), dim3(256), 0, st, *a);
+    if (a->d == MDN_ACTOR_OBS_POOLED)
+        hipLaunchKernelGGL(ppo::adam_kernel<MDN_ACTOR_OBS_POOLED>, dim3(2), dim3(256), 0, st, *a);
+    else if (a->d == MDN_ACTOR_OBS_PRIOR)
+        hipLaunchKernelGGL(ppo::adam_kernel<MDN_ACTOR_OBS_PRIOR>, dim3(2), dim3(256), 0, st, *a);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* aw, float* cw, hipStream_t st) {
-    hipLaunchKernelGGL(ppo::transpose_w1_kernel, dim3((ppo::HID * ppo::OBS + 255) / 256), dim3(256), 0, st, actor, critic,
-                       aw, cw);
+hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* aw, float* cw, uint32_t d,
+                                hipStream_t st) {
+    if (d == MDN_ACTOR_OBS_POOLED)
+        hipLaunchKernelGGL(ppo::transpose_w1_kernel<MDN_ACTOR_OBS_POOLED>, dim3((ppo::HID * d + 255) / 256), dim3(256), 0,
+                           st, actor, critic, aw, cw);
+    else if (d == MDN_ACTOR_OBS_PRIOR)
+        hipLaunchKernelGGL(ppo::transpose_w1_kernel<MDN_ACTOR_OBS_PRIOR>, dim3((ppo::HID * d + 255) / 256), dim3(256), 0,
+                           st, actor, critic, aw, cw);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
@@ -640,6 +671,8 @@ hipError_t ppo_launch_metric_mean(const float* rows, float* mean, uint32_t updat
     return hipGetLastError();
 }
 
-uint32_t ppo_partial_stride() { return ppo::P_TOTAL; }
+uint32_t ppo_partial_stride(uint32_t d) {
+    return d == MDN_ACTOR_OBS_PRIOR ? ppo::AL<MDN_ACTOR_OBS_PRIOR>::P_TOTAL : ppo::AL<MDN_ACTOR_OBS_POOLED>::P_TOTAL;
+}
 
 }  // extern "C"

@@ -357,19 +357,20 @@ __device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22]
 // global memory (L1/L2 resident).  W > 1: the workgroup stages one copy of the
 // actor first layer, the RAPTOR weights and the camera rays in LDS, shared by
 // its 64*W/G envs.
-template <int W>
+template <int W, uint32_t D>
 struct WeightLds {
-    float aw[OBS * HID];
+    float aw[D * HID];
     float rw[RAPTOR_WORDS];
     float cam[3 * PIX];
 };
-template <>
-struct WeightLds<1> {};
+template <uint32_t D>
+struct WeightLds<1, D> {};
 
 // X: split ticks. The kernel stops at the policy call and takes the means
 // from a.ext_means (a policy evaluated by other kernels between launches);
-// values and next values are the caller's.
-template <int G, int K, int W, bool X>
+// values and next values are the caller's.  D: actor inputs, 181 (pooled
+// observation) or 184 (with the geometry-prior hint, ppo.hpp:30-34).
+template <int G, int K, int W, bool X, uint32_t D>
 __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     constexpr int E = 64 * W / G;    // envs per workgroup
     constexpr int U = 16 / G;        // RAPTOR units per lane
@@ -387,13 +388,16 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     const bool live = n < N;
     const uint32_t nn = live ? n : 0;
 
-    __shared__ WeightLds<W> s_wt;
+    constexpr uint32_t OS = D % 2 ? D + 4 : D + 3;  // odd stride of the observation rows
+    // the 184-input kernel drops the world rows' alignment padding to fit LDS
+    constexpr uint32_t WSTR = D == OBS ? WORLD_WORDS + 3 : WORLD_WORDS;
+    __shared__ WeightLds<W, D> s_wt;
     const float* AW1;   // actor W1 transposed [input][hidden]
     const float* RW;    // RAPTOR weights (RaptorWeights layout)
     const float* CAM;   // camera rays [pixel][3]
     if constexpr (W > 1) {
         if constexpr (!X)
-            for (uint32_t i = threadIdx.x; i < OBS * HID; i += 64 * W) s_wt.aw[i] = a.actor_w1t[i];
+            for (uint32_t i = threadIdx.x; i < D * HID; i += 64 * W) s_wt.aw[i] = a.actor_w1t[i];
         for (uint32_t i = threadIdx.x; i < RAPTOR_WORDS; i += 64 * W) s_wt.rw[i] = a.raptor[i];
         for (uint32_t i = threadIdx.x; i < 3 * PIX; i += 64 * W) s_wt.cam[i] = a.camera[i];
         __syncthreads();
@@ -406,12 +410,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         CAM = a.camera;
     }
 
-    __shared__ float s_world[E][WORLD_WORDS + 3];
+    __shared__ float s_world[E][WSTR];
     // Per-env rows have odd word strides so that the E groups of a wavefront,
     // reading the same offset of their own rows, fall in distinct banks.
     __shared__ float s_cent[E][49];
     __shared__ float s_ring[E][K * POOL + 1];   // slot j at [j * POOL]
-    __shared__ float s_obs[E][OBS + 4];
+    __shared__ float s_obs[E][OS];
     __shared__ float s_co[E][COBS + 1];
     __shared__ float s_ah[E][HID + 1];
     __shared__ float s_ch[E][HID + 1];
@@ -454,7 +458,10 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         for (uint32_t c = lane; c < 16; c += G) s_rh[grp][c] = bits_float(a.run[size_t(RW_HIDDEN + c) * N + nn]);
     const float* A = a.actor;
     const float* CR = a.critic;
-    const uint32_t a_b1 = HID * OBS, a_w2 = a_b1 + HID, a_b2 = a_w2 + 4 * HID, a_ls = a_b2 + 4;
+    const uint32_t a_b1 = HID * D, a_w2 = a_b1 + HID, a_b2 = a_w2 + 4 * HID, a_ls = a_b2 + 4;
+    // guidance inputs (sim.metal:226): sensor period in seconds, its fp64 reciprocal
+    const float sensor_dt = float(C.sensor_period) * a.phys.dt * float(C.substeps);
+    const double inv_dt = 1.0 / double(fmax_f(sensor_dt, 1e-3f));
     const uint32_t c_b1 = HID * COBS, c_w2 = c_b1 + HID, c_b2 = c_w2 + HID;
     const uint32_t sdelay = clean_env(C, nn) ? 0 : C.sensor_delay;
     const uint32_t cdelay = clean_env(C, nn) ? 0 : C.command_delay;
@@ -528,12 +535,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         }
         group_sync();
 
-        // ---- observe (sim.metal:182-228, pooled 181-input actor)
+        // ---- observe (sim.metal:182-228, pooled actor inputs + optional hint)
         const uint32_t available = r.steps / C.sensor_period;
         const uint32_t frame = available > sdelay ? available - sdelay : 0;
         const uint32_t prev = frame > 0 ? frame - 1 : 0;
         const bool have = available >= sdelay;
-        float* og = a.obs + row * OBS;
+        float* og = a.obs + row * D;
         if (active && observe) {
             for (uint32_t b = lane; b < POOL; b += G) {
                 const float cur = have ? div_r(s_ring[grp][(frame % K) * POOL + b], 1.0 / 12.0) : 1.0f;
@@ -565,6 +572,15 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             // every lane of the group holds the same values and writes them
             // (equal stores to one address; cheaper than per-value owner branches)
             for (int j = 0; j < 21; j++) { s_obs[grp][2 * POOL + j] = ctx[j]; og[2 * POOL + j] = ctx[j]; }
+            if constexpr (D == MDN_ACTOR_OBS_PRIOR) {  // geometry-prior hint (sim.metal:226)
+                group_sync();                          // the group's pooled ranges are in s_obs
+                const float goal3[3] = {ctx[0], ctx[1], ctx[2]};
+                const float vel3[3] = {ctx[4] * 4.0f, ctx[5] * 4.0f, ctx[6] * 4.0f};
+                float hint[3];
+                guidance_group<G>(s_obs[grp], a.cells, goal3, distance, vel3, sensor_dt, inv_dt, lane, hint);
+#pragma unroll
+                for (int j = 0; j < 3; j++) { s_obs[grp][D - 3 + j] = hint[j]; og[D - 3 + j] = hint[j]; }
+            }
             // critic observation (sim.metal:159-181)
             float cob[COBS];
 #pragma unroll
@@ -603,7 +619,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         } else if constexpr (W > 1) {  // all 32 envs of the workgroup on the matrix cores
             static_assert(E == 32, "matrix-core layers assume 32 envs per workgroup");
             __syncthreads();
-            wg_layer<OBS, OBS + 4, HID + 1>(&s_obs[0][0], AW1, A + a_b1, &s_ah[0][0]);
+            wg_layer<D, OS, HID + 1>(&s_obs[0][0], AW1, A + a_b1, &s_ah[0][0]);
             wg_layer<COBS, COBS + 1, HID + 1>(&s_co[0][0], a.critic_w1t, CR + c_b1, &s_ch[0][0]);
             __syncthreads();
             // heads: means (waves 0-1) and value (waves 2-3) into s_x[env][0..4]
@@ -615,7 +631,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
             for (int k = 0; k < HU; k++) acc[k] = A[a_b1 + lane * HU + k];
 #pragma unroll 4
-            for (uint32_t i = 0; i < OBS; i++) {
+            for (uint32_t i = 0; i < D; i++) {
                 const float x = s_obs[grp][i];
                 const float* w = AW1 + i * HID + lane * HU;
 #pragma unroll
@@ -647,6 +663,9 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             } else if constexpr (W > 1) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) mean[q] = s_x[grp][q];
+                if constexpr (D == MDN_ACTOR_OBS_PRIOR)  // ppo.hpp:77
+#pragma unroll
+                    for (int q = 0; q < 3; q++) mean[q] += s_obs[grp][D - 3 + q];
                 value = s_x[grp][4];
             } else {
 #pragma unroll
@@ -654,6 +673,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                     float z = A[a_b2 + q];
 #pragma unroll 8
                     for (uint32_t h = 0; h < HID; h++) z = fma_f(A[a_w2 + q * HID + h], s_ah[grp][h], z);
+                    if (D == MDN_ACTOR_OBS_PRIOR && q < 3) z += s_obs[grp][D - 3 + q];  // ppo.hpp:77
                     mean[q] = z;
                 }
                 value = CR[c_b2];
@@ -757,7 +777,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             }
             float act[4];
             if constexpr (W > 1)
-                raptor_wg<G, OBS + 4>(RW, mo, &s_obs[0][0], &s_x[0][0], &s_rh[0][0], &s_h[0][0], grp, lane, !done, act);
+                raptor_wg<G, OS>(RW, mo, &s_obs[0][0], &s_x[0][0], &s_rh[0][0], &s_h[0][0], grp, lane, !done, act);
             else
                 raptor_group<G>(RW, mo, r.hidden, hu, s_x[grp], s_h[grp], lane, !done, act);
             if (!done) {
@@ -942,19 +962,24 @@ hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream) {
 // weights in LDS (32 envs, 159 KB of LDS, one workgroup per CU); the ring of
 // the other slot counts leaves no room for that, so they run one wavefront per
 // workgroup with the weights in L1/L2.
-// Split ticks (a->ext_means set) are built for 8 lanes per env only.
-hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, hipStream_t stream) {
-#define NAV_ROLLOUT_CASE(G, K, W, X)                                                                      \
-    if (lanes_per_env == G && ring_slots == K && (a->ext_means != nullptr) == X) {                        \
-        const uint32_t envs_per_block = 64 * W / G;                                                       \
-        const uint32_t blocks = (a->cfg.n + envs_per_block - 1) / envs_per_block;                         \
-        hipLaunchKernelGGL((nav::rollout_kernel<G, K, W, X>), dim3(blocks), dim3(64 * W), 0, stream, *a); \
-        return hipGetLastError();                                                                         \
+// Split ticks (a->ext_means set) and 184-input actors are built for 8 lanes
+// per env only.
+hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, uint32_t actor_obs,
+                              hipStream_t stream) {
+#define NAV_ROLLOUT_CASE(G, K, W, X, D)                                                                        \
+    if (lanes_per_env == G && ring_slots == K && (a->ext_means != nullptr) == X && actor_obs == D) {           \
+        const uint32_t envs_per_block = 64 * W / G;                                                            \
+        const uint32_t blocks = (a->cfg.n + envs_per_block - 1) / envs_per_block;                              \
+        hipLaunchKernelGGL((nav::rollout_kernel<G, K, W, X, D>), dim3(blocks), dim3(64 * W), 0, stream, *a);   \
+        return hipGetLastError();                                                                              \
     }
-    NAV_ROLLOUT_CASE(8, 2, 4, false) NAV_ROLLOUT_CASE(8, 4, 1, false) NAV_ROLLOUT_CASE(8, 8, 1, false)
-    NAV_ROLLOUT_CASE(16, 2, 1, false) NAV_ROLLOUT_CASE(16, 4, 1, false) NAV_ROLLOUT_CASE(16, 8, 1, false)
-    NAV_ROLLOUT_CASE(4, 2, 1, false) NAV_ROLLOUT_CASE(4, 4, 1, false) NAV_ROLLOUT_CASE(4, 8, 1, false)
-    NAV_ROLLOUT_CASE(8, 2, 4, true) NAV_ROLLOUT_CASE(8, 4, 1, true) NAV_ROLLOUT_CASE(8, 8, 1, true)
+    constexpr uint32_t P = MDN_ACTOR_OBS_POOLED, H = MDN_ACTOR_OBS_PRIOR;
+    NAV_ROLLOUT_CASE(8, 2, 4, false, P) NAV_ROLLOUT_CASE(8, 4, 1, false, P) NAV_ROLLOUT_CASE(8, 8, 1, false, P)
+    NAV_ROLLOUT_CASE(16, 2, 1, false, P) NAV_ROLLOUT_CASE(16, 4, 1, false, P) NAV_ROLLOUT_CASE(16, 8, 1, false, P)
+    NAV_ROLLOUT_CASE(4, 2, 1, false, P) NAV_ROLLOUT_CASE(4, 4, 1, false, P) NAV_ROLLOUT_CASE(4, 8, 1, false, P)
+    NAV_ROLLOUT_CASE(8, 2, 4, true, P) NAV_ROLLOUT_CASE(8, 4, 1, true, P) NAV_ROLLOUT_CASE(8, 8, 1, true, P)
+    NAV_ROLLOUT_CASE(8, 2, 4, false, H) NAV_ROLLOUT_CASE(8, 4, 1, false, H) NAV_ROLLOUT_CASE(8, 8, 1, false, H)
+    NAV_ROLLOUT_CASE(8, 2, 4, true, H) NAV_ROLLOUT_CASE(8, 4, 1, true, H) NAV_ROLLOUT_CASE(8, 8, 1, true, H)
 #undef NAV_ROLLOUT_CASE
     return hipErrorInvalidValue;
 }

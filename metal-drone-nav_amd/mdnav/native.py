@@ -15,7 +15,8 @@ EXPORTS = [
     "mdn_last_error", "mdn_version", "mdn_sim_create", "mdn_sim_destroy", "mdn_sim_set_config",
     "mdn_sim_get_config", "mdn_sim_reset", "mdn_sim_collect", "mdn_sim_sync", "mdn_sim_buffer_bytes",
     "mdn_sim_download", "mdn_sim_upload", "mdn_sim_set_timing", "mdn_sim_kernel_time",
-    "mdn_sim_reset_timing", "mdn_sim_set_lanes", "mdn_ppo_create", "mdn_ppo_destroy",
+    "mdn_sim_reset_timing", "mdn_sim_set_lanes", "mdn_sim_set_actor_obs", "mdn_sim_get_actor_obs",
+    "mdn_ppo_create", "mdn_ppo_destroy",
     "mdn_ppo_rollout_update", "mdn_ppo_gae", "mdn_ppo_normalize", "mdn_ppo_update",
     "mdn_ppo_metric_mean", "mdn_ppo_optimizer_step", "mdn_ppo_updates_per_rollout",
     "mdn_op_physics_step", "mdn_op_raptor_sequence", "mdn_op_ray_world", "mdn_op_clearance",
@@ -65,6 +66,8 @@ def lib():
         _sig(L, "mdn_sim_kernel_time", I32, P, U32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(U64))
         _sig(L, "mdn_sim_reset_timing", I32, P)
         _sig(L, "mdn_sim_set_lanes", I32, P, U32)
+        _sig(L, "mdn_sim_set_actor_obs", I32, P, U32)
+        _sig(L, "mdn_sim_get_actor_obs", I32, P, ctypes.POINTER(U32))
         _sig(L, "mdn_ppo_create", I32, P, U32, U32, ctypes.POINTER(P))
         _sig(L, "mdn_ppo_destroy", None, P)
         _sig(L, "mdn_ppo_rollout_update", I32, P, U32)

@@ -59,7 +59,7 @@ def crazyflie_params():
 class Sim:
     """Batched simulator handle (Sim, main.mm:516-603)."""
 
-    def __init__(self, cfg, horizon, raptor=None, physics=None, lanes=8):
+    def __init__(self, cfg, horizon, raptor=None, physics=None, lanes=8, actor_obs=181):
         L = lib()
         self.cfg = np.array(cfg, abi.SIM_CONFIG)
         self.horizon = int(horizon)
@@ -72,6 +72,8 @@ class Sim:
         self.ppo = None
         if lanes != 8:
             check(L.mdn_sim_set_lanes(self.h, lanes))
+        if actor_obs != 181:
+            self.set_actor_obs(actor_obs)
 
     @property
     def n(self):
@@ -92,6 +94,17 @@ class Sim:
 
     def set_lanes(self, lanes):
         check(lib().mdn_sim_set_lanes(self.h, lanes))
+
+    def set_actor_obs(self, d):
+        """Actor inputs: 181, or 184 with the geometry-prior hint
+        (FIXED_PPO_ACTOR_OBS_DIM, ppo.hpp:11-34).  Fresh policy."""
+        check(lib().mdn_sim_set_actor_obs(self.h, d))
+
+    @property
+    def actor_obs(self):
+        d = ctypes.c_uint32()
+        check(lib().mdn_sim_get_actor_obs(self.h, ctypes.byref(d)))
+        return d.value
 
     def reset(self):
         check(lib().mdn_sim_reset(self.h))
@@ -275,8 +288,8 @@ class LargePPOTrainer:
 class Trainer:
     """cpu_reference::Trainer interface (cpu_reference.hpp:112-615) on the GPU."""
 
-    def __init__(self, cfg, horizon, raptor=None, physics=None, epochs=2, minibatch=256, lanes=8):
-        self.sim = Sim(cfg, horizon, raptor, physics, lanes=lanes)
+    def __init__(self, cfg, horizon, raptor=None, physics=None, epochs=2, minibatch=256, lanes=8, actor_obs=181):
+        self.sim = Sim(cfg, horizon, raptor, physics, lanes=lanes, actor_obs=actor_obs)
         self.ppo = PPOTrainer(self.sim, epochs, minibatch)
         self.horizon = horizon
 

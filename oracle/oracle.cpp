@@ -31,6 +31,7 @@
 #include <vector>
 
 #include "oracle_world.h"
+#include "oracle_guidance.h"
 
 namespace orc {
 
@@ -53,6 +54,9 @@ inline void actor_forward(const PolicyShape& s, const float* w, const float* obs
         float z = w[s.actor_b2() + a];
         const float* row = w + s.actor_w2() + size_t(a) * s.hidden;
         for (uint32_t h = 0; h < s.hidden; ++h) z = fma_f(row[h], hidden[h], z);
+        // geometry prior (ppo.hpp:30-34, 77): a 184-input actor adds the
+        // observation's guidance hint to the first three means
+        if (s.obs == MDN_ACTOR_OBS_PRIOR && a < 3) z += obs[s.obs - 3 + a];
         mean[a] = z;
     }
 }
@@ -402,6 +406,23 @@ struct Trainer {
         const float ref[3] = {run.reference_position[0] - s.position[0], run.reference_position[1] - s.position[1],
                               run.reference_position[2] - s.position[2]};
         for (int j = 0; j < 3; j++) c[18 + j] = clamp_f((r[j] * ref[0] + r[3 + j] * ref[1] + r[6 + j] * ref[2]) * 2.0f, -1.0f, 1.0f);
+        if (shape.obs == MDN_ACTOR_OBS_PRIOR) {  // guidance hint (cpu_reference.hpp:353-375)
+            float cur[80], prv[80], goal[3], vel[3], hint[3];
+            for (int j = 0; j < 80; j++) { cur[j] = o[j] * 12.0f; prv[j] = o[80 + j] * 12.0f; }
+            for (int j = 0; j < 3; j++) { goal[j] = c[j]; vel[j] = c[4 + j] * 4.0f; }
+            const float sensor_dt = float(cfg.sensor_period) * physics.dt * float(cfg.substeps);
+            if (cfg.geometry_memory) {
+                float pose[12];
+                for (int j = 0; j < 3; j++) pose[j] = s.position[j];
+                for (int j = 0; j < 9; j++) pose[3 + j] = r[j];
+                const uint32_t valid = available >= delay ? std::min(frame + 1, 8u - delay) : 0u;
+                nav_guidance_memory(cur, prv, goal, distance, vel, sensor_dt, MDN_SENSOR_TAN_V,
+                                    &sensors[size_t(n) * 8 * 320], &poses[size_t(n) * 8 * 12], pose, frame, valid, hint);
+            } else {
+                nav_guidance(cur, prv, goal, distance, vel, sensor_dt, MDN_SENSOR_TAN_V, hint);
+            }
+            for (int j = 0; j < 3; j++) o[shape.obs - 3 + j] = hint[j];
+        }
         critic_observation(s, world, run, &co[(size_t(tick) * cfg.n + n) * shape.critic_obs]);
     }
 
@@ -729,6 +750,14 @@ struct Trainer {
         critic_m.assign(critic.size(), 0.0f); critic_v.assign(critic.size(), 0.0f);
         optimizer_step = 0;
     }
+    // Actor input width (ppo.hpp:11-34 FIXED_PPO_ACTOR_OBS_DIM): 181 (pooled
+    // observation) or 184 (with the geometry-prior hint).  Fresh policy and
+    // moments; observation rows resized.
+    void set_actor_obs(uint32_t d) {
+        shape.obs = d;
+        obs.assign(size_t(cfg.n) * horizon * d, 0.0f);
+        set_hidden(shape.hidden);
+    }
     // Log-probabilities of the stored actions and values at s and s' under the
     // current policy for every rollout row (the rollout's act and next-value
     // outputs re-evaluated with this policy).
@@ -780,6 +809,22 @@ void orc_trainer_minibatch_grads(void* h, uint32_t begin, uint32_t b, float* act
 }
 void orc_trainer_set_config(void* h, const MdnSimConfig* cfg) { static_cast<Trainer*>(h)->cfg = *cfg; }
 void orc_trainer_set_hidden(void* h, uint32_t hidden) { static_cast<Trainer*>(h)->set_hidden(hidden); }
+void orc_trainer_set_actor_obs(void* h, uint32_t d) { static_cast<Trainer*>(h)->set_actor_obs(d); }
+void orc_guidance(const float* cur, const float* prev, const float* goal, float distance, const float* vel,
+                  float sensor_dt, float* hint) {
+    orc::nav_guidance(cur, prev, goal, distance, vel, sensor_dt, MDN_SENSOR_TAN_V, hint);
+}
+void orc_memory_clearance(const float* direction, const float* range_ring, const float* pose_ring, const float* pose,
+                          uint32_t latest_frame, uint32_t valid_frames, float sensor_dt, float* out) {
+    *out = orc::nav_memory_clearance(direction, range_ring, pose_ring, pose, latest_frame, valid_frames, sensor_dt,
+                                     MDN_SENSOR_TAN_V);
+}
+void orc_guidance_memory(const float* cur, const float* prev, const float* goal, float distance, const float* vel,
+                         float sensor_dt, const float* range_ring, const float* pose_ring, const float* pose,
+                         uint32_t latest_frame, uint32_t valid_frames, float* hint) {
+    orc::nav_guidance_memory(cur, prev, goal, distance, vel, sensor_dt, MDN_SENSOR_TAN_V, range_ring, pose_ring, pose,
+                             latest_frame, valid_frames, hint);
+}
 void orc_trainer_evaluate(void* h) { static_cast<Trainer*>(h)->evaluate(); }
 void orc_trainer_set_ext_means(void* h, const float* means) { static_cast<Trainer*>(h)->ext_means = means; }
 uint64_t orc_trainer_optimizer_step(void* h) { return static_cast<Trainer*>(h)->optimizer_step; }

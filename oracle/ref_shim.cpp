@@ -18,6 +18,7 @@
 #include "physics.hpp"
 #include "raptor.hpp"
 #include "ppo.hpp"
+#include "guidance.hpp"
 #include "mdnav_types.h"
 
 static_assert(sizeof(WWorld) == sizeof(MdnWorld), "world layout");
@@ -137,4 +138,21 @@ void ref_adam_update(float* params, const float* grad, float* first, float* seco
     fixed_ppo::adam_update(params, grad, first, second, count, step, lr, b1, b2, eps, wd);
 }
 
+// guidance.hpp:38-98 and 152-194 (the CPU reference's call: clearances computed
+// directly, capture age 0), legacy sensor profile
+void ref_guidance(const float* cur, const float* prev, const float* goal, float distance, const float* vel,
+                  float sensor_dt, float* hint) {
+    nav_guidance(cur, prev, goal, distance, vel, sensor_dt, NAV_SENSOR_ACTIVE_TAN_V, hint);
+}
+void ref_guidance_memory(const float* cur, const float* prev, const float* goal, float distance, const float* vel,
+                         float sensor_dt, const float* range_ring, const float* pose_ring, const float* pose,
+                         uint32_t latest_frame, uint32_t valid_frames, float* hint) {
+    nav_guidance_memory(cur, prev, goal, distance, vel, sensor_dt, NAV_SENSOR_ACTIVE_TAN_V, range_ring, pose_ring,
+                        pose, latest_frame, valid_frames, hint, nullptr, 0.0f);
+}
+void ref_memory_clearance(const float* direction, const float* range_ring, const float* pose_ring, const float* pose,
+                          uint32_t latest_frame, uint32_t valid_frames, float sensor_dt, float* out) {
+    *out = nav_memory_clearance(direction, range_ring, pose_ring, pose, latest_frame, valid_frames, sensor_dt,
+                                NAV_SENSOR_ACTIVE_TAN_V);
+}
 } // extern "C"

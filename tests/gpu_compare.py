@@ -48,11 +48,13 @@ def compare(gpu, ora, names, tol=0.0, int_exact=True):
     return bad
 
 
-def make_pair(cfg, horizon, epochs=2, minibatch=256, lanes=8):
+def make_pair(cfg, horizon, epochs=2, minibatch=256, lanes=8, actor_obs=181):
     weights = raptor_fixture()[0]
-    sim = Sim(cfg, horizon, raptor=weights, lanes=lanes)
+    sim = Sim(cfg, horizon, raptor=weights, lanes=lanes, actor_obs=actor_obs)
     ppo = PPOTrainer(sim, epochs, minibatch)
     ora = OracleTrainer(cfg, horizon, weights, epochs=epochs, minibatch=minibatch)
+    if actor_obs != 181:
+        ora.set_actor_obs(actor_obs)
     return sim, ppo, ora
 
 

@@ -52,6 +52,10 @@ def oracle():
         _sig(lib, "orc_trainer_set_hidden", None, P, U32)
         _sig(lib, "orc_trainer_evaluate", None, P)
         _sig(lib, "orc_trainer_set_ext_means", None, P, P)
+        _sig(lib, "orc_trainer_set_actor_obs", None, P, U32)
+        _sig(lib, "orc_guidance", None, P, P, P, F32, P, F32, P)
+        _sig(lib, "orc_guidance_memory", None, P, P, P, F32, P, F32, P, P, P, U32, U32, P)
+        _sig(lib, "orc_memory_clearance", None, P, P, P, P, U32, U32, F32, P)
         _sig(lib, "orc_trainer_minibatch_grads", None, P, U32, U32, P, P, P, P, P, P)
         _sig(lib, "orc_trainer_optimizer_step", U64, P)
         _sig(lib, "orc_trainer_metric_mean", None, P, P)
@@ -113,6 +117,9 @@ def ref():
         _sig(lib, "ref_actor_critic_grads", None, P, P, P, P, P, P, P, U32, P, P)
         _sig(lib, "ref_adam_update", None, P, P, P, P, U64, U64, F32, F32, F32, F32, F32)
         _sig(lib, "ref_urand", F32, ctypes.POINTER(U32))
+        _sig(lib, "ref_guidance", None, P, P, P, F32, P, F32, P)
+        _sig(lib, "ref_guidance_memory", None, P, P, P, F32, P, F32, P, P, P, U32, U32, P)
+        _sig(lib, "ref_memory_clearance", None, P, P, P, P, U32, U32, F32, P)
         _ref = lib
     return _ref
 
@@ -207,6 +214,10 @@ class OracleTrainer:
     def evaluate(self):
         """logp / values / next_values of the stored rollout under the policy."""
         self.lib.orc_trainer_evaluate(self.h)
+
+    def set_actor_obs(self, d):
+        """Actor input width: 181, or 184 with the geometry-prior hint (fresh policy)."""
+        self.lib.orc_trainer_set_actor_obs(self.h, d)
 
     def set_ext_means(self, means):
         """Means [T*N*4] used by act() in place of the actor (None: the actor)."""

@@ -46,13 +46,17 @@ def test_constant_division_exhaustive():
     all 2^32 numerators (signed zeros, subnormals, infinities, NaN) this must
     equal the correctly rounded fp32 x / b for every divisor they use: the
     plant's mass and rotor time constants (default and golden-fixture
-    parameters), the RK4 weight 6 and the observation scales."""
+    parameters), the RK4 weight 6, the observation scales and the guidance
+    hint's sensor period (period x dt x substeps for periods 1-4)."""
     say("case: exhaustive fp64-reciprocal division, all 2^32 numerators")
     from mdnav import native
     divs = [6.0, 12.0, 10.0, 5.0, 200.0]
     for p in (crazyflie(), physics_fixture()[0]):
         divs += [float(p["mass"])] + [float(v) for v in p["rotor_time_constants_rising"]] + \
                 [float(v) for v in p["rotor_time_constants_falling"]]
+        for period in range(1, 5):
+            dt = np.float32(period) * np.float32(p["dt"]) * np.float32(5)
+            divs.append(float(max(dt, np.float32(1e-3))))
     d = np.unique(np.array(divs, np.float32))
     out = np.zeros(len(d), np.uint64)
     assert native.lib().mdn_op_check_division(ptr(d), len(d), ptr(out)) == 0
@@ -236,3 +240,31 @@ def test_stress_scale_bit_exact():
                              "metric_rows"] + ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
     assert not bad, bad
     assert ora.get("runs")["episodes"].sum() >= 65536
+
+
+@pytest.mark.parametrize("variant", ["k2_production", "k4_threats_delays", "k8_sensor_delay6"])
+def test_geometry_prior_bit_exact(variant):
+    """The 184-input actor (ppo.hpp:30-34): the geometry-prior hint computed in
+    the observe phase (sim.metal:226, guidance.hpp:38-96) and added to the
+    first three means (ppo.hpp:77), then a PPO iteration over the 184-wide rows.
+    Every buffer bit-identical to the oracle, on each ring-slot variant of the
+    8-lane kernel."""
+    kw = dict(n=128, family=1, speed=1.0, distance=3.0, max_steps=40)
+    if variant == "k4_threats_delays":
+        kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=1, wind=0.5,
+                  sensor_period=2)
+    elif variant == "k8_sensor_delay6":
+        kw.update(family=6, distance=4.0, sensor_delay=6, depth_noise=0.05, dropout=0.1)
+    say("case: 184-input actor %s N=128 T=48 epochs=1 minibatch=2048" % variant)
+    cfg = config(**kw)
+    sim, ppo, ora = make_pair(cfg, 48, epochs=1, minibatch=2048, actor_obs=184)
+    assert sim.actor_obs == 184
+    sim.collect()
+    ppo.rollout_update(0)
+    sim.sync()
+    ora.iteration(0)
+    bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v",
+                             "metric_rows"] + ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
+    assert not bad, bad
+    hint = sim.get("obs").reshape(-1, 184)[:, 181:]
+    assert np.count_nonzero(hint) > hint.size // 2, "hint mostly zero"
