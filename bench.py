@@ -31,6 +31,10 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 # 24.2 kFLOP; critic at s and s' 8.7 kFLOP.  Bytes: SoA state/run read+write,
 # world, one depth frame written, observation rows written: 4.34 KB.
 FLOP_ENV_STEP = 117e3 + 24.2e3 + 8.7e3
+# The guided (184-input) actor adds the geometry-prior hint: per pooled cell
+# goal alignment, 3x3 nearest range and the 3x3 closing-speed risk (~130
+# FLOP x 80 cells), and 3 more first-layer inputs (384 FLOP): 10.8 kFLOP.
+FLOP_GUIDANCE = 10.8e3
 BYTES_ENV_STEP = 4.34e3
 # GAE + normalisation: 14 B in + 8 B out (GAE) + 3 passes over advantages.
 BYTES_GAE = 22.0
@@ -43,7 +47,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(envs, target_s=12.0):
+def cpu_baseline(envs, target_s=12.0, actor_obs=181):
     """Bounded sample of the CPU oracle on this host: same world, policy and
     PPO schedule shape (1 epoch x 4 minibatches) at 16 ticks per iteration."""
     import numpy as np
@@ -52,6 +56,8 @@ def cpu_baseline(envs, target_s=12.0):
     horizon = 16
     cfg = abi.default_config(n=envs, family=1, speed=1.0, distance=3.0)
     t = OracleTrainer(cfg, horizon, raptor_fixture()[0], epochs=1, minibatch=envs * horizon // 4)
+    if actor_obs != 181:
+        t.set_actor_obs(actor_obs)
     done, start = 0, time.perf_counter()
     while True:
         t.iteration(done)
@@ -164,6 +170,9 @@ def main():
     ap.add_argument("--schedule", choices=["baseline", "reference"], default="baseline",
                     help="baseline: 1 epoch x 4 minibatches; reference: 2 epochs x 256-row minibatches")
     ap.add_argument("--lanes", type=int, default=8)
+    ap.add_argument("--actor-obs", type=int, choices=[181, 184], default=181,
+                    help="actor inputs: 181 (pooled depth + context) or 184 (plus the geometry-prior hint, "
+                         "computed in the env step and added to the first three means)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=["small", "large", "stress"], default="small",
                     help="small: 8,192 envs x 128 ticks, 181-64-4 actor (the headline metric); large: 8,192 envs x "
@@ -189,11 +198,11 @@ def main():
     if args.workload == "stress":
         args.envs, args.horizon, args.no_cpu_baseline = 65536, 128, True
     N, T = args.envs, args.horizon
-    headline = (N, T) == (8192, 128)
+    headline = (N, T) == (8192, 128) and args.actor_obs == 181
     epochs, minibatch = (1, N * T // 4) if args.schedule == "baseline" else (2, 256)
     cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0)
     log("bench: creating sim N=%d T=%d schedule=%s" % (N, T, args.schedule))
-    sim = Sim(cfg, T, lanes=args.lanes)
+    sim = Sim(cfg, T, lanes=args.lanes, actor_obs=args.actor_obs)
     ppo = PPOTrainer(sim, epochs, minibatch)
     it = 0
     for _ in range(args.warmup):
@@ -222,14 +231,15 @@ def main():
     roll = kernels["rollout"]
     env_steps_launch = N * T
     avg_s = roll["avg_ms"] * 1e-3
-    achieved = FLOP_ENV_STEP * env_steps_launch / avg_s
+    flop_env_step = FLOP_ENV_STEP + (FLOP_GUIDANCE if args.actor_obs == 184 else 0.0)
+    achieved = flop_env_step * env_steps_launch / avg_s
     roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic_from_profile() if headline else None,
                 "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)",
                 "kernel": "rollout_kernel (fused env step + rollout actor/critic, %d ticks per launch)" % T,
                 "roof_note": "fp32 compute roof: env step on the VALU, policy/critic layers and RAPTOR dense/GRU "
                              "on fp32 MFMA; algorithmic %.1f kFLOP and %.2f KB per env-step x %d env-steps per "
-                             "launch" % (FLOP_ENV_STEP / 1e3, BYTES_ENV_STEP / 1e3, env_steps_launch),
+                             "launch" % (flop_env_step / 1e3, BYTES_ENV_STEP / 1e3, env_steps_launch),
                 "hbm_frac_algorithmic": round(BYTES_ENV_STEP * env_steps_launch / avg_s / PEAK_HBM, 5)}
     secondary = {}
     if kernels["gae"]["launches"]:
@@ -249,9 +259,11 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic: seeded procedural worlds (reference family 1), random-init policy (seed 1789)",
-        "config": {"workload": "static-box world, %d envs x %d ticks, small actor 181-64-4, %s PPO schedule"
-                               % (N, T, args.schedule),
-                   "envs": N, "horizon": T, "family": 1, "rays": 320, "actor": "181-64-4", "critic": "32-64-1",
+        "config": {"workload": "static-box world, %d envs x %d ticks, %s actor %d-64-4, %s PPO schedule"
+                               % (N, T, "small" if args.actor_obs == 181 else "guided", args.actor_obs,
+                                  args.schedule),
+                   "envs": N, "horizon": T, "family": 1, "rays": 320, "actor": "%d-64-4" % args.actor_obs,
+                   "critic": "32-64-1",
                    "epochs": epochs, "minibatch": minibatch, "lanes_per_env": args.lanes,
                    "parallelism": "single GPU"},
         "roofline": roofline,
@@ -261,7 +273,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
-        out["cpu_baseline"] = cpu_baseline(N)
+        out["cpu_baseline"] = cpu_baseline(N, actor_obs=args.actor_obs)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

@@ -108,6 +108,8 @@ struct MdnSim {
         a.rewards = rewards; a.next_values = next_values; a.terminated = terminated; a.truncated = truncated;
         a.cfg = cfg; a.phys = phys; a.count = count; a.horizon = horizon;
         a.ext_means = nullptr; a.ext_log_std = nullptr; a.tick0 = 0; a.split = 0;
+        a.sensor_dt = float(cfg.sensor_period) * phys.dt * float(cfg.substeps);
+        a.inv_sensor_dt = 1.0 / double(std::max(a.sensor_dt, 1e-3f));
         return a;
     }
 };

@@ -22,6 +22,8 @@ struct RolloutArgs {
     const float* critic_w1t;  // [32][64]
     const float* camera;      // unit pixel rays [320][3]
     const float* cells;       // pooled-cell directions [80][3] (guidance.hpp:21-26 nav_ray)
+    float sensor_dt;          // sensor period in seconds: period x dt x substeps (sim.metal:226)
+    double inv_sensor_dt;     // RN64(1 / max(sensor_dt, 1e-3)), the guidance's closing-speed divisor
     float* obs;            // [T][N][181]
     float* co;             // [T][N][32]
     float* nco;            // [T][N][32] critic observation of s'

@@ -278,30 +278,33 @@ __device__ __forceinline__ float div_r(float x, double R) { return (float)(doubl
 
 // ---------------------------------------------------------------- guidance
 // Geometry-prior hint of a 184-input actor (guidance.hpp:38-98,
-// nav_guidance): one env's lane group scores the 80 pooled cells (cell
-// c = lane + G i), reduces the best cell and the goal cell over the group with
-// the sequential scan's rule (the maximum; on equal values the first cell in
-// row-major order), and finishes replicated in every lane.  `orow` is the
-// env's observation row (pooled ranges / 12, current then previous), `cells`
-// the 80 cell directions nav_ray(row, col) (computed on the host with the same
-// fp32 operations), `inv_dt` = RN64(1 / max(sensor_dt, 1e-3)).
-__device__ __forceinline__ float guid_min3x3(const float* orow, int row, int col) {
-    float nearest = 12.0f;
-#pragma unroll
-    for (int dr = -1; dr <= 1; dr++)
-#pragma unroll
-        for (int dc = -1; dc <= 1; dc++) {
-            const int r = row + dr, c = col + dc;
-            if (r >= 0 && r < 8 && c >= 0 && c < 10) nearest = fmin_f(nearest, orow[r * 10 + c] * 12.0f);
-        }
-    return nearest;
-}
+// nav_guidance), computed by one env's 8-lane group with one row of the 8x10
+// pooled grid per lane.  The 3x3 nearest range and the 3x3 closing-speed
+// risk around a cell are a min and a max over neighbours, so each is taken as
+// a 3-row window through the neighbouring lanes (DPP row shifts) and then a
+// 3-cell window along the lane's row; the risk contribution of a cell depends
+// on that cell alone and is computed once.  The best cell and the
+// goal cell are reduced over the group with the sequential scan's rule (the
+// maximum; on equal values the first cell in row-major order), and the rest
+// runs replicated in every lane.  `orow` is the env's observation row (pooled
+// ranges / 12, current then previous), `cells` the 80 cell directions
+// nav_ray(row, col) (computed on the host with the same fp32 operations),
+// `inv_dt` = RN64(1 / max(sensor_dt, 1e-3)).
 __device__ __forceinline__ float guid_atanh(float x) { return 0.5f * log_f((1.0f + x) / (1.0f - x)); }
+
+// value of lane - 1 (UP) or lane + 1 (down) within a 16-lane DPP row; the
+// caller masks the group's edge lanes
+template <bool UP>
+__device__ __forceinline__ float guid_row_shift(float x) {
+    constexpr int ctrl = UP ? 0x111 : 0x101;  // row_shr:1 / row_shl:1
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), ctrl, 0xf, 0xf, true));
+}
 
 template <int G>
 __device__ __forceinline__ void guidance_group(const float* orow, const float* __restrict__ cells, const float* goal_in,
                                                float goal_distance, const float* vel, float sensor_dt, double inv_dt,
                                                uint32_t lane, float (&hint)[3]) {
+    static_assert(G == 8, "one pooled row per lane");
     const float gnorm = sqrt_f(goal_in[0] * goal_in[0] + goal_in[1] * goal_in[1] + goal_in[2] * goal_in[2]);
     if (gnorm < 1e-6f || goal_distance < 0.05f) {
         hint[0] = hint[1] = hint[2] = 0.0f;
@@ -311,50 +314,64 @@ __device__ __forceinline__ void guidance_group(const float* orow, const float* _
     const float speed = sqrt_f(vel[0] * vel[0] + vel[1] * vel[1] + vel[2] * vel[2]);
     const float stop_margin = 0.28f + speed * fmax_f(sensor_dt, 0.0f) + 0.25f * speed * speed;
     const bool temporal = sensor_dt > 1e-4f;
-    float bscore = -1e20f, brange = 0.0f, galign = -1e20f;
+    const uint32_t row = lane;
+    // this row's ranges and per-cell closing-speed risk (guidance.hpp:55-63: a
+    // neighbour contributes min(0.2 u, 1) when its unexpected closing speed u
+    // exceeds 0.5 m/s, else nothing; contributions are positive and the scan
+    // starts from 0), then the 3-row windows through the neighbouring lanes
+    float vn[10], vr[10];
+#pragma unroll
+    for (int j = 0; j < 10; j++) {
+        const uint32_t k = row * 10 + j;
+        const float now = orow[k] * 12.0f, old = orow[80 + k] * 12.0f;
+        const float d0 = cells[3 * k], d1 = cells[3 * k + 1], d2 = cells[3 * k + 2];
+        const float unexpected = div_r(old - now, inv_dt) - (vel[0] * d0 + vel[1] * d1 + vel[2] * d2);
+        const bool hit = temporal & (old < 11.9f) & (now < 11.9f) & (unexpected > 0.5f);
+        vn[j] = now;
+        vr[j] = hit ? fmin_f(0.20f * unexpected, 1.0f) : 0.0f;
+    }
+    const bool has_up = row > 0, has_down = row < 7;
+#pragma unroll
+    for (int j = 0; j < 10; j++) {
+        const float un = guid_row_shift<true>(vn[j]), dn = guid_row_shift<false>(vn[j]);
+        const float ur = guid_row_shift<true>(vr[j]), dr = guid_row_shift<false>(vr[j]);
+        vn[j] = has_up ? fmin_f(vn[j], un) : vn[j];
+        vn[j] = has_down ? fmin_f(vn[j], dn) : vn[j];
+        vr[j] = has_up ? fmax_f(vr[j], ur) : vr[j];
+        vr[j] = has_down ? fmax_f(vr[j], dr) : vr[j];
+    }
+    // 3-cell windows along the row; the row's cells scored in order
+    float bscore = -1e20f, brange = 0.0f, galign = -1e20f, gnear = 0.0f, near0 = 0.0f;
     uint32_t bcell = 80, gcell = 80;  // 80: none (the scan's initial state)
-    for (uint32_t c = lane; c < 80; c += G) {
-        const int row = int(c / 10), col = int(c % 10);
-        const float* d = cells + 3 * c;
-        const float alignment = d[0] * goal[0] + d[1] * goal[1] + d[2] * goal[2];
-        const float nearby = guid_min3x3(orow, row, col);
-        float risk = 0.0f;
-        if (temporal)
 #pragma unroll
-            for (int dr = -1; dr <= 1; dr++)
-#pragma unroll
-                for (int dc = -1; dc <= 1; dc++) {
-                    const int r = row + dr, cc = col + dc;
-                    if (r < 0 || r >= 8 || cc < 0 || cc >= 10) continue;
-                    const uint32_t k = uint32_t(r * 10 + cc);
-                    const float old = orow[80 + k] * 12.0f, now = orow[k] * 12.0f;
-                    if (old < 11.9f && now < 11.9f) {
-                        const float* ray = cells + 3 * k;
-                        const float unexpected = div_r(old - now, inv_dt) -
-                                                 (vel[0] * ray[0] + vel[1] * ray[1] + vel[2] * ray[2]);
-                        if (unexpected > 0.5f) risk = fmax_f(risk, fmin_f(0.20f * unexpected, 1.0f));
-                    }
-                }
-        const float safe_range = fmax_f(nearby - risk, 0.0f);
+    for (int j = 0; j < 10; j++) {
+        float nearby = fmin_f(12.0f, vn[j]), r = vr[j];
+        if (j > 0) { nearby = fmin_f(nearby, vn[j - 1]); r = fmax_f(r, vr[j - 1]); }
+        if (j < 9) { nearby = fmin_f(nearby, vn[j + 1]); r = fmax_f(r, vr[j + 1]); }
+        if (j == 0) near0 = nearby;
+        const uint32_t c = row * 10 + j;
+        const float alignment = cells[3 * c] * goal[0] + cells[3 * c + 1] * goal[1] + cells[3 * c + 2] * goal[2];
+        const float safe_range = fmax_f(nearby - r, 0.0f);
         const float score = 1.4f * alignment + 0.12f * fmin_f(safe_range, 6.0f);
         if (score > bscore) { bscore = score; bcell = c; brange = safe_range; }
-        if (alignment > galign) { galign = alignment; gcell = c; }
+        if (alignment > galign) { galign = alignment; gcell = c; gnear = nearby; }
     }
 #pragma unroll
     for (int off = 1; off < G; off <<= 1) {
         const float os = __shfl_xor(bscore, off, G), orr = __shfl_xor(brange, off, G);
         const uint32_t oc = __shfl_xor(bcell, off, G);
         if (os > bscore || (os == bscore && oc < bcell)) { bscore = os; bcell = oc; brange = orr; }
-        const float oa = __shfl_xor(galign, off, G);
+        const float oa = __shfl_xor(galign, off, G), on = __shfl_xor(gnear, off, G);
         const uint32_t og = __shfl_xor(gcell, off, G);
-        if (oa > galign || (oa == galign && og < gcell)) { galign = oa; gcell = og; }
+        if (oa > galign || (oa == galign && og < gcell)) { galign = oa; gcell = og; gnear = on; }
     }
+    // no goal cell (non-finite alignments only): the scan's fallback is cell 0
+    const float near_cell0 = __shfl(near0, 0, G);
     float best_dir[3] = {1.0f, 0.0f, 0.0f};
     if (bcell < 80) { best_dir[0] = cells[3 * bcell]; best_dir[1] = cells[3 * bcell + 1]; best_dir[2] = cells[3 * bcell + 2]; }
-    const int goal_row = gcell < 80 ? int(gcell / 10) : 0, goal_col = gcell < 80 ? int(gcell % 10) : 0;
     const float max_speed = 1.6f;
     const float desired_speed = fmin_f(max_speed, sqrt_f(4.0f * fmax_f(goal_distance - 0.28f, 0.0f)));
-    const float direct_range = fmax_f(guid_min3x3(orow, goal_row, goal_col), 0.0f);
+    const float direct_range = fmax_f(gcell < 80 ? gnear : near_cell0, 0.0f);
     float direction[3] = {best_dir[0], best_dir[1], best_dir[2]}, available = brange;
     if (goal[0] > 0.0f && direct_range > stop_margin + 0.25f * desired_speed * desired_speed) {
         direction[0] = goal[0]; direction[1] = goal[1]; direction[2] = goal[2];

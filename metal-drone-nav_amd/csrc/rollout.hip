@@ -389,8 +389,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     const uint32_t nn = live ? n : 0;
 
     constexpr uint32_t OS = D % 2 ? D + 4 : D + 3;  // odd stride of the observation rows
-    // the 184-input kernel drops the world rows' alignment padding to fit LDS
-    constexpr uint32_t WSTR = D == OBS ? WORLD_WORDS + 3 : WORLD_WORDS;
+    constexpr uint32_t WSTR = WORLD_WORDS;  // odd: env rows start in distinct banks
     __shared__ WeightLds<W, D> s_wt;
     const float* AW1;   // actor W1 transposed [input][hidden]
     const float* RW;    // RAPTOR weights (RaptorWeights layout)
@@ -459,9 +458,6 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     const float* A = a.actor;
     const float* CR = a.critic;
     const uint32_t a_b1 = HID * D, a_w2 = a_b1 + HID, a_b2 = a_w2 + 4 * HID, a_ls = a_b2 + 4;
-    // guidance inputs (sim.metal:226): sensor period in seconds, its fp64 reciprocal
-    const float sensor_dt = float(C.sensor_period) * a.phys.dt * float(C.substeps);
-    const double inv_dt = 1.0 / double(fmax_f(sensor_dt, 1e-3f));
     const uint32_t c_b1 = HID * COBS, c_w2 = c_b1 + HID, c_b2 = c_w2 + HID;
     const uint32_t sdelay = clean_env(C, nn) ? 0 : C.sensor_delay;
     const uint32_t cdelay = clean_env(C, nn) ? 0 : C.command_delay;
@@ -577,7 +573,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 const float goal3[3] = {ctx[0], ctx[1], ctx[2]};
                 const float vel3[3] = {ctx[4] * 4.0f, ctx[5] * 4.0f, ctx[6] * 4.0f};
                 float hint[3];
-                guidance_group<G>(s_obs[grp], a.cells, goal3, distance, vel3, sensor_dt, inv_dt, lane, hint);
+                guidance_group<G>(s_obs[grp], a.cells, goal3, distance, vel3, a.sensor_dt, a.inv_sensor_dt, lane, hint);
 #pragma unroll
                 for (int j = 0; j < 3; j++) { s_obs[grp][D - 3 + j] = hint[j]; og[D - 3 + j] = hint[j]; }
             }

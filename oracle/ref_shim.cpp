@@ -8,7 +8,9 @@
  * cpu_reference.hpp and the Metal sources are not buildable here (Accelerate,
  * GCD, Metal); the oracle restates them.
  */
-#define FIXED_PPO_ACTOR_OBS_DIM 181
+#ifndef FIXED_PPO_ACTOR_OBS_DIM
+#define FIXED_PPO_ACTOR_OBS_DIM 181  // pooled actor; the Makefile also builds 184
+#endif
 #include <cstdint>
 #include <cstring>
 #include <vector>

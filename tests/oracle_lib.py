@@ -16,6 +16,8 @@ from mdnav import abi  # noqa: E402
 
 ORACLE_SO = os.path.join(ROOT, "oracle", "_build", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libmdnref.so")
+# the same headers built with FIXED_PPO_ACTOR_OBS_DIM=184 (the guided actor)
+REF184_SO = os.path.join(ROOT, "oracle", "_ref", "libmdnref184.so")
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 P = ctypes.c_void_p
@@ -34,7 +36,6 @@ def _sig(lib, name, res, *args):
 
 
 _oracle = None
-_ref = None
 
 
 def oracle():
@@ -86,14 +87,17 @@ def oracle():
     return _oracle
 
 
-def ref_available():
-    return os.path.exists(REF_SO)
+def ref_available(actor_obs=181):
+    return os.path.exists(REF_SO if actor_obs == 181 else REF184_SO)
 
 
-def ref():
-    global _ref
-    if _ref is None:
-        lib = ctypes.CDLL(REF_SO)
+_refs = {}
+
+
+def ref(actor_obs=181):
+    """The reference's headers built for an actor of `actor_obs` inputs."""
+    if actor_obs not in _refs:
+        lib = ctypes.CDLL(REF_SO if actor_obs == 181 else REF184_SO)
         _sig(lib, "ref_generate_world", None, P, U32, U32, F32)
         _sig(lib, "ref_ray_world_batch", None, P, P, P, U32, P, U64)
         _sig(lib, "ref_clearance_batch", None, P, P, P, P, U64)
@@ -120,8 +124,8 @@ def ref():
         _sig(lib, "ref_guidance", None, P, P, P, F32, P, F32, P)
         _sig(lib, "ref_guidance_memory", None, P, P, P, F32, P, F32, P, P, P, U32, U32, P)
         _sig(lib, "ref_memory_clearance", None, P, P, P, P, U32, U32, F32, P)
-        _ref = lib
-    return _ref
+        _refs[actor_obs] = lib
+    return _refs[actor_obs]
 
 
 # ---------------------------------------------------------------- fixtures
@@ -228,9 +232,8 @@ class OracleTrainer:
         self.lib.orc_trainer_iteration(self.h, rollout_index)
 
     def minibatch_grads(self, begin, b):
-        sh = abi.policy_shape()
-        ag = np.zeros(sh["actor_count"], np.float32)
-        cg = np.zeros(sh["critic_count"], np.float32)
+        ag = np.zeros(self.buffer("actor").size, np.float32)
+        cg = np.zeros(self.buffer("critic").size, np.float32)
         row = np.zeros(4, np.float32)
         dm = np.zeros((b, 4), np.float32)
         dls = np.zeros((b, 4), np.float32)

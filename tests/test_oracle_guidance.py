@@ -126,3 +126,36 @@ def test_guidance_closed_forms():
     d = np.array([1.0, y, z]) / math.sqrt(1 + y * y + z * z)
     want = [math.atanh(frac * v) for v in d]
     assert np.abs(h - want).max() < 1e-6, (h, want)
+
+
+@needs_ref
+@pytest.mark.parametrize("kw", [dict(), dict(sensor_period=2, sensor_delay=1, family=13, speed=1.5)])
+def test_rollout_rows_carry_reference_hint(kw):
+    """Wiring of the hint into a 184-input observation row (sim.metal:226):
+    the last three inputs of every row equal the reference's guidance applied
+    to that row's own inputs: ranges (first 80 inputs x 12), previous ranges
+    (next 80 x 12), goal direction (context 0-2), velocity (context 4-6 x 4),
+    sensor period x dt x substeps, and the goal distance (context 3 x 10, the
+    distance/10 the row stores, so the comparison has a tolerance)."""
+    from oracle_lib import OracleTrainer, crazyflie, raptor_fixture
+    from mdnav import abi
+    cfg = abi.default_config(n=32, family=kw.get("family", 1), speed=kw.get("speed", 1.0), distance=3.0,
+                             max_steps=30, **{k: v for k, v in kw.items() if k not in ("family", "speed")})
+    t = OracleTrainer(cfg, 24, raptor_fixture()[0])
+    t.set_actor_obs(184)
+    t.collect()
+    rows = t.get("obs").reshape(-1, 184)
+    p = crazyflie()
+    sensor_dt = F(cfg["sensor_period"]) * F(p["dt"]) * F(cfg["substeps"])
+    checked = 0
+    for r in rows:
+        c = r[160:181]
+        if c[3] >= 1.4:  # distance clipped at 15 m: not recoverable
+            continue
+        cur, prev = (r[:80] * F(12)).astype(F), (r[80:160] * F(12)).astype(F)
+        goal = c[0:3].copy()
+        vel = (c[4:7] * F(4)).astype(F)
+        want = hint(ref(), "ref", cur, prev, goal, F(c[3] * F(10)), vel, sensor_dt)
+        assert np.abs(want - r[181:]).max() < 1e-4, (want, r[181:])
+        checked += 1
+    assert checked > len(rows) // 2 and np.count_nonzero(rows[:, 181:]) > 0

@@ -164,6 +164,60 @@ def test_forward_against_reference():
         assert abs(v - cv[n]) < 2e-6
 
 
+@pytest.mark.skipif(not ref_available(184), reason="oracle/_ref not built")
+def test_guided_forward_against_reference():
+    """184-input actor (ppo.hpp:30-34): the first three means carry the last
+    three inputs, the hint, on top of the MLP output (ppo.hpp:77).  Checked
+    against the reference built with FIXED_PPO_ACTOR_OBS_DIM=184, and the hint
+    term against the same MLP with the hint inputs zeroed."""
+    rng = np.random.default_rng(9)
+    count = ref(184).ref_actor_param_count()
+    assert count == 184 * 64 + 64 + 256 + 4 + 4
+    actor = rng.normal(0, 0.05, count).astype(F)
+    obs = rng.uniform(-1, 1, (8, 184)).astype(F)
+    h = np.zeros((8, 64), F)
+    m = np.zeros((8, 4), F)
+    oracle().orc_actor_forward_batch(ptr(actor), ptr(obs), 184, 64, 8, ptr(h), ptr(m))
+    for n in range(8):
+        rh, rm = np.zeros(64, F), np.zeros(4, F)
+        ref(184).ref_actor_forward(ptr(actor), ptr(obs[n]), ptr(rh), ptr(rm))
+        assert np.abs(rh - h[n]).max() < 2e-6 and np.abs(rm - m[n]).max() < 2e-6, (rm, m[n])
+    # zeroing the hint inputs and their first-layer weights removes exactly the
+    # MLP's dependence on them; the means then differ by the hint itself
+    a0, o0 = actor.copy(), obs.copy()
+    a0[:64 * 184].reshape(64, 184)[:, 181:] = 0
+    o0[:, 181:] = 0
+    m0 = np.zeros((8, 4), F)
+    oracle().orc_actor_forward_batch(ptr(a0), ptr(obs), 184, 64, 8, ptr(h), ptr(m))
+    oracle().orc_actor_forward_batch(ptr(a0), ptr(o0), 184, 64, 8, ptr(h), ptr(m0))
+    assert np.array_equal(m[:, 3], m0[:, 3])
+    assert np.abs((m[:, :3] - m0[:, :3]) - obs[:, 181:]).max() < 2e-6
+
+
+@pytest.mark.skipif(not ref_available(184), reason="oracle/_ref not built")
+def test_guided_minibatch_grads_against_reference():
+    """The 184-input trainer's batched gradients (hint inputs in the rows from
+    the rollout's guidance) against the reference's per-sample backprop."""
+    weights = raptor_fixture()[0]
+    cfg = abi.default_config(n=16, family=1, speed=1.0, distance=3.0)
+    t = OracleTrainer(cfg, 16, weights, epochs=2, minibatch=256)
+    t.set_actor_obs(184)
+    t.collect()
+    t.gae()
+    t.normalize()
+    ag, cg, row, dm, dls, dv = t.minibatch_grads(0, 256)
+    assert ag.size == ref(184).ref_actor_param_count()
+    obs = t.get("obs")[:256 * 184].copy()
+    assert np.count_nonzero(obs.reshape(256, 184)[:, 181:]) > 0
+    co = t.get("critic_obs")[:256 * 32].copy()
+    ra, rc = np.zeros_like(ag), np.zeros_like(cg)
+    ref(184).ref_actor_critic_grads(ptr(t.get("actor")), ptr(t.get("critic")), ptr(obs), ptr(co), ptr(dm),
+                                    ptr(dls), ptr(dv), 256, ptr(ra), ptr(rc))
+    assert np.abs(ag - ra).max() < 3e-5 * max(1.0, np.abs(ra).max()), np.abs(ag - ra).max()
+    assert np.abs(cg - rc).max() < 3e-5 * max(1.0, np.abs(rc).max())
+    assert np.abs(ag[64 * 184 - 3:64 * 184]).max() > 0  # hint columns of W1 get gradient
+
+
 @pytest.fixture(scope="module")
 def filled_trainer():
     weights = raptor_fixture()[0]
