@@ -103,12 +103,14 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
     """Closed-loop rollout with the wide actor choosing every action (split
     ticks: env kernel, wide forward of the tick's rows, env kernel) and wide
     critic values, then the wide-policy PPO update; roofline of the
-    wide-policy GEMMs against the dense bf16 matrix-core peak."""
+    wide-policy GEMMs against the dense bf16 matrix-core peak.  The actor is
+    the reference's capacity actor: 184 inputs (geometry-prior hint
+    included), 5120 hidden units, 967,688 parameters."""
     from mdnav import LargePPOTrainer, Sim, abi
-    N, T = envs, horizon
+    N, T, D = envs, horizon, args.actor_obs if args.actor_obs_set else 184
     cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0)
-    log("bench: large workload N=%d T=%d hidden=%d" % (N, T, hidden))
-    sim = Sim(cfg, T, lanes=args.lanes)
+    log("bench: large workload N=%d T=%d actor %d-%d-4" % (N, T, D, hidden))
+    sim = Sim(cfg, T, lanes=args.lanes, actor_obs=D)
     lp = LargePPOTrainer(sim, hidden, epochs, minibatch)
     it = 0
     for _ in range(args.warmup):
@@ -132,7 +134,8 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
         ms, n = sim.kernel_time(name)
         kernels[name] = {"total_ms": round(ms, 3), "launches": n}
     rows = N * T
-    P = (181 * hidden + hidden + 4 * hidden + 8) + (32 * hidden + 2 * hidden + 1)
+    PA = D * hidden + hidden + 4 * hidden + 8
+    P = PA + (32 * hidden + 2 * hidden + 1)
     # algorithmic FLOP: rollout 2P per row (actor at s, critic at s and s'); update per row per epoch:
     # forward 2P, first/second-layer weight gradients 2P (the backward's recomputed forward is not counted)
     flop_eval = 2.0 * rows * (P + (32 * hidden + 2 * hidden + 1))
@@ -147,9 +150,9 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
         "warmup": args.warmup, "ms_per_step": round(wall / steps * 1e3, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16 GEMMs, fp32 weights/Adam",
         "data": "synthetic: seeded procedural worlds (family 1), random-init policies (seed 1789)",
-        "config": {"workload": "large actor: %d envs x %d ticks, actor 181-%d-4 and critic 32-%d-1, "
-                               "%d epochs x %d minibatches of %d" % (N, T, hidden, hidden, epochs, rows // minibatch,
-                                                                     minibatch),
+        "config": {"workload": "large actor: %d envs x %d ticks, actor %d-%d-4 (%d parameters) and critic "
+                               "32-%d-1, %d epochs x %d minibatches of %d"
+                               % (N, T, D, hidden, PA, hidden, epochs, rows // minibatch, minibatch),
                    "behaviour_actions": "wide actor in the loop every tick; wide critic values at s and s'"},
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(achieved / 2.5e15, 4), "traffic": None,
@@ -170,18 +173,23 @@ def main():
     ap.add_argument("--schedule", choices=["baseline", "reference"], default="baseline",
                     help="baseline: 1 epoch x 4 minibatches; reference: 2 epochs x 256-row minibatches")
     ap.add_argument("--lanes", type=int, default=8)
-    ap.add_argument("--actor-obs", type=int, choices=[181, 184], default=181,
+    ap.add_argument("--actor-obs", type=int, choices=[181, 184], default=None,
                     help="actor inputs: 181 (pooled depth + context) or 184 (plus the geometry-prior hint, "
-                         "computed in the env step and added to the first three means)")
+                         "computed in the env step and added to the first three means); default 181 for the "
+                         "small actor, 184 for the large one")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=["small", "large", "stress"], default="small",
                     help="small: 8,192 envs x 128 ticks, 181-64-4 actor (the headline metric); large: 8,192 envs x "
-                         "256 ticks, 181-5120-4 actor and 32-5120-1 critic on bf16 matrix cores, 4 epochs x 64 "
+                         "256 ticks, 184-5120-4 actor (967,688 parameters) and 32-5120-1 critic on bf16 matrix cores, "
+                         "4 epochs x 64 "
                          "minibatches of 32,768; stress: 65,536 envs x 128 ticks, small actor")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="BYTES",
                     help="run only the plain copy kernel over BYTES (reads BYTES, writes BYTES per launch); "
                          "its FETCH_SIZE/WRITE_SIZE readings scale the rollout kernel's counters to bytes")
     args = ap.parse_args()
+    args.actor_obs_set = args.actor_obs is not None
+    if args.actor_obs is None:
+        args.actor_obs = 181
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box holds one MI355X); "
               "run with --gpus 1", file=sys.stderr)

@@ -804,9 +804,14 @@ struct MdnLargePPO {
 namespace {
 int lp_pack(MdnLargePPO* p) {
     MdnSim* s = p->sim;
-    HIP_TRY(lp_launch_pack(p->actor, p->hidden, OBS, 192, p->awb, s->stream));
+    HIP_TRY(lp_launch_pack(p->actor, p->hidden, p->shape.obs, 192, p->awb, s->stream));
     HIP_TRY(lp_launch_pack(p->critic, p->hidden, COBS, 32, p->cwb, s->stream));
     return MDN_OK;
+}
+// The 184-input actor's hint inputs (the last three of each obs row, added
+// to the first three means), or nullptr.
+const float* lp_prior(const MdnLargePPO* p, const float* obs) {
+    return obs && p->shape.obs == MDN_ACTOR_OBS_PRIOR ? obs + p->shape.obs - 3 : nullptr;
 }
 // Wide forward over `rows` stored rows in slices of one minibatch (the size of
 // the prepared-copy buffers): actor means from obs rows and/or critic values
@@ -814,13 +819,15 @@ int lp_pack(MdnLargePPO* p) {
 hipError_t lp_forward_rows(MdnLargePPO* p, const float* obs, const float* co, uint32_t rows, float* means,
                            float* values) {
     MdnSim* s = p->sim;
+    const uint32_t D = p->shape.obs;
     hipError_t e = hipSuccess;
     for (uint32_t r0 = 0; r0 < rows && e == hipSuccess; r0 += p->minibatch) {
         const uint32_t b = std::min(p->minibatch, rows - r0);
-        e = lp_launch_prep(obs ? obs + size_t(r0) * OBS : nullptr, co ? co + size_t(r0) * COBS : nullptr, b, p->xa,
-                           p->xaT, p->xc, p->xcT, false, s->stream);
+        const float* x = obs ? obs + size_t(r0) * D : nullptr;
+        e = lp_launch_prep(x, co ? co + size_t(r0) * COBS : nullptr, b, D, p->xa, p->xaT, p->xc, p->xcT, false,
+                           s->stream);
         if (e == hipSuccess)
-            e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, p->hidden, b,
+            e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, p->hidden, D, b, lp_prior(p, x),
                                   means ? means + size_t(r0) * 4 : nullptr, values ? values + r0 : nullptr,
                                   p->fwd_part, s->stream);
     }
@@ -862,13 +869,13 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     if (hidden > 8192) return fail(MDN_E_ARG, "mdn_lppo_create: hidden above 8192");
     if (epochs < 1 || epochs > 8) return fail(MDN_E_ARG, "mdn_lppo_create: epochs must be 1..8");
     if (minibatch == 0) return fail(MDN_E_ARG, "mdn_lppo_create: minibatch must be positive");
-    if (s->shape.obs != OBS) return fail(MDN_E_ARG, "mdn_lppo_create: the wide policy takes the 181-input actor");
     MdnLargePPO* p = new MdnLargePPO();
     p->sim = s;
     p->hidden = hidden;
     p->epochs = epochs;
     p->minibatch = uint32_t(std::min<size_t>(minibatch, s->rows()));
     p->shape.hidden = p->shape.critic_hidden = hidden;
+    p->shape.obs = s->shape.obs;
     p->updates = uint32_t((s->rows() + p->minibatch - 1) / p->minibatch) * epochs;
     const size_t A = p->shape.actor_count(), C = p->shape.critic_count(), M = p->minibatch, R = s->rows();
     int rc = MDN_OK;
@@ -894,7 +901,7 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     guard(dev_alloc(&p->dls, M * 4));
     guard(dev_alloc(&p->dv, M));
     guard(dev_alloc(&p->loss, M * 4));
-    guard(dev_alloc(&p->part, size_t(lp_backward_part_floats(p->minibatch, hidden))));
+    guard(dev_alloc(&p->part, size_t(lp_backward_part_floats(p->minibatch, hidden, p->shape.obs))));
     guard(dev_alloc(&p->ga, A));
     guard(dev_alloc(&p->gc, C));
     guard(dev_alloc(&p->col_part, ((M + 63) / 64) * 13));
@@ -955,7 +962,7 @@ int mdn_lppo_collect(MdnLargePPO* p, uint32_t count) {
     for (uint32_t t = 0; t < count && rc == MDN_OK; t++) {
         const size_t row0 = size_t(t % s->horizon) * N;
         rc = timed(s, MDN_K_LP_FORWARD, [&] {
-            return lp_forward_rows(p, s->obs + row0 * OBS, nullptr, N, p->eval_means + row0 * 4, nullptr);
+            return lp_forward_rows(p, s->obs + row0 * s->shape.obs, nullptr, N, p->eval_means + row0 * 4, nullptr);
         });
         if (rc) break;
         const bool more = t + 1 < count;
@@ -1000,17 +1007,17 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
     if (rc) return rc;
     const std::vector<uint32_t> order = mdn::minibatch_schedule(rows, p->minibatch, p->epochs, rollout_index);
     if (order.size() != p->updates) return fail(MDN_E_STATE, "wide PPO update count mismatch");
-    const uint32_t H = p->hidden;
+    const uint32_t H = p->hidden, D = p->shape.obs;
     for (size_t u = 0; u < order.size(); u++) {
         const uint32_t begin = order[u];
         const uint32_t b = std::min(p->minibatch, rows - begin);
-        const float* obs = s->obs + size_t(begin) * OBS;
+        const float* obs = s->obs + size_t(begin) * D;
         const float* co = s->co + size_t(begin) * COBS;
         rc = timed(s, MDN_K_LP_FORWARD, [&] {
-            hipError_t e = lp_launch_prep(obs, co, b, p->xa, p->xaT, p->xc, p->xcT, true, s->stream);
+            hipError_t e = lp_launch_prep(obs, co, b, D, p->xa, p->xaT, p->xc, p->xcT, true, s->stream);
             if (e == hipSuccess)
-                e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, H, b, p->means, p->values,
-                                      p->fwd_part, s->stream);
+                e = lp_launch_forward(p->xa, p->xc, p->awb, p->cwb, p->actor, p->critic, H, D, b, lp_prior(p, obs),
+                                      p->means, p->values, p->fwd_part, s->stream);
             if (e == hipSuccess)
                 e = lp_launch_loss(p->means, p->values, s->actions + size_t(begin) * 4, s->logp + begin,
                                    s->advantages + begin, s->returns + begin, p->actor + p->shape.actor_log_std(), b,
@@ -1020,7 +1027,7 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
         if (rc) return rc;
         rc = timed(s, MDN_K_LP_BACKWARD, [&] {
             return lp_launch_backward(p->xa, p->xaT, p->xc, p->xcT, p->awb, p->cwb, p->actor, p->critic, p->dm, p->dls,
-                                      p->dv, p->loss, H, b, p->part, p->ga, p->gc, p->col_part, s->stream);
+                                      p->dv, p->loss, H, D, b, p->part, p->ga, p->gc, p->col_part, s->stream);
         });
         if (rc) return rc;
         ++p->optimizer_step;
@@ -1028,7 +1035,7 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
         mdn::adam_corrections(p->optimizer_step, 0.9f, 0.999f, &c1, &c2);
         rc = timed(s, MDN_K_LP_ADAM, [&] {
             return lp_launch_adam(p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->ga, p->gc,
-                                  p->scratch, p->col_part, b, H, s->cfg.learning_rate, c1, c2, p->metric_rows + u * 4,
+                                  p->scratch, p->col_part, b, H, D, s->cfg.learning_rate, c1, c2, p->metric_rows + u * 4,
                                   s->stream);
         });
         if (rc) return rc;

@@ -107,11 +107,11 @@ hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* 
 hipError_t ppo_launch_metric_mean(const float* rows, float* mean, uint32_t updates, hipStream_t st);
 // wide-policy kernels (large.hip)
 hipError_t lp_launch_pack(const float* W, uint32_t H, uint32_t D, uint32_t K, __bf16* out, hipStream_t st);
-hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, __bf16* xa, __bf16* xaT, __bf16* xc,
-                          __bf16* xcT, bool transposed, hipStream_t st);
+hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, uint32_t d, __bf16* xa, __bf16* xaT,
+                          __bf16* xc, __bf16* xcT, bool transposed, hipStream_t st);
 hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* awb, const __bf16* cwb,
-                             const float* actor, const float* critic, uint32_t H, uint32_t B, float* means,
-                             float* values, float* part, hipStream_t st);
+                             const float* actor, const float* critic, uint32_t H, uint32_t d, uint32_t B,
+                             const float* prior, float* means, float* values, float* part, hipStream_t st);
 uint64_t lp_forward_part_floats(uint32_t B);
 hipError_t lp_launch_logp(const float* means, const float* actions, const float* log_std, uint32_t B, float* logp,
                           hipStream_t st);
@@ -121,11 +121,11 @@ hipError_t lp_launch_loss(const float* means, const float* values, const float* 
 hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16* xc, const __bf16* xcT,
                               const __bf16* awb, const __bf16* cwb,
                               const float* actor, const float* critic, const float* dm, const float* dls,
-                              const float* dv, const float* loss, uint32_t H, uint32_t B,
+                              const float* dv, const float* loss, uint32_t H, uint32_t d, uint32_t B,
                               float* part, float* ga, float* gc, float* col_part, hipStream_t st);
-uint64_t lp_backward_part_floats(uint32_t B, uint32_t H);
+uint64_t lp_backward_part_floats(uint32_t B, uint32_t H, uint32_t d);
 hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
                           __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
-                          uint32_t H, float lr, float c1, float c2, float* metric_row, hipStream_t st);
+                          uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, hipStream_t st);
 uint32_t ppo_partial_stride(uint32_t d);
 }

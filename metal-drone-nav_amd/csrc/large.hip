@@ -2,9 +2,11 @@
 // FIXED_PPO_HIDDEN_DIM, ppo.hpp:17-45, e.g. 5120 for the 967,688-parameter
 // capacity actor) on gfx950 bf16 matrix cores.
 //
-// Parameters stay fp32 in the reference's flat layout (actor: W1 [H][181],
-// b1 [H], W2 [4][H], b2 [4], log_std [4]; critic: W1 [H][32], b1 [H],
-// w2 [H], b2) with fp32 Adam moments.  The first-layer matrices are also
+// Parameters stay fp32 in the reference's flat layout (actor: W1 [H][D] with
+// D = 181 or 184 inputs, b1 [H], W2 [4][H], b2 [4], log_std [4]; critic:
+// W1 [H][32], b1 [H], w2 [H], b2) with fp32 Adam moments.  The 184-input
+// actor adds its last three inputs (the geometry-prior hint) to the first
+// three means (ppo.hpp:77) in fp32.  The first-layer matrices are also
 // kept as bf16 copies [H][K] (inputs zero-padded to K = 192 / 32) for the
 // GEMMs, refreshed by every Adam step.  GEMMs accumulate in fp32
 // (v_mfma_f32_32x32x16_bf16); activations use a fast exp-based tanh; the
@@ -29,7 +31,6 @@ using namespace mdn;
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr uint32_t OBS = MDN_ACTOR_OBS_POOLED;
 constexpr uint32_t COBS = MDN_CRITIC_OBS;
 constexpr uint32_t KA = 192, KC = 32;  // first-layer inputs padded to whole 32-wide tiles
 constexpr uint32_t RB = 64;            // rows per block (two 32-row tiles); 2 workgroups fit a CU
@@ -181,7 +182,8 @@ __global__ __launch_bounds__(256, 1) void forward_kernel(const __bf16* __restric
                                                       const __bf16* __restrict__ Wb,
                                                       const float* __restrict__ b1, const float* __restrict__ W2,
                                                       const float* __restrict__ b2, uint32_t H, uint32_t B,
-                                                      float* __restrict__ out, float* __restrict__ part) {
+                                                      float* __restrict__ out, float* __restrict__ part,
+                                                      const float* __restrict__ prior, uint32_t prior_stride) {
     constexpr uint32_t KS = K / 16;
     __shared__ float zs[4][RB * NQ];
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64, half = l / 32, lr = l % 32;
@@ -243,21 +245,24 @@ __global__ __launch_bounds__(256, 1) void forward_kernel(const __bf16* __restric
         const float v = ((zs[0][i] + zs[1][i]) + zs[2][i]) + zs[3][i];
         if (row >= B) continue;
         if (gridDim.y == 1)
-            out[size_t(row) * NQ + q] = b2[q] + v;
+            out[size_t(row) * NQ + q] = prior && q < 3 ? (b2[q] + v) + prior[size_t(row) * prior_stride + q] : b2[q] + v;
         else
             part[(size_t(blockIdx.y) * BP + row) * NQ + q] = v;
     }
 }
 
-// out[row][q] = b2[q] + the hidden slices' partial sums, in slice order.
+// out[row][q] = b2[q] + the hidden slices' partial sums, in slice order
+// (+ prior[row][q] for q < 3 when given: the geometry-prior hint).
 __global__ __launch_bounds__(256) void part_sum_kernel(const float* __restrict__ part, uint32_t S, uint32_t BP,
                                                        uint32_t B, uint32_t NQ, const float* __restrict__ b2,
-                                                       float* __restrict__ out) {
+                                                       float* __restrict__ out, const float* __restrict__ prior,
+                                                       uint32_t prior_stride) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= B * NQ) return;
     float v = part[i];
     for (uint32_t s = 1; s < S; s++) v += part[size_t(s) * BP * NQ + i];
-    out[i] = b2[i % NQ] + v;
+    const uint32_t row = i / NQ, q = i % NQ;
+    out[i] = prior && q < 3 ? (b2[q] + v) + prior[size_t(row) * prior_stride + q] : b2[q] + v;
 }
 
 // ---------------------------------------------------------------- loss
@@ -561,15 +566,15 @@ __global__ __launch_bounds__(256) void column_part_kernel(const float* __restric
 // gradients into the flat vectors (actor b2, log_std; critic b2) and the four
 // metric sums into metric_sums.
 __global__ __launch_bounds__(64) void column_finish_kernel(const float* __restrict__ col_part, uint32_t blocks,
-                                                           uint32_t H, float* __restrict__ ga, float* __restrict__ gc,
-                                                           float* __restrict__ metric_sums) {
+                                                           uint32_t H, uint32_t D, float* __restrict__ ga,
+                                                           float* __restrict__ gc, float* __restrict__ metric_sums) {
     const uint32_t t = blockIdx.x, l = threadIdx.x;  // column t, lane l adds blocks l, l + 64, ...
     float s = 0.0f;
     for (uint32_t b = l; b < blocks; b += 64) s += col_part[size_t(b) * 13 + t];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
     if (l != 0) return;
-    const uint32_t A_B2 = H * OBS + H + 4 * H, A_LS = A_B2 + 4, C_B2 = H * COBS + 2 * H;
+    const uint32_t A_B2 = H * D + H + 4 * H, A_LS = A_B2 + 4, C_B2 = H * COBS + 2 * H;
     if (t < 4) ga[A_B2 + t] = s;
     else if (t < 8) ga[A_LS + t - 4] = s;
     else if (t == 8) gc[C_B2] = s;
@@ -624,13 +629,14 @@ struct LargeAdamArgs {
 
 // cpu_reference.hpp:553-567 per element: clipped gradient, Adam (0.9, 0.999,
 // 1e-8) with host bias corrections, log-std clamp (603), bf16 refresh of the
-// first-layer copies.
+// first-layer copies.  D: actor inputs.
+template <uint32_t D>
 __global__ __launch_bounds__(256) void adam_kernel(LargeAdamArgs a) {
     const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= uint64_t(a.PA) + a.PC) return;
     const bool critic = i >= a.PA;
     const uint32_t p = uint32_t(critic ? i - a.PA : i);
-    const uint32_t A_B1 = a.H * OBS, A_LS = A_B1 + a.H + 4 * a.H + 4, C_B1 = a.H * COBS;
+    const uint32_t A_B1 = a.H * D, A_LS = A_B1 + a.H + 4 * a.H + 4, C_B1 = a.H * COBS;
     const float gi = (critic ? a.gc[p] : a.ga[p]) * a.scale[critic ? 1 : 0];
     float* params = critic ? a.critic : a.actor;
     float* m = critic ? a.cm : a.am;
@@ -642,7 +648,7 @@ __global__ __launch_bounds__(256) void adam_kernel(LargeAdamArgs a) {
     float w = params[p] - a.lr * (mi / a.c1) / (sqrt_f(vi / a.c2) + 1.0e-8f);
     if (!critic && p >= A_LS) w = clamp_f(w, -2.0f, 0.5f);
     params[p] = w;
-    if (!critic && p < A_B1) a.actor_wb[wsw(p / OBS, p % OBS, KA)] = (__bf16)w;
+    if (!critic && p < A_B1) a.actor_wb[wsw(p / D, p % D, KA)] = (__bf16)w;
     if (critic && p < C_B1) a.critic_wb[wsw(p / COBS, p % COBS, KC)] = (__bf16)w;
 }
 
@@ -657,24 +663,30 @@ hipError_t lp_launch_pack(const float* W, uint32_t H, uint32_t D, uint32_t K, __
     return hipGetLastError();
 }
 
-// bf16 copies of the B rows (actor inputs and critic inputs): xa [BP][192],
-// xaT [192][BP], xc [BP][32], xcT [32][BP] with BP = B rounded up to 128.
-// `transposed` = false skips the transposed copies (forward-only use).
-hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, __bf16* xa, __bf16* xaT, __bf16* xc,
-                          __bf16* xcT, bool transposed, hipStream_t st) {
+// bf16 copies of the B rows (actor inputs of width d and critic inputs): xa
+// [BP][192], xaT [192][BP], xc [BP][32], xcT [32][BP] with BP = B rounded up
+// to 128.  `transposed` = false skips the transposed copies (forward-only use).
+hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, uint32_t d, __bf16* xa, __bf16* xaT,
+                          __bf16* xc, __bf16* xcT, bool transposed, hipStream_t st) {
     if (B == 0) return hipSuccess;
+    if (obs && d != MDN_ACTOR_OBS_POOLED && d != MDN_ACTOR_OBS_PRIOR) return hipErrorInvalidValue;
     const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
     const uint32_t gx = (BP + 255) / 256;
-    if (obs)
-        hipLaunchKernelGGL((lp::prep_kernel<lp::OBS, lp::KA>), dim3(gx, lp::KA / 8), dim3(256), 0, st, obs, B, BP, xa,
-                           transposed ? xaT : nullptr);
+    if (obs && d == MDN_ACTOR_OBS_POOLED)
+        hipLaunchKernelGGL((lp::prep_kernel<MDN_ACTOR_OBS_POOLED, lp::KA>), dim3(gx, lp::KA / 8), dim3(256), 0, st,
+                           obs, B, BP, xa, transposed ? xaT : nullptr);
+    if (obs && d == MDN_ACTOR_OBS_PRIOR)
+        hipLaunchKernelGGL((lp::prep_kernel<MDN_ACTOR_OBS_PRIOR, lp::KA>), dim3(gx, lp::KA / 8), dim3(256), 0, st,
+                           obs, B, BP, xa, transposed ? xaT : nullptr);
     if (co)
         hipLaunchKernelGGL((lp::prep_kernel<lp::COBS, lp::KC>), dim3(gx, lp::KC / 8), dim3(256), 0, st, co, B, BP, xc,
                            transposed ? xcT : nullptr);
     return hipGetLastError();
 }
 
-// Actor means [B][4] and critic values [B] of B prepared rows.  When the
+// Actor means [B][4] and critic values [B] of B prepared rows; a d = 184
+// actor adds prior[row][0..2] (its fp32 hint inputs, row stride d) to the
+// first three means.  When the
 // row blocks alone would leave CUs short of two workgroups each, the hidden
 // units are split in up to 8
 // slices; `part` then holds the slices' partial sums (capacity
@@ -692,27 +704,28 @@ uint64_t lp_forward_part_floats(uint32_t B) {
 }
 
 hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* awb, const __bf16* cwb,
-                             const float* actor, const float* critic, uint32_t H, uint32_t B, float* means,
-                             float* values, float* part, hipStream_t st) {
+                             const float* actor, const float* critic, uint32_t H, uint32_t d, uint32_t B,
+                             const float* prior, float* means, float* values, float* part, hipStream_t st) {
     if (B == 0) return hipSuccess;
+    if ((d == MDN_ACTOR_OBS_PRIOR) != (prior != nullptr) && means) return hipErrorInvalidValue;
     const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
     const uint32_t S = forward_slices(B, H);
     const dim3 grid(BP / lp::RB, S);
-    const uint32_t A_B1 = H * lp::OBS, A_W2 = A_B1 + H, A_B2 = A_W2 + 4 * H;
+    const uint32_t A_B1 = H * d, A_W2 = A_B1 + H, A_B2 = A_W2 + 4 * H;
     const uint32_t C_B1 = H * lp::COBS, C_W2 = C_B1 + H, C_B2 = C_W2 + H;
     if (means) {
         hipLaunchKernelGGL((lp::forward_kernel<lp::KA, 4>), grid, dim3(256), 0, st, xa, BP, awb, actor + A_B1,
-                           actor + A_W2, actor + A_B2, H, B, means, part);
+                           actor + A_W2, actor + A_B2, H, B, means, part, prior, d);
         if (S > 1)
             hipLaunchKernelGGL(lp::part_sum_kernel, dim3((B * 4 + 255) / 256), dim3(256), 0, st, part, S, BP, B, 4u,
-                               actor + A_B2, means);
+                               actor + A_B2, means, prior, d);
     }
     if (values) {
         hipLaunchKernelGGL((lp::forward_kernel<lp::KC, 1>), grid, dim3(256), 0, st, xc, BP, cwb, critic + C_B1,
-                           critic + C_W2, critic + C_B2, H, B, values, part);
+                           critic + C_W2, critic + C_B2, H, B, values, part, nullptr, 0u);
         if (S > 1)
             hipLaunchKernelGGL(lp::part_sum_kernel, dim3((B + 255) / 256), dim3(256), 0, st, part, S, BP, B, 1u,
-                               critic + C_B2, values);
+                               critic + C_B2, values, nullptr, 0u);
     }
     return hipGetLastError();
 }
@@ -735,8 +748,8 @@ hipError_t lp_launch_loss(const float* means, const float* values, const float* 
 
 // Backward of both networks into the partial slots, then the slot sums into
 // the flat gradients ga (actor layout) and gc (critic layout) and the
-// per-row column partials.  Scratch: part >= chunks * (H*(181+1+4) +
-// H*(32+1+1)) floats, col_part >= ceil(B/128) * 13.
+// per-row column partials.  Scratch: part >= lp_backward_part_floats(B, H, d)
+// floats, col_part >= ceil(B/64) * 13.
 // Row chunks of the backward for B rows: the actor's (hidden tile, chunk)
 // workgroups fill one round at one per CU; the critic, whose blocks are light,
 // takes four times as many chunks and runs two workgroups per CU.
@@ -746,41 +759,46 @@ void lp_backward_chunks(uint32_t B, uint32_t H, uint32_t* actor_chunks, uint32_t
     *critic_chunks = std::max(1u, std::min(blocks, 4 * (256 / tiles)));
 }
 
-uint64_t lp_backward_part_floats(uint32_t B, uint32_t H) {
+uint64_t lp_backward_part_floats(uint32_t B, uint32_t H, uint32_t d) {
     uint32_t na, nc;
     lp_backward_chunks(B, H, &na, &nc);
-    return uint64_t(na) * H * (lp::OBS + 1 + 4) + uint64_t(nc) * H * (lp::COBS + 1 + 1);
+    return uint64_t(na) * H * (d + 1 + 4) + uint64_t(nc) * H * (lp::COBS + 1 + 1);
 }
 
 hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16* xc, const __bf16* xcT,
                               const __bf16* awb, const __bf16* cwb,
                               const float* actor, const float* critic, const float* dm, const float* dls,
-                              const float* dv, const float* loss, uint32_t H, uint32_t B,
+                              const float* dv, const float* loss, uint32_t H, uint32_t d, uint32_t B,
                               float* part, float* ga, float* gc, float* col_part, hipStream_t st) {
     if (B == 0) return hipSuccess;
+    if (d != MDN_ACTOR_OBS_POOLED && d != MDN_ACTOR_OBS_PRIOR) return hipErrorInvalidValue;
     const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
     uint32_t ca, cc;
     lp_backward_chunks(B, H, &ca, &cc);
     auto rows_per = [&](uint32_t chunks) { return ((B + chunks - 1) / chunks + lp::RB - 1) / lp::RB * lp::RB; };
     const uint32_t RA = rows_per(ca), RCc = rows_per(cc);
     const uint32_t na = (B + RA - 1) / RA, nc = (B + RCc - 1) / RCc;
-    const uint32_t A_B1 = H * lp::OBS, A_W2 = A_B1 + H;
+    const uint32_t A_B1 = H * d, A_W2 = A_B1 + H;
     const uint32_t C_B1 = H * lp::COBS, C_W2 = C_B1 + H;
-    // partial slot layout: actor [na][H*181], [na][H], [na][4][H]; critic [nc][H*32], [nc][H], [nc][1][H]
+    // partial slot layout: actor [na][H*d], [na][H], [na][4][H]; critic [nc][H*32], [nc][H], [nc][1][H]
     float* aW1 = part;
-    float* ab1 = aW1 + size_t(na) * H * lp::OBS;
+    float* ab1 = aW1 + size_t(na) * H * d;
     float* aW2 = ab1 + size_t(na) * H;
     float* cW1 = aW2 + size_t(na) * 4 * H;
     float* cb1 = cW1 + size_t(nc) * H * lp::COBS;
     float* cw2 = cb1 + size_t(nc) * H;
-    hipLaunchKernelGGL((lp::backward_kernel<lp::OBS, lp::KA, 4>), dim3(H / lp::UT, na), dim3(256), 0, st, xa, xaT,
-                       BP, awb, actor + A_B1, actor + A_W2, dm, H, B, RA, aW1, ab1, aW2);
+    if (d == MDN_ACTOR_OBS_POOLED)
+        hipLaunchKernelGGL((lp::backward_kernel<MDN_ACTOR_OBS_POOLED, lp::KA, 4>), dim3(H / lp::UT, na), dim3(256), 0,
+                           st, xa, xaT, BP, awb, actor + A_B1, actor + A_W2, dm, H, B, RA, aW1, ab1, aW2);
+    else
+        hipLaunchKernelGGL((lp::backward_kernel<MDN_ACTOR_OBS_PRIOR, lp::KA, 4>), dim3(H / lp::UT, na), dim3(256), 0,
+                           st, xa, xaT, BP, awb, actor + A_B1, actor + A_W2, dm, H, B, RA, aW1, ab1, aW2);
     hipLaunchKernelGGL((lp::backward_kernel<lp::COBS, lp::KC, 1>), dim3(H / lp::UT, nc), dim3(256), 0, st, xc, xcT,
                        BP, cwb, critic + C_B1, critic + C_W2, dv, H, B, RCc, cW1, cb1, cw2);
     auto sum = [&](const float* p, uint64_t n, uint32_t slots, float* out) {
         hipLaunchKernelGGL(lp::sum_slots_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, p, n, slots, out);
     };
-    sum(aW1, uint64_t(H) * lp::OBS, na, ga);
+    sum(aW1, uint64_t(H) * d, na, ga);
     sum(ab1, H, na, ga + A_B1);
     sum(aW2, 4ull * H, na, ga + A_W2);
     sum(cW1, uint64_t(H) * lp::COBS, nc, gc);
@@ -795,20 +813,24 @@ hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16*
 // col_part as written by lp_launch_backward.
 hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
                           __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
-                          uint32_t H, float lr, float c1, float c2, float* metric_row, hipStream_t st) {
-    const uint32_t PA = H * lp::OBS + H + 4 * H + 8, PC = H * lp::COBS + 2 * H + 1;
+                          uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, hipStream_t st) {
+    if (d != MDN_ACTOR_OBS_POOLED && d != MDN_ACTOR_OBS_PRIOR) return hipErrorInvalidValue;
+    const uint32_t PA = H * d + H + 4 * H + 8, PC = H * lp::COBS + 2 * H + 1;
     float* norm_part = scratch;
     float* scale = scratch + 2 * lp::NP;
     float* metric_sums = scale + 2;
-    hipLaunchKernelGGL(lp::column_finish_kernel, dim3(13), dim3(64), 0, st, col_part, (B + lp::RB - 1) / lp::RB, H, ga,
-                       gc, metric_sums);
+    hipLaunchKernelGGL(lp::column_finish_kernel, dim3(13), dim3(64), 0, st, col_part, (B + lp::RB - 1) / lp::RB, H, d,
+                       ga, gc, metric_sums);
     hipLaunchKernelGGL(lp::sqnorm_kernel, dim3(lp::NP, 2), dim3(256), 0, st, ga, gc, PA, PC, norm_part);
     hipLaunchKernelGGL(lp::norm_finish_kernel, dim3(1), dim3(64), 0, st, norm_part, metric_sums, B, scale, metric_row);
     lp::LargeAdamArgs a;
     a.actor = actor; a.critic = critic; a.am = am; a.av = av; a.cm = cm; a.cv = cv;
     a.actor_wb = awb; a.critic_wb = cwb; a.ga = ga; a.gc = gc; a.scale = scale;
     a.H = H; a.PA = PA; a.PC = PC; a.lr = lr; a.c1 = c1; a.c2 = c2;
-    hipLaunchKernelGGL(lp::adam_kernel, dim3((PA + PC + 255) / 256), dim3(256), 0, st, a);
+    if (d == MDN_ACTOR_OBS_POOLED)
+        hipLaunchKernelGGL(lp::adam_kernel<MDN_ACTOR_OBS_POOLED>, dim3((PA + PC + 255) / 256), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL(lp::adam_kernel<MDN_ACTOR_OBS_PRIOR>, dim3((PA + PC + 255) / 256), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -32,11 +32,12 @@ def say(*args):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("hidden", [256, 5120])
-def test_wide_policy_against_oracle(hidden):
-    say("case: wide policy hidden=%d, N=64 T=32, 1 epoch x 2 minibatches of 1024" % hidden)
+@pytest.mark.parametrize("hidden,actor_obs", [(256, 181), (5120, 181), (5120, 184)])
+def test_wide_policy_against_oracle(hidden, actor_obs):
+    """(5120, 184) is the reference's 967,688-parameter capacity actor."""
+    say("case: wide policy hidden=%d actor_obs=%d, N=64 T=32, 1 epoch x 2 minibatches of 1024" % (hidden, actor_obs))
     cfg = config(n=64, family=1, speed=1.0, distance=3.0, max_steps=40)
-    sim, _, ora = make_pair(cfg, 32, epochs=1, minibatch=1024)
+    sim, _, ora = make_pair(cfg, 32, epochs=1, minibatch=1024, actor_obs=actor_obs)
     sim.collect()
     sim.sync()
     ora.collect()
@@ -46,6 +47,8 @@ def test_wide_policy_against_oracle(hidden):
     ora.set_hidden(hidden)
     for name in ("actor", "critic"):
         assert np.array_equal(lp.get(name), ora.get(name)), ("initialisation", name)
+    if (hidden, actor_obs) == (5120, 184):
+        assert lp.get("actor").size == 967_688
 
     lp.evaluate()
     sim.sync()
@@ -79,7 +82,7 @@ def test_wide_policy_against_oracle(hidden):
     assert np.abs(m_gpu - m_ora).max() <= 1e-2 + 1e-2 * np.abs(m_ora).max()
 
 
-@pytest.mark.parametrize("variant", ["static", "threat_mix_delays", "sensor_period2"])
+@pytest.mark.parametrize("variant", ["static", "threat_mix_delays", "sensor_period2", "guided"])
 def test_wide_policy_closed_loop(variant):
     """Sim::collect with the wide actor choosing every action (split ticks:
     env kernel up to the observation, wide forward, env kernel from act).
@@ -89,7 +92,9 @@ def test_wide_policy_closed_loop(variant):
     the means themselves against the oracle's fp32 forward of the same
     observation rows at bf16 tolerance, and the values at s and s' likewise.
     Two collects in a row cover the hand-over at a collect boundary; resets
-    happen inside the split launches (max_steps below the ticks run)."""
+    happen inside the split launches (max_steps below the ticks run).
+    "guided": the 184-input actor, hint computed in the env step and added to
+    the wide means."""
     from gpu_compare import ENV_BUFFERS, compare
     from oracle_lib import oracle, ptr
 
@@ -99,9 +104,10 @@ def test_wide_policy_closed_loop(variant):
         kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=2, max_steps=30)
     elif variant == "sensor_period2":   # a frame every other tick, one frame of delay
         kw.update(sensor_period=2, sensor_delay=1, command_delay=1)
+    D = 184 if variant == "guided" else 181
     say("case: wide closed loop %s hidden=%d N=64 T=%d, two collects" % (variant, hidden, T))
     cfg = config(**kw)
-    sim, _, ora = make_pair(cfg, T, epochs=1, minibatch=1024)
+    sim, _, ora = make_pair(cfg, T, epochs=1, minibatch=1024, actor_obs=D)
     lp = LargePPOTrainer(sim, hidden, epochs=1, minibatch=1024)
     ora.set_hidden(hidden)
     actor = lp.get("actor")
@@ -112,10 +118,10 @@ def test_wide_policy_closed_loop(variant):
         sim.sync()
         means = lp.means()
         obs = np.ascontiguousarray(sim.get("obs"), np.float32)
-        rows = obs.size // 181
+        rows = obs.size // D
         want = np.zeros(rows * 4, np.float32)
         scratch = np.zeros(rows * hidden, np.float32)
-        oracle().orc_actor_forward_batch(ptr(actor), ptr(obs), 181, hidden, rows, ptr(scratch), ptr(want))
+        oracle().orc_actor_forward_batch(ptr(actor), ptr(obs), D, hidden, rows, ptr(scratch), ptr(want))
         merr = float(np.abs(means.astype(np.float64) - want).max())
         ora.set_ext_means(means)
         ora.collect()
