@@ -35,6 +35,10 @@ FLOP_ENV_STEP = 117e3 + 24.2e3 + 8.7e3
 # goal alignment, 3x3 nearest range and the 3x3 closing-speed risk (~130
 # FLOP x 80 cells), and 3 more first-layer inputs (384 FLOP): 10.8 kFLOP.
 FLOP_GUIDANCE = 10.8e3
+# Geometry-memory hint per env-step: 640 remembered points built (~45 FLOP
+# each), 85 candidate sweeps x 640 points (~10 FLOP per pair: along, lateral,
+# contact), 85 candidate scores (~60 FLOP): 0.58 MFLOP.
+FLOP_MEMORY = 640 * 45 + 85 * 640 * 10 + 85 * 60
 BYTES_ENV_STEP = 4.34e3
 # GAE + normalisation: 14 B in + 8 B out (GAE) + 3 passes over advantages.
 BYTES_GAE = 22.0
@@ -47,14 +51,14 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(envs, target_s=12.0, actor_obs=181):
+def cpu_baseline(envs, target_s=12.0, actor_obs=181, geometry_memory=False):
     """Bounded sample of the CPU oracle on this host: same world, policy and
     PPO schedule shape (1 epoch x 4 minibatches) at 16 ticks per iteration."""
     import numpy as np
     from oracle_lib import OracleTrainer, oracle, raptor_fixture
     from mdnav import abi
     horizon = 16
-    cfg = abi.default_config(n=envs, family=1, speed=1.0, distance=3.0)
+    cfg = abi.default_config(n=envs, family=1, speed=1.0, distance=3.0, geometry_memory=1 if geometry_memory else 0)
     t = OracleTrainer(cfg, horizon, raptor_fixture()[0], epochs=1, minibatch=envs * horizon // 4)
     if actor_obs != 181:
         t.set_actor_obs(actor_obs)
@@ -177,6 +181,9 @@ def main():
                     help="actor inputs: 181 (pooled depth + context) or 184 (plus the geometry-prior hint, "
                          "computed in the env step and added to the first three means); default 181 for the "
                          "small actor, 184 for the large one")
+    ap.add_argument("--geometry-memory", action="store_true",
+                    help="with the 184-input actor: the history-aware hint (8-frame range and pose rings, 85 "
+                         "candidate sweeps) from the memory kernel, one env launch and one memory launch per tick")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=["small", "large", "stress"], default="small",
                     help="small: 8,192 envs x 128 ticks, 181-64-4 actor (the headline metric); large: 8,192 envs x "
@@ -189,7 +196,9 @@ def main():
     args = ap.parse_args()
     args.actor_obs_set = args.actor_obs is not None
     if args.actor_obs is None:
-        args.actor_obs = 181
+        args.actor_obs = 184 if args.geometry_memory else 181
+    if args.geometry_memory and args.actor_obs != 184:
+        sys.exit("--geometry-memory needs the 184-input actor")
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each GPU box holds one MI355X); "
               "run with --gpus 1", file=sys.stderr)
@@ -206,9 +215,10 @@ def main():
     if args.workload == "stress":
         args.envs, args.horizon, args.no_cpu_baseline = 65536, 128, True
     N, T = args.envs, args.horizon
-    headline = (N, T) == (8192, 128) and args.actor_obs == 181
+    headline = (N, T) == (8192, 128) and args.actor_obs == 181 and not args.geometry_memory
     epochs, minibatch = (1, N * T // 4) if args.schedule == "baseline" else (2, 256)
-    cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0)
+    cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0,
+                             geometry_memory=1 if args.geometry_memory else 0)
     log("bench: creating sim N=%d T=%d schedule=%s" % (N, T, args.schedule))
     sim = Sim(cfg, T, lanes=args.lanes, actor_obs=args.actor_obs)
     ppo = PPOTrainer(sim, epochs, minibatch)
@@ -233,23 +243,34 @@ def main():
     log("bench: timed %d iterations in %.3f s (GPU %.3f s)" % (args.steps, wall, gpu_s))
 
     kernels = {}
-    for name in ("rollout", "gae", "normalize", "rows", "grads", "adam"):
+    for name in ("rollout", "memory", "gae", "normalize", "rows", "grads", "adam"):
         ms, n = sim.kernel_time(name)
         kernels[name] = {"total_ms": round(ms, 4), "launches": n, "avg_ms": round(ms / n, 5) if n else None}
     roll = kernels["rollout"]
     env_steps_launch = N * T
-    avg_s = roll["avg_ms"] * 1e-3
+    # one launch per iteration (with the geometry memory: one per tick, timed
+    # here per iteration)
+    avg_s = roll["total_ms"] * 1e-3 / args.steps
     flop_env_step = FLOP_ENV_STEP + (FLOP_GUIDANCE if args.actor_obs == 184 else 0.0)
     achieved = flop_env_step * env_steps_launch / avg_s
     roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic_from_profile() if headline else None,
                 "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)",
-                "kernel": "rollout_kernel (fused env step + rollout actor/critic, %d ticks per launch)" % T,
+                "kernel": ("rollout_kernel (fused env step + rollout actor/critic, %d ticks per launch)" % T
+                           if not args.geometry_memory else
+                           "rollout_kernel (env step + rollout actor/critic, split at the hint: %d ticks in %d "
+                           "launches per iteration)" % (T, roll["launches"] // args.steps)),
                 "roof_note": "fp32 compute roof: env step on the VALU, policy/critic layers and RAPTOR dense/GRU "
                              "on fp32 MFMA; algorithmic %.1f kFLOP and %.2f KB per env-step x %d env-steps per "
                              "launch" % (flop_env_step / 1e3, BYTES_ENV_STEP / 1e3, env_steps_launch),
                 "hbm_frac_algorithmic": round(BYTES_ENV_STEP * env_steps_launch / avg_s / PEAK_HBM, 5)}
     secondary = {}
+    if kernels["memory"]["launches"]:
+        mem_s = kernels["memory"]["total_ms"] * 1e-3 / args.steps
+        secondary["memory"] = {"bound": "valu", "achieved_TFLOPs": round(FLOP_MEMORY * N * T / mem_s / 1e12, 3),
+                               "frac": round(FLOP_MEMORY * N * T / mem_s / PEAK_FP32, 4),
+                               "ms_per_iteration": round(mem_s * 1e3, 3),
+                               "note": "%.0f kFLOP per env-step" % (FLOP_MEMORY / 1e3)}
     if kernels["gae"]["launches"]:
         gae_s = kernels["gae"]["avg_ms"] * 1e-3
         secondary["gae"] = {"bound": "hbm", "achieved_GBps": round(BYTES_GAE * N * T / gae_s / 1e9, 1),
@@ -267,9 +288,9 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic: seeded procedural worlds (reference family 1), random-init policy (seed 1789)",
-        "config": {"workload": "static-box world, %d envs x %d ticks, %s actor %d-64-4, %s PPO schedule"
+        "config": {"workload": "static-box world, %d envs x %d ticks, %s actor %d-64-4%s, %s PPO schedule"
                                % (N, T, "small" if args.actor_obs == 181 else "guided", args.actor_obs,
-                                  args.schedule),
+                                  " with the geometry-memory hint" if args.geometry_memory else "", args.schedule),
                    "envs": N, "horizon": T, "family": 1, "rays": 320, "actor": "%d-64-4" % args.actor_obs,
                    "critic": "32-64-1",
                    "epochs": epochs, "minibatch": minibatch, "lanes_per_env": args.lanes,
@@ -281,7 +302,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
-        out["cpu_baseline"] = cpu_baseline(N, actor_obs=args.actor_obs)
+        out["cpu_baseline"] = cpu_baseline(N, actor_obs=args.actor_obs, geometry_memory=args.geometry_memory)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

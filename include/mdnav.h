@@ -43,7 +43,7 @@ enum MdnBuffer {
     MDN_BUF_COMMANDS = 5,    /* float[N][8][4]                commands     */
     MDN_BUF_ACTOR = 6,       /* float[actor_param_count]      actor        */
     MDN_BUF_CRITIC = 7,      /* float[critic_param_count]     critic       */
-    MDN_BUF_OBS = 8,         /* float[T][N][181]              obs          */
+    MDN_BUF_OBS = 8,         /* float[T][N][181 or 184]       obs          */
     MDN_BUF_CRITIC_OBS = 9,  /* float[T][N][32]               co           */
     MDN_BUF_ACTIONS = 10,    /* float[T][N][4]                actions      */
     MDN_BUF_LOGP = 11,       /* float[T][N]                   logp         */
@@ -73,7 +73,8 @@ enum MdnKernel {
     MDN_K_LP_FORWARD = 6,  /* wide-policy forward (evaluation and minibatch) + loss terms */
     MDN_K_LP_BACKWARD = 7, /* wide-policy backward partials and their sums */
     MDN_K_LP_ADAM = 8,     /* wide-policy clip + Adam + bf16 refresh */
-    MDN_K_COUNT = 9
+    MDN_K_MEMORY = 9,      /* geometry-memory hint of one tick (memory.metal + guidance.hpp:152-194) */
+    MDN_K_COUNT = 10
 };
 
 const char* mdn_last_error(void);
@@ -114,8 +115,10 @@ int mdn_sim_set_lanes(MdnSim* sim, uint32_t lanes);
  * cpu_reference.hpp:446).  Replaces the policy by a fresh initialisation of
  * the new shape (actor and critic, one seed stream) and resizes the
  * observation rows.  Call before mdn_ppo_create / mdn_lppo_create.  The
- * 184-input rollout runs 8 lanes per env; the geometry-memory variant of the
- * hint (cfg.geometry_memory = 1) returns MDN_E_ARG. */
+ * 184-input rollout runs 8 lanes per env.  With cfg.geometry_memory = 1 the
+ * hint is the history-aware one (guidance.hpp:152-194 over the 8-frame range
+ * and pose rings, cpu_reference.hpp:364-372): mdn_sim_collect then runs one
+ * env launch and one memory launch per tick. */
 int mdn_sim_set_actor_obs(MdnSim* sim, uint32_t actor_obs);
 int mdn_sim_get_actor_obs(const MdnSim* sim, uint32_t* actor_obs);
 

@@ -87,7 +87,9 @@ struct MdnSim {
     float* commands = nullptr;
     float* raptor = nullptr;
     float* camera = nullptr;
-    float* cells = nullptr;  // pooled-cell directions of the guidance hint [80][3]
+    float* cells = nullptr;     // pooled-cell directions of the guidance hint [80][3]
+    float* pix_rays = nullptr;  // raw-pixel directions of the geometry memory [320][3]
+    uint32_t* mem_head = nullptr;  // per-env memory header [N][16]
     // policy
     float* actor = nullptr;
     float* critic = nullptr;
@@ -110,6 +112,7 @@ struct MdnSim {
         a.ext_means = nullptr; a.ext_log_std = nullptr; a.tick0 = 0; a.split = 0;
         a.sensor_dt = float(cfg.sensor_period) * phys.dt * float(cfg.substeps);
         a.inv_sensor_dt = 1.0 / double(std::max(a.sensor_dt, 1e-3f));
+        a.mem_head = nullptr;
         return a;
     }
 };
@@ -239,6 +242,8 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
     guard(dev_alloc(&s->raptor, 2084));
     guard(dev_alloc(&s->camera, 960));
     guard(dev_alloc(&s->cells, 240));
+    guard(dev_alloc(&s->pix_rays, 960));
+    guard(dev_alloc(&s->mem_head, size_t(N) * nav::MEM_HEAD_WORDS));
     guard(dev_alloc(&s->actor, s->shape.actor_count()));
     guard(dev_alloc(&s->critic, s->shape.critic_count()));
     guard(dev_alloc(&s->actor_w1t, size_t(OBS) * HID));
@@ -281,10 +286,19 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
         const float inv = 1.0f / mdn::sqrt_f(1.0f + y * y + z * z);
         cells[3 * k] = inv; cells[3 * k + 1] = y * inv; cells[3 * k + 2] = z * inv;
     }
+    // guidance.hpp:122: unit direction through raw pixel `hit` of the 20x16 grid
+    std::vector<float> pix(960);
+    for (uint32_t hit = 0; hit < 320; hit++) {
+        const float ry = 1.0f - (float(hit % 20) + .5f) / 10.0f;
+        const float rz = MDN_SENSOR_TAN_V * (1.0f - (float(hit / 20) + .5f) / 8.0f);
+        const float inv = 1.0f / mdn::sqrt_f(1 + ry * ry + rz * rz);
+        pix[3 * hit] = inv; pix[3 * hit + 1] = ry * inv; pix[3 * hit + 2] = rz * inv;
+    }
     std::vector<float> actor(s->shape.actor_count()), critic(s->shape.critic_count());
     mdn::init_policy(s->shape, actor.data(), critic.data());
     if (hipMemcpy(s->camera, cam.data(), cam.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(s->cells, cells.data(), cells.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(s->pix_rays, pix.data(), pix.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(s->raptor, raptor, sizeof(MdnRaptorWeights), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(s->actor, actor.data(), actor.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(s->critic, critic.data(), critic.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
@@ -307,6 +321,7 @@ void mdn_sim_destroy(MdnSim* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->ppo) mdn_ppo_destroy(s->ppo);
     void* bufs[] = {s->state, s->run, s->world, s->sensors, s->poses, s->commands, s->raptor, s->camera, s->cells,
+                    s->pix_rays, s->mem_head,
                     s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->obs, s->co, s->nco, s->actions, s->logp,
                     s->values, s->rewards, s->next_values, s->advantages, s->returns, s->terminated, s->truncated};
     for (void* b : bufs)
@@ -325,8 +340,6 @@ int mdn_sim_set_config(MdnSim* s, const MdnSimConfig* cfg) {
     if (cfg->sensor_period == 0) return fail(MDN_E_ARG, "sensor_period must be positive");
     if (cfg->sensor_delay > 6 || cfg->command_delay > 7)
         return fail(MDN_E_ARG, "delay rings support <=6 sensor frames and <=7 command steps");
-    if (cfg->geometry_memory && s->shape.obs == MDN_ACTOR_OBS_PRIOR)
-        return fail(MDN_E_ARG, "the geometry-memory hint is not built; set geometry_memory = 0");
     s->cfg = *cfg;
     return MDN_OK;
 }
@@ -343,8 +356,6 @@ int mdn_sim_set_actor_obs(MdnSim* s, uint32_t actor_obs) {
     if (actor_obs != MDN_ACTOR_OBS_POOLED && actor_obs != MDN_ACTOR_OBS_PRIOR)
         return fail(MDN_E_ARG, "actor inputs must be 181 (pooled) or 184 (with the geometry-prior hint)");
     if (s->ppo) return fail(MDN_E_STATE, "set the actor's inputs before creating the PPO trainer");
-    if (s->cfg.geometry_memory && actor_obs == MDN_ACTOR_OBS_PRIOR)
-        return fail(MDN_E_ARG, "the geometry-memory hint is not built; set geometry_memory = 0");
     HIP_TRY(hipStreamSynchronize(s->stream));
     mdn::PolicyShape shape = s->shape;
     shape.obs = actor_obs;
@@ -399,7 +410,29 @@ int mdn_sim_collect(MdnSim* s, uint32_t count) {
     const int lanes = int(s->lanes), slots = ring_slots(s->cfg);
     if (s->shape.obs == MDN_ACTOR_OBS_PRIOR && lanes != 8)
         return fail(MDN_E_ARG, "the 184-input actor's rollout runs 8 lanes per env");
-    return timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, lanes, slots, s->shape.obs, s->stream); });
+    if (s->shape.obs != MDN_ACTOR_OBS_PRIOR || !s->cfg.geometry_memory)
+        return timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, lanes, slots, s->shape.obs, s->stream); });
+    // Geometry-memory hint: split ticks.  Tick 0 up to its observation; then
+    // per tick: the memory kernel writes the hint of the tick's rows, and one
+    // launch acts, advances, resets and observes the next tick.
+    nav::RolloutArgs b = s->args(1);
+    b.mem_head = s->mem_head;
+    b.split = nav::SPLIT_END_AFTER_OBSERVE;
+    rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&b, 8, slots, s->shape.obs, s->stream); });
+    nav::MemoryArgs m;
+    m.head = s->mem_head; m.sensors = s->sensors; m.poses = s->poses; m.pix_rays = s->pix_rays; m.cells = s->cells;
+    m.sensor_dt = b.sensor_dt; m.inv_sensor_dt = b.inv_sensor_dt; m.n = s->cfg.n;
+    for (uint32_t t = 0; t < count && rc == MDN_OK; t++) {
+        m.obs = s->obs + size_t(t % s->horizon) * s->cfg.n * s->shape.obs;
+        rc = timed(s, MDN_K_MEMORY, [&] { return nav_launch_memory_hint(&m, s->stream); });
+        if (rc) break;
+        const bool more = t + 1 < count;
+        b.count = more ? 2 : 1;
+        b.tick0 = t;
+        b.split = nav::SPLIT_BEGIN_AT_ACT | (more ? nav::SPLIT_END_AFTER_OBSERVE : 0u);
+        rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&b, 8, slots, s->shape.obs, s->stream); });
+    }
+    return rc;
 }
 
 int mdn_sim_sync(MdnSim* s, double* gpu_seconds) {
@@ -954,6 +987,11 @@ int mdn_lppo_collect(MdnLargePPO* p, uint32_t count) {
     nav::RolloutArgs a = s->args(1);
     a.ext_means = p->eval_means;
     a.ext_log_std = p->actor + p->shape.actor_log_std();
+    const bool memory = s->shape.obs == MDN_ACTOR_OBS_PRIOR && s->cfg.geometry_memory;
+    if (memory) a.mem_head = s->mem_head;
+    nav::MemoryArgs m;
+    m.head = s->mem_head; m.sensors = s->sensors; m.poses = s->poses; m.pix_rays = s->pix_rays; m.cells = s->cells;
+    m.sensor_dt = a.sensor_dt; m.inv_sensor_dt = a.inv_sensor_dt; m.n = N;
     // tick 0 up to its observation; then per tick: wide actor means of the
     // tick's rows, and one launch that acts, advances, resets and observes the
     // next tick
@@ -961,6 +999,11 @@ int mdn_lppo_collect(MdnLargePPO* p, uint32_t count) {
     rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, 8, slots, s->shape.obs, s->stream); });
     for (uint32_t t = 0; t < count && rc == MDN_OK; t++) {
         const size_t row0 = size_t(t % s->horizon) * N;
+        if (memory) {  // the geometry-memory hint of the tick's rows
+            m.obs = s->obs + row0 * s->shape.obs;
+            rc = timed(s, MDN_K_MEMORY, [&] { return nav_launch_memory_hint(&m, s->stream); });
+            if (rc) break;
+        }
         rc = timed(s, MDN_K_LP_FORWARD, [&] {
             return lp_forward_rows(p, s->obs + row0 * s->shape.obs, nullptr, N, p->eval_means + row0 * 4, nullptr);
         });

@@ -42,10 +42,37 @@ struct RolloutArgs {
     // tick t of this launch writes row block (tick0 + t) % horizon; means come
     // from ext_means [T][N][4] and log_std from ext_log_std; values and next
     // values are left to the caller.
+    // The in-kernel policy (ext_means null) runs split ticks too: a launch
+    // that begins at act reloads the observation rows of its first tick.
     const float* ext_means;
     const float* ext_log_std;
     uint32_t tick0;
     uint32_t split;        // SPLIT_* flags
+    // Geometry-memory hint (184-input actor, cfg.geometry_memory): instead of
+    // the memory-less hint, observe writes the env's memory header [N][16]
+    // (MEM_HEAD_* words) and a separate kernel writes the hint inputs of the
+    // tick's rows before the launch that acts on them.
+    uint32_t* mem_head;
+};
+// memory header words
+constexpr uint32_t MEM_HEAD_OBSERVED = 0;  // 1: observed this tick (else skip the env)
+constexpr uint32_t MEM_HEAD_FRAME = 1;     // newest usable frame (absolute; ring slot = frame % 8)
+constexpr uint32_t MEM_HEAD_VALID = 2;     // frames usable since reset (cpu_reference.hpp:366-367)
+constexpr uint32_t MEM_HEAD_DISTANCE = 3;  // goal distance (float bits)
+constexpr uint32_t MEM_HEAD_POSE = 4;      // position [3], body-to-world rotation row-major [9] (float bits)
+constexpr uint32_t MEM_HEAD_WORDS = 16;
+
+// Geometry-memory hint of one tick's rows (memory.hip).
+struct MemoryArgs {
+    const uint32_t* head;   // [N][MEM_HEAD_WORDS] written by the tick's observation
+    float* obs;             // the tick's rows [N][184]; the kernel writes inputs 181-183
+    const float* sensors;   // [N][8][320] range ring
+    const float* poses;     // [N][8][12] pose ring
+    const float* pix_rays;  // [320][3] unit rays through the raw pixels (guidance.hpp:122)
+    const float* cells;     // [80][3] pooled-cell rays (nav_ray)
+    float sensor_dt;
+    double inv_sensor_dt;
+    uint32_t n;
 };
 // The first tick's depth and observation were produced by the previous launch.
 constexpr uint32_t SPLIT_BEGIN_AT_ACT = 1;
@@ -87,6 +114,7 @@ extern "C" {
 hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream);
 hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, uint32_t actor_obs,
                               hipStream_t stream);
+hipError_t nav_launch_memory_hint(const nav::MemoryArgs* a, hipStream_t stream);
 hipError_t nav_launch_raptor_fixture(const float* RW, const float* obs, uint32_t steps, uint32_t copies,
                                      float* actions, float* hidden, int lanes_per_env, hipStream_t st);
 hipError_t nav_launch_physics_fixture(const MdnPhysicsState* in, const float* actions, const float* winds,

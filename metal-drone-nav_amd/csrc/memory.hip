@@ -1,0 +1,257 @@
+// memory.hip — the geometry-memory hint of the 184-input actor
+// (guidance.hpp:100-194 nav_memory_clearance / nav_guidance_memory, as the CPU
+// reference calls it: cpu_reference.hpp:353-375; the reference's GPU splits it
+// into memory.metal:9-153 + sim.metal:226).
+//
+// One 256-thread workgroup per env, run between the env kernel's observation
+// of a tick and the launch that acts on it:
+//   1. the env's up to 8 x 80 remembered range hits become body-frame points
+//      (position, |p|^2, 3 + radius, radius^2) in LDS, built once instead of
+//      once per candidate direction;
+//   2. 255 threads = 85 candidate sweeps x 3 thirds of the points scan them
+//      (every lane reads the same point: LDS broadcast); the thirds' nearest
+//      contacts are combined with a min, which is exact in any order;
+//   3. the 85 candidates are scored and reduced with the sequential scan's
+//      rule (maximum score, first candidate on ties), and one lane writes the
+//      hint to the row's last three inputs.
+// Every value is computed with the operations and order of the oracle's
+// restatement, so the hint is bit-identical to it.
+#include <hip/hip_runtime.h>
+
+#include "kernel_args.h"
+#include "mdnav_math.h"
+#include "mdnav_types.h"
+
+namespace mem {
+using namespace mdn;
+
+constexpr uint32_t OBS = MDN_ACTOR_OBS_PRIOR;
+constexpr uint32_t POINTS = 640, CANDIDATES = 85, PARTS = 3, PART = (POINTS + PARTS - 1) / PARTS;
+constexpr uint32_t THREADS = 256;
+
+__device__ __forceinline__ float fbits(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ float div_r(float x, double r) { return float(double(x) * r); }
+
+struct Point {
+    float4 xyz2;  // body-frame x, y, z and x^2 + y^2 + z^2
+    float2 lim;   // 3 + radius (-1: no point), radius^2
+};
+
+// guidance.hpp:27-34 over the LDS copy of the current ranges (already x 12)
+__device__ __forceinline__ float min3x3(const float* cur, int row, int col) {
+    float nearest = 12.0f;
+    for (int dr = -1; dr <= 1; dr++)
+        for (int dc = -1; dc <= 1; dc++) {
+            const int r = row + dr, c = col + dc;
+            if (r >= 0 && r < 8 && c >= 0 && c < 10) nearest = fmin_f(nearest, cur[r * 10 + c]);
+        }
+    return nearest;
+}
+// guidance.hpp:55-63 over the per-cell risk contributions (0 or min(0.2 u, 1))
+__device__ __forceinline__ float max3x3(const float* v, int row, int col) {
+    float risk = 0.0f;
+    for (int dr = -1; dr <= 1; dr++)
+        for (int dc = -1; dc <= 1; dc++) {
+            const int r = row + dr, c = col + dc;
+            if (r >= 0 && r < 8 && c >= 0 && c < 10) risk = fmax_f(risk, v[r * 10 + c]);
+        }
+    return risk;
+}
+
+// arg-max over a wavefront with the first index winning ties
+__device__ __forceinline__ void wave_argmax(float& v, uint32_t& idx) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off, 64);
+        const uint32_t oi = __shfl_xor(idx, off, 64);
+        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+    }
+}
+
+__global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a) {
+    __shared__ Point pts[POINTS];
+    __shared__ float cur[80], risk_v[80], part_near[PARTS][CANDIDATES];
+    __shared__ float cand_score[2], cand_free[CANDIDATES];
+    __shared__ uint32_t cand_idx[2], goal_cell_s[2];
+    __shared__ float goal_al_s[2];
+    const uint32_t n = blockIdx.x, t = threadIdx.x, wv = t / 64;
+    const uint32_t* hd = a.head + size_t(n) * nav::MEM_HEAD_WORDS;
+    if (hd[nav::MEM_HEAD_OBSERVED] == 0u) return;  // uniform over the workgroup
+    float* og = a.obs + size_t(n) * OBS;
+    const float* ctx = og + 160;
+    const float distance = fbits(hd[nav::MEM_HEAD_DISTANCE]);
+    const float gin[3] = {ctx[0], ctx[1], ctx[2]};
+    const float vel[3] = {ctx[4] * 4.0f, ctx[5] * 4.0f, ctx[6] * 4.0f};
+    const float gnorm = sqrt_f(gin[0] * gin[0] + gin[1] * gin[1] + gin[2] * gin[2]);
+    if (gnorm < 1e-6f || distance < 0.05f) {
+        if (t < 3) og[OBS - 3 + t] = 0.0f;
+        return;
+    }
+    const float goal[3] = {gin[0] / gnorm, gin[1] / gnorm, gin[2] / gnorm};
+    const float speed = sqrt_f(vel[0] * vel[0] + vel[1] * vel[1] + vel[2] * vel[2]);
+    const float sensor_dt = a.sensor_dt;
+    const float stop_margin = 0.28f + speed * fmax_f(sensor_dt, 0.0f) + 0.25f * speed * speed;
+    const uint32_t latest = hd[nav::MEM_HEAD_FRAME], valid = hd[nav::MEM_HEAD_VALID];
+    float pose[12];
+#pragma unroll
+    for (int j = 0; j < 12; j++) pose[j] = fbits(hd[nav::MEM_HEAD_POSE + j]);
+
+    // 1. remembered points (guidance.hpp:113-139 up to the sweep test)
+    for (uint32_t j = t; j < POINTS; j += THREADS) {
+        const uint32_t back = j / 80, cell = j % 80, row = cell / 10, col = cell % 10;
+        Point p;
+        p.xyz2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        p.lim = make_float2(-1.0f, 0.0f);
+        if (back < valid) {
+            const uint32_t frame = (latest + 8u - back) % 8u;
+            const float* old_pose = a.poses + (size_t(n) * 8 + frame) * 12;
+            const float* ranges = a.sensors + (size_t(n) * 8 + frame) * 320;
+            const uint32_t px = row * 2 * 20 + col * 2;
+            uint32_t hit = px;
+            float range = ranges[px];
+            const uint32_t pixels[3] = {px + 1, px + 20, px + 21};
+#pragma unroll
+            for (int k = 0; k < 3; k++)
+                if (ranges[pixels[k]] < range) { range = ranges[pixels[k]]; hit = pixels[k]; }
+            if (!(range <= 0.01f || range >= 11.9f)) {
+                const float* ray = a.pix_rays + 3 * hit;
+                const float wx = old_pose[3] * ray[0] + old_pose[4] * ray[1] + old_pose[5] * ray[2];
+                const float wy = old_pose[6] * ray[0] + old_pose[7] * ray[1] + old_pose[8] * ray[2];
+                const float wz = old_pose[9] * ray[0] + old_pose[10] * ray[1] + old_pose[11] * ray[2];
+                const float dx = old_pose[0] + range * wx - pose[0];
+                const float dy = old_pose[1] + range * wy - pose[1];
+                const float dz = old_pose[2] + range * wz - pose[2];
+                const float x = pose[3] * dx + pose[6] * dy + pose[9] * dz;
+                const float y = pose[4] * dx + pose[7] * dy + pose[10] * dz;
+                const float z = pose[5] * dx + pose[8] * dy + pose[11] * dz;
+                // nav_memory_point_radius with the capture-age term off
+                const float age = fmax_f(float(back) * fmax_f(sensor_dt, 0.0f), 0.0f) + 0.0f;
+                const float radius = 0.20f + 0.015f * range + 0.15f * age;
+                p.xyz2 = make_float4(x, y, z, x * x + y * y + z * z);
+                p.lim = make_float2(3.0f + radius, radius * radius);
+            }
+        }
+        pts[j] = p;
+    }
+    // per-cell current range x 12 and closing-speed risk contribution
+    if (t < 80) {
+        const float now = og[t] * 12.0f, old = og[80 + t] * 12.0f;
+        cur[t] = now;
+        const float* ray = a.cells + 3 * t;
+        const float unexpected = div_r(old - now, a.inv_sensor_dt) - (vel[0] * ray[0] + vel[1] * ray[1] + vel[2] * ray[2]);
+        const bool hit = (sensor_dt > 1e-4f) & (old < 11.9f) & (now < 11.9f) & (unexpected > 0.5f);
+        risk_v[t] = hit ? fmin_f(0.20f * unexpected, 1.0f) : 0.0f;
+    }
+    // goal cell: the cell ray best aligned with the goal (first on ties), wave 0 and 1
+    if (t < 128) {
+        float al = -1e20f;
+        uint32_t c = 80;
+        if (t < 80) {
+            const float* d = a.cells + 3 * t;
+            al = d[0] * goal[0] + d[1] * goal[1] + d[2] * goal[2];
+            if (!(al == al)) al = -INFINITY;  // the scan never selects a NaN
+            c = t;
+        }
+        wave_argmax(al, c);
+        if ((t & 63) == 0) { goal_al_s[wv] = al; goal_cell_s[wv] = c; }
+    }
+    __syncthreads();
+    uint32_t gcell = goal_cell_s[0];
+    if (goal_al_s[1] > goal_al_s[0] || (goal_al_s[1] == goal_al_s[0] && goal_cell_s[1] < gcell)) gcell = goal_cell_s[1];
+    const float gsel = goal_al_s[1] > goal_al_s[0] || (goal_al_s[1] == goal_al_s[0] && goal_cell_s[1] < goal_cell_s[0])
+                           ? goal_al_s[1] : goal_al_s[0];
+    // scan's fallback without any finite alignment: cell (0, 0)
+    const uint32_t goal_row = gsel > -1e20f ? gcell / 10 : 0, goal_col = gsel > -1e20f ? gcell % 10 : 0;
+
+    // candidate direction (guidance.hpp:164-166)
+    auto direction = [&](uint32_t c, float d[3]) {
+        if (c < 80) {
+            d[0] = a.cells[3 * c]; d[1] = a.cells[3 * c + 1]; d[2] = a.cells[3 * c + 2];
+        } else if (c == 80) {
+            d[0] = goal[0]; d[1] = goal[1]; d[2] = goal[2];
+        } else {
+            d[0] = 0.0f;
+            d[1] = c >= 83 ? (c == 83 ? 1.0f : -1.0f) : 0.0f;
+            d[2] = c < 83 ? (c == 81 ? 1.0f : -1.0f) : 0.0f;
+        }
+    };
+
+    // 2. swept-sphere clearance of every candidate over a third of the points
+    // (guidance.hpp:134-139)
+    if (t < PARTS * CANDIDATES) {
+        const uint32_t c = t % CANDIDATES, part = t / CANDIDATES;
+        float d[3];
+        direction(c, d);
+        float sw[3] = {1.2f * d[0] + 0.35f * vel[0], 1.2f * d[1] + 0.35f * vel[1], 1.2f * d[2] + 0.35f * vel[2]};
+        const float sn = sqrt_f(sw[0] * sw[0] + sw[1] * sw[1] + sw[2] * sw[2]);
+#pragma unroll
+        for (int j = 0; j < 3; j++) sw[j] /= fmax_f(sn, 1e-6f);
+        float nearest = 3.0f;
+        const uint32_t j0 = part * PART, j1 = min(POINTS, j0 + PART);
+        for (uint32_t j = j0; j < j1; j++) {
+            const float4 q = pts[j].xyz2;
+            const float2 l = pts[j].lim;
+            const float along = q.x * sw[0] + q.y * sw[1] + q.z * sw[2];
+            if (along <= 0.0f || along > l.x) continue;
+            const float lateral2 = fmax_f(q.w - along * along, 0.0f);
+            if (lateral2 < l.y) nearest = fmin_f(nearest, fmax_f(along - sqrt_f(l.y - lateral2), 0.0f));
+        }
+        part_near[part][c] = nearest;
+    }
+    __syncthreads();
+
+    // 3. candidate scores (guidance.hpp:167-183) and the best candidate
+    const float desired_speed = fmin_f(1.6f, sqrt_f(4.0f * fmax_f(distance - 0.28f, 0.0f)));
+    float score = -1e20f;
+    uint32_t ci = CANDIDATES;
+    if (t < CANDIDATES) {
+        float d[3];
+        direction(t, d);
+        const int row = t < 80 ? int(t / 10) : int(goal_row), col = t < 80 ? int(t % 10) : int(goal_col);
+        float free = fmin_f(fmin_f(part_near[0][t], part_near[1][t]), part_near[2][t]);
+        const float observed = min3x3(cur, row, col);
+        if (t < 81) free = fmin_f(free, observed);
+        const float temporal_risk = max3x3(risk_v, row, col);
+        free = fmax_f(free - temporal_risk, 0.0f);
+        const float alignment = d[0] * goal[0] + d[1] * goal[1] + d[2] * goal[2];
+        const float required = stop_margin + 0.15f + desired_speed * desired_speed * .25f;
+        score = 1.4f * alignment + 0.20f * fmin_f(free, 3.0f) - (free < required ? 3.0f * (required - free) / required : 0.0f);
+        if (!(score == score)) score = -INFINITY;  // the scan never selects a NaN
+        ci = t;
+        cand_free[t] = free;
+    }
+    if (t < 128) {
+        wave_argmax(score, ci);
+        if ((t & 63) == 0) { cand_score[wv] = score; cand_idx[wv] = ci; }
+    }
+    __syncthreads();
+    if (t == 0) {
+        uint32_t best = cand_idx[0];
+        if (cand_score[1] > cand_score[0] || (cand_score[1] == cand_score[0] && cand_idx[1] < best)) best = cand_idx[1];
+        const bool any = (cand_score[0] > -1e20f) | (cand_score[1] > -1e20f);
+        float best_dir[3] = {1.0f, 0.0f, 0.0f}, best_free = 0.0f;
+        if (any) {
+            direction(best, best_dir);
+            best_free = cand_free[best];
+        }
+        const float tan_v = MDN_SENSOR_TAN_V;
+        const bool goal_in_fov = goal[0] > 0.0f && fabs_f(goal[1]) <= goal[0] && fabs_f(goal[2]) <= tan_v * goal[0];
+        const float after_stop = fmax_f(best_free - stop_margin - 0.15f, 0.0f);
+        float command_speed = fmin_f(desired_speed, sqrt_f(4.0f * after_stop));
+        if (!goal_in_fov) command_speed = fmin_f(command_speed, 0.25f);
+        const float fraction = fmin_f(0.8f, command_speed * 0.5f);
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+            const float x = fraction * best_dir[i];
+            og[OBS - 3 + i] = 0.5f * log_f((1.0f + x) / (1.0f - x));
+        }
+    }
+}
+
+}  // namespace mem
+
+extern "C" hipError_t nav_launch_memory_hint(const nav::MemoryArgs* a, hipStream_t st) {
+    if (a->n == 0) return hipSuccess;
+    hipLaunchKernelGGL(mem::memory_hint_kernel, dim3(a->n), dim3(mem::THREADS), 0, st, *a);
+    return hipGetLastError();
+}

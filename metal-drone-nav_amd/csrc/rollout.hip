@@ -434,7 +434,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     {   // pooled ring cache: LDS slot f%K holds frame f for the last K frames
         // (a launch that begins at act already holds the frame cast for the
         // current step, if one was due)
-        const int last = (X && (a.split & SPLIT_BEGIN_AT_ACT)) ? int(r.steps / C.sensor_period)
+        const int last = (a.split & SPLIT_BEGIN_AT_ACT) ? int(r.steps / C.sensor_period)
                          : r.steps == 0                         ? -1
                                                                 : int((r.steps - 1) / C.sensor_period);
         for (uint32_t e = lane; e < uint32_t(K) * POOL; e += G) {
@@ -464,11 +464,11 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     group_sync();
 
     for (uint32_t t = 0; t < a.count; t++) {
-        const uint32_t tick = X ? (a.tick0 + t) % a.horizon : t % a.horizon;
+        const uint32_t tick = (a.tick0 + t) % a.horizon;
         const size_t row = size_t(tick) * N + nn;
         const bool active = live && !(C.eval && r.episodes);
         // depth and observation of this tick still to do
-        const bool observe = !X || t != 0 || !(a.split & SPLIT_BEGIN_AT_ACT);
+        const bool observe = t != 0 || !(a.split & SPLIT_BEGIN_AT_ACT);
         const uint32_t count = min(float_bits(world[160]), 16u);  // slots of WWorld
 
         // ---- obstacle centres at the current time (world.hpp:32-41)
@@ -568,7 +568,20 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             // every lane of the group holds the same values and writes them
             // (equal stores to one address; cheaper than per-value owner branches)
             for (int j = 0; j < 21; j++) { s_obs[grp][2 * POOL + j] = ctx[j]; og[2 * POOL + j] = ctx[j]; }
-            if constexpr (D == MDN_ACTOR_OBS_PRIOR) {  // geometry-prior hint (sim.metal:226)
+            if (D == MDN_ACTOR_OBS_PRIOR && a.mem_head) {  // geometry-memory hint: computed outside
+                uint32_t* hd = a.mem_head + size_t(nn) * MEM_HEAD_WORDS;
+                const uint32_t valid = have ? min(frame + 1, 8u - sdelay) : 0u;
+                if (lane == 0) {
+                    hd[MEM_HEAD_OBSERVED] = 1u;
+                    hd[MEM_HEAD_FRAME] = frame;
+                    hd[MEM_HEAD_VALID] = valid;
+                    hd[MEM_HEAD_DISTANCE] = float_bits(distance);
+#pragma unroll
+                    for (int j = 0; j < 3; j++) hd[MEM_HEAD_POSE + j] = float_bits(s.p[j]);
+#pragma unroll
+                    for (int j = 0; j < 9; j++) hd[MEM_HEAD_POSE + 3 + j] = float_bits(R[j]);
+                }
+            } else if constexpr (D == MDN_ACTOR_OBS_PRIOR) {  // geometry-prior hint (sim.metal:226)
                 group_sync();                          // the group's pooled ranges are in s_obs
                 const float goal3[3] = {ctx[0], ctx[1], ctx[2]};
                 const float vel3[3] = {ctx[4] * 4.0f, ctx[5] * 4.0f, ctx[6] * 4.0f};
@@ -605,9 +618,14 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             float* cg = a.co + row * COBS;
 #pragma unroll
             for (int j = 0; j < 32; j++) { s_co[grp][j] = cob[j]; cg[j] = cob[j]; }
+        } else if (active && !X) {  // begins at act: this tick's rows as written before
+            for (uint32_t i = lane; i < D; i += G) s_obs[grp][i] = og[i];
+            for (uint32_t i = lane; i < COBS; i += G) s_co[grp][i] = a.co[row * COBS + i];
+        } else if (live && observe && a.mem_head && lane == 0) {
+            a.mem_head[size_t(nn) * MEM_HEAD_WORDS + MEM_HEAD_OBSERVED] = 0u;
         }
         group_sync();
-        if (X && t + 1 == a.count && (a.split & SPLIT_END_AFTER_OBSERVE)) break;
+        if (t + 1 == a.count && (a.split & SPLIT_END_AFTER_OBSERVE)) break;
 
         // ---- actor and critic hidden layers (ppo.hpp:65-72, 82-89)
         if constexpr (X) {

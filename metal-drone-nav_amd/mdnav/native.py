@@ -29,7 +29,7 @@ EXPORTS = [
 P = ctypes.c_void_p
 U32, U64, F32, I32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_int
 KERNELS = {"rollout": 0, "gae": 1, "normalize": 2, "rows": 3, "grads": 4, "adam": 5, "lp_forward": 6,
-           "lp_backward": 7, "lp_adam": 8}
+           "lp_backward": 7, "lp_adam": 8, "memory": 9}
 
 _lib = None
 

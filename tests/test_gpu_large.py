@@ -82,7 +82,7 @@ def test_wide_policy_against_oracle(hidden, actor_obs):
     assert np.abs(m_gpu - m_ora).max() <= 1e-2 + 1e-2 * np.abs(m_ora).max()
 
 
-@pytest.mark.parametrize("variant", ["static", "threat_mix_delays", "sensor_period2", "guided"])
+@pytest.mark.parametrize("variant", ["static", "threat_mix_delays", "sensor_period2", "guided", "guided_memory"])
 def test_wide_policy_closed_loop(variant):
     """Sim::collect with the wide actor choosing every action (split ticks:
     env kernel up to the observation, wide forward, env kernel from act).
@@ -94,7 +94,8 @@ def test_wide_policy_closed_loop(variant):
     Two collects in a row cover the hand-over at a collect boundary; resets
     happen inside the split launches (max_steps below the ticks run).
     "guided": the 184-input actor, hint computed in the env step and added to
-    the wide means."""
+    the wide means; "guided_memory": the history-aware hint from the memory
+    kernel between the env launches."""
     from gpu_compare import ENV_BUFFERS, compare
     from oracle_lib import oracle, ptr
 
@@ -104,7 +105,9 @@ def test_wide_policy_closed_loop(variant):
         kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=2, max_steps=30)
     elif variant == "sensor_period2":   # a frame every other tick, one frame of delay
         kw.update(sensor_period=2, sensor_delay=1, command_delay=1)
-    D = 184 if variant == "guided" else 181
+    if variant == "guided_memory":
+        kw.update(geometry_memory=1)
+    D = 184 if variant.startswith("guided") else 181
     say("case: wide closed loop %s hidden=%d N=64 T=%d, two collects" % (variant, hidden, T))
     cfg = config(**kw)
     sim, _, ora = make_pair(cfg, T, epochs=1, minibatch=1024, actor_obs=D)

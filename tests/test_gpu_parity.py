@@ -268,3 +268,33 @@ def test_geometry_prior_bit_exact(variant):
     assert not bad, bad
     hint = sim.get("obs").reshape(-1, 184)[:, 181:]
     assert np.count_nonzero(hint) > hint.size // 2, "hint mostly zero"
+
+
+@pytest.mark.parametrize("variant", ["k2_production", "k4_threats_delays", "k8_sensor_delay6", "eval_inactive"])
+def test_geometry_memory_bit_exact(variant):
+    """The history-aware hint (cfg.geometry_memory = 1, guidance.hpp:152-194 as
+    cpu_reference.hpp:364-372 calls it): per tick the env kernel stops after
+    the observation, the memory kernel scores the 85 candidate sweeps against
+    the remembered points of up to 8 frames and writes the hint, and the next
+    launch acts on the row.  Every buffer after a rollout and a PPO update
+    bit-identical to the oracle.  "eval_inactive": evaluation mode, where envs
+    stop after one episode and must be left alone by the memory kernel."""
+    kw = dict(n=128, family=1, speed=1.0, distance=3.0, max_steps=40, geometry_memory=1)
+    if variant == "k4_threats_delays":
+        kw.update(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=1, wind=0.5, sensor_period=2)
+    elif variant == "k8_sensor_delay6":
+        kw.update(family=6, distance=4.0, sensor_delay=6, depth_noise=0.05, dropout=0.1)
+    elif variant == "eval_inactive":
+        kw.update(eval=1, max_steps=14)
+    say("case: geometry memory %s N=128 T=48 epochs=1 minibatch=2048" % variant)
+    cfg = config(**kw)
+    sim, ppo, ora = make_pair(cfg, 48, epochs=1, minibatch=2048, actor_obs=184)
+    sim.collect()
+    ppo.rollout_update(0)
+    sim.sync()
+    ora.iteration(0)
+    bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v",
+                             "metric_rows"] + ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
+    assert not bad, bad
+    hint = sim.get("obs").reshape(-1, 184)[:, 181:]
+    assert np.count_nonzero(hint) > hint.size // 4, "hint mostly zero"
