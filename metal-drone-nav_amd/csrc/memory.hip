@@ -6,11 +6,16 @@
 // One 256-thread workgroup per env, run between the env kernel's observation
 // of a tick and the launch that acts on it:
 //   1. the env's up to 8 x 80 remembered range hits become body-frame points
-//      (position, |p|^2, 3 + radius, radius^2) in LDS, built once instead of
-//      once per candidate direction;
-//   2. 255 threads = 85 candidate sweeps x 3 thirds of the points scan them
-//      (every lane reads the same point: LDS broadcast); the thirds' nearest
-//      contacts are combined with a min, which is exact in any order;
+//      (position, |p|^2, 3 + radius, radius^2), built once instead of once
+//      per candidate direction.  Only points that some sweep could touch are
+//      kept (compacted into LDS): a contact needs along <= 3 + radius and
+//      |p|^2 - along^2 < radius^2, so a point with |p|^2 above
+//      (3 + radius)^2 + radius^2 (with a 0.1 % margin for rounding) is never
+//      one, whatever the sweep;
+//   2. 255 threads = 85 candidate sweeps x 3 thirds of the kept points scan
+//      them (every lane reads the same point: LDS broadcast); the nearest
+//      contacts are combined with a min, which is exact in any order, so the
+//      order of the compacted points does not matter;
 //   3. the 85 candidates are scored and reduced with the sequential scan's
 //      rule (maximum score, first candidate on ties), and one lane writes the
 //      hint to the row's last three inputs.
@@ -26,7 +31,7 @@ namespace mem {
 using namespace mdn;
 
 constexpr uint32_t OBS = MDN_ACTOR_OBS_PRIOR;
-constexpr uint32_t POINTS = 640, CANDIDATES = 85, PARTS = 3, PART = (POINTS + PARTS - 1) / PARTS;
+constexpr uint32_t POINTS = 640, CANDIDATES = 85, PARTS = 3;
 constexpr uint32_t THREADS = 256;
 
 __device__ __forceinline__ float fbits(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -34,7 +39,7 @@ __device__ __forceinline__ float div_r(float x, double r) { return float(double(
 
 struct Point {
     float4 xyz2;  // body-frame x, y, z and x^2 + y^2 + z^2
-    float2 lim;   // 3 + radius (-1: no point), radius^2
+    float4 lim;   // 3 + radius, radius^2, an upper bound of sqrt(radius^2), unused
 };
 
 // guidance.hpp:27-34 over the LDS copy of the current ranges (already x 12)
@@ -74,7 +79,8 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
     __shared__ float cand_score[2], cand_free[CANDIDATES];
     __shared__ uint32_t cand_idx[2], goal_cell_s[2];
     __shared__ float goal_al_s[2];
-    const uint32_t n = blockIdx.x, t = threadIdx.x, wv = t / 64;
+    __shared__ uint32_t kept;
+    const uint32_t n = blockIdx.x, t = threadIdx.x, wv = t / 64, lane = t % 64;
     const uint32_t* hd = a.head + size_t(n) * nav::MEM_HEAD_WORDS;
     if (hd[nav::MEM_HEAD_OBSERVED] == 0u) return;  // uniform over the workgroup
     float* og = a.obs + size_t(n) * OBS;
@@ -96,13 +102,15 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
 #pragma unroll
     for (int j = 0; j < 12; j++) pose[j] = fbits(hd[nav::MEM_HEAD_POSE + j]);
 
+    if (t == 0) kept = 0;
+    __syncthreads();
     // 1. remembered points (guidance.hpp:113-139 up to the sweep test)
-    for (uint32_t j = t; j < POINTS; j += THREADS) {
+    for (uint32_t j0 = 0; j0 < POINTS; j0 += THREADS) {  // uniform trip count: whole waves ballot
+        const uint32_t j = j0 + t;
         const uint32_t back = j / 80, cell = j % 80, row = cell / 10, col = cell % 10;
         Point p;
-        p.xyz2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        p.lim = make_float2(-1.0f, 0.0f);
-        if (back < valid) {
+        bool keep = false;
+        if (j < POINTS && back < valid) {
             const uint32_t frame = (latest + 8u - back) % 8u;
             const float* old_pose = a.poses + (size_t(n) * 8 + frame) * 12;
             const float* ranges = a.sensors + (size_t(n) * 8 + frame) * 320;
@@ -128,10 +136,15 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
                 const float age = fmax_f(float(back) * fmax_f(sensor_dt, 0.0f), 0.0f) + 0.0f;
                 const float radius = 0.20f + 0.015f * range + 0.15f * age;
                 p.xyz2 = make_float4(x, y, z, x * x + y * y + z * z);
-                p.lim = make_float2(3.0f + radius, radius * radius);
+                p.lim = make_float4(3.0f + radius, radius * radius, radius * 1.0001f + 1e-6f, 0.0f);
+                keep = p.xyz2.w <= 1.001f * (p.lim.x * p.lim.x + p.lim.y);
             }
         }
-        pts[j] = p;
+        const uint64_t m = __ballot(keep);
+        uint32_t base = 0;
+        if (lane == 0 && m) base = atomicAdd(&kept, uint32_t(__popcll(m)));
+        base = __shfl(base, 0, 64);
+        if (keep) pts[base + uint32_t(__popcll(m & ((uint64_t(1) << lane) - 1)))] = p;
     }
     // per-cell current range x 12 and closing-speed risk contribution
     if (t < 80) {
@@ -178,6 +191,7 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
 
     // 2. swept-sphere clearance of every candidate over a third of the points
     // (guidance.hpp:134-139)
+    const uint32_t npts = kept;
     if (t < PARTS * CANDIDATES) {
         const uint32_t c = t % CANDIDATES, part = t / CANDIDATES;
         float d[3];
@@ -186,15 +200,22 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
         const float sn = sqrt_f(sw[0] * sw[0] + sw[1] * sw[1] + sw[2] * sw[2]);
 #pragma unroll
         for (int j = 0; j < 3; j++) sw[j] /= fmax_f(sn, 1e-6f);
+        // A contact is along - sqrt(radius^2 - lateral^2) >= along - radius
+        // (rounded values included: sqrt of at most radius^2 rounds to at most
+        // radius (1 + 2^-23)), so a point with along - 1.0001 radius >= nearest
+        // cannot lower nearest and its square root is skipped.  The state is
+        // finite at an observation (the advance resets non-finite states), so
+        // `along` is never NaN.
         float nearest = 3.0f;
-        const uint32_t j0 = part * PART, j1 = min(POINTS, j0 + PART);
+        const uint32_t j0 = part * npts / PARTS, j1 = (part + 1) * npts / PARTS;
+#pragma unroll 2
         for (uint32_t j = j0; j < j1; j++) {
             const float4 q = pts[j].xyz2;
-            const float2 l = pts[j].lim;
+            const float4 l = pts[j].lim;
             const float along = q.x * sw[0] + q.y * sw[1] + q.z * sw[2];
-            if (along <= 0.0f || along > l.x) continue;
             const float lateral2 = fmax_f(q.w - along * along, 0.0f);
-            if (lateral2 < l.y) nearest = fmin_f(nearest, fmax_f(along - sqrt_f(l.y - lateral2), 0.0f));
+            const bool contact = (along > 0.0f) & (along <= l.x) & (lateral2 < l.y) & (along - l.z < nearest);
+            if (contact) nearest = fmin_f(nearest, fmax_f(along - sqrt_f(l.y - lateral2), 0.0f));
         }
         part_near[part][c] = nearest;
     }
