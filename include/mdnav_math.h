@@ -198,6 +198,29 @@ MDN_HD float tanh_f(float x) {
 
 MDN_HD float sigmoid_f(float x) { return 1.0f / (1.0f + exp_f(-x)); }
 
+// atan: Cephes atanf (S. L. Moshier, Cephes Math Library): reduction at
+// tan(3 pi/8) and tan(pi/8), then a degree-4 polynomial in x^2; selects
+// instead of branches.
+MDN_HD float atan_f(float x) {
+    const float ax = fabs_f(x);
+    const bool big = ax > 2.414213562373095f, mid = ax > 0.4142135623730950f;
+    const float xr = big ? -1.0f / ax : (mid ? (ax - 1.0f) / (ax + 1.0f) : ax);
+    const float y0 = big ? 1.5707963267948966f : (mid ? 0.7853981633974483f : 0.0f);
+    const float z = xr * xr;
+    const float p = (((8.05374449538e-2f * z - 1.38776856032e-1f) * z + 1.99777106478e-1f) * z - 3.33329491539e-1f) *
+                    z * xr + xr;
+    const float r = y0 + p;
+    return x < 0.0f ? -r : r;
+}
+// atan2 by quadrant from atan_f(y / x); (0, 0) -> 0.
+MDN_HD float atan2_f(float y, float x) {
+    const float pi = 3.14159265358979f, half_pi = 1.5707963267948966f;
+    const float t = atan_f(y / x);
+    const float r = x > 0.0f ? t : (x < 0.0f ? (y < 0.0f ? t - pi : t + pi)
+                                             : (y > 0.0f ? half_pi : (y < 0.0f ? -half_pi : 0.0f)));
+    return (x == x && y == y) ? r : x + y;
+}
+
 MDN_HD float min_f(float a, float b) { return b < a ? b : a; }
 MDN_HD float max_f(float a, float b) { return a < b ? b : a; }
 MDN_HD float clamp_f(float x, float lo, float hi) { return max_f(lo, min_f(hi, x)); }

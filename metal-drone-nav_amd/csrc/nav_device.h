@@ -392,6 +392,36 @@ __device__ __forceinline__ void guidance_group(const float* orow, const float* _
 }
 
 
+// Pooled cells of the top two grid rows farther than 2.5 m (sim.metal:233, 236).
+__device__ __forceinline__ float overhead_cells(const float* o) {
+    float overhead = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 20; k++) overhead += o[k] * 12.0f > 2.5f ? 1.0f : 0.0f;
+    return overhead;
+}
+// sim.metal:233: evaluation modes 9-21 of the 184-input actor pull the means
+// toward the hint (inputs 181-183) by a mode-dependent scale.
+__device__ __forceinline__ void guided_mode_means(uint32_t mode, const float* o, float (&mean)[4]) {
+    float scale = (mode == 9 || mode == 13) ? 0.0f
+                  : ((mode == 10 || mode == 14 || mode == 16) ? 0.25f : (mode == 15 ? 1.0f : 0.5f));
+    if (mode >= 17) scale = 0.25f + 0.75f * (overhead_cells(o) / 20.0f);
+    if (mode == 12) {
+        float near = 12.0f;
+        for (int k = 0; k < 80; k++) near = fmin_f(near, o[k] * 12.0f);
+        scale = clamp_f((near - .3f) / 2, 0.2f, 1.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const float prior = o[MDN_ACTOR_OBS_PRIOR - 3 + j];
+        mean[j] = prior + scale * (mean[j] - prior);
+    }
+    mean[3] *= scale;
+    if (mode == 16) {
+        const float yaw = atan2_f(o[161], o[160]);
+        mean[3] += guid_atanh(clamp_f(yaw * 1.5f, -.85f, .85f));
+    }
+}
+
 // fp64 reciprocals of the plant's constant divisors
 struct PhysRecip {
     double mass, rise[4], fall[4];

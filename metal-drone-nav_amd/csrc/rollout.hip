@@ -389,6 +389,9 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     const uint32_t nn = live ? n : 0;
 
     constexpr uint32_t OS = D % 2 ? D + 4 : D + 3;  // odd stride of the observation rows
+    // split ticks: the wide actor's loop and the 184-input actor's geometry
+    // memory; the fused 181-input kernels keep the plain tick loop
+    constexpr bool SPLIT = X || D == MDN_ACTOR_OBS_PRIOR;
     constexpr uint32_t WSTR = WORLD_WORDS;  // odd: env rows start in distinct banks
     __shared__ WeightLds<W, D> s_wt;
     const float* AW1;   // actor W1 transposed [input][hidden]
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     {   // pooled ring cache: LDS slot f%K holds frame f for the last K frames
         // (a launch that begins at act already holds the frame cast for the
         // current step, if one was due)
-        const int last = (a.split & SPLIT_BEGIN_AT_ACT) ? int(r.steps / C.sensor_period)
+        const int last = (SPLIT && (a.split & SPLIT_BEGIN_AT_ACT)) ? int(r.steps / C.sensor_period)
                          : r.steps == 0                         ? -1
                                                                 : int((r.steps - 1) / C.sensor_period);
         for (uint32_t e = lane; e < uint32_t(K) * POOL; e += G) {
@@ -464,11 +467,11 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     group_sync();
 
     for (uint32_t t = 0; t < a.count; t++) {
-        const uint32_t tick = (a.tick0 + t) % a.horizon;
+        const uint32_t tick = SPLIT ? (a.tick0 + t) % a.horizon : t % a.horizon;
         const size_t row = size_t(tick) * N + nn;
         const bool active = live && !(C.eval && r.episodes);
         // depth and observation of this tick still to do
-        const bool observe = t != 0 || !(a.split & SPLIT_BEGIN_AT_ACT);
+        const bool observe = !SPLIT || t != 0 || !(a.split & SPLIT_BEGIN_AT_ACT);
         const uint32_t count = min(float_bits(world[160]), 16u);  // slots of WWorld
 
         // ---- obstacle centres at the current time (world.hpp:32-41)
@@ -540,7 +543,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         if (active && observe) {
             for (uint32_t b = lane; b < POOL; b += G) {
                 const float cur = have ? div_r(s_ring[grp][(frame % K) * POOL + b], 1.0 / 12.0) : 1.0f;
-                const float pre = have ? div_r(s_ring[grp][(prev % K) * POOL + b], 1.0 / 12.0) : 1.0f;
+                // mode 18 (sim.metal:211-213): evaluation without the previous frame
+                const float pre = C.mode == 18 ? cur : have ? div_r(s_ring[grp][(prev % K) * POOL + b], 1.0 / 12.0) : 1.0f;
                 s_obs[grp][b] = cur;
                 s_obs[grp][POOL + b] = pre;
                 og[b] = cur;
@@ -570,7 +574,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             for (int j = 0; j < 21; j++) { s_obs[grp][2 * POOL + j] = ctx[j]; og[2 * POOL + j] = ctx[j]; }
             if (D == MDN_ACTOR_OBS_PRIOR && a.mem_head) {  // geometry-memory hint: computed outside
                 uint32_t* hd = a.mem_head + size_t(nn) * MEM_HEAD_WORDS;
-                const uint32_t valid = have ? min(frame + 1, 8u - sdelay) : 0u;
+                uint32_t valid = have ? min(frame + 1, 8u - sdelay) : 0u;
+                if (C.mode == 18) valid = min(valid, 1u);  // memory.metal:34: newest frame only
                 if (lane == 0) {
                     hd[MEM_HEAD_OBSERVED] = 1u;
                     hd[MEM_HEAD_FRAME] = frame;
@@ -618,14 +623,14 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             float* cg = a.co + row * COBS;
 #pragma unroll
             for (int j = 0; j < 32; j++) { s_co[grp][j] = cob[j]; cg[j] = cob[j]; }
-        } else if (active && !X) {  // begins at act: this tick's rows as written before
+        } else if (SPLIT && active) {  // begins at act: this tick's rows as written before
             for (uint32_t i = lane; i < D; i += G) s_obs[grp][i] = og[i];
             for (uint32_t i = lane; i < COBS; i += G) s_co[grp][i] = a.co[row * COBS + i];
-        } else if (live && observe && a.mem_head && lane == 0) {
+        } else if (D == MDN_ACTOR_OBS_PRIOR && live && observe && a.mem_head && lane == 0) {
             a.mem_head[size_t(nn) * MEM_HEAD_WORDS + MEM_HEAD_OBSERVED] = 0u;
         }
         group_sync();
-        if (t + 1 == a.count && (a.split & SPLIT_END_AFTER_OBSERVE)) break;
+        if (SPLIT && t + 1 == a.count && (a.split & SPLIT_END_AFTER_OBSERVE)) break;
 
         // ---- actor and critic hidden layers (ppo.hpp:65-72, 82-89)
         if constexpr (X) {
@@ -694,6 +699,13 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll 8
                 for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
             }
+            float deployed = 1.0f;
+            if constexpr (D == MDN_ACTOR_OBS_PRIOR) {
+                if (C.mode >= 9 && C.mode <= 21) guided_mode_means(C.mode, s_obs[grp], mean);
+                // sim.metal:234-238, 246-252: mode 22 trains through the
+                // deployed mode-17 map of the sample (log-probability of the raw one)
+                if (C.mode == 22) deployed = 0.25f + 0.75f * (overhead_cells(s_obs[grp]) / 20.0f);
+            }
             uint32_t rng = r.rng;
             float lp = 0, act[4];
 #pragma unroll
@@ -703,7 +715,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 if (C.mode == 1) act[j] = normal_draw(rng);
                 const float diff = (act[j] - mean[j]) * exp_f(-ls);
                 lp += -0.5f * (diff * diff + 2 * ls + LOG_TWO_PI);
-                a_cmd[j] = tanh_f(act[j]);
+                float executed = act[j];
+                if (D == MDN_ACTOR_OBS_PRIOR && C.mode == 22) {
+                    const float prior = s_obs[grp][D - 3 + (j < 3 ? j : 0)];
+                    executed = j < 3 ? prior + deployed * (act[j] - prior) : deployed * act[j];
+                }
+                a_cmd[j] = tanh_f(executed);
             }
             r.rng = rng;
             if (C.mode == 2 || C.mode == 3 || C.mode == 20) {  // sim.metal:257-262

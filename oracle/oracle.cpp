@@ -391,6 +391,8 @@ struct Trainer {
             o[k] = available >= delay ? current / 12.0f : 1.0f;
             o[80 + k] = available >= delay ? previous / 12.0f : 1.0f;
         }
+        if (cfg.mode == 18)  // sim.metal:211-213: evaluation ablation without the previous frame
+            for (uint32_t k = 0; k < MDN_POOLED_FEATURES; k++) o[80 + k] = o[k];
         const V3 delta = v3(world.goal[0] - s.position[0], world.goal[1] - s.position[1], world.goal[2] - s.position[2]);
         const float distance = max_f(vlen(delta), 1.0e-6f);
         float* c = o + 160;
@@ -415,7 +417,8 @@ struct Trainer {
                 float pose[12];
                 for (int j = 0; j < 3; j++) pose[j] = s.position[j];
                 for (int j = 0; j < 9; j++) pose[3 + j] = r[j];
-                const uint32_t valid = available >= delay ? std::min(frame + 1, 8u - delay) : 0u;
+                uint32_t valid = available >= delay ? std::min(frame + 1, 8u - delay) : 0u;
+                if (cfg.mode == 18) valid = std::min(valid, 1u);  // memory.metal:34: newest frame only
                 nav_guidance_memory(cur, prv, goal, distance, vel, sensor_dt, MDN_SENSOR_TAN_V,
                                     &sensors[size_t(n) * 8 * 320], &poses[size_t(n) * 8 * 12], pose, frame, valid, hint);
             } else {
@@ -424,6 +427,36 @@ struct Trainer {
             for (int j = 0; j < 3; j++) o[shape.obs - 3 + j] = hint[j];
         }
         critic_observation(s, world, run, &co[(size_t(tick) * cfg.n + n) * shape.critic_obs]);
+    }
+
+    // Pooled cells of the top two grid rows farther than 2.5 m (sim.metal:233, 236).
+    static float overhead_cells(const float* o) {
+        float overhead = 0.0f;
+        for (int k = 0; k < 20; k++) overhead += o[k] * 12.0f > 2.5f ? 1.0f : 0.0f;
+        return overhead;
+    }
+    // sim.metal:233: evaluation modes 9-21 of the 184-input actor pull the
+    // means toward the hint (inputs 181-183) by a mode-dependent scale.
+    // Only the reference's GPU path has them (cpu_reference.hpp samples in
+    // mode 0 only); restated from the Metal source.
+    static void guided_mode_means(uint32_t mode, const float* o, float* mean) {
+        float scale = (mode == 9 || mode == 13) ? 0.0f
+                      : ((mode == 10 || mode == 14 || mode == 16) ? 0.25f : (mode == 15 ? 1.0f : 0.5f));
+        if (mode >= 17) scale = 0.25f + 0.75f * (overhead_cells(o) / 20.0f);
+        if (mode == 12) {
+            float near = 12.0f;
+            for (int k = 0; k < 80; k++) near = fmin_f(near, o[k] * 12.0f);
+            scale = clamp_f((near - .3f) / 2, 0.2f, 1.0f);
+        }
+        for (int j = 0; j < 3; j++) {
+            const float prior = o[MDN_ACTOR_OBS_PRIOR - 3 + j];
+            mean[j] = prior + scale * (mean[j] - prior);
+        }
+        mean[3] *= scale;
+        if (mode == 16) {
+            const float yaw = atan2_f(o[161], o[160]);
+            mean[3] += nav_atanh(clamp_f(yaw * 1.5f, -.85f, .85f));
+        }
     }
 
     // sim.metal:229-271 == cpu_reference.hpp:404-429
@@ -437,6 +470,13 @@ struct Trainer {
         else
             actor_forward(shape, actor.data(), &obs[row * shape.obs], hidden, mean);
         values[row] = critic_forward(shape, critic.data(), &co[row * shape.critic_obs], hidden);
+        const float* o = &obs[row * shape.obs];
+        const bool guided = shape.obs == MDN_ACTOR_OBS_PRIOR;
+        if (guided && cfg.mode >= 9 && cfg.mode <= 21) guided_mode_means(cfg.mode, o, mean);
+        // sim.metal:234-238, 246-252: mode 22 trains through the deployed
+        // mode-17 map of the sampled action (the log-probability stays on the
+        // raw sample)
+        const float deployed = guided && cfg.mode == 22 ? 0.25f + 0.75f * (overhead_cells(o) / 20.0f) : 1.0f;
         const float* log_std = &actor[shape.actor_log_std()];
         uint32_t rng = run.rng;
         float lp = 0, a[4];
@@ -446,7 +486,11 @@ struct Trainer {
             const float diff = (a[j] - mean[j]) * exp_f(-log_std[j]);
             lp += -0.5f * (diff * diff + 2 * log_std[j] + kLogTwoPi);
             actions[row * 4 + j] = a[j];
-            commands[(size_t(n) * 8 + run.steps % 8) * 4 + j] = tanh_f(a[j]);
+            float executed = a[j];
+            if (guided && cfg.mode == 22)
+                executed = j < 3 ? o[MDN_ACTOR_OBS_PRIOR - 3 + j] + deployed * (a[j] - o[MDN_ACTOR_OBS_PRIOR - 3 + j])
+                                 : deployed * a[j];
+            commands[(size_t(n) * 8 + run.steps % 8) * 4 + j] = tanh_f(executed);
         }
         logp[row] = lp;
         run.rng = rng;

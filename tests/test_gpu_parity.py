@@ -298,3 +298,33 @@ def test_geometry_memory_bit_exact(variant):
     assert not bad, bad
     hint = sim.get("obs").reshape(-1, 184)[:, 181:]
     assert np.count_nonzero(hint) > hint.size // 4, "hint mostly zero"
+
+
+@pytest.mark.parametrize("mode", [12, 13, 16, 17, 18, 19, 22])
+def test_guided_modes_bit_exact(mode):
+    """Guided evaluation modes of the 184-input actor (sim.metal:211-213,
+    233-269; memory.metal:34): means pulled toward the hint by a fixed or
+    overhead-dependent scale (12, 13, 16, 17, 19), the previous frame dropped
+    (18), fixed-speed commands (19), and mode 22's training through the
+    deployed map.  Evaluation settings as main.mm:605-610 uses them (family 8,
+    1.5 m/s, 4 m goals, geometry memory from mode 13 on); mode 22 trains
+    (sampling on, one PPO update).  Every buffer bit-identical to the oracle."""
+    train = mode == 22
+    kw = dict(n=128, family=8, speed=1.5, distance=4.0, max_steps=40, mode=mode, eval=0 if train else 1,
+              seed=800001, geometry_memory=1 if mode >= 13 else 0)
+    say("case: guided mode %d N=128 T=48 (%s)" % (mode, "train + update" if train else "eval"))
+    cfg = config(**kw)
+    sim, ppo, ora = make_pair(cfg, 48, epochs=1, minibatch=2048, actor_obs=184)
+    names = ENV_BUFFERS + ROW_BUFFERS
+    if train:
+        sim.collect()
+        ppo.rollout_update(0)
+        sim.sync()
+        ora.iteration(0)
+        names = names + ["advantages", "returns", "actor", "critic", "actor_m", "actor_v", "metric_rows"]
+    else:
+        sim.collect()
+        sim.sync()
+        ora.collect()
+    bad = compare(sim, ora, names, tol=0.0)
+    assert not bad, bad
