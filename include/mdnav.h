@@ -140,6 +140,34 @@ int mdn_ppo_metric_mean(MdnPPO* ppo, float out[4]);
 int mdn_ppo_optimizer_step(const MdnPPO* ppo, uint64_t* step);
 int mdn_ppo_updates_per_rollout(const MdnPPO* ppo, uint32_t* updates);
 
+/* On-disk formats.
+ * PPOTrainer::save_checkpoint (main.mm:1285-1317): PPOFIX1 version 6 (this
+ * build has no dynamics, task or shaping blocks and the legacy camera):
+ * header, actor, critic, their Adam moments, then the simulator's states,
+ * runs, worlds, sensor, pose and command rings, in the reference's layouts.
+ * Written to path.tmp and renamed. */
+int mdn_ppo_save_checkpoint(MdnPPO* ppo, const char* path, uint32_t family, uint32_t seed,
+                            uint32_t completed_rollouts);
+/* PPOTrainer::load_checkpoint (main.mm:1218-1284) with read_checkpoint_header
+ * (main.mm:986-994): versions 3-6 (7-10 return MDN_E_ARG).  A missing file
+ * is a fresh start (MDN_OK, *completed_rollouts = 0), as in the reference.
+ * The family, horizon, env count and seed must match the arguments and the
+ * run settings the simulator's; the simulator takes the file's config. */
+int mdn_ppo_load_checkpoint(MdnPPO* ppo, const char* path, uint32_t family, uint32_t horizon, uint32_t n,
+                            uint32_t seed, uint32_t* completed_rollouts);
+/* A checkpoint's header and, if `actor` is given, its actor parameters (the
+ * prefix evaluate_checkpoint reads, main.mm:1864-1866; versions 3-10). */
+int mdn_checkpoint_read(const char* path, MdnCheckpointHeader* header, float* actor, uint64_t actor_count);
+/* nav_deployment::NavigationPolicy::load / write_file (deployment.hpp:142-205):
+ * NAVPOL1 = magic, 56-byte metadata, 12,104 finite actor weights of the
+ * 184-64-4 actor, NAVSRC1 + FNV-1a 64 hash of the source checkpoint, no
+ * trailing bytes. */
+int mdn_navpol_read(const char* path, MdnNavPolicyMeta* meta, float* weights, uint64_t count, uint64_t* source_hash);
+int mdn_navpol_write(const char* path, const MdnNavPolicyMeta* meta, const float* weights, uint64_t count,
+                     uint64_t source_hash);
+/* fnv1a64_file (deployment.hpp:122-136). */
+int mdn_fnv1a64_file(const char* path, uint64_t* hash);
+
 /* PPOTrainer with the reference's FIXED_PPO_HIDDEN_DIM raised to `hidden`
  * (ppo.hpp:17-45; the capacity actors of ACTOR_CAPACITY_RESULTS, width 5120
  * for the 967,688-parameter actor at 184 inputs): actor 181 -> hidden -> 4,

@@ -106,6 +106,26 @@ typedef struct MdnSimConfig {
     uint32_t velocity_contract, geometry_memory;
 } MdnSimConfig;
 
+/* PPOFIX1 checkpoint header (PpoCheckpointHeader, main.mm:978-984), 136
+ * bytes: magic "PPOFIX1\0", then the trainer's counters and the SimConfig. */
+typedef struct MdnCheckpointHeader {
+    char magic[8];
+    uint32_t version, actor_count, critic_count, horizon, n, family;
+    uint32_t base_seed, completed_rollouts;
+    uint64_t optimizer_step;
+    MdnSimConfig config;
+} MdnCheckpointHeader;
+
+/* NAVPOL1 deployed-policy metadata (nav_deployment::Metadata,
+ * deployment.hpp:72-88), 56 bytes in file order. */
+typedef struct MdnNavPolicyMeta {
+    uint32_t version, observation_count, hidden_count, action_count, policy_mode, weight_count;
+    float max_speed_mps;
+    uint32_t sensor_rows, sensor_columns;
+    float range_max_m, navigation_period_s, native_period_s;
+    uint32_t memory_frames, body_frame;
+} MdnNavPolicyMeta;
+
 /* Rollout metrics of cpu_reference.hpp:55-70. */
 typedef struct MdnMetrics {
     double wall_seconds;
@@ -122,6 +142,8 @@ static_assert(sizeof(MdnRaptorWeights) == 2084 * 4, "RaptorWeights layout");
 static_assert(sizeof(MdnWorld) == 676, "WWorld layout");
 static_assert(sizeof(MdnSimRun) == 184, "SimRun layout");
 static_assert(sizeof(MdnSimConfig) == 84, "SimConfig layout");
+static_assert(sizeof(MdnCheckpointHeader) == 136, "PpoCheckpointHeader layout");
+static_assert(sizeof(MdnNavPolicyMeta) == 56, "NAV metadata layout");
 #endif
 
 #endif /* MDNAV_TYPES_H */

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -37,6 +38,7 @@ constexpr uint32_t OBS = MDN_ACTOR_OBS_POOLED;
 constexpr uint32_t COBS = MDN_CRITIC_OBS;
 constexpr uint32_t HID = MDN_HIDDEN;
 constexpr uint32_t STATE_WORDS = 17, RUN_WORDS = 46, WORLD_WORDS = 169;
+constexpr uint64_t kNavPolicyWeights = 184 * 64 + 64 + 4 * 64 + 4 + 4;  // deployment.hpp:26-38
 
 template <class T>
 int dev_alloc(T** p, size_t count) {
@@ -1130,6 +1132,240 @@ int mdn_lppo_metric_mean(MdnLargePPO* p, float out[4]) {
 int mdn_lppo_optimizer_step(const MdnLargePPO* p, uint64_t* step) {
     if (!p || !step) return fail(MDN_E_ARG, "mdn_lppo_optimizer_step: null");
     *step = p->optimizer_step;
+    return MDN_OK;
+}
+
+
+// ---------------------------------------------------------------- files
+}  // extern "C"
+
+namespace {
+
+struct File {
+    std::FILE* f = nullptr;
+    explicit File(const char* path, const char* mode) : f(std::fopen(path, mode)) {}
+    ~File() { if (f) std::fclose(f); }
+    bool read(void* p, size_t n) { return std::fread(p, 1, n, f) == n; }
+    bool write(const void* p, size_t n) { return std::fwrite(p, 1, n, f) == n; }
+    bool at_end() { unsigned char c; return std::fread(&c, 1, 1, f) == 0 && std::feof(f); }
+};
+
+// read_checkpoint_header (main.mm:986-994): the 48-byte prefix, the first 64
+// config bytes, then what each version adds; older versions default the rest.
+int read_checkpoint_header(File& file, MdnCheckpointHeader* h) {
+    std::memset(h, 0, sizeof(*h));
+    unsigned char* b = reinterpret_cast<unsigned char*>(h);
+    if (!file.read(b, 48) || std::memcmp(h->magic, "PPOFIX1", 7) != 0 || h->version < 3 || h->version > 10)
+        return fail(MDN_E_ARG, "checkpoint prefix/version");
+    if (!file.read(&h->config, 64)) return fail(MDN_E_ARG, "checkpoint header truncated");
+    if (h->version >= 4) {
+        if (!file.read(b + 112, 16)) return fail(MDN_E_ARG, "checkpoint header truncated");
+        if (h->version >= 6) {
+            if (!file.read(b + 128, 8)) return fail(MDN_E_ARG, "checkpoint header truncated");
+        } else {
+            h->config.geometry_memory = 0;
+        }
+        if (h->version == 4) h->config.velocity_contract = 0;
+    } else {
+        h->config.risk_coef = 0;
+        h->config.entropy_coef = h->family == 7 ? .002f : .005f;
+        h->config.learning_rate = .0003f;
+        h->config.velocity_contract = 0;
+        h->config.geometry_memory = 0;
+    }
+    return MDN_OK;
+}
+
+// Simulator settings a resume must match (main.mm:1224-1229).
+bool same_run_settings(const MdnSimConfig& a, const MdnSimConfig& b) {
+    return a.family == b.family && a.n == b.n && a.substeps == b.substeps && a.sensor_period == b.sensor_period &&
+           a.sensor_delay == b.sensor_delay && a.command_delay == b.command_delay && a.max_steps == b.max_steps &&
+           a.mode == b.mode && a.speed == b.speed && a.distance == b.distance && a.wind == b.wind &&
+           a.depth_noise == b.depth_noise && a.dropout == b.dropout && a.risk_coef == b.risk_coef &&
+           a.entropy_coef == b.entropy_coef && a.learning_rate == b.learning_rate &&
+           a.velocity_contract == b.velocity_contract && a.geometry_memory == b.geometry_memory;
+}
+
+// Buffers of a checkpoint body after the header, in file order
+// (main.mm:1302-1306): actor, critic, their Adam moments, then the
+// simulator's states, runs, worlds, sensor ring, pose ring, command ring.
+const uint32_t kCheckpointBuffers[] = {MDN_BUF_ACTOR, MDN_BUF_CRITIC, MDN_BUF_ACTOR_M, MDN_BUF_ACTOR_V,
+                                       MDN_BUF_CRITIC_M, MDN_BUF_CRITIC_V, MDN_BUF_STATES, MDN_BUF_RUNS,
+                                       MDN_BUF_WORLDS, MDN_BUF_SENSORS, MDN_BUF_POSES, MDN_BUF_COMMANDS};
+
+bool valid_navpol_meta(const MdnNavPolicyMeta& m) {  // deployment.hpp:260-267
+    return m.version == 1 && m.observation_count == MDN_ACTOR_OBS_PRIOR && m.hidden_count == MDN_HIDDEN &&
+           m.action_count == MDN_ACTIONS && m.policy_mode == 17 && m.weight_count == kNavPolicyWeights &&
+           std::isfinite(m.max_speed_mps) && m.max_speed_mps > 0 && m.sensor_rows == 16 && m.sensor_columns == 20 &&
+           std::fabs(m.range_max_m - 12.0f) < 1.0e-6f && std::fabs(m.navigation_period_s - 0.05f) < 1.0e-6f &&
+           std::fabs(m.native_period_s - 0.01f) < 1.0e-6f && m.memory_frames == 8 && m.body_frame == 0x00554c46u;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mdn_checkpoint_read(const char* path, MdnCheckpointHeader* header, float* actor, uint64_t actor_count) {
+    if (!path || !header) return fail(MDN_E_ARG, "mdn_checkpoint_read: null argument");
+    File file(path, "rb");
+    if (!file.f) return fail(MDN_E_ARG, std::string("cannot open checkpoint: ") + path);
+    int rc = read_checkpoint_header(file, header);
+    if (rc) return rc;
+    if (actor) {
+        if (actor_count != header->actor_count) return fail(MDN_E_ARG, "actor count differs from the checkpoint's");
+        if (!file.read(actor, size_t(actor_count) * 4)) return fail(MDN_E_ARG, "evaluation policy read");
+    }
+    return MDN_OK;
+}
+
+int mdn_ppo_load_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32_t horizon, uint32_t n, uint32_t seed,
+                            uint32_t* completed_rollouts) {
+    if (!p || !path) return fail(MDN_E_ARG, "mdn_ppo_load_checkpoint: null argument");
+    MdnSim* s = p->sim;
+    if (completed_rollouts) *completed_rollouts = 0;
+    File file(path, "rb");
+    if (!file.f) return MDN_OK;  // no checkpoint: a fresh start (main.mm:1219)
+    MdnCheckpointHeader h;
+    int rc = read_checkpoint_header(file, &h);
+    if (rc) return rc;
+    if (h.version >= 7)
+        return fail(MDN_E_ARG, "checkpoint versions 7-10 carry dynamics, task, shaping and camera blocks this "
+                               "build does not have; warm-start from the parameters instead");
+    if (h.actor_count != s->shape.actor_count() || h.critic_count != s->shape.critic_count())
+        return fail(MDN_E_ARG, "PPO checkpoint dimensions mismatch");
+    if (h.family != family || h.horizon != horizon || h.n != n || h.base_seed != seed)
+        return fail(MDN_E_ARG, "PPO checkpoint config mismatch");
+    if (h.horizon != s->horizon || !same_run_settings(h.config, s->cfg))
+        return fail(MDN_E_ARG, "PPO checkpoint simulator settings mismatch");
+    if (h.optimizer_step > uint64_t(UINT32_MAX)) return fail(MDN_E_ARG, "PPO checkpoint Adam step is too large");
+    std::vector<std::vector<unsigned char>> body;
+    for (uint32_t id : kCheckpointBuffers) {
+        uint64_t bytes = 0;
+        rc = mdn_sim_buffer_bytes(s, id, &bytes);
+        if (rc) return rc;
+        body.emplace_back(bytes, 0);
+        if (id == MDN_BUF_POSES && h.version < 6) continue;  // older files have no pose ring
+        if (!file.read(body.back().data(), bytes)) return fail(MDN_E_ARG, "truncated PPO checkpoint");
+    }
+    if (!file.at_end()) return fail(MDN_E_ARG, "PPO checkpoint has trailing data");
+    for (size_t i = 0; i < body.size(); i++) {
+        rc = mdn_sim_upload(s, kCheckpointBuffers[i], body[i].data(), body[i].size());
+        if (rc) return rc;
+    }
+    rc = mdn_sim_set_config(s, &h.config);
+    if (rc) return rc;
+    p->optimizer_step = h.optimizer_step;
+    if (completed_rollouts) *completed_rollouts = h.completed_rollouts;
+    return MDN_OK;
+}
+
+int mdn_ppo_save_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32_t seed, uint32_t completed_rollouts) {
+    if (!p || !path) return fail(MDN_E_ARG, "mdn_ppo_save_checkpoint: null argument");
+    MdnSim* s = p->sim;
+    MdnCheckpointHeader h;
+    std::memset(&h, 0, sizeof(h));  // padding bytes too, so equal states give equal files
+    std::memcpy(h.magic, "PPOFIX1", 7);
+    h.version = 6;  // no dynamics, task or shaping blocks; the legacy camera
+    h.actor_count = s->shape.actor_count();
+    h.critic_count = s->shape.critic_count();
+    h.horizon = s->horizon;
+    h.n = s->cfg.n;
+    h.family = family;
+    h.base_seed = seed;
+    h.completed_rollouts = completed_rollouts;
+    h.optimizer_step = p->optimizer_step;
+    h.config = s->cfg;
+    h.config.tick = 0;
+    const std::string temp = std::string(path) + ".tmp";
+    {
+        File file(temp.c_str(), "wb");
+        if (!file.f) return fail(MDN_E_ARG, "cannot write PPO checkpoint: " + temp);
+        bool ok = file.write(&h, sizeof(h));
+        for (uint32_t id : kCheckpointBuffers) {
+            uint64_t bytes = 0;
+            int rc = mdn_sim_buffer_bytes(s, id, &bytes);
+            if (rc) return rc;
+            std::vector<unsigned char> buf(bytes);
+            rc = mdn_sim_download(s, id, buf.data(), bytes);
+            if (rc) return rc;
+            ok = ok && file.write(buf.data(), bytes);
+        }
+        ok = ok && std::fflush(file.f) == 0;
+        if (!ok) {
+            std::remove(temp.c_str());
+            return fail(MDN_E_ARG, "PPO checkpoint write failed: " + temp);
+        }
+    }
+    if (std::rename(temp.c_str(), path) != 0) {
+        std::remove(temp.c_str());
+        return fail(MDN_E_ARG, std::string("cannot replace PPO checkpoint: ") + path);
+    }
+    return MDN_OK;
+}
+
+int mdn_fnv1a64_file(const char* path, uint64_t* hash) {
+    if (!path || !hash) return fail(MDN_E_ARG, "mdn_fnv1a64_file: null argument");
+    File file(path, "rb");
+    if (!file.f) return fail(MDN_E_ARG, std::string("cannot hash: ") + path);
+    uint64_t h = 14695981039346656037ull;  // FNV-1a 64 (deployment.hpp:122-136)
+    unsigned char buf[16384];
+    size_t got;
+    while ((got = std::fread(buf, 1, sizeof(buf), file.f)) > 0)
+        for (size_t i = 0; i < got; i++) { h ^= buf[i]; h *= 1099511628211ull; }
+    if (std::ferror(file.f)) return fail(MDN_E_ARG, std::string("read error while hashing: ") + path);
+    *hash = h;
+    return MDN_OK;
+}
+
+int mdn_navpol_read(const char* path, MdnNavPolicyMeta* meta, float* weights, uint64_t count, uint64_t* source_hash) {
+    if (!path || !meta || !weights) return fail(MDN_E_ARG, "mdn_navpol_read: null argument");
+    if (count != kNavPolicyWeights) return fail(MDN_E_ARG, "navigation policy holds 12,104 actor weights");
+    File file(path, "rb");
+    if (!file.f) return fail(MDN_E_ARG, std::string("cannot open navigation policy: ") + path);
+    char magic[8];
+    if (!file.read(magic, 8) || std::memcmp(magic, "NAVPOL1\0", 8) != 0)
+        return fail(MDN_E_ARG, "navigation policy magic mismatch");
+    MdnNavPolicyMeta m;
+    if (!file.read(&m, sizeof(m))) return fail(MDN_E_ARG, "truncated navigation policy metadata");
+    if (!valid_navpol_meta(m)) return fail(MDN_E_ARG, "unsupported navigation policy metadata");
+    std::vector<float> w(kNavPolicyWeights);
+    if (!file.read(w.data(), w.size() * 4)) return fail(MDN_E_ARG, "invalid navigation actor weight");
+    for (float v : w)
+        if (!std::isfinite(v)) return fail(MDN_E_ARG, "invalid navigation actor weight");
+    char tag[8];
+    uint64_t hash = 0;
+    if (!file.read(tag, 8) || std::memcmp(tag, "NAVSRC1\0", 8) != 0 || !file.read(&hash, 8))
+        return fail(MDN_E_ARG, "navigation source provenance is missing");
+    if (!file.at_end()) return fail(MDN_E_ARG, "navigation policy has trailing bytes");
+    *meta = m;
+    std::memcpy(weights, w.data(), w.size() * 4);
+    if (source_hash) *source_hash = hash;
+    return MDN_OK;
+}
+
+int mdn_navpol_write(const char* path, const MdnNavPolicyMeta* meta, const float* weights, uint64_t count,
+                     uint64_t source_hash) {
+    if (!path || !meta || !weights) return fail(MDN_E_ARG, "mdn_navpol_write: null argument");
+    if (count != kNavPolicyWeights || !valid_navpol_meta(*meta))
+        return fail(MDN_E_ARG, "invalid NAV actor export dimensions or metadata");
+    for (uint64_t i = 0; i < count; i++)
+        if (!std::isfinite(weights[i])) return fail(MDN_E_ARG, "actor has a non-finite parameter");
+    const std::string temp = std::string(path) + ".tmp";
+    {
+        File file(temp.c_str(), "wb");
+        if (!file.f) return fail(MDN_E_ARG, "cannot create navigation policy: " + temp);
+        const bool ok = file.write("NAVPOL1\0", 8) && file.write(meta, sizeof(*meta)) &&
+                        file.write(weights, size_t(count) * 4) && file.write("NAVSRC1\0", 8) &&
+                        file.write(&source_hash, 8) && std::fflush(file.f) == 0;
+        if (!ok) {
+            std::remove(temp.c_str());
+            return fail(MDN_E_ARG, "navigation policy write failed");
+        }
+    }
+    if (std::rename(temp.c_str(), path) != 0) {
+        std::remove(temp.c_str());
+        return fail(MDN_E_ARG, std::string("cannot replace navigation policy: ") + path);
+    }
     return MDN_OK;
 }
 

@@ -51,6 +51,20 @@ SIM_CONFIG = np.dtype([
     ("risk_coef", f4), ("entropy_coef", f4), ("learning_rate", f4),
     ("velocity_contract", u4), ("geometry_memory", u4)])
 
+# PpoCheckpointHeader (main.mm:978-984)
+CHECKPOINT_HEADER = np.dtype([
+    ("magic", "S8"), ("version", u4), ("actor_count", u4), ("critic_count", u4), ("horizon", u4), ("n", u4),
+    ("family", u4), ("base_seed", u4), ("completed_rollouts", u4), ("optimizer_step", np.uint64),
+    ("config", SIM_CONFIG), ("pad", u4)])
+
+# nav_deployment::Metadata (deployment.hpp:72-88)
+NAV_POLICY_META = np.dtype([
+    ("version", u4), ("observation_count", u4), ("hidden_count", u4), ("action_count", u4),
+    ("policy_mode", u4), ("weight_count", u4), ("max_speed_mps", f4), ("sensor_rows", u4),
+    ("sensor_columns", u4), ("range_max_m", f4), ("navigation_period_s", f4), ("native_period_s", f4),
+    ("memory_frames", u4), ("body_frame", u4)])
+
+assert CHECKPOINT_HEADER.itemsize == 136 and NAV_POLICY_META.itemsize == 56
 assert PHYSICS_STATE.itemsize == 68 and PHYSICS_PARAMS.itemsize == 352
 assert RAPTOR_WEIGHTS.itemsize == 8336 and WORLD.itemsize == 676
 assert SIM_RUN.itemsize == 184 and SIM_CONFIG.itemsize == 84

@@ -23,7 +23,8 @@ EXPORTS = [
     "mdn_op_gae", "mdn_op_normalize", "mdn_lppo_create", "mdn_lppo_destroy", "mdn_lppo_evaluate",
     "mdn_lppo_rollout_update", "mdn_lppo_param_count", "mdn_lppo_get_params", "mdn_lppo_set_params",
     "mdn_lppo_metric_mean", "mdn_lppo_optimizer_step", "mdn_lppo_collect", "mdn_lppo_means",
-    "mdn_op_check_division",
+    "mdn_op_check_division", "mdn_ppo_save_checkpoint", "mdn_ppo_load_checkpoint", "mdn_checkpoint_read",
+    "mdn_navpol_read", "mdn_navpol_write", "mdn_fnv1a64_file",
 ]
 
 P = ctypes.c_void_p
@@ -67,6 +68,12 @@ def lib():
         _sig(L, "mdn_sim_reset_timing", I32, P)
         _sig(L, "mdn_sim_set_lanes", I32, P, U32)
         _sig(L, "mdn_sim_set_actor_obs", I32, P, U32)
+        _sig(L, "mdn_ppo_save_checkpoint", I32, P, ctypes.c_char_p, U32, U32, U32)
+        _sig(L, "mdn_ppo_load_checkpoint", I32, P, ctypes.c_char_p, U32, U32, U32, U32, ctypes.POINTER(U32))
+        _sig(L, "mdn_checkpoint_read", I32, ctypes.c_char_p, P, P, U64)
+        _sig(L, "mdn_navpol_read", I32, ctypes.c_char_p, P, P, U64, ctypes.POINTER(U64))
+        _sig(L, "mdn_navpol_write", I32, ctypes.c_char_p, P, P, U64, U64)
+        _sig(L, "mdn_fnv1a64_file", I32, ctypes.c_char_p, ctypes.POINTER(U64))
         _sig(L, "mdn_sim_get_actor_obs", I32, P, ctypes.POINTER(U32))
         _sig(L, "mdn_ppo_create", I32, P, U32, U32, ctypes.POINTER(P))
         _sig(L, "mdn_ppo_destroy", None, P)

@@ -219,6 +219,17 @@ class PPOTrainer:
         check(lib().mdn_ppo_updates_per_rollout(self.h, ctypes.byref(u)))
         return u.value
 
+    def save_checkpoint(self, path, family, seed, completed_rollouts):
+        """PPOTrainer::save_checkpoint (main.mm:1285-1317): PPOFIX1 version 6."""
+        check(lib().mdn_ppo_save_checkpoint(self.h, str(path).encode(), family, seed, completed_rollouts))
+
+    def load_checkpoint(self, path, family, horizon, n, seed):
+        """PPOTrainer::load_checkpoint (main.mm:1218-1284), versions 3-6.
+        Returns the completed rollouts (0 when the file is absent)."""
+        done = ctypes.c_uint32()
+        check(lib().mdn_ppo_load_checkpoint(self.h, str(path).encode(), family, horizon, n, seed, ctypes.byref(done)))
+        return done.value
+
 
 class LargePPOTrainer:
     """PPO with the hidden width raised to `hidden` (ppo.hpp FIXED_PPO_HIDDEN_DIM;

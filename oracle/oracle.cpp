@@ -872,6 +872,7 @@ void orc_guidance_memory(const float* cur, const float* prev, const float* goal,
 void orc_trainer_evaluate(void* h) { static_cast<Trainer*>(h)->evaluate(); }
 void orc_trainer_set_ext_means(void* h, const float* means) { static_cast<Trainer*>(h)->ext_means = means; }
 uint64_t orc_trainer_optimizer_step(void* h) { return static_cast<Trainer*>(h)->optimizer_step; }
+void orc_trainer_set_optimizer_step(void* h, uint64_t step) { static_cast<Trainer*>(h)->optimizer_step = step; }
 void orc_trainer_metric_mean(void* h, float* out) {
     for (int k = 0; k < 4; k++) out[k] = static_cast<Trainer*>(h)->metric_mean[k];
 }

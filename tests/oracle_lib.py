@@ -59,6 +59,7 @@ def oracle():
         _sig(lib, "orc_memory_clearance", None, P, P, P, P, U32, U32, F32, P)
         _sig(lib, "orc_trainer_minibatch_grads", None, P, U32, U32, P, P, P, P, P, P)
         _sig(lib, "orc_trainer_optimizer_step", U64, P)
+        _sig(lib, "orc_trainer_set_optimizer_step", None, P, U64)
         _sig(lib, "orc_trainer_metric_mean", None, P, P)
         _sig(lib, "orc_trainer_buffer", P, P, U32, ctypes.POINTER(U64))
         _sig(lib, "orc_physics_step_batch", None, P, P, P, P, P, U64)
@@ -250,6 +251,31 @@ class OracleTrainer:
     @property
     def optimizer_step(self):
         return int(self.lib.orc_trainer_optimizer_step(self.h))
+
+    @optimizer_step.setter
+    def optimizer_step(self, step):
+        self.lib.orc_trainer_set_optimizer_step(self.h, step)
+
+    def set_config(self, cfg):
+        self.cfg = np.array(cfg, abi.SIM_CONFIG)
+        self.lib.orc_trainer_set_config(self.h, ptr(self.cfg))
+
+    def load_checkpoint(self, path):
+        """A PPOFIX1 version-6 body (main.mm:1302-1306) into the oracle's
+        buffers: parsed here with numpy, independently of the library's reader."""
+        data = np.fromfile(path, np.uint8)
+        h = data[:136].view(abi.CHECKPOINT_HEADER)[0]
+        assert h["magic"] == b"PPOFIX1" and h["version"] == 6, (h["magic"], h["version"])
+        off = 136
+        for name in ("actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v", "states", "runs", "worlds",
+                     "sensors", "poses", "commands"):
+            buf = self.buffer(name)
+            buf.view(np.uint8)[...] = data[off:off + buf.nbytes]
+            off += buf.nbytes
+        assert off == data.size
+        self.set_config(h["config"])
+        self.optimizer_step = int(h["optimizer_step"])
+        return h
 
 
 def math_batch(fn, x):

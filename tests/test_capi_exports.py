@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared(header="mdnav.h"):
     text = open(os.path.join(ROOT, "include", header)).read()
-    return sorted(set(re.findall(r"\b(mdn_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(mdn_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_every_declared_symbol_is_exported():

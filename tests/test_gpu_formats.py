@@ -1,0 +1,98 @@
+"""The reference's trained assets on the GPU path: resume of the PPOFIX1
+checkpoint guided-table-memory.bin.best (main.mm:1218-1284) and the
+eval-policy run of the policy exported from it, assets/navigation.bin
+(main.mm:1103-1108, 605-614)."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from gpu_compare import ENV_BUFFERS, ROW_BUFFERS, compare
+from mdnav import PPOTrainer, Sim, abi, formats, sim_evaluate
+from oracle_lib import GOLDEN, OracleTrainer, raptor_fixture
+
+pytestmark = pytest.mark.gpu
+
+NAVPOL = os.path.join(GOLDEN, "navigation.bin")
+CKPT = os.path.join(GOLDEN, "guided-table-memory.bin.best")
+PPO_BUFFERS = ["actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v"]
+
+
+def say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+def test_checkpoint_resume_bit_exact(tmp_path):
+    """Load the trained guided-memory checkpoint (128 envs mid-training: trainer
+    state, Adam moments, every env's state, world and sensor/pose/command
+    rings) into the GPU trainer and into the oracle, run the next rollout and
+    update on both, save, reload: every buffer bit-identical throughout."""
+    say("case: resume guided-table-memory.bin.best, one rollout + update, save, reload")
+    hd, _ = formats.read_checkpoint(CKPT)
+    cfg = np.array(hd["config"], abi.SIM_CONFIG)
+    weights = raptor_fixture()[0]
+    sim = Sim(cfg, 32, raptor=weights, actor_obs=184)
+    ppo = PPOTrainer(sim, 2, 256)
+    assert ppo.load_checkpoint(CKPT, 5, 32, 128, 42) == 1090
+    assert ppo.optimizer_step == 34880
+    ora = OracleTrainer(cfg, 32, weights, epochs=2, minibatch=256)
+    ora.set_actor_obs(184)
+    ora.load_checkpoint(CKPT)
+    bad = compare(sim, ora, ENV_BUFFERS + PPO_BUFFERS, tol=0.0)
+    assert not bad, ("loaded", bad)
+    sim.collect()
+    ppo.rollout_update(1090)
+    sim.sync()
+    ora.iteration(1090)
+    bad = compare(sim, ora, ENV_BUFFERS + ROW_BUFFERS + PPO_BUFFERS + ["advantages", "returns", "metric_rows"], tol=0.0)
+    assert not bad, ("resumed", bad)
+    assert ppo.optimizer_step == ora.optimizer_step
+    out = tmp_path / "resumed.bin"
+    ppo.save_checkpoint(out, 5, 42, 1091)
+    h2, a2 = formats.read_checkpoint(out)
+    assert int(h2["version"]) == 6 and int(h2["completed_rollouts"]) == 1091
+    assert int(h2["optimizer_step"]) == ppo.optimizer_step and np.array_equal(a2, sim.get("actor"))
+    assert os.path.getsize(out) == os.path.getsize(CKPT)
+    sim2 = Sim(cfg, 32, raptor=weights, actor_obs=184)
+    ppo2 = PPOTrainer(sim2, 2, 256)
+    assert ppo2.load_checkpoint(out, 5, 32, 128, 42) == 1091
+    for name in ENV_BUFFERS + PPO_BUFFERS:
+        assert sim2.get(name).tobytes() == sim.get(name).tobytes(), name
+
+
+def test_eval_policy_known_answer():
+    """eval-policy assets/navigation.bin 8 800001: 128 one-episode evaluations
+    of the deployed mode-17 policy with the geometry memory, 1.5 m/s, 4 m
+    goals.  The GPU run is bit-identical to the oracle's, and it reproduces
+    the reference's published result of the same command exactly: 114 of 128
+    successes (89.0625 %), 14 collisions (10.9375 %), no timeout, 2.83684 s
+    mean goal time (docs/BENCHMARKS.md:94, printed to 6 digits).  The
+    reference computed it on Metal with its own transcendental functions, so
+    this agreement is not guaranteed by construction; a change that alters a
+    last bit anywhere in the closed loop can move an episode, and this test
+    is the place that shows it."""
+    say("case: eval-policy navigation.bin family 8 seed 800001 (128 envs x 200 ticks, geometry memory)")
+    meta, w, _ = formats.read_navigation_policy(NAVPOL)
+    weights = raptor_fixture()[0]
+    score, report = sim_evaluate(8, int(meta["policy_mode"]), w, speed=float(meta["max_speed_mps"]), distance=4.0,
+                                 seed=800001, memory=1, raptor=weights)
+    say("  GPU:", score, report)
+    cfg = abi.default_config(n=128, family=8, mode=17, eval=1, seed=800001, distance=4.0, speed=1.5,
+                             geometry_memory=1, max_steps=200)
+    ora = OracleTrainer(cfg, 32, weights)
+    ora.set_actor_obs(184)
+    ora.set("actor", w)
+    ora.collect(200)
+    r = ora.get("runs")
+    n = len(r)
+    oscore = dict(success=r["successes"].sum() / n, collision=r["collisions"].sum() / n,
+                  timeout=r["timeouts"].sum() / n,
+                  goal_time=r["success_time"].astype(np.float64).sum() / max(r["successes"].sum(), 1))
+    say("  oracle:", oscore)
+    for k in ("success", "collision", "timeout"):
+        assert score[k] == oscore[k], (k, score[k], oscore[k])
+    assert abs(score["goal_time"] - oscore["goal_time"]) < 1e-9
+    assert (score["success"], score["collision"], score["timeout"]) == (114 / 128, 14 / 128, 0.0), score
+    assert abs(score["goal_time"] - 2.83684) < 5e-6, score
