@@ -96,3 +96,37 @@ def test_eval_policy_known_answer():
     assert abs(score["goal_time"] - oscore["goal_time"]) < 1e-9
     assert (score["success"], score["collision"], score["timeout"]) == (114 / 128, 14 / 128, 0.0), score
     assert abs(score["goal_time"] - 2.83684) < 5e-6, score
+
+
+def published_evaluations():
+    import csv
+    return list(csv.DictReader(open(os.path.join(GOLDEN, "evaluation.csv"))))
+
+
+@pytest.mark.parametrize("row", published_evaluations(), ids=lambda r: r["case_id"][:48])
+def test_published_evaluations(row):
+    """The reference's 28 published evaluations of this policy
+    (assets/evaluation.csv: modes 2/13/17, families 3/5/7/8, two seeds,
+    sensor and command delays, wind, depth noise, pixel dropout, combined),
+    each 128 one-episode runs.  The outcome counts (success, collision,
+    timeout) must be the reference's exactly; the continuous statistics agree
+    to the printed digits in most cases and within an episode tick where a
+    last-bit difference of Metal's transcendentals shifted one arrival."""
+    w = formats.read_navigation_policy(NAVPOL)[1]
+    score, rep = sim_evaluate(int(row["family"]), int(row["mode"]), w, speed=float(row["speed_mps"]),
+                              distance=float(row["distance_m"]), seed=int(row["seed"]),
+                              sensor_delay=int(row["sensor_delay_frames"]), wind=float(row["wind_param"]),
+                              noise=float(row["depth_noise_m"]), dropout=float(row["dropout_probability"]),
+                              command_delay=int(row["command_delay_steps"]), memory=1, raptor=raptor_fixture()[0])
+    want = {k: float(row[k]) for k in ("success", "collision", "timeout", "progress", "mean_goal_time_s",
+                                       "mean_speed_mps", "peak_speed_mps", "min_clearance_m")}
+    say("case %s: success %.6g/%.6g collision %.6g/%.6g goal %.6g/%.6g" % (
+        row["case_id"][:40], rep["success"], want["success"], rep["collision"], want["collision"],
+        rep["mean_goal_time"], want["mean_goal_time_s"]))
+    for k in ("success", "collision", "timeout"):  # 128 episodes: printed to 6 digits
+        assert round(rep[k] * 128) == round(want[k] * 128), (k, rep[k], want[k])
+    assert abs(rep["mean_goal_time"] - want["mean_goal_time_s"]) <= 0.02, rep
+    assert abs(rep["progress"] - want["progress"]) <= 1e-3, rep
+    assert abs(rep["mean_speed"] - want["mean_speed_mps"]) <= 5e-3, rep
+    assert abs(rep["peak_speed"] - want["peak_speed_mps"]) <= 1e-3, rep
+    assert abs(rep["min_clearance"] - want["min_clearance_m"]) <= 1e-5, rep
