@@ -130,3 +130,36 @@ def test_published_evaluations(row):
     assert abs(rep["mean_speed"] - want["mean_speed_mps"]) <= 5e-3, rep
     assert abs(rep["peak_speed"] - want["peak_speed_mps"]) <= 1e-3, rep
     assert abs(rep["min_clearance"] - want["min_clearance_m"]) <= 1e-5, rep
+
+
+def continuation_evaluations():
+    import csv
+    rows = csv.DictReader(open(os.path.join(GOLDEN, "continuation-evaluation.csv")))
+    return [r for r in rows if r["group"] != "controlled_threat"]
+
+
+@pytest.mark.parametrize("row", continuation_evaluations(),
+                         ids=lambda r: (r["candidate"] + ":" + r["case_id"])[:56])
+def test_continuation_evaluations(row):
+    """84 more published evaluations (assets/continuation-evaluation.csv) of
+    three further trained policies (broad stress, door stress, rehearsal
+    curricula; actors taken from the reference's checkpoints, identified by
+    SHA-256, by tests/golden/make_actor_fixtures.py), same bar as above."""
+    z = np.load(os.path.join(GOLDEN, "actors", row["candidate"] + ".npz"))
+    assert bytes(z["sha256"]).hex() == row["checkpoint_sha256"]
+    cfg = z["config"].view(abi.SIM_CONFIG)[0]
+    rep = sim_evaluate(int(row["family"]), int(row["mode"]), z["actor"], speed=float(row["speed_mps"]),
+                       distance=float(row["distance_m"]), seed=int(row["seed"]),
+                       sensor_delay=int(row["sensor_delay_frames"]), wind=float(row["wind_param"]),
+                       noise=float(row["depth_noise_m"]), dropout=float(row["dropout_probability"]),
+                       command_delay=int(row["command_delay_steps"]), velocity_contract=int(cfg["velocity_contract"]),
+                       memory=int(cfg["geometry_memory"]), raptor=raptor_fixture()[0])[1]
+    want = {k: float(row[k]) for k in ("success", "collision", "timeout", "progress", "mean_goal_time_s",
+                                       "mean_speed_mps", "peak_speed_mps", "min_clearance_m")}
+    for k in ("success", "collision", "timeout"):
+        assert round(rep[k] * 128) == round(want[k] * 128), (k, rep[k], want[k])
+    assert abs(rep["mean_goal_time"] - want["mean_goal_time_s"]) <= 0.02, rep
+    assert abs(rep["progress"] - want["progress"]) <= 1e-3, rep
+    assert abs(rep["mean_speed"] - want["mean_speed_mps"]) <= 5e-3, rep
+    assert abs(rep["peak_speed"] - want["peak_speed_mps"]) <= 1e-3, rep
+    assert abs(rep["min_clearance"] - want["min_clearance_m"]) <= 1e-5, rep
