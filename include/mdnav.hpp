@@ -44,6 +44,8 @@ public:
         cfg = config;
     }
     void reset() { require(mdn_sim_reset(handle_)); }
+    // The guided build's FIXED_PPO_ACTOR_OBS_DIM = 184 (ppo.hpp:11-34), chosen at run time.
+    void set_actor_obs(uint32_t d) { require(mdn_sim_set_actor_obs(handle_, d)); }
     // Sim::collect(cmdbuf, count): enqueue; finish() waits like Metal::finish.
     void collect(uint32_t count = 0) { require(mdn_sim_collect(handle_, count)); }
     double finish() {
@@ -99,10 +101,32 @@ public:
         require(mdn_ppo_optimizer_step(handle_, &s));
         return s;
     }
+    // PPOTrainer::save_checkpoint / load_checkpoint (main.mm:1218-1317); the
+    // load returns the completed rollouts (0 without a file).
+    void save_checkpoint(const std::string& path, uint32_t family, uint32_t seed, uint32_t completed_rollouts) {
+        require(mdn_ppo_save_checkpoint(handle_, path.c_str(), family, seed, completed_rollouts));
+    }
+    uint32_t load_checkpoint(const std::string& path, uint32_t family, uint32_t horizon, uint32_t n, uint32_t seed) {
+        uint32_t done = 0;
+        require(mdn_ppo_load_checkpoint(handle_, path.c_str(), family, horizon, n, seed, &done));
+        return done;
+    }
 
 private:
     Sim& sim_;
     MdnPPO* handle_ = nullptr;
+};
+
+// nav_deployment::NavigationPolicy::load (deployment.hpp:142-166): metadata,
+// the 12,104 weights of the 184-64-4 actor, the source checkpoint's hash.
+struct NavigationPolicy {
+    MdnNavPolicyMeta metadata{};
+    std::vector<float> weights;
+    uint64_t source_hash = 0;
+    void load(const std::string& path) {
+        weights.assign(184 * 64 + 64 + 4 * 64 + 4 + 4, 0.0f);
+        require(mdn_navpol_read(path.c_str(), &metadata, weights.data(), weights.size(), &source_hash));
+    }
 };
 
 // cpu_reference::Trainer on the GPU: Trainer(cfg, horizon, raptor, physics),

@@ -8,8 +8,21 @@
 
 int main(int argc, char** argv) {
     if (argc < 2) {
-        std::fprintf(stderr, "usage: facade_example RAPTOR_BIN [envs] [rollouts]\n");
+        std::fprintf(stderr, "usage: facade_example RAPTOR_BIN [envs] [rollouts] | --policy NAVPOL1_FILE\n");
         return 2;
+    }
+    if (std::strcmp(argv[1], "--policy") == 0 && argc > 2) {  // the deployed-policy loader, no GPU needed
+        try {
+            mdnav::NavigationPolicy policy;
+            policy.load(argv[2]);
+            std::printf("mode=%u observations=%u weights=%zu max_speed=%.2f source=%016llx\n",
+                        policy.metadata.policy_mode, policy.metadata.observation_count, policy.weights.size(),
+                        policy.metadata.max_speed_mps, (unsigned long long)policy.source_hash);
+        } catch (const std::exception& e) {
+            std::fprintf(stderr, "ERROR: %s\n", e.what());
+            return 1;
+        }
+        return 0;
     }
     MdnRaptorWeights raptor;
     if (!mdn::load_raptor_file(argv[1], &raptor)) { std::fprintf(stderr, "RAPTOR load failed\n"); return 2; }

@@ -26,6 +26,17 @@ def test_facade_compiles_and_reports_usage():
     assert r.returncode == 2 and "usage" in r.stderr
 
 
+def test_facade_loads_deployed_policy():
+    exe = build_example()
+    r = subprocess.run([exe, "--policy", os.path.join(ROOT, "tests", "golden", "navigation.bin")],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    assert "mode=17 observations=184 weights=12104 max_speed=1.50 source=1d991b0048dec80a" in r.stdout, r.stdout
+    r = subprocess.run([exe, "--policy", os.path.join(ROOT, "tests", "golden", "raptor.bin")],
+                       capture_output=True, text=True)
+    assert r.returncode == 1 and "magic mismatch" in r.stderr, r.stderr
+
+
 @pytest.mark.gpu
 def test_facade_trains_on_gpu():
     exe = build_example()
