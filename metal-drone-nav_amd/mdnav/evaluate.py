@@ -54,3 +54,107 @@ def sim_evaluate(family, mode, actor=None, speed=1.0, distance=3.0, seed=700001,
                  goal_time=float(r["success_time"].astype(np.float64).sum()) / success if success else 1e9)
     sim.close()
     return score, dict(report, gpu_s=gpu)
+
+
+# ---------------------------------------------------------------- controlled threats
+F32 = np.float32
+MASK = 0xFFFFFFFF
+
+
+def _urand(state):
+    """xorshift32 (13, 17, 5) and its 24-bit uniform (world.hpp:30-31)."""
+    state ^= (state << 13) & MASK
+    state ^= state >> 17
+    state ^= (state << 5) & MASK
+    return state, F32(state >> 8) * F32(1.0 / 16777216.0)
+
+
+def _inside_room(p, margin):
+    """threat_inside_room (threat_evaluation.hpp:9-13)."""
+    return (p[0] - margin >= F32(-2.0) and p[0] + margin <= F32(14.0) and p[1] - margin >= F32(-5.0) and
+            p[1] + margin <= F32(5.0) and p[2] - margin >= F32(0.0) and p[2] + margin <= F32(5.0))
+
+
+def add_threat_spheres(worlds, seed, kind, drone_speed, threat_speed, nominal_ttc):
+    """add_threat_sphere (threat_evaluation.hpp:20-70) for every env n with seed
+    seed + n * 747796405: one 0.35 m sphere on a nominal approach (kind 0) or
+    lateral-crossing (kind 1) course and the goal moved to (4, 0, 1.5).  The
+    clearance checks run on the GPU (ops.clearance = wclearance).  Raises if
+    any env's scene starts overlapped or its sphere path leaves the room or
+    meets geometry, as the reference's require() does."""
+    from . import ops
+    worlds = np.array(worlds, abi.WORLD).copy()
+    n = len(worlds)
+    drone_radius, sphere_radius = F32(0.18), F32(0.35)
+    combined = drone_radius + sphere_radius
+    drone_speed, threat_speed, nominal_ttc = F32(drone_speed), F32(threat_speed), F32(nominal_ttc)
+    if kind not in (0, 1) or drone_speed <= 0 or threat_speed <= 0 or nominal_ttc <= 0 or np.any(worlds["count"] >= 16):
+        raise ValueError("invalid threat kind, speeds or time to collision, or a full world")
+    candidates = worlds.copy()
+    candidates["goal"] = [4.0, 0.0, 1.5]
+    start = np.array([0.0, 0.0, 1.5], F32)
+    ok = ops.clearance(candidates, np.tile(start, (n, 1)), np.zeros(n, F32)) > 0
+    centers, velocities = np.zeros((n, 3), F32), np.zeros((n, 3), F32)
+    for e in range(n):
+        rng = ((seed + e * 747796405) & MASK) ^ 0x9E3779B9
+        if rng == 0:
+            rng = 1
+        rng, u = _urand(rng)
+        lateral = (u - F32(0.5)) * F32(0.20)
+        rng, u = _urand(rng)
+        vertical = (u - F32(0.5)) * F32(0.16)
+        if kind == 0:
+            centers[e] = [(drone_speed + threat_speed) * nominal_ttc + combined, lateral, F32(1.5) + vertical]
+            velocities[e, 0] = -threat_speed
+        else:
+            centers[e] = [drone_speed * nominal_ttc, -threat_speed * nominal_ttc + lateral, F32(1.5) + vertical]
+            velocities[e, 1] = threat_speed
+        c = centers[e]
+        d = c - start
+        ok[e] &= _inside_room(c, combined) and bool(np.sqrt(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]) > combined)
+    for sample in range(9):  # the nominal path against the room and existing geometry
+        t = nominal_ttc * (F32(sample) / F32(8.0))
+        p = (centers + velocities * t).astype(F32)
+        clear = ops.clearance(candidates, p, np.full(n, t, F32))
+        for e in range(n):
+            ok[e] &= _inside_room(p[e], combined) and bool(clear[e] > sphere_radius)
+    if not np.all(ok):
+        raise RuntimeError("invalid or overlapping threat scene (envs %s)" % np.flatnonzero(~ok)[:8].tolist())
+    for e in range(n):
+        i = int(candidates[e]["count"])
+        o = candidates[e]["obstacles"][i]
+        o["kind"], o["center"], o["size"], o["velocity"] = 1, centers[e], [sphere_radius] * 3, velocities[e]
+        candidates[e]["obstacles"][i] = o
+        candidates[e]["count"] = i + 1
+    return candidates
+
+
+def evaluate_threat(actor, mode, kind, threat_speed, nominal_ttc, seed=800001, sensor_delay=0, command_delay=0,
+                    velocity_contract=1, memory=1, raptor=None, physics=None):
+    """evaluate_threat (main.mm:2711-2728): 128 one-episode runs in family-0
+    worlds with one controlled threat sphere each, the drone starting at
+    1.5 m/s towards a goal 4 m ahead.  Returns the Sim::report dict."""
+    if kind not in (0, 1) or sensor_delay > 6 or command_delay > 7:
+        raise ValueError("invalid threat kind or delay")
+    actor = np.ascontiguousarray(actor, np.float32).reshape(-1)
+    sizes = {abi.policy_shape(obs=d)["actor_count"]: d for d in (181, 184)}
+    if actor.size not in sizes:
+        raise ValueError("threat actor dimensions")
+    cfg = abi.default_config(n=128, family=0, mode=mode, eval=1, seed=seed, speed=1.5, distance=4.0,
+                             sensor_delay=sensor_delay, command_delay=command_delay,
+                             velocity_contract=velocity_contract, geometry_memory=1 if (memory or mode >= 13) else 0)
+    sim = Sim(cfg, 32, raptor=raptor, physics=physics, actor_obs=sizes[actor.size])
+    sim.set("actor", actor)
+    sim.set("worlds", add_threat_spheres(sim.get("worlds"), seed, kind, 1.5, threat_speed, nominal_ttc))
+    states, runs = sim.get("states"), sim.get("runs")
+    states["linear_velocity"][:, 0] = cfg["speed"]
+    runs["desired_velocity"][:, 0] = cfg["speed"]
+    runs["previous_nav"][:, 0] = 1.0
+    sim.set("states", states)
+    sim.set("runs", runs)
+    start = time.perf_counter()
+    sim.collect(int(cfg["max_steps"]))
+    gpu = sim.sync()
+    report = sim.report("eval family=0 mode=%d" % mode, time.perf_counter() - start)
+    sim.close()
+    return dict(report, gpu_s=gpu)

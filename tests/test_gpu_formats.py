@@ -163,3 +163,37 @@ def test_continuation_evaluations(row):
     assert abs(rep["mean_speed"] - want["mean_speed_mps"]) <= 5e-3, rep
     assert abs(rep["peak_speed"] - want["peak_speed_mps"]) <= 1e-3, rep
     assert abs(rep["min_clearance"] - want["min_clearance_m"]) <= 1e-5, rep
+
+
+def threat_evaluations():
+    import csv
+    rows = csv.DictReader(open(os.path.join(GOLDEN, "continuation-evaluation.csv")))
+    return [r for r in rows if r["group"] == "controlled_threat"]
+
+
+@pytest.mark.parametrize("row", threat_evaluations(), ids=lambda r: r["case_id"][:48])
+def test_threat_evaluations(row):
+    """The 24 published controlled-threat evaluations of the table-memory
+    policy (continuation-evaluation.csv; threat-eval, main.mm:2711-2728 with
+    threat_evaluation.hpp): one 0.35 m sphere per env on an approach or
+    crossing course at 0.5 or 2 m/s, nominal time to collision 0.5 or 1 s,
+    modes 2/13/17.  Outcome counts exact; statistics as above."""
+    from mdnav import evaluate_threat
+    w = formats.read_navigation_policy(NAVPOL)[1]
+    assert row["checkpoint_sha256"].startswith("fdd62374")  # guided-table-memory, navigation.bin's source
+    kind = {"approach": 0, "crossing": 1}[row["threat_kind"]]
+    rep = evaluate_threat(w, int(row["mode"]), kind, float(row["threat_speed_mps"]), float(row["nominal_ttc_s"]),
+                          seed=int(row["seed"]), sensor_delay=int(row["sensor_delay_frames"]),
+                          command_delay=int(row["command_delay_steps"]), raptor=raptor_fixture()[0])
+    want = {k: float(row[k]) for k in ("success", "collision", "timeout", "progress", "mean_goal_time_s",
+                                       "mean_speed_mps", "peak_speed_mps", "min_clearance_m")}
+    say("case %s: success %.6g/%.6g collision %.6g/%.6g progress %.6g/%.6g" % (
+        row["case_id"][:40], rep["success"], want["success"], rep["collision"], want["collision"], rep["progress"],
+        want["progress"]))
+    for k in ("success", "collision", "timeout"):
+        assert round(rep[k] * 128) == round(want[k] * 128), (k, rep[k], want[k])
+    assert abs(rep["mean_goal_time"] - want["mean_goal_time_s"]) <= 0.02, rep
+    assert abs(rep["progress"] - want["progress"]) <= 1e-3, rep
+    assert abs(rep["mean_speed"] - want["mean_speed_mps"]) <= 5e-3, rep
+    assert abs(rep["peak_speed"] - want["peak_speed_mps"]) <= 1e-3, rep
+    assert abs(rep["min_clearance"] - want["min_clearance_m"]) <= 1e-5, rep
