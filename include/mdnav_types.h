@@ -126,6 +126,70 @@ typedef struct MdnNavPolicyMeta {
     uint32_t memory_frames, body_frame;
 } MdnNavPolicyMeta;
 
+/* Episode dynamics variation (RLPhysicsDomainRange, physics_domain.hpp:17-24;
+ * NavigationRuntimeConfig, navigation_runtime.hpp:9-14).  With `enabled`
+ * set, every env steps with its own plant parameters, drawn at each episode
+ * reset when domain_amplitude > 0 (sim.metal:63-69). */
+typedef struct MdnDomainRange {
+    float mass_scale_min, mass_scale_max;
+    float inertia_axis_scale_min, inertia_axis_scale_max;
+    float thrust_gain_min, thrust_gain_max;
+    float rising_lag_scale_min, rising_lag_scale_max;
+    float falling_lag_scale_min, falling_lag_scale_max;
+    float minimum_thrust_to_weight;
+} MdnDomainRange;
+
+typedef struct MdnRuntimeConfig {
+    uint32_t enabled;
+    float domain_amplitude;
+    uint32_t domain_seed;
+    MdnDomainRange domain_range;
+} MdnRuntimeConfig;
+
+/* Goal-conditioned navigation tasks (navigation_tasks.hpp:64-95, 150-188):
+ * a generated world, start state and goal per episode, stable-arrival
+ * success and the task reward. */
+#define MDN_TASK_STAGE_OPEN_GOAL 0u
+#define MDN_TASK_STAGE_NEAR_GOAL_HOLD 1u
+#define MDN_TASK_STAGE_CLUTTER_GOAL 2u
+#define MDN_TASK_OBJECTIVE_WAYPOINT 0u
+#define MDN_TASK_OBJECTIVE_FINAL_HOLD 1u
+#define MDN_TASK_INVALID_CONFIG 1u
+#define MDN_TASK_UNSUPPORTED_DYNAMIC 2u
+#define MDN_TASK_EXHAUSTED 3u
+#define MDN_TASK_READY 4u
+#define MDN_TASK_UNSUPPORTED_FAMILY 5u
+#define MDN_TASK_MAX_WITNESS_POINTS 4u
+#define MDN_TASK_MAX_ATTEMPTS 64u
+
+typedef struct MdnTaskConfig {
+    uint32_t family, stage, objective, require_detour, max_generation_attempts, max_nav_steps;
+    float scene_distance_m, difficulty, goal_distance_min_m, goal_distance_max_m;
+    float minimum_endpoint_clearance_m, minimum_witness_clearance_m;
+    float goal_radius_m, stable_speed_mps, stable_hold_s, nav_period_s;
+    float initial_speed_min_mps, initial_speed_max_mps;
+    float progress_reward_per_m, time_cost_per_s, contact_penalty, stable_arrival_bonus, command_smoothness_weight;
+    float start_min_xyz[3], start_max_xyz[3], goal_min_xyz[3], goal_max_xyz[3];
+    uint32_t generation_version;
+} MdnTaskConfig;
+
+typedef struct MdnTaskControl {
+    uint32_t enabled;
+    MdnTaskConfig config;
+} MdnTaskControl;
+
+typedef struct MdnTaskState {
+    uint32_t generation_status, valid, generation_attempts, family, stage, objective, max_nav_steps;
+    uint32_t step_count, stable_ticks, was_inside_goal, waypoint_event_latched, terminal;
+    float start_position[3], start_yaw_rad, start_velocity_world[3], goal_position[3];
+    float initial_distance_m, previous_distance_m, difficulty;
+    float start_clearance_m, goal_clearance_m, direct_segment_clearance_m;
+    float witness_min_clearance_m, witness_length_m, stable_time_s;
+    float last_executed_world_command[4];
+    uint32_t witness_point_count;
+    float witness_points[4][3];
+} MdnTaskState;
+
 /* Rollout metrics of cpu_reference.hpp:55-70. */
 typedef struct MdnMetrics {
     double wall_seconds;
@@ -144,6 +208,10 @@ static_assert(sizeof(MdnSimRun) == 184, "SimRun layout");
 static_assert(sizeof(MdnSimConfig) == 84, "SimConfig layout");
 static_assert(sizeof(MdnCheckpointHeader) == 136, "PpoCheckpointHeader layout");
 static_assert(sizeof(MdnNavPolicyMeta) == 56, "NAV metadata layout");
+static_assert(sizeof(MdnRuntimeConfig) == 56, "NavigationRuntimeConfig layout");
+static_assert(sizeof(MdnTaskConfig) == 144, "NavigationTaskConfig layout");
+static_assert(sizeof(MdnTaskControl) == 148, "NavigationTaskControl layout");
+static_assert(sizeof(MdnTaskState) == 192, "NavigationTaskState layout");
 #endif
 
 #endif /* MDNAV_TYPES_H */

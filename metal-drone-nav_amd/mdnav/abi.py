@@ -64,6 +64,43 @@ NAV_POLICY_META = np.dtype([
     ("sensor_columns", u4), ("range_max_m", f4), ("navigation_period_s", f4), ("native_period_s", f4),
     ("memory_frames", u4), ("body_frame", u4)])
 
+# RLPhysicsDomainRange / NavigationRuntimeConfig (physics_domain.hpp:17-24,
+# navigation_runtime.hpp:9-14)
+DOMAIN_RANGE = np.dtype([
+    ("mass_scale", f4, 2), ("inertia_axis_scale", f4, 2), ("thrust_gain", f4, 2), ("rising_lag_scale", f4, 2),
+    ("falling_lag_scale", f4, 2), ("minimum_thrust_to_weight", f4)])
+RUNTIME_CONFIG = np.dtype([("enabled", u4), ("domain_amplitude", f4), ("domain_seed", u4),
+                           ("domain_range", DOMAIN_RANGE)])
+# RLPhysicsDomainSample (physics_domain.hpp:26-33)
+DOMAIN_SAMPLE = np.dtype([("mass_scale", f4), ("inertia_axis_scale", f4, 3), ("thrust_gain", f4, 4),
+                          ("rising_lag_scale", f4, 4), ("falling_lag_scale", f4, 4), ("thrust_to_weight", f4)])
+# NavigationTaskConfig / Control / State (navigation_tasks.hpp:64-95, 150-178)
+TASK_CONFIG = np.dtype([
+    ("family", u4), ("stage", u4), ("objective", u4), ("require_detour", u4), ("max_generation_attempts", u4),
+    ("max_nav_steps", u4), ("scene_distance_m", f4), ("difficulty", f4), ("goal_distance_min_m", f4),
+    ("goal_distance_max_m", f4), ("minimum_endpoint_clearance_m", f4), ("minimum_witness_clearance_m", f4),
+    ("goal_radius_m", f4), ("stable_speed_mps", f4), ("stable_hold_s", f4), ("nav_period_s", f4),
+    ("initial_speed_min_mps", f4), ("initial_speed_max_mps", f4), ("progress_reward_per_m", f4),
+    ("time_cost_per_s", f4), ("contact_penalty", f4), ("stable_arrival_bonus", f4),
+    ("command_smoothness_weight", f4), ("start_min_xyz", f4, 3), ("start_max_xyz", f4, 3),
+    ("goal_min_xyz", f4, 3), ("goal_max_xyz", f4, 3), ("generation_version", u4)])
+TASK_CONTROL = np.dtype([("enabled", u4), ("config", TASK_CONFIG)])
+TASK_STATE = np.dtype([
+    ("generation_status", u4), ("valid", u4), ("generation_attempts", u4), ("family", u4), ("stage", u4),
+    ("objective", u4), ("max_nav_steps", u4), ("step_count", u4), ("stable_ticks", u4), ("was_inside_goal", u4),
+    ("waypoint_event_latched", u4), ("terminal", u4), ("start_position", f4, 3), ("start_yaw_rad", f4),
+    ("start_velocity_world", f4, 3), ("goal_position", f4, 3), ("initial_distance_m", f4),
+    ("previous_distance_m", f4), ("difficulty", f4), ("start_clearance_m", f4), ("goal_clearance_m", f4),
+    ("direct_segment_clearance_m", f4), ("witness_min_clearance_m", f4), ("witness_length_m", f4),
+    ("stable_time_s", f4), ("last_executed_world_command", f4, 4), ("witness_point_count", u4),
+    ("witness_points", f4, (4, 3))])
+TASK_READY = 4
+# the episode dynamics seed of the reference's task training and evaluation
+# (navigation_training.hpp:21)
+TASK_DOMAIN_SEED = 0x3f84d5b5
+
+assert RUNTIME_CONFIG.itemsize == 56 and DOMAIN_SAMPLE.itemsize == 68
+assert TASK_CONFIG.itemsize == 144 and TASK_CONTROL.itemsize == 148 and TASK_STATE.itemsize == 192
 assert CHECKPOINT_HEADER.itemsize == 136 and NAV_POLICY_META.itemsize == 56
 assert PHYSICS_STATE.itemsize == 68 and PHYSICS_PARAMS.itemsize == 352
 assert RAPTOR_WEIGHTS.itemsize == 8336 and WORLD.itemsize == 676
@@ -130,5 +167,6 @@ BUFFERS = {
     "terminated": (15, np.uint8), "truncated": (16, np.uint8), "advantages": (17, np.float32),
     "returns": (18, np.float32), "actor_m": (19, np.float32), "actor_v": (20, np.float32),
     "critic_m": (21, np.float32), "critic_v": (22, np.float32), "metric_rows": (23, np.float32),
-    "next_critic_obs": (24, np.float32),
+    "next_critic_obs": (24, np.float32), "environment_physics": (25, PHYSICS_PARAMS),
+    "task_states": (26, TASK_STATE),
 }

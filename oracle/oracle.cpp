@@ -32,6 +32,7 @@
 
 #include "oracle_world.h"
 #include "oracle_guidance.h"
+#include "oracle_tasks.h"
 
 namespace orc {
 
@@ -236,6 +237,11 @@ struct Trainer {
     std::vector<float> metric_rows;
     float metric_mean[4] = {0, 0, 0, 0};
     std::vector<float> means, camera;
+    // episode dynamics and navigation tasks (sim.metal:55-141, 287, 307-315)
+    MdnRuntimeConfig runtime;
+    MdnTaskControl tasks;
+    std::vector<MdnPhysicsParams> env_physics;
+    std::vector<MdnTaskState> task_states;
 
     Trainer(const MdnSimConfig& c, uint32_t h, const MdnRaptorWeights& r, const MdnPhysicsParams& p,
             uint32_t ep, uint32_t mb)
@@ -259,6 +265,11 @@ struct Trainer {
         rewards.assign(rows, 0.0f); next_values.assign(rows, 0.0f); advantages.assign(rows, 0.0f);
         returns.assign(rows, 0.0f); terminated.assign(rows, 0); truncated.assign(rows, 0);
         means.assign(n * MDN_ACTIONS, 0.0f);
+        std::memset(&runtime, 0, sizeof(runtime));
+        std::memset(&tasks, 0, sizeof(tasks));
+        env_physics.assign(n, p);
+        task_states.resize(n);
+        std::memset(task_states.data(), 0, n * sizeof(MdnTaskState));
         camera.resize(MDN_SENSOR_PIXELS * 3);
         for (uint32_t k = 0; k < MDN_SENSOR_PIXELS; k++) {
             const V3 ray = camera_ray(k);
@@ -297,13 +308,11 @@ struct Trainer {
         }
         s.orientation_wxyz[0] = 1;
         for (int j = 1; j < 4; j++) s.orientation_wxyz[j] = 0;
-        const float target = physics.mass * 9.81f / 4;
-        const float c0 = physics.rotor_thrust_coefficients[0], c1 = physics.rotor_thrust_coefficients[1],
-                    c2 = physics.rotor_thrust_coefficients[2];
-        const float hover = clamp_f((-c1 + sqrt_f(c1 * c1 - 4 * c2 * (c0 - target))) / (2 * c2), physics.action_min,
-                                    physics.action_max);
+        env_physics[n] = episode_params(runtime, physics, cfg.seed, n, first ? 0u : run.episodes);
+        float hover[4];
+        hover_rpm(runtime, physics, env_physics[n], hover);
         raptor_reset(raptor, run.hidden);
-        for (int j = 0; j < 4; j++) { s.rpm[j] = hover; run.motors[j] = 0; run.previous_nav[j] = 0; }
+        for (int j = 0; j < 4; j++) { s.rpm[j] = hover[j]; run.motors[j] = 0; run.previous_nav[j] = 0; }
         if (world.family == 10 || world.family == 11) {
             s.linear_velocity[0] = cfg.speed;
             run.desired_velocity[0] = cfg.speed;
@@ -319,6 +328,10 @@ struct Trainer {
             run.success_time = run.total_path = run.total_elapsed = run.final_progress = 0;
             std::fill(poses.begin() + size_t(n) * 96, poses.begin() + size_t(n + 1) * 96, 0.0f);
         }
+        reset_task(tasks, cfg.seed, wind_param(n), n, s, run, world, task_states[n]);
+    }
+    void reset_all() {
+        for (uint32_t e = 0; e < cfg.n; e++) reset_env(e, true);
     }
 
     // sim.metal:159-181 == cpu_reference.hpp:379-394
@@ -546,7 +559,8 @@ struct Trainer {
         sincos_f(yaw * 0.5f, &sh, &ch);
         bool collision = false;
         float step_clearance = 12.0f;
-        const float wind[3] = {world.wind[0] * physics.mass, world.wind[1] * physics.mass, world.wind[2] * physics.mass};
+        const MdnPhysicsParams& sp = runtime.enabled != 0 ? env_physics[n] : physics;
+        const float wind[3] = {world.wind[0] * sp.mass, world.wind[1] * sp.mass, world.wind[2] * sp.mass};
         for (uint32_t step = 0; step < cfg.substeps; step++) {
             float mo[22];
             const float v[3] = {run.desired_velocity[0], run.desired_velocity[1], run.desired_velocity[2]};
@@ -571,7 +585,7 @@ struct Trainer {
             raptor_forward(raptor, mo, h, motors);
             raptor_clip(motors);
             MdnPhysicsState next;
-            physics_step(s, motors, wind, physics, next);
+            physics_step(s, motors, wind, sp, next);
             bool valid = true;
             const float* nf = &next.position[0];
             for (int j = 0; j < 17; j++) valid = valid && isfinite_f(nf[j]);
@@ -591,13 +605,24 @@ struct Trainer {
         for (int j = 0; j < 16; j++) run.hidden[j] = h[j];
         for (int j = 0; j < 4; j++) run.motors[j] = motors[j];
         const float after = vlen(vsub(goal, v3(s.position[0], s.position[1], s.position[2])));
-        const bool success = after < (cfg.mode == 20 ? .10f : .35f) && !collision;
-        const bool timeout = run.steps >= cfg.max_steps;
+        bool success = after < (cfg.mode == 20 ? .10f : .35f) && !collision;
+        bool timeout = run.steps >= cfg.max_steps;
         const size_t row = size_t(tick) * cfg.n + n;
         rewards[row] = (before - after) * 2.0f - .01f - cfg.risk_coef * clamp_f((0.6f - step_clearance) / 0.6f, 0.0f, 1.0f) +
                        (success ? 10.0f : 0.0f) - (collision ? 10.0f : 0.0f);
         terminated[row] = uint8_t(collision || success);
         truncated[row] = uint8_t(timeout && !terminated[row]);
+        if (tasks.enabled != 0) {  // sim.metal:307-315
+            const float executed[4] = {run.desired_velocity[0], run.desired_velocity[1], run.desired_velocity[2],
+                                       run.previous_nav[3] * 0.5f};
+            const TaskStep o = task_step(task_states[n], tasks.config, s.position, s.linear_velocity, executed,
+                                         uint32_t(collision), uint32_t(timeout));
+            success = o.stable_success != 0 && !collision;
+            timeout = o.timeout != 0;
+            rewards[row] = o.reward;
+            terminated[row] = uint8_t(collision || success);
+            truncated[row] = uint8_t(timeout && !terminated[row]);
+        }
         float hidden[8192];
         float* cobs = &nco[row * shape.critic_obs];
         critic_observation(s, world, run, cobs);
@@ -869,6 +894,40 @@ void orc_guidance_memory(const float* cur, const float* prev, const float* goal,
     orc::nav_guidance_memory(cur, prev, goal, distance, vel, sensor_dt, MDN_SENSOR_TAN_V, range_ring, pose_ring, pose,
                              latest_frame, valid_frames, hint);
 }
+void orc_trainer_set_runtime(void* h, const MdnRuntimeConfig* r) { static_cast<Trainer*>(h)->runtime = *r; }
+void orc_trainer_set_tasks(void* h, const MdnTaskControl* t) { static_cast<Trainer*>(h)->tasks = *t; }
+void orc_trainer_reset(void* h) { static_cast<Trainer*>(h)->reset_all(); }
+// standalone operators of the dynamics draw and the task generator
+int orc_sample_domain(const MdnPhysicsParams* nominal, uint32_t* rng, float amplitude, const MdnDomainRange* range,
+                      MdnPhysicsParams* varied, float* sample) {
+    orc::DomainSample s;
+    std::memset(&s, 0, sizeof(s));
+    const bool ok = orc::sample_domain(*nominal, *rng, amplitude, *range, *varied, s);
+    std::memcpy(sample, &s, sizeof(s));
+    return ok ? 1 : 0;
+}
+uint32_t orc_domain_episode_seed(const MdnRuntimeConfig* r, uint32_t cfg_seed, uint32_t env, uint32_t episode) {
+    return orc::domain_episode_seed(*r, cfg_seed, env, episode);
+}
+void orc_domain_stress_range(MdnDomainRange* r) { *r = orc::domain_stress_range(); }
+int orc_task_default_config(MdnTaskConfig* c, uint32_t stage, uint32_t family, float difficulty) {
+    return orc::task_default_config(*c, stage, family, difficulty) ? 1 : 0;
+}
+int orc_task_settings(MdnTaskControl* t, uint32_t stage, uint32_t family) {
+    bool ok = false;
+    *t = orc::task_settings(stage, family, ok);
+    return ok ? 1 : 0;
+}
+uint32_t orc_generate_task(MdnWorld* w, MdnTaskState* t, uint32_t* rng, const MdnTaskConfig* c) {
+    return orc::generate_task(*w, *t, *rng, *c);
+}
+void orc_task_step(MdnTaskState* t, const MdnTaskConfig* c, const float* pos, const float* vel, const float* executed,
+                   uint32_t contact, uint32_t forced_timeout, float* out) {
+    const orc::TaskStep r = orc::task_step(*t, *c, pos, vel, executed, contact, forced_timeout);
+    out[0] = r.reward; out[1] = r.goal_distance; out[2] = r.speed;
+    out[3] = float(r.waypoint_passed); out[4] = float(r.stable_success); out[5] = float(r.collision);
+    out[6] = float(r.timeout); out[7] = float(r.done);
+}
 void orc_trainer_evaluate(void* h) { static_cast<Trainer*>(h)->evaluate(); }
 void orc_trainer_set_ext_means(void* h, const float* means) { static_cast<Trainer*>(h)->ext_means = means; }
 uint64_t orc_trainer_optimizer_step(void* h) { return static_cast<Trainer*>(h)->optimizer_step; }
@@ -910,6 +969,8 @@ void* orc_trainer_buffer(void* hp, uint32_t id, uint64_t* bytes) {
         case 22: return ret(t->critic_v);
         case 23: return ret(t->metric_rows);
         case 24: return ret(t->nco);
+        case 25: return ret(t->env_physics);
+        case 26: return ret(t->task_states);
         default: *bytes = 0; return nullptr;
     }
 }

@@ -11,6 +11,7 @@
 #ifndef FIXED_PPO_ACTOR_OBS_DIM
 #define FIXED_PPO_ACTOR_OBS_DIM 181  // pooled actor; the Makefile also builds 184
 #endif
+#include <math.h>  // physics_domain.hpp calls the C library's isfinite unqualified
 #include <cstdint>
 #include <cstring>
 #include <vector>
@@ -21,14 +22,56 @@
 #include "raptor.hpp"
 #include "ppo.hpp"
 #include "guidance.hpp"
+#include "physics_domain.hpp"
+#include "navigation_runtime.hpp"
+#include "navigation_tasks.hpp"
 #include "mdnav_types.h"
 
 static_assert(sizeof(WWorld) == sizeof(MdnWorld), "world layout");
 static_assert(sizeof(RLPhysicsState) == sizeof(MdnPhysicsState), "state layout");
 static_assert(sizeof(RLPhysicsParams) == sizeof(MdnPhysicsParams), "params layout");
 static_assert(sizeof(RaptorWeights) == sizeof(MdnRaptorWeights), "raptor layout");
+static_assert(sizeof(RLPhysicsDomainRange) == sizeof(MdnDomainRange), "domain range layout");
+static_assert(sizeof(NavigationRuntimeConfig) == sizeof(MdnRuntimeConfig), "runtime config layout");
+static_assert(sizeof(NavigationTaskConfig) == sizeof(MdnTaskConfig), "task config layout");
+static_assert(sizeof(NavigationTaskControl) == sizeof(MdnTaskControl), "task control layout");
+static_assert(sizeof(NavigationTaskState) == sizeof(MdnTaskState), "task state layout");
 
 extern "C" {
+
+// physics_domain.hpp:98-155 and navigation_tasks.hpp:99-548
+int ref_sample_domain(const MdnPhysicsParams* nominal, uint32_t* rng, float amplitude, const MdnDomainRange* range,
+                      MdnPhysicsParams* varied, float* sample) {
+    RLPhysicsDomainSample s{};
+    const bool ok = rl_physics_sample_domain(*reinterpret_cast<const RLPhysicsParams*>(nominal), *rng, amplitude,
+                                             *reinterpret_cast<const RLPhysicsDomainRange*>(range),
+                                             *reinterpret_cast<RLPhysicsParams*>(varied), s);
+    std::memcpy(sample, &s, sizeof(s));
+    return ok ? 1 : 0;
+}
+void ref_domain_stress_range(MdnDomainRange* r) {
+    const RLPhysicsDomainRange v = rl_physics_domain_stress_range();
+    std::memcpy(r, &v, sizeof(v));
+}
+int ref_task_default_config(MdnTaskConfig* c, uint32_t stage, uint32_t family, float difficulty) {
+    return navigation_task_default_config(*reinterpret_cast<NavigationTaskConfig*>(c), stage, family, difficulty) ? 1 : 0;
+}
+uint32_t ref_generate_task(MdnWorld* w, MdnTaskState* t, uint32_t* rng, const MdnTaskConfig* c) {
+    return navigation_generate_task(*reinterpret_cast<WWorld*>(w), *reinterpret_cast<NavigationTaskState*>(t), *rng,
+                                    *reinterpret_cast<const NavigationTaskConfig*>(c));
+}
+void ref_task_apply_start(const MdnTaskState* t, MdnPhysicsState* s) {
+    navigation_task_apply_start(*reinterpret_cast<const NavigationTaskState*>(t), *reinterpret_cast<RLPhysicsState*>(s));
+}
+void ref_task_step(MdnTaskState* t, const MdnTaskConfig* c, const float* pos, const float* vel, const float* executed,
+                   uint32_t contact, uint32_t forced_timeout, float* out) {
+    const NavigationTaskStep r = navigation_task_step(*reinterpret_cast<NavigationTaskState*>(t),
+                                                      *reinterpret_cast<const NavigationTaskConfig*>(c), pos, vel,
+                                                      executed, contact, forced_timeout);
+    out[0] = r.reward; out[1] = r.goal_distance_m; out[2] = r.actual_speed_mps;
+    out[3] = float(r.waypoint_passed); out[4] = float(r.stable_success); out[5] = float(r.collision);
+    out[6] = float(r.timeout); out[7] = float(r.episode_done);
+}
 
 void ref_generate_world(MdnWorld* w, uint32_t seed, uint32_t family, float distance) {
     std::memset(w, 0, sizeof(*w));

@@ -84,11 +84,28 @@ def oracle():
         _sig(lib, "orc_crazyflie_params", None, P)
         _sig(lib, "orc_default_config", None, P)
         _sig(lib, "orc_num_threads", ctypes.c_int)
+        _sig(lib, "orc_trainer_set_runtime", None, P, P)
+        _sig(lib, "orc_trainer_set_tasks", None, P, P)
+        _sig(lib, "orc_trainer_reset", None, P)
+        _sig(lib, "orc_sample_domain", ctypes.c_int, P, ctypes.POINTER(U32), F32, P, P, P)
+        _sig(lib, "orc_domain_episode_seed", U32, P, U32, U32, U32)
+        _sig(lib, "orc_domain_stress_range", None, P)
+        _sig(lib, "orc_task_default_config", ctypes.c_int, P, U32, U32, F32)
+        _sig(lib, "orc_task_settings", ctypes.c_int, P, U32, U32)
+        _sig(lib, "orc_generate_task", U32, P, P, ctypes.POINTER(U32), P)
+        _sig(lib, "orc_task_step", None, P, P, P, P, P, U32, U32, P)
         _oracle = lib
     return _oracle
 
 
+# the same headers built with clang++ (left-to-right argument evaluation, as
+# the reference's Metal compiler)
+REFCLANG_SO = os.path.join(ROOT, "oracle", "_ref", "libmdnref_clang.so")
+
+
 def ref_available(actor_obs=181):
+    if actor_obs == "clang":
+        return os.path.exists(REFCLANG_SO)
     return os.path.exists(REF_SO if actor_obs == 181 else REF184_SO)
 
 
@@ -98,7 +115,7 @@ _refs = {}
 def ref(actor_obs=181):
     """The reference's headers built for an actor of `actor_obs` inputs."""
     if actor_obs not in _refs:
-        lib = ctypes.CDLL(REF_SO if actor_obs == 181 else REF184_SO)
+        lib = ctypes.CDLL(REFCLANG_SO if actor_obs == "clang" else REF_SO if actor_obs == 181 else REF184_SO)
         _sig(lib, "ref_generate_world", None, P, U32, U32, F32)
         _sig(lib, "ref_ray_world_batch", None, P, P, P, U32, P, U64)
         _sig(lib, "ref_clearance_batch", None, P, P, P, P, U64)
@@ -125,6 +142,12 @@ def ref(actor_obs=181):
         _sig(lib, "ref_guidance", None, P, P, P, F32, P, F32, P)
         _sig(lib, "ref_guidance_memory", None, P, P, P, F32, P, F32, P, P, P, U32, U32, P)
         _sig(lib, "ref_memory_clearance", None, P, P, P, P, U32, U32, F32, P)
+        _sig(lib, "ref_sample_domain", ctypes.c_int, P, ctypes.POINTER(U32), F32, P, P, P)
+        _sig(lib, "ref_domain_stress_range", None, P)
+        _sig(lib, "ref_task_default_config", ctypes.c_int, P, U32, U32, F32)
+        _sig(lib, "ref_generate_task", U32, P, P, ctypes.POINTER(U32), P)
+        _sig(lib, "ref_task_apply_start", None, P, P)
+        _sig(lib, "ref_task_step", None, P, P, P, P, P, U32, U32, P)
         _refs[actor_obs] = lib
     return _refs[actor_obs]
 
@@ -195,6 +218,17 @@ class OracleTrainer:
 
     def get(self, name):
         return self.buffer(name).copy()
+
+    def set_runtime(self, runtime):
+        self._runtime = np.array(runtime, abi.RUNTIME_CONFIG)
+        self.lib.orc_trainer_set_runtime(self.h, ptr(self._runtime))
+
+    def set_tasks(self, tasks):
+        self._tasks = np.array(tasks, abi.TASK_CONTROL)
+        self.lib.orc_trainer_set_tasks(self.h, ptr(self._tasks))
+
+    def reset(self):
+        self.lib.orc_trainer_reset(self.h)
 
     def set(self, name, values):
         b = self.buffer(name)
@@ -284,3 +318,29 @@ def math_batch(fn, x):
     oracle().orc_math_batch({"exp": 0, "log": 1, "sin": 2, "cos": 3, "tanh": 4, "expm1": 5,
                              "sigmoid": 6}[fn], ptr(x), ptr(y), x.size)
     return y
+
+
+def task_runtime(amplitude, enabled=1):
+    """NavigationRuntimeConfig of the reference's task training and evaluation
+    (navigation_training.hpp:20-22): the stress range, seed 0x3f84d5b5."""
+    r = np.zeros((), abi.RUNTIME_CONFIG)
+    r["enabled"] = enabled
+    r["domain_amplitude"] = amplitude
+    r["domain_seed"] = abi.TASK_DOMAIN_SEED
+    rng = np.zeros((), abi.DOMAIN_RANGE)
+    oracle().orc_domain_stress_range(ptr(rng))
+    r["domain_range"] = rng
+    return r
+
+
+def task_settings(stage, family):
+    """task_settings of navigation_training.hpp:7-14."""
+    t = np.zeros((), abi.TASK_CONTROL)
+    assert oracle().orc_task_settings(ptr(t), stage, family) == 1
+    return t
+
+
+def task_eval_config(seed, family, mode=17, n=128):
+    """SimConfig of navigation_training::evaluate (navigation_training.hpp:68-71)."""
+    return abi.default_config(n=n, eval=1, mode=mode, seed=seed, family=family, speed=1.5, distance=8.0,
+                              max_steps=400, geometry_memory=1)
