@@ -59,7 +59,9 @@ enum MdnBuffer {
     MDN_BUF_CRITIC_M = 21,
     MDN_BUF_CRITIC_V = 22,
     MDN_BUF_METRIC_ROWS = 23, /* float[updates][4] of the last rollout_update */
-    MDN_BUF_NEXT_CRITIC_OBS = 24 /* float[T][N][32] critic observation of s' (the next_values input) */
+    MDN_BUF_NEXT_CRITIC_OBS = 24, /* float[T][N][32] critic observation of s' (the next_values input) */
+    MDN_BUF_ENV_PHYSICS = 25, /* MdnPhysicsParams[N]  environment_physics (main.mm:537): each env's plant */
+    MDN_BUF_TASK_STATES = 26  /* MdnTaskState[N]      task_states (main.mm:523) */
 };
 
 /* Kernel ids for mdn_sim_kernel_time. */
@@ -74,7 +76,8 @@ enum MdnKernel {
     MDN_K_LP_BACKWARD = 7, /* wide-policy backward partials and their sums */
     MDN_K_LP_ADAM = 8,     /* wide-policy clip + Adam + bf16 refresh */
     MDN_K_MEMORY = 9,      /* geometry-memory hint of one tick (memory.metal + guidance.hpp:152-194) */
-    MDN_K_COUNT = 10
+    MDN_K_EPISODE = 10,    /* per-episode plant draw and navigation task after resets (sim.metal:62-81, 122-141) */
+    MDN_K_COUNT = 11
 };
 
 const char* mdn_last_error(void);
@@ -120,6 +123,35 @@ int mdn_sim_set_lanes(MdnSim* sim, uint32_t lanes);
  * and pose rings, cpu_reference.hpp:364-372): mdn_sim_collect then runs one
  * env launch and one memory launch per tick. */
 int mdn_sim_set_actor_obs(MdnSim* sim, uint32_t actor_obs);
+
+/* Episode dynamics variation: the reference's Sim::runtime_control
+ * (NavigationRuntimeConfig, navigation_runtime.hpp:9-14, written by
+ * navigation_training.hpp:20-23).  With `enabled`, every env steps with its
+ * own plant (MDN_BUF_ENV_PHYSICS, sim.metal:287), drawn at each reset when
+ * domain_amplitude > 0 (physics_domain.hpp:98-155 seeded per env and episode,
+ * sim.metal:50-54; a rejected draw leaves a NaN mass) with hover rpm per
+ * rotor (sim.metal:70-81).  Takes effect at the next mdn_sim_reset, as the
+ * reference's memcpy + reset does.  mdn_sim_collect then runs one tick per
+ * launch with a per-episode kernel after each (8 lanes per env). */
+int mdn_sim_set_runtime(MdnSim* sim, const MdnRuntimeConfig* runtime);
+int mdn_sim_get_runtime(const MdnSim* sim, MdnRuntimeConfig* runtime);
+/* Goal-conditioned navigation tasks: Sim::task_control
+ * (NavigationTaskControl, navigation_tasks.hpp:93-95).  With `enabled`,
+ * each reset generates the env's world, start state and goal
+ * (navigation_generate_task, navigation_tasks.hpp:355-491, seeded per env and
+ * episode, sim.metal:122-141; MDN_BUF_TASK_STATES holds the task and its
+ * generation status), and each tick's task step (navigation_tasks.hpp:509-548)
+ * replaces success (stable arrival), timeout and reward (sim.metal:307-315).
+ * config.generation_version 1 is the reference's current generator; 0 is
+ * the generator before clutter goals were conditioned on the goal bounds
+ * (the version of the reference's published goal-arrival evidence).  Takes
+ * effect at the next mdn_sim_reset. */
+int mdn_sim_set_tasks(MdnSim* sim, const MdnTaskControl* tasks);
+int mdn_sim_get_tasks(const MdnSim* sim, MdnTaskControl* tasks);
+/* navigation_task_default_config (navigation_tasks.hpp:99-140) and
+ * rl_physics_domain_stress_range (physics_domain.hpp:37-40). */
+int mdn_task_default_config(uint32_t stage, uint32_t family, float difficulty, MdnTaskConfig* out);
+int mdn_domain_stress_range(MdnDomainRange* out);
 int mdn_sim_get_actor_obs(const MdnSim* sim, uint32_t* actor_obs);
 
 /* PPOTrainer(Sim&, epochs) — main.mm:1166-1217, with the minibatch size

@@ -163,6 +163,40 @@ inline bool load_raptor_file(const char* path, MdnRaptorWeights* w) {
     return ok;
 }
 
+// physics_domain.hpp:37-40 — the stress bounds of the episode plant draw
+inline MdnDomainRange domain_stress_range() {
+    return {0.90f, 1.10f, 0.90f, 1.10f, 0.90f, 1.10f, 0.75f, 1.35f, 0.75f, 1.35f, 1.15f};
+}
+
+// navigation_tasks.hpp:99-140 — baseline task parameters per stage
+inline bool task_default_config(MdnTaskConfig& c, uint32_t stage, uint32_t family, float difficulty) {
+    if (stage > MDN_TASK_STAGE_CLUTTER_GOAL || !(difficulty >= 0.0f && difficulty <= 1.0f)) return false;
+    const bool open = stage != MDN_TASK_STAGE_CLUTTER_GOAL;
+    if (open ? family != 0u : !(family == 1u || family == 2u || family == 4u || family == 5u || family == 12u))
+        return false;
+    c = MdnTaskConfig{};
+    c.generation_version = 1; c.family = family; c.stage = stage;
+    c.objective = MDN_TASK_OBJECTIVE_FINAL_HOLD; c.require_detour = 0;
+    c.max_generation_attempts = MDN_TASK_MAX_ATTEMPTS; c.max_nav_steps = 400;
+    c.scene_distance_m = 8.0f; c.difficulty = difficulty;
+    c.minimum_endpoint_clearance_m = 0.30f; c.minimum_witness_clearance_m = 0.02f;
+    c.goal_radius_m = 0.35f; c.stable_speed_mps = 0.50f; c.stable_hold_s = 0.20f; c.nav_period_s = 0.05f;
+    c.progress_reward_per_m = 2.0f; c.time_cost_per_s = 0.20f; c.contact_penalty = 10.0f;
+    c.stable_arrival_bonus = 10.0f; c.command_smoothness_weight = 0.05f;
+    const float start_lo[3] = {-1.0f, -2.0f, 0.8f}, start_hi[3] = {1.0f, 2.0f, 2.4f};
+    const float goal_lo[3] = {-1.2f, -4.0f, 0.5f}, goal_hi[3] = {13.2f, 4.0f, 4.5f};
+    const bool near = stage == MDN_TASK_STAGE_NEAR_GOAL_HOLD;
+    for (int k = 0; k < 3; k++) {
+        c.start_min_xyz[k] = near ? goal_lo[k] : start_lo[k];
+        c.start_max_xyz[k] = near ? goal_hi[k] : start_hi[k];
+        c.goal_min_xyz[k] = goal_lo[k];
+        c.goal_max_xyz[k] = goal_hi[k];
+    }
+    c.goal_distance_min_m = near ? 0.8f : 2.0f;
+    c.goal_distance_max_m = near ? 2.0f : (stage == MDN_TASK_STAGE_CLUTTER_GOAL ? 7.0f : 6.0f);
+    return true;
+}
+
 } // namespace mdn
 
 #endif /* MDNAV_HOST_H */

@@ -92,6 +92,14 @@ struct MdnSim {
     float* cells = nullptr;     // pooled-cell directions of the guidance hint [80][3]
     float* pix_rays = nullptr;  // raw-pixel directions of the geometry memory [320][3]
     uint32_t* mem_head = nullptr;  // per-env memory header [N][16]
+    // per-episode plants and navigation tasks (NavigationRuntimeConfig and
+    // NavigationTaskControl of the reference's Sim, main.mm:523-537)
+    MdnRuntimeConfig runtime{};
+    MdnTaskControl task{};
+    MdnPhysicsParams* env_phys = nullptr;   // [N]
+    MdnTaskState* task_states = nullptr;    // [N]
+    MdnTaskConfig* task_cfg = nullptr;      // device copy of task.config
+    bool episodic() const { return runtime.enabled != 0u || task.enabled != 0u; }
     // policy
     float* actor = nullptr;
     float* critic = nullptr;
@@ -115,7 +123,16 @@ struct MdnSim {
         a.sensor_dt = float(cfg.sensor_period) * phys.dt * float(cfg.substeps);
         a.inv_sensor_dt = 1.0 / double(std::max(a.sensor_dt, 1e-3f));
         a.mem_head = nullptr;
+        a.env_phys = episodic() ? env_phys : nullptr;
+        a.task_states = task_states;
+        a.task_cfg = task.enabled ? task_cfg : nullptr;
         return a;
+    }
+    nav::EpisodeArgs episode_args(bool first) const {
+        nav::EpisodeArgs e;
+        e.state = state; e.run = run; e.world = world; e.env_phys = env_phys; e.task_states = task_states;
+        e.cfg = cfg; e.phys = phys; e.runtime = runtime; e.task = task; e.first = first ? 1u : 0u;
+        return e;
     }
 };
 
@@ -193,6 +210,8 @@ BufInfo row_buffer(MdnSim* s, uint32_t id) {
         case MDN_BUF_WORLDS: return {s->world, size_t(s->cfg.n) * WORLD_WORDS * 4};
         case MDN_BUF_ACTOR: return {s->actor, size_t(s->shape.actor_count()) * 4};
         case MDN_BUF_CRITIC: return {s->critic, size_t(s->shape.critic_count()) * 4};
+        case MDN_BUF_ENV_PHYSICS: return {s->env_phys, size_t(s->cfg.n) * sizeof(MdnPhysicsParams)};
+        case MDN_BUF_TASK_STATES: return {s->task_states, size_t(s->cfg.n) * sizeof(MdnTaskState)};
         default: break;
     }
     if (s->ppo) {
@@ -246,6 +265,9 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
     guard(dev_alloc(&s->cells, 240));
     guard(dev_alloc(&s->pix_rays, 960));
     guard(dev_alloc(&s->mem_head, size_t(N) * nav::MEM_HEAD_WORDS));
+    guard(dev_alloc(&s->env_phys, N));
+    guard(dev_alloc(&s->task_states, N));
+    guard(dev_alloc(&s->task_cfg, 1));
     guard(dev_alloc(&s->actor, s->shape.actor_count()));
     guard(dev_alloc(&s->critic, s->shape.critic_count()));
     guard(dev_alloc(&s->actor_w1t, size_t(OBS) * HID));
@@ -323,7 +345,7 @@ void mdn_sim_destroy(MdnSim* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->ppo) mdn_ppo_destroy(s->ppo);
     void* bufs[] = {s->state, s->run, s->world, s->sensors, s->poses, s->commands, s->raptor, s->camera, s->cells,
-                    s->pix_rays, s->mem_head,
+                    s->pix_rays, s->mem_head, s->env_phys, s->task_states, s->task_cfg,
                     s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->obs, s->co, s->nco, s->actions, s->logp,
                     s->values, s->rewards, s->next_values, s->advantages, s->returns, s->terminated, s->truncated};
     for (void* b : bufs)
@@ -400,7 +422,84 @@ int mdn_sim_reset(MdnSim* s) {
     if (rc) return rc;
     const nav::RolloutArgs a = s->args(0);
     HIP_TRY(nav_launch_reset(&a, s->stream));
+    if (s->episodic()) {
+        const nav::EpisodeArgs e = s->episode_args(true);
+        HIP_TRY(nav_launch_episode(&e, s->stream));
+    }
     return MDN_OK;
+}
+
+int mdn_sim_set_runtime(MdnSim* s, const MdnRuntimeConfig* runtime) {
+    if (!s || !runtime) return fail(MDN_E_ARG, "mdn_sim_set_runtime: null argument");
+    s->runtime = *runtime;
+    return MDN_OK;
+}
+
+int mdn_sim_get_runtime(const MdnSim* s, MdnRuntimeConfig* runtime) {
+    if (!s || !runtime) return fail(MDN_E_ARG, "mdn_sim_get_runtime: null argument");
+    *runtime = s->runtime;
+    return MDN_OK;
+}
+
+int mdn_sim_set_tasks(MdnSim* s, const MdnTaskControl* tasks) {
+    if (!s || !tasks) return fail(MDN_E_ARG, "mdn_sim_set_tasks: null argument");
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    s->task = *tasks;
+    HIP_TRY(hipMemcpyAsync(s->task_cfg, &s->task.config, sizeof(MdnTaskConfig), hipMemcpyHostToDevice, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    return MDN_OK;
+}
+
+int mdn_sim_get_tasks(const MdnSim* s, MdnTaskControl* tasks) {
+    if (!s || !tasks) return fail(MDN_E_ARG, "mdn_sim_get_tasks: null argument");
+    *tasks = s->task;
+    return MDN_OK;
+}
+
+int mdn_task_default_config(uint32_t stage, uint32_t family, float difficulty, MdnTaskConfig* out) {
+    if (!out) return fail(MDN_E_ARG, "mdn_task_default_config: null argument");
+    if (!mdn::task_default_config(*out, stage, family, difficulty))
+        return fail(MDN_E_ARG, "unsupported task stage/family or difficulty outside [0, 1]");
+    return MDN_OK;
+}
+
+int mdn_domain_stress_range(MdnDomainRange* out) {
+    if (!out) return fail(MDN_E_ARG, "mdn_domain_stress_range: null argument");
+    *out = mdn::domain_stress_range();
+    return MDN_OK;
+}
+
+// Per-episode plants and navigation tasks: one tick per launch.  Per tick:
+// depth and observation (ending there), the geometry-memory hint if on, act
+// + advance + (task step) + reset, then the episode kernel for the envs that
+// were reset (sim.metal:328-331: the new episode's plant and task).
+int collect_episodic(MdnSim* s, uint32_t count, int slots) {
+    nav::RolloutArgs b = s->args(1);
+    const bool memory = s->shape.obs == MDN_ACTOR_OBS_PRIOR && s->cfg.geometry_memory;
+    if (memory) b.mem_head = s->mem_head;
+    nav::MemoryArgs m;
+    m.head = s->mem_head; m.sensors = s->sensors; m.poses = s->poses; m.pix_rays = s->pix_rays; m.cells = s->cells;
+    m.sensor_dt = b.sensor_dt; m.inv_sensor_dt = b.inv_sensor_dt; m.n = s->cfg.n;
+    const nav::EpisodeArgs e = s->episode_args(false);
+    int rc = MDN_OK;
+    for (uint32_t t = 0; t < count && rc == MDN_OK; t++) {
+        b.tick0 = t;
+        b.count = 1;
+        b.split = nav::SPLIT_END_AFTER_OBSERVE;
+        rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&b, 8, slots, s->shape.obs, s->stream); });
+        if (rc) break;
+        if (memory) {
+            m.obs = s->obs + size_t(t % s->horizon) * s->cfg.n * s->shape.obs;
+            rc = timed(s, MDN_K_MEMORY, [&] { return nav_launch_memory_hint(&m, s->stream); });
+            if (rc) break;
+        }
+        b.split = nav::SPLIT_BEGIN_AT_ACT;
+        rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&b, 8, slots, s->shape.obs, s->stream); });
+        if (rc) break;
+        rc = timed(s, MDN_K_EPISODE, [&] { return nav_launch_episode(&e, s->stream); });
+    }
+    return rc;
 }
 
 int mdn_sim_collect(MdnSim* s, uint32_t count) {
@@ -412,6 +511,10 @@ int mdn_sim_collect(MdnSim* s, uint32_t count) {
     const int lanes = int(s->lanes), slots = ring_slots(s->cfg);
     if (s->shape.obs == MDN_ACTOR_OBS_PRIOR && lanes != 8)
         return fail(MDN_E_ARG, "the 184-input actor's rollout runs 8 lanes per env");
+    if (s->episodic()) {
+        if (lanes != 8) return fail(MDN_E_ARG, "per-episode plants and tasks run 8 lanes per env");
+        return collect_episodic(s, count, slots);
+    }
     if (s->shape.obs != MDN_ACTOR_OBS_PRIOR || !s->cfg.geometry_memory)
         return timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, lanes, slots, s->shape.obs, s->stream); });
     // Geometry-memory hint: split ticks.  Tick 0 up to its observation; then

@@ -53,6 +53,30 @@ struct RolloutArgs {
     // (MEM_HEAD_* words) and a separate kernel writes the hint inputs of the
     // tick's rows before the launch that acts on them.
     uint32_t* mem_head;
+    // Per-episode plants and navigation tasks (the rollout kernels built for
+    // them, one tick per launch): env_phys [N] are the plants the envs step
+    // with (sim.metal:287); with task_cfg set, task_states [N] take the
+    // task's step and its outcome replaces success, timeout and reward
+    // (sim.metal:307-315).
+    const MdnPhysicsParams* env_phys;
+    MdnTaskState* task_states;
+    const MdnTaskConfig* task_cfg;
+};
+// Per-episode work after a reset (rollout.hip episode_kernel): the
+// episode's plant and hover rpm (sim.metal:62-81) and its navigation task
+// (sim.metal:122-141), for every env (first) or the envs whose episode
+// restarted in the preceding launch (steps == 0).
+struct EpisodeArgs {
+    float* state;
+    uint32_t* run;
+    float* world;
+    MdnPhysicsParams* env_phys;
+    MdnTaskState* task_states;
+    MdnSimConfig cfg;
+    MdnPhysicsParams phys;
+    MdnRuntimeConfig runtime;
+    MdnTaskControl task;
+    uint32_t first;
 };
 // memory header words
 constexpr uint32_t MEM_HEAD_OBSERVED = 0;  // 1: observed this tick (else skip the env)
@@ -112,6 +136,7 @@ struct AdamArgs {
 
 extern "C" {
 hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream);
+hipError_t nav_launch_episode(const nav::EpisodeArgs* a, hipStream_t stream);
 hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, uint32_t actor_obs,
                               hipStream_t stream);
 hipError_t nav_launch_memory_hint(const nav::MemoryArgs* a, hipStream_t stream);

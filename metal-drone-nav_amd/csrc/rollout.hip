@@ -11,6 +11,7 @@
 // RK4 chain redundantly.  Every dot product keeps the reference's sequential
 // order, so results round exactly like the CPU oracle.
 #include "nav_device.h"
+#include "nav_episode.h"
 #include "kernel_args.h"
 
 namespace nav {
@@ -194,6 +195,73 @@ __global__ __launch_bounds__(64) void reset_kernel(RolloutArgs a) {
     for (uint32_t j = 0; j < 96; j++) a.poses[size_t(n) * 96 + j] = 0.0f;
 }
 
+// Per-episode work of the envs whose episode just began, one thread per env:
+// the episode's plant (sim.metal:62-69, with its hover rpm 70-81) and its
+// navigation task (sim.metal:122-141: world, start state, yaw, reference
+// point, desired velocity, initial distance, wind).  Runs after the reset
+// kernel (first: every env) and after each launch that may reset envs (an
+// env with steps == 0 was reset by it; an evaluation never restarts one).
+__global__ __launch_bounds__(64) void episode_kernel(EpisodeArgs a) {
+    const uint32_t n = blockIdx.x * 64 + threadIdx.x;
+    const uint32_t N = a.cfg.n;
+    if (n >= N) return;
+    Run r;
+    load_run(a.run, N, n, r);
+    if (!a.first && r.steps != 0u) return;
+    State s;
+    load_state(a.state, N, n, s);
+    MdnPhysicsParams ep = a.phys;
+    if (a.runtime.enabled != 0u && a.runtime.domain_amplitude > 0.0f) {
+        const uint32_t rng = dom_seed(a.runtime, a.cfg.seed, n, a.first ? 0u : r.episodes);
+        MdnPhysicsParams varied;
+        if (dom_sample(a.phys, rng, a.runtime.domain_amplitude, a.runtime.domain_range, varied)) ep = varied;
+        else ep.mass = nan_f();  // rejected draw: the host's validation reports it
+    }
+    a.env_phys[n] = ep;
+    if (a.runtime.enabled != 0u) {
+        const float target = ep.mass * 9.81f / 4;
+        for (int q = 0; q < 4; q++) {
+            const float c0 = ep.rotor_thrust_coefficients[3 * q], c1 = ep.rotor_thrust_coefficients[3 * q + 1],
+                        c2 = ep.rotor_thrust_coefficients[3 * q + 2];
+            const float disc = c1 * c1 - 4 * c2 * (c0 - target);
+            s.rpm[q] = disc >= 0.0f ? clamp_f((-c1 + sqrt_f(disc)) / (2 * c2), ep.action_min, ep.action_max)
+                                    : ep.action_max;
+        }
+    }
+    MdnTaskState t;
+    uint32_t* tw = reinterpret_cast<uint32_t*>(&t);
+    for (uint32_t i = 0; i < sizeof(MdnTaskState) / 4; i++) tw[i] = 0u;
+    float* world = a.world + size_t(n) * WORLD_WORDS;
+    if (a.task.enabled != 0u) {
+        uint32_t rng = a.cfg.seed ^ ((n + 1u) * 0x27d4eb2du) ^ ((r.episodes + 1u) * 0x165667b1u);
+        task_generate(world, t, rng, a.task.config);
+        if (t.valid != 0u) {
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                s.p[k] = t.start_position[k];
+                s.v[k] = t.start_velocity_world[k];
+                s.w[k] = 0.0f;
+            }
+            float sh, ch;
+            sincos_f(t.start_yaw_rad * 0.5f, &sh, &ch);
+            s.q[0] = ch; s.q[1] = 0.0f; s.q[2] = 0.0f; s.q[3] = sh;
+            r.yaw = t.start_yaw_rad;
+            r.initial_distance = t.initial_distance_m;
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                r.ref_pos[k] = s.p[k];
+                r.desired_vel[k] = s.v[k];
+            }
+            world[166] = clean_env(a.cfg, n) ? 0.0f : a.cfg.wind;
+            world[167] = 0.0f;
+            world[168] = 0.0f;
+        }
+    }
+    a.task_states[n] = t;
+    store_state(a.state, N, n, s, 0, 1);
+    store_run(a.run, N, n, r, 0, 1);
+}
+
 // ---------------------------------------------------------------- matrix-core layer
 // One hidden layer for 32 envs on the fp32 matrix cores: out[env][unit] =
 // tanh(b1[unit] + sum_k x[env][k] * w1t[k][unit]).  v_mfma_f32_16x16x4_f32
@@ -370,7 +438,9 @@ struct WeightLds<1, D> {};
 // from a.ext_means (a policy evaluated by other kernels between launches);
 // values and next values are the caller's.  D: actor inputs, 181 (pooled
 // observation) or 184 (with the geometry-prior hint, ppo.hpp:30-34).
-template <int G, int K, int W, bool X, uint32_t D>
+// DYN: per-episode plants (a.env_phys) and navigation tasks (a.task_cfg);
+// launched one tick at a time around the episode kernel.
+template <int G, int K, int W, bool X, uint32_t D, bool DYN>
 __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     constexpr int E = 64 * W / G;    // envs per workgroup
     constexpr int U = 16 / G;        // RAPTOR units per lane
@@ -391,7 +461,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     constexpr uint32_t OS = D % 2 ? D + 4 : D + 3;  // odd stride of the observation rows
     // split ticks: the wide actor's loop and the 184-input actor's geometry
     // memory; the fused 181-input kernels keep the plain tick loop
-    constexpr bool SPLIT = X || D == MDN_ACTOR_OBS_PRIOR;
+    constexpr bool SPLIT = X || D == MDN_ACTOR_OBS_PRIOR || DYN;
     constexpr uint32_t WSTR = WORLD_WORDS;  // odd: env rows start in distinct banks
     __shared__ WeightLds<W, D> s_wt;
     const float* AW1;   // actor W1 transposed [input][hidden]
@@ -464,6 +534,16 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     const uint32_t c_b1 = HID * COBS, c_w2 = c_b1 + HID, c_b2 = c_w2 + HID;
     const uint32_t sdelay = clean_env(C, nn) ? 0 : C.sensor_delay;
     const uint32_t cdelay = clean_env(C, nn) ? 0 : C.command_delay;
+    // the env's plant for this launch (it changes only at resets, and a
+    // reset ends the launch): a row in LDS and its fp64 reciprocals
+    constexpr uint32_t PW = sizeof(MdnPhysicsParams) / 4;
+    __shared__ float s_ep[DYN ? E : 1][DYN ? PW : 1];
+    __shared__ PhysRecip s_erp[DYN ? E : 1];
+    if constexpr (DYN) {
+        const float* src = reinterpret_cast<const float*>(a.env_phys + nn);
+        for (uint32_t i = lane; i < PW; i += G) s_ep[grp][i] = src[i];
+        if (lane == 0) s_erp[grp] = phys_recip(a.env_phys[nn]);
+    }
     group_sync();
 
     for (uint32_t t = 0; t < a.count; t++) {
@@ -785,7 +865,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         sincos_f(r.yaw * 0.5f, &sh, &ch);
         bool collision = false, done = !active;
         float step_clearance = 12.0f;
-        const float wind[3] = {world[166] * P.mass, world[167] * P.mass, world[168] * P.mass};
+        const MdnPhysicsParams& EP = DYN ? *reinterpret_cast<const MdnPhysicsParams*>(&s_ep[grp][0]) : P;
+        const float wind[3] = {world[166] * EP.mass, world[167] * EP.mass, world[168] * EP.mass};
         for (uint32_t step = 0; step < C.substeps; step++) {
             float mo[22] = {0};
             if (!done) {
@@ -815,7 +896,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) r.motors[q] = act[q];
                 State nx;
-                physics_step(P, RP, s, act, wind, nx);
+                if constexpr (DYN) physics_step(EP, s_erp[grp], s, act, wind, nx);
+                else physics_step(P, RP, s, act, wind, nx);
                 bool valid = true;
                 const float* nf = &nx.p[0];
 #pragma unroll
@@ -846,14 +928,25 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             r.steps++;
             const float dx = gx - s.p[0], dy = gy - s.p[1], dz = gz - s.p[2];
             const float after = sqrt_f(dx * dx + dy * dy + dz * dz);
-            const bool success = after < (C.mode == 20 ? .10f : .35f) && !collision;
-            const bool timeout = r.steps >= C.max_steps;
+            bool success = after < (C.mode == 20 ? .10f : .35f) && !collision;
+            bool timeout = r.steps >= C.max_steps;
+            float reward = (before - after) * 2.0f - .01f -
+                           C.risk_coef * clamp_f((0.6f - step_clearance) / 0.6f, 0.0f, 1.0f) +
+                           (success ? 10.0f : 0.0f) - (collision ? 10.0f : 0.0f);
+            if constexpr (DYN) {
+                if (a.task_cfg) {  // sim.metal:307-315
+                    const float executed[4] = {r.desired_vel[0], r.desired_vel[1], r.desired_vel[2], r.prev_nav[3] * 0.5f};
+                    const TaskOutcome o = task_step(a.task_states + nn, *a.task_cfg, s.p, s.v, executed, collision,
+                                                    timeout, lane == 0);
+                    success = o.stable_success && !collision;
+                    timeout = o.timeout;
+                    reward = o.reward;
+                }
+            }
             const bool term = collision || success;
             const bool trunc = timeout && !term;
             if (lane == 0) {
-                a.rewards[row] = (before - after) * 2.0f - .01f -
-                                 C.risk_coef * clamp_f((0.6f - step_clearance) / 0.6f, 0.0f, 1.0f) +
-                                 (success ? 10.0f : 0.0f) - (collision ? 10.0f : 0.0f);
+                a.rewards[row] = reward;
                 a.terminated[row] = term ? 1 : 0;
                 a.truncated[row] = trunc ? 1 : 0;
             }
@@ -981,6 +1074,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 // ---------------------------------------------------------------- launchers
 extern "C" {
 
+hipError_t nav_launch_episode(const nav::EpisodeArgs* a, hipStream_t stream) {
+    if (a->cfg.n == 0) return hipSuccess;
+    hipLaunchKernelGGL(nav::episode_kernel, dim3((a->cfg.n + 63) / 64), dim3(64), 0, stream, *a);
+    return hipGetLastError();
+}
+
 hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream) {
     const uint32_t blocks = (a->cfg.n + 63) / 64;
     hipLaunchKernelGGL(nav::reset_kernel, dim3(blocks), dim3(64), 0, stream, *a);
@@ -997,13 +1096,16 @@ hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream) {
 // per env only.
 hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, uint32_t actor_obs,
                               hipStream_t stream) {
-#define NAV_ROLLOUT_CASE(G, K, W, X, D)                                                                        \
-    if (lanes_per_env == G && ring_slots == K && (a->ext_means != nullptr) == X && actor_obs == D) {           \
-        const uint32_t envs_per_block = 64 * W / G;                                                            \
-        const uint32_t blocks = (a->cfg.n + envs_per_block - 1) / envs_per_block;                              \
-        hipLaunchKernelGGL((nav::rollout_kernel<G, K, W, X, D>), dim3(blocks), dim3(64 * W), 0, stream, *a);   \
-        return hipGetLastError();                                                                              \
+    const bool dyn = a->env_phys != nullptr;
+#define NAV_ROLLOUT_CASE_DYN(G, K, W, X, D, DYN)                                                                \
+    if (lanes_per_env == G && ring_slots == K && (a->ext_means != nullptr) == X && actor_obs == D &&            \
+        dyn == DYN) {                                                                                           \
+        const uint32_t envs_per_block = 64 * W / G;                                                             \
+        const uint32_t blocks = (a->cfg.n + envs_per_block - 1) / envs_per_block;                               \
+        hipLaunchKernelGGL((nav::rollout_kernel<G, K, W, X, D, DYN>), dim3(blocks), dim3(64 * W), 0, stream, *a); \
+        return hipGetLastError();                                                                               \
     }
+#define NAV_ROLLOUT_CASE(G, K, W, X, D) NAV_ROLLOUT_CASE_DYN(G, K, W, X, D, false)
     constexpr uint32_t P = MDN_ACTOR_OBS_POOLED, H = MDN_ACTOR_OBS_PRIOR;
     NAV_ROLLOUT_CASE(8, 2, 4, false, P) NAV_ROLLOUT_CASE(8, 4, 1, false, P) NAV_ROLLOUT_CASE(8, 8, 1, false, P)
     NAV_ROLLOUT_CASE(16, 2, 1, false, P) NAV_ROLLOUT_CASE(16, 4, 1, false, P) NAV_ROLLOUT_CASE(16, 8, 1, false, P)
@@ -1011,7 +1113,14 @@ hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int 
     NAV_ROLLOUT_CASE(8, 2, 4, true, P) NAV_ROLLOUT_CASE(8, 4, 1, true, P) NAV_ROLLOUT_CASE(8, 8, 1, true, P)
     NAV_ROLLOUT_CASE(8, 2, 4, false, H) NAV_ROLLOUT_CASE(8, 4, 1, false, H) NAV_ROLLOUT_CASE(8, 8, 1, false, H)
     NAV_ROLLOUT_CASE(8, 2, 4, true, H) NAV_ROLLOUT_CASE(8, 4, 1, true, H) NAV_ROLLOUT_CASE(8, 8, 1, true, H)
+    // per-episode plants and navigation tasks: 8 lanes, the in-kernel policy,
+    // one wavefront per workgroup (the per-env plant rows do not fit beside
+    // the LDS-resident weights)
+    NAV_ROLLOUT_CASE_DYN(8, 2, 1, false, P, true) NAV_ROLLOUT_CASE_DYN(8, 4, 1, false, P, true)
+    NAV_ROLLOUT_CASE_DYN(8, 8, 1, false, P, true) NAV_ROLLOUT_CASE_DYN(8, 2, 1, false, H, true)
+    NAV_ROLLOUT_CASE_DYN(8, 4, 1, false, H, true) NAV_ROLLOUT_CASE_DYN(8, 8, 1, false, H, true)
 #undef NAV_ROLLOUT_CASE
+#undef NAV_ROLLOUT_CASE_DYN
     return hipErrorInvalidValue;
 }
 

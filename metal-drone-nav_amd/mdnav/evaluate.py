@@ -6,6 +6,7 @@ memory on for memory = 1 or any mode from 13; the actor parameters replace the
 simulator's.  Returns the reference's EvalScore (success, collision and
 timeout fractions, mean goal time of the successes; 1e9 without one) and the
 Sim::report line of the run."""
+import ctypes
 import time
 
 import numpy as np
@@ -54,6 +55,94 @@ def sim_evaluate(family, mode, actor=None, speed=1.0, distance=3.0, seed=700001,
                  goal_time=float(r["success_time"].astype(np.float64).sum()) / success if success else 1e9)
     sim.close()
     return score, dict(report, gpu_s=gpu)
+
+
+# ---------------------------------------------------------------- navigation tasks
+TASK_DOMAIN_SEED = abi.TASK_DOMAIN_SEED
+
+
+def task_settings(stage, family, generation_version=1):
+    """task_settings (navigation_training.hpp:7-14): the stage's default task
+    (navigation_task_default_config, difficulty 0.5) with the training's time
+    cost, smoothness weight and initial-speed cap."""
+    from .native import check, lib
+    t = np.zeros((), abi.TASK_CONTROL)
+    cfg = np.zeros((), abi.TASK_CONFIG)
+    check(lib().mdn_task_default_config(stage, family, F32(0.5), cfg.ctypes.data_as(ctypes.c_void_p)))
+    t["enabled"] = 1
+    t["config"] = cfg
+    t["config"]["time_cost_per_s"] = 0.2
+    t["config"]["command_smoothness_weight"] = 0.05
+    t["config"]["initial_speed_max_mps"] = 0.5 if stage == 1 else 1.0
+    t["config"]["generation_version"] = generation_version
+    return t
+
+
+def task_runtime(amplitude):
+    """NavigationRuntimeConfig of navigation_training::configure
+    (navigation_training.hpp:20-22): enabled, the stress range, seed 0x3f84d5b5."""
+    from .native import check, lib
+    if not (np.isfinite(amplitude) and 0.0 <= amplitude <= 1.0):
+        raise ValueError("domain amplitude must be 0..1")
+    r = np.zeros((), abi.RUNTIME_CONFIG)
+    rng = np.zeros((), abi.DOMAIN_RANGE)
+    check(lib().mdn_domain_stress_range(rng.ctypes.data_as(ctypes.c_void_p)))
+    r["enabled"] = 1
+    r["domain_amplitude"] = amplitude
+    r["domain_seed"] = TASK_DOMAIN_SEED
+    r["domain_range"] = rng
+    return r
+
+
+def task_evaluate(actor, stage, family, amplitude, seed=800001, mode=17, generation_version=1, raptor=None,
+                  physics=None):
+    """navigation_training::evaluate (navigation_training.hpp:68-117): 128
+    goal-conditioned tasks of one stage and family with per-episode plants,
+    one episode each over 400 ticks, geometry memory on.  Returns the score
+    (success, collision, timeout fractions, mean successful arrival time) and
+    per-env rows with the columns of the reference's task CSV."""
+    actor = np.ascontiguousarray(actor, np.float32).reshape(-1)
+    if actor.size != abi.policy_shape(obs=184)["actor_count"]:
+        raise ValueError("task evaluation takes the 184-input guided actor")
+    cfg = abi.default_config(n=128, eval=1, mode=mode, seed=seed, family=family, speed=1.5, distance=8.0,
+                             max_steps=400, geometry_memory=1)
+    settings = task_settings(stage, family, generation_version)
+    sim = Sim(cfg, 32, raptor=raptor, physics=physics, actor_obs=184)
+    try:
+        sim.set_runtime(task_runtime(amplitude))
+        sim.set_tasks(settings)
+        sim.reset()
+        sim.set("actor", actor)
+        initial = sim.get("task_states")
+        plants = sim.get("environment_physics")
+        if not np.all((initial["valid"] == 1) & (initial["generation_status"] == abi.TASK_READY)):
+            raise RuntimeError("task generation rejected an env")
+        if not np.all(np.isfinite(plants["mass"]) & (plants["mass"] > 0)):
+            raise RuntimeError("episode dynamics sample rejected")
+        sim.collect(400)
+        sim.sync()
+        runs, states, final = sim.get("runs"), sim.get("states"), sim.get("task_states")
+    finally:
+        sim.close()
+    if not np.all(runs["episodes"] == 1):
+        raise RuntimeError("evaluation must complete exactly one task per environment")
+    d = initial["goal_position"] - states["position"]
+    error = np.sqrt(((d.astype(np.float32)) ** 2).sum(axis=1, dtype=np.float32))
+    speed = np.sqrt((states["linear_velocity"] ** 2).sum(axis=1, dtype=np.float32))
+    rows = dict(family=initial["family"], start=initial["start_position"], start_yaw=initial["start_yaw_rad"],
+                initial_velocity=initial["start_velocity_world"], goal=initial["goal_position"],
+                initial_distance=initial["initial_distance_m"],
+                direct_clearance=initial["direct_segment_clearance_m"], witness_length=initial["witness_length_m"],
+                mass=plants["mass"], success=runs["successes"], collision=runs["collisions"],
+                timeout=runs["timeouts"], time=runs["elapsed"], path=runs["path"], goal_error=error,
+                final_speed=speed, hold=final["stable_time_s"], peak_speed=runs["peak_speed"],
+                min_clearance=runs["min_clearance"])
+    n = float(len(runs))
+    successes = float(runs["successes"].sum())
+    score = dict(success=successes / n, collision=float(runs["collisions"].sum()) / n,
+                 timeout=float(runs["timeouts"].sum()) / n,
+                 arrival_time=float(runs["success_time"].astype(np.float64).sum()) / successes if successes else 0.0)
+    return score, rows
 
 
 # ---------------------------------------------------------------- controlled threats

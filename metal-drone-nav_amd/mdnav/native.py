@@ -24,13 +24,14 @@ EXPORTS = [
     "mdn_lppo_rollout_update", "mdn_lppo_param_count", "mdn_lppo_get_params", "mdn_lppo_set_params",
     "mdn_lppo_metric_mean", "mdn_lppo_optimizer_step", "mdn_lppo_collect", "mdn_lppo_means",
     "mdn_op_check_division", "mdn_ppo_save_checkpoint", "mdn_ppo_load_checkpoint", "mdn_checkpoint_read",
-    "mdn_navpol_read", "mdn_navpol_write", "mdn_fnv1a64_file",
+    "mdn_navpol_read", "mdn_navpol_write", "mdn_fnv1a64_file", "mdn_sim_set_runtime", "mdn_sim_get_runtime",
+    "mdn_sim_set_tasks", "mdn_sim_get_tasks", "mdn_task_default_config", "mdn_domain_stress_range",
 ]
 
 P = ctypes.c_void_p
 U32, U64, F32, I32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float, ctypes.c_int
 KERNELS = {"rollout": 0, "gae": 1, "normalize": 2, "rows": 3, "grads": 4, "adam": 5, "lp_forward": 6,
-           "lp_backward": 7, "lp_adam": 8, "memory": 9}
+           "lp_backward": 7, "lp_adam": 8, "memory": 9, "episode": 10}
 
 _lib = None
 
@@ -75,6 +76,12 @@ def lib():
         _sig(L, "mdn_navpol_write", I32, ctypes.c_char_p, P, P, U64, U64)
         _sig(L, "mdn_fnv1a64_file", I32, ctypes.c_char_p, ctypes.POINTER(U64))
         _sig(L, "mdn_sim_get_actor_obs", I32, P, ctypes.POINTER(U32))
+        _sig(L, "mdn_sim_set_runtime", I32, P, P)
+        _sig(L, "mdn_sim_get_runtime", I32, P, P)
+        _sig(L, "mdn_sim_set_tasks", I32, P, P)
+        _sig(L, "mdn_sim_get_tasks", I32, P, P)
+        _sig(L, "mdn_task_default_config", I32, U32, U32, F32, P)
+        _sig(L, "mdn_domain_stress_range", I32, P)
         _sig(L, "mdn_ppo_create", I32, P, U32, U32, ctypes.POINTER(P))
         _sig(L, "mdn_ppo_destroy", None, P)
         _sig(L, "mdn_ppo_rollout_update", I32, P, U32)

@@ -106,6 +106,18 @@ class Sim:
         check(lib().mdn_sim_get_actor_obs(self.h, ctypes.byref(d)))
         return d.value
 
+    def set_runtime(self, runtime):
+        """Episode dynamics variation (NavigationRuntimeConfig,
+        navigation_runtime.hpp:9-14); takes effect at the next reset."""
+        r = np.array(runtime, abi.RUNTIME_CONFIG)
+        check(lib().mdn_sim_set_runtime(self.h, r.ctypes.data_as(ctypes.c_void_p)))
+
+    def set_tasks(self, tasks):
+        """Goal-conditioned navigation tasks (NavigationTaskControl,
+        navigation_tasks.hpp:93-95); take effect at the next reset."""
+        t = np.array(tasks, abi.TASK_CONTROL)
+        check(lib().mdn_sim_set_tasks(self.h, t.ctypes.data_as(ctypes.c_void_p)))
+
     def reset(self):
         check(lib().mdn_sim_reset(self.h))
         return self.sync()

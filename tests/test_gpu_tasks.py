@@ -1,0 +1,151 @@
+"""Per-episode plants and goal-conditioned navigation tasks on the GPU
+path: the episodic rollout (one tick per launch around the episode kernel)
+bit-exact against the oracle's trainer, and the reference's 16 published
+goal-arrival task evaluations (evidence/inputs/arrival-training, copied to
+tests/golden/arrival) reproduced end to end with its two trained policies."""
+import csv
+import glob
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from gpu_compare import ENV_BUFFERS, ROW_BUFFERS, compare, config, make_pair
+from mdnav import abi, formats, task_evaluate, task_runtime, task_settings
+from oracle_lib import GOLDEN, raptor_fixture
+
+pytestmark = pytest.mark.gpu
+TASK_BUFFERS = ["environment_physics", "task_states"]
+
+
+def say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+CASES = {
+    # clutter tasks (family 12 mixes four static families), per-episode
+    # plants, the guided actor with the geometry memory, short task limit so
+    # that episodes restart inside the window
+    "clutter_mix_memory": dict(stage=2, family=12, amp=1.0, obs=184, memory=1, steps=12, delay=0),
+    # near-goal hold with a 2-frame sensor delay, the pooled actor
+    "near_hold_delay_181": dict(stage=1, family=0, amp=0.5, obs=181, memory=0, steps=10, delay=2),
+    # plants only (no tasks) in doorway worlds, in-kernel hint
+    "plants_only_184": dict(stage=None, family=4, amp=1.0, obs=184, memory=0, steps=0, delay=0),
+    # tasks only (nominal plant), open goals, generator version 0
+    "open_goal_v0": dict(stage=0, family=0, amp=None, obs=184, memory=1, steps=15, delay=0, version=0),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_episodic_rollout_bit_exact(name):
+    c = CASES[name]
+    say("case: episodic rollout", name, c)
+    cfg = config(n=96, family=c["family"], seed=321, max_steps=30, sensor_delay=c["delay"],
+                 geometry_memory=c["memory"], speed=1.5, distance=8.0)
+    sim, ppo, ora = make_pair(cfg, 16, actor_obs=c["obs"])
+    if c["amp"] is not None:
+        rt = task_runtime(c["amp"])
+        sim.set_runtime(rt)
+        ora.set_runtime(rt)
+    if c["stage"] is not None:
+        t = task_settings(c["stage"], c["family"], c.get("version", 1))
+        t["config"]["max_nav_steps"] = c["steps"]
+        sim.set_tasks(t)
+        ora.set_tasks(t)
+    # the same fresh policy on both sides
+    ora.set("actor", sim.get("actor"))
+    ora.set("critic", sim.get("critic"))
+    sim.reset()
+    ora.reset()
+    bad = compare(sim, ora, ENV_BUFFERS + TASK_BUFFERS)
+    assert not bad, bad
+    resets = 0
+    for k in range(3):
+        sim.collect(16)
+        sim.sync()
+        ora.collect(16)
+        bad = compare(sim, ora, ENV_BUFFERS + TASK_BUFFERS + ROW_BUFFERS)
+        say("  collect %d: episodes %d, mismatches %s" % (k, int(sim.get("runs")["episodes"].sum()), bad))
+        assert not bad, (k, bad)
+        resets = int(sim.get("runs")["episodes"].sum())
+    assert resets > 20  # the episode kernel ran after in-rollout resets
+    if c["amp"]:
+        m = sim.get("environment_physics")["mass"]
+        assert np.unique(m).size > 50  # per-env plants
+
+
+def _fmt(x):
+    return "%.6g" % float(x)
+
+
+def _published():
+    out = []
+    for path in sorted(glob.glob(os.path.join(GOLDEN, "arrival", "*.csv"))):
+        base = os.path.basename(path)
+        if base in ("evaluations.csv", "retention.csv"):
+            continue
+        out.append((base, list(csv.DictReader(open(path)))))
+    return out
+
+
+def _actor(policy):
+    if policy == "original":
+        return formats.read_navigation_policy(os.path.join(GOLDEN, "navigation.bin"))[1]
+    return np.load(os.path.join(GOLDEN, "actors", "arrival.npz"))["actor"]
+
+
+def _policy_of(name):
+    # arrival-<policy>-holdout-*.csv; the dev files are the warm-start
+    # (initial) and the selected arrival policy (manifest)
+    if name.startswith("arrival-"):
+        return name.split("-")[1]
+    return "original" if name == "initial-dev.csv" else "arrival"
+
+
+@pytest.mark.parametrize("name,rows", _published(), ids=lambda v: v if isinstance(v, str) else "")
+def test_published_task_evaluations(name, rows):
+    """Each published evaluation: 128 generated tasks (stage, family,
+    per-episode plants at amplitude 0 or 1, seed 820001 holdout / 800001
+    dev), mode 17 with the geometry memory, 400 ticks.  The task set-ups match
+    the published columns to the printed digits; the outcomes (stable
+    arrival, collision, timeout) are the reference's env by env (at most one
+    long episode per evaluation diverges)."""
+    r0 = rows[0]
+    stage, family, amp, seed = int(r0["stage"]), int(r0["family"]), float(r0["domain_amplitude"]), int(r0["seed"])
+    policy = _policy_of(name)
+    say("case: task evaluation %s policy=%s stage=%d family=%d amp=%g seed=%d" % (name, policy, stage, family, amp,
+                                                                                     seed))
+    score, got = task_evaluate(_actor(policy), stage, family, amp, seed=seed, mode=int(r0["mode"]),
+                               generation_version=0, raptor=raptor_fixture()[0])
+    want = {k: sum(int(r[k]) for r in rows) for k in ("success", "collision", "timeout")}
+    have = {k: int(got[k].sum()) for k in ("success", "collision", "timeout")}
+    agree = sum(int(got["success"][i]) == int(r["success"]) and int(got["collision"][i]) == int(r["collision"])
+                for i, r in enumerate(rows))
+    times = [(float(got["time"][i]), float(r["time_s"])) for i, r in enumerate(rows) if int(r["success"])]
+    say("  counts %s / published %s; per-env outcome agreement %d/128" % (have, want, agree))
+    loose = 0
+    for i, r in enumerate(rows):
+        for col, v in (("start_x", got["start"][i][0]), ("goal_y", got["goal"][i][1]), ("mass_kg", got["mass"][i]),
+                       ("initial_distance_m", got["initial_distance"][i])):
+            if _fmt(v) != r[col]:
+                w = float(r[col])
+                unit = 10.0 ** (math.floor(math.log10(abs(w))) - 5) if w else 1e-6
+                assert abs(float(v) - w) <= 2.5 * unit + 1e-6, (i, col, float(v), r[col])
+                loose += 1
+    assert loose <= 0.02 * 4 * 128
+    for i, r in enumerate(rows):
+        if int(got["success"][i]) != int(r["success"]) or int(got["collision"][i]) != int(r["collision"]):
+            say("  env %d differs: published s/c/t %s/%s/%s at %s s, here %d/%d/%d at %.6g s" % (
+                i, r["success"], r["collision"], r["timeout"], r["time_s"], got["success"][i], got["collision"][i],
+                got["timeout"][i], got["time"][i]))
+    same_tick = sum(abs(a - b) < 1e-3 for a, b in times)
+    say("  successful arrival times equal to the printed digits: %d/%d" % (same_tick, len(times)))
+    # Every published outcome is reproduced env by env, except where one
+    # long episode (an env still flying near an obstacle after many seconds)
+    # diverges through last-bit differences of the Metal build's arithmetic:
+    # at most one env per evaluation, one count moved by one.
+    assert agree >= 127, agree
+    assert all(abs(have[k] - want[k]) <= 1 for k in have), (have, want)
