@@ -46,6 +46,10 @@ public:
     void reset() { require(mdn_sim_reset(handle_)); }
     // The guided build's FIXED_PPO_ACTOR_OBS_DIM = 184 (ppo.hpp:11-34), chosen at run time.
     void set_actor_obs(uint32_t d) { require(mdn_sim_set_actor_obs(handle_, d)); }
+    // Sim::runtime_control / task_control (main.mm:523-537): per-episode
+    // plants and navigation tasks, effective at the next reset().
+    void set_runtime(const MdnRuntimeConfig& r) { require(mdn_sim_set_runtime(handle_, &r)); }
+    void set_tasks(const MdnTaskControl& t) { require(mdn_sim_set_tasks(handle_, &t)); }
     // Sim::collect(cmdbuf, count): enqueue; finish() waits like Metal::finish.
     void collect(uint32_t count = 0) { require(mdn_sim_collect(handle_, count)); }
     double finish() {
@@ -162,6 +166,30 @@ public:
     Sim sim;
     PPOTrainer ppo;
 };
+
+// navigation_training::task_settings and configure (navigation_training.hpp:7-24):
+// the stage's default task with the training's costs, and the runtime with
+// the stress range and seed 0x3f84d5b5, installed before a reset.
+inline MdnTaskControl task_settings(uint32_t stage, uint32_t family) {
+    MdnTaskControl t{};
+    t.enabled = 1;
+    require(mdn_task_default_config(stage, family, .5f, &t.config));
+    t.config.time_cost_per_s = .2f;
+    t.config.command_smoothness_weight = .05f;
+    t.config.initial_speed_max_mps = stage == 1 ? .5f : 1.0f;
+    return t;
+}
+inline void configure(Sim& sim, const MdnTaskControl& tasks, float amplitude) {
+    if (!(amplitude >= 0.0f && amplitude <= 1.0f)) throw std::runtime_error("domain amplitude must be 0..1");
+    MdnRuntimeConfig r{};
+    r.enabled = 1;
+    r.domain_amplitude = amplitude;
+    r.domain_seed = 0x3f84d5b5u;
+    require(mdn_domain_stress_range(&r.domain_range));
+    sim.set_runtime(r);
+    sim.set_tasks(tasks);
+    sim.reset();
+}
 
 }  // namespace mdnav
 

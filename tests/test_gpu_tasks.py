@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from gpu_compare import ENV_BUFFERS, ROW_BUFFERS, compare, config, make_pair
-from mdnav import abi, formats, task_evaluate, task_runtime, task_settings
+from mdnav import abi, formats, sim_evaluate, task_evaluate, task_runtime, task_settings
 from oracle_lib import GOLDEN, raptor_fixture
 
 pytestmark = pytest.mark.gpu
@@ -149,3 +149,24 @@ def test_published_task_evaluations(name, rows):
     # at most one env per evaluation, one count moved by one.
     assert agree >= 127, agree
     assert all(abs(have[k] - want[k]) <= 1 for k in have), (have, want)
+
+
+def _retention():
+    return list(csv.DictReader(open(os.path.join(GOLDEN, "arrival", "retention.csv"))))
+
+
+@pytest.mark.parametrize("row", _retention(), ids=lambda r: "%s-family%s" % (r["policy"], r["family"]))
+def test_published_retention_evaluations(row):
+    """The retention check of the same evidence: eval-policy (main.mm:1103-1108,
+    first goal-region entry, 10 s budget, 1.5 m/s, 4 m goals, seed 800001,
+    mode 17 with the geometry memory) of both policies on seven scene
+    families.  Outcome counts exact; mean goal time to the printed digits."""
+    say("case: retention %s family %s" % (row["policy"], row["family"]))
+    score, rep = sim_evaluate(int(row["family"]), 17, _actor(row["policy"]), speed=float(row["speed_cap_mps"]),
+                              distance=4.0, seed=int(row["seed"]), memory=1, raptor=raptor_fixture()[0])
+    say("  success %.6g/%s collision %.6g/%s goal %.6g/%s" % (score["success"], row["success"], score["collision"],
+                                                              row["collision"], score["goal_time"],
+                                                              row["mean_goal_time_s"]))
+    for k in ("success", "collision", "timeout"):
+        assert round(score[k] * 128) == round(float(row[k]) * 128), (k, score[k], row[k])
+    assert abs(score["goal_time"] - float(row["mean_goal_time_s"])) <= 0.02, score
