@@ -173,18 +173,23 @@ int mdn_ppo_optimizer_step(const MdnPPO* ppo, uint64_t* step);
 int mdn_ppo_updates_per_rollout(const MdnPPO* ppo, uint32_t* updates);
 
 /* On-disk formats.
- * PPOTrainer::save_checkpoint (main.mm:1285-1317): PPOFIX1 version 6 (this
- * build has no dynamics, task or shaping blocks and the legacy camera):
- * header, actor, critic, their Adam moments, then the simulator's states,
- * runs, worlds, sensor, pose and command rings, in the reference's layouts.
- * Written to path.tmp and renamed. */
+ * PPOTrainer::save_checkpoint (main.mm:1285-1317): PPOFIX1 version 6 (no
+ * shaping block, the legacy camera): header, actor, critic, their Adam
+ * moments, then the simulator's states, runs, worlds, sensor, pose and
+ * command rings, in the reference's layouts; version 8 when per-episode
+ * plants or tasks are on, which appends the runtime and task configuration,
+ * every env's plant and task state, the nominal plant and the RAPTOR
+ * weights.  Written to path.tmp and renamed. */
 int mdn_ppo_save_checkpoint(MdnPPO* ppo, const char* path, uint32_t family, uint32_t seed,
                             uint32_t completed_rollouts);
 /* PPOTrainer::load_checkpoint (main.mm:1218-1284) with read_checkpoint_header
- * (main.mm:986-994): versions 3-6 (7-10 return MDN_E_ARG).  A missing file
+ * (main.mm:986-994): versions 3-8 (9-10 return MDN_E_ARG).  A missing file
  * is a fresh start (MDN_OK, *completed_rollouts = 0), as in the reference.
  * The family, horizon, env count and seed must match the arguments and the
- * run settings the simulator's; the simulator takes the file's config. */
+ * run settings the simulator's; versions 7-8 also their runtime and task
+ * configuration, nominal plant and RAPTOR weights (set them first), and a
+ * version 7 file resumes only without tasks; the simulator takes the file's
+ * config. */
 int mdn_ppo_load_checkpoint(MdnPPO* ppo, const char* path, uint32_t family, uint32_t horizon, uint32_t n,
                             uint32_t seed, uint32_t* completed_rollouts);
 /* A checkpoint's header and, if `actor` is given, its actor parameters (the

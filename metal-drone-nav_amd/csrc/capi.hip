@@ -1331,9 +1331,9 @@ int mdn_ppo_load_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
     MdnCheckpointHeader h;
     int rc = read_checkpoint_header(file, &h);
     if (rc) return rc;
-    if (h.version >= 7)
-        return fail(MDN_E_ARG, "checkpoint versions 7-10 carry dynamics, task, shaping and camera blocks this "
-                               "build does not have; warm-start from the parameters instead");
+    if (h.version >= 9)
+        return fail(MDN_E_ARG, "checkpoint versions 9-10 carry shaping and camera blocks this build does not "
+                               "have; warm-start from the parameters instead");
     if (h.actor_count != s->shape.actor_count() || h.critic_count != s->shape.critic_count())
         return fail(MDN_E_ARG, "PPO checkpoint dimensions mismatch");
     if (h.family != family || h.horizon != horizon || h.n != n || h.base_seed != seed)
@@ -1350,10 +1350,48 @@ int mdn_ppo_load_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
         if (id == MDN_BUF_POSES && h.version < 6) continue;  // older files have no pose ring
         if (!file.read(body.back().data(), bytes)) return fail(MDN_E_ARG, "truncated PPO checkpoint");
     }
+    // versions 7-8 (main.mm:1237-1257): the runtime and task configuration
+    // (version 7 stored the 144-byte task control of its time and resumes
+    // only without tasks), every env's plant and task state, then the
+    // nominal plant and controller, all of which must equal this sim's
+    std::vector<unsigned char> env_phys, task_states;
+    if (h.version >= 7) {
+        MdnRuntimeConfig saved_runtime;
+        MdnTaskControl saved_tasks;
+        std::memset(&saved_runtime, 0, sizeof(saved_runtime));
+        std::memset(&saved_tasks, 0, sizeof(saved_tasks));
+        if (!file.read(&saved_runtime, sizeof(saved_runtime)) ||
+            !file.read(&saved_tasks, h.version >= 8 ? sizeof(saved_tasks) : 144))
+            return fail(MDN_E_ARG, "truncated navigation runtime configuration");
+        if (h.version < 8 && saved_tasks.enabled != 0)
+            return fail(MDN_E_ARG, "task-generator semantics changed; use an explicit parameter warmstart from "
+                                   "version 7");
+        if (std::memcmp(&saved_runtime, &s->runtime, sizeof(saved_runtime)) != 0 ||
+            std::memcmp(&saved_tasks, &s->task, sizeof(saved_tasks)) != 0)
+            return fail(MDN_E_ARG, "checkpoint dynamics/task configuration mismatch");
+        env_phys.resize(size_t(s->cfg.n) * sizeof(MdnPhysicsParams));
+        task_states.resize(size_t(s->cfg.n) * sizeof(MdnTaskState));
+        MdnPhysicsParams saved_nominal;
+        std::vector<float> saved_raptor(2084), raptor(2084);
+        if (!file.read(env_phys.data(), env_phys.size()) || !file.read(task_states.data(), task_states.size()) ||
+            !file.read(&saved_nominal, sizeof(saved_nominal)) || !file.read(saved_raptor.data(), 2084 * 4))
+            return fail(MDN_E_ARG, "truncated checkpoint nominal plant/controller");
+        HIP_TRY(hipMemcpy(raptor.data(), s->raptor, 2084 * 4, hipMemcpyDeviceToHost));
+        if (std::memcmp(&saved_nominal, &s->phys, sizeof(saved_nominal)) != 0 ||
+            std::memcmp(saved_raptor.data(), raptor.data(), 2084 * 4) != 0)
+            return fail(MDN_E_ARG, "checkpoint nominal plant/controller mismatch");
+    } else if (s->episodic()) {
+        return fail(MDN_E_ARG, "legacy resume cannot infer new dynamics/task state; use explicit parameter warmstart");
+    }
     if (!file.at_end()) return fail(MDN_E_ARG, "PPO checkpoint has trailing data");
     for (size_t i = 0; i < body.size(); i++) {
         rc = mdn_sim_upload(s, kCheckpointBuffers[i], body[i].data(), body[i].size());
         if (rc) return rc;
+    }
+    if (h.version >= 7) {
+        if ((rc = mdn_sim_upload(s, MDN_BUF_ENV_PHYSICS, env_phys.data(), env_phys.size())) != MDN_OK) return rc;
+        if ((rc = mdn_sim_upload(s, MDN_BUF_TASK_STATES, task_states.data(), task_states.size())) != MDN_OK)
+            return rc;
     }
     rc = mdn_sim_set_config(s, &h.config);
     if (rc) return rc;
@@ -1368,7 +1406,9 @@ int mdn_ppo_save_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
     MdnCheckpointHeader h;
     std::memset(&h, 0, sizeof(h));  // padding bytes too, so equal states give equal files
     std::memcpy(h.magic, "PPOFIX1", 7);
-    h.version = 6;  // no dynamics, task or shaping blocks; the legacy camera
+    // main.mm:1292: version 8 with the dynamics/task blocks when either is
+    // on, else 6 (no shaping; the legacy camera)
+    h.version = s->episodic() ? 8 : 6;
     h.actor_count = s->shape.actor_count();
     h.critic_count = s->shape.critic_count();
     h.horizon = s->horizon;
@@ -1392,6 +1432,18 @@ int mdn_ppo_save_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
             rc = mdn_sim_download(s, id, buf.data(), bytes);
             if (rc) return rc;
             ok = ok && file.write(buf.data(), bytes);
+        }
+        if (h.version >= 7) {  // main.mm:1303-1307
+            std::vector<unsigned char> env_phys(size_t(s->cfg.n) * sizeof(MdnPhysicsParams));
+            std::vector<unsigned char> task_states(size_t(s->cfg.n) * sizeof(MdnTaskState));
+            std::vector<float> raptor(2084);
+            int rc = mdn_sim_download(s, MDN_BUF_ENV_PHYSICS, env_phys.data(), env_phys.size());
+            if (!rc) rc = mdn_sim_download(s, MDN_BUF_TASK_STATES, task_states.data(), task_states.size());
+            if (rc) return rc;
+            HIP_TRY(hipMemcpy(raptor.data(), s->raptor, 2084 * 4, hipMemcpyDeviceToHost));
+            ok = ok && file.write(&s->runtime, sizeof(s->runtime)) && file.write(&s->task, sizeof(s->task)) &&
+                 file.write(env_phys.data(), env_phys.size()) && file.write(task_states.data(), task_states.size()) &&
+                 file.write(&s->phys, sizeof(s->phys)) && file.write(raptor.data(), 2084 * 4);
         }
         ok = ok && std::fflush(file.f) == 0;
         if (!ok) {

@@ -232,11 +232,12 @@ class PPOTrainer:
         return u.value
 
     def save_checkpoint(self, path, family, seed, completed_rollouts):
-        """PPOTrainer::save_checkpoint (main.mm:1285-1317): PPOFIX1 version 6."""
+        """PPOTrainer::save_checkpoint (main.mm:1285-1317): PPOFIX1 version 6, or 8
+        with the dynamics/task blocks when per-episode plants or tasks are on."""
         check(lib().mdn_ppo_save_checkpoint(self.h, str(path).encode(), family, seed, completed_rollouts))
 
     def load_checkpoint(self, path, family, horizon, n, seed):
-        """PPOTrainer::load_checkpoint (main.mm:1218-1284), versions 3-6.
+        """PPOTrainer::load_checkpoint (main.mm:1218-1284), versions 3-8.
         Returns the completed rollouts (0 when the file is absent)."""
         done = ctypes.c_uint32()
         check(lib().mdn_ppo_load_checkpoint(self.h, str(path).encode(), family, horizon, n, seed, ctypes.byref(done)))

@@ -299,13 +299,22 @@ class OracleTrainer:
         buffers: parsed here with numpy, independently of the library's reader."""
         data = np.fromfile(path, np.uint8)
         h = data[:136].view(abi.CHECKPOINT_HEADER)[0]
-        assert h["magic"] == b"PPOFIX1" and h["version"] == 6, (h["magic"], h["version"])
+        assert h["magic"] == b"PPOFIX1" and h["version"] in (6, 8), (h["magic"], h["version"])
         off = 136
         for name in ("actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v", "states", "runs", "worlds",
                      "sensors", "poses", "commands"):
             buf = self.buffer(name)
             buf.view(np.uint8)[...] = data[off:off + buf.nbytes]
             off += buf.nbytes
+        if h["version"] == 8:  # main.mm:1303-1307: runtime, tasks, plants, task states, nominal plant, RAPTOR
+            self.set_runtime(data[off:off + 56].view(abi.RUNTIME_CONFIG)[0])
+            self.set_tasks(data[off + 56:off + 204].view(abi.TASK_CONTROL)[0])
+            off += 204
+            for name in ("environment_physics", "task_states"):
+                buf = self.buffer(name)
+                buf.view(np.uint8)[...] = data[off:off + buf.nbytes]
+                off += buf.nbytes
+            off += abi.PHYSICS_PARAMS.itemsize + abi.RAPTOR_WEIGHTS.itemsize
         assert off == data.size
         self.set_config(h["config"])
         self.optimizer_step = int(h["optimizer_step"])

@@ -170,3 +170,41 @@ def test_published_retention_evaluations(row):
     for k in ("success", "collision", "timeout"):
         assert round(score[k] * 128) == round(float(row[k]) * 128), (k, score[k], row[k])
     assert abs(score["goal_time"] - float(row["mean_goal_time_s"])) <= 0.02, score
+
+
+def test_task_checkpoint_resume_bit_exact(tmp_path):
+    """PPOFIX1 version 8 (main.mm:1292-1307): train with tasks and per-episode
+    plants, save, resume into a fresh GPU trainer and into the oracle, and
+    continue: every buffer (plants and task states included) bit-identical;
+    a sim without the matching configuration refuses the file."""
+    from mdnav import PPOTrainer, Sim
+    say("case: task checkpoint v8 save/resume")
+    cfg = config(n=64, family=2, seed=99, max_steps=40, geometry_memory=1, speed=1.5, distance=8.0)
+    rt, tasks = task_runtime(1.0), task_settings(2, 2)
+    tasks["config"]["max_nav_steps"] = 14
+    sim, ppo, _ = make_pair(cfg, 16, epochs=1, minibatch=256, actor_obs=184)
+    sim.set_runtime(rt)
+    sim.set_tasks(tasks)
+    sim.reset()
+    for r in range(2):
+        sim.collect()
+        ppo.rollout_update(r)
+    path = str(tmp_path / "tasks.bin")
+    ppo.save_checkpoint(path, 2, 99, 2)
+    h, _ = formats.read_checkpoint(path)
+    assert int(h["version"]) == 8
+    sim2, ppo2, ora = make_pair(cfg, 16, epochs=1, minibatch=256, actor_obs=184)
+    sim2.set_runtime(rt)
+    sim2.set_tasks(tasks)
+    assert ppo2.load_checkpoint(path, 2, 16, 64, 99) == 2
+    ora.load_checkpoint(path)
+    names = ENV_BUFFERS + TASK_BUFFERS + ["actor", "critic"]
+    bad = compare(sim2, ora, names)
+    assert not bad, bad
+    sim2.collect()
+    ora.collect()
+    bad = compare(sim2, ora, names + ROW_BUFFERS)
+    assert not bad, bad
+    sim3, ppo3, _ = make_pair(cfg, 16, epochs=1, minibatch=256, actor_obs=184)
+    with pytest.raises(Exception):
+        ppo3.load_checkpoint(path, 2, 16, 64, 99)  # no tasks configured: mismatch
