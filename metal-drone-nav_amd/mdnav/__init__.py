@@ -12,7 +12,8 @@ from . import abi  # noqa: F401
 from .native import MdnError  # noqa: F401
 from .sim import LargePPOTrainer, PPOTrainer, Sim, Trainer, crazyflie_params, load_raptor  # noqa: F401
 from . import formats  # noqa: F401
-from .evaluate import evaluate_threat, sim_evaluate, task_evaluate, task_runtime, task_settings  # noqa: F401
+from .evaluate import (bank_evaluate, evaluate_threat, load_bank, sim_evaluate, task_evaluate, task_runtime,  # noqa: F401
+                       task_settings)
 
 __all__ = ["abi", "formats", "MdnError", "Sim", "PPOTrainer", "Trainer", "crazyflie_params", "load_raptor",
-           "sim_evaluate", "evaluate_threat", "task_evaluate", "task_runtime", "task_settings"]
+           "sim_evaluate", "evaluate_threat", "task_evaluate", "task_runtime", "task_settings", "load_bank", "bank_evaluate"]

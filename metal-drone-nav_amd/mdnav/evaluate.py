@@ -145,6 +145,112 @@ def task_evaluate(actor, stage, family, amplitude, seed=800001, mode=17, generat
     return score, rows
 
 
+# ---------------------------------------------------------------- challenge banks
+BANK_ENV_STRIDE, BANK_ENV_OFFSET = 747796405, 2891336453  # the reset seed of sim.metal:56
+
+
+def load_bank(path, split):
+    """The levels of one split of a challenge bank (JSONL, schema 1), parsed
+    and checked as challenge_evaluation::parse_level does
+    (challenge_evaluation.hpp:163-283): families 14-16, the environment seed
+    derivation, room bounds, at most 16 obstacles.  Each level carries its
+    WWorld record (obstacles, count, family, seed, goal, wind)."""
+    import json
+    levels = []
+    for number, line in enumerate(open(path), 1):
+        rec = json.loads(line)
+        where = "JSONL line %d" % number
+        if rec.get("record_type") != "challenge" or rec.get("schema_version") != 1:
+            raise ValueError(where + ": unsupported record")
+        if rec["split"] not in ("train", "dev", "final"):
+            raise ValueError(where + ": invalid split")
+        if rec["split"] != split:
+            continue
+        family = int(rec["family"])
+        if not 14 <= family <= 16:
+            raise ValueError(where + ": family must be 14, 15 or 16")
+        cfg = rec["sim_config"]
+        if int(cfg["family"]) != family or int(cfg["environment_index"]) != int(rec["environment_index"]):
+            raise ValueError(where + ": sim_config does not match the record")
+        base, index = int(cfg["seed"]), int(rec["environment_index"])
+        state = (base + index * BANK_ENV_STRIDE + BANK_ENV_OFFSET) & MASK
+        state ^= (state << 13) & MASK
+        state ^= state >> 17
+        state ^= (state << 5) & MASK
+        if state != int(rec["seed"]):
+            raise ValueError(where + ": seed does not match the environment seed derivation")
+        obstacles = rec["obstacles"]
+        if len(obstacles) > 16:
+            raise ValueError(where + ": more than 16 obstacles")
+        w = np.zeros((), abi.WORLD)
+        w["family"] = family
+        w["seed"] = int(rec["seed"])
+        w["goal"] = np.array(rec["goal"], np.float32)
+        w["wind"] = np.array(rec["wind"], np.float32)
+        w["count"] = len(obstacles)
+        for i, o in enumerate(obstacles):
+            if int(o["kind"]) > 2 or min(o["half_extent"]) < 0:
+                raise ValueError(where + ": invalid obstacle")
+            w["obstacles"][i]["kind"] = int(o["kind"])
+            w["obstacles"][i]["center"] = np.array(o["center"], np.float32)
+            w["obstacles"][i]["size"] = np.array(o["half_extent"], np.float32)
+            w["obstacles"][i]["velocity"] = np.array(o["velocity"], np.float32)
+        levels.append(dict(failure_id=rec["failure_id"], family=family, seed=int(rec["seed"]), base_seed=base,
+                           environment_index=index, distance=F32(cfg["distance"]), world=w))
+    return levels
+
+
+def bank_evaluate(actor, levels, mode=17, speed=1.5, max_steps=400, velocity_contract=1, geometry_memory=1,
+                  raptor=None, physics=None):
+    """challenge_evaluation::run (challenge_evaluation.hpp:353-500): batches
+    of up to 128 levels, one episode each; the bank's world replaces the
+    reset's before any observation, with the level's own reset seed,
+    initial distance and reference point.  Returns per-level outcome rows."""
+    if mode not in (2, 13, 17):
+        raise ValueError("mode must be 2, 13 or 17")
+    if not (np.isfinite(speed) and 0 < speed <= 3.0) or not 1 <= max_steps <= 400:
+        raise ValueError("speed in (0, 3] and max_steps in 1..400")
+    actor = np.ascontiguousarray(actor, np.float32).reshape(-1)
+    sizes = {abi.policy_shape(obs=d)["actor_count"]: d for d in (181, 184)}
+    if actor.size not in sizes or (mode >= 13 and sizes[actor.size] != 184):
+        raise ValueError("guided modes require the 184-input actor")
+    rows = []
+    for begin in range(0, len(levels), 128):
+        batch = levels[begin:begin + 128]
+        cfg = abi.default_config(n=len(batch), family=0, mode=mode, seed=batch[0]["seed"], eval=1, speed=speed,
+                                 distance=batch[0]["distance"], max_steps=max_steps,
+                                 velocity_contract=velocity_contract, geometry_memory=geometry_memory)
+        sim = Sim(cfg, 32, raptor=raptor, physics=physics, actor_obs=sizes[actor.size])
+        try:
+            sim.set("actor", actor)
+            worlds, runs = sim.get("worlds"), sim.get("runs")
+            for n, lv in enumerate(batch):
+                worlds[n] = lv["world"]
+                runs[n]["rng"] = (lv["base_seed"] + lv["environment_index"] * BANK_ENV_STRIDE + BANK_ENV_OFFSET) & MASK
+                runs[n]["steps"] = 0
+                g = lv["world"]["goal"].astype(np.float32)
+                dz = F32(g[2] - F32(1.5))
+                runs[n]["initial_distance"] = np.sqrt(F32(F32(g[0] * g[0]) + F32(g[1] * g[1])) + F32(dz * dz),
+                                                      dtype=np.float32)
+                runs[n]["reference_position"] = (0.0, 0.0, 1.5)
+            sim.set("worlds", worlds)
+            sim.set("runs", runs)
+            sim.collect(max_steps)
+            sim.sync()
+            r = sim.get("runs")
+        finally:
+            sim.close()
+        for n, lv in enumerate(batch):
+            if r[n]["episodes"] != 1 or r[n]["successes"] + r[n]["collisions"] + r[n]["timeouts"] != 1:
+                raise RuntimeError("level did not produce exactly one terminal outcome: " + lv["failure_id"])
+            rows.append(dict(failure_id=lv["failure_id"], success=int(r[n]["successes"]),
+                             collision=int(r[n]["collisions"]), timeout=int(r[n]["timeouts"]),
+                             progress=float(r[n]["final_progress"]), path=float(r[n]["path"]),
+                             elapsed=float(r[n]["elapsed"]), goal_time=float(r[n]["success_time"]),
+                             peak_speed=float(r[n]["peak_speed"]), min_clearance=float(r[n]["min_clearance"])))
+    return rows
+
+
 # ---------------------------------------------------------------- controlled threats
 F32 = np.float32
 MASK = 0xFFFFFFFF

@@ -208,3 +208,51 @@ def test_task_checkpoint_resume_bit_exact(tmp_path):
     sim3, ppo3, _ = make_pair(cfg, 16, epochs=1, minibatch=256, actor_obs=184)
     with pytest.raises(Exception):
         ppo3.load_checkpoint(path, 2, 16, 64, 99)  # no tasks configured: mismatch
+
+
+# ---------------------------------------------------------------- challenge bank
+BANK_POLICIES = {"fdd62374c9a1": "table_memory", "469e7189af8e": "clean_stress", "fde3cc40baf0": "threat_joint"}
+
+
+def _bank_actor(sha):
+    if BANK_POLICIES[sha] == "table_memory":
+        h, a = formats.read_checkpoint(os.path.join(GOLDEN, "guided-table-memory.bin.best"))
+        return a, np.array(h["config"], abi.SIM_CONFIG)
+    z = np.load(os.path.join(GOLDEN, "actors", BANK_POLICIES[sha] + ".npz"))
+    return z["actor"], z["config"].view(abi.SIM_CONFIG)[0]
+
+
+@pytest.mark.parametrize("name", ["original", "geometry", "goal", "static", "dynamic"])
+def test_published_bank_evaluations(name):
+    """The reference's published dev-split evaluations of its challenge bank
+    (evidence/inputs/bank-*.csv: 90 hallway/room/vertical-choice levels,
+    three trained policies, modes 2, 13 and 17, 1.5 m/s, 400 ticks), run by
+    challenge_evaluation::run's protocol: every level's outcome."""
+    from mdnav import bank_evaluate, load_bank
+    rows = list(csv.DictReader(open(os.path.join(GOLDEN, "bank", "bank-%s.csv" % name))))
+    sha = rows[0]["checkpoint_sha256"][:12]
+    actor, ckcfg = _bank_actor(sha)
+    levels = {lv["failure_id"]: lv for lv in load_bank(os.path.join(GOLDEN, "bank", "challenge-bank-v1-dev.jsonl"),
+                                                       "dev")}
+    ordered = [levels[r["failure_id"]] for r in rows]
+    mode = int(rows[0]["mode"])
+    say("case: bank %s policy %s mode %d" % (name, BANK_POLICIES[sha], mode))
+    got = bank_evaluate(actor, ordered, mode=mode, speed=float(rows[0]["speed_mps"]),
+                        max_steps=int(rows[0]["max_steps"]), velocity_contract=int(ckcfg["velocity_contract"]),
+                        geometry_memory=int(ckcfg["geometry_memory"]), raptor=raptor_fixture()[0])
+    agree = 0
+    for g, r in zip(got, rows):
+        same = (g["success"], g["collision"], g["timeout"]) == (int(r["success"]), int(r["collision"]),
+                                                               int(r["timeout"]))
+        agree += same
+        if not same:
+            say("  %s differs: published %s/%s/%s at %s s, here %d/%d/%d at %.6g s" % (
+                r["failure_id"], r["success"], r["collision"], r["timeout"], r["elapsed_s"], g["success"],
+                g["collision"], g["timeout"], g["elapsed"]))
+    have = {k: sum(g[k] for g in got) for k in ("success", "collision", "timeout")}
+    want = {k: sum(int(r[k]) for r in rows) for k in ("success", "collision", "timeout")}
+    close = sum(abs(g["elapsed"] - float(r["elapsed_s"])) < 1e-3 for g, r in zip(got, rows))
+    say("  counts %s / published %s; agreement %d/90; elapsed equal to printed digits %d/90" % (have, want, agree,
+                                                                                                 close))
+    assert agree >= 89, agree
+    assert all(abs(have[k] - want[k]) <= 1 for k in have), (have, want)
