@@ -61,7 +61,10 @@ enum MdnBuffer {
     MDN_BUF_METRIC_ROWS = 23, /* float[updates][4] of the last rollout_update */
     MDN_BUF_NEXT_CRITIC_OBS = 24, /* float[T][N][32] critic observation of s' (the next_values input) */
     MDN_BUF_ENV_PHYSICS = 25, /* MdnPhysicsParams[N]  environment_physics (main.mm:537): each env's plant */
-    MDN_BUF_TASK_STATES = 26  /* MdnTaskState[N]      task_states (main.mm:523) */
+    MDN_BUF_TASK_STATES = 26, /* MdnTaskState[N]      task_states (main.mm:523) */
+    MDN_BUF_BANK_ACTIVE_IDS = 27,     /* uint32[N]     bank_active_ids: each env's challenge level */
+    MDN_BUF_BANK_TRANSITION_IDS = 28, /* uint32[T][N]  bank_transition_ids: the level of each row */
+    MDN_BUF_BANK_SCHEDULE = 29        /* uint32[N][stride] bank_schedule (after mdn_sim_set_bank) */
 };
 
 /* Kernel ids for mdn_sim_kernel_time. */
@@ -148,6 +151,16 @@ int mdn_sim_get_runtime(const MdnSim* sim, MdnRuntimeConfig* runtime);
  * effect at the next mdn_sim_reset. */
 int mdn_sim_set_tasks(MdnSim* sim, const MdnTaskControl* tasks);
 int mdn_sim_get_tasks(const MdnSim* sim, MdnTaskControl* tasks);
+/* Frozen challenge bank: Sim::bank_worlds / bank_schedule / bank_control
+ * (main.mm:522, 543-545, 2175-2178).  `count` worlds and an env-major
+ * schedule [N][schedule_stride] of level ids (MDN_BANK_REHEARSAL: a generated
+ * rehearsal world, family 12 or 13 alternating by env); each reset takes its
+ * slot (0 at mdn_sim_reset, tick + 1 after a reset at tick) and replaces the
+ * world, wind and initial distance (sim.metal:95-121); every row records
+ * the env's level (MDN_BUF_BANK_TRANSITION_IDS).  count = 0 disables it.
+ * Upload MDN_BUF_BANK_SCHEDULE to change the schedule between rollouts. */
+int mdn_sim_set_bank(MdnSim* sim, const MdnWorld* worlds, uint32_t count, const uint32_t* schedule,
+                     uint32_t schedule_stride);
 /* navigation_task_default_config (navigation_tasks.hpp:99-140) and
  * rl_physics_domain_stress_range (physics_domain.hpp:37-40). */
 int mdn_task_default_config(uint32_t stage, uint32_t family, float difficulty, MdnTaskConfig* out);

@@ -190,6 +190,14 @@ typedef struct MdnTaskState {
     float witness_points[4][3];
 } MdnTaskState;
 
+/* Frozen challenge bank (ChallengeBankControl, main.mm:511-514): with
+ * `enabled`, every reset takes its world from the bank per schedule slot
+ * (sim.metal:95-121). */
+typedef struct MdnBankControl {
+    uint32_t enabled, bank_count, schedule_stride, horizon;
+} MdnBankControl;
+#define MDN_BANK_REHEARSAL 0xffffffffu /* schedule slot: a generated rehearsal world */
+
 /* Rollout metrics of cpu_reference.hpp:55-70. */
 typedef struct MdnMetrics {
     double wall_seconds;
@@ -212,6 +220,7 @@ static_assert(sizeof(MdnRuntimeConfig) == 56, "NavigationRuntimeConfig layout");
 static_assert(sizeof(MdnTaskConfig) == 144, "NavigationTaskConfig layout");
 static_assert(sizeof(MdnTaskControl) == 148, "NavigationTaskControl layout");
 static_assert(sizeof(MdnTaskState) == 192, "NavigationTaskState layout");
+static_assert(sizeof(MdnBankControl) == 16, "ChallengeBankControl layout");
 #endif
 
 #endif /* MDNAV_TYPES_H */

@@ -99,7 +99,13 @@ struct MdnSim {
     MdnPhysicsParams* env_phys = nullptr;   // [N]
     MdnTaskState* task_states = nullptr;    // [N]
     MdnTaskConfig* task_cfg = nullptr;      // device copy of task.config
-    bool episodic() const { return runtime.enabled != 0u || task.enabled != 0u; }
+    // challenge bank (main.mm:522, 543-545)
+    MdnBankControl bank{};
+    float* bank_worlds = nullptr;           // [count][WORLD_WORDS]
+    uint32_t* bank_schedule = nullptr;      // [N][stride]
+    uint32_t* bank_active = nullptr;        // [N]
+    uint32_t* bank_transition = nullptr;    // [T][N]
+    bool episodic() const { return runtime.enabled != 0u || task.enabled != 0u || bank.enabled != 0u; }
     // policy
     float* actor = nullptr;
     float* critic = nullptr;
@@ -126,12 +132,16 @@ struct MdnSim {
         a.env_phys = episodic() ? env_phys : nullptr;
         a.task_states = task_states;
         a.task_cfg = task.enabled ? task_cfg : nullptr;
+        a.bank_active = bank.enabled ? bank_active : nullptr;
+        a.bank_transition = bank_transition;
         return a;
     }
     nav::EpisodeArgs episode_args(bool first) const {
         nav::EpisodeArgs e;
         e.state = state; e.run = run; e.world = world; e.env_phys = env_phys; e.task_states = task_states;
         e.cfg = cfg; e.phys = phys; e.runtime = runtime; e.task = task; e.first = first ? 1u : 0u;
+        e.bank_worlds = bank_worlds; e.bank_schedule = bank_schedule; e.bank_active = bank_active;
+        e.bank = bank; e.slot = 0;
         return e;
     }
 };
@@ -212,6 +222,10 @@ BufInfo row_buffer(MdnSim* s, uint32_t id) {
         case MDN_BUF_CRITIC: return {s->critic, size_t(s->shape.critic_count()) * 4};
         case MDN_BUF_ENV_PHYSICS: return {s->env_phys, size_t(s->cfg.n) * sizeof(MdnPhysicsParams)};
         case MDN_BUF_TASK_STATES: return {s->task_states, size_t(s->cfg.n) * sizeof(MdnTaskState)};
+        case MDN_BUF_BANK_ACTIVE_IDS: return {s->bank_active, size_t(s->cfg.n) * 4};
+        case MDN_BUF_BANK_TRANSITION_IDS: return {s->bank_transition, R * 4};
+        case MDN_BUF_BANK_SCHEDULE:
+            return {s->bank_schedule, s->bank_schedule ? size_t(s->cfg.n) * s->bank.schedule_stride * 4 : 0};
         default: break;
     }
     if (s->ppo) {
@@ -268,6 +282,12 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
     guard(dev_alloc(&s->env_phys, N));
     guard(dev_alloc(&s->task_states, N));
     guard(dev_alloc(&s->task_cfg, 1));
+    guard(dev_alloc(&s->bank_active, N));
+    guard(dev_alloc(&s->bank_transition, R));
+    if (rc == MDN_OK) {  // no bank: every id is MDN_BANK_REHEARSAL (sim.metal:143, 317)
+        guard(hipMemset(s->bank_active, 0xff, size_t(N) * 4) == hipSuccess ? MDN_OK : fail(MDN_E_HIP, "hipMemset"));
+        guard(hipMemset(s->bank_transition, 0xff, R * 4) == hipSuccess ? MDN_OK : fail(MDN_E_HIP, "hipMemset"));
+    }
     guard(dev_alloc(&s->actor, s->shape.actor_count()));
     guard(dev_alloc(&s->critic, s->shape.critic_count()));
     guard(dev_alloc(&s->actor_w1t, size_t(OBS) * HID));
@@ -345,7 +365,8 @@ void mdn_sim_destroy(MdnSim* s) {
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->ppo) mdn_ppo_destroy(s->ppo);
     void* bufs[] = {s->state, s->run, s->world, s->sensors, s->poses, s->commands, s->raptor, s->camera, s->cells,
-                    s->pix_rays, s->mem_head, s->env_phys, s->task_states, s->task_cfg,
+                    s->pix_rays, s->mem_head, s->env_phys, s->task_states, s->task_cfg, s->bank_worlds,
+                    s->bank_schedule, s->bank_active, s->bank_transition,
                     s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->obs, s->co, s->nco, s->actions, s->logp,
                     s->values, s->rewards, s->next_values, s->advantages, s->returns, s->terminated, s->truncated};
     for (void* b : bufs)
@@ -457,6 +478,34 @@ int mdn_sim_get_tasks(const MdnSim* s, MdnTaskControl* tasks) {
     return MDN_OK;
 }
 
+int mdn_sim_set_bank(MdnSim* s, const MdnWorld* worlds, uint32_t count, const uint32_t* schedule,
+                     uint32_t schedule_stride) {
+    if (!s || (count && (!worlds || !schedule || schedule_stride == 0)))
+        return fail(MDN_E_ARG, "mdn_sim_set_bank: null argument or zero schedule stride");
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    if (s->bank_worlds) HIP_TRY(hipFree(s->bank_worlds));
+    if (s->bank_schedule) HIP_TRY(hipFree(s->bank_schedule));
+    s->bank_worlds = nullptr;
+    s->bank_schedule = nullptr;
+    s->bank = MdnBankControl{};
+    const size_t N = s->cfg.n;
+    if (count == 0) {
+        HIP_TRY(hipMemset(s->bank_active, 0xff, N * 4));
+        return MDN_OK;
+    }
+    if ((rc = dev_alloc(&s->bank_worlds, size_t(count) * WORLD_WORDS)) != MDN_OK) return rc;
+    if ((rc = dev_alloc(&s->bank_schedule, N * schedule_stride)) != MDN_OK) return rc;
+    HIP_TRY(hipMemcpy(s->bank_worlds, worlds, size_t(count) * sizeof(MdnWorld), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(s->bank_schedule, schedule, N * schedule_stride * 4, hipMemcpyHostToDevice));
+    s->bank.enabled = 1;
+    s->bank.bank_count = count;
+    s->bank.schedule_stride = schedule_stride;
+    s->bank.horizon = s->horizon;
+    return MDN_OK;
+}
+
 int mdn_task_default_config(uint32_t stage, uint32_t family, float difficulty, MdnTaskConfig* out) {
     if (!out) return fail(MDN_E_ARG, "mdn_task_default_config: null argument");
     if (!mdn::task_default_config(*out, stage, family, difficulty))
@@ -481,7 +530,7 @@ int collect_episodic(MdnSim* s, uint32_t count, int slots) {
     nav::MemoryArgs m;
     m.head = s->mem_head; m.sensors = s->sensors; m.poses = s->poses; m.pix_rays = s->pix_rays; m.cells = s->cells;
     m.sensor_dt = b.sensor_dt; m.inv_sensor_dt = b.inv_sensor_dt; m.n = s->cfg.n;
-    const nav::EpisodeArgs e = s->episode_args(false);
+    nav::EpisodeArgs e = s->episode_args(false);
     int rc = MDN_OK;
     for (uint32_t t = 0; t < count && rc == MDN_OK; t++) {
         b.tick0 = t;
@@ -497,6 +546,7 @@ int collect_episodic(MdnSim* s, uint32_t count, int slots) {
         b.split = nav::SPLIT_BEGIN_AT_ACT;
         rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&b, 8, slots, s->shape.obs, s->stream); });
         if (rc) break;
+        e.slot = t % s->horizon + 1;  // the reset at tick t takes schedule slot tick + 1
         rc = timed(s, MDN_K_EPISODE, [&] { return nav_launch_episode(&e, s->stream); });
     }
     return rc;

@@ -61,6 +61,10 @@ struct RolloutArgs {
     const MdnPhysicsParams* env_phys;
     MdnTaskState* task_states;
     const MdnTaskConfig* task_cfg;
+    // challenge bank: each row's level id [T][N] (sim.metal:317), from the
+    // env's active level [N] (null: no bank, rows get MDN_BANK_REHEARSAL)
+    const uint32_t* bank_active;
+    uint32_t* bank_transition;
 };
 // Per-episode work after a reset (rollout.hip episode_kernel): the
 // episode's plant and hover rpm (sim.metal:62-81) and its navigation task
@@ -77,6 +81,14 @@ struct EpisodeArgs {
     MdnRuntimeConfig runtime;
     MdnTaskControl task;
     uint32_t first;
+    // challenge bank (sim.metal:95-121): worlds [count][WORLD_WORDS],
+    // schedule [N][stride]; a reset takes slot `slot` (0 at the first reset,
+    // tick + 1 after a reset at tick)
+    const float* bank_worlds;
+    const uint32_t* bank_schedule;
+    uint32_t* bank_active;
+    MdnBankControl bank;
+    uint32_t slot;
 };
 // memory header words
 constexpr uint32_t MEM_HEAD_OBSERVED = 0;  // 1: observed this tick (else skip the env)

@@ -196,9 +196,10 @@ __global__ __launch_bounds__(64) void reset_kernel(RolloutArgs a) {
 }
 
 // Per-episode work of the envs whose episode just began, one thread per env:
-// the episode's plant (sim.metal:62-69, with its hover rpm 70-81) and its
-// navigation task (sim.metal:122-141: world, start state, yaw, reference
-// point, desired velocity, initial distance, wind).  Runs after the reset
+// the episode's plant (sim.metal:62-69, with its hover rpm 70-81), its
+// challenge-bank world (sim.metal:95-121) and its navigation task
+// (sim.metal:122-141: world, start state, yaw, reference point, desired
+// velocity, initial distance, wind), in the reference's order.  Runs after the reset
 // kernel (first: every env) and after each launch that may reset envs (an
 // env with steps == 0 was reset by it; an evaluation never restarts one).
 __global__ __launch_bounds__(64) void episode_kernel(EpisodeArgs a) {
@@ -228,10 +229,44 @@ __global__ __launch_bounds__(64) void episode_kernel(EpisodeArgs a) {
                                     : ep.action_max;
         }
     }
+    float* world = a.world + size_t(n) * WORLD_WORDS;
+    if (a.bank.enabled != 0u) {  // sim.metal:95-121
+        if (a.bank.bank_count != 0u && a.slot < a.bank.schedule_stride) {
+            const uint32_t level = a.bank_schedule[size_t(n) * a.bank.schedule_stride + a.slot];
+            bool apply = true;
+            if (level == MDN_BANK_REHEARSAL) {  // alternating static / moving-threat rehearsal
+                uint32_t rng = r.rng;
+                const uint32_t family = training_family(n % 2 == 0 ? 12u : 13u, rng);
+                const uint32_t seed = xs(rng);
+                WorldGen{world}.generate(seed, family, 4.0f);
+                r.rng = rng;
+            } else if (level < a.bank.bank_count) {
+                const float* src = a.bank_worlds + size_t(level) * WORLD_WORDS;
+                for (uint32_t i = 0; i < WORLD_WORDS; i++) world[i] = src[i];
+            } else {
+                apply = false;
+            }
+            if (apply) {
+                world[166] = clean_env(a.cfg, n) ? 0.0f : a.cfg.wind;
+                world[167] = 0.0f;
+                world[168] = 0.0f;
+                const float gx = world[163], gy = world[164], gz = world[165] - 1.5f;
+                r.initial_distance = sqrt_f(gx * gx + gy * gy + gz * gz);
+                const uint32_t wfam = float_bits(world[162]);
+                if (wfam == 10u || wfam == 11u) {
+                    s.v[0] = a.cfg.speed;
+                    r.desired_vel[0] = a.cfg.speed;
+                    r.prev_nav[0] = 1.0f;
+                }
+                a.bank_active[n] = level;
+            }
+        }
+    } else {
+        a.bank_active[n] = MDN_BANK_REHEARSAL;
+    }
     MdnTaskState t;
     uint32_t* tw = reinterpret_cast<uint32_t*>(&t);
     for (uint32_t i = 0; i < sizeof(MdnTaskState) / 4; i++) tw[i] = 0u;
-    float* world = a.world + size_t(n) * WORLD_WORDS;
     if (a.task.enabled != 0u) {
         uint32_t rng = a.cfg.seed ^ ((n + 1u) * 0x27d4eb2du) ^ ((r.episodes + 1u) * 0x165667b1u);
         task_generate(world, t, rng, a.task.config);
@@ -949,6 +984,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 a.rewards[row] = reward;
                 a.terminated[row] = term ? 1 : 0;
                 a.truncated[row] = trunc ? 1 : 0;
+                if constexpr (DYN)  // sim.metal:317
+                    a.bank_transition[row] = a.bank_active ? a.bank_active[nn] : MDN_BANK_REHEARSAL;
             }
             // critic observation of the next state (time elapsed after the substeps)
             float cob[COBS];

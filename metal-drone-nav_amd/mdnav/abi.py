@@ -168,5 +168,7 @@ BUFFERS = {
     "returns": (18, np.float32), "actor_m": (19, np.float32), "actor_v": (20, np.float32),
     "critic_m": (21, np.float32), "critic_v": (22, np.float32), "metric_rows": (23, np.float32),
     "next_critic_obs": (24, np.float32), "environment_physics": (25, PHYSICS_PARAMS),
-    "task_states": (26, TASK_STATE),
+    "task_states": (26, TASK_STATE), "bank_active_ids": (27, np.uint32), "bank_transition_ids": (28, np.uint32),
+    "bank_schedule": (29, np.uint32),
 }
+BANK_REHEARSAL = 0xFFFFFFFF

@@ -25,7 +25,7 @@ EXPORTS = [
     "mdn_lppo_metric_mean", "mdn_lppo_optimizer_step", "mdn_lppo_collect", "mdn_lppo_means",
     "mdn_op_check_division", "mdn_ppo_save_checkpoint", "mdn_ppo_load_checkpoint", "mdn_checkpoint_read",
     "mdn_navpol_read", "mdn_navpol_write", "mdn_fnv1a64_file", "mdn_sim_set_runtime", "mdn_sim_get_runtime",
-    "mdn_sim_set_tasks", "mdn_sim_get_tasks", "mdn_task_default_config", "mdn_domain_stress_range",
+    "mdn_sim_set_tasks", "mdn_sim_get_tasks", "mdn_task_default_config", "mdn_domain_stress_range", "mdn_sim_set_bank",
 ]
 
 P = ctypes.c_void_p
@@ -82,6 +82,7 @@ def lib():
         _sig(L, "mdn_sim_get_tasks", I32, P, P)
         _sig(L, "mdn_task_default_config", I32, U32, U32, F32, P)
         _sig(L, "mdn_domain_stress_range", I32, P)
+        _sig(L, "mdn_sim_set_bank", I32, P, P, U32, P, U32)
         _sig(L, "mdn_ppo_create", I32, P, U32, U32, ctypes.POINTER(P))
         _sig(L, "mdn_ppo_destroy", None, P)
         _sig(L, "mdn_ppo_rollout_update", I32, P, U32)

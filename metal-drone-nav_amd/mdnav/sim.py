@@ -118,6 +118,16 @@ class Sim:
         t = np.array(tasks, abi.TASK_CONTROL)
         check(lib().mdn_sim_set_tasks(self.h, t.ctypes.data_as(ctypes.c_void_p)))
 
+    def set_bank(self, worlds, schedule):
+        """Frozen challenge bank (main.mm:2175-2178): WORLD records and an
+        env-major schedule [N][stride] of level ids (abi.BANK_REHEARSAL for
+        a generated rehearsal world); an empty bank disables it."""
+        w = np.ascontiguousarray(worlds, abi.WORLD).reshape(-1)
+        sch = np.ascontiguousarray(schedule, np.uint32)
+        stride = int(sch.shape[-1]) if sch.size else 0
+        check(lib().mdn_sim_set_bank(self.h, w.ctypes.data_as(ctypes.c_void_p), w.size,
+                                     sch.ctypes.data_as(ctypes.c_void_p), stride))
+
     def reset(self):
         check(lib().mdn_sim_reset(self.h))
         return self.sync()

@@ -242,6 +242,10 @@ struct Trainer {
     MdnTaskControl tasks;
     std::vector<MdnPhysicsParams> env_physics;
     std::vector<MdnTaskState> task_states;
+    // frozen challenge bank (sim.metal:95-121, 317)
+    MdnBankControl bank;
+    std::vector<MdnWorld> bank_worlds;
+    std::vector<uint32_t> bank_schedule, bank_active, bank_transition;
 
     Trainer(const MdnSimConfig& c, uint32_t h, const MdnRaptorWeights& r, const MdnPhysicsParams& p,
             uint32_t ep, uint32_t mb)
@@ -270,12 +274,15 @@ struct Trainer {
         env_physics.assign(n, p);
         task_states.resize(n);
         std::memset(task_states.data(), 0, n * sizeof(MdnTaskState));
+        std::memset(&bank, 0, sizeof(bank));
+        bank_active.assign(n, MDN_BANK_REHEARSAL);
+        bank_transition.assign(rows, MDN_BANK_REHEARSAL);
         camera.resize(MDN_SENSOR_PIXELS * 3);
         for (uint32_t k = 0; k < MDN_SENSOR_PIXELS; k++) {
             const V3 ray = camera_ray(k);
             camera[3 * k] = ray.x; camera[3 * k + 1] = ray.y; camera[3 * k + 2] = ray.z;
         }
-        for (uint32_t e = 0; e < cfg.n; e++) reset_env(e, true);
+        for (uint32_t e = 0; e < cfg.n; e++) reset_env(e, true, 0);
     }
 
     // cpu_reference.hpp:219-238 == sim.metal:17-36
@@ -290,7 +297,35 @@ struct Trainer {
     bool active(uint32_t n) const { return !(cfg.eval && runs[n].episodes); }
 
     // cpu_reference.hpp:240-273 == sim.metal:55-94 (runtime domain off)
-    void reset_env(uint32_t n, bool first) {
+    // sim.metal:95-121: the bank world of the env's schedule slot (a
+    // generated rehearsal world for MDN_BANK_REHEARSAL)
+    void apply_bank(uint32_t n, uint32_t slot) {
+        if (bank.bank_count == 0 || n >= cfg.n || slot >= bank.schedule_stride) return;
+        MdnPhysicsState& s = states[n];
+        MdnSimRun& run = runs[n];
+        MdnWorld& world = worlds[n];
+        const uint32_t level = bank_schedule[size_t(n) * bank.schedule_stride + slot];
+        if (level == MDN_BANK_REHEARSAL) {
+            uint32_t rng = run.rng;
+            const uint32_t family = training_family(n % 2 == 0 ? 12u : 13u, rng);
+            const uint32_t seed = xorshift(rng);
+            generate_world(world, seed, family, 4.0f);
+            run.rng = rng;
+        } else {
+            if (level >= bank.bank_count) return;
+            world = bank_worlds[level];
+        }
+        world.wind[0] = wind_param(n); world.wind[1] = 0; world.wind[2] = 0;
+        run.initial_distance = vlen(v3(world.goal[0], world.goal[1], world.goal[2] - 1.5f));
+        if (world.family == 10 || world.family == 11) {
+            s.linear_velocity[0] = cfg.speed;
+            run.desired_velocity[0] = cfg.speed;
+            run.previous_nav[0] = 1.0f;
+        }
+        bank_active[n] = level;
+    }
+
+    void reset_env(uint32_t n, bool first, uint32_t slot) {
         MdnPhysicsState& s = states[n];
         MdnSimRun& run = runs[n];
         MdnWorld& world = worlds[n];
@@ -328,10 +363,12 @@ struct Trainer {
             run.success_time = run.total_path = run.total_elapsed = run.final_progress = 0;
             std::fill(poses.begin() + size_t(n) * 96, poses.begin() + size_t(n + 1) * 96, 0.0f);
         }
+        if (bank.enabled != 0) apply_bank(n, slot);
+        else bank_active[n] = MDN_BANK_REHEARSAL;
         reset_task(tasks, cfg.seed, wind_param(n), n, s, run, world, task_states[n]);
     }
     void reset_all() {
-        for (uint32_t e = 0; e < cfg.n; e++) reset_env(e, true);
+        for (uint32_t e = 0; e < cfg.n; e++) reset_env(e, true, 0);
     }
 
     // sim.metal:159-181 == cpu_reference.hpp:379-394
@@ -623,6 +660,7 @@ struct Trainer {
             terminated[row] = uint8_t(collision || success);
             truncated[row] = uint8_t(timeout && !terminated[row]);
         }
+        bank_transition[row] = bank.enabled != 0 ? bank_active[n] : MDN_BANK_REHEARSAL;  // sim.metal:317
         float hidden[8192];
         float* cobs = &nco[row * shape.critic_obs];
         critic_observation(s, world, run, cobs);
@@ -636,7 +674,7 @@ struct Trainer {
             run.total_path += run.path;
             run.total_elapsed += run.elapsed;
             run.final_progress += 1.0f - after / max_f(run.initial_distance, 1.0e-4f);
-            if (!cfg.eval) reset_env(n, false);
+            if (!cfg.eval) reset_env(n, false, tick + 1);
         }
     }
 
@@ -897,6 +935,15 @@ void orc_guidance_memory(const float* cur, const float* prev, const float* goal,
 void orc_trainer_set_runtime(void* h, const MdnRuntimeConfig* r) { static_cast<Trainer*>(h)->runtime = *r; }
 void orc_trainer_set_tasks(void* h, const MdnTaskControl* t) { static_cast<Trainer*>(h)->tasks = *t; }
 void orc_trainer_reset(void* h) { static_cast<Trainer*>(h)->reset_all(); }
+void orc_trainer_set_bank(void* h, const MdnWorld* worlds, uint32_t count, const uint32_t* schedule, uint32_t stride) {
+    Trainer* t = static_cast<Trainer*>(h);
+    t->bank.enabled = count > 0 ? 1u : 0u;
+    t->bank.bank_count = count;
+    t->bank.schedule_stride = stride;
+    t->bank.horizon = t->horizon;
+    t->bank_worlds.assign(worlds, worlds + count);
+    t->bank_schedule.assign(schedule, schedule + size_t(t->cfg.n) * stride);
+}
 // standalone operators of the dynamics draw and the task generator
 int orc_sample_domain(const MdnPhysicsParams* nominal, uint32_t* rng, float amplitude, const MdnDomainRange* range,
                       MdnPhysicsParams* varied, float* sample) {
@@ -971,6 +1018,9 @@ void* orc_trainer_buffer(void* hp, uint32_t id, uint64_t* bytes) {
         case 24: return ret(t->nco);
         case 25: return ret(t->env_physics);
         case 26: return ret(t->task_states);
+        case 27: return ret(t->bank_active);
+        case 28: return ret(t->bank_transition);
+        case 29: return ret(t->bank_schedule);
         default: *bytes = 0; return nullptr;
     }
 }

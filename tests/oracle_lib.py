@@ -87,6 +87,7 @@ def oracle():
         _sig(lib, "orc_trainer_set_runtime", None, P, P)
         _sig(lib, "orc_trainer_set_tasks", None, P, P)
         _sig(lib, "orc_trainer_reset", None, P)
+        _sig(lib, "orc_trainer_set_bank", None, P, P, U32, P, U32)
         _sig(lib, "orc_sample_domain", ctypes.c_int, P, ctypes.POINTER(U32), F32, P, P, P)
         _sig(lib, "orc_domain_episode_seed", U32, P, U32, U32, U32)
         _sig(lib, "orc_domain_stress_range", None, P)
@@ -229,6 +230,12 @@ class OracleTrainer:
 
     def reset(self):
         self.lib.orc_trainer_reset(self.h)
+
+    def set_bank(self, worlds, schedule):
+        self._bank_w = np.ascontiguousarray(worlds, abi.WORLD).reshape(-1)
+        self._bank_s = np.ascontiguousarray(schedule, np.uint32)
+        self.lib.orc_trainer_set_bank(self.h, ptr(self._bank_w), self._bank_w.size, ptr(self._bank_s),
+                                      int(self._bank_s.shape[-1]) if self._bank_s.size else 0)
 
     def set(self, name, values):
         b = self.buffer(name)

@@ -256,3 +256,44 @@ def test_published_bank_evaluations(name):
                                                                                                  close))
     assert agree >= 89, agree
     assert all(abs(have[k] - want[k]) <= 1 for k in have), (have, want)
+
+
+
+@pytest.mark.parametrize("with_plants", [False, True])
+def test_bank_training_resets_bit_exact(with_plants):
+    """Training with a frozen challenge bank (sim.metal:95-121, 143, 317):
+    a schedule mixing bank levels, rehearsal slots (generated family 12 / 13
+    worlds) and out-of-range ids, resets inside the rollout taking slot
+    tick + 1; every buffer, the active and per-row level ids included,
+    bit-identical to the oracle."""
+    from mdnav import load_bank
+    say("case: bank training resets, plants=%s" % with_plants)
+    levels = load_bank(os.path.join(GOLDEN, "bank", "challenge-bank-v1-dev.jsonl"), "dev")[:12]
+    worlds = np.array([lv["world"] for lv in levels], abi.WORLD)
+    n, horizon = 64, 16
+    rng = np.random.default_rng(7)
+    schedule = rng.integers(0, 14, size=(n, horizon + 1)).astype(np.uint32)  # 12, 13: out of range
+    schedule[rng.uniform(size=schedule.shape) < 0.25] = abi.BANK_REHEARSAL
+    cfg = config(n=n, family=0, seed=5, max_steps=9, geometry_memory=1, speed=1.5, distance=8.0)
+    sim, ppo, ora = make_pair(cfg, horizon, actor_obs=184)
+    for side in (sim, ora):
+        side.set_bank(worlds, schedule)
+        if with_plants:
+            side.set_runtime(task_runtime(1.0))
+    ora.set("actor", sim.get("actor"))
+    ora.set("critic", sim.get("critic"))
+    sim.reset()
+    ora.reset()
+    names = ENV_BUFFERS + TASK_BUFFERS + ["bank_active_ids"]
+    bad = compare(sim, ora, names)
+    assert not bad, bad
+    for k in range(3):
+        sim.collect()
+        sim.sync()
+        ora.collect()
+        bad = compare(sim, ora, names + ROW_BUFFERS + ["bank_transition_ids"])
+        ids = sim.get("bank_transition_ids")
+        say("  collect %d: episodes %d, distinct row levels %d, mismatches %s" % (
+            k, int(sim.get("runs")["episodes"].sum()), np.unique(ids).size, bad))
+        assert not bad, (k, bad)
+    assert np.unique(sim.get("bank_transition_ids")).size >= 10
