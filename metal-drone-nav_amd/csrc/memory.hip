@@ -11,11 +11,17 @@
 //      kept (compacted into LDS): a contact needs along <= 3 + radius and
 //      |p|^2 - along^2 < radius^2, so a point with |p|^2 above
 //      (3 + radius)^2 + radius^2 (with a 0.1 % margin for rounding) is never
-//      one, whatever the sweep;
-//   2. 255 threads = 85 candidate sweeps x 3 thirds of the kept points scan
-//      them (every lane reads the same point: LDS broadcast); the nearest
+//      one, whatever the sweep.  The kept points are grouped nearest first
+//      in four distance shells, and padded with points no sweep touches to a
+//      multiple of three;
+//   2. 255 threads = 85 candidate sweeps x 3 interleaved thirds of the kept
+//      points scan them (every lane of a third reads the same point: LDS
+//      broadcast) with one trip count for the whole workgroup; the nearest
 //      contacts are combined with a min, which is exact in any order, so the
-//      order of the compacted points does not matter;
+//      order of the points does not change the result.  Near points first
+//      lower each sweep's running nearest contact early, which lets the
+//      exact skip test (below) drop most later contacts before their square
+//      root;
 //   3. the 85 candidates are scored and reduced with the sequential scan's
 //      rule (maximum score, first candidate on ties), and one lane writes the
 //      hint to the row's last three inputs.
@@ -35,6 +41,24 @@ constexpr uint32_t POINTS = 640, CANDIDATES = 85, PARTS = 3;
 constexpr uint32_t THREADS = 256;
 
 __device__ __forceinline__ float fbits(uint32_t u) { return __builtin_bit_cast(float, u); }
+// Correctly rounded square root of a positive normal x >= 2^-96: the
+// hardware estimate and the one-ulp correction of the compiler's own
+// correctly rounded sqrt lowering, without its scaling of tiny inputs and its
+// zero / infinity fix-up, neither of which applies in that range (the
+// instruction sequence is otherwise the same, so the results are equal).
+__device__ __forceinline__ float sqrt_pos(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const uint32_t b = __builtin_bit_cast(uint32_t, s);
+    const float dn = fbits(b - 1u), up = fbits(b + 1u);
+    float r = __builtin_fmaf(-dn, s, x) <= 0.0f ? dn : s;
+    r = __builtin_fmaf(-up, s, x) > 0.0f ? up : r;
+    return r;
+}
+constexpr uint32_t SHELLS = 4;
+// distance shell of a kept point by |p|^2: (< 1 m, < 2 m, < 3 m, beyond)
+__device__ __forceinline__ uint32_t shell_of(float p2) {
+    return p2 < 1.0f ? 0u : (p2 < 4.0f ? 1u : (p2 < 9.0f ? 2u : 3u));
+}
 __device__ __forceinline__ float div_r(float x, double r) { return float(double(x) * r); }
 
 struct Point {
@@ -74,12 +98,12 @@ __device__ __forceinline__ void wave_argmax(float& v, uint32_t& idx) {
 }
 
 __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a) {
-    __shared__ Point pts[POINTS];
+    __shared__ Point pts[POINTS + 2];  // + padding to a multiple of three
     __shared__ float cur[80], risk_v[80], part_near[PARTS][CANDIDATES];
     __shared__ float cand_score[2], cand_free[CANDIDATES];
     __shared__ uint32_t cand_idx[2], goal_cell_s[2];
     __shared__ float goal_al_s[2];
-    __shared__ uint32_t kept;
+    __shared__ uint32_t shell_count[SHELLS], shell_base[SHELLS + 1];
     const uint32_t n = blockIdx.x, t = threadIdx.x, wv = t / 64, lane = t % 64;
     const uint32_t* hd = a.head + size_t(n) * nav::MEM_HEAD_WORDS;
     if (hd[nav::MEM_HEAD_OBSERVED] == 0u) return;  // uniform over the workgroup
@@ -102,11 +126,17 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
 #pragma unroll
     for (int j = 0; j < 12; j++) pose[j] = fbits(hd[nav::MEM_HEAD_POSE + j]);
 
-    if (t == 0) kept = 0;
+    if (t < SHELLS) shell_count[t] = 0;
     __syncthreads();
-    // 1. remembered points (guidance.hpp:113-139 up to the sweep test)
-    for (uint32_t j0 = 0; j0 < POINTS; j0 += THREADS) {  // uniform trip count: whole waves ballot
-        const uint32_t j = j0 + t;
+    // 1. remembered points (guidance.hpp:113-139 up to the sweep test); each
+    // thread keeps its up to three points in registers while the shells are
+    // counted
+    constexpr uint32_t PER = (POINTS + THREADS - 1) / THREADS;
+    Point held[PER];
+    uint32_t held_shell[PER], held_slot[PER];
+#pragma unroll
+    for (uint32_t k = 0; k < PER; k++) {
+        const uint32_t j = k * THREADS + t;
         const uint32_t back = j / 80, cell = j % 80, row = cell / 10, col = cell % 10;
         Point p;
         bool keep = false;
@@ -140,11 +170,27 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
                 keep = p.xyz2.w <= 1.001f * (p.lim.x * p.lim.x + p.lim.y);
             }
         }
-        const uint64_t m = __ballot(keep);
-        uint32_t base = 0;
-        if (lane == 0 && m) base = atomicAdd(&kept, uint32_t(__popcll(m)));
-        base = __shfl(base, 0, 64);
-        if (keep) pts[base + uint32_t(__popcll(m & ((uint64_t(1) << lane) - 1)))] = p;
+        held[k] = p;
+        held_shell[k] = keep ? shell_of(p.xyz2.w) : SHELLS;
+        held_slot[k] = keep ? atomicAdd(&shell_count[held_shell[k]], 1u) : 0u;
+    }
+    __syncthreads();
+    if (t == 0) {
+        shell_base[0] = 0;
+        for (uint32_t k = 0; k < SHELLS; k++) shell_base[k + 1] = shell_base[k] + shell_count[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < PER; k++)
+        if (held_shell[k] < SHELLS) pts[shell_base[held_shell[k]] + held_slot[k]] = held[k];
+    {   // padding to a multiple of three: at the origin, no sweep has along > 0
+        const uint32_t total = shell_base[SHELLS], padded = (total + 2u) / 3u * 3u;
+        if (t < padded - total) {
+            Point z;
+            z.xyz2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            z.lim = make_float4(-1.0f, 0.0f, 0.0f, 0.0f);
+            pts[total + t] = z;
+        }
     }
     // per-cell current range x 12 and closing-speed risk contribution
     if (t < 80) {
@@ -191,7 +237,7 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
 
     // 2. swept-sphere clearance of every candidate over a third of the points
     // (guidance.hpp:134-139)
-    const uint32_t npts = kept;
+    const uint32_t iters = __builtin_amdgcn_readfirstlane((shell_base[SHELLS] + 2u) / 3u);
     if (t < PARTS * CANDIDATES) {
         const uint32_t c = t % CANDIDATES, part = t / CANDIDATES;
         float d[3];
@@ -206,16 +252,22 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
         // cannot lower nearest and its square root is skipped.  The state is
         // finite at an observation (the advance resets non-finite states), so
         // `along` is never NaN.
+        // The argument of the square root is l.y - lateral2 > 0 with
+        // l.y = radius^2 >= 0.04, so it is at least half an ulp of 0.04
+        // (about 2e-9), a normal number: sqrt_pos applies.  No operand of
+        // the min / max below is NaN (finite points and sweeps) or -0 (a
+        // difference of equal values rounds to +0), so the hardware min and
+        // max equal the oracle's fmin / fmax.
         float nearest = 3.0f;
-        const uint32_t j0 = part * npts / PARTS, j1 = (part + 1) * npts / PARTS;
+        const Point* pp = pts + part;
 #pragma unroll 2
-        for (uint32_t j = j0; j < j1; j++) {
-            const float4 q = pts[j].xyz2;
-            const float4 l = pts[j].lim;
+        for (uint32_t i = 0; i < iters; i++) {
+            const float4 q = pp[3 * i].xyz2;
+            const float4 l = pp[3 * i].lim;
             const float along = q.x * sw[0] + q.y * sw[1] + q.z * sw[2];
-            const float lateral2 = fmax_f(q.w - along * along, 0.0f);
+            const float lateral2 = __builtin_fmaxf(q.w - along * along, 0.0f);
             const bool contact = (along > 0.0f) & (along <= l.x) & (lateral2 < l.y) & (along - l.z < nearest);
-            if (contact) nearest = fmin_f(nearest, fmax_f(along - sqrt_f(l.y - lateral2), 0.0f));
+            if (contact) nearest = __builtin_fminf(nearest, __builtin_fmaxf(along - sqrt_pos(l.y - lateral2), 0.0f));
         }
         part_near[part][c] = nearest;
     }
