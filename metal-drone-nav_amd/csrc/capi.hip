@@ -125,6 +125,11 @@ struct MdnSim {
         a.camera = camera; a.cells = cells; a.obs = obs; a.co = co; a.nco = nco; a.actions = actions; a.logp = logp; a.values = values;
         a.rewards = rewards; a.next_values = next_values; a.terminated = terminated; a.truncated = truncated;
         a.cfg = cfg; a.phys = phys; a.count = count; a.horizon = horizon;
+        a.recip_mass = 1.0 / double(phys.mass);  // IEEE fp64 division: the device's phys_recip values
+        for (int i = 0; i < 4; i++) {
+            a.recip_rise[i] = 1.0 / double(phys.rotor_time_constants_rising[i]);
+            a.recip_fall[i] = 1.0 / double(phys.rotor_time_constants_falling[i]);
+        }
         a.ext_means = nullptr; a.ext_log_std = nullptr; a.tick0 = 0; a.split = 0;
         a.sensor_dt = float(cfg.sensor_period) * phys.dt * float(cfg.substeps);
         a.inv_sensor_dt = 1.0 / double(std::max(a.sensor_dt, 1e-3f));

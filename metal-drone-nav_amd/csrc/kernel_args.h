@@ -36,6 +36,11 @@ struct RolloutArgs {
     uint8_t* truncated;
     MdnSimConfig cfg;
     MdnPhysicsParams phys;
+    // RN64 reciprocals of the plant's divisors (mass, rising and falling
+    // rotor time constants), computed on the host so that they arrive as
+    // uniform kernel arguments (scalar registers) instead of occupying
+    // vector registers for the whole launch
+    double recip_mass, recip_rise[4], recip_fall[4];
     uint32_t count;        // ticks in this launch
     uint32_t horizon;      // row blocks of the rollout buffers
     // Split ticks (policy evaluated outside the kernel, e.g. a wide actor):

@@ -486,7 +486,10 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         reinterpret_cast<float*>(&s_phys)[i] = reinterpret_cast<const float*>(&a.phys)[i];
     __syncthreads();
     const MdnPhysicsParams& P = s_phys;
-    const PhysRecip RP = phys_recip(a.phys);
+    PhysRecip RP;
+    RP.mass = a.recip_mass;
+#pragma unroll
+    for (int i = 0; i < 4; i++) { RP.rise[i] = a.recip_rise[i]; RP.fall[i] = a.recip_fall[i]; }
     const uint32_t N = C.n;
     const uint32_t lane = threadIdx.x % G, grp = threadIdx.x / G;
     const uint32_t n = blockIdx.x * E + grp;
@@ -503,8 +506,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     const float* RW;    // RAPTOR weights (RaptorWeights layout)
     const float* CAM;   // camera rays [pixel][3]
     if constexpr (W > 1) {
-        if constexpr (!X)
+        // (unrolled: a split-tick launch stages the weights once per tick,
+        // so their loads are kept in flight together)
+        if constexpr (!X) {
+#pragma unroll 8
             for (uint32_t i = threadIdx.x; i < D * HID; i += 64 * W) s_wt.aw[i] = a.actor_w1t[i];
+        }
         for (uint32_t i = threadIdx.x; i < RAPTOR_WORDS; i += 64 * W) s_wt.rw[i] = a.raptor[i];
         for (uint32_t i = threadIdx.x; i < 3 * PIX; i += 64 * W) s_wt.cam[i] = a.camera[i];
         __syncthreads();
