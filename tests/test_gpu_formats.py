@@ -197,3 +197,55 @@ def test_threat_evaluations(row):
     assert abs(rep["mean_speed"] - want["mean_speed_mps"]) <= 5e-3, rep
     assert abs(rep["peak_speed"] - want["peak_speed_mps"]) <= 1e-3, rep
     assert abs(rep["min_clearance"] - want["min_clearance_m"]) <= 1e-5, rep
+
+
+# Further published evaluations (evidence/inputs, copied to tests/golden/evidence):
+# the speed sweep of the clean-stress policy and the inference ablations and
+# controlled-threat matrix of the threat-joint policy (docs/BENCHMARKS.md:157-183
+# and evidence.py:1644-1654 name the checkpoints).
+EVIDENCE_POLICY = {"static-speed.csv": "clean_stress", "threat-joint-ablations.csv": "threat_joint",
+                   "threat-joint-controlled.csv": "threat_joint"}
+
+
+def evidence_rows():
+    import csv
+    out = []
+    for name in sorted(EVIDENCE_POLICY):
+        for r in csv.DictReader(open(os.path.join(GOLDEN, "evidence", name))):
+            out.append(dict(r, _file=name))
+    return out
+
+
+@pytest.mark.parametrize("row", evidence_rows(), ids=lambda r: (r["_file"][:12] + ":" + r["case_id"])[:56])
+def test_evidence_evaluations(row):
+    """79 more published evaluations with the same bar: outcome counts exact,
+    statistics to the printed digits (within a tick's shift of an arrival)."""
+    from mdnav import evaluate_threat
+    z = np.load(os.path.join(GOLDEN, "actors", EVIDENCE_POLICY[row["_file"]] + ".npz"))
+    cfg = z["config"].view(abi.SIM_CONFIG)[0]
+    if row["group"] == "controlled_threat":
+        kind = {"approach": 0, "crossing": 1}[row["threat_kind"]]
+        rep = evaluate_threat(z["actor"], int(row["mode"]), kind, float(row["threat_speed_mps"]),
+                              float(row["nominal_ttc_s"]), seed=int(row["seed"]),
+                              sensor_delay=int(row["sensor_delay_frames"]),
+                              command_delay=int(row["command_delay_steps"]), raptor=raptor_fixture()[0])
+    else:
+        rep = sim_evaluate(int(row["family"]), int(row["mode"]), z["actor"], speed=float(row["speed_mps"]),
+                           distance=float(row["distance_m"]), seed=int(row["seed"]),
+                           sensor_delay=int(row["sensor_delay_frames"]), wind=float(row["wind_param"]),
+                           noise=float(row["depth_noise_m"]), dropout=float(row["dropout_probability"]),
+                           command_delay=int(row["command_delay_steps"]),
+                           velocity_contract=int(cfg["velocity_contract"]), memory=int(cfg["geometry_memory"]),
+                           raptor=raptor_fixture()[0])[1]
+    want = {k: float(row[k]) for k in ("success", "collision", "timeout", "progress", "mean_goal_time_s",
+                                       "mean_speed_mps", "peak_speed_mps", "min_clearance_m")}
+    say("case %s: success %.6g/%.6g collision %.6g/%.6g goal %.6g/%.6g" % (
+        row["case_id"][:40], rep["success"], want["success"], rep["collision"], want["collision"],
+        rep["mean_goal_time"], want["mean_goal_time_s"]))
+    for k in ("success", "collision", "timeout"):
+        assert round(rep[k] * 128) == round(want[k] * 128), (k, rep[k], want[k])
+    assert abs(rep["mean_goal_time"] - want["mean_goal_time_s"]) <= 0.02, rep
+    assert abs(rep["progress"] - want["progress"]) <= 1e-3, rep
+    assert abs(rep["mean_speed"] - want["mean_speed_mps"]) <= 5e-3, rep
+    assert abs(rep["peak_speed"] - want["peak_speed_mps"]) <= 1e-3, rep
+    assert abs(rep["min_clearance"] - want["min_clearance_m"]) <= 1e-5, rep
