@@ -530,6 +530,7 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
     __shared__ float part[256];
     const uint32_t t = threadIdx.x;
     float s = 0.0f;
+#pragma unroll 16
     for (uint32_t i = t; i < P; i += 256) s += g[i] * g[i];
     part[t] = s;
     __syncthreads();
@@ -540,19 +541,46 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
     const float norm = sqrt_f(part[0] + 1.0e-20f);
     const float scale = min_f(1.0f, 0.5f / norm);
     const float b1 = 0.9f, b2 = 0.999f;
-    for (uint32_t i = t; i < P; i += 256) {
-        const float gi = g[i] * scale;
-        m[i] = b1 * m[i] + (1.0f - b1) * gi;
-        v[i] = b2 * v[i] + (1.0f - b2) * gi * gi;
-        const float mh = m[i] / a.c1, vh = v[i] / a.c2;
-        params[i] -= a.lr * mh / (sqrt_f(vh) + 1.0e-8f);
+    // Batches of ADAM_BATCH elements per thread: every load of a batch is
+    // issued before its stores (the buffers are distinct, but the compiler
+    // cannot know it), so a batch costs one memory latency, not one per
+    // element.  The per-element arithmetic is unchanged.
+    constexpr uint32_t ADAM_BATCH = 16;
+    for (uint32_t i0 = t; i0 < P; i0 += 256 * ADAM_BATCH) {
+        float gv[ADAM_BATCH], mv[ADAM_BATCH], vv[ADAM_BATCH], pv[ADAM_BATCH];
+#pragma unroll
+        for (uint32_t k = 0; k < ADAM_BATCH; k++) {
+            const uint32_t i = i0 + 256 * k;
+            if (i < P) { gv[k] = g[i]; mv[k] = m[i]; vv[k] = v[i]; pv[k] = params[i]; }
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < ADAM_BATCH; k++) {
+            const uint32_t i = i0 + 256 * k;
+            if (i < P) {
+                const float gi = gv[k] * scale;
+                const float mi = b1 * mv[k] + (1.0f - b1) * gi;
+                const float vi = b2 * vv[k] + (1.0f - b2) * gi * gi;
+                const float mh = mi / a.c1, vh = vi / a.c2;
+                m[i] = mi;
+                v[i] = vi;
+                params[i] = pv[k] - a.lr * mh / (sqrt_f(vh) + 1.0e-8f);
+            }
+        }
     }
     __syncthreads();
     if (!critic) {
         if (t < 4) params[L::LS + t] = clamp_f(params[L::LS + t], -2.0f, .5f);
-        for (uint32_t e = t; e < HID * D; e += 256) {
-            const uint32_t h = e / D, i = e % D;
-            a.actor_w1t[size_t(i) * HID + h] = params[e];
+        __syncthreads();  // the clamped log-std before the copy below reads the vector
+        for (uint32_t e0 = t; e0 < HID * D; e0 += 256 * ADAM_BATCH) {
+            float pv[ADAM_BATCH];
+#pragma unroll
+            for (uint32_t k = 0; k < ADAM_BATCH; k++)
+                if (e0 + 256 * k < HID * D) pv[k] = params[e0 + 256 * k];
+#pragma unroll
+            for (uint32_t k = 0; k < ADAM_BATCH; k++) {
+                const uint32_t e = e0 + 256 * k;
+                if (e < HID * D) a.actor_w1t[size_t(e % D) * HID + e / D] = pv[k];
+            }
         }
         if (t == 0) {
             const float* ms = a.grad + L::COUNT + C_COUNT;
@@ -562,9 +590,16 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
             a.metric_row[3] = ms[3] / float(a.b);
         }
     } else {
-        for (uint32_t e = t; e < HID * COBS; e += 256) {
-            const uint32_t h = e / COBS, i = e % COBS;
-            a.critic_w1t[size_t(i) * HID + h] = params[e];
+        for (uint32_t e0 = t; e0 < HID * COBS; e0 += 256 * ADAM_BATCH) {
+            float pv[ADAM_BATCH];
+#pragma unroll
+            for (uint32_t k = 0; k < ADAM_BATCH; k++)
+                if (e0 + 256 * k < HID * COBS) pv[k] = params[e0 + 256 * k];
+#pragma unroll
+            for (uint32_t k = 0; k < ADAM_BATCH; k++) {
+                const uint32_t e = e0 + 256 * k;
+                if (e < HID * COBS) a.critic_w1t[size_t(e % COBS) * HID + e / COBS] = pv[k];
+            }
         }
     }
 }
