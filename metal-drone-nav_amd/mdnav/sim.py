@@ -124,6 +124,8 @@ class Sim:
         a generated rehearsal world); an empty bank disables it."""
         w = np.ascontiguousarray(worlds, abi.WORLD).reshape(-1)
         sch = np.ascontiguousarray(schedule, np.uint32)
+        if w.size and (sch.ndim != 2 or sch.shape[0] != int(self.cfg["n"])):
+            raise MdnError("bank schedule must be [n_envs][stride], got shape %s" % (sch.shape,))
         stride = int(sch.shape[-1]) if sch.size else 0
         check(lib().mdn_sim_set_bank(self.h, w.ctypes.data_as(ctypes.c_void_p), w.size,
                                      sch.ctypes.data_as(ctypes.c_void_p), stride))
