@@ -215,6 +215,16 @@ int mdn_checkpoint_read(const char* path, MdnCheckpointHeader* header, float* ac
 int mdn_navpol_read(const char* path, MdnNavPolicyMeta* meta, float* weights, uint64_t count, uint64_t* source_hash);
 int mdn_navpol_write(const char* path, const MdnNavPolicyMeta* meta, const float* weights, uint64_t count,
                      uint64_t source_hash);
+/* Wide deployed policy NAVWID4 (navigation_wide_deployment.hpp:15-40, written
+ * by navigation_export_wide.py:40-47): magic, the 56-byte metadata (version
+ * 4, 184 inputs, hidden width H in 64..8192, 189 H + 8 weights), the 32-byte
+ * camera contract, the weights of the 184-H-4 actor, NAVSRC4 + FNV-1a 64 of
+ * the source checkpoint, no trailing bytes.  Read with weights = NULL for
+ * the header alone. */
+int mdn_navwid_read(const char* path, MdnNavPolicyMeta* meta, MdnSensorContract* camera, float* weights,
+                    uint64_t count, uint64_t* source_hash);
+int mdn_navwid_write(const char* path, const MdnNavPolicyMeta* meta, const MdnSensorContract* camera,
+                     const float* weights, uint64_t count, uint64_t source_hash);
 /* fnv1a64_file (deployment.hpp:122-136). */
 int mdn_fnv1a64_file(const char* path, uint64_t* hash);
 

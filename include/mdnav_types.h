@@ -198,6 +198,14 @@ typedef struct MdnBankControl {
 } MdnBankControl;
 #define MDN_BANK_REHEARSAL 0xffffffffu /* schedule slot: a generated rehearsal world */
 
+/* Camera contract of a wide deployed policy (nav_deployment::SensorContract,
+ * deployment.hpp:54-63), 32 bytes: profile 1 legacy, 2 native. */
+typedef struct MdnSensorContract {
+    uint32_t profile_id;
+    float tan_h, tan_v, mount_x_m, min_range_m, max_range_m, noise_m;
+    uint32_t reserved;
+} MdnSensorContract;
+
 /* Rollout metrics of cpu_reference.hpp:55-70. */
 typedef struct MdnMetrics {
     double wall_seconds;
@@ -221,6 +229,7 @@ static_assert(sizeof(MdnTaskConfig) == 144, "NavigationTaskConfig layout");
 static_assert(sizeof(MdnTaskControl) == 148, "NavigationTaskControl layout");
 static_assert(sizeof(MdnTaskState) == 192, "NavigationTaskState layout");
 static_assert(sizeof(MdnBankControl) == 16, "ChallengeBankControl layout");
+static_assert(sizeof(MdnSensorContract) == 32, "SensorContract layout");
 #endif
 
 #endif /* MDNAV_TYPES_H */

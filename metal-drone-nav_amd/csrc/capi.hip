@@ -1579,4 +1579,79 @@ int mdn_navpol_write(const char* path, const MdnNavPolicyMeta* meta, const float
     return MDN_OK;
 }
 
+// navigation_wide_deployment.hpp:92-105 (WideNavigationPolicy::valid_metadata /
+// valid_sensor with deployment.hpp:66-70 for the native camera)
+static bool valid_navwid(const MdnNavPolicyMeta& m, const MdnSensorContract& c) {
+    const bool meta = m.version == 4 && m.observation_count == 184 && m.hidden_count >= 64 && m.hidden_count <= 8192 &&
+                      m.action_count == 4 && m.policy_mode == 17 && m.weight_count == 189 * m.hidden_count + 8 &&
+                      std::isfinite(m.max_speed_mps) && m.max_speed_mps > 0 && m.max_speed_mps <= 10 &&
+                      m.sensor_rows == 16 && m.sensor_columns == 20 && std::fabs(m.range_max_m - 12) < 1e-6f &&
+                      std::fabs(m.navigation_period_s - .05f) < 1e-6f &&
+                      std::fabs(m.native_period_s - .01f) < 1e-6f && m.memory_frames == 8 &&
+                      m.body_frame == 0x00554C46u;
+    const bool legacy = c.profile_id == 1 && std::fabs(c.tan_h - 1) < 1e-6f && std::fabs(c.tan_v - .75f) < 1e-6f &&
+                        std::fabs(c.mount_x_m) < 1e-6f;
+    const bool native = c.profile_id == 2 && std::fabs(c.tan_h - 1.0f) < 1e-6f && std::fabs(c.tan_v - 0.8f) < 1e-6f &&
+                        std::fabs(c.mount_x_m - 0.08f) < 1e-6f;
+    return meta && (legacy || native) && std::fabs(c.min_range_m - .03f) < 1e-6f &&
+           std::fabs(c.max_range_m - 12) < 1e-6f && c.noise_m == 0 && c.reserved == 0;
+}
+
+int mdn_navwid_read(const char* path, MdnNavPolicyMeta* meta, MdnSensorContract* camera, float* weights,
+                    uint64_t count, uint64_t* source_hash) {
+    if (!path || !meta || !camera) return fail(MDN_E_ARG, "mdn_navwid_read: null argument");
+    File file(path, "rb");
+    if (!file.f) return fail(MDN_E_ARG, std::string("cannot open wide policy: ") + path);
+    char magic[8];
+    if (!file.read(magic, 8) || std::memcmp(magic, "NAVWID4\0", 8) != 0)
+        return fail(MDN_E_ARG, "wide policy magic mismatch");
+    MdnNavPolicyMeta m;
+    MdnSensorContract c;
+    if (!file.read(&m, sizeof(m))) return fail(MDN_E_ARG, "truncated wide metadata");
+    if (!file.read(&c, sizeof(c))) return fail(MDN_E_ARG, "truncated camera contract");
+    if (!valid_navwid(m, c)) return fail(MDN_E_ARG, "unsupported wide policy contract");
+    *meta = m;
+    *camera = c;
+    if (!weights) return MDN_OK;  // header only: the caller sizes the weights from meta
+    if (count != m.weight_count) return fail(MDN_E_ARG, "wide policy weight count differs from the buffer");
+    std::vector<float> w(m.weight_count);
+    if (!file.read(w.data(), w.size() * 4)) return fail(MDN_E_ARG, "truncated wide weights");
+    for (float v : w)
+        if (!std::isfinite(v)) return fail(MDN_E_ARG, "non-finite wide weight");
+    char tag[8];
+    uint64_t hash = 0;
+    if (!file.read(tag, 8) || std::memcmp(tag, "NAVSRC4\0", 8) != 0 || !file.read(&hash, 8))
+        return fail(MDN_E_ARG, "missing wide provenance");
+    if (!file.at_end()) return fail(MDN_E_ARG, "wide policy has trailing bytes");
+    std::memcpy(weights, w.data(), w.size() * 4);
+    if (source_hash) *source_hash = hash;
+    return MDN_OK;
+}
+
+int mdn_navwid_write(const char* path, const MdnNavPolicyMeta* meta, const MdnSensorContract* camera,
+                     const float* weights, uint64_t count, uint64_t source_hash) {
+    if (!path || !meta || !camera || !weights) return fail(MDN_E_ARG, "mdn_navwid_write: null argument");
+    if (!valid_navwid(*meta, *camera) || count != meta->weight_count)
+        return fail(MDN_E_ARG, "invalid wide policy contract or weight count");
+    for (uint64_t i = 0; i < count; i++)
+        if (!std::isfinite(weights[i])) return fail(MDN_E_ARG, "non-finite actor parameter");
+    const std::string temp = std::string(path) + ".tmp";
+    {
+        File file(temp.c_str(), "wb");
+        if (!file.f) return fail(MDN_E_ARG, "cannot create wide policy: " + temp);
+        const bool ok = file.write("NAVWID4\0", 8) && file.write(meta, sizeof(*meta)) &&
+                        file.write(camera, sizeof(*camera)) && file.write(weights, size_t(count) * 4) &&
+                        file.write("NAVSRC4\0", 8) && file.write(&source_hash, 8) && std::fflush(file.f) == 0;
+        if (!ok) {
+            std::remove(temp.c_str());
+            return fail(MDN_E_ARG, "wide policy write failed");
+        }
+    }
+    if (std::rename(temp.c_str(), path) != 0) {
+        std::remove(temp.c_str());
+        return fail(MDN_E_ARG, std::string("cannot replace wide policy: ") + path);
+    }
+    return MDN_OK;
+}
+
 }  // extern "C"

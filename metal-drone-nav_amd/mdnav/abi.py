@@ -101,6 +101,10 @@ TASK_DOMAIN_SEED = 0x3f84d5b5
 
 assert RUNTIME_CONFIG.itemsize == 56 and DOMAIN_SAMPLE.itemsize == 68
 assert TASK_CONFIG.itemsize == 144 and TASK_CONTROL.itemsize == 148 and TASK_STATE.itemsize == 192
+# nav_deployment::SensorContract (deployment.hpp:54-63)
+SENSOR_CONTRACT = np.dtype([("profile_id", u4), ("tan_h", f4), ("tan_v", f4), ("mount_x_m", f4),
+                            ("min_range_m", f4), ("max_range_m", f4), ("noise_m", f4), ("reserved", u4)])
+assert SENSOR_CONTRACT.itemsize == 32
 assert CHECKPOINT_HEADER.itemsize == 136 and NAV_POLICY_META.itemsize == 56
 assert PHYSICS_STATE.itemsize == 68 and PHYSICS_PARAMS.itemsize == 352
 assert RAPTOR_WEIGHTS.itemsize == 8336 and WORLD.itemsize == 676

@@ -50,6 +50,51 @@ def write_navigation_policy(path, weights, meta=None, source_hash=0):
     check(lib().mdn_navpol_write(_path(path), ptr(meta), ptr(w), w.size, ctypes.c_uint64(source_hash)))
 
 
+def read_wide_policy(path):
+    """WideNavigationPolicy::load (navigation_wide_deployment.hpp:15-40):
+    (metadata, camera contract, weights[189 H + 8], source_hash)."""
+    meta = np.zeros((), abi.NAV_POLICY_META)
+    cam = np.zeros((), abi.SENSOR_CONTRACT)
+    check(lib().mdn_navwid_read(_path(path), ptr(meta), ptr(cam), None, 0, None))
+    w = np.zeros(int(meta["weight_count"]), np.float32)
+    h = ctypes.c_uint64()
+    check(lib().mdn_navwid_read(_path(path), ptr(meta), ptr(cam), ptr(w), w.size, ctypes.byref(h)))
+    return meta, cam, w, h.value
+
+
+def export_wide_policy(checkpoint, destination):
+    """navigation_export_wide.py:11-47: the 184-H-4 actor of a guided PPOFIX1
+    checkpoint (versions 6, 8, 9, 10; mode 17 or 22; 5 substeps, sensor period
+    1; body-velocity contract 1 with the geometry memory) as NAVWID4, with the
+    legacy camera (native for version 10) and the checkpoint's FNV-1a 64."""
+    import math
+    data = open(checkpoint, "rb").read()
+    if len(data) < 136 or data[:8] != b"PPOFIX1\0":
+        raise ValueError("Expected a PPOFIX1 checkpoint")
+    h = np.frombuffer(data[:136], abi.CHECKPOINT_HEADER)[0]
+    version, actor_count = int(h["version"]), int(h["actor_count"])
+    width, rem = divmod(actor_count - 8, 189)
+    if version not in (6, 8, 9, 10) or rem or width not in (64, 256, 768, 2560, 5120):
+        raise ValueError("Unsupported guided 184/H/4 actor or checkpoint version")
+    c = h["config"]
+    if int(c["mode"]) not in (17, 22) or int(c["substeps"]) != 5 or int(c["sensor_period"]) != 1:
+        raise ValueError("Unsupported action map or control cadence")
+    speed = float(c["speed"])
+    if int(c["velocity_contract"]) != 1 or int(c["geometry_memory"]) != 1 or not (math.isfinite(speed) and
+                                                                                      0 < speed <= 10):
+        raise ValueError("Unsupported body-velocity or geometry-memory contract")
+    weights = np.frombuffer(data[136:136 + 4 * actor_count], np.float32)
+    meta = default_navigation_metadata(speed)
+    meta["version"], meta["hidden_count"], meta["weight_count"] = 4, width, actor_count
+    cam = np.zeros((), abi.SENSOR_CONTRACT)
+    native = version == 10
+    cam["profile_id"], cam["tan_h"], cam["tan_v"] = (2 if native else 1), 1.0, (0.8 if native else 0.75)
+    cam["mount_x_m"], cam["min_range_m"], cam["max_range_m"] = (0.08 if native else 0.0), 0.03, 12.0
+    w = np.ascontiguousarray(weights)
+    check(lib().mdn_navwid_write(_path(destination), ptr(meta), ptr(cam), ptr(w), w.size,
+                                 ctypes.c_uint64(fnv1a64_file(checkpoint))))
+
+
 def read_checkpoint(path, actor=True):
     """(header, actor parameters or None) of a PPOFIX1 file, versions 3-10."""
     h = np.zeros((), abi.CHECKPOINT_HEADER)

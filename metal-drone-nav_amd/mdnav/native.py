@@ -25,7 +25,8 @@ EXPORTS = [
     "mdn_lppo_metric_mean", "mdn_lppo_optimizer_step", "mdn_lppo_collect", "mdn_lppo_means",
     "mdn_op_check_division", "mdn_ppo_save_checkpoint", "mdn_ppo_load_checkpoint", "mdn_checkpoint_read",
     "mdn_navpol_read", "mdn_navpol_write", "mdn_fnv1a64_file", "mdn_sim_set_runtime", "mdn_sim_get_runtime",
-    "mdn_sim_set_tasks", "mdn_sim_get_tasks", "mdn_task_default_config", "mdn_domain_stress_range", "mdn_sim_set_bank",
+    "mdn_sim_set_tasks", "mdn_sim_get_tasks", "mdn_task_default_config", "mdn_domain_stress_range", "mdn_sim_set_bank", "mdn_navwid_read",
+    "mdn_navwid_write",
 ]
 
 P = ctypes.c_void_p
@@ -83,6 +84,8 @@ def lib():
         _sig(L, "mdn_task_default_config", I32, U32, U32, F32, P)
         _sig(L, "mdn_domain_stress_range", I32, P)
         _sig(L, "mdn_sim_set_bank", I32, P, P, U32, P, U32)
+        _sig(L, "mdn_navwid_read", I32, ctypes.c_char_p, P, P, P, U64, ctypes.POINTER(U64))
+        _sig(L, "mdn_navwid_write", I32, ctypes.c_char_p, P, P, P, U64, U64)
         _sig(L, "mdn_ppo_create", I32, P, U32, U32, ctypes.POINTER(P))
         _sig(L, "mdn_ppo_destroy", None, P)
         _sig(L, "mdn_ppo_rollout_update", I32, P, U32)

@@ -25,6 +25,8 @@
 #include "physics_domain.hpp"
 #include "navigation_runtime.hpp"
 #include "navigation_tasks.hpp"
+#include "deployment.hpp"
+#include "navigation_wide_deployment.hpp"
 #include "mdnav_types.h"
 
 static_assert(sizeof(WWorld) == sizeof(MdnWorld), "world layout");
@@ -36,6 +38,8 @@ static_assert(sizeof(NavigationRuntimeConfig) == sizeof(MdnRuntimeConfig), "runt
 static_assert(sizeof(NavigationTaskConfig) == sizeof(MdnTaskConfig), "task config layout");
 static_assert(sizeof(NavigationTaskControl) == sizeof(MdnTaskControl), "task control layout");
 static_assert(sizeof(NavigationTaskState) == sizeof(MdnTaskState), "task state layout");
+static_assert(sizeof(nav_deployment::Metadata) == sizeof(MdnNavPolicyMeta), "NAV metadata layout");
+static_assert(sizeof(nav_deployment::SensorContract) == sizeof(MdnSensorContract), "sensor contract layout");
 
 extern "C" {
 
@@ -59,6 +63,19 @@ int ref_task_default_config(MdnTaskConfig* c, uint32_t stage, uint32_t family, f
 uint32_t ref_generate_task(MdnWorld* w, MdnTaskState* t, uint32_t* rng, const MdnTaskConfig* c) {
     return navigation_generate_task(*reinterpret_cast<WWorld*>(w), *reinterpret_cast<NavigationTaskState*>(t), *rng,
                                     *reinterpret_cast<const NavigationTaskConfig*>(c));
+}
+// WideNavigationPolicy::load and raw_mean (navigation_wide_deployment.hpp:15-66)
+int ref_navwid_load(const char* path, MdnNavPolicyMeta* meta, MdnSensorContract* camera, uint64_t* hash,
+                    const float* obs, uint32_t n, float* means) {
+    nav_deployment::WideNavigationPolicy p;
+    std::string error;
+    if (!p.load(path, &error)) return 0;
+    std::memcpy(meta, &p.metadata(), sizeof(*meta));
+    std::memcpy(camera, &p.sensor_contract(), sizeof(*camera));
+    *hash = p.source_checkpoint_hash();
+    for (uint32_t i = 0; i < n; i++)
+        if (!p.raw_mean(obs + size_t(i) * 184, means + size_t(i) * 4)) return -1;
+    return 1;
 }
 void ref_task_apply_start(const MdnTaskState* t, MdnPhysicsState* s) {
     navigation_task_apply_start(*reinterpret_cast<const NavigationTaskState*>(t), *reinterpret_cast<RLPhysicsState*>(s));

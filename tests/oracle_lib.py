@@ -149,6 +149,7 @@ def ref(actor_obs=181):
         _sig(lib, "ref_generate_task", U32, P, P, ctypes.POINTER(U32), P)
         _sig(lib, "ref_task_apply_start", None, P, P)
         _sig(lib, "ref_task_step", None, P, P, P, P, P, U32, U32, P)
+        _sig(lib, "ref_navwid_load", ctypes.c_int, ctypes.c_char_p, P, P, ctypes.POINTER(U64), P, U32, P)
         _refs[actor_obs] = lib
     return _refs[actor_obs]
 

@@ -109,3 +109,72 @@ def test_deployment_probe_parity():
         ref(184).ref_actor_forward(ptr(w), ptr(obs[k]), ptr(rh), ptr(rm))
         worst = max(worst, float(np.abs(rm - m[k]).max()))
     assert worst < 2e-5, worst
+
+
+# ---------------------------------------------------------------- NAVWID4
+def test_wide_policy_export_matches_reference_loader(tmp_path):
+    """navigation_export_wide.py's export of the trained guided checkpoint
+    (184-64-4) as NAVWID4, read back here and by the reference's own
+    WideNavigationPolicy::load (navigation_wide_deployment.hpp, built into
+    oracle/_ref): metadata, camera contract, weights (the checkpoint's
+    actor) and the FNV-1a provenance agree, and the reference's raw_mean on
+    random observations matches the oracle's forward of the same actor."""
+    import ctypes
+    from oracle_lib import ref, ref_available
+    # the trained checkpoint was saved in training mode 0, which the export
+    # refuses (navigation_export_wide.py:22-24); a copy with its config mode
+    # set to 22 (training through the deployed map) is exported
+    src = os.path.join(GOLDEN, "guided-table-memory.bin.best")
+    with pytest.raises(ValueError):
+        formats.export_wide_policy(src, str(tmp_path / "refused.bin"))
+    data = bytearray(open(src, "rb").read())
+    data[56:60] = np.uint32(22).tobytes()
+    ckpt = str(tmp_path / "mode22.bin")
+    open(ckpt, "wb").write(bytes(data))
+    out = str(tmp_path / "wide.bin")
+    formats.export_wide_policy(ckpt, out)
+    meta, cam, w, h = formats.read_wide_policy(out)
+    _, actor = formats.read_checkpoint(ckpt)
+    assert int(meta["version"]) == 4 and int(meta["hidden_count"]) == 64 and w.size == 189 * 64 + 8
+    assert np.array_equal(w, actor) and h == formats.fnv1a64_file(ckpt)
+    assert int(cam["profile_id"]) == 1 and abs(float(cam["tan_v"]) - 0.75) < 1e-7
+    if not ref_available():
+        pytest.skip("oracle/_ref not built (needs the reference tree)")
+    rng = np.random.default_rng(11)
+    obs = rng.uniform(0, 1, (16, 184)).astype(np.float32)
+    obs[:, 181:] = rng.normal(0, 0.5, (16, 3))
+    m2, c2 = np.zeros((), abi.NAV_POLICY_META), np.zeros((), abi.SENSOR_CONTRACT)
+    h2 = ctypes.c_uint64()
+    means = np.zeros((16, 4), np.float32)
+    assert ref().ref_navwid_load(out.encode(), ptr(m2), ptr(c2), ctypes.byref(h2), ptr(obs), 16, ptr(means)) == 1
+    assert m2.tobytes() == meta.tobytes() and c2.tobytes() == cam.tobytes() and h2.value == h
+    hid = np.zeros((16, 64), np.float32)
+    mine = np.zeros((16, 4), np.float32)
+    oracle().orc_actor_forward_batch(ptr(w), ptr(obs), 184, 64, 16, ptr(hid), ptr(mine))
+    assert np.abs(mine - means).max() < 1e-5
+
+
+def test_wide_policy_round_trip_and_rejections(tmp_path):
+    """A 184-256-4 actor written and read back bit for bit; the reader
+    rejects what WideNavigationPolicy::load rejects."""
+    rng = np.random.default_rng(5)
+    w = rng.normal(0, 0.1, 189 * 256 + 8).astype(np.float32)
+    meta = formats.default_navigation_metadata(2.0)
+    meta["version"], meta["hidden_count"], meta["weight_count"] = 4, 256, w.size
+    cam = np.zeros((), abi.SENSOR_CONTRACT)
+    cam["profile_id"], cam["tan_h"], cam["tan_v"], cam["min_range_m"], cam["max_range_m"] = 1, 1.0, 0.75, 0.03, 12.0
+    path = str(tmp_path / "w.bin")
+    from mdnav.native import lib
+    assert lib().mdn_navwid_write(path.encode(), ptr(meta), ptr(cam), ptr(w), w.size, 77) == 0
+    m2, c2, w2, h2 = formats.read_wide_policy(path)
+    assert np.array_equal(w2, w) and h2 == 77 and m2.tobytes() == meta.tobytes()
+    data = open(path, "rb").read()
+    for bad in (data + b"\0", b"NAVWID5\0" + data[8:], data[:100]):
+        open(path, "wb").write(bad)
+        with pytest.raises(Exception):
+            formats.read_wide_policy(path)
+    w[3] = np.nan
+    assert lib().mdn_navwid_write(path.encode(), ptr(meta), ptr(cam), ptr(w), w.size, 77) != 0
+    w[3] = 0.0
+    meta["policy_mode"] = 2
+    assert lib().mdn_navwid_write(path.encode(), ptr(meta), ptr(cam), ptr(w), w.size, 77) != 0
