@@ -105,7 +105,11 @@ __device__ __forceinline__ bool task_inside(V p, const float* lo, const float* h
     return p.x >= lo[0] && p.x <= hi[0] && p.y >= lo[1] && p.y <= hi[1] && p.z >= lo[2] && p.z <= hi[2];
 }
 // navigation_tasks.hpp:243-255: clearance of the static scene along a
-// segment, sampled at most 5 cm apart
+// segment, sampled at most 5 cm apart.  The episode kernel runs one
+// wavefront per env with every lane on the same values; the samples are
+// split over the 64 lanes and their minimum taken with xor shuffles (every
+// clearance is finite and none is -0, so the minimum does not depend on the
+// order).
 __device__ float task_segment_clearance(const float* w, uint32_t count, V a, V b) {
     const V d = sub3(b, a);
     const float distance = len3(d);
@@ -113,10 +117,12 @@ __device__ float task_segment_clearance(const float* w, uint32_t count, V a, V b
     if (samples < 1u) samples = 1u;
     if (samples > 512u) return -1e6f;
     float minimum = 1e20f;
-    for (uint32_t k = 0; k <= samples; k++) {
+    for (uint32_t k = threadIdx.x % 64u; k <= samples; k += 64u) {
         const float t = float(k) / float(samples);
         minimum = fmin_f(minimum, clearance_at(w, count, add3(a, mul3(d, t)), 0.0f));
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) minimum = fmin_f(minimum, __shfl_xor(minimum, off, 64));
     return minimum;
 }
 // navigation_tasks.hpp:257-263 over 2 to 4 points

@@ -202,10 +202,13 @@ __global__ __launch_bounds__(64) void reset_kernel(RolloutArgs a) {
 // velocity, initial distance, wind), in the reference's order.  Runs after the reset
 // kernel (first: every env) and after each launch that may reset envs (an
 // env with steps == 0 was reset by it; an evaluation never restarts one).
+// One wavefront per env: every lane computes the same values (and stores
+// the same words), except the task generator's segment clearances, whose
+// samples the lanes share.
 __global__ __launch_bounds__(64) void episode_kernel(EpisodeArgs a) {
-    const uint32_t n = blockIdx.x * 64 + threadIdx.x;
+    const uint32_t n = blockIdx.x;
     const uint32_t N = a.cfg.n;
-    if (n >= N) return;
+    if (n >= N) return;  // uniform over the wavefront
     Run r;
     load_run(a.run, N, n, r);
     if (!a.first && r.steps != 0u) return;
@@ -1120,7 +1123,7 @@ extern "C" {
 
 hipError_t nav_launch_episode(const nav::EpisodeArgs* a, hipStream_t stream) {
     if (a->cfg.n == 0) return hipSuccess;
-    hipLaunchKernelGGL(nav::episode_kernel, dim3((a->cfg.n + 63) / 64), dim3(64), 0, stream, *a);
+    hipLaunchKernelGGL(nav::episode_kernel, dim3(a->cfg.n), dim3(64), 0, stream, *a);
     return hipGetLastError();
 }
 
