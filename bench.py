@@ -184,6 +184,10 @@ def main():
     ap.add_argument("--geometry-memory", action="store_true",
                     help="with the 184-input actor: the history-aware hint (8-frame range and pose rings, 85 "
                          "candidate sweeps) from the memory kernel, one env launch and one memory launch per tick")
+    ap.add_argument("--task-training", action="store_true",
+                    help="the reference's task training loop (navigation_training.hpp:117-131): stage-2 clutter "
+                         "tasks of family 12 with per-episode plants at amplitude 1, mode 22, guided actor with the "
+                         "geometry memory, one tick per launch with the per-episode kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=["small", "large", "stress"], default="small",
                     help="small: 8,192 envs x 128 ticks, 181-64-4 actor (the headline metric); large: 8,192 envs x "
@@ -194,6 +198,8 @@ def main():
                     help="run only the plain copy kernel over BYTES (reads BYTES, writes BYTES per launch); "
                          "its FETCH_SIZE/WRITE_SIZE readings scale the rollout kernel's counters to bytes")
     args = ap.parse_args()
+    if args.task_training:
+        args.actor_obs, args.geometry_memory, args.no_cpu_baseline = 184, True, True
     args.actor_obs_set = args.actor_obs is not None
     if args.actor_obs is None:
         args.actor_obs = 184 if args.geometry_memory else 181
@@ -219,8 +225,16 @@ def main():
     epochs, minibatch = (1, N * T // 4) if args.schedule == "baseline" else (2, 256)
     cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0,
                              geometry_memory=1 if args.geometry_memory else 0)
+    if args.task_training:  # navigation_training.hpp:119-123
+        cfg = abi.default_config(n=N, family=12, mode=22, speed=1.5, distance=8.0, max_steps=400, geometry_memory=1,
+                                 entropy_coef=0.001, learning_rate=0.0001)
     log("bench: creating sim N=%d T=%d schedule=%s" % (N, T, args.schedule))
     sim = Sim(cfg, T, lanes=args.lanes, actor_obs=args.actor_obs)
+    if args.task_training:
+        from mdnav import task_runtime, task_settings
+        sim.set_runtime(task_runtime(1.0))
+        sim.set_tasks(task_settings(2, 12))
+        sim.reset()
     ppo = PPOTrainer(sim, epochs, minibatch)
     it = 0
     for _ in range(args.warmup):
@@ -243,7 +257,7 @@ def main():
     log("bench: timed %d iterations in %.3f s (GPU %.3f s)" % (args.steps, wall, gpu_s))
 
     kernels = {}
-    for name in ("rollout", "memory", "gae", "normalize", "rows", "grads", "adam"):
+    for name in ("rollout", "memory", "episode", "gae", "normalize", "rows", "grads", "adam"):
         ms, n = sim.kernel_time(name)
         kernels[name] = {"total_ms": round(ms, 4), "launches": n, "avg_ms": round(ms / n, 5) if n else None}
     roll = kernels["rollout"]
@@ -288,9 +302,12 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic: seeded procedural worlds (reference family 1), random-init policy (seed 1789)",
-        "config": {"workload": "static-box world, %d envs x %d ticks, %s actor %d-64-4%s, %s PPO schedule"
-                               % (N, T, "small" if args.actor_obs == 181 else "guided", args.actor_obs,
-                                  " with the geometry-memory hint" if args.geometry_memory else "", args.schedule),
+        "config": {"workload": ("task training: stage-2 clutter tasks (family 12) with per-episode plants, mode 22, "
+                                "%d envs x %d ticks, guided actor 184-64-4 with the geometry-memory hint, %s PPO "
+                                "schedule" % (N, T, args.schedule) if args.task_training else
+                                "static-box world, %d envs x %d ticks, %s actor %d-64-4%s, %s PPO schedule"
+                                % (N, T, "small" if args.actor_obs == 181 else "guided", args.actor_obs,
+                                   " with the geometry-memory hint" if args.geometry_memory else "", args.schedule)),
                    "envs": N, "horizon": T, "family": 1, "rays": 320, "actor": "%d-64-4" % args.actor_obs,
                    "critic": "32-64-1",
                    "epochs": epochs, "minibatch": minibatch, "lanes_per_env": args.lanes,
