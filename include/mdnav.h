@@ -148,7 +148,9 @@ int mdn_sim_get_runtime(const MdnSim* sim, MdnRuntimeConfig* runtime);
  * config.generation_version 1 is the reference's current generator; 0 is
  * the generator before clutter goals were conditioned on the goal bounds
  * (the version of the reference's published goal-arrival evidence).  Takes
- * effect at the next mdn_sim_reset. */
+ * effect at the next mdn_sim_reset.  Enabling tasks while a challenge bank is
+ * set returns MDN_E_ARG (the two cannot both own the world,
+ * navigation_training.hpp:19). */
 int mdn_sim_set_tasks(MdnSim* sim, const MdnTaskControl* tasks);
 int mdn_sim_get_tasks(const MdnSim* sim, MdnTaskControl* tasks);
 /* Frozen challenge bank: Sim::bank_worlds / bank_schedule / bank_control
@@ -158,9 +160,13 @@ int mdn_sim_get_tasks(const MdnSim* sim, MdnTaskControl* tasks);
  * slot (0 at mdn_sim_reset, tick + 1 after a reset at tick) and replaces the
  * world, wind and initial distance (sim.metal:95-121); every row records
  * the env's level (MDN_BUF_BANK_TRANSITION_IDS).  count = 0 disables it.
- * Upload MDN_BUF_BANK_SCHEDULE to change the schedule between rollouts. */
+ * Upload MDN_BUF_BANK_SCHEDULE to change the schedule between rollouts.
+ * Returns MDN_E_ARG for count > 0 while navigation tasks are enabled. */
 int mdn_sim_set_bank(MdnSim* sim, const MdnWorld* worlds, uint32_t count, const uint32_t* schedule,
                      uint32_t schedule_stride);
+/* Sim::bank_control (ChallengeBankControl, main.mm:511-514) as
+ * navigation_training::configure reads it (navigation_training.hpp:19). */
+int mdn_sim_get_bank(const MdnSim* sim, MdnBankControl* bank);
 /* navigation_task_default_config (navigation_tasks.hpp:99-140) and
  * rl_physics_domain_stress_range (physics_domain.hpp:37-40). */
 int mdn_task_default_config(uint32_t stage, uint32_t family, float difficulty, MdnTaskConfig* out);
@@ -279,6 +285,68 @@ int mdn_op_gae(uint32_t horizon, uint32_t n, const float* rewards, const float* 
                const uint8_t* terminated, const uint8_t* truncated, float gamma, float lambda, float* advantages,
                float* returns);
 int mdn_op_normalize(float* advantages, uint64_t count, float epsilon);
+
+/* fixed_ppo's operators (ppo.hpp:24-326), batched on the GPU over host
+ * arrays.  The reference's header functions take one sample; these take
+ * `batch` rows of the same layouts and return what a loop over the rows of
+ * the header function returns (within the fp32 tolerance of its libm
+ * transcendentals: tanh and exp are this library's own).  Parameter vectors
+ * use the flat layouts of ppo.hpp:35-45 at any input width D (1..1024) and
+ * hidden width H (1..8192, the reference's FIXED_PPO_*_DIM):
+ * actor W1[H][D], b1[H], W2[4][H], b2[4], log_std[4]; critic W1[H][D], b1[H],
+ * w2[H], b2.
+ *
+ * fixed_ppo::actor_forward (ppo.hpp:65-80): obs[batch][D] -> hidden[batch][H]
+ * (may be NULL) and mean[batch][4]; an input width of 184 (or 824) adds the
+ * last three inputs, the geometry-prior hint, to the first three means
+ * (ppo.hpp:30-34, 77). */
+int mdn_op_actor_forward(const float* params, uint32_t obs_dim, uint32_t hidden_dim, const float* obs, uint64_t batch,
+                         float* hidden, float* means);
+/* fixed_ppo::critic_forward (ppo.hpp:82-93): obs[batch][D] -> hidden[batch][H]
+ * (may be NULL) and values[batch]. */
+int mdn_op_critic_forward(const float* params, uint32_t obs_dim, uint32_t hidden_dim, const float* obs, uint64_t batch,
+                          float* hidden, float* values);
+/* fixed_ppo::gaussian_log_prob (ppo.hpp:95-103) per row of actions[batch][4]
+ * and means[batch][4]; log_std is one shared [4] (log_std_stride 0) or
+ * per row [batch][4] (stride 4). */
+int mdn_op_gaussian_log_prob(const float* actions, const float* means, const float* log_std, uint32_t log_std_stride,
+                             uint64_t batch, float* logp);
+/* fixed_ppo::sample_loss_and_grad (ppo.hpp:144-181) per row: the row's
+ * action, mean, log_std (shared or per row as above), old log-probability,
+ * old value (unused, as in the reference), value, advantage and target
+ * return, with the shared batch_size, clip, value and entropy coefficients
+ * -> d_mean[batch][4], d_log_std[batch][4], d_value[batch] and
+ * losses[batch][4] = PpoLoss {policy, value, entropy, ratio}. */
+int mdn_op_sample_loss_and_grad(const float* actions, const float* means, const float* log_std,
+                                uint32_t log_std_stride, const float* old_logp, const float* old_values,
+                                const float* values, const float* advantages, const float* returns, uint64_t batch,
+                                float batch_size, float clip_epsilon, float value_coefficient,
+                                float entropy_coefficient, float* d_mean, float* d_log_std, float* d_value,
+                                float* losses);
+/* fixed_ppo::adam_update (ppo.hpp:310-324): params, first and second moments
+ * updated in place; bias corrections 1 - beta^step as the reference computes
+ * them (float pow on the host). */
+int mdn_op_adam_update(float* params, const float* grad, float* first, float* second, uint64_t count, uint64_t step,
+                       float learning_rate, float beta1, float beta2, float epsilon, float weight_decay);
+/* fixed_ppo::run_cpu_self_tests (ppo.hpp:204-267) run through the operators
+ * above on the GPU: finite differences on the four surrogate branches, the
+ * value derivative and Adam's first step.  *passed = 1 when every check is
+ * within `tolerance` (the reference's default is 2e-3). */
+int mdn_op_ppo_self_tests(float tolerance, int* passed);
+
+/* navigation_training::validate_rollout (navigation_training.hpp:27-35):
+ * every env's task state is valid with generation status ready and its
+ * plant mass is finite and positive.  Returns MDN_E_STATE naming the first
+ * failing env ("task generation rejected env=K status=S" or "episode
+ * dynamics sample rejected env=K") otherwise.  Waits for the sim's stream. */
+int mdn_sim_validate_rollout(MdnSim* sim);
+/* The parameters of a PPOFIX1 checkpoint (read_checkpoint_header,
+ * main.mm:986-994, then the actor and critic vectors that follow it, as
+ * navigation_training::load_actor reads them, navigation_training.hpp:37-62):
+ * actor and critic may be NULL; non-NULL ones need exactly the header's
+ * counts. */
+int mdn_checkpoint_read_params(const char* path, MdnCheckpointHeader* header, float* actor, uint64_t actor_count,
+                               float* critic, uint64_t critic_count);
 
 /* Test support, no counterpart in the reference: the kernels divide by
  * constants (plant mass and rotor time constants, the RK4 weight 6, the

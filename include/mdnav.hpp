@@ -5,6 +5,9 @@
  *   mdnav::PPOTrainer  ~ PPOTrainer (main.mm:1110-1474)
  *   mdnav::Trainer     ~ cpu_reference::Trainer (cpu_reference.hpp:112-615),
  *                        same constructor and run() -> Metrics, on the GPU.
+ *   mdnav::navigation_training ~ navigation_training (navigation_training.hpp):
+ *                        task_settings, configure, validate_rollout, load_actor,
+ *                        evaluate, train.
  * Non-zero status codes become std::runtime_error, the reference's require()
  * convention (main.mm:27).  The reference exposes shared buffers as public
  * members; here they are methods returning host copies (sim.states() for
@@ -15,12 +18,17 @@
 
 #include <array>
 #include <chrono>
+#include <cmath>
 #include <cstdint>
+#include <filesystem>
+#include <fstream>
+#include <iostream>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "mdnav.h"
+#include "mdnav_host.h"
 
 namespace mdnav {
 
@@ -167,20 +175,44 @@ public:
     PPOTrainer ppo;
 };
 
-// navigation_training::task_settings and configure (navigation_training.hpp:7-24):
-// the stage's default task with the training's costs, and the runtime with
-// the stress range and seed 0x3f84d5b5, installed before a reset.
+// The reference's Sim constructor loads the RAPTOR controller and the nominal
+// plant itself (main.mm:531) and its free functions take a Metal&; here the
+// controller and plant travel in this context instead.
+struct Context {
+    MdnRaptorWeights raptor;
+    MdnPhysicsParams physics;
+};
+
+// navigation_training (navigation_training.hpp:5-173): goal-conditioned task
+// set-up, validation, evaluation and the task-training loop, on the C ABI.
+namespace navigation_training {
+
+inline void require_that(bool ok, const std::string& message) {
+    if (!ok) throw std::runtime_error(message);
+}
+
+// task_settings (navigation_training.hpp:7-14): the stage's default task with
+// the training's time cost, smoothness weight and initial-speed cap.
 inline MdnTaskControl task_settings(uint32_t stage, uint32_t family) {
     MdnTaskControl t{};
     t.enabled = 1;
-    require(mdn_task_default_config(stage, family, .5f, &t.config));
+    if (mdn_task_default_config(stage, family, .5f, &t.config) != MDN_OK)
+        throw std::runtime_error("unsupported task stage/family");
     t.config.time_cost_per_s = .2f;
     t.config.command_smoothness_weight = .05f;
     t.config.initial_speed_max_mps = stage == 1 ? .5f : 1.0f;
     return t;
 }
+
+// configure (navigation_training.hpp:16-25): per-episode plants with the
+// stress range and seed 0x3f84d5b5 at `amplitude`, the tasks, then a reset.
 inline void configure(Sim& sim, const MdnTaskControl& tasks, float amplitude) {
-    if (!(amplitude >= 0.0f && amplitude <= 1.0f)) throw std::runtime_error("domain amplitude must be 0..1");
+    require_that(std::isfinite(amplitude) && amplitude >= 0.0f && amplitude <= 1.0f, "domain amplitude must be0..1");
+    require_that(std::fabs(tasks.config.nav_period_s - float(sim.cfg.substeps) * .01f) < 1e-6f,
+                 "task/simulator clock mismatch");
+    MdnBankControl bank{};
+    require(mdn_sim_get_bank(sim.handle(), &bank));
+    require_that(bank.enabled == 0, "task generator and frozen bank cannot both own the world");
     MdnRuntimeConfig r{};
     r.enabled = 1;
     r.domain_amplitude = amplitude;
@@ -190,6 +222,207 @@ inline void configure(Sim& sim, const MdnTaskControl& tasks, float amplitude) {
     sim.set_tasks(tasks);
     sim.reset();
 }
+
+// validate_rollout (navigation_training.hpp:27-35).
+inline void validate_rollout(Sim& sim) {
+    if (mdn_sim_validate_rollout(sim.handle()) != MDN_OK) throw std::runtime_error(mdn_last_error());
+}
+
+// load_actor (navigation_training.hpp:37-62): a checkpoint's actor (and
+// critic) as the sim's parameters.  The 32-to-64-input critic migration of
+// the reference's control-state build has no counterpart: its critic takes
+// 32 inputs here, so another critic size is an incompatible warm start.
+inline void load_actor(Sim& sim, const std::string& path, bool critic = false) {
+    MdnCheckpointHeader header{};
+    if (mdn_checkpoint_read_params(path.c_str(), &header, nullptr, 0, nullptr, 0) != MDN_OK)
+        throw std::runtime_error(mdn_last_error());
+    std::vector<float> actor = sim.actor(), crit = sim.critic();
+    require_that(header.actor_count == actor.size(), "task actor dimensions");
+    require_that(!critic || header.critic_count == crit.size(), "task critic dimensions: incompatible warmstart");
+    if (mdn_checkpoint_read_params(path.c_str(), &header, actor.data(), actor.size(), critic ? crit.data() : nullptr,
+                                   critic ? crit.size() : 0) != MDN_OK)
+        throw std::runtime_error("task parameter load failed");
+    sim.upload(MDN_BUF_ACTOR, actor);
+    if (critic) sim.upload(MDN_BUF_CRITIC, crit);
+}
+
+struct Score {
+    double success = 0, collision = 0, timeout = 0, successful_time_s = 0;
+};
+
+// evaluate (navigation_training.hpp:68-115): 128 tasks of one stage and
+// family with per-episode plants at `amplitude`, one episode each over 400
+// ticks in `mode` (17: the deployed action map) with the geometry memory;
+// the score, and the per-env task CSV when `output` is given.
+inline Score evaluate(const Context& ctx, const float* actor, uint32_t stage, uint32_t family, float amplitude,
+                      uint32_t seed, const std::string& output = "", uint32_t mode = 17) {
+    MdnSimConfig config = mdn::default_config();
+    config.n = 128; config.eval = 1; config.mode = mode; config.seed = seed; config.family = family;
+    config.speed = 1.5f; config.distance = 8; config.max_steps = 400; config.geometry_memory = 1;
+    Sim sim(config, 32, ctx.raptor, ctx.physics);
+    sim.set_actor_obs(184);
+    const MdnTaskControl settings = task_settings(stage, family);
+    configure(sim, settings, amplitude);
+    std::vector<float> a = sim.actor();
+    std::copy(actor, actor + a.size(), a.begin());
+    sim.upload(MDN_BUF_ACTOR, a);
+    validate_rollout(sim);
+    const std::vector<MdnTaskState> tasks = sim.download<MdnTaskState>(MDN_BUF_TASK_STATES);
+    sim.collect(400);
+    sim.finish();
+    validate_rollout(sim);
+    std::ofstream file;
+    if (!output.empty()) {
+        const std::filesystem::path destination(output);
+        if (destination.has_parent_path()) std::filesystem::create_directories(destination.parent_path());
+        file.open(output);
+        require_that(bool(file), "cannot write task evaluation");
+        file << "seed,env,stage,family,mode,domain_amplitude,start_x,start_y,start_z,start_yaw,initial_vx,"
+                "initial_vy,initial_vz,goal_x,goal_y,goal_z,initial_distance_m,direct_clearance_m,"
+                "witness_length_m,mass_kg,success,collision,timeout,time_s,path_m,goal_error_m,final_speed_mps,"
+                "hold_s,peak_speed_mps,min_sphere_clearance_m,success_rule\n";
+    }
+    Score result;
+    const std::vector<MdnSimRun> runs = sim.runs();
+    const std::vector<MdnPhysicsState> states = sim.states();
+    const std::vector<MdnTaskState> final_tasks = sim.download<MdnTaskState>(MDN_BUF_TASK_STATES);
+    const std::vector<MdnPhysicsParams> plants = sim.download<MdnPhysicsParams>(MDN_BUF_ENV_PHYSICS);
+    for (uint32_t env = 0; env < config.n; env++) {
+        const MdnSimRun& run = runs[env];
+        const MdnTaskState& task = tasks[env];
+        const MdnPhysicsState& state = states[env];
+        require_that(run.episodes == 1, "evaluation must complete exactly one task per environment");
+        result.success += run.successes;
+        result.collision += run.collisions;
+        result.timeout += run.timeouts;
+        result.successful_time_s += run.success_time;
+        const float dx = task.goal_position[0] - state.position[0], dy = task.goal_position[1] - state.position[1],
+                    dz = task.goal_position[2] - state.position[2];
+        const float error = std::sqrt(dx * dx + dy * dy + dz * dz);
+        const float* v = state.linear_velocity;
+        const float speed = std::sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+        if (run.successes)
+            require_that(error <= settings.config.goal_radius_m + 1e-5f &&
+                             speed <= settings.config.stable_speed_mps + 1e-5f &&
+                             final_tasks[env].stable_time_s >= .2f - 1e-6f,
+                         "stable-arrival invariant failed");
+        if (file.is_open()) {
+            file << seed << ',' << env << ',' << stage << ',' << task.family << ',' << mode << ',' << amplitude;
+            for (float x : task.start_position) file << ',' << x;
+            file << ',' << task.start_yaw_rad;
+            for (float x : task.start_velocity_world) file << ',' << x;
+            for (float x : task.goal_position) file << ',' << x;
+            file << ',' << task.initial_distance_m << ',' << task.direct_segment_clearance_m << ','
+                 << task.witness_length_m << ',' << plants[env].mass << ',' << run.successes << ','
+                 << run.collisions << ',' << run.timeouts << ',' << run.elapsed << ',' << run.path << ',' << error
+                 << ',' << speed << ',' << final_tasks[env].stable_time_s << ',' << run.peak_speed << ','
+                 << run.min_clearance << ",radius0.35_speed0.5_hold0.2\n";
+        }
+    }
+    result.success /= config.n;
+    result.collision /= config.n;
+    result.timeout /= config.n;
+    if (result.success > 0) result.successful_time_s /= result.success * config.n;
+    std::cout << "task_eval stage=" << stage << " family=" << family << " seed=" << seed << " amplitude=" << amplitude
+              << " mode=" << mode << " success=" << result.success << " collision=" << result.collision
+              << " timeout=" << result.timeout << " mean_arrival_s=" << result.successful_time_s << "\n";
+    return result;
+}
+
+// train (navigation_training.hpp:117-171): goal-arrival PPO on 128 envs x 32
+// ticks in mode 22 with per-episode plants; resumes `checkpoint` when it
+// exists, else warm-starts from `warmstart` with log-std -1; validates every
+// rollout before its update; every 50 rollouts (and at the end) saves the
+// checkpoint, evaluates on seed 800001 and keeps the best by success, then
+// collisions, then arrival time; appends to `checkpoint`.history.csv.
+inline void train(const Context& ctx, uint32_t rollouts, const std::string& checkpoint, const std::string& warmstart,
+                  uint32_t stage, uint32_t family, float amplitude, uint32_t seed) {
+    require_that(rollouts > 0, "task training requires positive rollouts and guided build");
+    MdnSimConfig config = mdn::default_config();
+    config.n = 128; config.mode = 22; config.family = family; config.seed = seed;
+    config.speed = 1.5f; config.distance = 8; config.max_steps = 400; config.geometry_memory = 1;
+    config.entropy_coef = .001f; config.learning_rate = .0001f;
+    Sim sim(config, 32, ctx.raptor, ctx.physics);
+    sim.set_actor_obs(184);
+    const MdnTaskControl settings = task_settings(stage, family);
+    configure(sim, settings, amplitude);
+    PPOTrainer trainer(sim);
+    const bool resume = std::filesystem::exists(checkpoint);
+    uint32_t completed = 0;
+    if (resume) {
+        completed = trainer.load_checkpoint(checkpoint, family, 32, config.n, seed);
+    } else {
+        load_actor(sim, warmstart, true);
+        std::vector<float> a = sim.actor();
+        for (size_t axis = 0; axis < 4; axis++) a[a.size() - 4 + axis] = -1.0f;
+        sim.upload(MDN_BUF_ACTOR, a);
+    }
+    validate_rollout(sim);
+    const std::filesystem::path path(checkpoint);
+    if (path.has_parent_path()) std::filesystem::create_directories(path.parent_path());
+    std::ofstream history(checkpoint + ".history.csv", std::ios::app);
+    require_that(bool(history), "task history write");
+    if (!resume)
+        history << "rollout,total_transitions,wall_s,collect_gpu_s,update_gpu_s,policy_loss,value_loss,ratio,"
+                   "success,collision,timeout,mean_arrival_s\n";
+    const auto start = std::chrono::steady_clock::now();
+    const auto wall = [&] { return std::chrono::duration<double>(std::chrono::steady_clock::now() - start).count(); };
+    const uint32_t finish = completed + rollouts;
+    const auto evaluate_current = [&](const std::string& output) {
+        const std::vector<float> a = sim.actor();
+        return evaluate(ctx, a.data(), stage, family, amplitude, 800001, output);
+    };
+    Score best;
+    if (resume && std::filesystem::exists(checkpoint + ".best")) {
+        Sim selected(config, 32, ctx.raptor, ctx.physics);
+        selected.set_actor_obs(184);
+        load_actor(selected, checkpoint + ".best");
+        const std::vector<float> a = selected.actor();
+        best = evaluate(ctx, a.data(), stage, family, amplitude, 800001);
+    }
+    if (!resume) {
+        const Score baseline = evaluate_current(checkpoint + ".initial-dev.csv");
+        best = baseline;
+        trainer.save_checkpoint(checkpoint + ".best", family, seed, completed);
+        history << 0 << ",0,0,0,0,0,0,1," << baseline.success << ',' << baseline.collision << ','
+                << baseline.timeout << ',' << baseline.successful_time_s << '\n';
+        history.flush();
+    }
+    for (uint32_t rollout = completed; rollout < finish; rollout++) {
+        // generation and dynamics errors are rejected before their transitions reach PPO
+        sim.collect();
+        const double collection_gpu = sim.finish();
+        validate_rollout(sim);
+        trainer.rollout_update(rollout);
+        const double update_gpu = sim.finish();
+        if ((rollout + 1) % 50 == 0 || rollout + 1 == finish) {
+            trainer.save_checkpoint(checkpoint, family, seed, rollout + 1);
+            const Score score = evaluate_current(checkpoint + ".dev.csv");
+            if (score.success > best.success || (score.success == best.success && score.collision < best.collision) ||
+                (score.success == best.success && score.collision == best.collision &&
+                 score.successful_time_s < best.successful_time_s)) {
+                best = score;
+                trainer.save_checkpoint(checkpoint + ".best", family, seed, rollout + 1);
+                std::filesystem::copy_file(checkpoint + ".dev.csv", checkpoint + ".best-dev.csv",
+                                           std::filesystem::copy_options::overwrite_existing);
+            }
+            const std::array<float, 4> metrics = trainer.metric_mean();
+            history << rollout + 1 << ',' << uint64_t(rollout + 1) * config.n * 32 << ',' << wall() << ','
+                    << collection_gpu << ',' << update_gpu << ',' << metrics[0] << ',' << metrics[1] << ','
+                    << metrics[3] << ',' << score.success << ',' << score.collision << ',' << score.timeout << ','
+                    << score.successful_time_s << '\n';
+            history.flush();
+            std::cout << "task_train rollout=" << rollout + 1 << " policy_loss=" << metrics[0]
+                      << " value_loss=" << metrics[1] << " ratio=" << metrics[3] << " wall_s=" << wall() << "\n";
+        }
+    }
+}
+
+}  // namespace navigation_training
+
+// The reference's names at namespace scope of its own files.
+using navigation_training::configure;
+using navigation_training::task_settings;
 
 }  // namespace mdnav
 

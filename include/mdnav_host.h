@@ -112,14 +112,32 @@ inline void init_policy(const PolicyShape& s, float* actor, float* critic) {
 // Minibatch order of one rollout update (cpu_reference.hpp:569-579 ==
 // main.mm:1331-1338): contiguous row blocks, shuffled with
 // mt19937(0x9e3779b9 + rollout*0x85ebca6b), reshuffled only before epoch 1.
-// std::shuffle is implementation-defined, so the permutation is a
-// Fisher–Yates over the mt19937 stream (whose output the C++ standard fixes):
-// for i = n-1 .. 1, j = (u32 * (i+1)) >> 32.  Returns the start row of every
-// update in execution order.
-inline void fisher_yates(std::vector<uint32_t>& v, std::mt19937& rng) {
-    for (size_t i = v.size(); i > 1; --i) {
-        const uint64_t j = (uint64_t(rng()) * uint64_t(i)) >> 32;
-        std::swap(v[i - 1], v[size_t(j)]);
+// The reference is built with Apple clang against libc++, so its std::shuffle
+// is libc++'s, restated here over the mt19937 stream (whose output the C++
+// standard fixes):
+//   for k = 0 .. n-2: i = uniform integer in [0, n-1-k]; if i != 0, swap
+//   v[k] and v[k+i];
+// and libc++'s uniform_int_distribution<ptrdiff_t> over a 32-bit engine
+// draws an integer in [0, range) as the low w = ceil(log2(range)) bits of one
+// engine output, drawing again while the value is >= range (a range of 1
+// draws nothing).  Returns the start row of every update in execution order.
+inline uint32_t libcxx_uniform_below(std::mt19937& rng, uint64_t range) {
+    if (range <= 1) return 0;
+    uint32_t w = 0;
+    while ((uint64_t(1) << w) < range) ++w;  // ceil(log2(range)), range <= 2^32
+    const uint32_t mask = w >= 32 ? 0xffffffffu : ((1u << w) - 1u);
+    uint32_t u;
+    do {
+        u = uint32_t(rng()) & mask;
+    } while (u >= range);
+    return u;
+}
+
+inline void libcxx_shuffle(std::vector<uint32_t>& v, std::mt19937& rng) {
+    const size_t n = v.size();
+    for (size_t k = 0; k + 1 < n; ++k) {
+        const uint32_t i = libcxx_uniform_below(rng, uint64_t(n - k));
+        if (i != 0) std::swap(v[k], v[k + i]);
     }
 }
 
@@ -128,11 +146,11 @@ inline std::vector<uint32_t> minibatch_schedule(uint32_t rows, uint32_t minibatc
     std::vector<uint32_t> starts;
     for (uint32_t s = 0; s < rows; s += minibatch) starts.push_back(s);
     std::mt19937 rng(0x9e3779b9u + rollout_index * 0x85ebca6bu);
-    fisher_yates(starts, rng);
+    libcxx_shuffle(starts, rng);
     std::vector<uint32_t> order;
     order.reserve(size_t(starts.size()) * epochs);
     for (uint32_t e = 0; e < epochs; ++e) {
-        if (e == 1) fisher_yates(starts, rng);
+        if (e == 1) libcxx_shuffle(starts, rng);
         order.insert(order.end(), starts.begin(), starts.end());
     }
     return order;

@@ -105,6 +105,7 @@ struct MdnSim {
     uint32_t* bank_schedule = nullptr;      // [N][stride]
     uint32_t* bank_active = nullptr;        // [N]
     uint32_t* bank_transition = nullptr;    // [T][N]
+    uint32_t* validate_out = nullptr;       // [2] first failing env of validate_rollout
     bool episodic() const { return runtime.enabled != 0u || task.enabled != 0u || bank.enabled != 0u; }
     // policy
     float* actor = nullptr;
@@ -289,6 +290,7 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
     guard(dev_alloc(&s->task_cfg, 1));
     guard(dev_alloc(&s->bank_active, N));
     guard(dev_alloc(&s->bank_transition, R));
+    guard(dev_alloc(&s->validate_out, 2));
     if (rc == MDN_OK) {  // no bank: every id is MDN_BANK_REHEARSAL (sim.metal:143, 317)
         guard(hipMemset(s->bank_active, 0xff, size_t(N) * 4) == hipSuccess ? MDN_OK : fail(MDN_E_HIP, "hipMemset"));
         guard(hipMemset(s->bank_transition, 0xff, R * 4) == hipSuccess ? MDN_OK : fail(MDN_E_HIP, "hipMemset"));
@@ -371,7 +373,7 @@ void mdn_sim_destroy(MdnSim* s) {
     if (s->ppo) mdn_ppo_destroy(s->ppo);
     void* bufs[] = {s->state, s->run, s->world, s->sensors, s->poses, s->commands, s->raptor, s->camera, s->cells,
                     s->pix_rays, s->mem_head, s->env_phys, s->task_states, s->task_cfg, s->bank_worlds,
-                    s->bank_schedule, s->bank_active, s->bank_transition,
+                    s->bank_schedule, s->bank_active, s->bank_transition, s->validate_out,
                     s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->obs, s->co, s->nco, s->actions, s->logp,
                     s->values, s->rewards, s->next_values, s->advantages, s->returns, s->terminated, s->truncated};
     for (void* b : bufs)
@@ -469,6 +471,8 @@ int mdn_sim_get_runtime(const MdnSim* s, MdnRuntimeConfig* runtime) {
 
 int mdn_sim_set_tasks(MdnSim* s, const MdnTaskControl* tasks) {
     if (!s || !tasks) return fail(MDN_E_ARG, "mdn_sim_set_tasks: null argument");
+    if (tasks->enabled != 0u && s->bank.enabled != 0u)  // navigation_training.hpp:19
+        return fail(MDN_E_ARG, "task generator and frozen bank cannot both own the world");
     int rc = open_sync_window(s);
     if (rc) return rc;
     s->task = *tasks;
@@ -487,6 +491,8 @@ int mdn_sim_set_bank(MdnSim* s, const MdnWorld* worlds, uint32_t count, const ui
                      uint32_t schedule_stride) {
     if (!s || (count && (!worlds || !schedule || schedule_stride == 0)))
         return fail(MDN_E_ARG, "mdn_sim_set_bank: null argument or zero schedule stride");
+    if (count && s->task.enabled != 0u)  // navigation_training.hpp:19
+        return fail(MDN_E_ARG, "task generator and frozen bank cannot both own the world");
     int rc = open_sync_window(s);
     if (rc) return rc;
     HIP_TRY(hipStreamSynchronize(s->stream));
@@ -508,6 +514,12 @@ int mdn_sim_set_bank(MdnSim* s, const MdnWorld* worlds, uint32_t count, const ui
     s->bank.bank_count = count;
     s->bank.schedule_stride = schedule_stride;
     s->bank.horizon = s->horizon;
+    return MDN_OK;
+}
+
+int mdn_sim_get_bank(const MdnSim* s, MdnBankControl* bank) {
+    if (!s || !bank) return fail(MDN_E_ARG, "mdn_sim_get_bank: null argument");
+    *bank = s->bank;
     return MDN_OK;
 }
 
@@ -637,6 +649,25 @@ int mdn_sim_kernel_time(MdnSim* s, uint32_t kernel, double* total_ms, uint64_t* 
 int mdn_sim_reset_timing(MdnSim* s) {
     if (!s) return fail(MDN_E_ARG, "mdn_sim_reset_timing: null sim");
     for (int i = 0; i < MDN_K_COUNT; i++) { s->timing.total_ms[i] = 0; s->timing.launches[i] = 0; }
+    return MDN_OK;
+}
+
+int mdn_sim_validate_rollout(MdnSim* s) {
+    if (!s) return fail(MDN_E_ARG, "mdn_sim_validate_rollout: null");
+    int rc = open_sync_window(s);
+    if (rc) return rc;
+    uint32_t bad[2];
+    HIP_TRY(nav_launch_validate(s->task_states, s->env_phys, s->cfg.n, s->validate_out, s->stream));
+    HIP_TRY(hipMemcpyAsync(bad, s->validate_out, 8, hipMemcpyDeviceToHost, s->stream));
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    if (bad[0] != 0xffffffffu) {
+        MdnTaskState t;
+        HIP_TRY(hipMemcpy(&t, s->task_states + bad[0], sizeof(t), hipMemcpyDeviceToHost));
+        return fail(MDN_E_STATE, "task generation rejected env=" + std::to_string(bad[0]) +
+                                     " status=" + std::to_string(t.generation_status));
+    }
+    if (bad[1] != 0xffffffffu)
+        return fail(MDN_E_STATE, "episode dynamics sample rejected env=" + std::to_string(bad[1]));
     return MDN_OK;
 }
 
@@ -973,6 +1004,186 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon) {
     return MDN_OK;
 }
 
+// ---------------------------------------------------------------- fixed_ppo operators
+int mdn_op_actor_forward(const float* params, uint32_t obs_dim, uint32_t hidden_dim, const float* obs, uint64_t batch,
+                         float* hidden, float* means) {
+    if (!params || !obs || !means) return fail(MDN_E_ARG, "mdn_op_actor_forward: null");
+    if (obs_dim < 1 || obs_dim > 1024 || hidden_dim < 1 || hidden_dim > 8192)
+        return fail(MDN_E_ARG, "mdn_op_actor_forward: inputs must be 1..1024 and hidden units 1..8192");
+    if (batch == 0) return MDN_OK;
+    if (batch > 0x7fffffffull) return fail(MDN_E_ARG, "mdn_op_actor_forward: batch too large");
+    const size_t P = size_t(hidden_dim) * obs_dim + hidden_dim + 4 * size_t(hidden_dim) + 4 + 4;
+    DevBuf w, x, h, m;
+    int rc = upload_tmp(w, params, P * 4);
+    if (!rc) rc = upload_tmp(x, obs, batch * obs_dim * 4);
+    if (!rc) rc = upload_tmp(h, nullptr, batch * hidden_dim * 4);
+    if (!rc) rc = upload_tmp(m, nullptr, batch * 16);
+    if (rc) return rc;
+    // ppo.hpp:30: the 184 and 824 input layouts end in the geometry-prior hint
+    const uint32_t prior = obs_dim == 184 || obs_dim == 824;
+    HIP_TRY(fppo_launch_forward(static_cast<float*>(w.p), static_cast<float*>(x.p), obs_dim, hidden_dim, 4, prior,
+                                batch, static_cast<float*>(h.p), static_cast<float*>(m.p), nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(means, m.p, batch * 16, hipMemcpyDeviceToHost));
+    if (hidden) HIP_TRY(hipMemcpy(hidden, h.p, batch * hidden_dim * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_op_critic_forward(const float* params, uint32_t obs_dim, uint32_t hidden_dim, const float* obs, uint64_t batch,
+                          float* hidden, float* values) {
+    if (!params || !obs || !values) return fail(MDN_E_ARG, "mdn_op_critic_forward: null");
+    if (obs_dim < 1 || obs_dim > 1024 || hidden_dim < 1 || hidden_dim > 8192)
+        return fail(MDN_E_ARG, "mdn_op_critic_forward: inputs must be 1..1024 and hidden units 1..8192");
+    if (batch == 0) return MDN_OK;
+    if (batch > 0x7fffffffull) return fail(MDN_E_ARG, "mdn_op_critic_forward: batch too large");
+    const size_t P = size_t(hidden_dim) * obs_dim + 2 * size_t(hidden_dim) + 1;
+    DevBuf w, x, h, v;
+    int rc = upload_tmp(w, params, P * 4);
+    if (!rc) rc = upload_tmp(x, obs, batch * obs_dim * 4);
+    if (!rc) rc = upload_tmp(h, nullptr, batch * hidden_dim * 4);
+    if (!rc) rc = upload_tmp(v, nullptr, batch * 4);
+    if (rc) return rc;
+    HIP_TRY(fppo_launch_forward(static_cast<float*>(w.p), static_cast<float*>(x.p), obs_dim, hidden_dim, 1, 0, batch,
+                                static_cast<float*>(h.p), static_cast<float*>(v.p), nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(values, v.p, batch * 4, hipMemcpyDeviceToHost));
+    if (hidden) HIP_TRY(hipMemcpy(hidden, h.p, batch * hidden_dim * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_op_gaussian_log_prob(const float* actions, const float* means, const float* log_std, uint32_t log_std_stride,
+                             uint64_t batch, float* logp) {
+    if (!actions || !means || !log_std || !logp) return fail(MDN_E_ARG, "mdn_op_gaussian_log_prob: null");
+    if (log_std_stride != 0 && log_std_stride != 4) return fail(MDN_E_ARG, "log_std stride must be 0 or 4");
+    if (batch == 0) return MDN_OK;
+    DevBuf a, m, l, o;
+    int rc = upload_tmp(a, actions, batch * 16);
+    if (!rc) rc = upload_tmp(m, means, batch * 16);
+    if (!rc) rc = upload_tmp(l, log_std, (log_std_stride ? batch : 1) * 16);
+    if (!rc) rc = upload_tmp(o, nullptr, batch * 4);
+    if (rc) return rc;
+    HIP_TRY(fppo_launch_log_prob(static_cast<float*>(a.p), static_cast<float*>(m.p), static_cast<float*>(l.p),
+                                 log_std_stride, batch, static_cast<float*>(o.p), nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(logp, o.p, batch * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_op_sample_loss_and_grad(const float* actions, const float* means, const float* log_std,
+                                uint32_t log_std_stride, const float* old_logp, const float* old_values,
+                                const float* values, const float* advantages, const float* returns, uint64_t batch,
+                                float batch_size, float clip_epsilon, float value_coefficient,
+                                float entropy_coefficient, float* d_mean, float* d_log_std, float* d_value,
+                                float* losses) {
+    (void)old_values;  // kept in the ABI like the reference's unused old_value (ppo.hpp:180)
+    if (!actions || !means || !log_std || !old_logp || !values || !advantages || !returns || !d_mean || !d_log_std ||
+        !d_value || !losses)
+        return fail(MDN_E_ARG, "mdn_op_sample_loss_and_grad: null");
+    if (log_std_stride != 0 && log_std_stride != 4) return fail(MDN_E_ARG, "log_std stride must be 0 or 4");
+    if (batch == 0) return MDN_OK;
+    DevBuf a, m, l, ol, v, ad, re, dm, dl, dv, lo;
+    int rc = upload_tmp(a, actions, batch * 16);
+    if (!rc) rc = upload_tmp(m, means, batch * 16);
+    if (!rc) rc = upload_tmp(l, log_std, (log_std_stride ? batch : 1) * 16);
+    if (!rc) rc = upload_tmp(ol, old_logp, batch * 4);
+    if (!rc) rc = upload_tmp(v, values, batch * 4);
+    if (!rc) rc = upload_tmp(ad, advantages, batch * 4);
+    if (!rc) rc = upload_tmp(re, returns, batch * 4);
+    if (!rc) rc = upload_tmp(dm, nullptr, batch * 16);
+    if (!rc) rc = upload_tmp(dl, nullptr, batch * 16);
+    if (!rc) rc = upload_tmp(dv, nullptr, batch * 4);
+    if (!rc) rc = upload_tmp(lo, nullptr, batch * 16);
+    if (rc) return rc;
+    fppo_loss_args g;
+    g.actions = static_cast<float*>(a.p); g.means = static_cast<float*>(m.p); g.log_std = static_cast<float*>(l.p);
+    g.old_logp = static_cast<float*>(ol.p); g.values = static_cast<float*>(v.p);
+    g.advantages = static_cast<float*>(ad.p); g.returns = static_cast<float*>(re.p);
+    g.d_mean = static_cast<float*>(dm.p); g.d_log_std = static_cast<float*>(dl.p);
+    g.d_value = static_cast<float*>(dv.p); g.losses = static_cast<float*>(lo.p);
+    g.b = batch; g.ls_stride = log_std_stride;
+    g.batch_size = batch_size; g.clip = clip_epsilon; g.vcoef = value_coefficient; g.ecoef = entropy_coefficient;
+    HIP_TRY(fppo_launch_loss_grad(&g, nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(d_mean, dm.p, batch * 16, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(d_log_std, dl.p, batch * 16, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(d_value, dv.p, batch * 4, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(losses, lo.p, batch * 16, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+int mdn_op_adam_update(float* params, const float* grad, float* first, float* second, uint64_t count, uint64_t step,
+                       float learning_rate, float beta1, float beta2, float epsilon, float weight_decay) {
+    if (!params || !grad || !first || !second) return fail(MDN_E_ARG, "mdn_op_adam_update: null");
+    if (count == 0) return MDN_OK;
+    float c1 = 0.0f, c2 = 0.0f;
+    mdn::adam_corrections(step, beta1, beta2, &c1, &c2);
+    DevBuf p, g, m, v;
+    int rc = upload_tmp(p, params, count * 4);
+    if (!rc) rc = upload_tmp(g, grad, count * 4);
+    if (!rc) rc = upload_tmp(m, first, count * 4);
+    if (!rc) rc = upload_tmp(v, second, count * 4);
+    if (rc) return rc;
+    HIP_TRY(fppo_launch_adam(static_cast<float*>(p.p), static_cast<float*>(g.p), static_cast<float*>(m.p),
+                             static_cast<float*>(v.p), count, learning_rate, beta1, beta2, epsilon, weight_decay, c1,
+                             c2, nullptr));
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(params, p.p, count * 4, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(first, m.p, count * 4, hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(second, v.p, count * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+// fixed_ppo::run_cpu_self_tests (ppo.hpp:204-267) with the GPU operators
+// above: central differences of the per-sample objective (the sum of the
+// policy, value and entropy losses at batch size 1, which is
+// sample_objective) against the analytic derivatives on the four surrogate
+// branches, the value derivative, and Adam's closed-form first step.
+int mdn_op_ppo_self_tests(float tolerance, int* passed) {
+    if (!passed) return fail(MDN_E_ARG, "mdn_op_ppo_self_tests: null");
+    *passed = 0;
+    float action[4] = {0.4f, 0, 0, 0}, mean[4] = {0.1f, 0, 0, 0}, log_std[4] = {0, 0, 0, 0};
+    const float clip = 0.2f, vcoef = 0.7f, ecoef = 0.03f, value = 0.25f, target = -0.3f, h = 1.0e-3f;
+    float base_logp = 0.0f;
+    int rc = mdn_op_gaussian_log_prob(action, mean, log_std, 0, 1, &base_logp);
+    if (rc) return rc;
+    float dm[4], dl[4], dv, loss[4];
+    auto run = [&](float old_logp, float adv, float* objective) {
+        const int r = mdn_op_sample_loss_and_grad(action, mean, log_std, 0, &old_logp, &value, &value, &adv, &target, 1,
+                                                  1.0f, clip, vcoef, ecoef, dm, dl, &dv, loss);
+        if (objective) *objective = loss[0] + loss[1] + loss[2];
+        return r;
+    };
+    const float old_values[4] = {base_logp - std::log(1.1f), base_logp - std::log(0.9f), base_logp - std::log(1.3f),
+                                 base_logp - std::log(0.7f)};
+    const float advantages[4] = {1.0f, -1.0f, 1.0f, -1.0f};
+    for (int branch = 0; branch < 4; branch++) {
+        float grad_mean[4], grad_std[4], plus = 0, minus = 0;
+        if ((rc = run(old_values[branch], advantages[branch], nullptr)) != MDN_OK) return rc;
+        std::copy(dm, dm + 4, grad_mean);
+        std::copy(dl, dl + 4, grad_std);
+        for (int which = 0; which < 2; which++) {
+            float* x = which == 0 ? &mean[0] : &log_std[0];
+            const float saved = *x;
+            *x = saved + h;
+            if ((rc = run(old_values[branch], advantages[branch], &plus)) != MDN_OK) return rc;
+            *x = saved - h;
+            if ((rc = run(old_values[branch], advantages[branch], &minus)) != MDN_OK) return rc;
+            *x = saved;
+            const float numeric = (plus - minus) / (2.0f * h);
+            if (std::fabs(numeric - (which == 0 ? grad_mean[0] : grad_std[0])) > tolerance) return MDN_OK;
+        }
+    }
+    if ((rc = run(base_logp, 0.0f, nullptr)) != MDN_OK) return rc;
+    if (std::fabs(vcoef * (value - target) - dv) > tolerance) return MDN_OK;
+    float parameter = 1.0f, gradient = 0.25f, first = 0.0f, second = 0.0f;
+    if ((rc = mdn_op_adam_update(&parameter, &gradient, &first, &second, 1, 1, 0.01f, 0.9f, 0.999f, 1.0e-8f, 0.0f)))
+        return rc;
+    const float want_first = 0.1f * gradient, want_second = 0.001f * gradient * gradient;
+    const float want_parameter = 1.0f - 0.01f * (want_first / 0.1f) / (std::sqrt(want_second / 0.001f) + 1.0e-8f);
+    *passed = std::fabs(first - want_first) <= tolerance && std::fabs(second - want_second) <= tolerance &&
+              std::fabs(parameter - want_parameter) <= tolerance;
+    return MDN_OK;
+}
 
 // ---------------------------------------------------------------- wide policy
 }  // extern "C"
@@ -1376,6 +1587,25 @@ int mdn_checkpoint_read(const char* path, MdnCheckpointHeader* header, float* ac
     return MDN_OK;
 }
 
+int mdn_checkpoint_read_params(const char* path, MdnCheckpointHeader* header, float* actor, uint64_t actor_count,
+                               float* critic, uint64_t critic_count) {
+    if (!path || !header) return fail(MDN_E_ARG, "mdn_checkpoint_read_params: null argument");
+    File file(path, "rb");
+    if (!file.f) return fail(MDN_E_ARG, std::string("cannot open checkpoint: ") + path);
+    int rc = read_checkpoint_header(file, header);
+    if (rc) return rc;
+    if (actor && actor_count != header->actor_count) return fail(MDN_E_ARG, "task actor dimensions");
+    if (critic && critic_count != header->critic_count)
+        return fail(MDN_E_ARG, "task critic dimensions: incompatible warmstart");
+    std::vector<float> skip;
+    if (!actor && critic) skip.resize(header->actor_count);
+    float* first = actor ? actor : skip.data();
+    if ((actor || critic) && !file.read(first, size_t(header->actor_count) * 4))
+        return fail(MDN_E_ARG, "task parameter load failed");
+    if (critic && !file.read(critic, size_t(critic_count) * 4)) return fail(MDN_E_ARG, "task parameter load failed");
+    return MDN_OK;
+}
+
 int mdn_ppo_load_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32_t horizon, uint32_t n, uint32_t seed,
                             uint32_t* completed_rollouts) {
     if (!p || !path) return fail(MDN_E_ARG, "mdn_ppo_load_checkpoint: null argument");
@@ -1435,7 +1665,7 @@ int mdn_ppo_load_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
         if (std::memcmp(&saved_nominal, &s->phys, sizeof(saved_nominal)) != 0 ||
             std::memcmp(saved_raptor.data(), raptor.data(), 2084 * 4) != 0)
             return fail(MDN_E_ARG, "checkpoint nominal plant/controller mismatch");
-    } else if (s->episodic()) {
+    } else if (s->runtime.enabled != 0u || s->task.enabled != 0u) {  // main.mm:1254-1257: a bank alone is fine
         return fail(MDN_E_ARG, "legacy resume cannot infer new dynamics/task state; use explicit parameter warmstart");
     }
     if (!file.at_end()) return fail(MDN_E_ARG, "PPO checkpoint has trailing data");
@@ -1461,9 +1691,10 @@ int mdn_ppo_save_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
     MdnCheckpointHeader h;
     std::memset(&h, 0, sizeof(h));  // padding bytes too, so equal states give equal files
     std::memcpy(h.magic, "PPOFIX1", 7);
-    // main.mm:1292: version 8 with the dynamics/task blocks when either is
-    // on, else 6 (no shaping; the legacy camera)
-    h.version = s->episodic() ? 8 : 6;
+    // main.mm:1292: version 8 with the dynamics/task blocks when per-episode
+    // plants or tasks are on, else 6 (no shaping; the legacy camera).  A
+    // challenge bank alone writes version 6, as in the reference.
+    h.version = (s->runtime.enabled != 0u || s->task.enabled != 0u) ? 8 : 6;
     h.actor_count = s->shape.actor_count();
     h.critic_count = s->shape.critic_count();
     h.horizon = s->horizon;

@@ -151,12 +151,25 @@ struct AdamArgs {
 };
 }  // namespace ppo
 
+// Per-sample loss and derivatives of fixed_ppo::sample_loss_and_grad over a
+// batch (fixed_ppo.hip); log_std is shared (stride 0) or per row (stride 4).
+struct fppo_loss_args {
+    const float* actions; const float* means; const float* log_std; const float* old_logp;
+    const float* values; const float* advantages; const float* returns;
+    float* d_mean; float* d_log_std; float* d_value; float* losses;
+    uint64_t b;
+    uint32_t ls_stride;
+    float batch_size, clip, vcoef, ecoef;
+};
+
 extern "C" {
 hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream);
 hipError_t nav_launch_episode(const nav::EpisodeArgs* a, hipStream_t stream);
 hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int ring_slots, uint32_t actor_obs,
                               hipStream_t stream);
 hipError_t nav_launch_memory_hint(const nav::MemoryArgs* a, hipStream_t stream);
+hipError_t nav_launch_validate(const MdnTaskState* tasks, const MdnPhysicsParams* phys, uint32_t n, uint32_t* out,
+                               hipStream_t stream);
 hipError_t nav_launch_raptor_fixture(const float* RW, const float* obs, uint32_t steps, uint32_t copies,
                                      float* actions, float* hidden, int lanes_per_env, hipStream_t st);
 hipError_t nav_launch_physics_fixture(const MdnPhysicsState* in, const float* actions, const float* winds,
@@ -198,4 +211,12 @@ hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, flo
                           __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
                           uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, hipStream_t st);
 uint32_t ppo_partial_stride(uint32_t d);
+// fixed_ppo operators over caller arrays (fixed_ppo.hip)
+hipError_t fppo_launch_forward(const float* w, const float* x, uint32_t D, uint32_t H, uint32_t O, uint32_t prior,
+                               uint64_t B, float* hidden, float* out, hipStream_t st);
+hipError_t fppo_launch_log_prob(const float* act, const float* mean, const float* log_std, uint32_t ls_stride,
+                                uint64_t B, float* out, hipStream_t st);
+hipError_t fppo_launch_loss_grad(const fppo_loss_args* a, hipStream_t st);
+hipError_t fppo_launch_adam(float* p, const float* g, float* m, float* v, uint64_t n, float lr, float b1, float b2,
+                            float eps, float wd, float c1, float c2, hipStream_t st);
 }

@@ -1116,10 +1116,33 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     }
 }
 
+// navigation_training::validate_rollout (navigation_training.hpp:27-35): the
+// lowest env whose task is not valid and ready (out[0]) and the lowest whose
+// plant mass is not finite and positive (out[1]); 0xffffffff when none.  The
+// caller fills out with 0xffffffff first.
+__global__ __launch_bounds__(256) void validate_kernel(const MdnTaskState* __restrict__ tasks,
+                                                       const MdnPhysicsParams* __restrict__ phys, uint32_t n,
+                                                       uint32_t* __restrict__ out) {
+    const uint32_t e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= n) return;
+    const MdnTaskState& t = tasks[e];
+    if (!(t.valid != 0u && t.generation_status == MDN_TASK_READY)) atomicMin(out, e);
+    const float m = phys[e].mass;
+    if (!(isfinite_f(m) && m > 0.0f)) atomicMin(out + 1, e);
+}
+
 }  // namespace nav
 
 // ---------------------------------------------------------------- launchers
 extern "C" {
+
+hipError_t nav_launch_validate(const MdnTaskState* tasks, const MdnPhysicsParams* phys, uint32_t n, uint32_t* out,
+                               hipStream_t stream) {
+    hipError_t e = hipMemsetAsync(out, 0xff, 8, stream);
+    if (e != hipSuccess || n == 0) return e;
+    hipLaunchKernelGGL(nav::validate_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, tasks, phys, n, out);
+    return hipGetLastError();
+}
 
 hipError_t nav_launch_episode(const nav::EpisodeArgs* a, hipStream_t stream) {
     if (a->cfg.n == 0) return hipSuccess;

@@ -61,3 +61,73 @@ def normalize(advantages, eps=1e-8):
     a = contiguous(advantages, np.float32).reshape(-1).copy()
     check(lib().mdn_op_normalize(ptr(a), len(a), ctypes.c_float(eps)))
     return a
+
+
+# ---------------------------------------------------------------- fixed_ppo operators (ppo.hpp:65-324)
+def actor_forward(params, obs, hidden_dim=64):
+    """fixed_ppo::actor_forward over rows of obs[batch][D]: (hidden, means)."""
+    x = contiguous(obs, np.float32)
+    x = x.reshape(-1, x.shape[-1])
+    w = contiguous(params, np.float32).reshape(-1)
+    h = np.zeros((len(x), hidden_dim), np.float32)
+    m = np.zeros((len(x), 4), np.float32)
+    check(lib().mdn_op_actor_forward(ptr(w), x.shape[1], hidden_dim, ptr(x), len(x), ptr(h), ptr(m)))
+    return h, m
+
+
+def critic_forward(params, obs, hidden_dim=64):
+    """fixed_ppo::critic_forward over rows of obs[batch][D]: (hidden, values)."""
+    x = contiguous(obs, np.float32)
+    x = x.reshape(-1, x.shape[-1])
+    w = contiguous(params, np.float32).reshape(-1)
+    h = np.zeros((len(x), hidden_dim), np.float32)
+    v = np.zeros(len(x), np.float32)
+    check(lib().mdn_op_critic_forward(ptr(w), x.shape[1], hidden_dim, ptr(x), len(x), ptr(h), ptr(v)))
+    return h, v
+
+
+def _log_std(log_std, rows):
+    ls = contiguous(log_std, np.float32)
+    return ls.reshape(-1), (0 if ls.size == 4 else 4)
+
+
+def gaussian_log_prob(actions, means, log_std):
+    a = contiguous(actions, np.float32).reshape(-1, 4)
+    m = contiguous(means, np.float32).reshape(-1, 4)
+    ls, stride = _log_std(log_std, len(a))
+    out = np.zeros(len(a), np.float32)
+    check(lib().mdn_op_gaussian_log_prob(ptr(a), ptr(m), ptr(ls), stride, len(a), ptr(out)))
+    return out
+
+
+def sample_loss_and_grad(actions, means, log_std, old_logp, values, advantages, returns, batch_size,
+                         clip=0.2, value_coef=0.5, entropy_coef=0.005, old_values=None):
+    """fixed_ppo::sample_loss_and_grad per row: (d_mean, d_log_std, d_value,
+    losses[policy, value, entropy, ratio])."""
+    a = contiguous(actions, np.float32).reshape(-1, 4)
+    b = len(a)
+    m = contiguous(means, np.float32).reshape(-1, 4)
+    ls, stride = _log_std(log_std, b)
+    ol, v, adv, ret = (contiguous(x, np.float32).reshape(-1) for x in (old_logp, values, advantages, returns))
+    ov = v if old_values is None else contiguous(old_values, np.float32).reshape(-1)
+    dm, dl = np.zeros((b, 4), np.float32), np.zeros((b, 4), np.float32)
+    dv, loss = np.zeros(b, np.float32), np.zeros((b, 4), np.float32)
+    check(lib().mdn_op_sample_loss_and_grad(ptr(a), ptr(m), ptr(ls), stride, ptr(ol), ptr(ov), ptr(v), ptr(adv),
+                                            ptr(ret), b, batch_size, clip, value_coef, entropy_coef, ptr(dm),
+                                            ptr(dl), ptr(dv), ptr(loss)))
+    return dm, dl, dv, loss
+
+
+def adam_update(params, grad, first, second, step, lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0):
+    """fixed_ppo::adam_update; returns updated (params, first, second) copies."""
+    p, g, m, v = (contiguous(x, np.float32).reshape(-1).copy() for x in (params, grad, first, second))
+    check(lib().mdn_op_adam_update(ptr(p), ptr(g), ptr(m), ptr(v), len(p), step, lr, beta1, beta2, eps,
+                                   weight_decay))
+    return p, m, v
+
+
+def ppo_self_tests(tolerance=2e-3):
+    """fixed_ppo::run_cpu_self_tests through the GPU operators."""
+    ok = ctypes.c_int(0)
+    check(lib().mdn_op_ppo_self_tests(tolerance, ctypes.byref(ok)))
+    return bool(ok.value)

@@ -134,6 +134,12 @@ class Sim:
         check(lib().mdn_sim_reset(self.h))
         return self.sync()
 
+    def validate_rollout(self):
+        """navigation_training::validate_rollout (navigation_training.hpp:27-35):
+        raises MdnError naming the first env whose task is not valid and
+        ready or whose plant mass is not finite and positive."""
+        check(lib().mdn_sim_validate_rollout(self.h))
+
     def collect(self, count=0):
         """Enqueue ``count`` ticks (0 = horizon); returns immediately."""
         check(lib().mdn_sim_collect(self.h, count))

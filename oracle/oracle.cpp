@@ -220,6 +220,16 @@ inline void clip_and_adam(std::vector<float>& grad, float* params, float* m, flo
 }
 
 // ---- Trainer: cpu_reference.hpp:112-615 + sim.metal semantics ------------
+// Default-mode shaping reward of one env-step (cpu_reference.hpp:497-500 ==
+// sim.metal:305): progress toward the goal doubled, a 0.01 step cost, a risk
+// penalty growing linearly as the step's minimum clearance falls below
+// 0.6 m, +10 on success and -10 on collision.
+inline float step_reward(float before, float after, float step_clearance, float risk_coef, bool success,
+                         bool collision) {
+    return (before - after) * 2.0f - .01f - risk_coef * clamp_f((0.6f - step_clearance) / 0.6f, 0.0f, 1.0f) +
+           (success ? 10.0f : 0.0f) - (collision ? 10.0f : 0.0f);
+}
+
 struct Trainer {
     MdnSimConfig cfg;
     uint32_t horizon, epochs, minibatch;
@@ -372,7 +382,7 @@ struct Trainer {
     }
 
     // sim.metal:159-181 == cpu_reference.hpp:379-394
-    void critic_observation(const MdnPhysicsState& s, const MdnWorld& w, const MdnSimRun& run, float* out) const {
+    static void critic_observation(const MdnPhysicsState& s, const MdnWorld& w, const MdnSimRun& run, float* out) {
         for (uint32_t j = 0; j < MDN_CRITIC_OBS; j++) out[j] = 0;
         for (int j = 0; j < 3; j++) {
             out[j] = (w.goal[j] - s.position[j]) / 10.0f;
@@ -645,8 +655,7 @@ struct Trainer {
         bool success = after < (cfg.mode == 20 ? .10f : .35f) && !collision;
         bool timeout = run.steps >= cfg.max_steps;
         const size_t row = size_t(tick) * cfg.n + n;
-        rewards[row] = (before - after) * 2.0f - .01f - cfg.risk_coef * clamp_f((0.6f - step_clearance) / 0.6f, 0.0f, 1.0f) +
-                       (success ? 10.0f : 0.0f) - (collision ? 10.0f : 0.0f);
+        rewards[row] = step_reward(before, after, step_clearance, cfg.risk_coef, success, collision);
         terminated[row] = uint8_t(collision || success);
         truncated[row] = uint8_t(timeout && !terminated[row]);
         if (tasks.enabled != 0) {  // sim.metal:307-315
@@ -1116,6 +1125,25 @@ void orc_init_policy(float* actor, float* critic) {
 void orc_minibatch_schedule(uint32_t rows, uint32_t minibatch, uint32_t epochs, uint32_t rollout, uint32_t* out) {
     const auto v = mdn::minibatch_schedule(rows, minibatch, epochs, rollout);
     std::copy(v.begin(), v.end(), out);
+}
+// fixed_ppo::adam_update (ppo.hpp:310-324) with weight decay; bias
+// corrections 1 - beta^step in float as the reference computes them.
+void orc_adam_update(float* p, const float* g, float* m, float* v, uint64_t n, uint64_t step, float lr, float b1,
+                     float b2, float eps, float wd) {
+    float c1 = 0.0f, c2 = 0.0f;
+    mdn::adam_corrections(step, b1, b2, &c1, &c2);
+    for (uint64_t i = 0; i < n; i++) {
+        const float gi = g[i] + wd * p[i];
+        m[i] = b1 * m[i] + (1.0f - b1) * gi;
+        v[i] = b2 * v[i] + (1.0f - b2) * gi * gi;
+        p[i] -= lr * (m[i] / c1) / (mdn::sqrt_f(v[i] / c2) + eps);
+    }
+}
+float orc_step_reward(float before, float after, float step_clearance, float risk_coef, int success, int collision) {
+    return orc::step_reward(before, after, step_clearance, risk_coef, success != 0, collision != 0);
+}
+void orc_critic_observation(const MdnPhysicsState* s, const MdnWorld* w, const MdnSimRun* run, float* out) {
+    orc::Trainer::critic_observation(*s, *w, *run, out);
 }
 void orc_crazyflie_params(MdnPhysicsParams* p) { *p = mdn::crazyflie_params(); }
 void orc_default_config(MdnSimConfig* c) { *c = mdn::default_config(); }

@@ -81,6 +81,9 @@ def oracle():
         _sig(lib, "orc_critic_forward_batch", None, P, P, U64, P, P)
         _sig(lib, "orc_init_policy", None, P, P)
         _sig(lib, "orc_minibatch_schedule", None, U32, U32, U32, U32, P)
+        _sig(lib, "orc_step_reward", F32, F32, F32, F32, F32, ctypes.c_int, ctypes.c_int)
+        _sig(lib, "orc_adam_update", None, P, P, P, P, U64, U64, F32, F32, F32, F32, F32)
+        _sig(lib, "orc_critic_observation", None, P, P, P, P)
         _sig(lib, "orc_crazyflie_params", None, P)
         _sig(lib, "orc_default_config", None, P)
         _sig(lib, "orc_num_threads", ctypes.c_int)

@@ -132,8 +132,14 @@ def test_wide_policy_export_matches_reference_loader(tmp_path):
     ckpt = str(tmp_path / "mode22.bin")
     open(ckpt, "wb").write(bytes(data))
     out = str(tmp_path / "wide.bin")
-    formats.export_wide_policy(ckpt, out)
+    record = formats.export_wide_policy(ckpt, out)
     meta, cam, w, h = formats.read_wide_policy(out)
+    import hashlib
+    import json
+    assert json.load(open(out + ".json")) == record
+    assert record["source_fnv1a64"] == h and record["actor_hidden"] == 64 and record["bytes"] == os.path.getsize(out)
+    assert record["nav_sha256"] == hashlib.sha256(open(out, "rb").read()).hexdigest()
+    assert record["source_critic_parameters"] == 2177 and record["sensor_profile"] == 1
     _, actor = formats.read_checkpoint(ckpt)
     assert int(meta["version"]) == 4 and int(meta["hidden_count"]) == 64 and w.size == 189 * 64 + 8
     assert np.array_equal(w, actor) and h == formats.fnv1a64_file(ckpt)
@@ -178,3 +184,34 @@ def test_wide_policy_round_trip_and_rejections(tmp_path):
     w[3] = 0.0
     meta["policy_mode"] = 2
     assert lib().mdn_navwid_write(path.encode(), ptr(meta), ptr(cam), ptr(w), w.size, 77) != 0
+
+
+def test_wide_policy_export_rejections(tmp_path):
+    """navigation_export_wide.py:27-40: a truncated actor/critic payload, a
+    non-finite actor weight and a sidecar naming another architecture or
+    camera are refused."""
+    import json
+    data = bytearray(open(os.path.join(GOLDEN, "guided-table-memory.bin.best"), "rb").read())
+    data[56:60] = np.uint32(22).tobytes()
+    actor_count, critic_count = np.frombuffer(bytes(data[12:20]), np.uint32)
+    end = 136 + 4 * int(actor_count + critic_count)
+    cases = {"truncated": bytes(data[:end - 4]), "nan": None}
+    bad = bytearray(data)
+    bad[136 + 40:136 + 44] = np.float32(np.nan).tobytes()
+    cases["nan"] = bytes(bad)
+    for name, blob in cases.items():
+        src = str(tmp_path / (name + ".bin"))
+        open(src, "wb").write(blob)
+        with pytest.raises(ValueError):
+            formats.export_wide_policy(src, str(tmp_path / (name + ".out")))
+    src = str(tmp_path / "ok.bin")
+    open(src, "wb").write(bytes(data[:end]))  # the actor/critic prefix alone is enough
+    formats.export_wide_policy(src, str(tmp_path / "ok.out"))
+    for sidecar in ({"actor_obs_dim": 184, "actor_hidden_dim": 256, "sensor_profile": "legacy"},
+                    {"actor_obs_dim": 184, "actor_hidden_dim": 64, "sensor_profile": "native"}):
+        open(src + ".train.json", "w").write(json.dumps(sidecar))
+        with pytest.raises(ValueError):
+            formats.export_wide_policy(src, str(tmp_path / "side.out"))
+    open(src + ".train.json", "w").write(json.dumps({"actor_obs_dim": 184, "actor_hidden_dim": 64,
+                                                      "sensor_profile": "legacy"}))
+    formats.export_wide_policy(src, str(tmp_path / "side.out"))

@@ -315,6 +315,34 @@ def test_adam_step_against_reference():
         assert np.abs(t.get(name + "_m") - m).max() < 1e-9
 
 
+def test_adam_update_operator():
+    """The oracle's fixed_ppo::adam_update: the closed-form first step
+    (ppo.hpp:254-266: m = 0.1 g, v = 0.001 g^2, p -= lr sign(g) at step 1),
+    the weight-decay term entering the gradient, and the reference's own
+    adam_update over several steps."""
+    p, g, m, v = (np.array([x], F) for x in (1.0, 0.25, 0.0, 0.0))
+    oracle().orc_adam_update(ptr(p), ptr(g), ptr(m), ptr(v), 1, 1, 0.01, 0.9, 0.999, 1e-8, 0.0)
+    # (1 - 0.999f) = 0.00100005 in float: the second moment is within 5e-5 relative
+    assert m[0] == pytest.approx(0.025, rel=1e-6) and v[0] == pytest.approx(6.25e-5, rel=1e-4)
+    assert p[0] == pytest.approx(0.99, abs=1e-6)
+    # weight decay 0.5 on p = 2 with g = 0 acts as a gradient of 1
+    p, g, m, v = (np.array([x], F) for x in (2.0, 0.0, 0.0, 0.0))
+    oracle().orc_adam_update(ptr(p), ptr(g), ptr(m), ptr(v), 1, 1, 0.01, 0.9, 0.999, 1e-8, 0.5)
+    assert m[0] == pytest.approx(0.1, rel=1e-6) and p[0] == pytest.approx(1.99, abs=1e-6)
+    if not ref_available():
+        pytest.skip("oracle/_ref not built")
+    rng = np.random.default_rng(2)
+    n = 4097
+    p = rng.normal(0, 1, n).astype(F)
+    m, v = np.zeros(n, F), np.zeros(n, F)
+    pr, mr, vr = p.copy(), m.copy(), v.copy()
+    for step in range(1, 6):
+        g = rng.normal(0, 1, n).astype(F)
+        oracle().orc_adam_update(ptr(p), ptr(g), ptr(m), ptr(v), n, step, 1e-3, 0.9, 0.999, 1e-8, 0.02)
+        ref().ref_adam_update(ptr(pr), ptr(g), ptr(mr), ptr(vr), n, step, 1e-3, 0.9, 0.999, 1e-8, 0.02)
+    assert np.array_equal(p, pr) and np.array_equal(m, mr) and np.array_equal(v, vr)
+
+
 def mt19937(seed):
     """std::mt19937 (the standard fixes its output sequence)."""
     mt = [0] * 624
@@ -337,28 +365,63 @@ def mt19937(seed):
         yield y
 
 
+def libcxx_shuffle(v, gen):
+    """libc++'s std::shuffle with uniform_int_distribution<ptrdiff_t> over a
+    32-bit engine: position k swaps with k + i, i drawn in [0, n-1-k] as the
+    low ceil(log2(range)) bits of one engine output, redrawn while >= range."""
+    n = len(v)
+    for k in range(n - 1):
+        rng = n - k
+        w = (rng - 1).bit_length()
+        while True:
+            u = next(gen) & ((1 << w) - 1)
+            if u < rng:
+                break
+        if u:
+            v[k], v[k + u] = v[k + u], v[k]
+
+
 def test_minibatch_schedule():
     g = mt19937(5489)
     for _ in range(9999):
         next(g)
     assert next(g) == 4123659995  # C++ standard [rand.predef]
-    rows, mb, epochs, rollout = 4096, 256, 3, 5
-    got = np.zeros(16 * epochs, np.uint32)
-    oracle().orc_minibatch_schedule(rows, mb, epochs, rollout, ptr(got))
-    starts = list(range(0, rows, mb))
-    gen = mt19937((0x9e3779b9 + rollout * 0x85ebca6b) & 0xffffffff)
+    # Known answer worked by hand from the first nine outputs of
+    # mt19937(0x9e3779b9) (rollout 0), five 256-row minibatches:
+    #   1596107820 & 7 = 4 -> swap 0,4;  3571572850 & 3 = 2 -> swap 1,3;
+    #   453773831 & 3 = 3 >= 3 rejected; 3932114620 & 3 = 0 -> keep;
+    #   2314964120 & 1 = 0 -> keep: epoch 0 = 1024 768 512 256 0.
+    #   1166738570 & 7 = 2 -> swap 0,2;  465115713 & 3 = 1 -> swap 1,2;
+    #   4090974150 & 3 = 2 -> swap 2,4;  1413185717 & 1 = 1 -> swap 3,4:
+    #   epoch 1 = 512 1024 0 768 256.
+    g = mt19937(0x9e3779b9)
+    assert [next(g) for _ in range(9)] == [1596107820, 3571572850, 453773831, 3932114620, 2314964120,
+                                           1166738570, 465115713, 4090974150, 1413185717]
+    got = np.zeros(10, np.uint32)
+    oracle().orc_minibatch_schedule(1280, 256, 2, 0, ptr(got))
+    assert got.tolist() == [1024, 768, 512, 256, 0, 512, 1024, 0, 768, 256]
+    # the restatement above over larger cases (ranges that are and are not
+    # powers of two, a ragged last minibatch, reshuffle only before epoch 1)
+    for rows, mb, epochs, rollout in [(4096, 256, 3, 5), (1000, 96, 2, 17), (262144, 256, 2, 3),
+                                      (1048576, 262144, 1, 9)]:
+        nb = (rows + mb - 1) // mb
+        got = np.zeros(nb * epochs, np.uint32)
+        oracle().orc_minibatch_schedule(rows, mb, epochs, rollout, ptr(got))
+        starts = list(range(0, rows, mb))
+        gen = mt19937((0x9e3779b9 + rollout * 0x85ebca6b) & 0xffffffff)
+        libcxx_shuffle(starts, gen)
+        want = list(starts)
+        for e in range(1, epochs):
+            if e == 1:
+                libcxx_shuffle(starts, gen)
+            want += starts
+        assert got.tolist() == want
+        for e in range(epochs):
+            assert sorted(got[nb * e:nb * (e + 1)].tolist()) == starts_sorted(rows, mb)
 
-    def fy(v):
-        for i in range(len(v), 1, -1):
-            j = (next(gen) * i) >> 32
-            v[i - 1], v[j] = v[j], v[i - 1]
-    fy(starts)
-    e0 = list(starts)
-    fy(starts)
-    want = e0 + starts + starts  # reshuffled only before epoch 1
-    assert got.tolist() == want
-    for e in range(epochs):
-        assert sorted(got[16 * e:16 * (e + 1)].tolist()) == list(range(0, rows, mb))
+
+def starts_sorted(rows, mb):
+    return list(range(0, rows, mb))
 
 
 @needs_ref
