@@ -286,6 +286,20 @@ int mdn_op_gae(uint32_t horizon, uint32_t n, const float* rewards, const float* 
                float* returns);
 int mdn_op_normalize(float* advantages, uint64_t count, float epsilon);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): mdn_op_normalize on `count` advantages already in device
+ * memory, normalised in place, enqueued on `stream` (a hipStream_t; NULL for
+ * the default stream) and not waited for.  It allocates nothing: the
+ * statistics' scratch is a fixed array in the library (about 2 MiB per GPU,
+ * held until the process ends) and `count` may not exceed
+ * MDN_NORMALIZE_NOALLOC_MAX (MDN_E_ARG otherwise).  Calls on one GPU share
+ * that array: calls that overlap in time on one GPU (other streams, other
+ * threads) race and must be serialised by the caller.  Results equal
+ * mdn_op_normalize's bit for bit. */
+#define MDN_NORMALIZE_NOALLOC_MAX (1ull << 26)
+int mdn_op_normalize_noalloc(float* advantages, uint64_t count, float epsilon, void* stream);
+
 /* fixed_ppo's operators (ppo.hpp:24-326), batched on the GPU over host
  * arrays.  The reference's header functions take one sample; these take
  * `batch` rows of the same layouts and return what a loop over the rows of

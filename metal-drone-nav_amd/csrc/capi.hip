@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1001,6 +1002,59 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon) {
                                  static_cast<float*>(stats.p), epsilon, nullptr));
     HIP_TRY(hipDeviceSynchronize());
     HIP_TRY(hipMemcpy(advantages, a.p, count * 4, hipMemcpyDeviceToHost));
+    return MDN_OK;
+}
+
+// ---------------------------------------------------------------- normalisation without allocation
+}  // extern "C"
+
+namespace {
+// Scratch of mdn_op_normalize_noalloc: the chunk partials of the advantage
+// statistics (one double per 256 rows) followed by the two statistics
+// (mean, inverse deviation).  Every GPU the library runs on holds its own
+// copy for the life of the process.
+constexpr uint64_t kNoallocPartials = MDN_NORMALIZE_NOALLOC_MAX / 256;
+constexpr size_t kNoallocBytes = kNoallocPartials * sizeof(double) + 2 * sizeof(float);
+static __device__ __align__(256) unsigned char scratch[kNoallocBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+unsigned char* g_scratch[kMaxDevices] = {};
+
+// The device address of the current GPU's scratch (host code never uses the
+// symbol itself: its host-side name is not a device address).
+int scratch_address(unsigned char** out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(MDN_E_ARG, "device ordinal beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(MDN_E_HIP, "hipGetSymbolAddress returned no address for the scratch array");
+        g_scratch[dev] = static_cast<unsigned char*>(p);
+    }
+    *out = g_scratch[dev];
+    return MDN_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int mdn_op_normalize_noalloc(float* advantages, uint64_t count, float epsilon, void* stream) {
+    if (!advantages) return fail(MDN_E_ARG, "mdn_op_normalize_noalloc: null");
+    if (count > MDN_NORMALIZE_NOALLOC_MAX)
+        return fail(MDN_E_ARG, "mdn_op_normalize_noalloc: count " + std::to_string(count) + " exceeds the scratch limit of " +
+                                   std::to_string(uint64_t(MDN_NORMALIZE_NOALLOC_MAX)) + " rows");
+    if (count == 0) return MDN_OK;
+    unsigned char* base = nullptr;
+    int rc = scratch_address(&base);
+    if (rc) return rc;
+    // partials are written by the first pass before any read, the
+    // statistics by the finishing passes: nothing needs clearing
+    double* part = reinterpret_cast<double*>(base);
+    float* stats = reinterpret_cast<float*>(base + kNoallocPartials * sizeof(double));
+    HIP_TRY(ppo_launch_normalize(advantages, count, part, stats, epsilon, static_cast<hipStream_t>(stream)));
     return MDN_OK;
 }
 

@@ -28,7 +28,7 @@ EXPORTS = [
     "mdn_sim_set_tasks", "mdn_sim_get_tasks", "mdn_task_default_config", "mdn_domain_stress_range", "mdn_sim_set_bank", "mdn_navwid_read",
     "mdn_navwid_write", "mdn_op_actor_forward", "mdn_op_critic_forward", "mdn_op_gaussian_log_prob",
     "mdn_op_sample_loss_and_grad", "mdn_op_adam_update", "mdn_op_ppo_self_tests", "mdn_sim_validate_rollout",
-    "mdn_checkpoint_read_params", "mdn_sim_get_bank",
+    "mdn_checkpoint_read_params", "mdn_op_normalize_noalloc", "mdn_sim_get_bank",
 ]
 
 P = ctypes.c_void_p
@@ -124,6 +124,7 @@ def lib():
         _sig(L, "mdn_op_ppo_self_tests", I32, F32, ctypes.POINTER(I32))
         _sig(L, "mdn_sim_validate_rollout", I32, P)
         _sig(L, "mdn_checkpoint_read_params", I32, ctypes.c_char_p, P, P, U64, P, U64)
+        _sig(L, "mdn_op_normalize_noalloc", I32, P, U64, F32, P)
         _sig(L, "mdn_sim_get_bank", I32, P, P)
         _lib = L
     return _lib
