@@ -51,28 +51,58 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(envs, target_s=12.0, actor_obs=181, geometry_memory=False):
-    """Bounded sample of the CPU oracle on this host: same world, policy and
-    PPO schedule shape (1 epoch x 4 minibatches) at 16 ticks per iteration."""
-    import numpy as np
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg_kw, horizon, actor_obs=181, target_s=10.0, envs_all=2048, envs_one=256):
+    """Bounded sample of the CPU oracle on this host: the workload's world,
+    policy, horizon and PPO schedule shape (1 epoch x 4 minibatches) at a
+    smaller env count (env-steps/s does not depend on it).  All cores: one
+    untimed iteration, then iterations until `target_s` has passed; one
+    core: one iteration at `envs_one` envs."""
     from oracle_lib import OracleTrainer, oracle, raptor_fixture
     from mdnav import abi
-    horizon = 16
-    cfg = abi.default_config(n=envs, family=1, speed=1.0, distance=3.0, geometry_memory=1 if geometry_memory else 0)
-    t = OracleTrainer(cfg, horizon, raptor_fixture()[0], epochs=1, minibatch=envs * horizon // 4)
-    if actor_obs != 181:
-        t.set_actor_obs(actor_obs)
-    done, start = 0, time.perf_counter()
-    while True:
-        t.iteration(done)
-        done += 1
-        el = time.perf_counter() - start
-        if el >= target_s or done >= 64:
-            break
-    threads = int(oracle().orc_num_threads())
-    return {"value": envs * horizon * done / el, "unit": "env-steps/s", "cores": threads, "kind": "port",
-            "sample": "%d envs x %d ticks x %d iterations (rollout + GAE + 1 epoch x 4 minibatches), %.1f s, "
-                      "%d OpenMP threads on %d host CPUs" % (envs, horizon, done, el, threads, os.cpu_count())}
+    lib = oracle()
+    all_threads = int(lib.orc_num_threads())
+
+    def run(envs, timed_min_s, warm):
+        cfg = abi.default_config(**dict(cfg_kw, n=envs))
+        t = OracleTrainer(cfg, horizon, raptor_fixture()[0], epochs=1, minibatch=envs * horizon // 4)
+        if actor_obs != 181:
+            t.set_actor_obs(actor_obs)
+        it = 0
+        for _ in range(warm):
+            t.iteration(it)
+            it += 1
+        done, start = 0, time.perf_counter()
+        while True:
+            t.iteration(it)
+            it += 1
+            done += 1
+            el = time.perf_counter() - start
+            if el >= timed_min_s or done >= 16:
+                return envs * horizon * done / el, done, el
+
+    value, done, el = run(envs_all, target_s, 1)
+    lib.orc_set_num_threads(1)
+    try:
+        single, done1, el1 = run(envs_one, 0.0, 0)
+    finally:
+        lib.orc_set_num_threads(all_threads)
+    return {"value": value, "unit": "env-steps/s", "cores": all_threads, "kind": "port",
+            "single_thread_value": single, "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
+            "sample": "all %d OpenMP threads: %d envs x %d ticks x %d timed iterations after one untimed "
+                      "(rollout + GAE + normalisation + 1 epoch x 4 minibatches), %.1f s; one thread: %d envs x "
+                      "%d ticks x %d iteration, %.1f s" % (all_threads, envs_all, horizon, done, el, envs_one,
+                                                          horizon, done1, el1)}
 
 
 def calib_copy(nbytes, repeats=3):
@@ -89,18 +119,44 @@ def calib_copy(nbytes, repeats=3):
                       "GBps": 2 * nbytes / (ms.value * 1e-3) / 1e9}), flush=True)
 
 
+TRAFFIC_PROFILE = "profiles/rollout_kernel_pmc_8192x128.md"
+MFMA_PROFILES = ("profiles/rollout_chunk_kernels_sq_mfma_8192x128.md",
+                 "profiles/wide_policy_kernels_mfma_8192x256_h5120.md")
+
+
+def profile_values(relpath, prefix):
+    """Machine-readable 'prefix<name>: value' lines of a committed rocprofv3
+    summary, as {name: value}."""
+    out = {}
+    try:
+        with open(os.path.join(ROOT, relpath)) as f:
+            for line in f:
+                if line.startswith(prefix) and ":" in line:
+                    name, value = line[len(prefix):].split(":", 1)
+                    out[name.strip()] = float(value)
+    except OSError:
+        pass
+    return out
+
+
 def traffic_from_profile():
     """HBM bytes per rollout launch from the committed PMC summary (the line
     'traffic_bytes_per_launch: N'), or None when it is absent."""
-    path = os.path.join(ROOT, "profiles", "rollout_kernel_pmc_8192x128.md")
-    try:
-        with open(path) as f:
-            for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return float(line.split(":", 1)[1])
-    except OSError:
-        pass
-    return None
+    return profile_values(TRAFFIC_PROFILE, "traffic_").get("bytes_per_launch")
+
+
+def mfma_util(kernels):
+    """Matrix-core utilisation per kernel from the committed rocprofv3
+    counter summaries (lines 'mfma_util_<kernel>: fraction')."""
+    out = {}
+    for path in MFMA_PROFILES:
+        for name, v in profile_values(path, "mfma_util_").items():
+            if name in kernels:
+                out[name] = v
+    if out:
+        out["source"] = ("rocprofv3 MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1,024 SIMDs), "
+                         "per dispatch of this workload, read from " + " and ".join(MFMA_PROFILES))
+    return out
 
 
 def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatch=32768):
@@ -162,7 +218,10 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
                      "frac": round(achieved / 2.5e15, 4), "traffic": None,
                      "kernel": "wide-policy forward + backward GEMM kernels (bf16 dense peak 2.5 PFLOP/s)",
                      "algorithmic_tflop_per_iteration": round((flop_eval + flop_fwd + flop_bwd) / 1e12, 2)},
-        "kernels": kernels, "gpu_seconds": round(gpu_s, 4), "cpu_baseline": None,
+        "kernels": kernels, "gpu_seconds": round(gpu_s, 4),
+        "mfma_util": mfma_util(("lp_actor_backward", "lp_actor_forward", "lp_critic_backward", "lp_critic_forward")),
+        "cpu_baseline": None,
+        "cpu_baseline_note": "not run: the CPU update of this workload is about 1e14 FLOP per iteration",
     }
     print(json.dumps(out), flush=True)
 
@@ -189,11 +248,14 @@ def main():
                          "tasks of family 12 with per-episode plants at amplitude 1, mode 22, guided actor with the "
                          "geometry memory, one tick per launch with the per-episode kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["small", "large", "stress"], default="small",
+    ap.add_argument("--workload", choices=["small", "large", "stress", "threats"], default="small",
                     help="small: 8,192 envs x 128 ticks, 181-64-4 actor (the headline metric); large: 8,192 envs x "
                          "256 ticks, 184-5120-4 actor (967,688 parameters) and 32-5120-1 critic on bf16 matrix cores, "
                          "4 epochs x 64 "
-                         "minibatches of 32,768; stress: 65,536 envs x 128 ticks, small actor")
+                         "minibatches of 32,768; stress: 65,536 envs x 128 ticks, small actor; threats: 8,192 envs "
+                         "x 256 ticks of the reference's moving-threat rehearsal mix (family 13: doorways, tables, "
+                         "random families and the two moving-sphere threat families, clean even lanes) with "
+                         "100 ms sensor and command delays, small actor")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="BYTES",
                     help="run only the plain copy kernel over BYTES (reads BYTES, writes BYTES per launch); "
                          "its FETCH_SIZE/WRITE_SIZE readings scale the rollout kernel's counters to bytes")
@@ -220,14 +282,19 @@ def main():
     from mdnav import PPOTrainer, Sim, abi
     if args.workload == "stress":
         args.envs, args.horizon, args.no_cpu_baseline = 65536, 128, True
+    if args.workload == "threats":
+        args.envs, args.horizon = 8192, 256
     N, T = args.envs, args.horizon
-    headline = (N, T) == (8192, 128) and args.actor_obs == 181 and not args.geometry_memory
+    headline = (N, T) == (8192, 128) and args.actor_obs == 181 and not args.geometry_memory and \
+        args.workload == "small" and not args.task_training
     epochs, minibatch = (1, N * T // 4) if args.schedule == "baseline" else (2, 256)
-    cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0,
-                             geometry_memory=1 if args.geometry_memory else 0)
+    cfg_kw = dict(family=1, speed=1.0, distance=3.0, geometry_memory=1 if args.geometry_memory else 0)
+    if args.workload == "threats":  # the reference's threat rehearsal with 100 ms delays (2 ticks at 20 Hz)
+        cfg_kw = dict(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=2)
     if args.task_training:  # navigation_training.hpp:119-123
-        cfg = abi.default_config(n=N, family=12, mode=22, speed=1.5, distance=8.0, max_steps=400, geometry_memory=1,
-                                 entropy_coef=0.001, learning_rate=0.0001)
+        cfg_kw = dict(family=12, mode=22, speed=1.5, distance=8.0, max_steps=400, geometry_memory=1,
+                      entropy_coef=0.001, learning_rate=0.0001)
+    cfg = abi.default_config(n=N, **cfg_kw)
     log("bench: creating sim N=%d T=%d schedule=%s" % (N, T, args.schedule))
     sim = Sim(cfg, T, lanes=args.lanes, actor_obs=args.actor_obs)
     if args.task_training:
@@ -249,6 +316,8 @@ def main():
     t0 = time.perf_counter()
     for _ in range(args.steps):
         sim.collect()
+        if args.task_training:  # navigation_training.hpp:149-150: reject bad draws before the update
+            sim.validate_rollout()
         ppo.rollout_update(it)
         it += 1
     gpu_s = sim.sync()
@@ -269,7 +338,8 @@ def main():
     achieved = flop_env_step * env_steps_launch / avg_s
     roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic_from_profile() if headline else None,
-                "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-kernel scaled)",
+                "traffic_unit": ("HBM bytes per launch, from %s (rocprofv3 FETCH_SIZE + WRITE_SIZE of this workload, "
+                                 "copy-kernel scaled), not measured in this run" % TRAFFIC_PROFILE),
                 "kernel": ("rollout_kernel (fused env step + rollout actor/critic, %d ticks per launch)" % T
                            if not args.geometry_memory else
                            "rollout_kernel (env step + rollout actor/critic, split at the hint: %d ticks in %d "
@@ -295,31 +365,47 @@ def main():
                                   "frac": round(BYTES_NORM * N * T / ns / PEAK_HBM, 4)}
 
     value = N * T * args.steps / wall
+    family = cfg_kw["family"]
+    if args.task_training:
+        data = ("synthetic: navigation tasks generated per episode (stage 2 clutter goals, family 12 worlds) with "
+                "per-episode plants at amplitude 1, random-init guided policy (seed 1789)")
+        workload = ("task training: stage-2 clutter tasks (family 12) with per-episode plants, mode 22, %d envs x "
+                    "%d ticks, guided actor 184-64-4 with the geometry-memory hint, %s PPO schedule, "
+                    "validate_rollout after every collect" % (N, T, args.schedule))
+    elif args.workload == "threats":
+        data = ("synthetic: seeded procedural worlds of the reference's threat rehearsal family 13 (per episode: "
+                "doorway, table, a random family 0-6, or a moving-sphere threat, families 10/11), random-init policy")
+        workload = ("moving-threat rehearsal mix, %d envs x %d ticks, 100 ms sensor and command delays (even envs "
+                    "clean), small actor 181-64-4, %s PPO schedule" % (N, T, args.schedule))
+    else:
+        data = "synthetic: seeded procedural worlds (reference family 1), random-init policy (seed 1789)"
+        workload = ("static-box world, %d envs x %d ticks, %s actor %d-64-4%s, %s PPO schedule"
+                    % (N, T, "small" if args.actor_obs == 181 else "guided", args.actor_obs,
+                       " with the geometry-memory hint" if args.geometry_memory else "", args.schedule))
     out = {
         "metric": ("env-steps/sec (rollout+PPO update) at 8,192 envs; HBM GB/s and MFMA util %" if headline else
                    "env-steps/sec (rollout+PPO update) at %d envs x %d ticks" % (N, T)),
         "value": round(value, 1), "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
-        "data": "synthetic: seeded procedural worlds (reference family 1), random-init policy (seed 1789)",
-        "config": {"workload": ("task training: stage-2 clutter tasks (family 12) with per-episode plants, mode 22, "
-                                "%d envs x %d ticks, guided actor 184-64-4 with the geometry-memory hint, %s PPO "
-                                "schedule" % (N, T, args.schedule) if args.task_training else
-                                "static-box world, %d envs x %d ticks, %s actor %d-64-4%s, %s PPO schedule"
-                                % (N, T, "small" if args.actor_obs == 181 else "guided", args.actor_obs,
-                                   " with the geometry-memory hint" if args.geometry_memory else "", args.schedule)),
-                   "envs": N, "horizon": T, "family": 1, "rays": 320, "actor": "%d-64-4" % args.actor_obs,
+        "data": data,
+        "config": {"workload": workload,
+                   "envs": N, "horizon": T, "family": family, "rays": 320, "actor": "%d-64-4" % args.actor_obs,
                    "critic": "32-64-1",
                    "epochs": epochs, "minibatch": minibatch, "lanes_per_env": args.lanes,
+                   "shapes": "the reference's own: 20x16 = 320 rays, 2x2-pooled %d-input actor, 32-input critic "
+                             "(BASELINE's literal 192-ray / 208-input / 64-64 shapes are not a configuration the "
+                             "reference builds)" % args.actor_obs,
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "kernels": kernels,
         "secondary_roofline": secondary,
+        "mfma_util": mfma_util(("rollout_kernel", "chunk_kernel")) if headline else {},
         "gpu_seconds": round(gpu_s, 4),
     }
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
-        out["cpu_baseline"] = cpu_baseline(N, actor_obs=args.actor_obs, geometry_memory=args.geometry_memory)
+        out["cpu_baseline"] = cpu_baseline(cfg_kw, T, actor_obs=args.actor_obs)
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)

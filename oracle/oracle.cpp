@@ -1148,5 +1148,6 @@ void orc_critic_observation(const MdnPhysicsState* s, const MdnWorld* w, const M
 void orc_crazyflie_params(MdnPhysicsParams* p) { *p = mdn::crazyflie_params(); }
 void orc_default_config(MdnSimConfig* c) { *c = mdn::default_config(); }
 int orc_num_threads() { return omp_get_max_threads(); }
+void orc_set_num_threads(int n) { omp_set_num_threads(n); }
 
 } // extern "C"

@@ -87,6 +87,7 @@ def oracle():
         _sig(lib, "orc_crazyflie_params", None, P)
         _sig(lib, "orc_default_config", None, P)
         _sig(lib, "orc_num_threads", ctypes.c_int)
+        _sig(lib, "orc_set_num_threads", None, ctypes.c_int)
         _sig(lib, "orc_trainer_set_runtime", None, P, P)
         _sig(lib, "orc_trainer_set_tasks", None, P, P)
         _sig(lib, "orc_trainer_reset", None, P)
