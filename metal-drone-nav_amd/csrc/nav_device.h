@@ -221,6 +221,194 @@ __device__ __forceinline__ float cast_ray_boxes(const BoxSlabs& bs, V d) {
     return fmax_f(0.0f, best);
 }
 
+// Fast path of cast_ray for worlds of up to 16 boxes, 8 spheres (kinds 1 and
+// 3) and 8 capped cylinders when no ray direction component is below the slab
+// epsilon.  Per env and frame the obstacles are tabulated in the env's LDS
+// scratch row by kind, with every per-obstacle constant of world.hpp:42-70
+// (q = p - c, q.q - r*r, r*r, the slab bounds -e - pp and e - pp) formed
+// once with the reference's operations; per ray only the ray-dependent terms
+// remain and the loops are branch-free with trip counts uniform over the
+// wavefront (the largest count of each kind among its envs; slots past an
+// env's own count are ignored).  Each obstacle's hit value is the one
+// cast_ray computes, and the minimum of hit values that are never NaN and
+// never negative does not depend on their order (a zero may change sign,
+// which the final fmax(0, best) maps to +0), so depths are bit-identical.
+constexpr uint32_t MIX_MAX_SPHERES = 8, MIX_MAX_CYLINDERS = 8;
+// Table words for wave-wide counts: boxes (6 each), spheres (4), cylinders (6).
+__device__ __forceinline__ uint32_t mix_words(uint32_t nb, uint32_t ns, uint32_t nc) { return 6 * nb + 4 * ns + 6 * nc; }
+struct MixCounts { uint32_t nb, ns, nc; };
+__device__ __forceinline__ bool mix_counts(const float* world, uint32_t count, MixCounts& m) {
+    m.nb = m.ns = m.nc = 0;
+    bool ok = count <= 16;
+    for (uint32_t i = 0; i < count && i < 16; i++) {
+        const uint32_t kind = float_bits(world[10 * i]);
+        m.nb += kind == 0u;
+        m.ns += kind == 1u || kind == 3u;
+        m.nc += kind == 2u;
+        ok = ok && kind <= 3u;
+    }
+    return ok && m.ns <= MIX_MAX_SPHERES && m.nc <= MIX_MAX_CYLINDERS;
+}
+// Writes the env's table for wave-wide counts (NB, NS, NC); lane `lane` of the
+// env's G-lane group takes obstacles lane, lane + G, ...  `centers` holds the
+// obstacle centres at the frame's time.
+__device__ __forceinline__ void mix_table(const float* world, const float* centers, uint32_t count, V p, uint32_t NB,
+                                          uint32_t NS, uint32_t lane, uint32_t G, float* tbl) {
+    for (uint32_t i = lane; i < count; i += G) {
+        const float* o = world + 10 * i;
+        const uint32_t kind = float_bits(o[0]);
+        const bool sph = kind == 1u || kind == 3u;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < i; j++) {
+            const uint32_t kj = float_bits(world[10 * j]);
+            rank += sph ? (kj == 1u || kj == 3u) : kj == kind;
+        }
+        const V c = mk(centers[3 * i], centers[3 * i + 1], centers[3 * i + 2]);
+        if (kind == 0u) {  // world.hpp:53: -e - pp and e - pp per axis
+            float* e = tbl + 6 * rank;
+            const float pp[3] = {p.x - c.x, p.y - c.y, p.z - c.z};
+#pragma unroll
+            for (int j = 0; j < 3; j++) { e[j] = -o[4 + j] - pp[j]; e[3 + j] = o[4 + j] - pp[j]; }
+        } else if (sph) {  // world.hpp:43: q and q.q - r*r
+            float* e = tbl + 6 * NB + 4 * rank;
+            const V q = sub3(p, c);
+            e[0] = q.x; e[1] = q.y; e[2] = q.z;
+            e[3] = dot3(q, q) - o[4] * o[4];
+        } else {  // world.hpp:60: q, q.x^2 + q.y^2 - r*r, half height, r*r
+            float* e = tbl + 6 * NB + 4 * NS + 6 * rank;
+            const V q = sub3(p, c);
+            const float r = o[4];
+            e[0] = q.x; e[1] = q.y; e[2] = q.z;
+            e[3] = q.x * q.x + q.y * q.y - r * r;
+            e[4] = o[6];
+            e[5] = r * r;
+        }
+    }
+}
+__device__ __forceinline__ float cast_ray_mixed(const float (&RA)[3], const float (&RB)[3], const float* tbl,
+                                                const MixCounts& own, uint32_t NB, uint32_t NS, uint32_t NC, V d) {
+    const float inv[3] = {recip_rn(d.x), recip_rn(d.y), recip_rn(d.z)};
+    float best = __builtin_fminf(12.0f, slab_fast(RA, RB, inv));
+    for (uint32_t i = 0; i < NB; i++) {
+        const float* e = tbl + 6 * i;
+        const float A[3] = {e[0], e[1], e[2]}, B[3] = {e[3], e[4], e[5]};
+        const float t = slab_fast(A, B, inv);
+        best = __builtin_fminf(best, i < own.nb ? t : 1000.0f);
+    }
+    const float* sp = tbl + 6 * NB;
+    for (uint32_t i = 0; i < NS; i++) {  // hit_sphere (world.hpp:42-47)
+        const float* e = sp + 4 * i;
+        const V q = mk(e[0], e[1], e[2]);
+        const float b = dot3(q, d), disc = b * b - e[3];
+        const float root = sqrt_f(disc);
+        const float lo = -b - root, hi = -b + root;
+        const float t = disc < 0 ? 1000.0f : (lo >= 0 ? lo : (hi >= 0 ? hi : 1000.0f));
+        best = __builtin_fminf(best, i < own.ns ? t : 1000.0f);
+    }
+    const float* cy = sp + 4 * NS;
+    const float a = d.x * d.x + d.y * d.y;
+    const bool caps = fabs_f(d.z) > 1e-8f;
+    for (uint32_t i = 0; i < NC; i++) {  // hit_cylinder (world.hpp:58-70)
+        const float* e = cy + 6 * i;
+        const V q = mk(e[0], e[1], e[2]);
+        const float h = e[4], rr = e[5];
+        const float b = q.x * d.x + q.y * d.y;
+        float t = 1000;
+        const float disc = b * b - a * e[3];
+        if (a > 1e-10f && disc >= 0) {
+            const float r0 = (-b - sqrt_f(disc)) / a, r1 = (-b + sqrt_f(disc)) / a;
+            if (r0 >= 0 && fabs_f(q.z + r0 * d.z) <= h) t = fmin_f(t, r0);
+            if (r1 >= 0 && fabs_f(q.z + r1 * d.z) <= h) t = fmin_f(t, r1);
+        }
+        if (caps)
+            for (int sign = -1; sign <= 1; sign += 2) {
+                const float tc = (float(sign) * h - q.z) / d.z;
+                const float x = q.x + tc * d.x, y = q.y + tc * d.y;
+                if (tc >= 0 && x * x + y * y <= rr) t = fmin_f(t, tc);
+            }
+        best = __builtin_fminf(best, i < own.nc ? t : 1000.0f);
+    }
+    return fmax_f(0.0f, best);
+}
+// cast_ray_mixed for the four rays of a pooled 2x2 block at once: each table
+// entry is read from LDS once for the four rays, and the four rays' chains
+// are independent.  Every ray needs all direction components >= 1e-8.
+// Data-dependent branches of world.hpp:42-70 are selects here: both sides
+// are evaluated and the taken side's value kept, which is the same value.
+__device__ __forceinline__ void cast_block_mixed(const float (&RA)[3], const float (&RB)[3], const float* tbl,
+                                                 const MixCounts& own, uint32_t NB, uint32_t NS, uint32_t NC,
+                                                 const V (&d)[4], float (&out)[4]) {
+    float inv[4][3], best[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        inv[r][0] = recip_rn(d[r].x); inv[r][1] = recip_rn(d[r].y); inv[r][2] = recip_rn(d[r].z);
+        best[r] = __builtin_fminf(12.0f, slab_fast(RA, RB, inv[r]));
+    }
+    for (uint32_t i = 0; i < NB; i++) {
+        const float* e = tbl + 6 * i;
+        const float A[3] = {e[0], e[1], e[2]}, B[3] = {e[3], e[4], e[5]};
+        const bool live = i < own.nb;
+#pragma unroll
+        for (int r = 0; r < 4; r++) best[r] = __builtin_fminf(best[r], live ? slab_fast(A, B, inv[r]) : 1000.0f);
+    }
+    const float* sp = tbl + 6 * NB;
+    for (uint32_t i = 0; i < NS; i++) {  // hit_sphere (world.hpp:42-47)
+        const float* e = sp + 4 * i;
+        const V q = mk(e[0], e[1], e[2]);
+        const float k = e[3];
+        const bool live = i < own.ns;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float b = dot3(q, d[r]), disc = b * b - k;
+            const float root = sqrt_f(disc);
+            const float lo = -b - root, hi = -b + root;
+            const float t = disc < 0 ? 1000.0f : (lo >= 0 ? lo : (hi >= 0 ? hi : 1000.0f));
+            best[r] = __builtin_fminf(best[r], live ? t : 1000.0f);
+        }
+    }
+    const float* cy = sp + 4 * NS;
+    float a[4];
+    bool caps[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        a[r] = d[r].x * d[r].x + d[r].y * d[r].y;
+        caps[r] = fabs_f(d[r].z) > 1e-8f;
+    }
+    for (uint32_t i = 0; i < NC; i++) {  // hit_cylinder (world.hpp:58-70)
+        const float* e = cy + 6 * i;
+        const V q = mk(e[0], e[1], e[2]);
+        const float k = e[3], h = e[4], rr = e[5];
+        const bool live = i < own.nc;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float b = q.x * d[r].x + q.y * d[r].y;
+            const float disc = b * b - a[r] * k;
+            const bool side = a[r] > 1e-10f && disc >= 0;
+            const float root = sqrt_f(disc);
+            const float r0 = (-b - root) / a[r], r1 = (-b + root) / a[r];
+            float t = 1000;
+            t = side && r0 >= 0 && fabs_f(q.z + r0 * d[r].z) <= h ? fmin_f(t, r0) : t;
+            t = side && r1 >= 0 && fabs_f(q.z + r1 * d[r].z) <= h ? fmin_f(t, r1) : t;
+#pragma unroll
+            for (int sign = -1; sign <= 1; sign += 2) {
+                const float tc = (float(sign) * h - q.z) / d[r].z;
+                const float x = q.x + tc * d[r].x, y = q.y + tc * d[r].y;
+                t = caps[r] && tc >= 0 && x * x + y * y <= rr ? fmin_f(t, tc) : t;
+            }
+            best[r] = __builtin_fminf(best[r], live ? t : 1000.0f);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) out[r] = fmax_f(0.0f, best[r]);
+}
+
+// Largest value of a wave-uniform-call argument over the 64 lanes.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = max(v, uint32_t(__shfl_xor(int(v), off, 64)));
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
 // world.hpp:84-99
 __device__ __forceinline__ float room_clearance(V p) {
     return fmin_f(fmin_f(p.x + 2, 14 - p.x), fmin_f(fmin_f(p.y + 5, 5 - p.y), fmin_f(p.z, 5 - p.z))) - 0.18f;

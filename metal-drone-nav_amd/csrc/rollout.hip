@@ -611,7 +611,23 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         // its pooled 2x2 blocks and keeps their minimum
         float R[9];
         rotation(s.q, R);
-        if (active && observe && r.steps % C.sensor_period == 0) {
+        const bool depth_now = active && observe && r.steps % C.sensor_period == 0;
+        // ray-cast path: the register box table when every env of the
+        // wavefront casting this tick has a boxes-only world, else the
+        // per-kind LDS tables (envs whose world they cannot hold take the
+        // generic cast); the env's observation row is free until observe
+        const bool boxes = boxes_only(world, count);
+        const bool wave_boxes = !__any(depth_now && !boxes);
+        MixCounts mix{0, 0, 0};
+        bool mix_ok = false;
+        uint32_t NB = 0, NS = 0, NC = 0;
+        if (!wave_boxes) {
+            if (depth_now) mix_ok = mix_counts(world, count, mix);
+            NB = wave_max_u32(mix_ok ? mix.nb : 0u);
+            NS = wave_max_u32(mix_ok ? mix.ns : 0u);
+            NC = wave_max_u32(mix_ok ? mix.nc : 0u);
+        }
+        if (depth_now) {
             const uint32_t fidx = r.steps / C.sensor_period;
             const uint32_t slot8 = fidx % 8, slotk = fidx % K;
             const float mx = 0.0f;
@@ -625,12 +641,39 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             const float noise = clean_env(C, nn) ? 0.0f : C.depth_noise;
             const float drop = clean_env(C, nn) ? 0.0f : C.dropout;
             float* ring = a.sensors + (size_t(nn) * 8 + slot8) * PIX;
-            const bool fast = boxes_only(world, count);
+            const bool fast = wave_boxes && boxes;
             BoxSlabs bs;
             if (fast) make_box_slabs(world, s_cent[grp], count, origin, bs);
+            float* tbl = s_obs[grp];
+            float RA[3], RB[3];
+            if (mix_ok) {
+                mix_table(world, s_cent[grp], count, origin, NB, NS, lane, G, tbl);
+                const float pr[3] = {origin.x - 6.0f, origin.y - 0.0f, origin.z - 2.5f}, er[3] = {8.0f, 5.0f, 2.5f};
+#pragma unroll
+                for (int j = 0; j < 3; j++) { RA[j] = -er[j] - pr[j]; RB[j] = er[j] - pr[j]; }
+            }
+            group_sync();
             for (uint32_t b = lane; b < POOL; b += G) {
                 const uint32_t y = (b / 10) * 2, x = (b % 10) * 2;
                 float pooled = 12.0f;
+                // the block's four rays through the per-kind tables together
+                float mixed[4] = {0, 0, 0, 0};
+                bool block_mixed = false;
+                if (mix_ok) {
+                    V dq[4];
+                    bool all_axes = true;
+#pragma unroll
+                    for (uint32_t q4 = 0; q4 < 4; q4++) {
+                        const uint32_t k = (y + q4 / 2) * 20 + x + q4 % 2;
+                        const float rx = CAM[3 * k], ry = CAM[3 * k + 1], rz = CAM[3 * k + 2];
+                        dq[q4] = mk(R[0] * rx + R[1] * ry + R[2] * rz, R[3] * rx + R[4] * ry + R[5] * rz,
+                                    R[6] * rx + R[7] * ry + R[8] * rz);
+                        all_axes = all_axes && (__builtin_fabsf(dq[q4].x) >= 1e-8f) &&
+                                   (__builtin_fabsf(dq[q4].y) >= 1e-8f) && (__builtin_fabsf(dq[q4].z) >= 1e-8f);
+                    }
+                    block_mixed = all_axes;
+                    if (block_mixed) cast_block_mixed(RA, RB, tbl, mix, NB, NS, NC, dq, mixed);
+                }
 #pragma unroll
                 for (uint32_t dy = 0; dy < 2; dy++)
 #pragma unroll
@@ -644,6 +687,10 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                                           (__builtin_fabsf(d.z) >= 1e-8f);
                         if (fast && axes)
                             depth = cast_ray_boxes(bs, d);
+                        else if (block_mixed)
+                            depth = mixed[dy * 2 + dx];
+                        else if (mix_ok && axes)
+                            depth = cast_ray_mixed(RA, RB, tbl, mix, NB, NS, NC, d);
                         else
                             depth = cast_ray(world, s_cent[grp], count, origin, d);
                         if (noise != 0 || drop != 0) {

@@ -242,6 +242,27 @@ def test_stress_scale_bit_exact():
     assert ora.get("runs")["episodes"].sum() >= 65536
 
 
+@pytest.mark.parametrize("family,ticks", [(13, 12), (6, 6), (2, 6), (3, 6), (7, 6)])
+def test_mixed_world_depth_bit_exact(family, ticks):
+    """Worlds of boxes, spheres (moving ones among them) and cylinders at
+    scale (2,048 envs, so wavefronts mix world kinds): the per-kind LDS
+    tables of the ray cast and the generic cast give depth frames, pooled
+    observations and every other buffer bit-identical to the oracle, through
+    resets (episodes end after 4 steps)."""
+    say("case: mixed worlds family %d, N=2048 T=%d" % (family, ticks))
+    cfg = config(n=2048, family=family, speed=1.5, distance=4.0, max_steps=4)
+    sim, _, ora = make_pair(cfg, ticks)
+    sim.collect()
+    sim.sync()
+    ora.collect()
+    bad = compare(sim, ora, ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
+    assert not bad, bad
+    kinds = ora.get("worlds")["obstacles"]["kind"]
+    counts = ora.get("worlds")["count"]
+    present = {int(k) for n in range(len(counts)) for k in kinds[n][:counts[n]]}
+    say("  obstacle kinds present: %s" % sorted(present))
+
+
 @pytest.mark.parametrize("variant", ["k2_production", "k4_threats_delays", "k8_sensor_delay6"])
 def test_geometry_prior_bit_exact(variant):
     """The 184-input actor (ppo.hpp:30-34): the geometry-prior hint computed in
