@@ -78,6 +78,26 @@ inline MdnPhysicsParams crazyflie_params() {
     return p;
 }
 
+// Whether a plant has the standard quadrotor structure the device's
+// specialised derivative assumes: thrust directions (0, 0, 1), torque
+// directions (0, 0, +-1), rotors in the z = 0 plane, diagonal inertia and
+// inverse, gravity along z (zeros as +0.0 bit patterns).
+inline bool quad_structure(const MdnPhysicsParams& p) {
+    auto bits = [](float x) { uint32_t u; std::memcpy(&u, &x, 4); return u; };
+    bool ok = true;
+    for (int r = 0; r < 4; ++r) {
+        ok = ok && bits(p.rotor_thrust_directions[3 * r]) == 0u && bits(p.rotor_thrust_directions[3 * r + 1]) == 0u &&
+             bits(p.rotor_thrust_directions[3 * r + 2]) == bits(1.0f);
+        ok = ok && bits(p.rotor_torque_directions[3 * r]) == 0u && bits(p.rotor_torque_directions[3 * r + 1]) == 0u &&
+             (bits(p.rotor_torque_directions[3 * r + 2]) == bits(1.0f) ||
+              bits(p.rotor_torque_directions[3 * r + 2]) == bits(-1.0f));
+        ok = ok && bits(p.rotor_positions[3 * r + 2]) == 0u;
+    }
+    for (int i = 0; i < 9; ++i)
+        if (i % 4 != 0) ok = ok && bits(p.inertia[i]) == 0u && bits(p.inertia_inverse[i]) == 0u;
+    return ok && bits(p.gravity_world[0]) == 0u && bits(p.gravity_world[1]) == 0u;
+}
+
 // Default run configuration of main.mm:461-464.
 inline MdnSimConfig default_config() {
     MdnSimConfig c;

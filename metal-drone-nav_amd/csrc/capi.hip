@@ -132,6 +132,7 @@ struct MdnSim {
             a.recip_rise[i] = 1.0 / double(phys.rotor_time_constants_rising[i]);
             a.recip_fall[i] = 1.0 / double(phys.rotor_time_constants_falling[i]);
         }
+        a.quad = mdn::quad_structure(phys) ? 1u : 0u;
         a.ext_means = nullptr; a.ext_log_std = nullptr; a.tick0 = 0; a.split = 0;
         a.sensor_dt = float(cfg.sensor_period) * phys.dt * float(cfg.substeps);
         a.inv_sensor_dt = 1.0 / double(std::max(a.sensor_dt, 1e-3f));

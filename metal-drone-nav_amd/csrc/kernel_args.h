@@ -41,6 +41,9 @@ struct RolloutArgs {
     // uniform kernel arguments (scalar registers) instead of occupying
     // vector registers for the whole launch
     double recip_mass, recip_rise[4], recip_fall[4];
+    // 1 when the nominal plant has the standard quadrotor structure
+    // (derivative_quad applies); set by the host per launch
+    uint32_t quad;
     uint32_t count;        // ticks in this launch
     uint32_t horizon;      // row blocks of the rollout buffers
     // Split ticks (policy evaluated outside the kernel, e.g. a wide actor):

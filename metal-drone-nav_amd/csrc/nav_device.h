@@ -155,37 +155,82 @@ __device__ __forceinline__ float cast_ray(const float* world, const float* cente
 }
 
 // Fast path of cast_ray for a world of up to 8 axis-aligned boxes when no
-// ray direction component is below the slab epsilon.  Per env and tick the
+// ray direction component is below the slab epsilon.  Per env and frame the
 // constants (-e - pp) and (e - pp) of world.hpp:53 are formed once (same
-// operations, hoisted out of the ray loop); per ray only the products with
-// 1/d and the interval updates remain.  Inside the slab the hardware
-// min/max may differ from the select form only in the sign of a zero, which
-// the final fmax(0, best) of world.hpp:82 maps to +0, so depths are
-// bit-identical to cast_ray.
-// Slot 0: room; slots 1..8: boxes.  Slots past the world's count hold a
-// zero-size box at (1e30, 1e30, 1e30): a ray either misses it (1000) or hits
-// it beyond 1e22, so it never lowers a depth capped at 12 and the slab loop
-// needs no per-box test.
-struct BoxSlabs {
-    float A[9][3], B[9][3];
-};
-__device__ __forceinline__ void make_box_slabs(const float* world, const float* centers, uint32_t count, V p,
-                                               BoxSlabs& bs) {
-    const float pr[3] = {p.x - 6.0f, p.y - 0.0f, p.z - 2.5f}, er[3] = {8.0f, 5.0f, 2.5f};
+// operations, hoisted out of the ray loop) into a slab table in LDS; per ray
+// only the products with 1/d and the interval updates remain.  Inside the
+// slab the hardware min/max may differ from the select form only in the sign
+// of a zero, which the final fmax(0, best) of world.hpp:82 maps to +0, and
+// the minimum of hit values that are never NaN does not depend on their
+// order, so depths are bit-identical to cast_ray.
+// Table words: slab 0 the room, slab 1 + i box i, 6 words each
+// [A0 A1 A2 B0 B1 B2]; then the ray origin (3), the camera rotation (9) and
+// the strip masks of the boxes (2 words, BOX_TABLE_STRIPS).
+constexpr uint32_t BOX_TABLE_ORIGIN = 54, BOX_TABLE_ROT = 57, BOX_TABLE_STRIPS = 66, BOX_TABLE_WORDS = 68;
+__device__ __forceinline__ void box_slab(const float* world, const float* centers, uint32_t i, V p, float (&A)[3],
+                                         float (&B)[3]) {
+    if (i == 0) {  // the room
+        const float pr[3] = {p.x - 6.0f, p.y - 0.0f, p.z - 2.5f}, er[3] = {8.0f, 5.0f, 2.5f};
 #pragma unroll
-    for (int j = 0; j < 3; j++) { bs.A[0][j] = -er[j] - pr[j]; bs.B[0][j] = er[j] - pr[j]; }
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float* o = world + 10 * i;
-        const bool live = uint32_t(i) < count;
-        const float cc[3] = {centers[3 * i], centers[3 * i + 1], centers[3 * i + 2]};
-        const float pp[3] = {p.x - cc[0], p.y - cc[1], p.z - cc[2]};
-#pragma unroll
-        for (int j = 0; j < 3; j++) {
-            bs.A[i + 1][j] = live ? -o[4 + j] - pp[j] : 1e30f;
-            bs.B[i + 1][j] = live ? o[4 + j] - pp[j] : 1e30f;
-        }
+        for (int j = 0; j < 3; j++) { A[j] = -er[j] - pr[j]; B[j] = er[j] - pr[j]; }
+        return;
     }
+    const float* o = world + 10 * (i - 1);
+    const float* c = centers + 3 * (i - 1);
+    const float pp[3] = {p.x - c[0], p.y - c[1], p.z - c[2]};
+#pragma unroll
+    for (int j = 0; j < 3; j++) { A[j] = -o[4 + j] - pp[j]; B[j] = o[4 + j] - pp[j]; }
+}
+
+// Vertical strips of the depth frame (4 of its 20 columns each, 5 strips)
+// whose rays can reach box [A, B] (coordinates relative to the ray origin)
+// at a hit value below 12, as a 5-bit mask.  R is the camera rotation
+// (row-major, world = R camera).  Camera rays are (1, -y, -z) normalised with
+// |y| <= 0.95 and |z| <= 0.703125 at the pixel centres, so the rays of a strip
+// lie in the wedge between the planes through its outer columns (the
+// frame's rows and columns follow the camera rays of the sim's setup).  A box is
+// left out of a strip only when one of those planes (or the image's top,
+// bottom or back plane) separates it from the wedge with a gap above 1e-3 m,
+// or when all of it lies beyond 12.01 m.  Rounding moves a slab test's
+// interval ends by about 1e-6 m (relative 2^-24 of distances under 20 m, and
+// of a rotation within 1e-6 of orthonormal), so such a box yields a miss or a
+// value of at least 12 for every ray of the strip, and leaving it out does
+// not change the depth.
+__device__ __forceinline__ uint32_t box_strips(const float (&A)[3], const float (&B)[3], const float* R) {
+    const float gap = 2e-3f;  // plane normals below have length <= 1.7
+    float d2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const float c = fmin_f(fmax_f(0.0f, A[j]), B[j]);
+        d2 += c * c;
+    }
+    if (d2 > 12.01f * 12.01f) return 0u;
+    const float f[3] = {R[0], R[3], R[6]}, l[3] = {R[1], R[4], R[7]}, u[3] = {R[2], R[5], R[8]};
+    // smallest value of n . x over the box
+    auto support = [&](const float (&n)[3]) {
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 3; j++) m += fmin_f(n[j] * A[j], n[j] * B[j]);
+        return m;
+    };
+    const float tv = 0.9375f * MDN_SENSOR_TAN_V;  // |z| of the outer pixel rows
+    {
+        const float behind[3] = {-f[0], -f[1], -f[2]};
+        const float top[3] = {-tv * f[0] - u[0], -tv * f[1] - u[1], -tv * f[2] - u[2]};
+        const float bottom[3] = {-tv * f[0] + u[0], -tv * f[1] + u[1], -tv * f[2] + u[2]};
+        if (support(behind) > gap || support(top) > gap || support(bottom) > gap) return 0u;
+    }
+    uint32_t mask = 0;
+#pragma unroll
+    for (uint32_t st = 0; st < 5; st++) {
+        // ray ratio Y/X = -y(col), decreasing with the column
+        const float r_hi = -((float(4 * st) + 0.5f) / 20.0f * 2.0f - 1.0f) * MDN_SENSOR_TAN_H;
+        const float r_lo = -((float(4 * st + 3) + 0.5f) / 20.0f * 2.0f - 1.0f) * MDN_SENSOR_TAN_H;
+        const float left[3] = {-r_hi * f[0] + l[0], -r_hi * f[1] + l[1], -r_hi * f[2] + l[2]};
+        const float right[3] = {r_lo * f[0] - l[0], r_lo * f[1] - l[1], r_lo * f[2] - l[2]};
+        if (!(support(left) > gap || support(right) > gap)) mask |= 1u << st;
+    }
+    return mask;
 }
 __device__ __forceinline__ bool boxes_only(const float* world, uint32_t count) {
     if (count > 8) return false;
@@ -213,14 +258,6 @@ __device__ __forceinline__ float recip_rn(float d) {
     const float y = __builtin_amdgcn_rcpf(d);
     return __builtin_fmaf(__builtin_fmaf(-d, y, 1.0f), y, y);
 }
-__device__ __forceinline__ float cast_ray_boxes(const BoxSlabs& bs, V d) {
-    const float inv[3] = {recip_rn(d.x), recip_rn(d.y), recip_rn(d.z)};
-    float best = __builtin_fminf(12.0f, slab_fast(bs.A[0], bs.B[0], inv));
-#pragma unroll
-    for (int i = 1; i < 9; i++) best = __builtin_fminf(best, slab_fast(bs.A[i], bs.B[i], inv));
-    return fmax_f(0.0f, best);
-}
-
 // Fast path of cast_ray for worlds of up to 16 boxes, 8 spheres (kinds 1 and
 // 3) and 8 capped cylinders when no ray direction component is below the slab
 // epsilon.  Per env and frame the obstacles are tabulated in the env's LDS
@@ -689,6 +726,81 @@ __device__ __forceinline__ void derivative(const MdnPhysicsParams& P, const Phys
     }
 }
 
+// derivative() for a plant of the standard quadrotor structure (the host
+// checks it per launch): every rotor thrusts along body z (direction
+// (0, 0, 1)) with a torque direction (0, 0, +-1), rotors sit in the z = 0
+// plane, the inertia and its inverse are diagonal and gravity points along
+// z.  The terms that structure makes zero are left out; every other term is
+// the same operation on the same operands in the same order, so each
+// derivative value equals derivative()'s (x + 0 = x and 0 - y = -y exactly;
+// only the sign of a zero may differ, and the derivative has no operation -
+// a division by a computed value, a sign test - that turns the sign of a zero
+// into a difference of value).  Those values reach the state only as addends
+// of state components, so when no state component is -0 (no_negative_zero)
+// every stage state and the next state are bit-identical: s + (+-0) is s for
+// s != 0 and +0 for s = +0.  wm = wind / mass, formed once per tick with the
+// same division.
+__device__ __forceinline__ void derivative_quad(const MdnPhysicsParams& P, const PhysRecip& RP, const State& s,
+                                                const float sp[4], const float wm[3], State& d) {
+    float m[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float speed = s.rpm[r];
+        const float* c = &P.rotor_thrust_coefficients[3 * r];
+        m[r] = c[0] + c[1] * speed + c[2] * speed * speed;
+    }
+    const float* a = P.rotor_positions;
+    const float* td = P.rotor_torque_directions;
+    const float* K = P.rotor_torque_constants;
+    // thrust (0, 0, T); torque from the rotor arms (y m, -x m, 0) and the
+    // rotor drag (0, 0, td m K), accumulated rotor by rotor as physics.hpp:70-86
+    const float T = ((m[0] + m[1]) + m[2]) + m[3];
+    const float t0 = ((a[1] * m[0] + a[4] * m[1]) + a[7] * m[2]) + a[10] * m[3];
+    const float t1 = ((-(a[0] * m[0]) - a[3] * m[1]) - a[6] * m[2]) - a[9] * m[3];
+    const float t2 = ((td[2] * m[0] * K[0] + td[5] * m[1] * K[1]) + td[8] * m[2] * K[2]) + td[11] * m[3] * K[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) d.p[i] = s.v[i];
+    const float* q = s.q;
+    const float* w = s.w;
+    d.q[0] = -q[1] * w[0] - q[2] * w[1] - q[3] * w[2];
+    d.q[1] = q[0] * w[0] + q[2] * w[2] - q[3] * w[1];
+    d.q[2] = q[0] * w[1] + q[3] * w[0] - q[1] * w[2];
+    d.q[3] = q[0] * w[2] + q[1] * w[1] - q[2] * w[0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d.q[i] *= 0.5f;
+    // rotate_body_to_world (physics.hpp:51-58) of (0, 0, T)
+    const float tx = 2.0f * (q[2] * T);
+    const float ty = 2.0f * -(q[1] * T);
+    d.v[0] = q[0] * tx - q[3] * ty;
+    d.v[1] = q[0] * ty + q[3] * tx;
+    d.v[2] = T + q[1] * ty - q[2] * tx;
+    d.v[0] = div_r(d.v[0], RP.mass) + wm[0];
+    d.v[1] = div_r(d.v[1], RP.mass) + wm[1];
+    d.v[2] = div_r(d.v[2], RP.mass) + P.gravity_world[2] + wm[2];
+    const float am0 = P.inertia[0] * w[0], am1 = P.inertia[4] * w[1], am2 = P.inertia[8] * w[2];
+    const float g0 = w[1] * am2 - w[2] * am1;
+    const float g1 = w[2] * am0 - w[0] * am2;
+    const float g2 = w[0] * am1 - w[1] * am0;
+    d.w[0] = P.inertia_inverse[0] * (t0 - g0);
+    d.w[1] = P.inertia_inverse[4] * (t1 - g1);
+    d.w[2] = P.inertia_inverse[8] * (t2 - g2);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const double inv_tau = sp[r] >= s.rpm[r] ? RP.rise[r] : RP.fall[r];
+        d.rpm[r] = div_r(sp[r] - s.rpm[r], inv_tau);
+    }
+}
+
+// true when no component of s is -0 (the condition derivative_quad needs;
+// a physics step keeps it, since a sum is -0 only when both addends are)
+__device__ __forceinline__ bool no_negative_zero(const State& s) {
+    const float* a = &s.p[0];
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 17; ++i) ok = ok && float_bits(a[i]) != 0x80000000u;
+    return ok;
+}
+
 __device__ __forceinline__ void axpy_state(const State& s, const State& d, float scale, State& out) {
     const float* a = &s.p[0];
     const float* b = &d.p[0];
@@ -697,7 +809,9 @@ __device__ __forceinline__ void axpy_state(const State& s, const State& d, float
     for (int i = 0; i < 17; ++i) o[i] = a[i] + scale * b[i];
 }
 
-// physics.hpp:122-179
+// physics.hpp:122-179.  QUAD: the standard-structure derivative
+// (derivative_quad; `wind` is then wind / mass).
+template <bool QUAD = false>
 __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const PhysRecip& RP, const State& s,
                                              const float action[4], const float wind[3], State& next) {
     float sp[4];
@@ -712,10 +826,10 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const Ph
     // k1 + 2 k2 + 2 k3 + k4 accumulated left to right as it is written in
     // physics.hpp:133-142, so only one stage derivative is live at a time.
     State k, acc, tmp;
-    derivative(P, RP, s, sp, wind, k);
+    if constexpr (QUAD) derivative_quad(P, RP, s, sp, wind, k); else derivative(P, RP, s, sp, wind, k);
     axpy_state(s, k, 0.5f * P.dt, tmp);
     acc = k;
-    derivative(P, RP, tmp, sp, wind, k);
+    if constexpr (QUAD) derivative_quad(P, RP, tmp, sp, wind, k); else derivative(P, RP, tmp, sp, wind, k);
     axpy_state(s, k, 0.5f * P.dt, tmp);
     {
         float* a = &acc.p[0];
@@ -723,7 +837,7 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const Ph
 #pragma unroll
         for (int i = 0; i < 17; ++i) a[i] = a[i] + 2.0f * b[i];
     }
-    derivative(P, RP, tmp, sp, wind, k);
+    if constexpr (QUAD) derivative_quad(P, RP, tmp, sp, wind, k); else derivative(P, RP, tmp, sp, wind, k);
     axpy_state(s, k, P.dt, tmp);
     {
         float* a = &acc.p[0];
@@ -731,7 +845,7 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const Ph
 #pragma unroll
         for (int i = 0; i < 17; ++i) a[i] = a[i] + 2.0f * b[i];
     }
-    derivative(P, RP, tmp, sp, wind, k);
+    if constexpr (QUAD) derivative_quad(P, RP, tmp, sp, wind, k); else derivative(P, RP, tmp, sp, wind, k);
     const float* a0 = &s.p[0];
     const float* ak = &k.p[0];
     float* ac = &acc.p[0];

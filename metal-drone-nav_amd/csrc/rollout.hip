@@ -341,6 +341,48 @@ __device__ __forceinline__ void wg_layer(const float* x, const float* w1t, const
     }
 }
 
+// wg_layer with the weight operands already in registers: bw[q][kk] is
+// w1t[4 kk + l/16][unit of tile q] for lane l (see critic_operands).
+template <uint32_t D, uint32_t XS, uint32_t OS>
+__device__ __forceinline__ void wg_layer_rb(const float* x, const float (&bw)[2][D / 4], const float* b1, float* out) {
+    static_assert(D % 4 == 0, "whole k-steps");
+    const uint32_t wv = threadIdx.x / 64, l = threadIdx.x % 64;
+    uint32_t env[2], unit[2];
+    v4f acc[2];
+#pragma unroll
+    for (uint32_t q = 0; q < 2; q++) {
+        const uint32_t tile = 2 * wv + q;
+        env[q] = 16 * (tile / 4) + l % 16;
+        unit[q] = 16 * (tile % 4) + l % 16;
+        const float bias = b1[unit[q]];
+        acc[q][0] = bias; acc[q][1] = bias; acc[q][2] = bias; acc[q][3] = bias;
+    }
+#pragma unroll
+    for (uint32_t kk = 0; kk < D / 4; kk++) {
+        const uint32_t k = 4 * kk + l / 16;
+#pragma unroll
+        for (uint32_t q = 0; q < 2; q++)
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[env[q] * XS + k], bw[q][kk], acc[q], 0, 0, 0);
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < 2; q++) {
+        const uint32_t e0 = env[q] - l % 16 + 4 * (l / 16);
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) out[(e0 + r) * OS + unit[q]] = tanh_f(acc[q][r]);
+    }
+}
+// This lane's weight operands of wg_layer_rb for w1t[D][HID].
+template <uint32_t D>
+__device__ __forceinline__ void critic_operands(const float* w1t, float (&bw)[2][D / 4]) {
+    const uint32_t wv = threadIdx.x / 64, l = threadIdx.x % 64;
+#pragma unroll
+    for (uint32_t q = 0; q < 2; q++) {
+        const uint32_t unit = 16 * ((2 * wv + q) % 4) + l % 16;
+#pragma unroll
+        for (uint32_t kk = 0; kk < D / 4; kk++) bw[q][kk] = w1t[(4 * kk + l / 16) * HID + unit];
+    }
+}
+
 // Output heads for the 32 envs of a workgroup on the matrix cores:
 // out[env * 17 + c] = b[c] + sum_h w[c][h] * x[env][h] (c < NC), the fma chain
 // over the 64 hidden units ascending from the bias, as a 16x16x4 tile per
@@ -366,86 +408,94 @@ __device__ __forceinline__ void wg_head(const float* x, const float* w, uint32_t
         for (uint32_t r = 0; r < 4; r++) out[(16 * eb + 4 * (l / 16) + r) * 17 + col0 + c] = acc[r];
 }
 
-// RAPTOR step (raptor.hpp:52-97) for the 32 envs of a workgroup with the
-// dense and GRU layers on the matrix cores (16x16x4 tiles, fma chains from the
-// biases as in the group step).  Every env's group writes its observation row
-// mo[22] to `smo` (stride MS, at least 120 words per env row: the gate
-// pre-activations are staged there too); wavefronts 0 and 1 evaluate the
-// dense layer of env blocks 0 and 1, all four the GRU products; each env's
-// group evaluates its own gates.  The new hidden state lands in `snh`, the old
-// one is read from `srh`.  Three workgroup barriers; call from uniform control
-// flow.  `on` masks envs whose step is skipped.
+// RAPTOR step (raptor.hpp:52-97) for the 8 envs of one wavefront on the
+// matrix cores, with no workgroup barrier: 16x16x4 tiles whose fma chains
+// run from the biases over the inputs in ascending order (the chain of
+// raptor_group), tile row i holding the wavefront's env i % 8 (rows 8-15
+// repeat rows 0-7).  The GRU's input-side and hidden-side
+// products land in the same lanes, so each lane evaluates the gates of two
+// (env, unit) pairs from registers.  `smo` holds the group's observation row
+// (stride MS), `sx` the dense output, `srh` the hidden state (stride 17).
+// Call from uniform control flow; `on` masks envs whose step is skipped.
 template <int G, uint32_t MS>
-__device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22], float* smo, float* sx, float* srh,
-                                          float* snh, uint32_t grp, uint32_t lane, bool on, float (&act)[4]) {
-    const uint32_t wv = threadIdx.x / 64, l = threadIdx.x % 64, j = l % 16;
+__device__ __forceinline__ void raptor_wave(const float* RW, const float (&mo)[22], float* smo, float* sx, float* srh,
+                                            uint32_t grp, uint32_t lane, bool on, float (&act)[4]) {
+    static_assert(G == 8, "one tile row per env: 8 envs per wavefront");
+    const uint32_t l = threadIdx.x % 64, j = l % 16, kq = l / 16;
+    const uint32_t base = (threadIdx.x / 64) * 8, env = base + j % 8;
 #pragma unroll
-    for (int c = 0; c < 22; c++)
-        smo[grp * MS + c] = mo[c];  // the group's lanes hold equal values: no owner test
-    __syncthreads();
-    if (wv < 2) {  // Dense 22->16 + ReLU (raptor.hpp:54-60)
-        const uint32_t env = 16 * wv + j;
+    for (int c = 0; c < 22; c++) smo[grp * MS + c] = mo[c];  // equal values from the group's lanes
+    group_sync();
+    {   // Dense 22->16 + ReLU (raptor.hpp:54-60)
         v4f acc;
         const float bias = RW[352 + j];
         acc[0] = bias; acc[1] = bias; acc[2] = bias; acc[3] = bias;
 #pragma unroll
         for (uint32_t k0 = 0; k0 < 22; k0 += 4) {
-            const uint32_t k = k0 + l / 16;
+            const uint32_t k = k0 + kq;
             const float av = k < 22 ? smo[env * MS + k] : 0.0f;
             const float bv = k < 22 ? RW[j * 22 + k] : -0.0f;
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
         }
+        if (kq < 2)
 #pragma unroll
-        for (uint32_t r = 0; r < 4; r++) sx[(16 * wv + 4 * (l / 16) + r) * 17 + j] = max_f(acc[r], 0.0f);
-    }
-    __syncthreads();
-    {   // GRU gate products (raptor.hpp:62-84): wavefront w takes env block w%2,
-        // input side (x, w < 2) or hidden side (h, w >= 2); gate g of unit u is
-        // row 16g + u.  Pre-activations go to the env rows of smo at 24 + 16g
-        // (input side) and 72 + 16g (hidden side).
-        const uint32_t eb = wv % 2, env = 16 * eb + j;
-        const bool hid = wv >= 2;
-        const float* src = hid ? srh : sx;
-        const uint32_t wofs = hid ? 1136u : 368u, bofs = hid ? 1952u : 1904u, gofs = hid ? 72u : 24u;
-        v4f acc[3];
-#pragma unroll
-        for (uint32_t g = 0; g < 3; g++) {
-            const float bias = RW[bofs + 16 * g + j];
-            acc[g][0] = bias; acc[g][1] = bias; acc[g][2] = bias; acc[g][3] = bias;
-        }
-#pragma unroll
-        for (uint32_t k0 = 0; k0 < 16; k0 += 4) {
-            const uint32_t k = k0 + l / 16;
-            const float av = src[env * 17 + k];
-#pragma unroll
-            for (uint32_t g = 0; g < 3; g++)
-                acc[g] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, RW[wofs + (16 * g + j) * 16 + k], acc[g], 0, 0, 0);
-        }
-#pragma unroll
-        for (uint32_t r = 0; r < 4; r++) {
-            const uint32_t e = 16 * eb + 4 * (l / 16) + r;
-#pragma unroll
-            for (uint32_t g = 0; g < 3; g++) smo[e * MS + gofs + 16 * g + j] = acc[g][r];
-        }
-    }
-    __syncthreads();
-    if (on) {  // gates of this lane's units, new hidden state
-        const float* gi = smo + grp * MS + 24;
-        const float* gh = gi + 48;
-#pragma unroll
-        for (int i = 0; i < 16 / G; i++) {
-            const uint32_t u = lane + G * i;
-            const float reset = sigmoid_f(gi[u] + gh[u]);
-            const float update = sigmoid_f(gi[16 + u] + gh[16 + u]);
-            const float cand = tanh_f(gi[32 + u] + reset * gh[32 + u]);
-            snh[grp * 17 + u] = (1.0f - update) * cand + update * srh[grp * 17 + u];
-        }
+            for (uint32_t r = 0; r < 4; r++) sx[(base + 4 * kq + r) * 17 + j] = max_f(acc[r], 0.0f);
     }
     group_sync();
-    if (on) {  // output dense + clip (raptor.hpp:86-97), commit the hidden state
+    // GRU gate products (raptor.hpp:62-84): gate g of unit u is row 16g + u.
+    // Lane (kq, j) holds envs 4 kq + r (mod 8) of unit j; lanes kq < 2 keep
+    // rows r = 0, 1 and lanes kq >= 2 rows 2, 3, so each env is taken once.
+    const bool lo = kq < 2;
+    float ax[4], ah[4];
+#pragma unroll
+    for (uint32_t kk = 0; kk < 4; kk++) {
+        ax[kk] = sx[env * 17 + 4 * kk + kq];
+        ah[kk] = srh[env * 17 + 4 * kk + kq];
+    }
+    // one gate at a time (two chains live), each folded into the gate
+    // values as soon as it is complete
+    float reset[2], update[2], nh[2];
+    uint32_t e2[2];
+#pragma unroll
+    for (uint32_t p = 0; p < 2; p++) e2[p] = base + (4 * kq + (lo ? p : 2 + p)) % 8;
+#pragma unroll
+    for (uint32_t g = 0; g < 3; g++) {
+        v4f ci, ch;
+        const float bi = RW[1904 + 16 * g + j], bh = RW[1952 + 16 * g + j];
+        ci[0] = bi; ci[1] = bi; ci[2] = bi; ci[3] = bi;
+        ch[0] = bh; ch[1] = bh; ch[2] = bh; ch[3] = bh;
+#pragma unroll
+        for (uint32_t kk = 0; kk < 4; kk++) {
+            const uint32_t k = 4 * kk + kq;
+            ci = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[kk], RW[368 + (16 * g + j) * 16 + k], ci, 0, 0, 0);
+            ch = __builtin_amdgcn_mfma_f32_16x16x4f32(ah[kk], RW[1136 + (16 * g + j) * 16 + k], ch, 0, 0, 0);
+        }
+#pragma unroll
+        for (uint32_t p = 0; p < 2; p++) {
+            const float iv = lo ? ci[p] : ci[2 + p], hv = lo ? ch[p] : ch[2 + p];
+            if (g == 0) {
+                reset[p] = sigmoid_f(iv + hv);
+            } else if (g == 1) {
+                update[p] = sigmoid_f(iv + hv);
+            } else {
+                const float cand = tanh_f(iv + reset[p] * hv);
+                nh[p] = (1.0f - update[p]) * cand + update[p] * srh[e2[p] * 17 + j];
+            }
+        }
+    }
+    const uint64_t live = __ballot(on);
+    bool on2[2];
+#pragma unroll
+    for (uint32_t p = 0; p < 2; p++) on2[p] = (live >> ((e2[p] - base) * G)) & 1ull;
+    group_sync();  // every lane's reads of the old hidden state precede the writes
+#pragma unroll
+    for (uint32_t p = 0; p < 2; p++)
+        if (on2[p]) srh[e2[p] * 17 + j] = nh[p];
+    group_sync();
+    if (on) {  // output dense + clip (raptor.hpp:86-97)
         float hidden[16];
 #pragma unroll
-        for (int c = 0; c < 16; c++) hidden[c] = snh[grp * 17 + c];
+        for (int c = 0; c < 16; c++) hidden[c] = srh[grp * 17 + c];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             float val = RW[2080 + q];
@@ -453,8 +503,6 @@ __device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22]
             for (int c = 0; c < 16; c++) val = fma_f(RW[2016 + q * 16 + c], hidden[c], val);
             act[q] = max_f(-1.0f, min_f(1.0f, val));
         }
-#pragma unroll
-        for (int c = 0; c < 16; c++) srh[grp * 17 + c] = hidden[c];
     }
 }
 
@@ -463,11 +511,15 @@ __device__ __forceinline__ void raptor_wg(const float* RW, const float (&mo)[22]
 // global memory (L1/L2 resident).  W > 1: the workgroup stages one copy of the
 // actor first layer, the RAPTOR weights and the camera rays in LDS, shared by
 // its 64*W/G envs.
+// Tails of the flat policy vectors (ppo.hpp:35-45) from the first bias on:
+// actor b1[HID], W2[4][HID], b2[4], log_std[4]; critic b1[HID], W2[HID], b2.
+constexpr uint32_t ACTOR_TAIL = 5 * HID + 8, CRITIC_TAIL = 2 * HID + 1;
 template <int W, uint32_t D>
 struct WeightLds {
     float aw[D * HID];
     float rw[RAPTOR_WORDS];
     float cam[3 * PIX];
+    float pol[ACTOR_TAIL + CRITIC_TAIL];
 };
 template <uint32_t D>
 struct WeightLds<1, D> {};
@@ -517,6 +569,10 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         }
         for (uint32_t i = threadIdx.x; i < RAPTOR_WORDS; i += 64 * W) s_wt.rw[i] = a.raptor[i];
         for (uint32_t i = threadIdx.x; i < 3 * PIX; i += 64 * W) s_wt.cam[i] = a.camera[i];
+        if constexpr (!X)
+            for (uint32_t i = threadIdx.x; i < ACTOR_TAIL; i += 64 * W) s_wt.pol[i] = a.actor[HID * D + i];
+        for (uint32_t i = threadIdx.x; i < CRITIC_TAIL; i += 64 * W)
+            s_wt.pol[ACTOR_TAIL + i] = a.critic[HID * COBS + i];
         __syncthreads();
         AW1 = s_wt.aw;
         RW = s_wt.rw;
@@ -538,7 +594,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     __shared__ float s_ch[E][HID + 1];
     __shared__ float s_cmd[E][33];
     __shared__ float s_x[E][17];
-    __shared__ float s_h[E][17];
+    __shared__ float s_h[W > 1 ? 1 : E][17];  // W == 1: the group step's new hidden state
     // W > 1: RAPTOR hidden state of each env, resident in LDS for the launch
     __shared__ float s_rh[W > 1 ? E : 1][17];
 
@@ -575,8 +631,18 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         for (uint32_t c = lane; c < 16; c += G) s_rh[grp][c] = bits_float(a.run[size_t(RW_HIDDEN + c) * N + nn]);
     const float* A = a.actor;
     const float* CR = a.critic;
-    const uint32_t a_b1 = HID * D, a_w2 = a_b1 + HID, a_b2 = a_w2 + 4 * HID, a_ls = a_b2 + 4;
+    const uint32_t a_b1 = HID * D, a_w2 = a_b1 + HID, a_b2 = a_w2 + 4 * HID;
     const uint32_t c_b1 = HID * COBS, c_w2 = c_b1 + HID, c_b2 = c_w2 + HID;
+    // W > 1: the policy tails from LDS and the critic's first layer in
+    // registers (the tick loop then reads no weights from global memory)
+    float cw1[2][COBS / 4];
+    if constexpr (W > 1) critic_operands<COBS>(a.critic_w1t, cw1);
+    const float* AT = A + a_b1;
+    const float* CT = CR + c_b1;
+    if constexpr (W > 1) {
+        AT = s_wt.pol;
+        CT = s_wt.pol + ACTOR_TAIL;
+    }
     const uint32_t sdelay = clean_env(C, nn) ? 0 : C.sensor_delay;
     const uint32_t cdelay = clean_env(C, nn) ? 0 : C.command_delay;
     // the env's plant for this launch (it changes only at resets, and a
@@ -607,43 +673,133 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             }
         group_sync();
 
-        // ---- depth (sim.metal:145-158): each lane casts the four rays of
-        // its pooled 2x2 blocks and keeps their minimum
+        // ---- depth (sim.metal:145-158)
         float R[9];
         rotation(s.q, R);
         const bool depth_now = active && observe && r.steps % C.sensor_period == 0;
-        // ray-cast path: the register box table when every env of the
-        // wavefront casting this tick has a boxes-only world, else the
-        // per-kind LDS tables (envs whose world they cannot hold take the
-        // generic cast); the env's observation row is free until observe
+        // ray-cast path: when every env of the wavefront casting this tick has
+        // a boxes-only world, the wavefront casts its envs' frames one env at a
+        // time over all its lanes, each 4-column strip of the frame testing
+        // only the boxes that can reach it; else each lane casts the four rays
+        // of its pooled 2x2 blocks through the per-kind LDS tables (envs whose
+        // world they cannot hold take the generic cast).  The env's
+        // observation row is free until observe and holds the tables.
         const bool boxes = boxes_only(world, count);
         const bool wave_boxes = !__any(depth_now && !boxes);
+        const float mx = 0.0f;
+        const V origin = mk(s.p[0] + mx * R[0], s.p[1] + mx * R[3], s.p[2] + mx * R[6]);
+        if (depth_now && lane == 0) {
+            float* pose = a.poses + (size_t(nn) * 8 + (r.steps / C.sensor_period) % 8) * 12;
+            pose[0] = origin.x; pose[1] = origin.y; pose[2] = origin.z;
+#pragma unroll
+            for (int j = 0; j < 9; j++) pose[3 + j] = R[j];
+        }
         MixCounts mix{0, 0, 0};
         bool mix_ok = false;
         uint32_t NB = 0, NS = 0, NC = 0;
-        if (!wave_boxes) {
+        if (!wave_boxes) {  // table sizes: the largest counts among the wavefront's casting envs
             if (depth_now) mix_ok = mix_counts(world, count, mix);
             NB = wave_max_u32(mix_ok ? mix.nb : 0u);
             NS = wave_max_u32(mix_ok ? mix.ns : 0u);
             NC = wave_max_u32(mix_ok ? mix.nc : 0u);
         }
-        if (depth_now) {
+        if (wave_boxes) {
+            float* tbl = s_obs[grp];
+            uint32_t vis0 = 0, vis1 = 0;  // strip masks, bit 8 st + box (strip 4 in vis1)
+            if (depth_now) {
+                for (uint32_t i = lane; i < 9; i += G) {
+                    float A[3], B[3];
+                    box_slab(world, s_cent[grp], i, origin, A, B);
+#pragma unroll
+                    for (int j = 0; j < 3; j++) { tbl[6 * i + j] = A[j]; tbl[6 * i + 3 + j] = B[j]; }
+                    if (i >= 1 && i - 1 < count) {
+                        const uint32_t m = box_strips(A, B, R);
+                        for (uint32_t st = 0; st < 4; st++) vis0 |= ((m >> st) & 1u) << (8 * st + i - 1);
+                        vis1 |= ((m >> 4) & 1u) << (i - 1);
+                    }
+                }
+                for (uint32_t m = 1; m < uint32_t(G); m *= 2) {
+                    vis0 |= uint32_t(__shfl_xor(int(vis0), int(m), G));
+                    vis1 |= uint32_t(__shfl_xor(int(vis1), int(m), G));
+                }
+                if (lane == 0) {
+                    tbl[BOX_TABLE_ORIGIN] = origin.x; tbl[BOX_TABLE_ORIGIN + 1] = origin.y;
+                    tbl[BOX_TABLE_ORIGIN + 2] = origin.z;
+#pragma unroll
+                    for (int j = 0; j < 9; j++) tbl[BOX_TABLE_ROT + j] = R[j];
+                    tbl[BOX_TABLE_STRIPS] = bits_float(vis0);
+                    tbl[BOX_TABLE_STRIPS + 1] = bits_float(vis1);
+                }
+            }
+            const uint64_t casting = __ballot(depth_now);
+            group_sync();
+            constexpr uint32_t EW = 64 / G;  // envs per wavefront
+            const uint32_t l = threadIdx.x % 64, wbase = (threadIdx.x / 64) * EW;
+            // lane l: ray q = l % 4 of block l / 4 of the strip (2 blocks across, 8 down)
+            const uint32_t q = l % 4, jb = l / 4;
+            for (uint32_t e = 0; e < EW; e++) {
+                if (!((casting >> (e * G)) & 1ull)) continue;
+                const uint32_t ge = wbase + e, ne = blockIdx.x * E + ge;
+                const float* et = s_obs[ge];
+                float SA[9][3], SB[9][3], ER[9];
+#pragma unroll
+                for (int i = 0; i < 9; i++)
+#pragma unroll
+                    for (int j = 0; j < 3; j++) { SA[i][j] = et[6 * i + j]; SB[i][j] = et[6 * i + 3 + j]; }
+#pragma unroll
+                for (int j = 0; j < 9; j++) ER[j] = et[BOX_TABLE_ROT + j];
+                const V eo = mk(et[BOX_TABLE_ORIGIN], et[BOX_TABLE_ORIGIN + 1], et[BOX_TABLE_ORIGIN + 2]);
+                const uint32_t w0 = __builtin_amdgcn_readfirstlane(float_bits(et[BOX_TABLE_STRIPS]));
+                const uint32_t w1 = __builtin_amdgcn_readfirstlane(float_bits(et[BOX_TABLE_STRIPS + 1]));
+                const uint32_t steps_e = __builtin_amdgcn_readlane(r.steps, e * G);
+                const uint32_t rng_e = __builtin_amdgcn_readlane(r.rng, e * G);
+                const uint32_t count_e = __builtin_amdgcn_readfirstlane(min(float_bits(s_world[ge][160]), 16u));
+                const uint32_t fidx = steps_e / C.sensor_period;
+                const uint32_t slot8 = fidx % 8, slotk = fidx % K;
+                const float noise = clean_env(C, ne) ? 0.0f : C.depth_noise;
+                const float drop = clean_env(C, ne) ? 0.0f : C.dropout;
+                float* ring = a.sensors + (size_t(ne) * 8 + slot8) * PIX;
+#pragma unroll 1
+                for (uint32_t st = 0; st < 5; st++) {
+                    const uint32_t by = jb / 2, bx = 2 * st + jb % 2;
+                    const uint32_t k = (2 * by + q / 2) * 20 + 2 * bx + q % 2, b = by * 10 + bx;
+                    const float rx = CAM[3 * k], ry = CAM[3 * k + 1], rz = CAM[3 * k + 2];
+                    const V d = mk(ER[0] * rx + ER[1] * ry + ER[2] * rz, ER[3] * rx + ER[4] * ry + ER[5] * rz,
+                                   ER[6] * rx + ER[7] * ry + ER[8] * rz);
+                    const bool axes = (__builtin_fabsf(d.x) >= 1e-8f) & (__builtin_fabsf(d.y) >= 1e-8f) &
+                                      (__builtin_fabsf(d.z) >= 1e-8f);
+                    float depth;
+                    if (axes) {
+                        const float inv[3] = {recip_rn(d.x), recip_rn(d.y), recip_rn(d.z)};
+                        float best = __builtin_fminf(12.0f, slab_fast(SA[0], SB[0], inv));
+                        const uint32_t m = st < 4 ? (w0 >> (8 * st)) & 0xffu : w1 & 0xffu;
+#pragma unroll
+                        for (int i = 0; i < 8; i++)
+                            if ((m >> i) & 1u) best = __builtin_fminf(best, slab_fast(SA[i + 1], SB[i + 1], inv));
+                        depth = fmax_f(0.0f, best);
+                    } else {
+                        depth = cast_ray(s_world[ge], s_cent[ge], count_e, eo, d);
+                    }
+                    if (noise != 0 || drop != 0) {
+                        uint32_t nr = rng_e + k * 1664525u + steps_e * 1013904223u;
+                        depth = clamp_f(depth + noise * normal_draw(nr), 0.0f, 12.0f);
+                        if (ur(nr) < drop) depth = 12.0f;
+                    }
+                    ring[k] = depth;
+                    // pooled 2x2 minimum over the quad's lanes (values in [0, 12], never NaN)
+                    float pooled = min_f(depth, bits_float(uint32_t(
+                                                    __builtin_amdgcn_update_dpp(0, int(float_bits(depth)), 0xB1, 0xF, 0xF, false))));
+                    pooled = min_f(pooled, bits_float(uint32_t(
+                                               __builtin_amdgcn_update_dpp(0, int(float_bits(pooled)), 0x4E, 0xF, 0xF, false))));
+                    if (q == 0) s_ring[ge][slotk * POOL + b] = pooled;
+                }
+            }
+        } else if (depth_now) {
             const uint32_t fidx = r.steps / C.sensor_period;
             const uint32_t slot8 = fidx % 8, slotk = fidx % K;
-            const float mx = 0.0f;
-            const V origin = mk(s.p[0] + mx * R[0], s.p[1] + mx * R[3], s.p[2] + mx * R[6]);
-            if (lane == 0) {
-                float* pose = a.poses + (size_t(nn) * 8 + slot8) * 12;
-                pose[0] = origin.x; pose[1] = origin.y; pose[2] = origin.z;
-#pragma unroll
-                for (int j = 0; j < 9; j++) pose[3 + j] = R[j];
-            }
             const float noise = clean_env(C, nn) ? 0.0f : C.depth_noise;
             const float drop = clean_env(C, nn) ? 0.0f : C.dropout;
             float* ring = a.sensors + (size_t(nn) * 8 + slot8) * PIX;
-            const bool fast = wave_boxes && boxes;
-            BoxSlabs bs;
-            if (fast) make_box_slabs(world, s_cent[grp], count, origin, bs);
             float* tbl = s_obs[grp];
             float RA[3], RB[3];
             if (mix_ok) {
@@ -685,9 +841,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                         float depth;
                         const bool axes = (__builtin_fabsf(d.x) >= 1e-8f) & (__builtin_fabsf(d.y) >= 1e-8f) &
                                           (__builtin_fabsf(d.z) >= 1e-8f);
-                        if (fast && axes)
-                            depth = cast_ray_boxes(bs, d);
-                        else if (block_mixed)
+                        if (block_mixed)
                             depth = mixed[dy * 2 + dx];
                         else if (mix_ok && axes)
                             depth = cast_ray_mixed(RA, RB, tbl, mix, NB, NS, NC, d);
@@ -810,12 +964,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         } else if constexpr (W > 1) {  // all 32 envs of the workgroup on the matrix cores
             static_assert(E == 32, "matrix-core layers assume 32 envs per workgroup");
             __syncthreads();
-            wg_layer<D, OS, HID + 1>(&s_obs[0][0], AW1, A + a_b1, &s_ah[0][0]);
-            wg_layer<COBS, COBS + 1, HID + 1>(&s_co[0][0], a.critic_w1t, CR + c_b1, &s_ch[0][0]);
+            wg_layer<D, OS, HID + 1>(&s_obs[0][0], AW1, AT, &s_ah[0][0]);
+            wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
             __syncthreads();
             // heads: means (waves 0-1) and value (waves 2-3) into s_x[env][0..4]
-            wg_head<4, HID + 1>(&s_ah[0][0], A + a_w2, HID, A + a_b2, 0, &s_x[0][0], 0);
-            wg_head<1, HID + 1>(&s_ch[0][0], CR + c_w2, 0, CR + c_b2, 2, &s_x[0][0], 4);
+            wg_head<4, HID + 1>(&s_ah[0][0], AT + HID, HID, AT + 5 * HID, 0, &s_x[0][0], 0);
+            wg_head<1, HID + 1>(&s_ch[0][0], CT + HID, 0, CT + 2 * HID, 2, &s_x[0][0], 4);
             __syncthreads();
         } else if (active) {
             float acc[HU];
@@ -882,7 +1036,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             float lp = 0, act[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float ls = X ? a.ext_log_std[j] : A[a_ls + j];
+                const float ls = X ? a.ext_log_std[j] : AT[5 * HID + 4 + j];
                 act[j] = mean[j] + ((C.mode == 0 || C.mode == 22) ? exp_f(ls) * normal_draw(rng) : 0.0f);
                 if (C.mode == 1) act[j] = normal_draw(rng);
                 const float diff = (act[j] - mean[j]) * exp_f(-ls);
@@ -959,6 +1113,9 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         float step_clearance = 12.0f;
         const MdnPhysicsParams& EP = DYN ? *reinterpret_cast<const MdnPhysicsParams*>(&s_ep[grp][0]) : P;
         const float wind[3] = {world[166] * EP.mass, world[167] * EP.mass, world[168] * EP.mass};
+        // the standard-structure derivative takes wind / mass, the same
+        // division physics.hpp:101 repeats in every derivative evaluation
+        const float wm[3] = {div_r(wind[0], RP.mass), div_r(wind[1], RP.mass), div_r(wind[2], RP.mass)};
         for (uint32_t step = 0; step < C.substeps; step++) {
             float mo[22] = {0};
             if (!done) {
@@ -981,7 +1138,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             }
             float act[4];
             if constexpr (W > 1)
-                raptor_wg<G, OS>(RW, mo, &s_obs[0][0], &s_x[0][0], &s_rh[0][0], &s_h[0][0], grp, lane, !done, act);
+                raptor_wave<G, OS>(RW, mo, &s_obs[0][0], &s_x[0][0], &s_rh[0][0], grp, lane, !done, act);
             else
                 raptor_group<G>(RW, mo, r.hidden, hu, s_x[grp], s_h[grp], lane, !done, act);
             if (!done) {
@@ -989,6 +1146,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 for (int q = 0; q < 4; q++) r.motors[q] = act[q];
                 State nx;
                 if constexpr (DYN) physics_step(EP, s_erp[grp], s, act, wind, nx);
+                else if (a.quad && !__any(!no_negative_zero(s))) physics_step<true>(P, RP, s, act, wm, nx);
                 else physics_step(P, RP, s, act, wind, nx);
                 bool valid = true;
                 const float* nf = &nx.p[0];
@@ -1089,9 +1247,9 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             // next values are the caller's (from the stored next critic observations)
         } else if constexpr (W > 1) {  // next value: critic hidden of s' for all 32 envs
             __syncthreads();
-            wg_layer<COBS, COBS + 1, HID + 1>(&s_co[0][0], a.critic_w1t, CR + c_b1, &s_ch[0][0]);
+            wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
             __syncthreads();
-            wg_head<1, HID + 1>(&s_ch[0][0], CR + c_w2, 0, CR + c_b2, 0, &s_x[0][0], 4);
+            wg_head<1, HID + 1>(&s_ch[0][0], CT + HID, 0, CT + 2 * HID, 0, &s_x[0][0], 4);
             __syncthreads();
         } else {  // next value: critic hidden split over the group
             group_sync();
