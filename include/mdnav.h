@@ -291,7 +291,7 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon);
  * forbid hipMalloc): mdn_op_normalize on `count` advantages already in device
  * memory, normalised in place, enqueued on `stream` (a hipStream_t; NULL for
  * the default stream) and not waited for.  It allocates nothing: the
- * statistics' scratch is a fixed array in the library (about 2 MiB per GPU,
+ * statistics' scratch is a fixed array in the library (4 MiB per GPU,
  * held until the process ends) and `count` may not exceed
  * MDN_NORMALIZE_NOALLOC_MAX (MDN_E_ARG otherwise).  Calls on one GPU share
  * that array: calls that overlap in time on one GPU (other streams, other

@@ -756,7 +756,7 @@ int mdn_ppo_create(MdnSim* s, uint32_t epochs, uint32_t minibatch, MdnPPO** out)
     guard(dev_alloc(&p->cv, s->shape.critic_count()));
     guard(dev_alloc(&p->part, size_t(chunks) * ppo_partial_stride(s->shape.obs)));
     guard(dev_alloc(&p->grad, ppo_partial_stride(s->shape.obs)));
-    guard(dev_alloc(&p->norm_part, (s->rows() + 255) / 256));
+    guard(dev_alloc(&p->norm_part, ppo_normalize_part_words(s->rows())));
     guard(dev_alloc(&p->norm_stats, 2));
     guard(dev_alloc(&p->metric_rows, size_t(p->updates) * 4));
     guard(dev_alloc(&p->metric_mean, 4));
@@ -996,7 +996,7 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon) {
     if (count == 0) return MDN_OK;
     DevBuf a, part, stats;
     int rc = upload_tmp(a, advantages, count * 4);
-    if (!rc) rc = upload_tmp(part, nullptr, ((count + 255) / 256) * 8);
+    if (!rc) rc = upload_tmp(part, nullptr, ppo_normalize_part_words(count) * 8);
     if (!rc) rc = upload_tmp(stats, nullptr, 8);
     if (rc) return rc;
     HIP_TRY(ppo_launch_normalize(static_cast<float*>(a.p), count, static_cast<double*>(part.p),
@@ -1011,10 +1011,10 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon) {
 
 namespace {
 // Scratch of mdn_op_normalize_noalloc: the chunk partials of the advantage
-// statistics (one double per 256 rows) followed by the two statistics
+// statistics (two doubles per 256 rows) followed by the two statistics
 // (mean, inverse deviation).  Every GPU the library runs on holds its own
 // copy for the life of the process.
-constexpr uint64_t kNoallocPartials = MDN_NORMALIZE_NOALLOC_MAX / 256;
+constexpr uint64_t kNoallocPartials = ppo_normalize_part_words(MDN_NORMALIZE_NOALLOC_MAX);
 constexpr size_t kNoallocBytes = kNoallocPartials * sizeof(double) + 2 * sizeof(float);
 static __device__ __align__(256) unsigned char scratch[kNoallocBytes];
 
@@ -1365,7 +1365,7 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     guard(dev_alloc(&p->gc, C));
     guard(dev_alloc(&p->col_part, ((M + 63) / 64) * 13));
     guard(dev_alloc(&p->scratch, 2 * 512 + 2 + 4));
-    guard(dev_alloc(&p->norm_part, (R + 255) / 256));
+    guard(dev_alloc(&p->norm_part, ppo_normalize_part_words(R)));
     guard(dev_alloc(&p->norm_stats, 2));
     guard(dev_alloc(&p->metric_rows, size_t(p->updates) * 4));
     guard(dev_alloc(&p->metric_mean, 4));

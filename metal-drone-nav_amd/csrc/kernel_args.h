@@ -185,6 +185,9 @@ hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const
                           float* adv, float* ret, uint32_t horizon, uint32_t n, float gamma, float lambda,
                           hipStream_t st);
 hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st);
+// doubles of ppo_launch_normalize's `part` for `count` elements: both
+// passes' partials, one per chunk of 256 elements
+constexpr uint64_t ppo_normalize_part_words(uint64_t count) { return 2 * ((count + 255) / 256); }
 hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st);
 hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, uint32_t d, hipStream_t st);
 hipError_t ppo_launch_adam(const ppo::AdamArgs* a, hipStream_t st);

@@ -46,7 +46,7 @@ struct AL {
 // threads load the tile coalesced and form delta = r + gamma*V'(s') - V(s)
 // in LDS, one lane per env then runs the carry recurrence over the tile (the
 // only serial part), and the tile of advantages/returns is stored coalesced.
-constexpr uint32_t GAE_ENVS = 32, GAE_TICKS = 32, GAE_PER = GAE_ENVS * GAE_TICKS / 256;
+constexpr uint32_t GAE_ENVS = 32, GAE_TICKS = 128, GAE_PER = GAE_ENVS * GAE_TICKS / 256, GAE_SCAN = 32;
 struct GaeTile {
     float delta[GAE_PER], value[GAE_PER];
     uint32_t boundary[GAE_PER];
@@ -101,9 +101,27 @@ __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, c
         const uint32_t n1 = t0, n0 = n1 > GAE_TICKS ? n1 - GAE_TICKS : 0;
         if (n1 > 0) gae_load(cur, r, v, nv, te, tr, n0, n1, e0, n, gamma);
         if (tid < GAE_ENVS && e0 + tid < n) {
-            for (uint32_t tt = t1 - t0; tt-- > 0;) {
-                carry = s_delta[tt][tid] + (s_bnd[tt][tid] ? 0.0f : gamma * lambda * carry);
-                s_adv[tt][tid] = carry;
+            // the column in registers GAE_SCAN ticks at a time (one LDS round
+            // trip each), the carry chain without memory operations
+            const uint32_t len = t1 - t0;
+            for (uint32_t b1 = (len + GAE_SCAN - 1) / GAE_SCAN * GAE_SCAN; b1 > 0; b1 -= GAE_SCAN) {
+                const uint32_t b0 = b1 - GAE_SCAN;
+                float dl[GAE_SCAN];
+                uint32_t bd[GAE_SCAN];
+#pragma unroll
+                for (uint32_t k = 0; k < GAE_SCAN; k++) {
+                    dl[k] = s_delta[b0 + k][tid];
+                    bd[k] = s_bnd[b0 + k][tid];
+                }
+#pragma unroll
+                for (uint32_t k = GAE_SCAN; k-- > 0;) {
+                    if (b0 + k < len) {
+                        carry = dl[k] + (bd[k] ? 0.0f : gamma * lambda * carry);
+                        dl[k] = carry;
+                    }
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < GAE_SCAN; k++) s_adv[b0 + k][tid] = dl[k];
             }
         }
         __syncthreads();
@@ -125,68 +143,135 @@ __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, c
 }
 
 // ---------------------------------------------------------------- normalisation
-// ppo.hpp:128-140 with double statistics.  One wavefront per 256-element
-// chunk: lane l adds elements 4l..4l+3 in order, then an xor butterfly over
-// the 64 lanes (pass 0: sum a; pass 1: sum (a-mean)^2).
-__global__ __launch_bounds__(256) void norm_chunks_kernel(const float* __restrict__ a, uint64_t count,
-                                                          double* __restrict__ part, const float* __restrict__ stats,
-                                                          int pass) {
-    const uint64_t c = uint64_t(blockIdx.x) * 4 + threadIdx.x / 64;
-    const uint32_t l = threadIdx.x % 64;
-    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
-    if (c >= chunks) return;  // whole wavefronts leave together
-    const uint64_t begin = c * CHUNK + 4 * l;
-    const float mean = pass == 0 ? 0.0f : stats[0];
-    double s = 0.0;
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-        const uint64_t i = begin + j;
-        if (i < count) {
-            if (pass == 0) {
-                s += double(a[i]);
-            } else {
-                const double d = double(a[i] - mean);
-                s += d * d;
-            }
-        }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) s = s + __shfl_xor(s, off, 64);
-    if (l == 0) part[c] = s;
-}
-// Chunk partials summed sequentially within groups of NORM_GROUP, then the
-// group sums sequentially; pass 0 writes the float mean, pass 1 the inverse
-// standard deviation 1/sqrt(var + eps).
-__global__ __launch_bounds__(256) void norm_finish_kernel(const double* __restrict__ part, uint64_t count,
-                                                          float* __restrict__ stats, float eps, int pass) {
-    __shared__ double gs[256];
-    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
+// ppo.hpp:128-140 with double statistics in the canonical order: a chunk's
+// partial is formed by one wavefront (lane l adds elements 4l..4l+3 in order,
+// then an xor butterfly over the 64 lanes); chunk partials are summed
+// sequentially within groups of NORM_GROUP chunks, then the group sums
+// sequentially.  Three launches: pass 0 stores the chunk partials of sum a;
+// pass 1 forms the mean from them in every workgroup, then stores the chunk
+// partials of sum (a - mean)^2; the rescale kernel forms both totals the same
+// way and applies (a - mean) / sqrt(var + eps).
+//
+// The grouped sum of up to two partial arrays (threads 0-127 take array 0,
+// 128-255 array 1), returned to every thread: rounds of 128 groups, a thread
+// per group loads its NORM_GROUP partials at once and adds them in order,
+// then one thread per array adds the round's group sums in order.
+// gs: LDS double[2 * 129].
+__device__ __forceinline__ void norm_totals(const double* __restrict__ p0, const double* __restrict__ p1,
+                                            uint64_t chunks, double* gs, double& t0, double& t1) {
+    const uint32_t arr = threadIdx.x / 128, tid = threadIdx.x % 128;
+    const double* __restrict__ part = arr == 0 ? p0 : p1;
+    double* g = gs + arr * 129;
     const uint64_t groups = (chunks + NORM_GROUP - 1) / NORM_GROUP;
     double total = 0.0;
-    for (uint64_t g0 = 0; g0 < groups; g0 += 256) {
-        const uint64_t g = g0 + threadIdx.x;
-        if (g < groups) {
-            const uint64_t c0 = g * NORM_GROUP, end = c0 + NORM_GROUP < chunks ? c0 + NORM_GROUP : chunks;
-            double s = 0.0;
-            for (uint64_t c = c0; c < end; ++c) s += part[c];
-            gs[threadIdx.x] = s;
+    for (uint64_t g0 = 0; g0 < groups; g0 += 128) {
+        const uint32_t n = uint32_t(groups - g0 < 128 ? groups - g0 : 128);
+        if (part && tid < n) {
+            const uint64_t c0 = (g0 + tid) * NORM_GROUP;
+            const uint32_t m = uint32_t(chunks - c0 < NORM_GROUP ? chunks - c0 : NORM_GROUP);
+            double x[NORM_GROUP];
+#pragma unroll
+            for (uint32_t c = 0; c < NORM_GROUP; ++c) x[c] = c < m ? part[c0 + c] : 0.0;
+            double v = 0.0;
+#pragma unroll
+            for (uint32_t c = 0; c < NORM_GROUP; ++c)
+                if (c < m) v += x[c];
+            g[tid] = v;
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            const uint64_t m = groups - g0 < 256 ? groups - g0 : 256;
-            for (uint64_t j = 0; j < m; ++j) total += gs[j];
+        if (part && tid == 0) {
+            for (uint32_t j0 = 0; j0 < n; j0 += 16) {
+                double y[16];
+#pragma unroll
+                for (uint32_t j = 0; j < 16; ++j) y[j] = j0 + j < n ? g[j0 + j] : 0.0;
+#pragma unroll
+                for (uint32_t j = 0; j < 16; ++j)
+                    if (j0 + j < n) total += y[j];
+            }
+            g[128] = total;
         }
+        __syncthreads();
+        t0 = gs[128];
+        t1 = gs[129 + 128];
+        total = arr == 0 ? t0 : t1;
         __syncthreads();
     }
-    if (threadIdx.x != 0) return;
-    if (pass == 0) stats[0] = float(total / double(count));
-    else stats[1] = 1.0f / sqrt_f(float(total / double(count)) + eps);
 }
-__global__ __launch_bounds__(256) void norm_apply_kernel(float* __restrict__ a, uint64_t count,
-                                                         const float* __restrict__ stats) {
-    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= count) return;
-    a[i] = (a[i] - stats[0]) * stats[1];
+// Chunk partials (one wavefront per chunk, NORM_WAVE_CHUNKS chunks per
+// wavefront with their loads issued together), into out[chunk].  Pass 1
+// first forms the mean from the pass-0 partials in p0.
+constexpr uint32_t NORM_WAVE_CHUNKS = 4, NORM_WG_CHUNKS = 4 * NORM_WAVE_CHUNKS;
+__global__ __launch_bounds__(256) void norm_chunks_kernel(const float* __restrict__ a, uint64_t count,
+                                                          const double* __restrict__ p0, double* __restrict__ out,
+                                                          int pass) {
+    __shared__ double gs[2 * 129];
+    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
+    const uint32_t w = threadIdx.x / 64, l = threadIdx.x % 64;
+    const uint64_t cb = uint64_t(blockIdx.x) * NORM_WG_CHUNKS + w;  // chunks cb + 4i
+    float x[NORM_WAVE_CHUNKS][4];
+#pragma unroll
+    for (uint32_t i = 0; i < NORM_WAVE_CHUNKS; i++)
+#pragma unroll
+        for (uint32_t j = 0; j < 4; j++) {
+            const uint64_t e = (cb + 4 * i) * CHUNK + 4 * l + j;
+            x[i][j] = e < count ? a[e] : 0.0f;
+        }
+    float mean = 0.0f;
+    if (pass != 0) {
+        double t0 = 0.0, t1 = 0.0;
+        norm_totals(p0, nullptr, chunks, gs, t0, t1);
+        mean = float(t0 / double(count));
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < NORM_WAVE_CHUNKS; i++) {
+        const uint64_t c = cb + 4 * i;
+        double v = 0.0;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            if (c * CHUNK + 4 * l + j < count) {
+                if (pass == 0) {
+                    v += double(x[i][j]);
+                } else {
+                    const double d = double(x[i][j] - mean);
+                    v += d * d;
+                }
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v = v + __shfl_xor(v, off, 64);
+        if (l == 0 && c < chunks) out[c] = v;
+    }
+}
+// mean and 1/sqrt(var + eps) from both passes' partials, then the apply over
+// the workgroup's NORM_APPLY elements (loaded at once); workgroup 0 also
+// stores them in stats[0..1].
+constexpr uint32_t NORM_APPLY = 4096;
+__global__ __launch_bounds__(256) void norm_rescale_kernel(float* __restrict__ a, uint64_t count,
+                                                           const double* __restrict__ p0,
+                                                           const double* __restrict__ p1,
+                                                           float* __restrict__ stats, float eps) {
+    __shared__ double gs[2 * 129];
+    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
+    const uint64_t e0 = uint64_t(blockIdx.x) * NORM_APPLY;
+    float x[NORM_APPLY / 256];
+#pragma unroll
+    for (uint32_t j = 0; j < NORM_APPLY / 256; j++) {
+        const uint64_t i = e0 + threadIdx.x + 256 * j;
+        x[j] = i < count ? a[i] : 0.0f;
+    }
+    double t0 = 0.0, t1 = 0.0;
+    norm_totals(p0, p1, chunks, gs, t0, t1);
+    const float mean = float(t0 / double(count));
+    const float inv = 1.0f / sqrt_f(float(t1 / double(count)) + eps);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        stats[0] = mean;
+        stats[1] = inv;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < NORM_APPLY / 256; j++) {
+        const uint64_t i = e0 + threadIdx.x + 256 * j;
+        if (i < count) a[i] = (x[j] - mean) * inv;
+    }
 }
 
 // ---------------------------------------------------------------- minibatch chunk
@@ -643,16 +728,20 @@ hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const
     return hipGetLastError();
 }
 
-// stats: device float[2] (mean, inv_std); part: device double[ceil(count/256)]
+// stats: device float[2] (mean, inv_std); part: device
+// double[ppo_normalize_part_words(count)] (both passes' chunk partials).
 hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st) {
     if (count == 0) return hipSuccess;
     const uint64_t chunks = (count + ppo::CHUNK - 1) / ppo::CHUNK;
-    const uint32_t cb = uint32_t((chunks + 3) / 4);  // one wavefront per chunk
-    for (int pass = 0; pass < 2; pass++) {
-        hipLaunchKernelGGL(ppo::norm_chunks_kernel, dim3(cb), dim3(256), 0, st, a, count, part, stats, pass);
-        hipLaunchKernelGGL(ppo::norm_finish_kernel, dim3(1), dim3(256), 0, st, part, count, stats, eps, pass);
-    }
-    hipLaunchKernelGGL(ppo::norm_apply_kernel, dim3(uint32_t((count + 255) / 256)), dim3(256), 0, st, a, count, stats);
+    const uint64_t wgs = (chunks + ppo::NORM_WG_CHUNKS - 1) / ppo::NORM_WG_CHUNKS;
+    const uint64_t applies = (count + ppo::NORM_APPLY - 1) / ppo::NORM_APPLY;
+    if (wgs > 0x7fffffffull || applies > 0x7fffffffull) return hipErrorInvalidValue;
+    double* p0 = part;
+    double* p1 = part + chunks;
+    hipLaunchKernelGGL(ppo::norm_chunks_kernel, dim3(uint32_t(wgs)), dim3(256), 0, st, a, count, p0, p0, 0);
+    hipLaunchKernelGGL(ppo::norm_chunks_kernel, dim3(uint32_t(wgs)), dim3(256), 0, st, a, count, p0, p1, 1);
+    hipLaunchKernelGGL(ppo::norm_rescale_kernel, dim3(uint32_t(applies)), dim3(256), 0, st, a, count, p0, p1, stats,
+                       eps);
     return hipGetLastError();
 }
 
