@@ -469,8 +469,39 @@ __device__ __forceinline__ float clearance_at(const float* world, uint32_t count
     for (uint32_t i = 0; i < count; i++) best = fmin_f(best, obstacle_clearance(world + 10 * i, p, time));
     return best;
 }
+// Group reductions by DPP lane swaps inside the group's own lanes (quad
+// swaps 1 and 2, then the mirror of each 8-lane half row and of each 16-lane
+// row): every step pairs a lane with one of the other half of its block, so
+// after log2 G steps every lane of the group holds the combination of all G
+// values.  A VALU operand modifier in place of an LDS-latency shuffle.
+template <int STEP>
+__device__ __forceinline__ uint32_t group_swap(uint32_t v) {
+    constexpr int ctrl = STEP == 0 ? 0xB1 : STEP == 1 ? 0x4E : STEP == 2 ? 0x141 : 0x140;
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), ctrl, 0xF, 0xF, false));
+}
+// min over the group of values that are never NaN and never -0 (then the
+// minimum does not depend on the order of the pairings)
+template <int G>
+__device__ __forceinline__ float group_min(float v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "DPP group within one row");
+    if constexpr (G > 1) v = fmin_f(v, bits_float(group_swap<0>(float_bits(v))));
+    if constexpr (G > 2) v = fmin_f(v, bits_float(group_swap<1>(float_bits(v))));
+    if constexpr (G > 4) v = fmin_f(v, bits_float(group_swap<2>(float_bits(v))));
+    if constexpr (G > 8) v = fmin_f(v, bits_float(group_swap<3>(float_bits(v))));
+    return v;
+}
+template <int G>
+__device__ __forceinline__ uint32_t group_or(uint32_t v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "DPP group within one row");
+    if constexpr (G > 1) v |= group_swap<0>(v);
+    if constexpr (G > 2) v |= group_swap<1>(v);
+    if constexpr (G > 4) v |= group_swap<2>(v);
+    if constexpr (G > 8) v |= group_swap<3>(v);
+    return v;
+}
+
 // The same clearance evaluated by a lane group: lane l takes obstacles l,
-// l+G, ... and the group combines by xor shuffles.  For a finite point every
+// l+G, ... and the group combines them (group_min).  For a finite point every
 // term is finite and none is -0 (x - 0.18f rounds an exact cancellation to
 // +0), so the minimum does not depend on the order and equals clearance_at.
 // Call with the whole group active.
@@ -478,6 +509,7 @@ template <int G>
 __device__ __forceinline__ float clearance_group(const float* world, uint32_t count, V p, float time, uint32_t lane) {
     float best = room_clearance(p);
     for (uint32_t i = lane; i < count; i += G) best = fmin_f(best, obstacle_clearance(world + 10 * i, p, time));
+    if constexpr (G <= 16) return group_min<G>(best);
 #pragma unroll
     for (int off = 1; off < G; off <<= 1) best = fmin_f(best, __shfl_xor(best, off, G));
     return best;

@@ -51,29 +51,81 @@ struct GaeTile {
     float delta[GAE_PER], value[GAE_PER];
     uint32_t boundary[GAE_PER];
 };
-// Loads the tile [t0, t1) x [e0, e0+32) into registers (4 elements per
-// thread) and forms the deltas.
+// Loads the tile [t0, t1) x [e0, e0+32) into registers (16 elements per
+// thread) and forms the deltas.  Every load is issued before any is used
+// (the bootstrap value is read whether or not the step terminated, then
+// selected).  V4: n % 4 == 0, so each thread takes four consecutive envs of
+// four rows with 16-byte (float) and 4-byte (flag) loads; thread tid holds
+// envs 4 (tid % 8) + c of rows tid / 8 + 32 j as element 4 j + c.
+template <bool V4>
 __device__ __forceinline__ void gae_load(GaeTile& g, const float* __restrict__ r, const float* __restrict__ v,
                                          const float* __restrict__ nv, const uint8_t* __restrict__ te,
                                          const uint8_t* __restrict__ tr, uint32_t t0, uint32_t t1, uint32_t e0,
                                          uint32_t n, float gamma) {
+    if constexpr (V4) {
+        const uint32_t eq = threadIdx.x % 8, row = threadIdx.x / 8;
+        float4 rr[GAE_PER / 4], vv[GAE_PER / 4], nn[GAE_PER / 4];
+        uint32_t tt4[GAE_PER / 4], tu4[GAE_PER / 4];
+        bool in[GAE_PER / 4];
 #pragma unroll
-    for (uint32_t j = 0; j < GAE_PER; j++) {
-        const uint32_t i = threadIdx.x + 256 * j;
-        const uint32_t t = t0 + i / GAE_ENVS, env = e0 + i % GAE_ENVS;
-        g.delta[j] = 0.0f; g.value[j] = 0.0f; g.boundary[j] = 0;
-        if (t < t1 && env < n) {
-            const size_t k = size_t(t) * n + env;
-            const bool term = te[k] != 0;
-            const bool boundary = term || tr[k] != 0;
-            const float bootstrap = term ? 0.0f : nv[k];
-            const float value = v[k];
-            g.delta[j] = r[k] + gamma * bootstrap - value;
-            g.value[j] = value;
-            g.boundary[j] = boundary;
+        for (uint32_t j = 0; j < GAE_PER / 4; j++) {
+            const uint32_t t = t0 + row + 32 * j, env = e0 + 4 * eq;
+            in[j] = t < t1 && env < n;
+            const size_t k = in[j] ? size_t(t) * n + env : 0;
+            rr[j] = *reinterpret_cast<const float4*>(r + k);
+            vv[j] = *reinterpret_cast<const float4*>(v + k);
+            nn[j] = *reinterpret_cast<const float4*>(nv + k);
+            tt4[j] = *reinterpret_cast<const uint32_t*>(te + k);
+            tu4[j] = *reinterpret_cast<const uint32_t*>(tr + k);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < GAE_PER / 4; j++) {
+            const float rc[4] = {rr[j].x, rr[j].y, rr[j].z, rr[j].w};
+            const float vc[4] = {vv[j].x, vv[j].y, vv[j].z, vv[j].w};
+            const float nc[4] = {nn[j].x, nn[j].y, nn[j].z, nn[j].w};
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+                const bool term = ((tt4[j] >> (8 * c)) & 0xffu) != 0;
+                const bool boundary = term || ((tu4[j] >> (8 * c)) & 0xffu) != 0;
+                const float bootstrap = term ? 0.0f : nc[c];
+                g.delta[4 * j + c] = in[j] ? rc[c] + gamma * bootstrap - vc[c] : 0.0f;
+                g.value[4 * j + c] = in[j] ? vc[c] : 0.0f;
+                g.boundary[4 * j + c] = in[j] && boundary;
+            }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t j = 0; j < GAE_PER; j++) {
+            const uint32_t i = threadIdx.x + 256 * j;
+            const uint32_t t = t0 + i / GAE_ENVS, env = e0 + i % GAE_ENVS;
+            g.delta[j] = 0.0f; g.value[j] = 0.0f; g.boundary[j] = 0;
+            if (t < t1 && env < n) {
+                const size_t k = size_t(t) * n + env;
+                const bool term = te[k] != 0;
+                const bool boundary = term || tr[k] != 0;
+                const float nvk = nv[k];
+                const float bootstrap = term ? 0.0f : nvk;
+                const float value = v[k];
+                g.delta[j] = r[k] + gamma * bootstrap - value;
+                g.value[j] = value;
+                g.boundary[j] = boundary;
+            }
         }
     }
 }
+// LDS position (tick, env) of a thread's element j in either load layout.
+template <bool V4>
+__device__ __forceinline__ void gae_pos(uint32_t j, uint32_t& tt, uint32_t& e) {
+    if constexpr (V4) {
+        tt = threadIdx.x / 8 + 32 * (j / 4);
+        e = 4 * (threadIdx.x % 8) + j % 4;
+    } else {
+        const uint32_t i = threadIdx.x + 256 * j;
+        tt = i / GAE_ENVS;
+        e = i % GAE_ENVS;
+    }
+}
+template <bool V4>
 __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, const float* __restrict__ v,
                                                   const float* __restrict__ nv, const uint8_t* __restrict__ te,
                                                   const uint8_t* __restrict__ tr, float* __restrict__ adv,
@@ -87,11 +139,12 @@ __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, c
     float carry = 0.0f;
     GaeTile cur;
     uint32_t t1 = horizon, t0 = t1 > GAE_TICKS ? t1 - GAE_TICKS : 0;
-    gae_load(cur, r, v, nv, te, tr, t0, t1, e0, n, gamma);
+    gae_load<V4>(cur, r, v, nv, te, tr, t0, t1, e0, n, gamma);
     while (t1 > 0) {
 #pragma unroll
         for (uint32_t j = 0; j < GAE_PER; j++) {
-            const uint32_t i = tid + 256 * j, tt = i / GAE_ENVS, e = i % GAE_ENVS;
+            uint32_t tt, e;
+            gae_pos<V4>(j, tt, e);
             s_delta[tt][e] = cur.delta[j];
             s_val[tt][e] = cur.value[j];
             s_bnd[tt][e] = cur.boundary[j];
@@ -99,7 +152,7 @@ __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, c
         __syncthreads();
         // the next (earlier) tile's loads are in flight during the scan
         const uint32_t n1 = t0, n0 = n1 > GAE_TICKS ? n1 - GAE_TICKS : 0;
-        if (n1 > 0) gae_load(cur, r, v, nv, te, tr, n0, n1, e0, n, gamma);
+        if (n1 > 0) gae_load<V4>(cur, r, v, nv, te, tr, n0, n1, e0, n, gamma);
         if (tid < GAE_ENVS && e0 + tid < n) {
             // the column in registers GAE_SCAN ticks at a time (one LDS round
             // trip each), the carry chain without memory operations
@@ -127,7 +180,8 @@ __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, c
         __syncthreads();
 #pragma unroll
         for (uint32_t j = 0; j < GAE_PER; j++) {
-            const uint32_t i = tid + 256 * j, tt = i / GAE_ENVS, e = i % GAE_ENVS;
+            uint32_t tt, e;
+            gae_pos<V4>(j, tt, e);
             const uint32_t t = t0 + tt, env = e0 + e;
             if (t < t1 && env < n) {
                 const size_t k = size_t(t) * n + env;
@@ -723,8 +777,17 @@ hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const
                           float* adv, float* ret, uint32_t horizon, uint32_t n, float gamma, float lambda,
                           hipStream_t st) {
     if (n == 0 || horizon == 0) return hipSuccess;
-    hipLaunchKernelGGL(ppo::gae_kernel, dim3((n + ppo::GAE_ENVS - 1) / ppo::GAE_ENVS), dim3(256), 0, st, r, v, nv, te, tr,
-                       adv, ret, horizon, n, gamma, lambda);
+    const dim3 grid((n + ppo::GAE_ENVS - 1) / ppo::GAE_ENVS);
+    // 16-byte row loads when every row starts 16-byte aligned
+    const bool v4 = n % 4 == 0 && (reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(v) |
+                                   reinterpret_cast<uintptr_t>(nv) | reinterpret_cast<uintptr_t>(te) |
+                                   reinterpret_cast<uintptr_t>(tr)) % 16 == 0;
+    if (v4)
+        hipLaunchKernelGGL(ppo::gae_kernel<true>, grid, dim3(256), 0, st, r, v, nv, te, tr, adv, ret, horizon, n, gamma,
+                           lambda);
+    else
+        hipLaunchKernelGGL(ppo::gae_kernel<false>, grid, dim3(256), 0, st, r, v, nv, te, tr, adv, ret, horizon, n, gamma,
+                           lambda);
     return hipGetLastError();
 }
 

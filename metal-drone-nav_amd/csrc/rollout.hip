@@ -310,35 +310,45 @@ __global__ __launch_bounds__(64) void episode_kernel(EpisodeArgs a) {
 // D[4(l/16) + r][l%16].  Wavefront w computes tiles 2w and 2w+1 of the 2 x 4
 // grid of 16x16 tiles (env block = tile / 4, unit block = tile % 4).
 typedef float v4f __attribute__((ext_vector_type(4)));
+// The operands of k-step s are read from LDS PF steps before its MFMAs issue
+// (a scheduling fence between steps keeps that order), so the LDS latency of
+// one step overlaps the matrix-core work of the previous ones.
+constexpr uint32_t MFMA_PF = 3;
 template <uint32_t D, uint32_t XS, uint32_t OS>
 __device__ __forceinline__ void wg_layer(const float* x, const float* w1t, const float* b1, float* out) {
     const uint32_t wv = threadIdx.x / 64, l = threadIdx.x % 64;
-    uint32_t env[2], unit[2];
+    // tiles 2w and 2w+1 share env block w/2: one A operand for both
+    const uint32_t env = 16 * (wv / 2) + l % 16;
+    uint32_t unit[2];
     v4f acc[2];
 #pragma unroll
     for (uint32_t q = 0; q < 2; q++) {
-        const uint32_t tile = 2 * wv + q;
-        env[q] = 16 * (tile / 4) + l % 16;
-        unit[q] = 16 * (tile % 4) + l % 16;
+        unit[q] = 16 * ((2 * wv + q) % 4) + l % 16;
         const float bias = b1[unit[q]];
         acc[q][0] = bias; acc[q][1] = bias; acc[q][2] = bias; acc[q][3] = bias;
     }
-#pragma unroll 8
-    for (uint32_t k0 = 0; k0 < D; k0 += 4) {
-        const uint32_t k = k0 + l / 16;
+    constexpr uint32_t NK = (D + 3) / 4;
+    float av[NK], bv[NK][2];
 #pragma unroll
-        for (uint32_t q = 0; q < 2; q++) {
-            const float av = k < D ? x[env[q] * XS + k] : 0.0f;
-            const float bv = k < D ? w1t[k * HID + unit[q]] : -0.0f;
-            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[q], 0, 0, 0);
+    for (uint32_t st = 0; st < NK + MFMA_PF; st++) {
+        if (st < NK) {
+            const uint32_t k = 4 * st + l / 16;
+            av[st] = k < D ? x[env * XS + k] : 0.0f;
+#pragma unroll
+            for (uint32_t q = 0; q < 2; q++) bv[st][q] = k < D ? w1t[k * HID + unit[q]] : -0.0f;
         }
-    }
+        if (st >= MFMA_PF) {
+            const uint32_t u = st - MFMA_PF;
 #pragma unroll
-    for (uint32_t q = 0; q < 2; q++) {
-        const uint32_t e0 = env[q] - l % 16 + 4 * (l / 16);
+            for (uint32_t q = 0; q < 2; q++) acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv[u][q], acc[q], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const uint32_t e0 = env - l % 16 + 4 * (l / 16);
+#pragma unroll
+    for (uint32_t q = 0; q < 2; q++)
 #pragma unroll
         for (uint32_t r = 0; r < 4; r++) out[(e0 + r) * OS + unit[q]] = tanh_f(acc[q][r]);
-    }
 }
 
 // wg_layer with the weight operands already in registers: bw[q][kk] is
@@ -347,29 +357,32 @@ template <uint32_t D, uint32_t XS, uint32_t OS>
 __device__ __forceinline__ void wg_layer_rb(const float* x, const float (&bw)[2][D / 4], const float* b1, float* out) {
     static_assert(D % 4 == 0, "whole k-steps");
     const uint32_t wv = threadIdx.x / 64, l = threadIdx.x % 64;
-    uint32_t env[2], unit[2];
+    const uint32_t env = 16 * (wv / 2) + l % 16;
+    uint32_t unit[2];
     v4f acc[2];
 #pragma unroll
     for (uint32_t q = 0; q < 2; q++) {
-        const uint32_t tile = 2 * wv + q;
-        env[q] = 16 * (tile / 4) + l % 16;
-        unit[q] = 16 * (tile % 4) + l % 16;
+        unit[q] = 16 * ((2 * wv + q) % 4) + l % 16;
         const float bias = b1[unit[q]];
         acc[q][0] = bias; acc[q][1] = bias; acc[q][2] = bias; acc[q][3] = bias;
     }
+    constexpr uint32_t NK = D / 4;
+    float av[NK];
 #pragma unroll
-    for (uint32_t kk = 0; kk < D / 4; kk++) {
-        const uint32_t k = 4 * kk + l / 16;
+    for (uint32_t st = 0; st < NK + MFMA_PF; st++) {
+        if (st < NK) av[st] = x[env * XS + 4 * st + l / 16];
+        if (st >= MFMA_PF) {
+            const uint32_t u = st - MFMA_PF;
 #pragma unroll
-        for (uint32_t q = 0; q < 2; q++)
-            acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[env[q] * XS + k], bw[q][kk], acc[q], 0, 0, 0);
+            for (uint32_t q = 0; q < 2; q++) acc[q] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bw[q][u], acc[q], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
+    const uint32_t e0 = env - l % 16 + 4 * (l / 16);
 #pragma unroll
-    for (uint32_t q = 0; q < 2; q++) {
-        const uint32_t e0 = env[q] - l % 16 + 4 * (l / 16);
+    for (uint32_t q = 0; q < 2; q++)
 #pragma unroll
         for (uint32_t r = 0; r < 4; r++) out[(e0 + r) * OS + unit[q]] = tanh_f(acc[q][r]);
-    }
 }
 // This lane's weight operands of wg_layer_rb for w1t[D][HID].
 template <uint32_t D>
@@ -397,15 +410,50 @@ __device__ __forceinline__ void wg_head(const float* x, const float* w, uint32_t
     v4f acc;
     const float bias = c < NC ? b[c] : 0.0f;
     acc[0] = bias; acc[1] = bias; acc[2] = bias; acc[3] = bias;
+    constexpr uint32_t NK = HID / 4;
+    float av[NK], bv[NK];
 #pragma unroll
-    for (uint32_t k0 = 0; k0 < HID; k0 += 4) {
-        const uint32_t k = k0 + l / 16;
-        const float bv = c < NC ? w[c * wstride + k] : -0.0f;
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x[env * XS + k], bv, acc, 0, 0, 0);
+    for (uint32_t st = 0; st < NK + MFMA_PF; st++) {
+        if (st < NK) {
+            const uint32_t k = 4 * st + l / 16;
+            av[st] = x[env * XS + k];
+            bv[st] = c < NC ? w[c * wstride + k] : -0.0f;
+        }
+        if (st >= MFMA_PF) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[st - MFMA_PF], bv[st - MFMA_PF], acc, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (c < NC)
 #pragma unroll
         for (uint32_t r = 0; r < 4; r++) out[(16 * eb + 4 * (l / 16) + r) * 17 + col0 + c] = acc[r];
+}
+
+// Lane-constant RAPTOR operands of raptor_wave, read once per launch: the
+// B operands of the dense layer (dense[kk] = W[j][4 kk + kq]) and of the GRU
+// gate products (gi/gh[g][kk] = W_ih/W_hh[16 g + j][4 kk + kq]), and the
+// output layer as an A operand (out[kk] = W_out[j][4 kk + kq], rows j >= 4
+// zero) with its bias in the accumulator rows this lane holds (lane l, kq =
+// l / 16, j = l % 16).
+struct RaptorRegs {
+    float dense[6], gi[3][4], gh[3][4], out[4], obias[4];
+};
+__device__ __forceinline__ void raptor_operands(const float* RW, RaptorRegs& o) {
+    const uint32_t l = threadIdx.x % 64, j = l % 16, kq = l / 16;
+#pragma unroll
+    for (uint32_t kk = 0; kk < 6; kk++) {
+        const uint32_t k = 4 * kk + kq;
+        o.dense[kk] = k < 22 ? RW[j * 22 + k] : -0.0f;
+    }
+#pragma unroll
+    for (uint32_t g = 0; g < 3; g++)
+#pragma unroll
+        for (uint32_t kk = 0; kk < 4; kk++) {
+            o.gi[g][kk] = RW[368 + (16 * g + j) * 16 + 4 * kk + kq];
+            o.gh[g][kk] = RW[1136 + (16 * g + j) * 16 + 4 * kk + kq];
+        }
+#pragma unroll
+    for (uint32_t kk = 0; kk < 4; kk++) o.out[kk] = j < 4 ? RW[2016 + j * 16 + 4 * kk + kq] : 0.0f;
+#pragma unroll
+    for (uint32_t r = 0; r < 4; r++) o.obias[r] = kq == 0 ? RW[2080 + r] : 0.0f;
 }
 
 // RAPTOR step (raptor.hpp:52-97) for the 8 envs of one wavefront on the
@@ -414,12 +462,17 @@ __device__ __forceinline__ void wg_head(const float* x, const float* w, uint32_t
 // raptor_group), tile row i holding the wavefront's env i % 8 (rows 8-15
 // repeat rows 0-7).  The GRU's input-side and hidden-side
 // products land in the same lanes, so each lane evaluates the gates of two
-// (env, unit) pairs from registers.  `smo` holds the group's observation row
-// (stride MS), `sx` the dense output, `srh` the hidden state (stride 17).
-// Call from uniform control flow; `on` masks envs whose step is skipped.
+// (env, unit) pairs from registers.  The output layer is the product
+// W_out . h^T (outputs as rows, envs as columns), its chain over the 16
+// hidden units ascending from the bias; lane e < 8 then holds env e's four
+// outputs and each group reads them from there.  `smo` holds the group's
+// observation row (stride MS), `sx` the dense output, `srh` the hidden state
+// (stride 17).  Call from uniform control flow; `on` masks envs whose step
+// is skipped.
 template <int G, uint32_t MS>
-__device__ __forceinline__ void raptor_wave(const float* RW, const float (&mo)[22], float* smo, float* sx, float* srh,
-                                            uint32_t grp, uint32_t lane, bool on, float (&act)[4]) {
+__device__ __forceinline__ void raptor_wave(const float* RW, const RaptorRegs& o, const float (&mo)[22], float* smo,
+                                            float* sx, float* srh, uint32_t grp, uint32_t lane, bool on,
+                                            float (&act)[4]) {
     static_assert(G == 8, "one tile row per env: 8 envs per wavefront");
     const uint32_t l = threadIdx.x % 64, j = l % 16, kq = l / 16;
     const uint32_t base = (threadIdx.x / 64) * 8, env = base + j % 8;
@@ -430,13 +483,14 @@ __device__ __forceinline__ void raptor_wave(const float* RW, const float (&mo)[2
         v4f acc;
         const float bias = RW[352 + j];
         acc[0] = bias; acc[1] = bias; acc[2] = bias; acc[3] = bias;
+        float av[6];
 #pragma unroll
-        for (uint32_t k0 = 0; k0 < 22; k0 += 4) {
-            const uint32_t k = k0 + kq;
-            const float av = k < 22 ? smo[env * MS + k] : 0.0f;
-            const float bv = k < 22 ? RW[j * 22 + k] : -0.0f;
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+        for (uint32_t kk = 0; kk < 6; kk++) {
+            const uint32_t k = 4 * kk + kq;
+            av[kk] = k < 22 ? smo[env * MS + k] : 0.0f;
         }
+#pragma unroll
+        for (uint32_t kk = 0; kk < 6; kk++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[kk], o.dense[kk], acc, 0, 0, 0);
         if (kq < 2)
 #pragma unroll
             for (uint32_t r = 0; r < 4; r++) sx[(base + 4 * kq + r) * 17 + j] = max_f(acc[r], 0.0f);
@@ -454,10 +508,13 @@ __device__ __forceinline__ void raptor_wave(const float* RW, const float (&mo)[2
     }
     // one gate at a time (two chains live), each folded into the gate
     // values as soon as it is complete
-    float reset[2], update[2], nh[2];
+    float reset[2], update[2], nh[2], hold[2];
     uint32_t e2[2];
 #pragma unroll
-    for (uint32_t p = 0; p < 2; p++) e2[p] = base + (4 * kq + (lo ? p : 2 + p)) % 8;
+    for (uint32_t p = 0; p < 2; p++) {
+        e2[p] = base + (4 * kq + (lo ? p : 2 + p)) % 8;
+        hold[p] = srh[e2[p] * 17 + j];
+    }
 #pragma unroll
     for (uint32_t g = 0; g < 3; g++) {
         v4f ci, ch;
@@ -466,9 +523,8 @@ __device__ __forceinline__ void raptor_wave(const float* RW, const float (&mo)[2
         ch[0] = bh; ch[1] = bh; ch[2] = bh; ch[3] = bh;
 #pragma unroll
         for (uint32_t kk = 0; kk < 4; kk++) {
-            const uint32_t k = 4 * kk + kq;
-            ci = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[kk], RW[368 + (16 * g + j) * 16 + k], ci, 0, 0, 0);
-            ch = __builtin_amdgcn_mfma_f32_16x16x4f32(ah[kk], RW[1136 + (16 * g + j) * 16 + k], ch, 0, 0, 0);
+            ci = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[kk], o.gi[g][kk], ci, 0, 0, 0);
+            ch = __builtin_amdgcn_mfma_f32_16x16x4f32(ah[kk], o.gh[g][kk], ch, 0, 0, 0);
         }
 #pragma unroll
         for (uint32_t p = 0; p < 2; p++) {
@@ -479,7 +535,7 @@ __device__ __forceinline__ void raptor_wave(const float* RW, const float (&mo)[2
                 update[p] = sigmoid_f(iv + hv);
             } else {
                 const float cand = tanh_f(iv + reset[p] * hv);
-                nh[p] = (1.0f - update[p]) * cand + update[p] * srh[e2[p] * 17 + j];
+                nh[p] = (1.0f - update[p]) * cand + update[p] * hold[p];
             }
         }
     }
@@ -492,17 +548,18 @@ __device__ __forceinline__ void raptor_wave(const float* RW, const float (&mo)[2
     for (uint32_t p = 0; p < 2; p++)
         if (on2[p]) srh[e2[p] * 17 + j] = nh[p];
     group_sync();
-    if (on) {  // output dense + clip (raptor.hpp:86-97)
-        float hidden[16];
+    {   // output dense + clip (raptor.hpp:86-97)
+        v4f acc;
 #pragma unroll
-        for (int c = 0; c < 16; c++) hidden[c] = srh[grp * 17 + c];
+        for (uint32_t r = 0; r < 4; r++) acc[r] = o.obias[r];
+        float bh[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            float val = RW[2080 + q];
+        for (uint32_t kk = 0; kk < 4; kk++) bh[kk] = srh[env * 17 + 4 * kk + kq];
 #pragma unroll
-            for (int c = 0; c < 16; c++) val = fma_f(RW[2016 + q * 16 + c], hidden[c], val);
-            act[q] = max_f(-1.0f, min_f(1.0f, val));
-        }
+        for (uint32_t kk = 0; kk < 4; kk++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(o.out[kk], bh[kk], acc, 0, 0, 0);
+        const int src = int((threadIdx.x % 64) / G);  // lane holding this group's env column
+#pragma unroll
+        for (uint32_t q = 0; q < 4; q++) act[q] = max_f(-1.0f, min_f(1.0f, __shfl(acc[q], src, 64)));
     }
 }
 
@@ -519,7 +576,7 @@ struct WeightLds {
     float aw[D * HID];
     float rw[RAPTOR_WORDS];
     float cam[3 * PIX];
-    float pol[ACTOR_TAIL + CRITIC_TAIL];
+    float pol[ACTOR_TAIL + CRITIC_TAIL + 8];  // + exp(log_std), exp(-log_std)
 };
 template <uint32_t D>
 struct WeightLds<1, D> {};
@@ -574,6 +631,13 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         for (uint32_t i = threadIdx.x; i < CRITIC_TAIL; i += 64 * W)
             s_wt.pol[ACTOR_TAIL + i] = a.critic[HID * COBS + i];
         __syncthreads();
+        if constexpr (!X) {  // the action noise scales are fixed for the launch
+            if (threadIdx.x < 8) {
+                const float ls = s_wt.pol[5 * HID + 4 + threadIdx.x % 4];
+                s_wt.pol[ACTOR_TAIL + CRITIC_TAIL + threadIdx.x] = exp_f(threadIdx.x < 4 ? ls : -ls);
+            }
+            __syncthreads();
+        }
         AW1 = s_wt.aw;
         RW = s_wt.rw;
         CAM = s_wt.cam;
@@ -637,6 +701,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     // registers (the tick loop then reads no weights from global memory)
     float cw1[2][COBS / 4];
     if constexpr (W > 1) critic_operands<COBS>(a.critic_w1t, cw1);
+    RaptorRegs rops;
+    if constexpr (W > 1) raptor_operands(RW, rops);
     const float* AT = A + a_b1;
     const float* CT = CR + c_b1;
     if constexpr (W > 1) {
@@ -718,10 +784,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                         vis1 |= ((m >> 4) & 1u) << (i - 1);
                     }
                 }
-                for (uint32_t m = 1; m < uint32_t(G); m *= 2) {
-                    vis0 |= uint32_t(__shfl_xor(int(vis0), int(m), G));
-                    vis1 |= uint32_t(__shfl_xor(int(vis1), int(m), G));
-                }
+                vis0 = group_or<G>(vis0);
+                vis1 = group_or<G>(vis1);
                 if (lane == 0) {
                     tbl[BOX_TABLE_ORIGIN] = origin.x; tbl[BOX_TABLE_ORIGIN + 1] = origin.y;
                     tbl[BOX_TABLE_ORIGIN + 2] = origin.z;
@@ -759,11 +823,19 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 const float noise = clean_env(C, ne) ? 0.0f : C.depth_noise;
                 const float drop = clean_env(C, ne) ? 0.0f : C.dropout;
                 float* ring = a.sensors + (size_t(ne) * 8 + slot8) * PIX;
+                // camera ray of the next strip read one strip ahead
+                const uint32_t by = jb / 2, k0 = (2 * by + q / 2) * 20 + 2 * (jb % 2) + q % 2;
+                float nrx = CAM[3 * k0], nry = CAM[3 * k0 + 1], nrz = CAM[3 * k0 + 2];
 #pragma unroll 1
                 for (uint32_t st = 0; st < 5; st++) {
-                    const uint32_t by = jb / 2, bx = 2 * st + jb % 2;
-                    const uint32_t k = (2 * by + q / 2) * 20 + 2 * bx + q % 2, b = by * 10 + bx;
-                    const float rx = CAM[3 * k], ry = CAM[3 * k + 1], rz = CAM[3 * k + 2];
+                    const uint32_t bx = 2 * st + jb % 2;
+                    const uint32_t k = k0 + 4 * st, b = by * 10 + bx;
+                    const float rx = nrx, ry = nry, rz = nrz;
+                    if (st < 4) {
+                        nrx = CAM[3 * (k + 4)];
+                        nry = CAM[3 * (k + 4) + 1];
+                        nrz = CAM[3 * (k + 4) + 2];
+                    }
                     const V d = mk(ER[0] * rx + ER[1] * ry + ER[2] * rz, ER[3] * rx + ER[4] * ry + ER[5] * rz,
                                    ER[6] * rx + ER[7] * ry + ER[8] * rz);
                     const bool axes = (__builtin_fabsf(d.x) >= 1e-8f) & (__builtin_fabsf(d.y) >= 1e-8f) &
@@ -1037,9 +1109,17 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const float ls = X ? a.ext_log_std[j] : AT[5 * HID + 4 + j];
-                act[j] = mean[j] + ((C.mode == 0 || C.mode == 22) ? exp_f(ls) * normal_draw(rng) : 0.0f);
+                float sd, isd;
+                if constexpr (W > 1 && !X) {
+                    sd = s_wt.pol[ACTOR_TAIL + CRITIC_TAIL + j];
+                    isd = s_wt.pol[ACTOR_TAIL + CRITIC_TAIL + 4 + j];
+                } else {
+                    sd = exp_f(ls);
+                    isd = exp_f(-ls);
+                }
+                act[j] = mean[j] + ((C.mode == 0 || C.mode == 22) ? sd * normal_draw(rng) : 0.0f);
                 if (C.mode == 1) act[j] = normal_draw(rng);
-                const float diff = (act[j] - mean[j]) * exp_f(-ls);
+                const float diff = (act[j] - mean[j]) * isd;
                 lp += -0.5f * (diff * diff + 2 * ls + LOG_TWO_PI);
                 float executed = act[j];
                 if (D == MDN_ACTOR_OBS_PRIOR && C.mode == 22) {
@@ -1138,7 +1218,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             }
             float act[4];
             if constexpr (W > 1)
-                raptor_wave<G, OS>(RW, mo, &s_obs[0][0], &s_x[0][0], &s_rh[0][0], grp, lane, !done, act);
+                raptor_wave<G, OS>(RW, rops, mo, &s_obs[0][0], &s_x[0][0], &s_rh[0][0], grp, lane, !done, act);
             else
                 raptor_group<G>(RW, mo, r.hidden, hu, s_x[grp], s_h[grp], lane, !done, act);
             if (!done) {
