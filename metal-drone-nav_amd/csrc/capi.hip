@@ -160,8 +160,9 @@ struct MdnPPO {
     uint64_t optimizer_step = 0;
     uint32_t updates = 0;
     float *am = nullptr, *av = nullptr, *cm = nullptr, *cv = nullptr;
-    // minibatch workspaces: per-chunk partials and the reduced gradient
-    float *part = nullptr, *grad = nullptr;
+    // minibatch workspaces: per-chunk partials and the reduced gradient; row
+    // records of the one-chunk path (minibatches of at most 256 rows)
+    float *part = nullptr, *grad = nullptr, *mb_rec = nullptr;
     double* norm_part = nullptr;
     float* norm_stats = nullptr;
     float *metric_rows = nullptr, *metric_mean = nullptr;
@@ -756,6 +757,7 @@ int mdn_ppo_create(MdnSim* s, uint32_t epochs, uint32_t minibatch, MdnPPO** out)
     guard(dev_alloc(&p->cv, s->shape.critic_count()));
     guard(dev_alloc(&p->part, size_t(chunks) * ppo_partial_stride(s->shape.obs)));
     guard(dev_alloc(&p->grad, ppo_partial_stride(s->shape.obs)));
+    if (M <= ppo::MB_ROWS) guard(dev_alloc(&p->mb_rec, ppo::MB_REC_WORDS));
     guard(dev_alloc(&p->norm_part, ppo_normalize_part_words(s->rows())));
     guard(dev_alloc(&p->norm_stats, 2));
     guard(dev_alloc(&p->metric_rows, size_t(p->updates) * 4));
@@ -776,8 +778,8 @@ void mdn_ppo_destroy(MdnPPO* p) {
         hipStreamSynchronize(p->sim->stream);
         if (p->sim->ppo == p) p->sim->ppo = nullptr;
     }
-    void* bufs[] = {p->am, p->av, p->cm, p->cv, p->part, p->grad, p->norm_part, p->norm_stats, p->metric_rows,
-                    p->metric_mean};
+    void* bufs[] = {p->am, p->av, p->cm, p->cv, p->part, p->grad, p->mb_rec, p->norm_part, p->norm_stats,
+                    p->metric_rows, p->metric_mean};
     for (void* b : bufs)
         if (b) hipFree(b);
     delete p;
@@ -825,12 +827,21 @@ int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
         ra.actor = s->actor; ra.actor_w1t = s->actor_w1t; ra.critic = s->critic; ra.critic_w1t = s->critic_w1t;
         ra.part = p->part;
         ra.b = b; ra.d = s->shape.obs; ra.clip = 0.2f; ra.vcoef = 0.5f; ra.ecoef = s->cfg.entropy_coef;
-        rc = timed(s, MDN_K_ROWS, [&] { return ppo_launch_rows(&ra, s->stream); });
-        if (rc) return rc;
-        rc = timed(s, MDN_K_GRADS, [&] {
-            return ppo_launch_grads(p->part, p->grad, b, s->shape.obs, s->stream);
-        });
-        if (rc) return rc;
+        if (p->mb_rec && b <= ppo::MB_ROWS) {  // one chunk: row and parameter passes over many CUs
+            ppo::MbArgs ma;
+            ma.r = ra;
+            ma.rec = p->mb_rec;
+            ma.grad = p->grad;
+            rc = timed(s, MDN_K_ROWS, [&] { return ppo_launch_minibatch(&ma, s->stream); });
+            if (rc) return rc;
+        } else {
+            rc = timed(s, MDN_K_ROWS, [&] { return ppo_launch_rows(&ra, s->stream); });
+            if (rc) return rc;
+            rc = timed(s, MDN_K_GRADS, [&] {
+                return ppo_launch_grads(p->part, p->grad, b, s->shape.obs, s->stream);
+            });
+            if (rc) return rc;
+        }
         ++p->optimizer_step;
         ppo::AdamArgs aa;
         aa.actor = s->actor; aa.critic = s->critic; aa.actor_w1t = s->actor_w1t; aa.critic_w1t = s->critic_w1t;

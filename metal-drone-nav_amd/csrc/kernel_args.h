@@ -143,6 +143,16 @@ struct RowArgs {
 };
 
 // cpu_reference.hpp:553-567 inputs for one update of both networks.
+// One minibatch of at most 256 rows (a single gradient chunk) split over many
+// workgroups: the row-parallel forward writes per-row records to `rec`, the
+// parameter-parallel pass writes the finished gradient to `grad`.
+struct MbArgs {
+    RowArgs r;
+    float* rec;   // [MB_REC_WORDS]: h and delta of actor and critic [4][256][64], row scalars [256][16]
+    float* grad;  // P_TOTAL: actor, critic, metric sums
+};
+constexpr uint32_t MB_ROWS = 256, MB_REC_WORDS = 4 * 256 * 64 + 256 * 16;
+
 struct AdamArgs {
     float* actor; float* critic; float* actor_w1t; float* critic_w1t;
     float* am; float* av; float* cm; float* cv;
@@ -190,6 +200,7 @@ hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* s
 constexpr uint64_t ppo_normalize_part_words(uint64_t count) { return 2 * ((count + 255) / 256); }
 hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st);
 hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, uint32_t d, hipStream_t st);
+hipError_t ppo_launch_minibatch(const ppo::MbArgs* m, hipStream_t st);
 hipError_t ppo_launch_adam(const ppo::AdamArgs* a, hipStream_t st);
 hipError_t ppo_launch_transpose(const float* actor, const float* critic, float* aw, float* cw, uint32_t d,
                                 hipStream_t st);

@@ -345,6 +345,7 @@ __global__ __launch_bounds__(256) void norm_rescale_kernel(float* __restrict__ a
 // holds D[8(r/4) + 4(l/32) + r%4][l%32].  Padding steps multiply by -0.0,
 // which leaves every accumulator (including -0.0) unchanged.
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ v16f mfma32(float a, float b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
@@ -499,6 +500,54 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
     }
 }
 
+// Per-row objective (ppo.hpp:144-181): log-probability of the stored
+// action, clipped surrogate with its active branch, value loss, and the
+// derivatives of the minibatch-mean objective (scale = 1/b).  Writes rs[0..3]
+// = d mean, rs[4..7] = d log_std, rs[8..11] = the row's policy, value and
+// entropy terms and its ratio.
+__device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls, uint32_t m, const float (&mean)[4],
+                                              float value, float target, float scale, float (&dmean)[4], float* rs) {
+    const float* act = a.actions + size_t(m) * 4;
+    float logp = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        const float inv_std = exp_f(-ls[q]);
+        const float d = (act[q] - mean[q]) * inv_std;
+        logp += -0.5f * (d * d + 2.0f * ls[q] + LOG_TWO_PI);
+    }
+    const float raw = logp - a.old_logp[m];
+    const float lr = clamp_f(raw, -20.0f, 20.0f);
+    const float ratio = exp_f(lr);
+    const float adv = a.adv[m];
+    const float clipped = clamp_f(ratio, 1.0f - a.clip, 1.0f + a.clip);
+    const float chosen = min_f(ratio * adv, clipped * adv);
+    const bool in_range = raw >= -20.0f && raw <= 20.0f;
+    const bool active = in_range && (adv >= 0.0f ? ratio <= 1.0f + a.clip : ratio >= 1.0f - a.clip);
+    float entropy = 0.0f;
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) {
+        const float inv_var = exp_f(-2.0f * ls[q]);
+        const float diff = act[q] - mean[q];
+        float dl;
+        if (active) {
+            const float dlogp = -ratio * adv * scale;
+            dmean[q] = dlogp * diff * inv_var;
+            dl = dlogp * (diff * diff * inv_var - 1.0f);
+        } else {
+            dmean[q] = 0.0f;
+            dl = 0.0f;
+        }
+        dl -= a.ecoef * scale;
+        entropy += -a.ecoef * (ls[q] + 0.5f * (1.0f + LOG_TWO_PI)) * scale;
+        rs[q] = dmean[q];
+        rs[4 + q] = dl;
+    }
+    rs[8] = -chosen * scale;
+    rs[9] = 0.5f * a.vcoef * (value - target) * (value - target) * scale;
+    rs[10] = entropy;
+    rs[11] = ratio;
+}
+
 template <uint32_t D>
 __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
     using L = AL<D>;
@@ -557,47 +606,9 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
         if (D == MDN_ACTOR_OBS_PRIOR && q < 3) z += a.obs[size_t(m) * D + D - 3 + q];
         mean[q] = z;
     }
-    const float* act = a.actions + size_t(m) * 4;
-    const float* ls = a.actor + L::LS;
-    float logp = 0.0f;
-#pragma unroll
-    for (uint32_t q = 0; q < 4; q++) {
-        const float inv_std = exp_f(-ls[q]);
-        const float d = (act[q] - mean[q]) * inv_std;
-        logp += -0.5f * (d * d + 2.0f * ls[q] + LOG_TWO_PI);
-    }
-    const float raw = logp - a.old_logp[m];
-    const float lr = clamp_f(raw, -20.0f, 20.0f);
-    const float ratio = exp_f(lr);
-    const float adv = a.adv[m];
-    const float clipped = clamp_f(ratio, 1.0f - a.clip, 1.0f + a.clip);
-    const float chosen = min_f(ratio * adv, clipped * adv);
-    const bool in_range = raw >= -20.0f && raw <= 20.0f;
-    const bool active = in_range && (adv >= 0.0f ? ratio <= 1.0f + a.clip : ratio >= 1.0f - a.clip);
-    float dmean[4], entropy = 0.0f;
+    float dmean[4];
     float* rs = s_u + t * RS;  // the forward's scratch is free now
-#pragma unroll
-    for (uint32_t q = 0; q < 4; q++) {
-        const float inv_var = exp_f(-2.0f * ls[q]);
-        const float diff = act[q] - mean[q];
-        float dl;
-        if (active) {
-            const float dlogp = -ratio * adv * scale;
-            dmean[q] = dlogp * diff * inv_var;
-            dl = dlogp * (diff * diff * inv_var - 1.0f);
-        } else {
-            dmean[q] = 0.0f;
-            dl = 0.0f;
-        }
-        dl -= a.ecoef * scale;
-        entropy += -a.ecoef * (ls[q] + 0.5f * (1.0f + LOG_TWO_PI)) * scale;
-        rs[q] = dmean[q];
-        rs[4 + q] = dl;
-    }
-    rs[8] = -chosen * scale;
-    rs[9] = 0.5f * a.vcoef * (value - target) * (value - target) * scale;
-    rs[10] = entropy;
-    rs[11] = ratio;
+    row_objective(a, a.actor + L::LS, m, mean, value, target, scale, dmean, rs);
     __syncthreads();
     {   // actor W2[q][k]: fma over rows; then b2, log_std and the metric sums
         const uint32_t q = t / HID, k = t % HID;
@@ -653,24 +664,310 @@ __global__ __launch_bounds__(256) void chunk_reduce_kernel(const float* __restri
     grad[p] = total;
 }
 
-// ---------------------------------------------------------------- clip + Adam
-// cpu_reference.hpp:553-567 + log-std clamp (603); block 0 = actor, 1 = critic.
-// Also refreshes the transposed first-layer copy and the metric row.
-
+// ---------------------------------------------------------------- minibatches of one chunk
+// A minibatch of at most 256 rows is one gradient chunk, so every parameter's
+// sum runs over its rows in order (the reference's own order at its 256-row
+// minibatch).  chunk_kernel would run it in one workgroup; here the rows'
+// forward, objective and hidden deltas run in ceil(b/16) workgroups and the
+// parameter sums in 69 more, each chain still over the rows ascending:
+//   mb_forward_kernel: 16 rows per workgroup, wavefronts 0-3 take the actor's
+//     hidden units 16w..16w+15 and 4-7 the critic's on 16x16x4 fp32 MFMA
+//     chains over the inputs from the bias (the fma chain of chunk_forward);
+//     then means and value (fma chains over the 64 units), row_objective and
+//     the hidden deltas, all written to the row records;
+//   mb_grad_kernel: every parameter's sum as a 16x16x4 MFMA chain over the
+//     rows, one 16x16 tile per wavefront (below).
+// Each gradient is stored as 0 + (0 + sum), the value the chunk reduction
+// (group sum from 0, then the sum of groups from 0) gives for one chunk.
+constexpr uint32_t MB_HA = 0, MB_DA = 256 * 64, MB_HC = 2 * 256 * 64, MB_DC = 3 * 256 * 64, MB_RS = 4 * 256 * 64;
+constexpr uint32_t MB_FWD_ROWS = 16;
 template <uint32_t D>
-__global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
+__global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
     using L = AL<D>;
-    const bool critic = blockIdx.x == 1;
+    const RowArgs& a = m.r;
+    constexpr uint32_t XS = D | 1u, WS = HID + 1;  // odd strides: rows fall in distinct banks
+    __shared__ float s_w[D * WS];                  // actor W1^T [input][unit]
+    __shared__ float s_cw[COBS * WS];              // critic W1^T
+    __shared__ float s_t[5 * HID + 8 + 2 * HID + 1];  // actor b1, W2, b2, log_std; critic b1, w2, b2
+    __shared__ float s_x[MB_FWD_ROWS][XS];
+    __shared__ float s_c[MB_FWD_ROWS][COBS + 1];
+    __shared__ float s_ha[MB_FWD_ROWS][HID + 1];
+    __shared__ float s_hc[MB_FWD_ROWS][HID + 1];
+    __shared__ float s_mv[MB_FWD_ROWS][5];   // means, value
+    __shared__ float s_rs[MB_FWD_ROWS][16];  // d mean, d log_std, metric terms, d value
+    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
+    const uint32_t n0 = blockIdx.x * MB_FWD_ROWS;
+    const uint32_t live_rows = a.b - n0 < MB_FWD_ROWS ? a.b - n0 : MB_FWD_ROWS;
+    constexpr uint32_t AT = 5 * HID + 8;  // actor tail words from b1 on
+    float* s_at = s_t;
+    float* s_ct = s_t + AT;
+    {   // every load of the staging issued before any store
+        constexpr uint32_t NW = (D * HID + 511) / 512, NCW = COBS * HID / 512, NX = (MB_FWD_ROWS * D + 511) / 512;
+        float w[NW], cw[NCW], xv[NX], cv, tv[2];
+#pragma unroll
+        for (uint32_t k = 0; k < NW; k++) {
+            const uint32_t e = t + 512 * k;
+            w[k] = e < D * HID ? a.actor_w1t[e] : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < NCW; k++) cw[k] = a.critic_w1t[t + 512 * k];
+#pragma unroll
+        for (uint32_t k = 0; k < NX; k++) {
+            const uint32_t e = t + 512 * k, r = e / D;
+            xv[k] = e < MB_FWD_ROWS * D && r < live_rows ? a.obs[size_t(n0) * D + e] : 0.0f;
+        }
+        {
+            const uint32_t r = t / COBS;
+            cv = r < live_rows ? a.co[size_t(n0) * COBS + t] : 0.0f;  // 512 = 16 rows x 32
+        }
+        tv[0] = t < AT ? a.actor[L::B1 + t] : 0.0f;
+        tv[1] = t < 2 * HID + 1 ? a.critic[C_B1 + t] : 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < NW; k++) {
+            const uint32_t e = t + 512 * k;
+            if (e < D * HID) s_w[(e / HID) * WS + e % HID] = w[k];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < NCW; k++) {
+            const uint32_t e = t + 512 * k;
+            s_cw[(e / HID) * WS + e % HID] = cw[k];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < NX; k++) {
+            const uint32_t e = t + 512 * k;
+            if (e < MB_FWD_ROWS * D) s_x[e / D][e % D] = xv[k];
+        }
+        s_c[t / COBS][t % COBS] = cv;
+        if (t < AT) s_at[t] = tv[0];
+        if (t < 2 * HID + 1) s_ct[t] = tv[1];
+    }
+    static_assert(MB_FWD_ROWS * COBS == 512 && COBS * HID % 512 == 0 && 5 * HID + 8 <= 512, "staging map");
+    __syncthreads();
+    {
+        const bool actor = wv < 4;
+        const uint32_t unit = 16 * (wv % 4) + l % 16;
+        const float bias = actor ? s_at[unit] : s_ct[unit];
+        v4f acc = {bias, bias, bias, bias};
+        if (actor) {
+            constexpr uint32_t NK = (D + 3) / 4;
+#pragma unroll 8
+            for (uint32_t st = 0; st < NK; st++) {
+                const uint32_t k = 4 * st + l / 16;
+                const float av = k < D ? s_x[l % 16][k] : 0.0f;
+                const float bv = k < D ? s_w[k * WS + unit] : -0.0f;
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (uint32_t st = 0; st < COBS / 4; st++) {
+                const uint32_t k = 4 * st + l / 16;
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(s_c[l % 16][k], s_cw[k * WS + unit], acc, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < 4; r++) {
+            const float h = tanh_f(acc[r]);
+            if (actor) s_ha[4 * (l / 16) + r][unit] = h;
+            else s_hc[4 * (l / 16) + r][unit] = h;
+        }
+    }
+    __syncthreads();
+    const float* w2 = s_at + HID;          // actor W2 [4][64]
+    const float* cw2 = s_ct + HID;         // critic w2 [64]
+    if (t < 4 * MB_FWD_ROWS) {  // means (ppo.hpp:73-78)
+        const uint32_t r = t / 4, q = t % 4;
+        float z = s_at[5 * HID + q];
+        for (uint32_t k = 0; k < HID; k++) z = fma_f(w2[q * HID + k], s_ha[r][k], z);
+        if (D == MDN_ACTOR_OBS_PRIOR && q < 3) z += s_x[r][D - 3 + q];
+        s_mv[r][q] = z;
+    } else if (t < 5 * MB_FWD_ROWS) {  // value (ppo.hpp:82-93)
+        const uint32_t r = t - 4 * MB_FWD_ROWS;
+        float v = s_ct[2 * HID];
+        for (uint32_t k = 0; k < HID; k++) v = fma_f(cw2[k], s_hc[r][k], v);
+        s_mv[r][4] = v;
+    }
+    __syncthreads();
+    const float scale = 1.0f / max_f(float(a.b), 1.0f);
+    if (t < MB_FWD_ROWS) {
+        float* rs = s_rs[t];
+        if (t < live_rows) {
+            const uint32_t mrow = n0 + t;
+            const float mean[4] = {s_mv[t][0], s_mv[t][1], s_mv[t][2], s_mv[t][3]};
+            const float value = s_mv[t][4], target = a.ret[mrow];
+            float dmean[4];
+            row_objective(a, s_at + 5 * HID + 4, mrow, mean, value, target, scale, dmean, rs);
+            rs[12] = a.vcoef * (value - target) * scale;
+        } else {
+            for (uint32_t c = 0; c < 13; c++) rs[c] = 0.0f;
+        }
+    }
+    __syncthreads();
+    {   // hidden deltas (ppo.metal:470-485, 618-631) and the row records
+        const uint32_t r = t / 32, k0 = t % 32;
+        const bool live = r < live_rows;
+        const size_t row = n0 + r;
+#pragma unroll
+        for (uint32_t u = 0; u < 2; u++) {
+            const uint32_t k = k0 + 32 * u;
+            float d = 0.0f;
+#pragma unroll
+            for (uint32_t q = 0; q < 4; q++) d = fma_f(s_rs[r][q], w2[q * HID + k], d);
+            const float ha = s_ha[r][k], hc = s_hc[r][k];
+            m.rec[MB_HA + row * HID + k] = ha;
+            m.rec[MB_DA + row * HID + k] = live ? d * (1.0f - ha * ha) : 0.0f;
+            m.rec[MB_HC + row * HID + k] = hc;
+            m.rec[MB_DC + row * HID + k] = live ? s_rs[r][12] * cw2[k] * (1.0f - hc * hc) : 0.0f;
+        }
+        if (k0 < 16) m.rec[MB_RS + row * 16 + k0] = s_rs[r][k0];
+    }
+}
+
+// Every gradient of the minibatch is a chain over its rows, so all of them
+// run as 16x16x4 MFMA chains with the rows as the reduction index:
+//   first layers: A = deltas^T (unit rows), B = inputs with a column of ones
+//     after the last input, so the tile holding that column also yields the
+//     first-layer bias sums (fma(d, 1, s) rounds as s + d);
+//   row scalars: A = the records' scalars^T (rows dmean 0-3, dlog_std 4-7,
+//     metric terms 8-11, dvalue 12), B = [actor h | 1] or critic h: actor W2
+//     (rows 0-3 x h), b2, log_std, metrics and critic b2 (x the ones column),
+//     critic w2 (row 12 x critic h).
+// Rows past b multiply 0 by -0.0 and leave every chain unchanged.  Tiles:
+// actor inputs ceil((D+1)/16) x 4 unit blocks, critic 3 x 4, actor row
+// scalars 5 (h blocks 0-3 and the ones column), critic row scalars 4.
+template <uint32_t D>
+constexpr uint32_t mb_actor_in_tiles() { return (D + 1 + 15) / 16; }
+template <uint32_t D>
+constexpr uint32_t mb_tiles() { return 4 * mb_actor_in_tiles<D>() + 4 * ((COBS + 1 + 15) / 16) + 5 + 4; }
+template <uint32_t D>
+__global__ __launch_bounds__(64) void mb_grad_kernel(MbArgs m) {
+    using L = AL<D>;
+    const RowArgs& a = m.r;
+    const uint32_t l = threadIdx.x, rows = a.b;
+    constexpr uint32_t AIT = mb_actor_in_tiles<D>(), CIT = (COBS + 1 + 15) / 16;
+    constexpr uint32_t A_W1 = 4 * AIT, C_W1 = A_W1 + 4 * CIT, A_RS = C_W1 + 5;
+    const float* RS = m.rec + MB_RS;
+    uint32_t tile = blockIdx.x;
+    // operand sources: A[row][r] = arow(r), B[r][col] = bcol(r)
+    uint32_t kind;  // 0 actor W1, 1 critic W1, 2 actor row scalars, 3 critic row scalars
+    if (tile < A_W1) kind = 0;
+    else if (tile < C_W1) { kind = 1; tile -= A_W1; }
+    else if (tile < A_RS) { kind = 2; tile -= C_W1; }
+    else { kind = 3; tile -= A_RS; }
+    const uint32_t jt = kind < 2 ? tile % 4 : 0, it = kind < 2 ? tile / 4 : tile;
+    const uint32_t ar = 16 * jt + l % 16;        // A row (unit, or row-scalar index)
+    const uint32_t bc = 16 * it + l % 16;        // B column
+    // per-lane operand columns, resolved once so the row loop is branch-free:
+    // A[ar][r] = pa[r * sa] when a_ok; B[r][bc] = pb[r * sb] when b_ok, else
+    // 1 for the ones column, else -0 (an out-of-range lane reads column 0)
+    const float* pa;
+    const float* pb;
+    uint32_t sa, sb;
+    bool a_ok = true, b_ok, b_one;
+    if (kind == 0) {
+        pa = m.rec + MB_DA + ar; sa = HID;
+        b_ok = bc < D; b_one = bc == D; pb = a.obs + (b_ok ? bc : 0); sb = D;
+    } else if (kind == 1) {
+        pa = m.rec + MB_DC + ar; sa = HID;
+        b_ok = bc < COBS; b_one = bc == COBS; pb = a.co + (b_ok ? bc : 0); sb = COBS;
+    } else if (kind == 2) {
+        a_ok = ar < 13; pa = RS + (a_ok ? ar : 0); sa = 16;
+        b_ok = bc < HID; b_one = bc == HID; pb = m.rec + MB_HA + (b_ok ? bc : 0); sb = HID;
+    } else {
+        a_ok = ar < 13; pa = RS + (a_ok ? ar : 0); sa = 16;
+        b_ok = true; b_one = false; pb = m.rec + MB_HC + bc; sb = HID;
+    }
+    const float b_pad = b_one ? 1.0f : -0.0f;
+    float av[64], bv[64];
+#pragma unroll
+    for (uint32_t s = 0; s < 64; s++) {
+        const uint32_t r = 4 * s + l / 16;
+        const bool rv = r < rows;
+        const size_t rr = rv ? r : 0;
+        const float x = pa[rr * sa], y = pb[rr * sb];
+        av[s] = rv && a_ok ? x : 0.0f;
+        bv[s] = rv ? (b_ok ? y : b_pad) : -0.0f;
+    }
+    // rows past b contribute fma(0, -0, acc) = acc
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t s = 0; s < 64; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc, 0, 0, 0);
+    float* g = m.grad;
+    // accumulator register r of lane l holds D[4 (l/16) + r][l % 16]
+#pragma unroll
+    for (uint32_t r = 0; r < 4; r++) {
+        const uint32_t row = 16 * jt + 4 * (l / 16) + r;  // A row of this value
+        const uint32_t col = bc;
+        const float val = 0.0f + (0.0f + acc[r]);
+        int32_t out = -1;
+        if (kind == 0) {
+            if (col < D) out = int32_t(row * D + col);
+            else if (col == D) out = int32_t(L::B1 + row);
+        } else if (kind == 1) {
+            if (col < COBS) out = int32_t(L::COUNT + row * COBS + col);
+            else if (col == COBS) out = int32_t(L::COUNT + C_B1 + row);
+        } else if (kind == 2) {
+            if (col < HID && row < 4) out = int32_t(L::W2 + row * HID + col);
+            else if (col == HID && row < 4) out = int32_t(L::B2 + row);
+            else if (col == HID && row < 8) out = int32_t(L::LS + row - 4);
+            else if (col == HID && row < 12) out = int32_t(L::COUNT + C_COUNT + row - 8);
+            else if (col == HID && row == 12) out = int32_t(L::COUNT + C_B2);
+        } else {
+            if (row == 12) out = int32_t(L::COUNT + C_W2 + col);
+        }
+        if (out >= 0) g[out] = val;
+    }
+}
+
+// ---------------------------------------------------------------- clip + Adam
+// cpu_reference.hpp:553-567 + log-std clamp (603), over many workgroups: the
+// first AW take slices of the actor, the rest slices of the critic.  Each
+// recomputes its net's squared gradient norm in the canonical order (256
+// strided partials, then the pairwise tree) and updates a slice of ADAM_SLICE
+// parameters, refreshing the transposed first-layer copy and clamping the
+// log-stds it owns; workgroup 0 writes the metric row.
+constexpr uint32_t ADAM_SLICE = 1024;
+template <uint32_t D>
+constexpr uint32_t adam_groups() {
+    return (AL<D>::COUNT + ADAM_SLICE - 1) / ADAM_SLICE + (C_COUNT + ADAM_SLICE - 1) / ADAM_SLICE;
+}
+template <uint32_t D>
+__global__ __launch_bounds__(256) void adam_slices_kernel(AdamArgs a) {
+    using L = AL<D>;
+    constexpr uint32_t AW = (L::COUNT + ADAM_SLICE - 1) / ADAM_SLICE;
+    constexpr uint32_t NA = (L::COUNT + 255) / 256, NC = (C_COUNT + 255) / 256;
+    const bool critic = blockIdx.x >= AW;
     const uint32_t P = critic ? C_COUNT : L::COUNT;
+    const uint32_t i0 = (critic ? blockIdx.x - AW : blockIdx.x) * ADAM_SLICE;
     float* params = critic ? a.critic : a.actor;
     float* m = critic ? a.cm : a.am;
     float* v = critic ? a.cv : a.av;
     const float* g = a.grad + (critic ? L::COUNT : 0);
     __shared__ float part[256];
     const uint32_t t = threadIdx.x;
+    // this slice's operands, loaded while the norm is formed
+    constexpr uint32_t PER = ADAM_SLICE / 256;
+    float gv[PER], mv[PER], vv[PER], pv[PER];
+#pragma unroll
+    for (uint32_t k = 0; k < PER; k++) {
+        const uint32_t i = i0 + t + 256 * k;
+        if (i < P) { gv[k] = g[i]; mv[k] = m[i]; vv[k] = v[i]; pv[k] = params[i]; }
+    }
     float s = 0.0f;
-#pragma unroll 16
-    for (uint32_t i = t; i < P; i += 256) s += g[i] * g[i];
+    if (critic) {
+        float x[NC];
+#pragma unroll
+        for (uint32_t k = 0; k < NC; k++) x[k] = t + 256 * k < C_COUNT ? g[t + 256 * k] : 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < NC; k++)
+            if (t + 256 * k < C_COUNT) s += x[k] * x[k];
+    } else {
+        float x[NA];
+#pragma unroll
+        for (uint32_t k = 0; k < NA; k++) x[k] = t + 256 * k < L::COUNT ? g[t + 256 * k] : 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < NA; k++)
+            if (t + 256 * k < L::COUNT) s += x[k] * x[k];
+    }
     part[t] = s;
     __syncthreads();
     for (uint32_t stride = 128; stride > 0; stride >>= 1) {
@@ -680,66 +977,29 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
     const float norm = sqrt_f(part[0] + 1.0e-20f);
     const float scale = min_f(1.0f, 0.5f / norm);
     const float b1 = 0.9f, b2 = 0.999f;
-    // Batches of ADAM_BATCH elements per thread: every load of a batch is
-    // issued before its stores (the buffers are distinct, but the compiler
-    // cannot know it), so a batch costs one memory latency, not one per
-    // element.  The per-element arithmetic is unchanged.
-    constexpr uint32_t ADAM_BATCH = 16;
-    for (uint32_t i0 = t; i0 < P; i0 += 256 * ADAM_BATCH) {
-        float gv[ADAM_BATCH], mv[ADAM_BATCH], vv[ADAM_BATCH], pv[ADAM_BATCH];
 #pragma unroll
-        for (uint32_t k = 0; k < ADAM_BATCH; k++) {
-            const uint32_t i = i0 + 256 * k;
-            if (i < P) { gv[k] = g[i]; mv[k] = m[i]; vv[k] = v[i]; pv[k] = params[i]; }
-        }
-#pragma unroll
-        for (uint32_t k = 0; k < ADAM_BATCH; k++) {
-            const uint32_t i = i0 + 256 * k;
-            if (i < P) {
-                const float gi = gv[k] * scale;
-                const float mi = b1 * mv[k] + (1.0f - b1) * gi;
-                const float vi = b2 * vv[k] + (1.0f - b2) * gi * gi;
-                const float mh = mi / a.c1, vh = vi / a.c2;
-                m[i] = mi;
-                v[i] = vi;
-                params[i] = pv[k] - a.lr * mh / (sqrt_f(vh) + 1.0e-8f);
-            }
+    for (uint32_t k = 0; k < PER; k++) {
+        const uint32_t i = i0 + t + 256 * k;
+        if (i < P) {
+            const float gi = gv[k] * scale;
+            const float mi = b1 * mv[k] + (1.0f - b1) * gi;
+            const float vi = b2 * vv[k] + (1.0f - b2) * gi * gi;
+            const float mh = mi / a.c1, vh = vi / a.c2;
+            m[i] = mi;
+            v[i] = vi;
+            float p = pv[k] - a.lr * mh / (sqrt_f(vh) + 1.0e-8f);
+            if (!critic && i >= L::LS && i < L::LS + 4) p = clamp_f(p, -2.0f, .5f);
+            params[i] = p;
+            if (!critic && i < HID * D) a.actor_w1t[size_t(i % D) * HID + i / D] = p;
+            if (critic && i < HID * COBS) a.critic_w1t[size_t(i % COBS) * HID + i / COBS] = p;
         }
     }
-    __syncthreads();
-    if (!critic) {
-        if (t < 4) params[L::LS + t] = clamp_f(params[L::LS + t], -2.0f, .5f);
-        __syncthreads();  // the clamped log-std before the copy below reads the vector
-        for (uint32_t e0 = t; e0 < HID * D; e0 += 256 * ADAM_BATCH) {
-            float pv[ADAM_BATCH];
-#pragma unroll
-            for (uint32_t k = 0; k < ADAM_BATCH; k++)
-                if (e0 + 256 * k < HID * D) pv[k] = params[e0 + 256 * k];
-#pragma unroll
-            for (uint32_t k = 0; k < ADAM_BATCH; k++) {
-                const uint32_t e = e0 + 256 * k;
-                if (e < HID * D) a.actor_w1t[size_t(e % D) * HID + e / D] = pv[k];
-            }
-        }
-        if (t == 0) {
-            const float* ms = a.grad + L::COUNT + C_COUNT;
-            a.metric_row[0] = ms[0];
-            a.metric_row[1] = ms[1];
-            a.metric_row[2] = ms[2];
-            a.metric_row[3] = ms[3] / float(a.b);
-        }
-    } else {
-        for (uint32_t e0 = t; e0 < HID * COBS; e0 += 256 * ADAM_BATCH) {
-            float pv[ADAM_BATCH];
-#pragma unroll
-            for (uint32_t k = 0; k < ADAM_BATCH; k++)
-                if (e0 + 256 * k < HID * COBS) pv[k] = params[e0 + 256 * k];
-#pragma unroll
-            for (uint32_t k = 0; k < ADAM_BATCH; k++) {
-                const uint32_t e = e0 + 256 * k;
-                if (e < HID * COBS) a.critic_w1t[size_t(e % COBS) * HID + e / COBS] = pv[k];
-            }
-        }
+    if (!critic && blockIdx.x == 0 && t == 0) {
+        const float* ms = a.grad + L::COUNT + C_COUNT;
+        a.metric_row[0] = ms[0];
+        a.metric_row[1] = ms[1];
+        a.metric_row[2] = ms[2];
+        a.metric_row[3] = ms[3] / float(a.b);
     }
 }
 
@@ -821,6 +1081,26 @@ hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st) {
     return hipGetLastError();
 }
 
+// A minibatch of at most 256 rows: forward/objective/deltas, then the
+// finished gradient in grad (no chunk reduction).
+hipError_t ppo_launch_minibatch(const ppo::MbArgs* m, hipStream_t st) {
+    const uint32_t b = m->r.b;
+    if (b == 0 || b > ppo::MB_ROWS) return hipErrorInvalidValue;
+    const dim3 fwd((b + ppo::MB_FWD_ROWS - 1) / ppo::MB_FWD_ROWS);
+    if (m->r.d == MDN_ACTOR_OBS_POOLED) {
+        hipLaunchKernelGGL(ppo::mb_forward_kernel<MDN_ACTOR_OBS_POOLED>, fwd, dim3(512), 0, st, *m);
+        hipLaunchKernelGGL(ppo::mb_grad_kernel<MDN_ACTOR_OBS_POOLED>,
+                           dim3(ppo::mb_tiles<MDN_ACTOR_OBS_POOLED>()), dim3(64), 0, st, *m);
+    } else if (m->r.d == MDN_ACTOR_OBS_PRIOR) {
+        hipLaunchKernelGGL(ppo::mb_forward_kernel<MDN_ACTOR_OBS_PRIOR>, fwd, dim3(512), 0, st, *m);
+        hipLaunchKernelGGL(ppo::mb_grad_kernel<MDN_ACTOR_OBS_PRIOR>,
+                           dim3(ppo::mb_tiles<MDN_ACTOR_OBS_PRIOR>()), dim3(64), 0, st, *m);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, uint32_t d, hipStream_t st) {
     const uint32_t chunks = (b + ppo::CHUNK - 1) / ppo::CHUNK;
     const uint32_t groups = (chunks + ppo::GRAD_GROUP - 1) / ppo::GRAD_GROUP;
@@ -832,9 +1112,11 @@ hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, uint32_t d, hi
 
 hipError_t ppo_launch_adam(const ppo::AdamArgs* a, hipStream_t st) {
     if (a->d == MDN_ACTOR_OBS_POOLED)
-        hipLaunchKernelGGL(ppo::adam_kernel<MDN_ACTOR_OBS_POOLED>, dim3(2), dim3(256), 0, st, *a);
+        hipLaunchKernelGGL(ppo::adam_slices_kernel<MDN_ACTOR_OBS_POOLED>,
+                           dim3(ppo::adam_groups<MDN_ACTOR_OBS_POOLED>()), dim3(256), 0, st, *a);
     else if (a->d == MDN_ACTOR_OBS_PRIOR)
-        hipLaunchKernelGGL(ppo::adam_kernel<MDN_ACTOR_OBS_PRIOR>, dim3(2), dim3(256), 0, st, *a);
+        hipLaunchKernelGGL(ppo::adam_slices_kernel<MDN_ACTOR_OBS_PRIOR>,
+                           dim3(ppo::adam_groups<MDN_ACTOR_OBS_PRIOR>()), dim3(256), 0, st, *a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
