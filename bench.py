@@ -226,6 +226,35 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
     print(json.dumps(out), flush=True)
 
 
+def reference_schedule(iters=3):
+    """The reference's own GPU benchmark schedule (docs/BENCHMARKS.md:56-67,
+    `gpu-bench 8192 3 1`): 8,192 envs x 32 ticks, then 2 epochs of 256-row
+    minibatches (2,048 Adam steps per iteration, main.mm:1321-1384), here with
+    the pooled 181-input actor.  Wall clock of `iters` iterations after one
+    warmup, without per-kernel timing events."""
+    from mdnav import PPOTrainer, Sim, abi
+    N, T = 8192, 32
+    cfg = abi.default_config(n=N, family=1, speed=1.0, distance=3.0)
+    sim = Sim(cfg, T, lanes=8, actor_obs=181)
+    ppo = PPOTrainer(sim, 2, 256)
+    sim.collect()
+    ppo.rollout_update(0)
+    sim.sync()
+    t0 = time.perf_counter()
+    for it in range(iters):
+        sim.collect()
+        ppo.rollout_update(1 + it)
+    sim.sync()
+    wall = time.perf_counter() - t0
+    return {"workload": "8192 envs x 32 ticks, then 2 epochs x 256-row minibatches (2048 Adam steps per iteration), "
+                        "actor 181-64-4", "value": round(N * T * iters / wall, 1), "unit": "env-steps/s",
+            "ms_per_step": round(wall / iters * 1e3, 3), "iterations": iters,
+            "reference_published": {"value": 290.5e3, "unit": "env-steps/s", "hardware": "Apple M3 GPU (Metal)",
+                                    "actor": "661-input raw-depth actor", "source": "docs/BENCHMARKS.md:56-67"},
+            "note": "the reference's benchmark schedule; the reference's figure is for its 661-input actor, which "
+                    "this build does not run, so it is context, not a like-for-like baseline"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -403,6 +432,9 @@ def main():
         "mfma_util": mfma_util(("rollout_kernel", "chunk_kernel")) if headline else {},
         "gpu_seconds": round(gpu_s, 4),
     }
+    if headline:
+        log("bench: reference schedule")
+        out["reference_schedule"] = reference_schedule()
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
         out["cpu_baseline"] = cpu_baseline(cfg_kw, T, actor_obs=args.actor_obs)
