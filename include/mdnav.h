@@ -136,6 +136,16 @@ int mdn_sim_set_actor_obs(MdnSim* sim, uint32_t actor_obs);
  * rotor (sim.metal:70-81).  Takes effect at the next mdn_sim_reset, as the
  * reference's memcpy + reset does.  mdn_sim_collect then runs one tick per
  * launch with a per-episode kernel after each (8 lanes per env). */
+/* Camera profile (sensor_profile.hpp:16-25, 111-126): 1 legacy (default,
+ * the source model of world.hpp::wcamera), 2 native (the measured planar
+ * range finder: vertical half-tangent 0.8, rays cast from 0.08 m ahead of
+ * the body point).  The reference selects it at compile time
+ * (NAV_SENSOR_PROFILE); here per simulator.  It sets the pixel rays, the ray
+ * origin (sim.metal:147-152), the guidance hint's cell directions and the
+ * geometry memory's reprojection (guidance.hpp:21-26, 110-146), and which
+ * checkpoint versions resume.  Waits for the simulator's stream. */
+int mdn_sim_set_camera(MdnSim* sim, uint32_t profile_id);
+int mdn_sim_get_camera(const MdnSim* sim, MdnCameraProfile* profile);
 int mdn_sim_set_runtime(MdnSim* sim, const MdnRuntimeConfig* runtime);
 int mdn_sim_get_runtime(const MdnSim* sim, MdnRuntimeConfig* runtime);
 /* Goal-conditioned navigation tasks: Sim::task_control
@@ -198,17 +208,23 @@ int mdn_ppo_updates_per_rollout(const MdnPPO* ppo, uint32_t* updates);
  * command rings, in the reference's layouts; version 8 when per-episode
  * plants or tasks are on, which appends the runtime and task configuration,
  * every env's plant and task state, the nominal plant and the RAPTOR
- * weights.  Written to path.tmp and renamed. */
+ * weights; version 10 with the native camera, which appends the version-8
+ * blocks, the (disabled) shaping block and the camera contract.  Version 9
+ * (the training potential) is never written: this build does not run the
+ * potential.  Written to path.tmp and renamed. */
 int mdn_ppo_save_checkpoint(MdnPPO* ppo, const char* path, uint32_t family, uint32_t seed,
                             uint32_t completed_rollouts);
 /* PPOTrainer::load_checkpoint (main.mm:1218-1284) with read_checkpoint_header
- * (main.mm:986-994): versions 3-8 (9-10 return MDN_E_ARG).  A missing file
- * is a fresh start (MDN_OK, *completed_rollouts = 0), as in the reference.
- * The family, horizon, env count and seed must match the arguments and the
- * run settings the simulator's; versions 7-8 also their runtime and task
- * configuration, nominal plant and RAPTOR weights (set them first), and a
- * version 7 file resumes only without tasks; the simulator takes the file's
- * config. */
+ * (main.mm:986-994): versions 3-10.  A missing file is a fresh start (MDN_OK,
+ * *completed_rollouts = 0), as in the reference.  The family, horizon, env
+ * count and seed must match the arguments and the run settings the
+ * simulator's; versions 7 and up also their runtime and task configuration,
+ * nominal plant and RAPTOR weights (set them first), and a version 7 file
+ * resumes only without tasks; versions 9-10 carry a shaping block, which must
+ * be the disabled one (a file trained with the potential returns MDN_E_ARG);
+ * version 10 carries the camera contract, which must be the simulator's
+ * profile (mdn_sim_set_camera), and older versions resume only with the
+ * legacy camera.  The simulator takes the file's config. */
 int mdn_ppo_load_checkpoint(MdnPPO* ppo, const char* path, uint32_t family, uint32_t horizon, uint32_t n,
                             uint32_t seed, uint32_t* completed_rollouts);
 /* A checkpoint's header and, if `actor` is given, its actor parameters (the

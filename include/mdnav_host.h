@@ -235,6 +235,18 @@ inline bool task_default_config(MdnTaskConfig& c, uint32_t stage, uint32_t famil
     return true;
 }
 
+// nav_sensor::legacy / native (sensor_profile.hpp:118-126)
+inline MdnCameraProfile camera_profile(uint32_t id) {
+    MdnCameraProfile c;
+    c.id = id == MDN_CAMERA_NATIVE ? MDN_CAMERA_NATIVE : MDN_CAMERA_LEGACY;
+    c.tan_h = MDN_SENSOR_TAN_H;
+    c.tan_v = id == MDN_CAMERA_NATIVE ? MDN_SENSOR_NATIVE_TAN_V : MDN_SENSOR_TAN_V;
+    c.mount_x_m = id == MDN_CAMERA_NATIVE ? MDN_SENSOR_NATIVE_MOUNT_X : 0.0f;
+    c.min_range_m = MDN_SENSOR_MIN_RANGE;
+    c.max_range_m = MDN_SENSOR_MAX_RANGE;
+    return c;
+}
+
 } // namespace mdn
 
 #endif /* MDNAV_HOST_H */

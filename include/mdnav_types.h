@@ -28,7 +28,14 @@ extern "C" {
 #define MDN_SENSOR_FRAMES 8u
 #define MDN_POOLED_FEATURES 80u
 #define MDN_SENSOR_TAN_H 1.0f
-#define MDN_SENSOR_TAN_V 0.75f
+#define MDN_SENSOR_TAN_V 0.75f /* legacy profile (world.hpp::wcamera) */
+/* native profile: the measured 20x16 planar range finder, 0.08 m forward of
+ * the body reference point (sensor_profile.hpp:18-25, 46-51) */
+#define MDN_SENSOR_NATIVE_TAN_V 0.8f
+#define MDN_SENSOR_NATIVE_MOUNT_X 0.08f
+#define MDN_SENSOR_MIN_RANGE 0.03f
+#define MDN_CAMERA_LEGACY 1u
+#define MDN_CAMERA_NATIVE 2u
 #define MDN_SENSOR_MAX_RANGE 12.0f
 #define MDN_MAX_OBSTACLES 16u
 
@@ -206,6 +213,13 @@ typedef struct MdnSensorContract {
     uint32_t reserved;
 } MdnSensorContract;
 
+/* Camera profile (nav_sensor::Profile, sensor_profile.hpp:113-126), 24 bytes:
+ * the contract a PPOFIX1 version-10 checkpoint carries. */
+typedef struct MdnCameraProfile {
+    uint32_t id;
+    float tan_h, tan_v, mount_x_m, min_range_m, max_range_m;
+} MdnCameraProfile;
+
 /* Rollout metrics of cpu_reference.hpp:55-70. */
 typedef struct MdnMetrics {
     double wall_seconds;
@@ -230,6 +244,7 @@ static_assert(sizeof(MdnTaskControl) == 148, "NavigationTaskControl layout");
 static_assert(sizeof(MdnTaskState) == 192, "NavigationTaskState layout");
 static_assert(sizeof(MdnBankControl) == 16, "ChallengeBankControl layout");
 static_assert(sizeof(MdnSensorContract) == 32, "SensorContract layout");
+static_assert(sizeof(MdnCameraProfile) == 24, "nav_sensor::Profile layout");
 #endif
 
 #endif /* MDNAV_TYPES_H */

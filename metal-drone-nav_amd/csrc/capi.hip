@@ -91,6 +91,7 @@ struct MdnSim {
     float* raptor = nullptr;
     float* camera = nullptr;
     float* cells = nullptr;     // pooled-cell directions of the guidance hint [80][3]
+    MdnCameraProfile camera_profile{};  // legacy unless mdn_sim_set_camera chose native
     float* pix_rays = nullptr;  // raw-pixel directions of the geometry memory [320][3]
     uint32_t* mem_head = nullptr;  // per-env memory header [N][16]
     // per-episode plants and navigation tasks (NavigationRuntimeConfig and
@@ -135,6 +136,8 @@ struct MdnSim {
         a.quad = mdn::quad_structure(phys) ? 1u : 0u;
         a.ext_means = nullptr; a.ext_log_std = nullptr; a.tick0 = 0; a.split = 0;
         a.sensor_dt = float(cfg.sensor_period) * phys.dt * float(cfg.substeps);
+        a.mount_x = camera_profile.mount_x_m;
+        a.tan_v = camera_profile.tan_v;
         a.inv_sensor_dt = 1.0 / double(std::max(a.sensor_dt, 1e-3f));
         a.mem_head = nullptr;
         a.env_phys = episodic() ? env_phys : nullptr;
@@ -258,6 +261,45 @@ extern "C" {
 const char* mdn_last_error(void) { return g_error.c_str(); }
 const char* mdn_version(void) { return "mdnav 0.1 gfx950"; }
 
+namespace {
+// Camera tables of the sim's profile (sensor_profile.hpp:81-97,
+// guidance.hpp:21-26, 122): unit pixel rays (nav_sensor_pixel_ray), the
+// pooled-cell directions of the guidance hint and the raw-pixel directions
+// of the geometry memory.  Synchronous copies.
+int upload_camera(MdnSim* s) {
+    const float tan_h = s->camera_profile.tan_h, tan_v = s->camera_profile.tan_v;
+    std::vector<float> cam(960);
+    for (uint32_t k = 0; k < 320; k++) {
+        const uint32_t row = k / 20, col = k % 20;
+        const float y = ((float(col) + 0.5f) / 20.0f * 2.0f - 1.0f) * tan_h;
+        const float z = ((float(row) + 0.5f) / 16.0f * 2.0f - 1.0f) * tan_v;
+        const float dx = 1.0f, dy = -y, dz = -z;
+        const float len = mdn::sqrt_f(dx * dx + dy * dy + dz * dz);
+        const float inv = 1.0f / mdn::fmax_f(len, 1e-8f);
+        cam[3 * k] = dx * inv; cam[3 * k + 1] = dy * inv; cam[3 * k + 2] = dz * inv;
+    }
+    std::vector<float> cells(240);
+    for (uint32_t k = 0; k < 80; k++) {
+        const uint32_t row = k / 10, col = k % 10;
+        const float y = 0.9f - 0.2f * float(col), z = (0.875f - 0.25f * float(row)) * tan_v;
+        const float inv = 1.0f / mdn::sqrt_f(1.0f + y * y + z * z);
+        cells[3 * k] = inv; cells[3 * k + 1] = y * inv; cells[3 * k + 2] = z * inv;
+    }
+    std::vector<float> pix(960);
+    for (uint32_t hit = 0; hit < 320; hit++) {
+        const float ry = 1.0f - (float(hit % 20) + .5f) / 10.0f;
+        const float rz = tan_v * (1.0f - (float(hit / 20) + .5f) / 8.0f);
+        const float inv = 1.0f / mdn::sqrt_f(1 + ry * ry + rz * rz);
+        pix[3 * hit] = inv; pix[3 * hit + 1] = ry * inv; pix[3 * hit + 2] = rz * inv;
+    }
+    if (hipMemcpy(s->camera, cam.data(), cam.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(s->cells, cells.data(), cells.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(s->pix_rays, pix.data(), pix.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return fail(MDN_E_HIP, "camera table upload failed");
+    return MDN_OK;
+}
+}  // namespace
+
 int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWeights* raptor,
                    const MdnPhysicsParams* physics, MdnSim** out) {
     if (!cfg || !raptor || !physics || !out) return fail(MDN_E_ARG, "mdn_sim_create: null argument");
@@ -319,41 +361,16 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
         mdn_sim_destroy(s);
         return rc;
     }
-    // camera rays and policy initialisation are host computations shared with
-    // the oracle (mdnav_host.h); copies are synchronous.
-    std::vector<float> cam(960);
-    for (uint32_t k = 0; k < 320; k++) {
-        const uint32_t row = k / 20, col = k % 20;
-        const float y = ((float(col) + 0.5f) / 20.0f * 2.0f - 1.0f) * MDN_SENSOR_TAN_H;
-        const float z = ((float(row) + 0.5f) / 16.0f * 2.0f - 1.0f) * MDN_SENSOR_TAN_V;
-        const float dx = 1.0f, dy = -y, dz = -z;
-        const float len = mdn::sqrt_f(dx * dx + dy * dy + dz * dz);
-        const float inv = 1.0f / mdn::fmax_f(len, 1e-8f);
-        cam[3 * k] = dx * inv; cam[3 * k + 1] = dy * inv; cam[3 * k + 2] = dz * inv;
+    s->camera_profile = mdn::camera_profile(MDN_CAMERA_LEGACY);
+    if (upload_camera(s) != MDN_OK) {
+        mdn_sim_destroy(s);
+        return MDN_E_HIP;
     }
-    // guidance.hpp:21-26: unit direction through the centre of pooled cell
-    // (row, col) of the 8x10 grid
-    std::vector<float> cells(240);
-    for (uint32_t k = 0; k < 80; k++) {
-        const uint32_t row = k / 10, col = k % 10;
-        const float y = 0.9f - 0.2f * float(col), z = (0.875f - 0.25f * float(row)) * MDN_SENSOR_TAN_V;
-        const float inv = 1.0f / mdn::sqrt_f(1.0f + y * y + z * z);
-        cells[3 * k] = inv; cells[3 * k + 1] = y * inv; cells[3 * k + 2] = z * inv;
-    }
-    // guidance.hpp:122: unit direction through raw pixel `hit` of the 20x16 grid
-    std::vector<float> pix(960);
-    for (uint32_t hit = 0; hit < 320; hit++) {
-        const float ry = 1.0f - (float(hit % 20) + .5f) / 10.0f;
-        const float rz = MDN_SENSOR_TAN_V * (1.0f - (float(hit / 20) + .5f) / 8.0f);
-        const float inv = 1.0f / mdn::sqrt_f(1 + ry * ry + rz * rz);
-        pix[3 * hit] = inv; pix[3 * hit + 1] = ry * inv; pix[3 * hit + 2] = rz * inv;
-    }
+    // policy initialisation is a host computation shared with the oracle
+    // (mdnav_host.h); copies are synchronous.
     std::vector<float> actor(s->shape.actor_count()), critic(s->shape.critic_count());
     mdn::init_policy(s->shape, actor.data(), critic.data());
-    if (hipMemcpy(s->camera, cam.data(), cam.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(s->cells, cells.data(), cells.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(s->pix_rays, pix.data(), pix.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(s->raptor, raptor, sizeof(MdnRaptorWeights), hipMemcpyHostToDevice) != hipSuccess ||
+    if (hipMemcpy(s->raptor, raptor, sizeof(MdnRaptorWeights), hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(s->actor, actor.data(), actor.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(s->critic, critic.data(), critic.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
         mdn_sim_destroy(s);
@@ -460,6 +477,21 @@ int mdn_sim_reset(MdnSim* s) {
     return MDN_OK;
 }
 
+int mdn_sim_set_camera(MdnSim* s, uint32_t profile_id) {
+    if (!s) return fail(MDN_E_ARG, "mdn_sim_set_camera: null");
+    if (profile_id != MDN_CAMERA_LEGACY && profile_id != MDN_CAMERA_NATIVE)
+        return fail(MDN_E_ARG, "camera profile must be 1 (legacy) or 2 (native)");
+    HIP_TRY(hipStreamSynchronize(s->stream));  // no launch in flight reads the tables
+    s->camera_profile = mdn::camera_profile(profile_id);
+    return upload_camera(s);
+}
+
+int mdn_sim_get_camera(const MdnSim* s, MdnCameraProfile* out) {
+    if (!s || !out) return fail(MDN_E_ARG, "mdn_sim_get_camera: null");
+    *out = s->camera_profile;
+    return MDN_OK;
+}
+
 int mdn_sim_set_runtime(MdnSim* s, const MdnRuntimeConfig* runtime) {
     if (!s || !runtime) return fail(MDN_E_ARG, "mdn_sim_set_runtime: null argument");
     s->runtime = *runtime;
@@ -550,6 +582,7 @@ int collect_episodic(MdnSim* s, uint32_t count, int slots) {
     nav::MemoryArgs m;
     m.head = s->mem_head; m.sensors = s->sensors; m.poses = s->poses; m.pix_rays = s->pix_rays; m.cells = s->cells;
     m.sensor_dt = b.sensor_dt; m.inv_sensor_dt = b.inv_sensor_dt; m.n = s->cfg.n;
+    m.tan_v = s->camera_profile.tan_v;
     nav::EpisodeArgs e = s->episode_args(false);
     int rc = MDN_OK;
     for (uint32_t t = 0; t < count && rc == MDN_OK; t++) {
@@ -597,6 +630,7 @@ int mdn_sim_collect(MdnSim* s, uint32_t count) {
     nav::MemoryArgs m;
     m.head = s->mem_head; m.sensors = s->sensors; m.poses = s->poses; m.pix_rays = s->pix_rays; m.cells = s->cells;
     m.sensor_dt = b.sensor_dt; m.inv_sensor_dt = b.inv_sensor_dt; m.n = s->cfg.n;
+    m.tan_v = s->camera_profile.tan_v;
     for (uint32_t t = 0; t < count && rc == MDN_OK; t++) {
         m.obs = s->obs + size_t(t % s->horizon) * s->cfg.n * s->shape.obs;
         rc = timed(s, MDN_K_MEMORY, [&] { return nav_launch_memory_hint(&m, s->stream); });
@@ -1429,6 +1463,7 @@ int mdn_lppo_collect(MdnLargePPO* p, uint32_t count) {
     nav::MemoryArgs m;
     m.head = s->mem_head; m.sensors = s->sensors; m.poses = s->poses; m.pix_rays = s->pix_rays; m.cells = s->cells;
     m.sensor_dt = a.sensor_dt; m.inv_sensor_dt = a.inv_sensor_dt; m.n = N;
+    m.tan_v = s->camera_profile.tan_v;
     // tick 0 up to its observation; then per tick: wide actor means of the
     // tick's rows, and one launch that acts, advances, resets and observes the
     // next tick
@@ -1624,6 +1659,9 @@ bool same_run_settings(const MdnSimConfig& a, const MdnSimConfig& b) {
 // Buffers of a checkpoint body after the header, in file order
 // (main.mm:1302-1306): actor, critic, their Adam moments, then the
 // simulator's states, runs, worlds, sensor ring, pose ring, command ring.
+// TrainingPotentialControl (16 B) + TrainingPotentialGridSpec (44 B) + the
+// 64-byte field hash (training_potential.hpp:33-52; main.mm:1259-1262)
+constexpr size_t kShapingBlockBytes = 16 + 44 + 64;
 const uint32_t kCheckpointBuffers[] = {MDN_BUF_ACTOR, MDN_BUF_CRITIC, MDN_BUF_ACTOR_M, MDN_BUF_ACTOR_V,
                                        MDN_BUF_CRITIC_M, MDN_BUF_CRITIC_V, MDN_BUF_STATES, MDN_BUF_RUNS,
                                        MDN_BUF_WORLDS, MDN_BUF_SENSORS, MDN_BUF_POSES, MDN_BUF_COMMANDS};
@@ -1682,13 +1720,14 @@ int mdn_ppo_load_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
     MdnCheckpointHeader h;
     int rc = read_checkpoint_header(file, &h);
     if (rc) return rc;
-    if (h.version >= 9)
-        return fail(MDN_E_ARG, "checkpoint versions 9-10 carry shaping and camera blocks this build does not "
-                               "have; warm-start from the parameters instead");
     if (h.actor_count != s->shape.actor_count() || h.critic_count != s->shape.critic_count())
         return fail(MDN_E_ARG, "PPO checkpoint dimensions mismatch");
     if (h.family != family || h.horizon != horizon || h.n != n || h.base_seed != seed)
         return fail(MDN_E_ARG, "PPO checkpoint config mismatch");
+    // main.mm:1225-1226: before version 10 a checkpoint had the legacy camera
+    if (h.version < 10 && s->camera_profile.id != MDN_CAMERA_LEGACY)
+        return fail(MDN_E_ARG, "legacy checkpoint cannot resume with calibrated sensors; use an explicit parameter "
+                               "warmstart");
     if (h.horizon != s->horizon || !same_run_settings(h.config, s->cfg))
         return fail(MDN_E_ARG, "PPO checkpoint simulator settings mismatch");
     if (h.optimizer_step > uint64_t(UINT32_MAX)) return fail(MDN_E_ARG, "PPO checkpoint Adam step is too large");
@@ -1734,6 +1773,29 @@ int mdn_ppo_load_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
     } else if (s->runtime.enabled != 0u || s->task.enabled != 0u) {  // main.mm:1254-1257: a bank alone is fine
         return fail(MDN_E_ARG, "legacy resume cannot infer new dynamics/task state; use explicit parameter warmstart");
     }
+    // version 9 (main.mm:1258-1266): the shaping control, grid spec and field
+    // hash, which must equal this sim's.  This sim trains without the
+    // training potential, i.e. with the reference's disabled block: a
+    // value-initialised control and grid and a zeroed hash (main.mm:534-536).
+    if (h.version >= 9) {
+        unsigned char shaping[kShapingBlockBytes];
+        if (!file.read(shaping, sizeof(shaping))) return fail(MDN_E_ARG, "truncated shaping configuration");
+        for (unsigned char c : shaping)
+            if (c != 0)
+                return fail(MDN_E_ARG, "checkpoint shaping configuration or field hash mismatch: it was trained with "
+                                       "the geodesic training potential, which this build does not run; use an "
+                                       "explicit parameter warmstart");
+    }
+    // version 10 (main.mm:1268-1277): the camera contract, which must be this
+    // sim's profile
+    if (h.version >= 10) {
+        MdnCameraProfile saved;
+        const MdnCameraProfile& c = s->camera_profile;
+        if (!file.read(&saved, sizeof(saved)) || saved.id != c.id || saved.tan_h != c.tan_h ||
+            saved.tan_v != c.tan_v || saved.mount_x_m != c.mount_x_m || saved.min_range_m != c.min_range_m ||
+            saved.max_range_m != c.max_range_m)
+            return fail(MDN_E_ARG, "checkpoint camera contract mismatch; use an explicit parameter warmstart");
+    }
     if (!file.at_end()) return fail(MDN_E_ARG, "PPO checkpoint has trailing data");
     for (size_t i = 0; i < body.size(); i++) {
         rc = mdn_sim_upload(s, kCheckpointBuffers[i], body[i].data(), body[i].size());
@@ -1757,10 +1819,13 @@ int mdn_ppo_save_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
     MdnCheckpointHeader h;
     std::memset(&h, 0, sizeof(h));  // padding bytes too, so equal states give equal files
     std::memcpy(h.magic, "PPOFIX1", 7);
-    // main.mm:1292: version 8 with the dynamics/task blocks when per-episode
-    // plants or tasks are on, else 6 (no shaping; the legacy camera).  A
-    // challenge bank alone writes version 6, as in the reference.
-    h.version = (s->runtime.enabled != 0u || s->task.enabled != 0u) ? 8 : 6;
+    // main.mm:1292-1293: version 10 with the native camera; else 8 with the
+    // dynamics/task blocks when per-episode plants or tasks are on, else 6
+    // (version 9 needs the training potential, which this build does not run).
+    // A challenge bank alone writes version 6, as in the reference.
+    h.version = s->camera_profile.id == MDN_CAMERA_NATIVE                   ? 10
+                : (s->runtime.enabled != 0u || s->task.enabled != 0u) ? 8
+                                                                        : 6;
     h.actor_count = s->shape.actor_count();
     h.critic_count = s->shape.critic_count();
     h.horizon = s->horizon;
@@ -1797,6 +1862,11 @@ int mdn_ppo_save_checkpoint(MdnPPO* p, const char* path, uint32_t family, uint32
                  file.write(env_phys.data(), env_phys.size()) && file.write(task_states.data(), task_states.size()) &&
                  file.write(&s->phys, sizeof(s->phys)) && file.write(raptor.data(), 2084 * 4);
         }
+        if (h.version >= 9) {  // main.mm:1310-1312: the disabled shaping block
+            const unsigned char shaping[kShapingBlockBytes] = {};
+            ok = ok && file.write(shaping, sizeof(shaping));
+        }
+        if (h.version >= 10) ok = ok && file.write(&s->camera_profile, sizeof(s->camera_profile));  // 1313-1317
         ok = ok && std::fflush(file.f) == 0;
         if (!ok) {
             std::remove(temp.c_str());

@@ -23,6 +23,8 @@ struct RolloutArgs {
     const float* camera;      // unit pixel rays [320][3]
     const float* cells;       // pooled-cell directions [80][3] (guidance.hpp:21-26 nav_ray)
     float sensor_dt;          // sensor period in seconds: period x dt x substeps (sim.metal:226)
+    float mount_x;            // camera mount ahead of the body point (sim.metal:151)
+    float tan_v;              // camera vertical half-tangent (sensor_profile.hpp:46-51)
     double inv_sensor_dt;     // RN64(1 / max(sensor_dt, 1e-3)), the guidance's closing-speed divisor
     float* obs;            // [T][N][181]
     float* co;             // [T][N][32]
@@ -115,6 +117,7 @@ struct MemoryArgs {
     const float* pix_rays;  // [320][3] unit rays through the raw pixels (guidance.hpp:122)
     const float* cells;     // [80][3] pooled-cell rays (nav_ray)
     float sensor_dt;
+    float tan_v;            // camera vertical half-tangent (the goal's field-of-view test)
     double inv_sensor_dt;
     uint32_t n;
 };

@@ -307,7 +307,7 @@ __global__ __launch_bounds__(THREADS) void memory_hint_kernel(nav::MemoryArgs a)
             direction(best, best_dir);
             best_free = cand_free[best];
         }
-        const float tan_v = MDN_SENSOR_TAN_V;
+        const float tan_v = a.tan_v;
         const bool goal_in_fov = goal[0] > 0.0f && fabs_f(goal[1]) <= goal[0] && fabs_f(goal[2]) <= tan_v * goal[0];
         const float after_stop = fmax_f(best_free - stop_margin - 0.15f, 0.0f);
         float command_speed = fmin_f(desired_speed, sqrt_f(4.0f * after_stop));

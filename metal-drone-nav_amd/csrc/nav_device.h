@@ -186,7 +186,7 @@ __device__ __forceinline__ void box_slab(const float* world, const float* center
 // whose rays can reach box [A, B] (coordinates relative to the ray origin)
 // at a hit value below 12, as a 5-bit mask.  R is the camera rotation
 // (row-major, world = R camera).  Camera rays are (1, -y, -z) normalised with
-// |y| <= 0.95 and |z| <= 0.703125 at the pixel centres, so the rays of a strip
+// |y| <= 0.95 tan_h and |z| <= 0.9375 tan_v at the pixel centres, so the rays of a strip
 // lie in the wedge between the planes through its outer columns (the
 // frame's rows and columns follow the camera rays of the sim's setup).  A box is
 // left out of a strip only when one of those planes (or the image's top,
@@ -196,7 +196,7 @@ __device__ __forceinline__ void box_slab(const float* world, const float* center
 // of a rotation within 1e-6 of orthonormal), so such a box yields a miss or a
 // value of at least 12 for every ray of the strip, and leaving it out does
 // not change the depth.
-__device__ __forceinline__ uint32_t box_strips(const float (&A)[3], const float (&B)[3], const float* R) {
+__device__ __forceinline__ uint32_t box_strips(const float (&A)[3], const float (&B)[3], const float* R, float tan_v) {
     const float gap = 2e-3f;  // plane normals below have length <= 1.7
     float d2 = 0.0f;
 #pragma unroll
@@ -213,7 +213,7 @@ __device__ __forceinline__ uint32_t box_strips(const float (&A)[3], const float 
         for (int j = 0; j < 3; j++) m += fmin_f(n[j] * A[j], n[j] * B[j]);
         return m;
     };
-    const float tv = 0.9375f * MDN_SENSOR_TAN_V;  // |z| of the outer pixel rows
+    const float tv = 0.9375f * tan_v;  // |z| of the outer pixel rows
     {
         const float behind[3] = {-f[0], -f[1], -f[2]};
         const float top[3] = {-tv * f[0] - u[0], -tv * f[1] - u[1], -tv * f[2] - u[2]};

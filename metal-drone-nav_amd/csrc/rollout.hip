@@ -752,7 +752,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         // observation row is free until observe and holds the tables.
         const bool boxes = boxes_only(world, count);
         const bool wave_boxes = !__any(depth_now && !boxes);
-        const float mx = 0.0f;
+        const float mx = a.mount_x;  // sim.metal:149-152
         const V origin = mk(s.p[0] + mx * R[0], s.p[1] + mx * R[3], s.p[2] + mx * R[6]);
         if (depth_now && lane == 0) {
             float* pose = a.poses + (size_t(nn) * 8 + (r.steps / C.sensor_period) % 8) * 12;
@@ -779,7 +779,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
                     for (int j = 0; j < 3; j++) { tbl[6 * i + j] = A[j]; tbl[6 * i + 3 + j] = B[j]; }
                     if (i >= 1 && i - 1 < count) {
-                        const uint32_t m = box_strips(A, B, R);
+                        const uint32_t m = box_strips(A, B, R, a.tan_v);
                         for (uint32_t st = 0; st < 4; st++) vis0 |= ((m >> st) & 1u) << (8 * st + i - 1);
                         vis1 |= ((m >> 4) & 1u) << (i - 1);
                     }

@@ -105,6 +105,12 @@ assert TASK_CONFIG.itemsize == 144 and TASK_CONTROL.itemsize == 148 and TASK_STA
 SENSOR_CONTRACT = np.dtype([("profile_id", u4), ("tan_h", f4), ("tan_v", f4), ("mount_x_m", f4),
                             ("min_range_m", f4), ("max_range_m", f4), ("noise_m", f4), ("reserved", u4)])
 assert SENSOR_CONTRACT.itemsize == 32
+# nav_sensor::Profile (sensor_profile.hpp:113-116): the camera of a simulator
+# and of a PPOFIX1 version-10 checkpoint
+CAMERA_PROFILE = np.dtype([("id", u4), ("tan_h", f4), ("tan_v", f4), ("mount_x_m", f4), ("min_range_m", f4),
+                           ("max_range_m", f4)])
+assert CAMERA_PROFILE.itemsize == 24
+CAMERA_LEGACY, CAMERA_NATIVE = 1, 2
 assert CHECKPOINT_HEADER.itemsize == 136 and NAV_POLICY_META.itemsize == 56
 assert PHYSICS_STATE.itemsize == 68 and PHYSICS_PARAMS.itemsize == 352
 assert RAPTOR_WEIGHTS.itemsize == 8336 and WORLD.itemsize == 676

@@ -28,7 +28,8 @@ EXPORTS = [
     "mdn_sim_set_tasks", "mdn_sim_get_tasks", "mdn_task_default_config", "mdn_domain_stress_range", "mdn_sim_set_bank", "mdn_navwid_read",
     "mdn_navwid_write", "mdn_op_actor_forward", "mdn_op_critic_forward", "mdn_op_gaussian_log_prob",
     "mdn_op_sample_loss_and_grad", "mdn_op_adam_update", "mdn_op_ppo_self_tests", "mdn_sim_validate_rollout",
-    "mdn_checkpoint_read_params", "mdn_op_normalize_noalloc", "mdn_sim_get_bank",
+    "mdn_checkpoint_read_params", "mdn_op_normalize_noalloc", "mdn_sim_get_bank", "mdn_sim_set_camera",
+    "mdn_sim_get_camera",
 ]
 
 P = ctypes.c_void_p
@@ -79,6 +80,8 @@ def lib():
         _sig(L, "mdn_navpol_write", I32, ctypes.c_char_p, P, P, U64, U64)
         _sig(L, "mdn_fnv1a64_file", I32, ctypes.c_char_p, ctypes.POINTER(U64))
         _sig(L, "mdn_sim_get_actor_obs", I32, P, ctypes.POINTER(U32))
+        _sig(L, "mdn_sim_set_camera", I32, P, U32)
+        _sig(L, "mdn_sim_get_camera", I32, P, P)
         _sig(L, "mdn_sim_set_runtime", I32, P, P)
         _sig(L, "mdn_sim_get_runtime", I32, P, P)
         _sig(L, "mdn_sim_set_tasks", I32, P, P)

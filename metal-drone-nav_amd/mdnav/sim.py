@@ -106,6 +106,17 @@ class Sim:
         check(lib().mdn_sim_get_actor_obs(self.h, ctypes.byref(d)))
         return d.value
 
+    def set_camera(self, profile):
+        """Camera profile: abi.CAMERA_LEGACY (1) or abi.CAMERA_NATIVE (2)
+        (sensor_profile.hpp:16-25, 111-126)."""
+        check(lib().mdn_sim_set_camera(self.h, int(profile)))
+
+    @property
+    def camera(self):
+        c = np.zeros((), abi.CAMERA_PROFILE)
+        check(lib().mdn_sim_get_camera(self.h, c.ctypes.data_as(ctypes.c_void_p)))
+        return c
+
     def set_runtime(self, runtime):
         """Episode dynamics variation (NavigationRuntimeConfig,
         navigation_runtime.hpp:9-14); takes effect at the next reset."""
@@ -250,13 +261,16 @@ class PPOTrainer:
         return u.value
 
     def save_checkpoint(self, path, family, seed, completed_rollouts):
-        """PPOTrainer::save_checkpoint (main.mm:1285-1317): PPOFIX1 version 6, or 8
-        with the dynamics/task blocks when per-episode plants or tasks are on."""
+        """PPOTrainer::save_checkpoint (main.mm:1285-1317): PPOFIX1 version 6, 8
+        with the dynamics/task blocks when per-episode plants or tasks are on,
+        10 with the native camera."""
         check(lib().mdn_ppo_save_checkpoint(self.h, str(path).encode(), family, seed, completed_rollouts))
 
     def load_checkpoint(self, path, family, horizon, n, seed):
-        """PPOTrainer::load_checkpoint (main.mm:1218-1284), versions 3-8.
-        Returns the completed rollouts (0 when the file is absent)."""
+        """PPOTrainer::load_checkpoint (main.mm:1218-1284), versions 3-10 (a
+        shaping block must be the disabled one; version 10's camera contract
+        must be this simulator's).  Returns the completed rollouts (0 when the
+        file is absent)."""
         done = ctypes.c_uint32()
         check(lib().mdn_ppo_load_checkpoint(self.h, str(path).encode(), family, horizon, n, seed, ctypes.byref(done)))
         return done.value

@@ -247,6 +247,8 @@ struct Trainer {
     std::vector<float> metric_rows;
     float metric_mean[4] = {0, 0, 0, 0};
     std::vector<float> means, camera;
+    // camera profile (sensor_profile.hpp:46-51): legacy unless set_camera
+    float camera_tan_v = MDN_SENSOR_TAN_V, camera_mount_x = 0.0f;
     // episode dynamics and navigation tasks (sim.metal:55-141, 287, 307-315)
     MdnRuntimeConfig runtime;
     MdnTaskControl tasks;
@@ -287,12 +289,19 @@ struct Trainer {
         std::memset(&bank, 0, sizeof(bank));
         bank_active.assign(n, MDN_BANK_REHEARSAL);
         bank_transition.assign(rows, MDN_BANK_REHEARSAL);
+        set_camera(MDN_SENSOR_TAN_V, 0.0f);
+        for (uint32_t e = 0; e < cfg.n; e++) reset_env(e, true, 0);
+    }
+
+    // the profile's pixel rays and mount (sim.metal:147-152)
+    void set_camera(float tan_v, float mount_x) {
+        camera_tan_v = tan_v;
+        camera_mount_x = mount_x;
         camera.resize(MDN_SENSOR_PIXELS * 3);
         for (uint32_t k = 0; k < MDN_SENSOR_PIXELS; k++) {
-            const V3 ray = camera_ray(k);
+            const V3 ray = camera_ray(k, tan_v);
             camera[3 * k] = ray.x; camera[3 * k + 1] = ray.y; camera[3 * k + 2] = ray.z;
         }
-        for (uint32_t e = 0; e < cfg.n; e++) reset_env(e, true, 0);
     }
 
     // cpu_reference.hpp:219-238 == sim.metal:17-36
@@ -413,7 +422,7 @@ struct Trainer {
         rotation(s.orientation_wxyz, r);
         if (run.steps % cfg.sensor_period == 0) {
             const uint32_t frame = (run.steps / cfg.sensor_period) % 8;
-            const float mx = 0.0f;
+            const float mx = camera_mount_x;
             const V3 origin = v3(s.position[0] + mx * r[0], s.position[1] + mx * r[3], s.position[2] + mx * r[6]);
             float* pose = &poses[(size_t(n) * 8 + frame) * 12];
             pose[0] = origin.x; pose[1] = origin.y; pose[2] = origin.z;
@@ -479,10 +488,10 @@ struct Trainer {
                 for (int j = 0; j < 9; j++) pose[3 + j] = r[j];
                 uint32_t valid = available >= delay ? std::min(frame + 1, 8u - delay) : 0u;
                 if (cfg.mode == 18) valid = std::min(valid, 1u);  // memory.metal:34: newest frame only
-                nav_guidance_memory(cur, prv, goal, distance, vel, sensor_dt, MDN_SENSOR_TAN_V,
+                nav_guidance_memory(cur, prv, goal, distance, vel, sensor_dt, camera_tan_v,
                                     &sensors[size_t(n) * 8 * 320], &poses[size_t(n) * 8 * 12], pose, frame, valid, hint);
             } else {
-                nav_guidance(cur, prv, goal, distance, vel, sensor_dt, MDN_SENSOR_TAN_V, hint);
+                nav_guidance(cur, prv, goal, distance, vel, sensor_dt, camera_tan_v, hint);
             }
             for (int j = 0; j < 3; j++) o[shape.obs - 3 + j] = hint[j];
         }
@@ -926,6 +935,10 @@ void orc_trainer_minibatch_grads(void* h, uint32_t begin, uint32_t b, float* act
 void orc_trainer_set_config(void* h, const MdnSimConfig* cfg) { static_cast<Trainer*>(h)->cfg = *cfg; }
 void orc_trainer_set_hidden(void* h, uint32_t hidden) { static_cast<Trainer*>(h)->set_hidden(hidden); }
 void orc_trainer_set_actor_obs(void* h, uint32_t d) { static_cast<Trainer*>(h)->set_actor_obs(d); }
+void orc_trainer_set_camera(void* h, uint32_t profile_id) {
+    const MdnCameraProfile c = mdn::camera_profile(profile_id);
+    static_cast<Trainer*>(h)->set_camera(c.tan_v, c.mount_x_m);
+}
 void orc_guidance(const float* cur, const float* prev, const float* goal, float distance, const float* vel,
                   float sensor_dt, float* hint) {
     orc::nav_guidance(cur, prev, goal, distance, vel, sensor_dt, MDN_SENSOR_TAN_V, hint);
@@ -1076,6 +1089,12 @@ float orc_ray_cylinder(const float* p, const float* d, const float* c, float r, 
 void orc_camera_rays(float* out) {
     for (uint32_t k = 0; k < MDN_SENSOR_PIXELS; k++) {
         const orc::V3 r = orc::camera_ray(k);
+        out[3 * k] = r.x; out[3 * k + 1] = r.y; out[3 * k + 2] = r.z;
+    }
+}
+void orc_camera_rays_tan(float tan_v, float* out) {
+    for (uint32_t k = 0; k < MDN_SENSOR_PIXELS; k++) {
+        const orc::V3 r = orc::camera_ray(k, tan_v);
         out[3 * k] = r.x; out[3 * k + 1] = r.y; out[3 * k + 2] = r.z;
     }
 }

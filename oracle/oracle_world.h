@@ -147,11 +147,12 @@ inline float clearance(const MdnWorld& w, V3 p, float time) {
     return best;
 }
 
-// sensor_profile.hpp:81-91 — unit ray of pixel k (row-major 20x16, row 0 up).
-inline V3 camera_ray(uint32_t pixel) {
+// sensor_profile.hpp:81-91 — unit ray of pixel k (row-major 20x16, row 0 up)
+// for the profile's vertical half-tangent (0.75 legacy, 0.8 native).
+inline V3 camera_ray(uint32_t pixel, float tan_v = MDN_SENSOR_TAN_V) {
     const uint32_t row = pixel / MDN_SENSOR_WIDTH, col = pixel % MDN_SENSOR_WIDTH;
     const float y = ((float(col) + 0.5f) / 20.0f * 2.0f - 1.0f) * MDN_SENSOR_TAN_H;
-    const float z = ((float(row) + 0.5f) / 16.0f * 2.0f - 1.0f) * MDN_SENSOR_TAN_V;
+    const float z = ((float(row) + 0.5f) / 16.0f * 2.0f - 1.0f) * tan_v;
     return vnorm(v3(1.0f, -y, -z));
 }
 

@@ -115,6 +115,18 @@ void ref_camera_rays(float* out) {
         out[3 * k] = r.x; out[3 * k + 1] = r.y; out[3 * k + 2] = r.z;
     }
 }
+// the native profile's rays and either profile's contract (sensor_profile.hpp:111-126)
+void ref_camera_rays_native(float* out) {
+    for (uint32_t k = 0; k < NAV_SENSOR_PIXELS; k++) {
+        const WVec r = nav_sensor_pixel_ray(NAV_SENSOR_TAN_H, NAV_SENSOR_NATIVE_TAN_V, k);
+        out[3 * k] = r.x; out[3 * k + 1] = r.y; out[3 * k + 2] = r.z;
+    }
+}
+void ref_camera_profile(uint32_t id, void* out) {
+    const nav_sensor::Profile p = nav_sensor::by_id(id);
+    static_assert(sizeof(p) == 24, "nav_sensor::Profile layout");
+    std::memcpy(out, &p, sizeof(p));
+}
 void ref_physics_step_batch(const MdnPhysicsState* s, const float* actions, const float* winds,
                             const MdnPhysicsParams* p, MdnPhysicsState* out, uint64_t n) {
     for (uint64_t i = 0; i < n; i++)

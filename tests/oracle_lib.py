@@ -54,6 +54,8 @@ def oracle():
         _sig(lib, "orc_trainer_evaluate", None, P)
         _sig(lib, "orc_trainer_set_ext_means", None, P, P)
         _sig(lib, "orc_trainer_set_actor_obs", None, P, U32)
+        _sig(lib, "orc_trainer_set_camera", None, P, U32)
+        _sig(lib, "orc_camera_rays_tan", None, F32, P)
         _sig(lib, "orc_guidance", None, P, P, P, F32, P, F32, P)
         _sig(lib, "orc_guidance_memory", None, P, P, P, F32, P, F32, P, P, P, U32, U32, P)
         _sig(lib, "orc_memory_clearance", None, P, P, P, P, U32, U32, F32, P)
@@ -125,6 +127,8 @@ def ref(actor_obs=181):
         _sig(lib, "ref_ray_world_batch", None, P, P, P, U32, P, U64)
         _sig(lib, "ref_clearance_batch", None, P, P, P, P, U64)
         _sig(lib, "ref_camera_rays", None, P)
+        _sig(lib, "ref_camera_rays_native", None, P)
+        _sig(lib, "ref_camera_profile", None, U32, P)
         _sig(lib, "ref_physics_step_batch", None, P, P, P, P, P, U64)
         _sig(lib, "ref_crazyflie_params", None, P)
         _sig(lib, "ref_raptor_sequence", None, P, P, U32, P, P)
@@ -265,6 +269,10 @@ class OracleTrainer:
     def evaluate(self):
         """logp / values / next_values of the stored rollout under the policy."""
         self.lib.orc_trainer_evaluate(self.h)
+
+    def set_camera(self, profile):
+        """Camera profile 1 (legacy) or 2 (native), sensor_profile.hpp:111-126."""
+        self.lib.orc_trainer_set_camera(self.h, int(profile))
 
     def set_actor_obs(self, d):
         """Actor input width: 181, or 184 with the geometry-prior hint (fresh policy)."""

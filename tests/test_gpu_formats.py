@@ -249,3 +249,68 @@ def test_evidence_evaluations(row):
     assert abs(rep["mean_speed"] - want["mean_speed_mps"]) <= 5e-3, rep
     assert abs(rep["peak_speed"] - want["peak_speed_mps"]) <= 1e-3, rep
     assert abs(rep["min_clearance"] - want["min_clearance_m"]) <= 1e-5, rep
+
+
+def test_checkpoint_versions_9_10_camera_and_shaping(tmp_path):
+    """PPOFIX1 versions 9-10 (main.mm:1258-1277, 1292-1317).  With the native
+    camera the trainer writes version 10: the version-8 blocks, the disabled
+    shaping block (the reference's value-initialised control and grid and a
+    zeroed field hash, 124 bytes, main.mm:534-536) and the 24-byte camera
+    contract.  A native simulator resumes it bit for bit and continues
+    identically to the simulator that wrote it; a legacy simulator refuses
+    it (camera contract); a native simulator refuses an older file (legacy
+    camera); a file whose shaping block is not the disabled one is refused;
+    a version-9 file with the disabled block resumes in a legacy simulator."""
+    from mdnav.native import MdnError
+    say("case: PPOFIX1 v10 native camera save/resume, v9 shaping block, refusals")
+    cfg = abi.default_config(n=64, family=1, speed=1.0, distance=3.0, max_steps=30)
+    weights = raptor_fixture()[0]
+
+    def trainer(native):
+        s = Sim(cfg, 16, raptor=weights)
+        if native:
+            s.set_camera(abi.CAMERA_NATIVE)
+        return s, PPOTrainer(s, 1, 256)
+
+    sim, ppo = trainer(True)
+    sim.collect()
+    ppo.rollout_update(0)
+    sim.sync()
+    out = tmp_path / "native.bin"
+    ppo.save_checkpoint(out, 1, 42, 1)
+    h, _ = formats.read_checkpoint(out)
+    assert int(h["version"]) == 10
+    raw = open(out, "rb").read()
+    cam = np.frombuffer(raw[-24:], abi.CAMERA_PROFILE)[0]
+    assert int(cam["id"]) == 2 and float(cam["tan_v"]) == np.float32(0.8)
+    assert float(cam["mount_x_m"]) == np.float32(0.08) and float(cam["max_range_m"]) == 12.0
+    assert raw[-148:-24] == bytes(124)
+    sim2, ppo2 = trainer(True)
+    assert ppo2.load_checkpoint(out, 1, 16, 64, 42) == 1
+    for name in ENV_BUFFERS + PPO_BUFFERS:
+        assert sim2.get(name).tobytes() == sim.get(name).tobytes(), name
+    for s_, p_ in ((sim, ppo), (sim2, ppo2)):
+        s_.collect()
+        p_.rollout_update(1)
+        s_.sync()
+    for name in ENV_BUFFERS + ROW_BUFFERS + PPO_BUFFERS:
+        assert sim2.get(name).tobytes() == sim.get(name).tobytes(), ("continued", name)
+    sim3, ppo3 = trainer(False)
+    with pytest.raises(MdnError, match="camera contract"):
+        ppo3.load_checkpoint(out, 1, 16, 64, 42)
+    old = tmp_path / "legacy.bin"
+    ppo3.save_checkpoint(old, 1, 42, 0)
+    assert int(formats.read_checkpoint(old)[0]["version"]) == 6
+    with pytest.raises(MdnError, match="calibrated sensors"):
+        ppo2.load_checkpoint(old, 1, 16, 64, 42)
+    shaped = bytearray(raw)
+    shaped[-148] = 1  # TrainingPotentialControl.enabled
+    (tmp_path / "shaped.bin").write_bytes(bytes(shaped))
+    with pytest.raises(MdnError, match="shaping"):
+        ppo2.load_checkpoint(tmp_path / "shaped.bin", 1, 16, 64, 42)
+    v9 = bytearray(raw[:-24])
+    hdr = np.frombuffer(bytes(v9[:abi.CHECKPOINT_HEADER.itemsize]), abi.CHECKPOINT_HEADER).copy()
+    hdr["version"] = 9
+    v9[:abi.CHECKPOINT_HEADER.itemsize] = hdr.tobytes()
+    (tmp_path / "v9.bin").write_bytes(bytes(v9))
+    assert ppo3.load_checkpoint(tmp_path / "v9.bin", 1, 16, 64, 42) == 1

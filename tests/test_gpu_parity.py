@@ -349,3 +349,53 @@ def test_guided_modes_bit_exact(mode):
         ora.collect()
     bad = compare(sim, ora, names, tol=0.0)
     assert not bad, bad
+
+
+@pytest.mark.parametrize("variant", ["boxes_production", "mixed_family3", "guided184", "memory184", "plants_tasks"])
+def test_native_camera_bit_exact(variant):
+    """The native camera profile (sensor_profile.hpp:18-25, 111-126): vertical
+    half-tangent 0.8 and rays cast from 0.08 m ahead of the body point
+    (sim.metal:147-152), set on both sides after creation.  Depth frames and
+    poses, observations (with the guidance hint's and the geometry memory's
+    cell and pixel directions of the same profile), the outcome and a PPO
+    update are bit-identical to the oracle at tolerance 0, on the benchmark
+    kernel, the mixed-world tables, the 184-input actor with and without the
+    geometry memory, and the per-episode path."""
+    kw = dict(n=128, family=1, speed=1.0, distance=3.0, max_steps=40)
+    actor_obs, ticks = 181, 48
+    if variant == "mixed_family3":
+        kw.update(family=3, n=512, speed=1.5, distance=4.0, max_steps=8)
+    elif variant == "guided184":
+        actor_obs = 184
+    elif variant == "memory184":
+        actor_obs = 184
+        kw.update(geometry_memory=1, max_steps=30)
+        ticks = 24
+    elif variant == "plants_tasks":
+        kw.update(family=12, mode=22, speed=1.5, distance=8.0, max_steps=60, geometry_memory=1)
+        actor_obs, ticks = 184, 16
+    say("case: native camera %s" % variant)
+    cfg = config(**kw)
+    sim, ppo, ora = make_pair(cfg, ticks, epochs=1, minibatch=2048, actor_obs=actor_obs)
+    if variant == "plants_tasks":
+        from oracle_lib import task_runtime, task_settings
+        rt, ts = task_runtime(1.0), task_settings(2, 12)
+        sim.set_runtime(rt); sim.set_tasks(ts); sim.reset()
+        ora.set_runtime(rt); ora.set_tasks(ts); ora.reset()
+    sim.set_camera(abi.CAMERA_NATIVE)
+    ora.set_camera(abi.CAMERA_NATIVE)
+    cam = sim.camera
+    assert int(cam["id"]) == 2 and float(cam["tan_v"]) == np.float32(0.8)
+    sim.collect()
+    ppo.rollout_update(0)
+    sim.sync()
+    ora.iteration(0)
+    bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v",
+                             "metric_rows"] + ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
+    assert not bad, bad
+    if variant == "boxes_production":  # the same envs with the legacy camera see other depths
+        leg = Sim(cfg, ticks, raptor=raptor_fixture()[0])
+        leg.collect()
+        leg.sync()
+        assert not np.array_equal(leg.get("sensors"), sim.get("sensors"))
+        assert not np.array_equal(leg.get("poses"), sim.get("poses"))

@@ -62,3 +62,26 @@ def test_monotone(fn):
     x = np.linspace(0.01 if fn == "log" else -8, 8, 100001, dtype=np.float32)
     y = math_batch(fn, x)
     assert np.all(np.diff(y) >= 0)
+
+
+def test_native_camera_rays_closed_form():
+    """sensor_profile.hpp:81-91 at the native tangents (1, 0.8): the corner
+    pixel (row 0, col 0) looks along (1, 0.95, 0.75) normalised, the centre
+    rows and columns straddle the optical axis symmetrically, and the legacy
+    rays are the tan_v = 0.75 case."""
+    from oracle_lib import oracle, ptr
+    F = np.float32
+    nat = np.zeros((320, 3), F)
+    leg = np.zeros((320, 3), F)
+    oracle().orc_camera_rays_tan(F(0.8), ptr(nat))
+    oracle().orc_camera_rays(ptr(leg))
+    d = np.array([1.0, 0.95, 0.75])
+    assert np.abs(nat[0] - d / np.linalg.norm(d)).max() < 2e-7
+    # pixel (15, 19): the opposite corner
+    assert np.abs(nat[15 * 20 + 19] - np.array([1.0, -0.95, -0.75]) / np.linalg.norm(d)).max() < 2e-7
+    assert np.allclose(nat[:, 0] ** 2 + nat[:, 1] ** 2 + nat[:, 2] ** 2, 1.0, atol=3e-7)
+    # up-down mirror: row r and row 15-r differ only in the sign of z
+    assert np.array_equal(nat[0:20, 2], -nat[300:320, 2]) and np.array_equal(nat[0:20, :2], nat[300:320, :2])
+    leg2 = np.zeros((320, 3), F)
+    oracle().orc_camera_rays_tan(F(0.75), ptr(leg2))
+    assert leg.tobytes() == leg2.tobytes()

@@ -145,3 +145,26 @@ def test_raptor_against_reference():
     oracle().orc_raptor_sequence(ptr(w), ptr(seq), 64, ptr(a), ptr(ha))
     ref().ref_raptor_sequence(ptr(w), ptr(seq), 64, ptr(b), ptr(hb))
     assert np.abs(a - b).max() < 2e-6 and np.abs(ha - hb).max() < 2e-6
+
+
+@needs_ref
+def test_native_camera_against_reference():
+    """The native profile (sensor_profile.hpp:18-25, 111-126): the oracle's
+    pixel rays at tan_v = 0.8 equal the reference's nav_sensor_pixel_ray bit
+    for bit, and both profiles' contracts (id, tangents, mount, ranges) equal
+    the reference's nav_sensor::by_id."""
+    a = np.zeros(960, F)
+    b = np.zeros(960, F)
+    oracle().orc_camera_rays_tan(F(0.8), ptr(a))
+    ref().ref_camera_rays_native(ptr(b))
+    assert a.tobytes() == b.tobytes()
+    for pid in (abi.CAMERA_LEGACY, abi.CAMERA_NATIVE):
+        want = np.zeros((), abi.CAMERA_PROFILE)
+        ref().ref_camera_profile(pid, ptr(want))
+        assert int(want["id"]) == pid
+        if pid == abi.CAMERA_NATIVE:
+            assert float(want["tan_v"]) == F(0.8) and float(want["mount_x_m"]) == F(0.08)
+        else:
+            assert float(want["tan_v"]) == F(0.75) and float(want["mount_x_m"]) == 0.0
+        assert float(want["tan_h"]) == 1.0 and float(want["min_range_m"]) == F(0.03)
+        assert float(want["max_range_m"]) == 12.0
