@@ -189,7 +189,9 @@ int mdn_ppo_create(MdnSim* sim, uint32_t epochs, uint32_t minibatch, MdnPPO** ou
 void mdn_ppo_destroy(MdnPPO* ppo);
 /* PPOTrainer::rollout_update (main.mm:1321-1384): GAE, advantage
  * normalisation, epochs x minibatches of loss/grad, norm clip, Adam,
- * log-std clamp, metric mean.  Asynchronous on the sim's stream. */
+ * log-std clamp, metric mean.  Asynchronous on the sim's stream.  The
+ * advantages end normalised, as with the pieces below; the rescale itself
+ * runs inside the first epoch's minibatches. */
 int mdn_ppo_rollout_update(MdnPPO* ppo, uint32_t rollout_index);
 /* Pieces of rollout_update, for callers that validate between them
  * (navigation_training.hpp:149-152). */
@@ -307,7 +309,7 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon);
  * forbid hipMalloc): mdn_op_normalize on `count` advantages already in device
  * memory, normalised in place, enqueued on `stream` (a hipStream_t; NULL for
  * the default stream) and not waited for.  It allocates nothing: the
- * statistics' scratch is a fixed array in the library (4 MiB per GPU,
+ * statistics' scratch is a fixed array in the library (64 KiB per GPU,
  * held until the process ends) and `count` may not exceed
  * MDN_NORMALIZE_NOALLOC_MAX (MDN_E_ARG otherwise).  Calls on one GPU share
  * that array: calls that overlap in time on one GPU (other streams, other

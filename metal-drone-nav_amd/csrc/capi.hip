@@ -840,14 +840,21 @@ int mdn_ppo_normalize(MdnPPO* p) {
     });
 }
 
-int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
-    if (!p) return fail(MDN_E_ARG, "mdn_ppo_update: null");
+}  // extern "C"
+
+namespace {
+// main.mm:1331-1384.  normalize_rows: the advantages hold GAE's values and
+// norm_stats (mean, inv); the first epoch's minibatches (which together
+// cover every row once) normalise their rows as they read them and store
+// them back (ppo.hpp:139), so no separate rescale pass runs.
+int ppo_update(MdnPPO* p, uint32_t rollout_index, bool normalize_rows) {
     MdnSim* s = p->sim;
     int rc = open_sync_window(s);
     if (rc) return rc;
     const uint32_t rows = uint32_t(s->rows());
     const std::vector<uint32_t> order = mdn::minibatch_schedule(rows, p->minibatch, p->epochs, rollout_index);
     if (order.size() != p->updates) return fail(MDN_E_STATE, "PPO update count mismatch");
+    const size_t first_epoch = order.size() / p->epochs;
     for (size_t u = 0; u < order.size(); u++) {
         const uint32_t begin = order[u];
         const uint32_t b = std::min(p->minibatch, rows - begin);
@@ -858,6 +865,10 @@ int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
         ra.old_logp = s->logp + begin;
         ra.adv = s->advantages + begin;
         ra.ret = s->returns + begin;
+        if (normalize_rows && u < first_epoch) {
+            ra.norm = p->norm_stats;
+            ra.adv_out = s->advantages + begin;
+        }
         ra.actor = s->actor; ra.actor_w1t = s->actor_w1t; ra.critic = s->critic; ra.critic_w1t = s->critic_w1t;
         ra.part = p->part;
         ra.b = b; ra.d = s->shape.obs; ra.clip = 0.2f; ra.vcoef = 0.5f; ra.ecoef = s->cfg.entropy_coef;
@@ -891,12 +902,25 @@ int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
     HIP_TRY(ppo_launch_metric_mean(p->metric_rows, p->metric_mean, p->updates, s->stream));
     return MDN_OK;
 }
+}  // namespace
+
+extern "C" {
+
+int mdn_ppo_update(MdnPPO* p, uint32_t rollout_index) {
+    if (!p) return fail(MDN_E_ARG, "mdn_ppo_update: null");
+    return ppo_update(p, rollout_index, false);
+}
 
 int mdn_ppo_rollout_update(MdnPPO* p, uint32_t rollout_index) {
     int rc = mdn_ppo_gae(p);
-    if (!rc) rc = mdn_ppo_normalize(p);
-    if (!rc) rc = mdn_ppo_update(p, rollout_index);
-    return rc;
+    if (rc) return rc;
+    MdnSim* s = p->sim;
+    rc = timed(s, MDN_K_NORMALIZE, [&] {
+        return ppo_launch_normalize_stats(s->advantages, s->rows(), p->norm_part, p->norm_stats, 1.0e-8f, 0,
+                                          s->stream);
+    });
+    if (rc) return rc;
+    return ppo_update(p, rollout_index, true);
 }
 
 int mdn_ppo_metric_mean(MdnPPO* p, float out[4]) {
@@ -1044,6 +1068,7 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon) {
     if (!rc) rc = upload_tmp(part, nullptr, ppo_normalize_part_words(count) * 8);
     if (!rc) rc = upload_tmp(stats, nullptr, 8);
     if (rc) return rc;
+    HIP_TRY(hipMemset(part.p, 0, ppo_normalize_part_words(count) * 8));  // the ticket starts at zero
     HIP_TRY(ppo_launch_normalize(static_cast<float*>(a.p), count, static_cast<double*>(part.p),
                                  static_cast<float*>(stats.p), epsilon, nullptr));
     HIP_TRY(hipDeviceSynchronize());
@@ -1055,9 +1080,9 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon) {
 }  // extern "C"
 
 namespace {
-// Scratch of mdn_op_normalize_noalloc: the chunk partials of the advantage
-// statistics (two doubles per 256 rows) followed by the two statistics
-// (mean, inverse deviation).  Every GPU the library runs on holds its own
+// Scratch of mdn_op_normalize_noalloc: a 32-bit ticket and the group
+// partials of the advantage statistics (two doubles per 16,384 rows),
+// followed by the two statistics (mean, inverse deviation).  Every GPU the library runs on holds its own
 // copy for the life of the process.
 constexpr uint64_t kNoallocPartials = ppo_normalize_part_words(MDN_NORMALIZE_NOALLOC_MAX);
 constexpr size_t kNoallocBytes = kNoallocPartials * sizeof(double) + 2 * sizeof(float);
@@ -1096,8 +1121,9 @@ int mdn_op_normalize_noalloc(float* advantages, uint64_t count, float epsilon, v
     unsigned char* base = nullptr;
     int rc = scratch_address(&base);
     if (rc) return rc;
-    // partials are written by the first pass before any read, the
-    // statistics by the finishing passes: nothing needs clearing
+    // partials are written by each pass before the next reads them and the
+    // statistics by the passes; the ticket is zero from load time and each
+    // call leaves it zero, so nothing needs clearing
     double* part = reinterpret_cast<double*>(base);
     float* stats = reinterpret_cast<float*>(base + kNoallocPartials * sizeof(double));
     HIP_TRY(ppo_launch_normalize(advantages, count, part, stats, epsilon, static_cast<hipStream_t>(stream)));

@@ -135,6 +135,10 @@ struct RowArgs {
     const float* old_logp;  // [b]
     const float* adv;       // [b]
     const float* ret;       // [b]
+    // (mean, inv) when the rows' advantages are still to be normalised:
+    // each row's (adv - mean) * inv is used and stored back to adv_out
+    const float* norm = nullptr;
+    float* adv_out = nullptr;  // [b]
     const float* actor;     // flat params
     const float* actor_w1t; // [OBS][HID]
     const float* critic;
@@ -198,9 +202,13 @@ hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const
                           float* adv, float* ret, uint32_t horizon, uint32_t n, float gamma, float lambda,
                           hipStream_t st);
 hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st);
-// doubles of ppo_launch_normalize's `part` for `count` elements: both
-// passes' partials, one per chunk of 256 elements
-constexpr uint64_t ppo_normalize_part_words(uint64_t count) { return 2 * ((count + 255) / 256); }
+// The statistics only (stats = mean, inv) when apply == 0.
+hipError_t ppo_launch_normalize_stats(float* a, uint64_t count, double* part, float* stats, float eps, int apply,
+                                      hipStream_t st);
+// doubles of ppo_launch_normalize's `part` for `count` elements: a 32-bit
+// ticket that must be zero when allocated, then both passes' partials, one
+// per group of 64 chunks of 256 elements
+constexpr uint64_t ppo_normalize_part_words(uint64_t count) { return 1 + 2 * ((count + 16383) / 16384); }
 hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st);
 hipError_t ppo_launch_grads(float* part, float* grad, uint32_t b, uint32_t d, hipStream_t st);
 hipError_t ppo_launch_minibatch(const ppo::MbArgs* m, hipStream_t st);

@@ -10,8 +10,8 @@
 //     ppo_actor_grad_direct's order, ppo.metal:497-519);
 //   * squared gradient norm: 256 strided partials then a pairwise tree;
 //   * advantage statistics in double: within each 256-element chunk, lane
-//     sums of 4 elements combined by a wavefront xor butterfly; chunk
-//     partials sequential within groups of 64, then over the groups.
+//     sums of 4 elements combined by a pairwise tree over adjacent lanes;
+//     chunk partials sequential within groups of 64, then over the groups.
 // Dot products and weight-gradient sums are fma chains (one rounding per
 // step), which the fp32 matrix-core GEMMs below reproduce exactly.
 #include <hip/hip_runtime.h>
@@ -42,10 +42,11 @@ struct AL {
 
 // ---------------------------------------------------------------- GAE
 // ppo.hpp:108-126 == ppo.metal:279-304, reverse scan per env.  A workgroup
-// owns 32 envs and walks the horizon backwards in tiles of 32 ticks: all 256
-// threads load the tile coalesced and form delta = r + gamma*V'(s') - V(s)
-// in LDS, one lane per env then runs the carry recurrence over the tile (the
-// only serial part), and the tile of advantages/returns is stored coalesced.
+// owns a slice of 32 envs and walks the horizon backwards in tiles of 128
+// ticks: all 256 threads load the tile coalesced and form
+// delta = r + gamma*V'(s') - V(s) in LDS, one lane per env then runs the
+// carry recurrence over the tile (the only serial part), and the tile of
+// advantages/returns is stored coalesced.
 constexpr uint32_t GAE_ENVS = 32, GAE_TICKS = 128, GAE_PER = GAE_ENVS * GAE_TICKS / 256, GAE_SCAN = 32;
 struct GaeTile {
     float delta[GAE_PER], value[GAE_PER];
@@ -125,6 +126,16 @@ __device__ __forceinline__ void gae_pos(uint32_t j, uint32_t& tt, uint32_t& e) {
         e = i % GAE_ENVS;
     }
 }
+// The slice workgroup b takes out of S.  Workgroups go to the eight XCDs
+// round-robin (b % 8); with S % 64 == 0 the eight slices of each 256-env
+// block run on one XCD, so a 128-byte line of flags (four slices) is fetched
+// into one L2.
+__device__ __forceinline__ uint32_t gae_slice(uint32_t b, uint32_t S) {
+    if (S % 64 != 0) return b;
+    const uint32_t k = b / 8;
+    return 8 * (b % 8 + 8 * (k / 8)) + k % 8;
+}
+
 template <bool V4>
 __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, const float* __restrict__ v,
                                                   const float* __restrict__ nv, const uint8_t* __restrict__ te,
@@ -135,7 +146,9 @@ __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, c
     __shared__ float s_val[GAE_TICKS][GAE_ENVS + 1];
     __shared__ float s_adv[GAE_TICKS][GAE_ENVS + 1];
     __shared__ uint32_t s_bnd[GAE_TICKS][GAE_ENVS + 1];
-    const uint32_t e0 = blockIdx.x * GAE_ENVS, tid = threadIdx.x;
+    const uint32_t S = (n + GAE_ENVS - 1) / GAE_ENVS;
+    const uint32_t slice = gae_slice(blockIdx.x, S);
+    const uint32_t e0 = slice * GAE_ENVS, tid = threadIdx.x;
     float carry = 0.0f;
     GaeTile cur;
     uint32_t t1 = horizon, t0 = t1 > GAE_TICKS ? t1 - GAE_TICKS : 0;
@@ -178,16 +191,34 @@ __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, c
             }
         }
         __syncthreads();
+        if constexpr (V4) {
+            // thread tid stores envs 4 (tid % 8) .. + 3 of rows tid / 8 + 32 j
+            // with 16-byte stores
+            const uint32_t e = 4 * (tid % 8);
 #pragma unroll
-        for (uint32_t j = 0; j < GAE_PER; j++) {
-            uint32_t tt, e;
-            gae_pos<V4>(j, tt, e);
-            const uint32_t t = t0 + tt, env = e0 + e;
-            if (t < t1 && env < n) {
-                const size_t k = size_t(t) * n + env;
-                const float a = s_adv[tt][e];
-                adv[k] = a;
-                ret[k] = a + s_val[tt][e];
+            for (uint32_t j = 0; j < GAE_PER / 4; j++) {
+                const uint32_t tt = tid / 8 + 32 * j, t = t0 + tt, env = e0 + e;
+                const float4 a4 = make_float4(s_adv[tt][e], s_adv[tt][e + 1], s_adv[tt][e + 2], s_adv[tt][e + 3]);
+                const float4 r4 = make_float4(a4.x + s_val[tt][e], a4.y + s_val[tt][e + 1], a4.z + s_val[tt][e + 2],
+                                              a4.w + s_val[tt][e + 3]);
+                if (t < t1 && env < n) {
+                    const size_t k = size_t(t) * n + env;
+                    *reinterpret_cast<float4*>(adv + k) = a4;
+                    *reinterpret_cast<float4*>(ret + k) = r4;
+                }
+            }
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < GAE_PER; j++) {
+                uint32_t tt, e;
+                gae_pos<V4>(j, tt, e);
+                const uint32_t t = t0 + tt, env = e0 + e;
+                if (t < t1 && env < n) {
+                    const size_t k = size_t(t) * n + env;
+                    const float a = s_adv[tt][e];
+                    adv[k] = a;
+                    ret[k] = a + s_val[tt][e];
+                }
             }
         }
         __syncthreads();
@@ -196,116 +227,164 @@ __global__ __launch_bounds__(256) void gae_kernel(const float* __restrict__ r, c
     }
 }
 
-// ---------------------------------------------------------------- normalisation
-// ppo.hpp:128-140 with double statistics in the canonical order: a chunk's
-// partial is formed by one wavefront (lane l adds elements 4l..4l+3 in order,
-// then an xor butterfly over the 64 lanes); chunk partials are summed
-// sequentially within groups of NORM_GROUP chunks, then the group sums
-// sequentially.  Three launches: pass 0 stores the chunk partials of sum a;
-// pass 1 forms the mean from them in every workgroup, then stores the chunk
-// partials of sum (a - mean)^2; the rescale kernel forms both totals the same
-// way and applies (a - mean) / sqrt(var + eps).
+// ---------------------------------------------------------------- advantage statistics
+// ppo.hpp:128-140 with double statistics in the canonical order: a chunk of
+// 256 elements is summed by one wavefront (lane l adds elements 4l..4l+3 in
+// order, then xor levels 1, 2, ..., 32: a pairwise tree over adjacent
+// lanes); chunk partials are added sequentially within groups of NORM_GROUP
+// chunks, then the group sums sequentially.
 //
-// The grouped sum of up to two partial arrays (threads 0-127 take array 0,
-// 128-255 array 1), returned to every thread: rounds of 128 groups, a thread
-// per group loads its NORM_GROUP partials at once and adds them in order,
-// then one thread per array adds the round's group sums in order.
-// gs: LDS double[2 * 129].
-__device__ __forceinline__ void norm_totals(const double* __restrict__ p0, const double* __restrict__ p1,
-                                            uint64_t chunks, double* gs, double& t0, double& t1) {
-    const uint32_t arr = threadIdx.x / 128, tid = threadIdx.x % 128;
-    const double* __restrict__ part = arr == 0 ? p0 : p1;
-    double* g = gs + arr * 129;
-    const uint64_t groups = (chunks + NORM_GROUP - 1) / NORM_GROUP;
+// Two passes, each storing one partial per group (a 1024-thread workgroup
+// per group of 64 chunks): the values, then the squared deviations.  The
+// second pass forms the mean from the first's group partials (64 per
+// million values) in every workgroup while its own values load; its last
+// workgroup to finish forms 1 / sqrt(var + eps).  The rescale itself is a
+// third launch or, in PPOTrainer::rollout_update, part of the first epoch's
+// minibatch kernels.
+//
+// part: a 32-bit ticket (zero when allocated; the last workgroup of each
+// second pass resets it), then pass 0's group partials, then pass 1's.
+constexpr uint32_t NORM_THREADS = 1024, NORM_WAVE_CHUNKS = NORM_GROUP / (NORM_THREADS / 64);
+static_assert(NORM_WAVE_CHUNKS * (NORM_THREADS / 64) == NORM_GROUP, "a workgroup per group of chunks");
+
+// Sum of the 64 lanes' values in the canonical tree (xor levels 1..32).
+__device__ __forceinline__ double chunk_tree(double v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+// Sequential sum of p[0, m) (the group partials, in order), returned to
+// every thread: rounds of 256 loaded coalesced into LDS, thread 0 adds them
+// 16 at a time.  `first` holds p[threadIdx.x] (0 past m), loaded by the
+// caller before its own values so that this wait does not include them.
+// sp: LDS double[257].
+__device__ double sequential_total(const double* __restrict__ p, uint64_t m, double first, double* sp) {
     double total = 0.0;
-    for (uint64_t g0 = 0; g0 < groups; g0 += 128) {
-        const uint32_t n = uint32_t(groups - g0 < 128 ? groups - g0 : 128);
-        if (part && tid < n) {
-            const uint64_t c0 = (g0 + tid) * NORM_GROUP;
-            const uint32_t m = uint32_t(chunks - c0 < NORM_GROUP ? chunks - c0 : NORM_GROUP);
-            double x[NORM_GROUP];
-#pragma unroll
-            for (uint32_t c = 0; c < NORM_GROUP; ++c) x[c] = c < m ? part[c0 + c] : 0.0;
-            double v = 0.0;
-#pragma unroll
-            for (uint32_t c = 0; c < NORM_GROUP; ++c)
-                if (c < m) v += x[c];
-            g[tid] = v;
-        }
+#pragma unroll 1
+    for (uint64_t c0 = 0; c0 < m; c0 += 256) {
+        const uint32_t k = uint32_t(m - c0 < 256 ? m - c0 : 256);
+        if (threadIdx.x < 256) sp[threadIdx.x] = c0 == 0 ? first : (threadIdx.x < k ? p[c0 + threadIdx.x] : 0.0);
         __syncthreads();
-        if (part && tid == 0) {
-            for (uint32_t j0 = 0; j0 < n; j0 += 16) {
+        if (threadIdx.x == 0) {
+#pragma unroll 1
+            for (uint32_t j0 = 0; j0 < k; j0 += 16) {
                 double y[16];
 #pragma unroll
-                for (uint32_t j = 0; j < 16; ++j) y[j] = j0 + j < n ? g[j0 + j] : 0.0;
+                for (uint32_t j = 0; j < 16; j++) y[j] = sp[j0 + j];
+                if (j0 + 16 <= k) {
 #pragma unroll
-                for (uint32_t j = 0; j < 16; ++j)
-                    if (j0 + j < n) total += y[j];
+                    for (uint32_t j = 0; j < 16; j++) total += y[j];
+                } else {
+#pragma unroll
+                    for (uint32_t j = 0; j < 16; j++)
+                        if (j0 + j < k) total += y[j];
+                }
             }
-            g[128] = total;
+            sp[256] = total;
         }
         __syncthreads();
-        t0 = gs[128];
-        t1 = gs[129 + 128];
-        total = arr == 0 ? t0 : t1;
+        total = sp[256];
         __syncthreads();
     }
+    return total;
 }
-// Chunk partials (one wavefront per chunk, NORM_WAVE_CHUNKS chunks per
-// wavefront with their loads issued together), into out[chunk].  Pass 1
-// first forms the mean from the pass-0 partials in p0.
-constexpr uint32_t NORM_WAVE_CHUNKS = 4, NORM_WG_CHUNKS = 4 * NORM_WAVE_CHUNKS;
-__global__ __launch_bounds__(256) void norm_chunks_kernel(const float* __restrict__ a, uint64_t count,
-                                                          const double* __restrict__ p0, double* __restrict__ out,
-                                                          int pass) {
-    __shared__ double gs[2 * 129];
-    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
+// One pass over a[0, count): workgroup g sums chunks 64g..64g+63 (wavefront
+// w the four chunks from 64g + 4w, loads issued together), then thread 0
+// adds the 64 chunk partials in order into the pass's group partial g.
+// Pass 0 sums a; pass 1 first forms the mean from pass 0's group partials
+// (workgroup 0 stores it in stats[0]) and sums (a - mean)^2, and its last
+// workgroup stores inv in stats[1].  A16: a is 16-byte aligned (each lane's
+// four elements in one load).
+template <bool A16>
+__global__ __launch_bounds__(NORM_THREADS) void norm_pass_kernel(const float* __restrict__ a, uint64_t count,
+                                                                 double* __restrict__ part, float* __restrict__ stats,
+                                                                 float eps, int pass) {
+    __shared__ double sp[257];
+    __shared__ double s_chunk[NORM_GROUP];
+    __shared__ uint32_t s_last;
+    const uint64_t chunks = (count + CHUNK - 1) / CHUNK, groups = (chunks + NORM_GROUP - 1) / NORM_GROUP;
+    uint32_t* ticket = reinterpret_cast<uint32_t*>(part);
+    double* p0 = part + 1;
+    double* p1 = p0 + groups;
     const uint32_t w = threadIdx.x / 64, l = threadIdx.x % 64;
-    const uint64_t cb = uint64_t(blockIdx.x) * NORM_WG_CHUNKS + w;  // chunks cb + 4i
+    const double first = pass != 0 && threadIdx.x < groups ? p0[threadIdx.x] : 0.0;
+    const uint64_t c0 = uint64_t(blockIdx.x) * NORM_GROUP + NORM_WAVE_CHUNKS * w;
     float x[NORM_WAVE_CHUNKS][4];
 #pragma unroll
-    for (uint32_t i = 0; i < NORM_WAVE_CHUNKS; i++)
+    for (uint32_t i = 0; i < NORM_WAVE_CHUNKS; i++) {
+        const uint64_t e = (c0 + i) * CHUNK + 4 * l;
+        if (A16 && e + 3 < count) {
+            const float4 v4 = *reinterpret_cast<const float4*>(a + e);
+            x[i][0] = v4.x; x[i][1] = v4.y; x[i][2] = v4.z; x[i][3] = v4.w;
+        } else {
 #pragma unroll
-        for (uint32_t j = 0; j < 4; j++) {
-            const uint64_t e = (cb + 4 * i) * CHUNK + 4 * l + j;
-            x[i][j] = e < count ? a[e] : 0.0f;
+            for (uint32_t j = 0; j < 4; j++) x[i][j] = e + j < count ? a[e + j] : 0.0f;
         }
+    }
     float mean = 0.0f;
     if (pass != 0) {
-        double t0 = 0.0, t1 = 0.0;
-        norm_totals(p0, nullptr, chunks, gs, t0, t1);
-        mean = float(t0 / double(count));
+        mean = float(sequential_total(p0, groups, first, sp) / double(count));
+        if (blockIdx.x == 0 && threadIdx.x == 0) stats[0] = mean;
     }
 #pragma unroll
     for (uint32_t i = 0; i < NORM_WAVE_CHUNKS; i++) {
-        const uint64_t c = cb + 4 * i;
-        double v = 0.0;
+        const uint64_t e = (c0 + i) * CHUNK + 4 * l;
+        double s = 0.0;
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
-            if (c * CHUNK + 4 * l + j < count) {
+            if (e + j < count) {
                 if (pass == 0) {
-                    v += double(x[i][j]);
+                    s += double(x[i][j]);
                 } else {
                     const double d = double(x[i][j] - mean);
-                    v += d * d;
+                    s += d * d;
                 }
             }
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) v = v + __shfl_xor(v, off, 64);
-        if (l == 0 && c < chunks) out[c] = v;
+        s = chunk_tree(s);
+        if (l == 0) s_chunk[NORM_WAVE_CHUNKS * w + i] = s;
     }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint64_t cg = uint64_t(blockIdx.x) * NORM_GROUP;
+        const uint32_t k = uint32_t(chunks - cg < NORM_GROUP ? chunks - cg : NORM_GROUP);
+        double v = 0.0;
+#pragma unroll 1
+        for (uint32_t c = 0; c < NORM_GROUP; c += 16) {
+            double y[16];
+#pragma unroll
+            for (uint32_t j = 0; j < 16; j++) y[j] = s_chunk[c + j];
+            if (c + 16 <= k) {
+#pragma unroll
+                for (uint32_t j = 0; j < 16; j++) v += y[j];
+            } else {
+#pragma unroll
+                for (uint32_t j = 0; j < 16; j++)
+                    if (c + j < k) v += y[j];
+            }
+        }
+        if (pass == 0) {
+            p0[blockIdx.x] = v;
+        } else {
+            // the partial is released with the count; the workgroup that
+            // takes the last ticket acquires every other one's partial
+            p1[blockIdx.x] = v;
+            const uint32_t taken = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = taken == groups - 1;
+            if (s_last) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (pass == 0) return;
+    __syncthreads();
+    if (!s_last) return;
+    const double total = sequential_total(p1, groups, threadIdx.x < groups ? p1[threadIdx.x] : 0.0, sp);
+    if (threadIdx.x == 0) stats[1] = 1.0f / sqrt_f(float(total / double(count)) + eps);
 }
-// mean and 1/sqrt(var + eps) from both passes' partials, then the apply over
-// the workgroup's NORM_APPLY elements (loaded at once); workgroup 0 also
-// stores them in stats[0..1].
+// (a - mean) * inv over the workgroup's NORM_APPLY elements (loaded at
+// once), with (mean, inv) from stats.
 constexpr uint32_t NORM_APPLY = 4096;
-__global__ __launch_bounds__(256) void norm_rescale_kernel(float* __restrict__ a, uint64_t count,
-                                                           const double* __restrict__ p0,
-                                                           const double* __restrict__ p1,
-                                                           float* __restrict__ stats, float eps) {
-    __shared__ double gs[2 * 129];
-    const uint64_t chunks = (count + CHUNK - 1) / CHUNK;
+__global__ __launch_bounds__(256) void norm_apply_kernel(float* __restrict__ a, uint64_t count,
+                                                         const float* __restrict__ stats) {
     const uint64_t e0 = uint64_t(blockIdx.x) * NORM_APPLY;
     float x[NORM_APPLY / 256];
 #pragma unroll
@@ -313,14 +392,7 @@ __global__ __launch_bounds__(256) void norm_rescale_kernel(float* __restrict__ a
         const uint64_t i = e0 + threadIdx.x + 256 * j;
         x[j] = i < count ? a[i] : 0.0f;
     }
-    double t0 = 0.0, t1 = 0.0;
-    norm_totals(p0, p1, chunks, gs, t0, t1);
-    const float mean = float(t0 / double(count));
-    const float inv = 1.0f / sqrt_f(float(t1 / double(count)) + eps);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        stats[0] = mean;
-        stats[1] = inv;
-    }
+    const float mean = stats[0], inv = stats[1];
 #pragma unroll
     for (uint32_t j = 0; j < NORM_APPLY / 256; j++) {
         const uint64_t i = e0 + threadIdx.x + 256 * j;
@@ -500,13 +572,19 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
     }
 }
 
+// Row m's advantage, normalised on the fly when a.norm is set (ppo.hpp:139).
+__device__ __forceinline__ float row_advantage(const RowArgs& a, uint32_t m) {
+    const float adv = a.adv[m];
+    return a.norm ? (adv - a.norm[0]) * a.norm[1] : adv;
+}
 // Per-row objective (ppo.hpp:144-181): log-probability of the stored
 // action, clipped surrogate with its active branch, value loss, and the
 // derivatives of the minibatch-mean objective (scale = 1/b).  Writes rs[0..3]
 // = d mean, rs[4..7] = d log_std, rs[8..11] = the row's policy, value and
 // entropy terms and its ratio.
-__device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls, uint32_t m, const float (&mean)[4],
-                                              float value, float target, float scale, float (&dmean)[4], float* rs) {
+__device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls, uint32_t m, float adv,
+                                              const float (&mean)[4], float value, float target, float scale,
+                                              float (&dmean)[4], float* rs) {
     const float* act = a.actions + size_t(m) * 4;
     float logp = 0.0f;
 #pragma unroll
@@ -518,7 +596,6 @@ __device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls,
     const float raw = logp - a.old_logp[m];
     const float lr = clamp_f(raw, -20.0f, 20.0f);
     const float ratio = exp_f(lr);
-    const float adv = a.adv[m];
     const float clipped = clamp_f(ratio, 1.0f - a.clip, 1.0f + a.clip);
     const float chosen = min_f(ratio * adv, clipped * adv);
     const bool in_range = raw >= -20.0f && raw <= 20.0f;
@@ -561,6 +638,8 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
     const uint32_t n = n0 + t, m = live ? n : n0;
     float* P = a.part + size_t(blockIdx.x) * L::P_TOTAL;
     const float scale = 1.0f / max_f(float(a.b), 1.0f);
+    // read before the first barrier, stored back (live rows) after it
+    const float adv = row_advantage(a, m);
 
     // ---- critic: forward, value, dV (ppo.hpp:82-93, 176-180)
     chunk_forward<COBS>(a.co, a.critic_w1t, a.critic + C_B1, n0, a.b, s_u, s_h);
@@ -608,7 +687,8 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
     }
     float dmean[4];
     float* rs = s_u + t * RS;  // the forward's scratch is free now
-    row_objective(a, a.actor + L::LS, m, mean, value, target, scale, dmean, rs);
+    row_objective(a, a.actor + L::LS, m, adv, mean, value, target, scale, dmean, rs);
+    if (a.norm && live) a.adv_out[m] = adv;
     __syncthreads();
     {   // actor W2[q][k]: fma over rows; then b2, log_std and the metric sums
         const uint32_t q = t / HID, k = t % HID;
@@ -795,7 +875,9 @@ __global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
             const float mean[4] = {s_mv[t][0], s_mv[t][1], s_mv[t][2], s_mv[t][3]};
             const float value = s_mv[t][4], target = a.ret[mrow];
             float dmean[4];
-            row_objective(a, s_at + 5 * HID + 4, mrow, mean, value, target, scale, dmean, rs);
+            const float adv = row_advantage(a, mrow);
+            if (a.norm) a.adv_out[mrow] = adv;
+            row_objective(a, s_at + 5 * HID + 4, mrow, adv, mean, value, target, scale, dmean, rs);
             rs[12] = a.vcoef * (value - target) * scale;
         } else {
             for (uint32_t c = 0; c < 13; c++) rs[c] = 0.0f;
@@ -1033,39 +1115,56 @@ __global__ void metric_mean_kernel(const float* __restrict__ rows, float* __rest
 // ---------------------------------------------------------------- launchers
 extern "C" {
 
+namespace {
+bool gae_v4(const float* r, const float* v, const float* nv, const uint8_t* te, const uint8_t* tr, uint32_t n) {
+    return n % 4 == 0 && (reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(v) |
+                          reinterpret_cast<uintptr_t>(nv) | reinterpret_cast<uintptr_t>(te) |
+                          reinterpret_cast<uintptr_t>(tr)) % 16 == 0;
+}
+}  // namespace
+
 hipError_t ppo_launch_gae(const float* r, const float* v, const float* nv, const uint8_t* te, const uint8_t* tr,
                           float* adv, float* ret, uint32_t horizon, uint32_t n, float gamma, float lambda,
                           hipStream_t st) {
     if (n == 0 || horizon == 0) return hipSuccess;
     const dim3 grid((n + ppo::GAE_ENVS - 1) / ppo::GAE_ENVS);
     // 16-byte row loads when every row starts 16-byte aligned
-    const bool v4 = n % 4 == 0 && (reinterpret_cast<uintptr_t>(r) | reinterpret_cast<uintptr_t>(v) |
-                                   reinterpret_cast<uintptr_t>(nv) | reinterpret_cast<uintptr_t>(te) |
-                                   reinterpret_cast<uintptr_t>(tr)) % 16 == 0;
-    if (v4)
-        hipLaunchKernelGGL(ppo::gae_kernel<true>, grid, dim3(256), 0, st, r, v, nv, te, tr, adv, ret, horizon, n, gamma,
-                           lambda);
+    if (gae_v4(r, v, nv, te, tr, n))
+        hipLaunchKernelGGL(ppo::gae_kernel<true>, grid, dim3(256), 0, st, r, v, nv, te, tr, adv, ret, horizon, n,
+                           gamma, lambda);
     else
-        hipLaunchKernelGGL(ppo::gae_kernel<false>, grid, dim3(256), 0, st, r, v, nv, te, tr, adv, ret, horizon, n, gamma,
-                           lambda);
+        hipLaunchKernelGGL(ppo::gae_kernel<false>, grid, dim3(256), 0, st, r, v, nv, te, tr, adv, ret, horizon, n,
+                           gamma, lambda);
     return hipGetLastError();
 }
 
 // stats: device float[2] (mean, inv_std); part: device
-// double[ppo_normalize_part_words(count)] (both passes' chunk partials).
-hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st) {
+// double[ppo_normalize_part_words(count)] (the ticket, zero when allocated,
+// and both passes' group partials).  `apply` = 0 leaves the rescale to the
+// caller's consumers.
+hipError_t ppo_launch_normalize_stats(float* a, uint64_t count, double* part, float* stats, float eps, int apply,
+                                      hipStream_t st) {
     if (count == 0) return hipSuccess;
     const uint64_t chunks = (count + ppo::CHUNK - 1) / ppo::CHUNK;
-    const uint64_t wgs = (chunks + ppo::NORM_WG_CHUNKS - 1) / ppo::NORM_WG_CHUNKS;
+    const uint64_t groups = (chunks + ppo::NORM_GROUP - 1) / ppo::NORM_GROUP;
     const uint64_t applies = (count + ppo::NORM_APPLY - 1) / ppo::NORM_APPLY;
-    if (wgs > 0x7fffffffull || applies > 0x7fffffffull) return hipErrorInvalidValue;
-    double* p0 = part;
-    double* p1 = part + chunks;
-    hipLaunchKernelGGL(ppo::norm_chunks_kernel, dim3(uint32_t(wgs)), dim3(256), 0, st, a, count, p0, p0, 0);
-    hipLaunchKernelGGL(ppo::norm_chunks_kernel, dim3(uint32_t(wgs)), dim3(256), 0, st, a, count, p0, p1, 1);
-    hipLaunchKernelGGL(ppo::norm_rescale_kernel, dim3(uint32_t(applies)), dim3(256), 0, st, a, count, p0, p1, stats,
-                       eps);
+    if (groups > 0x7fffffffull || applies > 0x7fffffffull) return hipErrorInvalidValue;
+    const bool a16 = reinterpret_cast<uintptr_t>(a) % 16 == 0;
+    for (int pass = 0; pass < 2; pass++) {
+        if (a16)
+            hipLaunchKernelGGL(ppo::norm_pass_kernel<true>, dim3(uint32_t(groups)), dim3(ppo::NORM_THREADS), 0, st, a,
+                               count, part, stats, eps, pass);
+        else
+            hipLaunchKernelGGL(ppo::norm_pass_kernel<false>, dim3(uint32_t(groups)), dim3(ppo::NORM_THREADS), 0, st,
+                               a, count, part, stats, eps, pass);
+    }
+    if (apply)
+        hipLaunchKernelGGL(ppo::norm_apply_kernel, dim3(uint32_t(applies)), dim3(256), 0, st, a, count, stats);
     return hipGetLastError();
+}
+
+hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* stats, float eps, hipStream_t st) {
+    return ppo_launch_normalize_stats(a, count, part, stats, eps, 1, st);
 }
 
 // Actor input widths built: 181 (pooled observation) and 184 (with the

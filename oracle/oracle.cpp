@@ -18,8 +18,9 @@
  *     ppo.metal:497-519);
  *   - squared gradient norm: 256 strided partial sums, then a pairwise tree;
  *   - advantage mean/variance: double; within each 256-row chunk 64 slots
- *     of 4 sequential rows combined by an xor butterfly, chunk partials
- *     sequential within groups of 64 chunks, then over the groups.
+ *     of 4 sequential rows combined by a pairwise tree over adjacent slots,
+ *     chunk partials sequential within groups of 64 chunks, then over the
+ *     groups.
  * Build: g++ -O2 -fopenmp -ffp-contract=off (see oracle/Makefile).
  */
 #include <omp.h>
@@ -149,8 +150,11 @@ inline T grouped_sum(const std::vector<T>& part, size_t group) {
 }
 // Sum of f(a[i]) over one 256-element chunk in the canonical order: slot l
 // (0..63) adds elements 4l..4l+3 sequentially from 0.0, then six butterfly
-// levels s[l] = s[l] + s[l ^ off] for off = 32, 16, ..., 1 (a wavefront xor
+// levels s[l] = s[l] + s[l ^ off] for off = 1, 2, ..., 32 (a wavefront xor
 // reduction; every slot ends with the same value since + is commutative).
+// Adjacent slots pair first, so slots 8k..8k+7 (elements 32k..32k+31) form a
+// subtree after three levels and the chunk's sum is the pairwise tree
+// ((u0 + u1) + (u2 + u3)) + ((u4 + u5) + (u6 + u7)) of those eight subtrees.
 template <class F>
 inline double chunk_tree_sum(const float* a, size_t begin, size_t end, F f) {
     double s[64];
@@ -161,7 +165,7 @@ inline double chunk_tree_sum(const float* a, size_t begin, size_t end, F f) {
             if (i < end) s[l] += f(a[i]);
         }
     }
-    for (size_t off = 32; off > 0; off >>= 1) {
+    for (size_t off = 1; off < 64; off <<= 1) {
         double t[64];
         for (size_t l = 0; l < 64; ++l) t[l] = s[l] + s[l ^ off];
         for (size_t l = 0; l < 64; ++l) s[l] = t[l];

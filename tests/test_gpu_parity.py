@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from gpu_compare import ENV_BUFFERS, ROW_BUFFERS, compare, config, make_pair
-from mdnav import Sim, abi, ops
+from mdnav import PPOTrainer, Sim, abi, ops
 from oracle_lib import crazyflie, oracle, physics_fixture, ptr, raptor_fixture
 
 pytestmark = pytest.mark.gpu
@@ -123,7 +123,47 @@ def test_gae_and_normalize_operators():
     y = ops.normalize(x)
     z = x.copy()
     oracle().orc_normalize_advantages(ptr(z), len(z), np.float32(1e-8))
-    assert np.abs(y - z).max() <= 1e-6, np.abs(y - z).max()
+    assert np.array_equal(y, z), np.abs(y - z).max()
+
+
+@pytest.mark.parametrize("n,T,epochs,minibatch", [(512, 40, 2, 256), (2048, 136, 1, 1 << 20),
+                                                   (8192, 33, 2, 65536), (96, 20, 2, 1000)])
+def test_gae_normalize_in_update_bit_exact(n, T, epochs, minibatch):
+    """PPOTrainer::rollout_update's GAE and advantage normalisation
+    (ppo.hpp:108-140; main.mm:1327-1330) on synthetic rollouts equal the
+    oracle's bit for bit.  The update's first epoch rescales the rows as it
+    reads them and stores them back, so the advantages after the update are
+    the normalised ones: 512 envs (16 slices of 32 envs in plain order; 256-row
+    minibatches, two epochs), 2,048 envs over 136 ticks (two 128-tick tiles,
+    slices grouped by XCD; one minibatch of many chunks), 8,192 envs over 33
+    ticks (17 groups of 64 chunks, the last partial) and 96 envs (scalar row
+    loads; a partial last minibatch).  Two updates in a row on one trainer."""
+    say("case: GAE + normalisation in rollout_update, N=%d T=%d epochs=%d minibatch=%d" % (n, T, epochs, minibatch))
+    rng = np.random.default_rng(n + T)
+    R = n * T
+    sim = Sim(config(n=n, family=1), T, raptor=raptor_fixture()[0])
+    ppo = PPOTrainer(sim, epochs, minibatch)
+    try:
+        for it in range(2):
+            r = (rng.normal(0.2, 1.5, R) * rng.uniform(0.1, 2.0, R)).astype(np.float32)
+            v, nv = (rng.normal(0, 3, R).astype(np.float32) for _ in range(2))
+            te = (rng.random(R) < 0.04).astype(np.uint8)
+            tr = ((rng.random(R) < 0.03) & (te == 0)).astype(np.uint8)
+            for name, x in (("rewards", r), ("values", v), ("next_values", nv), ("terminated", te),
+                            ("truncated", tr)):
+                sim.set(name, x)
+            ppo.rollout_update(it)
+            sim.sync()
+            a_o, r_o = np.zeros(R, np.float32), np.zeros(R, np.float32)
+            oracle().orc_compute_gae(T, n, ptr(r), ptr(v), ptr(nv), ptr(te), ptr(tr), np.float32(.99),
+                                     np.float32(.95), ptr(a_o), ptr(r_o))
+            oracle().orc_normalize_advantages(ptr(a_o), R, np.float32(1e-8))
+            assert np.array_equal(sim.get("returns"), r_o), it
+            got = sim.get("advantages")
+            assert np.array_equal(got, a_o), (it, np.abs(got - a_o).max())
+    finally:
+        ppo.close()
+        sim.close()
 
 
 @pytest.mark.parametrize("lanes", [8, 16, 4])
