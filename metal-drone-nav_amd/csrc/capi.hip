@@ -86,6 +86,7 @@ struct MdnSim {
     uint32_t* run = nullptr;
     float* world = nullptr;
     float* sensors = nullptr;
+    float* pool_ring = nullptr;  // [N][8][80]
     float* poses = nullptr;
     float* commands = nullptr;
     float* raptor = nullptr;
@@ -123,7 +124,7 @@ struct MdnSim {
     size_t rows() const { return size_t(cfg.n) * horizon; }
     nav::RolloutArgs args(uint32_t count) const {
         nav::RolloutArgs a;
-        a.state = state; a.run = run; a.world = world; a.sensors = sensors; a.poses = poses; a.commands = commands;
+        a.state = state; a.run = run; a.world = world; a.sensors = sensors; a.pool_ring = pool_ring; a.poses = poses; a.commands = commands;
         a.raptor = raptor; a.actor = actor; a.actor_w1t = actor_w1t; a.critic = critic; a.critic_w1t = critic_w1t;
         a.camera = camera; a.cells = cells; a.obs = obs; a.co = co; a.nco = nco; a.actions = actions; a.logp = logp; a.values = values;
         a.rewards = rewards; a.next_values = next_values; a.terminated = terminated; a.truncated = truncated;
@@ -323,6 +324,7 @@ int mdn_sim_create(const MdnSimConfig* cfg, uint32_t horizon, const MdnRaptorWei
     guard(dev_alloc(&s->run, size_t(RUN_WORDS) * N));
     guard(dev_alloc(&s->world, size_t(WORLD_WORDS) * N));
     guard(dev_alloc(&s->sensors, size_t(N) * 8 * 320));
+    guard(dev_alloc(&s->pool_ring, size_t(N) * 8 * 80));
     guard(dev_alloc(&s->poses, size_t(N) * 96));
     guard(dev_alloc(&s->commands, size_t(N) * 32));
     guard(dev_alloc(&s->raptor, 2084));
@@ -391,7 +393,7 @@ void mdn_sim_destroy(MdnSim* s) {
     if (!s) return;
     if (s->stream) hipStreamSynchronize(s->stream);
     if (s->ppo) mdn_ppo_destroy(s->ppo);
-    void* bufs[] = {s->state, s->run, s->world, s->sensors, s->poses, s->commands, s->raptor, s->camera, s->cells,
+    void* bufs[] = {s->state, s->run, s->world, s->sensors, s->pool_ring, s->poses, s->commands, s->raptor, s->camera, s->cells,
                     s->pix_rays, s->mem_head, s->env_phys, s->task_states, s->task_cfg, s->bank_worlds,
                     s->bank_schedule, s->bank_active, s->bank_transition, s->validate_out,
                     s->actor, s->critic, s->actor_w1t, s->critic_w1t, s->obs, s->co, s->nco, s->actions, s->logp,

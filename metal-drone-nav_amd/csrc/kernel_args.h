@@ -13,6 +13,10 @@ struct RolloutArgs {
     uint32_t* run;         // [46][N]
     float* world;          // [N][169]
     float* sensors;        // [N][8][320]
+    // pooled 2x2 minima of the last K frames, slot f % K ([N][K][80]): the
+    // ring the four-wavefront kernels with K > 2 keep in HBM (their LDS has
+    // no room for it); rebuilt from `sensors` at every launch
+    float* pool_ring;
     float* poses;          // [N][8][12]
     float* commands;       // [N][8][4]
     const float* raptor;   // RaptorWeights, 2084 floats

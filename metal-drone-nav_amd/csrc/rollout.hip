@@ -651,7 +651,20 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     // Per-env rows have odd word strides so that the E groups of a wavefront,
     // reading the same offset of their own rows, fall in distinct banks.
     __shared__ float s_cent[E][49];
-    __shared__ float s_ring[E][K * POOL + 1];   // slot j at [j * POOL]
+    // Pooled ring: slot j of the group's env at pring(g)[j * POOL].  In LDS,
+    // except for the four-wavefront kernels with more than two slots, whose
+    // LDS has no room for it: theirs is the env's row of a.pool_ring (read
+    // back by the wavefront that wrote it, in program order).
+    constexpr bool RING_HBM = W > 1 && K > 2;
+    __shared__ float s_ring[E][RING_HBM ? 1 : K * POOL + 1];
+    auto pring = [&](uint32_t g) -> float* {
+        if constexpr (RING_HBM) {
+            const uint32_t ng = blockIdx.x * E + g;
+            return a.pool_ring + size_t(ng < N ? ng : 0) * K * POOL;
+        } else {
+            return s_ring[g];
+        }
+    };
     __shared__ float s_obs[E][OS];
     __shared__ float s_co[E][COBS + 1];
     __shared__ float s_ah[E][HID + 1];
@@ -684,7 +697,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             float m = 12.0f;
             for (uint32_t dy = 0; dy < 2; dy++)
                 for (uint32_t dx = 0; dx < 2; dx++) m = min_f(m, src[(y + dy) * 20 + x + dx]);
-            s_ring[grp][slotk * POOL + b] = m;
+            if (live) pring(grp)[slotk * POOL + b] = m;
         }
     }
     // this lane's RAPTOR units (hidden values it owns)
@@ -863,7 +876,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                                                     __builtin_amdgcn_update_dpp(0, int(float_bits(depth)), 0xB1, 0xF, 0xF, false))));
                     pooled = min_f(pooled, bits_float(uint32_t(
                                                __builtin_amdgcn_update_dpp(0, int(float_bits(pooled)), 0x4E, 0xF, 0xF, false))));
-                    if (q == 0) s_ring[ge][slotk * POOL + b] = pooled;
+                    if (q == 0) pring(ge)[slotk * POOL + b] = pooled;
                 }
             }
         } else if (depth_now) {
@@ -927,7 +940,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                         ring[k] = depth;
                         pooled = min_f(pooled, depth);
                     }
-                s_ring[grp][slotk * POOL + b] = pooled;
+                pring(grp)[slotk * POOL + b] = pooled;
             }
         }
         group_sync();
@@ -940,9 +953,10 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         float* og = a.obs + row * D;
         if (active && observe) {
             for (uint32_t b = lane; b < POOL; b += G) {
-                const float cur = have ? div_r(s_ring[grp][(frame % K) * POOL + b], 1.0 / 12.0) : 1.0f;
+                const float* rg = pring(grp);
+                const float cur = have ? div_r(rg[(frame % K) * POOL + b], 1.0 / 12.0) : 1.0f;
                 // mode 18 (sim.metal:211-213): evaluation without the previous frame
-                const float pre = C.mode == 18 ? cur : have ? div_r(s_ring[grp][(prev % K) * POOL + b], 1.0 / 12.0) : 1.0f;
+                const float pre = C.mode == 18 ? cur : have ? div_r(rg[(prev % K) * POOL + b], 1.0 / 12.0) : 1.0f;
                 s_obs[grp][b] = cur;
                 s_obs[grp][POOL + b] = pre;
                 og[b] = cur;
@@ -1378,7 +1392,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             for (int j = 0; j < U; j++) hu[j] = RW[2000 + lane + G * j];
             if constexpr (W > 1)
                 for (uint32_t c = lane; c < 16; c += G) s_rh[grp][c] = RW[2000 + c];
-            for (uint32_t i = lane; i < uint32_t(K) * POOL; i += G) s_ring[grp][i] = 12.0f;
+            for (uint32_t i = lane; i < uint32_t(K) * POOL; i += G) pring(grp)[i] = 12.0f;
             for (uint32_t i = lane; i < 32; i += G) {
                 s_cmd[grp][i] = 0.0f;
                 a.commands[size_t(nn) * 32 + i] = 0.0f;
@@ -1441,11 +1455,11 @@ hipError_t nav_launch_reset(const nav::RolloutArgs* a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Lanes per env G and LDS ring slots K are compile-time; K = sensor_delay+2
+// Lanes per env G and pooled ring slots K are compile-time; K = sensor_delay+2
 // rounded up to 2, 4 or 8.
-// The (8 lanes, 2 slots) case runs four wavefronts per workgroup with the
-// weights in LDS (32 envs, 159 KB of LDS, one workgroup per CU); the ring of
-// the other slot counts leaves no room for that, so they run one wavefront per
+// The 8-lane cases run four wavefronts per workgroup with the weights in LDS
+// (32 envs, one workgroup per CU); with 4 or 8 slots the pooled ring lives
+// in HBM (a.pool_ring).  16 and 4 lanes per env run one wavefront per
 // workgroup with the weights in L1/L2.
 // Split ticks (a->ext_means set) and 184-input actors are built for 8 lanes
 // per env only.
@@ -1462,12 +1476,12 @@ hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int 
     }
 #define NAV_ROLLOUT_CASE(G, K, W, X, D) NAV_ROLLOUT_CASE_DYN(G, K, W, X, D, false)
     constexpr uint32_t P = MDN_ACTOR_OBS_POOLED, H = MDN_ACTOR_OBS_PRIOR;
-    NAV_ROLLOUT_CASE(8, 2, 4, false, P) NAV_ROLLOUT_CASE(8, 4, 1, false, P) NAV_ROLLOUT_CASE(8, 8, 1, false, P)
+    NAV_ROLLOUT_CASE(8, 2, 4, false, P) NAV_ROLLOUT_CASE(8, 4, 4, false, P) NAV_ROLLOUT_CASE(8, 8, 4, false, P)
     NAV_ROLLOUT_CASE(16, 2, 1, false, P) NAV_ROLLOUT_CASE(16, 4, 1, false, P) NAV_ROLLOUT_CASE(16, 8, 1, false, P)
     NAV_ROLLOUT_CASE(4, 2, 1, false, P) NAV_ROLLOUT_CASE(4, 4, 1, false, P) NAV_ROLLOUT_CASE(4, 8, 1, false, P)
-    NAV_ROLLOUT_CASE(8, 2, 4, true, P) NAV_ROLLOUT_CASE(8, 4, 1, true, P) NAV_ROLLOUT_CASE(8, 8, 1, true, P)
-    NAV_ROLLOUT_CASE(8, 2, 4, false, H) NAV_ROLLOUT_CASE(8, 4, 1, false, H) NAV_ROLLOUT_CASE(8, 8, 1, false, H)
-    NAV_ROLLOUT_CASE(8, 2, 4, true, H) NAV_ROLLOUT_CASE(8, 4, 1, true, H) NAV_ROLLOUT_CASE(8, 8, 1, true, H)
+    NAV_ROLLOUT_CASE(8, 2, 4, true, P) NAV_ROLLOUT_CASE(8, 4, 4, true, P) NAV_ROLLOUT_CASE(8, 8, 4, true, P)
+    NAV_ROLLOUT_CASE(8, 2, 4, false, H) NAV_ROLLOUT_CASE(8, 4, 4, false, H) NAV_ROLLOUT_CASE(8, 8, 4, false, H)
+    NAV_ROLLOUT_CASE(8, 2, 4, true, H) NAV_ROLLOUT_CASE(8, 4, 4, true, H) NAV_ROLLOUT_CASE(8, 8, 4, true, H)
     // per-episode plants and navigation tasks: 8 lanes, the in-kernel policy,
     // one wavefront per workgroup (the per-env plant rows do not fit beside
     // the LDS-resident weights)
