@@ -424,6 +424,7 @@ __device__ __forceinline__ v16f mfma32(float a, float b, v16f c) {
 __device__ __forceinline__ uint32_t acc_row(uint32_t l, uint32_t r) { return 8 * (r / 4) + 4 * (l / 32) + (r % 4); }
 
 constexpr uint32_t HS = HID + 1;       // row stride of the [256][64] activation buffer
+constexpr uint32_t CHUNK_PF = 3;       // MFMA steps between an operand's LDS read and its use
 constexpr uint32_t XK = 16;            // forward: inputs per k-slab
 constexpr uint32_t XKS = XK + 1;       // stride of the forward row tile [256][16]
 constexpr uint32_t WKS = HID + 32;     // stride of the forward weight slab [16][64]
@@ -483,18 +484,28 @@ __device__ __forceinline__ void chunk_forward(const float* __restrict__ X, const
         for (uint32_t j = 0; j < XK * HID / 256; j++) sw[(t / HID + 4 * j) * WKS + t % HID] = f.w[j];
         __syncthreads();
         if (k0 + XK < D) fwd_load<D>(f, X, W1T, n0, b, k0 + XK);
-        const uint32_t cnt = D - k0 < XK ? D - k0 : XK;
-        for (uint32_t kk = 0; kk < cnt; kk += 2) {
-            const uint32_t kr = kk + l / 32;
-            float av[2], bv[2];
+        // every slab runs all XK inputs (columns past D hold x = +0 and
+        // w = -0, whose product -0 leaves each accumulator unchanged); each
+        // step's LDS operands are read CHUNK_PF steps ahead of its MFMAs
+        constexpr uint32_t NK = XK / 2;
+        float av[NK][2], bv[NK][2];
 #pragma unroll
-            for (uint32_t rt = 0; rt < 2; rt++) av[rt] = sx[(64 * wv + 32 * rt + l % 32) * XKS + kr];
+        for (uint32_t st = 0; st < NK + CHUNK_PF; st++) {
+            if (st < NK) {
+                const uint32_t kr = 2 * st + l / 32;
 #pragma unroll
-            for (uint32_t ct = 0; ct < 2; ct++) bv[ct] = sw[kr * WKS + 32 * ct + l % 32];
+                for (uint32_t rt = 0; rt < 2; rt++) av[st][rt] = sx[(64 * wv + 32 * rt + l % 32) * XKS + kr];
 #pragma unroll
-            for (uint32_t rt = 0; rt < 2; rt++)
+                for (uint32_t ct = 0; ct < 2; ct++) bv[st][ct] = sw[kr * WKS + 32 * ct + l % 32];
+            }
+            if (st >= CHUNK_PF) {
+                const uint32_t u = st - CHUNK_PF;
 #pragma unroll
-                for (uint32_t ct = 0; ct < 2; ct++) acc[rt][ct] = mfma32(av[rt], bv[ct], acc[rt][ct]);
+                for (uint32_t rt = 0; rt < 2; rt++)
+#pragma unroll
+                    for (uint32_t ct = 0; ct < 2; ct++) acc[rt][ct] = mfma32(av[u][rt], bv[u][ct], acc[rt][ct]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
         __syncthreads();
     }
@@ -549,15 +560,27 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
         __syncthreads();
         if (r0 + BR < rows) row_load<D, W>(f, X, n0, rows, r0 + BR);
         if (owner) {
-            const uint32_t steps = rows - r0 < BR ? rows - r0 : BR;
-            for (uint32_t k = 0; k < steps; k += 2) {
-                const uint32_t rr = k + l / 32;
+            // every slab runs all BR rows (rows past the chunk's hold
+            // deltas +0 and inputs -0: a -0 product, no change); each step's
+            // LDS operands are read CHUNK_PF steps ahead of its MFMAs
+            constexpr uint32_t NS = BR / 2;
+            float av[NS][T], bv[NS][T];
 #pragma unroll
-                for (uint32_t q = 0; q < T; q++) {
-                    const float av = s_h[(r0 + rr) * HS + 32 * jt[q] + l % 32];
-                    const float bv = sx[rr * WS + 32 * it[q] + l % 32];
-                    acc[q] = mfma32(av, bv, acc[q]);
+            for (uint32_t st = 0; st < NS + CHUNK_PF; st++) {
+                if (st < NS) {
+                    const uint32_t rr = 2 * st + l / 32;
+#pragma unroll
+                    for (uint32_t q = 0; q < T; q++) {
+                        av[st][q] = s_h[(r0 + rr) * HS + 32 * jt[q] + l % 32];
+                        bv[st][q] = sx[rr * WS + 32 * it[q] + l % 32];
+                    }
                 }
+                if (st >= CHUNK_PF) {
+                    const uint32_t u = st - CHUNK_PF;
+#pragma unroll
+                    for (uint32_t q = 0; q < T; q++) acc[q] = mfma32(av[u][q], bv[u][q], acc[q]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         __syncthreads();
