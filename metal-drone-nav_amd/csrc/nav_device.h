@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include "mdnav_math.h"
+#include "mdnav_plant.h"
 #include "mdnav_types.h"
 
 namespace nav {
@@ -683,6 +684,20 @@ __device__ __forceinline__ void guided_mode_means(uint32_t mode, const float* o,
 struct PhysRecip {
     double mass, rise[4], fall[4];
 };
+// The Crazyflie profile's reciprocals, RN64(1/x) as phys_recip forms them.
+constexpr PhysRecip kCrazyflieRecip = {
+    1.0 / double(mdn::kCrazyflie.mass),
+    {1.0 / double(mdn::kCrazyflie.rotor_time_constants_rising[0]), 1.0 / double(mdn::kCrazyflie.rotor_time_constants_rising[1]),
+     1.0 / double(mdn::kCrazyflie.rotor_time_constants_rising[2]), 1.0 / double(mdn::kCrazyflie.rotor_time_constants_rising[3])},
+    {1.0 / double(mdn::kCrazyflie.rotor_time_constants_falling[0]), 1.0 / double(mdn::kCrazyflie.rotor_time_constants_falling[1]),
+     1.0 / double(mdn::kCrazyflie.rotor_time_constants_falling[2]), 1.0 / double(mdn::kCrazyflie.rotor_time_constants_falling[3])}};
+// The plant a kernel instance reads: its LDS copy of the launch's plant, or
+// (CF) the Crazyflie profile as compile-time constants, which the compiler
+// folds into the physics instructions as immediates.
+template <bool CF>
+__device__ __forceinline__ const MdnPhysicsParams& plant_ref(const MdnPhysicsParams& lds) {
+    if constexpr (CF) return mdn::kCrazyflie; else return lds;
+}
 __device__ __forceinline__ PhysRecip phys_recip(const MdnPhysicsParams& P) {
     PhysRecip r;
     r.mass = 1.0 / double(P.mass);

@@ -587,21 +587,26 @@ struct WeightLds<1, D> {};
 // observation) or 184 (with the geometry-prior hint, ppo.hpp:30-34).
 // DYN: per-episode plants (a.env_phys) and navigation tasks (a.task_cfg);
 // launched one tick at a time around the episode kernel.
-template <int G, int K, int W, bool X, uint32_t D, bool DYN>
+// CF: the launch's plant is the Crazyflie profile (checked byte for byte on
+// the host), read as compile-time constants instead of from LDS.
+template <int G, int K, int W, bool X, uint32_t D, bool DYN, bool CF = false>
 __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     constexpr int E = 64 * W / G;    // envs per workgroup
     constexpr int U = 16 / G;        // RAPTOR units per lane
     constexpr int HU = 64 / G;       // actor/critic hidden units per lane
     const MdnSimConfig& C = a.cfg;
     __shared__ MdnPhysicsParams s_phys;
-    for (uint32_t i = threadIdx.x; i < sizeof(MdnPhysicsParams) / 4; i += 64 * W)
-        reinterpret_cast<float*>(&s_phys)[i] = reinterpret_cast<const float*>(&a.phys)[i];
+    if constexpr (!CF)
+        for (uint32_t i = threadIdx.x; i < sizeof(MdnPhysicsParams) / 4; i += 64 * W)
+            reinterpret_cast<float*>(&s_phys)[i] = reinterpret_cast<const float*>(&a.phys)[i];
     __syncthreads();
-    const MdnPhysicsParams& P = s_phys;
-    PhysRecip RP;
-    RP.mass = a.recip_mass;
+    const MdnPhysicsParams& P = plant_ref<CF>(s_phys);
+    PhysRecip RP = kCrazyflieRecip;
+    if constexpr (!CF) {
+        RP.mass = a.recip_mass;
 #pragma unroll
-    for (int i = 0; i < 4; i++) { RP.rise[i] = a.recip_rise[i]; RP.fall[i] = a.recip_fall[i]; }
+        for (int i = 0; i < 4; i++) { RP.rise[i] = a.recip_rise[i]; RP.fall[i] = a.recip_fall[i]; }
+    }
     const uint32_t N = C.n;
     const uint32_t lane = threadIdx.x % G, grp = threadIdx.x / G;
     const uint32_t n = blockIdx.x * E + grp;
@@ -1240,7 +1245,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 for (int q = 0; q < 4; q++) r.motors[q] = act[q];
                 State nx;
                 if constexpr (DYN) physics_step(EP, s_erp[grp], s, act, wind, nx);
-                else if (a.quad && !__any(!no_negative_zero(s))) physics_step<true>(P, RP, s, act, wm, nx);
+                else if ((CF || a.quad) && !__any(!no_negative_zero(s))) physics_step<true>(P, RP, s, act, wm, nx);
                 else physics_step(P, RP, s, act, wind, nx);
                 bool valid = true;
                 const float* nf = &nx.p[0];
@@ -1476,6 +1481,19 @@ hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int 
     }
 #define NAV_ROLLOUT_CASE(G, K, W, X, D) NAV_ROLLOUT_CASE_DYN(G, K, W, X, D, false)
     constexpr uint32_t P = MDN_ACTOR_OBS_POOLED, H = MDN_ACTOR_OBS_PRIOR;
+    // the Crazyflie plant as compile-time constants (the common plant of the
+    // fused 8-lane instances)
+    const bool cf = !dyn && std::memcmp(&a->phys, &mdn::kCrazyflie, sizeof(MdnPhysicsParams)) == 0;
+#define NAV_ROLLOUT_CASE_CF(G, K, W, X, D)                                                                     \
+    if (cf && lanes_per_env == G && ring_slots == K && (a->ext_means != nullptr) == X && actor_obs == D) {     \
+        const uint32_t blocks = (a->cfg.n + 64 * W / G - 1) / (64 * W / G);                                    \
+        hipLaunchKernelGGL((nav::rollout_kernel<G, K, W, X, D, false, true>), dim3(blocks), dim3(64 * W), 0,   \
+                           stream, *a);                                                                        \
+        return hipGetLastError();                                                                              \
+    }
+    NAV_ROLLOUT_CASE_CF(8, 2, 4, false, P) NAV_ROLLOUT_CASE_CF(8, 4, 4, false, P)
+    NAV_ROLLOUT_CASE_CF(8, 2, 4, false, H)
+#undef NAV_ROLLOUT_CASE_CF
     NAV_ROLLOUT_CASE(8, 2, 4, false, P) NAV_ROLLOUT_CASE(8, 4, 4, false, P) NAV_ROLLOUT_CASE(8, 8, 4, false, P)
     NAV_ROLLOUT_CASE(16, 2, 1, false, P) NAV_ROLLOUT_CASE(16, 4, 1, false, P) NAV_ROLLOUT_CASE(16, 8, 1, false, P)
     NAV_ROLLOUT_CASE(4, 2, 1, false, P) NAV_ROLLOUT_CASE(4, 4, 1, false, P) NAV_ROLLOUT_CASE(4, 8, 1, false, P)

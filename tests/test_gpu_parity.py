@@ -12,7 +12,7 @@ import pytest
 
 from gpu_compare import ENV_BUFFERS, ROW_BUFFERS, compare, config, make_pair
 from mdnav import PPOTrainer, Sim, abi, ops
-from oracle_lib import crazyflie, oracle, physics_fixture, ptr, raptor_fixture
+from oracle_lib import OracleTrainer, crazyflie, oracle, physics_fixture, ptr, raptor_fixture
 
 pytestmark = pytest.mark.gpu
 
@@ -179,6 +179,33 @@ def test_rollout_parity(lanes):
     bad = compare(sim, ora, ENV_BUFFERS + ROW_BUFFERS, tol=TOL)
     assert not bad, bad
     assert ora.get("runs")["episodes"].sum() > 0
+
+
+@pytest.mark.parametrize("plant", ["crazyflie", "heavier", "tilted_rotor"])
+def test_rollout_parity_plants(plant):
+    """The fused 8-lane kernel with the Crazyflie plant runs an instance whose
+    plant constants are compiled in; any other plant runs the instance that
+    reads the launch's plant (standard structure: `heavier`, 10 % more mass;
+    general derivative: `tilted_rotor`, rotor 0 thrust tilted)."""
+    say("case: rollout N=64 T=40 plant=%s" % plant)
+    p = crazyflie().copy()
+    if plant == "heavier":
+        p["mass"] = np.float32(p["mass"] * np.float32(1.1))
+    elif plant == "tilted_rotor":
+        p["rotor_thrust_directions"][:3] = np.array([0.05, 0.0, 0.99875], np.float32)
+    cfg = config(n=64, family=1, speed=1.0, distance=3.0, max_steps=25)
+    weights = raptor_fixture()[0]
+    sim = Sim(cfg, 40, raptor=weights, physics=p)
+    ora = OracleTrainer(cfg, 40, weights, physics=p)
+    try:
+        sim.collect()
+        sim.sync()
+        ora.collect()
+        bad = compare(sim, ora, ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
+        assert not bad, bad
+        assert ora.get("runs")["episodes"].sum() > 0
+    finally:
+        sim.close()
 
 
 @pytest.mark.parametrize("variant", ["delays_wind_noise", "eval", "movers3", "mixed6", "rehearsal13",
