@@ -106,8 +106,10 @@ constexpr float LN2_LO = 1.42860677e-06f;
 constexpr float LOG2E = 1.44269502f;
 
 MDN_HD float exp_f(float x) {
-    // straight-line: the special cases are selected at the end (no branches)
-    const float xc = (x == x) ? (x > 88.8f ? 88.8f : (x < -104.0f ? -104.0f : x)) : 0.0f;
+    // straight-line: the argument is clamped with min/max, the function
+    // evaluated, and the special cases selected at the end (no branches)
+    const bool nan = !(x == x);
+    const float xc = nan ? 0.0f : __builtin_fminf(__builtin_fmaxf(x, -104.0f), 88.8f);
     const float k = floor_f(xc * LOG2E + 0.5f);
     const float r = (xc - k * LN2_HI) - k * LN2_LO;
     float p = 1.98412698e-04f;      // 1/7!
@@ -119,11 +121,13 @@ MDN_HD float exp_f(float x) {
     p = p * r + 1.0f;
     p = p * r + 1.0f;
     const float v = ldexp_f(p, (int)k);
-    return !(x == x) ? x : (x > 88.8f ? inf_f() : (x < -104.0f ? 0.0f : v));
+    const float lo = x < -104.0f ? 0.0f : v;
+    const float hi = x > 88.8f ? inf_f() : lo;
+    return nan ? x : hi;
 }
 
-MDN_HD float expm1_f(float x) {
-    const float xc = (x == x) ? (x > 88.0f ? 88.0f : (x < -18.0f ? -18.0f : x)) : 0.0f;
+// expm1 of an argument already in [-18, 88] (not NaN)
+MDN_HD float expm1_core(float xc) {
     const float k = floor_f(xc * LOG2E + 0.5f);
     const float r = (xc - k * LN2_HI) - k * LN2_LO;
     float p = 2.48015873e-05f;      // 1/8!
@@ -135,8 +139,16 @@ MDN_HD float expm1_f(float x) {
     p = p * r + 0.5f;               // 1/2!
     const float em1 = r + (r * r) * p;
     const float scale = ldexp_f(1.0f, (int)k);
-    const float v = k == 0.0f ? em1 : scale * em1 + (scale - 1.0f);
-    return !(x == x) ? x : (x > 88.0f ? inf_f() : (x < -18.0f ? -1.0f : v));
+    const float big = scale * em1 + (scale - 1.0f);
+    return k == 0.0f ? em1 : big;
+}
+
+MDN_HD float expm1_f(float x) {
+    const bool nan = !(x == x);
+    const float v = expm1_core(nan ? 0.0f : __builtin_fminf(__builtin_fmaxf(x, -18.0f), 88.0f));
+    const float lo = x < -18.0f ? -1.0f : v;
+    const float hi = x > 88.0f ? inf_f() : lo;
+    return nan ? x : hi;
 }
 
 MDN_HD float log_f(float x) {
@@ -159,7 +171,11 @@ MDN_HD float log_f(float x) {
     const float lm = (2.0f * s) * p;
     const float ef = (float)e;
     const float v = ef * LN2_HI + (ef * LN2_LO + lm);
-    return !(x > 0.0f) ? (x == 0.0f ? -inf_f() : nan_f()) : (!isfinite_f(x) ? x : v);
+    // special cases as single selects (no branches): +-0 -> -inf, negative
+    // or NaN -> NaN, +inf -> +inf
+    const float fin = isfinite_f(x) ? v : x;
+    const float pos = x > 0.0f ? fin : nan_f();
+    return x == 0.0f ? -inf_f() : pos;
 }
 
 // Cephes pi/2 split: PIO2_1 + PIO2_2 + PIO2_3 = pi/2; k*PIO2_1 is exact.
@@ -189,9 +205,12 @@ MDN_HD float sin_f(float x) { float s, c; sincos_f(x, &s, &c); return s; }
 MDN_HD float cos_f(float x) { float s, c; sincos_f(x, &s, &c); return c; }
 
 MDN_HD float tanh_f(float x) {
+    // 2 min(|x|, 10) is inside expm1_core's range; NaN takes 0 and is
+    // selected out at the end
     const float a = fabs_f(x);
-    const float e = expm1_f(2.0f * (a > 10.0f ? 10.0f : a));
-    const float t = a > 10.0f ? 1.0f : e / (e + 2.0f);
+    const float e = expm1_core(2.0f * (a == a ? __builtin_fminf(a, 10.0f) : 0.0f));
+    const float q = e / (e + 2.0f);
+    const float t = a > 10.0f ? 1.0f : q;
     const float v = x < 0.0f ? -t : t;
     return !(a == a) ? x : v;
 }

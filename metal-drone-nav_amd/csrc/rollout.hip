@@ -528,7 +528,12 @@ __device__ __forceinline__ void raptor_wave(const float* RW, const RaptorRegs& o
         }
 #pragma unroll
         for (uint32_t p = 0; p < 2; p++) {
-            const float iv = lo ? ci[p] : ci[2 + p], hv = lo ? ch[p] : ch[2 + p];
+            // rows p and 2 + p as two fixed registers and one select each (an
+            // empty asm keeps the compiler from turning the pair into a
+            // lane-dependent row index, which it expands to a compare chain)
+            float i0 = ci[p], i2 = ci[2 + p], h0 = ch[p], h2 = ch[2 + p];
+            asm volatile("" : "+v"(i0), "+v"(i2), "+v"(h0), "+v"(h2));
+            const float iv = lo ? i0 : i2, hv = lo ? h0 : h2;
             if (g == 0) {
                 reset[p] = sigmoid_f(iv + hv);
             } else if (g == 1) {
