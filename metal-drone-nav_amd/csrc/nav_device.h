@@ -259,6 +259,18 @@ __device__ __forceinline__ float recip_rn(float d) {
     const float y = __builtin_amdgcn_rcpf(d);
     return __builtin_fmaf(__builtin_fmaf(-d, y, 1.0f), y, y);
 }
+// Depth along d (every component at least the slab epsilon in magnitude)
+// through an env's slab table: the room (row 0) and the boxes whose bits are
+// set in the wavefront-uniform strip mask m (row i + 1 for bit i); the
+// minimum of hit values, as cast_ray forms it for a boxes-only world.
+__device__ __forceinline__ float strip_depth(const float (&SA)[9][3], const float (&SB)[9][3], V d, uint32_t m) {
+    const float inv[3] = {recip_rn(d.x), recip_rn(d.y), recip_rn(d.z)};
+    float best = __builtin_fminf(12.0f, slab_fast(SA[0], SB[0], inv));
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        if ((m >> i) & 1u) best = __builtin_fminf(best, slab_fast(SA[i + 1], SB[i + 1], inv));
+    return fmax_f(0.0f, best);
+}
 // Fast path of cast_ray for worlds of up to 16 boxes, 8 spheres (kinds 1 and
 // 3) and 8 capped cylinders when no ray direction component is below the slab
 // epsilon.  Per env and frame the obstacles are tabulated in the env's LDS

@@ -846,47 +846,49 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 const float noise = clean_env(C, ne) ? 0.0f : C.depth_noise;
                 const float drop = clean_env(C, ne) ? 0.0f : C.dropout;
                 float* ring = a.sensors + (size_t(ne) * 8 + slot8) * PIX;
-                // camera ray of the next strip read one strip ahead
                 const uint32_t by = jb / 2, k0 = (2 * by + q / 2) * 20 + 2 * (jb % 2) + q % 2;
-                float nrx = CAM[3 * k0], nry = CAM[3 * k0 + 1], nrz = CAM[3 * k0 + 2];
-#pragma unroll 1
+                // the five strips unrolled: no loop branches, and each strip's
+                // camera ray is loaded ahead of the strips before it
+                float dep[5];
+#pragma unroll
                 for (uint32_t st = 0; st < 5; st++) {
-                    const uint32_t bx = 2 * st + jb % 2;
-                    const uint32_t k = k0 + 4 * st, b = by * 10 + bx;
-                    const float rx = nrx, ry = nry, rz = nrz;
-                    if (st < 4) {
-                        nrx = CAM[3 * (k + 4)];
-                        nry = CAM[3 * (k + 4) + 1];
-                        nrz = CAM[3 * (k + 4) + 2];
-                    }
+                    const uint32_t k = k0 + 4 * st;
+                    const float rx = CAM[3 * k], ry = CAM[3 * k + 1], rz = CAM[3 * k + 2];
                     const V d = mk(ER[0] * rx + ER[1] * ry + ER[2] * rz, ER[3] * rx + ER[4] * ry + ER[5] * rz,
                                    ER[6] * rx + ER[7] * ry + ER[8] * rz);
                     const bool axes = (__builtin_fabsf(d.x) >= 1e-8f) & (__builtin_fabsf(d.y) >= 1e-8f) &
                                       (__builtin_fabsf(d.z) >= 1e-8f);
-                    float depth;
-                    if (axes) {
-                        const float inv[3] = {recip_rn(d.x), recip_rn(d.y), recip_rn(d.z)};
-                        float best = __builtin_fminf(12.0f, slab_fast(SA[0], SB[0], inv));
-                        const uint32_t m = st < 4 ? (w0 >> (8 * st)) & 0xffu : w1 & 0xffu;
-#pragma unroll
-                        for (int i = 0; i < 8; i++)
-                            if ((m >> i) & 1u) best = __builtin_fminf(best, slab_fast(SA[i + 1], SB[i + 1], inv));
-                        depth = fmax_f(0.0f, best);
+                    const uint32_t m = st < 4 ? (w0 >> (8 * st)) & 0xffu : w1 & 0xffu;
+                    // one wavefront-uniform branch: every lane's ray takes the
+                    // slab path unless some component is below the slab epsilon
+                    if (__builtin_expect(__all(axes), 1)) {
+                        dep[st] = strip_depth(SA, SB, d, m);
+                    } else if (axes) {
+                        dep[st] = strip_depth(SA, SB, d, m);
                     } else {
-                        depth = cast_ray(s_world[ge], s_cent[ge], count_e, eo, d);
+                        dep[st] = cast_ray(s_world[ge], s_cent[ge], count_e, eo, d);
                     }
-                    if (noise != 0 || drop != 0) {
-                        uint32_t nr = rng_e + k * 1664525u + steps_e * 1013904223u;
-                        depth = clamp_f(depth + noise * normal_draw(nr), 0.0f, 12.0f);
-                        if (ur(nr) < drop) depth = 12.0f;
+                }
+                if (noise != 0 || drop != 0) {
+#pragma unroll
+                    for (uint32_t st = 0; st < 5; st++) {
+                        uint32_t nr = rng_e + (k0 + 4 * st) * 1664525u + steps_e * 1013904223u;
+                        dep[st] = clamp_f(dep[st] + noise * normal_draw(nr), 0.0f, 12.0f);
+                        if (ur(nr) < drop) dep[st] = 12.0f;
                     }
-                    ring[k] = depth;
-                    // pooled 2x2 minimum over the quad's lanes (values in [0, 12], never NaN)
+                }
+#pragma unroll
+                for (uint32_t st = 0; st < 5; st++) {
+                    const float depth = dep[st];
+                    ring[k0 + 4 * st] = depth;
+                    // pooled 2x2 minimum over the quad's lanes (values in [0, 12],
+                    // never NaN); after the two swaps every lane of the quad holds
+                    // it, and all four store it (one value to one address)
                     float pooled = min_f(depth, bits_float(uint32_t(
                                                     __builtin_amdgcn_update_dpp(0, int(float_bits(depth)), 0xB1, 0xF, 0xF, false))));
                     pooled = min_f(pooled, bits_float(uint32_t(
                                                __builtin_amdgcn_update_dpp(0, int(float_bits(pooled)), 0x4E, 0xF, 0xF, false))));
-                    if (q == 0) pring(ge)[slotk * POOL + b] = pooled;
+                    pring(ge)[slotk * POOL + by * 10 + 2 * st + jb % 2] = pooled;
                 }
             }
         } else if (depth_now) {
