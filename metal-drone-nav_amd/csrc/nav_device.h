@@ -528,6 +528,24 @@ __device__ __forceinline__ float clearance_group(const float* world, uint32_t co
     return best;
 }
 
+// clearance_group for a group whose env has at most G obstacles, all boxes
+// (kind 0, fixed or at constant velocity): lane l holds obstacle l's record in
+// registers (`o`, valid when `mine`), so no LDS read sits on the substep's
+// dependency chain.  The same operations as room_clearance, obstacle_center
+// and obstacle_clearance for a box, and the same order-free minimum.
+template <int G>
+__device__ __forceinline__ float clearance_boxes(const float (&o)[10], bool mine, V p, float time) {
+    float best = room_clearance(p);
+    const V c = mk(o[1] + time * o[7], o[2] + time * o[8], o[3] + time * o[9]);
+    const V q = sub3(p, c);
+    const V k = mk(fabs_f(q.x) - o[4], fabs_f(q.y) - o[5], fabs_f(q.z) - o[6]);
+    const float distance = len3(mk(fmax_f(k.x, 0.0f), fmax_f(k.y, 0.0f), fmax_f(k.z, 0.0f))) +
+                           fmin_f(fmax_f(k.x, fmax_f(k.y, k.z)), 0.0f);
+    const float oc = distance - 0.18f;
+    best = mine ? fmin_f(best, oc) : best;
+    return group_min<G>(best);
+}
+
 // sim.metal:43-48
 __device__ __forceinline__ void rotation(const float q[4], float r[9]) {
     const float w = q[0], x = q[1], y = q[2], z = q[3];

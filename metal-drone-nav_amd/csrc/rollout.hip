@@ -754,12 +754,32 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         const bool observe = !SPLIT || t != 0 || !(a.split & SPLIT_BEGIN_AT_ACT);
         const uint32_t count = min(float_bits(world[160]), 16u);  // slots of WWorld
 
+        // this lane's obstacle record (slot `lane` of the world, in range for
+        // G <= 16) and whether every env of the wavefront can take the
+        // register-held box clearance this tick
+        float orec[10];
+#pragma unroll
+        for (int j = 0; j < 10; j++) orec[j] = world[10 * (lane % 16) + j];
+        const bool omine = lane < count;
+        const bool fastclr = __all(count <= uint32_t(G) && (!omine || float_bits(orec[0]) == 0u));
+        auto clearance = [&](V p, float time) {
+            return fastclr ? clearance_boxes<G>(orec, omine, p, time) : clearance_group<G>(world, count, p, time, lane);
+        };
+
         // ---- obstacle centres at the current time (world.hpp:32-41)
-        if (active && observe)
-            for (uint32_t i = lane; i < count; i += G) {
-                const V c = obstacle_center(world + 10 * i, r.elapsed);
-                s_cent[grp][3 * i] = c.x; s_cent[grp][3 * i + 1] = c.y; s_cent[grp][3 * i + 2] = c.z;
+        if (active && observe) {
+            if (count <= uint32_t(G)) {
+                if (omine) {
+                    const V c = obstacle_center(world + 10 * lane, r.elapsed);
+                    s_cent[grp][3 * lane] = c.x; s_cent[grp][3 * lane + 1] = c.y; s_cent[grp][3 * lane + 2] = c.z;
+                }
+            } else {
+                for (uint32_t i = lane; i < count; i += G) {
+                    const V c = obstacle_center(world + 10 * i, r.elapsed);
+                    s_cent[grp][3 * i] = c.x; s_cent[grp][3 * i + 1] = c.y; s_cent[grp][3 * i + 2] = c.z;
+                }
             }
+        }
         group_sync();
 
         // ---- depth (sim.metal:145-158)
@@ -796,12 +816,20 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             float* tbl = s_obs[grp];
             uint32_t vis0 = 0, vis1 = 0;  // strip masks, bit 8 st + box (strip 4 in vis1)
             if (depth_now) {
-                for (uint32_t i = lane; i < 9; i += G) {
+                {   // row 0, the room: the same values in every lane of the group
+                    float A[3], B[3];
+                    box_slab(world, s_cent[grp], 0, origin, A, B);
+#pragma unroll
+                    for (int j = 0; j < 3; j++) { tbl[j] = A[j]; tbl[3 + j] = B[j]; }
+                }
+                // rows 1-8, the boxes: lane l takes box l (rows of absent boxes
+                // are written and never read: their strip bits stay 0)
+                for (uint32_t i = lane + 1; i < 9; i += G) {
                     float A[3], B[3];
                     box_slab(world, s_cent[grp], i, origin, A, B);
 #pragma unroll
                     for (int j = 0; j < 3; j++) { tbl[6 * i + j] = A[j]; tbl[6 * i + 3 + j] = B[j]; }
-                    if (i >= 1 && i - 1 < count) {
+                    if (i - 1 < count) {
                         const uint32_t m = box_strips(A, B, R, a.tan_v);
                         for (uint32_t st = 0; st < 4; st++) vis0 |= ((m >> st) & 1u) << (8 * st + i - 1);
                         vis1 |= ((m >> 4) & 1u) << (i - 1);
@@ -809,14 +837,13 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 }
                 vis0 = group_or<G>(vis0);
                 vis1 = group_or<G>(vis1);
-                if (lane == 0) {
-                    tbl[BOX_TABLE_ORIGIN] = origin.x; tbl[BOX_TABLE_ORIGIN + 1] = origin.y;
-                    tbl[BOX_TABLE_ORIGIN + 2] = origin.z;
+                // equal values from every lane of the group
+                tbl[BOX_TABLE_ORIGIN] = origin.x; tbl[BOX_TABLE_ORIGIN + 1] = origin.y;
+                tbl[BOX_TABLE_ORIGIN + 2] = origin.z;
 #pragma unroll
-                    for (int j = 0; j < 9; j++) tbl[BOX_TABLE_ROT + j] = R[j];
-                    tbl[BOX_TABLE_STRIPS] = bits_float(vis0);
-                    tbl[BOX_TABLE_STRIPS + 1] = bits_float(vis1);
-                }
+                for (int j = 0; j < 9; j++) tbl[BOX_TABLE_ROT + j] = R[j];
+                tbl[BOX_TABLE_STRIPS] = bits_float(vis0);
+                tbl[BOX_TABLE_STRIPS + 1] = bits_float(vis1);
             }
             const uint64_t casting = __ballot(depth_now);
             group_sync();
@@ -1035,7 +1062,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
             cob[30] = world[166];
             cob[31] = world[167];
-            cob[19] = div_r(clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane), 1.0 / 5.0);
+            cob[19] = div_r(clearance(mk(s.p[0], s.p[1], s.p[2]), r.elapsed), 1.0 / 5.0);
             cob[20] = div_r(float(r.steps), 1.0 / 200.0);
 #pragma unroll
             for (uint32_t j = 0; j < 3; j++)
@@ -1266,7 +1293,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                     r.path += sqrt_f(ex * ex + ey * ey + ez * ez);
                     s = nx;
                     r.elapsed += P.dt;
-                    const float cl = clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane);
+                    const float cl = clearance(mk(s.p[0], s.p[1], s.p[2]), r.elapsed);
                     step_clearance = min_f(step_clearance, cl);
                     r.min_clearance = min_f(r.min_clearance, cl);
                     r.peak_speed = max_f(r.peak_speed, sqrt_f(s.v[0] * s.v[0] + s.v[1] * s.v[1] + s.v[2] * s.v[2]));
@@ -1324,7 +1351,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
             cob[30] = world[166];
             cob[31] = world[167];
-            cob[19] = div_r(clearance_group<G>(world, count, mk(s.p[0], s.p[1], s.p[2]), r.elapsed, lane), 1.0 / 5.0);
+            cob[19] = div_r(clearance(mk(s.p[0], s.p[1], s.p[2]), r.elapsed), 1.0 / 5.0);
             cob[20] = div_r(float(r.steps), 1.0 / 200.0);
 #pragma unroll
             for (uint32_t j = 0; j < 3; j++)
