@@ -196,13 +196,15 @@ __device__ __forceinline__ void box_slab(const float* world, const float* center
 // interval ends by about 1e-6 m (relative 2^-24 of distances under 20 m, and
 // of a rotation within 1e-6 of orthonormal), so such a box yields a miss or a
 // value of at least 12 for every ray of the strip, and leaving it out does
-// not change the depth.
+// not change the depth.  The mask depends only on comparisons of finite
+// values, so the hardware min/max (whose treatment of signed zeros differs
+// from fmin_f's) gives the same mask.
 __device__ __forceinline__ uint32_t box_strips(const float (&A)[3], const float (&B)[3], const float* R, float tan_v) {
     const float gap = 2e-3f;  // plane normals below have length <= 1.7
     float d2 = 0.0f;
 #pragma unroll
     for (int j = 0; j < 3; j++) {
-        const float c = fmin_f(fmax_f(0.0f, A[j]), B[j]);
+        const float c = __builtin_fminf(__builtin_fmaxf(0.0f, A[j]), B[j]);
         d2 += c * c;
     }
     if (d2 > 12.01f * 12.01f) return 0u;
@@ -211,7 +213,7 @@ __device__ __forceinline__ uint32_t box_strips(const float (&A)[3], const float 
     auto support = [&](const float (&n)[3]) {
         float m = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 3; j++) m += fmin_f(n[j] * A[j], n[j] * B[j]);
+        for (int j = 0; j < 3; j++) m += __builtin_fminf(n[j] * A[j], n[j] * B[j]);
         return m;
     };
     const float tv = 0.9375f * tan_v;  // |z| of the outer pixel rows

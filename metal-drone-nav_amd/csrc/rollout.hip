@@ -890,10 +890,14 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                     // slab path unless some component is below the slab epsilon
                     if (__builtin_expect(__all(axes), 1)) {
                         dep[st] = strip_depth(SA, SB, d, m);
-                    } else if (axes) {
-                        dep[st] = strip_depth(SA, SB, d, m);
                     } else {
-                        dep[st] = cast_ray(s_world[ge], s_cent[ge], count_e, eo, d);
+                        // rare: some ray component below the slab epsilon.  The
+                        // origin passes through an empty asm so that the generic
+                        // cast's per-env set-up stays here instead of being
+                        // hoisted into every env's cast
+                        V o2 = eo;
+                        asm volatile("" : "+v"(o2.x), "+v"(o2.y), "+v"(o2.z));
+                        dep[st] = axes ? strip_depth(SA, SB, d, m) : cast_ray(s_world[ge], s_cent[ge], count_e, o2, d);
                     }
                 }
                 if (noise != 0 || drop != 0) {
@@ -991,7 +995,10 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         const bool have = available >= sdelay;
         float* og = a.obs + row * D;
         if (active && observe) {
-            for (uint32_t b = lane; b < POOL; b += G) {
+            static_assert(POOL % G == 0, "whole pooled rows per lane");
+#pragma unroll
+            for (uint32_t bi = 0; bi < POOL / G; bi++) {
+                const uint32_t b = lane + G * bi;
                 const float* rg = pring(grp);
                 const float cur = have ? div_r(rg[(frame % K) * POOL + b], 1.0 / 12.0) : 1.0f;
                 // mode 18 (sim.metal:211-213): evaluation without the previous frame
