@@ -746,6 +746,9 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     }
     group_sync();
 
+    // whether some env of the workgroup was reset (or the launch is starting),
+    // so that the critic at s must be evaluated this tick
+    bool wg_reset = true;
     for (uint32_t t = 0; t < a.count; t++) {
         const uint32_t tick = SPLIT ? (a.tick0 + t) % a.horizon : t % a.horizon;
         const size_t row = size_t(tick) * N + nn;
@@ -1097,11 +1100,16 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             static_assert(E == 32, "matrix-core layers assume 32 envs per workgroup");
             __syncthreads();
             wg_layer<D, OS, HID + 1>(&s_obs[0][0], AW1, AT, &s_ah[0][0]);
-            wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
+            // When no env of the workgroup was reset at the end of the previous
+            // tick of this launch, every env's critic observation now is the
+            // one that tick evaluated as its next state (the same operations on
+            // the same state, time and step count), so the values it left in
+            // s_x[env][4] are this tick's values; else evaluate the critic.
+            if (wg_reset) wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
             __syncthreads();
             // heads: means (waves 0-1) and value (waves 2-3) into s_x[env][0..4]
             wg_head<4, HID + 1>(&s_ah[0][0], AT + HID, HID, AT + 5 * HID, 0, &s_x[0][0], 0);
-            wg_head<1, HID + 1>(&s_ch[0][0], CT + HID, 0, CT + 2 * HID, 2, &s_x[0][0], 4);
+            if (wg_reset) wg_head<1, HID + 1>(&s_ch[0][0], CT + HID, 0, CT + 2 * HID, 2, &s_x[0][0], 4);
             __syncthreads();
         } else if (active) {
             float acc[HU];
@@ -1386,7 +1394,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         if constexpr (X) {
             // next values are the caller's (from the stored next critic observations)
         } else if constexpr (W > 1) {  // next value: critic hidden of s' for all 32 envs
-            __syncthreads();
+            wg_reset = __syncthreads_or(ended) != 0;
             wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
             __syncthreads();
             wg_head<1, HID + 1>(&s_ch[0][0], CT + HID, 0, CT + 2 * HID, 0, &s_x[0][0], 4);
