@@ -30,6 +30,11 @@ __device__ __forceinline__ void group_sync() {
 }
 
 __device__ __forceinline__ float fbits(uint32_t u) { return bits_float(u); }
+// lane Q of this lane's quad (DPP quad_perm [Q,Q,Q,Q])
+template <int Q>
+__device__ __forceinline__ float quad_bcast(float x) {
+    return bits_float(uint32_t(__builtin_amdgcn_update_dpp(0, int(float_bits(x)), 0x55 * Q, 0xF, 0xF, false)));
+}
 __device__ __forceinline__ uint32_t ubits(float f) { return float_bits(f); }
 
 // RAPTOR step over a group of G lanes (raptor.hpp:52-97): lane `lane` owns
@@ -1172,31 +1177,54 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 // deployed mode-17 map of the sample (log-probability of the raw one)
                 if (C.mode == 22) deployed = 0.25f + 0.75f * (overhead_cells(s_obs[grp]) / 20.0f);
             }
-            uint32_t rng = r.rng;
-            float lp = 0, act[4];
+            // The four actions are drawn in parallel: lane j of each quad
+            // takes action j from the stream state the sequential draw would
+            // have reached (each action draws one normal, two xorshift steps,
+            // in the sampling modes), and the quad exchanges the results.
+            const bool draws = C.mode == 0 || C.mode == 22 || C.mode == 1;
+            uint32_t rs[5];
+            rs[0] = r.rng;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float ls = X ? a.ext_log_std[j] : AT[5 * HID + 4 + j];
-                float sd, isd;
-                if constexpr (W > 1 && !X) {
-                    sd = s_wt.pol[ACTOR_TAIL + CRITIC_TAIL + j];
-                    isd = s_wt.pol[ACTOR_TAIL + CRITIC_TAIL + 4 + j];
-                } else {
-                    sd = exp_f(ls);
-                    isd = exp_f(-ls);
-                }
-                act[j] = mean[j] + ((C.mode == 0 || C.mode == 22) ? sd * normal_draw(rng) : 0.0f);
-                if (C.mode == 1) act[j] = normal_draw(rng);
-                const float diff = (act[j] - mean[j]) * isd;
-                lp += -0.5f * (diff * diff + 2 * ls + LOG_TWO_PI);
-                float executed = act[j];
-                if (D == MDN_ACTOR_OBS_PRIOR && C.mode == 22) {
-                    const float prior = s_obs[grp][D - 3 + (j < 3 ? j : 0)];
-                    executed = j < 3 ? prior + deployed * (act[j] - prior) : deployed * act[j];
-                }
-                a_cmd[j] = tanh_f(executed);
+            for (int q = 1; q < 5; q++) {
+                uint32_t x = rs[q - 1];
+                xs(x);
+                xs(x);
+                rs[q] = draws ? x : rs[q - 1];
             }
-            r.rng = rng;
+            static_assert(G % 4 == 0, "whole quads per lane group");
+            const uint32_t jl = lane % 4;
+            uint32_t rng = jl == 0 ? rs[0] : jl == 1 ? rs[1] : jl == 2 ? rs[2] : rs[3];
+            const float mj = jl == 0 ? mean[0] : jl == 1 ? mean[1] : jl == 2 ? mean[2] : mean[3];
+            const float ls = X ? a.ext_log_std[jl] : AT[5 * HID + 4 + jl];
+            float sd, isd;
+            if constexpr (W > 1 && !X) {
+                sd = s_wt.pol[ACTOR_TAIL + CRITIC_TAIL + jl];
+                isd = s_wt.pol[ACTOR_TAIL + CRITIC_TAIL + 4 + jl];
+            } else {
+                sd = exp_f(ls);
+                isd = exp_f(-ls);
+            }
+            float actj = mj + ((C.mode == 0 || C.mode == 22) ? sd * normal_draw(rng) : 0.0f);
+            if (C.mode == 1) actj = normal_draw(rng);
+            const float diff = (actj - mj) * isd;
+            const float term = -0.5f * (diff * diff + 2 * ls + LOG_TWO_PI);
+            float executed = actj;
+            if (D == MDN_ACTOR_OBS_PRIOR && C.mode == 22) {
+                const float prior = s_obs[grp][D - 3 + (jl < 3 ? jl : 0)];
+                executed = jl < 3 ? prior + deployed * (actj - prior) : deployed * actj;
+            }
+            const float cmdj = tanh_f(executed);
+            // quad broadcasts (DPP quad_perm [q,q,q,q]); log-probability terms
+            // summed in action order, as the sequential loop does
+            float lp = 0;
+            const float act[4] = {quad_bcast<0>(actj), quad_bcast<1>(actj), quad_bcast<2>(actj), quad_bcast<3>(actj)};
+            a_cmd[0] = quad_bcast<0>(cmdj); a_cmd[1] = quad_bcast<1>(cmdj);
+            a_cmd[2] = quad_bcast<2>(cmdj); a_cmd[3] = quad_bcast<3>(cmdj);
+            lp += quad_bcast<0>(term);
+            lp += quad_bcast<1>(term);
+            lp += quad_bcast<2>(term);
+            lp += quad_bcast<3>(term);
+            r.rng = rs[4];
             if (C.mode == 2 || C.mode == 3 || C.mode == 20) {  // sim.metal:257-262
                 float dd[3] = {world[163] - s.p[0], world[164] - s.p[1], world[165] - s.p[2]};
                 const float ln = sqrt_f(dd[0] * dd[0] + dd[1] * dd[1] + dd[2] * dd[2]);
