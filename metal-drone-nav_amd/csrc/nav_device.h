@@ -535,17 +535,27 @@ __device__ __forceinline__ float clearance_group(const float* world, uint32_t co
 // registers (`o`, valid when `mine`), so no LDS read sits on the substep's
 // dependency chain.  The same operations as room_clearance, obstacle_center
 // and obstacle_clearance for a box, and the same order-free minimum.
+// For a finite point no operand here is NaN, and no minimum or maximum sees a
+// -0 whose sign could reach the result (the box terms are sums that cancel to
+// +0 and every clearance ends in x - 0.18f), so the hardware min/max give
+// fmin_f's and fmax_f's values.
 template <int G>
 __device__ __forceinline__ float clearance_boxes(const float (&o)[10], bool mine, V p, float time) {
-    float best = room_clearance(p);
+    float best = __builtin_fminf(__builtin_fminf(p.x + 2, 14 - p.x),
+                                 __builtin_fminf(__builtin_fminf(p.y + 5, 5 - p.y), __builtin_fminf(p.z, 5 - p.z))) -
+                 0.18f;
     const V c = mk(o[1] + time * o[7], o[2] + time * o[8], o[3] + time * o[9]);
     const V q = sub3(p, c);
     const V k = mk(fabs_f(q.x) - o[4], fabs_f(q.y) - o[5], fabs_f(q.z) - o[6]);
-    const float distance = len3(mk(fmax_f(k.x, 0.0f), fmax_f(k.y, 0.0f), fmax_f(k.z, 0.0f))) +
-                           fmin_f(fmax_f(k.x, fmax_f(k.y, k.z)), 0.0f);
+    const float distance = len3(mk(__builtin_fmaxf(k.x, 0.0f), __builtin_fmaxf(k.y, 0.0f), __builtin_fmaxf(k.z, 0.0f))) +
+                           __builtin_fminf(__builtin_fmaxf(k.x, __builtin_fmaxf(k.y, k.z)), 0.0f);
     const float oc = distance - 0.18f;
-    best = mine ? fmin_f(best, oc) : best;
-    return group_min<G>(best);
+    best = mine ? __builtin_fminf(best, oc) : best;
+    if constexpr (G > 1) best = __builtin_fminf(best, bits_float(group_swap<0>(float_bits(best))));
+    if constexpr (G > 2) best = __builtin_fminf(best, bits_float(group_swap<1>(float_bits(best))));
+    if constexpr (G > 4) best = __builtin_fminf(best, bits_float(group_swap<2>(float_bits(best))));
+    if constexpr (G > 8) best = __builtin_fminf(best, bits_float(group_swap<3>(float_bits(best))));
+    return best;
 }
 
 // sim.metal:43-48
@@ -914,7 +924,7 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const Ph
         float* a = &acc.p[0];
         const float* b = &k.p[0];
 #pragma unroll
-        for (int i = 0; i < 17; ++i) a[i] = a[i] + 2.0f * b[i];
+        for (int i = 0; i < 17; ++i) a[i] = fma_f(2.0f, b[i], a[i]);  // = a + 2b: 2b is exact
     }
     if constexpr (QUAD) derivative_quad(P, RP, tmp, sp, wind, k); else derivative(P, RP, tmp, sp, wind, k);
     axpy_state(s, k, P.dt, tmp);
@@ -922,7 +932,7 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const Ph
         float* a = &acc.p[0];
         const float* b = &k.p[0];
 #pragma unroll
-        for (int i = 0; i < 17; ++i) a[i] = a[i] + 2.0f * b[i];
+        for (int i = 0; i < 17; ++i) a[i] = fma_f(2.0f, b[i], a[i]);  // = a + 2b: 2b is exact
     }
     if constexpr (QUAD) derivative_quad(P, RP, tmp, sp, wind, k); else derivative(P, RP, tmp, sp, wind, k);
     const float* a0 = &s.p[0];
