@@ -277,6 +277,8 @@ def main():
                          "tasks of family 12 with per-episode plants at amplitude 1, mode 22, guided actor with the "
                          "geometry memory, one tick per launch with the per-episode kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-reference-schedule", action="store_true",
+                    help="skip the reference-schedule line (its thousands of small launches; for counter passes)")
     ap.add_argument("--workload", choices=["small", "large", "stress", "threats"], default="small",
                     help="small: 8,192 envs x 128 ticks, 181-64-4 actor (the headline metric); large: 8,192 envs x "
                          "256 ticks, 184-5120-4 actor (967,688 parameters) and 32-5120-1 critic on bf16 matrix cores, "
@@ -432,7 +434,7 @@ def main():
         "mfma_util": mfma_util(("rollout_kernel", "chunk_kernel")) if headline else {},
         "gpu_seconds": round(gpu_s, 4),
     }
-    if headline:
+    if headline and not args.no_reference_schedule:
         log("bench: reference schedule")
         out["reference_schedule"] = reference_schedule()
     if not args.no_cpu_baseline:
