@@ -1292,6 +1292,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         // the standard-structure derivative takes wind / mass, the same
         // division physics.hpp:101 repeats in every derivative evaluation
         const float wm[3] = {div_r(wind[0], RP.mass), div_r(wind[1], RP.mass), div_r(wind[2], RP.mass)};
+        bool nzero = no_negative_zero(s);  // no component of s is -0 (derivative_quad's condition)
         for (uint32_t step = 0; step < C.substeps; step++) {
             float mo[22] = {0};
             if (!done) {
@@ -1322,12 +1323,19 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 for (int q = 0; q < 4; q++) r.motors[q] = act[q];
                 State nx;
                 if constexpr (DYN) physics_step(EP, s_erp[grp], s, act, wind, nx);
-                else if ((CF || a.quad) && !__any(!no_negative_zero(s))) physics_step<true>(P, RP, s, act, wm, nx);
+                else if ((CF || a.quad) && !__any(!nzero)) physics_step<true>(P, RP, s, act, wm, nx);
                 else physics_step(P, RP, s, act, wind, nx);
-                bool valid = true;
+                // every component finite (isfinite_f) and none -0, in integer
+                // form: the largest exponent field and the smallest bits ^ sign
                 const float* nf = &nx.p[0];
+                uint32_t emax = 0u, zmin = 0xffffffffu;
 #pragma unroll
-                for (int j = 0; j < 17; j++) valid = valid && isfinite_f(nf[j]);
+                for (int j = 0; j < 17; j++) {
+                    const uint32_t u = float_bits(nf[j]);
+                    emax = max(emax, u & 0x7f800000u);
+                    zmin = min(zmin, u ^ 0x80000000u);
+                }
+                const bool valid = emax != 0x7f800000u;
                 if (!valid) {
                     collision = true;
                     done = true;
@@ -1335,6 +1343,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                     const float ex = s.p[0] - nx.p[0], ey = s.p[1] - nx.p[1], ez = s.p[2] - nx.p[2];
                     r.path += sqrt_f(ex * ex + ey * ey + ez * ez);
                     s = nx;
+                    nzero = zmin != 0u;
                     r.elapsed += P.dt;
                     const float cl = clearance(mk(s.p[0], s.p[1], s.p[2]), r.elapsed);
                     step_clearance = min_f(step_clearance, cl);
