@@ -907,9 +907,10 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const Ph
     const float half = (P.action_max - P.action_min) * 0.5f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        float a = action[i];
-        if (a < -1.0f) a = -1.0f;
-        if (a > 1.0f) a = 1.0f;
+        // the clamps to nonzero bounds as a median of three: for a non-NaN
+        // value it is the comparisons' result, -0 included (a NaN state is
+        // rejected by the caller's validity check either way)
+        const float a = __builtin_amdgcn_fmed3f(action[i], -1.0f, 1.0f);
         sp[i] = a * half + P.action_min + half;
     }
     // k1 + 2 k2 + 2 k3 + k4 accumulated left to right as it is written in
@@ -947,12 +948,9 @@ __device__ __forceinline__ void physics_step(const MdnPhysicsParams& P, const Ph
     for (int i = 0; i < 4; ++i) next.q[i] = div_r(next.q[i], inv_norm);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
-        if (next.p[i] < -P.position_limit) next.p[i] = -P.position_limit;
-        if (next.p[i] > P.position_limit) next.p[i] = P.position_limit;
-        if (next.v[i] < -P.velocity_limit) next.v[i] = -P.velocity_limit;
-        if (next.v[i] > P.velocity_limit) next.v[i] = P.velocity_limit;
-        if (next.w[i] < -P.angular_velocity_limit) next.w[i] = -P.angular_velocity_limit;
-        if (next.w[i] > P.angular_velocity_limit) next.w[i] = P.angular_velocity_limit;
+        next.p[i] = __builtin_amdgcn_fmed3f(next.p[i], -P.position_limit, P.position_limit);
+        next.v[i] = __builtin_amdgcn_fmed3f(next.v[i], -P.velocity_limit, P.velocity_limit);
+        next.w[i] = __builtin_amdgcn_fmed3f(next.w[i], -P.angular_velocity_limit, P.angular_velocity_limit);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

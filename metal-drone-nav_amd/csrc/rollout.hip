@@ -1300,15 +1300,16 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 r.ref_pos[0] += v0 * P.dt; r.ref_pos[1] += v1 * P.dt; r.ref_pos[2] += v2 * P.dt;
                 const float dp0 = s.p[0] - r.ref_pos[0], dp1 = s.p[1] - r.ref_pos[1], dp2 = s.p[2] - r.ref_pos[2];
                 const float dv0 = s.v[0] - v0, dv1 = s.v[1] - v1, dv2 = s.v[2] - v2;
-                mo[0] = clamp_f(c * dp0 + si * dp1, -.5f, .5f);
-                mo[1] = clamp_f(-si * dp0 + c * dp1, -.5f, .5f);
-                mo[2] = clamp_f(dp2, -.5f, .5f);
+                // clamps to nonzero bounds of finite values: the median of three
+                mo[0] = __builtin_amdgcn_fmed3f(c * dp0 + si * dp1, -.5f, .5f);
+                mo[1] = __builtin_amdgcn_fmed3f(-si * dp0 + c * dp1, -.5f, .5f);
+                mo[2] = __builtin_amdgcn_fmed3f(dp2, -.5f, .5f);
                 const float q[4] = {ch * s.q[0] + sh * s.q[3], ch * s.q[1] + sh * s.q[2], ch * s.q[2] - sh * s.q[1],
                                     ch * s.q[3] - sh * s.q[0]};
                 rotation(q, mo + 3);
-                mo[12] = clamp_f(c * dv0 + si * dv1, -1.0f, 1.0f);
-                mo[13] = clamp_f(-si * dv0 + c * dv1, -1.0f, 1.0f);
-                mo[14] = clamp_f(dv2, -1.0f, 1.0f);
+                mo[12] = __builtin_amdgcn_fmed3f(c * dv0 + si * dv1, -1.0f, 1.0f);
+                mo[13] = __builtin_amdgcn_fmed3f(-si * dv0 + c * dv1, -1.0f, 1.0f);
+                mo[14] = __builtin_amdgcn_fmed3f(dv2, -1.0f, 1.0f);
                 mo[15] = s.w[0]; mo[16] = s.w[1]; mo[17] = s.w[2];
 #pragma unroll
                 for (int j = 0; j < 4; j++) mo[18 + j] = r.motors[j];
