@@ -74,7 +74,7 @@ MDN_HD float sqrt_f(float x) {
 // also exactly what the fp32 matrix-core instructions compute.
 MDN_HD float fma_f(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
-MDN_HD float fabs_f(float x) { return x < 0.0f ? -x : (x == 0.0f ? 0.0f : x); }
+MDN_HD float fabs_f(float x) { return __builtin_fabsf(x); }  // the sign bit cleared
 
 MDN_HD uint32_t float_bits(float x) {
     uint32_t u;

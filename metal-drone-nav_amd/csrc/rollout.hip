@@ -569,7 +569,7 @@ __device__ __forceinline__ void raptor_wave(const float* RW, const RaptorRegs& o
         for (uint32_t kk = 0; kk < 4; kk++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(o.out[kk], bh[kk], acc, 0, 0, 0);
         const int src = int((threadIdx.x % 64) / G);  // lane holding this group's env column
 #pragma unroll
-        for (uint32_t q = 0; q < 4; q++) act[q] = max_f(-1.0f, min_f(1.0f, __shfl(acc[q], src, 64)));
+        for (uint32_t q = 0; q < 4; q++) act[q] = __builtin_amdgcn_fmed3f(__shfl(acc[q], src, 64), -1.0f, 1.0f);
     }
 }
 
@@ -1033,7 +1033,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             ctx[17] = float(r.steps - frame * C.sensor_period) * P.dt * float(C.substeps);
             const float ref0 = r.ref_pos[0] - s.p[0], ref1 = r.ref_pos[1] - s.p[1], ref2 = r.ref_pos[2] - s.p[2];
 #pragma unroll
-            for (int j = 0; j < 3; j++) ctx[18 + j] = clamp_f((R[j] * ref0 + R[3 + j] * ref1 + R[6 + j] * ref2) * 2.0f, -1.0f, 1.0f);
+            for (int j = 0; j < 3; j++) ctx[18 + j] = __builtin_amdgcn_fmed3f((R[j] * ref0 + R[3 + j] * ref1 + R[6 + j] * ref2) * 2.0f, -1.0f, 1.0f);
 #pragma unroll
             // every lane of the group holds the same values and writes them
             // (equal stores to one address; cheaper than per-value owner branches)
