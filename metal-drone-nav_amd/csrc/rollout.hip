@@ -754,6 +754,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     // whether some env of the workgroup was reset (or the launch is starting),
     // so that the critic at s must be evaluated this tick
     bool wg_reset = true;
+    // fused kernels: the next values of a tick with no reset in the workgroup
+    // are formed by the next tick's critic at s (the same critic
+    // observations); `deferred` is workgroup-uniform, `prev_due` says that
+    // this env's previous row awaits its next value
+    bool deferred = false, prev_due = false;
+    size_t prev_row = 0;
     for (uint32_t t = 0; t < a.count; t++) {
         const uint32_t tick = SPLIT ? (a.tick0 + t) % a.horizon : t % a.horizon;
         const size_t row = size_t(tick) * N + nn;
@@ -1110,12 +1116,17 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             // one that tick evaluated as its next state (the same operations on
             // the same state, time and step count), so the values it left in
             // s_x[env][4] are this tick's values; else evaluate the critic.
-            if (wg_reset) wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
+            // After a tick whose next values were deferred, the critic at s
+            // forms them too: an env active now has the same critic
+            // observation, an env that went inactive kept its row.
+            const bool critic_s = wg_reset || deferred;
+            if (critic_s) wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
             __syncthreads();
             // heads: means (waves 0-1) and value (waves 2-3) into s_x[env][0..4]
             wg_head<4, HID + 1>(&s_ah[0][0], AT + HID, HID, AT + 5 * HID, 0, &s_x[0][0], 0);
-            if (wg_reset) wg_head<1, HID + 1>(&s_ch[0][0], CT + HID, 0, CT + 2 * HID, 2, &s_x[0][0], 4);
+            if (critic_s) wg_head<1, HID + 1>(&s_ch[0][0], CT + HID, 0, CT + 2 * HID, 2, &s_x[0][0], 4);
             __syncthreads();
+            if (deferred && prev_due && lane == 0) a.next_values[prev_row] = s_x[grp][4];
         } else if (active) {
             float acc[HU];
 #pragma unroll
@@ -1433,10 +1444,15 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             // next values are the caller's (from the stored next critic observations)
         } else if constexpr (W > 1) {  // next value: critic hidden of s' for all 32 envs
             wg_reset = __syncthreads_or(ended) != 0;
-            wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
-            __syncthreads();
-            wg_head<1, HID + 1>(&s_ch[0][0], CT + HID, 0, CT + 2 * HID, 0, &s_x[0][0], 4);
-            __syncthreads();
+            // with no reset in the workgroup and another tick to come in this
+            // launch, the next tick's critic at s forms these next values
+            deferred = !SPLIT && !wg_reset && t + 1 < a.count;
+            if (!deferred) {
+                wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
+                __syncthreads();
+                wg_head<1, HID + 1>(&s_ch[0][0], CT + HID, 0, CT + 2 * HID, 0, &s_x[0][0], 4);
+                __syncthreads();
+            }
         } else {  // next value: critic hidden split over the group
             group_sync();
             if (active) {
@@ -1456,6 +1472,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             group_sync();
         }
         uint32_t reset_rng = 0, reset_family = 0, reset_seed = 0;
+        prev_due = deferred && active;
+        prev_row = row;
         if (active) {
             if constexpr (!X) {
                 float value;
@@ -1466,7 +1484,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll 8
                     for (uint32_t h = 0; h < HID; h++) value = fma_f(CR[c_w2 + h], s_ch[grp][h], value);
                 }
-                if (lane == 0) a.next_values[row] = value;
+                if (!deferred && lane == 0) a.next_values[row] = value;
             }
             if (ended) {
                 reset_rng = r.rng;
