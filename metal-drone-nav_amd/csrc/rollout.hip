@@ -1446,7 +1446,9 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             wg_reset = __syncthreads_or(ended) != 0;
             // with no reset in the workgroup and another tick to come in this
             // launch, the next tick's critic at s forms these next values
-            deferred = !SPLIT && !wg_reset && t + 1 < a.count;
+            // (a launch without split-tick flags observes every tick and runs
+            // to its last tick, so the guided actor's fused launches qualify)
+            deferred = (!SPLIT || a.split == 0u) && !wg_reset && t + 1 < a.count;
             if (!deferred) {
                 wg_layer_rb<COBS, COBS + 1, HID + 1>(&s_co[0][0], cw1, CT, &s_ch[0][0]);
                 __syncthreads();
