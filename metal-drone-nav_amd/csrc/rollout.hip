@@ -759,6 +759,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     // observations); `deferred` is workgroup-uniform, `prev_due` says that
     // this env's previous row awaits its next value
     bool deferred = false, prev_due = false;
+    bool co_fresh = false;  // s_co holds this env's critic observation of its current state
     size_t prev_row = 0;
     for (uint32_t t = 0; t < a.count; t++) {
         const uint32_t tick = SPLIT ? (a.tick0 + t) % a.horizon : t % a.horizon;
@@ -1067,34 +1068,42 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll
                 for (int j = 0; j < 3; j++) { s_obs[grp][D - 3 + j] = hint[j]; og[D - 3 + j] = hint[j]; }
             }
-            // critic observation (sim.metal:159-181)
-            float cob[COBS];
-#pragma unroll
-            for (int j = 0; j < 32; j++) cob[j] = 0;
-#pragma unroll
-            for (int j = 0; j < 3; j++) {
-                cob[j] = div_r(gw[j] - s.p[j], 1.0 / 10.0);
-                cob[j + 3] = s.v[j] / 4.0f;
-                cob[j + 6] = s.w[j] / 4.0f;
-                cob[j + 13] = div_r(s.p[j], 1.0 / 10.0);
-                cob[j + 16] = (r.ref_pos[j] - s.p[j]) * 2.0f;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
-            cob[30] = world[166];
-            cob[31] = world[167];
-            cob[19] = div_r(clearance(mk(s.p[0], s.p[1], s.p[2]), r.elapsed), 1.0 / 5.0);
-            cob[20] = div_r(float(r.steps), 1.0 / 200.0);
-#pragma unroll
-            for (uint32_t j = 0; j < 3; j++)
-                if (j < count) {
-                    cob[21 + j * 3] = div_r(s_cent[grp][3 * j] - s.p[0], 1.0 / 10.0);
-                    cob[22 + j * 3] = div_r(s_cent[grp][3 * j + 1] - s.p[1], 1.0 / 10.0);
-                    cob[23 + j * 3] = div_r(s_cent[grp][3 * j + 2] - s.p[2], 1.0 / 10.0);
-                }
+            // critic observation (sim.metal:159-181).  When the previous tick
+            // of this launch formed it as its next state's and did not reset
+            // the env, s_co already holds it (the same operations on the same
+            // state, time and step count) and it is only stored.
             float* cg = a.co + row * COBS;
+            if (co_fresh) {
 #pragma unroll
-            for (int j = 0; j < 32; j++) { s_co[grp][j] = cob[j]; cg[j] = cob[j]; }
+                for (int j = 0; j < 32; j++) cg[j] = s_co[grp][j];
+            } else {
+                float cob[COBS];
+#pragma unroll
+                for (int j = 0; j < 32; j++) cob[j] = 0;
+#pragma unroll
+                for (int j = 0; j < 3; j++) {
+                    cob[j] = div_r(gw[j] - s.p[j], 1.0 / 10.0);
+                    cob[j + 3] = s.v[j] / 4.0f;
+                    cob[j + 6] = s.w[j] / 4.0f;
+                    cob[j + 13] = div_r(s.p[j], 1.0 / 10.0);
+                    cob[j + 16] = (r.ref_pos[j] - s.p[j]) * 2.0f;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) cob[9 + j] = s.q[j];
+                cob[30] = world[166];
+                cob[31] = world[167];
+                cob[19] = div_r(clearance(mk(s.p[0], s.p[1], s.p[2]), r.elapsed), 1.0 / 5.0);
+                cob[20] = div_r(float(r.steps), 1.0 / 200.0);
+#pragma unroll
+                for (uint32_t j = 0; j < 3; j++)
+                    if (j < count) {
+                        cob[21 + j * 3] = div_r(s_cent[grp][3 * j] - s.p[0], 1.0 / 10.0);
+                        cob[22 + j * 3] = div_r(s_cent[grp][3 * j + 1] - s.p[1], 1.0 / 10.0);
+                        cob[23 + j * 3] = div_r(s_cent[grp][3 * j + 2] - s.p[2], 1.0 / 10.0);
+                    }
+#pragma unroll
+                for (int j = 0; j < 32; j++) { s_co[grp][j] = cob[j]; cg[j] = cob[j]; }
+            }
         } else if (SPLIT && active) {  // begins at act: this tick's rows as written before
             for (uint32_t i = lane; i < D; i += G) s_obs[grp][i] = og[i];
             for (uint32_t i = lane; i < COBS; i += G) s_co[grp][i] = a.co[row * COBS + i];
@@ -1440,6 +1449,7 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 ended = !C.eval;
             }
         }
+        co_fresh = active && !ended;
         if constexpr (X) {
             // next values are the caller's (from the stored next critic observations)
         } else if constexpr (W > 1) {  // next value: critic hidden of s' for all 32 envs
