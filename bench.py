@@ -40,6 +40,12 @@ FLOP_GUIDANCE = 10.8e3
 # contact), 85 candidate scores (~60 FLOP): 0.58 MFLOP.
 FLOP_MEMORY = 640 * 45 + 85 * 640 * 10 + 85 * 60
 BYTES_ENV_STEP = 4.34e3
+# The moving-threat mix (4 bounded movers on 8 boxes, or a 10-obstacle
+# course) averages 11.5 obstacles per world: 2.5 more per-ray tests (~30 FLOP
+# each) over 320 rays, and 2 ring frames re-read per tick with the 100 ms
+# sensor delay (SURVEY-style count: R (15 + 30 (K + 1)) per frame).
+FLOP_C3_EXTRA = 320 * 30 * 2.5
+BYTES_C3_EXTRA = 4 * 320 + 40 * 3.5
 # GAE + normalisation: 14 B in + 8 B out (GAE) + 3 passes over advantages.
 BYTES_GAE = 22.0
 BYTES_NORM = 16.0
@@ -279,13 +285,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-reference-schedule", action="store_true",
                     help="skip the reference-schedule line (its thousands of small launches; for counter passes)")
-    ap.add_argument("--workload", choices=["small", "large", "stress", "threats"], default="small",
+    ap.add_argument("--workload", choices=["small", "large", "stress", "threats", "c3"], default="small",
                     help="small: 8,192 envs x 128 ticks, 181-64-4 actor (the headline metric); large: 8,192 envs x "
                          "256 ticks, 184-5120-4 actor (967,688 parameters) and 32-5120-1 critic on bf16 matrix cores, "
                          "4 epochs x 64 "
                          "minibatches of 32,768; stress: 65,536 envs x 128 ticks, small actor; threats: 8,192 envs "
                          "x 256 ticks of the reference's moving-threat rehearsal mix (family 13: doorways, tables, "
                          "random families and the two moving-sphere threat families, clean even lanes) with "
+                         "100 ms sensor and command delays, small actor; c3: 8,192 envs x 256 ticks of the "
+                         "moving-threat mix (env lanes n %% 4: 0-1 eight boxes + four kind-3 bounded movers, 2 the "
+                         "same with a long 8-13 m goal, 3 a combined course with a bounded crossing sphere) with "
                          "100 ms sensor and command delays, small actor")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="BYTES",
                     help="run only the plain copy kernel over BYTES (reads BYTES, writes BYTES per launch); "
@@ -313,7 +322,7 @@ def main():
     from mdnav import PPOTrainer, Sim, abi
     if args.workload == "stress":
         args.envs, args.horizon, args.no_cpu_baseline = 65536, 128, True
-    if args.workload == "threats":
+    if args.workload in ("threats", "c3"):
         args.envs, args.horizon = 8192, 256
     N, T = args.envs, args.horizon
     headline = (N, T) == (8192, 128) and args.actor_obs == 181 and not args.geometry_memory and \
@@ -322,6 +331,8 @@ def main():
     cfg_kw = dict(family=1, speed=1.0, distance=3.0, geometry_memory=1 if args.geometry_memory else 0)
     if args.workload == "threats":  # the reference's threat rehearsal with 100 ms delays (2 ticks at 20 Hz)
         cfg_kw = dict(family=13, speed=1.5, distance=4.0, sensor_delay=2, command_delay=2)
+    if args.workload == "c3":  # moving-threat mix: kind-3 movers, long goals, courses; 100 ms delays
+        cfg_kw = dict(family=abi.FAMILY_C3_MIX, speed=1.5, distance=4.0, sensor_delay=2, command_delay=2)
     if args.task_training:  # navigation_training.hpp:119-123
         cfg_kw = dict(family=12, mode=22, speed=1.5, distance=8.0, max_steps=400, geometry_memory=1,
                       entropy_coef=0.001, learning_rate=0.0001)
@@ -365,7 +376,9 @@ def main():
     # one launch per iteration (with the geometry memory: one per tick, timed
     # here per iteration)
     avg_s = roll["total_ms"] * 1e-3 / args.steps
-    flop_env_step = FLOP_ENV_STEP + (FLOP_GUIDANCE if args.actor_obs == 184 else 0.0)
+    flop_env_step = FLOP_ENV_STEP + (FLOP_GUIDANCE if args.actor_obs == 184 else 0.0) + \
+        (FLOP_C3_EXTRA if args.workload == "c3" else 0.0)
+    bytes_env_step = BYTES_ENV_STEP + (BYTES_C3_EXTRA if args.workload == "c3" else 0.0)
     achieved = flop_env_step * env_steps_launch / avg_s
     roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic_from_profile() if headline else None,
@@ -377,8 +390,8 @@ def main():
                            "launches per iteration)" % (T, roll["launches"] // args.steps)),
                 "roof_note": "fp32 compute roof: env step on the VALU, policy/critic layers and RAPTOR dense/GRU "
                              "on fp32 MFMA; algorithmic %.1f kFLOP and %.2f KB per env-step x %d env-steps per "
-                             "launch" % (flop_env_step / 1e3, BYTES_ENV_STEP / 1e3, env_steps_launch),
-                "hbm_frac_algorithmic": round(BYTES_ENV_STEP * env_steps_launch / avg_s / PEAK_HBM, 5)}
+                             "launch" % (flop_env_step / 1e3, bytes_env_step / 1e3, env_steps_launch),
+                "hbm_frac_algorithmic": round(bytes_env_step * env_steps_launch / avg_s / PEAK_HBM, 5)}
     secondary = {}
     if kernels["memory"]["launches"]:
         mem_s = kernels["memory"]["total_ms"] * 1e-3 / args.steps
@@ -408,6 +421,13 @@ def main():
                 "doorway, table, a random family 0-6, or a moving-sphere threat, families 10/11), random-init policy")
         workload = ("moving-threat rehearsal mix, %d envs x %d ticks, 100 ms sensor and command delays (even envs "
                     "clean), small actor 181-64-4, %s PPO schedule" % (N, T, args.schedule))
+    elif args.workload == "c3":
+        data = ("synthetic: seeded moving-threat mix per env lane n % 4 (lanes 0-1: family-1 boxes + 4 kind-3 "
+                "bounded spheres, r 0.2-0.5 m, peak speed 0.3-1.5 m/s; lane 2: the same with an 8-13 m goal; "
+                "lane 3: a combined corridor course with a bounded crossing sphere), random-init policy")
+        workload = ("moving-threat mix (kind-3 bounded movers, static/long/course lanes 50/25/25), %d envs x %d "
+                    "ticks, 100 ms sensor and command delays, small actor 181-64-4, %s PPO schedule"
+                    % (N, T, args.schedule))
     else:
         data = "synthetic: seeded procedural worlds (reference family 1), random-init policy (seed 1789)"
         workload = ("static-box world, %d envs x %d ticks, %s actor %d-64-4%s, %s PPO schedule"

@@ -250,12 +250,19 @@ MDN_HD float atan_f(float x) {
     const float r = y0 + p;
     return x < 0.0f ? -r : r;
 }
-// atan2 by quadrant from atan_f(y / x); (0, 0) -> 0.
+// atan2 with the special values of C99 Annex F.9.1.4: a = atan_f(|y| / |x|)
+// in [0, pi/2] (pi/4 when both are infinite, 0 when both are zero), then
+// pi - a when x is negative or -0, with the sign of y.  For finite nonzero
+// operands this is the quadrant rule t, t + pi, t - pi on t = atan_f(y / x)
+// operation for operation (atan_f is odd and -(pi - a) = a - pi exactly).
 MDN_HD float atan2_f(float y, float x) {
-    const float pi = 3.14159265358979f, half_pi = 1.5707963267948966f;
-    const float t = atan_f(y / x);
-    const float r = x > 0.0f ? t : (x < 0.0f ? (y < 0.0f ? t - pi : t + pi)
-                                             : (y > 0.0f ? half_pi : (y < 0.0f ? -half_pi : 0.0f)));
+    const float pi = 3.14159265358979f, quarter_pi = 0.7853981633974483f;
+    const float ay = fabs_f(y), ax = fabs_f(x);
+    const float t = atan_f(ay / ax);
+    const bool both_inf = ay == inf_f() && ax == inf_f(), both_zero = ay == 0.0f && ax == 0.0f;
+    const float a0 = both_inf ? quarter_pi : (both_zero ? 0.0f : t);
+    const float a = (float_bits(x) >> 31) != 0u ? pi - a0 : a0;
+    const float r = bits_float(float_bits(a) | (float_bits(y) & 0x80000000u));
     return (x == x && y == y) ? r : x + y;
 }
 

@@ -39,6 +39,21 @@ extern "C" {
 #define MDN_SENSOR_MAX_RANGE 12.0f
 #define MDN_MAX_OBSTACLES 16u
 
+/* World families of the moving-threat mix, numbered after the reference's
+ * 0-16 (world.hpp:293-318).  MDN_FAMILY_C3_MIX picks per env lane n % 4,
+ * the reference's static / long / course lane split of 50/25/25
+ * (navigation_training_mix.py:25-38): lanes 0 and 1 the mover world with the
+ * config's goal distance, lane 2 the mover world with a long goal, lane 3 a
+ * combined course.  The mover world is family 1's eight boxes plus four
+ * kind-3 bounded movers (world.hpp:26-41); the course follows the combined
+ * course of navigation_challenge_tasks.py:47-117. */
+#define MDN_FAMILY_C3_MIX 32u
+#define MDN_FAMILY_MOVERS 33u
+#define MDN_FAMILY_MOVERS_LONG 34u
+#define MDN_FAMILY_COURSE 35u
+#define MDN_C3_LANE_FAMILY(env) \
+    ((env) % 4u < 2u ? MDN_FAMILY_MOVERS : ((env) % 4u == 2u ? MDN_FAMILY_MOVERS_LONG : MDN_FAMILY_COURSE))
+
 /* Policy shapes (ppo.hpp:26-45 with FIXED_PPO_ACTOR_OBS_DIM=181). */
 #define MDN_CONTEXT_DIM 21u
 #define MDN_ACTOR_OBS_POOLED 181u

@@ -1002,6 +1002,63 @@ struct WorldGen {
         w[164] = (ur(rng) - 0.5f) * 1.20f;
         w[165] = 1.10f + 0.80f * ur(rng);
     }
+    // Four bounded movers (kind 3, world.hpp:26-41: size = {radius, travel
+    // amplitude, phase}, velocity = direction times peak speed): radius
+    // U[0.2, 0.5] m, peak speed U[0.3, 1.5] m/s along a horizontal heading,
+    // amplitude U[0.5, 2] m, phase U[-pi, pi), centres spread along the route
+    // to `reach`.  Every draw is a statement of its own (draw order fixed).
+    __device__ void movers(uint32_t& rng, float reach) {
+        for (int i = 0; i < 4; i++) {
+            const float cx = 1.5f + ur(rng) * fmax_f(0.5f, reach - 2.5f);
+            const float cy = (ur(rng) - 0.5f) * 5.0f;
+            const float cz = 0.8f + ur(rng) * 1.6f;
+            const float radius = 0.2f + 0.3f * ur(rng);
+            const float speed = 0.3f + 1.2f * ur(rng);
+            const float heading = 6.28318530718f * ur(rng);
+            const float amplitude = 0.5f + 1.5f * ur(rng);
+            const float phase = (ur(rng) - 0.5f) * 6.28318530718f;
+            float sh, ch;
+            sincos_f(heading, &sh, &ch);
+            add(3, mk(cx, cy, cz), mk(radius, amplitude, phase), mk(speed * ch, speed * sh, 0.0f));
+        }
+    }
+    // The combined course of navigation_challenge_tasks.py:47-117 (kind
+    // "combined") with xorshift draws: a 3.2 m corridor with a side opening
+    // at 0.59 L, staggered openings at 0.32 L and 0.68 L, a hanging beam at
+    // 0.5 L and one bounded sphere crossing the side opening; the start
+    // height is the reset's 1.5 m.  Ten obstacles.
+    __device__ void course(uint32_t& rng) {
+        const float length = 8.5f + 3.0f * ur(rng);
+        const float yg = (ur(rng) - 0.5f) * 0.4f;
+        const float z = 1.5f, width = 3.2f, cross = length * 0.59f;
+        w[163] = length; w[164] = yg; w[165] = z;
+        for (int side = -1; side <= 1; side += 2) {
+            const float y = float(side) * (width * 0.5f + 0.06f);
+            const float l0 = -2.0f, h0 = cross - 0.7f, l1 = cross + 0.7f, h1 = 14.0f;
+            box(mk((l0 + h0) * 0.5f, y, 2.5f), mk((h0 - l0) * 0.5f, 0.06f, 2.5f));
+            box(mk((l1 + h1) * 0.5f, y, 2.5f), mk((h1 - l1) * 0.5f, 0.06f, 2.5f));
+        }
+        const bool hard = ur(rng) < 0.5f;
+        const float ug = ur(rng);
+        const float gap = hard ? 0.85f + 0.35f * ug : 1.15f + 0.40f * ug;
+        const float uo = ur(rng);
+        const float offset = hard ? 0.65f + 0.20f * uo : 0.45f + 0.20f * uo;
+        const float sign = ur(rng) < 0.5f ? -1.0f : 1.0f;
+        for (int stage = 0; stage < 2; stage++) {
+            const float x = length * (stage == 0 ? 0.32f : 0.68f);
+            const float cy = sign * offset * (stage == 0 ? 1.0f : -1.0f);
+            const float l0 = -width * 0.5f, h0 = cy - gap * 0.5f, l1 = cy + gap * 0.5f, h1 = width * 0.5f;
+            box(mk(x, (l0 + h0) * 0.5f, 2.5f), mk(0.12f, (h0 - l0) * 0.5f, 2.5f));
+            box(mk(x, (l1 + h1) * 0.5f, 2.5f), mk(0.12f, (h1 - l1) * 0.5f, 2.5f));
+        }
+        box(mk(length * 0.5f, 0.0f, 3.35f), mk(0.25f, width * 0.5f, 1.65f));
+        const float us = ur(rng);
+        const float speed = hard ? 0.65f + 0.35f * us : 0.35f + 0.30f * us;
+        const float phase = -1.57079632679f + (ur(rng) - 0.5f) * 0.5f;
+        const float dir = ur(rng) < 0.5f ? -1.0f : 1.0f;
+        const float amplitude = 2.2f + 1.2f * ur(rng);
+        add(3, mk(cross, 0.0f, z), mk(0.28f, amplitude, phase), mk(0.0f, dir * speed, 0.0f));
+    }
     // Like wgenerate, slots beyond the new count keep their previous contents.
     __device__ void generate(uint32_t seed, uint32_t family, float distance) {
         uint32_t rng = seed ? seed : 1;
@@ -1160,11 +1217,22 @@ struct WorldGen {
             box(mk(choice_x, 0, 2.0f + choice_half_z), mk(0.10f, 5.0f, choice_half_z));
             return;
         }
+        if (family == MDN_FAMILY_COURSE) {
+            set_count(0);
+            course(rng);
+            return;
+        }
+        const bool mover_world = family == MDN_FAMILY_MOVERS || family == MDN_FAMILY_MOVERS_LONG;
+        float reach = distance;
+        if (family == MDN_FAMILY_MOVERS_LONG) {  // a long goal, 8-13 m (the room ends at x = 14)
+            reach = 8.0f + 5.0f * ur(rng);
+            w[163] = reach;
+        }
         // world.hpp:311-317: sixteen random slots, the first eight live
         for (uint32_t i = 0; i < 16; i++) {
             float* o = w + 10 * i;
             o[0] = bits_float(family == 2 ? 2u : (family == 3 ? 1u : 0u));
-            o[1] = 1.2f + ur(rng) * fmax_f(0.1f, distance - 2.2f);
+            o[1] = 1.2f + ur(rng) * fmax_f(0.1f, reach - 2.2f);
             o[2] = (ur(rng) - 0.5f) * 7;
             o[3] = family == 2 ? 2.5f : 0.6f + ur(rng) * 3;
             o[4] = 0.2f + ur(rng) * 0.35f;
@@ -1174,6 +1242,7 @@ struct WorldGen {
             o[8] = family == 3 ? (ur(rng) - 0.5f) * 0.8f : 0;
             o[9] = 0;
         }
+        if (mover_world) movers(rng, reach);  // slots 8-11
     }
 };
 

@@ -135,7 +135,7 @@ __device__ __forceinline__ void store_run(uint32_t* g, uint32_t N, uint32_t n, c
 __device__ __forceinline__ void reset_draw(const MdnSimConfig& c, uint32_t n, bool first, uint32_t& rng,
                                            uint32_t& family, uint32_t& world_seed) {
     rng = first ? c.seed + n * 747796405u + 2891336453u : rng;
-    family = training_family(c.family, rng);
+    family = c.family == MDN_FAMILY_C3_MIX ? MDN_C3_LANE_FAMILY(n) : training_family(c.family, rng);
     world_seed = xs(rng);
 }
 

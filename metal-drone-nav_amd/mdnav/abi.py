@@ -182,3 +182,9 @@ BUFFERS = {
     "bank_schedule": (29, np.uint32),
 }
 BANK_REHEARSAL = 0xFFFFFFFF
+# moving-threat mix families (include/mdnav_types.h): per env lane n % 4,
+# 0-1 FAMILY_MOVERS, 2 FAMILY_MOVERS_LONG, 3 FAMILY_COURSE
+FAMILY_C3_MIX = 32
+FAMILY_MOVERS = 33
+FAMILY_MOVERS_LONG = 34
+FAMILY_COURSE = 35

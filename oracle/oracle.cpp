@@ -353,7 +353,8 @@ struct Trainer {
         MdnSimRun& run = runs[n];
         MdnWorld& world = worlds[n];
         uint32_t rng = first ? cfg.seed + n * 747796405u + 2891336453u : run.rng;
-        const uint32_t family = training_family(cfg.family, rng);
+        // the moving-threat mix takes its family from the env's lane
+        const uint32_t family = cfg.family == MDN_FAMILY_C3_MIX ? MDN_C3_LANE_FAMILY(n) : training_family(cfg.family, rng);
         const uint32_t world_seed = xorshift(rng);
         generate_world(world, world_seed, family, cfg.distance);
         world.wind[0] = wind_param(n); world.wind[1] = 0; world.wind[2] = 0;
@@ -1075,6 +1076,15 @@ void orc_ray_world_batch(const MdnWorld* worlds, const float* rays, const float*
         const float* r = rays + 6 * i;
         out[i] = orc::ray_world(w, orc::v3(r[0], r[1], r[2]), orc::v3(r[3], r[4], r[5]), times[i / rays_per_world]);
     }
+}
+void orc_atan2_batch(const float* y, const float* x, float* out, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) out[i] = mdn::atan2_f(y[i], x[i]);
+}
+// sim.metal:233: the guided evaluation modes' means for one 184-input row
+void orc_guided_mode_means(uint32_t mode, const float* obs, float* mean) { orc::Trainer::guided_mode_means(mode, obs, mean); }
+void orc_obstacle_center(const MdnWorld* w, uint32_t i, float t, float* out) {
+    const orc::V3 c = orc::obstacle_center(w->obstacles[i], t);
+    out[0] = c.x; out[1] = c.y; out[2] = c.z;
 }
 void orc_clearance_batch(const MdnWorld* worlds, const float* points, const float* times, float* out, uint64_t n) {
     for (uint64_t i = 0; i < n; i++)

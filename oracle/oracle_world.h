@@ -343,6 +343,67 @@ inline uint32_t training_family(uint32_t family, uint32_t& rng) {
     }
     return family;
 }
+// Moving-threat mix (families MDN_FAMILY_MOVERS, _MOVERS_LONG, _COURSE; a
+// workload of this library, not a reference generator).  Four kind-3
+// bounded movers (world.hpp:26-41): radius U[0.2, 0.5] m, peak speed
+// U[0.3, 1.5] m/s on a horizontal heading, amplitude U[0.5, 2] m, phase
+// U[-pi, pi), centres along the route to `reach`.
+inline void gen_movers(MdnWorld& w, uint32_t& rng, float reach) {
+    for (int i = 0; i < 4; i++) {
+        const float cx = 1.5f + urand(rng) * fmax_f(0.5f, reach - 2.5f);
+        const float cy = (urand(rng) - 0.5f) * 5.0f;
+        const float cz = 0.8f + urand(rng) * 1.6f;
+        const float radius = 0.2f + 0.3f * urand(rng);
+        const float speed = 0.3f + 1.2f * urand(rng);
+        const float heading = 6.28318530718f * urand(rng);
+        const float amplitude = 0.5f + 1.5f * urand(rng);
+        const float phase = (urand(rng) - 0.5f) * 6.28318530718f;
+        float sh, ch;
+        sincos_f(heading, &sh, &ch);
+        world_add(w, 3, v3(cx, cy, cz), v3(radius, amplitude, phase), v3(speed * ch, speed * sh, 0.0f));
+    }
+}
+// The combined course of navigation_challenge_tasks.py:47-117 with xorshift
+// draws: corridor walls with a side opening at 0.59 L (4 boxes), openings
+// at 0.32 L and 0.68 L offset to alternate sides (4 boxes), a hanging beam
+// at 0.5 L, and a bounded sphere of radius 0.28 m crossing at the side
+// opening.  Start height 1.5 m (the reset's), goal (L, U[-0.2, 0.2], 1.5).
+inline void gen_course(MdnWorld& w, uint32_t& rng) {
+    const float length = 8.5f + 3.0f * urand(rng);
+    const float yg = (urand(rng) - 0.5f) * 0.4f;
+    const float z = 1.5f, width = 3.2f, cross = length * 0.59f;
+    w.goal[0] = length; w.goal[1] = yg; w.goal[2] = z;
+    for (int side = -1; side <= 1; side += 2) {
+        const float y = float(side) * (width * 0.5f + 0.06f);
+        const float spans[2][2] = {{-2.0f, cross - 0.7f}, {cross + 0.7f, 14.0f}};
+        for (int k = 0; k < 2; k++) {
+            const float lo = spans[k][0], hi = spans[k][1];
+            world_add_box(w, v3((lo + hi) * 0.5f, y, 2.5f), v3((hi - lo) * 0.5f, 0.06f, 2.5f));
+        }
+    }
+    const bool hard = urand(rng) < 0.5f;
+    const float ug = urand(rng);
+    const float gap = hard ? 0.85f + 0.35f * ug : 1.15f + 0.40f * ug;
+    const float uo = urand(rng);
+    const float offset = hard ? 0.65f + 0.20f * uo : 0.45f + 0.20f * uo;
+    const float sign = urand(rng) < 0.5f ? -1.0f : 1.0f;
+    for (int stage = 0; stage < 2; stage++) {
+        const float x = length * (stage == 0 ? 0.32f : 0.68f);
+        const float cy = sign * offset * (stage == 0 ? 1.0f : -1.0f);
+        const float spans[2][2] = {{-width * 0.5f, cy - gap * 0.5f}, {cy + gap * 0.5f, width * 0.5f}};
+        for (int k = 0; k < 2; k++) {
+            const float lo = spans[k][0], hi = spans[k][1];
+            world_add_box(w, v3(x, (lo + hi) * 0.5f, 2.5f), v3(0.12f, (hi - lo) * 0.5f, 2.5f));
+        }
+    }
+    world_add_box(w, v3(length * 0.5f, 0.0f, 3.35f), v3(0.25f, width * 0.5f, 1.65f));
+    const float us = urand(rng);
+    const float speed = hard ? 0.65f + 0.35f * us : 0.35f + 0.30f * us;
+    const float phase = -1.57079632679f + (urand(rng) - 0.5f) * 0.5f;
+    const float dir = urand(rng) < 0.5f ? -1.0f : 1.0f;
+    const float amplitude = 2.2f + 1.2f * urand(rng);
+    world_add(w, 3, v3(cross, 0.0f, z), v3(0.28f, amplitude, phase), v3(0.0f, dir * speed, 0.0f));
+}
 // world.hpp:299-318
 inline void generate_world(MdnWorld& w, uint32_t seed, uint32_t family, float distance) {
     uint32_t rng = seed ? seed : 1;
@@ -359,10 +420,14 @@ inline void generate_world(MdnWorld& w, uint32_t seed, uint32_t family, float di
     if (family == 14) { w.count = 0; gen_bent_hallway(w, rng, distance); return; }
     if (family == 15) { w.count = 0; gen_connected_rooms(w, rng, distance); return; }
     if (family == 16) { w.count = 0; gen_vertical_choices(w, rng, distance); return; }
+    if (family == MDN_FAMILY_COURSE) { w.count = 0; gen_course(w, rng); return; }
+    const bool mover_world = family == MDN_FAMILY_MOVERS || family == MDN_FAMILY_MOVERS_LONG;
+    float reach = distance;
+    if (family == MDN_FAMILY_MOVERS_LONG) { reach = 8.0f + 5.0f * urand(rng); w.goal[0] = reach; }
     for (uint32_t i = 0; i < 16; i++) {
         MdnObstacle& o = w.obstacles[i];
         o.kind = family == 2 ? 2 : (family == 3 ? 1 : 0);
-        o.center[0] = 1.2f + urand(rng) * fmax_f(0.1f, distance - 2.2f);
+        o.center[0] = 1.2f + urand(rng) * fmax_f(0.1f, reach - 2.2f);
         o.center[1] = (urand(rng) - 0.5f) * 7;
         o.center[2] = family == 2 ? 2.5f : 0.6f + urand(rng) * 3;
         o.size[0] = 0.2f + urand(rng) * 0.35f;
@@ -372,6 +437,7 @@ inline void generate_world(MdnWorld& w, uint32_t seed, uint32_t family, float di
         o.velocity[1] = family == 3 ? (urand(rng) - 0.5f) * 0.8f : 0;
         o.velocity[2] = 0;
     }
+    if (mover_world) gen_movers(w, rng, reach);  // slots 8-11
 }
 
 // ---- L2F plant: physics.hpp:44-179 --------------------------------------

@@ -109,6 +109,11 @@ void ref_clearance_batch(const MdnWorld* worlds, const float* points, const floa
     for (uint64_t i = 0; i < n; i++)
         out[i] = wclearance(reinterpret_cast<const WWorld*>(worlds)[i], wv(points[3 * i], points[3 * i + 1], points[3 * i + 2]), times[i]);
 }
+// wc (world.hpp:32-41): obstacle i's centre at time t
+void ref_obstacle_center(const MdnWorld* w, uint32_t i, float t, float* out) {
+    const WVec c = wc(reinterpret_cast<const WWorld*>(w)->obstacles[i], t);
+    out[0] = c.x; out[1] = c.y; out[2] = c.z;
+}
 void ref_camera_rays(float* out) {
     for (uint32_t k = 0; k < NAV_SENSOR_PIXELS; k++) {
         const WVec r = nav_sensor_pixel_ray(NAV_SENSOR_TAN_H, NAV_SENSOR_ACTIVE_TAN_V, k);

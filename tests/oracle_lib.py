@@ -69,6 +69,9 @@ def oracle():
         _sig(lib, "orc_generate_world", None, P, U32, U32, F32)
         _sig(lib, "orc_ray_world_batch", None, P, P, P, U32, P, U64)
         _sig(lib, "orc_clearance_batch", None, P, P, P, P, U64)
+        _sig(lib, "orc_obstacle_center", None, P, U32, F32, P)
+        _sig(lib, "orc_atan2_batch", None, P, P, P, U64)
+        _sig(lib, "orc_guided_mode_means", None, U32, P, P)
         _sig(lib, "orc_ray_box", F32, P, P, P, P)
         _sig(lib, "orc_ray_sphere", F32, P, P, P, F32)
         _sig(lib, "orc_ray_cylinder", F32, P, P, P, F32, F32)
@@ -126,6 +129,7 @@ def ref(actor_obs=181):
         _sig(lib, "ref_generate_world", None, P, U32, U32, F32)
         _sig(lib, "ref_ray_world_batch", None, P, P, P, U32, P, U64)
         _sig(lib, "ref_clearance_batch", None, P, P, P, P, U64)
+        _sig(lib, "ref_obstacle_center", None, P, U32, F32, P)
         _sig(lib, "ref_camera_rays", None, P)
         _sig(lib, "ref_camera_rays_native", None, P)
         _sig(lib, "ref_camera_profile", None, U32, P)
