@@ -64,7 +64,11 @@ enum MdnBuffer {
     MDN_BUF_TASK_STATES = 26, /* MdnTaskState[N]      task_states (main.mm:523) */
     MDN_BUF_BANK_ACTIVE_IDS = 27,     /* uint32[N]     bank_active_ids: each env's challenge level */
     MDN_BUF_BANK_TRANSITION_IDS = 28, /* uint32[T][N]  bank_transition_ids: the level of each row */
-    MDN_BUF_BANK_SCHEDULE = 29        /* uint32[N][stride] bank_schedule (after mdn_sim_set_bank) */
+    MDN_BUF_BANK_SCHEDULE = 29,       /* uint32[N][stride] bank_schedule (after mdn_sim_set_bank) */
+    MDN_BUF_GRAD_NORM_ROWS = 30       /* float[updates][2] grad_norm_rows (main.mm:1111, 1370-1373): the
+                                         pre-clip actor and critic gradient norms of each update of the last
+                                         rollout_update (needs a PPO handle; the wide policy's
+                                         summary is mdn_lppo_grad_norm_summary) */
 };
 
 /* Kernel ids for mdn_sim_kernel_time. */
@@ -200,6 +204,18 @@ int mdn_ppo_normalize(MdnPPO* ppo);
 int mdn_ppo_update(MdnPPO* ppo, uint32_t rollout_index);
 /* PPOTrainer::metric_mean (main.mm:1383): [policy, value, entropy, ratio]. */
 int mdn_ppo_metric_mean(MdnPPO* ppo, float out[4]);
+/* PPOTrainer::GradNormSummary (main.mm:1439-1442). */
+typedef struct MdnGradNormSummary {
+    float actor_mean, actor_max, actor_clip_frac;
+    float critic_mean, critic_max, critic_clip_frac;
+} MdnGradNormSummary;
+/* PPOTrainer::grad_norm_summary (main.mm:1443-1465): over the last
+ * rollout_update's updates, the mean (a double sum), the maximum and the
+ * fraction above the clip limit 0.5 of the pre-clip actor and critic
+ * gradient norms sqrt(|g|^2 + 1e-20) (MDN_BUF_GRAD_NORM_ROWS).  Waits for the
+ * sim's stream.  MDN_E_STATE, "non-finite pre-clip gradient norm", when a
+ * norm is NaN or infinite (main.mm:1451); all zeros before any update. */
+int mdn_ppo_grad_norm_summary(MdnPPO* ppo, MdnGradNormSummary* out);
 int mdn_ppo_optimizer_step(const MdnPPO* ppo, uint64_t* step);
 int mdn_ppo_updates_per_rollout(const MdnPPO* ppo, uint32_t* updates);
 
@@ -283,6 +299,8 @@ int mdn_lppo_param_count(const MdnLargePPO* lp, uint32_t which, uint64_t* count)
 int mdn_lppo_get_params(MdnLargePPO* lp, uint32_t which, float* host, uint64_t count);
 int mdn_lppo_set_params(MdnLargePPO* lp, uint32_t which, const float* host, uint64_t count);
 int mdn_lppo_metric_mean(MdnLargePPO* lp, float out[4]);
+/* mdn_ppo_grad_norm_summary for the wide policy (main.mm:1443-1465). */
+int mdn_lppo_grad_norm_summary(MdnLargePPO* lp, MdnGradNormSummary* out);
 int mdn_lppo_optimizer_step(const MdnLargePPO* lp, uint64_t* step);
 
 /* Stateless operators over host arrays (the reference's fixture kernels

@@ -16,6 +16,7 @@
 #ifndef MDNAV_HPP
 #define MDNAV_HPP
 
+#include <algorithm>
 #include <array>
 #include <chrono>
 #include <cmath>
@@ -23,6 +24,7 @@
 #include <filesystem>
 #include <fstream>
 #include <iostream>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -85,6 +87,29 @@ public:
     std::vector<float> critic() { return download<float>(MDN_BUF_CRITIC); }
     std::vector<float> rewards() { return download<float>(MDN_BUF_REWARDS); }
 
+    // Sim::report (main.mm:599-602): episode totals of every env, printed as
+    // the reference prints them (and returned).
+    std::string report(const std::string& label, double wall) {
+        const std::vector<MdnSimRun> r = runs();
+        uint64_t success = 0, collision = 0, timeout = 0, ep = 0;
+        double time = 0, path = 0, total = 0, progress = 0;
+        float clearance = 12, peak = 0;
+        for (const MdnSimRun& x : r) {
+            success += x.successes; collision += x.collisions; timeout += x.timeouts; ep += x.episodes;
+            time += x.success_time; path += x.total_path; total += x.total_elapsed; progress += x.final_progress;
+            clearance = std::fmin(clearance, x.min_clearance);
+            peak = std::fmax(peak, x.peak_speed);
+        }
+        std::ostringstream line;
+        line << label << " episodes=" << ep << " success=" << (ep ? double(success) / ep : 0)
+             << " collision=" << (ep ? double(collision) / ep : 0) << " timeout=" << (ep ? double(timeout) / ep : 0)
+             << " progress=" << (ep ? progress / ep : 0) << " mean_goal_time=" << (success ? time / success : 0)
+             << " mean_speed=" << (total ? path / total : 0) << " peak_speed=" << peak
+             << " min_clearance=" << clearance << " wall_s=" << wall << "\n";
+        std::cout << line.str();
+        return line.str();
+    }
+
     MdnSim* handle() const { return handle_; }
     MdnSimConfig cfg;
     uint32_t horizon;
@@ -111,6 +136,14 @@ public:
     uint64_t optimizer_step() const {
         uint64_t s = 0;
         require(mdn_ppo_optimizer_step(handle_, &s));
+        return s;
+    }
+    // PPOTrainer::grad_norm_summary (main.mm:1443-1465); throws on a
+    // non-finite pre-clip norm like the reference's require.
+    using GradNormSummary = MdnGradNormSummary;
+    GradNormSummary grad_norm_summary() const {
+        GradNormSummary s{};
+        require(mdn_ppo_grad_norm_summary(handle_, &s));
         return s;
     }
     // PPOTrainer::save_checkpoint / load_checkpoint (main.mm:1218-1317); the
@@ -170,6 +203,52 @@ public:
         return m;
     }
     void reset_all() { sim.reset(); }
+
+    // Trainer::validate_batched_forward (cpu_reference.hpp:187-208): the
+    // batched forward of the current actor and critic (on the GPU, over three
+    // synthetic rows obs[i] = 0.2 sin(0.0037 i), critic obs[i] = 0.3 cos(0.17 i))
+    // against the scalar fixed_ppo forward of each row (ppo.hpp:65-93); true
+    // when hidden activations, means and values agree within `tolerance`.
+    bool validate_batched_forward(float tolerance = 2.0e-5f) {
+        constexpr uint32_t b = 3, H = MDN_HIDDEN, A = MDN_ACTIONS, C = MDN_CRITIC_OBS;
+        uint32_t D = 0;
+        require(mdn_sim_get_actor_obs(sim.handle(), &D));
+        const std::vector<float> actor = sim.actor(), critic = sim.critic();
+        std::vector<float> obs(size_t(b) * D), co(size_t(b) * C);
+        for (size_t i = 0; i < obs.size(); i++) obs[i] = .2f * std::sin(float(i) * .0037f);
+        for (size_t i = 0; i < co.size(); i++) co[i] = .3f * std::cos(float(i) * .17f);
+        std::vector<float> ah(size_t(b) * H), am(size_t(b) * A), ch(size_t(b) * H), cv(b);
+        require(mdn_op_actor_forward(actor.data(), D, H, obs.data(), b, ah.data(), am.data()));
+        require(mdn_op_critic_forward(critic.data(), C, H, co.data(), b, ch.data(), cv.data()));
+        float error = 0.0f;
+        std::vector<float> h(H);
+        for (uint32_t n = 0; n < b; n++) {
+            const float* x = obs.data() + size_t(n) * D;
+            for (uint32_t j = 0; j < H; j++) {  // ppo.hpp:66-72
+                float z = actor[size_t(H) * D + j];
+                for (uint32_t i = 0; i < D; i++) z += actor[size_t(j) * D + i] * x[i];
+                h[j] = std::tanh(z);
+                error = std::max(error, std::fabs(h[j] - ah[size_t(n) * H + j]));
+            }
+            for (uint32_t a = 0; a < A; a++) {  // ppo.hpp:73-79, the hint of a 184-input actor
+                float z = actor[size_t(H) * D + H + size_t(A) * H + a];
+                for (uint32_t j = 0; j < H; j++) z += actor[size_t(H) * D + H + size_t(a) * H + j] * h[j];
+                if (D == MDN_ACTOR_OBS_PRIOR && a < 3) z += x[D - 3 + a];
+                error = std::max(error, std::fabs(z - am[size_t(n) * A + a]));
+            }
+            const float* c = co.data() + size_t(n) * C;
+            float value = critic[size_t(H) * C + 2 * H];
+            for (uint32_t j = 0; j < H; j++) {  // ppo.hpp:82-93
+                float z = critic[size_t(H) * C + j];
+                for (uint32_t i = 0; i < C; i++) z += critic[size_t(j) * C + i] * c[i];
+                h[j] = std::tanh(z);
+                error = std::max(error, std::fabs(h[j] - ch[size_t(n) * H + j]));
+            }
+            for (uint32_t j = 0; j < H; j++) value += critic[size_t(H) * C + H + j] * h[j];
+            error = std::max(error, std::fabs(value - cv[n]));
+        }
+        return error <= tolerance;
+    }
 
     Sim sim;
     PPOTrainer ppo;
@@ -414,6 +493,7 @@ inline void train(const Context& ctx, uint32_t rollouts, const std::string& chec
             history.flush();
             std::cout << "task_train rollout=" << rollout + 1 << " policy_loss=" << metrics[0]
                       << " value_loss=" << metrics[1] << " ratio=" << metrics[3] << " wall_s=" << wall() << "\n";
+            sim.report("train-arrival", 0);
         }
     }
 }

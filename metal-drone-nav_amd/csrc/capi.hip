@@ -170,6 +170,7 @@ struct MdnPPO {
     double* norm_part = nullptr;
     float* norm_stats = nullptr;
     float *metric_rows = nullptr, *metric_mean = nullptr;
+    float* grad_norm_rows = nullptr;  // [updates][2] pre-clip norms of the last rollout_update
 };
 
 namespace {
@@ -249,6 +250,7 @@ BufInfo row_buffer(MdnSim* s, uint32_t id) {
             case MDN_BUF_CRITIC_M: return {p->cm, size_t(s->shape.critic_count()) * 4};
             case MDN_BUF_CRITIC_V: return {p->cv, size_t(s->shape.critic_count()) * 4};
             case MDN_BUF_METRIC_ROWS: return {p->metric_rows, size_t(p->updates) * 16};
+            case MDN_BUF_GRAD_NORM_ROWS: return {p->grad_norm_rows, size_t(p->updates) * 8};
             default: break;
         }
     }
@@ -472,10 +474,12 @@ int mdn_sim_reset(MdnSim* s) {
     if (rc) return rc;
     const nav::RolloutArgs a = s->args(0);
     HIP_TRY(nav_launch_reset(&a, s->stream));
-    if (s->episodic()) {
-        const nav::EpisodeArgs e = s->episode_args(true);
-        HIP_TRY(nav_launch_episode(&e, s->stream));
-    }
+    // Always, as sim_reset_one writes every env's plant (sim.metal:69): with
+    // per-episode plants, tasks and banks off, the episode kernel writes the
+    // nominal plant, a zero task state and the rehearsal level, so that a bank
+    // or a resume set later starts from the reference's buffers.
+    const nav::EpisodeArgs e = s->episode_args(true);
+    HIP_TRY(nav_launch_episode(&e, s->stream));
     return MDN_OK;
 }
 
@@ -798,6 +802,7 @@ int mdn_ppo_create(MdnSim* s, uint32_t epochs, uint32_t minibatch, MdnPPO** out)
     guard(dev_alloc(&p->norm_stats, 2));
     guard(dev_alloc(&p->metric_rows, size_t(p->updates) * 4));
     guard(dev_alloc(&p->metric_mean, 4));
+    guard(dev_alloc(&p->grad_norm_rows, size_t(p->updates) * 2));
     s->ppo = p;
     if (rc == MDN_OK && hipDeviceSynchronize() != hipSuccess) rc = fail(MDN_E_HIP, "mdn_ppo_create: allocation sync");
     if (rc != MDN_OK) {
@@ -815,7 +820,7 @@ void mdn_ppo_destroy(MdnPPO* p) {
         if (p->sim->ppo == p) p->sim->ppo = nullptr;
     }
     void* bufs[] = {p->am, p->av, p->cm, p->cv, p->part, p->grad, p->mb_rec, p->norm_part, p->norm_stats,
-                    p->metric_rows, p->metric_mean};
+                    p->metric_rows, p->metric_mean, p->grad_norm_rows};
     for (void* b : bufs)
         if (b) hipFree(b);
     delete p;
@@ -894,6 +899,7 @@ int ppo_update(MdnPPO* p, uint32_t rollout_index, bool normalize_rows) {
         aa.actor = s->actor; aa.critic = s->critic; aa.actor_w1t = s->actor_w1t; aa.critic_w1t = s->critic_w1t;
         aa.am = p->am; aa.av = p->av; aa.cm = p->cm; aa.cv = p->cv;
         aa.grad = p->grad; aa.metric_row = p->metric_rows + u * 4;
+        aa.norm_row = p->grad_norm_rows + u * 2;
         aa.lr = s->cfg.learning_rate;
         mdn::adam_corrections(p->optimizer_step, 0.9f, 0.999f, &aa.c1, &aa.c2);
         aa.b = b;
@@ -923,6 +929,46 @@ int mdn_ppo_rollout_update(MdnPPO* p, uint32_t rollout_index) {
     });
     if (rc) return rc;
     return ppo_update(p, rollout_index, true);
+}
+
+}  // extern "C"
+
+namespace {
+// main.mm:1443-1465 over `updates` rows of (actor, critic) pre-clip norms.
+int grad_norm_summary(const float* dev_rows, uint32_t updates, hipStream_t stream, MdnGradNormSummary* out) {
+    HIP_TRY(hipStreamSynchronize(stream));
+    std::vector<float> rows(size_t(updates) * 2);
+    if (!rows.empty()) HIP_TRY(hipMemcpy(rows.data(), dev_rows, rows.size() * 4, hipMemcpyDeviceToHost));
+    const float limit = 0.5f;  // the clip norm of both networks (cpu_reference.hpp:47)
+    MdnGradNormSummary s{};
+    double actor_sum = 0.0, critic_sum = 0.0;
+    uint32_t actor_clipped = 0, critic_clipped = 0;
+    for (uint32_t u = 0; u < updates; u++) {
+        const float a = rows[2 * u], c = rows[2 * u + 1];
+        if (!std::isfinite(a) || !std::isfinite(c)) return fail(MDN_E_STATE, "non-finite pre-clip gradient norm");
+        actor_sum += a;
+        critic_sum += c;
+        actor_clipped += a > limit ? 1u : 0u;
+        critic_clipped += c > limit ? 1u : 0u;
+        s.actor_max = std::max(s.actor_max, a);
+        s.critic_max = std::max(s.critic_max, c);
+    }
+    if (updates > 0) {
+        s.actor_mean = float(actor_sum / double(updates));
+        s.critic_mean = float(critic_sum / double(updates));
+        s.actor_clip_frac = float(actor_clipped) / float(updates);
+        s.critic_clip_frac = float(critic_clipped) / float(updates);
+    }
+    *out = s;
+    return MDN_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int mdn_ppo_grad_norm_summary(MdnPPO* p, MdnGradNormSummary* out) {
+    if (!p || !out) return fail(MDN_E_ARG, "mdn_ppo_grad_norm_summary: null");
+    return grad_norm_summary(p->grad_norm_rows, p->updates, p->sim->stream, out);
 }
 
 int mdn_ppo_metric_mean(MdnPPO* p, float out[4]) {
@@ -1331,6 +1377,7 @@ struct MdnLargePPO {
     double* norm_part = nullptr;
     float* norm_stats = nullptr;
     float *metric_rows = nullptr, *metric_mean = nullptr;
+    float* grad_norm_rows = nullptr;  // [updates][2] pre-clip norms of the last rollout_update
 };
 
 namespace {
@@ -1388,7 +1435,7 @@ void mdn_lppo_destroy(MdnLargePPO* p) {
     void* bufs[] = {p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->xa, p->xaT, p->xc, p->xcT,
                     p->eval_means, p->fwd_part, p->means,
                     p->values, p->dm, p->dls, p->dv, p->loss, p->part, p->ga, p->gc, p->col_part, p->scratch,
-                    p->norm_part, p->norm_stats, p->metric_rows, p->metric_mean};
+                    p->norm_part, p->norm_stats, p->metric_rows, p->metric_mean, p->grad_norm_rows};
     for (void* b : bufs)
         if (b) hipFree(b);
     delete p;
@@ -1442,6 +1489,7 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     guard(dev_alloc(&p->norm_stats, 2));
     guard(dev_alloc(&p->metric_rows, size_t(p->updates) * 4));
     guard(dev_alloc(&p->metric_mean, 4));
+    guard(dev_alloc(&p->grad_norm_rows, size_t(p->updates) * 2));
     if (rc == MDN_OK) {
         std::vector<float> a(A), c(C);
         mdn::init_policy(p->shape, a.data(), c.data());
@@ -1579,7 +1627,7 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
         rc = timed(s, MDN_K_LP_ADAM, [&] {
             return lp_launch_adam(p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->ga, p->gc,
                                   p->scratch, p->col_part, b, H, D, s->cfg.learning_rate, c1, c2, p->metric_rows + u * 4,
-                                  s->stream);
+                                  p->grad_norm_rows + u * 2, s->stream);
         });
         if (rc) return rc;
     }
@@ -1618,6 +1666,11 @@ int mdn_lppo_set_params(MdnLargePPO* p, uint32_t which, const float* host, uint6
         HIP_TRY(hipStreamSynchronize(p->sim->stream));
     }
     return MDN_OK;
+}
+
+int mdn_lppo_grad_norm_summary(MdnLargePPO* p, MdnGradNormSummary* out) {
+    if (!p || !out) return fail(MDN_E_ARG, "mdn_lppo_grad_norm_summary: null");
+    return grad_norm_summary(p->grad_norm_rows, p->updates, p->sim->stream, out);
 }
 
 int mdn_lppo_metric_mean(MdnLargePPO* p, float out[4]) {

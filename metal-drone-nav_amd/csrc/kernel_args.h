@@ -169,6 +169,7 @@ struct AdamArgs {
     float* am; float* av; float* cm; float* cv;
     const float* grad;   // P_TOTAL: actor, critic, metric sums
     float* metric_row;   // [4]
+    float* norm_row;     // [2] pre-clip gradient norms, actor then critic (main.mm:1370-1373)
     float lr, c1, c2;    // host bias corrections 1-beta^step
     uint32_t b;
     uint32_t d;          // actor inputs
@@ -241,7 +242,8 @@ hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16*
 uint64_t lp_backward_part_floats(uint32_t B, uint32_t H, uint32_t d);
 hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
                           __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
-                          uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, hipStream_t st);
+                          uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, float* norm_row,
+                          hipStream_t st);
 uint32_t ppo_partial_stride(uint32_t d);
 // fixed_ppo operators over caller arrays (fixed_ppo.hip)
 hipError_t fppo_launch_forward(const float* w, const float* x, uint32_t D, uint32_t H, uint32_t O, uint32_t prior,

@@ -604,14 +604,17 @@ __global__ __launch_bounds__(256) void sqnorm_kernel(const float* __restrict__ g
     if (t == 0) part[blockIdx.y * NP + s] = red[0];
 }
 // Clip scales min(1, 0.5 / ||g||) of both networks (partials added in slot
-// order) and the update's metric row.
+// order), their pre-clip norms ||g|| = sqrt(|g|^2 + 1e-20) (ppo_grad_norm,
+// main.mm:963-975) and the update's metric row.
 __global__ void norm_finish_kernel(const float* __restrict__ part, const float* __restrict__ metric_sums, uint32_t b,
-                                   float* __restrict__ scale, float* __restrict__ metric_row) {
+                                   float* __restrict__ scale, float* __restrict__ metric_row, float* __restrict__ norm_row) {
     const uint32_t t = threadIdx.x;
     if (t < 2) {
         float s = 0.0f;
         for (uint32_t i = 0; i < NP; i++) s += part[t * NP + i];
-        scale[t] = min_f(1.0f, 0.5f / sqrt_f(s + 1.0e-20f));
+        const float norm = sqrt_f(s + 1.0e-20f);
+        scale[t] = min_f(1.0f, 0.5f / norm);
+        norm_row[t] = norm;
     } else if (t < 6) {
         metric_row[t - 2] = t == 5 ? metric_sums[3] / float(b) : metric_sums[t - 2];
     }
@@ -813,7 +816,8 @@ hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16*
 // col_part as written by lp_launch_backward.
 hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
                           __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
-                          uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, hipStream_t st) {
+                          uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, float* norm_row,
+                          hipStream_t st) {
     if (d != MDN_ACTOR_OBS_POOLED && d != MDN_ACTOR_OBS_PRIOR) return hipErrorInvalidValue;
     const uint32_t PA = H * d + H + 4 * H + 8, PC = H * lp::COBS + 2 * H + 1;
     float* norm_part = scratch;
@@ -822,7 +826,8 @@ hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, flo
     hipLaunchKernelGGL(lp::column_finish_kernel, dim3(13), dim3(64), 0, st, col_part, (B + lp::RB - 1) / lp::RB, H, d,
                        ga, gc, metric_sums);
     hipLaunchKernelGGL(lp::sqnorm_kernel, dim3(lp::NP, 2), dim3(256), 0, st, ga, gc, PA, PC, norm_part);
-    hipLaunchKernelGGL(lp::norm_finish_kernel, dim3(1), dim3(64), 0, st, norm_part, metric_sums, B, scale, metric_row);
+    hipLaunchKernelGGL(lp::norm_finish_kernel, dim3(1), dim3(64), 0, st, norm_part, metric_sums, B, scale, metric_row,
+                       norm_row);
     lp::LargeAdamArgs a;
     a.actor = actor; a.critic = critic; a.am = am; a.av = av; a.cm = cm; a.cv = cv;
     a.actor_wb = awb; a.critic_wb = cwb; a.ga = ga; a.gc = gc; a.scale = scale;

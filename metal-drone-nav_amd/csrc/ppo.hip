@@ -1081,6 +1081,7 @@ __global__ __launch_bounds__(256) void adam_slices_kernel(AdamArgs a) {
     }
     const float norm = sqrt_f(part[0] + 1.0e-20f);
     const float scale = min_f(1.0f, 0.5f / norm);
+    if (i0 == 0 && t == 0) a.norm_row[critic ? 1 : 0] = norm;  // ppo_grad_norm's row (main.mm:963-975)
     const float b1 = 0.9f, b2 = 0.999f;
 #pragma unroll
     for (uint32_t k = 0; k < PER; k++) {

@@ -117,6 +117,12 @@ assert RAPTOR_WEIGHTS.itemsize == 8336 and WORLD.itemsize == 676
 assert SIM_RUN.itemsize == 184 and SIM_CONFIG.itemsize == 84
 
 
+class GradNormSummary(ctypes.Structure):
+    """PPOTrainer::GradNormSummary (main.mm:1439-1442)."""
+    _fields_ = [("actor_mean", ctypes.c_float), ("actor_max", ctypes.c_float), ("actor_clip_frac", ctypes.c_float),
+                ("critic_mean", ctypes.c_float), ("critic_max", ctypes.c_float), ("critic_clip_frac", ctypes.c_float)]
+
+
 class Metrics(ctypes.Structure):
     """cpu_reference::Metrics (cpu_reference.hpp:55-70)."""
     _fields_ = [("wall_seconds", ctypes.c_double), ("updates", ctypes.c_uint64),
@@ -179,7 +185,7 @@ BUFFERS = {
     "critic_m": (21, np.float32), "critic_v": (22, np.float32), "metric_rows": (23, np.float32),
     "next_critic_obs": (24, np.float32), "environment_physics": (25, PHYSICS_PARAMS),
     "task_states": (26, TASK_STATE), "bank_active_ids": (27, np.uint32), "bank_transition_ids": (28, np.uint32),
-    "bank_schedule": (29, np.uint32),
+    "bank_schedule": (29, np.uint32), "grad_norm_rows": (30, np.float32),
 }
 BANK_REHEARSAL = 0xFFFFFFFF
 # moving-threat mix families (include/mdnav_types.h): per env lane n % 4,

@@ -29,7 +29,7 @@ EXPORTS = [
     "mdn_navwid_write", "mdn_op_actor_forward", "mdn_op_critic_forward", "mdn_op_gaussian_log_prob",
     "mdn_op_sample_loss_and_grad", "mdn_op_adam_update", "mdn_op_ppo_self_tests", "mdn_sim_validate_rollout",
     "mdn_checkpoint_read_params", "mdn_op_normalize_noalloc", "mdn_sim_get_bank", "mdn_sim_set_camera",
-    "mdn_sim_get_camera",
+    "mdn_sim_get_camera", "mdn_ppo_grad_norm_summary", "mdn_lppo_grad_norm_summary",
 ]
 
 P = ctypes.c_void_p
@@ -129,6 +129,8 @@ def lib():
         _sig(L, "mdn_checkpoint_read_params", I32, ctypes.c_char_p, P, P, U64, P, U64)
         _sig(L, "mdn_op_normalize_noalloc", I32, P, U64, F32, P)
         _sig(L, "mdn_sim_get_bank", I32, P, P)
+        _sig(L, "mdn_ppo_grad_norm_summary", I32, P, P)
+        _sig(L, "mdn_lppo_grad_norm_summary", I32, P, P)
         _lib = L
     return _lib
 

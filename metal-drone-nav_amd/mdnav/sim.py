@@ -248,6 +248,14 @@ class PPOTrainer:
         check(lib().mdn_ppo_metric_mean(self.h, ptr(out)))
         return out
 
+    def grad_norm_summary(self):
+        """PPOTrainer::grad_norm_summary (main.mm:1443-1465): mean, max and
+        clipped fraction of the last update's pre-clip gradient norms; raises
+        on a non-finite norm."""
+        out = abi.GradNormSummary()
+        check(lib().mdn_ppo_grad_norm_summary(self.h, ctypes.byref(out)))
+        return out
+
     @property
     def optimizer_step(self):
         s = ctypes.c_uint64()
@@ -334,6 +342,12 @@ class LargePPOTrainer:
         check(lib().mdn_lppo_metric_mean(self.h, ptr(out)))
         return out
 
+    def grad_norm_summary(self):
+        """PPOTrainer::grad_norm_summary (main.mm:1443-1465) of the wide policy."""
+        out = abi.GradNormSummary()
+        check(lib().mdn_lppo_grad_norm_summary(self.h, ctypes.byref(out)))
+        return out
+
     @property
     def optimizer_step(self):
         s = ctypes.c_uint64()
@@ -368,6 +382,36 @@ class Trainer:
             setattr(metrics, f, float(runs[f].astype(np.float64).sum()))
         metrics.policy_loss, metrics.value_loss, metrics.entropy_loss, metrics.ratio = (float(x) for x in m)
         return metrics
+
+    def validate_batched_forward(self, tolerance=2.0e-5):
+        """Trainer::validate_batched_forward (cpu_reference.hpp:187-208): the
+        batched GPU forward of the current actor and critic over three
+        synthetic rows (obs[i] = 0.2 sin(0.0037 i), critic obs[i] =
+        0.3 cos(0.17 i)) against a row-by-row evaluation of ppo.hpp:65-93
+        (float64 here); True when every hidden activation, mean and value
+        agrees within `tolerance`."""
+        from . import ops
+        d = int(self.sim.actor_obs)
+        actor = self.sim.get("actor").astype(np.float64)
+        critic = self.sim.get("critic").astype(np.float64)
+        obs = (0.2 * np.sin(np.arange(3 * d, dtype=np.float32) * np.float32(0.0037))).astype(np.float32)
+        co = (0.3 * np.cos(np.arange(3 * 32, dtype=np.float32) * np.float32(0.17))).astype(np.float32)
+        obs, co = obs.reshape(3, d), co.reshape(3, 32)
+        ah, am = ops.actor_forward(actor.astype(np.float32), obs)
+        ch, cv = ops.critic_forward(critic.astype(np.float32), co)
+        H = 64
+        w1, b1 = actor[:H * d].reshape(H, d), actor[H * d:H * d + H]
+        w2, b2 = actor[H * d + H:H * d + 5 * H].reshape(4, H), actor[H * d + 5 * H:H * d + 5 * H + 4]
+        h = np.tanh(obs.astype(np.float64) @ w1.T + b1)
+        mean = h @ w2.T + b2
+        if d == 184:  # the geometry-prior hint of the 184-input actor (ppo.hpp:77)
+            mean[:, :3] += obs[:, d - 3:]
+        cw1, cb1 = critic[:H * 32].reshape(H, 32), critic[H * 32:H * 33]
+        cw2, cb2 = critic[H * 33:H * 34], critic[H * 34]
+        hc = np.tanh(co.astype(np.float64) @ cw1.T + cb1)
+        value = hc @ cw2 + cb2
+        err = max(np.abs(h - ah).max(), np.abs(mean - am).max(), np.abs(hc - ch).max(), np.abs(value - cv).max())
+        return bool(err <= tolerance)
 
     def get(self, name):
         return self.sim.get(name)

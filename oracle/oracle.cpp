@@ -208,7 +208,8 @@ inline float squared_norm(const float* g, size_t count) {
     return part[0];
 }
 // cpu_reference.hpp:553-567 (norm clip then Adam; corrections from the host).
-inline void clip_and_adam(std::vector<float>& grad, float* params, float* m, float* v, uint64_t step, float lr) {
+// Returns the pre-clip norm sqrt(|g|^2 + 1e-20) (ppo_grad_norm, main.mm:963-975).
+inline float clip_and_adam(std::vector<float>& grad, float* params, float* m, float* v, uint64_t step, float lr) {
     const float sum = squared_norm(grad.data(), grad.size());
     const float norm = sqrt_f(sum + 1.0e-20f);
     const float scale = min_f(1.0f, kGradClip / norm);
@@ -221,6 +222,7 @@ inline void clip_and_adam(std::vector<float>& grad, float* params, float* m, flo
         const float mh = m[i] / c1, vh = v[i] / c2;
         params[i] -= lr * mh / (sqrt_f(vh) + kAdamEps);
     }
+    return norm;
 }
 
 // ---- Trainer: cpu_reference.hpp:112-615 + sim.metal semantics ------------
@@ -249,6 +251,7 @@ struct Trainer {
     std::vector<float> obs, co, nco, actions, logp, values, rewards, next_values, advantages, returns;
     std::vector<uint8_t> terminated, truncated;
     std::vector<float> metric_rows;
+    std::vector<float> grad_norm_rows;  // [updates][2] pre-clip norms (main.mm:1370-1373)
     float metric_mean[4] = {0, 0, 0, 0};
     std::vector<float> means, camera;
     // camera profile (sensor_profile.hpp:46-51): legacy unless set_camera
@@ -832,13 +835,13 @@ struct Trainer {
     }
 
     // One minibatch update (main.mm:1349-1378 == cpu_reference.hpp:580-603).
-    void update_minibatch(uint32_t begin, uint32_t b, float* metric_row) {
+    void update_minibatch(uint32_t begin, uint32_t b, float* metric_row, float* norm_row) {
         const PolicyShape& S = shape;
         std::vector<float> ag, cg;
         minibatch_grads(begin, b, ag, cg, metric_row);
         ++optimizer_step;
-        clip_and_adam(ag, actor.data(), actor_m.data(), actor_v.data(), optimizer_step, cfg.learning_rate);
-        clip_and_adam(cg, critic.data(), critic_m.data(), critic_v.data(), optimizer_step, cfg.learning_rate);
+        norm_row[0] = clip_and_adam(ag, actor.data(), actor_m.data(), actor_v.data(), optimizer_step, cfg.learning_rate);
+        norm_row[1] = clip_and_adam(cg, critic.data(), critic_m.data(), critic_v.data(), optimizer_step, cfg.learning_rate);
         for (uint32_t a = 0; a < 4; a++) {
             float& x = actor[S.actor_log_std() + a];
             x = clamp_f(x, -2.0f, .5f);
@@ -851,10 +854,11 @@ struct Trainer {
         const uint32_t rows = cfg.n * horizon;
         const std::vector<uint32_t> order = minibatch_schedule(rows, minibatch, epochs, rollout_index);
         metric_rows.assign(order.size() * 4, 0.0f);
+        grad_norm_rows.assign(order.size() * 2, 0.0f);
         for (size_t u = 0; u < order.size(); u++) {
             const uint32_t begin = order[u];
             const uint32_t b = std::min(minibatch, rows - begin);
-            update_minibatch(begin, b, &metric_rows[u * 4]);
+            update_minibatch(begin, b, &metric_rows[u * 4], &grad_norm_rows[u * 2]);
         }
         // main.mm:952-962
         for (int k = 0; k < 4; k++) metric_mean[k] = 0.0f;
@@ -1048,6 +1052,7 @@ void* orc_trainer_buffer(void* hp, uint32_t id, uint64_t* bytes) {
         case 27: return ret(t->bank_active);
         case 28: return ret(t->bank_transition);
         case 29: return ret(t->bank_schedule);
+        case 30: return ret(t->grad_norm_rows);
         default: *bytes = 0; return nullptr;
     }
 }

@@ -32,9 +32,17 @@ int main(int argc, char** argv) {
     const uint32_t rollouts = argc > 3 ? uint32_t(std::atoi(argv[3])) : 2;
     try {
         mdnav::Trainer trainer(cfg, 32, raptor, mdn::crazyflie_params());
+        // cpu_reference_benchmark checks the batched forward before training (main.mm:491)
+        std::printf("validate_batched_forward=%d strict=%d\n", int(trainer.validate_batched_forward()),
+                    int(trainer.validate_batched_forward(1e-9f)));
         const MdnMetrics m = trainer.run(rollouts);
         std::printf("envs=%u rollouts=%u wall_s=%.4f updates=%llu episodes=%llu ratio=%.4f\n", cfg.n, rollouts,
                     m.wall_seconds, (unsigned long long)m.updates, (unsigned long long)m.episodes, m.ratio);
+        const mdnav::PPOTrainer::GradNormSummary g = trainer.ppo.grad_norm_summary();
+        std::printf("grad_norm actor_mean=%.9g actor_max=%.9g actor_clip_frac=%.9g critic_mean=%.9g "
+                    "critic_max=%.9g critic_clip_frac=%.9g\n",
+                    g.actor_mean, g.actor_max, g.actor_clip_frac, g.critic_mean, g.critic_max, g.critic_clip_frac);
+        trainer.sim.report("facade-train", 0);
     } catch (const std::exception& e) {
         std::fprintf(stderr, "ERROR: %s\n", e.what());
         return 1;

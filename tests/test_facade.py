@@ -37,14 +37,71 @@ def test_facade_loads_deployed_policy():
     assert r.returncode == 1 and "magic mismatch" in r.stderr, r.stderr
 
 
+def grad_norm_summary(rows, limit=0.5):
+    """main.mm:1443-1465 over [updates][2] pre-clip norms (double sums)."""
+    import numpy as np
+    rows = np.asarray(rows, np.float32).reshape(-1, 2)
+    out = {}
+    for k, name in enumerate(("actor", "critic")):
+        col = rows[:, k]
+        acc = 0.0  # a sequential double sum, as the reference takes it
+        for x in col:
+            acc += float(x)
+        out[name + "_mean"] = np.float32(acc / len(col))
+        out[name + "_max"] = np.float32(max(0.0, float(col.max())))
+        out[name + "_clip_frac"] = np.float32(np.float32(int((col > np.float32(limit)).sum())) / np.float32(len(col)))
+    return out
+
+
+def report_line(label, runs, wall=0):
+    """Sim::report's line (main.mm:599-602), formatted as std::ostream prints
+    doubles (six significant digits)."""
+    import numpy as np
+    ep, succ = int(runs["episodes"].sum()), int(runs["successes"].sum())
+    time_ = runs["success_time"].astype(np.float64).sum()
+    path, total = runs["total_path"].astype(np.float64).sum(), runs["total_elapsed"].astype(np.float64).sum()
+    progress = runs["final_progress"].astype(np.float64).sum()
+    clearance = float(min(np.float32(12), runs["min_clearance"].min()))
+    peak = float(max(np.float32(0), runs["peak_speed"].max()))
+    g = lambda x: "%g" % x
+    return ("%s episodes=%d success=%s collision=%s timeout=%s progress=%s mean_goal_time=%s mean_speed=%s "
+            "peak_speed=%s min_clearance=%s wall_s=%s" % (
+                label, ep, g(succ / ep if ep else 0), g(int(runs["collisions"].sum()) / ep if ep else 0),
+                g(int(runs["timeouts"].sum()) / ep if ep else 0), g(progress / ep if ep else 0),
+                g(time_ / succ if succ else 0), g(path / total if total else 0), g(peak), g(clearance), g(wall)))
+
+
 @pytest.mark.gpu
 def test_facade_trains_on_gpu():
+    """cpu_reference_benchmark's use of the façade (main.mm:478-509):
+    Trainer::validate_batched_forward before training (true at the reference's
+    2e-5, false at 1e-9: the GPU forward is not the scalar one), run(2), then
+    PPOTrainer::grad_norm_summary and Sim::report, both equal to the oracle's
+    replay of the same two iterations (the GPU path is bit-exact, so the
+    summary's floats and the report's text match exactly)."""
+    import numpy as np
+    from mdnav import abi
+    from oracle_lib import OracleTrainer, raptor_fixture
     exe = build_example()
     print("case: facade example 256 envs x 2 rollouts", flush=True)
     r = subprocess.run([exe, os.path.join(ROOT, "tests", "golden", "raptor.bin"), "256", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     assert "updates=128" in r.stdout, r.stdout  # 2 rollouts x 2 epochs x 32 minibatches
+    assert "validate_batched_forward=1 strict=0" in r.stdout, r.stdout
+    print("case: oracle replay of the facade run", flush=True)
+    ora = OracleTrainer(abi.default_config(n=256, family=1, speed=1.0, distance=3.0), 32, raptor_fixture()[0],
+                        epochs=2, minibatch=256)
+    for it in range(2):
+        ora.iteration(it)
+    want = grad_norm_summary(ora.get("grad_norm_rows"))
+    line = [l for l in r.stdout.splitlines() if l.startswith("grad_norm ")][0]
+    got = dict(kv.split("=") for kv in line.split()[1:])
+    for k, v in want.items():
+        assert np.float32(got[k]) == v, (k, got[k], v)
+    assert 0 < want["actor_mean"] and 0 <= want["actor_clip_frac"] <= 1
+    rep = [l for l in r.stdout.splitlines() if l.startswith("facade-train ")]
+    assert rep == [report_line("facade-train", ora.get("runs"))], (rep, report_line("facade-train", ora.get("runs")))
 
 
 TRAIN_SRC = os.path.join(ROOT, "tests", "cpp", "training_example.cpp")

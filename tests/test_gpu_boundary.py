@@ -199,3 +199,119 @@ def test_checkpoint_params_reader():
     na, nc = int(h["actor_count"]), int(h["critic_count"])
     assert na == 12104 and nc == 2177
     assert a.tobytes() == data[136:136 + 4 * na] and c.tobytes() == data[136 + 4 * na:136 + 4 * (na + nc)]
+
+
+# ---------------------------------------------------------------- PPOTrainer::grad_norm_summary
+@pytest.mark.gpu
+def test_grad_norm_rows_and_summary():
+    """The pre-clip gradient norms of every update (grad_norm_rows,
+    main.mm:1370-1373) equal the oracle's bit for bit, for the one-chunk path
+    (256-row minibatches) and the chunked path (1,024 rows), and
+    grad_norm_summary (main.mm:1443-1465) is their mean, maximum and
+    clipped fraction."""
+    from gpu_compare import config, make_pair
+    from test_facade import grad_norm_summary
+    for mb in (256, 1024):
+        say("case: grad-norm rows, N=64 T=32 minibatch %d" % mb)
+        cfg = config(n=64, family=1, speed=1.0, distance=3.0, max_steps=25)
+        sim, ppo, ora = make_pair(cfg, 32, epochs=2, minibatch=mb)
+        try:
+            for it in range(2):
+                sim.collect()
+                ppo.rollout_update(it)
+                ora.iteration(it)
+                rows, want = sim.get("grad_norm_rows"), ora.get("grad_norm_rows")
+                assert rows.shape == (ppo.updates_per_rollout * 2,) and np.array_equal(rows, want), it
+            s = ppo.grad_norm_summary()
+            w = grad_norm_summary(want)
+            for k, v in w.items():
+                assert np.float32(getattr(s, k)) == v, (k, getattr(s, k), v)
+            assert s.actor_max >= s.actor_mean > 0 and s.critic_max >= s.critic_mean > 0
+        finally:
+            ppo.close()
+            sim.close()
+
+
+@pytest.mark.gpu
+def test_grad_norm_summary_rejects_non_finite():
+    """A NaN reward reaches the gradients through GAE and the loss: the
+    summary raises the reference's "non-finite pre-clip gradient norm"
+    (main.mm:1451).  The kernels only carry the NaN as a value."""
+    from gpu_compare import config, make_pair
+    from mdnav.native import MdnError
+    say("case: grad-norm summary with a NaN gradient")
+    cfg = config(n=64, family=1, speed=1.0, distance=3.0, max_steps=25)
+    sim, ppo, _ = make_pair(cfg, 16, epochs=1, minibatch=256)
+    try:
+        s0 = ppo.grad_norm_summary()  # before any update: all zero
+        assert (s0.actor_mean, s0.actor_max, s0.critic_clip_frac) == (0, 0, 0)
+        sim.collect()
+        r = sim.get("rewards")
+        r[5] = np.nan
+        sim.set("rewards", r)
+        ppo.rollout_update(0)
+        with pytest.raises(MdnError, match="non-finite pre-clip gradient norm"):
+            ppo.grad_norm_summary()
+    finally:
+        ppo.close()
+        sim.close()
+
+
+@pytest.mark.gpu
+def test_wide_policy_grad_norm_summary():
+    """The wide policy's pre-clip norms (H = 256, bf16 products) against the
+    oracle's fp32 update of the same rollout: means and maxima within 2 %,
+    equal clipped fractions where no norm sits within 0.01 of the limit."""
+    from gpu_compare import config, make_pair
+    from mdnav import LargePPOTrainer
+    from test_facade import grad_norm_summary
+    say("case: wide-policy grad-norm summary, H=256 N=64 T=32")
+    cfg = config(n=64, family=1, speed=1.0, distance=3.0, max_steps=25)
+    sim, _, ora = make_pair(cfg, 32, epochs=1, minibatch=512)
+    sim.collect()
+    sim.sync()
+    ora.collect()
+    lp = LargePPOTrainer(sim, 256, epochs=1, minibatch=512)
+    ora.set_hidden(256)
+    try:
+        lp.evaluate()
+        sim.sync()
+        for name in ("logp", "values", "next_values"):
+            ora.set(name, sim.get(name))
+        lp.rollout_update(0)
+        ora.gae()
+        ora.normalize()
+        ora.update(0)
+        s = lp.grad_norm_summary()
+        want = grad_norm_summary(ora.get("grad_norm_rows"))
+        say("  gpu %s / oracle %s" % ({k: getattr(s, k) for k in want}, want))
+        for k in ("actor_mean", "actor_max", "critic_mean", "critic_max"):
+            assert abs(getattr(s, k) - want[k]) <= 0.02 * want[k], (k, getattr(s, k), want[k])
+        rows = ora.get("grad_norm_rows").reshape(-1, 2)
+        for k, name in enumerate(("actor", "critic")):
+            if np.all(np.abs(rows[:, k] - 0.5) > 0.01):
+                assert np.float32(getattr(s, name + "_clip_frac")) == want[name + "_clip_frac"], name
+    finally:
+        lp.close()
+        sim.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("d", [181, 184])
+def test_trainer_validate_batched_forward(d):
+    """Trainer::validate_batched_forward (cpu_reference.hpp:187-208) on the
+    freshly initialised policy and after an update: true at the reference's
+    2e-5, false at 1e-9 (the GPU's fma chains and tanh are not float64's)."""
+    from gpu_compare import config
+    from mdnav import Trainer
+    from oracle_lib import raptor_fixture
+    say("case: validate_batched_forward, %d inputs" % d)
+    t = Trainer(config(n=32, family=1, speed=1.0, distance=3.0), 16, raptor=raptor_fixture()[0], actor_obs=d)
+    try:
+        assert t.validate_batched_forward()
+        assert not t.validate_batched_forward(1e-9)
+        t.run(1)
+        assert t.validate_batched_forward()
+    finally:
+        t.ppo.close()
+        t.sim.close()

@@ -297,3 +297,50 @@ def test_bank_training_resets_bit_exact(with_plants):
             k, int(sim.get("runs")["episodes"].sum()), np.unique(ids).size, bad))
         assert not bad, (k, bad)
     assert np.unique(sim.get("bank_transition_ids")).size >= 10
+
+
+def test_bank_checkpoint_resume_bit_exact(tmp_path):
+    """Save and resume with a challenge bank active (a bank alone writes
+    PPOFIX1 version 6, main.mm:1254-1257, 1292-1293): the resumed GPU trainer
+    holds the saved state, and it and the oracle resumed from the same file
+    continue bit for bit through bank resets, rehearsal slots and out-of-range
+    ids.  The file carries no level ids (main.mm:1302-1306), so both resume
+    with the default active level."""
+    from mdnav import load_bank
+    say("case: bank checkpoint save/resume")
+    levels = load_bank(os.path.join(GOLDEN, "bank", "challenge-bank-v1-dev.jsonl"), "dev")[:12]
+    worlds = np.array([lv["world"] for lv in levels], abi.WORLD)
+    n, horizon = 64, 16
+    rng = np.random.default_rng(11)
+    schedule = rng.integers(0, 14, size=(n, horizon + 1)).astype(np.uint32)
+    schedule[rng.uniform(size=schedule.shape) < 0.25] = abi.BANK_REHEARSAL
+    cfg = config(n=n, family=0, seed=5, max_steps=9, geometry_memory=1, speed=1.5, distance=8.0)
+    sim, ppo, _ = make_pair(cfg, horizon, epochs=1, minibatch=256, actor_obs=184)
+    sim.set_bank(worlds, schedule)
+    sim.reset()
+    for r in range(2):
+        sim.collect()
+        ppo.rollout_update(r)
+    path = str(tmp_path / "bank.bin")
+    ppo.save_checkpoint(path, 0, 5, 2)
+    h, _ = formats.read_checkpoint(path)
+    assert int(h["version"]) == 6
+    sim2, ppo2, ora = make_pair(cfg, horizon, epochs=1, minibatch=256, actor_obs=184)
+    sim2.set_bank(worlds, schedule)
+    ora.set_bank(worlds, schedule)
+    assert ppo2.load_checkpoint(path, 0, horizon, n, 5) == 2
+    ora.load_checkpoint(path)
+    params = ["actor", "critic", "actor_m", "actor_v", "critic_m", "critic_v"]
+    bad = compare(sim2, sim, ENV_BUFFERS + params)
+    assert not bad, ("resumed state", bad)
+    bad = compare(sim2, ora, ENV_BUFFERS + params)
+    assert not bad, ("oracle resume", bad)
+    for r in (2, 3):
+        sim2.collect()
+        ppo2.rollout_update(r)
+        sim2.sync()
+        ora.iteration(r)
+        bad = compare(sim2, ora, ENV_BUFFERS + ROW_BUFFERS + params + ["advantages", "returns", "bank_active_ids",
+                                                                      "bank_transition_ids"])
+        assert not bad, (r, bad)
+    assert int(sim2.get("runs")["episodes"].sum()) > n
