@@ -325,8 +325,11 @@ int mdn_op_normalize(float* advantages, uint64_t count, float epsilon);
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): mdn_op_normalize on `count` advantages already in device
- * memory, normalised in place, enqueued on `stream` (a hipStream_t; NULL for
- * the default stream) and not waited for.  It allocates nothing: the
+ * memory, normalised in place, enqueued on `stream` (a hipStream_t of the
+ * current device; NULL for its default stream) and not waited for.  The
+ * scratch is the current device's; its address is resolved once per device,
+ * so like every device pointer of the library it does not survive a
+ * hipDeviceReset.  It allocates nothing: the
  * statistics' scratch is a fixed array in the library (64 KiB per GPU,
  * held until the process ends) and `count` may not exceed
  * MDN_NORMALIZE_NOALLOC_MAX (MDN_E_ARG otherwise).  Calls on one GPU share

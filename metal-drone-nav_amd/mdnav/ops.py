@@ -64,11 +64,19 @@ def normalize(advantages, eps=1e-8):
 
 
 # ---------------------------------------------------------------- fixed_ppo operators (ppo.hpp:65-324)
+def _need(name, arr, size):
+    """The C call reads exactly `size` floats of `arr`: refuse any other size
+    before it reads past a numpy buffer."""
+    if arr.size != size:
+        raise ValueError("%s has %d values, expected %d" % (name, arr.size, size))
+
+
 def actor_forward(params, obs, hidden_dim=64):
     """fixed_ppo::actor_forward over rows of obs[batch][D]: (hidden, means)."""
     x = contiguous(obs, np.float32)
     x = x.reshape(-1, x.shape[-1])
     w = contiguous(params, np.float32).reshape(-1)
+    _need("actor params", w, hidden_dim * x.shape[1] + 5 * hidden_dim + 8)
     h = np.zeros((len(x), hidden_dim), np.float32)
     m = np.zeros((len(x), 4), np.float32)
     check(lib().mdn_op_actor_forward(ptr(w), x.shape[1], hidden_dim, ptr(x), len(x), ptr(h), ptr(m)))
@@ -80,6 +88,7 @@ def critic_forward(params, obs, hidden_dim=64):
     x = contiguous(obs, np.float32)
     x = x.reshape(-1, x.shape[-1])
     w = contiguous(params, np.float32).reshape(-1)
+    _need("critic params", w, hidden_dim * x.shape[1] + 2 * hidden_dim + 1)
     h = np.zeros((len(x), hidden_dim), np.float32)
     v = np.zeros(len(x), np.float32)
     check(lib().mdn_op_critic_forward(ptr(w), x.shape[1], hidden_dim, ptr(x), len(x), ptr(h), ptr(v)))
@@ -87,13 +96,17 @@ def critic_forward(params, obs, hidden_dim=64):
 
 
 def _log_std(log_std, rows):
+    """A shared [4] log-std (stride 0) or one per row [rows][4] (stride 4)."""
     ls = contiguous(log_std, np.float32)
+    if ls.size != 4 and ls.size != 4 * rows:
+        raise ValueError("log_std has %d values, expected 4 or %d" % (ls.size, 4 * rows))
     return ls.reshape(-1), (0 if ls.size == 4 else 4)
 
 
 def gaussian_log_prob(actions, means, log_std):
     a = contiguous(actions, np.float32).reshape(-1, 4)
     m = contiguous(means, np.float32).reshape(-1, 4)
+    _need("means", m, a.size)
     ls, stride = _log_std(log_std, len(a))
     out = np.zeros(len(a), np.float32)
     check(lib().mdn_op_gaussian_log_prob(ptr(a), ptr(m), ptr(ls), stride, len(a), ptr(out)))
@@ -107,9 +120,12 @@ def sample_loss_and_grad(actions, means, log_std, old_logp, values, advantages, 
     a = contiguous(actions, np.float32).reshape(-1, 4)
     b = len(a)
     m = contiguous(means, np.float32).reshape(-1, 4)
+    _need("means", m, a.size)
     ls, stride = _log_std(log_std, b)
     ol, v, adv, ret = (contiguous(x, np.float32).reshape(-1) for x in (old_logp, values, advantages, returns))
     ov = v if old_values is None else contiguous(old_values, np.float32).reshape(-1)
+    for name, x in (("old_logp", ol), ("values", v), ("advantages", adv), ("returns", ret), ("old_values", ov)):
+        _need(name, x, b)
     dm, dl = np.zeros((b, 4), np.float32), np.zeros((b, 4), np.float32)
     dv, loss = np.zeros(b, np.float32), np.zeros((b, 4), np.float32)
     check(lib().mdn_op_sample_loss_and_grad(ptr(a), ptr(m), ptr(ls), stride, ptr(ol), ptr(ov), ptr(v), ptr(adv),
@@ -121,6 +137,8 @@ def sample_loss_and_grad(actions, means, log_std, old_logp, values, advantages, 
 def adam_update(params, grad, first, second, step, lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0):
     """fixed_ppo::adam_update; returns updated (params, first, second) copies."""
     p, g, m, v = (contiguous(x, np.float32).reshape(-1).copy() for x in (params, grad, first, second))
+    for name, x in (("grad", g), ("first", m), ("second", v)):
+        _need(name, x, p.size)
     check(lib().mdn_op_adam_update(ptr(p), ptr(g), ptr(m), ptr(v), len(p), step, lr, beta1, beta2, eps,
                                    weight_decay))
     return p, m, v

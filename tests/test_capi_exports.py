@@ -5,6 +5,7 @@ import os
 import re
 
 import numpy as np
+import pytest
 
 from mdnav import abi, native
 from oracle_lib import crazyflie, oracle, ptr
@@ -51,3 +52,26 @@ def test_error_path_without_gpu_call():
     assert rc == -1 and b"null" in lib.mdn_last_error()
     rc = lib.mdn_ppo_create(None, 2, 256, ctypes.byref(out))
     assert rc == -1
+
+
+def test_operator_wrappers_refuse_wrong_sizes():
+    """The fixed_ppo wrappers check every array against the shape the C call
+    reads, before any call (no GPU needed): a params vector of another
+    layout, a log_std neither shared nor per row, short per-row arrays."""
+    import numpy as np
+    from mdnav import ops
+    obs = np.zeros((3, 181), np.float32)
+    with pytest.raises(ValueError, match="actor params"):
+        ops.actor_forward(np.zeros(64 * 181 + 5 * 64 + 7, np.float32), obs)
+    with pytest.raises(ValueError, match="critic params"):
+        ops.critic_forward(np.zeros(64 * 32 + 2 * 64, np.float32), np.zeros((3, 32), np.float32))
+    a = np.zeros((5, 4), np.float32)
+    with pytest.raises(ValueError, match="log_std"):
+        ops.gaussian_log_prob(a, a, np.zeros(6, np.float32))
+    with pytest.raises(ValueError, match="means"):
+        ops.gaussian_log_prob(a, np.zeros((4, 4), np.float32), np.zeros(4, np.float32))
+    with pytest.raises(ValueError, match="advantages"):
+        ops.sample_loss_and_grad(a, a, np.zeros(4, np.float32), np.zeros(5), np.zeros(5), np.zeros(4),
+                                 np.zeros(5), 5)
+    with pytest.raises(ValueError, match="second"):
+        ops.adam_update(np.zeros(10), np.zeros(10), np.zeros(10), np.zeros(9), 1, 1e-3)

@@ -22,9 +22,19 @@ def test_noalloc_rejects_oversize():
     assert lib.mdn_op_normalize_noalloc(None, 10, 1e-8, None) == -1
 
 
+def loaded_hip_runtime():
+    """Path of the HIP runtime this process mapped when it loaded libmdnav.so
+    (from /proc/self/maps), so the test's own HIP calls go to that runtime
+    whatever its version suffix."""
+    native.lib()
+    with open("/proc/self/maps") as f:
+        paths = {line.split()[-1] for line in f if "libamdhip64.so" in line}
+    assert len(paths) == 1, paths
+    return paths.pop()
+
+
 def hip_runtime():
-    native.lib()  # loads libmdnav.so and with it the HIP runtime it links
-    hip = ctypes.CDLL("libamdhip64.so.7", mode=ctypes.RTLD_GLOBAL)
+    hip = ctypes.CDLL(loaded_hip_runtime(), mode=ctypes.RTLD_GLOBAL)
     for name, args in (("hipMalloc", [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]),
                        ("hipFree", [ctypes.c_void_p]),
                        ("hipMemcpy", [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]),
