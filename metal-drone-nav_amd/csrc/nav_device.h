@@ -273,6 +273,127 @@ __device__ __forceinline__ float strip_depth(const float (&SA)[9][3], const floa
         if ((m >> i) & 1u) best = __builtin_fminf(best, slab_fast(SA[i + 1], SB[i + 1], inv));
     return fmax_f(0.0f, best);
 }
+// Strip-culled cast of any world (boxes, spheres, bounded movers and capped
+// cylinders; up to 16 obstacles), the wavefront casting one env's frame at a
+// time as for boxes.  Per env and frame the env's lane group tabulates every
+// obstacle with the per-obstacle constants of world.hpp:42-70, formed with
+// the reference's operations (box: -e - pp and e - pp; sphere: q = p - c and
+// q.q - r*r; cylinder: q, q.x^2 + q.y^2 - r*r, half height, r*r), and marks
+// the 4-column strips its bounding box can reach (box_strips).  Per ray only
+// the strip's obstacles are tested, by kind, with the operations of
+// cast_ray, so each hit value is cast_ray's.
+// A strip leaves out an obstacle only when a plane separates its bounding box
+// from every ray of the strip by more than 2e-3 m, or when it lies beyond
+// 12.01 m.  For a box that gives a miss or a value of at least 12 (above).
+// For a sphere or cylinder of radius r the exact discriminant of such a ray is
+// below -(0.004 r + 4e-6), while its fp32 rounding error is at most about
+// 4e-5 (terms up to 12.5^2 = 156, a few ulps of 2^-23 each), so the computed
+// discriminant stays negative when r >= 0.05 m; the cap test's point lies
+// at least 2e-3 m outside the cap disk, again above its rounding error.
+// Worlds with a smaller radius take the per-lane cast below.
+// Table words: room slab 0-5, obstacle i at 6 + 6 i, then the ray origin,
+// the camera rotation, strip masks (bit 16 (st % 2) + i of word st / 2) and
+// two kind bits per obstacle (0 box, 1 sphere, 2 cylinder).
+constexpr uint32_t STRIP_TABLE_ORIGIN = 102, STRIP_TABLE_ROT = 105, STRIP_TABLE_MASKS = 114,
+                   STRIP_TABLE_KINDS = 117, STRIP_TABLE_WORDS = 118;
+constexpr float STRIP_MIN_RADIUS = 0.05f;
+__device__ __forceinline__ bool strip_castable(const float* world, uint32_t count) {
+    if (count > 16) return false;
+    bool ok = true;
+    for (uint32_t i = 0; i < count; i++) {
+        const uint32_t kind = float_bits(world[10 * i]);
+        ok = ok && kind <= 3u && (kind == 0u || world[10 * i + 4] >= STRIP_MIN_RADIUS);
+    }
+    return ok;
+}
+// Obstacle i's table entry `e` (6 words) for origin p, its kind code and its
+// bounding box relative to p (A = low corner, B = high corner).
+__device__ __forceinline__ uint32_t strip_entry(const float* world, const float* centers, uint32_t i, V p, float* e,
+                                                float (&A)[3], float (&B)[3]) {
+    const float* o = world + 10 * i;
+    const uint32_t kind = float_bits(o[0]);
+    const V c = mk(centers[3 * i], centers[3 * i + 1], centers[3 * i + 2]);
+    const float pp[3] = {p.x - c.x, p.y - c.y, p.z - c.z};
+    if (kind == 0u) {  // world.hpp:53
+#pragma unroll
+        for (int j = 0; j < 3; j++) { A[j] = -o[4 + j] - pp[j]; B[j] = o[4 + j] - pp[j]; e[j] = A[j]; e[3 + j] = B[j]; }
+        return 0u;
+    }
+    const V q = sub3(p, c);
+    const float r = o[4];
+    const float ext[3] = {r, r, kind == 2u ? o[6] : r};
+#pragma unroll
+    for (int j = 0; j < 3; j++) { A[j] = -ext[j] - pp[j]; B[j] = ext[j] - pp[j]; }
+    e[0] = q.x; e[1] = q.y; e[2] = q.z;
+    if (kind == 2u) {  // world.hpp:60
+        e[3] = q.x * q.x + q.y * q.y - r * r;
+        e[4] = o[6];
+        e[5] = r * r;
+        return 2u;
+    }
+    e[3] = dot3(q, q) - r * r;  // world.hpp:43 (kinds 1 and 3)
+    return 1u;
+}
+// Depth along d (every component at least the slab epsilon in magnitude)
+// over the room (RA, RB) and the obstacles of the wavefront-uniform strip
+// mask m16 of the env table et; kinds holds two bits per obstacle.  The next
+// entry's words are read while the current obstacle is tested.
+__device__ __forceinline__ float strip_depth_mixed(const float* et, V d, uint32_t m16, uint32_t kinds,
+                                                   const float (&RA)[3], const float (&RB)[3]) {
+    const float inv[3] = {recip_rn(d.x), recip_rn(d.y), recip_rn(d.z)};
+    float best = __builtin_fminf(12.0f, slab_fast(RA, RB, inv));
+    const float a = d.x * d.x + d.y * d.y;
+    const bool caps = fabs_f(d.z) > 1e-8f;
+    uint32_t m = m16;
+    float cur[6] = {0, 0, 0, 0, 0, 0};
+    uint32_t ci = m ? uint32_t(__builtin_ctz(m)) : 0u;
+    if (m) {
+#pragma unroll
+        for (int j = 0; j < 6; j++) cur[j] = et[6 + 6 * ci + j];
+    }
+    while (m) {
+        m &= m - 1u;
+        const uint32_t ni = m ? uint32_t(__builtin_ctz(m)) : ci;
+        float nxt[6];
+#pragma unroll
+        for (int j = 0; j < 6; j++) nxt[j] = et[6 + 6 * ni + j];
+        const uint32_t kind = (kinds >> (2u * ci)) & 3u;
+        float t;
+        if (kind == 0u) {
+            const float A[3] = {cur[0], cur[1], cur[2]}, B[3] = {cur[3], cur[4], cur[5]};
+            t = slab_fast(A, B, inv);
+        } else if (kind == 1u) {  // hit_sphere (world.hpp:42-47)
+            const V q = mk(cur[0], cur[1], cur[2]);
+            const float b = dot3(q, d), disc = b * b - cur[3];
+            const float root = sqrt_f(disc);
+            const float lo = -b - root, hi = -b + root;
+            t = disc < 0 ? 1000.0f : (lo >= 0 ? lo : (hi >= 0 ? hi : 1000.0f));
+        } else {  // hit_cylinder (world.hpp:58-70)
+            const V q = mk(cur[0], cur[1], cur[2]);
+            const float k = cur[3], h = cur[4], rr = cur[5];
+            const float b = q.x * d.x + q.y * d.y;
+            const float disc = b * b - a * k;
+            t = 1000.0f;
+            if (a > 1e-10f && disc >= 0) {
+                const float r0 = (-b - sqrt_f(disc)) / a, r1 = (-b + sqrt_f(disc)) / a;
+                if (r0 >= 0 && fabs_f(q.z + r0 * d.z) <= h) t = fmin_f(t, r0);
+                if (r1 >= 0 && fabs_f(q.z + r1 * d.z) <= h) t = fmin_f(t, r1);
+            }
+            if (caps)
+                for (int sign = -1; sign <= 1; sign += 2) {
+                    const float tc = (float(sign) * h - q.z) / d.z;
+                    const float x = q.x + tc * d.x, y = q.y + tc * d.y;
+                    if (tc >= 0 && x * x + y * y <= rr) t = fmin_f(t, tc);
+                }
+        }
+        best = __builtin_fminf(best, t);
+        ci = ni;
+#pragma unroll
+        for (int j = 0; j < 6; j++) cur[j] = nxt[j];
+    }
+    return fmax_f(0.0f, best);
+}
+
 // Fast path of cast_ray for worlds of up to 16 boxes, 8 spheres (kinds 1 and
 // 3) and 8 capped cylinders when no ray direction component is below the slab
 // epsilon.  Per env and frame the obstacles are tabulated in the env's LDS

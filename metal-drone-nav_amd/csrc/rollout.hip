@@ -810,6 +810,8 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         // observation row is free until observe and holds the tables.
         const bool boxes = boxes_only(world, count);
         const bool wave_boxes = !__any(depth_now && !boxes);
+        // else: every casting env's world tabulated for the strip-culled cast
+        const bool wave_strips = !wave_boxes && !__any(depth_now && !strip_castable(world, count));
         const float mx = a.mount_x;  // sim.metal:149-152
         const V origin = mk(s.p[0] + mx * R[0], s.p[1] + mx * R[3], s.p[2] + mx * R[6]);
         if (depth_now && lane == 0) {
@@ -821,12 +823,48 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
         MixCounts mix{0, 0, 0};
         bool mix_ok = false;
         uint32_t NB = 0, NS = 0, NC = 0;
-        if (!wave_boxes) {  // table sizes: the largest counts among the wavefront's casting envs
+        if (!wave_boxes && !wave_strips) {  // table sizes: the largest counts among the wavefront's casting envs
             if (depth_now) mix_ok = mix_counts(world, count, mix);
             NB = wave_max_u32(mix_ok ? mix.nb : 0u);
             NS = wave_max_u32(mix_ok ? mix.ns : 0u);
             NC = wave_max_u32(mix_ok ? mix.nc : 0u);
         }
+        // Wavefront casts (boxes-only or strip tables): lane l takes ray
+        // q = l % 4 of block l / 4 of each strip (2 blocks across, 8 down);
+        // the env's five depths (one per strip) pass through depth noise and
+        // dropout into its sensor ring, and their 2x2 minima into its pooled
+        // ring (sim.metal:145-158).
+        constexpr uint32_t EW = 64 / G;  // envs per wavefront
+        const uint32_t wl = threadIdx.x % 64, wbase = (threadIdx.x / 64) * EW;
+        const uint32_t q4 = wl % 4, jb = wl / 4, by = jb / 2, k0 = (2 * by + q4 / 2) * 20 + 2 * (jb % 2) + q4 % 2;
+        auto emit_frame = [&](uint32_t ge, uint32_t ne, uint32_t steps_e, uint32_t rng_e, float (&dep)[5]) {
+            const uint32_t fidx = steps_e / C.sensor_period;
+            const uint32_t slot8 = fidx % 8, slotk = fidx % K;
+            const float noise = clean_env(C, ne) ? 0.0f : C.depth_noise;
+            const float drop = clean_env(C, ne) ? 0.0f : C.dropout;
+            float* ring = a.sensors + (size_t(ne) * 8 + slot8) * PIX;
+            if (noise != 0 || drop != 0) {
+#pragma unroll
+                for (uint32_t st = 0; st < 5; st++) {
+                    uint32_t nr = rng_e + (k0 + 4 * st) * 1664525u + steps_e * 1013904223u;
+                    dep[st] = clamp_f(dep[st] + noise * normal_draw(nr), 0.0f, 12.0f);
+                    if (ur(nr) < drop) dep[st] = 12.0f;
+                }
+            }
+#pragma unroll
+            for (uint32_t st = 0; st < 5; st++) {
+                const float depth = dep[st];
+                ring[k0 + 4 * st] = depth;
+                // pooled 2x2 minimum over the quad's lanes (values in [0, 12],
+                // never NaN); after the two swaps every lane of the quad holds
+                // it, and all four store it (one value to one address)
+                float pooled = min_f(depth, bits_float(uint32_t(
+                                                __builtin_amdgcn_update_dpp(0, int(float_bits(depth)), 0xB1, 0xF, 0xF, false))));
+                pooled = min_f(pooled, bits_float(uint32_t(
+                                           __builtin_amdgcn_update_dpp(0, int(float_bits(pooled)), 0x4E, 0xF, 0xF, false))));
+                pring(ge)[slotk * POOL + by * 10 + 2 * st + jb % 2] = pooled;
+            }
+        };
         if (wave_boxes) {
             float* tbl = s_obs[grp];
             uint32_t vis0 = 0, vis1 = 0;  // strip masks, bit 8 st + box (strip 4 in vis1)
@@ -862,10 +900,6 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
             }
             const uint64_t casting = __ballot(depth_now);
             group_sync();
-            constexpr uint32_t EW = 64 / G;  // envs per wavefront
-            const uint32_t l = threadIdx.x % 64, wbase = (threadIdx.x / 64) * EW;
-            // lane l: ray q = l % 4 of block l / 4 of the strip (2 blocks across, 8 down)
-            const uint32_t q = l % 4, jb = l / 4;
             for (uint32_t e = 0; e < EW; e++) {
                 if (!((casting >> (e * G)) & 1ull)) continue;
                 const uint32_t ge = wbase + e, ne = blockIdx.x * E + ge;
@@ -883,12 +917,6 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 const uint32_t steps_e = __builtin_amdgcn_readlane(r.steps, e * G);
                 const uint32_t rng_e = __builtin_amdgcn_readlane(r.rng, e * G);
                 const uint32_t count_e = __builtin_amdgcn_readfirstlane(min(float_bits(s_world[ge][160]), 16u));
-                const uint32_t fidx = steps_e / C.sensor_period;
-                const uint32_t slot8 = fidx % 8, slotk = fidx % K;
-                const float noise = clean_env(C, ne) ? 0.0f : C.depth_noise;
-                const float drop = clean_env(C, ne) ? 0.0f : C.dropout;
-                float* ring = a.sensors + (size_t(ne) * 8 + slot8) * PIX;
-                const uint32_t by = jb / 2, k0 = (2 * by + q / 2) * 20 + 2 * (jb % 2) + q % 2;
                 // the five strips unrolled: no loop branches, and each strip's
                 // camera ray is loaded ahead of the strips before it
                 float dep[5];
@@ -915,27 +943,79 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                         dep[st] = axes ? strip_depth(SA, SB, d, m) : cast_ray(s_world[ge], s_cent[ge], count_e, o2, d);
                     }
                 }
-                if (noise != 0 || drop != 0) {
+                emit_frame(ge, ne, steps_e, rng_e, dep);
+            }
+        } else if (wave_strips) {
+            // any world of at most 16 obstacles: the env's strip table in its
+            // observation row (free until observe), lane l taking obstacles
+            // l and l + G
+            float* tbl = s_obs[grp];
+            if (depth_now) {
+                uint32_t vm[3] = {0u, 0u, 0u}, kinds = 0u;
+                {   // the room: the same values in every lane of the group
+                    float A[3], B[3];
+                    box_slab(world, s_cent[grp], 0, origin, A, B);
 #pragma unroll
-                    for (uint32_t st = 0; st < 5; st++) {
-                        uint32_t nr = rng_e + (k0 + 4 * st) * 1664525u + steps_e * 1013904223u;
-                        dep[st] = clamp_f(dep[st] + noise * normal_draw(nr), 0.0f, 12.0f);
-                        if (ur(nr) < drop) dep[st] = 12.0f;
-                    }
+                    for (int j = 0; j < 3; j++) { tbl[j] = A[j]; tbl[3 + j] = B[j]; }
                 }
+                for (uint32_t i = lane; i < count; i += G) {
+                    float A[3], B[3];
+                    kinds |= strip_entry(world, s_cent[grp], i, origin, tbl + 6 + 6 * i, A, B) << (2 * i);
+                    const uint32_t m = box_strips(A, B, R, a.tan_v);
+#pragma unroll
+                    for (uint32_t st = 0; st < 5; st++) vm[st / 2] |= ((m >> st) & 1u) << (16 * (st % 2) + i);
+                }
+#pragma unroll
+                for (int j = 0; j < 3; j++) vm[j] = group_or<G>(vm[j]);
+                kinds = group_or<G>(kinds);
+                // equal values from every lane of the group
+                tbl[STRIP_TABLE_ORIGIN] = origin.x; tbl[STRIP_TABLE_ORIGIN + 1] = origin.y;
+                tbl[STRIP_TABLE_ORIGIN + 2] = origin.z;
+#pragma unroll
+                for (int j = 0; j < 9; j++) tbl[STRIP_TABLE_ROT + j] = R[j];
+#pragma unroll
+                for (int j = 0; j < 3; j++) tbl[STRIP_TABLE_MASKS + j] = bits_float(vm[j]);
+                tbl[STRIP_TABLE_KINDS] = bits_float(kinds);
+            }
+            const uint64_t casting = __ballot(depth_now);
+            group_sync();
+            for (uint32_t e = 0; e < EW; e++) {
+                if (!((casting >> (e * G)) & 1ull)) continue;
+                const uint32_t ge = wbase + e, ne = blockIdx.x * E + ge;
+                const float* et = s_obs[ge];
+                float ER[9], RA[3], RB[3];
+#pragma unroll
+                for (int j = 0; j < 3; j++) { RA[j] = et[j]; RB[j] = et[3 + j]; }
+#pragma unroll
+                for (int j = 0; j < 9; j++) ER[j] = et[STRIP_TABLE_ROT + j];
+                const V eo = mk(et[STRIP_TABLE_ORIGIN], et[STRIP_TABLE_ORIGIN + 1], et[STRIP_TABLE_ORIGIN + 2]);
+                uint32_t wm[3];
+#pragma unroll
+                for (int j = 0; j < 3; j++) wm[j] = __builtin_amdgcn_readfirstlane(float_bits(et[STRIP_TABLE_MASKS + j]));
+                const uint32_t kinds_e = __builtin_amdgcn_readfirstlane(float_bits(et[STRIP_TABLE_KINDS]));
+                const uint32_t steps_e = __builtin_amdgcn_readlane(r.steps, e * G);
+                const uint32_t rng_e = __builtin_amdgcn_readlane(r.rng, e * G);
+                const uint32_t count_e = __builtin_amdgcn_readfirstlane(min(float_bits(s_world[ge][160]), 16u));
+                float dep[5];
 #pragma unroll
                 for (uint32_t st = 0; st < 5; st++) {
-                    const float depth = dep[st];
-                    ring[k0 + 4 * st] = depth;
-                    // pooled 2x2 minimum over the quad's lanes (values in [0, 12],
-                    // never NaN); after the two swaps every lane of the quad holds
-                    // it, and all four store it (one value to one address)
-                    float pooled = min_f(depth, bits_float(uint32_t(
-                                                    __builtin_amdgcn_update_dpp(0, int(float_bits(depth)), 0xB1, 0xF, 0xF, false))));
-                    pooled = min_f(pooled, bits_float(uint32_t(
-                                               __builtin_amdgcn_update_dpp(0, int(float_bits(pooled)), 0x4E, 0xF, 0xF, false))));
-                    pring(ge)[slotk * POOL + by * 10 + 2 * st + jb % 2] = pooled;
+                    const uint32_t k = k0 + 4 * st;
+                    const float rx = CAM[3 * k], ry = CAM[3 * k + 1], rz = CAM[3 * k + 2];
+                    const V d = mk(ER[0] * rx + ER[1] * ry + ER[2] * rz, ER[3] * rx + ER[4] * ry + ER[5] * rz,
+                                   ER[6] * rx + ER[7] * ry + ER[8] * rz);
+                    const bool axes = (__builtin_fabsf(d.x) >= 1e-8f) & (__builtin_fabsf(d.y) >= 1e-8f) &
+                                      (__builtin_fabsf(d.z) >= 1e-8f);
+                    const uint32_t m = (wm[st / 2] >> (16 * (st % 2))) & 0xffffu;
+                    if (__builtin_expect(__all(axes), 1)) {
+                        dep[st] = strip_depth_mixed(et, d, m, kinds_e, RA, RB);
+                    } else {  // rare: some ray component below the slab epsilon
+                        V o2 = eo;
+                        asm volatile("" : "+v"(o2.x), "+v"(o2.y), "+v"(o2.z));
+                        dep[st] = axes ? strip_depth_mixed(et, d, m, kinds_e, RA, RB)
+                                       : cast_ray(s_world[ge], s_cent[ge], count_e, o2, d);
+                    }
                 }
+                emit_frame(ge, ne, steps_e, rng_e, dep);
             }
         } else if (depth_now) {
             const uint32_t fidx = r.steps / C.sensor_period;

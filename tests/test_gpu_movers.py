@@ -106,3 +106,22 @@ def test_threat_mix_rollout_update_bit_exact(n, T, max_steps):
     finally:
         ppo.close()
         sim.close()
+
+
+def test_small_radius_worlds_take_the_lane_cast():
+    """Spheres below the strip cast's 0.05 m radius bound (its culling proof
+    needs it) send their wavefronts to the per-lane cast: family-3 worlds
+    whose spheres shrink to 0.03 m in every other env, 256 envs x 12 ticks,
+    every buffer equal to the oracle's."""
+    say("case: small-radius spheres, N=256 T=12")
+    cfg = config(n=256, family=3, speed=1.0, distance=4.0, max_steps=200)
+    sim, _, ora = make_pair(cfg, 12)
+    w = ora.get("worlds")
+    w["obstacles"]["size"][0::2, :, 0] = np.float32(0.03)
+    for side in (sim, ora):
+        side.set("worlds", w)
+    sim.collect()
+    sim.sync()
+    ora.collect()
+    bad = compare(sim, ora, ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
+    assert not bad, bad
