@@ -380,7 +380,9 @@ def main():
         (FLOP_C3_EXTRA if args.workload == "c3" else 0.0)
     bytes_env_step = BYTES_ENV_STEP + (BYTES_C3_EXTRA if args.workload == "c3" else 0.0)
     achieved = flop_env_step * env_steps_launch / avg_s
-    roofline = {"bound": "mfma", "achieved": round(achieved / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
+    # VALU-issue bound (SQ counters: VALU busy 53 % of wave cycles, matrix
+    # cores 8 %); the fp32 vector and fp32 matrix peaks are both 157.3 TFLOP/s
+    roofline = {"bound": "valu", "achieved": round(achieved / 1e12, 3), "peak": 157.3, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32, 4), "traffic": traffic_from_profile() if headline else None,
                 "traffic_unit": ("HBM bytes per launch, from %s (rocprofv3 FETCH_SIZE + WRITE_SIZE of this workload, "
                                  "copy-kernel scaled), not measured in this run" % TRAFFIC_PROFILE),

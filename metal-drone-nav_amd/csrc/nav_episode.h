@@ -153,7 +153,10 @@ __device__ __forceinline__ bool task_accept(const float* w, uint32_t count, cons
 __device__ bool task_witness(const float* w, uint32_t count, V start, V goal, const MdnTaskConfig& c,
                              TaskWitness& out, float& direct) {
     const float thr = c.minimum_witness_clearance_m;
-    V path[4] = {start, goal, goal, goal};
+    // the candidate path in the wavefront's LDS (every lane holds the same
+    // points; indexed by segment, it would otherwise live in scratch)
+    __shared__ V path[4];
+    path[0] = start; path[1] = goal; path[2] = goal; path[3] = goal;
     direct = task_path_clearance(w, count, path, 2);
     if (direct > thr && c.require_detour == 0u) {
         task_save(out, path, 2, direct);

@@ -436,31 +436,37 @@ constexpr uint32_t U_WORDS = BR * XRS > 256 * XKS + XK * WKS ? BR * XRS : 256 * 
 static_assert(256 % XK == 0 && (256 / XK) * XK == 256 && 16 * XK == 256, "forward slab mapping");
 static_assert(256 * RS <= U_WORDS, "per-row scalars fit the shared scratch");
 
-// Forward slab in registers: thread t holds column t % XK of rows t/XK + 16j
-// (j < XK) and weights [t/64 + 4j][t % 64] (j < 4).
+// A chunk's workgroup: CW = 8 wavefronts, two per SIMD, so that one
+// wavefront's LDS reads and VALU work overlap the other's matrix-core work.
+// Row-wise phases run on threads 0-255 (thread t owns row t of the chunk).
+constexpr uint32_t CW = 8, CT = 64 * CW;
+
+// Forward slab in registers: element e = t + CT j of the slab's [256][XK]
+// inputs (row e / XK, column e % XK) and of its [XK][64] weights.
 struct FwdSlab {
-    float x[XK];
-    float w[XK * HID / 256];
+    float x[256 * XK / CT];
+    float w[XK * HID / CT];
 };
 template <uint32_t D>
 __device__ __forceinline__ void fwd_load(FwdSlab& f, const float* __restrict__ X, const float* __restrict__ W1T,
                                          uint32_t n0, uint32_t b, uint32_t k0) {
-    const uint32_t t = threadIdx.x, cc = t % XK, col = k0 + cc;
+    const uint32_t t = threadIdx.x;
 #pragma unroll
-    for (uint32_t j = 0; j < XK; j++) {
-        const uint32_t row = n0 + t / XK + 16 * j;
+    for (uint32_t j = 0; j < 256 * XK / CT; j++) {
+        const uint32_t e = t + CT * j, row = n0 + e / XK, col = k0 + e % XK;
         f.x[j] = (row < b && col < D) ? X[size_t(row) * D + col] : 0.0f;
     }
 #pragma unroll
-    for (uint32_t j = 0; j < XK * HID / 256; j++) {
-        const uint32_t kc = k0 + t / HID + 4 * j;
-        f.w[j] = kc < D ? W1T[kc * HID + t % HID] : -0.0f;
+    for (uint32_t j = 0; j < XK * HID / CT; j++) {
+        const uint32_t e = t + CT * j, kc = k0 + e / HID;
+        f.w[j] = kc < D ? W1T[kc * HID + e % HID] : -0.0f;
     }
 }
 
 // h[256][64] = tanh(X W1^T + b1) for the chunk's rows (rows past b read as 0).
-// Wavefront w owns rows 64w..64w+63 as 2x2 tiles of 32x32.  The next slab's
-// global loads are in flight while the current slab's MFMAs run.
+// Wavefront w owns rows 32w..32w+31 as two 32x32 tiles (hidden units 0-31,
+// 32-63).  The next slab's global loads are in flight while the current
+// slab's MFMAs run.
 template <uint32_t D>
 __device__ __forceinline__ void chunk_forward(const float* __restrict__ X, const float* __restrict__ W1T,
                                               const float* __restrict__ b1, uint32_t n0, uint32_t b, float* s_u,
@@ -468,68 +474,68 @@ __device__ __forceinline__ void chunk_forward(const float* __restrict__ X, const
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
     float* sx = s_u;                 // [256][XKS]
     float* sw = s_u + 256 * XKS;     // [XK][WKS]
-    v16f acc[2][2];
+    v16f acc[2];
 #pragma unroll
     for (uint32_t ct = 0; ct < 2; ct++) {
         const float bias = b1[32 * ct + l % 32];
 #pragma unroll
-        for (uint32_t r = 0; r < 16; r++) { acc[0][ct][r] = bias; acc[1][ct][r] = bias; }
+        for (uint32_t r = 0; r < 16; r++) acc[ct][r] = bias;
     }
     FwdSlab f;
     fwd_load<D>(f, X, W1T, n0, b, 0);
     for (uint32_t k0 = 0; k0 < D; k0 += XK) {
 #pragma unroll
-        for (uint32_t j = 0; j < XK; j++) sx[(t / XK + 16 * j) * XKS + t % XK] = f.x[j];
+        for (uint32_t j = 0; j < 256 * XK / CT; j++) {
+            const uint32_t e = t + CT * j;
+            sx[(e / XK) * XKS + e % XK] = f.x[j];
+        }
 #pragma unroll
-        for (uint32_t j = 0; j < XK * HID / 256; j++) sw[(t / HID + 4 * j) * WKS + t % HID] = f.w[j];
+        for (uint32_t j = 0; j < XK * HID / CT; j++) {
+            const uint32_t e = t + CT * j;
+            sw[(e / HID) * WKS + e % HID] = f.w[j];
+        }
         __syncthreads();
         if (k0 + XK < D) fwd_load<D>(f, X, W1T, n0, b, k0 + XK);
         // every slab runs all XK inputs (columns past D hold x = +0 and
         // w = -0, whose product -0 leaves each accumulator unchanged); each
         // step's LDS operands are read CHUNK_PF steps ahead of its MFMAs
         constexpr uint32_t NK = XK / 2;
-        float av[NK][2], bv[NK][2];
+        float av[NK], bv[NK][2];
 #pragma unroll
         for (uint32_t st = 0; st < NK + CHUNK_PF; st++) {
             if (st < NK) {
                 const uint32_t kr = 2 * st + l / 32;
-#pragma unroll
-                for (uint32_t rt = 0; rt < 2; rt++) av[st][rt] = sx[(64 * wv + 32 * rt + l % 32) * XKS + kr];
+                av[st] = sx[(32 * wv + l % 32) * XKS + kr];
 #pragma unroll
                 for (uint32_t ct = 0; ct < 2; ct++) bv[st][ct] = sw[kr * WKS + 32 * ct + l % 32];
             }
             if (st >= CHUNK_PF) {
                 const uint32_t u = st - CHUNK_PF;
 #pragma unroll
-                for (uint32_t rt = 0; rt < 2; rt++)
-#pragma unroll
-                    for (uint32_t ct = 0; ct < 2; ct++) acc[rt][ct] = mfma32(av[u][rt], bv[u][ct], acc[rt][ct]);
+                for (uint32_t ct = 0; ct < 2; ct++) acc[ct] = mfma32(av[u], bv[u][ct], acc[ct]);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
         __syncthreads();
     }
 #pragma unroll
-    for (uint32_t rt = 0; rt < 2; rt++)
+    for (uint32_t ct = 0; ct < 2; ct++)
 #pragma unroll
-        for (uint32_t ct = 0; ct < 2; ct++)
-#pragma unroll
-            for (uint32_t r = 0; r < 16; r++)
-                s_h[(64 * wv + 32 * rt + acc_row(l, r)) * HS + 32 * ct + l % 32] = tanh_f(acc[rt][ct][r]);
+        for (uint32_t r = 0; r < 16; r++) s_h[(32 * wv + acc_row(l, r)) * HS + 32 * ct + l % 32] = tanh_f(acc[ct][r]);
     __syncthreads();
 }
 
-// Backward row slab in registers: BR rows x W columns, element e = t + 256 j.
+// Backward row slab in registers: BR rows x W columns, element e = t + CT j.
 template <uint32_t W>
 struct RowSlab {
-    float x[BR * W / 256];
+    float x[BR * W / CT];
 };
 template <uint32_t D, uint32_t W>
 __device__ __forceinline__ void row_load(RowSlab<W>& f, const float* __restrict__ X, uint32_t n0, uint32_t rows,
                                          uint32_t r0) {
 #pragma unroll
-    for (uint32_t j = 0; j < BR * W / 256; j++) {
-        const uint32_t e = threadIdx.x + 256 * j, rr = e / W, cc = e % W;
+    for (uint32_t j = 0; j < BR * W / CT; j++) {
+        const uint32_t e = threadIdx.x + CT * j, rr = e / W, cc = e % W;
         f.x[j] = (r0 + rr < rows && cc < D) ? X[size_t(n0 + r0 + rr) * D + cc] : -0.0f;
     }
 }
@@ -553,8 +559,8 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
     row_load<D, W>(f, X, n0, rows, 0);
     for (uint32_t r0 = 0; r0 < rows; r0 += BR) {
 #pragma unroll
-        for (uint32_t j = 0; j < BR * W / 256; j++) {
-            const uint32_t e = t + 256 * j;
+        for (uint32_t j = 0; j < BR * W / CT; j++) {
+            const uint32_t e = t + CT * j;
             sx[(e / W) * WS + e % W] = f.x[j];
         }
         __syncthreads();
@@ -649,12 +655,13 @@ __device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls,
 }
 
 template <uint32_t D>
-__global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
+__global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     using L = AL<D>;
     __shared__ float s_h[256 * HS];
     __shared__ float s_u[U_WORDS];
     __shared__ float s_dv[256];
     const uint32_t t = threadIdx.x, wv = t / 64;
+    const bool rowt = t < 256;  // the row-wise phases' threads
     const uint32_t n0 = blockIdx.x * 256;
     const uint32_t rows = a.b - n0 < 256 ? a.b - n0 : 256;
     const bool live = t < rows;
@@ -667,10 +674,11 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
     // ---- critic: forward, value, dV (ppo.hpp:82-93, 176-180)
     chunk_forward<COBS>(a.co, a.critic_w1t, a.critic + C_B1, n0, a.b, s_u, s_h);
     float value = a.critic[C_B2];
-    for (uint32_t k = 0; k < HID; k++) value = fma_f(a.critic[C_W2 + k], s_h[t * HS + k], value);
+    if (rowt)
+        for (uint32_t k = 0; k < HID; k++) value = fma_f(a.critic[C_W2 + k], s_h[t * HS + k], value);
     const float target = a.ret[m];
     const float dvalue = a.vcoef * (value - target) * scale;
-    s_dv[t] = live ? dvalue : 0.0f;
+    if (rowt) s_dv[t] = live ? dvalue : 0.0f;
     __syncthreads();
     if (t < HID) {  // critic w2: fma over rows
         float g = 0.0f;
@@ -682,10 +690,11 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
         P[L::COUNT + C_B2] = g;
     }
     __syncthreads();
-    for (uint32_t k = 0; k < HID; k++) {  // critic hidden delta, in place
-        const float g = s_h[t * HS + k];
-        s_h[t * HS + k] = live ? dvalue * a.critic[C_W2 + k] * (1.0f - g * g) : 0.0f;
-    }
+    if (rowt)
+        for (uint32_t k = 0; k < HID; k++) {  // critic hidden delta, in place
+            const float g = s_h[t * HS + k];
+            s_h[t * HS + k] = live ? dvalue * a.critic[C_W2 + k] * (1.0f - g * g) : 0.0f;
+        }
     __syncthreads();
     if (t < HID) {  // critic b1
         float g = 0.0f;
@@ -699,21 +708,23 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
 
     // ---- actor: forward, means, loss and derivatives
     chunk_forward<D>(a.obs, a.actor_w1t, a.actor + L::B1, n0, a.b, s_u, s_h);
-    float mean[4];
+    float dmean[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (rowt) {
+        float mean[4];
 #pragma unroll
-    for (uint32_t q = 0; q < 4; q++) {
-        float z = a.actor[L::B2 + q];
-        for (uint32_t k = 0; k < HID; k++) z = fma_f(a.actor[L::W2 + q * HID + k], s_h[t * HS + k], z);
-        // geometry prior (ppo.hpp:77): the hint inputs add to the first three means
-        if (D == MDN_ACTOR_OBS_PRIOR && q < 3) z += a.obs[size_t(m) * D + D - 3 + q];
-        mean[q] = z;
+        for (uint32_t q = 0; q < 4; q++) {
+            float z = a.actor[L::B2 + q];
+            for (uint32_t k = 0; k < HID; k++) z = fma_f(a.actor[L::W2 + q * HID + k], s_h[t * HS + k], z);
+            // geometry prior (ppo.hpp:77): the hint inputs add to the first three means
+            if (D == MDN_ACTOR_OBS_PRIOR && q < 3) z += a.obs[size_t(m) * D + D - 3 + q];
+            mean[q] = z;
+        }
+        float* rs = s_u + t * RS;  // the forward's scratch is free now
+        row_objective(a, a.actor + L::LS, m, adv, mean, value, target, scale, dmean, rs);
+        if (a.norm && live) a.adv_out[m] = adv;
     }
-    float dmean[4];
-    float* rs = s_u + t * RS;  // the forward's scratch is free now
-    row_objective(a, a.actor + L::LS, m, adv, mean, value, target, scale, dmean, rs);
-    if (a.norm && live) a.adv_out[m] = adv;
     __syncthreads();
-    {   // actor W2[q][k]: fma over rows; then b2, log_std and the metric sums
+    if (rowt) {   // actor W2[q][k]: fma over rows; then b2, log_std and the metric sums
         const uint32_t q = t / HID, k = t % HID;
         float g = 0.0f;
         for (uint32_t r = 0; r < rows; r++) g = fma_f(s_u[r * RS + q], s_h[r * HS + k], g);
@@ -726,23 +737,24 @@ __global__ __launch_bounds__(256) void chunk_kernel(RowArgs a) {
         }
     }
     __syncthreads();
-    for (uint32_t k = 0; k < HID; k++) {  // actor hidden delta, in place
-        float d = 0.0f;
+    if (rowt)
+        for (uint32_t k = 0; k < HID; k++) {  // actor hidden delta, in place
+            float d = 0.0f;
 #pragma unroll
-        for (uint32_t q = 0; q < 4; q++) d = fma_f(dmean[q], a.actor[L::W2 + q * HID + k], d);
-        const float h = s_h[t * HS + k];
-        s_h[t * HS + k] = live ? d * (1.0f - h * h) : 0.0f;
-    }
+            for (uint32_t q = 0; q < 4; q++) d = fma_f(dmean[q], a.actor[L::W2 + q * HID + k], d);
+            const float h = s_h[t * HS + k];
+            s_h[t * HS + k] = live ? d * (1.0f - h * h) : 0.0f;
+        }
     __syncthreads();
     if (t < HID) {  // actor b1
         float g = 0.0f;
         for (uint32_t r = 0; r < rows; r++) g += s_h[r * HS + t];
         P[L::B1 + t] = g;
     }
-    {   // actor W1 [64][D]: 2 x 6 tiles, three per wavefront
-        const uint32_t jt[3] = {(3 * wv) / 6, (3 * wv + 1) / 6, (3 * wv + 2) / 6};
-        const uint32_t it[3] = {(3 * wv) % 6, (3 * wv + 1) % 6, (3 * wv + 2) % 6};
-        chunk_weight_grad<D, OBS_PAD, 3>(a.obs, n0, rows, jt, it, true, s_u, s_h, P);
+    {   // actor W1 [64][D]: 2 x 6 tiles, two per wavefront on wavefronts 0-5
+        const uint32_t jt[2] = {(2 * wv) / 6, (2 * wv + 1) / 6};
+        const uint32_t it[2] = {(2 * wv) % 6, (2 * wv + 1) % 6};
+        chunk_weight_grad<D, OBS_PAD, 2>(a.obs, n0, rows, jt, it, wv < 6, s_u, s_h, P);
     }
 }
 
@@ -1196,9 +1208,9 @@ hipError_t ppo_launch_normalize(float* a, uint64_t count, double* part, float* s
 hipError_t ppo_launch_rows(const ppo::RowArgs* a, hipStream_t st) {
     if (a->b == 0) return hipSuccess;
     if (a->d == MDN_ACTOR_OBS_POOLED)
-        hipLaunchKernelGGL(ppo::chunk_kernel<MDN_ACTOR_OBS_POOLED>, dim3((a->b + 255) / 256), dim3(256), 0, st, *a);
+        hipLaunchKernelGGL(ppo::chunk_kernel<MDN_ACTOR_OBS_POOLED>, dim3((a->b + 255) / 256), dim3(ppo::CT), 0, st, *a);
     else if (a->d == MDN_ACTOR_OBS_PRIOR)
-        hipLaunchKernelGGL(ppo::chunk_kernel<MDN_ACTOR_OBS_PRIOR>, dim3((a->b + 255) / 256), dim3(256), 0, st, *a);
+        hipLaunchKernelGGL(ppo::chunk_kernel<MDN_ACTOR_OBS_PRIOR>, dim3((a->b + 255) / 256), dim3(ppo::CT), 0, st, *a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

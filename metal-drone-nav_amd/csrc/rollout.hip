@@ -209,7 +209,8 @@ __global__ __launch_bounds__(64) void reset_kernel(RolloutArgs a) {
 // env with steps == 0 was reset by it; an evaluation never restarts one).
 // One wavefront per env: every lane computes the same values (and stores
 // the same words), except the task generator's segment clearances, whose
-// samples the lanes share.
+// samples the lanes share.  The workgroup is that one wavefront, so the
+// plant, its draw, the task state and the witness path live in its LDS.
 __global__ __launch_bounds__(64) void episode_kernel(EpisodeArgs a) {
     const uint32_t n = blockIdx.x;
     const uint32_t N = a.cfg.n;
@@ -219,11 +220,14 @@ __global__ __launch_bounds__(64) void episode_kernel(EpisodeArgs a) {
     if (!a.first && r.steps != 0u) return;
     State s;
     load_state(a.state, N, n, s);
-    MdnPhysicsParams ep = a.phys;
+    // the plant and its draw live in the wavefront's LDS (88 words each, the
+    // same values from every lane), not in registers
+    __shared__ MdnPhysicsParams s_ep, s_varied;
+    MdnPhysicsParams& ep = s_ep;
+    ep = a.phys;
     if (a.runtime.enabled != 0u && a.runtime.domain_amplitude > 0.0f) {
         const uint32_t rng = dom_seed(a.runtime, a.cfg.seed, n, a.first ? 0u : r.episodes);
-        MdnPhysicsParams varied;
-        if (dom_sample(a.phys, rng, a.runtime.domain_amplitude, a.runtime.domain_range, varied)) ep = varied;
+        if (dom_sample(a.phys, rng, a.runtime.domain_amplitude, a.runtime.domain_range, s_varied)) ep = s_varied;
         else ep.mass = nan_f();  // rejected draw: the host's validation reports it
     }
     a.env_phys[n] = ep;
@@ -272,7 +276,8 @@ __global__ __launch_bounds__(64) void episode_kernel(EpisodeArgs a) {
     } else {
         a.bank_active[n] = MDN_BANK_REHEARSAL;
     }
-    MdnTaskState t;
+    __shared__ MdnTaskState s_task;  // in LDS like the plant
+    MdnTaskState& t = s_task;
     uint32_t* tw = reinterpret_cast<uint32_t*>(&t);
     for (uint32_t i = 0; i < sizeof(MdnTaskState) / 4; i++) tw[i] = 0u;
     if (a.task.enabled != 0u) {
