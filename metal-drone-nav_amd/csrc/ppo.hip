@@ -426,14 +426,14 @@ __device__ __forceinline__ uint32_t acc_row(uint32_t l, uint32_t r) { return 8 *
 constexpr uint32_t HS = HID + 1;       // row stride of the [256][64] activation buffer
 constexpr uint32_t CHUNK_PF = 3;       // MFMA steps between an operand's LDS read and its use
 constexpr uint32_t XK = 16;            // forward: inputs per k-slab
-constexpr uint32_t XKS = XK + 1;       // stride of the forward row tile [256][16]
-constexpr uint32_t WKS = HID + 32;     // stride of the forward weight slab [16][64]
+constexpr uint32_t XKS = XK + 1;       // stride of the forward row tile [256][XK]
+constexpr uint32_t WKS = HID + 32;     // stride of the forward weight slab [XK][64]
 constexpr uint32_t BR = 32;            // backward: rows per row-slab
 constexpr uint32_t OBS_PAD = 192;      // inputs rounded up to whole 32-wide tiles
 constexpr uint32_t XRS = OBS_PAD + 32; // stride of the backward row slab [32][192]
 constexpr uint32_t RS = 13;            // per-row scalars: dm[4], dls[4], loss[4]
 constexpr uint32_t U_WORDS = BR * XRS > 256 * XKS + XK * WKS ? BR * XRS : 256 * XKS + XK * WKS;
-static_assert(256 % XK == 0 && (256 / XK) * XK == 256 && 16 * XK == 256, "forward slab mapping");
+static_assert(256 % XK == 0, "forward slab mapping");
 static_assert(256 * RS <= U_WORDS, "per-row scalars fit the shared scratch");
 
 // A chunk's workgroup: CW = 8 wavefronts, two per SIMD, so that one
@@ -660,8 +660,13 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     __shared__ float s_h[256 * HS];
     __shared__ float s_u[U_WORDS];
     __shared__ float s_dv[256];
+    // the critic's w2 and the actor's W2 [4][64], read by every row's chains:
+    // one LDS copy (broadcast reads) instead of per-step global loads
+    __shared__ float s_w2[5 * HID];
     const uint32_t t = threadIdx.x, wv = t / 64;
     const bool rowt = t < 256;  // the row-wise phases' threads
+    if (t < HID) s_w2[t] = a.critic[C_W2 + t];
+    else if (t < 5 * HID) s_w2[t] = a.actor[L::W2 + t - HID];
     const uint32_t n0 = blockIdx.x * 256;
     const uint32_t rows = a.b - n0 < 256 ? a.b - n0 : 256;
     const bool live = t < rows;
@@ -675,17 +680,19 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     chunk_forward<COBS>(a.co, a.critic_w1t, a.critic + C_B1, n0, a.b, s_u, s_h);
     float value = a.critic[C_B2];
     if (rowt)
-        for (uint32_t k = 0; k < HID; k++) value = fma_f(a.critic[C_W2 + k], s_h[t * HS + k], value);
+        for (uint32_t k = 0; k < HID; k++) value = fma_f(s_w2[k], s_h[t * HS + k], value);
     const float target = a.ret[m];
     const float dvalue = a.vcoef * (value - target) * scale;
     if (rowt) s_dv[t] = live ? dvalue : 0.0f;
     __syncthreads();
     if (t < HID) {  // critic w2: fma over rows
         float g = 0.0f;
+        #pragma unroll 16
         for (uint32_t r = 0; r < rows; r++) g = fma_f(s_dv[r], s_h[r * HS + t], g);
         P[L::COUNT + C_W2 + t] = g;
     } else if (t == HID) {  // critic b2
         float g = 0.0f;
+        #pragma unroll 16
         for (uint32_t r = 0; r < rows; r++) g += s_dv[r];
         P[L::COUNT + C_B2] = g;
     }
@@ -693,11 +700,13 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     if (rowt)
         for (uint32_t k = 0; k < HID; k++) {  // critic hidden delta, in place
             const float g = s_h[t * HS + k];
-            s_h[t * HS + k] = live ? dvalue * a.critic[C_W2 + k] * (1.0f - g * g) : 0.0f;
+            const float d = dvalue * s_w2[k] * (1.0f - g * g);
+            s_h[t * HS + k] = live ? d : 0.0f;
         }
     __syncthreads();
     if (t < HID) {  // critic b1
         float g = 0.0f;
+        #pragma unroll 16
         for (uint32_t r = 0; r < rows; r++) g += s_h[r * HS + t];
         P[L::COUNT + C_B1 + t] = g;
     }
@@ -714,7 +723,7 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
 #pragma unroll
         for (uint32_t q = 0; q < 4; q++) {
             float z = a.actor[L::B2 + q];
-            for (uint32_t k = 0; k < HID; k++) z = fma_f(a.actor[L::W2 + q * HID + k], s_h[t * HS + k], z);
+            for (uint32_t k = 0; k < HID; k++) z = fma_f(s_w2[HID + q * HID + k], s_h[t * HS + k], z);
             // geometry prior (ppo.hpp:77): the hint inputs add to the first three means
             if (D == MDN_ACTOR_OBS_PRIOR && q < 3) z += a.obs[size_t(m) * D + D - 3 + q];
             mean[q] = z;
@@ -727,11 +736,13 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     if (rowt) {   // actor W2[q][k]: fma over rows; then b2, log_std and the metric sums
         const uint32_t q = t / HID, k = t % HID;
         float g = 0.0f;
+        #pragma unroll 16
         for (uint32_t r = 0; r < rows; r++) g = fma_f(s_u[r * RS + q], s_h[r * HS + k], g);
         P[L::W2 + q * HID + k] = g;
         if (t < 12) {
             const uint32_t col = t < 4 ? t : t < 8 ? 4 + (t - 4) : 8 + (t - 8);
             float g2 = 0.0f;
+            #pragma unroll 16
             for (uint32_t r = 0; r < rows; r++) g2 += s_u[r * RS + col];
             P[t < 4 ? L::B2 + t : t < 8 ? L::LS + (t - 4) : L::COUNT + C_COUNT + (t - 8)] = g2;
         }
@@ -741,20 +752,29 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
         for (uint32_t k = 0; k < HID; k++) {  // actor hidden delta, in place
             float d = 0.0f;
 #pragma unroll
-            for (uint32_t q = 0; q < 4; q++) d = fma_f(dmean[q], a.actor[L::W2 + q * HID + k], d);
+            for (uint32_t q = 0; q < 4; q++) d = fma_f(dmean[q], s_w2[HID + q * HID + k], d);
             const float h = s_h[t * HS + k];
-            s_h[t * HS + k] = live ? d * (1.0f - h * h) : 0.0f;
+            const float dh = d * (1.0f - h * h);
+            s_h[t * HS + k] = live ? dh : 0.0f;
         }
     __syncthreads();
     if (t < HID) {  // actor b1
         float g = 0.0f;
+        #pragma unroll 16
         for (uint32_t r = 0; r < rows; r++) g += s_h[r * HS + t];
         P[L::B1 + t] = g;
     }
-    {   // actor W1 [64][D]: 2 x 6 tiles, two per wavefront on wavefronts 0-5
+    // actor W1 [64][D]: 2 x 6 tiles of 32x32.  Wavefronts w and w + 4 share
+    // a SIMD and take three tiles between them: tiles 2w and 2w + 1 for
+    // w < 4, tile w + 4 for the others.  Both paths run the same slabs and
+    // barriers (a workgroup barrier counts arrivals, not code positions).
+    if (wv < 4) {
         const uint32_t jt[2] = {(2 * wv) / 6, (2 * wv + 1) / 6};
         const uint32_t it[2] = {(2 * wv) % 6, (2 * wv + 1) % 6};
-        chunk_weight_grad<D, OBS_PAD, 2>(a.obs, n0, rows, jt, it, wv < 6, s_u, s_h, P);
+        chunk_weight_grad<D, OBS_PAD, 2>(a.obs, n0, rows, jt, it, true, s_u, s_h, P);
+    } else {
+        const uint32_t jt[1] = {(wv + 4) / 6}, it[1] = {(wv + 4) % 6};
+        chunk_weight_grad<D, OBS_PAD, 1>(a.obs, n0, rows, jt, it, true, s_u, s_h, P);
     }
 }
 
