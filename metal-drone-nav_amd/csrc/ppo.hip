@@ -425,55 +425,68 @@ __device__ __forceinline__ uint32_t acc_row(uint32_t l, uint32_t r) { return 8 *
 
 constexpr uint32_t HS = HID + 1;       // row stride of the [256][64] activation buffer
 constexpr uint32_t CHUNK_PF = 3;       // MFMA steps between an operand's LDS read and its use
-constexpr uint32_t XK = 16;            // forward: inputs per k-slab
-constexpr uint32_t XKS = XK + 1;       // stride of the forward row tile [256][XK]
-constexpr uint32_t WKS = HID + 32;     // stride of the forward weight slab [XK][64]
 constexpr uint32_t BR = 32;            // backward: rows per row-slab
 constexpr uint32_t OBS_PAD = 192;      // inputs rounded up to whole 32-wide tiles
 constexpr uint32_t XRS = OBS_PAD + 32; // stride of the backward row slab [32][192]
-constexpr uint32_t RS = 13;            // per-row scalars: dm[4], dls[4], loss[4]
-constexpr uint32_t U_WORDS = BR * XRS > 256 * XKS + XK * WKS ? BR * XRS : 256 * XKS + XK * WKS;
-static_assert(256 % XK == 0, "forward slab mapping");
-static_assert(256 * RS <= U_WORDS, "per-row scalars fit the shared scratch");
+constexpr uint32_t RS = 12;            // per-row scalars: dm[4], dls[4], loss terms and ratio[4]
 
 // A chunk's workgroup: CW = 8 wavefronts, two per SIMD, so that one
 // wavefront's LDS reads and VALU work overlap the other's matrix-core work.
 // Row-wise phases run on threads 0-255 (thread t owns row t of the chunk).
 constexpr uint32_t CW = 8, CT = 64 * CW;
+// shared scratch: the critic's staged first layer and the forwards' input
+// tiles (one [32][XWS] tile per wavefront), the backward row slabs, after
+// the actor forward the per-row scalars
+constexpr uint32_t XWS = 17;  // row stride of a wavefront's input tile
+constexpr uint32_t XW_BASE = COBS * HID;
+constexpr uint32_t U_WORDS = BR * XRS > XW_BASE + CW * 32 * XWS ? BR * XRS : XW_BASE + CW * 32 * XWS;
+static_assert(256 * RS <= U_WORDS, "the per-row scalars fit the shared scratch");
 
-// Forward slab in registers: element e = t + CT j of the slab's [256][XK]
-// inputs (row e / XK, column e % XK) and of its [XK][64] weights.
-struct FwdSlab {
-    float x[256 * XK / CT];
-    float w[XK * HID / CT];
-};
-template <uint32_t D>
-__device__ __forceinline__ void fwd_load(FwdSlab& f, const float* __restrict__ X, const float* __restrict__ W1T,
-                                         uint32_t n0, uint32_t b, uint32_t k0) {
+// A first layer staged in LDS, transposed: W1[u][k] at w1_pos(k, u) =
+// 64 k + (u ^ 32 (k & 1)), so the two input rows of one MFMA step's B
+// operand (k even in lanes 0-31, odd in lanes 32-63) fall in different halves
+// of the banks.
+__device__ __forceinline__ uint32_t w1_pos(uint32_t k, uint32_t u) { return k * HID + (u ^ (32u * (k & 1u))); }
+// W1T [D][64] (global, input-major) into LDS for inputs 0 .. KP-1, the
+// inputs past D as -0.
+template <uint32_t D, uint32_t KP>
+__device__ __forceinline__ void stage_w1(const float* __restrict__ W1T, float* sw) {
+    static_assert(KP * HID % CT == 0, "whole staging rounds");
+    constexpr uint32_t N = KP * HID / CT;
     const uint32_t t = threadIdx.x;
+    float v[N];
 #pragma unroll
-    for (uint32_t j = 0; j < 256 * XK / CT; j++) {
-        const uint32_t e = t + CT * j, row = n0 + e / XK, col = k0 + e % XK;
-        f.x[j] = (row < b && col < D) ? X[size_t(row) * D + col] : 0.0f;
+    for (uint32_t j = 0; j < N; j++) {
+        const uint32_t e = t + CT * j;
+        v[j] = e / HID < D ? W1T[e] : -0.0f;
     }
 #pragma unroll
-    for (uint32_t j = 0; j < XK * HID / CT; j++) {
-        const uint32_t e = t + CT * j, kc = k0 + e / HID;
-        f.w[j] = kc < D ? W1T[kc * HID + e % HID] : -0.0f;
+    for (uint32_t j = 0; j < N; j++) {
+        const uint32_t e = t + CT * j;
+        sw[w1_pos(e / HID, e % HID)] = v[j];
     }
 }
 
-// h[256][64] = tanh(X W1^T + b1) for the chunk's rows (rows past b read as 0).
-// Wavefront w owns rows 32w..32w+31 as two 32x32 tiles (hidden units 0-31,
-// 32-63).  The next slab's global loads are in flight while the current
-// slab's MFMAs run.
-template <uint32_t D>
-__device__ __forceinline__ void chunk_forward(const float* __restrict__ X, const float* __restrict__ W1T,
-                                              const float* __restrict__ b1, uint32_t n0, uint32_t b, float* s_u,
-                                              float* s_h) {
-    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
-    float* sx = s_u;                 // [256][XKS]
-    float* sw = s_u + 256 * XKS;     // [XK][WKS]
+// h[256][64] = tanh(X W1^T + b1) for the chunk's rows (rows past b read as
+// 0), with W1 staged by stage_w1<D, KP>.  Wavefront w owns rows 32w..32w+31
+// as two 32x32 tiles (hidden units 0-31, 32-63).  It fetches its rows'
+// inputs in blocks of 16 (each load instruction covering 4 rows x 16
+// consecutive inputs), two blocks ahead of the matrix cores, and passes each
+// block through its own LDS tile xw [32][17] into the A operand (lane l: row
+// l % 32, the inputs of parity l / 32); each step's B operand comes from the
+// staged layer.  Every block runs all 16 inputs (inputs past D hold x = +0
+// and w = -0, whose product -0 leaves each accumulator unchanged).  No
+// workgroup barrier falls before the activations (tanh) are formed, so one
+// wavefront's activations overlap the other's MFMAs on a SIMD; with WAIT a
+// barrier separates them from the stores into s_h (whose previous readers
+// may still run).
+template <uint32_t D, uint32_t KP, bool WAIT>
+__device__ __forceinline__ void chunk_forward(const float* __restrict__ X, const float* sw, float* xw_all,
+                                              const float* __restrict__ b1, uint32_t n0, uint32_t b, float* s_h) {
+    static_assert(KP % 16 == 0 && KP >= D, "whole input blocks");
+    constexpr uint32_t NB = KP / 16;
+    const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64, hf = l / 32;
+    float* xw = xw_all + wv * 32 * XWS;
     v16f acc[2];
 #pragma unroll
     for (uint32_t ct = 0; ct < 2; ct++) {
@@ -481,48 +494,117 @@ __device__ __forceinline__ void chunk_forward(const float* __restrict__ X, const
 #pragma unroll
         for (uint32_t r = 0; r < 16; r++) acc[ct][r] = bias;
     }
-    FwdSlab f;
-    fwd_load<D>(f, X, W1T, n0, b, 0);
-    for (uint32_t k0 = 0; k0 < D; k0 += XK) {
+    // load i of a block: row 4 i + l / 16 of the wavefront's rows, input l % 16
+    const uint32_t lr = l / 16, lk = l % 16;
+    float xg[3][8];
+    auto xload = [&](uint32_t p, uint32_t blk) {
+        const uint32_t k = 16 * blk + lk;
 #pragma unroll
-        for (uint32_t j = 0; j < 256 * XK / CT; j++) {
-            const uint32_t e = t + CT * j;
-            sx[(e / XK) * XKS + e % XK] = f.x[j];
+        for (uint32_t i = 0; i < 8; i++) {
+            const uint32_t row = n0 + 32 * wv + 4 * i + lr;
+            const bool ok = row < b && k < D;
+            const float v = X[size_t(row < b ? row : n0) * D + (k < D ? k : D - 1)];
+            xg[p][i] = ok ? v : 0.0f;
         }
+    };
+    xload(0, 0);
+    if (NB > 1) xload(1, 1);
+    for (uint32_t j0 = 0; j0 < NB; j0 += 3) {
 #pragma unroll
-        for (uint32_t j = 0; j < XK * HID / CT; j++) {
-            const uint32_t e = t + CT * j;
-            sw[(e / HID) * WKS + e % HID] = f.w[j];
-        }
-        __syncthreads();
-        if (k0 + XK < D) fwd_load<D>(f, X, W1T, n0, b, k0 + XK);
-        // every slab runs all XK inputs (columns past D hold x = +0 and
-        // w = -0, whose product -0 leaves each accumulator unchanged); each
-        // step's LDS operands are read CHUNK_PF steps ahead of its MFMAs
-        constexpr uint32_t NK = XK / 2;
-        float av[NK], bv[NK][2];
+        for (uint32_t p = 0; p < 3; p++) {
+            const uint32_t j = j0 + p;
+            if (j >= NB) break;
 #pragma unroll
-        for (uint32_t st = 0; st < NK + CHUNK_PF; st++) {
-            if (st < NK) {
-                const uint32_t kr = 2 * st + l / 32;
-                av[st] = sx[(32 * wv + l % 32) * XKS + kr];
+            for (uint32_t i = 0; i < 8; i++) xw[(4 * i + lr) * XWS + lk] = xg[p][i];
+            if (j + 2 < NB) xload((p + 2) % 3, j + 2);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            float av[8], bv[8][2];
 #pragma unroll
-                for (uint32_t ct = 0; ct < 2; ct++) bv[st][ct] = sw[kr * WKS + 32 * ct + l % 32];
+            for (uint32_t i = 0; i < 8; i++) {
+                av[i] = xw[(l % 32) * XWS + 2 * i + hf];
+                const uint32_t k = 16 * j + 2 * i + hf;
+#pragma unroll
+                for (uint32_t ct = 0; ct < 2; ct++) bv[i][ct] = sw[k * HID + 32 * (ct ^ hf) + l % 32];
             }
-            if (st >= CHUNK_PF) {
-                const uint32_t u = st - CHUNK_PF;
 #pragma unroll
-                for (uint32_t ct = 0; ct < 2; ct++) acc[ct] = mfma32(av[u], bv[u][ct], acc[ct]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
+            for (uint32_t i = 0; i < 8; i++)
+#pragma unroll
+                for (uint32_t ct = 0; ct < 2; ct++) acc[ct] = mfma32(av[i], bv[i][ct], acc[ct]);
+            // this block's tile reads precede the next block's writes
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        __syncthreads();
     }
 #pragma unroll
     for (uint32_t ct = 0; ct < 2; ct++)
 #pragma unroll
-        for (uint32_t r = 0; r < 16; r++) s_h[(32 * wv + acc_row(l, r)) * HS + 32 * ct + l % 32] = tanh_f(acc[ct][r]);
+        for (uint32_t r = 0; r < 16; r++) acc[ct][r] = tanh_f(acc[ct][r]);
+    if (WAIT) __syncthreads();  // s_h's previous readers are done
+#pragma unroll
+    for (uint32_t ct = 0; ct < 2; ct++)
+#pragma unroll
+        for (uint32_t r = 0; r < 16; r++) s_h[(32 * wv + acc_row(l, r)) * HS + 32 * ct + l % 32] = acc[ct][r];
     __syncthreads();
+}
+
+// s = fma(a[r], b[r * bs], s) (MUL) or s = s + b[r * bs] for r = r0 .. r1-1
+// ascending, operands in LDS; a is read four rows at a time (16-byte reads,
+// r0 a multiple of 4).  The reads of a block of CH_NB rows are issued before
+// the previous block's arithmetic, so a dependent chain does not wait on
+// every read.  A span of exactly FULL rows (a whole chunk or slab) takes a
+// loop with a fixed trip count; other spans take the general loop.
+constexpr uint32_t CH_NB = 8;
+template <bool MUL, uint32_t FULL>
+__device__ __forceinline__ float lds_chain(const float* a, const float* b, uint32_t bs, uint32_t r0, uint32_t r1,
+                                           float s) {
+    static_assert(FULL % (2 * CH_NB) == 0, "whole block pairs");
+    float4 av[2][CH_NB / 4];
+    float bv[2][CH_NB];
+    auto load = [&](uint32_t p, uint32_t r) {
+        if (MUL)
+#pragma unroll
+            for (uint32_t i = 0; i < CH_NB / 4; i++) av[p][i] = *reinterpret_cast<const float4*>(a + r + 4 * i);
+#pragma unroll
+        for (uint32_t i = 0; i < CH_NB; i++) bv[p][i] = b[(r + i) * bs];
+    };
+    auto use = [&](uint32_t p) {
+#pragma unroll
+        for (uint32_t i = 0; i < CH_NB; i++) {
+            if (MUL) s = fma_f(av[p][i / 4][i % 4], bv[p][i], s);
+            else s = s + bv[p][i];
+        }
+    };
+    if (r1 - r0 == FULL) {
+        load(0, r0);
+#pragma unroll 4
+        for (uint32_t j = 0; j < FULL; j += 2 * CH_NB) {
+            load(1, r0 + j + CH_NB);
+            use(0);
+            if (j + 2 * CH_NB < FULL) load(0, r0 + j + 2 * CH_NB);
+            use(1);
+        }
+        return s;
+    }
+    const uint32_t nfull = r0 + (r1 - r0) / CH_NB * CH_NB;
+    uint32_t r = r0;
+    if (r < nfull) load(0, r);
+    while (r < nfull) {
+        const bool more = r + CH_NB < nfull;
+        if (more) load(1, r + CH_NB);
+        use(0);
+        r += CH_NB;
+        if (!more) break;
+        const bool more2 = r + CH_NB < nfull;
+        if (more2) load(0, r + CH_NB);
+        use(1);
+        r += CH_NB;
+        if (!more2) break;
+    }
+    for (; r < r1; r++) s = MUL ? fma_f(a[r], b[r * bs], s) : s + b[r * bs];
+    return s;
 }
 
 // Backward row slab in registers: BR rows x W columns, element e = t + CT j.
@@ -542,11 +624,16 @@ __device__ __forceinline__ void row_load(RowSlab<W>& f, const float* __restrict_
 
 // dW1[j][i] partial over the chunk's rows: A = delta^T (s_h, [row][64]),
 // B = the input rows streamed from global in slabs of 32 rows (W columns, a
-// multiple of 32 covering D).  Wavefront tiles are the (jt[q], it[q]) pairs.
+// multiple of 32 covering D) through LDS.  Wavefront tiles are the (jt[q],
+// it[q]) pairs.  The wavefront `side` (if any) also forms the first-layer
+// bias gradient of its lane's unit, the sum of s_h's column over the chunk's
+// rows (ascending from 0), slab by slab while the others run their tiles,
+// into side_out[lane].
 template <uint32_t D, uint32_t W, uint32_t T>
 __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, uint32_t n0, uint32_t rows,
                                                   const uint32_t (&jt)[T], const uint32_t (&it)[T], bool owner,
-                                                  float* s_u, const float* s_h, float* __restrict__ out) {
+                                                  bool side, float* s_u, const float* s_h, float* __restrict__ out,
+                                                  float* __restrict__ side_out) {
     constexpr uint32_t WS = W + 32;  // slab row stride: the two k halves fall in different banks
     const uint32_t t = threadIdx.x, l = t % 64;
     float* sx = s_u;  // [BR][WS]
@@ -555,6 +642,7 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
     for (uint32_t q = 0; q < T; q++)
 #pragma unroll
         for (uint32_t r = 0; r < 16; r++) acc[q][r] = 0.0f;
+    float colsum = 0.0f;
     RowSlab<W> f;
     row_load<D, W>(f, X, n0, rows, 0);
     for (uint32_t r0 = 0; r0 < rows; r0 += BR) {
@@ -565,6 +653,7 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
         }
         __syncthreads();
         if (r0 + BR < rows) row_load<D, W>(f, X, n0, rows, r0 + BR);
+        if (side) colsum = lds_chain<false, BR>(nullptr, s_h + l, HS, r0, r0 + BR < rows ? r0 + BR : rows, colsum);
         if (owner) {
             // every slab runs all BR rows (rows past the chunk's hold
             // deltas +0 and inputs -0: a -0 product, no change); each step's
@@ -591,6 +680,7 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
         }
         __syncthreads();
     }
+    if (side) side_out[l] = colsum;
     if (!owner) return;
 #pragma unroll
     for (uint32_t q = 0; q < T; q++) {
@@ -608,9 +698,10 @@ __device__ __forceinline__ float row_advantage(const RowArgs& a, uint32_t m) {
 }
 // Per-row objective (ppo.hpp:144-181): log-probability of the stored
 // action, clipped surrogate with its active branch, value loss, and the
-// derivatives of the minibatch-mean objective (scale = 1/b).  Writes rs[0..3]
-// = d mean, rs[4..7] = d log_std, rs[8..11] = the row's policy, value and
-// entropy terms and its ratio.
+// derivatives of the minibatch-mean objective (scale = 1/b).  Writes scalar
+// i at rs[RSTRIDE i]: 0..3 d mean, 4..7 d log_std, 8..11 the row's policy,
+// value and entropy terms and its ratio.
+template <uint32_t RSTRIDE = 1>
 __device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls, uint32_t m, float adv,
                                               const float (&mean)[4], float value, float target, float scale,
                                               float (&dmean)[4], float* rs) {
@@ -645,28 +736,31 @@ __device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls,
         }
         dl -= a.ecoef * scale;
         entropy += -a.ecoef * (ls[q] + 0.5f * (1.0f + LOG_TWO_PI)) * scale;
-        rs[q] = dmean[q];
-        rs[4 + q] = dl;
+        rs[RSTRIDE * q] = dmean[q];
+        rs[RSTRIDE * (4 + q)] = dl;
     }
-    rs[8] = -chosen * scale;
-    rs[9] = 0.5f * a.vcoef * (value - target) * (value - target) * scale;
-    rs[10] = entropy;
-    rs[11] = ratio;
+    rs[RSTRIDE * 8] = -chosen * scale;
+    rs[RSTRIDE * 9] = 0.5f * a.vcoef * (value - target) * (value - target) * scale;
+    rs[RSTRIDE * 10] = entropy;
+    rs[RSTRIDE * 11] = ratio;
 }
 
 template <uint32_t D>
 __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     using L = AL<D>;
     __shared__ float s_h[256 * HS];
-    __shared__ float s_u[U_WORDS];
-    __shared__ float s_dv[256];
+    __shared__ __attribute__((aligned(16))) float s_u[U_WORDS];
+    __shared__ float s_aw[OBS_PAD * HID];  // the actor's first layer (stage_w1)
+    __shared__ __attribute__((aligned(16))) float s_dv[256];
     // the critic's w2 and the actor's W2 [4][64], read by every row's chains:
     // one LDS copy (broadcast reads) instead of per-step global loads
-    __shared__ float s_w2[5 * HID];
+    __shared__ __attribute__((aligned(16))) float s_w2[5 * HID];
     const uint32_t t = threadIdx.x, wv = t / 64;
     const bool rowt = t < 256;  // the row-wise phases' threads
     if (t < HID) s_w2[t] = a.critic[C_W2 + t];
     else if (t < 5 * HID) s_w2[t] = a.actor[L::W2 + t - HID];
+    stage_w1<COBS, COBS>(a.critic_w1t, s_u);
+    stage_w1<D, OBS_PAD>(a.actor_w1t, s_aw);
     const uint32_t n0 = blockIdx.x * 256;
     const uint32_t rows = a.b - n0 < 256 ? a.b - n0 : 256;
     const bool live = t < rows;
@@ -677,104 +771,122 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     const float adv = row_advantage(a, m);
 
     // ---- critic: forward, value, dV (ppo.hpp:82-93, 176-180)
-    chunk_forward<COBS>(a.co, a.critic_w1t, a.critic + C_B1, n0, a.b, s_u, s_h);
+    __syncthreads();
+    chunk_forward<COBS, COBS, false>(a.co, s_u, s_u + XW_BASE, a.critic + C_B1, n0, a.b, s_h);
     float value = a.critic[C_B2];
-    if (rowt)
-        for (uint32_t k = 0; k < HID; k++) value = fma_f(s_w2[k], s_h[t * HS + k], value);
+    if (rowt) value = lds_chain<true, HID>(s_w2, s_h + t * HS, 1, 0, HID, value);
     const float target = a.ret[m];
     const float dvalue = a.vcoef * (value - target) * scale;
     if (rowt) s_dv[t] = live ? dvalue : 0.0f;
     __syncthreads();
-    if (t < HID) {  // critic w2: fma over rows
-        float g = 0.0f;
-        #pragma unroll 16
-        for (uint32_t r = 0; r < rows; r++) g = fma_f(s_dv[r], s_h[r * HS + t], g);
-        P[L::COUNT + C_W2 + t] = g;
-    } else if (t == HID) {  // critic b2
-        float g = 0.0f;
-        #pragma unroll 16
-        for (uint32_t r = 0; r < rows; r++) g += s_dv[r];
-        P[L::COUNT + C_B2] = g;
-    }
+    if (t < HID)  // critic w2: fma over rows
+        P[L::COUNT + C_W2 + t] = lds_chain<true, 256>(s_dv, s_h + t, HS, 0, rows, 0.0f);
+    else if (t == 256)  // critic b2
+        P[L::COUNT + C_B2] = lds_chain<false, 256>(nullptr, s_dv, 1, 0, rows, 0.0f);
     __syncthreads();
-    if (rowt)
-        for (uint32_t k = 0; k < HID; k++) {  // critic hidden delta, in place
-            const float g = s_h[t * HS + k];
-            const float d = dvalue * s_w2[k] * (1.0f - g * g);
-            s_h[t * HS + k] = live ? d : 0.0f;
+    // critic hidden delta in place, row t % 256, units 32 (t / 256) .. + 31
+    const uint32_t hrow = t % 256, hk0 = 32 * (t / 256);
+    const bool hlive = hrow < rows;
+    {
+        const float dv = s_dv[hrow];
+#pragma unroll 8
+        for (uint32_t k = hk0; k < hk0 + 32; k++) {
+            const float g = s_h[hrow * HS + k];
+            const float d = dv * s_w2[k] * (1.0f - g * g);
+            s_h[hrow * HS + k] = hlive ? d : 0.0f;
         }
-    __syncthreads();
-    if (t < HID) {  // critic b1
-        float g = 0.0f;
-        #pragma unroll 16
-        for (uint32_t r = 0; r < rows; r++) g += s_h[r * HS + t];
-        P[L::COUNT + C_B1 + t] = g;
     }
-    {   // critic W1 [64][32]: wavefronts 0 and 1 own one 32x32 tile each
+    // critic W1 [64][32]: wavefronts 0 and 1 own one 32x32 tile each;
+    // wavefront 2 forms b1 meanwhile
+    {
         const uint32_t jt[1] = {wv & 1}, it[1] = {0};
-        chunk_weight_grad<COBS, 32, 1>(a.co, n0, rows, jt, it, wv < 2, s_u, s_h, P + L::COUNT);
+        chunk_weight_grad<COBS, 32, 1>(a.co, n0, rows, jt, it, wv < 2, wv == 2, s_u, s_h, P + L::COUNT,
+                                       P + L::COUNT + C_B1);
     }
 
     // ---- actor: forward, means, loss and derivatives
-    chunk_forward<D>(a.obs, a.actor_w1t, a.actor + L::B1, n0, a.b, s_u, s_h);
-    float dmean[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    chunk_forward<D, OBS_PAD, false>(a.obs, s_aw, s_u + XW_BASE, a.actor + L::B1, n0, a.b, s_h);
+    float* rs_t = s_u;  // per-row scalars [12][256] (scalar-major): the row slabs are done with
     if (rowt) {
         float mean[4];
 #pragma unroll
-        for (uint32_t q = 0; q < 4; q++) {
-            float z = a.actor[L::B2 + q];
-            for (uint32_t k = 0; k < HID; k++) z = fma_f(s_w2[HID + q * HID + k], s_h[t * HS + k], z);
-            // geometry prior (ppo.hpp:77): the hint inputs add to the first three means
-            if (D == MDN_ACTOR_OBS_PRIOR && q < 3) z += a.obs[size_t(m) * D + D - 3 + q];
-            mean[q] = z;
+        for (uint32_t q = 0; q < 4; q++) mean[q] = a.actor[L::B2 + q];
+        {   // the four chains over the hidden units side by side, each block
+            // of 8 units read before the previous block's fmas
+            constexpr uint32_t MB = 8;
+            float hv[2][MB];
+            float4 wv4[2][4][MB / 4];
+            auto load = [&](uint32_t p, uint32_t k0) {
+#pragma unroll
+                for (uint32_t i = 0; i < MB; i++) hv[p][i] = s_h[t * HS + k0 + i];
+#pragma unroll
+                for (uint32_t q = 0; q < 4; q++)
+#pragma unroll
+                    for (uint32_t i = 0; i < MB / 4; i++)
+                        wv4[p][q][i] = *reinterpret_cast<const float4*>(s_w2 + HID + q * HID + k0 + 4 * i);
+            };
+            auto use = [&](uint32_t p) {
+#pragma unroll
+                for (uint32_t i = 0; i < MB; i++)
+#pragma unroll
+                    for (uint32_t q = 0; q < 4; q++) mean[q] = fma_f(wv4[p][q][i / 4][i % 4], hv[p][i], mean[q]);
+            };
+            load(0, 0);
+#pragma unroll
+            for (uint32_t k0 = 0; k0 < HID; k0 += 2 * MB) {
+                load(1, k0 + MB);
+                use(0);
+                if (k0 + 2 * MB < HID) load(0, k0 + 2 * MB);
+                use(1);
+            }
         }
-        float* rs = s_u + t * RS;  // the forward's scratch is free now
-        row_objective(a, a.actor + L::LS, m, adv, mean, value, target, scale, dmean, rs);
+        // geometry prior (ppo.hpp:77): the hint inputs add to the first three means
+        if (D == MDN_ACTOR_OBS_PRIOR)
+#pragma unroll
+            for (uint32_t q = 0; q < 3; q++) mean[q] += a.obs[size_t(m) * D + D - 3 + q];
+        float dmean[4];
+        row_objective<256>(a, a.actor + L::LS, m, adv, mean, value, target, scale, dmean, rs_t + t);
         if (a.norm && live) a.adv_out[m] = adv;
     }
     __syncthreads();
-    if (rowt) {   // actor W2[q][k]: fma over rows; then b2, log_std and the metric sums
+    // the d means of row t % 256, read before the barrier after which the
+    // weight gradient's row slabs overwrite the per-row scalars
+    float dm[4];
+#pragma unroll
+    for (uint32_t q = 0; q < 4; q++) dm[q] = rs_t[q * 256 + hrow];
+    if (rowt) {   // actor W2[q][k]: fma over rows
         const uint32_t q = t / HID, k = t % HID;
-        float g = 0.0f;
-        #pragma unroll 16
-        for (uint32_t r = 0; r < rows; r++) g = fma_f(s_u[r * RS + q], s_h[r * HS + k], g);
-        P[L::W2 + q * HID + k] = g;
-        if (t < 12) {
-            const uint32_t col = t < 4 ? t : t < 8 ? 4 + (t - 4) : 8 + (t - 8);
-            float g2 = 0.0f;
-            #pragma unroll 16
-            for (uint32_t r = 0; r < rows; r++) g2 += s_u[r * RS + col];
-            P[t < 4 ? L::B2 + t : t < 8 ? L::LS + (t - 4) : L::COUNT + C_COUNT + (t - 8)] = g2;
-        }
+        P[L::W2 + q * HID + k] = lds_chain<true, 256>(rs_t + q * 256, s_h + k, HS, 0, rows, 0.0f);
+    } else if (t < 256 + 12) {  // b2, log_std and the metric sums: sums over rows
+        const uint32_t col = t - 256;
+        P[col < 4 ? L::B2 + col : col < 8 ? L::LS + (col - 4) : L::COUNT + C_COUNT + (col - 8)] =
+            lds_chain<false, 256>(nullptr, rs_t + col * 256, 1, 0, rows, 0.0f);
     }
     __syncthreads();
-    if (rowt)
-        for (uint32_t k = 0; k < HID; k++) {  // actor hidden delta, in place
+    {   // actor hidden delta in place, row t % 256, units 32 (t / 256) .. + 31
+#pragma unroll 8
+        for (uint32_t k = hk0; k < hk0 + 32; k++) {
             float d = 0.0f;
 #pragma unroll
-            for (uint32_t q = 0; q < 4; q++) d = fma_f(dmean[q], s_w2[HID + q * HID + k], d);
-            const float h = s_h[t * HS + k];
+            for (uint32_t q = 0; q < 4; q++) d = fma_f(dm[q], s_w2[HID + q * HID + k], d);
+            const float h = s_h[hrow * HS + k];
             const float dh = d * (1.0f - h * h);
-            s_h[t * HS + k] = live ? dh : 0.0f;
+            s_h[hrow * HS + k] = hlive ? dh : 0.0f;
         }
-    __syncthreads();
-    if (t < HID) {  // actor b1
-        float g = 0.0f;
-        #pragma unroll 16
-        for (uint32_t r = 0; r < rows; r++) g += s_h[r * HS + t];
-        P[L::B1 + t] = g;
     }
     // actor W1 [64][D]: 2 x 6 tiles of 32x32.  Wavefronts w and w + 4 share
     // a SIMD and take three tiles between them: tiles 2w and 2w + 1 for
-    // w < 4, tile w + 4 for the others.  Both paths run the same slabs and
-    // barriers (a workgroup barrier counts arrivals, not code positions).
+    // w < 4, tile w + 4 for the others; wavefront 4 also forms b1.  Both
+    // paths run the same slabs and barriers (a workgroup barrier counts
+    // arrivals, not code positions); the first slab's barrier also orders
+    // the deltas before their reads.
     if (wv < 4) {
         const uint32_t jt[2] = {(2 * wv) / 6, (2 * wv + 1) / 6};
         const uint32_t it[2] = {(2 * wv) % 6, (2 * wv + 1) % 6};
-        chunk_weight_grad<D, OBS_PAD, 2>(a.obs, n0, rows, jt, it, true, s_u, s_h, P);
+        chunk_weight_grad<D, OBS_PAD, 2>(a.obs, n0, rows, jt, it, true, false, s_u, s_h, P, nullptr);
     } else {
         const uint32_t jt[1] = {(wv + 4) / 6}, it[1] = {(wv + 4) % 6};
-        chunk_weight_grad<D, OBS_PAD, 1>(a.obs, n0, rows, jt, it, true, s_u, s_h, P);
+        chunk_weight_grad<D, OBS_PAD, 1>(a.obs, n0, rows, jt, it, true, wv == 4, s_u, s_h, P, P + L::B1);
     }
 }
 
