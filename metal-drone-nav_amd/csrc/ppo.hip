@@ -612,28 +612,33 @@ template <uint32_t W>
 struct RowSlab {
     float x[BR * W / CT];
 };
+// Column D (inside the padding, D < W) holds 1 for the chunk's rows: its
+// products with the deltas form the first-layer bias gradient in the same
+// chain (fma(d, 1, s) rounds as s + d).
 template <uint32_t D, uint32_t W>
 __device__ __forceinline__ void row_load(RowSlab<W>& f, const float* __restrict__ X, uint32_t n0, uint32_t rows,
                                          uint32_t r0) {
+    static_assert(D < W, "a padding column for the bias");
 #pragma unroll
     for (uint32_t j = 0; j < BR * W / CT; j++) {
         const uint32_t e = threadIdx.x + CT * j, rr = e / W, cc = e % W;
-        f.x[j] = (r0 + rr < rows && cc < D) ? X[size_t(n0 + r0 + rr) * D + cc] : -0.0f;
+        const bool rok = r0 + rr < rows;
+        const float v = X[size_t(n0 + (rok ? r0 + rr : 0)) * D + (cc < D ? cc : 0)];
+        f.x[j] = rok && cc < D ? v : (rok && cc == D ? 1.0f : -0.0f);
     }
 }
 
 // dW1[j][i] partial over the chunk's rows: A = delta^T (s_h, [row][64]),
 // B = the input rows streamed from global in slabs of 32 rows (W columns, a
-// multiple of 32 covering D) through LDS.  Wavefront tiles are the (jt[q],
-// it[q]) pairs.  The wavefront `side` (if any) also forms the first-layer
-// bias gradient of its lane's unit, the sum of s_h's column over the chunk's
-// rows (ascending from 0), slab by slab while the others run their tiles,
-// into side_out[lane].
+// multiple of 32 covering D and the ones column D) through LDS; the first
+// slab arrives in f, fetched by the caller ahead of time.  Wavefront tiles
+// are the (jt[q], it[q]) pairs; the tile holding column D also yields b1
+// (into b1_out).
 template <uint32_t D, uint32_t W, uint32_t T>
-__device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, uint32_t n0, uint32_t rows,
-                                                  const uint32_t (&jt)[T], const uint32_t (&it)[T], bool owner,
-                                                  bool side, float* s_u, const float* s_h, float* __restrict__ out,
-                                                  float* __restrict__ side_out) {
+__device__ __forceinline__ void chunk_weight_grad(RowSlab<W>& f, const float* __restrict__ X, uint32_t n0,
+                                                  uint32_t rows, const uint32_t (&jt)[T], const uint32_t (&it)[T],
+                                                  bool owner, float* s_u, const float* s_h, float* __restrict__ out,
+                                                  float* __restrict__ b1_out) {
     constexpr uint32_t WS = W + 32;  // slab row stride: the two k halves fall in different banks
     const uint32_t t = threadIdx.x, l = t % 64;
     float* sx = s_u;  // [BR][WS]
@@ -642,9 +647,6 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
     for (uint32_t q = 0; q < T; q++)
 #pragma unroll
         for (uint32_t r = 0; r < 16; r++) acc[q][r] = 0.0f;
-    float colsum = 0.0f;
-    RowSlab<W> f;
-    row_load<D, W>(f, X, n0, rows, 0);
     for (uint32_t r0 = 0; r0 < rows; r0 += BR) {
 #pragma unroll
         for (uint32_t j = 0; j < BR * W / CT; j++) {
@@ -653,7 +655,6 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
         }
         __syncthreads();
         if (r0 + BR < rows) row_load<D, W>(f, X, n0, rows, r0 + BR);
-        if (side) colsum = lds_chain<false, BR>(nullptr, s_h + l, HS, r0, r0 + BR < rows ? r0 + BR : rows, colsum);
         if (owner) {
             // every slab runs all BR rows (rows past the chunk's hold
             // deltas +0 and inputs -0: a -0 product, no change); each step's
@@ -680,14 +681,17 @@ __device__ __forceinline__ void chunk_weight_grad(const float* __restrict__ X, u
         }
         __syncthreads();
     }
-    if (side) side_out[l] = colsum;
     if (!owner) return;
 #pragma unroll
     for (uint32_t q = 0; q < T; q++) {
         const uint32_t i = 32 * it[q] + l % 32;
-        if (i < D)
+        if (i < D) {
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++) out[(32 * jt[q] + acc_row(l, r)) * D + i] = acc[q][r];
+        } else if (i == D) {
+#pragma unroll
+            for (uint32_t r = 0; r < 16; r++) b1_out[32 * jt[q] + acc_row(l, r)] = acc[q][r];
+        }
     }
 }
 
@@ -773,6 +777,8 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     // ---- critic: forward, value, dV (ppo.hpp:82-93, 176-180)
     __syncthreads();
     chunk_forward<COBS, COBS, false>(a.co, s_u, s_u + XW_BASE, a.critic + C_B1, n0, a.b, s_h);
+    RowSlab<2 * COBS> fc;  // the critic inputs' first row slab, fetched ahead of the W1 gradient
+    row_load<COBS, 2 * COBS>(fc, a.co, n0, rows, 0);
     float value = a.critic[C_B2];
     if (rowt) value = lds_chain<true, HID>(s_w2, s_h + t * HS, 1, 0, HID, value);
     const float target = a.ret[m];
@@ -796,16 +802,18 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
             s_h[hrow * HS + k] = hlive ? d : 0.0f;
         }
     }
-    // critic W1 [64][32]: wavefronts 0 and 1 own one 32x32 tile each;
-    // wavefront 2 forms b1 meanwhile
+    // critic W1 [64][32] and b1: wavefronts 0-3 own one 32x32 tile each
+    // (inputs 0-31, then the ones column and its padding)
     {
-        const uint32_t jt[1] = {wv & 1}, it[1] = {0};
-        chunk_weight_grad<COBS, 32, 1>(a.co, n0, rows, jt, it, wv < 2, wv == 2, s_u, s_h, P + L::COUNT,
-                                       P + L::COUNT + C_B1);
+        const uint32_t jt[1] = {wv & 1}, it[1] = {(wv / 2) & 1};
+        chunk_weight_grad<COBS, 2 * COBS, 1>(fc, a.co, n0, rows, jt, it, wv < 4, s_u, s_h, P + L::COUNT,
+                                             P + L::COUNT + C_B1);
     }
 
     // ---- actor: forward, means, loss and derivatives
     chunk_forward<D, OBS_PAD, false>(a.obs, s_aw, s_u + XW_BASE, a.actor + L::B1, n0, a.b, s_h);
+    RowSlab<OBS_PAD> fa;  // the inputs' first row slab, fetched ahead of the W1 gradient
+    row_load<D, OBS_PAD>(fa, a.obs, n0, rows, 0);
     float* rs_t = s_u;  // per-row scalars [12][256] (scalar-major): the row slabs are done with
     if (rowt) {
         float mean[4];
@@ -874,19 +882,19 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
             s_h[hrow * HS + k] = hlive ? dh : 0.0f;
         }
     }
-    // actor W1 [64][D]: 2 x 6 tiles of 32x32.  Wavefronts w and w + 4 share
-    // a SIMD and take three tiles between them: tiles 2w and 2w + 1 for
-    // w < 4, tile w + 4 for the others; wavefront 4 also forms b1.  Both
-    // paths run the same slabs and barriers (a workgroup barrier counts
-    // arrivals, not code positions); the first slab's barrier also orders
-    // the deltas before their reads.
+    // actor W1 [64][D] and b1 (the ones column D in tiles (j, 5)): 2 x 6
+    // tiles of 32x32.  Wavefronts w and w + 4 share a SIMD and take three
+    // tiles between them: tiles 2w and 2w + 1 for w < 4, tile w + 4 for the
+    // others.  Both paths run the same slabs and barriers (a workgroup
+    // barrier counts arrivals, not code positions); the first slab's barrier
+    // also orders the deltas before their reads.
     if (wv < 4) {
         const uint32_t jt[2] = {(2 * wv) / 6, (2 * wv + 1) / 6};
         const uint32_t it[2] = {(2 * wv) % 6, (2 * wv + 1) % 6};
-        chunk_weight_grad<D, OBS_PAD, 2>(a.obs, n0, rows, jt, it, true, false, s_u, s_h, P, nullptr);
+        chunk_weight_grad<D, OBS_PAD, 2>(fa, a.obs, n0, rows, jt, it, true, s_u, s_h, P, P + L::B1);
     } else {
         const uint32_t jt[1] = {(wv + 4) / 6}, it[1] = {(wv + 4) % 6};
-        chunk_weight_grad<D, OBS_PAD, 1>(a.obs, n0, rows, jt, it, true, wv == 4, s_u, s_h, P, P + L::B1);
+        chunk_weight_grad<D, OBS_PAD, 1>(fa, a.obs, n0, rows, jt, it, true, s_u, s_h, P, P + L::B1);
     }
 }
 
