@@ -177,72 +177,165 @@ __device__ __forceinline__ void fwd_first(v16f (&acc)[RT], const FwdW1<K>& f, co
         for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = mfma(f.w[ks], xf[rt][ks], acc[rt]);
 }
 
-template <uint32_t K, uint32_t NQ>
-__global__ __launch_bounds__(256, 1) void forward_kernel(const __bf16* __restrict__ Xb, uint32_t BP,
-                                                      const __bf16* __restrict__ Wb,
-                                                      const float* __restrict__ b1, const float* __restrict__ W2,
-                                                      const float* __restrict__ b2, uint32_t H, uint32_t B,
-                                                      float* __restrict__ out, float* __restrict__ part,
-                                                      const float* __restrict__ prior, uint32_t prior_stride) {
-    constexpr uint32_t KS = K / 16;
-    __shared__ float zs[4][RB * NQ];
+// WV = 4: one workgroup of four wavefronts per RB rows, each streaming its
+// units' W1 fragments from global memory (L2).  WV = 8: a workgroup covers
+// 2 RB rows; wavefronts g and g + 4 take the same 32 units of each tile for
+// their own RB rows, and the tile's W1 fragments (4 x K/16 x 1 KB, contiguous
+// in Wb) are staged once in LDS for both (double-buffered, one barrier per
+// tile), halving the W1 traffic per row; the per-wavefront partial sums of
+// a row meet in the same order as with WV = 4, so both give the same values.
+template <uint32_t K, uint32_t NQ, uint32_t WV>
+__global__ __launch_bounds__(64 * WV, 1) void forward_kernel(const __bf16* __restrict__ Xb, uint32_t BP,
+                                                          const __bf16* __restrict__ Wb,
+                                                          const float* __restrict__ b1, const float* __restrict__ W2,
+                                                          const float* __restrict__ b2, uint32_t H, uint32_t B,
+                                                          float* __restrict__ out, float* __restrict__ part,
+                                                          const float* __restrict__ prior, uint32_t prior_stride) {
+    static_assert(WV == 4 || WV == 8, "one or two row halves");
+    constexpr uint32_t KS = K / 16, NTH = 64 * WV, RBW = RB * WV / 4;
+    __shared__ float zs[WV][RB * NQ];
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64, half = l / 32, lr = l % 32;
-    const uint32_t r0 = blockIdx.x * RB;
+    const uint32_t grp = wv % 4, rh = wv / 4;
+    const uint32_t r0 = blockIdx.x * RBW + rh * RB;
     const uint32_t span = H / gridDim.y, h0 = blockIdx.y * span, h1 = h0 + span;
     bf8 xf[RT][KS];  // B operand: X[row r0 + 32 rt + l%32][16 ks + 8(l/32) ..]
 #pragma unroll
-    for (uint32_t rt = 0; rt < RT; rt++)
+    for (uint32_t rt = 0; rt < RT; rt++) {
+        const uint32_t row = r0 + 32 * rt + lr;
 #pragma unroll
-        for (uint32_t ks = 0; ks < KS; ks++)
-            xf[rt][ks] = *reinterpret_cast<const bf8*>(Xb + size_t(r0 + 32 * rt + lr) * K + 16 * ks + 8 * half);
+        for (uint32_t ks = 0; ks < KS; ks++) {
+            const bf8 v = *reinterpret_cast<const bf8*>(Xb + size_t(row < BP ? row : 0) * K + 16 * ks + 8 * half);
+            xf[rt][ks] = row < BP ? v : bf8{};
+        }
+    }
     v16f z[RT];
 #pragma unroll
     for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
         for (uint32_t r = 0; r < 16; r++) z[rt][r] = 0.0f;
-    // Software pipeline: the first layer of tile i+1 is issued before the
-    // activation and second layer of tile i, so the matrix cores work while
-    // the VALU evaluates tanh; weights are fetched two tiles ahead.  Tile
-    // indices past the slice are clamped (the extra work is discarded).
-    auto tile_unit = [&](uint32_t i) { return min(h0 + UT * i, h1 - UT) + 32 * wv; };
     const uint32_t ntile = span / UT;
-    FwdW1<K> w1;
-    fwd_load_w1(w1, Wb, b1, tile_unit(0), l);
-    bf8 wa[2];
-    fwd_load_w2<NQ>(wa, W2, H, tile_unit(0), l);
-    v16f acc[RT];
-    fwd_first(acc, w1, xf);
-    fwd_load_w1(w1, Wb, b1, tile_unit(1), l);
-    for (uint32_t i = 0; i < ntile; i++) {
-        bf8 wn[2];
-        fwd_load_w2<NQ>(wn, W2, H, tile_unit(i + 1), l);
-        v16f nx[RT];
-        fwd_first(nx, w1, xf);
-        fwd_load_w1(w1, Wb, b1, tile_unit(i + 2), l);
+    if constexpr (WV == 8) {
+        constexpr uint32_t NF = 4 * KS * 64, PER = (NF + NTH - 1) / NTH;  // 16-byte fragments per tile
+        constexpr uint32_t NV = (1 + NQ) * UT, PV = (NV + NTH - 1) / NTH;  // b1 and W2 [NQ][unit] of a tile's units
+        __shared__ bf8 ws[2][NF];
+        __shared__ __attribute__((aligned(16))) float wv2[2][NV];
+        auto tile_base = [&](uint32_t i) { return h0 + UT * i; };
+        bf8 stg[PER];
+        float stv[PV];
+        auto fetch = [&](uint32_t i) {
+            const uint32_t base = tile_base(i);
+            const bf8* src = reinterpret_cast<const bf8*>(Wb + frag(base, 0, 0, K));
 #pragma unroll
-        for (uint32_t rt = 0; rt < RT; rt++)
+            for (uint32_t j = 0; j < PER; j++) stg[j] = src[min(t + NTH * j, NF - 1)];
 #pragma unroll
-            for (uint32_t m = 0; m < 2; m++) {
-                bf8 hb;
+            for (uint32_t j = 0; j < PV; j++) {
+                const uint32_t e = min(t + NTH * j, NV - 1), q = e / UT, u = e % UT;  // q = 0: b1, else W2 row q - 1
+                stv[j] = q == 0 ? b1[base + u] : W2[size_t(q - 1) * H + base + u];
+            }
+        };
+        auto stage = [&](uint32_t buf) {
 #pragma unroll
-                for (uint32_t e = 0; e < 8; e++) hb[e] = (__bf16)tanh_fast(acc[rt][8 * m + e]);
-                z[rt] = mfma(wa[m], hb, z[rt]);
+            for (uint32_t j = 0; j < PER; j++)
+                if (t + NTH * j < NF) ws[buf][t + NTH * j] = stg[j];
+#pragma unroll
+            for (uint32_t j = 0; j < PV; j++)
+                if (t + NTH * j < NV) wv2[buf][t + NTH * j] = stv[j];
+        };
+        fetch(0);
+        stage(0);
+        for (uint32_t i = 0; i < ntile; i++) {
+            __syncthreads();  // tile i staged in buffer i & 1; the other is no longer read
+            if (i + 1 < ntile) fetch(i + 1);
+            const float* tv = wv2[i & 1];
+            const uint32_t uo = 32 * grp;  // the wavefront's units within the tile
+            v16f acc[RT];
+#pragma unroll
+            for (uint32_t g = 0; g < 4; g++) {
+                const float4 bias = *reinterpret_cast<const float4*>(tv + uo + 8 * g + 4 * half);
+#pragma unroll
+                for (uint32_t rt = 0; rt < RT; rt++) {
+                    acc[rt][4 * g] = bias.x; acc[rt][4 * g + 1] = bias.y;
+                    acc[rt][4 * g + 2] = bias.z; acc[rt][4 * g + 3] = bias.w;
+                }
+            }
+            // second-layer A operand: W2[q = l%32][unit of k slot 8(l/32) + e] (zero for q >= NQ)
+            bf8 wa[2];
+            {
+                const float* w2row = tv + UT * (1 + min(lr, NQ - 1));
+                const bool on = lr < NQ;
+#pragma unroll
+                for (uint32_t m = 0; m < 2; m++) {
+                    const float4 p = *reinterpret_cast<const float4*>(w2row + uo + 16 * m + 4 * half);
+                    const float4 q = *reinterpret_cast<const float4*>(w2row + uo + 16 * m + 8 + 4 * half);
+                    wa[m][0] = (__bf16)(on ? p.x : 0.0f); wa[m][1] = (__bf16)(on ? p.y : 0.0f);
+                    wa[m][2] = (__bf16)(on ? p.z : 0.0f); wa[m][3] = (__bf16)(on ? p.w : 0.0f);
+                    wa[m][4] = (__bf16)(on ? q.x : 0.0f); wa[m][5] = (__bf16)(on ? q.y : 0.0f);
+                    wa[m][6] = (__bf16)(on ? q.z : 0.0f); wa[m][7] = (__bf16)(on ? q.w : 0.0f);
+                }
+            }
+            const bf8* wt = ws[i & 1] + grp * KS * 64 + l;
+#pragma unroll
+            for (uint32_t ks = 0; ks < KS; ks++) {
+                const bf8 w = wt[ks * 64];
+#pragma unroll
+                for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = mfma(w, xf[rt][ks], acc[rt]);
             }
 #pragma unroll
-        for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = nx[rt];
-        wa[0] = wn[0];
-        wa[1] = wn[1];
+            for (uint32_t rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (uint32_t m = 0; m < 2; m++) {
+                    bf8 hb;
+#pragma unroll
+                    for (uint32_t e = 0; e < 8; e++) hb[e] = (__bf16)tanh_fast(acc[rt][8 * m + e]);
+                    z[rt] = mfma(wa[m], hb, z[rt]);
+                }
+            if (i + 1 < ntile) stage((i + 1) & 1);
+        }
+    } else {
+        // Software pipeline: the first layer of tile i+1 is issued before the
+        // activation and second layer of tile i, so the matrix cores work while
+        // the VALU evaluates tanh; weights are fetched two tiles ahead.  Tile
+        // indices past the slice are clamped (the extra work is discarded).
+        auto tile_unit = [&](uint32_t i) { return min(h0 + UT * i, h1 - UT) + 32 * wv; };
+        FwdW1<K> w1;
+        fwd_load_w1(w1, Wb, b1, tile_unit(0), l);
+        bf8 wa[2];
+        fwd_load_w2<NQ>(wa, W2, H, tile_unit(0), l);
+        v16f acc[RT];
+        fwd_first(acc, w1, xf);
+        fwd_load_w1(w1, Wb, b1, tile_unit(1), l);
+        for (uint32_t i = 0; i < ntile; i++) {
+            bf8 wn[2];
+            fwd_load_w2<NQ>(wn, W2, H, tile_unit(i + 1), l);
+            v16f nx[RT];
+            fwd_first(nx, w1, xf);
+            fwd_load_w1(w1, Wb, b1, tile_unit(i + 2), l);
+#pragma unroll
+            for (uint32_t rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (uint32_t m = 0; m < 2; m++) {
+                    bf8 hb;
+#pragma unroll
+                    for (uint32_t e = 0; e < 8; e++) hb[e] = (__bf16)tanh_fast(acc[rt][8 * m + e]);
+                    z[rt] = mfma(wa[m], hb, z[rt]);
+                }
+#pragma unroll
+            for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = nx[rt];
+            wa[0] = wn[0];
+            wa[1] = wn[1];
+        }
     }
-    // zT[q][row]: lanes 0-31, registers q < NQ
+    // zT[q][row]: lanes 0-31, registers q
     if (half == 0)
 #pragma unroll
         for (uint32_t rt = 0; rt < RT; rt++)
 #pragma unroll
             for (uint32_t q = 0; q < NQ; q++) zs[wv][(32 * rt + lr) * NQ + q] = z[rt][q];
     __syncthreads();
-    for (uint32_t i = t; i < RB * NQ; i += 256) {
-        const uint32_t row = r0 + i / NQ, q = i % NQ;
-        const float v = ((zs[0][i] + zs[1][i]) + zs[2][i]) + zs[3][i];
+    for (uint32_t i = t; i < RBW * NQ; i += NTH) {
+        const uint32_t hr = i / (RB * NQ), li = i % (RB * NQ);  // row half, entry within it
+        const uint32_t row = blockIdx.x * RBW + i / NQ, q = i % NQ;
+        const float v = ((zs[4 * hr][li] + zs[4 * hr + 1][li]) + zs[4 * hr + 2][li]) + zs[4 * hr + 3][li];
         if (row >= B) continue;
         if (gridDim.y == 1)
             out[size_t(row) * NQ + q] = prior && q < 3 ? (b2[q] + v) + prior[size_t(row) * prior_stride + q] : b2[q] + v;
@@ -334,10 +427,13 @@ __global__ __launch_bounds__(256) void logp_kernel(const float* __restrict__ mea
 }
 
 // ---------------------------------------------------------------- backward
-// Partial gradients of one (hidden tile, row chunk).  Each wavefront owns 32
-// units of the workgroup's 128-unit tile (W1 rows resident in registers) and
-// walks the chunk's rows in blocks of RB, everything in one accumulator
-// layout (lane -> unit l%32, register r -> row 32 rt + 8(r/4) + 4(l/32) + r%4):
+// Partial gradients of one (hidden tile, row chunk).  The workgroup's 128
+// units are four groups of 32; with WV = 4 wavefronts wavefront g owns group
+// g and both 32-row tiles of each RB-row block, with WV = 8 wavefronts g and
+// g + 4 share group g (each holding its W1 rows) and take one 32-row tile
+// each, so that two wavefronts per SIMD overlap one's matrix-core work with
+// the other's activations.  Everything runs in one accumulator layout
+// (lane -> unit l%32, register r -> row 32 rt + 8(r/4) + 4(l/32) + r%4):
 //   h      = tanh(X W1^T + b1)            bf16 MFMA, rows as A (from LDS)
 //   g      = dm W2^T                      fp32 MFMA 32x32x2 (the fma chain over q)
 //   delta  = g (1 - h^2);  db1 += delta   VALU, per lane
@@ -349,51 +445,53 @@ __global__ __launch_bounds__(256) void logp_kernel(const float* __restrict__ mea
 // register 8m + e), and the LDS operands are read in that order.  Rows of the
 // next block are fetched into registers during the current block (two LDS
 // buffers, one barrier per block).  Rows past the chunk carry dm = 0 and
-// contribute nothing.  Output: partial slot c = blockIdx.y of dW1p [c][H][D],
-// db1p [c][H], dW2p [c][NQ][H].
-template <uint32_t K, uint32_t NQ>
+// contribute nothing.  With WV = 8 the second wavefront of each group adds
+// its sums to the first's through LDS at the end.  Output: partial slot c =
+// blockIdx.y of dW1p [c][H][D], db1p [c][H], dW2p [c][NQ][H].
+template <uint32_t K, uint32_t NQ, uint32_t NTH>
 struct BwdStage {
     static constexpr uint32_t XS = K + 8, TS = RB + 4;   // row strides (bf16) of xs and xt
     static constexpr uint32_t XCH = RB * K / 8;          // 16-byte chunks of a block's rows
     static constexpr uint32_t TCH = K * RB / 8;
-    static constexpr uint32_t NX = (XCH + 255) / 256, NT = (TCH + 255) / 256;
+    static constexpr uint32_t NX = (XCH + NTH - 1) / NTH, NT = (TCH + NTH - 1) / NTH;
     bf8 x[NX], xt[NT];
     float d;
 };
 
-template <uint32_t K, uint32_t NQ>
-__device__ __forceinline__ void bwd_fetch(BwdStage<K, NQ>& f, const __bf16* __restrict__ Xb,
+template <uint32_t K, uint32_t NQ, uint32_t NTH>
+__device__ __forceinline__ void bwd_fetch(BwdStage<K, NQ, NTH>& f, const __bf16* __restrict__ Xb,
                                           const __bf16* __restrict__ XbT, uint32_t BP, uint32_t r0, uint32_t rend,
                                           const float* __restrict__ dm, uint32_t t) {
-    using S = BwdStage<K, NQ>;
+    using S = BwdStage<K, NQ, NTH>;
     constexpr uint32_t CH = K / 8;
 #pragma unroll
     for (uint32_t i = 0; i < S::NX; i++) {
-        const uint32_t e = min(t + 256 * i, S::XCH - 1);
+        const uint32_t e = min(t + NTH * i, S::XCH - 1);
         f.x[i] = *reinterpret_cast<const bf8*>(Xb + size_t(r0 + e / CH) * K + 8 * (e % CH));
     }
 #pragma unroll
     for (uint32_t i = 0; i < S::NT; i++) {
-        const uint32_t e = min(t + 256 * i, S::TCH - 1);
+        const uint32_t e = min(t + NTH * i, S::TCH - 1);
         f.xt[i] = *reinterpret_cast<const bf8*>(XbT + size_t(e / (RB / 8)) * BP + r0 + 8 * (e % (RB / 8)));
     }
     const uint32_t row = r0 + t / NQ;  // t < RB * NQ (256 threads cover RB * 4)
     f.d = (t < RB * NQ && row < rend) ? dm[size_t(min(row, rend - 1)) * NQ + t % NQ] : 0.0f;
 }
 
-template <uint32_t K, uint32_t NQ>
-__device__ __forceinline__ void bwd_store(const BwdStage<K, NQ>& f, __bf16* xs, __bf16* xt, float* dmt, uint32_t t) {
-    using S = BwdStage<K, NQ>;
+template <uint32_t K, uint32_t NQ, uint32_t NTH>
+__device__ __forceinline__ void bwd_store(const BwdStage<K, NQ, NTH>& f, __bf16* xs, __bf16* xt, float* dmt,
+                                          uint32_t t) {
+    using S = BwdStage<K, NQ, NTH>;
     constexpr uint32_t CH = K / 8;
     typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (uint32_t i = 0; i < S::NX; i++) {
-        const uint32_t e = t + 256 * i;
+        const uint32_t e = t + NTH * i;
         if (e < S::XCH) *reinterpret_cast<bf8*>(xs + (e / CH) * S::XS + 8 * (e % CH)) = f.x[i];
     }
 #pragma unroll
     for (uint32_t i = 0; i < S::NT; i++) {
-        const uint32_t e = t + 256 * i;
+        const uint32_t e = t + NTH * i;
         if (e < S::TCH) {
             __bf16* dst = xt + (e / (RB / 8)) * S::TS + 8 * (e % (RB / 8));  // 8-byte aligned rows
             const bf8 v = f.xt[i];
@@ -404,28 +502,40 @@ __device__ __forceinline__ void bwd_store(const BwdStage<K, NQ>& f, __bf16* xs, 
     if (t < RB * NQ) dmt[(t % NQ) * RB + t / NQ] = f.d;  // transposed: dmt [q][row]
 }
 
-template <uint32_t D, uint32_t K, uint32_t NQ>
-__global__ __launch_bounds__(256, NQ == 1 ? 2 : 1) void backward_kernel(const __bf16* __restrict__ Xb, const __bf16* __restrict__ XbT,
-                                                       uint32_t BP, const __bf16* __restrict__ Wb,
-                                                       const float* __restrict__ b1, const float* __restrict__ W2,
-                                                       const float* __restrict__ dm, uint32_t H, uint32_t B,
-                                                       uint32_t RC, float* __restrict__ dW1p,
-                                                       float* __restrict__ db1p, float* __restrict__ dW2p) {
-    using S = BwdStage<K, NQ>;
+template <uint32_t D, uint32_t K, uint32_t NQ, uint32_t WV>
+__global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_kernel(
+    const __bf16* __restrict__ Xb, const __bf16* __restrict__ XbT, uint32_t BP, const __bf16* __restrict__ Wb,
+    const float* __restrict__ b1, const float* __restrict__ W2, const float* __restrict__ dm, uint32_t H, uint32_t B,
+    uint32_t RC, float* __restrict__ dW1p, float* __restrict__ db1p, float* __restrict__ dW2p) {
+    static_assert(WV == 4 || WV == 8, "one or two wavefronts per unit group");
+    constexpr uint32_t NTH = 64 * WV, RTW = RT * 4 / WV;  // threads; 32-row tiles per wavefront and block
+    using S = BwdStage<K, NQ, NTH>;
     constexpr uint32_t XS = S::XS, TS = S::TS, JT = K / 32;
-    typedef float v2f __attribute__((ext_vector_type(2)));
     __shared__ __bf16 xs[2][RB * XS];   // [row][k]
     __shared__ __bf16 xt[2][K * TS];    // [k][row]
     __shared__ __attribute__((aligned(16))) float dmt[2][NQ * RB];  // [q][row]
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64, half = l / 32, lr = l % 32;
+    const uint32_t grp = wv % 4, rh = wv / 4;  // unit group; row tiles rh * RTW ..
     const uint32_t u0 = blockIdx.x * UT, c = blockIdx.y;
-    const uint32_t unit = u0 + 32 * wv + lr;
+    const uint32_t unit = u0 + 32 * grp + lr;
     const uint32_t rbeg = c * RC, rend = min(B, rbeg + RC);
     const float bias = b1[unit];
-    bf8 bw[K / 16];  // B operand of h: W1[unit][16 ks + 8(l/32) ..]
+    // B operand of h: W1[unit][16 ks + 8(l/32) ..].  WV = 4: in registers;
+    // WV = 8: the workgroup's 128 units (48 KB in fragment order, contiguous
+    // in Wb) staged once in LDS and read per step, which leaves the registers
+    // to the two wavefronts per SIMD.
+    constexpr uint32_t WF = WV == 8 ? 4 * (K / 16) * 64 : 1;  // 16-byte fragments staged
+    __shared__ bf8 ws[WF];
+    bf8 bw[WV == 8 ? 1 : K / 16];
+    if constexpr (WV == 8) {
+        const bf8* src = reinterpret_cast<const bf8*>(Wb + frag(u0, 0, 0, K));
+#pragma unroll 4
+        for (uint32_t i = t; i < WF; i += NTH) ws[i] = src[i];
+    } else {
 #pragma unroll
-    for (uint32_t ks = 0; ks < K / 16; ks++)
-        bw[ks] = *reinterpret_cast<const bf8*>(Wb + frag(u0 + 32 * wv, ks, l, K));
+        for (uint32_t ks = 0; ks < K / 16; ks++)
+            bw[ks] = *reinterpret_cast<const bf8*>(Wb + frag(u0 + 32 * grp, ks, l, K));
+    }
     // B operand of g: W2[q = 2 p + l/32][unit] (zero for q >= NQ)
     constexpr uint32_t NP = (NQ + 1) / 2;
     float w2f[NP];
@@ -443,7 +553,7 @@ __global__ __launch_bounds__(256, NQ == 1 ? 2 : 1) void backward_kernel(const __
     for (uint32_t r = 0; r < 16; r++) w2acc[r] = 0.0f;
     float db1a = 0.0f;
 
-    BwdStage<K, NQ> st;
+    S st;
     if (rbeg < rend) {
         bwd_fetch(st, Xb, XbT, BP, rbeg, rend, dm, t);
         bwd_store(st, xs[0], xt[0], dmt[0], t);
@@ -457,14 +567,16 @@ __global__ __launch_bounds__(256, NQ == 1 ? 2 : 1) void backward_kernel(const __
         const __bf16* XT = xt[buf];
         const float* DM = dmt[buf];
 #pragma unroll
-        for (uint32_t rt = 0; rt < RT; rt++) {
+        for (uint32_t ri = 0; ri < RTW; ri++) {
+            const uint32_t rt = rh * RTW + ri;
             v16f h;
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++) h[r] = bias;
 #pragma unroll
             for (uint32_t ks = 0; ks < K / 16; ks++) {
                 const bf8 av = *reinterpret_cast<const bf8*>(X + (32 * rt + lr) * XS + 16 * ks + 8 * half);
-                h = mfma(av, bw[ks], h);
+                const bf8 bv = WV == 8 ? ws[(grp * (K / 16) + ks) * 64 + l] : bw[WV == 8 ? 0 : ks];
+                h = mfma(av, bv, h);
             }
             v16f g;
 #pragma unroll
@@ -512,16 +624,52 @@ __global__ __launch_bounds__(256, NQ == 1 ? 2 : 1) void backward_kernel(const __
         }
         if (more) bwd_store(st, xs[buf ^ 1], xt[buf ^ 1], dmt[buf ^ 1], t);
     }
+    // lanes l and l + 32 hold the same unit
+    db1a += __shfl_xor(db1a, 32, 64);
+    if constexpr (WV == 8) {
+        // the second wavefront of each group hands its sums to the first
+        // through the (now idle) row staging buffer, three 16-register
+        // pieces (dW1 tiles, then dW2^T) per round: hand [piece][group][16][64],
+        // then db1 [group][64] in the first round
+        constexpr uint32_t NPC = JT + 1, PR = 3;
+        static_assert((PR * 4 * 16 + 4) * 64 * 4 <= sizeof(xs), "hand-over space");
+        float* hand = reinterpret_cast<float*>(&xs[0][0]);
+#pragma unroll
+        for (uint32_t p0 = 0; p0 < NPC; p0 += PR) {
+            __syncthreads();  // the staging buffers (or the previous round) are free
+            if (rh == 1) {
+#pragma unroll
+                for (uint32_t pi = 0; pi < PR; pi++) {
+                    if (p0 + pi >= NPC) break;
+                    const v16f& v = p0 + pi < JT ? gacc[p0 + pi] : w2acc;
+#pragma unroll
+                    for (uint32_t r = 0; r < 16; r++) hand[((pi * 4 + grp) * 16 + r) * 64 + l] = v[r];
+                }
+                if (p0 == 0) hand[PR * 4 * 16 * 64 + grp * 64 + l] = db1a;
+            }
+            __syncthreads();
+            if (rh == 0) {
+#pragma unroll
+                for (uint32_t pi = 0; pi < PR; pi++) {
+                    if (p0 + pi >= NPC) break;
+                    v16f& v = p0 + pi < JT ? gacc[p0 + pi] : w2acc;
+#pragma unroll
+                    for (uint32_t r = 0; r < 16; r++) v[r] += hand[((pi * 4 + grp) * 16 + r) * 64 + l];
+                }
+                if (p0 == 0) db1a += hand[PR * 4 * 16 * 64 + grp * 64 + l];
+            }
+        }
+        if (rh == 1) return;
+    }
 #pragma unroll
     for (uint32_t jt = 0; jt < JT; jt++) {
         const uint32_t j = 32 * jt + lr;
         if (j < D)
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++)
-                dW1p[(size_t(c) * H + u0 + 32 * wv + acc_row(l, r)) * D + j] = gacc[jt][r];
+                dW1p[(size_t(c) * H + u0 + 32 * grp + acc_row(l, r)) * D + j] = gacc[jt][r];
     }
-    // lanes l and l + 32 hold the same unit; dW2^T[q][unit] sits in lanes 0-31, registers q
-    db1a += __shfl_xor(db1a, 32, 64);
+    // dW2^T[q][unit] sits in lanes 0-31, registers q
     if (half == 0) {
         db1p[size_t(c) * H + unit] = db1a;
 #pragma unroll
@@ -694,10 +842,13 @@ hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, uint32_
 // units are split in up to 8
 // slices; `part` then holds the slices' partial sums (capacity
 // lp_forward_part_floats(B)).
+// Hidden-unit slices of a forward launch of B rows (workgroups of FWD_ROWS
+// rows): enough workgroups for one per CU where the tiles divide evenly.
+constexpr uint32_t FWD_WAVES = 8, FWD_ROWS = lp::RB * FWD_WAVES / 4;
 static uint32_t forward_slices(uint32_t B, uint32_t H) {
-    const uint32_t blocks = (B + lp::RB - 1) / lp::RB, tiles = H / lp::UT;
+    const uint32_t blocks = (B + FWD_ROWS - 1) / FWD_ROWS, tiles = H / lp::UT;
     uint32_t S = 1;
-    while (blocks * S < 512 && S < 8 && tiles % (2 * S) == 0) S *= 2;  // two workgroups per CU
+    while (blocks * S < 256 && S < 8 && tiles % (2 * S) == 0) S *= 2;
     return S;
 }
 
@@ -713,18 +864,18 @@ hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* a
     if ((d == MDN_ACTOR_OBS_PRIOR) != (prior != nullptr) && means) return hipErrorInvalidValue;
     const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
     const uint32_t S = forward_slices(B, H);
-    const dim3 grid(BP / lp::RB, S);
+    const dim3 grid((BP + FWD_ROWS - 1) / FWD_ROWS, S);
     const uint32_t A_B1 = H * d, A_W2 = A_B1 + H, A_B2 = A_W2 + 4 * H;
     const uint32_t C_B1 = H * lp::COBS, C_W2 = C_B1 + H, C_B2 = C_W2 + H;
     if (means) {
-        hipLaunchKernelGGL((lp::forward_kernel<lp::KA, 4>), grid, dim3(256), 0, st, xa, BP, awb, actor + A_B1,
+        hipLaunchKernelGGL((lp::forward_kernel<lp::KA, 4, FWD_WAVES>), grid, dim3(64 * FWD_WAVES), 0, st, xa, BP, awb, actor + A_B1,
                            actor + A_W2, actor + A_B2, H, B, means, part, prior, d);
         if (S > 1)
             hipLaunchKernelGGL(lp::part_sum_kernel, dim3((B * 4 + 255) / 256), dim3(256), 0, st, part, S, BP, B, 4u,
                                actor + A_B2, means, prior, d);
     }
     if (values) {
-        hipLaunchKernelGGL((lp::forward_kernel<lp::KC, 1>), grid, dim3(256), 0, st, xc, BP, cwb, critic + C_B1,
+        hipLaunchKernelGGL((lp::forward_kernel<lp::KC, 1, FWD_WAVES>), grid, dim3(64 * FWD_WAVES), 0, st, xc, BP, cwb, critic + C_B1,
                            critic + C_W2, critic + C_B2, H, B, values, part, nullptr, 0u);
         if (S > 1)
             hipLaunchKernelGGL(lp::part_sum_kernel, dim3((B + 255) / 256), dim3(256), 0, st, part, S, BP, B, 1u,
@@ -791,12 +942,12 @@ hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16*
     float* cb1 = cW1 + size_t(nc) * H * lp::COBS;
     float* cw2 = cb1 + size_t(nc) * H;
     if (d == MDN_ACTOR_OBS_POOLED)
-        hipLaunchKernelGGL((lp::backward_kernel<MDN_ACTOR_OBS_POOLED, lp::KA, 4>), dim3(H / lp::UT, na), dim3(256), 0,
+        hipLaunchKernelGGL((lp::backward_kernel<MDN_ACTOR_OBS_POOLED, lp::KA, 4, 8>), dim3(H / lp::UT, na), dim3(512), 0,
                            st, xa, xaT, BP, awb, actor + A_B1, actor + A_W2, dm, H, B, RA, aW1, ab1, aW2);
     else
-        hipLaunchKernelGGL((lp::backward_kernel<MDN_ACTOR_OBS_PRIOR, lp::KA, 4>), dim3(H / lp::UT, na), dim3(256), 0,
+        hipLaunchKernelGGL((lp::backward_kernel<MDN_ACTOR_OBS_PRIOR, lp::KA, 4, 8>), dim3(H / lp::UT, na), dim3(512), 0,
                            st, xa, xaT, BP, awb, actor + A_B1, actor + A_W2, dm, H, B, RA, aW1, ab1, aW2);
-    hipLaunchKernelGGL((lp::backward_kernel<lp::COBS, lp::KC, 1>), dim3(H / lp::UT, nc), dim3(256), 0, st, xc, xcT,
+    hipLaunchKernelGGL((lp::backward_kernel<lp::COBS, lp::KC, 1, 4>), dim3(H / lp::UT, nc), dim3(256), 0, st, xc, xcT,
                        BP, cwb, critic + C_B1, critic + C_W2, dv, H, B, RCc, cW1, cb1, cw2);
     auto sum = [&](const float* p, uint64_t n, uint32_t slots, float* out) {
         hipLaunchKernelGGL(lp::sum_slots_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, p, n, slots, out);
