@@ -631,9 +631,11 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
         // through the (now idle) row staging buffer, three 16-register
         // pieces (dW1 tiles, then dW2^T) per round: hand [piece][group][16][64],
         // then db1 [group][64] in the first round
-        constexpr uint32_t NPC = JT + 1, PR = 3;
-        static_assert((PR * 4 * 16 + 4) * 64 * 4 <= sizeof(xs), "hand-over space");
-        float* hand = reinterpret_cast<float*>(&xs[0][0]);
+        constexpr uint32_t NPC = JT + 1, PIECE = 4 * 16 * 64, ROOM = (sizeof(xs) / 4 - 4 * 64) / PIECE;
+        constexpr uint32_t PR = ROOM == 0 ? 1 : (ROOM < 3 ? ROOM : 3);
+        // staging buffers too small for one piece (small K): a buffer of its own
+        __shared__ float hand_own[ROOM == 0 ? PIECE + 4 * 64 : 1];
+        float* hand = ROOM == 0 ? hand_own : reinterpret_cast<float*>(&xs[0][0]);
 #pragma unroll
         for (uint32_t p0 = 0; p0 < NPC; p0 += PR) {
             __syncthreads();  // the staging buffers (or the previous round) are free
