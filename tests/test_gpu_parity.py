@@ -290,6 +290,26 @@ def test_production_path_bit_exact():
     assert not bad, bad
 
 
+@pytest.mark.parametrize("actor_obs", [181, 184])
+def test_partial_chunks_bit_exact(actor_obs):
+    """Minibatches whose last chunk is partial: 1,920 rows in minibatches of
+    600 (chunks of 256, 256 and 88 rows: the row sums' general loop, the
+    masked rows of the forward tiles and of the weight-gradient slabs with
+    their ones column) and a last minibatch of 120 rows (the one-chunk
+    path), two epochs and two iterations: every buffer at tolerance 0."""
+    say("case: partial chunks N=48 T=40 epochs=2 minibatch=600 actor_obs=%d" % actor_obs)
+    cfg = config(n=48, family=1, speed=1.0, distance=3.0, max_steps=30)
+    sim, ppo, ora = make_pair(cfg, 40, epochs=2, minibatch=600, actor_obs=actor_obs)
+    for it in range(2):
+        sim.collect()
+        ppo.rollout_update(it)
+        sim.sync()
+        ora.iteration(it)
+        bad = compare(sim, ora, ["advantages", "returns", "actor", "critic", "actor_m", "actor_v", "critic_m",
+                                 "critic_v", "metric_rows", "grad_norm_rows"] + ENV_BUFFERS + ROW_BUFFERS, tol=0.0)
+        assert not bad, (it, bad)
+
+
 def test_stress_scale_bit_exact():
     """65,536 envs (the scale-stress env count: 2,048 workgroups of the
     benchmark kernel), 4 ticks with episodes ending after 3 steps (resets at
