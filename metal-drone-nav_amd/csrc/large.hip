@@ -52,22 +52,38 @@ __device__ __forceinline__ float tanh_fast(float x) {
 // bf16 copies of the B rows of X[B][D] prepared once per minibatch: Xb
 // [BP][K] row-major and XbT [K][BP] transposed (BP = B rounded up to RB; inputs
 // past D and rows past B are zero).  Every hidden tile reads these instead of
-// converting the rows itself.
+// converting the rows itself.  A workgroup takes RB rows: each thread reads 8
+// consecutive inputs of a row (consecutive threads, consecutive inputs) and
+// writes them as one 16-byte bf16 chunk of Xb; the transposed copy goes
+// through an LDS tile so that each row of XbT is written in 16-byte chunks
+// of 8 rows.
 template <uint32_t D, uint32_t K>
 __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ X, uint32_t B, uint32_t BP,
                                                    __bf16* __restrict__ Xb, __bf16* __restrict__ XbT) {
-    const uint32_t row = blockIdx.x * 256 + threadIdx.x, k0 = 8 * blockIdx.y;
-    if (row >= BP) return;
-    bf8 v;
+    constexpr uint32_t CH = K / 8, TS = K + 8;  // chunks per row; tile row stride (bf16)
+    __shared__ __attribute__((aligned(16))) __bf16 tile[RB * TS];
+    const uint32_t t = threadIdx.x, r0 = blockIdx.x * RB;
+    for (uint32_t e = t; e < RB * CH; e += 256) {
+        const uint32_t rr = e / CH, c = e % CH, row = r0 + rr;
+        bf8 v;
 #pragma unroll
-    for (uint32_t j = 0; j < 8; j++) {
-        const uint32_t k = k0 + j;
-        v[j] = (__bf16)((row < B && k < D) ? X[size_t(row) * D + k] : 0.0f);
+        for (uint32_t j = 0; j < 8; j++) {
+            const uint32_t k = 8 * c + j;
+            const float x = X[size_t(row < B ? row : 0) * D + (k < D ? k : 0)];
+            v[j] = (__bf16)((row < B && k < D) ? x : 0.0f);
+        }
+        *reinterpret_cast<bf8*>(Xb + size_t(row) * K + 8 * c) = v;
+        if (XbT) *reinterpret_cast<bf8*>(tile + rr * TS + 8 * c) = v;
     }
-    *reinterpret_cast<bf8*>(Xb + size_t(row) * K + k0) = v;
-    if (XbT)
+    if (!XbT) return;
+    __syncthreads();
+    for (uint32_t e = t; e < K * (RB / 8); e += 256) {
+        const uint32_t k = e / (RB / 8), r8 = e % (RB / 8);
+        bf8 v;
 #pragma unroll
-        for (uint32_t j = 0; j < 8; j++) XbT[size_t(k0 + j) * BP + row] = v[j];
+        for (uint32_t j = 0; j < 8; j++) v[j] = tile[(8 * r8 + j) * TS + k];
+        *reinterpret_cast<bf8*>(XbT + size_t(k) * BP + r0 + 8 * r8) = v;
+    }
 }
 
 // Rows r0 .. r0+RB of the prepared copies into LDS: xs [RB][XS] from Xb and,
@@ -680,14 +696,24 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
 }
 
 // ---------------------------------------------------------------- reductions
-// grad[i] = sum over the `chunks` partial slots (slot-major, stride n).
-__global__ __launch_bounds__(256) void sum_slots_kernel(const float* __restrict__ part, uint64_t n, uint32_t chunks,
-                                                        float* __restrict__ grad) {
+// Up to six gradient segments in one launch: dst[s][j] = the sum over the
+// segment's `slots` partial slots (slot-major, stride n_s) in slot order.
+struct SumSegs {
+    const float* src[6];
+    float* dst[6];
+    uint64_t start[7];  // element offsets of the segments in the launch; start[6] = total
+    uint32_t slots[6];
+};
+__global__ __launch_bounds__(256) void sum_segments_kernel(SumSegs g) {
     const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= n) return;
+    if (i >= g.start[6]) return;
+    uint32_t sg = 0;
+    while (sg < 5 && i >= g.start[sg + 1]) sg++;
+    const uint64_t j = i - g.start[sg], n = g.start[sg + 1] - g.start[sg];
+    const float* src = g.src[sg];
     float s = 0.0f;
-    for (uint32_t c = 0; c < chunks; c++) s += part[uint64_t(c) * n + i];
-    grad[i] = s;
+    for (uint32_t c = 0; c < g.slots[sg]; c++) s += src[uint64_t(c) * n + j];
+    g.dst[sg][j] = s;
 }
 // Column sums over the minibatch rows of the 13 per-row terms (dm[4] -> b2,
 // dls[4] -> log_std, dv -> critic b2, loss[4] -> metrics): block b sums rows
@@ -824,15 +850,15 @@ hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, uint32_
     if (B == 0) return hipSuccess;
     if (obs && d != MDN_ACTOR_OBS_POOLED && d != MDN_ACTOR_OBS_PRIOR) return hipErrorInvalidValue;
     const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
-    const uint32_t gx = (BP + 255) / 256;
+    const uint32_t gx = BP / lp::RB;
     if (obs && d == MDN_ACTOR_OBS_POOLED)
-        hipLaunchKernelGGL((lp::prep_kernel<MDN_ACTOR_OBS_POOLED, lp::KA>), dim3(gx, lp::KA / 8), dim3(256), 0, st,
-                           obs, B, BP, xa, transposed ? xaT : nullptr);
+        hipLaunchKernelGGL((lp::prep_kernel<MDN_ACTOR_OBS_POOLED, lp::KA>), dim3(gx), dim3(256), 0, st, obs, B, BP, xa,
+                           transposed ? xaT : nullptr);
     if (obs && d == MDN_ACTOR_OBS_PRIOR)
-        hipLaunchKernelGGL((lp::prep_kernel<MDN_ACTOR_OBS_PRIOR, lp::KA>), dim3(gx, lp::KA / 8), dim3(256), 0, st,
-                           obs, B, BP, xa, transposed ? xaT : nullptr);
+        hipLaunchKernelGGL((lp::prep_kernel<MDN_ACTOR_OBS_PRIOR, lp::KA>), dim3(gx), dim3(256), 0, st, obs, B, BP, xa,
+                           transposed ? xaT : nullptr);
     if (co)
-        hipLaunchKernelGGL((lp::prep_kernel<lp::COBS, lp::KC>), dim3(gx, lp::KC / 8), dim3(256), 0, st, co, B, BP, xc,
+        hipLaunchKernelGGL((lp::prep_kernel<lp::COBS, lp::KC>), dim3(gx), dim3(256), 0, st, co, B, BP, xc,
                            transposed ? xcT : nullptr);
     return hipGetLastError();
 }
@@ -951,15 +977,19 @@ hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16*
                            st, xa, xaT, BP, awb, actor + A_B1, actor + A_W2, dm, H, B, RA, aW1, ab1, aW2);
     hipLaunchKernelGGL((lp::backward_kernel<lp::COBS, lp::KC, 1, 4>), dim3(H / lp::UT, nc), dim3(256), 0, st, xc, xcT,
                        BP, cwb, critic + C_B1, critic + C_W2, dv, H, B, RCc, cW1, cb1, cw2);
-    auto sum = [&](const float* p, uint64_t n, uint32_t slots, float* out) {
-        hipLaunchKernelGGL(lp::sum_slots_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, st, p, n, slots, out);
-    };
-    sum(aW1, uint64_t(H) * d, na, ga);
-    sum(ab1, H, na, ga + A_B1);
-    sum(aW2, 4ull * H, na, ga + A_W2);
-    sum(cW1, uint64_t(H) * lp::COBS, nc, gc);
-    sum(cb1, H, nc, gc + C_B1);
-    sum(cw2, H, nc, gc + C_W2);
+    lp::SumSegs g;
+    const float* srcs[6] = {aW1, ab1, aW2, cW1, cb1, cw2};
+    float* dsts[6] = {ga, ga + A_B1, ga + A_W2, gc, gc + C_B1, gc + C_W2};
+    const uint64_t ns[6] = {uint64_t(H) * d, H, 4ull * H, uint64_t(H) * lp::COBS, H, H};
+    const uint32_t slots[6] = {na, na, na, nc, nc, nc};
+    g.start[0] = 0;
+    for (int k = 0; k < 6; k++) {
+        g.src[k] = srcs[k];
+        g.dst[k] = dsts[k];
+        g.slots[k] = slots[k];
+        g.start[k + 1] = g.start[k] + ns[k];
+    }
+    hipLaunchKernelGGL(lp::sum_segments_kernel, dim3(uint32_t((g.start[6] + 255) / 256)), dim3(256), 0, st, g);
     hipLaunchKernelGGL(lp::column_part_kernel, dim3((B + lp::RB - 1) / lp::RB), dim3(256), 0, st, dm, dls, dv, loss, B,
                        col_part);
     return hipGetLastError();
