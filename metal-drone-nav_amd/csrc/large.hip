@@ -86,25 +86,6 @@ __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ X, 
     }
 }
 
-// Rows r0 .. r0+RB of the prepared copies into LDS: xs [RB][XS] from Xb and,
-// when xt is given, xt [K][TS] from XbT (16-byte copies).
-template <uint32_t K, uint32_t XS, uint32_t TS>
-__device__ __forceinline__ void stage_rows(const __bf16* __restrict__ Xb, const __bf16* __restrict__ XbT, uint32_t BP,
-                                           uint32_t r0, __bf16* xs, __bf16* xt) {
-    constexpr uint32_t CH = K / 8;
-#pragma unroll 4
-    for (uint32_t e = threadIdx.x; e < RB * CH; e += 256) {
-        const uint32_t rr = e / CH, k0 = 8 * (e % CH);
-        *reinterpret_cast<bf8*>(xs + rr * XS + k0) = *reinterpret_cast<const bf8*>(Xb + size_t(r0 + rr) * K + k0);
-    }
-    if (xt)
-#pragma unroll 4
-        for (uint32_t e = threadIdx.x; e < K * (RB / 8); e += 256) {
-            const uint32_t k = e / (RB / 8), c = 8 * (e % (RB / 8));
-            *reinterpret_cast<bf8*>(xt + k * TS + c) = *reinterpret_cast<const bf8*>(XbT + size_t(k) * BP + r0 + c);
-        }
-}
-
 // ---------------------------------------------------------------- weights
 // The bf16 copy of a first-layer matrix W [H][D] (inputs zero-padded to K) is
 // stored in fragment order: for each group of 32 units and each 16-wide k
@@ -136,80 +117,26 @@ __global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ W, 
 // 8(r/4) + 4(l/32) + r%4) is, rounded to bf16, already the B operand of the
 // second product zT[q][row] += W2[q][units] hT[units][row]: k slot
 // 8(l/32) + e of product m is register 8m + e, and the A operand holds W2
-// columns in that same unit order (rows q >= NQ zero).  A workgroup owns RB
-// rows; each wavefront takes 32 units of every 128-unit tile, keeps its rows'
-// fragments in registers, prefetches the next tile's weights and runs the
-// tile loop without barriers; the four wavefronts' partial sums meet once
-// in LDS.  blockIdx.y splits the hidden units into gridDim.y slices when
-// there are too few rows to fill the GPU: each slice writes part [S][BP][NQ]
-// and part_sum_kernel adds them in slice order.
-template <uint32_t K>
-struct FwdW1 {
-    bf8 w[K / 16];  // W1 rows of the wavefront's 32 units (A operand)
-    float4 bias[4]; // b1 of accumulator registers 4g .. 4g+3
-};
-
-template <uint32_t K>
-__device__ __forceinline__ void fwd_load_w1(FwdW1<K>& f, const __bf16* __restrict__ Wb, const float* __restrict__ b1,
-                                            uint32_t ub, uint32_t l) {
-    const uint32_t half = l / 32;
-#pragma unroll
-    for (uint32_t ks = 0; ks < K / 16; ks++)
-        f.w[ks] = *reinterpret_cast<const bf8*>(Wb + frag(ub, ks, l, K));
-#pragma unroll
-    for (uint32_t g = 0; g < 4; g++) f.bias[g] = *reinterpret_cast<const float4*>(b1 + ub + 8 * g + 4 * half);
-}
-
-// second-layer A operands of 32 units: W2[q = l%32][unit of k slot 8(l/32) + e] (zero for q >= NQ)
-template <uint32_t NQ>
-__device__ __forceinline__ void fwd_load_w2(bf8 (&wa)[2], const float* __restrict__ W2, uint32_t H, uint32_t ub,
-                                            uint32_t l) {
-    const uint32_t half = l / 32, lr = l % 32;
-    const float* w2row = W2 + size_t(min(lr, NQ - 1)) * H;
-#pragma unroll
-    for (uint32_t m = 0; m < 2; m++) {
-        const float4 p = *reinterpret_cast<const float4*>(w2row + ub + 16 * m + 4 * half);
-        const float4 q = *reinterpret_cast<const float4*>(w2row + ub + 16 * m + 8 + 4 * half);
-        const bool on = lr < NQ;
-        wa[m][0] = (__bf16)(on ? p.x : 0.0f); wa[m][1] = (__bf16)(on ? p.y : 0.0f);
-        wa[m][2] = (__bf16)(on ? p.z : 0.0f); wa[m][3] = (__bf16)(on ? p.w : 0.0f);
-        wa[m][4] = (__bf16)(on ? q.x : 0.0f); wa[m][5] = (__bf16)(on ? q.y : 0.0f);
-        wa[m][6] = (__bf16)(on ? q.z : 0.0f); wa[m][7] = (__bf16)(on ? q.w : 0.0f);
-    }
-}
-
-template <uint32_t K>
-__device__ __forceinline__ void fwd_first(v16f (&acc)[RT], const FwdW1<K>& f, const bf8 (&xf)[RT][K / 16]) {
-#pragma unroll
-    for (uint32_t rt = 0; rt < RT; rt++)
-#pragma unroll
-        for (uint32_t g = 0; g < 4; g++) {
-            acc[rt][4 * g] = f.bias[g].x; acc[rt][4 * g + 1] = f.bias[g].y;
-            acc[rt][4 * g + 2] = f.bias[g].z; acc[rt][4 * g + 3] = f.bias[g].w;
-        }
-#pragma unroll
-    for (uint32_t ks = 0; ks < K / 16; ks++)
-#pragma unroll
-        for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = mfma(f.w[ks], xf[rt][ks], acc[rt]);
-}
-
-// WV = 4: one workgroup of four wavefronts per RB rows, each streaming its
-// units' W1 fragments from global memory (L2).  WV = 8: a workgroup covers
-// 2 RB rows; wavefronts g and g + 4 take the same 32 units of each tile for
-// their own RB rows, and the tile's W1 fragments (4 x K/16 x 1 KB, contiguous
-// in Wb) are staged once in LDS for both (double-buffered, one barrier per
-// tile), halving the W1 traffic per row; the per-wavefront partial sums of
-// a row meet in the same order as with WV = 4, so both give the same values.
-template <uint32_t K, uint32_t NQ, uint32_t WV>
-__global__ __launch_bounds__(64 * WV, 1) void forward_kernel(const __bf16* __restrict__ Xb, uint32_t BP,
+// columns in that same unit order (rows q >= NQ zero).  A workgroup of eight
+// wavefronts owns FWD_RB = 2 RB rows: wavefronts g and g + 4 take the same
+// 32 units of every 128-unit tile for their own RB rows, whose fragments stay
+// in registers, and the tile's W1 fragments (4 x K/16 x 1 KB, contiguous in
+// Wb), biases and W2 columns are staged once in LDS for both (double-
+// buffered, one barrier per tile).  The four wavefronts of a row half meet
+// in LDS at the end, their partial sums added in unit-group order.
+// blockIdx.y splits the hidden units into gridDim.y slices when there are
+// too few rows to fill the GPU: each slice writes part [S][BP][NQ] and
+// part_sum_kernel adds them in slice order.
+constexpr uint32_t FWD_RB = 2 * RB;
+template <uint32_t K, uint32_t NQ>
+__global__ __launch_bounds__(512, 1) void forward_kernel(const __bf16* __restrict__ Xb, uint32_t BP,
                                                           const __bf16* __restrict__ Wb,
                                                           const float* __restrict__ b1, const float* __restrict__ W2,
                                                           const float* __restrict__ b2, uint32_t H, uint32_t B,
                                                           float* __restrict__ out, float* __restrict__ part,
                                                           const float* __restrict__ prior, uint32_t prior_stride) {
-    static_assert(WV == 4 || WV == 8, "one or two row halves");
-    constexpr uint32_t KS = K / 16, NTH = 64 * WV, RBW = RB * WV / 4;
-    __shared__ float zs[WV][RB * NQ];
+    constexpr uint32_t KS = K / 16, NTH = 512, RBW = FWD_RB;
+    __shared__ float zs[8][RB * NQ];
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64, half = l / 32, lr = l % 32;
     const uint32_t grp = wv % 4, rh = wv / 4;
     const uint32_t r0 = blockIdx.x * RBW + rh * RB;
@@ -230,7 +157,7 @@ __global__ __launch_bounds__(64 * WV, 1) void forward_kernel(const __bf16* __res
 #pragma unroll
         for (uint32_t r = 0; r < 16; r++) z[rt][r] = 0.0f;
     const uint32_t ntile = span / UT;
-    if constexpr (WV == 8) {
+    {
         constexpr uint32_t NF = 4 * KS * 64, PER = (NF + NTH - 1) / NTH;  // 16-byte fragments per tile
         constexpr uint32_t NV = (1 + NQ) * UT, PV = (NV + NTH - 1) / NTH;  // b1 and W2 [NQ][unit] of a tile's units
         __shared__ bf8 ws[2][NF];
@@ -306,39 +233,6 @@ __global__ __launch_bounds__(64 * WV, 1) void forward_kernel(const __bf16* __res
                     z[rt] = mfma(wa[m], hb, z[rt]);
                 }
             if (i + 1 < ntile) stage((i + 1) & 1);
-        }
-    } else {
-        // Software pipeline: the first layer of tile i+1 is issued before the
-        // activation and second layer of tile i, so the matrix cores work while
-        // the VALU evaluates tanh; weights are fetched two tiles ahead.  Tile
-        // indices past the slice are clamped (the extra work is discarded).
-        auto tile_unit = [&](uint32_t i) { return min(h0 + UT * i, h1 - UT) + 32 * wv; };
-        FwdW1<K> w1;
-        fwd_load_w1(w1, Wb, b1, tile_unit(0), l);
-        bf8 wa[2];
-        fwd_load_w2<NQ>(wa, W2, H, tile_unit(0), l);
-        v16f acc[RT];
-        fwd_first(acc, w1, xf);
-        fwd_load_w1(w1, Wb, b1, tile_unit(1), l);
-        for (uint32_t i = 0; i < ntile; i++) {
-            bf8 wn[2];
-            fwd_load_w2<NQ>(wn, W2, H, tile_unit(i + 1), l);
-            v16f nx[RT];
-            fwd_first(nx, w1, xf);
-            fwd_load_w1(w1, Wb, b1, tile_unit(i + 2), l);
-#pragma unroll
-            for (uint32_t rt = 0; rt < RT; rt++)
-#pragma unroll
-                for (uint32_t m = 0; m < 2; m++) {
-                    bf8 hb;
-#pragma unroll
-                    for (uint32_t e = 0; e < 8; e++) hb[e] = (__bf16)tanh_fast(acc[rt][8 * m + e]);
-                    z[rt] = mfma(wa[m], hb, z[rt]);
-                }
-#pragma unroll
-            for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = nx[rt];
-            wa[0] = wn[0];
-            wa[1] = wn[1];
         }
     }
     // zT[q][row]: lanes 0-31, registers q
@@ -648,10 +542,9 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
         // pieces (dW1 tiles, then dW2^T) per round: hand [piece][group][16][64],
         // then db1 [group][64] in the first round
         constexpr uint32_t NPC = JT + 1, PIECE = 4 * 16 * 64, ROOM = (sizeof(xs) / 4 - 4 * 64) / PIECE;
-        constexpr uint32_t PR = ROOM == 0 ? 1 : (ROOM < 3 ? ROOM : 3);
-        // staging buffers too small for one piece (small K): a buffer of its own
-        __shared__ float hand_own[ROOM == 0 ? PIECE + 4 * 64 : 1];
-        float* hand = ROOM == 0 ? hand_own : reinterpret_cast<float*>(&xs[0][0]);
+        static_assert(ROOM >= 1, "the staging buffer holds a hand-over round");
+        constexpr uint32_t PR = ROOM < 3 ? ROOM : 3;
+        float* hand = reinterpret_cast<float*>(&xs[0][0]);
 #pragma unroll
         for (uint32_t p0 = 0; p0 < NPC; p0 += PR) {
             __syncthreads();  // the staging buffers (or the previous round) are free
@@ -872,7 +765,7 @@ hipError_t lp_launch_prep(const float* obs, const float* co, uint32_t B, uint32_
 // lp_forward_part_floats(B)).
 // Hidden-unit slices of a forward launch of B rows (workgroups of FWD_ROWS
 // rows): enough workgroups for one per CU where the tiles divide evenly.
-constexpr uint32_t FWD_WAVES = 8, FWD_ROWS = lp::RB * FWD_WAVES / 4;
+constexpr uint32_t FWD_ROWS = lp::FWD_RB;
 static uint32_t forward_slices(uint32_t B, uint32_t H) {
     const uint32_t blocks = (B + FWD_ROWS - 1) / FWD_ROWS, tiles = H / lp::UT;
     uint32_t S = 1;
@@ -896,14 +789,14 @@ hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* a
     const uint32_t A_B1 = H * d, A_W2 = A_B1 + H, A_B2 = A_W2 + 4 * H;
     const uint32_t C_B1 = H * lp::COBS, C_W2 = C_B1 + H, C_B2 = C_W2 + H;
     if (means) {
-        hipLaunchKernelGGL((lp::forward_kernel<lp::KA, 4, FWD_WAVES>), grid, dim3(64 * FWD_WAVES), 0, st, xa, BP, awb, actor + A_B1,
+        hipLaunchKernelGGL((lp::forward_kernel<lp::KA, 4>), grid, dim3(512), 0, st, xa, BP, awb, actor + A_B1,
                            actor + A_W2, actor + A_B2, H, B, means, part, prior, d);
         if (S > 1)
             hipLaunchKernelGGL(lp::part_sum_kernel, dim3((B * 4 + 255) / 256), dim3(256), 0, st, part, S, BP, B, 4u,
                                actor + A_B2, means, prior, d);
     }
     if (values) {
-        hipLaunchKernelGGL((lp::forward_kernel<lp::KC, 1, FWD_WAVES>), grid, dim3(64 * FWD_WAVES), 0, st, xc, BP, cwb, critic + C_B1,
+        hipLaunchKernelGGL((lp::forward_kernel<lp::KC, 1>), grid, dim3(512), 0, st, xc, BP, cwb, critic + C_B1,
                            critic + C_W2, critic + C_B2, H, B, values, part, nullptr, 0u);
         if (S > 1)
             hipLaunchKernelGGL(lp::part_sum_kernel, dim3((B + 255) / 256), dim3(256), 0, st, part, S, BP, B, 1u,
