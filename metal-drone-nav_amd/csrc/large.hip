@@ -360,7 +360,7 @@ __global__ __launch_bounds__(256) void logp_kernel(const float* __restrict__ mea
 // blockIdx.y of dW1p [c][H][D], db1p [c][H], dW2p [c][NQ][H].
 template <uint32_t K, uint32_t NQ, uint32_t NTH>
 struct BwdStage {
-    static constexpr uint32_t XS = K + 8, TS = RB + 4;   // row strides (bf16) of xs and xt
+    static constexpr uint32_t XS = K + 8, TS = RB + 8;   // row strides (bf16) of xs and xt (16-byte multiples)
     static constexpr uint32_t XCH = RB * K / 8;          // 16-byte chunks of a block's rows
     static constexpr uint32_t TCH = K * RB / 8;
     static constexpr uint32_t NX = (XCH + NTH - 1) / NTH, NT = (TCH + NTH - 1) / NTH;
@@ -388,9 +388,17 @@ __device__ __forceinline__ void bwd_fetch(BwdStage<K, NQ, NTH>& f, const __bf16*
     f.d = (t < RB * NQ && row < rend) ? dm[size_t(min(row, rend - 1)) * NQ + t % NQ] : 0.0f;
 }
 
+// Position of a block row in the transposed LDS copies (xt, the bf16 dm):
+// bits 2 and 3 of the row swapped, so that the rows of one product's k slots
+// (16 m + 4 (l/32) + {0..3, 8..11}) lie in 8 consecutive positions and a
+// lane reads its B (or A) operand in one 16-byte load.
+__device__ __forceinline__ uint32_t kpos(uint32_t row) {
+    return (row & ~15u) | ((row & 4u) << 1) | ((row & 8u) >> 1) | (row & 3u);
+}
+
 template <uint32_t K, uint32_t NQ, uint32_t NTH>
 __device__ __forceinline__ void bwd_store(const BwdStage<K, NQ, NTH>& f, __bf16* xs, __bf16* xt, float* dmt,
-                                          uint32_t t) {
+                                          __bf16* dmb, uint32_t t) {
     using S = BwdStage<K, NQ, NTH>;
     constexpr uint32_t CH = K / 8;
     typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
@@ -403,13 +411,17 @@ __device__ __forceinline__ void bwd_store(const BwdStage<K, NQ, NTH>& f, __bf16*
     for (uint32_t i = 0; i < S::NT; i++) {
         const uint32_t e = t + NTH * i;
         if (e < S::TCH) {
-            __bf16* dst = xt + (e / (RB / 8)) * S::TS + 8 * (e % (RB / 8));  // 8-byte aligned rows
+            __bf16* dst = xt + (e / (RB / 8)) * S::TS;
+            const uint32_t r8 = 8 * (e % (RB / 8));
             const bf8 v = f.xt[i];
-            *reinterpret_cast<bf4*>(dst) = bf4{v[0], v[1], v[2], v[3]};
-            *reinterpret_cast<bf4*>(dst + 4) = bf4{v[4], v[5], v[6], v[7]};
+            *reinterpret_cast<bf4*>(dst + kpos(r8)) = bf4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<bf4*>(dst + kpos(r8 + 4)) = bf4{v[4], v[5], v[6], v[7]};
         }
     }
-    if (t < RB * NQ) dmt[(t % NQ) * RB + t / NQ] = f.d;  // transposed: dmt [q][row]
+    if (t < RB * NQ) {  // transposed: dmt [q][row] (fp32), dmb [q][kpos(row)] (bf16)
+        dmt[(t % NQ) * RB + t / NQ] = f.d;
+        dmb[(t % NQ) * RB + kpos(t / NQ)] = (__bf16)f.d;
+    }
 }
 
 template <uint32_t D, uint32_t K, uint32_t NQ, uint32_t WV>
@@ -424,6 +436,7 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
     __shared__ __bf16 xs[2][RB * XS];   // [row][k]
     __shared__ __bf16 xt[2][K * TS];    // [k][row]
     __shared__ __attribute__((aligned(16))) float dmt[2][NQ * RB];  // [q][row]
+    __shared__ __attribute__((aligned(16))) __bf16 dmb[2][NQ * RB];  // [q][kpos(row)]
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64, half = l / 32, lr = l % 32;
     const uint32_t grp = wv % 4, rh = wv / 4;  // unit group; row tiles rh * RTW ..
     const uint32_t u0 = blockIdx.x * UT, c = blockIdx.y;
@@ -466,7 +479,7 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
     S st;
     if (rbeg < rend) {
         bwd_fetch(st, Xb, XbT, BP, rbeg, rend, dm, t);
-        bwd_store(st, xs[0], xt[0], dmt[0], t);
+        bwd_store(st, xs[0], xt[0], dmt[0], dmb[0], t);
     }
     uint32_t buf = 0;
     for (uint32_t r0 = rbeg; r0 < rend; r0 += RB, buf ^= 1) {
@@ -476,6 +489,7 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
         const __bf16* X = xs[buf];
         const __bf16* XT = xt[buf];
         const float* DM = dmt[buf];
+        const __bf16* DMB = dmb[buf];
 #pragma unroll
         for (uint32_t ri = 0; ri < RTW; ri++) {
             const uint32_t rt = rh * RTW + ri;
@@ -508,31 +522,22 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
                     hb[e] = (__bf16)hv;
                     db[e] = (__bf16)d;
                 }
-                // rows of this product's k slots: 32 rt + 16 m + 4(l/32) + {0..3, 8..11}
-                const uint32_t rr = 32 * rt + 16 * m + 4 * half;
+                // rows of this product's k slots: 32 rt + 16 m + 4(l/32) + {0..3, 8..11},
+                // consecutive at kpos 32 rt + 16 m + 8(l/32) of the transposed copies
+                const uint32_t kp = 32 * rt + 16 * m + 8 * half;
                 {   // dW2^T: A = dm^T [q][rows] (q = l%32, zero past NQ)
-                    const float* dq = DM + min(lr, NQ - 1) * RB + rr;
-                    const float4 v0 = *reinterpret_cast<const float4*>(dq);
-                    const float4 v1 = *reinterpret_cast<const float4*>(dq + 8);
-                    const bool on = lr < NQ;
-                    bf8 am;
-                    am[0] = (__bf16)(on ? v0.x : 0.0f); am[1] = (__bf16)(on ? v0.y : 0.0f);
-                    am[2] = (__bf16)(on ? v0.z : 0.0f); am[3] = (__bf16)(on ? v0.w : 0.0f);
-                    am[4] = (__bf16)(on ? v1.x : 0.0f); am[5] = (__bf16)(on ? v1.y : 0.0f);
-                    am[6] = (__bf16)(on ? v1.z : 0.0f); am[7] = (__bf16)(on ? v1.w : 0.0f);
+                    const bf8 v = *reinterpret_cast<const bf8*>(DMB + min(lr, NQ - 1) * RB + kp);
+                    const bf8 am = lr < NQ ? v : bf8{};
                     w2acc = mfma(am, hb, w2acc);
                 }
 #pragma unroll
                 for (uint32_t jt = 0; jt < JT; jt++) {  // dW1: B = X [rows][k = 32 jt + l%32]
-                    typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
-                    const __bf16* src = XT + (32 * jt + lr) * TS + rr;
-                    const bf4 lo = *reinterpret_cast<const bf4*>(src), hi = *reinterpret_cast<const bf4*>(src + 8);
-                    const bf8 xb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    const bf8 xb = *reinterpret_cast<const bf8*>(XT + (32 * jt + lr) * TS + kp);
                     gacc[jt] = mfma(db, xb, gacc[jt]);
                 }
             }
         }
-        if (more) bwd_store(st, xs[buf ^ 1], xt[buf ^ 1], dmt[buf ^ 1], t);
+        if (more) bwd_store(st, xs[buf ^ 1], xt[buf ^ 1], dmt[buf ^ 1], dmb[buf ^ 1], t);
     }
     // lanes l and l + 32 hold the same unit
     db1a += __shfl_xor(db1a, 32, 64);
