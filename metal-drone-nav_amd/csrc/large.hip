@@ -159,37 +159,48 @@ __global__ __launch_bounds__(512, 1) void forward_kernel(const __bf16* __restric
     const uint32_t ntile = span / UT;
     {
         constexpr uint32_t NF = 4 * KS * 64, PER = (NF + NTH - 1) / NTH;  // 16-byte fragments per tile
-        constexpr uint32_t NV = (1 + NQ) * UT, PV = (NV + NTH - 1) / NTH;  // b1 and W2 [NQ][unit] of a tile's units
+        // per tile: the W1 fragments, b1 of the tile's units, and the second
+        // layer's A operand as bf16 fragments: thread t = (group g, product m,
+        // lane l) holds W2[q = l%32][unit 32 g + 16 m + 4(l/32) + {0..3, 8..11}]
+        // (zero for q >= NQ)
         __shared__ bf8 ws[2][NF];
-        __shared__ __attribute__((aligned(16))) float wv2[2][NV];
+        __shared__ __attribute__((aligned(16))) float wb1[2][UT];
+        __shared__ bf8 wfa[2][4 * 2 * 64];
+        static_assert(NTH == 4 * 2 * 64 && UT <= NTH, "one second-layer fragment and one bias per thread");
         auto tile_base = [&](uint32_t i) { return h0 + UT * i; };
         bf8 stg[PER];
-        float stv[PV];
+        float sb1 = 0.0f;
+        float4 sw2[2];
+        const uint32_t fg = t / 128, fm = (t / 64) % 2, fl = t % 64, fq = fl % 32, fh = fl / 32;
         auto fetch = [&](uint32_t i) {
             const uint32_t base = tile_base(i);
             const bf8* src = reinterpret_cast<const bf8*>(Wb + frag(base, 0, 0, K));
 #pragma unroll
             for (uint32_t j = 0; j < PER; j++) stg[j] = src[min(t + NTH * j, NF - 1)];
-#pragma unroll
-            for (uint32_t j = 0; j < PV; j++) {
-                const uint32_t e = min(t + NTH * j, NV - 1), q = e / UT, u = e % UT;  // q = 0: b1, else W2 row q - 1
-                stv[j] = q == 0 ? b1[base + u] : W2[size_t(q - 1) * H + base + u];
-            }
+            if (t < UT) sb1 = b1[base + t];
+            const float* w2 = W2 + size_t(min(fq, NQ - 1)) * H + base + 32 * fg + 16 * fm + 4 * fh;
+            sw2[0] = *reinterpret_cast<const float4*>(w2);
+            sw2[1] = *reinterpret_cast<const float4*>(w2 + 8);
         };
         auto stage = [&](uint32_t buf) {
 #pragma unroll
             for (uint32_t j = 0; j < PER; j++)
                 if (t + NTH * j < NF) ws[buf][t + NTH * j] = stg[j];
-#pragma unroll
-            for (uint32_t j = 0; j < PV; j++)
-                if (t + NTH * j < NV) wv2[buf][t + NTH * j] = stv[j];
+            if (t < UT) wb1[buf][t] = sb1;
+            const bool on = fq < NQ;
+            bf8 a;
+            a[0] = (__bf16)(on ? sw2[0].x : 0.0f); a[1] = (__bf16)(on ? sw2[0].y : 0.0f);
+            a[2] = (__bf16)(on ? sw2[0].z : 0.0f); a[3] = (__bf16)(on ? sw2[0].w : 0.0f);
+            a[4] = (__bf16)(on ? sw2[1].x : 0.0f); a[5] = (__bf16)(on ? sw2[1].y : 0.0f);
+            a[6] = (__bf16)(on ? sw2[1].z : 0.0f); a[7] = (__bf16)(on ? sw2[1].w : 0.0f);
+            wfa[buf][t] = a;
         };
         fetch(0);
         stage(0);
         for (uint32_t i = 0; i < ntile; i++) {
             __syncthreads();  // tile i staged in buffer i & 1; the other is no longer read
             if (i + 1 < ntile) fetch(i + 1);
-            const float* tv = wv2[i & 1];
+            const float* tv = wb1[i & 1];
             const uint32_t uo = 32 * grp;  // the wavefront's units within the tile
             v16f acc[RT];
 #pragma unroll
@@ -202,20 +213,7 @@ __global__ __launch_bounds__(512, 1) void forward_kernel(const __bf16* __restric
                 }
             }
             // second-layer A operand: W2[q = l%32][unit of k slot 8(l/32) + e] (zero for q >= NQ)
-            bf8 wa[2];
-            {
-                const float* w2row = tv + UT * (1 + min(lr, NQ - 1));
-                const bool on = lr < NQ;
-#pragma unroll
-                for (uint32_t m = 0; m < 2; m++) {
-                    const float4 p = *reinterpret_cast<const float4*>(w2row + uo + 16 * m + 4 * half);
-                    const float4 q = *reinterpret_cast<const float4*>(w2row + uo + 16 * m + 8 + 4 * half);
-                    wa[m][0] = (__bf16)(on ? p.x : 0.0f); wa[m][1] = (__bf16)(on ? p.y : 0.0f);
-                    wa[m][2] = (__bf16)(on ? p.z : 0.0f); wa[m][3] = (__bf16)(on ? p.w : 0.0f);
-                    wa[m][4] = (__bf16)(on ? q.x : 0.0f); wa[m][5] = (__bf16)(on ? q.y : 0.0f);
-                    wa[m][6] = (__bf16)(on ? q.z : 0.0f); wa[m][7] = (__bf16)(on ? q.w : 0.0f);
-                }
-            }
+            const bf8 wa[2] = {wfa[i & 1][(grp * 2 + 0) * 64 + l], wfa[i & 1][(grp * 2 + 1) * 64 + l]};
             const bf8* wt = ws[i & 1] + grp * KS * 64 + l;
 #pragma unroll
             for (uint32_t ks = 0; ks < KS; ks++) {
