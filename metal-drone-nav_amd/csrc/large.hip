@@ -7,8 +7,9 @@
 // W1 [H][32], b1 [H], w2 [H], b2) with fp32 Adam moments.  The 184-input
 // actor adds its last three inputs (the geometry-prior hint) to the first
 // three means (ppo.hpp:77) in fp32.  The first-layer matrices are also
-// kept as bf16 copies [H][K] (inputs zero-padded to K = 192 / 32) for the
-// GEMMs, refreshed by every Adam step.  GEMMs accumulate in fp32
+// kept as bf16 copies [H][K] (inputs zero-padded to K = 192 / 32, scaled by
+// 2 log2(e) for the activation's base-2 form) for the GEMMs, refreshed by
+// every Adam step.  GEMMs accumulate in fp32
 // (v_mfma_f32_32x32x16_bf16); activations use a fast exp-based tanh; the
 // hidden activations are never written to HBM: the backward pass recomputes
 // each tile.  Results match the fp32 CPU oracle within bf16 tolerance, not
@@ -42,10 +43,15 @@ __device__ __forceinline__ v16f mfma(bf8 a, bf8 b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 __device__ __forceinline__ uint32_t acc_row(uint32_t l, uint32_t r) { return 8 * (r / 4) + 4 * (l / 32) + (r % 4); }
-// tanh(x) = 1 - 2 / (e^{2x} + 1) with the hardware base-2 exponential and
-// reciprocal (v_exp_f32, v_rcp_f32; about 1 ulp each).
-__device__ __forceinline__ float tanh_fast(float x) {
-    const float e = __builtin_amdgcn_exp2f(x * 2.8853900817779268f);  // 2 log2(e) x
+// tanh(x) = 1 - 2 / (2^y + 1) with y = 2 log2(e) x, on the hardware base-2
+// exponential and reciprocal (v_exp_f32, v_rcp_f32; about 1 ulp each).  The
+// first layers' bf16 copies and biases are held multiplied by TANH_SCALE =
+// 2 log2(e) (pack_kernel, adam_kernel, the kernels' bias loads), so a hidden
+// unit's accumulator already holds y and the activation costs no multiply.
+constexpr float TANH_SCALE = 2.8853900817779268f;
+
+__device__ __forceinline__ float tanh_scaled(float y) {
+    const float e = __builtin_amdgcn_exp2f(y);
     return fma_f(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
 }
 
@@ -73,6 +79,9 @@ __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ X, 
             v[j] = (__bf16)((row < B && k < D) ? x : 0.0f);
         }
         *reinterpret_cast<bf8*>(Xb + size_t(row) * K + 8 * c) = v;
+        // the transposed copy carries a one in the first padding input: the
+        // backward's bias column (rows past B have zero deltas)
+        if (D < K && c == D / 8) v[D % 8] = (__bf16)1.0f;
         if (XbT) *reinterpret_cast<bf8*>(tile + rr * TS + 8 * c) = v;
     }
     if (!XbT) return;
@@ -104,7 +113,7 @@ __global__ __launch_bounds__(256) void pack_kernel(const float* __restrict__ W, 
     const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= uint64_t(H) * K) return;
     const uint32_t u = uint32_t(i / K), k = uint32_t(i % K);
-    out[wsw(u, k, K)] = (__bf16)(k < D ? W[uint64_t(u) * D + k] : 0.0f);
+    out[wsw(u, k, K)] = (__bf16)(k < D ? W[uint64_t(u) * D + k] * TANH_SCALE : 0.0f);
 }
 
 // ---------------------------------------------------------------- forward
@@ -167,16 +176,17 @@ __global__ __launch_bounds__(512, 1) void forward_kernel(const __bf16* __restric
         __shared__ __attribute__((aligned(16))) float wb1[2][UT];
         __shared__ bf8 wfa[2][4 * 2 * 64];
         static_assert(NTH == 4 * 2 * 64 && UT <= NTH, "one second-layer fragment and one bias per thread");
+        static_assert(NF % NTH == 0, "whole fragment rounds");
         auto tile_base = [&](uint32_t i) { return h0 + UT * i; };
-        bf8 stg[PER];
         float sb1 = 0.0f;
         float4 sw2[2];
         const uint32_t fg = t / 128, fm = (t / 64) % 2, fl = t % 64, fq = fl % 32, fh = fl / 32;
+        bf8 stg[PER];
         auto fetch = [&](uint32_t i) {
             const uint32_t base = tile_base(i);
             const bf8* src = reinterpret_cast<const bf8*>(Wb + frag(base, 0, 0, K));
 #pragma unroll
-            for (uint32_t j = 0; j < PER; j++) stg[j] = src[min(t + NTH * j, NF - 1)];
+            for (uint32_t j = 0; j < PER; j++) stg[j] = src[t + NTH * j];
             if (t < UT) sb1 = b1[base + t];
             const float* w2 = W2 + size_t(min(fq, NQ - 1)) * H + base + 32 * fg + 16 * fm + 4 * fh;
             sw2[0] = *reinterpret_cast<const float4*>(w2);
@@ -184,9 +194,8 @@ __global__ __launch_bounds__(512, 1) void forward_kernel(const __bf16* __restric
         };
         auto stage = [&](uint32_t buf) {
 #pragma unroll
-            for (uint32_t j = 0; j < PER; j++)
-                if (t + NTH * j < NF) ws[buf][t + NTH * j] = stg[j];
-            if (t < UT) wb1[buf][t] = sb1;
+            for (uint32_t j = 0; j < PER; j++) ws[buf][t + NTH * j] = stg[j];
+            if (t < UT) wb1[buf][t] = sb1 * TANH_SCALE;
             const bool on = fq < NQ;
             bf8 a;
             a[0] = (__bf16)(on ? sw2[0].x : 0.0f); a[1] = (__bf16)(on ? sw2[0].y : 0.0f);
@@ -195,6 +204,16 @@ __global__ __launch_bounds__(512, 1) void forward_kernel(const __bf16* __restric
             a[6] = (__bf16)(on ? sw2[1].z : 0.0f); a[7] = (__bf16)(on ? sw2[1].w : 0.0f);
             wfa[buf][t] = a;
         };
+        // activations of one row tile and their second-layer products
+        auto activate = [&](const v16f& a, const bf8 (&w)[2], v16f& zz) {
+#pragma unroll
+            for (uint32_t m = 0; m < 2; m++) {
+                bf8 hb;
+#pragma unroll
+                for (uint32_t e = 0; e < 8; e++) hb[e] = (__bf16)tanh_scaled(a[8 * m + e]);
+                zz = mfma(w[m], hb, zz);
+            }
+        };
         fetch(0);
         stage(0);
         for (uint32_t i = 0; i < ntile; i++) {
@@ -202,34 +221,27 @@ __global__ __launch_bounds__(512, 1) void forward_kernel(const __bf16* __restric
             if (i + 1 < ntile) fetch(i + 1);
             const float* tv = wb1[i & 1];
             const uint32_t uo = 32 * grp;  // the wavefront's units within the tile
-            v16f acc[RT];
+            v16f bias;
 #pragma unroll
             for (uint32_t g = 0; g < 4; g++) {
-                const float4 bias = *reinterpret_cast<const float4*>(tv + uo + 8 * g + 4 * half);
-#pragma unroll
-                for (uint32_t rt = 0; rt < RT; rt++) {
-                    acc[rt][4 * g] = bias.x; acc[rt][4 * g + 1] = bias.y;
-                    acc[rt][4 * g + 2] = bias.z; acc[rt][4 * g + 3] = bias.w;
-                }
+                const float4 b4 = *reinterpret_cast<const float4*>(tv + uo + 8 * g + 4 * half);
+                bias[4 * g] = b4.x; bias[4 * g + 1] = b4.y; bias[4 * g + 2] = b4.z; bias[4 * g + 3] = b4.w;
             }
             // second-layer A operand: W2[q = l%32][unit of k slot 8(l/32) + e] (zero for q >= NQ)
             const bf8 wa[2] = {wfa[i & 1][(grp * 2 + 0) * 64 + l], wfa[i & 1][(grp * 2 + 1) * 64 + l]};
             const bf8* wt = ws[i & 1] + grp * KS * 64 + l;
+            v16f acc[RT];
 #pragma unroll
-            for (uint32_t ks = 0; ks < KS; ks++) {
-                const bf8 w = wt[ks * 64];
+            for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = bias;
+            bf8 wv[KS];  // the tile's W1 fragments, all requested before the first product
 #pragma unroll
-                for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = mfma(w, xf[rt][ks], acc[rt]);
-            }
+            for (uint32_t ks = 0; ks < KS; ks++) wv[ks] = wt[ks * 64];
 #pragma unroll
-            for (uint32_t rt = 0; rt < RT; rt++)
+            for (uint32_t ks = 0; ks < KS; ks++)
 #pragma unroll
-                for (uint32_t m = 0; m < 2; m++) {
-                    bf8 hb;
+                for (uint32_t rt = 0; rt < RT; rt++) acc[rt] = mfma(wv[ks], xf[rt][ks], acc[rt]);
 #pragma unroll
-                    for (uint32_t e = 0; e < 8; e++) hb[e] = (__bf16)tanh_fast(acc[rt][8 * m + e]);
-                    z[rt] = mfma(wa[m], hb, z[rt]);
-                }
+            for (uint32_t rt = 0; rt < RT; rt++) activate(acc[rt], wa, z[rt]);
             if (i + 1 < ntile) stage((i + 1) & 1);
         }
     }
@@ -344,10 +356,13 @@ __global__ __launch_bounds__(256) void logp_kernel(const float* __restrict__ mea
 // (lane -> unit l%32, register r -> row 32 rt + 8(r/4) + 4(l/32) + r%4):
 //   h      = tanh(X W1^T + b1)            bf16 MFMA, rows as A (from LDS)
 //   g      = dm W2^T                      fp32 MFMA 32x32x2 (the fma chain over q)
-//   delta  = g (1 - h^2);  db1 += delta   VALU, per lane
+//   delta  = g (1 - h^2)                  VALU, per lane
 //   dW2^T += dm^T h                       bf16 MFMA, h from registers as B
 //   dW1   += delta^T X                    bf16 MFMA, delta from registers as A,
 //                                         X^T rows from LDS as B
+//   db1   += delta                        the dW1 product's column of ones
+//                                         (input D) when the inputs are
+//                                         padded (D < K), else VALU per lane
 // The rows are the reduction dimension of the last two products; their k
 // slots follow the accumulator's row order (slot 8(l/32) + e of product m is
 // register 8m + e), and the LDS operands are read in that order.  Rows of the
@@ -434,13 +449,13 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
     __shared__ __bf16 xs[2][RB * XS];   // [row][k]
     __shared__ __bf16 xt[2][K * TS];    // [k][row]
     __shared__ __attribute__((aligned(16))) float dmt[2][NQ * RB];  // [q][row]
-    __shared__ __attribute__((aligned(16))) __bf16 dmb[2][NQ * RB];  // [q][kpos(row)]
+    __shared__ __attribute__((aligned(16))) __bf16 dmb[2][(NQ + 1) * RB];  // [q][kpos(row)]; row NQ zero
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64, half = l / 32, lr = l % 32;
     const uint32_t grp = wv % 4, rh = wv / 4;  // unit group; row tiles rh * RTW ..
     const uint32_t u0 = blockIdx.x * UT, c = blockIdx.y;
     const uint32_t unit = u0 + 32 * grp + lr;
     const uint32_t rbeg = c * RC, rend = min(B, rbeg + RC);
-    const float bias = b1[unit];
+    const float bias = b1[unit] * TANH_SCALE;
     // B operand of h: W1[unit][16 ks + 8(l/32) ..].  WV = 4: in registers;
     // WV = 8: the workgroup's 128 units (48 KB in fragment order, contiguous
     // in Wb) staged once in LDS and read per step, which leaves the registers
@@ -472,7 +487,12 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
         for (uint32_t r = 0; r < 16; r++) gacc[jt][r] = 0.0f;
 #pragma unroll
     for (uint32_t r = 0; r < 16; r++) w2acc[r] = 0.0f;
+    // db1: with padding inputs (D < K) the transposed rows carry ones in
+    // input column D (prep_kernel), so the dW1 tile holding that column also
+    // yields the bias sums; otherwise the deltas are summed per lane
+    constexpr bool ONES = D < K;
     float db1a = 0.0f;
+    for (uint32_t i = t; i < 2 * RB; i += NTH) dmb[i / RB][NQ * RB + i % RB] = (__bf16)0.0f;
 
     S st;
     if (rbeg < rend) {
@@ -483,7 +503,6 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
     for (uint32_t r0 = rbeg; r0 < rend; r0 += RB, buf ^= 1) {
         __syncthreads();  // block r0 staged in buf; buf ^ 1 no longer read
         const bool more = r0 + RB < rend;
-        if (more) bwd_fetch(st, Xb, XbT, BP, r0 + RB, rend, dm, t);
         const __bf16* X = xs[buf];
         const __bf16* XT = xt[buf];
         const float* DM = dmt[buf];
@@ -494,12 +513,17 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
             v16f h;
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++) h[r] = bias;
+            bf8 av[K / 16], bv[K / 16];  // requested ahead of the products (the compiler keeps several in flight)
 #pragma unroll
             for (uint32_t ks = 0; ks < K / 16; ks++) {
-                const bf8 av = *reinterpret_cast<const bf8*>(X + (32 * rt + lr) * XS + 16 * ks + 8 * half);
-                const bf8 bv = WV == 8 ? ws[(grp * (K / 16) + ks) * 64 + l] : bw[WV == 8 ? 0 : ks];
-                h = mfma(av, bv, h);
+                av[ks] = *reinterpret_cast<const bf8*>(X + (32 * rt + lr) * XS + 16 * ks + 8 * half);
+                bv[ks] = WV == 8 ? ws[(grp * (K / 16) + ks) * 64 + l] : bw[WV == 8 ? 0 : ks];
             }
+#pragma unroll
+            for (uint32_t ks = 0; ks < K / 16; ks++) h = mfma(av[ks], bv[ks], h);
+            // the next block's rows, requested once the products no longer
+            // need the registers
+            if (ri == 0 && more) bwd_fetch(st, Xb, XbT, BP, r0 + RB, rend, dm, t);
             v16f g;
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++) g[r] = 0.0f;
@@ -514,9 +538,9 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
                 bf8 hb, db;
 #pragma unroll
                 for (uint32_t e = 0; e < 8; e++) {
-                    const float hv = tanh_fast(h[8 * m + e]);
-                    const float d = g[8 * m + e] * (1.0f - hv * hv);
-                    db1a += d;
+                    const float hv = tanh_scaled(h[8 * m + e]);
+                    const float d = g[8 * m + e] * fma_f(-hv, hv, 1.0f);
+                    if constexpr (!ONES) db1a += d;
                     hb[e] = (__bf16)hv;
                     db[e] = (__bf16)d;
                 }
@@ -524,8 +548,7 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
                 // consecutive at kpos 32 rt + 16 m + 8(l/32) of the transposed copies
                 const uint32_t kp = 32 * rt + 16 * m + 8 * half;
                 {   // dW2^T: A = dm^T [q][rows] (q = l%32, zero past NQ)
-                    const bf8 v = *reinterpret_cast<const bf8*>(DMB + min(lr, NQ - 1) * RB + kp);
-                    const bf8 am = lr < NQ ? v : bf8{};
+                    const bf8 am = *reinterpret_cast<const bf8*>(DMB + min(lr, NQ) * RB + kp);
                     w2acc = mfma(am, hb, w2acc);
                 }
 #pragma unroll
@@ -538,7 +561,7 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
         if (more) bwd_store(st, xs[buf ^ 1], xt[buf ^ 1], dmt[buf ^ 1], dmb[buf ^ 1], t);
     }
     // lanes l and l + 32 hold the same unit
-    db1a += __shfl_xor(db1a, 32, 64);
+    if constexpr (!ONES) db1a += __shfl_xor(db1a, 32, 64);
     if constexpr (WV == 8) {
         // the second wavefront of each group hands its sums to the first
         // through the (now idle) row staging buffer, three 16-register
@@ -559,7 +582,7 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
 #pragma unroll
                     for (uint32_t r = 0; r < 16; r++) hand[((pi * 4 + grp) * 16 + r) * 64 + l] = v[r];
                 }
-                if (p0 == 0) hand[PR * 4 * 16 * 64 + grp * 64 + l] = db1a;
+                if (!ONES && p0 == 0) hand[PR * 4 * 16 * 64 + grp * 64 + l] = db1a;
             }
             __syncthreads();
             if (rh == 0) {
@@ -570,7 +593,7 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
 #pragma unroll
                     for (uint32_t r = 0; r < 16; r++) v[r] += hand[((pi * 4 + grp) * 16 + r) * 64 + l];
                 }
-                if (p0 == 0) db1a += hand[PR * 4 * 16 * 64 + grp * 64 + l];
+                if (!ONES && p0 == 0) db1a += hand[PR * 4 * 16 * 64 + grp * 64 + l];
             }
         }
         if (rh == 1) return;
@@ -578,14 +601,18 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
 #pragma unroll
     for (uint32_t jt = 0; jt < JT; jt++) {
         const uint32_t j = 32 * jt + lr;
-        if (j < D)
+        if (j < D) {
 #pragma unroll
             for (uint32_t r = 0; r < 16; r++)
                 dW1p[(size_t(c) * H + u0 + 32 * grp + acc_row(l, r)) * D + j] = gacc[jt][r];
+        } else if (ONES && j == D) {
+#pragma unroll
+            for (uint32_t r = 0; r < 16; r++) db1p[size_t(c) * H + u0 + 32 * grp + acc_row(l, r)] = gacc[jt][r];
+        }
     }
     // dW2^T[q][unit] sits in lanes 0-31, registers q
     if (half == 0) {
-        db1p[size_t(c) * H + unit] = db1a;
+        if (!ONES) db1p[size_t(c) * H + unit] = db1a;
 #pragma unroll
         for (uint32_t q = 0; q < NQ; q++) dW2p[(size_t(c) * NQ + q) * H + unit] = w2acc[q];
     }
@@ -723,8 +750,8 @@ __global__ __launch_bounds__(256) void adam_kernel(LargeAdamArgs a) {
     float w = params[p] - a.lr * (mi / a.c1) / (sqrt_f(vi / a.c2) + 1.0e-8f);
     if (!critic && p >= A_LS) w = clamp_f(w, -2.0f, 0.5f);
     params[p] = w;
-    if (!critic && p < A_B1) a.actor_wb[wsw(p / D, p % D, KA)] = (__bf16)w;
-    if (critic && p < C_B1) a.critic_wb[wsw(p / COBS, p % COBS, KC)] = (__bf16)w;
+    if (!critic && p < A_B1) a.actor_wb[wsw(p / D, p % D, KA)] = (__bf16)(w * TANH_SCALE);
+    if (critic && p < C_B1) a.critic_wb[wsw(p / COBS, p % COBS, KC)] = (__bf16)(w * TANH_SCALE);
 }
 
 }  // namespace lp
