@@ -1684,7 +1684,7 @@ hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int 
 #define NAV_ROLLOUT_CASE(G, K, W, X, D) NAV_ROLLOUT_CASE_DYN(G, K, W, X, D, false)
     constexpr uint32_t P = MDN_ACTOR_OBS_POOLED, H = MDN_ACTOR_OBS_PRIOR;
     // the Crazyflie plant as compile-time constants (the common plant of the
-    // fused 8-lane instances)
+    // 8-lane instances with two ring slots, fused or split)
     const bool cf = !dyn && std::memcmp(&a->phys, &mdn::kCrazyflie, sizeof(MdnPhysicsParams)) == 0;
 #define NAV_ROLLOUT_CASE_CF(G, K, W, X, D)                                                                     \
     if (cf && lanes_per_env == G && ring_slots == K && (a->ext_means != nullptr) == X && actor_obs == D) {     \
@@ -1695,6 +1695,7 @@ hipError_t nav_launch_rollout(const nav::RolloutArgs* a, int lanes_per_env, int 
     }
     NAV_ROLLOUT_CASE_CF(8, 2, 4, false, P) NAV_ROLLOUT_CASE_CF(8, 4, 4, false, P)
     NAV_ROLLOUT_CASE_CF(8, 2, 4, false, H)
+    NAV_ROLLOUT_CASE_CF(8, 2, 4, true, P) NAV_ROLLOUT_CASE_CF(8, 2, 4, true, H)
 #undef NAV_ROLLOUT_CASE_CF
     NAV_ROLLOUT_CASE(8, 2, 4, false, P) NAV_ROLLOUT_CASE(8, 4, 4, false, P) NAV_ROLLOUT_CASE(8, 8, 4, false, P)
     NAV_ROLLOUT_CASE(16, 2, 1, false, P) NAV_ROLLOUT_CASE(16, 4, 1, false, P) NAV_ROLLOUT_CASE(16, 8, 1, false, P)
