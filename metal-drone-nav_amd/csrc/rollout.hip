@@ -700,24 +700,65 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     Run r;
     load_state(a.state, N, nn, s);
     load_run(a.run, N, nn, r);
-    for (uint32_t i = lane; i < WORLD_WORDS; i += G) world[i] = a.world[size_t(nn) * WORLD_WORDS + i];
-    for (uint32_t i = lane; i < 32; i += G) s_cmd[grp][i] = a.commands[size_t(nn) * 32 + i];
+    // the env's rows: fixed trip counts, every load issued before the first
+    // store (a split-tick launch pays this once per tick)
+    {
+        constexpr uint32_t WR = (WORLD_WORDS + G - 1) / G;
+        float wv[WR];
+#pragma unroll
+        for (uint32_t j = 0; j < WR; j++) {
+            const uint32_t i = lane + G * j;
+            wv[j] = a.world[size_t(nn) * WORLD_WORDS + (i < WORLD_WORDS ? i : 0)];
+        }
+        constexpr uint32_t CR = (32 + G - 1) / G;
+        float cv[CR];
+#pragma unroll
+        for (uint32_t j = 0; j < CR; j++) {
+            const uint32_t i = lane + G * j;
+            cv[j] = a.commands[size_t(nn) * 32 + (i < 32 ? i : 0)];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < WR; j++)
+            if (lane + G * j < WORLD_WORDS) world[lane + G * j] = wv[j];
+#pragma unroll
+        for (uint32_t j = 0; j < CR; j++)
+            if (lane + G * j < 32) s_cmd[grp][lane + G * j] = cv[j];
+    }
     {   // pooled ring cache: LDS slot f%K holds frame f for the last K frames
         // (a launch that begins at act already holds the frame cast for the
-        // current step, if one was due)
+        // current step, if one was due); the 2x2 minima of the group's
+        // K * POOL cells, ten cells' loads per lane in flight per round
         const int last = (SPLIT && (a.split & SPLIT_BEGIN_AT_ACT)) ? int(r.steps / C.sensor_period)
                          : r.steps == 0                         ? -1
                                                                 : int((r.steps - 1) / C.sensor_period);
-        for (uint32_t e = lane; e < uint32_t(K) * POOL; e += G) {
-            const int j = int(e / POOL), b = int(e % POOL);
-            const int f = last - j;
-            const uint32_t slot8 = uint32_t(((f % 8) + 8) % 8), slotk = uint32_t(((f % K) + K) % K);
-            const float* src = a.sensors + (size_t(nn) * 8 + slot8) * PIX;
-            const uint32_t y = (b / 10) * 2, x = (b % 10) * 2;
-            float m = 12.0f;
-            for (uint32_t dy = 0; dy < 2; dy++)
-                for (uint32_t dx = 0; dx < 2; dx++) m = min_f(m, src[(y + dy) * 20 + x + dx]);
-            if (live) pring(grp)[slotk * POOL + b] = m;
+        constexpr uint32_t RC = (uint32_t(K) * POOL + G - 1) / G, CH = 10;  // cells per lane; per round
+        for (uint32_t c0 = 0; c0 < RC; c0 += CH) {
+            float px[CH][4];
+#pragma unroll
+            for (uint32_t c = 0; c < CH; c++) {
+                const uint32_t e0 = lane + G * (c0 + c), e = e0 < uint32_t(K) * POOL ? e0 : 0;
+                const int j = int(e / POOL), b = int(e % POOL);
+                const int f = last - j;
+                const uint32_t slot8 = uint32_t(((f % 8) + 8) % 8);
+                const float* src = a.sensors + (size_t(nn) * 8 + slot8) * PIX;
+                const uint32_t y = (b / 10) * 2, x = (b % 10) * 2;
+#pragma unroll
+                for (uint32_t dy = 0; dy < 2; dy++)
+#pragma unroll
+                    for (uint32_t dx = 0; dx < 2; dx++) px[c][2 * dy + dx] = src[(y + dy) * 20 + x + dx];
+            }
+#pragma unroll
+            for (uint32_t c = 0; c < CH; c++) {
+                const uint32_t e = lane + G * (c0 + c);
+                if (e >= uint32_t(K) * POOL) continue;
+                const int j = int(e / POOL), b = int(e % POOL);
+                const int f = last - j;
+                const uint32_t slotk = uint32_t(((f % K) + K) % K);
+                float m = 12.0f;
+#pragma unroll
+                for (uint32_t q = 0; q < 4; q++) m = min_f(m, px[c][q]);
+                if (live) pring(grp)[slotk * POOL + b] = m;
+            }
         }
     }
     // this lane's RAPTOR units (hidden values it owns)
