@@ -586,6 +586,26 @@ __device__ __forceinline__ void raptor_wave(const float* RW, const RaptorRegs& o
 // Tails of the flat policy vectors (ppo.hpp:35-45) from the first bias on:
 // actor b1[HID], W2[4][HID], b2[4], log_std[4]; critic b1[HID], W2[HID], b2.
 constexpr uint32_t ACTOR_TAIL = 5 * HID + 8, CRITIC_TAIL = 2 * HID + 1;
+
+// Stages NW consecutive words into LDS with the workgroup's NTH threads:
+// every thread's loads are issued before its first store (fixed trip count).
+template <uint32_t NW, uint32_t NTH>
+struct WordStage {
+    static constexpr uint32_t R = (NW + NTH - 1) / NTH;
+    float v[R];
+    __device__ __forceinline__ void load(const float* __restrict__ src, uint32_t t) {
+#pragma unroll
+        for (uint32_t j = 0; j < R; j++) {
+            const uint32_t i = t + NTH * j;
+            v[j] = src[i < NW ? i : 0];
+        }
+    }
+    __device__ __forceinline__ void store(float* dst, uint32_t t) const {
+#pragma unroll
+        for (uint32_t j = 0; j < R; j++)
+            if (t + NTH * j < NW) dst[t + NTH * j] = v[j];
+    }
+};
 template <int W, uint32_t D>
 struct WeightLds {
     float aw[D * HID];
@@ -644,12 +664,18 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
 #pragma unroll 8
             for (uint32_t i = threadIdx.x; i < D * HID; i += 64 * W) s_wt.aw[i] = a.actor_w1t[i];
         }
-        for (uint32_t i = threadIdx.x; i < RAPTOR_WORDS; i += 64 * W) s_wt.rw[i] = a.raptor[i];
-        for (uint32_t i = threadIdx.x; i < 3 * PIX; i += 64 * W) s_wt.cam[i] = a.camera[i];
-        if constexpr (!X)
-            for (uint32_t i = threadIdx.x; i < ACTOR_TAIL; i += 64 * W) s_wt.pol[i] = a.actor[HID * D + i];
-        for (uint32_t i = threadIdx.x; i < CRITIC_TAIL; i += 64 * W)
-            s_wt.pol[ACTOR_TAIL + i] = a.critic[HID * COBS + i];
+        WordStage<RAPTOR_WORDS, 64 * W> st_rw;
+        WordStage<3 * PIX, 64 * W> st_cam;
+        WordStage<ACTOR_TAIL, 64 * W> st_at;
+        WordStage<CRITIC_TAIL, 64 * W> st_ct;
+        st_rw.load(a.raptor, threadIdx.x);
+        st_cam.load(a.camera, threadIdx.x);
+        if constexpr (!X) st_at.load(a.actor + HID * D, threadIdx.x);
+        st_ct.load(a.critic + HID * COBS, threadIdx.x);
+        st_rw.store(s_wt.rw, threadIdx.x);
+        st_cam.store(s_wt.cam, threadIdx.x);
+        if constexpr (!X) st_at.store(s_wt.pol, threadIdx.x);
+        st_ct.store(s_wt.pol + ACTOR_TAIL, threadIdx.x);
         __syncthreads();
         if constexpr (!X) {  // the action noise scales are fixed for the launch
             if (threadIdx.x < 8) {
@@ -765,8 +791,18 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     float hu[U];
 #pragma unroll
     for (int j = 0; j < U; j++) hu[j] = bits_float(a.run[size_t(RW_HIDDEN + lane + G * j) * N + nn]);
-    if constexpr (W > 1)
-        for (uint32_t c = lane; c < 16; c += G) s_rh[grp][c] = bits_float(a.run[size_t(RW_HIDDEN + c) * N + nn]);
+    if constexpr (W > 1) {
+        constexpr uint32_t HR = (16 + G - 1) / G;
+        float hv[HR];
+#pragma unroll
+        for (uint32_t j = 0; j < HR; j++) {
+            const uint32_t c = lane + G * j;
+            hv[j] = bits_float(a.run[size_t(RW_HIDDEN + (c < 16 ? c : 0)) * N + nn]);
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < HR; j++)
+            if (lane + G * j < 16) s_rh[grp][lane + G * j] = hv[j];
+    }
     const float* A = a.actor;
     const float* CR = a.critic;
     const uint32_t a_b1 = HID * D, a_w2 = a_b1 + HID, a_b2 = a_w2 + 4 * HID;
