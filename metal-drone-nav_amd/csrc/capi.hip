@@ -1612,13 +1612,14 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
             if (e == hipSuccess)
                 e = lp_launch_loss(p->means, p->values, s->actions + size_t(begin) * 4, s->logp + begin,
                                    s->advantages + begin, s->returns + begin, p->actor + p->shape.actor_log_std(), b,
-                                   0.2f, 0.5f, s->cfg.entropy_coef, p->dm, p->dls, p->dv, p->loss, s->stream);
+                                   0.2f, 0.5f, s->cfg.entropy_coef, p->dm, p->dls, p->dv, p->loss, p->col_part,
+                                   s->stream);
             return e;
         });
         if (rc) return rc;
         rc = timed(s, MDN_K_LP_BACKWARD, [&] {
-            return lp_launch_backward(p->xa, p->xaT, p->xc, p->xcT, p->awb, p->cwb, p->actor, p->critic, p->dm, p->dls,
-                                      p->dv, p->loss, H, D, b, p->part, p->ga, p->gc, p->col_part, s->stream);
+            return lp_launch_backward(p->xa, p->xaT, p->xc, p->xcT, p->awb, p->cwb, p->actor, p->critic, p->dm, p->dv, H,
+                                      D, b, p->part, p->ga, p->gc, s->stream);
         });
         if (rc) return rc;
         ++p->optimizer_step;

@@ -233,12 +233,12 @@ hipError_t lp_launch_logp(const float* means, const float* actions, const float*
                           hipStream_t st);
 hipError_t lp_launch_loss(const float* means, const float* values, const float* actions, const float* old_logp,
                           const float* adv, const float* ret, const float* log_std, uint32_t B, float clip,
-                          float vcoef, float ecoef, float* dm, float* dls, float* dv, float* loss, hipStream_t st);
+                          float vcoef, float ecoef, float* dm, float* dls, float* dv, float* loss, float* col_part,
+                          hipStream_t st);
 hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16* xc, const __bf16* xcT,
-                              const __bf16* awb, const __bf16* cwb,
-                              const float* actor, const float* critic, const float* dm, const float* dls,
-                              const float* dv, const float* loss, uint32_t H, uint32_t d, uint32_t B,
-                              float* part, float* ga, float* gc, float* col_part, hipStream_t st);
+                              const __bf16* awb, const __bf16* cwb, const float* actor, const float* critic,
+                              const float* dm, const float* dv, uint32_t H, uint32_t d, uint32_t B, float* part,
+                              float* ga, float* gc, hipStream_t st);
 uint64_t lp_backward_part_floats(uint32_t B, uint32_t H, uint32_t d);
 hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
                           __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,

@@ -282,15 +282,15 @@ __global__ __launch_bounds__(256) void part_sum_kernel(const float* __restrict__
 // sample_loss_and_grad (ppo.hpp:144-181) per minibatch row from the means and
 // values of the forward kernels.  Writes dmean[4], dlog_std[4], dvalue and the
 // four loss terms.
-__global__ __launch_bounds__(256) void loss_kernel(const float* __restrict__ mean, const float* __restrict__ value,
-                                                   const float* __restrict__ actions, const float* __restrict__ old_logp,
-                                                   const float* __restrict__ adv, const float* __restrict__ ret,
-                                                   const float* __restrict__ log_std, uint32_t B, float clip,
-                                                   float vcoef, float ecoef, float* __restrict__ dm,
-                                                   float* __restrict__ dls, float* __restrict__ dv,
-                                                   float* __restrict__ loss) {
-    const uint32_t n = blockIdx.x * 256 + threadIdx.x;
-    if (n >= B) return;
+// Per-row clipped-surrogate, value and entropy terms (ppo.hpp:144-181) of
+// row n, written to the row records and to column t of cs.
+__device__ __forceinline__ void row_loss(const float* __restrict__ mean, const float* __restrict__ value,
+                                         const float* __restrict__ actions, const float* __restrict__ old_logp,
+                                         const float* __restrict__ adv, const float* __restrict__ ret,
+                                         const float* __restrict__ log_std, uint32_t B, float clip, float vcoef,
+                                         float ecoef, uint32_t n, float* __restrict__ dm, float* __restrict__ dls,
+                                         float* __restrict__ dv, float* __restrict__ loss, float (*cs)[RB + 1],
+                                         uint32_t t) {
     const float* act = actions + size_t(n) * 4;
     const float* mu = mean + size_t(n) * 4;
     const float scale = 1.0f / max_f(float(B), 1.0f);
@@ -322,13 +322,48 @@ __global__ __launch_bounds__(256) void loss_kernel(const float* __restrict__ mea
         entropy += -ecoef * (log_std[q] + 0.5f * (1.0f + LOG_TWO_PI)) * scale;
         dm[size_t(n) * 4 + q] = g;
         dls[size_t(n) * 4 + q] = gl;
+        cs[q][t] = g;
+        cs[4 + q][t] = gl;
     }
-    dv[n] = vcoef * (v - target) * scale;
+    const float dvn = vcoef * (v - target) * scale;
+    const float l0 = -chosen * scale, l1 = 0.5f * vcoef * (v - target) * (v - target) * scale;
+    dv[n] = dvn;
     float* lo = loss + size_t(n) * 4;
-    lo[0] = -chosen * scale;
-    lo[1] = 0.5f * vcoef * (v - target) * (v - target) * scale;
+    lo[0] = l0;
+    lo[1] = l1;
     lo[2] = entropy;
     lo[3] = ratio;
+    cs[8][t] = dvn;
+    cs[9][t] = l0;
+    cs[10][t] = l1;
+    cs[11][t] = entropy;
+    cs[12][t] = ratio;
+}
+
+__global__ __launch_bounds__(RB) void loss_kernel(const float* __restrict__ mean, const float* __restrict__ value,
+                                                  const float* __restrict__ actions, const float* __restrict__ old_logp,
+                                                  const float* __restrict__ adv, const float* __restrict__ ret,
+                                                  const float* __restrict__ log_std, uint32_t B, float clip,
+                                                  float vcoef, float ecoef, float* __restrict__ dm,
+                                                  float* __restrict__ dls, float* __restrict__ dv,
+                                                  float* __restrict__ loss, float* __restrict__ col_part) {
+    // block b takes rows b*RB ..; its 13 per-row terms (dm[4] -> b2,
+    // dls[4] -> log_std, dv -> critic b2, loss[4] -> metrics) are then summed
+    // over those rows in order into col_part[b][13] (column_finish_kernel
+    // adds the blocks in order)
+    __shared__ float cs[13][RB + 1];
+    const uint32_t t = threadIdx.x, n = blockIdx.x * RB + t;
+    if (n >= B) {
+        for (uint32_t c = 0; c < 13; c++) cs[c][t] = 0.0f;
+    } else {
+        row_loss(mean, value, actions, old_logp, adv, ret, log_std, B, clip, vcoef, ecoef, n, dm, dls, dv, loss, cs, t);
+    }
+    __syncthreads();
+    if (t < 13) {
+        float a = 0.0f;
+        for (uint32_t rr = 0; rr < RB; rr++) a += cs[t][rr];
+        col_part[size_t(blockIdx.x) * 13 + t] = a;
+    }
 }
 
 // gaussian_log_prob (ppo.hpp:95-103) of the stored actions under the means.
@@ -638,29 +673,6 @@ __global__ __launch_bounds__(256) void sum_segments_kernel(SumSegs g) {
     for (uint32_t c = 0; c < g.slots[sg]; c++) s += src[uint64_t(c) * n + j];
     g.dst[sg][j] = s;
 }
-// Column sums over the minibatch rows of the 13 per-row terms (dm[4] -> b2,
-// dls[4] -> log_std, dv -> critic b2, loss[4] -> metrics): block b sums rows
-// b*RB .. into part[b][13]; column_finish_kernel adds the blocks in order.
-__global__ __launch_bounds__(256) void column_part_kernel(const float* __restrict__ dm, const float* __restrict__ dls,
-                                                          const float* __restrict__ dv, const float* __restrict__ loss,
-                                                          uint32_t B, float* __restrict__ part) {
-    __shared__ float s[13][RB + 1];
-    const uint32_t t = threadIdx.x, r0 = blockIdx.x * RB;
-    for (uint32_t e = t; e < 13 * RB; e += 256) {
-        const uint32_t col = e / RB, rr = e % RB, row = r0 + rr;
-        float v = 0.0f;
-        if (row < B) v = col < 4 ? dm[size_t(row) * 4 + col] : col < 8 ? dls[size_t(row) * 4 + col - 4]
-                         : col == 8 ? dv[row] : loss[size_t(row) * 4 + col - 9];
-        s[col][rr] = v;
-    }
-    __syncthreads();
-    if (t < 13) {
-        float a = 0.0f;
-        for (uint32_t rr = 0; rr < RB; rr++) a += s[t][rr];
-        part[size_t(blockIdx.x) * 13 + t] = a;
-    }
-}
-
 // Adds the column partials in block order and writes the per-row-column
 // gradients into the flat vectors (actor b2, log_std; critic b2) and the four
 // metric sums into metric_sums.
@@ -702,21 +714,27 @@ __global__ __launch_bounds__(256) void sqnorm_kernel(const float* __restrict__ g
     }
     if (t == 0) part[blockIdx.y * NP + s] = red[0];
 }
-// Clip scales min(1, 0.5 / ||g||) of both networks (partials added in slot
-// order), their pre-clip norms ||g|| = sqrt(|g|^2 + 1e-20) (ppo_grad_norm,
-// main.mm:963-975) and the update's metric row.
-__global__ void norm_finish_kernel(const float* __restrict__ part, const float* __restrict__ metric_sums, uint32_t b,
-                                   float* __restrict__ scale, float* __restrict__ metric_row, float* __restrict__ norm_row) {
-    const uint32_t t = threadIdx.x;
-    if (t < 2) {
-        float s = 0.0f;
-        for (uint32_t i = 0; i < NP; i++) s += part[t * NP + i];
+// Clip scales min(1, 0.5 / ||g||) of both networks, their pre-clip norms
+// ||g|| = sqrt(|g|^2 + 1e-20) (ppo_grad_norm, main.mm:963-975) and the
+// update's metric row.  One wavefront per network: each lane adds NP / 64
+// partials, then a butterfly over the lanes.
+__global__ __launch_bounds__(128) void norm_finish_kernel(const float* __restrict__ part,
+                                                          const float* __restrict__ metric_sums, uint32_t b,
+                                                          float* __restrict__ scale, float* __restrict__ metric_row,
+                                                          float* __restrict__ norm_row) {
+    static_assert(NP % 64 == 0, "whole partial rounds");
+    const uint32_t t = threadIdx.x, net = t / 64, l = t % 64;
+    float s = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < NP / 64; i++) s += part[net * NP + l + 64 * i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (l == 0) {
         const float norm = sqrt_f(s + 1.0e-20f);
-        scale[t] = min_f(1.0f, 0.5f / norm);
-        norm_row[t] = norm;
-    } else if (t < 6) {
-        metric_row[t - 2] = t == 5 ? metric_sums[3] / float(b) : metric_sums[t - 2];
+        scale[net] = min_f(1.0f, 0.5f / norm);
+        norm_row[net] = norm;
     }
+    if (net == 1 && l < 4) metric_row[l] = l == 3 ? metric_sums[3] / float(b) : metric_sums[l];
 }
 
 struct LargeAdamArgs {
@@ -844,17 +862,18 @@ hipError_t lp_launch_logp(const float* means, const float* actions, const float*
 
 hipError_t lp_launch_loss(const float* means, const float* values, const float* actions, const float* old_logp,
                           const float* adv, const float* ret, const float* log_std, uint32_t B, float clip,
-                          float vcoef, float ecoef, float* dm, float* dls, float* dv, float* loss, hipStream_t st) {
+                          float vcoef, float ecoef, float* dm, float* dls, float* dv, float* loss, float* col_part,
+                          hipStream_t st) {
     if (B == 0) return hipSuccess;
-    hipLaunchKernelGGL(lp::loss_kernel, dim3((B + 255) / 256), dim3(256), 0, st, means, values, actions, old_logp, adv,
-                       ret, log_std, B, clip, vcoef, ecoef, dm, dls, dv, loss);
+    hipLaunchKernelGGL(lp::loss_kernel, dim3((B + lp::RB - 1) / lp::RB), dim3(lp::RB), 0, st, means, values, actions,
+                       old_logp, adv, ret, log_std, B, clip, vcoef, ecoef, dm, dls, dv, loss, col_part);
     return hipGetLastError();
 }
 
 // Backward of both networks into the partial slots, then the slot sums into
-// the flat gradients ga (actor layout) and gc (critic layout) and the
-// per-row column partials.  Scratch: part >= lp_backward_part_floats(B, H, d)
-// floats, col_part >= ceil(B/64) * 13.
+// the flat gradients ga (actor layout) and gc (critic layout).  Scratch:
+// part >= lp_backward_part_floats(B, H, d) floats.  (The per-row column
+// partials, col_part >= ceil(B/64) * 13 floats, come from lp_launch_loss.)
 // Row chunks of the backward for B rows: the actor's (hidden tile, chunk)
 // workgroups fill one round at one per CU; the critic, whose blocks are light,
 // takes four times as many chunks and runs two workgroups per CU.
@@ -871,10 +890,9 @@ uint64_t lp_backward_part_floats(uint32_t B, uint32_t H, uint32_t d) {
 }
 
 hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16* xc, const __bf16* xcT,
-                              const __bf16* awb, const __bf16* cwb,
-                              const float* actor, const float* critic, const float* dm, const float* dls,
-                              const float* dv, const float* loss, uint32_t H, uint32_t d, uint32_t B,
-                              float* part, float* ga, float* gc, float* col_part, hipStream_t st) {
+                              const __bf16* awb, const __bf16* cwb, const float* actor, const float* critic,
+                              const float* dm, const float* dv, uint32_t H, uint32_t d, uint32_t B, float* part,
+                              float* ga, float* gc, hipStream_t st) {
     if (B == 0) return hipSuccess;
     if (d != MDN_ACTOR_OBS_POOLED && d != MDN_ACTOR_OBS_PRIOR) return hipErrorInvalidValue;
     const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
@@ -913,13 +931,11 @@ hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16*
         g.start[k + 1] = g.start[k] + ns[k];
     }
     hipLaunchKernelGGL(lp::sum_segments_kernel, dim3(uint32_t((g.start[6] + 255) / 256)), dim3(256), 0, st, g);
-    hipLaunchKernelGGL(lp::column_part_kernel, dim3((B + lp::RB - 1) / lp::RB), dim3(256), 0, st, dm, dls, dv, loss, B,
-                       col_part);
     return hipGetLastError();
 }
 
 // Clip + Adam of both networks.  scratch >= 2 * 512 + 2 + 4 floats;
-// col_part as written by lp_launch_backward.
+// col_part as written by lp_launch_loss.
 hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
                           __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
                           uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, float* norm_row,
@@ -932,7 +948,7 @@ hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, flo
     hipLaunchKernelGGL(lp::column_finish_kernel, dim3(13), dim3(64), 0, st, col_part, (B + lp::RB - 1) / lp::RB, H, d,
                        ga, gc, metric_sums);
     hipLaunchKernelGGL(lp::sqnorm_kernel, dim3(lp::NP, 2), dim3(256), 0, st, ga, gc, PA, PC, norm_part);
-    hipLaunchKernelGGL(lp::norm_finish_kernel, dim3(1), dim3(64), 0, st, norm_part, metric_sums, B, scale, metric_row,
+    hipLaunchKernelGGL(lp::norm_finish_kernel, dim3(1), dim3(128), 0, st, norm_part, metric_sums, B, scale, metric_row,
                        norm_row);
     lp::LargeAdamArgs a;
     a.actor = actor; a.critic = critic; a.am = am; a.av = av; a.cm = cm; a.cv = cv;
