@@ -1484,7 +1484,7 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     guard(dev_alloc(&p->ga, A));
     guard(dev_alloc(&p->gc, C));
     guard(dev_alloc(&p->col_part, ((M + 63) / 64) * 13));
-    guard(dev_alloc(&p->scratch, 2 * 512 + 2 + 4));
+    guard(dev_alloc(&p->scratch, lp_adam_scratch_floats()));
     guard(dev_alloc(&p->norm_part, ppo_normalize_part_words(R)));
     guard(dev_alloc(&p->norm_stats, 2));
     guard(dev_alloc(&p->metric_rows, size_t(p->updates) * 4));
@@ -1618,8 +1618,8 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
         });
         if (rc) return rc;
         rc = timed(s, MDN_K_LP_BACKWARD, [&] {
-            return lp_launch_backward(p->xa, p->xaT, p->xc, p->xcT, p->awb, p->cwb, p->actor, p->critic, p->dm, p->dv, H,
-                                      D, b, p->part, p->ga, p->gc, s->stream);
+            return lp_launch_backward(p->xa, p->xaT, p->xc, p->xcT, p->awb, p->cwb, p->actor, p->critic, p->dm, p->dv,
+                                      p->col_part, H, D, b, p->part, p->ga, p->gc, p->scratch, s->stream);
         });
         if (rc) return rc;
         ++p->optimizer_step;
@@ -1627,7 +1627,7 @@ int mdn_lppo_rollout_update(MdnLargePPO* p, uint32_t rollout_index) {
         mdn::adam_corrections(p->optimizer_step, 0.9f, 0.999f, &c1, &c2);
         rc = timed(s, MDN_K_LP_ADAM, [&] {
             return lp_launch_adam(p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->ga, p->gc,
-                                  p->scratch, p->col_part, b, H, D, s->cfg.learning_rate, c1, c2, p->metric_rows + u * 4,
+                                  p->scratch, b, H, D, s->cfg.learning_rate, c1, c2, p->metric_rows + u * 4,
                                   p->grad_norm_rows + u * 2, s->stream);
         });
         if (rc) return rc;

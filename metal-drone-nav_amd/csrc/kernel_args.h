@@ -237,13 +237,13 @@ hipError_t lp_launch_loss(const float* means, const float* values, const float* 
                           hipStream_t st);
 hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16* xc, const __bf16* xcT,
                               const __bf16* awb, const __bf16* cwb, const float* actor, const float* critic,
-                              const float* dm, const float* dv, uint32_t H, uint32_t d, uint32_t B, float* part,
-                              float* ga, float* gc, hipStream_t st);
+                              const float* dm, const float* dv, const float* col_part, uint32_t H, uint32_t d,
+                              uint32_t B, float* part, float* ga, float* gc, float* scratch, hipStream_t st);
 uint64_t lp_backward_part_floats(uint32_t B, uint32_t H, uint32_t d);
+uint64_t lp_adam_scratch_floats();
 hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
-                          __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
-                          uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, float* norm_row,
-                          hipStream_t st);
+                          __bf16* cwb, float* ga, float* gc, float* scratch, uint32_t B, uint32_t H, uint32_t d,
+                          float lr, float c1, float c2, float* metric_row, float* norm_row, hipStream_t st);
 uint32_t ppo_partial_stride(uint32_t d);
 // fixed_ppo operators over caller arrays (fixed_ppo.hip)
 hipError_t fppo_launch_forward(const float* w, const float* x, uint32_t D, uint32_t H, uint32_t O, uint32_t prior,

@@ -654,24 +654,52 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
 }
 
 // ---------------------------------------------------------------- reductions
-// Up to six gradient segments in one launch: dst[s][j] = the sum over the
-// segment's `slots` partial slots (slot-major, stride n_s) in slot order.
+constexpr uint32_t NP = 4096;  // most squared-norm partial slots (workgroups) per network
+
+// The six gradient segments (actor W1, b1, W2, then critic W1, b1, w2) in
+// one launch of at most NP workgroups striding over their elements: dst[s][j] = the
+// sum over the segment's `slots` partial slots (slot-major, stride n_s) in
+// slot order.  Each workgroup also leaves the sums of squares of what it
+// wrote, per network, in norm_part[net][blockIdx.x] (workgroup 0 adds the
+// column-sum parameters written before the launch: actor b2 and log_std,
+// critic b2), the partials of the clip norm.
 struct SumSegs {
     const float* src[6];
     float* dst[6];
     uint64_t start[7];  // element offsets of the segments in the launch; start[6] = total
     uint32_t slots[6];
+    const float* cols_a;  // actor b2, log_std (8 values)
+    const float* cols_c;  // critic b2
+    float* norm_part;     // [2][NP], the first gridDim.x slots of each
 };
 __global__ __launch_bounds__(256) void sum_segments_kernel(SumSegs g) {
-    const uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= g.start[6]) return;
-    uint32_t sg = 0;
-    while (sg < 5 && i >= g.start[sg + 1]) sg++;
-    const uint64_t j = i - g.start[sg], n = g.start[sg + 1] - g.start[sg];
-    const float* src = g.src[sg];
-    float s = 0.0f;
-    for (uint32_t c = 0; c < g.slots[sg]; c++) s += src[uint64_t(c) * n + j];
-    g.dst[sg][j] = s;
+    const uint32_t t = threadIdx.x;
+    float sq[2] = {0.0f, 0.0f};
+    for (uint64_t i = uint64_t(blockIdx.x) * 256 + t; i < g.start[6]; i += uint64_t(gridDim.x) * 256) {
+        uint32_t sg = 0;
+        while (sg < 5 && i >= g.start[sg + 1]) sg++;
+        const uint64_t j = i - g.start[sg], n = g.start[sg + 1] - g.start[sg];
+        const float* src = g.src[sg];
+        float s = 0.0f;
+        for (uint32_t c = 0; c < g.slots[sg]; c++) s += src[uint64_t(c) * n + j];
+        g.dst[sg][j] = s;
+        sq[sg < 3 ? 0 : 1] += s * s;
+    }
+    if (blockIdx.x == 0 && t == 0)
+        for (uint32_t k = 0; k < 8; k++) sq[0] += g.cols_a[k] * g.cols_a[k];
+    if (blockIdx.x == 0 && t == 1) sq[1] += g.cols_c[0] * g.cols_c[0];
+    __shared__ float red[2][256];
+    red[0][t] = sq[0];
+    red[1][t] = sq[1];
+    __syncthreads();
+    for (uint32_t w = 128; w > 0; w >>= 1) {
+        if (t < w) {
+            red[0][t] += red[0][t + w];
+            red[1][t] += red[1][t + w];
+        }
+        __syncthreads();
+    }
+    if (t < 2) g.norm_part[t * NP + blockIdx.x] = red[t][0];
 }
 // Adds the column partials in block order and writes the per-row-column
 // gradients into the flat vectors (actor b2, log_std; critic b2) and the four
@@ -692,41 +720,22 @@ __global__ __launch_bounds__(64) void column_finish_kernel(const float* __restri
     else metric_sums[t - 9] = s;
 }
 
-constexpr uint32_t NP = 512;  // squared-norm partial slots (workgroups) per network
-
-// Per-network squared-norm partials: workgroup s of net k sums g[i]^2 over
-// i = 256 s + t, + 256 NP, ... and reduces its 256 lanes by a tree
-// (both networks in one grid: blockIdx.y = net).
-__global__ __launch_bounds__(256) void sqnorm_kernel(const float* __restrict__ ga, const float* __restrict__ gc,
-                                                     uint32_t PA, uint32_t PC, float* __restrict__ part) {
-    __shared__ float red[256];
-    const uint32_t t = threadIdx.x, s = blockIdx.x;
-    const bool critic = blockIdx.y == 1;
-    const float* g = critic ? gc : ga;
-    const uint32_t P = critic ? PC : PA;
-    float a = 0.0f;
-    for (uint32_t i = 256 * s + t; i < P; i += 256 * NP) a += g[i] * g[i];
-    red[t] = a;
-    __syncthreads();
-    for (uint32_t w = 128; w > 0; w >>= 1) {
-        if (t < w) red[t] += red[t + w];
-        __syncthreads();
-    }
-    if (t == 0) part[blockIdx.y * NP + s] = red[0];
-}
 // Clip scales min(1, 0.5 / ||g||) of both networks, their pre-clip norms
 // ||g|| = sqrt(|g|^2 + 1e-20) (ppo_grad_norm, main.mm:963-975) and the
-// update's metric row.  One wavefront per network: each lane adds NP / 64
-// partials, then a butterfly over the lanes.
+// update's metric row.  One wavefront per network: each lane adds every
+// 64th of the `parts` partials (of the NP slots), then a butterfly over the
+// lanes.
 __global__ __launch_bounds__(128) void norm_finish_kernel(const float* __restrict__ part,
                                                           const float* __restrict__ metric_sums, uint32_t b,
-                                                          float* __restrict__ scale, float* __restrict__ metric_row,
-                                                          float* __restrict__ norm_row) {
-    static_assert(NP % 64 == 0, "whole partial rounds");
+                                                          uint32_t parts, float* __restrict__ scale,
+                                                          float* __restrict__ metric_row, float* __restrict__ norm_row) {
     const uint32_t t = threadIdx.x, net = t / 64, l = t % 64;
     float s = 0.0f;
 #pragma unroll
-    for (uint32_t i = 0; i < NP / 64; i++) s += part[net * NP + l + 64 * i];
+    for (uint32_t k = 0; k < NP / 64; k++) {  // every load in flight; slots past `parts` add 0
+        const float v = part[net * NP + l + 64 * k];
+        s += l + 64 * k < parts ? v : 0.0f;
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
     if (l == 0) {
@@ -870,13 +879,25 @@ hipError_t lp_launch_loss(const float* means, const float* values, const float* 
     return hipGetLastError();
 }
 
-// Backward of both networks into the partial slots, then the slot sums into
-// the flat gradients ga (actor layout) and gc (critic layout).  Scratch:
-// part >= lp_backward_part_floats(B, H, d) floats.  (The per-row column
-// partials, col_part >= ceil(B/64) * 13 floats, come from lp_launch_loss.)
+// The column sums of the per-row terms (col_part, as written by
+// lp_launch_loss) into ga / gc and the metric sums, the backward of both
+// networks into the partial slots, then the slot sums into the flat
+// gradients ga (actor layout) and gc (critic layout) with the clip norm's
+// partials.  part >= lp_backward_part_floats(B, H, d) floats; scratch >=
+// lp_adam_scratch_floats() (norm partials, clip scales, metric sums), read by
+// lp_launch_adam.
 // Row chunks of the backward for B rows: the actor's (hidden tile, chunk)
 // workgroups fill one round at one per CU; the critic, whose blocks are light,
 // takes four times as many chunks and runs two workgroups per CU.
+// workgroups of the segment sums (one element per thread up to NP of them),
+// the number of clip-norm partials per network
+static uint32_t lp_norm_parts(uint32_t H, uint32_t d) {
+    const uint64_t total = uint64_t(H) * (d + 1 + 4) + uint64_t(H) * (lp::COBS + 1 + 1);
+    return uint32_t(std::min<uint64_t>(lp::NP, (total + 255) / 256));
+}
+
+uint64_t lp_adam_scratch_floats() { return 2 * uint64_t(lp::NP) + 2 + 4; }
+
 void lp_backward_chunks(uint32_t B, uint32_t H, uint32_t* actor_chunks, uint32_t* critic_chunks) {
     const uint32_t tiles = H / lp::UT, blocks = (B + lp::RB - 1) / lp::RB;
     *actor_chunks = std::max(1u, std::min(blocks, 256 / tiles));
@@ -891,10 +912,13 @@ uint64_t lp_backward_part_floats(uint32_t B, uint32_t H, uint32_t d) {
 
 hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16* xc, const __bf16* xcT,
                               const __bf16* awb, const __bf16* cwb, const float* actor, const float* critic,
-                              const float* dm, const float* dv, uint32_t H, uint32_t d, uint32_t B, float* part,
-                              float* ga, float* gc, hipStream_t st) {
+                              const float* dm, const float* dv, const float* col_part, uint32_t H, uint32_t d,
+                              uint32_t B, float* part, float* ga, float* gc, float* scratch, hipStream_t st) {
     if (B == 0) return hipSuccess;
     if (d != MDN_ACTOR_OBS_POOLED && d != MDN_ACTOR_OBS_PRIOR) return hipErrorInvalidValue;
+    float* metric_sums = scratch + 2 * lp::NP + 2;
+    hipLaunchKernelGGL(lp::column_finish_kernel, dim3(13), dim3(64), 0, st, col_part, (B + lp::RB - 1) / lp::RB, H, d,
+                       ga, gc, metric_sums);
     const uint32_t BP = (B + lp::RB - 1) / lp::RB * lp::RB;
     uint32_t ca, cc;
     lp_backward_chunks(B, H, &ca, &cc);
@@ -930,26 +954,25 @@ hipError_t lp_launch_backward(const __bf16* xa, const __bf16* xaT, const __bf16*
         g.slots[k] = slots[k];
         g.start[k + 1] = g.start[k] + ns[k];
     }
-    hipLaunchKernelGGL(lp::sum_segments_kernel, dim3(uint32_t((g.start[6] + 255) / 256)), dim3(256), 0, st, g);
+    g.cols_a = ga + A_W2 + 4 * H;
+    g.cols_c = gc + C_W2 + H;
+    g.norm_part = scratch;
+    hipLaunchKernelGGL(lp::sum_segments_kernel, dim3(lp_norm_parts(H, d)), dim3(256), 0, st, g);
     return hipGetLastError();
 }
 
-// Clip + Adam of both networks.  scratch >= 2 * 512 + 2 + 4 floats;
-// col_part as written by lp_launch_loss.
+// Clip + Adam of both networks from the gradients, norm partials and metric
+// sums lp_launch_backward left in ga, gc and scratch.
 hipError_t lp_launch_adam(float* actor, float* critic, float* am, float* av, float* cm, float* cv, __bf16* awb,
-                          __bf16* cwb, float* ga, float* gc, float* scratch, const float* col_part, uint32_t B,
-                          uint32_t H, uint32_t d, float lr, float c1, float c2, float* metric_row, float* norm_row,
-                          hipStream_t st) {
+                          __bf16* cwb, float* ga, float* gc, float* scratch, uint32_t B, uint32_t H, uint32_t d,
+                          float lr, float c1, float c2, float* metric_row, float* norm_row, hipStream_t st) {
     if (d != MDN_ACTOR_OBS_POOLED && d != MDN_ACTOR_OBS_PRIOR) return hipErrorInvalidValue;
     const uint32_t PA = H * d + H + 4 * H + 8, PC = H * lp::COBS + 2 * H + 1;
     float* norm_part = scratch;
     float* scale = scratch + 2 * lp::NP;
     float* metric_sums = scale + 2;
-    hipLaunchKernelGGL(lp::column_finish_kernel, dim3(13), dim3(64), 0, st, col_part, (B + lp::RB - 1) / lp::RB, H, d,
-                       ga, gc, metric_sums);
-    hipLaunchKernelGGL(lp::sqnorm_kernel, dim3(lp::NP, 2), dim3(256), 0, st, ga, gc, PA, PC, norm_part);
-    hipLaunchKernelGGL(lp::norm_finish_kernel, dim3(1), dim3(128), 0, st, norm_part, metric_sums, B, scale, metric_row,
-                       norm_row);
+    hipLaunchKernelGGL(lp::norm_finish_kernel, dim3(1), dim3(128), 0, st, norm_part, metric_sums, B,
+                       lp_norm_parts(H, d), scale, metric_row, norm_row);
     lp::LargeAdamArgs a;
     a.actor = actor; a.critic = critic; a.am = am; a.av = av; a.cm = cm; a.cv = cv;
     a.actor_wb = awb; a.critic_wb = cwb; a.ga = ga; a.gc = gc; a.scale = scale;
