@@ -202,9 +202,11 @@ def large_workload(args, hidden=5120, envs=8192, horizon=256, epochs=4, minibatc
     rows = N * T
     PA = D * hidden + hidden + 4 * hidden + 8
     P = PA + (32 * hidden + 2 * hidden + 1)
-    # algorithmic FLOP: rollout 2P per row (actor at s, critic at s and s'); update per row per epoch:
-    # forward 2P, first/second-layer weight gradients 2P (the backward's recomputed forward is not counted)
-    flop_eval = 2.0 * rows * (P + (32 * hidden + 2 * hidden + 1))
+    # algorithmic FLOP: rollout 2P per row (actor and critic at s; the critic at s' is the next row's value
+    # at s wherever the inputs are equal, and the few rows evaluated on their own, the last tick and resets,
+    # are not counted); update per row per epoch: forward 2P, first/second-layer weight gradients 2P (the
+    # backward's recomputed forward is not counted)
+    flop_eval = 2.0 * rows * P
     flop_fwd = 2.0 * rows * epochs * P
     flop_bwd = 2.0 * rows * epochs * P
     t_fwd = kernels["lp_forward"]["total_ms"] * 1e-3 / steps

@@ -1378,6 +1378,11 @@ struct MdnLargePPO {
     float* norm_stats = nullptr;
     float *metric_rows = nullptr, *metric_mean = nullptr;
     float* grad_norm_rows = nullptr;  // [updates][2] pre-clip norms of the last rollout_update
+    // values at s': the rows evaluated on their own (count, row indices,
+    // their critic inputs, their values)
+    uint32_t* nv_count = nullptr;
+    uint32_t* nv_idx = nullptr;
+    float *nv_gather = nullptr, *nv_vals = nullptr;
 };
 
 namespace {
@@ -1413,6 +1418,27 @@ hipError_t lp_forward_rows(MdnLargePPO* p, const float* obs, const float* co, ui
     return e;
 }
 
+// Values at s and s' of the first `ticks` ticks' rows: the critic over the
+// critic observations, then only the rows whose next-state observation is
+// not the next tick's observation (the last tick, resets) over theirs; the
+// others take the next tick's value (next_value_split_kernel).
+hipError_t lp_values(MdnLargePPO* p, uint32_t ticks) {
+    MdnSim* s = p->sim;
+    const uint32_t N = s->cfg.n, rows = ticks * N;
+    hipError_t e = lp_forward_rows(p, nullptr, s->co, rows, nullptr, s->values);
+    if (e == hipSuccess) e = hipMemsetAsync(p->nv_count, 0, sizeof(uint32_t), s->stream);
+    if (e == hipSuccess)
+        e = lp_launch_next_value_split(s->co, s->nco, s->values, ticks, N, s->next_values, p->nv_count, p->nv_idx,
+                                       p->nv_gather, s->stream);
+    uint32_t n = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&n, p->nv_count, sizeof(n), hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    if (e == hipSuccess && n > rows) e = hipErrorInvalidValue;
+    if (e == hipSuccess) e = lp_forward_rows(p, nullptr, p->nv_gather, n, nullptr, p->nv_vals);
+    if (e == hipSuccess) e = lp_launch_next_value_scatter(p->nv_idx, p->nv_vals, n, s->next_values, s->stream);
+    return e;
+}
+
 float* lp_param(MdnLargePPO* p, uint32_t which, uint64_t* count) {
     const uint64_t A = p->shape.actor_count(), C = p->shape.critic_count();
     switch (which) {
@@ -1435,7 +1461,8 @@ void mdn_lppo_destroy(MdnLargePPO* p) {
     void* bufs[] = {p->actor, p->critic, p->am, p->av, p->cm, p->cv, p->awb, p->cwb, p->xa, p->xaT, p->xc, p->xcT,
                     p->eval_means, p->fwd_part, p->means,
                     p->values, p->dm, p->dls, p->dv, p->loss, p->part, p->ga, p->gc, p->col_part, p->scratch,
-                    p->norm_part, p->norm_stats, p->metric_rows, p->metric_mean, p->grad_norm_rows};
+                    p->norm_part, p->norm_stats, p->metric_rows, p->metric_mean, p->grad_norm_rows,
+                    p->nv_count, p->nv_idx, p->nv_gather, p->nv_vals};
     for (void* b : bufs)
         if (b) hipFree(b);
     delete p;
@@ -1473,6 +1500,10 @@ int mdn_lppo_create(MdnSim* s, uint32_t hidden, uint32_t epochs, uint32_t miniba
     guard(dev_alloc(&p->xc, MP * 32));
     guard(dev_alloc(&p->xcT, MP * 32));
     guard(dev_alloc(&p->eval_means, R * 4));
+    guard(dev_alloc(&p->nv_count, 1));
+    guard(dev_alloc(&p->nv_idx, R));
+    guard(dev_alloc(&p->nv_gather, R * COBS));
+    guard(dev_alloc(&p->nv_vals, R));
     guard(dev_alloc(&p->fwd_part, size_t(lp_forward_part_floats(p->minibatch))));
     guard(dev_alloc(&p->means, M * 4));
     guard(dev_alloc(&p->values, M));
@@ -1514,8 +1545,8 @@ int mdn_lppo_evaluate(MdnLargePPO* p) {
     if (rc) return rc;
     const uint32_t R = uint32_t(s->rows());
     return timed(s, MDN_K_LP_FORWARD, [&] {
-        hipError_t e = lp_forward_rows(p, s->obs, s->co, R, p->eval_means, s->values);
-        if (e == hipSuccess) e = lp_forward_rows(p, nullptr, s->nco, R, nullptr, s->next_values);
+        hipError_t e = lp_forward_rows(p, s->obs, nullptr, R, p->eval_means, nullptr);
+        if (e == hipSuccess) e = lp_values(p, s->horizon);
         if (e == hipSuccess)
             e = lp_launch_logp(p->eval_means, s->actions, p->actor + p->shape.actor_log_std(), R, s->logp, s->stream);
         return e;
@@ -1563,13 +1594,10 @@ int mdn_lppo_collect(MdnLargePPO* p, uint32_t count) {
         rc = timed(s, MDN_K_ROLLOUT, [&] { return nav_launch_rollout(&a, 8, slots, s->shape.obs, s->stream); });
     }
     if (rc) return rc;
-    // values at s and s' (sim.metal:254, 322) under the wide critic
-    const uint32_t rows = uint32_t(size_t(std::min(count, s->horizon)) * N);
-    return timed(s, MDN_K_LP_FORWARD, [&] {
-        hipError_t e = lp_forward_rows(p, nullptr, s->co, rows, nullptr, s->values);
-        if (e == hipSuccess) e = lp_forward_rows(p, nullptr, s->nco, rows, nullptr, s->next_values);
-        return e;
-    });
+    // values at s and s' (sim.metal:254, 322) under the wide critic (a row
+    // reuses the next row's value only where their inputs are equal bit for
+    // bit, so a collect that wrapped the horizon is handled too)
+    return timed(s, MDN_K_LP_FORWARD, [&] { return lp_values(p, std::min(count, s->horizon)); });
 }
 
 int mdn_lppo_means(MdnLargePPO* p, float* host, uint64_t count) {

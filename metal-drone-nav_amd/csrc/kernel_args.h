@@ -229,6 +229,11 @@ hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* a
                              const float* actor, const float* critic, uint32_t H, uint32_t d, uint32_t B,
                              const float* prior, float* means, float* values, float* part, hipStream_t st);
 uint64_t lp_forward_part_floats(uint32_t B);
+hipError_t lp_launch_next_value_split(const float* co, const float* nco, const float* values, uint32_t ticks,
+                                      uint32_t N, float* next_values, uint32_t* count, uint32_t* idx, float* gather,
+                                      hipStream_t st);
+hipError_t lp_launch_next_value_scatter(const uint32_t* idx, const float* vals, uint32_t n, float* next_values,
+                                        hipStream_t st);
 hipError_t lp_launch_logp(const float* means, const float* actions, const float* log_std, uint32_t B, float* logp,
                           hipStream_t st);
 hipError_t lp_launch_loss(const float* means, const float* values, const float* actions, const float* old_logp,

@@ -653,6 +653,51 @@ __global__ __launch_bounds__(64 * WV, WV == 4 && NQ == 1 ? 2 : 1) void backward_
     }
 }
 
+// ---------------------------------------------------------------- values at s'
+// Rows [tick][N]: a row whose next-state critic observation equals the next
+// tick's critic observation of the same env bit for bit takes that row's
+// value (the same input through the same network gives the same value); the
+// others (the last tick, resets) are gathered, in any order, for their own
+// evaluation: idx[i] the row, gather[i] its 32 inputs, *count of them.
+__global__ __launch_bounds__(256) void next_value_split_kernel(const float* __restrict__ co,
+                                                               const float* __restrict__ nco,
+                                                               const float* __restrict__ values, uint32_t ticks,
+                                                               uint32_t N, float* __restrict__ next_values,
+                                                               uint32_t* __restrict__ count, uint32_t* __restrict__ idx,
+                                                               float* __restrict__ gather) {
+    static_assert(COBS == 32, "eight 16-byte pieces per row");
+    const uint64_t r = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (r >= uint64_t(ticks) * N) return;
+    const uint4* a = reinterpret_cast<const uint4*>(nco + r * COBS);
+    uint4 v[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8; k++) v[k] = a[k];
+    bool same = r / N + 1 < ticks;
+    if (same) {
+        const uint4* b = reinterpret_cast<const uint4*>(co + (r + N) * COBS);
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) {
+            const uint4 w = b[k];
+            same = same && v[k].x == w.x && v[k].y == w.y && v[k].z == w.z && v[k].w == w.w;
+        }
+    }
+    if (same) {
+        next_values[r] = values[r + N];
+    } else {
+        const uint32_t i = atomicAdd(count, 1u);
+        idx[i] = uint32_t(r);
+        uint4* g = reinterpret_cast<uint4*>(gather + size_t(i) * COBS);
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) g[k] = v[k];
+    }
+}
+__global__ __launch_bounds__(256) void next_value_scatter_kernel(const uint32_t* __restrict__ idx,
+                                                                 const float* __restrict__ vals, uint32_t n,
+                                                                 float* __restrict__ next_values) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) next_values[idx[i]] = vals[i];
+}
+
 // ---------------------------------------------------------------- reductions
 constexpr uint32_t NP = 4096;  // most squared-norm partial slots (workgroups) per network
 
@@ -859,6 +904,27 @@ hipError_t lp_launch_forward(const __bf16* xa, const __bf16* xc, const __bf16* a
             hipLaunchKernelGGL(lp::part_sum_kernel, dim3((B + 255) / 256), dim3(256), 0, st, part, S, BP, B, 1u,
                                critic + C_B2, values, nullptr, 0u);
     }
+    return hipGetLastError();
+}
+
+hipError_t lp_launch_next_value_split(const float* co, const float* nco, const float* values, uint32_t ticks,
+                                      uint32_t N, float* next_values, uint32_t* count, uint32_t* idx, float* gather,
+                                      hipStream_t st) {
+    const uint64_t rows = uint64_t(ticks) * N;
+    if (rows == 0) return hipSuccess;
+    if (rows > 0xffffffffull || (reinterpret_cast<uintptr_t>(co) | reinterpret_cast<uintptr_t>(nco) |
+                                 reinterpret_cast<uintptr_t>(gather)) % 16)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(lp::next_value_split_kernel, dim3(uint32_t((rows + 255) / 256)), dim3(256), 0, st, co, nco,
+                       values, ticks, N, next_values, count, idx, gather);
+    return hipGetLastError();
+}
+
+hipError_t lp_launch_next_value_scatter(const uint32_t* idx, const float* vals, uint32_t n, float* next_values,
+                                        hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(lp::next_value_scatter_kernel, dim3((n + 255) / 256), dim3(256), 0, st, idx, vals, n,
+                       next_values);
     return hipGetLastError();
 }
 
