@@ -665,31 +665,33 @@ __global__ __launch_bounds__(256) void next_value_split_kernel(const float* __re
                                                                uint32_t N, float* __restrict__ next_values,
                                                                uint32_t* __restrict__ count, uint32_t* __restrict__ idx,
                                                                float* __restrict__ gather) {
+    // eight lanes per row, one 16-byte piece each (each load instruction
+    // covers eight whole rows)
     static_assert(COBS == 32, "eight 16-byte pieces per row");
-    const uint64_t r = uint64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (r >= uint64_t(ticks) * N) return;
-    const uint4* a = reinterpret_cast<const uint4*>(nco + r * COBS);
-    uint4 v[8];
-#pragma unroll
-    for (uint32_t k = 0; k < 8; k++) v[k] = a[k];
-    bool same = r / N + 1 < ticks;
+    const uint64_t e = uint64_t(blockIdx.x) * 256 + threadIdx.x, r = e / 8;
+    const uint32_t k = threadIdx.x % 8, lane = threadIdx.x % 64;
+    const bool live = r < uint64_t(ticks) * N;
+    const uint64_t rr = live ? r : 0;
+    const uint4 v = reinterpret_cast<const uint4*>(nco)[rr * 8 + k];
+    bool same = live && rr / N + 1 < ticks;
     if (same) {
-        const uint4* b = reinterpret_cast<const uint4*>(co + (r + N) * COBS);
-#pragma unroll
-        for (uint32_t k = 0; k < 8; k++) {
-            const uint4 w = b[k];
-            same = same && v[k].x == w.x && v[k].y == w.y && v[k].z == w.z && v[k].w == w.w;
-        }
+        const uint4 w = reinterpret_cast<const uint4*>(co)[(rr + N) * 8 + k];
+        same = v.x == w.x && v.y == w.y && v.z == w.z && v.w == w.w;
     }
-    if (same) {
-        next_values[r] = values[r + N];
-    } else {
-        const uint32_t i = atomicAdd(count, 1u);
+    const uint64_t differ = __ballot(live && !same);
+    const bool row_same = ((differ >> (lane & ~7u)) & 0xffull) == 0;
+    if (!live) return;
+    if (row_same) {
+        if (k == 0) next_values[r] = values[r + N];
+        return;
+    }
+    uint32_t i = 0;
+    if (k == 0) {
+        i = atomicAdd(count, 1u);
         idx[i] = uint32_t(r);
-        uint4* g = reinterpret_cast<uint4*>(gather + size_t(i) * COBS);
-#pragma unroll
-        for (uint32_t k = 0; k < 8; k++) g[k] = v[k];
     }
+    i = __shfl(i, lane & ~7u, 64);
+    reinterpret_cast<uint4*>(gather)[size_t(i) * 8 + k] = v;
 }
 __global__ __launch_bounds__(256) void next_value_scatter_kernel(const uint32_t* __restrict__ idx,
                                                                  const float* __restrict__ vals, uint32_t n,
@@ -915,8 +917,8 @@ hipError_t lp_launch_next_value_split(const float* co, const float* nco, const f
     if (rows > 0xffffffffull || (reinterpret_cast<uintptr_t>(co) | reinterpret_cast<uintptr_t>(nco) |
                                  reinterpret_cast<uintptr_t>(gather)) % 16)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(lp::next_value_split_kernel, dim3(uint32_t((rows + 255) / 256)), dim3(256), 0, st, co, nco,
-                       values, ticks, N, next_values, count, idx, gather);
+    hipLaunchKernelGGL(lp::next_value_split_kernel, dim3(uint32_t((rows * 8 + 255) / 256)), dim3(256), 0, st, co,
+                       nco, values, ticks, N, next_values, count, idx, gather);
     return hipGetLastError();
 }
 
