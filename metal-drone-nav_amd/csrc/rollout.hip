@@ -828,7 +828,13 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     __shared__ PhysRecip s_erp[DYN ? E : 1];
     if constexpr (DYN) {
         const float* src = reinterpret_cast<const float*>(a.env_phys + nn);
-        for (uint32_t i = lane; i < PW; i += G) s_ep[grp][i] = src[i];
+        constexpr uint32_t PR = (PW + G - 1) / G;
+        float pv[PR];
+#pragma unroll
+        for (uint32_t j = 0; j < PR; j++) pv[j] = src[lane + G * j < PW ? lane + G * j : 0];
+#pragma unroll
+        for (uint32_t j = 0; j < PR; j++)
+            if (lane + G * j < PW) s_ep[grp][lane + G * j] = pv[j];
         if (lane == 0) s_erp[grp] = phys_recip(a.env_phys[nn]);
     }
     group_sync();
@@ -1267,8 +1273,19 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
                 for (int j = 0; j < 32; j++) { s_co[grp][j] = cob[j]; cg[j] = cob[j]; }
             }
         } else if (SPLIT && active) {  // begins at act: this tick's rows as written before
-            for (uint32_t i = lane; i < D; i += G) s_obs[grp][i] = og[i];
-            for (uint32_t i = lane; i < COBS; i += G) s_co[grp][i] = a.co[row * COBS + i];
+            // (fixed trip counts, every load issued before the first store)
+            constexpr uint32_t OR = (D + G - 1) / G, CR = (COBS + G - 1) / G;
+            float ov[OR], cv[CR];
+#pragma unroll
+            for (uint32_t j = 0; j < OR; j++) ov[j] = og[lane + G * j < D ? lane + G * j : 0];
+#pragma unroll
+            for (uint32_t j = 0; j < CR; j++) cv[j] = a.co[row * COBS + (lane + G * j < COBS ? lane + G * j : 0)];
+#pragma unroll
+            for (uint32_t j = 0; j < OR; j++)
+                if (lane + G * j < D) s_obs[grp][lane + G * j] = ov[j];
+#pragma unroll
+            for (uint32_t j = 0; j < CR; j++)
+                if (lane + G * j < COBS) s_co[grp][lane + G * j] = cv[j];
         } else if (D == MDN_ACTOR_OBS_PRIOR && live && observe && a.mem_head && lane == 0) {
             a.mem_head[size_t(nn) * MEM_HEAD_WORDS + MEM_HEAD_OBSERVED] = 0u;
         }
