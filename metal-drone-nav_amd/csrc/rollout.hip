@@ -653,6 +653,25 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     // memory; the fused 181-input kernels keep the plain tick loop
     constexpr bool SPLIT = X || D == MDN_ACTOR_OBS_PRIOR || DYN;
     constexpr uint32_t WSTR = WORLD_WORDS;  // odd: env rows start in distinct banks
+    // the env's state, counters, world and command rows are requested first,
+    // so that their latency overlaps the shared weights' staging (a
+    // split-tick launch pays this prologue once per tick)
+    State s;
+    Run r;
+    load_state(a.state, N, nn, s);
+    load_run(a.run, N, nn, r);
+    constexpr uint32_t WR = (WORLD_WORDS + G - 1) / G, CMR = (32 + G - 1) / G;
+    float wv[WR], cv[CMR];
+#pragma unroll
+    for (uint32_t j = 0; j < WR; j++) {
+        const uint32_t i = lane + G * j;
+        wv[j] = a.world[size_t(nn) * WORLD_WORDS + (i < WORLD_WORDS ? i : 0)];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < CMR; j++) {
+        const uint32_t i = lane + G * j;
+        cv[j] = a.commands[size_t(nn) * 32 + (i < 32 ? i : 0)];
+    }
     __shared__ WeightLds<W, D> s_wt;
     const float* AW1;   // actor W1 transposed [input][hidden]
     const float* RW;    // RAPTOR weights (RaptorWeights layout)
@@ -722,34 +741,12 @@ __global__ __launch_bounds__(64 * W) void rollout_kernel(RolloutArgs a) {
     __shared__ float s_rh[W > 1 ? E : 1][17];
 
     float* world = s_world[grp];
-    State s;
-    Run r;
-    load_state(a.state, N, nn, s);
-    load_run(a.run, N, nn, r);
-    // the env's rows: fixed trip counts, every load issued before the first
-    // store (a split-tick launch pays this once per tick)
-    {
-        constexpr uint32_t WR = (WORLD_WORDS + G - 1) / G;
-        float wv[WR];
 #pragma unroll
-        for (uint32_t j = 0; j < WR; j++) {
-            const uint32_t i = lane + G * j;
-            wv[j] = a.world[size_t(nn) * WORLD_WORDS + (i < WORLD_WORDS ? i : 0)];
-        }
-        constexpr uint32_t CR = (32 + G - 1) / G;
-        float cv[CR];
+    for (uint32_t j = 0; j < WR; j++)
+        if (lane + G * j < WORLD_WORDS) world[lane + G * j] = wv[j];
 #pragma unroll
-        for (uint32_t j = 0; j < CR; j++) {
-            const uint32_t i = lane + G * j;
-            cv[j] = a.commands[size_t(nn) * 32 + (i < 32 ? i : 0)];
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < WR; j++)
-            if (lane + G * j < WORLD_WORDS) world[lane + G * j] = wv[j];
-#pragma unroll
-        for (uint32_t j = 0; j < CR; j++)
-            if (lane + G * j < 32) s_cmd[grp][lane + G * j] = cv[j];
-    }
+    for (uint32_t j = 0; j < CMR; j++)
+        if (lane + G * j < 32) s_cmd[grp][lane + G * j] = cv[j];
     {   // pooled ring cache: LDS slot f%K holds frame f for the last K frames
         // (a launch that begins at act already holds the frame cast for the
         // current step, if one was due); the 2x2 minima of the group's
