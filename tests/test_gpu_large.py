@@ -206,4 +206,14 @@ def test_wide_policy_closed_loop(variant):
         assert not bad, (rollout, bad)
         assert merr <= MEAN_TOL, merr
         assert verr["values"] <= VALUE_TOL and verr["next_values"] <= VALUE_TOL, verr
+        # a value at s' whose critic input is the next tick's input is that
+        # tick's value at s, bit for bit (the reuse; the last tick's rows and
+        # resets are evaluated on their own)
+        co = np.ascontiguousarray(sim.get("critic_obs"), np.float32).reshape(T, -1, 32).view(np.uint32)
+        nco = np.ascontiguousarray(sim.get("next_critic_obs"), np.float32).reshape(T, -1, 32).view(np.uint32)
+        v = np.ascontiguousarray(sim.get("values"), np.float32).reshape(T, -1)
+        nv = np.ascontiguousarray(sim.get("next_values"), np.float32).reshape(T, -1)
+        same = np.all(nco[:-1] == co[1:], axis=2)
+        assert same.any()
+        assert np.array_equal(nv[:-1][same].view(np.uint32), v[1:][same].view(np.uint32))
     assert ora.get("runs")["episodes"].sum() > 0
