@@ -700,24 +700,32 @@ __device__ __forceinline__ float row_advantage(const RowArgs& a, uint32_t m) {
     const float adv = a.adv[m];
     return a.norm ? (adv - a.norm[0]) * a.norm[1] : adv;
 }
+// exp_f(-ls[j]) for j < 4, exp_f(-2 ls[j - 4]) for j = 4..7: the per-action
+// scale factors of row_objective, the same for every row, formed once per
+// workgroup
+__device__ __forceinline__ float row_scale_exp(const float* ls, uint32_t j) {
+    return j < 4 ? exp_f(-ls[j]) : exp_f(-2.0f * ls[j - 4]);
+}
 // Per-row objective (ppo.hpp:144-181): log-probability of the stored
 // action, clipped surrogate with its active branch, value loss, and the
-// derivatives of the minibatch-mean objective (scale = 1/b).  Writes scalar
-// i at rs[RSTRIDE i]: 0..3 d mean, 4..7 d log_std, 8..11 the row's policy,
-// value and entropy terms and its ratio.
+// derivatives of the minibatch-mean objective (scale = 1/b).  ex holds
+// row_scale_exp of j = 0..7; act and old_logp are the row's stored action
+// and log-probability.  Writes scalar i at rs[RSTRIDE i]: 0..3 d mean,
+// 4..7 d log_std, 8..11 the row's policy, value and entropy terms and its
+// ratio.
 template <uint32_t RSTRIDE = 1>
-__device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls, uint32_t m, float adv,
+__device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls, const float* ex,
+                                              const float (&act)[4], float old_logp, float adv,
                                               const float (&mean)[4], float value, float target, float scale,
                                               float (&dmean)[4], float* rs) {
-    const float* act = a.actions + size_t(m) * 4;
     float logp = 0.0f;
 #pragma unroll
     for (uint32_t q = 0; q < 4; q++) {
-        const float inv_std = exp_f(-ls[q]);
+        const float inv_std = ex[q];  // exp_f(-ls[q])
         const float d = (act[q] - mean[q]) * inv_std;
         logp += -0.5f * (d * d + 2.0f * ls[q] + LOG_TWO_PI);
     }
-    const float raw = logp - a.old_logp[m];
+    const float raw = logp - old_logp;
     const float lr = clamp_f(raw, -20.0f, 20.0f);
     const float ratio = exp_f(lr);
     const float clipped = clamp_f(ratio, 1.0f - a.clip, 1.0f + a.clip);
@@ -727,7 +735,7 @@ __device__ __forceinline__ void row_objective(const RowArgs& a, const float* ls,
     float entropy = 0.0f;
 #pragma unroll
     for (uint32_t q = 0; q < 4; q++) {
-        const float inv_var = exp_f(-2.0f * ls[q]);
+        const float inv_var = ex[4 + q];  // exp_f(-2.0f * ls[q])
         const float diff = act[q] - mean[q];
         float dl;
         if (active) {
@@ -759,10 +767,12 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     // the critic's w2 and the actor's W2 [4][64], read by every row's chains:
     // one LDS copy (broadcast reads) instead of per-step global loads
     __shared__ __attribute__((aligned(16))) float s_w2[5 * HID];
+    __shared__ float s_ex[8];  // exp(-log_std), exp(-2 log_std): the same for every row
     const uint32_t t = threadIdx.x, wv = t / 64;
     const bool rowt = t < 256;  // the row-wise phases' threads
     if (t < HID) s_w2[t] = a.critic[C_W2 + t];
     else if (t < 5 * HID) s_w2[t] = a.actor[L::W2 + t - HID];
+    else if (t < 5 * HID + 8) s_ex[t - 5 * HID] = row_scale_exp(a.actor + L::LS, t - 5 * HID);
     stage_w1<COBS, COBS>(a.critic_w1t, s_u);
     stage_w1<D, OBS_PAD>(a.actor_w1t, s_aw);
     const uint32_t n0 = blockIdx.x * 256;
@@ -853,7 +863,10 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
 #pragma unroll
             for (uint32_t q = 0; q < 3; q++) mean[q] += a.obs[size_t(m) * D + D - 3 + q];
         float dmean[4];
-        row_objective<256>(a, a.actor + L::LS, m, adv, mean, value, target, scale, dmean, rs_t + t);
+        const float* ap = a.actions + size_t(m) * 4;
+        const float act[4] = {ap[0], ap[1], ap[2], ap[3]};
+        row_objective<256>(a, a.actor + L::LS, s_ex, act, a.old_logp[m], adv, mean, value, target, scale, dmean,
+                           rs_t + t);
         if (a.norm && live) a.adv_out[m] = adv;
     }
     __syncthreads();
@@ -950,12 +963,15 @@ __global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
     __shared__ float s_hc[MB_FWD_ROWS][HID + 1];
     __shared__ float s_mv[MB_FWD_ROWS][5];   // means, value
     __shared__ float s_rs[MB_FWD_ROWS][16];  // d mean, d log_std, metric terms, d value
+    __shared__ float s_ex[8];                 // row_scale_exp
     const uint32_t t = threadIdx.x, wv = t / 64, l = t % 64;
     const uint32_t n0 = blockIdx.x * MB_FWD_ROWS;
     const uint32_t live_rows = a.b - n0 < MB_FWD_ROWS ? a.b - n0 : MB_FWD_ROWS;
     constexpr uint32_t AT = 5 * HID + 8;  // actor tail words from b1 on
     float* s_at = s_t;
     float* s_ct = s_t + AT;
+    float ract[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float rolp = 0.0f, radv = 0.0f, rret = 0.0f;
     {   // every load of the staging issued before any store
         constexpr uint32_t NW = (D * HID + 511) / 512, NCW = COBS * HID / 512, NX = (MB_FWD_ROWS * D + 511) / 512;
         float w[NW], cw[NCW], xv[NX], cv, tv[2];
@@ -977,6 +993,14 @@ __global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
         }
         tv[0] = t < AT ? a.actor[L::B1 + t] : 0.0f;
         tv[1] = t < 2 * HID + 1 ? a.critic[C_B1 + t] : 0.0f;
+        if (t < live_rows) {  // the row's objective inputs, used after the layers
+            const uint32_t mrow = n0 + t;
+#pragma unroll
+            for (uint32_t q = 0; q < 4; q++) ract[q] = a.actions[size_t(mrow) * 4 + q];
+            rolp = a.old_logp[mrow];
+            radv = row_advantage(a, mrow);
+            rret = a.ret[mrow];
+        }
 #pragma unroll
         for (uint32_t k = 0; k < NW; k++) {
             const uint32_t e = t + 512 * k;
@@ -1040,6 +1064,8 @@ __global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
         float v = s_ct[2 * HID];
         for (uint32_t k = 0; k < HID; k++) v = fma_f(cw2[k], s_hc[r][k], v);
         s_mv[r][4] = v;
+    } else if (t < 5 * MB_FWD_ROWS + 8) {
+        s_ex[t - 5 * MB_FWD_ROWS] = row_scale_exp(s_at + 5 * HID + 4, t - 5 * MB_FWD_ROWS);
     }
     __syncthreads();
     const float scale = 1.0f / max_f(float(a.b), 1.0f);
@@ -1048,11 +1074,11 @@ __global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
         if (t < live_rows) {
             const uint32_t mrow = n0 + t;
             const float mean[4] = {s_mv[t][0], s_mv[t][1], s_mv[t][2], s_mv[t][3]};
-            const float value = s_mv[t][4], target = a.ret[mrow];
+            const float value = s_mv[t][4], target = rret;
             float dmean[4];
-            const float adv = row_advantage(a, mrow);
+            const float adv = radv;
             if (a.norm) a.adv_out[mrow] = adv;
-            row_objective(a, s_at + 5 * HID + 4, mrow, adv, mean, value, target, scale, dmean, rs);
+            row_objective(a, s_at + 5 * HID + 4, s_ex, ract, rolp, adv, mean, value, target, scale, dmean, rs);
             rs[12] = a.vcoef * (value - target) * scale;
         } else {
             for (uint32_t c = 0; c < 13; c++) rs[c] = 0.0f;
