@@ -695,10 +695,13 @@ __device__ __forceinline__ void chunk_weight_grad(RowSlab<W>& f, const float* __
     }
 }
 
-// Row m's advantage, normalised on the fly when a.norm is set (ppo.hpp:139).
-__device__ __forceinline__ float row_advantage(const RowArgs& a, uint32_t m) {
-    const float adv = a.adv[m];
+// A stored advantage, normalised on the fly when a.norm is set (ppo.hpp:139).
+__device__ __forceinline__ float normalized_advantage(const RowArgs& a, float adv) {
     return a.norm ? (adv - a.norm[0]) * a.norm[1] : adv;
+}
+// Row m's advantage, normalised when a.norm is set.
+__device__ __forceinline__ float row_advantage(const RowArgs& a, uint32_t m) {
+    return normalized_advantage(a, a.adv[m]);
 }
 // exp_f(-ls[j]) for j < 4, exp_f(-2 ls[j - 4]) for j = 4..7: the per-action
 // scale factors of row_objective, the same for every row, formed once per
@@ -998,7 +1001,7 @@ __global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
 #pragma unroll
             for (uint32_t q = 0; q < 4; q++) ract[q] = a.actions[size_t(mrow) * 4 + q];
             rolp = a.old_logp[mrow];
-            radv = row_advantage(a, mrow);
+            radv = a.adv[mrow];  // normalised where it is used, so no load waits on it here
             rret = a.ret[mrow];
         }
 #pragma unroll
@@ -1076,7 +1079,7 @@ __global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
             const float mean[4] = {s_mv[t][0], s_mv[t][1], s_mv[t][2], s_mv[t][3]};
             const float value = s_mv[t][4], target = rret;
             float dmean[4];
-            const float adv = radv;
+            const float adv = normalized_advantage(a, radv);
             if (a.norm) a.adv_out[mrow] = adv;
             row_objective(a, s_at + 5 * HID + 4, s_ex, ract, rolp, adv, mean, value, target, scale, dmean, rs);
             rs[12] = a.vcoef * (value - target) * scale;
@@ -1160,20 +1163,26 @@ __global__ __launch_bounds__(64) void mb_grad_kernel(MbArgs m) {
         b_ok = true; b_one = false; pb = m.rec + MB_HC + bc; sb = HID;
     }
     const float b_pad = b_one ? 1.0f : -0.0f;
-    float av[64], bv[64];
+    float xv[64], yv[64];
 #pragma unroll
     for (uint32_t s = 0; s < 64; s++) {
         const uint32_t r = 4 * s + l / 16;
-        const bool rv = r < rows;
-        const size_t rr = rv ? r : 0;
-        const float x = pa[rr * sa], y = pb[rr * sb];
-        av[s] = rv && a_ok ? x : 0.0f;
-        bv[s] = rv ? (b_ok ? y : b_pad) : -0.0f;
+        const size_t rr = r < rows ? r : 0;
+        xv[s] = pa[rr * sa];
+        yv[s] = pb[rr * sb];
     }
+    // every operand load issued before the chain selects and consumes the
+    // first (the scheduler would otherwise interleave them in short batches)
+    __builtin_amdgcn_sched_barrier(0);
     // rows past b contribute fma(0, -0, acc) = acc
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (uint32_t s = 0; s < 64; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bv[s], acc, 0, 0, 0);
+    for (uint32_t s = 0; s < 64; s++) {
+        const bool rv = 4 * s + l / 16 < rows;
+        const float av = rv && a_ok ? xv[s] : 0.0f;
+        const float bv = rv ? (b_ok ? yv[s] : b_pad) : -0.0f;
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+    }
     float* g = m.grad;
     // accumulator register r of lane l holds D[4 (l/16) + r][l % 16]
 #pragma unroll
@@ -1235,6 +1244,13 @@ __global__ __launch_bounds__(256) void adam_slices_kernel(AdamArgs a) {
         const uint32_t i = i0 + t + 256 * k;
         if (i < P) { gv[k] = g[i]; mv[k] = m[i]; vv[k] = v[i]; pv[k] = params[i]; }
     }
+    // the metric row's sums (workgroup 0) read with the first loads
+    float met[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (blockIdx.x == 0 && t == 0) {
+        const float* ms = a.grad + L::COUNT + C_COUNT;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; q++) met[q] = ms[q];
+    }
     float s = 0.0f;
     if (critic) {
         float x[NC];
@@ -1253,10 +1269,17 @@ __global__ __launch_bounds__(256) void adam_slices_kernel(AdamArgs a) {
     }
     part[t] = s;
     __syncthreads();
-    for (uint32_t stride = 128; stride > 0; stride >>= 1) {
-        if (t < stride) part[t] = part[t] + part[t + stride];
-        __syncthreads();
+    // the pairwise tree: strides 128 and 64 through LDS, 32 to 1 by shuffles
+    // within wavefront 0 (lane t adds lane t + stride, as the LDS steps do)
+    if (t < 128) part[t] = part[t] + part[t + 128];
+    __syncthreads();
+    if (t < 64) {
+        float v = part[t] + part[t + 64];
+#pragma unroll
+        for (uint32_t stride = 32; stride > 0; stride >>= 1) v = v + __shfl_down(v, stride, 64);
+        if (t == 0) part[0] = v;
     }
+    __syncthreads();
     const float norm = sqrt_f(part[0] + 1.0e-20f);
     const float scale = min_f(1.0f, 0.5f / norm);
     if (i0 == 0 && t == 0) a.norm_row[critic ? 1 : 0] = norm;  // ppo_grad_norm's row (main.mm:963-975)
@@ -1279,11 +1302,10 @@ __global__ __launch_bounds__(256) void adam_slices_kernel(AdamArgs a) {
         }
     }
     if (!critic && blockIdx.x == 0 && t == 0) {
-        const float* ms = a.grad + L::COUNT + C_COUNT;
-        a.metric_row[0] = ms[0];
-        a.metric_row[1] = ms[1];
-        a.metric_row[2] = ms[2];
-        a.metric_row[3] = ms[3] / float(a.b);
+        a.metric_row[0] = met[0];
+        a.metric_row[1] = met[1];
+        a.metric_row[2] = met[2];
+        a.metric_row[3] = met[3] / float(a.b);
     }
 }
 
