@@ -862,6 +862,7 @@ int ppo_update(MdnPPO* p, uint32_t rollout_index, bool normalize_rows) {
     const std::vector<uint32_t> order = mdn::minibatch_schedule(rows, p->minibatch, p->epochs, rollout_index);
     if (order.size() != p->updates) return fail(MDN_E_STATE, "PPO update count mismatch");
     const size_t first_epoch = order.size() / p->epochs;
+    bool stale_w1t = false;  // transposed first layers behind the flat vectors
     for (size_t u = 0; u < order.size(); u++) {
         const uint32_t begin = order[u];
         const uint32_t b = std::min(p->minibatch, rows - begin);
@@ -879,7 +880,8 @@ int ppo_update(MdnPPO* p, uint32_t rollout_index, bool normalize_rows) {
         ra.actor = s->actor; ra.actor_w1t = s->actor_w1t; ra.critic = s->critic; ra.critic_w1t = s->critic_w1t;
         ra.part = p->part;
         ra.b = b; ra.d = s->shape.obs; ra.clip = 0.2f; ra.vcoef = 0.5f; ra.ecoef = s->cfg.entropy_coef;
-        if (p->mb_rec && b <= ppo::MB_ROWS) {  // one chunk: row and parameter passes over many CUs
+        const bool one_chunk = p->mb_rec && b <= ppo::MB_ROWS;
+        if (one_chunk) {  // one chunk: row and parameter passes over many CUs
             ppo::MbArgs ma;
             ma.r = ra;
             ma.rec = p->mb_rec;
@@ -904,7 +906,15 @@ int ppo_update(MdnPPO* p, uint32_t rollout_index, bool normalize_rows) {
         mdn::adam_corrections(p->optimizer_step, 0.9f, 0.999f, &aa.c1, &aa.c2);
         aa.b = b;
         aa.d = s->shape.obs;
+        // the one-chunk forward stages the flat first layers, so their
+        // transposed copies are formed once, after the last step
+        aa.keep_w1t = one_chunk ? 0u : 1u;
+        stale_w1t = stale_w1t || one_chunk;
         rc = timed(s, MDN_K_ADAM, [&] { return ppo_launch_adam(&aa, s->stream); });
+        if (rc) return rc;
+    }
+    if (stale_w1t) {
+        rc = refresh_transposes(s);
         if (rc) return rc;
     }
     HIP_TRY(ppo_launch_metric_mean(p->metric_rows, p->metric_mean, p->updates, s->stream));

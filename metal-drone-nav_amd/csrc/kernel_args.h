@@ -173,6 +173,7 @@ struct AdamArgs {
     float lr, c1, c2;    // host bias corrections 1-beta^step
     uint32_t b;
     uint32_t d;          // actor inputs
+    uint32_t keep_w1t = 1;  // 0: leave actor_w1t / critic_w1t for one transpose after the update
 };
 }  // namespace ppo
 

@@ -978,13 +978,15 @@ __global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
     {   // every load of the staging issued before any store
         constexpr uint32_t NW = (D * HID + 511) / 512, NCW = COBS * HID / 512, NX = (MB_FWD_ROWS * D + 511) / 512;
         float w[NW], cw[NCW], xv[NX], cv, tv[2];
+        // the first layers from the flat vectors ([unit][input]), transposed
+        // into LDS (the transposed copies are refreshed once per update)
 #pragma unroll
         for (uint32_t k = 0; k < NW; k++) {
             const uint32_t e = t + 512 * k;
-            w[k] = e < D * HID ? a.actor_w1t[e] : 0.0f;
+            w[k] = e < D * HID ? a.actor[e] : 0.0f;
         }
 #pragma unroll
-        for (uint32_t k = 0; k < NCW; k++) cw[k] = a.critic_w1t[t + 512 * k];
+        for (uint32_t k = 0; k < NCW; k++) cw[k] = a.critic[t + 512 * k];
 #pragma unroll
         for (uint32_t k = 0; k < NX; k++) {
             const uint32_t e = t + 512 * k, r = e / D;
@@ -1007,12 +1009,12 @@ __global__ __launch_bounds__(512) void mb_forward_kernel(MbArgs m) {
 #pragma unroll
         for (uint32_t k = 0; k < NW; k++) {
             const uint32_t e = t + 512 * k;
-            if (e < D * HID) s_w[(e / HID) * WS + e % HID] = w[k];
+            if (e < D * HID) s_w[(e % D) * WS + e / D] = w[k];
         }
 #pragma unroll
         for (uint32_t k = 0; k < NCW; k++) {
             const uint32_t e = t + 512 * k;
-            s_cw[(e / HID) * WS + e % HID] = cw[k];
+            s_cw[(e % COBS) * WS + e / COBS] = cw[k];
         }
 #pragma unroll
         for (uint32_t k = 0; k < NX; k++) {
@@ -1297,8 +1299,10 @@ __global__ __launch_bounds__(256) void adam_slices_kernel(AdamArgs a) {
             float p = pv[k] - a.lr * mh / (sqrt_f(vh) + 1.0e-8f);
             if (!critic && i >= L::LS && i < L::LS + 4) p = clamp_f(p, -2.0f, .5f);
             params[i] = p;
-            if (!critic && i < HID * D) a.actor_w1t[size_t(i % D) * HID + i / D] = p;
-            if (critic && i < HID * COBS) a.critic_w1t[size_t(i % COBS) * HID + i / COBS] = p;
+            if (a.keep_w1t) {
+                if (!critic && i < HID * D) a.actor_w1t[size_t(i % D) * HID + i / D] = p;
+                if (critic && i < HID * COBS) a.critic_w1t[size_t(i % COBS) * HID + i / COBS] = p;
+            }
         }
     }
     if (!critic && blockIdx.x == 0 && t == 0) {
