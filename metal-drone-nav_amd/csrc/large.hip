@@ -272,8 +272,17 @@ __global__ __launch_bounds__(256) void part_sum_kernel(const float* __restrict__
                                                        uint32_t prior_stride) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= B * NQ) return;
+    // the slices in order, 8 loads in flight at a time; slices past the
+    // last are loaded as 0 and not added (the first slice may be -0)
     float v = part[i];
-    for (uint32_t s = 1; s < S; s++) v += part[size_t(s) * BP * NQ + i];
+    for (uint32_t s0 = 1; s0 < S; s0 += 8) {
+        float x[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) x[k] = s0 + k < S ? part[size_t(s0 + k) * BP * NQ + i] : 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++)
+            if (s0 + k < S) v += x[k];
+    }
     const uint32_t row = i / NQ, q = i % NQ;
     out[i] = prior && q < 3 ? (b2[q] + v) + prior[size_t(row) * prior_stride + q] : b2[q] + v;
 }
@@ -723,13 +732,37 @@ __global__ __launch_bounds__(256) void sum_segments_kernel(SumSegs g) {
     const uint32_t t = threadIdx.x;
     float sq[2] = {0.0f, 0.0f};
     for (uint64_t i = uint64_t(blockIdx.x) * 256 + t; i < g.start[6]; i += uint64_t(gridDim.x) * 256) {
+        // the element's segment (the starts ascend), its fields picked with
+        // constant indices so they stay in scalar registers (an indexed read
+        // of the argument arrays is a memory load the sums would wait on)
         uint32_t sg = 0;
-        while (sg < 5 && i >= g.start[sg + 1]) sg++;
-        const uint64_t j = i - g.start[sg], n = g.start[sg + 1] - g.start[sg];
-        const float* src = g.src[sg];
+#pragma unroll
+        for (uint32_t q = 1; q < 6; q++) sg += i >= g.start[q] ? 1u : 0u;
+        const float* src = g.src[0];
+        float* dst = g.dst[0];
+        uint64_t s0 = g.start[0], s1 = g.start[1];
+        uint32_t slots = g.slots[0];
+#pragma unroll
+        for (uint32_t q = 1; q < 6; q++) {
+            const bool h = sg == q;
+            src = h ? g.src[q] : src;
+            dst = h ? g.dst[q] : dst;
+            s0 = h ? g.start[q] : s0;
+            s1 = h ? g.start[q + 1] : s1;
+            slots = h ? g.slots[q] : slots;
+        }
+        const uint64_t j = i - s0, n = s1 - s0;
+        // the slots in order, 32 loads in flight at a time; a slot past the
+        // last adds +0, which leaves the sum (never -0) unchanged
         float s = 0.0f;
-        for (uint32_t c = 0; c < g.slots[sg]; c++) s += src[uint64_t(c) * n + j];
-        g.dst[sg][j] = s;
+        for (uint32_t c0 = 0; c0 < slots; c0 += 32) {
+            float v[32];
+#pragma unroll
+            for (uint32_t k = 0; k < 32; k++) v[k] = c0 + k < slots ? src[uint64_t(c0 + k) * n + j] : 0.0f;
+#pragma unroll
+            for (uint32_t k = 0; k < 32; k++) s += v[k];
+        }
+        dst[j] = s;
         sq[sg < 3 ? 0 : 1] += s * s;
     }
     if (blockIdx.x == 0 && t == 0)
