@@ -448,27 +448,30 @@ static_assert(256 * RS <= U_WORDS, "the per-row scalars fit the shared scratch")
 // of the banks.
 __device__ __forceinline__ uint32_t w1_pos(uint32_t k, uint32_t u) { return k * HID + (u ^ (32u * (k & 1u))); }
 // W1T [D][64] (global, input-major) into LDS for inputs 0 .. KP-1, the
-// inputs past D as -0.
+// inputs past D as -0, in two halves so that a kernel can issue every load
+// of its prologue before the first store.
 template <uint32_t D, uint32_t KP>
-__device__ __forceinline__ void stage_w1(const float* __restrict__ W1T, float* sw) {
+__device__ __forceinline__ void stage_w1_load(const float* __restrict__ W1T, float (&v)[KP * HID / CT]) {
     static_assert(KP * HID % CT == 0, "whole staging rounds");
-    constexpr uint32_t N = KP * HID / CT;
     const uint32_t t = threadIdx.x;
-    float v[N];
 #pragma unroll
-    for (uint32_t j = 0; j < N; j++) {
+    for (uint32_t j = 0; j < KP * HID / CT; j++) {
         const uint32_t e = t + CT * j;
         v[j] = e / HID < D ? W1T[e] : -0.0f;
     }
+}
+template <uint32_t D, uint32_t KP>
+__device__ __forceinline__ void stage_w1_store(const float (&v)[KP * HID / CT], float* sw) {
+    const uint32_t t = threadIdx.x;
 #pragma unroll
-    for (uint32_t j = 0; j < N; j++) {
+    for (uint32_t j = 0; j < KP * HID / CT; j++) {
         const uint32_t e = t + CT * j;
         sw[w1_pos(e / HID, e % HID)] = v[j];
     }
 }
 
 // h[256][64] = tanh(X W1^T + b1) for the chunk's rows (rows past b read as
-// 0), with W1 staged by stage_w1<D, KP>.  Wavefront w owns rows 32w..32w+31
+// 0), with W1 staged by stage_w1_load/stage_w1_store<D, KP>.  Wavefront w owns rows 32w..32w+31
 // as two 32x32 tiles (hidden units 0-31, 32-63).  It fetches its rows'
 // inputs in blocks of 16 (each load instruction covering 4 rows x 16
 // consecutive inputs), two blocks ahead of the matrix cores, and passes each
@@ -765,7 +768,7 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     using L = AL<D>;
     __shared__ float s_h[256 * HS];
     __shared__ __attribute__((aligned(16))) float s_u[U_WORDS];
-    __shared__ float s_aw[OBS_PAD * HID];  // the actor's first layer (stage_w1)
+    __shared__ float s_aw[OBS_PAD * HID];  // the actor's first layer (stage_w1_store)
     __shared__ __attribute__((aligned(16))) float s_dv[256];
     // the critic's w2 and the actor's W2 [4][64], read by every row's chains:
     // one LDS copy (broadcast reads) instead of per-step global loads
@@ -773,19 +776,30 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     __shared__ float s_ex[8];  // exp(-log_std), exp(-2 log_std): the same for every row
     const uint32_t t = threadIdx.x, wv = t / 64;
     const bool rowt = t < 256;  // the row-wise phases' threads
-    if (t < HID) s_w2[t] = a.critic[C_W2 + t];
-    else if (t < 5 * HID) s_w2[t] = a.actor[L::W2 + t - HID];
-    else if (t < 5 * HID + 8) s_ex[t - 5 * HID] = row_scale_exp(a.actor + L::LS, t - 5 * HID);
-    stage_w1<COBS, COBS>(a.critic_w1t, s_u);
-    stage_w1<D, OBS_PAD>(a.actor_w1t, s_aw);
     const uint32_t n0 = blockIdx.x * 256;
     const uint32_t rows = a.b - n0 < 256 ? a.b - n0 : 256;
     const bool live = t < rows;
     const uint32_t n = n0 + t, m = live ? n : n0;
     float* P = a.part + size_t(blockIdx.x) * L::P_TOTAL;
     const float scale = 1.0f / max_f(float(a.b), 1.0f);
-    // read before the first barrier, stored back (live rows) after it
-    const float adv = row_advantage(a, m);
+    // every global load of the prologue issued before its first LDS store:
+    // the output layers' weights (thread t < 5 HID) or a log-std (the next
+    // 8), both first layers, and the row's advantage (read before the first
+    // barrier, stored back for live rows after it) and return
+    const uint32_t xj = t - 5 * HID;  // row_scale_exp index of threads 5 HID .. 5 HID + 7
+    const float w2v = t < HID ? a.critic[C_W2 + t]
+                    : t < 5 * HID ? a.actor[L::W2 + t - HID]
+                                  : a.actor[L::LS + (t < 5 * HID + 8 ? xj % 4 : 0)];
+    float cwv[COBS * HID / CT], awv[OBS_PAD * HID / CT];
+    stage_w1_load<COBS, COBS>(a.critic_w1t, cwv);
+    stage_w1_load<D, OBS_PAD>(a.actor_w1t, awv);
+    const float adv_raw = a.adv[m];
+    const float target = a.ret[m];
+    if (t < 5 * HID) s_w2[t] = w2v;
+    else if (t < 5 * HID + 8) s_ex[xj] = xj < 4 ? exp_f(-w2v) : exp_f(-2.0f * w2v);  // row_scale_exp
+    stage_w1_store<COBS, COBS>(cwv, s_u);
+    stage_w1_store<D, OBS_PAD>(awv, s_aw);
+    const float adv = normalized_advantage(a, adv_raw);
 
     // ---- critic: forward, value, dV (ppo.hpp:82-93, 176-180)
     __syncthreads();
@@ -794,7 +808,6 @@ __global__ __launch_bounds__(CT) void chunk_kernel(RowArgs a) {
     row_load<COBS, 2 * COBS>(fc, a.co, n0, rows, 0);
     float value = a.critic[C_B2];
     if (rowt) value = lds_chain<true, HID>(s_w2, s_h + t * HS, 1, 0, HID, value);
-    const float target = a.ret[m];
     const float dvalue = a.vcoef * (value - target) * scale;
     if (rowt) s_dv[t] = live ? dvalue : 0.0f;
     __syncthreads();
