@@ -238,12 +238,14 @@ def test_rollout_parity_variants(variant):
     assert not bad, bad
 
 
-@pytest.mark.parametrize("epochs,minibatch", [(2, 256), (1, 512), (1, 200), (2, 200)])
+@pytest.mark.parametrize("epochs,minibatch", [(2, 256), (1, 512), (1, 200), (2, 200), (1, 17)])
 def test_iteration_parity(epochs, minibatch):
     """Two iterations against the oracle.  Minibatches of at most 256 rows
     take the one-chunk path (row-parallel forward, parameter-parallel
     gradient); 200-row minibatches leave a 48-row last one and end an update
-    after an odd (11) and an even (22) number of steps."""
+    after an odd (11) and an even (22) number of steps; 17-row minibatches
+    give the forward a one-row workgroup in every step and an 8-row last
+    minibatch (121 steps)."""
     say("case: iteration N=32 T=64 epochs=%d minibatch=%d" % (epochs, minibatch))
     cfg = config(n=32, family=1, speed=1.0, distance=3.0, max_steps=40)
     sim, ppo, ora = make_pair(cfg, 64, epochs=epochs, minibatch=minibatch)
