@@ -889,6 +889,11 @@ int ppo_update(MdnPPO* p, uint32_t rollout_index, bool normalize_rows) {
             rc = timed(s, MDN_K_ROWS, [&] { return ppo_launch_minibatch(&ma, s->stream); });
             if (rc) return rc;
         } else {
+            if (stale_w1t) {  // the chunk kernel stages the transposed copies
+                rc = refresh_transposes(s);
+                if (rc) return rc;
+                stale_w1t = false;
+            }
             rc = timed(s, MDN_K_ROWS, [&] { return ppo_launch_rows(&ra, s->stream); });
             if (rc) return rc;
             rc = timed(s, MDN_K_GRADS, [&] {
