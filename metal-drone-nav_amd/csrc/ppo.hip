@@ -1230,8 +1230,9 @@ __global__ __launch_bounds__(64) void mb_grad_kernel(MbArgs m) {
 // first AW take slices of the actor, the rest slices of the critic.  Each
 // recomputes its net's squared gradient norm in the canonical order (256
 // strided partials, then the pairwise tree) and updates a slice of ADAM_SLICE
-// parameters, refreshing the transposed first-layer copy and clamping the
-// log-stds it owns; workgroup 0 writes the metric row.
+// parameters, clamping the log-stds it owns and, unless keep_w1t is 0 (the
+// 256-row path, which transposes once after the update), refreshing the
+// transposed first-layer copy; workgroup 0 writes the metric row.
 constexpr uint32_t ADAM_SLICE = 1024;
 template <uint32_t D>
 constexpr uint32_t adam_groups() {
