@@ -1233,7 +1233,7 @@ __global__ __launch_bounds__(64) void mb_grad_kernel(MbArgs m) {
 // parameters, clamping the log-stds it owns and, unless keep_w1t is 0 (the
 // 256-row path, which transposes once after the update), refreshing the
 // transposed first-layer copy; workgroup 0 writes the metric row.
-constexpr uint32_t ADAM_SLICE = 1024;
+constexpr uint32_t ADAM_SLICE = 256;
 template <uint32_t D>
 constexpr uint32_t adam_groups() {
     return (AL<D>::COUNT + ADAM_SLICE - 1) / ADAM_SLICE + (C_COUNT + ADAM_SLICE - 1) / ADAM_SLICE;
